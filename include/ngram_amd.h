@@ -1,0 +1,85 @@
+/* ngram_amd: the C ABI of the MI355X (gfx950) n-gram hint engine, libngram_amd.so.
+ *
+ * Conventions (those of the reference's ctypes binding, old_records/gpu_val_stats.py:133-158): plain pointers to
+ * device memory, 64-bit sizes, the HIP stream last (a hipStream_t passed as void*); calls are asynchronous on that
+ * stream; the return value is 0 or a hipError_t value, -1 for unsupported arguments. No entry point allocates device
+ * memory: buffers are the caller's; the *_temp_bytes / two-phase calls size the caller's scratch.
+ * Tokens are uint16 (GPT-2 ids, BOS = 50256); SENT = 0xFFFF marks the gaps between concatenated shards.
+ */
+#ifndef NGRAM_AMD_H
+#define NGRAM_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef unsigned long long ng_u64;
+typedef long long ng_i64;
+
+/* ------------------------------------------------------------------------------------------------------------
+ * gpu_val_stats flavour: the entry points old_records/gpu_val_stats.py binds (replacing
+ * old_records/gpu_val_stats.cu, same names, arguments and return codes). k: 1..64 (the reference's LEVEL_SWITCH
+ * accepts 1-8, 10, 12, 16, 20 and returns -1 otherwise; this build also runs the other k up to 64).
+ * ------------------------------------------------------------------------------------------------------------ */
+
+/* per query position i: the key of x[i-k+1..i] if avail[i] >= k, else EMPTY (gpu_val_stats.cu:96-99) */
+int val_keys(const uint16_t* x, const int* avail, ng_i64 n, int k, ng_u64* out, void* stream);
+/* each valid position's k tokens vs its group representative's; mismatches counted in *bad (gpu_val_stats.cu:114-119) */
+int val_verify(const uint16_t* x, const ng_i64* spos, const ng_i64* gid, const ng_i64* rep, ng_i64 n, int k,
+               ng_u64* bad, void* stream);
+/* home slot umulhi(key, cap) of each key (gpu_val_stats.cu:129-132) */
+int val_homes(const ng_u64* keys, ng_i64 n, ng_u64 cap, ng_i64* home, void* stream);
+/* one level's scan: probe, bitmap of hits, count (mode 0 dense / 1 sparse) or emit (2 dense / 3 by words)
+ * (gpu_val_stats.cu:306-338) */
+int scan_level(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, uint32_t* bm_out, const ng_u64* vt,
+               ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, ng_u64* pk, uint32_t* pc, ng_u64 sub_cap,
+               int pbits, uint32_t* flags, int grid, int mode, ng_u64* emit, ng_u64* emitted, void* stream);
+/* emitted keys per sub-table (gpu_val_stats.cu:410-418) */
+int subpart_count(const ng_u64* keys, ng_i64 n, int pbits, ng_u64* counts, void* stream);
+/* emitted keys grouped by sub-table (gpu_val_stats.cu:420-428) */
+int subpart_scatter(const ng_u64* keys, ng_i64 n, int pbits, ng_u64* cursor, ng_u64* out, void* stream);
+/* grouped keys counted into the pair table (gpu_val_stats.cu:430-434) */
+int aggregate(const ng_u64* keys, ng_i64 n, ng_u64* pk, uint32_t* wraps, ng_u64 sub_cap, int pbits, uint32_t* flags,
+              int grid, void* stream);
+/* the most sub-table bits the LDS histograms allow on this device (gpu_val_stats.cu:396-403; no stream) */
+int max_pbits(void);
+/* set bits of a bitmap added to *out (gpu_val_stats.cu:443-446) */
+int popcount(const uint32_t* bm, ng_i64 n, ng_u64* out, void* stream);
+/* pair-table entries per owner (gpu_val_stats.cu:472-476) */
+int part_count(const ng_u64* pk, ng_u64 cap, const ng_i64* bounds, int W, ng_u64* counts, void* stream);
+/* pair-table entries as (key, count) grouped by owner (gpu_val_stats.cu:518-523) */
+int part_scatter(const ng_u64* pk, const uint32_t* pc, ng_u64 cap, const ng_i64* bounds, int W, ng_u64* cursor,
+                 ng_u64* ok, uint32_t* oc, void* stream);
+/* stable radix sort of (u64 key, u32 value) by key bits [begin_bit, end_bit); temp == NULL: *temp_bytes = the
+ * scratch needed (CUB-style; gpu_val_stats.cu:530-536) */
+int sort_pairs(void* temp, size_t* temp_bytes, const ng_u64* kin, ng_u64* kout, const uint32_t* vin, uint32_t* vout,
+               ng_i64 n, int begin_bit, int end_bit, void* stream);
+/* inclusive running maximum of int64 (gpu_val_stats.cu:539-543) */
+int inclusive_max(void* temp, size_t* temp_bytes, const ng_i64* in, ng_i64* out, ng_i64 n, void* stream);
+/* runs of equal keys -> unique keys, summed values, *nruns (gpu_val_stats.cu:545-551) */
+int reduce_by_key(void* temp, size_t* temp_bytes, const ng_u64* kin, ng_u64* kout, const uint32_t* vin,
+                  uint32_t* vout, ng_i64* nruns, ng_i64 n, void* stream);
+/* per context id: [start, end) of its pairs in sorted keys (gpu_val_stats.cu:561-564) */
+int seg_bounds(const ng_u64* uk, ng_i64 U, ng_i64* start, ng_i64* end, void* stream);
+/* per context: total = sum of its pair counts (gpu_val_stats.cu:574-577) */
+int ctx_tot(const ng_i64* start, const ng_i64* end, const uint32_t* agg, ng_i64 nctx, ng_u64* tot, void* stream);
+/* ranking keys: context << 32 | (2^32 - 1 - count), value = pair index (gpu_val_stats.cu:587-590) */
+int rank_keys(const ng_u64* uk, const uint32_t* agg, ng_i64 U, ng_u64* key2, uint32_t* val2, void* stream);
+/* rank of each pair within its context; the top `top` tokens/counts per context (gpu_val_stats.cu:606-612) */
+int rank_scatter(const uint32_t* sv, ng_i64 U, const ng_u64* uk, const uint32_t* agg, const ng_i64* start,
+                 uint32_t* rank_of, uint16_t* top_tok, uint32_t* top_cnt, int top, void* stream);
+/* per query position: tot, dist, cnt (TOP rule), mask bit li (gpu_val_stats.cu:637-644) */
+int pos_outputs(const int* ctx_of, ng_i64 N, ng_i64 lo, ng_i64 hi, const uint16_t* tgt, const ng_u64* uk,
+                const uint32_t* agg, const uint32_t* rank_of, const ng_i64* start, const ng_i64* end,
+                const ng_u64* tot, int li, int cnt_top, int* out_tot, int* out_dist, int* out_cnt, int* mask,
+                void* stream);
+/* one variant's hint rows: cell, 8 tokens, 8 weights packed in int32[N, 9] (gpu_val_stats.cu:696-699) */
+int variant_rows(ng_i64 N, const int* mask, int nv, const ng_i64* desc, int* rows, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NGRAM_AMD_H */

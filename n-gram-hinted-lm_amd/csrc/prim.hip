@@ -1,0 +1,417 @@
+// Device-wide primitives: scans, stable LSD radix sort, reduce-by-key (see prim.h). Own kernels for gfx950: 256-thread
+// workgroups (four wave64s), 4096-item tiles, LDS block scans and wave ballots for stable ranking.
+#include "prim.h"
+
+namespace prim {
+
+static constexpr int BLOCK = 256;
+static constexpr int ITEMS = 16;
+static constexpr int TILE = BLOCK * ITEMS;
+static constexpr int NWAVES = BLOCK / WAVE;
+
+static inline size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
+static inline i64 ntiles_of(i64 n) { return (n + TILE - 1) / TILE; }
+
+template <typename T>
+struct Sum {
+    __device__ static T id() { return (T)0; }
+    __device__ static T op(T a, T b) { return a + b; }
+};
+struct MaxI64 {
+    __device__ static i64 id() { return (i64)0x8000000000000000ll; }
+    __device__ static i64 op(i64 a, i64 b) { return a > b ? a : b; }
+};
+
+template <typename T>
+__device__ __forceinline__ T shfl_up_t(T v, int d) {
+    if constexpr (sizeof(T) == 8) return (T)shfl_up_u64((u64)v, d);
+    else return (T)__shfl_up((int)v, d, WAVE);
+}
+
+// Exclusive scan of one value per thread over the 256-thread block; *block_total receives the reduction.
+template <typename T, typename Op>
+__device__ __forceinline__ T block_exclusive(T v, T* block_total) {
+    __shared__ T wave_tot[NWAVES];
+    const int lane = lane_id(), w = threadIdx.x / WAVE;
+    T incl = v;
+#pragma unroll
+    for (int d = 1; d < WAVE; d <<= 1) {
+        T o = shfl_up_t(incl, d);
+        if (lane >= d) incl = Op::op(o, incl);
+    }
+    if (lane == WAVE - 1) wave_tot[w] = incl;
+    __syncthreads();
+    T before = Op::id(), total = Op::id();
+#pragma unroll
+    for (int i = 0; i < NWAVES; ++i) {
+        if (i < w) before = Op::op(before, wave_tot[i]);
+        total = Op::op(total, wave_tot[i]);
+    }
+    __syncthreads();
+    // exclusive within the wave
+    T excl_w = shfl_up_t(incl, 1);
+    if (lane == 0) excl_w = Op::id();
+    if (block_total) *block_total = total;
+    return Op::op(before, excl_w);
+}
+
+template <typename T, typename Op>
+__global__ void __launch_bounds__(BLOCK) tile_reduce_k(const T* __restrict__ in, i64 n, T* __restrict__ partial) {
+    const i64 base = (i64)blockIdx.x * TILE;
+    T acc = Op::id();
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+        const i64 i = base + (i64)j * BLOCK + threadIdx.x;
+        if (i < n) acc = Op::op(acc, in[i]);
+    }
+    T total;
+    block_exclusive<T, Op>(acc, &total);
+    if (threadIdx.x == 0) partial[blockIdx.x] = total;
+}
+
+// Scan of one tile with the tile's exclusive prefix (prefix null: identity). The last tile writes the grand total.
+template <typename T, typename Op, bool INCLUSIVE>
+__global__ void __launch_bounds__(BLOCK) tile_scan_k(const T* in, T* out, i64 n, const T* __restrict__ prefix,
+                                                      T* total) {
+    __shared__ T s[TILE + TILE / 32];
+    const i64 base = (i64)blockIdx.x * TILE;
+    auto at = [](int i) { return i + (i >> 5); };  // padded index (fewer bank conflicts)
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+        const int l = j * BLOCK + threadIdx.x;
+        const i64 i = base + l;
+        s[at(l)] = i < n ? in[i] : Op::id();
+    }
+    __syncthreads();
+    T local[ITEMS];
+    T run = Op::id();
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+        local[j] = s[at(threadIdx.x * ITEMS + j)];
+        run = Op::op(run, local[j]);
+    }
+    T btot;
+    T carry = block_exclusive<T, Op>(run, &btot);
+    if (prefix) carry = Op::op(prefix[blockIdx.x], carry);
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+        if (INCLUSIVE) {
+            carry = Op::op(carry, local[j]);
+            s[at(threadIdx.x * ITEMS + j)] = carry;
+        } else {
+            s[at(threadIdx.x * ITEMS + j)] = carry;
+            carry = Op::op(carry, local[j]);
+        }
+    }
+    if (total && blockIdx.x == gridDim.x - 1 && threadIdx.x == BLOCK - 1) *total = carry;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+        const int l = j * BLOCK + threadIdx.x;
+        const i64 i = base + l;
+        if (i < n) out[i] = s[at(l)];
+    }
+}
+
+template <typename T>
+static size_t scan_temp(i64 n) {
+    size_t bytes = 0;
+    i64 m = ntiles_of(n);
+    while (m > 1) {
+        bytes += align_up((size_t)m * sizeof(T));
+        m = ntiles_of(m);
+    }
+    return bytes + 256;
+}
+
+template <typename T, typename Op, bool INCLUSIVE>
+static int scan_impl(const T* in, T* out, i64 n, T* total, char* temp, hipStream_t st) {
+    if (n <= 0) return 0;
+    const i64 nt = ntiles_of(n);
+    if (nt == 1) {
+        tile_scan_k<T, Op, INCLUSIVE><<<1, BLOCK, 0, st>>>(in, out, n, nullptr, total);
+        return (int)hipGetLastError();
+    }
+    T* partial = (T*)temp;
+    temp += align_up((size_t)nt * sizeof(T));
+    tile_reduce_k<T, Op><<<(unsigned)nt, BLOCK, 0, st>>>(in, n, partial);
+    int e = scan_impl<T, Op, false>(partial, partial, nt, nullptr, temp, st);
+    if (e) return e;
+    tile_scan_k<T, Op, INCLUSIVE><<<(unsigned)nt, BLOCK, 0, st>>>(in, out, n, partial, total);
+    return (int)hipGetLastError();
+}
+
+__global__ void cast_total_k(const u32* t32, u64* out) { *out = (u64)*t32; }
+
+size_t scan_u32_temp_bytes(i64 n) { return scan_temp<u32>(n) + 256; }
+
+int exclusive_scan_u32(const u32* in, u32* out, i64 n, u64* total, void* temp, hipStream_t st) {
+    if (n < 0) return -1;
+    if (n == 0) {
+        if (total) return fill_u64(total, 0ull, 1, st);
+        return 0;
+    }
+    char* t = (char*)temp;
+    u32* t32 = (u32*)t;
+    t += 256;
+    int e = scan_impl<u32, Sum<u32>, false>(in, out, n, total ? t32 : nullptr, t, st);
+    if (e) return e;
+    if (total) {
+        cast_total_k<<<1, 1, 0, st>>>(t32, total);
+        return (int)hipGetLastError();
+    }
+    return 0;
+}
+
+size_t scan_u64_temp_bytes(i64 n) { return scan_temp<u64>(n); }
+
+int exclusive_scan_u64(const u64* in, u64* out, i64 n, u64* total, void* temp, hipStream_t st) {
+    if (n < 0) return -1;
+    if (n == 0) {
+        if (total) return fill_u64(total, 0ull, 1, st);
+        return 0;
+    }
+    return scan_impl<u64, Sum<u64>, false>(in, out, n, total, (char*)temp, st);
+}
+
+size_t max_i64_temp_bytes(i64 n) { return scan_temp<i64>(n); }
+
+int inclusive_max_i64(const i64* in, i64* out, i64 n, void* temp, hipStream_t st) {
+    if (n < 0) return -1;
+    return scan_impl<i64, MaxI64, true>(in, out, n, nullptr, (char*)temp, st);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Radix sort
+// ---------------------------------------------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(BLOCK) rs_hist_k(const u64* __restrict__ keys, i64 n, int shift, u32 mask,
+                                                   u32* __restrict__ hist, i64 ntiles) {
+    __shared__ u32 h[256];
+    h[threadIdx.x] = 0;
+    __syncthreads();
+    const i64 base = (i64)blockIdx.x * TILE;
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+        const i64 i = base + (i64)j * BLOCK + threadIdx.x;
+        if (i < n) atomicAdd(&h[(u32)(keys[i] >> shift) & mask], 1u);
+    }
+    __syncthreads();
+    hist[(i64)threadIdx.x * ntiles + blockIdx.x] = h[threadIdx.x];
+}
+
+// Stable scatter of one tile: items in tile order (row j, thread t) = index j * 256 + t; per row, each wave ranks its
+// lanes by digit with eight ballots; the per-(row, wave, digit) counts are scanned in LDS in tile order.
+template <bool VALUES>
+__global__ void __launch_bounds__(BLOCK) rs_scatter_k(const u64* __restrict__ kin, const u32* __restrict__ vin,
+                                                      u64* __restrict__ kout, u32* __restrict__ vout, i64 n, int shift,
+                                                      int nbits, const u32* __restrict__ hist, i64 ntiles) {
+    __shared__ u32 cnt[ITEMS][NWAVES][256];
+    __shared__ u32 base_s[256];
+    const int t = threadIdx.x, lane = lane_id(), w = t / WAVE;
+    const u32 mask = (1u << nbits) - 1u;
+    base_s[t] = hist[(i64)t * ntiles + blockIdx.x];
+    for (int i = t; i < ITEMS * NWAVES * 256; i += BLOCK) (&cnt[0][0][0])[i] = 0;
+    __syncthreads();
+    const i64 base = (i64)blockIdx.x * TILE;
+    u64 key[ITEMS];
+    u32 val[ITEMS];
+    u32 dr[ITEMS];  // digit | rank << 16 ; rank 0xFFFF = invalid
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+        const i64 i = base + (i64)j * BLOCK + t;
+        const bool valid = i < n;
+        key[j] = valid ? kin[i] : 0;
+        if (VALUES) val[j] = valid ? vin[i] : 0;
+        const u32 d = (u32)(key[j] >> shift) & mask;
+        u64 peers = __ballot(valid);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            if (b < nbits) {
+                const bool bit = (d >> b) & 1u;
+                const u64 bal = __ballot(bit);
+                peers &= bit ? bal : ~bal;
+            }
+        }
+        const u32 rank = (u32)__popcll(peers & lanemask_lt());
+        if (valid && rank == 0) cnt[j][w][d] = (u32)__popcll(peers);
+        dr[j] = valid ? (d | (rank << 16)) : 0xFFFF0000u;
+    }
+    __syncthreads();
+    {
+        u32 run = 0;
+        for (int j = 0; j < ITEMS; ++j)
+#pragma unroll
+            for (int ww = 0; ww < NWAVES; ++ww) {
+                const u32 c = cnt[j][ww][t];
+                cnt[j][ww][t] = run;
+                run += c;
+            }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+        if ((dr[j] >> 16) == 0xFFFFu) continue;
+        const u32 d = dr[j] & 0xFFFFu;
+        const u32 pos = base_s[d] + cnt[j][w][d] + (dr[j] >> 16);
+        kout[pos] = key[j];
+        if (VALUES) vout[pos] = val[j];
+    }
+}
+
+__global__ void copy_pairs_k(const u64* kin, u64* kout, const u32* vin, u32* vout, i64 n) {
+    for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n; i += (i64)gridDim.x * blockDim.x) {
+        kout[i] = kin[i];
+        if (vin) vout[i] = vin[i];
+    }
+}
+
+size_t radix_sort_temp_bytes(i64 n, bool with_values) {
+    if (n <= 0) return 256;
+    const i64 nt = ntiles_of(n);
+    size_t b = align_up((size_t)n * 8);
+    if (with_values) b += align_up((size_t)n * 4);
+    b += align_up((size_t)nt * 256 * 4);
+    b += scan_u32_temp_bytes(nt * 256);
+    return b;
+}
+
+int radix_sort_pairs(const u64* kin, u64* kout, const u32* vin, u32* vout, i64 n, int begin_bit, int end_bit,
+                     void* temp, size_t temp_bytes, hipStream_t st) {
+    if (n < 0 || begin_bit < 0 || end_bit > 64 || begin_bit > end_bit) return -1;
+    if (n == 0) return 0;
+    if ((n >> 32) != 0) return -1;  // offsets are 32-bit
+    const bool values = vin != nullptr && vout != nullptr;
+    if (kin == kout) return -1;
+    if (temp_bytes < radix_sort_temp_bytes(n, values)) return -1;
+    if (begin_bit == end_bit) {
+        copy_pairs_k<<<grid_for(n, 256) > 4096 ? 4096 : grid_for(n, 256), 256, 0, st>>>(kin, kout, values ? vin : nullptr,
+                                                                                     vout, n);
+        return (int)hipGetLastError();
+    }
+    const i64 nt = ntiles_of(n);
+    char* t = (char*)temp;
+    u64* tk = (u64*)t;
+    t += align_up((size_t)n * 8);
+    u32* tv = nullptr;
+    if (values) {
+        tv = (u32*)t;
+        t += align_up((size_t)n * 4);
+    }
+    u32* hist = (u32*)t;
+    t += align_up((size_t)nt * 256 * 4);
+    void* stemp = t;
+    const int passes = (end_bit - begin_bit + 7) / 8;
+    const u64* sk = kin;
+    const u32* sv = vin;
+    for (int p = 0; p < passes; ++p) {
+        const int shift = begin_bit + 8 * p;
+        const int nb = end_bit - shift < 8 ? end_bit - shift : 8;
+        const bool to_out = ((passes - 1 - p) % 2) == 0;
+        u64* dk = to_out ? kout : tk;
+        u32* dv = to_out ? vout : tv;
+        rs_hist_k<<<(unsigned)nt, BLOCK, 0, st>>>(sk, n, shift, (1u << nb) - 1u, hist, nt);
+        int e = exclusive_scan_u32(hist, hist, nt * 256, nullptr, stemp, st);
+        if (e) return e;
+        if (values)
+            rs_scatter_k<true><<<(unsigned)nt, BLOCK, 0, st>>>(sk, sv, dk, dv, n, shift, nb, hist, nt);
+        else
+            rs_scatter_k<false><<<(unsigned)nt, BLOCK, 0, st>>>(sk, nullptr, dk, nullptr, n, shift, nb, hist, nt);
+        e = (int)hipGetLastError();
+        if (e) return e;
+        sk = dk;
+        sv = dv;
+    }
+    return 0;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Reduce by key
+// ---------------------------------------------------------------------------------------------------------------
+
+__global__ void rbk_heads_k(const u64* __restrict__ k, i64 n, u32* __restrict__ heads) {
+    for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n; i += (i64)gridDim.x * blockDim.x)
+        heads[i] = (i == 0 || k[i] != k[i - 1]) ? 1u : 0u;
+}
+
+// heads scanned (exclusive) -> run of item i = excl[i] + head[i] - 1
+__global__ void rbk_keys_k(const u64* __restrict__ k, i64 n, const u32* __restrict__ excl, u64* __restrict__ kout) {
+    for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n; i += (i64)gridDim.x * blockDim.x)
+        if (i == 0 || k[i] != k[i - 1]) kout[excl[i]] = k[i];
+}
+
+// Each thread sums 16 consecutive items run by run: runs wholly inside its chunk are stored, runs crossing a chunk
+// edge are added atomically (vout zeroed first).
+__global__ void rbk_values_k(const u64* __restrict__ k, const u32* __restrict__ v, i64 n, const u32* __restrict__ excl,
+                             u32* __restrict__ vout) {
+    const i64 chunks = (n + 15) / 16;
+    for (i64 c = blockIdx.x * (i64)blockDim.x + threadIdx.x; c < chunks; c += (i64)gridDim.x * blockDim.x) {
+        const i64 a = c * 16, b = a + 16 < n ? a + 16 : n;
+        i64 i = a;
+        while (i < b) {
+            const u64 key = k[i];
+            const bool starts_here = i == 0 || k[i - 1] != key;
+            u32 s = 0;
+            i64 j = i;
+            while (j < b && k[j] == key) s += v[j++];
+            const bool ends_here = j == n || k[j] != key;
+            const u32 r = starts_here ? excl[i] : excl[i] - 1u;
+            if (starts_here && ends_here) vout[r] = s;
+            else atomicAdd(&vout[r], s);
+            i = j;
+        }
+    }
+}
+
+__global__ void rbk_nruns_k(const u64* total, i64* nruns) { *nruns = (i64)*total; }
+
+__global__ void fill_u64_k(u64* p, u64 v, i64 n) {
+    for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n; i += (i64)gridDim.x * blockDim.x) p[i] = v;
+}
+__global__ void fill_u32_k(u32* p, u32 v, i64 n) {
+    for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n; i += (i64)gridDim.x * blockDim.x) p[i] = v;
+}
+
+int fill_u64(u64* p, u64 v, i64 n, hipStream_t st) {
+    if (n <= 0) return 0;
+    int g = grid_for(n, 256);
+    fill_u64_k<<<g > 8192 ? 8192 : g, 256, 0, st>>>(p, v, n);
+    return (int)hipGetLastError();
+}
+int fill_u32(u32* p, u32 v, i64 n, hipStream_t st) {
+    if (n <= 0) return 0;
+    int g = grid_for(n, 256);
+    fill_u32_k<<<g > 8192 ? 8192 : g, 256, 0, st>>>(p, v, n);
+    return (int)hipGetLastError();
+}
+
+size_t reduce_by_key_temp_bytes(i64 n) {
+    if (n <= 0) return 512;
+    return align_up((size_t)n * 4) + 256 + scan_u32_temp_bytes(n);
+}
+
+int reduce_by_key(const u64* kin, u64* kout, const u32* vin, u32* vout, i64* nruns, i64 n, void* temp,
+                  hipStream_t st) {
+    if (n < 0) return -1;
+    if (n == 0) return fill_u64((u64*)nruns, 0ull, 1, st);
+    if ((n >> 32) != 0) return -1;
+    char* t = (char*)temp;
+    u32* heads = (u32*)t;
+    t += align_up((size_t)n * 4);
+    u64* total = (u64*)t;
+    t += 256;
+    int g = grid_for(n, 256);
+    if (g > 8192) g = 8192;
+    rbk_heads_k<<<g, 256, 0, st>>>(kin, n, heads);
+    int e = exclusive_scan_u32(heads, heads, n, total, t, st);
+    if (e) return e;
+    rbk_keys_k<<<g, 256, 0, st>>>(kin, n, heads, kout);
+    e = fill_u32(vout, 0u, n, st);
+    if (e) return e;
+    int g2 = grid_for((n + 15) / 16, 256);
+    rbk_values_k<<<g2 > 8192 ? 8192 : g2, 256, 0, st>>>(kin, vin, n, heads, vout);
+    rbk_nruns_k<<<1, 1, 0, st>>>(total, nruns);
+    return (int)hipGetLastError();
+}
+
+}  // namespace prim

@@ -1,0 +1,65 @@
+"""Build of the HIP library (gfx950) in-tree: every csrc/*.hip compiled with hipcc into one shared library,
+ngram_amd/_lib/libngram_amd.so (the reference builds its kernels with nvcc into a .so per source digest:
+old_records/gpu_val_stats.py:102-130; here hipcc --offload-arch=gfx950)."""
+
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = ROOT / "csrc"
+OUT_DIR = PKG / "_lib"
+LIB_NAME = "libngram_amd.so"
+ARCH = os.environ.get("NGRAM_AMD_ARCH", "gfx950")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+FLAGS = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
+         # compiler-formed packed fp32 ops are kept off (they have given wrong results on these machines)
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def lib_path() -> Path:
+    return OUT_DIR / LIB_NAME
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC.glob("*.hip"))
+
+
+def build(verbose: bool = False, extra: list[str] | None = None) -> Path:
+    """Compile every source (in parallel) and link the library; returns its path. Raises on a compiler error."""
+    OUT_DIR.mkdir(parents=True, exist_ok=True)
+    obj_dir = OUT_DIR / "obj"
+    obj_dir.mkdir(exist_ok=True)
+    extra = extra or []
+
+    def compile_one(src: Path) -> Path:
+        obj = obj_dir / (src.stem + ".o")
+        cmd = [HIPCC, *FLAGS, *extra, "-I", str(CSRC), "-c", str(src), "-o", str(obj)]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"hipcc failed on {src.name}:\n{r.stderr}")
+        if verbose and r.stderr.strip():
+            print(r.stderr, file=sys.stderr)
+        return obj
+
+    srcs = sources()
+    with ThreadPoolExecutor(max(1, min(len(srcs), os.cpu_count() or 4))) as ex:
+        objs = list(ex.map(compile_one, srcs))
+    out = lib_path()
+    tmp = out.with_suffix(f".so.tmp{os.getpid()}")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stderr}")
+    tmp.replace(out)
+    return out
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,347 @@
+// CPU oracle of the n-gram hint path: TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and bench.py's
+// cpu_baseline leg load this library, as the checker (or as the CPU baseline that is timed beside the GPU); nothing in
+// the product calls it.
+//
+// A restatement, in plain C++ (std::thread, std::sort), of the reference's CPU algorithms for this path:
+//   * oracle_query_counts: exact_match/src/kgram.rs count_with/scan/Contexts (:308-399, :406-489, :505-565), the
+//     query-filtered counting: the distinct valid query k-contexts are indexed, the corpus is streamed, every hit is
+//     verified token by token and (context id, next token) collected, then sorted per context; plus
+//     old_records.val_count_features (src/retrieval_blog_post/old_records.py:236-294) for tot/dist/cnt with the
+//     top-`cnt_top` rule, and the context's `ntop` most frequent next tokens (count descending, then token
+//     ascending: kgram.rs:357-368).
+//   * oracle_table_counts: exact_match/src/count_table.rs build_level/runs/query_counts (:491-631, :726-777,
+//     :291-331), the corpus-wide table: every context of the corpus counted (here with exact 128-bit packed keys,
+//     k <= 8), then queried.
+//   * oracle_longest_match: the largest k <= cap whose query k-context is valid and occurred (kgram.rs kgram_stats'
+//     "matched" at each k, :252-277, with the monotonicity of kgram.rs:12-15), and that context's most frequent next
+//     token and its count.
+// Definitions (kgram.rs:7-9): a query position i's k-context is x[i-k+1..=i], valid iff avail[i] >= k; a corpus
+// occurrence is any k tokens within one shard followed by a token of the same shard; tot = occurrences (u32; the
+// caller checks >= 2^32), dist = distinct next tokens (saturated at 65535), cnt = the target's count if its rank
+// (count descending, token ascending) is below cnt_top, else 0; all 0 where the context is invalid or never occurred.
+#include <algorithm>
+#include <atomic>
+#include <cstdint>
+#include <cstring>
+#include <thread>
+#include <unordered_map>
+#include <vector>
+
+typedef uint64_t u64;
+typedef uint32_t u32;
+typedef uint16_t u16;
+typedef int64_t i64;
+typedef int32_t i32;
+typedef unsigned __int128 u128;
+
+static u64 mix(u64 h) {
+    h ^= h >> 30;
+    h *= 0xbf58476d1ce4e5b9ull;
+    h ^= h >> 27;
+    h *= 0x94d049bb133111ebull;
+    return h ^ (h >> 31);
+}
+
+static u64 hash_tokens(const u16* t, int k) {
+    u64 h = 0;
+    for (int j = 0; j < k; ++j) h = h * 0x9e3779b185ebca87ull + (u64)t[j] + 1;
+    return mix(h) | 1;
+}
+
+template <class F>
+static void parallel_for(i64 n, int threads, F f) {
+    if (threads <= 1 || n < 2) {
+        f(0, n, 0);
+        return;
+    }
+    std::vector<std::thread> ts;
+    for (int t = 0; t < threads; ++t) {
+        i64 a = n * t / threads, b = n * (t + 1) / threads;
+        ts.emplace_back([=, &f] { f(a, b, t); });
+    }
+    for (auto& th : ts) th.join();
+}
+
+// The distinct valid query k-contexts (kgram.rs Contexts::new): an open-addressing table from a 64-bit hash to the
+// ids of the contexts with that hash (a hash shared by different contexts keeps them apart: every lookup compares
+// tokens, so the index is exact whatever the hash).
+struct Contexts {
+    int k;
+    std::vector<u32> key_of;  // per position: id or UINT32_MAX
+    std::vector<u32> reps;    // per id: a position
+    std::vector<u64> slot_hash;
+    std::vector<u32> slot_id;
+    u64 mask;
+    const u16* x;
+
+    void build(const u16* x_, const i32* avail, i64 n, int k_) {
+        x = x_;
+        k = k_;
+        key_of.assign(n, UINT32_MAX);
+        reps.clear();
+        u64 cap = 1024;
+        while (cap < 2 * (u64)n + 2) cap <<= 1;
+        slot_hash.assign(cap, 0);
+        slot_id.assign(cap, 0);
+        mask = cap - 1;
+        for (i64 i = 0; i < n; ++i) {
+            if (avail[i] < k) continue;
+            const u16* c = x + i + 1 - k;
+            u64 h = hash_tokens(c, k);
+            u64 s = h & mask;
+            while (true) {
+                if (slot_hash[s] == 0) {
+                    slot_hash[s] = h;
+                    slot_id[s] = (u32)reps.size();
+                    key_of[i] = (u32)reps.size();
+                    reps.push_back((u32)i);
+                    break;
+                }
+                if (slot_hash[s] == h) {
+                    u32 id = slot_id[s];
+                    const u16* r = x + reps[id] + 1 - k;
+                    if (memcmp(r, c, 2 * (size_t)k) == 0) {
+                        key_of[i] = id;
+                        break;
+                    }
+                }
+                s = (s + 1) & mask;
+            }
+        }
+    }
+
+    // The id of the context c (k tokens), or UINT32_MAX.
+    u32 find(const u16* c) const {
+        u64 h = hash_tokens(c, k);
+        u64 s = h & mask;
+        while (true) {
+            if (slot_hash[s] == 0) return UINT32_MAX;
+            if (slot_hash[s] == h) {
+                u32 id = slot_id[s];
+                if (memcmp(x + reps[id] + 1 - k, c, 2 * (size_t)k) == 0) return id;
+            }
+            s = (s + 1) & mask;
+        }
+    }
+};
+
+// One context's counted pairs: the next tokens and counts, ranked (count descending, token ascending).
+struct Ranked {
+    u64 total = 0;
+    std::vector<std::pair<u32, u16>> ranked;  // (count, token)
+};
+
+static void rank_pairs(std::vector<std::pair<u32, u16>>& v) {
+    std::sort(v.begin(), v.end(), [](const std::pair<u32, u16>& a, const std::pair<u32, u16>& b) {
+        if (a.first != b.first) return a.first > b.first;
+        return a.second < b.second;
+    });
+}
+
+// Per-position outputs from per-context ranked lists.
+static void position_outputs(const std::vector<u32>& ctx, const std::vector<Ranked>& per, const u16* tgt, i64 n,
+                             int cnt_top, int ntop, u32* tot, u16* dist, u32* cnt, u16* top_tok, u32* top_cnt) {
+    for (i64 i = 0; i < n; ++i) {
+        if (tot) tot[i] = 0;
+        if (dist) dist[i] = 0;
+        if (cnt) cnt[i] = 0;
+        for (int r = 0; r < ntop; ++r) {
+            top_tok[i * ntop + r] = 0;
+            top_cnt[i * ntop + r] = 0;
+        }
+        u32 id = ctx[i];
+        if (id == UINT32_MAX) continue;
+        const Ranked& c = per[id];
+        if (c.total == 0) continue;
+        if (tot) tot[i] = (u32)c.total;
+        if (dist) dist[i] = (u16)std::min<size_t>(c.ranked.size(), 65535);
+        if (cnt) {
+            size_t lim = std::min<size_t>(c.ranked.size(), (size_t)cnt_top);
+            for (size_t r = 0; r < lim; ++r)
+                if (c.ranked[r].second == tgt[i]) {
+                    cnt[i] = c.ranked[r].first;
+                    break;
+                }
+        }
+        for (int r = 0; r < ntop && r < (int)c.ranked.size(); ++r) {
+            top_tok[i * ntop + r] = c.ranked[r].second;
+            top_cnt[i * ntop + r] = c.ranked[r].first;
+        }
+    }
+}
+
+// Group sorted (id << 16 | next) entries into per-context ranked lists.
+static void group_entries(std::vector<u64>& all, std::vector<Ranked>& per) {
+    std::sort(all.begin(), all.end());
+    size_t i = 0;
+    while (i < all.size()) {
+        u64 id = all[i] >> 16;
+        Ranked& c = per[id];
+        size_t j = i;
+        while (j < all.size() && (all[j] >> 16) == id) {
+            u64 v = all[j];
+            size_t a = j;
+            while (j < all.size() && all[j] == v) ++j;
+            c.ranked.push_back({(u32)(j - a), (u16)(v & 0xFFFF)});
+        }
+        c.total = j - i;
+        rank_pairs(c.ranked);
+        i = j;
+    }
+}
+
+extern "C" {
+
+// Query-filtered counts of level k (see the file comment). `tok` holds the shards concatenated, shard s being
+// [bounds[s], bounds[s + 1]); `x`, `tgt`, `avail` are the query positions' inputs, targets and segment lengths.
+// Outputs per position (any may be null except top arrays when ntop > 0). `hits`, if not null, receives per corpus
+// position whose k-context matched a query context (the next token's index, as kgram.rs's bitmap) a 1 byte.
+// Returns the number of matched corpus occurrences, or -1 on bad arguments.
+i64 oracle_query_counts(const u16* tok, const i64* bounds, int nshards, const u16* x, const u16* tgt,
+                        const i32* avail, i64 n, int k, int cnt_top, int ntop, u32* tot, u16* dist, u32* cnt,
+                        u16* top_tok, u32* top_cnt, uint8_t* hits, int threads) {
+    if (k < 1 || n < 0 || nshards < 1 || ntop < 0) return -1;
+    Contexts ctx;
+    ctx.build(x, avail, n, k);
+    std::vector<std::pair<i64, i64>> pieces;
+    const i64 PIECE = 1 << 20;
+    for (int s = 0; s < nshards; ++s)
+        for (i64 p = bounds[s] + k; p < bounds[s + 1]; p += PIECE) pieces.push_back({p, std::min(bounds[s + 1], p + PIECE)});
+    if (threads < 1) threads = 1;
+    std::vector<std::vector<u64>> acc(threads);
+    std::atomic<size_t> next_piece(0);
+    std::vector<std::thread> ts;
+    for (int t = 0; t < threads; ++t)
+        ts.emplace_back([&, t] {
+            while (true) {
+                size_t q = next_piece++;
+                if (q >= pieces.size()) break;
+                for (i64 p = pieces[q].first; p < pieces[q].second; ++p) {
+                    u32 id = ctx.find(tok + p - k);
+                    if (id == UINT32_MAX) continue;
+                    if (hits) hits[p] = 1;
+                    acc[t].push_back(((u64)id << 16) | tok[p]);
+                }
+            }
+        });
+    for (auto& th : ts) th.join();
+    std::vector<u64> all;
+    size_t total = 0;
+    for (auto& a : acc) total += a.size();
+    all.reserve(total);
+    for (auto& a : acc) all.insert(all.end(), a.begin(), a.end());
+    std::vector<Ranked> per(ctx.reps.size());
+    group_entries(all, per);
+    position_outputs(ctx.key_of, per, tgt, n, cnt_top, ntop, tot, dist, cnt, top_tok, top_cnt);
+    return (i64)total;
+}
+
+// Corpus-wide counts of level k <= 8 (count_table.rs): every context of every shard is counted, keyed by its tokens
+// packed 16 bits each (exact), then each query position looks its context up. Same outputs as oracle_query_counts.
+// Also returns (through the pointers, if not null) the level's distinct contexts and distinct (context, next) pairs.
+i64 oracle_table_counts(const u16* tok, const i64* bounds, int nshards, const u16* x, const u16* tgt,
+                        const i32* avail, i64 n, int k, int cnt_top, int ntop, u32* tot, u16* dist, u32* cnt,
+                        u16* top_tok, u32* top_cnt, i64* n_contexts, i64* n_pairs, int threads) {
+    if (k < 1 || k > 8 || n < 0 || nshards < 1) return -1;  // a context packs into 128 bits up to k = 8
+    struct E {
+        u128 ctx;
+        u16 next;
+        bool operator<(const E& o) const { return ctx != o.ctx ? ctx < o.ctx : next < o.next; }
+    };
+    auto pack = [k](const u16* c) {
+        u128 v = 0;
+        for (int j = 0; j < k; ++j) v = (v << 16) | c[j];
+        return v;
+    };
+    std::vector<E> all;
+    i64 events = 0;
+    for (int s = 0; s < nshards; ++s) events += std::max<i64>(0, bounds[s + 1] - bounds[s] - k);
+    all.resize(events);
+    i64 at = 0;
+    for (int s = 0; s < nshards; ++s)
+        for (i64 p = bounds[s] + k; p < bounds[s + 1]; ++p) all[at++] = E{pack(tok + p - k), tok[p]};
+    if (threads > 1) {
+        // sort in parallel pieces, then merge
+        std::vector<i64> cut;
+        for (int t = 0; t <= threads; ++t) cut.push_back(events * t / threads);
+        parallel_for(threads, threads, [&](i64 a, i64 b, int) {
+            for (i64 t = a; t < b; ++t) std::sort(all.begin() + cut[t], all.begin() + cut[t + 1]);
+        });
+        for (int w = 1; w < threads; w *= 2)
+            for (int t = 0; t + w < threads; t += 2 * w)
+                std::inplace_merge(all.begin() + cut[t], all.begin() + cut[t + w],
+                                   all.begin() + cut[std::min(threads, t + 2 * w)]);
+    } else {
+        std::sort(all.begin(), all.end());
+    }
+    // contexts: sorted packed keys with their ranked pairs
+    std::vector<u128> keys;
+    std::vector<Ranked> per;
+    i64 pairs = 0;
+    size_t i = 0;
+    while (i < all.size()) {
+        u128 c = all[i].ctx;
+        Ranked r;
+        size_t j = i;
+        while (j < all.size() && all[j].ctx == c) {
+            u16 t = all[j].next;
+            size_t a = j;
+            while (j < all.size() && all[j].ctx == c && all[j].next == t) ++j;
+            r.ranked.push_back({(u32)(j - a), t});
+        }
+        r.total = j - i;
+        pairs += r.ranked.size();
+        rank_pairs(r.ranked);
+        keys.push_back(c);
+        per.push_back(std::move(r));
+        i = j;
+    }
+    if (n_contexts) *n_contexts = (i64)keys.size();
+    if (n_pairs) *n_pairs = pairs;
+    std::vector<u32> ctx(n, UINT32_MAX);
+    for (i64 q = 0; q < n; ++q) {
+        if (avail[q] < k) continue;
+        u128 c = pack(x + q + 1 - k);
+        auto it = std::lower_bound(keys.begin(), keys.end(), c);
+        if (it != keys.end() && *it == c) ctx[q] = (u32)(it - keys.begin());
+    }
+    position_outputs(ctx, per, tgt, n, cnt_top, ntop, tot, dist, cnt, top_tok, top_cnt);
+    return events;
+}
+
+// Longest match: per query position, the largest k <= cap whose k-context is valid and occurred in the corpus (0 if
+// none), that context's most frequent next token (count descending, token ascending) and its count.
+int oracle_longest_match(const u16* tok, const i64* bounds, int nshards, const u16* x, const i32* avail, i64 n,
+                         int cap, u32* length, u16* next, u32* count, int threads) {
+    if (cap < 1 || n < 0) return -1;
+    std::vector<u32> tt(n), dd(1);
+    std::vector<u16> t1(n);
+    std::vector<u32> c1(n);
+    std::vector<i32> av(avail, avail + n);
+    for (i64 i = 0; i < n; ++i) {
+        length[i] = 0;
+        next[i] = 0;
+        count[i] = 0;
+    }
+    std::vector<u16> dummy_tgt(n, 0);
+    for (int k = 1; k <= cap; ++k) {
+        // positions that matched at k - 1 (all valid at k = 1) keep their avail; the others drop out
+        bool any = false;
+        for (i64 i = 0; i < n; ++i) {
+            if (k > 1 && length[i] != (u32)(k - 1)) av[i] = 0;
+            if (av[i] >= k) any = true;
+        }
+        if (!any) break;
+        oracle_query_counts(tok, bounds, nshards, x, dummy_tgt.data(), av.data(), n, k, 1, 1, tt.data(), nullptr,
+                            nullptr, t1.data(), c1.data(), nullptr, threads);
+        for (i64 i = 0; i < n; ++i)
+            if (av[i] >= k && tt[i] > 0) {
+                length[i] = k;
+                next[i] = t1[i];
+                count[i] = c1[i];
+            }
+    }
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,159 @@
+"""CPU: the oracle pinned against brute force, closed forms and hand-computed cases (no GPU)."""
+
+import numpy as np
+import pytest
+
+import oracle as O
+from ngram_amd import data
+
+
+def _case(rng, vocab, n_shards, max_len, nq):
+    shards = [rng.integers(0, vocab, size=int(rng.integers(0, max_len))).astype(np.uint16) for _ in range(n_shards)]
+    for s in shards:
+        s[rng.random(len(s)) < 0.08] = O.BOS
+    train = np.concatenate(shards) if shards else np.zeros(0, np.uint16)
+    bounds = np.cumsum([0] + [len(s) for s in shards]).astype(np.int64)
+    q = rng.integers(0, vocab, size=nq).astype(np.uint16)
+    q[rng.random(nq) < 0.08] = O.BOS
+    return shards, train, bounds, q[:-1], q[1:]
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_restatements_match_brute_force(seed):
+    rng = np.random.default_rng(seed)
+    shards, train, bounds, x, tgt = _case(rng, int(rng.integers(2, 7)), int(rng.integers(1, 4)), 80, 50)
+    avail = O.segments(x)
+    for k in (1, 2, 3, 4, 5):
+        b = O.brute_counts(shards, x, tgt, avail, k, cnt_top=2, ntop=3)
+        a = O.query_counts(train, bounds, x, tgt, avail, k, cnt_top=2, ntop=3)
+        c = O.table_counts(train, bounds, x, tgt, avail, k, cnt_top=2, ntop=3)
+        for name in ("tot", "dist", "cnt", "top_tok", "top_cnt"):
+            assert np.array_equal(a[name], b[name]), (k, name)
+            assert np.array_equal(c[name], b[name]), (k, name, "table")
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_longest_match_matches_brute_force(seed):
+    rng = np.random.default_rng(100 + seed)
+    shards, train, bounds, x, tgt = _case(rng, 3, 2, 60, 40)
+    avail = O.segments(x)
+    got = O.longest_match(train, bounds, x, avail, 7)
+    want = O.brute_longest(shards, x, avail, 7)
+    for g, w in zip(got, want):
+        assert np.array_equal(g, w)
+
+
+def test_constant_stream_closed_form():
+    # one shard of n copies of token 7: every k-context (7,)*k occurs n - k times, always followed by 7
+    n = 1000
+    train = np.full(n, 7, np.uint16)
+    bounds = np.array([0, n], np.int64)
+    x = np.full(50, 7, np.uint16)
+    tgt = np.full(50, 7, np.uint16)
+    avail = O.segments(x)
+    for k in (1, 2, 3, 6):
+        o = O.query_counts(train, bounds, x, tgt, avail, k, ntop=2)
+        valid = avail >= k
+        assert np.all(o["tot"][valid] == n - k) and np.all(o["tot"][~valid] == 0)
+        assert np.all(o["dist"][valid] == 1) and np.all(o["cnt"][valid] == n - k)
+        assert np.all(o["top_tok"][valid, 0] == 7) and np.all(o["top_cnt"][valid, 1] == 0)
+
+
+def test_shards_do_not_join():
+    # "a b" ends shard 0, "c" starts shard 1: the context (a, b) has no next token, (b,) is never followed by c
+    a, b, c = 1, 2, 3
+    shards = [np.array([a, b], np.uint16), np.array([c, a, b, c], np.uint16)]
+    train = np.concatenate(shards)
+    bounds = np.array([0, 2, 6], np.int64)
+    x = np.array([a, b], np.uint16)
+    tgt = np.array([b, c], np.uint16)
+    avail = O.segments(x)
+    o1 = O.query_counts(train, bounds, x, tgt, avail, 1)
+    assert o1["tot"][1] == 1 and o1["cnt"][1] == 1  # (b,) -> c once (shard 1 only)
+    o2 = O.query_counts(train, bounds, x, tgt, avail, 2)
+    assert o2["tot"][1] == 1 and o2["cnt"][1] == 1  # (a, b) -> c once
+
+
+def test_ranking_and_top_rule():
+    # context (5,) followed by 9 x3, 4 x2, 8 x2, 6 x1: ranks 9, 4, 8, 6 (ties by token ascending)
+    seq = [5, 9, 5, 9, 5, 9, 5, 4, 5, 4, 5, 8, 5, 8, 5, 6]
+    train = np.array(seq, np.uint16)
+    bounds = np.array([0, len(seq)], np.int64)
+    x = np.array([5, 5, 5, 5], np.uint16)
+    tgt = np.array([9, 4, 8, 6], np.uint16)
+    avail = np.array([1, 1, 1, 1], np.int32)
+    o = O.query_counts(train, bounds, x, tgt, avail, 1, cnt_top=2, ntop=4)
+    assert list(o["top_tok"][0]) == [9, 4, 8, 6] and list(o["top_cnt"][0]) == [3, 2, 2, 1]
+    assert list(o["cnt"]) == [3, 2, 0, 0]  # 8 and 6 rank 3rd and 4th: outside cnt_top = 2
+    assert o["dist"][0] == 4 and o["tot"][0] == 8
+
+
+def test_segments_rule():
+    x = np.array([3, 4, O.BOS, 5, 6, O.BOS], np.uint16)
+    assert list(O.segments(x)) == [1, 2, 1, 2, 3, 1]
+    assert list(data.segments(x)) == [1, 2, 1, 2, 3, 1]
+    assert list(data.segments(x, breaks=[4])) == [1, 2, 1, 2, 1, 1]
+
+
+def test_weights_round_half_even():
+    c = np.array([[1, 1, 0, 0, 0, 0, 0, 0], [1, 3, 0, 0, 0, 0, 0, 0], [0] * 8], np.uint32)
+    w = O.weights(c)
+    assert list(w[0, :2]) == [32768, 32768]  # 32767.5 rounds to even
+    assert list(w[1, :2]) == [16384, 49151]  # 16383.75, 49151.25
+    assert not w[2].any()
+
+
+def test_deepest_rows_cell_by_hand():
+    # one position, variant (2, 3): level 3 matched with total 10 and top count 9 -> bucket 1 (LEVELS.index(3)),
+    # count bin #{2,3,5,9 <= 10} = 4, purity 0.9 -> #{.3,.5,.7,.85 <= .9} = 4: ((1+1)*7+4)*6+4 = 112
+    per = {}
+    for k, tot, top in ((2, 30, 5), (3, 10, 9)):
+        o = O._alloc(1, 8)
+        o["tot"][0] = tot
+        o["top_cnt"][0, :2] = [top, tot - top]
+        o["top_tok"][0, :2] = [11, 12]
+        per[k] = o
+    cell, tokens, w = O.deepest_rows(per, (2, 3))
+    assert cell[0] == 112 and list(tokens[0, :2]) == [11, 12]
+    assert list(w[0, :2]) == [round(9 / 10 * 65535), round(1 / 10 * 65535)]
+
+
+def test_features_bins():
+    tot = np.array([[0, 1, 2, 3, 1024, 2 ** 31]], np.int64)  # one level
+    counts = np.zeros((3, 1, tot.shape[1]), np.int32)
+    counts[0, 0] = (tot[0] & 0xFFFFFFFF).astype(np.uint32).view(np.int32)
+    counts[1, 0] = [0, 1, 1, 2, 5, 1]
+    counts[2, 0] = [0, 1, 3, 1, 0, 7]
+    t, d, c, b, s = O.features(counts)
+    assert list(b[:, 0]) == [0, 0, 1, 1, 10, 24]  # floor(log2), clamped to 24
+    assert list(s[:, 0]) == [25, 26, 26, 25, 25, 26]  # (dist == 1) + 25 * L
+    assert list(c[:, 0]) == [0, 1, 2, 1, 0, 7]  # min(cnt, tot)
+
+
+def test_generator_deterministic_and_shaped():
+    a = data.make_corpus("c1", train_tokens=100_000, query_tokens=5_001, shard_tokens=40_000)
+    b = data.make_corpus("c1", train_tokens=100_000, query_tokens=5_001, shard_tokens=40_000)
+    assert np.array_equal(a.train, b.train) and np.array_equal(a.query, b.query)
+    assert len(a.train) == 100_000 and len(a.query) == 5_001
+    assert list(a.bounds) == [0, 40_000, 80_000, 100_000]
+    assert a.train.max() <= data.BOS
+    eos = np.flatnonzero(a.train == data.BOS)
+    assert len(eos) > 50  # documents of mean 1025 tokens
+    gaps = np.diff(eos)
+    assert 500 < gaps.mean() < 2000
+    assert len(a.train_plan.copies) > 0 and len(a.query_plan.copies) > 0
+    # a copied span of the query stream is a span of the training stream
+    dst, src, n = a.query_plan.copies[0]
+    assert np.array_equal(a.query[dst : dst + n], a.train[src : src + n])
+
+
+def test_shard_file_roundtrip(tmp_path):
+    t = np.arange(100, dtype=np.uint16)
+    p = tmp_path / "s.bin"
+    data.write_shard(p, t)
+    assert data.shard_tokens(p) == 100
+    assert np.array_equal(data.read_shard(p), t)
+    bad = tmp_path / "bad.bin"
+    bad.write_bytes(b"\0" * 1024)
+    with pytest.raises(ValueError):
+        data.shard_tokens(bad)

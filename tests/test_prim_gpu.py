@@ -1,0 +1,64 @@
+"""GPU: our device-wide primitives behind the CUB-style ABI calls (sort_pairs, inclusive_max, reduce_by_key) against
+numpy (np.argsort kind="stable", np.maximum.accumulate, run sums) -- pinning the reference's CUB boundary."""
+
+import numpy as np
+import pytest
+import torch
+
+from ngram_amd.lib import i32
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@pytest.mark.parametrize("n,b0,b1,dups", [(1, 0, 64, 0), (4095, 0, 64, 0), (4097, 0, 64, 16), (100_003, 16, 40, 1000),
+                                           (300_000, 0, 64, 50), (70_000, 8, 8, 0), (65_536, 0, 12, 3)])
+def test_sort_pairs_is_a_stable_radix_sort(lib, n, b0, b1, dups):
+    rng = np.random.default_rng(n + b0)
+    keys = rng.integers(0, 2 ** 63, size=n, dtype=np.int64).astype(np.uint64) * np.uint64(2) + \
+        rng.integers(0, 2, size=n).astype(np.uint64)
+    if dups:
+        keys = rng.choice(keys[:dups], size=n)
+    vals = np.arange(n, dtype=np.uint32)
+    kin, vin = _t(keys.view(np.int64)), _t(vals.view(np.int32))
+    kout, vout = torch.empty_like(kin), torch.empty_like(vin)
+    lib.cub("sort_pairs", kin, kout, vin, vout, n, i32(b0), i32(b1))
+    width = b1 - b0
+    sk = (keys >> np.uint64(b0)) & np.uint64((1 << width) - 1) if width < 64 else keys
+    order = np.argsort(sk, kind="stable")
+    assert np.array_equal(vout.cpu().numpy().view(np.uint32), vals[order])
+    assert np.array_equal(kout.cpu().numpy().view(np.uint64), keys[order])
+
+
+def test_sort_pairs_empty_and_temp_query(lib):
+    kin = torch.zeros(0, dtype=torch.int64, device="cuda")
+    lib.cub("sort_pairs", kin, torch.empty_like(kin), None, None, 0, i32(0), i32(64))
+
+
+@pytest.mark.parametrize("n", [1, 4096, 4097, 1_000_000, 17_000_000])
+def test_inclusive_max(lib, n):
+    rng = np.random.default_rng(n)
+    a = rng.integers(-2 ** 40, 2 ** 40, size=n, dtype=np.int64)
+    out = torch.empty(n, dtype=torch.int64, device="cuda")
+    lib.cub("inclusive_max", _t(a), out, n)
+    assert np.array_equal(out.cpu().numpy(), np.maximum.accumulate(a))
+
+
+@pytest.mark.parametrize("n,runs", [(1, 1), (1000, 7), (100_000, 99_000), (2_000_000, 50), (3_000_000, 2_000_000)])
+def test_reduce_by_key(lib, n, runs):
+    rng = np.random.default_rng(n)
+    keys = np.sort(rng.integers(0, runs, size=n)).astype(np.uint64) * np.uint64(977)
+    vals = rng.integers(0, 2 ** 31, size=n, dtype=np.int64).astype(np.uint32)
+    kout = torch.empty(n, dtype=torch.int64, device="cuda")
+    vout = torch.empty(n, dtype=torch.int32, device="cuda")
+    nr = torch.zeros(1, dtype=torch.int64, device="cuda")
+    lib.cub("reduce_by_key", _t(keys.view(np.int64)), kout, _t(vals.view(np.int32)), vout, nr, n)
+    u, first = np.unique(keys, return_index=True)
+    sums = np.add.reduceat(vals.astype(np.uint64), first) & np.uint64(0xFFFFFFFF)
+    m = int(nr.item())
+    assert m == len(u)
+    assert np.array_equal(kout[:m].cpu().numpy().view(np.uint64), u)
+    assert np.array_equal(vout[:m].cpu().numpy().view(np.uint32), sums.astype(np.uint32))
