@@ -1,0 +1,168 @@
+"""Benchmark of the n-gram hint path on one MI355X: the one-GPU share of the record's GPU counts build at BASELINE's
+third configuration (c3): a 1B-token seeded synthetic corpus (10 shards of 100M tokens, Zipf(1.1) over permuted ids,
+geometric documents of mean 1024 ending with BOS 50256, 5% of documents with a copied span of 32-1024 tokens), exact
+counts of the query contexts for n = 2..8, then for 16M query positions each level's tot / dist / cnt, the top-4 next
+tokens with counts, and hit/miss. One step = one whole count build + query over the resident corpus and queries.
+
+Prints one JSON line: value = corpus tokens counted per second (T x steps / timed seconds), plus query positions/s,
+the roofline of the dominant kernel (scan_level: algorithmic bytes 2 per corpus position + 16 per hit, over its
+average launch duration timed with HIP events on the launch stream) and the CPU baseline (the oracle's C++ restatement
+of kgram.rs's query-filtered counting, timed on this host on a bounded sample)."""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "n-gram-hinted-lm_amd"))
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--config", default="c3", choices=("c3",))
+    ap.add_argument("--train-tokens", type=int, default=0, help="override the corpus size (smaller runs)")
+    ap.add_argument("--query-tokens", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-tokens", type=int, default=100_000_000, help="CPU baseline: corpus prefix")
+    ap.add_argument("--cpu-queries", type=int, default=2_000_000, help="CPU baseline: query positions")
+    return ap.parse_args()
+
+
+def log(*a) -> None:
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_workload(cfg_name: str, train_tokens: int, query_tokens: int):
+    """The configuration's corpus laid out in shards on the GPU and its query stream (both generated on the GPU)."""
+    import numpy as np
+    import torch
+
+    from ngram_amd import data
+    from ngram_amd.gpu_val_stats import layout
+    from ngram_amd.lib import Lib
+
+    cfg = data.CONFIGS[cfg_name]
+    t0 = time.time()
+    zipf, tp, qp = data.make_plans(cfg, train_tokens or None, query_tokens or None)
+    log(f"plans: {time.time() - t0:.1f}s ({len(tp.eos)} documents, {len(tp.copies)} + {len(qp.copies)} copies)")
+    lib = Lib()
+    flat = data.realize_gpu(tp, zipf, lib)
+    q = data.realize_gpu(qp, zipf, lib, source=flat)
+    bounds = data.train_bounds(tp.n, cfg.shard_tokens)
+    sizes = [int(b - a) for a, b in zip(bounds[:-1], bounds[1:])]
+    starts, L = layout(sizes)
+    tok = torch.full((L,), -1, dtype=torch.int16, device=flat.device)
+    for (a, b), st in zip(zip(bounds[:-1], bounds[1:]), starts):
+        tok[st : st + (b - a)].copy_(flat[a:b])
+    torch.cuda.synchronize()
+    log(f"workload on the GPU: {time.time() - t0:.1f}s")
+    return cfg, flat, bounds, tok, sizes, starts, q, np
+
+
+def cpu_baseline(flat, bounds, q, levels, n_tokens: int, n_queries: int) -> dict:
+    """The oracle's query-filtered counting (C++ restatement of kgram.rs, one thread per core) over a bounded sample:
+    the corpus' first n_tokens tokens and the first n_queries query positions, every level."""
+    import numpy as np
+
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as O
+
+    train = flat[:n_tokens].cpu().numpy().view(np.uint16)
+    b = bounds[bounds < n_tokens].tolist() + [n_tokens]
+    qq = q[: n_queries + 1].cpu().numpy().view(np.uint16)
+    x, tgt = qq[:-1], qq[1:]
+    avail = O.segments(x)
+    cores = O.threads()
+    t0 = time.perf_counter()
+    for k in levels:
+        O.query_counts(train, np.array(b, np.int64), x, tgt, avail, k, ntop=4, nthreads=cores)
+    dt = time.perf_counter() - t0
+    return {"value": n_tokens / dt, "unit": "corpus tokens/s", "cores": cores, "kind": "port",
+            "sample": f"first {n_tokens} corpus tokens x {n_queries} query positions, levels {list(levels)}, "
+                      f"tot/dist/cnt + top-4; {dt:.1f} s", "seconds": dt}
+
+
+def main() -> None:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs one GPU only (got --gpus {args.gpus}): this build has no multi-GPU path", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from ngram_amd.counts import CountBuild, device_queries
+
+    torch.cuda.set_device(0)
+    cfg, flat, bounds, tok, sizes, starts, q, np = make_workload(args.config, args.train_tokens, args.query_tokens)
+    T = sum(sizes)
+    cb = CountBuild.from_device(tok, sizes, starts, levels=cfg.levels, level_shards={}, topk=cfg.topk)
+    x, tgt, avail = device_queries(q, cb.lib)
+    N = x.numel()
+    # one untimed build with hit counts: the events E of the roofline (deterministic, the same every step)
+    cb.counts(x, tgt, avail, stats=True)
+    info = {k: dict(v) for k, v in cb.info.items()}
+    log("levels:", json.dumps(info))
+    for _ in range(max(0, args.warmup - 1)):
+        cb.counts(x, tgt, avail)
+    torch.cuda.synchronize()
+    cb.timing.clear()
+    t0 = time.perf_counter()
+    scan_ms, scan_launches = 0.0, 0
+    for step in range(args.steps):
+        out = cb.counts(x, tgt, avail)
+        log(f"step {step}: {sum(cb.timing.values()) / (step + 1):.4f} s/step so far")
+        # the dominant kernel's launches of this step (HIP events on the stream they ran on)
+        for name, k, i, n, e0, e1 in cb.kernel_events:
+            scan_ms += e0.elapsed_time(e1)
+            scan_launches += 1
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    hits = sum(v["hits"] for v in info.values())
+    positions = sum(n for _, _, _, n, _, _ in cb.kernel_events)  # per step
+    scan_bytes = args.steps * (2.0 * positions + 16.0 * hits)
+    achieved = scan_bytes / (scan_ms / 1e3) / 1e9 if scan_ms > 0 else 0.0
+    ms = dt / args.steps * 1e3
+    mask_hits = int((out[0] != 0).sum().item())
+    res = {
+        "metric": "corpus tokens counted/s + hint queries/s on 1 GPU; % of HBM peak GB/s",
+        "value": T * args.steps / dt,
+        "unit": "corpus tokens/s",
+        "query_positions_per_s": N * args.steps / dt,
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u16/u64 (integer)",
+        "data": "synthetic (seeded Zipf(1.1) documents with copied spans, generated on the GPU)",
+        "config": {"workload": f"{cfg.name}: count build of {T} corpus tokens ({len(sizes)} shards) for n="
+                               f"{list(cfg.levels)} + top-{cfg.topk}/count/hit queries at {N} positions",
+                   "corpus_tokens": T, "query_positions": N, "levels": list(cfg.levels), "topk": cfg.topk},
+        "roofline": {"bound": "hbm", "kernel": "scan_level (scan_dense_k/scan_sparse_k)",
+                     "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "launches_per_step": scan_launches // max(1, args.steps),
+                     "avg_launch_ms": scan_ms / max(1, scan_launches),
+                     "algorithmic_bytes_per_step": 2.0 * positions + 16.0 * hits,
+                     "scan_share_of_step": scan_ms / args.steps / ms},
+        "events_per_step": hits, "position_level_hits": mask_hits,
+        "phases_s": {k: v / args.steps for k, v in cb.timing.items()},
+        "levels": info,
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        nt = min(args.cpu_tokens, int(flat.numel()))
+        nq = min(args.cpu_queries, N)
+        cpu = cpu_baseline(flat, bounds, q, cfg.levels, nt, nq)
+        log(f"cpu baseline: {cpu['seconds']:.1f}s")
+        res["cpu_baseline"] = cpu
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -79,6 +79,23 @@ int pos_outputs(const int* ctx_of, ng_i64 N, ng_i64 lo, ng_i64 hi, const uint16_
 /* one variant's hint rows: cell, 8 tokens, 8 weights packed in int32[N, 9] (gpu_val_stats.cu:696-699) */
 int variant_rows(ng_i64 N, const int* mask, int nv, const ng_i64* desc, int* rows, void* stream);
 
+/* ------------------------------------------------------------------------------------------------------------
+ * Synthetic streams (no counterpart in the reference, whose data are FineWeb shards): the seeded generator of the
+ * benchmark configurations, byte-identical to ngram_amd/data.py's numpy generator. A body token of stream `key` at
+ * position p: h = splitmix64_finalizer(key + (p + 1) * 0x9E3779B97F4A7C15), u = (h >> 11) * 2^-53,
+ * token = perm[min(#{cdf[j] <= u}, ncdf - 1)].
+ * ------------------------------------------------------------------------------------------------------------ */
+
+/* out[i] = the draw of position start + i of stream key, i in [0, n) */
+int gen_tokens(uint16_t* out, ng_i64 start, ng_i64 n, ng_u64 key, const double* cdf, int ncdf, const uint16_t* perm,
+               void* stream);
+/* out[pos[i]] = value (the documents' BOS) */
+int gen_set(uint16_t* out, const ng_i64* pos, ng_i64 m, int value, void* stream);
+/* per copy (dst, src, length) of copies[m][3]: out[dst + j] = src_tokens[src + j], or the draw of position src + j of
+ * stream key when src_tokens is NULL */
+int gen_copies(uint16_t* out, const ng_i64* copies, ng_i64 m, const uint16_t* src_tokens, ng_u64 key,
+               const double* cdf, int ncdf, const uint16_t* perm, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

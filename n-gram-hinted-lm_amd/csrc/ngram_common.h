@@ -71,17 +71,27 @@ __host__ __device__ __forceinline__ u64 ctx_key_rt(const u16* e, int k) {
 // start, whatever k.
 template <int K>
 __device__ __forceinline__ u64 ctx_key_stop(const u16* e, int k) {
-    const int kk = K > 0 ? K : k;
     u64 h = 0, bp = 1;
+    if constexpr (K > 0) {
 #pragma unroll
-    for (int j = 1; j <= (K > 0 ? K : MAXK); ++j) {
-        if (K == 0 && j > kk) break;
-        const u32 t = e[-j];
-        if (t == SENT) return EMPTY;
-        if (kk <= 4) h |= (u64)t << (16 * (j - 1));
-        else {
-            h += tok_code(t) * bp;
-            bp *= POLY_BASE;
+        for (int j = 1; j <= K; ++j) {
+            const u32 t = e[-j];
+            if (t == SENT) return EMPTY;
+            if (K <= 4) h |= (u64)t << (16 * (j - 1));
+            else {
+                h += tok_code(t) * bp;
+                bp *= POLY_BASE;
+            }
+        }
+    } else {
+        for (int j = 1; j <= k; ++j) {
+            const u32 t = e[-j];
+            if (t == SENT) return EMPTY;
+            if (k <= 4) h |= (u64)t << (16 * (j - 1));
+            else {
+                h += tok_code(t) * bp;
+                bp *= POLY_BASE;
+            }
         }
     }
     return key_finish(h);

@@ -208,7 +208,7 @@ __global__ void __launch_bounds__(BLOCK) rs_scatter_k(const u64* __restrict__ ki
                                                       int nbits, const u32* __restrict__ hist, i64 ntiles) {
     __shared__ u32 cnt[ITEMS][NWAVES][256];
     __shared__ u32 base_s[256];
-    const int t = threadIdx.x, lane = lane_id(), w = t / WAVE;
+    const int t = threadIdx.x, w = t / WAVE;
     const u32 mask = (1u << nbits) - 1u;
     base_s[t] = hist[(i64)t * ntiles + blockIdx.x];
     for (int i = t; i < ITEMS * NWAVES * 256; i += BLOCK) (&cnt[0][0][0])[i] = 0;

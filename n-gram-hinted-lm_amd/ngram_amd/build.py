@@ -1,6 +1,8 @@
-"""Build of the HIP library (gfx950) in-tree: every csrc/*.hip compiled with hipcc into one shared library,
-ngram_amd/_lib/libngram_amd.so (the reference builds its kernels with nvcc into a .so per source digest:
-old_records/gpu_val_stats.py:102-130; here hipcc --offload-arch=gfx950)."""
+"""Build of the HIP libraries (gfx950) in-tree: the csrc/ sources compiled with hipcc and linked into
+ngram_amd/_lib/libngram_amd.so (the gpu_val_stats flavour of the C ABI plus the engine's own entry points) and
+ngram_amd/_lib/libngram_amd_record.so (the record flavour: the same names with the record's signatures). The reference
+builds its kernels with nvcc into a .so per source digest (old_records/gpu_val_stats.py:102-130,
+record_367_gpu_counts/track_1_short/counts/build.py:58-71); here hipcc --offload-arch=gfx950."""
 
 from __future__ import annotations
 
@@ -15,6 +17,12 @@ ROOT = PKG.parent
 CSRC = ROOT / "csrc"
 OUT_DIR = PKG / "_lib"
 LIB_NAME = "libngram_amd.so"
+RECORD_LIB_NAME = "libngram_amd_record.so"
+# each library's sources (relative to csrc/); an object shared by both is compiled once
+LIBS = {
+    LIB_NAME: ["prim.hip", "common_abi.hip", "gvs_abi.hip", "gen.hip"],
+    RECORD_LIB_NAME: ["prim.hip", "common_abi.hip", "record/record_abi.hip"],
+}
 ARCH = os.environ.get("NGRAM_AMD_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -23,12 +31,12 @@ FLAGS = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
-def lib_path() -> Path:
-    return OUT_DIR / LIB_NAME
+def lib_path(name: str = LIB_NAME) -> Path:
+    return OUT_DIR / name
 
 
 def sources() -> list[Path]:
-    return sorted(CSRC.glob("*.hip"))
+    return sorted({CSRC / s for srcs in LIBS.values() for s in srcs})
 
 
 def build(verbose: bool = False, extra: list[str] | None = None) -> Path:
@@ -39,7 +47,7 @@ def build(verbose: bool = False, extra: list[str] | None = None) -> Path:
     extra = extra or []
 
     def compile_one(src: Path) -> Path:
-        obj = obj_dir / (src.stem + ".o")
+        obj = obj_dir / (str(src.relative_to(CSRC).with_suffix("")).replace("/", "_") + ".o")
         cmd = [HIPCC, *FLAGS, *extra, "-I", str(CSRC), "-c", str(src), "-o", str(obj)]
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode != 0:
@@ -50,15 +58,17 @@ def build(verbose: bool = False, extra: list[str] | None = None) -> Path:
 
     srcs = sources()
     with ThreadPoolExecutor(max(1, min(len(srcs), os.cpu_count() or 4))) as ex:
-        objs = list(ex.map(compile_one, srcs))
-    out = lib_path()
-    tmp = out.with_suffix(f".so.tmp{os.getpid()}")
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stderr}")
-    tmp.replace(out)
-    return out
+        objs = dict(zip(srcs, ex.map(compile_one, srcs)))
+    for name, lib_srcs in LIBS.items():
+        out = lib_path(name)
+        tmp = out.with_suffix(f".so.tmp{os.getpid()}")
+        cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+               *[str(objs[CSRC / s]) for s in lib_srcs]]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"link of {name} failed:\n{r.stderr}")
+        tmp.replace(out)
+    return lib_path()
 
 
 if __name__ == "__main__":

@@ -1,0 +1,365 @@
+"""Exact n-gram counts of the query contexts over a training corpus on one MI355X: the mirror of the record's GPU
+counts build, record_367_gpu_counts/track_1_short/counts/build.py (`CountBuild` :161-403, `QueryIndex` :99-141,
+`queries` :144-158), on the record flavour of our C ABI (libngram_amd_record.so: 25-bit context ids, 41-bit pair keys).
+
+Per level k the query index (the distinct valid query k-contexts in a canonical linear-probing table, a
+representative position each); every shard scanned through its levels as one pass (a level probes only the
+positions whose context matched at the previous level: a hit bitmap per level); then per level the table's pairs
+compacted, sorted by (context, next token), and per query position tot (uint32 bits), dist (at most 65535) and cnt
+(the target's count), plus the record's validation rows from ROW_LEVELS (cells, and the 8 most frequent next tokens with
+their 15-bit weights). Beyond the record: `levels`, `level_shards` and `topk` are parameters (the one-GPU share of
+the record at BASELINE's third configuration counts k = 2..8 over every shard and returns each level's top 4 next
+tokens per position), and a level whose pair table overflows reruns with twice the slots (the record raises).
+
+One GPU: `world` must be 1 (the owner exchange is then the identity, as the reference's world == 1 path); the
+all-to-all and all-reduce of a multi-GPU build are not part of this build."""
+
+from __future__ import annotations
+
+import time
+
+import numpy as np
+import torch
+
+from .build import RECORD_LIB_NAME, lib_path
+from .data import BOS, HEADER_BYTES, shard_tokens
+from .gpu_val_stats import PAIRS as GVS_PAIRS
+from .gpu_val_stats import ValIndex, layout
+from .lib import Lib, i32, u64
+
+GAP = 32
+LEVELS = (2, 3, 4, 5, 6, 10, 20)
+LEVEL_SHARDS = {2: 103, 3: 370, 4: 370, 5: 370}
+PAIRS = {2: (82.17e6, 0.620), 3: (62.30e6, 0.667), 4: (26.39e6, 0.694), 5: (8.99e6, 0.706), 6: (3.17e6, 0.705),
+         10: (0.223e6, 0.604), 20: (0.102e6, 0.581)}
+SAFETY = 1.6
+LOAD = 0.7
+MAX_IDS = (1 << 25) - 4096
+ROW_LEVELS = (6, 10, 20)
+ROW_K = 8
+ROW_COUNTS = (2, 3, 5, 9, 17, 33)
+ROW_PURITIES = (0.3, 0.5, 0.7, 0.85, 0.95)
+
+
+def record_lib() -> Lib:
+    """The record flavour of the library (its scan_level, part_*, rank_scatter and pos_outputs signatures)."""
+    return Lib(lib_path(RECORD_LIB_NAME))
+
+
+def pairs_fit(k: int) -> tuple[float, float]:
+    """The reference's fit of distinct (context, next) pairs in n tokens for level k (u, beta): the record's PAIRS,
+    gpu_val_stats' for levels it lacks, the deepest fit beyond (levels in between take the shallower neighbour)."""
+    if k in PAIRS:
+        return PAIRS[k]
+    if k in GVS_PAIRS:
+        return GVS_PAIRS[k]
+    known = sorted(set(PAIRS) | set(GVS_PAIRS))
+    below = [j for j in known if j < k]
+    j = below[-1] if below else known[0]
+    return PAIRS.get(j, GVS_PAIRS.get(j))
+
+
+def queries(val: np.ndarray, blocks: list[np.ndarray], device, lib: Lib):
+    """x, tgt, avail of the validation stream `val` (inputs, then one more token) and then each fit block (likewise),
+    each block a segment of its own; a BOS starts a segment (build.py:144-158)."""
+    parts = [np.asarray(val, np.uint16), *[np.asarray(b, np.uint16) for b in blocks]]
+    x = np.concatenate([p[:-1] for p in parts])
+    tgt = np.concatenate([p[1:] for p in parts])
+    first = np.zeros(len(x), dtype=bool)
+    first[np.cumsum([0, *[len(p) - 1 for p in parts[:-1]]])] = True
+    x_t = torch.from_numpy(x.view(np.int16)).to(device)
+    idx = torch.arange(len(x), device=device)
+    start = (x_t.to(torch.int32) & 0xFFFF) == BOS
+    start |= torch.from_numpy(first).to(device)
+    seg = torch.empty_like(idx)
+    lib.cub("inclusive_max", torch.where(start, idx, torch.zeros_like(idx)), seg, len(x))
+    return x_t, torch.from_numpy(tgt.view(np.int16)).to(device), (idx - seg + 1).to(torch.int32)
+
+
+def device_queries(q: torch.Tensor, lib: Lib):
+    """x, tgt, avail of a query stream already on the GPU (int16 tensor: the inputs, then the last target)."""
+    x = q[:-1]
+    n = x.numel()
+    idx = torch.arange(n, device=q.device)
+    start = (x.to(torch.int32) & 0xFFFF) == BOS
+    start[:1] = True
+    seg = torch.empty_like(idx)
+    lib.cub("inclusive_max", torch.where(start, idx, torch.zeros_like(idx)), seg, n)
+    return x, q[1:], (idx - seg + 1).to(torch.int32)
+
+
+class CountBuild:
+    """The record's count build on one GPU. `shards`: shard file paths (read into pinned host memory, then copied by
+    start_load/pace) or uint16 arrays. `levels` ascending; `level_shards`: per level, how many leading shards it
+    counts; `topk`: per level the first topk ranked next tokens/counts of each position's context (self.top_tok /
+    self.top_cnt [len(levels), N, topk]) when > 0. Construct with `from_device` for tokens already in GPU memory."""
+
+    def __init__(self, shards: list, rank: int = 0, world: int = 1, levels=LEVELS, level_shards=None, topk: int = 0,
+                 lib: Lib | None = None):
+        if world != 1 or rank != 0:
+            raise ValueError("this build runs on one GPU: world must be 1 (the owner exchange is out of scope)")
+        self.rank, self.world = rank, world
+        self.min_cap = 1 << 20
+        self.levels = tuple(levels)
+        if not self.levels or list(self.levels) != sorted(set(self.levels)) or self.levels[0] < 1:
+            raise ValueError(f"levels must ascend from >= 1: {self.levels}")
+        ls = LEVEL_SHARDS if level_shards is None else level_shards
+        self.topk = topk
+        self.lib = lib or record_lib()
+        self.timing: dict[str, float] = {}
+        self.info: dict = {}
+        self.events: list = []
+        self.host: list = []
+        arrays = []
+        for s in shards:
+            if isinstance(s, (str, bytes)) or hasattr(s, "__fspath__"):
+                n = shard_tokens(s)
+                a = torch.empty(n, dtype=torch.int16, pin_memory=True)
+                a.numpy()[:] = np.fromfile(s, dtype="<i2", count=n, offset=HEADER_BYTES)
+                arrays.append(a)
+            else:
+                arrays.append(torch.from_numpy(np.ascontiguousarray(s, dtype=np.uint16).view(np.int16)))
+        self.sizes = [int(a.numel()) for a in arrays]
+        self.level_shards = {k: min(len(arrays), ls.get(k, len(arrays))) for k in self.levels}
+        self.starts, self.L = layout(self.sizes)
+        self.tok = torch.full((self.L,), -1, dtype=torch.int16, device="cuda")
+        self.host = arrays
+        self.stream = torch.cuda.Stream()  # the copies' stream (default priority)
+        self.pending: list = []
+
+    @classmethod
+    def from_device(cls, tok: torch.Tensor, sizes: list[int], starts: list[int], levels=LEVELS, level_shards=None,
+                    topk: int = 0, lib: Lib | None = None) -> "CountBuild":
+        """A build over shards already laid out in GPU memory (`tok` int16 [L] with SENT gaps, layout()'s starts)."""
+        self = cls.__new__(cls)
+        self.rank, self.world = 0, 1
+        self.min_cap = 1 << 20
+        self.levels = tuple(levels)
+        ls = LEVEL_SHARDS if level_shards is None else level_shards
+        self.topk = topk
+        self.lib = lib or record_lib()
+        self.timing, self.info, self.events, self.host, self.pending = {}, {}, [], [], []
+        self.sizes, self.starts, self.L = list(sizes), list(starts), int(tok.numel())
+        self.level_shards = {k: min(len(sizes), ls.get(k, len(sizes))) for k in self.levels}
+        self.tok = tok
+        self.stream = torch.cuda.current_stream()
+        ev = torch.cuda.Event()
+        ev.record()
+        self.events = [ev] * len(sizes)
+        return self
+
+    def caps(self) -> dict[int, int]:
+        """Each level's pair table slots: the estimated pairs of the level's tokens, at LOAD (build.py:205-212)."""
+        caps = {}
+        for k in self.levels:
+            n_k = sum(self.sizes[: self.level_shards[k]])
+            u, beta = pairs_fit(k)
+            caps[k] = max(self.min_cap, int(min(SAFETY * u * (max(n_k, 1) / 4e8) ** beta, n_k) / LOAD))
+        return caps
+
+    def prepare(self) -> None:
+        """Before the clock: the caching allocator's blocks for the pair tables (no collectives on one GPU)."""
+        warm = torch.empty(int(1.33 * sum(9 * cap for cap in self.caps().values())), dtype=torch.uint8, device="cuda")
+        del warm
+        torch.cuda.synchronize()
+
+    def start_load(self, steps: int = 1) -> None:
+        """The host shards' copies split into `steps` equal shares, the first enqueued (build.py:231-243)."""
+        self.pending = []
+        for a, st in zip(self.host, self.starts):
+            n = a.numel()
+            for lo in range(0, n, 4 << 20):
+                hi = min(n, lo + (4 << 20))
+                self.pending.append((st + lo, a, lo, hi, hi == n))
+        self.pending.reverse()
+        self.per_step = -(-len(self.pending) // max(1, steps))
+        self.events = []
+        self.pace()
+
+    def pace(self) -> None:
+        """The next share of the copies (build.py:245-255)."""
+        with torch.cuda.stream(self.stream):
+            for _ in range(min(self.per_step, len(self.pending))):
+                at, a, lo, hi, last = self.pending.pop()
+                self.tok[at : at + hi - lo].copy_(a[lo:hi], non_blocking=True)
+                if last:
+                    ev = torch.cuda.Event()
+                    ev.record(self.stream)
+                    self.events.append(ev)
+
+    def _scan(self, index, tables, bms, shard_ids, levels) -> None:
+        lib, grid = self.lib, self.grid
+        for i in shard_ids:
+            st, n = self.starts[i], self.sizes[i]
+            torch.cuda.current_stream().wait_event(self.events[i])
+            scanned = [k for k in self.levels if i < self.level_shards[k]]
+            for li, k in enumerate(scanned):
+                if k not in levels:
+                    continue
+                vi = index[k]
+                pk, pc, cap, flags = tables[k]
+                # gated by this shard's previous scanned level; a shard that level skipped is probed whole
+                bm_in = None if li == 0 else bms[scanned[li - 1]][st // 32 :]
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                lib("scan_level", self.tok[st:], (n + 31) // 32 * 32, i32(k), bm_in, bms[k][st // 32 :], vi.table,
+                    u64(vi.cap), vi.rep, self.x, pk, pc, u64(cap), flags, i32(grid), i32(int(li > 0 and k > 5)))
+                e1.record()
+                self.kernel_events.append(("scan_level", k, i, (n + 31) // 32 * 32, e0, e1))
+
+    def counts(self, x: torch.Tensor, tgt: torch.Tensor, avail: torch.Tensor, stats: bool = False) -> torch.Tensor:
+        """int32 [3, len(levels), len(x)]: per query position and level its context's total occurrences (uint32 bits),
+        distinct next tokens (at most 65535) and its target's count; also the rows (batch_rows) and, with topk, the
+        per-level top next tokens (build.py:261-388). `stats`: also count each level's corpus hits (self.info)."""
+        self.stats = stats
+        lib, timing, info = self.lib, self.timing, self.info
+        dev = self.tok.device
+
+        def lap(name: str) -> None:
+            torch.cuda.current_stream().synchronize()
+            now = time.perf_counter()
+            timing[name] = timing.get(name, 0.0) + now - lap.t
+            lap.t = now
+
+        lap.t = time.perf_counter()
+        self.kernel_events = []
+        self.x = x
+        N = x.numel()
+        index = {k: ValIndex(lib, x, avail, k, max_ids=MAX_IDS) for k in self.levels}
+        lap("index")
+        self.grid = torch.cuda.get_device_properties(dev).multi_processor_count * 32
+        caps = self.caps()
+        tables = {}
+        for k in self.levels:
+            tables[k] = self._table(caps[k], dev)
+        nwords = self.L // 32
+        bms = {k: torch.zeros(nwords, dtype=torch.int32, device=dev) for k in self.levels}
+        self._scan(index, tables, bms, range(len(self.sizes)), set(self.levels))
+        reruns = {k: 0 for k in self.levels}
+        while True:
+            fl = {k: tables[k][3].cpu().tolist() for k in self.levels}
+            over = [k for k in self.levels if fl[k][0]]
+            if not over:
+                break
+            for k in over:  # the bitmaps are whole: only the overflowed level reruns, with twice the slots
+                reruns[k] += 1
+                tables[k] = self._table(2 * tables[k][2], dev)
+            self._scan(index, tables, bms, range(len(self.sizes)), set(over))
+        lap("scan")
+        hits = {k: int(self._popcount(bms[k]).item()) for k in self.levels} if self.stats else {}
+        del bms
+        out = torch.zeros((3, len(self.levels), N), dtype=torch.int32, device=dev)
+        rows = all(k in self.levels for k in ROW_LEVELS)
+        if rows:
+            row_entries = torch.zeros((len(ROW_LEVELS), N, ROW_K), dtype=torch.int32, device=dev)
+            row_top = torch.zeros((len(ROW_LEVELS), N), dtype=torch.int32, device=dev)
+        if self.topk:
+            self.top_tok = torch.zeros((len(self.levels), N, self.topk), dtype=torch.int16, device=dev)
+            self.top_cnt = torch.zeros((len(self.levels), N, self.topk), dtype=torch.int32, device=dev)
+        for li, k in enumerate(self.levels):
+            vi = index.pop(k)
+            pk, pc, cap, _ = tables.pop(k)
+            lo, hi = 0, vi.ids
+            bounds = torch.tensor([lo, hi], dtype=torch.int64, device=dev)
+            cnt = torch.zeros(1, dtype=torch.int64, device=dev)
+            lib("part_count", pk, u64(cap), bounds, i32(1), cnt)
+            U = int(cnt.item())
+            cursor = torch.zeros(1, dtype=torch.int64, device=dev)
+            send_k = torch.empty(U, dtype=torch.int64, device=dev)
+            send_c = torch.empty(U, dtype=torch.int32, device=dev)
+            lib("part_scatter", pk, pc, u64(cap), bounds, i32(1), cursor, send_k, send_c)
+            del pk, pc
+            n_own = hi - lo
+            ctx_bits = max(1, (max(n_own, 2) - 1).bit_length())
+            uk, agg = torch.empty_like(send_k), torch.empty_like(send_c)
+            if U:  # one GPU: the table's keys are already distinct (no reduce_by_key)
+                lib.cub("sort_pairs", send_k, uk, send_c, agg, U, i32(0), i32(16 + ctx_bits))
+            del send_k, send_c
+            start = torch.zeros(n_own, dtype=torch.int64, device=dev)
+            end = torch.zeros(n_own, dtype=torch.int64, device=dev)
+            lib("seg_bounds", uk, U, start, end)
+            tot = torch.empty(n_own, dtype=torch.int64, device=dev)
+            lib("ctx_tot", start, end, agg, n_own, tot)
+            lib("pos_outputs", vi.ctx_of, N, lo, hi, tgt, uk, agg, start, end, tot, out[0, li], out[1, li], out[2, li])
+            want = max(self.topk, ROW_K if (rows and k in ROW_LEVELS) else 0)
+            if want:
+                key2 = torch.empty(U, dtype=torch.int64, device=dev)
+                val2 = torch.empty(U, dtype=torch.int32, device=dev)
+                lib("rank_keys", uk, agg, U, key2, val2)
+                k2s, sv = torch.empty_like(key2), torch.empty_like(val2)
+                if U:
+                    lib.cub("sort_pairs", key2, k2s, val2, sv, U, i32(0), i32(32 + ctx_bits))
+                del key2, val2, k2s
+                top_tok = torch.zeros(n_own * want, dtype=torch.int16, device=dev)
+                top_cnt = torch.zeros(n_own * want, dtype=torch.int32, device=dev)
+                lib("rank_scatter", sv, U, uk, agg, start, top_tok, top_cnt, i32(want))
+                del sv
+                if self.topk:
+                    lib("pos_topk", vi.ctx_of, N, lo, hi, top_tok, top_cnt, i32(want), i32(self.topk),
+                        self.top_tok[li], self.top_cnt[li])
+                if rows and k in ROW_LEVELS:
+                    ri = ROW_LEVELS.index(k)
+                    ctx = vi.ctx_of.long()
+                    at = ((ctx >= lo) & (ctx < hi)).nonzero().squeeze(1)
+                    c = ctx[at] - lo
+                    tt = top_tok.view(-1, want)[c, :ROW_K].to(torch.int32) & 0xFFFF
+                    tc = top_cnt.view(-1, want)[c, :ROW_K].to(torch.int64)
+                    top = tc[:, :1].clamp_min(1)
+                    w = torch.where(top > 32767, (tc * 32767 + top - 1) // top, tc)
+                    row_entries[ri, at] = torch.where(tc > 0, tt | (w.to(torch.int32) << 16), 0)
+                    row_top[ri, at] = tc[:, 0].clamp_max((1 << 31) - 1).to(torch.int32)
+                    del ctx, at, c, tt, tc, top, w
+                del top_tok, top_cnt
+            if n_own and int(tot.max().item()) >= 1 << 32:
+                raise RuntimeError(f"k={k}: a total does not fit uint32")
+            info[k] = dict(contexts=vi.n, ids=vi.ids, pairs=U, cap=cap, hits=hits.get(k), reruns=reruns[k])
+            del uk, agg, start, end, tot, vi
+        lap("outputs")
+        if rows:
+            self._rows(out, row_entries, row_top, N)
+            lap("rows")
+        self.out = out
+        return out
+
+    def _table(self, cap: int, dev):
+        return (torch.full((cap,), -1, dtype=torch.int64, device=dev),
+                torch.zeros((cap + 3) // 4, dtype=torch.int32, device=dev), cap,
+                torch.zeros(2, dtype=torch.int32, device=dev))
+
+    def _popcount(self, bm: torch.Tensor) -> torch.Tensor:
+        # bit count of an int32 bitmap, in torch (a byte table lookup)
+        table = torch.tensor([bin(i).count("1") for i in range(256)], dtype=torch.int64, device=bm.device)
+        b = bm.view(torch.uint8).long()
+        return table[b].sum()
+
+    def _rows(self, out, row_entries, row_top, N) -> None:
+        """Per position its cell (0: no match at ROW_LEVELS[0]) and the ROW_K candidates of its deepest matched level
+        (build.py:376-387)."""
+        dev = out.device
+        tot = out[0, [self.levels.index(k) for k in ROW_LEVELS]].to(torch.int64) & 0xFFFFFFFF
+        depth = ((tot > 0).to(torch.int64) * torch.arange(1, len(ROW_LEVELS) + 1, device=dev)[:, None]).amax(0) - 1
+        sel = depth.clamp_min(0)
+        pos = torch.arange(N, device=dev)
+        total = tot[sel, pos].double()
+        share = row_top[sel, pos].double() / total.clamp_min(1)
+        count_bin = sum((total >= e).to(torch.int64) for e in ROW_COUNTS)
+        purity = sum((share >= e).to(torch.int64) for e in ROW_PURITIES)
+        cell = (((1 + depth) * (len(ROW_COUNTS) + 1) + count_bin) * (len(ROW_PURITIES) + 1) + purity) * (depth >= 0)
+        self.row_cells = cell.to(torch.int32)
+        self.row_entries = torch.where((depth >= 0)[:, None], row_entries[sel, pos], 0)
+
+    def batch_rows(self, at: int, n: int, capacity: int) -> torch.Tensor:
+        """The record's rows of the n query positions from `at`: their cells, then `capacity` entries (position,
+        token | count << 16), padded with (i % n, 0) (build.py:390-403)."""
+        cell, e = self.row_cells[at : at + n], self.row_entries[at : at + n]
+        pos, k = (e != 0).nonzero(as_tuple=True)
+        m = pos.numel()
+        if m > capacity:
+            raise AssertionError(f"{m} candidates overflow the rows' {capacity} entries")
+        rows = torch.zeros(n + 2 * capacity, dtype=torch.int32, device=e.device)
+        rows[:n] = cell
+        ent = rows[n:].view(-1, 2)
+        ent[:, 0] = torch.arange(capacity, device=e.device, dtype=torch.int32) % n
+        ent[:m, 0] = pos.to(torch.int32)
+        ent[:m, 1] = e[pos, k]
+        return rows

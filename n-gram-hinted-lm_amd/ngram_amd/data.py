@@ -12,7 +12,7 @@ source stream (the training corpus, for held-out query streams).
 Every body token is a pure function of (stream key, absolute position): a counter-based draw (SplitMix64's finalizer
 over key + (position + 1) * 2^64/phi, Steele, Lea & Flood 2014), a 53-bit uniform, and the first Zipf CDF entry above
 it. The plan (document lengths, copies) is drawn on the host with numpy's PCG64. So the GPU generator
-(`gen_zipf` in the HIP library) and this module's numpy generator produce the same bytes."""
+(`gen_tokens`, `gen_set`, `gen_copies` in the HIP library) and this module's numpy generator produce the same bytes."""
 
 from __future__ import annotations
 
@@ -218,6 +218,34 @@ def realize(plan: Plan, zipf: Zipf, source_tokens: np.ndarray | None = None) -> 
     src = source_tokens if plan.external else pure
     for dst, s, length in plan.copies:
         out[dst : dst + length] = src[s : s + length]
+    return out
+
+
+def realize_gpu(plan: Plan, zipf: Zipf, lib, source=None, out=None):
+    """The stream's tokens generated on the GPU by the library's gen_tokens / gen_set / gen_copies (the same bytes as
+    `realize`): a torch int16 tensor (uint16 bits) of plan.n tokens, or written into `out`. `source`: the source
+    stream's tokens on the GPU (int16 tensor), needed when the plan's copies are external."""
+    import torch
+
+    from .lib import i32, u64
+
+    if plan.external and source is None:
+        raise ValueError("the plan copies from a source stream: pass its tokens")
+    dev = torch.device("cuda", torch.cuda.current_device())
+    if out is None:
+        out = torch.empty(plan.n, dtype=torch.int16, device=dev)
+    elif out.numel() != plan.n or out.dtype != torch.int16:
+        raise ValueError("out must be int16 of plan.n tokens")
+    cdf = torch.from_numpy(zipf.cdf).to(dev)
+    perm = torch.from_numpy(zipf.perm.view(np.int16)).to(dev)
+    lib("gen_tokens", out, 0, plan.n, u64(plan.key), cdf, i32(len(zipf.cdf)), perm)
+    eos = torch.from_numpy(plan.eos).to(dev)
+    lib("gen_set", out, eos, len(plan.eos), i32(BOS))
+    if len(plan.copies):
+        cp = torch.from_numpy(np.ascontiguousarray(plan.copies)).to(dev)
+        lib("gen_copies", out, cp, len(plan.copies), source if plan.external else None, u64(plan.key), cdf,
+            i32(len(zipf.cdf)), perm)
+    torch.cuda.current_stream().synchronize()
     return out
 
 

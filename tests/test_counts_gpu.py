@@ -1,0 +1,100 @@
+"""GPU: the record flavour (libngram_amd_record.so through CountBuild, the mirror of
+record_367_gpu_counts/track_1_short/counts/build.py) bit-exact against the CPU oracle on seeded synthetic streams:
+per level tot / dist / cnt (no TOP rule), the top-4 next tokens, the record's rows and batch_rows."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from ngram_amd import counts as C
+from ngram_amd import data
+
+pytestmark = pytest.mark.gpu
+
+LEVELS = (2, 3, 4, 5, 6, 10, 20)
+
+
+@pytest.fixture(scope="module")
+def corpus():
+    return data.make_corpus("c3", train_tokens=700_000, query_tokens=50_001, shard_tokens=250_000)
+
+
+def _reference(corpus, levels, level_shards, ntop=8):
+    x, tgt = corpus.query[:-1], corpus.query[1:]
+    avail = O.segments(x)
+    ref = {}
+    nshards = len(corpus.bounds) - 1
+    for k in levels:
+        m = min(nshards, level_shards.get(k, nshards))
+        b = corpus.bounds[: m + 1]
+        ref[k] = O.query_counts(corpus.train[: b[-1]], b, x, tgt, avail, k, cnt_top=1 << 30, ntop=ntop)
+    return ref
+
+
+@pytest.mark.parametrize("level_shards", [{}, {2: 1, 3: 2}])
+def test_counts_match_oracle(corpus, level_shards):
+    lib = C.record_lib()
+    cb = C.CountBuild(corpus.shards(), levels=LEVELS, level_shards=level_shards, topk=4)
+    cb.start_load(3)
+    cb.pace()
+    cb.pace()
+    x, tgt, avail = C.queries(corpus.query, [], "cuda", lib)
+    out = cb.counts(x, tgt, avail, stats=True).cpu().numpy()
+    ref = _reference(corpus, LEVELS, level_shards)
+    top_tok = cb.top_tok.cpu().numpy().view(np.uint16)
+    top_cnt = cb.top_cnt.cpu().numpy().view(np.uint32)
+    for li, k in enumerate(LEVELS):
+        o = ref[k]
+        assert np.array_equal(out[0, li].view(np.uint32), o["tot"]), f"tot k={k}"
+        assert np.array_equal(out[1, li].astype(np.uint16), o["dist"]), f"dist k={k}"
+        assert np.array_equal(out[2, li].view(np.uint32), o["cnt"]), f"cnt k={k}"
+        assert np.array_equal(top_tok[li], o["top_tok"][:, :4]), f"top_tok k={k}"
+        assert np.array_equal(top_cnt[li], o["top_cnt"][:, :4]), f"top_cnt k={k}"
+        assert cb.info[k]["hits"] == o["events"], f"hits k={k}"
+    assert (ref[2]["tot"] > 0).sum() > 1000 and (ref[20]["tot"] > 0).sum() > 10
+    # the record's rows from ROW_LEVELS, and a batch of them
+    ri = [LEVELS.index(k) for k in C.ROW_LEVELS]
+    tot_rows = np.stack([ref[k]["tot"] for k in C.ROW_LEVELS])
+    cells, entries = O.record_rows(tot_rows, np.stack([ref[k]["top_tok"] for k in C.ROW_LEVELS]),
+                                   np.stack([ref[k]["top_cnt"] for k in C.ROW_LEVELS]))
+    assert np.array_equal(cb.row_cells.cpu().numpy(), cells)
+    assert np.array_equal(cb.row_entries.cpu().numpy(), entries)
+    n = 500
+    cap = int((entries[1000 : 1000 + n] != 0).sum()) + 7
+    assert np.array_equal(cb.batch_rows(1000, n, cap).cpu().numpy(), O.batch_rows(cells, entries, 1000, n, cap))
+    del ri
+
+
+def test_overflow_reruns_only_the_level(corpus, monkeypatch):
+    lib = C.record_lib()
+    tok_cb = C.CountBuild(corpus.shards(), levels=(2, 3, 6), topk=2)
+    tok_cb.start_load(1)
+    x, tgt, avail = C.queries(corpus.query, [], "cuda", lib)
+    monkeypatch.setattr(C, "LOAD", 1e9)
+    tok_cb.min_cap = 1024
+    out = tok_cb.counts(x, tgt, avail).cpu().numpy()
+    assert tok_cb.info[2]["reruns"] > 0
+    ref = _reference(corpus, (2, 3, 6), {})
+    for li, k in enumerate((2, 3, 6)):
+        assert np.array_equal(out[0, li].view(np.uint32), ref[k]["tot"]), k
+        assert np.array_equal(out[2, li].view(np.uint32), ref[k]["cnt"]), k
+
+
+def test_device_queries_match_host_queries(corpus):
+    lib = C.record_lib()
+    q = torch.from_numpy(corpus.query.view(np.int16)).cuda()
+    a = C.device_queries(q, lib)
+    b = C.queries(corpus.query, [], "cuda", lib)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+
+
+def test_fit_blocks_start_segments(corpus):
+    lib = C.record_lib()
+    blocks = [corpus.query[:300], corpus.query[300:700]]
+    x, tgt, avail = C.queries(corpus.query[:1001], blocks, "cuda", lib)
+    av = avail.cpu().numpy()
+    assert av[1000] == 1 and av[1000 + 299] == 1
+    xs = np.concatenate([corpus.query[:1000], blocks[0][:-1], blocks[1][:-1]])
+    assert np.array_equal(av, data.segments(xs, breaks=[1000, 1299]))

@@ -1,4 +1,4 @@
-"""CPU: the C-ABI library builds for gfx950, loads, and exports every entry point include/*.h declares (no GPU calls)."""
+"""CPU: the C-ABI libraries build for gfx950, load, and export every entry point include/*.h declares (no GPU calls)."""
 
 import ctypes
 import re
@@ -7,38 +7,46 @@ from pathlib import Path
 import pytest
 
 ROOT = Path(__file__).resolve().parent.parent
+# header -> the library that exports its declarations
+HEADERS = {"ngram_amd.h": "libngram_amd.so", "ngram_amd_record.h": "libngram_amd_record.so"}
 
 
-def declared_symbols() -> list[str]:
-    names = []
-    for h in sorted((ROOT / "include").glob("*.h")):
-        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
-        names += re.findall(r"^\s*(?:int|size_t|void)\s+(\w+)\s*\(", text, flags=re.M)
-    return names
+def declared_symbols(header: str) -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / header).read_text(), flags=re.S)
+    return re.findall(r"^\s*(?:int|size_t|void)\s+(\w+)\s*\(", text, flags=re.M)
 
 
 @pytest.fixture(scope="module")
-def so():
+def libs():
     from ngram_amd import build
 
-    path = build.lib_path()
-    if not path.exists():
+    if not all(build.lib_path(n).exists() for n in HEADERS.values()):
         build.build()
-    return ctypes.CDLL(str(path))
+    return {h: ctypes.CDLL(str(build.lib_path(n))) for h, n in HEADERS.items()}
+
+
+def test_every_header_is_mapped():
+    assert sorted(p.name for p in (ROOT / "include").glob("*.h")) == sorted(HEADERS)
 
 
 def test_header_declares_the_reference_abi():
-    names = set(declared_symbols())
+    gvs = set(declared_symbols("ngram_amd.h"))
     reference = {"val_keys", "val_verify", "val_homes", "scan_level", "subpart_count", "subpart_scatter", "aggregate",
                  "max_pbits", "popcount", "part_count", "part_scatter", "sort_pairs", "inclusive_max",
                  "reduce_by_key", "seg_bounds", "ctx_tot", "rank_keys", "rank_scatter", "pos_outputs",
                  "variant_rows"}
-    assert reference <= names, reference - names
+    assert reference <= gvs, reference - gvs
+    record = set(declared_symbols("ngram_amd_record.h"))
+    reference_rec = {"val_keys", "val_verify", "val_homes", "scan_level", "part_count", "part_scatter", "sort_pairs",
+                     "inclusive_max", "reduce_by_key", "seg_bounds", "ctx_tot", "rank_keys", "rank_scatter",
+                     "pos_outputs"}
+    assert reference_rec <= record, reference_rec - record
 
 
-def test_library_exports_every_declared_symbol(so):
-    missing = [n for n in declared_symbols() if not hasattr(so, n)]
-    assert not missing, missing
+def test_libraries_export_every_declared_symbol(libs):
+    for h, so in libs.items():
+        missing = [n for n in declared_symbols(h) if not hasattr(so, n)]
+        assert not missing, (h, missing)
 
 
 def test_product_does_not_import_the_oracle():
