@@ -22,6 +22,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "n-gram-hinted-lm_amd"))
 
 HBM_PEAK_GBS = 8000.0
+SCAN_KERNELS = ("scan_count", "scan_level", "scan_emit")  # the level scans, whichever counting CountBuild uses
 
 
 def parse() -> argparse.Namespace:
@@ -33,6 +34,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--train-tokens", type=int, default=0, help="override the corpus size (smaller runs)")
     ap.add_argument("--query-tokens", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--mode", default="engine", choices=("engine", "record", "partitioned"), help="CountBuild.mode")
     ap.add_argument("--cpu-tokens", type=int, default=100_000_000, help="CPU baseline: corpus prefix")
     ap.add_argument("--cpu-queries", type=int, default=2_000_000, help="CPU baseline: query positions")
     return ap.parse_args()
@@ -105,6 +107,7 @@ def main() -> None:
     cfg, flat, bounds, tok, sizes, starts, q, np = make_workload(args.config, args.train_tokens, args.query_tokens)
     T = sum(sizes)
     cb = CountBuild.from_device(tok, sizes, starts, levels=cfg.levels, level_shards={}, topk=cfg.topk)
+    cb.mode = args.mode
     x, tgt, avail = device_queries(q, cb.lib)
     N = x.numel()
     # one untimed build with hit counts: the events E of the roofline (deterministic, the same every step)
@@ -116,20 +119,32 @@ def main() -> None:
     torch.cuda.synchronize()
     cb.timing.clear()
     t0 = time.perf_counter()
+    class_ms: dict[str, float] = {}
     scan_ms, scan_launches = 0.0, 0
     for step in range(args.steps):
         out = cb.counts(x, tgt, avail)
         log(f"step {step}: {sum(cb.timing.values()) / (step + 1):.4f} s/step so far")
-        # the dominant kernel's launches of this step (HIP events on the stream they ran on)
+        # the timed launches of this step (HIP events on the stream they ran on)
         for name, k, i, n, e0, e1 in cb.kernel_events:
-            scan_ms += e0.elapsed_time(e1)
-            scan_launches += 1
+            ms = e0.elapsed_time(e1)
+            class_ms[name] = class_ms.get(name, 0.0) + ms
+            if name in SCAN_KERNELS:
+                scan_ms += ms
+                scan_launches += 1
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     hits = sum(v["hits"] for v in info.values())
-    positions = sum(n for _, _, _, n, _, _ in cb.kernel_events)  # per step
-    scan_bytes = args.steps * (2.0 * positions + 16.0 * hits)
+    # algorithmic bytes of the scan launches of one step: 2 per position scanned, and per hit 16 (counted in place:
+    # the 8-byte slot read and written, or the split table's key read + count read and written) or 8 (emitted: the key
+    # written)
+    positions = {k: 0 for k in cfg.levels}
+    for name, k, i, n, _, _ in cb.kernel_events:
+        if name in SCAN_KERNELS:
+            positions[k] += n
+    step_bytes = sum(2.0 * positions[k] + (8.0 if info[k]["pbits"] else 16.0) * info[k]["hits"] for k in cfg.levels)
+    scan_bytes = args.steps * step_bytes
     achieved = scan_bytes / (scan_ms / 1e3) / 1e9 if scan_ms > 0 else 0.0
+    build_bytes = 2.0 * T + 16.0 * hits  # the count build's B_build = 2 T + 16 E
     ms = dt / args.steps * 1e3
     mask_hits = int((out[0] != 0).sum().item())
     res = {
@@ -143,13 +158,16 @@ def main() -> None:
         "config": {"workload": f"{cfg.name}: count build of {T} corpus tokens ({len(sizes)} shards) for n="
                                f"{list(cfg.levels)} + top-{cfg.topk}/count/hit queries at {N} positions",
                    "corpus_tokens": T, "query_positions": N, "levels": list(cfg.levels), "topk": cfg.topk},
-        "roofline": {"bound": "hbm", "kernel": "scan_level (scan_dense_k/scan_sparse_k)",
+        "roofline": {"bound": "hbm", "kernel": f"level scan ({cb.mode}: " + ", ".join(sorted({n for n, *_ in cb.kernel_events if n in SCAN_KERNELS})) + ")",
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None,
                      "launches_per_step": scan_launches // max(1, args.steps),
                      "avg_launch_ms": scan_ms / max(1, scan_launches),
-                     "algorithmic_bytes_per_step": 2.0 * positions + 16.0 * hits,
+                     "algorithmic_bytes_per_step": step_bytes,
                      "scan_share_of_step": scan_ms / args.steps / ms},
+        "build_roofline": {"bytes": build_bytes, "GBps_over_step": build_bytes / (ms / 1e3) / 1e9,
+                           "frac_over_step": build_bytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS},
+        "kernel_ms_per_step": {k: v / args.steps for k, v in class_ms.items()},
         "events_per_step": hits, "position_level_hits": mask_hits,
         "phases_s": {k: v / args.steps for k, v in cb.timing.items()},
         "levels": info,

@@ -54,6 +54,19 @@ int pos_outputs(const int* ctx_of, ng_i64 N, ng_i64 lo, ng_i64 hi, const uint16_
 int pos_topk(const int* ctx_of, ng_i64 N, ng_i64 lo, ng_i64 hi, const uint16_t* top_tok, const uint32_t* top_cnt,
              int top, int kout, uint16_t* out_tok, uint32_t* out_cnt, void* stream);
 
+/* Extensions: the gpu_val_stats library's partitioned counting (gpu_val_stats.cu:268-446) on 41-bit pair keys, for a
+ * host that counts dense levels in L2/MALL-sized sub-tables instead of one table (same semantics as there):
+ * scan_emit = scan_level modes 2 (words = 0) / 3 (words = 1); popcount adds a bitmap's set bits to *out. */
+int scan_emit(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, uint32_t* bm_out, const ng_u64* vt,
+              ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, uint32_t* flags, int grid, int words,
+              ng_u64* emit, ng_u64* emitted, void* stream);
+int max_pbits(void);
+int subpart_count(const ng_u64* keys, ng_i64 n, int pbits, ng_u64* counts, void* stream);
+int subpart_scatter(const ng_u64* keys, ng_i64 n, int pbits, ng_u64* cursor, ng_u64* out, void* stream);
+int aggregate(const ng_u64* keys, ng_i64 n, ng_u64* pk, uint32_t* wraps, ng_u64 sub_cap, int pbits, uint32_t* flags,
+              int grid, void* stream);
+int popcount(const uint32_t* bm, ng_i64 n, ng_u64* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

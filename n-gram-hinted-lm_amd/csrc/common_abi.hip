@@ -57,6 +57,25 @@ extern "C" int val_homes(const u64* keys, i64 n, u64 cap, i64* home, void* strea
     return (int)hipGetLastError();
 }
 
+__device__ __forceinline__ u64 wave_sum_pc(u64 v) {
+#pragma unroll
+    for (int d = WAVE / 2; d > 0; d >>= 1) v += shfl_down_u64(v, d);
+    return v;
+}
+
+__global__ void popcount_k(const u32* __restrict__ bm, i64 n, u64* out) {
+    u64 c = 0;
+    for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n; i += (i64)gridDim.x * blockDim.x) c += __popc(bm[i]);
+    c = wave_sum_pc(c);
+    if (lane_id() == 0 && c) atomicAdd((unsigned long long*)out, (unsigned long long)c);
+}
+
+// set bits of a bitmap of n words added to *out (gpu_val_stats.cu:436-446)
+extern "C" int popcount(const u32* bm, i64 n, u64* out, void* stream) {
+    if (n > 0) popcount_k<<<1024, 256, 0, (hipStream_t)stream>>>(bm, n, out);
+    return (int)hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // CUB-style two-phase calls (gpu_val_stats.cu:529-551): temp == NULL writes *temp_bytes and returns
 // ---------------------------------------------------------------------------------------------------------------

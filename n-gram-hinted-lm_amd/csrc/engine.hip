@@ -1,0 +1,335 @@
+// The engine's own counting and output kernels (no counterpart in the reference's libraries; they replace, inside this
+// build's hosts, the record's one-table scan and its owner side of two radix sorts):
+//
+//   * a split pair table: pair keys (context id << 16 | next token) in u64 slots, their counts in a parallel u32
+//     array. An insert reads the key slot (read-only once written, so repeated hits of a hot pair stay cheap) and adds
+//     to the count with a no-return atomic. The packed slot of the C ABI (key and count in one word) needs a read and
+//     an atomic on the same hot line, which on MI355X runs about three times slower under Zipf-skewed keys.
+//   * owner side without a ranking sort: the table compacted, one radix sort by pair key (contexts grouped, tokens
+//     ascending), then per context its total and top-k (count descending, token ascending) by selection in registers,
+//     and per query position tot / dist / cnt (binary search) / top-k in one gather.
+#include "pairs.h"
+
+namespace {
+
+__device__ __forceinline__ u64 split_home(u64 key, u64 cap) { return __umul64hi(mix64(key), cap); }
+
+// Count `key` in the split table; MAXPROBE probes without a slot set flags[0].
+__device__ __forceinline__ void split_add(u64* keys, u32* cnts, u64 cap, u64 key, u32 add, u32* flags) {
+    u64 s = split_home(key, cap);
+    for (int probe = 0; probe < MAXPROBE; ++probe) {
+        const u64 cur = keys[s];
+        if (cur == key) {
+            atomicAdd(&cnts[s], add);
+            return;
+        }
+        if (cur == EMPTY) {
+            const u64 prev = atomicCAS((unsigned long long*)&keys[s], EMPTY, key);
+            if (prev == EMPTY || prev == key) {
+                atomicAdd(&cnts[s], add);
+                return;
+            }
+        }
+        s = s + 1 == cap ? 0 : s + 1;
+    }
+    atomicOr(&flags[0], 1u);
+}
+
+// Dense levels: a lane per position (a wave per two bitmap words), hits counted in the split table. Once the table
+// has overflowed only the bitmap is still made (the level reruns bigger).
+template <int K>
+__global__ void __launch_bounds__(256) scan_count_dense_k(const u16* __restrict__ tok, i64 L, int k,
+                                                          const u32* __restrict__ bm_in, u32* __restrict__ bm_out,
+                                                          const u64* __restrict__ vt, u64 vcap, const u32* __restrict__ vrep,
+                                                          const u16* __restrict__ x, u64* keys, u32* cnts, u64 cap,
+                                                          u32* flags) {
+    const int lane = lane_id();
+    const i64 nwords = (L + 31) >> 5;
+    const i64 stride = (i64)gridDim.x * blockDim.x;
+    for (i64 base = blockIdx.x * (i64)blockDim.x + (threadIdx.x & ~(WAVE - 1)); base < L; base += stride) {
+        const bool full = *(volatile u32*)&flags[0] != 0u;
+        const i64 p = base + lane;
+        const i64 w = (base >> 5) + (lane >> 5);
+        u32 word = 0xFFFFFFFFu;
+        if (bm_in) word = w < nwords ? bm_in[w] : 0u;
+        u64 key = EMPTY;
+        if (p < L && ((word >> (lane & 31)) & 1u)) key = probe_key<K>(tok, p, k, vt, vcap, vrep, x, flags);
+        const bool hit = key != EMPTY;
+        const u64 b = __ballot(hit);
+        if (lane == 0) bm_out[base >> 5] = (u32)b;
+        if (lane == 32 && w < nwords) bm_out[w] = (u32)(b >> 32);
+        if (hit && !full) split_add(keys, cnts, cap, key, 1u, flags);
+    }
+}
+
+// Sparse levels: a lane per bitmap word, its set bits in turn.
+template <int K>
+__global__ void __launch_bounds__(256) scan_count_sparse_k(const u16* __restrict__ tok, i64 L, int k,
+                                                           const u32* __restrict__ bm_in, u32* __restrict__ bm_out,
+                                                           const u64* __restrict__ vt, u64 vcap, const u32* __restrict__ vrep,
+                                                           const u16* __restrict__ x, u64* keys, u32* cnts, u64 cap,
+                                                           u32* flags) {
+    const i64 nwords = (L + 31) >> 5;
+    for (i64 w = blockIdx.x * (i64)blockDim.x + threadIdx.x; w < nwords; w += (i64)gridDim.x * blockDim.x) {
+        const bool full = *(volatile u32*)&flags[0] != 0u;
+        u32 word = bm_in[w], out = 0;
+        while (word) {
+            const int b = __ffs(word) - 1;
+            word &= word - 1;
+            const i64 p = (w << 5) + b;
+            if (p >= L) continue;
+            const u64 key = probe_key<K>(tok, p, k, vt, vcap, vrep, x, flags);
+            if (key != EMPTY) {
+                out |= 1u << b;
+                if (!full) split_add(keys, cnts, cap, key, 1u, flags);
+            }
+        }
+        bm_out[w] = out;
+    }
+}
+
+// Occupied slots appended to (out_k, out_c): a block-wide count, one global atomic per block and tile.
+#define CP_ITEMS 8
+__global__ void __launch_bounds__(256) table_compact_k(const u64* __restrict__ keys, const u32* __restrict__ cnts, u64 cap,
+                                                       u64* __restrict__ out_k, u32* __restrict__ out_c, u64* counter) {
+    __shared__ u32 wave_n[4];
+    __shared__ u64 block_base;
+    const int lane = lane_id(), w = threadIdx.x / WAVE;
+    const u64 tile = 256ull * CP_ITEMS;
+    for (u64 t0 = blockIdx.x * tile; t0 < cap; t0 += (u64)gridDim.x * tile) {
+        u64 key[CP_ITEMS];
+        u32 mine = 0;
+#pragma unroll
+        for (int j = 0; j < CP_ITEMS; ++j) {
+            const u64 s = t0 + (u64)j * 256 + threadIdx.x;
+            key[j] = s < cap ? keys[s] : EMPTY;
+            mine += key[j] != EMPTY;
+        }
+        // exclusive scan of `mine` over the block
+        u32 incl = mine;
+#pragma unroll
+        for (int d = 1; d < WAVE; d <<= 1) {
+            const u32 o = (u32)__shfl_up((int)incl, d, WAVE);
+            if (lane >= d) incl += o;
+        }
+        if (lane == WAVE - 1) wave_n[w] = incl;
+        __syncthreads();
+        u32 before = 0, total = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (i < w) before += wave_n[i];
+            total += wave_n[i];
+        }
+        if (threadIdx.x == 0) block_base = total ? atomicAdd((unsigned long long*)counter, (unsigned long long)total) : 0;
+        __syncthreads();
+        u64 at = block_base + before + incl - mine;
+#pragma unroll
+        for (int j = 0; j < CP_ITEMS; ++j) {
+            if (key[j] != EMPTY) {
+                const u64 s = t0 + (u64)j * 256 + threadIdx.x;
+                out_k[at] = key[j];
+                out_c[at] = cnts[s];
+                ++at;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// top-k insertion of a score (count << 16 | (65535 - token): larger = ranked higher) into a descending list (static
+// indices only: the list stays in registers)
+template <int KT>
+__device__ __forceinline__ void topk_insert(u64 (&t)[KT], u64 v) {
+#pragma unroll
+    for (int j = 0; j < KT; ++j)
+        if (v > t[j]) {
+            const u64 tmp = t[j];
+            t[j] = v;
+            v = tmp;
+        }
+}
+
+__device__ __forceinline__ u64 rank_score(u64 key, u32 n) { return ((u64)n << 16) | (0xFFFFu - (u32)(key & 0xFFFF)); }
+
+// Per context c in [0, nctx): tot[c] = sum of its pair counts, its first KT pairs by (count desc, token asc) into
+// top_tok/top_cnt [nctx, KT] (0-padded). Pairs sorted by key (context, token), context c's in [start[c], end[c]).
+// A lane per context; contexts with more than 64 pairs are done by the whole wave in turn.
+template <int KT>
+__global__ void __launch_bounds__(256) ctx_topk_k(const u64* __restrict__ uk, const u32* __restrict__ agg,
+                                                  const i64* __restrict__ start, const i64* __restrict__ end, i64 nctx,
+                                                  u64* __restrict__ tot, u16* __restrict__ top_tok,
+                                                  u32* __restrict__ top_cnt) {
+    const int lane = lane_id();
+    const i64 wave = (blockIdx.x * (i64)blockDim.x + threadIdx.x) >> 6;
+    const i64 nwaves = ((i64)gridDim.x * blockDim.x) >> 6;
+    for (i64 c0 = wave * WAVE; c0 < nctx; c0 += nwaves * WAVE) {
+        const i64 c = c0 + lane;
+        i64 a = 0, b = 0;
+        if (c < nctx) {
+            a = start[c];
+            b = end[c];
+        }
+        const bool big = b - a > 64;
+        u64 t[KT];
+#pragma unroll
+        for (int r = 0; r < KT; ++r) t[r] = 0;
+        u64 s = 0;
+        if (!big)
+            for (i64 j = a; j < b; ++j) {
+                const u32 n = agg[j];
+                s += n;
+                topk_insert<KT>(t, rank_score(uk[j], n));
+            }
+        u64 bigs = __ballot(big);
+        while (bigs) {
+            const int l = __ffsll((unsigned long long)bigs) - 1;
+            bigs &= bigs - 1;
+            const i64 ba = (i64)bcast_u64((u64)a, l), bb = (i64)bcast_u64((u64)b, l);
+            u64 part = 0;
+            u64 lt[KT];
+#pragma unroll
+            for (int r = 0; r < KT; ++r) lt[r] = 0;
+            for (i64 j = ba + lane; j < bb; j += WAVE) {
+                const u32 n = agg[j];
+                part += n;
+                topk_insert<KT>(lt, rank_score(uk[j], n));
+            }
+#pragma unroll
+            for (int d = WAVE / 2; d > 0; d >>= 1) part += shfl_down_u64(part, d);
+            part = bcast_u64(part, 0);
+            // merge the lanes' lists: KT rounds of a wave-wide maximum; the lane holding it moves to its next entry
+            // (scores are distinct within a context, so exactly one lane holds a nonzero maximum)
+            int head = 0;
+            u64 merged[KT];
+#pragma unroll
+            for (int r = 0; r < KT; ++r) {
+                u64 mine = 0;
+#pragma unroll
+                for (int q = 0; q < KT; ++q)
+                    if (q == head) mine = lt[q];
+                u64 m = mine;
+#pragma unroll
+                for (int d = WAVE / 2; d > 0; d >>= 1) {
+                    const u64 o = shfl_down_u64(m, d);
+                    m = o > m ? o : m;
+                }
+                m = bcast_u64(m, 0);
+                merged[r] = m;
+                if (m != 0 && mine == m) ++head;
+            }
+            if (lane == l) {
+                s = part;
+#pragma unroll
+                for (int r = 0; r < KT; ++r) t[r] = merged[r];
+            }
+        }
+        if (c < nctx) {
+            tot[c] = s;
+#pragma unroll
+            for (int r = 0; r < KT; ++r) {
+                top_tok[c * KT + r] = t[r] ? (u16)(0xFFFFu - (u32)(t[r] & 0xFFFF)) : (u16)0;
+                top_cnt[c * KT + r] = (u32)(t[r] >> 16);
+            }
+        }
+    }
+}
+
+// Per query position i whose context id c is in [lo, hi): tot, dist, cnt (the target's count, binary search of
+// (c - lo) << 16 | tgt in the context's pairs), the first kout of its context's top entries (top_tok/top_cnt
+// [hi - lo, ktop]) and bit li of mask; other positions untouched.
+__global__ void __launch_bounds__(256) pos_gather_k(const int* __restrict__ ctx_of, i64 N, i64 lo, i64 hi,
+                                                    const u16* __restrict__ tgt, const u64* __restrict__ uk,
+                                                    const u32* __restrict__ agg, const i64* __restrict__ start,
+                                                    const i64* __restrict__ end, const u64* __restrict__ tot,
+                                                    const u16* __restrict__ top_tok, const u32* __restrict__ top_cnt,
+                                                    int ktop, int kout, int li, int* __restrict__ out_tot,
+                                                    int* __restrict__ out_dist,
+                                                    int* __restrict__ out_cnt, u16* __restrict__ out_tok,
+                                                    u32* __restrict__ out_tcnt, int* __restrict__ mask) {
+    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    if (i >= N) return;
+    i64 c = ctx_of[i];
+    if (c < lo || c >= hi) return;
+    c -= lo;
+    i64 a = start[c], b = end[c];
+    if (b <= a) return;
+    const i64 e = b;
+    out_tot[i] = (int)(u32)tot[c];
+    out_dist[i] = (int)(b - a < 65535 ? b - a : 65535);
+    const u64 want = ((u64)c << 16) | tgt[i];
+    while (a < b) {
+        const i64 m = (a + b) >> 1;
+        if (uk[m] < want) a = m + 1;
+        else b = m;
+    }
+    if (a < e && uk[a] == want) out_cnt[i] = (int)agg[a];
+    for (int r = 0; r < kout; ++r) {
+        out_tok[i * kout + r] = top_tok[c * ktop + r];
+        out_tcnt[i * kout + r] = top_cnt[c * ktop + r];
+    }
+    if (mask) mask[i] |= 1 << li;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------------------------------------
+// C ABI (engine extensions)
+// ---------------------------------------------------------------------------------------------------------------
+
+// One level's scan counted in a split table (keys u64[cap] filled with EMPTY, cnts u32[cap] zeroed): the record's
+// scan_level with the split table (sparse: walk the set bits of bm_in).
+extern "C" int ng_scan_count(const u16* tok, i64 L, int k, const u32* bm_in, u32* bm_out, const u64* vt, u64 vcap,
+                             const u32* vrep, const u16* x, u64* keys, u32* cnts, u64 cap, u32* flags, int grid,
+                             int sparse, void* stream) {
+    if (L <= 0) return 0;
+    if (cap == 0) return -1;
+    if (grid <= 0) grid = grid_for(L, 256);
+    hipStream_t st = (hipStream_t)stream;
+    if (sparse && bm_in) {
+        LEVEL_SWITCH(k, (scan_count_sparse_k<K><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, keys, cnts, cap, flags)));
+    } else {
+        LEVEL_SWITCH(k, (scan_count_dense_k<K><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, keys, cnts, cap, flags)));
+    }
+    return (int)hipGetLastError();
+}
+
+// The split table's occupied slots appended to (out_k, out_c) from *counter (zeroed by the caller; any order).
+extern "C" int ng_table_compact(const u64* keys, const u32* cnts, u64 cap, u64* out_k, u32* out_c, u64* counter,
+                                void* stream) {
+    if (cap == 0) return 0;
+    u64 tiles = (cap + 256 * CP_ITEMS - 1) / (256 * CP_ITEMS);
+    const int g = tiles > 16384 ? 16384 : (int)tiles;
+    table_compact_k<<<g, 256, 0, (hipStream_t)stream>>>(keys, cnts, cap, out_k, out_c, counter);
+    return (int)hipGetLastError();
+}
+
+// Per context: total and top-k (topk of 1, 2, 4, 8) from pairs sorted by key with seg_bounds' start/end.
+extern "C" int ng_ctx_topk(const u64* uk, const u32* agg, const i64* start, const i64* end, i64 nctx, int topk,
+                           u64* tot, u16* top_tok, u32* top_cnt, void* stream) {
+    if (nctx <= 0) return 0;
+    int g = grid_for(nctx, 256);
+    g = g > 16384 ? 16384 : g;
+    hipStream_t st = (hipStream_t)stream;
+    switch (topk) {
+        case 1: ctx_topk_k<1><<<g, 256, 0, st>>>(uk, agg, start, end, nctx, tot, top_tok, top_cnt); break;
+        case 2: ctx_topk_k<2><<<g, 256, 0, st>>>(uk, agg, start, end, nctx, tot, top_tok, top_cnt); break;
+        case 4: ctx_topk_k<4><<<g, 256, 0, st>>>(uk, agg, start, end, nctx, tot, top_tok, top_cnt); break;
+        case 8: ctx_topk_k<8><<<g, 256, 0, st>>>(uk, agg, start, end, nctx, tot, top_tok, top_cnt); break;
+        default: return -1;
+    }
+    return (int)hipGetLastError();
+}
+
+// Per query position: tot, dist, cnt, the first kout <= ktop top entries (out_tok/out_tcnt [N, kout]; kout 0: none)
+// and mask bit li (mask may be NULL).
+extern "C" int ng_pos_gather(const int* ctx_of, i64 N, i64 lo, i64 hi, const u16* tgt, const u64* uk, const u32* agg,
+                             const i64* start, const i64* end, const u64* tot, const u16* top_tok, const u32* top_cnt,
+                             int ktop, int kout, int li, int* out_tot, int* out_dist, int* out_cnt, u16* out_tok,
+                             u32* out_tcnt, int* mask, void* stream) {
+    if (kout < 0 || kout > ktop || (mask && (li < 0 || li > 30))) return -1;
+    if (N > 0)
+        pos_gather_k<<<grid_for(N, 256), 256, 0, (hipStream_t)stream>>>(ctx_of, N, lo, hi, tgt, uk, agg, start, end, tot,
+                                                                        top_tok, top_cnt, ktop, kout, li, out_tot,
+                                                                        out_dist, out_cnt, out_tok, out_tcnt, mask);
+    return (int)hipGetLastError();
+}

@@ -34,118 +34,25 @@ extern "C" int scan_level(const u16* tok, i64 L, int k, const u32* bm_in, u32* b
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Partitioned aggregation: emitted keys grouped by sub-table in LDS, then counted sub-table by sub-table
+// Partitioned aggregation (kernels in pairs.h)
 // ---------------------------------------------------------------------------------------------------------------
 
-__global__ void subpart_count_k(const u64* __restrict__ keys, i64 n, int pbits, u64* counts) {
-    extern __shared__ u32 h[];
-    const int P = 1 << pbits;
-    for (int b = threadIdx.x; b < P; b += blockDim.x) h[b] = 0;
-    __syncthreads();
-    for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n; i += (i64)gridDim.x * blockDim.x)
-        atomicAdd(&h[mix64(keys[i]) >> (64 - pbits)], 1u);
-    __syncthreads();
-    for (int b = threadIdx.x; b < P; b += blockDim.x)
-        if (h[b]) atomicAdd((unsigned long long*)&counts[b], (unsigned long long)h[b]);
-}
+extern "C" int max_pbits() { return ng_max_pbits(); }
 
-#define SP_ITEMS 16
-__global__ void subpart_scatter_k(const u64* __restrict__ keys, i64 n, int pbits, u64* cursor, u64* __restrict__ out) {
-    extern __shared__ u32 sm[];
-    const int P = 1 << pbits;
-    u32* cnt = sm;
-    u32* base = sm + P;
-    const i64 tile_size = (i64)blockDim.x * SP_ITEMS;
-    for (i64 tile = blockIdx.x * tile_size; tile < n; tile += (i64)gridDim.x * tile_size) {
-        for (int b = threadIdx.x; b < P; b += blockDim.x) cnt[b] = 0;
-        __syncthreads();
-        u64 key[SP_ITEMS];
-        int o[SP_ITEMS];
-        u32 local[SP_ITEMS];
-#pragma unroll
-        for (int j = 0; j < SP_ITEMS; ++j) {
-            const i64 i = tile + (i64)j * blockDim.x + threadIdx.x;
-            o[j] = -1;
-            if (i < n) {
-                key[j] = keys[i];
-                o[j] = (int)(mix64(key[j]) >> (64 - pbits));
-                local[j] = atomicAdd(&cnt[o[j]], 1u);
-            }
-        }
-        __syncthreads();
-        for (int b = threadIdx.x; b < P; b += blockDim.x)
-            if (cnt[b]) base[b] = (u32)atomicAdd((unsigned long long*)&cursor[b], (unsigned long long)cnt[b]);
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < SP_ITEMS; ++j)
-            if (o[j] >= 0) out[(u64)base[o[j]] + local[j]] = key[j];
-        __syncthreads();
-    }
-}
-
-__global__ void aggregate_k(const u64* __restrict__ keys, i64 n, u64* pk, u32* wraps, u64 sub_cap, int pbits, u32* flags) {
-    for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n; i += (i64)gridDim.x * blockDim.x) {
-        if (*(volatile u32*)&flags[0]) return;
-        pair_add<KB_GVS>(pk, wraps, sub_cap, pbits, keys[i], flags);
-    }
-}
-
-extern "C" int max_pbits() {
-    int dev = 0, smem = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 1;
-    if (hipDeviceGetAttribute(&smem, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess) return 1;
-    int b = 1;
-    while (b < 14 && (8 << (b + 1)) <= smem) ++b;
-    return b;
-}
-
-static int set_smem(const void* fn, size_t bytes) {
-    if (bytes > 64 * 1024) return (int)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
-    return 0;
-}
-
+// emitted keys per sub-table (gpu_val_stats.cu:340-418)
 extern "C" int subpart_count(const u64* keys, i64 n, int pbits, u64* counts, void* stream) {
-    if (pbits < 1 || pbits > 14) return -1;
-    const size_t bytes = 4u << pbits;
-    int e = set_smem((const void*)subpart_count_k, bytes);
-    if (e) return e;
-    if (n > 0) subpart_count_k<<<1024, 256, bytes, (hipStream_t)stream>>>(keys, n, pbits, counts);
-    return (int)hipGetLastError();
+    return launch_subpart_count(keys, n, pbits, counts, (hipStream_t)stream);
 }
 
+// emitted keys grouped by sub-table (gpu_val_stats.cu:420-428)
 extern "C" int subpart_scatter(const u64* keys, i64 n, int pbits, u64* cursor, u64* out, void* stream) {
-    if (pbits < 1 || pbits > 14) return -1;
-    const size_t bytes = 8u << pbits;
-    int e = set_smem((const void*)subpart_scatter_k, bytes);
-    if (e) return e;
-    if (n > 0) subpart_scatter_k<<<1024, 256, bytes, (hipStream_t)stream>>>(keys, n, pbits, cursor, out);
-    return (int)hipGetLastError();
+    return launch_subpart_scatter(keys, n, pbits, cursor, out, (hipStream_t)stream);
 }
 
+// grouped keys counted into the pair table (gpu_val_stats.cu:384-393, 430-434)
 extern "C" int aggregate(const u64* keys, i64 n, u64* pk, u32* wraps, u64 sub_cap, int pbits, u32* flags, int grid,
                          void* stream) {
-    if (n > 0)
-        aggregate_k<<<grid > 0 ? grid : grid_for(n, 256), 256, 0, (hipStream_t)stream>>>(keys, n, pk, wraps, sub_cap, pbits,
-                                                                                           flags);
-    return (int)hipGetLastError();
-}
-
-__device__ __forceinline__ u64 wave_sum_pc(u64 v) {
-#pragma unroll
-    for (int d = WAVE / 2; d > 0; d >>= 1) v += shfl_down_u64(v, d);
-    return v;
-}
-
-__global__ void popcount_k(const u32* __restrict__ bm, i64 n, u64* out) {
-    u64 c = 0;
-    for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n; i += (i64)gridDim.x * blockDim.x) c += __popc(bm[i]);
-    c = wave_sum_pc(c);
-    if (lane_id() == 0 && c) atomicAdd((unsigned long long*)out, (unsigned long long)c);
-}
-
-extern "C" int popcount(const u32* bm, i64 n, u64* out, void* stream) {
-    if (n > 0) popcount_k<<<1024, 256, 0, (hipStream_t)stream>>>(bm, n, out);
-    return (int)hipGetLastError();
+    return launch_aggregate<KB_GVS>(keys, n, pk, wraps, sub_cap, pbits, flags, grid, (hipStream_t)stream);
 }
 
 // ---------------------------------------------------------------------------------------------------------------

@@ -217,6 +217,109 @@ __global__ void __launch_bounds__(256) scan_words_emit_k(const u16* __restrict__
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// Partitioned aggregation: emitted keys grouped by sub-table in LDS, then counted sub-table by sub-table
+// ---------------------------------------------------------------------------------------------------------------
+
+namespace {  // internal linkage: this header is compiled into several objects of one library
+
+__global__ void subpart_count_k(const u64* __restrict__ keys, i64 n, int pbits, u64* counts) {
+    extern __shared__ u32 h[];
+    const int P = 1 << pbits;
+    for (int b = threadIdx.x; b < P; b += blockDim.x) h[b] = 0;
+    __syncthreads();
+    for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n; i += (i64)gridDim.x * blockDim.x)
+        atomicAdd(&h[mix64(keys[i]) >> (64 - pbits)], 1u);
+    __syncthreads();
+    for (int b = threadIdx.x; b < P; b += blockDim.x)
+        if (h[b]) atomicAdd((unsigned long long*)&counts[b], (unsigned long long)h[b]);
+}
+
+#define SP_ITEMS 16
+__global__ void subpart_scatter_k(const u64* __restrict__ keys, i64 n, int pbits, u64* cursor, u64* __restrict__ out) {
+    extern __shared__ u32 sm[];
+    const int P = 1 << pbits;
+    u32* cnt = sm;
+    u32* base = sm + P;
+    const i64 tile_size = (i64)blockDim.x * SP_ITEMS;
+    for (i64 tile = blockIdx.x * tile_size; tile < n; tile += (i64)gridDim.x * tile_size) {
+        for (int b = threadIdx.x; b < P; b += blockDim.x) cnt[b] = 0;
+        __syncthreads();
+        u64 key[SP_ITEMS];
+        int o[SP_ITEMS];
+        u32 local[SP_ITEMS];
+#pragma unroll
+        for (int j = 0; j < SP_ITEMS; ++j) {
+            const i64 i = tile + (i64)j * blockDim.x + threadIdx.x;
+            o[j] = -1;
+            if (i < n) {
+                key[j] = keys[i];
+                o[j] = (int)(mix64(key[j]) >> (64 - pbits));
+                local[j] = atomicAdd(&cnt[o[j]], 1u);
+            }
+        }
+        __syncthreads();
+        for (int b = threadIdx.x; b < P; b += blockDim.x)
+            if (cnt[b]) base[b] = (u32)atomicAdd((unsigned long long*)&cursor[b], (unsigned long long)cnt[b]);
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < SP_ITEMS; ++j)
+            if (o[j] >= 0) out[(u64)base[o[j]] + local[j]] = key[j];
+        __syncthreads();
+    }
+}
+
+template <int KB>
+__global__ void aggregate_k(const u64* __restrict__ keys, i64 n, u64* pk, u32* wraps, u64 sub_cap, int pbits, u32* flags) {
+    for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n; i += (i64)gridDim.x * blockDim.x) {
+        if (*(volatile u32*)&flags[0]) return;
+        pair_add<KB>(pk, wraps, sub_cap, pbits, keys[i], flags);
+    }
+}
+
+static int ng_max_pbits() {
+    int dev = 0, smem = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 1;
+    if (hipDeviceGetAttribute(&smem, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess) return 1;
+    int b = 1;
+    while (b < 14 && (8 << (b + 1)) <= smem) ++b;
+    return b;
+}
+
+static int set_smem(const void* fn, size_t bytes) {
+    if (bytes > 64 * 1024) return (int)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    return 0;
+}
+
+static int launch_subpart_count(const u64* keys, i64 n, int pbits, u64* counts, hipStream_t stream) {
+    if (pbits < 1 || pbits > 14) return -1;
+    const size_t bytes = 4u << pbits;
+    int e = set_smem((const void*)subpart_count_k, bytes);
+    if (e) return e;
+    if (n > 0) subpart_count_k<<<1024, 256, bytes, stream>>>(keys, n, pbits, counts);
+    return (int)hipGetLastError();
+}
+
+static int launch_subpart_scatter(const u64* keys, i64 n, int pbits, u64* cursor, u64* out, hipStream_t stream) {
+    if (pbits < 1 || pbits > 14) return -1;
+    const size_t bytes = 8u << pbits;
+    int e = set_smem((const void*)subpart_scatter_k, bytes);
+    if (e) return e;
+    if (n > 0) subpart_scatter_k<<<1024, 256, bytes, stream>>>(keys, n, pbits, cursor, out);
+    return (int)hipGetLastError();
+}
+
+template <int KB>
+static int launch_aggregate(const u64* keys, i64 n, u64* pk, u32* wraps, u64 sub_cap, int pbits, u32* flags, int grid,
+                            hipStream_t stream) {
+    if (n > 0)
+        aggregate_k<KB><<<grid > 0 ? grid : grid_for(n, 256), 256, 0, stream>>>(keys, n, pk, wraps, sub_cap, pbits,
+                                                                                           flags);
+    return (int)hipGetLastError();
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------------------------------------
 // Local aggregation by owner (context-id ranges [bounds[o], bounds[o + 1]))
 // ---------------------------------------------------------------------------------------------------------------
 

@@ -5,8 +5,10 @@
 //   * scan_level takes one table (no sub-tables, no emit) and a `sparse` flag instead of a mode;
 //   * rank_scatter has no rank_of, pos_outputs no TOP rule, rank_of, level index or mask (kernels.cu:377-437).
 // The shared entry points (val_keys, val_verify, val_homes, sort_pairs, inclusive_max, reduce_by_key, seg_bounds,
-// ctx_tot, rank_keys) come from common_abi.hip. One extension: pos_topk, the per-position gather of a context's top
-// next tokens that the record's host does with torch indexing (build.py:360-368).
+// ctx_tot, rank_keys) come from common_abi.hip. Extensions (no counterpart in the record's library): pos_topk, the
+// per-position gather of a context's top next tokens that the record's host does with torch indexing
+// (build.py:360-368); and the partitioned counting of the gpu_val_stats library (scan_emit = its scan_level modes 2/3,
+// subpart_count, subpart_scatter, aggregate, popcount; gpu_val_stats.cu:268-446) on this flavour's 41-bit pair keys.
 #include "../pairs.h"
 
 #define KB_REC 41
@@ -70,4 +72,35 @@ extern "C" int pos_topk(const int* ctx_of, i64 N, i64 lo, i64 hi, const u16* top
         pos_topk_k<<<grid_for(N, 256), 256, 0, (hipStream_t)stream>>>(ctx_of, N, lo, hi, top_tok, top_cnt, top, kout,
                                                                        out_tok, out_cnt);
     return (int)hipGetLastError();
+}
+
+// A level's scan that appends every hit's pair key to emit[*emitted ...] instead of counting it (words: a lane per
+// bitmap word, for sparse levels; bm_in required); the hit bitmap as scan_level's.
+extern "C" int scan_emit(const u16* tok, i64 L, int k, const u32* bm_in, u32* bm_out, const u64* vt, u64 vcap,
+                         const u32* vrep, const u16* x, u32* flags, int grid, int words, u64* emit, u64* emitted,
+                         void* stream) {
+    if (L <= 0) return 0;
+    if (grid <= 0) grid = grid_for(L, 256);
+    hipStream_t st = (hipStream_t)stream;
+    if (words && bm_in) {
+        LEVEL_SWITCH(k, (scan_words_emit_k<K><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, flags, emit, emitted)));
+    } else {
+        LEVEL_SWITCH(k, (scan_dense_k<K, true, KB_REC><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, nullptr, nullptr, 0, 0, flags, emit, emitted)));
+    }
+    return (int)hipGetLastError();
+}
+
+extern "C" int max_pbits() { return ng_max_pbits(); }
+
+extern "C" int subpart_count(const u64* keys, i64 n, int pbits, u64* counts, void* stream) {
+    return launch_subpart_count(keys, n, pbits, counts, (hipStream_t)stream);
+}
+
+extern "C" int subpart_scatter(const u64* keys, i64 n, int pbits, u64* cursor, u64* out, void* stream) {
+    return launch_subpart_scatter(keys, n, pbits, cursor, out, (hipStream_t)stream);
+}
+
+extern "C" int aggregate(const u64* keys, i64 n, u64* pk, u32* wraps, u64 sub_cap, int pbits, u32* flags, int grid,
+                         void* stream) {
+    return launch_aggregate<KB_REC>(keys, n, pk, wraps, sub_cap, pbits, flags, grid, (hipStream_t)stream);
 }

@@ -39,6 +39,12 @@ ROW_LEVELS = (6, 10, 20)
 ROW_K = 8
 ROW_COUNTS = (2, 3, 5, 9, 17, 33)
 ROW_PURITIES = (0.3, 0.5, 0.7, 0.85, 0.95)
+# Partitioned counting: a level whose pair table is larger than PART_MIN_BYTES emits its hits' keys, groups them by
+# sub-table (the key hash's top bits) and counts them sub-table by sub-table, each sub-table about SUB_BYTES so that it
+# stays in the MALL (256 MB Infinity Cache) while its keys are counted; smaller tables are counted directly.
+SUB_BYTES = 64 << 20
+PART_MIN_BYTES = 128 << 20
+EMIT_CHUNK = 1 << 28  # emitted keys held before a flush (at least one shard's positions)
 
 
 def record_lib() -> Lib:
@@ -92,7 +98,12 @@ class CountBuild:
     """The record's count build on one GPU. `shards`: shard file paths (read into pinned host memory, then copied by
     start_load/pace) or uint16 arrays. `levels` ascending; `level_shards`: per level, how many leading shards it
     counts; `topk`: per level the first topk ranked next tokens/counts of each position's context (self.top_tok /
-    self.top_cnt [len(levels), N, topk]) when > 0. Construct with `from_device` for tokens already in GPU memory."""
+    self.top_cnt [len(levels), N, topk]) when > 0. Construct with `from_device` for tokens already in GPU memory.
+
+    `mode` (attribute): "engine" (default) counts in split pair tables (keys and u32 counts apart) and ranks by
+    per-context selection after one sort (libngram_amd.so's ng_* entry points); "record" runs the record's own C ABI
+    calls, as its host does (one packed table per level, two sorts); "partitioned" is "record" with the large tables'
+    hits emitted, grouped by sub-table and counted sub-table by sub-table."""
 
     def __init__(self, shards: list, rank: int = 0, world: int = 1, levels=LEVELS, level_shards=None, topk: int = 0,
                  lib: Lib | None = None):
@@ -100,12 +111,14 @@ class CountBuild:
             raise ValueError("this build runs on one GPU: world must be 1 (the owner exchange is out of scope)")
         self.rank, self.world = rank, world
         self.min_cap = 1 << 20
+        self.mode = "engine"
         self.levels = tuple(levels)
         if not self.levels or list(self.levels) != sorted(set(self.levels)) or self.levels[0] < 1:
             raise ValueError(f"levels must ascend from >= 1: {self.levels}")
         ls = LEVEL_SHARDS if level_shards is None else level_shards
         self.topk = topk
         self.lib = lib or record_lib()
+        self.elib = Lib()
         self.timing: dict[str, float] = {}
         self.info: dict = {}
         self.events: list = []
@@ -134,10 +147,12 @@ class CountBuild:
         self = cls.__new__(cls)
         self.rank, self.world = 0, 1
         self.min_cap = 1 << 20
+        self.mode = "engine"
         self.levels = tuple(levels)
         ls = LEVEL_SHARDS if level_shards is None else level_shards
         self.topk = topk
         self.lib = lib or record_lib()
+        self.elib = Lib()
         self.timing, self.info, self.events, self.host, self.pending = {}, {}, [], [], []
         self.sizes, self.starts, self.L = list(sizes), list(starts), int(tok.numel())
         self.level_shards = {k: min(len(sizes), ls.get(k, len(sizes))) for k in self.levels}
@@ -187,25 +202,77 @@ class CountBuild:
                     ev.record(self.stream)
                     self.events.append(ev)
 
+    def _event(self, name: str, k: int, i: int, n: int):
+        """A pair of timing events around a launch (recorded on the current stream), kept in kernel_events."""
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        self.kernel_events.append((name, k, i, n, e0, e1))
+        return e0, e1
+
     def _scan(self, index, tables, bms, shard_ids, levels) -> None:
         lib, grid = self.lib, self.grid
         for i in shard_ids:
             st, n = self.starts[i], self.sizes[i]
+            n32 = (n + 31) // 32 * 32
             torch.cuda.current_stream().wait_event(self.events[i])
             scanned = [k for k in self.levels if i < self.level_shards[k]]
             for li, k in enumerate(scanned):
                 if k not in levels:
                     continue
                 vi = index[k]
-                pk, pc, cap, flags = tables[k]
+                t = tables[k]
                 # gated by this shard's previous scanned level; a shard that level skipped is probed whole
                 bm_in = None if li == 0 else bms[scanned[li - 1]][st // 32 :]
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record()
-                lib("scan_level", self.tok[st:], (n + 31) // 32 * 32, i32(k), bm_in, bms[k][st // 32 :], vi.table,
-                    u64(vi.cap), vi.rep, self.x, pk, pc, u64(cap), flags, i32(grid), i32(int(li > 0 and k > 5)))
-                e1.record()
-                self.kernel_events.append(("scan_level", k, i, (n + 31) // 32 * 32, e0, e1))
+                if self.mode == "engine":
+                    e0, e1 = self._event("scan_count", k, i, n32)
+                    e0.record()
+                    self.elib("ng_scan_count", self.tok[st:], n32, i32(k), bm_in, bms[k][st // 32 :], vi.table,
+                              u64(vi.cap), vi.rep, self.x, t["keys"], t["cnts"], u64(t["cap"]), t["flags"], i32(grid),
+                              i32(int(li > 0 and k > 5)))
+                    e1.record()
+                elif t["pbits"]:
+                    if t["pending"] + n32 > t["emit"].numel():
+                        self._flush(t, k)
+                    e0, e1 = self._event("scan_emit", k, i, n32)
+                    e0.record()
+                    lib("scan_emit", self.tok[st:], n32, i32(k), bm_in, bms[k][st // 32 :], vi.table, u64(vi.cap),
+                        vi.rep, self.x, t["flags"], i32(grid), i32(0), t["emit"], t["emitted"])
+                    e1.record()
+                    t["pending"] += n32
+                else:
+                    e0, e1 = self._event("scan_level", k, i, n32)
+                    e0.record()
+                    lib("scan_level", self.tok[st:], n32, i32(k), bm_in, bms[k][st // 32 :], vi.table, u64(vi.cap),
+                        vi.rep, self.x, t["pk"], t["pc"], u64(t["cap"]), t["flags"], i32(grid),
+                        i32(int(li > 0 and k > 5)))
+                    e1.record()
+        for k in levels:
+            if tables[k]["pbits"]:
+                self._flush(tables[k], k)
+
+    def _flush(self, t: dict, k: int) -> None:
+        """Count a partitioned level's emitted keys: group them by sub-table, then count sub-table by sub-table."""
+        if t["pending"] == 0:
+            return
+        lib = self.lib
+        n = int(t["emitted"].item())
+        if getattr(self, "grouped", None) is None or self.grouped.numel() < t["emit"].numel():
+            self.grouped = torch.empty(t["emit"].numel(), dtype=torch.int64, device=t["emit"].device)
+        if n:
+            pbits = t["pbits"]
+            counts = torch.zeros(1 << pbits, dtype=torch.int64, device=t["pk"].device)
+            e0, e1 = self._event("group", k, -1, n)
+            e0.record()
+            lib("subpart_count", t["emit"], n, i32(pbits), counts)
+            cursor = torch.cumsum(counts, 0) - counts
+            lib("subpart_scatter", t["emit"], n, i32(pbits), cursor, self.grouped)
+            e1.record()
+            e0, e1 = self._event("aggregate", k, -1, n)
+            e0.record()
+            lib("aggregate", self.grouped, n, t["pk"], t["pc"], u64(t["sub_cap"]), i32(pbits), t["flags"],
+                i32(self.grid))
+            e1.record()
+        t["emitted"].zero_()
+        t["pending"] = 0
 
     def counts(self, x: torch.Tensor, tgt: torch.Tensor, avail: torch.Tensor, stats: bool = False) -> torch.Tensor:
         """int32 [3, len(levels), len(x)]: per query position and level its context's total occurrences (uint32 bits),
@@ -230,20 +297,21 @@ class CountBuild:
         self.grid = torch.cuda.get_device_properties(dev).multi_processor_count * 32
         caps = self.caps()
         tables = {}
+        chunk = max([EMIT_CHUNK] + [(n + 31) // 32 * 32 for n in self.sizes])
         for k in self.levels:
-            tables[k] = self._table(caps[k], dev)
+            tables[k] = self._table(caps[k], dev, chunk)
         nwords = self.L // 32
         bms = {k: torch.zeros(nwords, dtype=torch.int32, device=dev) for k in self.levels}
         self._scan(index, tables, bms, range(len(self.sizes)), set(self.levels))
         reruns = {k: 0 for k in self.levels}
         while True:
-            fl = {k: tables[k][3].cpu().tolist() for k in self.levels}
+            fl = {k: tables[k]["flags"].cpu().tolist() for k in self.levels}
             over = [k for k in self.levels if fl[k][0]]
             if not over:
                 break
             for k in over:  # the bitmaps are whole: only the overflowed level reruns, with twice the slots
                 reruns[k] += 1
-                tables[k] = self._table(2 * tables[k][2], dev)
+                tables[k] = self._table(2 * tables[k]["cap"], dev, chunk)
             self._scan(index, tables, bms, range(len(self.sizes)), set(over))
         lap("scan")
         hits = {k: int(self._popcount(bms[k]).item()) for k in self.levels} if self.stats else {}
@@ -258,62 +326,32 @@ class CountBuild:
             self.top_cnt = torch.zeros((len(self.levels), N, self.topk), dtype=torch.int32, device=dev)
         for li, k in enumerate(self.levels):
             vi = index.pop(k)
-            pk, pc, cap, _ = tables.pop(k)
-            lo, hi = 0, vi.ids
-            bounds = torch.tensor([lo, hi], dtype=torch.int64, device=dev)
-            cnt = torch.zeros(1, dtype=torch.int64, device=dev)
-            lib("part_count", pk, u64(cap), bounds, i32(1), cnt)
-            U = int(cnt.item())
-            cursor = torch.zeros(1, dtype=torch.int64, device=dev)
-            send_k = torch.empty(U, dtype=torch.int64, device=dev)
-            send_c = torch.empty(U, dtype=torch.int32, device=dev)
-            lib("part_scatter", pk, pc, u64(cap), bounds, i32(1), cursor, send_k, send_c)
-            del pk, pc
-            n_own = hi - lo
-            ctx_bits = max(1, (max(n_own, 2) - 1).bit_length())
-            uk, agg = torch.empty_like(send_k), torch.empty_like(send_c)
-            if U:  # one GPU: the table's keys are already distinct (no reduce_by_key)
-                lib.cub("sort_pairs", send_k, uk, send_c, agg, U, i32(0), i32(16 + ctx_bits))
-            del send_k, send_c
-            start = torch.zeros(n_own, dtype=torch.int64, device=dev)
-            end = torch.zeros(n_own, dtype=torch.int64, device=dev)
-            lib("seg_bounds", uk, U, start, end)
-            tot = torch.empty(n_own, dtype=torch.int64, device=dev)
-            lib("ctx_tot", start, end, agg, n_own, tot)
-            lib("pos_outputs", vi.ctx_of, N, lo, hi, tgt, uk, agg, start, end, tot, out[0, li], out[1, li], out[2, li])
+            t = tables.pop(k)
             want = max(self.topk, ROW_K if (rows and k in ROW_LEVELS) else 0)
-            if want:
-                key2 = torch.empty(U, dtype=torch.int64, device=dev)
-                val2 = torch.empty(U, dtype=torch.int32, device=dev)
-                lib("rank_keys", uk, agg, U, key2, val2)
-                k2s, sv = torch.empty_like(key2), torch.empty_like(val2)
-                if U:
-                    lib.cub("sort_pairs", key2, k2s, val2, sv, U, i32(0), i32(32 + ctx_bits))
-                del key2, val2, k2s
-                top_tok = torch.zeros(n_own * want, dtype=torch.int16, device=dev)
-                top_cnt = torch.zeros(n_own * want, dtype=torch.int32, device=dev)
-                lib("rank_scatter", sv, U, uk, agg, start, top_tok, top_cnt, i32(want))
-                del sv
-                if self.topk:
-                    lib("pos_topk", vi.ctx_of, N, lo, hi, top_tok, top_cnt, i32(want), i32(self.topk),
-                        self.top_tok[li], self.top_cnt[li])
-                if rows and k in ROW_LEVELS:
-                    ri = ROW_LEVELS.index(k)
-                    ctx = vi.ctx_of.long()
-                    at = ((ctx >= lo) & (ctx < hi)).nonzero().squeeze(1)
-                    c = ctx[at] - lo
-                    tt = top_tok.view(-1, want)[c, :ROW_K].to(torch.int32) & 0xFFFF
-                    tc = top_cnt.view(-1, want)[c, :ROW_K].to(torch.int64)
-                    top = tc[:, :1].clamp_min(1)
-                    w = torch.where(top > 32767, (tc * 32767 + top - 1) // top, tc)
-                    row_entries[ri, at] = torch.where(tc > 0, tt | (w.to(torch.int32) << 16), 0)
-                    row_top[ri, at] = tc[:, 0].clamp_max((1 << 31) - 1).to(torch.int32)
-                    del ctx, at, c, tt, tc, top, w
-                del top_tok, top_cnt
-            if n_own and int(tot.max().item()) >= 1 << 32:
+            if self.mode == "engine":
+                U, tot, top_tok, top_cnt, want = self._outputs_engine(li, k, vi, t, tgt, out, want)
+            else:
+                U, tot, top_tok, top_cnt = self._outputs_record(li, k, vi, t, tgt, out, want)
+            lo, hi = 0, vi.ids
+            if rows and k in ROW_LEVELS:
+                ri = ROW_LEVELS.index(k)
+                ctx = vi.ctx_of.long()
+                at = ((ctx >= lo) & (ctx < hi)).nonzero().squeeze(1)
+                c = ctx[at] - lo
+                tt = top_tok.view(-1, want)[c, :ROW_K].to(torch.int32) & 0xFFFF
+                tc = top_cnt.view(-1, want)[c, :ROW_K].to(torch.int64)
+                top = tc[:, :1].clamp_min(1)
+                # the weights as the model reads them (15 bits): scaled down where the top count is larger
+                w = torch.where(top > 32767, (tc * 32767 + top - 1) // top, tc)
+                row_entries[ri, at] = torch.where(tc > 0, tt | (w.to(torch.int32) << 16), 0)
+                row_top[ri, at] = tc[:, 0].clamp_max((1 << 31) - 1).to(torch.int32)
+                del ctx, at, c, tt, tc, top, w
+            del top_tok, top_cnt
+            if vi.ids and int(tot.max().item()) >= 1 << 32:
                 raise RuntimeError(f"k={k}: a total does not fit uint32")
-            info[k] = dict(contexts=vi.n, ids=vi.ids, pairs=U, cap=cap, hits=hits.get(k), reruns=reruns[k])
-            del uk, agg, start, end, tot, vi
+            info[k] = dict(contexts=vi.n, ids=vi.ids, pairs=U, cap=t["cap"], pbits=t["pbits"], hits=hits.get(k),
+                           reruns=reruns[k])
+            del t, tot, vi
         lap("outputs")
         if rows:
             self._rows(out, row_entries, row_top, N)
@@ -321,10 +359,116 @@ class CountBuild:
         self.out = out
         return out
 
-    def _table(self, cap: int, dev):
-        return (torch.full((cap,), -1, dtype=torch.int64, device=dev),
-                torch.zeros((cap + 3) // 4, dtype=torch.int32, device=dev), cap,
-                torch.zeros(2, dtype=torch.int32, device=dev))
+    def _outputs_engine(self, li, k, vi, t, tgt, out, want):
+        """One level's outputs with the engine: the split table compacted, sorted by pair key, per-context totals and
+        top entries by selection, then one gather per query position."""
+        elib, lib, dev = self.elib, self.lib, self.tok.device
+        N, lo, hi = vi.ctx_of.numel(), 0, vi.ids
+        counter = torch.zeros(1, dtype=torch.int64, device=dev)
+        cap = t["cap"]
+        U_max = cap
+        ck = torch.empty(U_max, dtype=torch.int64, device=dev)
+        cc = torch.empty(U_max, dtype=torch.int32, device=dev)
+        e0, e1 = self._event("compact", k, -1, cap)
+        e0.record()
+        elib("ng_table_compact", t["keys"], t["cnts"], u64(cap), ck, cc, counter)
+        e1.record()
+        t.pop("keys"), t.pop("cnts")
+        U = int(counter.item())
+        n_own = hi - lo
+        ctx_bits = max(1, (max(n_own, 2) - 1).bit_length())
+        uk, agg = torch.empty(U, dtype=torch.int64, device=dev), torch.empty(U, dtype=torch.int32, device=dev)
+        e0, e1 = self._event("sort", k, -1, U)
+        e0.record()
+        if U:
+            lib.cub("sort_pairs", ck, uk, cc, agg, U, i32(0), i32(16 + ctx_bits))
+        e1.record()
+        del ck, cc
+        start = torch.zeros(n_own, dtype=torch.int64, device=dev)
+        end = torch.zeros(n_own, dtype=torch.int64, device=dev)
+        ktop = 1 if want <= 1 else 2 if want <= 2 else 4 if want <= 4 else 8
+        tot = torch.empty(n_own, dtype=torch.int64, device=dev)
+        top_tok = torch.zeros(n_own * ktop, dtype=torch.int16, device=dev)
+        top_cnt = torch.zeros(n_own * ktop, dtype=torch.int32, device=dev)
+        e0, e1 = self._event("ctx_topk", k, -1, U)
+        e0.record()
+        lib("seg_bounds", uk, U, start, end)
+        elib("ng_ctx_topk", uk, agg, start, end, n_own, i32(ktop), tot, top_tok, top_cnt)
+        e1.record()
+        e0, e1 = self._event("pos_gather", k, -1, N)
+        e0.record()
+        kout = self.topk
+        elib("ng_pos_gather", vi.ctx_of, N, lo, hi, tgt, uk, agg, start, end, tot, top_tok, top_cnt, i32(ktop),
+             i32(kout), i32(li), out[0, li], out[1, li], out[2, li], self.top_tok[li] if kout else None,
+             self.top_cnt[li] if kout else None, None)
+        e1.record()
+        return U, tot, top_tok, top_cnt, ktop
+
+    def _outputs_record(self, li, k, vi, t, tgt, out, want):
+        """One level's outputs with the record's calls: part_count/part_scatter, sort by pair key, seg_bounds,
+        ctx_tot, pos_outputs, and for top entries rank_keys + a stable sort + rank_scatter (build.py:307-371)."""
+        lib, dev = self.lib, self.tok.device
+        N, lo, hi = vi.ctx_of.numel(), 0, vi.ids
+        pk, pc, cap = t.pop("pk"), t.pop("pc"), t["cap"]
+        bounds = torch.tensor([lo, hi], dtype=torch.int64, device=dev)
+        cnt = torch.zeros(1, dtype=torch.int64, device=dev)
+        lib("part_count", pk, u64(cap), bounds, i32(1), cnt)
+        U = int(cnt.item())
+        cursor = torch.zeros(1, dtype=torch.int64, device=dev)
+        send_k = torch.empty(U, dtype=torch.int64, device=dev)
+        send_c = torch.empty(U, dtype=torch.int32, device=dev)
+        lib("part_scatter", pk, pc, u64(cap), bounds, i32(1), cursor, send_k, send_c)
+        del pk, pc
+        n_own = hi - lo
+        ctx_bits = max(1, (max(n_own, 2) - 1).bit_length())
+        uk, agg = torch.empty_like(send_k), torch.empty_like(send_c)
+        if U:  # one GPU: the table's keys are already distinct (no reduce_by_key)
+            lib.cub("sort_pairs", send_k, uk, send_c, agg, U, i32(0), i32(16 + ctx_bits))
+        del send_k, send_c
+        start = torch.zeros(n_own, dtype=torch.int64, device=dev)
+        end = torch.zeros(n_own, dtype=torch.int64, device=dev)
+        lib("seg_bounds", uk, U, start, end)
+        tot = torch.empty(n_own, dtype=torch.int64, device=dev)
+        lib("ctx_tot", start, end, agg, n_own, tot)
+        lib("pos_outputs", vi.ctx_of, N, lo, hi, tgt, uk, agg, start, end, tot, out[0, li], out[1, li], out[2, li])
+        top_tok = top_cnt = None
+        if want:
+            key2 = torch.empty(U, dtype=torch.int64, device=dev)
+            val2 = torch.empty(U, dtype=torch.int32, device=dev)
+            lib("rank_keys", uk, agg, U, key2, val2)
+            k2s, sv = torch.empty_like(key2), torch.empty_like(val2)
+            if U:
+                lib.cub("sort_pairs", key2, k2s, val2, sv, U, i32(0), i32(32 + ctx_bits))
+            del key2, val2, k2s
+            top_tok = torch.zeros(n_own * want, dtype=torch.int16, device=dev)
+            top_cnt = torch.zeros(n_own * want, dtype=torch.int32, device=dev)
+            lib("rank_scatter", sv, U, uk, agg, start, top_tok, top_cnt, i32(want))
+            del sv
+            if self.topk:
+                lib("pos_topk", vi.ctx_of, N, lo, hi, top_tok, top_cnt, i32(want), i32(self.topk), self.top_tok[li],
+                    self.top_cnt[li])
+        return U, tot, top_tok, top_cnt
+
+    def _table(self, cap: int, dev, chunk: int) -> dict:
+        """A level's pair table of at least `cap` slots: split (engine), packed and counted directly (record), or
+        (partitioned, larger than PART_MIN_BYTES) packed in 2^pbits sub-tables of about SUB_BYTES with an emit buffer
+        of `chunk` keys."""
+        if self.mode == "engine":
+            return {"keys": torch.full((cap,), -1, dtype=torch.int64, device=dev),
+                    "cnts": torch.zeros(cap, dtype=torch.int32, device=dev), "cap": cap, "pbits": 0,
+                    "flags": torch.zeros(2, dtype=torch.int32, device=dev), "pending": 0}
+        pbits, sub_cap = 0, cap
+        if self.mode == "partitioned" and cap * 8 > PART_MIN_BYTES:
+            pbits = min(int(self.lib.plain("max_pbits")), max(1, -(-(cap * 8) // SUB_BYTES) - 1).bit_length())
+            sub_cap = -(-cap // (1 << pbits))
+            cap = sub_cap << pbits
+        t = {"pk": torch.full((cap,), -1, dtype=torch.int64, device=dev),
+             "pc": torch.zeros((cap + 3) // 4, dtype=torch.int32, device=dev), "cap": cap, "pbits": pbits,
+             "sub_cap": sub_cap, "flags": torch.zeros(2, dtype=torch.int32, device=dev), "pending": 0}
+        if pbits:
+            t["emit"] = torch.empty(chunk, dtype=torch.int64, device=dev)
+            t["emitted"] = torch.zeros(1, dtype=torch.int64, device=dev)
+        return t
 
     def _popcount(self, bm: torch.Tensor) -> torch.Tensor:
         # bit count of an int32 bitmap, in torch (a byte table lookup)

@@ -32,10 +32,22 @@ def _reference(corpus, levels, level_shards, ntop=8):
     return ref
 
 
-@pytest.mark.parametrize("level_shards", [{}, {2: 1, 3: 2}])
-def test_counts_match_oracle(corpus, level_shards):
+def _partition_small_tables(monkeypatch):
+    # every table is partitioned into several sub-tables, and each shard's emitted keys are flushed on their own
+    monkeypatch.setattr(C, "PART_MIN_BYTES", 1 << 16)
+    monkeypatch.setattr(C, "SUB_BYTES", 1 << 18)
+    monkeypatch.setattr(C, "EMIT_CHUNK", 1)
+
+
+@pytest.mark.parametrize("level_shards,mode", [({}, "engine"), ({2: 1, 3: 2}, "engine"), ({}, "record"),
+                                               ({2: 1, 3: 2}, "record"), ({}, "partitioned"),
+                                               ({2: 1, 3: 2}, "partitioned")])
+def test_counts_match_oracle(corpus, level_shards, mode, monkeypatch):
+    if mode == "partitioned":
+        _partition_small_tables(monkeypatch)
     lib = C.record_lib()
     cb = C.CountBuild(corpus.shards(), levels=LEVELS, level_shards=level_shards, topk=4)
+    cb.mode = mode
     cb.start_load(3)
     cb.pace()
     cb.pace()
@@ -52,6 +64,7 @@ def test_counts_match_oracle(corpus, level_shards):
         assert np.array_equal(top_tok[li], o["top_tok"][:, :4]), f"top_tok k={k}"
         assert np.array_equal(top_cnt[li], o["top_cnt"][:, :4]), f"top_cnt k={k}"
         assert cb.info[k]["hits"] == o["events"], f"hits k={k}"
+        assert (cb.info[k]["pbits"] > 0) == (mode == "partitioned"), k
     assert (ref[2]["tot"] > 0).sum() > 1000 and (ref[20]["tot"] > 0).sum() > 10
     # the record's rows from ROW_LEVELS, and a batch of them
     ri = [LEVELS.index(k) for k in C.ROW_LEVELS]
@@ -66,13 +79,17 @@ def test_counts_match_oracle(corpus, level_shards):
     del ri
 
 
-def test_overflow_reruns_only_the_level(corpus, monkeypatch):
+@pytest.mark.parametrize("mode", ["engine", "record", "partitioned"])
+def test_overflow_reruns_only_the_level(corpus, monkeypatch, mode):
+    if mode == "partitioned":
+        _partition_small_tables(monkeypatch)
     lib = C.record_lib()
     tok_cb = C.CountBuild(corpus.shards(), levels=(2, 3, 6), topk=2)
     tok_cb.start_load(1)
     x, tgt, avail = C.queries(corpus.query, [], "cuda", lib)
     monkeypatch.setattr(C, "LOAD", 1e9)
     tok_cb.min_cap = 1024
+    tok_cb.mode = mode
     out = tok_cb.counts(x, tgt, avail).cpu().numpy()
     assert tok_cb.info[2]["reruns"] > 0
     ref = _reference(corpus, (2, 3, 6), {})
