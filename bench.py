@@ -30,10 +30,11 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--config", default="c3", choices=("c3",))
+    ap.add_argument("--config", default="c3", choices=("c3",), help="the headline workload")
     ap.add_argument("--train-tokens", type=int, default=0, help="override the corpus size (smaller runs)")
     ap.add_argument("--query-tokens", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-secondary", action="store_true", help="skip the other configurations' measurements")
     ap.add_argument("--mode", default="engine", choices=("engine", "record", "partitioned"), help="CountBuild.mode")
     ap.add_argument("--cpu-tokens", type=int, default=100_000_000, help="CPU baseline: corpus prefix")
     ap.add_argument("--cpu-queries", type=int, default=2_000_000, help="CPU baseline: query positions")
@@ -71,6 +72,64 @@ def make_workload(cfg_name: str, train_tokens: int, query_tokens: int):
     return cfg, flat, bounds, tok, sizes, starts, q, np
 
 
+def bench_c2(steps: int, warmup: int, with_cpu: bool) -> dict:
+    """BASELINE's second configuration: a corpus-wide CountTable over a 100M-token corpus for n = 2..4, then the
+    top-4 continuations (with counts), tot / dist / cnt of 8M query positions; one step = build + query."""
+    import numpy as np
+    import torch
+
+    from ngram_amd.count_table import CountTable
+
+    cfg, flat, bounds, tok, sizes, starts, q, _ = make_workload("c2", 0, 0)
+    x, tgt = q[:-1], q[1:]
+    levels = list(cfg.levels)
+    ct0 = CountTable.from_device(tok, sizes, starts, levels)
+    from ngram_amd.count_table import _segments_device
+
+    avail = _segments_device(x, ct0.lib)
+    times = []
+    for step in range(warmup + steps):
+        ct = CountTable.from_device(tok, sizes, starts, levels)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ct.build()
+        r = ct.query_device(x, tgt, avail, topk=cfg.topk)
+        torch.cuda.synchronize()
+        if step >= warmup:
+            times.append(time.perf_counter() - t0)
+        sizes_out = ct.sizes()
+        ev = {}
+        for name, k, e0, e1 in ct.events:
+            ev[name] = ev.get(name, 0.0) + e0.elapsed_time(e1)
+        del ct, r
+    dt = sum(times) / len(times)
+    T = sum(sizes)
+    res = {"value": T / dt, "unit": "corpus tokens/s", "query_positions_per_s": x.numel() / dt, "ms_per_step": dt * 1e3,
+           "workload": f"c2: CountTable of {T} corpus tokens for n={levels} + top-{cfg.topk}/tot/dist/cnt queries at "
+                       f"{x.numel()} positions", "kernel_ms_per_step": ev,
+           "sizes": [list(v) for v in sizes_out]}
+    build_bytes = 2.0 * T * len(levels) + 16.0 * T * len(levels)  # every position at every level is an event
+    res["build_bytes"] = build_bytes
+    res["build_GBps_over_step"] = build_bytes / dt / 1e9
+    if with_cpu:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as O
+
+        n_t = 10_000_000
+        train = flat[:n_t].cpu().numpy().view(np.uint16)
+        qq = q[: 1_000_001].cpu().numpy().view(np.uint16)
+        xs, ts = qq[:-1], qq[1:]
+        av = O.segments(xs)
+        t0 = time.perf_counter()
+        for k in levels:
+            O.table_counts(train, np.array([0, n_t], np.int64), xs, ts, av, k, ntop=4, nthreads=O.threads())
+        cdt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": n_t / cdt, "unit": "corpus tokens/s", "cores": O.threads(), "kind": "port",
+                               "sample": f"count_table.rs restatement over the first {n_t} tokens x 1M queries, "
+                                         f"levels {levels}; {cdt:.1f} s"}
+    return res
+
+
 def cpu_baseline(flat, bounds, q, levels, n_tokens: int, n_queries: int) -> dict:
     """The oracle's query-filtered counting (C++ restatement of kgram.rs, one thread per core) over a bounded sample:
     the corpus' first n_tokens tokens and the first n_queries query positions, every level."""
@@ -79,9 +138,9 @@ def cpu_baseline(flat, bounds, q, levels, n_tokens: int, n_queries: int) -> dict
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle as O
 
-    train = flat[:n_tokens].cpu().numpy().view(np.uint16)
+    train = flat[:n_tokens].numpy().view(np.uint16)
     b = bounds[bounds < n_tokens].tolist() + [n_tokens]
-    qq = q[: n_queries + 1].cpu().numpy().view(np.uint16)
+    qq = q[: n_queries + 1].numpy().view(np.uint16)
     x, tgt = qq[:-1], qq[1:]
     avail = O.segments(x)
     cores = O.threads()
@@ -106,6 +165,8 @@ def main() -> None:
     torch.cuda.set_device(0)
     cfg, flat, bounds, tok, sizes, starts, q, np = make_workload(args.config, args.train_tokens, args.query_tokens)
     T = sum(sizes)
+    flat_host = flat[: min(args.cpu_tokens, int(flat.numel()))].cpu()
+    q_host = q[: args.cpu_queries + 1].cpu()
     cb = CountBuild.from_device(tok, sizes, starts, levels=cfg.levels, level_shards={}, topk=cfg.topk)
     cb.mode = args.mode
     x, tgt, avail = device_queries(q, cb.lib)
@@ -173,10 +234,15 @@ def main() -> None:
         "levels": info,
         "cpu_baseline": None,
     }
+    if not args.no_secondary:
+        del cb, out, flat, tok, q, x, tgt, avail
+        torch.cuda.empty_cache()
+        log("secondary: c2")
+        res["secondary"] = {"c2": bench_c2(2, 1, not args.no_cpu)}
     if not args.no_cpu:
-        nt = min(args.cpu_tokens, int(flat.numel()))
+        nt = min(args.cpu_tokens, int(flat_host.numel()))
         nq = min(args.cpu_queries, N)
-        cpu = cpu_baseline(flat, bounds, q, cfg.levels, nt, nq)
+        cpu = cpu_baseline(flat_host, bounds, q_host, cfg.levels, nt, nq)
         log(f"cpu baseline: {cpu['seconds']:.1f}s")
         res["cpu_baseline"] = cpu
     print(json.dumps(res), flush=True)

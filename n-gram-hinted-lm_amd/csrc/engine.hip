@@ -242,7 +242,8 @@ __global__ void __launch_bounds__(256) pos_gather_k(const int* __restrict__ ctx_
                                                     const u32* __restrict__ agg, const i64* __restrict__ start,
                                                     const i64* __restrict__ end, const u64* __restrict__ tot,
                                                     const u16* __restrict__ top_tok, const u32* __restrict__ top_cnt,
-                                                    int ktop, int kout, int li, int* __restrict__ out_tot,
+                                                    const u64* __restrict__ thr, int ktop, int kout, int li,
+                                                    int* __restrict__ out_tot,
                                                     int* __restrict__ out_dist,
                                                     int* __restrict__ out_cnt, u16* __restrict__ out_tok,
                                                     u32* __restrict__ out_tcnt, int* __restrict__ mask) {
@@ -262,7 +263,12 @@ __global__ void __launch_bounds__(256) pos_gather_k(const int* __restrict__ ctx_
         if (uk[m] < want) a = m + 1;
         else b = m;
     }
-    if (a < e && uk[a] == want) out_cnt[i] = (int)agg[a];
+    if (a < e && uk[a] == want) {
+        const u32 n = agg[a];
+        // the CNT_TOP rule: with a threshold, only a pair ranked at or above it (its score >= thr) gives its count
+        const u64 th = thr ? thr[c] : 0;
+        if (th == 0 || rank_score(want, n) >= th) out_cnt[i] = (int)n;
+    }
     for (int r = 0; r < kout; ++r) {
         out_tok[i * kout + r] = top_tok[c * ktop + r];
         out_tcnt[i * kout + r] = top_cnt[c * ktop + r];
@@ -321,15 +327,16 @@ extern "C" int ng_ctx_topk(const u64* uk, const u32* agg, const i64* start, cons
 }
 
 // Per query position: tot, dist, cnt, the first kout <= ktop top entries (out_tok/out_tcnt [N, kout]; kout 0: none)
-// and mask bit li (mask may be NULL).
+// and mask bit li (mask may be NULL). thr (may be NULL): per context the score (count << 16 | 65535 - token) of its
+// last pair that still gives cnt (0: every pair does).
 extern "C" int ng_pos_gather(const int* ctx_of, i64 N, i64 lo, i64 hi, const u16* tgt, const u64* uk, const u32* agg,
                              const i64* start, const i64* end, const u64* tot, const u16* top_tok, const u32* top_cnt,
-                             int ktop, int kout, int li, int* out_tot, int* out_dist, int* out_cnt, u16* out_tok,
-                             u32* out_tcnt, int* mask, void* stream) {
+                             const u64* thr, int ktop, int kout, int li, int* out_tot, int* out_dist, int* out_cnt,
+                             u16* out_tok, u32* out_tcnt, int* mask, void* stream) {
     if (kout < 0 || kout > ktop || (mask && (li < 0 || li > 30))) return -1;
     if (N > 0)
         pos_gather_k<<<grid_for(N, 256), 256, 0, (hipStream_t)stream>>>(ctx_of, N, lo, hi, tgt, uk, agg, start, end, tot,
-                                                                        top_tok, top_cnt, ktop, kout, li, out_tot,
+                                                                        top_tok, top_cnt, thr, ktop, kout, li, out_tot,
                                                                         out_dist, out_cnt, out_tok, out_tcnt, mask);
     return (int)hipGetLastError();
 }

@@ -1,0 +1,324 @@
+"""Corpus-wide exact count tables on one MI355X behind exact_match's CountTable surface (exact_match/exact_match.pyi
+:100-118; exact_match/src/count_table.rs :173-438): `create` (read the shards, before the clock), `build` (on the
+clock: every level), `query_counts`, `query_rows`, `sizes`, `release`, `levels`, `tokens`; plus `query_topk` (each
+level's top-k next tokens per position, BASELINE's second configuration) and `query_device` (the same on GPU
+tensors, for callers that keep their queries in device memory).
+
+Definitions (count_table.rs:6-9, kgram.rs's): an occurrence of a k-context is any k consecutive tokens within one
+shard and the token after them (it may cross a BOS); a query position's k-context is the k tokens ending at it, valid
+iff they lie in its segment (segments start at the first query token and at every BOS). Per level and position:
+tot (uint32), dist (uint16, at most 65535), cnt (uint32: the count of the position's next token if among its
+context's top CNT_TOP = 1024 next tokens by count descending then token ascending, or any rank when top >= 65536);
+0 where the context is invalid or never occurred. Keys: packed tokens for k <= 4 (exact), a 64-bit polynomial hash
+beyond (count_table.rs:11-14: ~2^-64 per pair of contexts to merge).
+
+GPU layout per level (libngram_amd.so: ng_table_build, ng_table_compact, sort_pairs, seg_bounds, ng_ctx_topk,
+ng_ctx_kth, ng_table_lookup, ng_pos_gather, ng_pos_rows): the context table (u64 keys, slot = context id), the pairs
+sorted by (slot << 16 | token) with their u32 counts, per slot its pair range, total, top-8 and the CNT_TOP
+threshold."""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import torch
+
+from .data import BOS, HEADER_BYTES, shard_tokens
+from .gpu_val_stats import layout
+from .lib import Lib, i32, u64
+
+CNT_TOP = 1024
+TOPE = 8
+COUNTS = (2, 3, 5, 9, 17, 33)
+PURITIES = (0.3, 0.5, 0.7, 0.85, 0.95)
+LOAD = 0.7
+
+
+def _segments_device(x: torch.Tensor, lib: Lib) -> torch.Tensor:
+    """avail of query inputs x (int16 tensor): tokens since the segment start, a segment starting at 0 and at BOS."""
+    n = x.numel()
+    idx = torch.arange(n, device=x.device)
+    start = (x.to(torch.int32) & 0xFFFF) == BOS
+    start[:1] = True
+    seg = torch.empty_like(idx)
+    if n:
+        lib.cub("inclusive_max", torch.where(start, idx, torch.zeros_like(idx)), seg, n)
+    return (idx - seg + 1).to(torch.int32)
+
+
+class _Level:
+    """One built level on the GPU."""
+
+    def __init__(self, k, ck, ccap, uk, agg, start, end, tot, top_tok, top_cnt, thr, U, contexts):
+        self.k, self.ck, self.ccap = k, ck, ccap
+        self.uk, self.agg, self.start, self.end = uk, agg, start, end
+        self.tot, self.top_tok, self.top_cnt, self.thr = tot, top_tok, top_cnt, thr
+        self.pairs, self.contexts = U, contexts
+
+
+class CountTable:
+    """Exact next-token counts of every k-context (k of `levels`) in the training shards (count_table.rs), on the GPU:
+    create before the clock, build on it, query the validation tokens (inputs + the last target) after it."""
+
+    def __init__(self):
+        raise TypeError("use CountTable.create(files, levels, threads, cpus)")
+
+    @staticmethod
+    def create(files: list, levels: list[int], threads: int = 1, cpus: list[int] = (), huge_pages: bool = False,
+               device=None) -> "CountTable":
+        """Before the clock: read the shards `files` (paths; uint16 arrays are also taken) into GPU memory in the
+        layout of the scans (SENT gaps). `threads`, `cpus` and `huge_pages` are the CPU build's and have no effect
+        here. ValueError on no files, levels not ascending from >= 1, a bad shard or a token above BOS."""
+        levels = list(levels)
+        if not files or not levels or levels[0] < 1 or any(a >= b for a, b in zip(levels, levels[1:])) or threads < 1:
+            raise ValueError(f"need files, ascending levels >= 1 and threads: {levels}")
+        self = object.__new__(CountTable)
+        self.lib = Lib()
+        self._levels = levels
+        dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+        arrays = []
+        for f in files:
+            if isinstance(f, (str, bytes, os.PathLike)):
+                n = shard_tokens(f)
+                arrays.append(np.fromfile(f, dtype="<u2", count=n, offset=HEADER_BYTES))
+            else:
+                arrays.append(np.ascontiguousarray(f, dtype=np.uint16))
+        if any(len(a) and int(a.max()) > BOS for a in arrays):
+            raise ValueError("invalid GPT-2 token in the shards")
+        self.sizes_ = [len(a) for a in arrays]
+        self.starts, self.L = layout(self.sizes_)
+        self.tok = torch.full((self.L,), -1, dtype=torch.int16, device=dev)
+        for a, st in zip(arrays, self.starts):
+            if len(a):
+                self.tok[st : st + len(a)].copy_(torch.from_numpy(a.view(np.int16)))
+        self._tokens = int(sum(self.sizes_))
+        self.tables: list[_Level] = []
+        self.built = self.released = False
+        self.grid = torch.cuda.get_device_properties(dev).multi_processor_count * 32
+        self.events: list = []
+        torch.cuda.synchronize(dev)
+        return self
+
+    @classmethod
+    def from_device(cls, tok: torch.Tensor, sizes: list[int], starts: list[int], levels: list[int]) -> "CountTable":
+        """A table over shards already laid out in GPU memory (`tok` int16 with SENT gaps at layout()'s starts)."""
+        self = object.__new__(CountTable)
+        self.lib = Lib()
+        self._levels = list(levels)
+        self.sizes_, self.starts, self.L = list(sizes), list(starts), int(tok.numel())
+        self.tok = tok
+        self._tokens = int(sum(sizes))
+        self.tables, self.built, self.released = [], False, False
+        self.grid = torch.cuda.get_device_properties(tok.device).multi_processor_count * 32
+        self.events = []
+        return self
+
+    @property
+    def levels(self) -> list[int]:
+        return list(self._levels)
+
+    @property
+    def tokens(self) -> int:
+        return self._tokens
+
+    def build(self) -> None:
+        """On the clock: build every level (once)."""
+        if self.built or self.released:
+            raise ValueError("the count table is already built")
+        self.built = True
+        self.reruns = {}
+        for k in self._levels:
+            self.tables.append(self._build_level(k))
+
+    def _timed(self, name: str, k: int):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        self.events.append((name, k, e0, e1))
+        return e0, e1
+
+    def _build_level(self, k: int) -> _Level:
+        lib, dev = self.lib, self.tok.device
+        n_k = sum(max(0, n - k) for n in self.sizes_)  # occurrences: an upper bound of contexts and of pairs
+        ccap = max(1 << 16, int(n_k / LOAD) + 1)
+        pcap = ccap
+        reruns = 0
+        while True:
+            if ccap >= 1 << 31:
+                raise RuntimeError(f"k={k}: {n_k} occurrences need more than 2^31 context slots")
+            ck = torch.full((ccap,), -1, dtype=torch.int64, device=dev)
+            pk = torch.full((pcap,), -1, dtype=torch.int64, device=dev)
+            pc = torch.zeros(pcap, dtype=torch.int32, device=dev)
+            flags = torch.zeros(2, dtype=torch.int32, device=dev)
+            e0, e1 = self._timed("table_build", k)
+            e0.record()
+            lib("ng_table_build", self.tok, self.L, i32(k), ck, u64(ccap), pk, pc, u64(pcap), flags, i32(self.grid))
+            e1.record()
+            f = int(flags[0].item())
+            if f == 0:
+                break
+            reruns += 1
+            if f & 2:
+                ccap *= 2
+            if f & 1:
+                pcap *= 2
+            del ck, pk, pc
+        self.reruns[k] = reruns
+        counter = torch.zeros(1, dtype=torch.int64, device=dev)
+        ckeys = torch.empty(pcap, dtype=torch.int64, device=dev)
+        ccnt = torch.empty(pcap, dtype=torch.int32, device=dev)
+        e0, e1 = self._timed("compact", k)
+        e0.record()
+        lib("ng_table_compact", pk, pc, u64(pcap), ckeys, ccnt, counter)
+        e1.record()
+        del pk, pc
+        U = int(counter.item())
+        uk = torch.empty(U, dtype=torch.int64, device=dev)
+        agg = torch.empty(U, dtype=torch.int32, device=dev)
+        ctx_bits = max(1, (ccap - 1).bit_length())
+        e0, e1 = self._timed("sort", k)
+        e0.record()
+        if U:
+            lib.cub("sort_pairs", ckeys, uk, ccnt, agg, U, i32(0), i32(16 + ctx_bits))
+        e1.record()
+        del ckeys, ccnt
+        start = torch.zeros(ccap, dtype=torch.int64, device=dev)
+        end = torch.zeros(ccap, dtype=torch.int64, device=dev)
+        tot = torch.zeros(ccap, dtype=torch.int64, device=dev)
+        top_tok = torch.zeros(ccap * TOPE, dtype=torch.int16, device=dev)
+        top_cnt = torch.zeros(ccap * TOPE, dtype=torch.int32, device=dev)
+        thr = torch.zeros(ccap, dtype=torch.int64, device=dev)
+        e0, e1 = self._timed("ctx_stats", k)
+        e0.record()
+        lib("seg_bounds", uk, U, start, end)
+        lib("ng_ctx_topk", uk, agg, start, end, ccap, i32(TOPE), tot, top_tok, top_cnt)
+        deep = ((end - start) > CNT_TOP).nonzero().squeeze(1)
+        if deep.numel():
+            lib("ng_ctx_kth", uk, agg, start, end, deep, deep.numel(), i32(CNT_TOP), thr)
+        e1.record()
+        if ccap and int(tot.max().item()) >= 1 << 32:
+            raise RuntimeError(f"k={k}: a context's total does not fit uint32")
+        contexts = int((end > start).sum().item())
+        return _Level(k, ck, ccap, uk, agg, start, end, tot, top_tok, top_cnt, thr, U, contexts)
+
+    def _check(self):
+        if not self.built or self.released or len(self.tables) != len(self._levels):
+            raise ValueError("the count table is not built (or released)")
+
+    @staticmethod
+    def _host_tokens(tokens) -> np.ndarray:
+        x = np.ascontiguousarray(tokens, dtype=np.uint16)
+        if x.ndim != 1 or len(x) < 2 or int(x.max()) > BOS:
+            raise ValueError("need 2+ valid tokens")
+        return x
+
+    def _slots(self, x: torch.Tensor, avail: torch.Tensor, lv: _Level) -> torch.Tensor:
+        n = x.numel()
+        keys = torch.empty(n, dtype=torch.int64, device=x.device)
+        slot = torch.empty(n, dtype=torch.int32, device=x.device)
+        self.lib("val_keys", x, avail, n, i32(lv.k), keys)
+        self.lib("ng_table_lookup", keys, n, lv.ck, u64(lv.ccap), slot)
+        return slot
+
+    def query_device(self, x: torch.Tensor, tgt: torch.Tensor, avail: torch.Tensor, top: int = CNT_TOP,
+                     topk: int = 0) -> dict:
+        """Per position and level on the GPU: counts int32 [3, L, n] (tot, dist, cnt; tot and cnt as uint32 bits) and
+        with topk > 0 top_tok int16 [L, n, topk] / top_cnt int32 [L, n, topk] (uint16/uint32 bits)."""
+        self._check()
+        if top != CNT_TOP and top < 1 << 16:
+            raise ValueError(f"top must be {CNT_TOP} or at least 65536")
+        if not 0 <= topk <= TOPE:
+            raise ValueError(f"topk must be in [0, {TOPE}]")
+        n, L = x.numel(), len(self.tables)
+        out = torch.zeros((3, L, n), dtype=torch.int32, device=x.device)
+        res = {"counts": out}
+        if topk:
+            res["top_tok"] = torch.zeros((L, n, topk), dtype=torch.int16, device=x.device)
+            res["top_cnt"] = torch.zeros((L, n, topk), dtype=torch.int32, device=x.device)
+        for li, lv in enumerate(self.tables):
+            slot = self._slots(x, avail, lv)
+            e0, e1 = self._timed("pos_gather", lv.k)
+            e0.record()
+            self.lib("ng_pos_gather", slot, n, 0, lv.ccap, tgt, lv.uk, lv.agg, lv.start, lv.end, lv.tot, lv.top_tok,
+                     lv.top_cnt, lv.thr if top == CNT_TOP else None, i32(TOPE), i32(topk), i32(0), out[0, li],
+                     out[1, li], out[2, li], res["top_tok"][li] if topk else None,
+                     res["top_cnt"][li] if topk else None, None)
+            e1.record()
+        return res
+
+    def _device_inputs(self, tokens):
+        x = self._host_tokens(tokens)
+        dev = self.tok.device
+        xt = torch.from_numpy(x.view(np.int16)).to(dev)
+        inp, tgt = xt[:-1], xt[1:]
+        return inp, tgt, _segments_device(inp, self.lib)
+
+    def query_counts(self, tokens, top: int = CNT_TOP):
+        """Per position of `tokens` (the inputs, then the last one's next token) and level: tot (uint32), dist
+        (uint16), cnt (uint32), each [n, levels] (count_table.rs query_counts :287-331)."""
+        self._check()
+        if top != CNT_TOP and top < 1 << 16:
+            raise ValueError(f"top must be {CNT_TOP} or at least 65536")
+        x, tgt, avail = self._device_inputs(tokens)
+        c = self.query_device(x, tgt, avail, top)["counts"]
+        tot = c[0].t().contiguous().cpu().numpy().view(np.uint32)
+        dist = c[1].t().contiguous().to(torch.int16).cpu().numpy().view(np.uint16)
+        cnt = c[2].t().contiguous().cpu().numpy().view(np.uint32)
+        return tot, dist, cnt
+
+    def query_topk(self, tokens, k: int = 4):
+        """Per position and level its context's k most frequent next tokens (uint16 [n, levels, k], count
+        descending then token ascending, 0-padded) and their counts (uint32 [n, levels, k])."""
+        self._check()
+        x, tgt, avail = self._device_inputs(tokens)
+        r = self.query_device(x, tgt, avail, CNT_TOP, k)
+        tt = r["top_tok"].permute(1, 0, 2).contiguous().cpu().numpy().view(np.uint16)
+        tc = r["top_cnt"].permute(1, 0, 2).contiguous().cpu().numpy().view(np.uint32)
+        return tt, tc
+
+    def query_rows(self, tokens, row_levels: list[int], buckets: list[int], entries: int = TOPE):
+        """Per position the hint row of the deepest of `row_levels` whose context occurred: cell (int16), its
+        `entries` most frequent next tokens (uint16 [n, entries]), weights (uint16: round(count / their sum * 65535),
+        ties to even), and its level's index in `buckets` (int8, -1 without a hint) (count_table.rs :338-404)."""
+        self._check()
+        if not 1 <= entries <= TOPE:
+            raise ValueError(f"need 2+ valid tokens and 1 <= entries <= {TOPE}")
+        x, tgt, avail = self._device_inputs(tokens)
+        use = []
+        for k in row_levels:
+            if k not in self._levels:
+                raise ValueError(f"level {k} is not in the table")
+            if k not in buckets:
+                raise ValueError(f"level {k} is not in buckets")
+            use.append((self._levels.index(k), list(buckets).index(k)))
+        use.sort(key=lambda tb: -self._levels[tb[0]])
+        n = x.numel()
+        dev = x.device
+        slots = [self._slots(x, avail, self.tables[t]) for t, _ in use]
+        desc = []
+        for (t, b), slot in zip(use, slots):
+            lv = self.tables[t]
+            desc += [slot.data_ptr(), lv.tot.data_ptr(), lv.top_tok.data_ptr(), lv.top_cnt.data_ptr(), b]
+        desc_t = torch.tensor(desc if desc else [0], dtype=torch.int64, device=dev)
+        cell = torch.zeros(n, dtype=torch.int16, device=dev)
+        nxt = torch.zeros((n, entries), dtype=torch.int16, device=dev)
+        w = torch.zeros((n, entries), dtype=torch.int16, device=dev)
+        level = torch.full((n,), -1, dtype=torch.int8, device=dev)
+        self.lib("ng_pos_rows", n, i32(len(use)), desc_t, i32(entries), cell, nxt, w, level)
+        torch.cuda.current_stream().synchronize()  # desc_t's pointers stay valid until the kernel ran
+        return (cell.cpu().numpy(), nxt.cpu().numpy().view(np.uint16), w.cpu().numpy().view(np.uint16),
+                level.cpu().numpy())
+
+    def sizes(self) -> list[tuple[int, int, int, int]]:
+        """Per level (as built): (k, contexts, pairs, bytes held on the GPU)."""
+        out = []
+        for lv in self.tables:
+            b = sum(t.numel() * t.element_size() for t in (lv.ck, lv.uk, lv.agg, lv.start, lv.end, lv.tot,
+                                                             lv.top_tok, lv.top_cnt, lv.thr))
+            out.append((lv.k, lv.contexts, lv.pairs, b))
+        return out
+
+    def release(self) -> None:
+        """Off the clock: free the tables and the corpus copy."""
+        self.released = True
+        self.tables = []
+        self.tok = None

@@ -398,7 +398,7 @@ class CountBuild:
         e0, e1 = self._event("pos_gather", k, -1, N)
         e0.record()
         kout = self.topk
-        elib("ng_pos_gather", vi.ctx_of, N, lo, hi, tgt, uk, agg, start, end, tot, top_tok, top_cnt, i32(ktop),
+        elib("ng_pos_gather", vi.ctx_of, N, lo, hi, tgt, uk, agg, start, end, tot, top_tok, top_cnt, None, i32(ktop),
              i32(kout), i32(li), out[0, li], out[1, li], out[2, li], self.top_tok[li] if kout else None,
              self.top_cnt[li] if kout else None, None)
         e1.record()

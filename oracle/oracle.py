@@ -279,6 +279,33 @@ def features(counts: np.ndarray):
     return tot, dist, cnt, b, s
 
 
+def table_rows(per_level: dict[int, Outputs], row_levels, buckets, entries: int = 8):
+    """exact_match/src/count_table.rs query_rows (:338-404): per position the deepest of `row_levels` whose context
+    occurred -> (cell int16 [N], next uint16 [N, entries], weights uint16 [N, entries], level int8 [N]); weights are
+    round_ties_even(count / sum of the kept counts * 65535) in float64."""
+    n = len(next(iter(per_level.values()))["tot"])
+    cell = np.zeros(n, np.int16)
+    nxt = np.zeros((n, entries), np.uint16)
+    w = np.zeros((n, entries), np.uint16)
+    level = np.full(n, -1, np.int8)
+    filled = np.zeros(n, bool)
+    for k in sorted(row_levels, reverse=True):
+        o = per_level[k]
+        b = list(buckets).index(k)
+        at = np.flatnonzero((o["tot"] > 0) & ~filled)
+        total = o["tot"][at].astype(np.float64)
+        top1 = o["top_cnt"][at, 0].astype(np.float64)
+        count_bin = np.searchsorted(COUNT_EDGES, total, side="right")
+        purity = np.searchsorted(PURITY_EDGES, top1 / total, side="right")
+        cell[at] = ((1 + b) * (len(COUNT_EDGES) + 1) + count_bin) * (len(PURITY_EDGES) + 1) + purity
+        kept = o["top_cnt"][at, :entries].astype(np.float64)
+        w[at] = np.round(kept / kept.sum(1, keepdims=True) * WEIGHT_ONE).astype(np.uint16)
+        nxt[at] = o["top_tok"][at, :entries]
+        level[at] = b
+        filled[at] = True
+    return cell, nxt, w, level
+
+
 ROW_LEVELS = (6, 10, 20)
 ROW_K = 8
 

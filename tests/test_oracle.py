@@ -157,3 +157,24 @@ def test_shard_file_roundtrip(tmp_path):
     bad.write_bytes(b"\0" * 1024)
     with pytest.raises(ValueError):
         data.shard_tokens(bad)
+
+
+def test_table_rows_by_hand():
+    # two positions, row levels (2, 3): position 0 matched level 3 (total 4, counts 3, 1 -> tokens 7, 9), position 1
+    # only level 2 (total 40, top 10 of it): entries = 2
+    per = {}
+    for k, tot, cnts, toks in ((2, (40, 40), (10, 6), (5, 6)), (3, (4, 0), (3, 1), (7, 9))):
+        o = O._alloc(2, 8)
+        o["tot"][:] = tot
+        for i in range(2):
+            if tot[i]:
+                o["top_cnt"][i, :2] = cnts
+                o["top_tok"][i, :2] = toks
+        per[k] = o
+    cell, nxt, w, level = O.table_rows(per, (2, 3), buckets=(1, 2, 3), entries=2)
+    # position 0: bucket 2 (level 3), count bin #{2,3 <= 4} = 2, purity 3/4 = .75 -> #{.3,.5,.7} = 3
+    assert cell[0] == ((1 + 2) * 7 + 2) * 6 + 3 and level[0] == 2
+    assert list(nxt[0]) == [7, 9] and list(w[0]) == [round(3 / 4 * 65535), round(1 / 4 * 65535)]
+    # position 1: bucket 1, count bin 6 (40 >= 33), purity 10/40 = .25 -> 0; weights 10/16, 6/16 of the kept counts
+    assert cell[1] == ((1 + 1) * 7 + 6) * 6 + 0 and level[1] == 1
+    assert list(w[1]) == [40959, 24576]  # 40959.375, 24575.625
