@@ -130,6 +130,60 @@ def bench_c2(steps: int, warmup: int, with_cpu: bool) -> dict:
     return res
 
 
+def bench_c5(tok, flat, steps: int, warmup: int, with_cpu: bool) -> dict:
+    """BASELINE's fifth configuration over the c3 corpus already in `tok` (`flat`: its tokens without gaps): a
+    held-out 64M-token stream (15% of documents with a copied span of 16-2048 corpus tokens), queried at every
+    fourth position (16M positions): the longest exact suffix match (cap 64), its top next token and count."""
+    import numpy as np
+    import torch
+
+    from ngram_amd import data
+    from ngram_amd.lib import Lib
+    from ngram_amd.longest import _segments, longest_match
+
+    c3 = data.CONFIGS["c3"]
+    zipf, tp, _ = data.make_plans(c3)
+    n = 64_000_000 + 1
+    qp = data.make_plan(data.stream_key("c5", "query", n), n, copy_rate=0.15, copy_len=(16, 2048), source=tp)
+    lib = Lib()
+    q = data.realize_gpu(qp, zipf, lib, source=flat)
+    x = q[:-1]
+    avail = _segments(x, lib)
+    query = torch.zeros(x.numel(), dtype=torch.bool, device=x.device)
+    query[3::4] = True
+    nq = int(query.sum().item())
+    times, timing = [], {}
+    for step in range(warmup + steps):
+        timing.clear()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        length, nxt, cnt, ladder = longest_match(tok, x, avail, 64, timing=timing, query=query)
+        torch.cuda.synchronize()
+        if step >= warmup:
+            times.append(time.perf_counter() - t0)
+    dt = sum(times) / len(times)
+    T = int(flat.numel())
+    hist = torch.bincount(length[query].long(), minlength=65).cpu().tolist()
+    res = {"value": T / dt, "unit": "corpus tokens/s", "query_positions_per_s": nq / dt, "ms_per_step": dt * 1e3,
+           "workload": f"c5: longest exact suffix match (cap 64) + top next token and count of {nq} positions of a "
+                       f"64M-token held-out stream against {T} corpus tokens", "phases_s": dict(timing),
+           "levels": len(ladder), "length_histogram": hist}
+    if with_cpu:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as O
+
+        n_t, n_q = 100_000_000, 200_000
+        train = flat[:n_t].cpu().numpy().view(np.uint16)
+        xs = x[: 4 * n_q].cpu().numpy().view(np.uint16)
+        t0 = time.perf_counter()
+        O.longest_match(train, np.array([0, n_t], np.int64), xs, O.segments(xs), 64, nthreads=O.threads())
+        cdt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": n_t / cdt, "unit": "corpus tokens/s", "cores": O.threads(), "kind": "port",
+                               "sample": f"kgram.rs-style ladder over the first {n_t} corpus tokens x {4 * n_q} "
+                                         f"contiguous query positions, cap 64; {cdt:.1f} s"}
+    return res
+
+
 def cpu_baseline(flat, bounds, q, levels, n_tokens: int, n_queries: int) -> dict:
     """The oracle's query-filtered counting (C++ restatement of kgram.rs, one thread per core) over a bounded sample:
     the corpus' first n_tokens tokens and the first n_queries query positions, every level."""
@@ -235,10 +289,15 @@ def main() -> None:
         "cpu_baseline": None,
     }
     if not args.no_secondary:
-        del cb, out, flat, tok, q, x, tgt, avail
+        del cb, out, q, x, tgt, avail
+        torch.cuda.empty_cache()
+        res["secondary"] = {}
+        log("secondary: c5")
+        res["secondary"]["c5"] = bench_c5(tok, flat, 2, 1, not args.no_cpu)
+        del flat, tok
         torch.cuda.empty_cache()
         log("secondary: c2")
-        res["secondary"] = {"c2": bench_c2(2, 1, not args.no_cpu)}
+        res["secondary"]["c2"] = bench_c2(2, 1, not args.no_cpu)
     if not args.no_cpu:
         nt = min(args.cpu_tokens, int(flat_host.numel()))
         nq = min(args.cpu_queries, N)

@@ -88,6 +88,55 @@ __global__ void __launch_bounds__(256) scan_count_sparse_k(const u16* __restrict
     }
 }
 
+// Existence only (the first phase of the longest match): the hit bitmap, and hit[context id] = 1 for every query
+// context that occurred (plain byte stores: every writer stores the same value).
+template <int K>
+__global__ void __launch_bounds__(256) scan_exist_dense_k(const u16* __restrict__ tok, i64 L, int k,
+                                                          const u32* __restrict__ bm_in, u32* __restrict__ bm_out,
+                                                          const u64* __restrict__ vt, u64 vcap, const u32* __restrict__ vrep,
+                                                          const u16* __restrict__ x, unsigned char* __restrict__ hit,
+                                                          u32* flags) {
+    const int lane = lane_id();
+    const i64 nwords = (L + 31) >> 5;
+    const i64 stride = (i64)gridDim.x * blockDim.x;
+    for (i64 base = blockIdx.x * (i64)blockDim.x + (threadIdx.x & ~(WAVE - 1)); base < L; base += stride) {
+        const i64 p = base + lane;
+        const i64 w = (base >> 5) + (lane >> 5);
+        u32 word = 0xFFFFFFFFu;
+        if (bm_in) word = w < nwords ? bm_in[w] : 0u;
+        u64 key = EMPTY;
+        if (p < L && ((word >> (lane & 31)) & 1u)) key = probe_key<K>(tok, p, k, vt, vcap, vrep, x, flags);
+        const u64 b = __ballot(key != EMPTY);
+        if (lane == 0) bm_out[base >> 5] = (u32)b;
+        if (lane == 32 && w < nwords) bm_out[w] = (u32)(b >> 32);
+        if (key != EMPTY) hit[key >> 16] = 1;
+    }
+}
+
+template <int K>
+__global__ void __launch_bounds__(256) scan_exist_sparse_k(const u16* __restrict__ tok, i64 L, int k,
+                                                           const u32* __restrict__ bm_in, u32* __restrict__ bm_out,
+                                                           const u64* __restrict__ vt, u64 vcap, const u32* __restrict__ vrep,
+                                                           const u16* __restrict__ x, unsigned char* __restrict__ hit,
+                                                           u32* flags) {
+    const i64 nwords = (L + 31) >> 5;
+    for (i64 w = blockIdx.x * (i64)blockDim.x + threadIdx.x; w < nwords; w += (i64)gridDim.x * blockDim.x) {
+        u32 word = bm_in[w], out = 0;
+        while (word) {
+            const int b = __ffs(word) - 1;
+            word &= word - 1;
+            const i64 p = (w << 5) + b;
+            if (p >= L) continue;
+            const u64 key = probe_key<K>(tok, p, k, vt, vcap, vrep, x, flags);
+            if (key != EMPTY) {
+                out |= 1u << b;
+                hit[key >> 16] = 1;
+            }
+        }
+        bm_out[w] = out;
+    }
+}
+
 // Occupied slots appended to (out_k, out_c): a block-wide count, one global atomic per block and tile.
 #define CP_ITEMS 8
 __global__ void __launch_bounds__(256) table_compact_k(const u64* __restrict__ keys, const u32* __restrict__ cnts, u64 cap,
@@ -295,6 +344,22 @@ extern "C" int ng_scan_count(const u16* tok, i64 L, int k, const u32* bm_in, u32
         LEVEL_SWITCH(k, (scan_count_sparse_k<K><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, keys, cnts, cap, flags)));
     } else {
         LEVEL_SWITCH(k, (scan_count_dense_k<K><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, keys, cnts, cap, flags)));
+    }
+    return (int)hipGetLastError();
+}
+
+// One level's existence scan: bm_out = the corpus positions (gated by bm_in) whose k-context is a query context of the
+// table, hit[id] = 1 for each such context id (hit zeroed by the caller).
+extern "C" int ng_scan_exist(const u16* tok, i64 L, int k, const u32* bm_in, u32* bm_out, const u64* vt, u64 vcap,
+                             const u32* vrep, const u16* x, unsigned char* hit, u32* flags, int grid, int sparse,
+                             void* stream) {
+    if (L <= 0) return 0;
+    if (grid <= 0) grid = grid_for(L, 256);
+    hipStream_t st = (hipStream_t)stream;
+    if (sparse && bm_in) {
+        LEVEL_SWITCH(k, (scan_exist_sparse_k<K><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, hit, flags)));
+    } else {
+        LEVEL_SWITCH(k, (scan_exist_dense_k<K><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, hit, flags)));
     }
     return (int)hipGetLastError();
 }

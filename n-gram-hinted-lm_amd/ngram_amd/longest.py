@@ -1,0 +1,201 @@
+"""Longest exact suffix match of query positions against a training corpus on one MI355X (BASELINE's fifth
+configuration; the match-length notion of exact_match/src/kgram.rs kgram_stats :38-56, 237-278, taken up to k = 64 by
+src/retrieval_blog_post/kgram.py :16, 84-108): per query position i the largest k <= cap whose k-context
+x[i-k+1..i] is valid (within its segment) and occurred in the corpus (k tokens within one shard followed by a token
+of that shard), that context's most frequent next token (count descending, then token ascending) and its count; 0, 0,
+0 if not even the 1-context occurred.
+
+Two phases, both on libngram_amd.so. Existence, k = 1, 2, ...: the query contexts of the positions still matching
+(a query index per level), the corpus positions whose (k-1)-context matched (a hit bitmap per level) probed for
+their k-context (ng_scan_exist: a bitmap and a per-context hit flag, no counting), until no position matches. A match
+is monotone in k (kgram.rs:12-15), so each position's length is its last matching level. Then counting, only for each
+position's final context: per level, the final contexts' query index, the corpus positions of that level's bitmap
+probed and (context, next) counted in a split pair table (ng_scan_count), the pairs sorted, each context's top entry
+(ng_ctx_topk) gathered to its positions (ng_pos_gather). Most positions match past the short levels, whose contexts
+are the corpus' most frequent: counting only final contexts skips nearly all of their occurrences.
+
+Surfaces: `longest_match(...)` on GPU tensors, and `LongestMatch.create(files, tokens, threads, cpus)` /
+`build() -> dict` in cache_ladder's shape (cache_ladder/src/lib.rs:1-8, cache_ladder.pyi)."""
+
+from __future__ import annotations
+
+import os
+import time
+
+import numpy as np
+import torch
+
+from .counts import MAX_IDS, record_lib
+from .data import BOS, HEADER_BYTES, shard_tokens
+from .gpu_val_stats import ValIndex, layout
+from .lib import Lib, i32, u64
+
+LOAD = 0.7
+
+
+def _popcount(lib: Lib, bm: torch.Tensor) -> int:
+    c = torch.zeros(1, dtype=torch.int64, device=bm.device)
+    lib("popcount", bm, bm.numel(), c)
+    return int(c.item())
+
+
+def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: int = 64, elib: Lib | None = None,
+                  lib: Lib | None = None, timing: dict | None = None, query: torch.Tensor | None = None):
+    """Per query position (x int16 [N] inputs, avail int32 [N] tokens since the segment start): (length int32,
+    next int16 (uint16 bits), count int32 (uint32 bits)) of its longest match <= cap, and per level
+    (k, eligible, matched) over the existence phase. `tok`: the corpus laid out with SENT gaps (layout()).
+    `query` (bool [N], optional): only these positions are queried (their contexts still read x before them); the
+    others get 0, 0, 0."""
+    if not 1 <= cap <= 64:
+        raise ValueError("cap must be in [1, 64]")
+    elib = elib or Lib()
+    lib = lib or record_lib()
+    dev = x.device
+    N, L = x.numel(), tok.numel()
+    nwords = L // 32
+    grid = torch.cuda.get_device_properties(dev).multi_processor_count * 32
+    t0 = time.perf_counter()
+    length = torch.zeros(N, dtype=torch.int32, device=dev)
+    active = avail >= 1
+    if query is not None:
+        active &= query
+    bms: list[torch.Tensor] = []
+    prev = None
+    ladder = []
+    flags = torch.zeros(2, dtype=torch.int32, device=dev)
+    for k in range(1, cap + 1):
+        act = active & (avail >= k)
+        n_act = int(act.sum().item())
+        if n_act == 0:
+            break
+        vi = ValIndex(lib, x, torch.where(act, avail, torch.zeros_like(avail)), k, max_ids=MAX_IDS)
+        hit = torch.zeros(vi.ids, dtype=torch.uint8, device=dev)
+        bm = torch.empty(nwords, dtype=torch.int32, device=dev)
+        sparse = prev is not None and _popcount(lib, prev) * 16 < L
+        elib("ng_scan_exist", tok, L, i32(k), prev, bm, vi.table, u64(vi.cap), vi.rep, x, hit, flags, i32(grid),
+             i32(int(sparse)))
+        ctx = vi.ctx_of.long()
+        matched = (ctx >= 0) & (hit[ctx.clamp_min(0)] != 0)
+        length[matched] = k
+        eligible = (avail >= k) if query is None else (avail >= k) & query
+        ladder.append((k, int(eligible.sum().item()), int(matched.sum().item())))
+        active = matched
+        bms.append(bm)
+        prev = bm
+        del vi, hit, ctx
+    if timing is not None:
+        torch.cuda.synchronize()
+        timing["exist"] = timing.get("exist", 0.0) + time.perf_counter() - t0
+        t0 = time.perf_counter()
+    nxt = torch.zeros(N, dtype=torch.int16, device=dev)
+    cnt = torch.zeros(N, dtype=torch.int32, device=dev)
+    scratch_bm = torch.empty(nwords, dtype=torch.int32, device=dev)
+    o_tot = torch.zeros(N, dtype=torch.int32, device=dev)
+    o_dist = torch.zeros(N, dtype=torch.int32, device=dev)
+    o_cnt = torch.zeros(N, dtype=torch.int32, device=dev)
+    for k in range(1, len(bms) + 1):
+        fin = length == k
+        if not bool(fin.any()):
+            continue
+        vi = ValIndex(lib, x, torch.where(fin, avail, torch.zeros_like(avail)), k, max_ids=MAX_IDS)
+        bm_k = bms[k - 1]
+        events = _popcount(lib, bm_k)
+        sparse = events * 16 < L
+        tcap = max(1 << 16, int(min(events, 64 * vi.n + (1 << 20)) / LOAD))
+        while True:
+            keys = torch.full((tcap,), -1, dtype=torch.int64, device=dev)
+            cnts = torch.zeros(tcap, dtype=torch.int32, device=dev)
+            flags.zero_()
+            elib("ng_scan_count", tok, L, i32(k), bm_k, scratch_bm, vi.table, u64(vi.cap), vi.rep, x, keys, cnts,
+                 u64(tcap), flags, i32(grid), i32(int(sparse)))
+            if int(flags[0].item()) == 0:
+                break
+            tcap *= 2
+        counter = torch.zeros(1, dtype=torch.int64, device=dev)
+        ck = torch.empty(tcap, dtype=torch.int64, device=dev)
+        cc = torch.empty(tcap, dtype=torch.int32, device=dev)
+        elib("ng_table_compact", keys, cnts, u64(tcap), ck, cc, counter)
+        del keys, cnts
+        U = int(counter.item())
+        ctx_bits = max(1, (max(vi.ids, 2) - 1).bit_length())
+        uk = torch.empty(U, dtype=torch.int64, device=dev)
+        agg = torch.empty(U, dtype=torch.int32, device=dev)
+        if U:
+            lib.cub("sort_pairs", ck, uk, cc, agg, U, i32(0), i32(16 + ctx_bits))
+        del ck, cc
+        start = torch.zeros(vi.ids, dtype=torch.int64, device=dev)
+        end = torch.zeros(vi.ids, dtype=torch.int64, device=dev)
+        tot = torch.zeros(vi.ids, dtype=torch.int64, device=dev)
+        top_tok = torch.zeros(vi.ids, dtype=torch.int16, device=dev)
+        top_cnt = torch.zeros(vi.ids, dtype=torch.int32, device=dev)
+        lib("seg_bounds", uk, U, start, end)
+        elib("ng_ctx_topk", uk, agg, start, end, vi.ids, i32(1), tot, top_tok, top_cnt)
+        elib("ng_pos_gather", vi.ctx_of, N, 0, vi.ids, x, uk, agg, start, end, tot, top_tok, top_cnt, None, i32(1),
+             i32(1), i32(0), o_tot, o_dist, o_cnt, nxt, cnt, None)
+        del vi, uk, agg, start, end, tot, top_tok, top_cnt
+    if timing is not None:
+        torch.cuda.synchronize()
+        timing["count"] = timing.get("count", 0.0) + time.perf_counter() - t0
+    return length, nxt, cnt, ladder
+
+
+def _segments(x: torch.Tensor, lib: Lib) -> torch.Tensor:
+    n = x.numel()
+    idx = torch.arange(n, device=x.device)
+    start = (x.to(torch.int32) & 0xFFFF) == BOS
+    start[:1] = True
+    seg = torch.empty_like(idx)
+    if n:
+        lib.cub("inclusive_max", torch.where(start, idx, torch.zeros_like(idx)), seg, n)
+    return (idx - seg + 1).to(torch.int32)
+
+
+class LongestMatch:
+    """The longest match as a ladder rung (cache_ladder's interface, cache_ladder/src/lib.rs:1-8): create(files,
+    tokens, threads, cpus) reads the training shards and the query stream (`tokens`: the inputs, then the last one's
+    next token) before the clock; build() runs the match on the clock and returns its timings (seconds) and sizes;
+    afterwards `length`, `next` (uint16) and `count` (uint32) hold the per-position results (numpy)."""
+
+    def __init__(self):
+        raise TypeError("use LongestMatch.create(files, tokens, threads, cpus)")
+
+    @staticmethod
+    def create(files: list, tokens, threads: int = 1, cpus: list[int] = (), cap: int = 64) -> "LongestMatch":
+        self = object.__new__(LongestMatch)
+        arrays = []
+        for f in files:
+            if isinstance(f, (str, bytes, os.PathLike)):
+                n = shard_tokens(f)
+                arrays.append(np.fromfile(f, dtype="<u2", count=n, offset=HEADER_BYTES))
+            else:
+                arrays.append(np.ascontiguousarray(f, dtype=np.uint16))
+        q = np.ascontiguousarray(tokens, dtype=np.uint16)
+        if not arrays or len(q) < 2 or int(q.max()) > BOS or any(len(a) and int(a.max()) > BOS for a in arrays):
+            raise ValueError("need training shards and 2+ valid query tokens")
+        sizes = [len(a) for a in arrays]
+        starts, L = layout(sizes)
+        dev = torch.device("cuda", torch.cuda.current_device())
+        self.tok = torch.full((L,), -1, dtype=torch.int16, device=dev)
+        for a, st in zip(arrays, starts):
+            if len(a):
+                self.tok[st : st + len(a)].copy_(torch.from_numpy(a.view(np.int16)))
+        self.x = torch.from_numpy(q[:-1].view(np.int16).copy()).to(dev)
+        self.cap = cap
+        self.elib, self.lib = Lib(), record_lib()
+        self.avail = _segments(self.x, self.lib)
+        self.tokens = int(sum(sizes))
+        torch.cuda.synchronize()
+        return self
+
+    def build(self) -> dict:
+        timing: dict = {}
+        t0 = time.perf_counter()
+        length, nxt, cnt, ladder = longest_match(self.tok, self.x, self.avail, self.cap, self.elib, self.lib, timing)
+        torch.cuda.synchronize()
+        timing["total"] = time.perf_counter() - t0
+        self.length = length.cpu().numpy().view(np.uint32)
+        self.next = nxt.cpu().numpy().view(np.uint16)
+        self.count = cnt.cpu().numpy().view(np.uint32)
+        self.ladder = ladder
+        timing["levels"] = float(len(ladder))
+        return timing

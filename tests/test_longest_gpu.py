@@ -1,0 +1,51 @@
+"""GPU: the longest exact suffix match (ngram_amd.longest, BASELINE's fifth configuration) against the oracle's
+restatement (oracle_longest_match, pinned by brute force on tiny streams): length, next token, its count."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from ngram_amd import data
+from ngram_amd.counts import record_lib
+from ngram_amd.gpu_val_stats import load_shards
+from ngram_amd.longest import LongestMatch, _segments, longest_match
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def corpus():
+    # held-out queries with 15% of documents carrying copied spans of 16-2048 training tokens: long matches
+    return data.make_corpus("c5", train_tokens=700_000, query_tokens=60_001, shard_tokens=300_000)
+
+
+@pytest.mark.parametrize("cap", [64, 8, 1])
+def test_longest_match_matches_oracle(corpus, cap):
+    x = corpus.query[:-1]
+    avail = O.segments(x)
+    want = O.longest_match(corpus.train, corpus.bounds, x, avail, cap)
+    tok, sizes, starts, L = load_shards(corpus.shards())
+    xt = torch.from_numpy(x.view(np.int16).copy()).cuda()
+    av = _segments(xt, record_lib())
+    assert np.array_equal(av.cpu().numpy(), avail)
+    length, nxt, cnt, ladder = longest_match(tok, xt, av, cap)
+    got = (length.cpu().numpy().view(np.uint32), nxt.cpu().numpy().view(np.uint16), cnt.cpu().numpy().view(np.uint32))
+    for g, w, name in zip(got, want, ("length", "next", "count")):
+        assert np.array_equal(g, w), name
+    assert want[0].max() == cap  # the copies reach the cap
+    # the ladder's matched counts are the positions whose length reaches k
+    for k, eligible, matched in ladder:
+        assert matched == int((want[0] >= k).sum()) and eligible == int((avail >= k).sum())
+
+
+def test_ladder_interface(corpus, tmp_path):
+    paths, _ = corpus.write(tmp_path)
+    lm = LongestMatch.create(paths, corpus.query[:20_001], 4, [])
+    t = lm.build()
+    assert t["total"] > 0 and t["levels"] >= 1
+    x = corpus.query[:20_000]
+    want = O.longest_match(corpus.train, corpus.bounds, x, O.segments(x), 64)
+    assert np.array_equal(lm.length, want[0]) and np.array_equal(lm.next, want[1]) and np.array_equal(lm.count, want[2])
+    with pytest.raises(ValueError):
+        LongestMatch.create(paths, np.array([3], np.uint16))
