@@ -184,6 +184,63 @@ def bench_c5(tok, flat, steps: int, warmup: int, with_cpu: bool) -> dict:
     return res
 
 
+def bench_c4(with_cpu: bool) -> dict:
+    """BASELINE's fourth configuration: 92 steps of 2^19 fresh tokens (copied-span rate ramping 0 -> 20%); each step
+    answers its 2^19 queries (hint rows at n = 2..6: the deepest level with a count, 8 next tokens and weights, and
+    count rows tot / dist / cnt per level) from the occurrences of earlier steps, its own occurrences becoming
+    available to the next step (OnlineRows.advance, the step rule). Per-step latency over all 92 steps."""
+    import numpy as np
+    import torch
+
+    from ngram_amd import data
+    from ngram_amd.lib import Lib
+    from ngram_amd.online import OnlineRows
+
+    zipf, plan, spans = data.c4_stream()
+    tok = data.realize_gpu(plan, zipf, Lib()).cpu().numpy().view(np.uint16)
+    n = len(tok)
+    levels = [2, 3, 4, 5, 6]
+    buckets = [2, 3, 4, 5, 6, 10, 20]
+    rows = OnlineRows(tok, [0, n], spans)
+    rows.prepare(levels, buckets, 8, levels)
+    # one untimed pass over a copy of the state warms the allocator and the kernels
+    warm = OnlineRows(tok, [0, n], spans)
+    warm.prepare(levels, buckets, 8, levels)
+    warm.advance_device(4)
+    torch.cuda.synchronize()
+    del warm
+    lat = []
+    for s in range(len(spans)):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        rows.advance_device(s + 1)
+        torch.cuda.synchronize()
+        lat.append(time.perf_counter() - t0)
+    rows._check_flags(rows.state)
+    lat_ms = np.array(lat) * 1e3
+    step_tokens = int(spans[0, 1] - spans[0, 0])
+    res = {"value": n / sum(lat), "unit": "stream tokens/s (insert + query)", "steps": len(spans),
+           "step_tokens": step_tokens, "ms_per_step_mean": float(lat_ms.mean()),
+           "ms_per_step_median": float(np.median(lat_ms)), "ms_per_step_p99": float(np.percentile(lat_ms, 99)),
+           "ms_per_step_max": float(lat_ms.max()),
+           "workload": f"c4: OnlineRows.advance over {len(spans)} steps x {step_tokens} tokens, hint rows (n={levels}, "
+                       f"8 entries) + count rows per step"}
+    if with_cpu:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as O
+
+        m = 4 * step_tokens
+        sub = tok[:m]
+        tau, tau_in = O.spans_tau(m, [0, m], spans[:4])
+        t0 = time.perf_counter()
+        O.online(sub, [0, m], tau, tau_in, levels, buckets, 8, levels, 0, 4)
+        cdt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": m / cdt, "unit": "stream tokens/s (insert + query)", "cores": 1,
+                               "kind": "port", "sample": f"online.rs step-rule walk (oracle_online, one thread) over "
+                                                         f"the first 4 steps ({m} tokens); {cdt:.1f} s"}
+    return res
+
+
 def cpu_baseline(flat, bounds, q, levels, n_tokens: int, n_queries: int) -> dict:
     """The oracle's query-filtered counting (C++ restatement of kgram.rs, one thread per core) over a bounded sample:
     the corpus' first n_tokens tokens and the first n_queries query positions, every level."""
@@ -298,6 +355,9 @@ def main() -> None:
         torch.cuda.empty_cache()
         log("secondary: c2")
         res["secondary"]["c2"] = bench_c2(2, 1, not args.no_cpu)
+        torch.cuda.empty_cache()
+        log("secondary: c4")
+        res["secondary"]["c4"] = bench_c4(not args.no_cpu)
     if not args.no_cpu:
         nt = min(args.cpu_tokens, int(flat_host.numel()))
         nq = min(args.cpu_queries, N)

@@ -1,0 +1,280 @@
+// Online rows under the step rule on the GPU: the incremental state behind ngram_amd/online.py's OnlineRows (the
+// surface of exact_match/src/online.rs :102-1382; no counterpart in the reference's GPU libraries). Per level k the
+// state persists between steps: a context table (u64 keys, slot = context id) with per-context total, distinct next
+// tokens and its top-E (count descending, then token ascending) as packed scores (count << 16 | 65535 - token), and a
+// split pair table ((slot << 16 | next) keys, u32 counts). A step inserts the occurrences that become available in it,
+// then answers its queries (online.rs:11-13: an occurrence counts for a step-s query iff all its tokens were trained
+// before s). The top-E lists stay exact: a step's touched pairs are sorted and merged into their context's list with
+// their new counts (counts only grow, so untouched tokens outside a list stay below its last entry).
+#include "ngram_common.h"
+
+namespace {
+
+__device__ __forceinline__ i64 octx_find_insert(u64* ck, u64 ccap, u64 key, u32* flags) {
+    u64 s = __umul64hi(key, ccap);
+    for (int probe = 0; probe < MAXPROBE; ++probe) {
+        const u64 cur = ck[s];
+        if (cur == key) return (i64)s;
+        if (cur == EMPTY) {
+            const u64 prev = atomicCAS((unsigned long long*)&ck[s], EMPTY, key);
+            if (prev == EMPTY || prev == key) return (i64)s;
+        }
+        s = s + 1 == ccap ? 0 : s + 1;
+    }
+    atomicOr(&flags[0], 2u);
+    return -1;
+}
+
+__device__ __forceinline__ i64 octx_find(const u64* __restrict__ ck, u64 ccap, u64 key) {
+    u64 s = __umul64hi(key, ccap);
+    for (u64 probe = 0; probe < ccap; ++probe) {
+        const u64 cur = ck[s];
+        if (cur == key) return (i64)s;
+        if (cur == EMPTY) return -1;
+        s = s + 1 == ccap ? 0 : s + 1;
+    }
+    return -1;
+}
+
+// Count a pair; returns 1 if this call inserted it (its first occurrence), 0 if it was there, -1 if the table is full.
+__device__ __forceinline__ int opair_add(u64* keys, u32* cnts, u64 cap, u64 key, u32* flags) {
+    u64 s = __umul64hi(mix64(key), cap);
+    for (int probe = 0; probe < MAXPROBE; ++probe) {
+        const u64 cur = keys[s];
+        if (cur == key) {
+            atomicAdd(&cnts[s], 1u);
+            return 0;
+        }
+        if (cur == EMPTY) {
+            const u64 prev = atomicCAS((unsigned long long*)&keys[s], EMPTY, key);
+            if (prev == EMPTY || prev == key) {
+                atomicAdd(&cnts[s], 1u);
+                return prev == EMPTY ? 1 : 0;
+            }
+        }
+        s = s + 1 == cap ? 0 : s + 1;
+    }
+    atomicOr(&flags[0], 1u);
+    return -1;
+}
+
+__device__ __forceinline__ u32 opair_count(const u64* __restrict__ keys, const u32* __restrict__ cnts, u64 cap, u64 key) {
+    u64 s = __umul64hi(mix64(key), cap);
+    for (u64 probe = 0; probe < cap; ++probe) {
+        const u64 cur = keys[s];
+        if (cur == key) return cnts[s];
+        if (cur == EMPTY) return 0;
+        s = s + 1 == cap ? 0 : s + 1;
+    }
+    return 0;
+}
+
+template <int K>
+__device__ __forceinline__ u64 okey(const u16* e, int k) {
+    if constexpr (K > 0) return ctx_key<K>(e);
+    else return ctx_key_rt(e, k);
+}
+
+// Occurrences ending at pos[i] (context tok[g-k+1..g], next tok[g+1]; the caller lists valid ones only).
+template <int K>
+__global__ void online_insert_k(const u16* __restrict__ tok, const int* __restrict__ pos, i64 m, int k, u64* ck,
+                                u64 ccap, u64* pk, u32* pcnt, u64 pcap, u32* ctx_tot, u32* ctx_dist,
+                                u64* __restrict__ ev, u32* flags) {
+    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    if (i >= m) return;
+    const i64 g = pos[i];
+    const u64 key = okey<K>(tok + g + 1, k);
+    const i64 slot = octx_find_insert(ck, ccap, key, flags);
+    if (slot < 0) {
+        ev[i] = EMPTY;
+        return;
+    }
+    const u64 pair = ((u64)slot << 16) | tok[g + 1];
+    const int added = opair_add(pk, pcnt, pcap, pair, flags);
+    if (added < 0) {
+        ev[i] = EMPTY;
+        return;
+    }
+    atomicAdd(&ctx_tot[slot], 1u);
+    if (added) atomicAdd(&ctx_dist[slot], 1u);
+    ev[i] = pair;
+}
+
+// Scores of a step's distinct touched pairs (sorted), i < *n.
+__global__ void online_scores_k(const u64* __restrict__ uk, const i64* __restrict__ n, i64 m, const u64* __restrict__ pk,
+                                const u32* __restrict__ pcnt, u64 pcap, u64* __restrict__ score) {
+    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    if (i >= m || i >= *n) return;
+    const u64 key = uk[i];
+    if (key == EMPTY) {
+        score[i] = 0;
+        return;
+    }
+    const u32 c = opair_count(pk, pcnt, pcap, key);
+    score[i] = ((u64)c << 16) | (0xFFFFu - (u32)(key & 0xFFFF));
+}
+
+__device__ __forceinline__ void top8_insert(u64 (&t)[8], u64 v) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        if (v > t[j]) {
+            const u64 tmp = t[j];
+            t[j] = v;
+            v = tmp;
+        }
+}
+
+// One thread per context group of the sorted touched pairs: the context's top-E list merged with the group's new
+// scores (an old entry of a touched token is superseded by its new score).
+__global__ void online_top_k(const u64* __restrict__ uk, const u64* __restrict__ score, const i64* __restrict__ n, i64 m,
+                             u64* __restrict__ ctx_top, int E) {
+    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    const i64 nn = *n;
+    if (i >= m || i >= nn) return;
+    const u64 key = uk[i];
+    if (key == EMPTY) return;
+    const u64 c = key >> 16;
+    if (i > 0 && (uk[i - 1] >> 16) == c) return;  // not the group's head
+    i64 j = i;
+    while (j < nn && uk[j] != EMPTY && (uk[j] >> 16) == c) ++j;
+    u64 t[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) t[r] = 0;
+    u64* top = ctx_top + c * E;
+    for (int r = 0; r < E; ++r) {
+        const u64 old = top[r];
+        if (old == 0) break;
+        const u64 tk = (c << 16) | (0xFFFFu - (u32)(old & 0xFFFF));
+        i64 a = i, b = j;  // is the token touched in this step? (the group is sorted by token)
+        while (a < b) {
+            const i64 mid = (a + b) >> 1;
+            if (uk[mid] < tk) a = mid + 1;
+            else b = mid;
+        }
+        if (!(a < j && uk[a] == tk)) top8_insert(t, old);
+    }
+    for (i64 q = i; q < j; ++q) top8_insert(t, score[q]);
+    for (int r = 0; r < E; ++r) top[r] = t[r];
+}
+
+// Queries at pos[i] (input position g, context tok[g-k+1..g] valid iff avail[g] >= k): per level its context's
+// slot (or -1) into qslot[i]; with count outputs (tot != NULL) tot / dist / cnt of the position into row g, column ci
+// of [n, nc] arrays (cnt: the count of tok[g+1] if has_next[g]).
+template <int K>
+__global__ void online_query_k(const u16* __restrict__ tok, const int* __restrict__ avail,
+                               const unsigned char* __restrict__ has_next, const int* __restrict__ pos, i64 m, int k,
+                               const u64* __restrict__ ck, u64 ccap, const u64* __restrict__ pk,
+                               const u32* __restrict__ pcnt, u64 pcap, const u32* __restrict__ ctx_tot,
+                               const u32* __restrict__ ctx_dist, int* __restrict__ qslot, u32* __restrict__ tot,
+                               u16* __restrict__ dist, u32* __restrict__ cnt, int nc, int ci) {
+    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    if (i >= m) return;
+    const i64 g = pos[i];
+    i64 slot = -1;
+    if (avail[g] >= (K > 0 ? K : k)) slot = octx_find(ck, ccap, okey<K>(tok + g + 1, k));
+    if (slot >= 0 && ctx_tot[slot] == 0) slot = -1;
+    if (qslot) qslot[i] = (int)slot;
+    if (tot && slot >= 0) {
+        const i64 at = g * nc + ci;
+        tot[at] = ctx_tot[slot];
+        const u32 d = ctx_dist[slot];
+        dist[at] = (u16)(d < 65535u ? d : 65535u);
+        cnt[at] = has_next[g] ? opair_count(pk, pcnt, pcap, ((u64)slot << 16) | tok[g + 1]) : 0u;
+    }
+}
+
+// Hint rows of the queries pos[i]: the deepest described level (desc[v * 5 ...], deepest first: qslot (int [m]),
+// ctx_tot (u32), ctx_top (u64 [slots, E]), bucket, unused) whose context occurred: cell, E next tokens, weights.
+__global__ void online_rows_k(const int* __restrict__ pos, i64 m, int nlv, const i64* __restrict__ desc, int E,
+                              short* __restrict__ cell, u16* __restrict__ next, u16* __restrict__ weights,
+                              int* __restrict__ hinted) {
+    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    if (i >= m) return;
+    const i64 g = pos[i];
+    for (int v = 0; v < nlv; ++v) {
+        const i64* d = desc + v * 5;
+        const int slot = ((const int*)d[0])[i];
+        if (slot < 0) continue;
+        const u32 total = ((const u32*)d[1])[slot];
+        const u64* top = (const u64*)d[2] + (i64)slot * E;
+        const int b = (int)d[3];
+        const u32 top1 = (u32)(top[0] >> 16);
+        int cb = 0, pb = 0;
+        const u32 CE[6] = {2, 3, 5, 9, 17, 33};
+        const double PE[5] = {0.3, 0.5, 0.7, 0.85, 0.95};
+#pragma unroll
+        for (int e = 0; e < 6; ++e) cb += CE[e] <= total;
+        const double share = (double)top1 / (double)total;
+#pragma unroll
+        for (int e = 0; e < 5; ++e) pb += PE[e] <= share;
+        double sum = 0;
+        for (int r = 0; r < E; ++r) sum += (double)(u32)(top[r] >> 16);
+        cell[g] = (short)(((1 + b) * 7 + cb) * 6 + pb);
+        for (int r = 0; r < E; ++r) {
+            const u64 sc = top[r];
+            next[g * E + r] = sc ? (u16)(0xFFFFu - (u32)(sc & 0xFFFF)) : (u16)0;
+            weights[g * E + r] = sc ? (u16)rint((double)(u32)(sc >> 16) / sum * 65535.0) : (u16)0;
+        }
+        atomicAdd(hinted, 1);
+        return;
+    }
+}
+
+}  // namespace
+
+#define OLEVELS(k, ...)                                        \
+    switch (k) {                                               \
+        case 1: { constexpr int K = 1; __VA_ARGS__; } break;   \
+        case 2: { constexpr int K = 2; __VA_ARGS__; } break;   \
+        case 3: { constexpr int K = 3; __VA_ARGS__; } break;   \
+        case 4: { constexpr int K = 4; __VA_ARGS__; } break;   \
+        case 5: { constexpr int K = 5; __VA_ARGS__; } break;   \
+        case 6: { constexpr int K = 6; __VA_ARGS__; } break;   \
+        case 8: { constexpr int K = 8; __VA_ARGS__; } break;   \
+        case 10: { constexpr int K = 10; __VA_ARGS__; } break; \
+        case 20: { constexpr int K = 20; __VA_ARGS__; } break; \
+        default:                                               \
+            if (k < 1 || k > MAXK) return -1;                  \
+            { constexpr int K = 0; __VA_ARGS__; }              \
+            break;                                             \
+    }
+
+// Insert the occurrences ending at pos[0..m) at level k; ev[i] = their pair keys (EMPTY if a table was full: flags).
+extern "C" int ng_online_insert(const u16* tok, const int* pos, i64 m, int k, u64* ck, u64 ccap, u64* pk, u32* pcnt,
+                                u64 pcap, u32* ctx_tot, u32* ctx_dist, u64* ev, u32* flags, void* stream) {
+    if (m <= 0) return 0;
+    if (ccap == 0 || pcap == 0 || ccap > (1ull << 40)) return -1;
+    hipStream_t st = (hipStream_t)stream;
+    OLEVELS(k, (online_insert_k<K><<<grid_for(m, 256), 256, 0, st>>>(tok, pos, m, k, ck, ccap, pk, pcnt, pcap, ctx_tot, ctx_dist, ev, flags)));
+    return (int)hipGetLastError();
+}
+
+// The distinct touched pairs uk[0..*n) (sorted) merged into their contexts' top-E lists (score: scratch [m]).
+extern "C" int ng_online_top(const u64* uk, const i64* n, i64 m, const u64* pk, const u32* pcnt, u64 pcap, u64* score,
+                             u64* ctx_top, int E, void* stream) {
+    if (E < 1 || E > 8) return -1;
+    if (m <= 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    online_scores_k<<<grid_for(m, 256), 256, 0, st>>>(uk, n, m, pk, pcnt, pcap, score);
+    online_top_k<<<grid_for(m, 256), 256, 0, st>>>(uk, score, n, m, ctx_top, E);
+    return (int)hipGetLastError();
+}
+
+extern "C" int ng_online_query(const u16* tok, const int* avail, const unsigned char* has_next, const int* pos, i64 m,
+                               int k, const u64* ck, u64 ccap, const u64* pk, const u32* pcnt, u64 pcap,
+                               const u32* ctx_tot, const u32* ctx_dist, int* qslot, u32* tot, u16* dist, u32* cnt,
+                               int nc, int ci, void* stream) {
+    if (m <= 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    OLEVELS(k, (online_query_k<K><<<grid_for(m, 256), 256, 0, st>>>(tok, avail, has_next, pos, m, k, ck, ccap, pk, pcnt, pcap, ctx_tot, ctx_dist, qslot, tot, dist, cnt, nc, ci)));
+    return (int)hipGetLastError();
+}
+
+extern "C" int ng_online_rows(const int* pos, i64 m, int nlv, const i64* desc, int E, short* cell, u16* next,
+                              u16* weights, int* hinted, void* stream) {
+    if (E < 1 || E > 8) return -1;
+    if (m > 0)
+        online_rows_k<<<grid_for(m, 256), 256, 0, (hipStream_t)stream>>>(pos, m, nlv, desc, E, cell, next, weights,
+                                                                         hinted);
+    return (int)hipGetLastError();
+}

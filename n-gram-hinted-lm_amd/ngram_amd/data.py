@@ -331,3 +331,20 @@ def make_corpus(name: str, train_tokens: int | None = None, query_tokens: int | 
     query = realize(qp, zipf, train)
     bounds = train_bounds(tp.n, shard_tokens or cfg.shard_tokens)
     return Corpus(cfg, zipf, tp, qp, train, bounds, query)
+
+
+C4_STEPS = 92
+C4_STEP_TOKENS = 1 << 19
+
+
+def c4_stream(steps: int = C4_STEPS, step_tokens: int = C4_STEP_TOKENS, copy_rate_end: float = 0.20):
+    """BASELINE's fourth configuration: a stream of `steps` x `step_tokens` tokens (same generator: Zipf(1.1)
+    documents ending with BOS), the share of documents with a copied span (32-256 tokens of an earlier document)
+    ramping linearly from 0 at the stream's start to `copy_rate_end` at its end. Returns (zipf, plan, spans), spans
+    (s * step_tokens, (s + 1) * step_tokens, s): step s trains its inputs and, as its last target, the next step's
+    first token."""
+    n = steps * step_tokens
+    zipf = Zipf.make(1.1, seed=stream_key("c4", "perm") & 0xFFFFFFFF)
+    plan = make_plan(stream_key("c4", "stream", n), n, copy_rate=lambda f: copy_rate_end * f, copy_len=(32, 256))
+    spans = np.array([(s * step_tokens, (s + 1) * step_tokens, s) for s in range(steps)], np.int64)
+    return zipf, plan, spans

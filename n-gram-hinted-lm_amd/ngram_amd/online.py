@@ -1,0 +1,323 @@
+"""Online causal rows under the step rule on one MI355X, behind exact_match's OnlineRows surface
+(exact_match/exact_match.pyi :120-171; exact_match/src/online.rs): a run's training stream (`tokens` in parts
+`bounds`), when each position is trained (`spans` [m, 3]: (lo, hi, step), inputs [lo, hi) of `step`, hi its last
+target), and per step the hint rows (train_hints.rs's: the deepest of `levels` whose context has a counted
+occurrence; its cell, `entries` next tokens and weights) and count rows (train_counts.rs's: tot, dist, cnt of the own
+next token) of the queries trained in that step. An occurrence (k tokens within a part and the token after them)
+counts for a step-s query iff all its k + 1 tokens were trained before s (alpha = 1 + max tau <= s, online.rs:11-13);
+a query's k-context must lie in its segment (segments start at each part's start and at every BOS).
+
+`advance(step_hi, ...)` is the incremental path (online.rs :333): the GPU state (per level a context table with
+totals, distinct counts and exact top-`entries` lists, and a split pair table) persists between calls; a step inserts
+its newly available occurrences, then answers its queries (libngram_amd.so: ng_online_insert, sort_pairs,
+reduce_by_key, ng_online_top, ng_online_query, ng_online_rows). `hints` / `counts` answer a step range from a fresh
+state. rule="segment" (the reference's exactness-test rule) is not provided."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from .data import BOS
+from .lib import Lib, i32, u64
+
+NONE = 0xFFFFFFFF
+LOAD = 0.5
+
+
+def _tau(n: int, bounds: list[int], spans: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """tau (first step training a position as an input or a target) and tau_in (as an input) (online.rs:137-158)."""
+    tau = np.full(n, NONE, np.uint64)
+    tau_in = np.full(n, NONE, np.uint64)
+    b = np.asarray(bounds, np.int64)
+    sp = np.asarray(spans, np.int64).reshape(-1, 3)
+    order = np.argsort(sp[:, 2], kind="stable")[::-1]  # larger steps first: smaller ones overwrite (a minimum)
+    for lo, hi, step in sp[order]:
+        tau[lo:hi] = np.minimum(tau[lo:hi], step)
+        tau_in[lo:hi] = np.minimum(tau_in[lo:hi], step)
+        if hi > lo and hi < n:
+            part = int(np.searchsorted(b, hi - 1, side="right"))
+            if hi < b[part]:
+                tau[hi] = min(int(tau[hi]), int(step))
+    return tau, tau_in
+
+
+class OnlineRows:
+    """A run's training stream and when each of its positions is trained, for its online hint and count rows under
+    the step rule, on the GPU (ValueError on bad tokens, bounds or spans, as online.rs new :118-181)."""
+
+    def __init__(self, tokens, bounds: list[int], spans, threads: int = 1, cpus: list[int] = ()):
+        tok = np.ascontiguousarray(tokens, dtype=np.uint16)
+        n = len(tok)
+        if n == 0 or n >= 1 << 30:
+            raise ValueError(f"{n} tokens: need 1 to 2^30")
+        bounds = [int(b) for b in bounds]
+        if len(bounds) < 2 or bounds[0] != 0 or bounds[-1] != n or any(a >= b for a, b in zip(bounds, bounds[1:])):
+            raise ValueError("bounds must ascend strictly from 0 to the token count")
+        sp = np.asarray(spans, dtype=np.int64)
+        if sp.ndim != 2 or sp.shape[1] != 3:
+            raise ValueError("spans must be [m, 3]: (lo, hi, step)")
+        if len(sp) and ((sp[:, 0] < 0).any() or (sp[:, 0] > sp[:, 1]).any() or (sp[:, 1] > n).any()
+                        or (sp[:, 2] < 0).any() or (sp[:, 2] >= NONE).any()):
+            raise ValueError("bad span")
+        self.n = n
+        self.bounds = bounds
+        self.lib = Lib()
+        dev = torch.device("cuda", torch.cuda.current_device())
+        self.dev = dev
+        self.tok = torch.from_numpy(tok.view(np.int16).copy()).to(dev)
+        tau, tau_in = _tau(n, bounds, sp)
+        self.tau = torch.from_numpy(tau.astype(np.int64)).to(dev)
+        self.tau_in = torch.from_numpy(tau_in.astype(np.int64)).to(dev)
+        # segments (start at each part and at every BOS), the next token's part, each position's part bounds
+        idx = torch.arange(n, device=dev)
+        part_of = torch.bucketize(idx, torch.tensor(bounds[1:], device=dev), right=True)
+        bt = torch.tensor(bounds, device=dev)
+        self.part_lo, self.part_hi = bt[part_of], bt[part_of + 1]
+        start = ((self.tok.to(torch.int32) & 0xFFFF) == BOS) | (idx == self.part_lo)
+        seg = torch.cummax(torch.where(start, idx, torch.zeros_like(idx)), 0).values
+        self.avail = (idx - seg + 1).to(torch.int32)
+        self.has_next = (idx + 1 < self.part_hi).to(torch.uint8)
+        self._done = 0
+        self.config = None
+        self.state = None
+
+    def __len__(self) -> int:
+        return self.n
+
+    @property
+    def done(self) -> int:
+        return self._done
+
+    def prefault(self) -> None:
+        torch.cuda.synchronize(self.dev)
+
+    # -----------------------------------------------------------------------------------------------------------
+    def _check_config(self, levels, buckets, entries, count_levels):
+        levels, buckets, count_levels = list(levels), list(buckets), list(count_levels)
+        if levels or entries:
+            if entries < 1 or entries > 8 or not buckets or len(buckets) > 127 or buckets[0] < 1 or any(
+                    a >= b for a, b in zip(buckets, buckets[1:])):
+                raise ValueError(f"need 1 <= entries <= 8 and buckets ascending from 1: {entries}, {buckets}")
+            if any(k not in buckets for k in levels) or any(a >= b for a, b in zip(levels, levels[1:])):
+                raise ValueError(f"levels must ascend and be of {buckets}: {levels}")
+        if any(k < 1 for k in count_levels):
+            raise ValueError(f"levels must be >= 1: {count_levels}")
+        return tuple(levels), tuple(buckets), int(entries), tuple(count_levels)
+
+    def prepare(self, levels, buckets, entries, count_levels) -> None:
+        """Before the clock: advance()'s GPU state for this configuration, and per level the occurrences ordered by the
+        step they become available in (online.rs :320-331)."""
+        cfg = self._check_config(levels, buckets, entries, count_levels)
+        if self.config is not None:
+            if self.config != cfg:
+                raise ValueError("advance()'s configuration is fixed by its first call")
+            return
+        self.config = cfg
+        self.state = self._new_state(cfg)
+
+    def _new_state(self, cfg) -> dict:
+        levels, buckets, entries, count_levels = cfg
+        dev, n = self.dev, self.n
+        E = max(1, entries)
+        st = {"levels": {}, "E": E}
+        # queries: positions trained as inputs, by step
+        q_valid = self.tau_in != NONE
+        q_pos = torch.nonzero(q_valid).squeeze(1)
+        q_step = self.tau_in[q_pos]
+        order = torch.sort(q_step, stable=True).indices
+        st["q_pos"] = q_pos[order].to(torch.int32).contiguous()
+        st["q_step"] = q_step[order].cpu().numpy()
+        idx = torch.arange(n, device=dev)
+        for k in sorted(set(levels) | set(count_levels)):
+            # occurrences ending at g: tokens g-k+1..g and next g+1 within g's part; alpha = 1 + max tau over them
+            ok = (idx - k + 1 >= self.part_lo) & (idx + 1 < self.part_hi)
+            a = torch.full((n,), -1, dtype=torch.int64, device=dev)
+            for d in range(-k + 1, 2):
+                sh = torch.full((n,), NONE, dtype=torch.int64, device=dev)
+                lo, hi = max(0, -d), min(n, n - d)
+                if hi > lo:
+                    sh[lo:hi] = self.tau[lo + d : hi + d]
+                a = torch.maximum(a, sh)
+            ok &= a != NONE
+            occ = torch.nonzero(ok).squeeze(1)
+            alpha = a[occ] + 1
+            o = torch.sort(alpha, stable=True).indices
+            m = int(occ.numel())
+            cap = max(1 << 16, int(m / LOAD) + 1)
+            st["levels"][k] = {
+                "occ": occ[o].to(torch.int32).contiguous(), "alpha": alpha[o].cpu().numpy(),
+                "ck": torch.full((cap,), -1, dtype=torch.int64, device=dev), "ccap": cap,
+                "pk": torch.full((cap,), -1, dtype=torch.int64, device=dev),
+                "pcnt": torch.zeros(cap, dtype=torch.int32, device=dev), "pcap": cap,
+                "tot": torch.zeros(cap, dtype=torch.int32, device=dev),
+                "dist": torch.zeros(cap, dtype=torch.int32, device=dev),
+                "top": torch.zeros(cap * E, dtype=torch.int64, device=dev) if k in levels else
+                torch.zeros(1, dtype=torch.int64, device=dev),
+                "flags": torch.zeros(2, dtype=torch.int32, device=dev),
+                "ctx_bits": max(1, (cap - 1).bit_length()),
+            }
+        most = max([1] + [int(np.bincount(lv["alpha"]).max()) if len(lv["alpha"]) else 1
+                          for lv in st["levels"].values()])
+        st["ev"] = torch.empty(most, dtype=torch.int64, device=dev)
+        st["ev_sorted"] = torch.empty(most, dtype=torch.int64, device=dev)
+        st["uk"] = torch.empty(most, dtype=torch.int64, device=dev)
+        st["ones"] = torch.ones(most, dtype=torch.int32, device=dev)
+        st["agg"] = torch.empty(most, dtype=torch.int32, device=dev)
+        st["nruns"] = torch.zeros(1, dtype=torch.int64, device=dev)
+        st["score"] = torch.empty(most, dtype=torch.int64, device=dev)
+        nq = int(np.bincount(st["q_step"]).max()) if len(st["q_step"]) else 1
+        st["qslot"] = {k: torch.empty(max(1, nq), dtype=torch.int32, device=dev) for k in levels}
+        st["hinted"] = torch.zeros(1, dtype=torch.int32, device=dev)
+        st["done"] = 0
+        return st
+
+    def _range(self, arr: np.ndarray, lo: int, hi: int) -> tuple[int, int]:
+        return int(np.searchsorted(arr, lo, side="left")), int(np.searchsorted(arr, hi, side="left"))
+
+    def _step(self, st: dict, s: int, outs: dict, queries: bool = True) -> None:
+        """Step s: its newly available occurrences inserted at every level, then (queries) its queries answered."""
+        lib = self.lib
+        levels, buckets, entries, count_levels = outs["cfg"]
+        E = st["E"]
+        for k, lv in st["levels"].items():
+            a, b = self._range(lv["alpha"], s, s + 1)
+            m = b - a
+            if m == 0:
+                continue
+            ev = st["ev"][:m]
+            lib("ng_online_insert", self.tok, lv["occ"][a:b], m, i32(k), lv["ck"], u64(lv["ccap"]), lv["pk"], lv["pcnt"],
+                u64(lv["pcap"]), lv["tot"], lv["dist"], ev, lv["flags"])
+            if k in levels:
+                lib.cub("sort_pairs", ev, st["ev_sorted"], None, None, m, i32(0), i32(min(64, 16 + lv["ctx_bits"])))
+                lib.cub("reduce_by_key", st["ev_sorted"], st["uk"], st["ones"], st["agg"], st["nruns"], m)
+                lib("ng_online_top", st["uk"], st["nruns"], m, lv["pk"], lv["pcnt"], u64(lv["pcap"]), st["score"],
+                    lv["top"], i32(E))
+        qa, qb = self._range(st["q_step"], s, s + 1)
+        mq = qb - qa
+        if mq == 0 or not queries:
+            return
+        qpos = st["q_pos"][qa:qb]
+        for ci, k in enumerate(count_levels):
+            lv = st["levels"][k]
+            lib("ng_online_query", self.tok, self.avail, self.has_next, qpos, mq, i32(k), lv["ck"], u64(lv["ccap"]),
+                lv["pk"], lv["pcnt"], u64(lv["pcap"]), lv["tot"], lv["dist"], st["qslot"][k] if k in levels else None,
+                outs["tot"], outs["dist"], outs["cnt"], i32(len(count_levels)), i32(ci))
+        for k in levels:
+            if k in count_levels:
+                continue
+            lv = st["levels"][k]
+            lib("ng_online_query", self.tok, self.avail, self.has_next, qpos, mq, i32(k), lv["ck"], u64(lv["ccap"]),
+                lv["pk"], lv["pcnt"], u64(lv["pcap"]), lv["tot"], lv["dist"], st["qslot"][k], None, None, None,
+                i32(1), i32(0))
+        if levels:
+            desc = []
+            for k in sorted(levels, reverse=True):
+                lv = st["levels"][k]
+                desc += [st["qslot"][k].data_ptr(), lv["tot"].data_ptr(), lv["top"].data_ptr(), buckets.index(k), 0]
+            desc_t = torch.tensor(desc, dtype=torch.int64, device=self.dev)
+            lib("ng_online_rows", qpos, mq, i32(len(levels)), desc_t, i32(E), outs["cell"], outs["next"],
+                outs["weights"], st["hinted"])
+            outs["keep"].append(desc_t)  # the descriptor lives until the kernel has run
+
+    def _device_outputs(self, cfg) -> dict:
+        levels, buckets, entries, count_levels = cfg
+        n, dev = self.n, self.dev
+        E = max(1, entries)
+        return {"cfg": cfg, "keep": [],
+                "cell": torch.zeros(n, dtype=torch.int16, device=dev),
+                "next": torch.zeros((n, E), dtype=torch.int16, device=dev),
+                "weights": torch.zeros((n, E), dtype=torch.int16, device=dev),
+                "tot": torch.zeros((n, max(1, len(count_levels))), dtype=torch.int32, device=dev),
+                "dist": torch.zeros((n, max(1, len(count_levels))), dtype=torch.int16, device=dev),
+                "cnt": torch.zeros((n, max(1, len(count_levels))), dtype=torch.int32, device=dev)}
+
+    def _check_flags(self, st) -> None:
+        for k, lv in st["levels"].items():
+            if int(lv["flags"][0].item()):
+                raise RuntimeError(f"k={k}: a table of the online state overflowed")
+
+    @staticmethod
+    def _copy_rows(outs: dict, rows: torch.Tensor, cell, nxt, weights, tot, dist, cnt) -> None:
+        """The rows of `rows` (positions) from the device outputs into the caller's host arrays."""
+        r = rows.long()
+        rn = r.cpu().numpy()
+        if cell is not None:
+            cell[rn] = outs["cell"][r].cpu().numpy()
+            nxt[rn] = outs["next"][r].cpu().numpy().view(np.uint16)
+            weights[rn] = outs["weights"][r].cpu().numpy().view(np.uint16)
+        if tot is not None:
+            nc = tot.shape[1]
+            tot[rn] = outs["tot"][r, :nc].cpu().numpy().view(np.uint32)
+            dist[rn] = outs["dist"][r, :nc].cpu().numpy().view(np.uint16)
+            cnt[rn] = outs["cnt"][r, :nc].cpu().numpy().view(np.uint32)
+
+    def advance(self, step_hi: int, levels, buckets, entries: int, count_levels, cell=None, next=None, weights=None,
+                tot=None, dist=None, cnt=None) -> int:
+        """The rows of the queries trained in steps [done, step_hi) (what hints + counts write, rule "step"), with the
+        counted occurrences kept between calls; returns the queries hinted (online.rs :333)."""
+        self.prepare(levels, buckets, entries, count_levels)
+        st = self.state
+        if step_hi < self._done or step_hi >= 1 << 30:
+            raise ValueError(f"bad step range [{self._done}, {step_hi})")
+        if "outs" not in st:
+            st["outs"] = self._device_outputs(self.config)
+        outs = st["outs"]
+        st["hinted"].zero_()
+        outs["keep"] = []
+        for s in range(self._done, step_hi):
+            self._step(st, s, outs)
+        self._check_flags(st)
+        qa, qb = self._range(st["q_step"], self._done, step_hi)
+        if cell is not None or tot is not None:
+            self._copy_rows(outs, st["q_pos"][qa:qb], cell, next, weights, tot, dist, cnt)
+        self._done = step_hi
+        return int(st["hinted"].item())
+
+    def advance_device(self, step_hi: int) -> None:
+        """advance() to step_hi with the prepared configuration, leaving the rows in GPU memory (self.state["outs"]),
+        without synchronizing."""
+        st = self.state
+        if "outs" not in st:
+            st["outs"] = self._device_outputs(self.config)
+        outs = st["outs"]
+        outs["keep"] = []
+        for s in range(self._done, step_hi):
+            self._step(st, s, outs)
+        self._done = step_hi
+
+    def _range_rows(self, levels, buckets, entries, count_levels, step_lo, step_hi, rule):
+        if rule != "step":
+            raise ValueError(f"rule must be 'step' (the 'segment' rule is not provided): {rule}")
+        if step_lo > step_hi or step_hi >= 1 << 30:
+            raise ValueError(f"bad step range [{step_lo}, {step_hi})")
+        cfg = self._check_config(levels, buckets, entries, count_levels)
+        st = self._new_state(cfg)
+        outs = self._device_outputs(cfg)
+        for s in range(0, step_hi):  # earlier steps only insert their occurrences
+            self._step(st, s, outs, queries=s >= step_lo)
+        self._check_flags(st)
+        qa, qb = self._range(st["q_step"], step_lo, step_hi)
+        return st, outs, st["q_pos"][qa:qb]
+
+    def hints(self, levels, buckets, entries, step_lo, step_hi, cell, next, weights, rule: str = "step") -> int:
+        """The hint rows of the queries trained in steps [step_lo, step_hi), written into the stream-sized cell [n],
+        next / weights [n, entries]; returns the queries hinted (online.rs :190)."""
+        if entries < 1:
+            raise ValueError("need entries >= 1")
+        if len(cell) != self.n or next.shape != (self.n, entries) or weights.shape != (self.n, entries):
+            raise ValueError(f"outputs must be [{self.n}] and [{self.n}, {entries}]")
+        st, outs, rows = self._range_rows(levels, buckets, entries, (), step_lo, step_hi, rule)
+        self._copy_rows(outs, rows, cell, next, weights, None, None, None)
+        return int(st["hinted"].item())
+
+    def counts(self, levels, step_lo, step_hi, tot, dist, cnt, rule: str = "step") -> None:
+        """The count rows of the queries trained in steps [step_lo, step_hi) at each level, written into the
+        stream-sized tot / dist / cnt [n, L] (online.rs :259)."""
+        nl = len(levels)
+        if not nl or min(levels) < 1:
+            raise ValueError(f"levels must be >= 1: {levels}")
+        if tot.shape != (self.n, nl) or dist.shape != (self.n, nl) or cnt.shape != (self.n, nl):
+            raise ValueError(f"outputs must be [{self.n}, {nl}]")
+        st, outs, rows = self._range_rows((), (1,), 0, levels, step_lo, step_hi, rule)
+        self._copy_rows(outs, rows, None, None, None, tot, dist, cnt)

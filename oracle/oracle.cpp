@@ -15,11 +15,16 @@
 //   * oracle_longest_match: the largest k <= cap whose query k-context is valid and occurred (kgram.rs kgram_stats'
 //     "matched" at each k, :252-277, with the monotonicity of kgram.rs:12-15), and that context's most frequent next
 //     token and its count.
+//   * oracle_online: exact_match/src/online.rs's step rule (:1-17) and walks (Walker :574-672, Counter :674-705): per
+//     level, occurrences (time alpha = 1 + max tau over their k + 1 tokens) and queries (time tau_in) sorted by
+//     (context, time, occurrences first, position) and walked; hint rows (deepest level first) and count rows.
 // Definitions (kgram.rs:7-9): a query position i's k-context is x[i-k+1..=i], valid iff avail[i] >= k; a corpus
 // occurrence is any k tokens within one shard followed by a token of the same shard; tot = occurrences (u32; the
 // caller checks >= 2^32), dist = distinct next tokens (saturated at 65535), cnt = the target's count if its rank
 // (count descending, token ascending) is below cnt_top, else 0; all 0 where the context is invalid or never occurred.
 #include <algorithm>
+#include <cmath>
+#include <functional>
 #include <atomic>
 #include <cstdint>
 #include <cstring>
@@ -342,6 +347,142 @@ int oracle_longest_match(const u16* tok, const i64* bounds, int nshards, const u
             }
     }
     return 0;
+}
+
+// Online rows under the step rule (online.rs): tokens in parts [bounds[j], bounds[j + 1]); tau / tau_in per position
+// (0xFFFFFFFF: never). Queries: positions with tau_in in [step_lo, step_hi) whose k-context lies in their segment
+// (segments start at each part start and at every BOS). Hint rows for `levels` (deepest first; bucket = index in
+// `buckets`; `entries` next tokens) into cell / next / weights; count rows for `count_levels` into tot / dist / cnt
+// [n, nc] (cnt: the count of the query's own next token, if within its part). Outputs are written only where a row
+// exists (callers zero them). Returns the queries hinted, or -1 on bad arguments.
+i64 oracle_online(const u16* tok, i64 n, const i64* bounds, int nparts, const u32* tau, const u32* tau_in,
+                  const int* levels, int nl, const int* buckets, int nb, int entries, const int* count_levels, int nc,
+                  u32 step_lo, u32 step_hi, int16_t* cell, u16* next, u16* weights, u32* tot, u16* dist, u32* cnt) {
+    const u32 NONE = 0xFFFFFFFFu;
+    if (entries < 1 || nparts < 1 || step_lo > step_hi) return -1;
+    std::vector<u32> seg(n), part_end(n), part_lo(n);
+    for (int j = 0; j < nparts; ++j) {
+        i64 s0 = bounds[j];
+        for (i64 g = bounds[j]; g < bounds[j + 1]; ++g) {
+            if (tok[g] == 50256) s0 = g;
+            seg[g] = (u32)s0;
+            part_end[g] = (u32)bounds[j + 1];
+            part_lo[g] = (u32)bounds[j];
+        }
+    }
+    struct El {
+        i64 g;
+        u32 time;
+        int kind;  // 0 occurrence, 1 query
+    };
+    std::vector<uint8_t> filled(n, 0);
+    i64 hinted = 0;
+    // levels needed: hint levels (descending) and count levels
+    std::vector<int> all;
+    for (int i = 0; i < nl; ++i) all.push_back(levels[i]);
+    for (int i = 0; i < nc; ++i) all.push_back(count_levels[i]);
+    std::sort(all.begin(), all.end(), std::greater<int>());
+    all.erase(std::unique(all.begin(), all.end()), all.end());
+    std::vector<u32> counts(1 << 16, 0);
+    for (int k : all) {
+        int li = -1, ci = -1;
+        for (int i = 0; i < nl; ++i)
+            if (levels[i] == k)
+                for (int b = 0; b < nb; ++b)
+                    if (buckets[b] == k) li = b;
+        for (int i = 0; i < nc; ++i)
+            if (count_levels[i] == k) ci = i;
+        std::vector<El> els;
+        for (i64 g = 0; g < n; ++g) {
+            // occurrence ending at g: tokens g-k+1..g and next g+1 within g's part
+            if (g - k + 1 >= (i64)part_lo[g] && g + 1 < (i64)part_end[g]) {
+                u32 a = 0;
+                bool ok = true;
+                for (i64 q = g - k + 1; q <= g + 1; ++q) {
+                    if (tau[q] == NONE) ok = false;
+                    else a = std::max(a, tau[q]);
+                }
+                if (ok && a + 1 < step_hi) els.push_back({g, a + 1, 0});
+            }
+            if (tau_in[g] != NONE && tau_in[g] >= step_lo && tau_in[g] < step_hi && g - (i64)seg[g] + 1 >= k)
+                els.push_back({g, tau_in[g], 1});
+        }
+        auto ctx_less = [&](i64 a, i64 b) {
+            return std::lexicographical_compare(tok + a - k + 1, tok + a + 1, tok + b - k + 1, tok + b + 1);
+        };
+        std::sort(els.begin(), els.end(), [&](const El& x, const El& y) {
+            if (ctx_less(x.g, y.g)) return true;
+            if (ctx_less(y.g, x.g)) return false;
+            if (x.time != y.time) return x.time < y.time;
+            if (x.kind != y.kind) return x.kind < y.kind;
+            return x.g < y.g;
+        });
+        size_t i = 0;
+        while (i < els.size()) {
+            size_t j = i;
+            while (j < els.size() && !ctx_less(els[i].g, els[j].g) && !ctx_less(els[j].g, els[i].g)) ++j;
+            std::vector<u16> touched;
+            std::vector<std::pair<u32, u16>> top;  // (count, token), best first
+            u32 total = 0;
+            auto better = [](std::pair<u32, u16> a, std::pair<u32, u16> b) {
+                return a.first > b.first || (a.first == b.first && a.second < b.second);
+            };
+            for (size_t e = i; e < j; ++e) {
+                const El& el = els[e];
+                if (el.kind == 0) {
+                    u16 t = tok[el.g + 1];
+                    if (counts[t] == 0) touched.push_back(t);
+                    u32 c = ++counts[t];
+                    ++total;
+                    int pos = -1;
+                    for (size_t q = 0; q < top.size(); ++q)
+                        if (top[q].second == t) pos = (int)q;
+                    if (pos < 0) {
+                        if ((int)top.size() < entries) {
+                            top.push_back({c, t});
+                            pos = (int)top.size() - 1;
+                        } else if (better({c, t}, top[entries - 1])) {
+                            pos = entries - 1;
+                        }
+                    }
+                    if (pos >= 0) {
+                        top[pos] = {c, t};
+                        while (pos > 0 && better(top[pos], top[pos - 1])) {
+                            std::swap(top[pos], top[pos - 1]);
+                            --pos;
+                        }
+                    }
+                } else if (total > 0) {
+                    const i64 g = el.g;
+                    if (ci >= 0) {
+                        tot[g * nc + ci] = total;
+                        dist[g * nc + ci] = (u16)std::min<size_t>(touched.size(), 65535);
+                        cnt[g * nc + ci] = g + 1 < (i64)part_end[g] ? counts[tok[g + 1]] : 0;
+                    }
+                    if (li >= 0 && !filled[g]) {
+                        static const u32 CE[6] = {2, 3, 5, 9, 17, 33};
+                        static const double PE[5] = {0.3, 0.5, 0.7, 0.85, 0.95};
+                        int cb = 0, pb = 0;
+                        for (u32 c : CE) cb += c <= total;
+                        for (double p : PE) pb += p <= (double)top[0].first / (double)total;
+                        cell[g] = (int16_t)(((1 + li) * 7 + cb) * 6 + pb);
+                        double sum = 0;
+                        for (auto& tc : top) sum += tc.first;
+                        for (int r = 0; r < entries; ++r) {
+                            next[g * entries + r] = r < (int)top.size() ? top[r].second : 0;
+                            weights[g * entries + r] =
+                                r < (int)top.size() ? (u16)std::nearbyint((double)top[r].first / sum * 65535.0) : 0;
+                        }
+                        filled[g] = 1;
+                        ++hinted;
+                    }
+                }
+            }
+            for (u16 t : touched) counts[t] = 0;
+            i = j;
+        }
+    }
+    return hinted;
 }
 
 }  // extern "C"

@@ -57,6 +57,9 @@ def lib() -> ctypes.CDLL:
         so.oracle_table_counts.restype = ctypes.c_int64
         so.oracle_table_counts.argtypes = [P, P, ctypes.c_int, P, P, P, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
                                            ctypes.c_int, P, P, P, P, P, P, P, ctypes.c_int]
+        so.oracle_online.restype = ctypes.c_int64
+        so.oracle_online.argtypes = [P, ctypes.c_int64, P, ctypes.c_int, P, P, P, ctypes.c_int, P, ctypes.c_int,
+                                     ctypes.c_int, P, ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32, P, P, P, P, P, P]
         so.oracle_longest_match.restype = ctypes.c_int
         so.oracle_longest_match.argtypes = [P, P, ctypes.c_int, P, P, ctypes.c_int64, ctypes.c_int, P, P, P,
                                             ctypes.c_int]
@@ -161,6 +164,116 @@ def longest_match(train: np.ndarray, bounds: np.ndarray, x: np.ndarray, avail: n
     if rc:
         raise ValueError("oracle_longest_match: bad arguments")
     return length, nxt, cnt
+
+
+NONE = 0xFFFFFFFF
+
+
+def spans_tau(n: int, bounds, spans) -> tuple[np.ndarray, np.ndarray]:
+    """online.rs new (:137-158): tau (first step training a position as input or target) and tau_in (as input) from
+    spans (lo, hi, step): inputs [lo, hi) of `step`, position hi its last target if within the part of hi - 1."""
+    tau = np.full(n, NONE, np.uint32)
+    tau_in = np.full(n, NONE, np.uint32)
+    b = np.asarray(bounds, np.int64)
+    for lo, hi, step in np.asarray(spans, np.int64).reshape(-1, 3):
+        tau[lo:hi] = np.minimum(tau[lo:hi], step)
+        tau_in[lo:hi] = np.minimum(tau_in[lo:hi], step)
+        if hi > lo and hi < n:
+            part = int(np.searchsorted(b, hi - 1, side="right"))
+            if hi < b[part]:
+                tau[hi] = min(tau[hi], step)
+    return tau, tau_in
+
+
+def online(tokens, bounds, tau, tau_in, levels, buckets, entries, count_levels, step_lo: int, step_hi: int):
+    """The step rule's hint rows and count rows (oracle_online): (cell int16 [n], next uint16 [n, entries], weights
+    uint16 [n, entries], tot uint32 [n, nc], dist uint16 [n, nc], cnt uint32 [n, nc], queries hinted)."""
+    tok = np.ascontiguousarray(tokens, np.uint16)
+    n = len(tok)
+    b = np.ascontiguousarray(bounds, np.int64)
+    lv = np.ascontiguousarray(levels, np.int32)
+    bk = np.ascontiguousarray(buckets, np.int32)
+    cl = np.ascontiguousarray(count_levels, np.int32)
+    cell = np.zeros(n, np.int16)
+    nxt = np.zeros((n, entries), np.uint16)
+    w = np.zeros((n, entries), np.uint16)
+    tot = np.zeros((n, max(len(cl), 1)), np.uint32)
+    dist = np.zeros((n, max(len(cl), 1)), np.uint16)
+    cnt = np.zeros((n, max(len(cl), 1)), np.uint32)
+    hinted = lib().oracle_online(_p(tok), n, _p(b), len(b) - 1, _p(np.ascontiguousarray(tau, np.uint32)),
+                                 _p(np.ascontiguousarray(tau_in, np.uint32)), _p(lv), len(lv), _p(bk), len(bk), entries,
+                                 _p(cl), len(cl), step_lo, step_hi, _p(cell), _p(nxt), _p(w), _p(tot), _p(dist),
+                                 _p(cnt))
+    if hinted < 0:
+        raise ValueError("oracle_online: bad arguments")
+    return cell, nxt, w, tot[:, : len(cl)], dist[:, : len(cl)], cnt[:, : len(cl)], int(hinted)
+
+
+def brute_online(tokens, bounds, tau, tau_in, levels, buckets, entries, count_levels, step_lo, step_hi):
+    """online.rs's definitions directly (tiny inputs): per query and level, every valid occurrence of its context with
+    alpha <= the query's step counted from scratch."""
+    tok = [int(t) for t in tokens]
+    n = len(tok)
+    part_lo, part_hi, seg = [0] * n, [0] * n, [0] * n
+    for a, bnd in zip(bounds[:-1], bounds[1:]):
+        s0 = a
+        for g in range(a, bnd):
+            if tok[g] == BOS:
+                s0 = g
+            part_lo[g], part_hi[g], seg[g] = a, bnd, s0
+    cell = np.zeros(n, np.int16)
+    nxt = np.zeros((n, entries), np.uint16)
+    w = np.zeros((n, entries), np.uint16)
+    nc = len(count_levels)
+    tot = np.zeros((n, nc), np.uint32)
+    dist = np.zeros((n, nc), np.uint16)
+    cnt = np.zeros((n, nc), np.uint32)
+
+    def alpha(g, k):
+        if g - k + 1 < part_lo[g] or g + 1 >= part_hi[g]:
+            return None
+        ts = [int(tau[q]) for q in range(g - k + 1, g + 2)]
+        return None if NONE in ts else 1 + max(ts)
+
+    def table(g, k):
+        c = tok[g - k + 1 : g + 1]
+        found = Counter()
+        for h in range(n):
+            a = alpha(h, k)
+            if a is not None and a <= tau_in[g] and tok[h - k + 1 : h + 1] == c:
+                found[tok[h + 1]] += 1
+        return found
+
+    hinted = 0
+    queries = [g for g in range(n) if tau_in[g] != NONE and step_lo <= tau_in[g] < step_hi]
+    for g in queries:
+        for j, k in enumerate(count_levels):
+            if g - seg[g] + 1 < k:
+                continue
+            f = table(g, k)
+            if f:
+                tot[g, j] = sum(f.values())
+                dist[g, j] = min(len(f), 65535)
+                cnt[g, j] = f[tok[g + 1]] if g + 1 < part_hi[g] else 0
+        for k in sorted(levels, reverse=True):
+            if g - seg[g] + 1 < k:
+                continue
+            f = table(g, k)
+            if not f:
+                continue
+            ranked = sorted(f.items(), key=lambda tc: (-tc[1], tc[0]))[:entries]
+            total = sum(f.values())
+            li = list(buckets).index(k)
+            cb = sum(e <= total for e in COUNT_EDGES)
+            pb = sum(e <= ranked[0][1] / total for e in PURITY_EDGES)
+            cell[g] = ((1 + li) * 7 + cb) * 6 + pb
+            s = float(sum(c for _, c in ranked))
+            for r, (t, c) in enumerate(ranked):
+                nxt[g, r] = t
+                w[g, r] = int(np.round(c / s * WEIGHT_ONE))
+            hinted += 1
+            break
+    return cell, nxt, w, tot, dist, cnt, hinted
 
 
 # ---------------------------------------------------------------------------------------------------------------

@@ -178,3 +178,43 @@ def test_table_rows_by_hand():
     # position 1: bucket 1, count bin 6 (40 >= 33), purity 10/40 = .25 -> 0; weights 10/16, 6/16 of the kept counts
     assert cell[1] == ((1 + 1) * 7 + 6) * 6 + 0 and level[1] == 1
     assert list(w[1]) == [40959, 24576]  # 40959.375, 24575.625
+
+
+def _online_case(rng, n_parts, part_len, steps):
+    shards = [rng.integers(0, 4, size=part_len).astype(np.uint16) for _ in range(n_parts)]
+    for sh in shards:
+        sh[rng.random(len(sh)) < 0.06] = O.BOS
+    tok = np.concatenate(shards)
+    bounds = np.cumsum([0] + [len(sh) for sh in shards])
+    # spans: each part consumed in `steps` chunks, steps interleaved over the parts
+    spans = []
+    for j in range(n_parts):
+        cuts = np.linspace(bounds[j], bounds[j + 1] - 1, steps + 1).astype(int)
+        for s in range(steps):
+            if cuts[s] < cuts[s + 1]:
+                spans.append((cuts[s], cuts[s + 1], s))
+    return tok, bounds, np.array(spans, np.int64)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_online_oracle_matches_brute_force(seed):
+    rng = np.random.default_rng(300 + seed)
+    tok, bounds, spans = _online_case(rng, int(rng.integers(1, 3)), int(rng.integers(30, 70)), int(rng.integers(2, 6)))
+    tau, tau_in = O.spans_tau(len(tok), bounds, spans)
+    args = (tok, bounds, tau, tau_in, [1, 2, 3], [1, 2, 3, 4], 3, [1, 2, 4], 0, 10)
+    got = O.online(*args)
+    want = O.brute_online(*args)
+    for g, w, name in zip(got, want, ("cell", "next", "weights", "tot", "dist", "cnt", "hinted")):
+        assert np.array_equal(g, w), name
+    assert got[-1] > 0
+    # a sub-range of steps writes only its own queries' rows
+    part = O.online(tok, bounds, tau, tau_in, [1, 2, 3], [1, 2, 3, 4], 3, [1, 2, 4], 1, 3)
+    part_b = O.brute_online(tok, bounds, tau, tau_in, [1, 2, 3], [1, 2, 3, 4], 3, [1, 2, 4], 1, 3)
+    for g, w in zip(part, part_b):
+        assert np.array_equal(g, w)
+
+
+def test_spans_tau():
+    # two parts [0, 6), [6, 10); step 0 trains inputs 0..2 (target 3), step 1 inputs 3..5 (target 6 is another part)
+    tau, tau_in = O.spans_tau(10, [0, 6, 10], [(0, 3, 0), (3, 6, 1), (6, 9, 0)])
+    assert list(tau[:7]) == [0, 0, 0, 0, 1, 1, 0] and tau[9] == 0 and tau_in[3] == 1 and tau_in[9] == O.NONE
