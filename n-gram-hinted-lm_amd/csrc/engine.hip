@@ -88,6 +88,61 @@ __global__ void __launch_bounds__(256) scan_count_sparse_k(const u16* __restrict
     }
 }
 
+// Gated levels, any density: a block takes 256 bitmap words (8192 positions) at a time; each wave lists its 64 words'
+// set positions in LDS (a wave prefix sum of their popcounts), and its lanes then probe the listed positions 64 at a
+// time, so every lane has work whatever the density and no position outside the bitmap is visited. Hits set their
+// bit in an LDS copy of the words (written out whole) and are counted in the split table, or (COUNT false) only
+// flagged per context in hit[] (the longest match's existence phase).
+template <int K, bool COUNT>
+__global__ void __launch_bounds__(256) scan_compact_k(const u16* __restrict__ tok, i64 L, int k,
+                                                      const u32* __restrict__ bm_in, u32* __restrict__ bm_out,
+                                                      const u64* __restrict__ vt, u64 vcap, const u32* __restrict__ vrep,
+                                                      const u16* __restrict__ x, u64* keys, u32* cnts, u64 cap,
+                                                      unsigned char* __restrict__ hit, u32* flags) {
+    __shared__ u32 list[4][64 * 32];
+    __shared__ u32 words[4][64];
+    const int lane = lane_id(), w = threadIdx.x / WAVE;
+    const i64 nwords = (L + 31) >> 5;
+    for (i64 g0 = (i64)blockIdx.x * 256; g0 < nwords; g0 += (i64)gridDim.x * 256) {
+        const i64 wi = g0 + w * 64 + lane;
+        const u32 word = wi < nwords ? bm_in[wi] : 0u;
+        const u32 c = __popc(word);
+        u32 incl = c;
+#pragma unroll
+        for (int d = 1; d < WAVE; d <<= 1) {
+            const u32 o = (u32)__shfl_up((int)incl, d, WAVE);
+            if (lane >= d) incl += o;
+        }
+        const u32 total = (u32)__shfl((int)incl, WAVE - 1, WAVE);
+        u32 at = incl - c;
+        u32 bits = word;
+        while (bits) {
+            const int b = __ffs(bits) - 1;
+            bits &= bits - 1;
+            list[w][at++] = (u32)(lane * 32 + b);
+        }
+        words[w][lane] = 0;
+        __syncthreads();
+        const bool full = COUNT && *(volatile u32*)&flags[0] != 0u;
+        for (u32 r = lane; r < total; r += WAVE) {
+            const u32 lp = list[w][r];
+            const i64 p = ((g0 + w * 64) << 5) + lp;
+            if (p >= L) continue;
+            const u64 key = probe_key<K>(tok, p, k, vt, vcap, vrep, x, flags);
+            if (key == EMPTY) continue;
+            atomicOr(&words[w][lp >> 5], 1u << (lp & 31));
+            if (COUNT) {
+                if (!full) split_add(keys, cnts, cap, key, 1u, flags);
+            } else {
+                hit[key >> 16] = 1;
+            }
+        }
+        __syncthreads();
+        if (wi < nwords) bm_out[wi] = words[w][lane];
+        __syncthreads();
+    }
+}
+
 // Existence only (the first phase of the longest match): the hit bitmap, and hit[context id] = 1 for every query
 // context that occurred (plain byte stores: every writer stores the same value).
 template <int K>
@@ -332,7 +387,8 @@ __global__ void __launch_bounds__(256) pos_gather_k(const int* __restrict__ ctx_
 // ---------------------------------------------------------------------------------------------------------------
 
 // One level's scan counted in a split table (keys u64[cap] filled with EMPTY, cnts u32[cap] zeroed): the record's
-// scan_level with the split table (sparse: walk the set bits of bm_in).
+// scan_level with the split table. sparse 0: a lane per position; 1: a lane per bitmap word walking its set bits;
+// 2: the set positions listed per wave in LDS and probed 64 at a time (any density, bm_in required).
 extern "C" int ng_scan_count(const u16* tok, i64 L, int k, const u32* bm_in, u32* bm_out, const u64* vt, u64 vcap,
                              const u32* vrep, const u16* x, u64* keys, u32* cnts, u64 cap, u32* flags, int grid,
                              int sparse, void* stream) {
@@ -340,7 +396,9 @@ extern "C" int ng_scan_count(const u16* tok, i64 L, int k, const u32* bm_in, u32
     if (cap == 0) return -1;
     if (grid <= 0) grid = grid_for(L, 256);
     hipStream_t st = (hipStream_t)stream;
-    if (sparse && bm_in) {
+    if (sparse == 2 && bm_in) {
+        LEVEL_SWITCH(k, (scan_compact_k<K, true><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, keys, cnts, cap, nullptr, flags)));
+    } else if (sparse && bm_in) {
         LEVEL_SWITCH(k, (scan_count_sparse_k<K><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, keys, cnts, cap, flags)));
     } else {
         LEVEL_SWITCH(k, (scan_count_dense_k<K><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, keys, cnts, cap, flags)));
@@ -349,14 +407,16 @@ extern "C" int ng_scan_count(const u16* tok, i64 L, int k, const u32* bm_in, u32
 }
 
 // One level's existence scan: bm_out = the corpus positions (gated by bm_in) whose k-context is a query context of the
-// table, hit[id] = 1 for each such context id (hit zeroed by the caller).
+// table, hit[id] = 1 for each such context id (hit zeroed by the caller). sparse as ng_scan_count's.
 extern "C" int ng_scan_exist(const u16* tok, i64 L, int k, const u32* bm_in, u32* bm_out, const u64* vt, u64 vcap,
                              const u32* vrep, const u16* x, unsigned char* hit, u32* flags, int grid, int sparse,
                              void* stream) {
     if (L <= 0) return 0;
     if (grid <= 0) grid = grid_for(L, 256);
     hipStream_t st = (hipStream_t)stream;
-    if (sparse && bm_in) {
+    if (sparse == 2 && bm_in) {
+        LEVEL_SWITCH(k, (scan_compact_k<K, false><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, nullptr, nullptr, 0, hit, flags)));
+    } else if (sparse && bm_in) {
         LEVEL_SWITCH(k, (scan_exist_sparse_k<K><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, hit, flags)));
     } else {
         LEVEL_SWITCH(k, (scan_exist_dense_k<K><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, hit, flags)));

@@ -201,19 +201,28 @@ __global__ void __launch_bounds__(BLOCK) rs_hist_k(const u64* __restrict__ keys,
 }
 
 // Stable scatter of one tile: items in tile order (row j, thread t) = index j * 256 + t; per row, each wave ranks its
-// lanes by digit with eight ballots; the per-(row, wave, digit) counts are scanned in LDS in tile order.
+// lanes by digit with eight ballots; the per-(row, wave, digit) counts (u16) are scanned in LDS in tile order, giving
+// each item its place in the tile sorted by digit. The tile is then staged in LDS in that order (aliasing the counts)
+// and written out by consecutive threads, so each digit's run of the tile leaves as contiguous, coalesced stores.
 template <bool VALUES>
 __global__ void __launch_bounds__(BLOCK) rs_scatter_k(const u64* __restrict__ kin, const u32* __restrict__ vin,
                                                       u64* __restrict__ kout, u32* __restrict__ vout, i64 n, int shift,
                                                       int nbits, const u32* __restrict__ hist, i64 ntiles) {
-    __shared__ u32 cnt[ITEMS][NWAVES][256];
-    __shared__ u32 base_s[256];
+    constexpr int STAGE_U64 = TILE + TILE / 2;  // keys (TILE u64) then values (TILE u32)
+    static_assert(ITEMS * NWAVES * 256 * 2 <= STAGE_U64 * 8, "the counts fit the staging area");
+    __shared__ u64 smem[STAGE_U64];
+    __shared__ u32 gbase[256];
+    __shared__ u32 tile_off[256];
+    u16* cnt = (u16*)smem;  // [ITEMS][NWAVES][256]
+    u64* stage_k = smem;
+    u32* stage_v = (u32*)(smem + TILE);
     const int t = threadIdx.x, w = t / WAVE;
     const u32 mask = (1u << nbits) - 1u;
-    base_s[t] = hist[(i64)t * ntiles + blockIdx.x];
-    for (int i = t; i < ITEMS * NWAVES * 256; i += BLOCK) (&cnt[0][0][0])[i] = 0;
+    gbase[t] = hist[(i64)t * ntiles + blockIdx.x];
+    for (int i = t; i < ITEMS * NWAVES * 256 / 2; i += BLOCK) ((u32*)smem)[i] = 0;
     __syncthreads();
     const i64 base = (i64)blockIdx.x * TILE;
+    const int tile_n = (int)(n - base < TILE ? n - base : TILE);
     u64 key[ITEMS];
     u32 val[ITEMS];
     u32 dr[ITEMS];  // digit | rank << 16 ; rank 0xFFFF = invalid
@@ -234,28 +243,43 @@ __global__ void __launch_bounds__(BLOCK) rs_scatter_k(const u64* __restrict__ ki
             }
         }
         const u32 rank = (u32)__popcll(peers & lanemask_lt());
-        if (valid && rank == 0) cnt[j][w][d] = (u32)__popcll(peers);
+        if (valid && rank == 0) cnt[(j * NWAVES + w) * 256 + d] = (u16)__popcll(peers);
         dr[j] = valid ? (d | (rank << 16)) : 0xFFFF0000u;
     }
     __syncthreads();
-    {
-        u32 run = 0;
-        for (int j = 0; j < ITEMS; ++j)
+    u32 run = 0;  // thread t = digit t: its items' exclusive offsets in (row, wave) order, and its tile total
+    for (int j = 0; j < ITEMS; ++j)
 #pragma unroll
-            for (int ww = 0; ww < NWAVES; ++ww) {
-                const u32 c = cnt[j][ww][t];
-                cnt[j][ww][t] = run;
-                run += c;
-            }
-    }
+        for (int ww = 0; ww < NWAVES; ++ww) {
+            u16* c = &cnt[(j * NWAVES + ww) * 256 + t];
+            const u32 v = *c;
+            *c = (u16)run;
+            run += v;
+        }
+    u32 total;
+    const u32 off = block_exclusive<u32, Sum<u32>>(run, &total);
+    tile_off[t] = off;
     __syncthreads();
+    u32 local[ITEMS];
 #pragma unroll
     for (int j = 0; j < ITEMS; ++j) {
-        if ((dr[j] >> 16) == 0xFFFFu) continue;
         const u32 d = dr[j] & 0xFFFFu;
-        const u32 pos = base_s[d] + cnt[j][w][d] + (dr[j] >> 16);
-        kout[pos] = key[j];
-        if (VALUES) vout[pos] = val[j];
+        local[j] = (dr[j] >> 16) == 0xFFFFu ? 0xFFFFFFFFu : tile_off[d] + cnt[(j * NWAVES + w) * 256 + d] + (dr[j] >> 16);
+    }
+    __syncthreads();  // the counts are read: the staging area may overwrite them
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+        if (local[j] == 0xFFFFFFFFu) continue;
+        stage_k[local[j]] = key[j];
+        if (VALUES) stage_v[local[j]] = val[j];
+    }
+    __syncthreads();
+    for (int i = t; i < tile_n; i += BLOCK) {
+        const u64 k = stage_k[i];
+        const u32 d = (u32)(k >> shift) & mask;
+        const u32 pos = gbase[d] + (u32)i - tile_off[d];
+        kout[pos] = k;
+        if (VALUES) vout[pos] = stage_v[i];
     }
 }
 

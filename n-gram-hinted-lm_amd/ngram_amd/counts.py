@@ -112,6 +112,7 @@ class CountBuild:
         self.rank, self.world = rank, world
         self.min_cap = 1 << 20
         self.mode = "engine"
+        self.density: dict[int, float] = {}  # each level's hit density, from the last build with stats
         self.levels = tuple(levels)
         if not self.levels or list(self.levels) != sorted(set(self.levels)) or self.levels[0] < 1:
             raise ValueError(f"levels must ascend from >= 1: {self.levels}")
@@ -148,6 +149,7 @@ class CountBuild:
         self.rank, self.world = 0, 1
         self.min_cap = 1 << 20
         self.mode = "engine"
+        self.density: dict[int, float] = {}  # each level's hit density, from the last build with stats
         self.levels = tuple(levels)
         ls = LEVEL_SHARDS if level_shards is None else level_shards
         self.topk = topk
@@ -227,7 +229,7 @@ class CountBuild:
                     e0.record()
                     self.elib("ng_scan_count", self.tok[st:], n32, i32(k), bm_in, bms[k][st // 32 :], vi.table,
                               u64(vi.cap), vi.rep, self.x, t["keys"], t["cnts"], u64(t["cap"]), t["flags"], i32(grid),
-                              i32(int(li > 0 and k > 5)))
+                              i32(self._scan_mode(li, scanned)))
                     e1.record()
                 elif t["pbits"]:
                     if t["pending"] + n32 > t["emit"].numel():
@@ -248,6 +250,15 @@ class CountBuild:
         for k in levels:
             if tables[k]["pbits"]:
                 self._flush(tables[k], k)
+
+    def _scan_mode(self, li: int, scanned: list) -> int:
+        """The engine scan's mode for a shard's li-th scanned level: a lane per position (0) for the first level and
+        behind a dense previous level, else the LDS-listed set positions (2). The previous level's density is the
+        one its last build measured (stats), dense when unknown."""
+        if li == 0:
+            return 0
+        d = self.density.get(scanned[li - 1])
+        return 2 if d is not None and d < 0.5 else 0
 
     def _flush(self, t: dict, k: int) -> None:
         """Count a partitioned level's emitted keys: group them by sub-table, then count sub-table by sub-table."""
@@ -315,6 +326,9 @@ class CountBuild:
             self._scan(index, tables, bms, range(len(self.sizes)), set(over))
         lap("scan")
         hits = {k: int(self._popcount(bms[k]).item()) for k in self.levels} if self.stats else {}
+        for k, h in hits.items():
+            n_k = sum(self.sizes[: self.level_shards[k]])
+            self.density[k] = h / max(1, n_k)
         del bms
         out = torch.zeros((3, len(self.levels), N), dtype=torch.int32, device=dev)
         rows = all(k in self.levels for k in ROW_LEVELS)

@@ -71,9 +71,9 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
         vi = ValIndex(lib, x, torch.where(act, avail, torch.zeros_like(avail)), k, max_ids=MAX_IDS)
         hit = torch.zeros(vi.ids, dtype=torch.uint8, device=dev)
         bm = torch.empty(nwords, dtype=torch.int32, device=dev)
-        sparse = prev is not None and _popcount(lib, prev) * 16 < L
+        mode = 0 if prev is None or prev_hits * 2 > L else 2  # a lane per position while the gate is dense
         elib("ng_scan_exist", tok, L, i32(k), prev, bm, vi.table, u64(vi.cap), vi.rep, x, hit, flags, i32(grid),
-             i32(int(sparse)))
+             i32(mode))
         ctx = vi.ctx_of.long()
         matched = (ctx >= 0) & (hit[ctx.clamp_min(0)] != 0)
         length[matched] = k
@@ -82,6 +82,7 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
         active = matched
         bms.append(bm)
         prev = bm
+        prev_hits = _popcount(lib, bm)
         del vi, hit, ctx
     if timing is not None:
         torch.cuda.synchronize()
@@ -100,14 +101,14 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
         vi = ValIndex(lib, x, torch.where(fin, avail, torch.zeros_like(avail)), k, max_ids=MAX_IDS)
         bm_k = bms[k - 1]
         events = _popcount(lib, bm_k)
-        sparse = events * 16 < L
+        mode = 0 if events * 2 > L else 2
         tcap = max(1 << 16, int(min(events, 64 * vi.n + (1 << 20)) / LOAD))
         while True:
             keys = torch.full((tcap,), -1, dtype=torch.int64, device=dev)
             cnts = torch.zeros(tcap, dtype=torch.int32, device=dev)
             flags.zero_()
             elib("ng_scan_count", tok, L, i32(k), bm_k, scratch_bm, vi.table, u64(vi.cap), vi.rep, x, keys, cnts,
-                 u64(tcap), flags, i32(grid), i32(int(sparse)))
+                 u64(tcap), flags, i32(grid), i32(mode))
             if int(flags[0].item()) == 0:
                 break
             tcap *= 2
