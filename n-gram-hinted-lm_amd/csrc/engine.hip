@@ -465,3 +465,40 @@ extern "C" int ng_pos_gather(const int* ctx_of, i64 N, i64 lo, i64 hi, const u16
                                                                         out_dist, out_cnt, out_tok, out_tcnt, mask);
     return (int)hipGetLastError();
 }
+
+// ---------------------------------------------------------------------------------------------------------------
+// The count mixture's features (record_367_gpu_counts/track_1_short/counts/mix.py features :22-31)
+// ---------------------------------------------------------------------------------------------------------------
+
+namespace {
+__global__ void features_k(const int* __restrict__ counts, int L, i64 n, int nb, float* __restrict__ tot,
+                           float* __restrict__ dist, float* __restrict__ cnt, i64* __restrict__ bin,
+                           i64* __restrict__ sparse) {
+    const i64 q = blockIdx.x * (i64)blockDim.x + threadIdx.x;  // q = i * L + j, the outputs' [n, L] order
+    if (q >= n * L) return;
+    const i64 i = q / L;
+    const int j = (int)(q - i * L);
+    const u32 t = (u32)counts[(i64)j * n + i];
+    const float tf = (float)t;  // the uint32 total rounded to float32, as the reference converts it
+    const float df = (float)counts[((i64)L + j) * n + i];
+    const float cf = (float)counts[(2 * (i64)L + j) * n + i];
+    tot[q] = tf;
+    dist[q] = df;
+    cnt[q] = cf < tf ? cf : tf;
+    // floor(log2) of the float32 total (at least 1), as the float64 log2 rounded to float32
+    const float lg = (float)log2((double)(tf > 1.0f ? tf : 1.0f));
+    float fl = floorf(lg);
+    fl = fl < 0.0f ? 0.0f : (fl > (float)(nb - 1) ? (float)(nb - 1) : fl);
+    bin[q] = (i64)fl + (i64)nb * j;
+    sparse[q] = (i64)(df == 1.0f) + 2 * (i64)j + (i64)nb * L;
+}
+}  // namespace
+
+// counts int32 [3, L, n] (tot as uint32 bits, dist, cnt) -> tot, dist, min(cnt, tot) float32 [n, L], the bin index
+// clamp(floor(log2(max(tot, 1))), 0, nb - 1) + nb * level and the sparse index (dist == 1) + 2 * level + nb * L, int64.
+extern "C" int ng_features(const int* counts, int L, i64 n, int nb, float* tot, float* dist, float* cnt, i64* bin,
+                           i64* sparse, void* stream) {
+    if (L < 1 || nb < 1) return -1;
+    if (n > 0) features_k<<<grid_for(n * L, 256), 256, 0, (hipStream_t)stream>>>(counts, L, n, nb, tot, dist, cnt, bin, sparse);
+    return (int)hipGetLastError();
+}
