@@ -111,3 +111,25 @@ def test_overflow_reruns(corpus, reference, monkeypatch):
     assert ct.reruns[4] > 0
     tot, dist, cnt = ct.query_counts(corpus.query)
     assert np.array_equal(tot[:, 0], reference[4]["tot"]) and np.array_equal(cnt[:, 0], reference[4]["cnt"])
+
+
+def test_cache_ladder_rung(corpus, tmp_path):
+    from ngram_amd.cache_ladder import GpuCountIndex
+
+    paths, _ = corpus.write(tmp_path)
+    idx = GpuCountIndex.create(paths, 500_000, 4, [])
+    stats = idx.build()
+    train = corpus.train[:500_000]
+    bounds = np.array([0, 250_000, 500_000])
+    x = corpus.query[:-1]
+    from numpy.lib.stride_tricks import sliding_window_view
+
+    for k in (6, 10, 20):
+        # every (k + 1)-window within a shard is an occurrence: distinct windows = pairs, distinct k-prefixes = contexts
+        wins = np.concatenate([sliding_window_view(train[a:b], k + 1) for a, b in zip(bounds[:-1], bounds[1:])])
+        pairs = np.unique(wins, axis=0)
+        contexts = np.unique(pairs[:, :k], axis=0)
+        assert stats[f"contexts_{k}"] == len(contexts) and stats[f"pairs_{k}"] == len(pairs), k
+    assert stats["tokens"] == 500_000 and stats["seconds"] > 0
+    with pytest.raises(ValueError):
+        GpuCountIndex.create(paths, 10_000_000)
