@@ -96,6 +96,66 @@ int gen_set(uint16_t* out, const ng_i64* pos, ng_i64 m, int value, void* stream)
 int gen_copies(uint16_t* out, const ng_i64* copies, ng_i64 m, const uint16_t* src_tokens, ng_u64 key,
                const double* cdf, int ncdf, const uint16_t* perm, void* stream);
 
+/* ------------------------------------------------------------------------------------------------------------
+ * Engine entry points: no counterpart in the reference's libraries. They implement, for this repository's hosts
+ * (ngram_amd.counts / count_table / online / longest / exact_match), the query-filtered counting of
+ * record_367_gpu_counts/track_1_short/counts/build.py, exact_match/src/count_table.rs, online.rs and kgram.rs with
+ * split pair tables (u64 pair keys and u32 counts in two arrays) and selection-based ranking. Same conventions as
+ * above. k: 1..64.
+ * ------------------------------------------------------------------------------------------------------------ */
+
+/* one level's scan counted in a split table (keys EMPTY-filled, cnts zeroed); sparse 0: a lane per position, 1: a
+ * lane per bitmap word, 2: the set positions listed per wave in LDS (bm_in required for 1 and 2); flags[0] = full */
+int ng_scan_count(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, uint32_t* bm_out, const ng_u64* vt,
+                  ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, ng_u64* keys, uint32_t* cnts, ng_u64 cap,
+                  uint32_t* flags, int grid, int sparse, void* stream);
+/* existence only: hit bitmap and hit[context id] = 1 (hit zeroed by the caller); sparse as ng_scan_count's */
+int ng_scan_exist(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, uint32_t* bm_out, const ng_u64* vt,
+                  ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, unsigned char* hit, uint32_t* flags, int grid,
+                  int sparse, void* stream);
+/* a split table's occupied slots appended to (out_k, out_c) from *counter (zeroed by the caller) */
+int ng_table_compact(const ng_u64* keys, const uint32_t* cnts, ng_u64 cap, ng_u64* out_k, uint32_t* out_c,
+                     ng_u64* counter, void* stream);
+/* per context (pairs sorted by key, seg_bounds' start/end): total and top-k (1, 2, 4, 8) by count desc, token asc */
+int ng_ctx_topk(const ng_u64* uk, const uint32_t* agg, const ng_i64* start, const ng_i64* end, ng_i64 nctx, int topk,
+                ng_u64* tot, uint16_t* top_tok, uint32_t* top_cnt, void* stream);
+/* per query position with context in [lo, hi): tot, dist, cnt (binary search; with thr, only if its score
+ * count << 16 | 65535 - token >= thr[c]), the first kout of ktop top entries, mask bit li (mask may be NULL) */
+int ng_pos_gather(const int* ctx_of, ng_i64 N, ng_i64 lo, ng_i64 hi, const uint16_t* tgt, const ng_u64* uk,
+                  const uint32_t* agg, const ng_i64* start, const ng_i64* end, const ng_u64* tot,
+                  const uint16_t* top_tok, const uint32_t* top_cnt, const ng_u64* thr, int ktop, int kout, int li,
+                  int* out_tot, int* out_dist, int* out_cnt, uint16_t* out_tok, uint32_t* out_tcnt, int* mask,
+                  void* stream);
+/* corpus-wide level build (count_table.rs build_level): contexts into ck (slot = id), (slot << 16 | next) counted in
+ * the split table pk/pcnt; flags[0] bit 0 pair table full, bit 1 context table full */
+int ng_table_build(const uint16_t* tok, ng_i64 L, int k, ng_u64* ck, ng_u64 ccap, ng_u64* pk, uint32_t* pcnt,
+                   ng_u64 pcap, uint32_t* flags, int grid, void* stream);
+/* per key (EMPTY: none) its context-table slot or -1 */
+int ng_table_lookup(const ng_u64* keys, ng_i64 n, const ng_u64* ck, ng_u64 ccap, int* slot, void* stream);
+/* thr[c] = the kth largest pair score of each listed context (ids[m]; count_table.rs deep_last) */
+int ng_ctx_kth(const ng_u64* uk, const uint32_t* agg, const ng_i64* start, const ng_i64* end, const ng_i64* ids,
+               ng_i64 m, int kth, ng_u64* thr, void* stream);
+/* hint rows over table levels (count_table.rs query_rows); desc[v * 5]: slot_of, tot, top_tok, top_cnt, bucket */
+int ng_pos_rows(ng_i64 N, int nlv, const ng_i64* desc, int entries, short* cell, uint16_t* next, uint16_t* weights,
+                signed char* level, void* stream);
+/* online state (online.rs step rule): insert occurrences ending at pos[i]; merge a step's sorted distinct touched
+ * pairs (uk[0..*n)) into their contexts' top-E lists; answer queries; build hint rows */
+int ng_online_insert(const uint16_t* tok, const int* pos, ng_i64 m, int k, ng_u64* ck, ng_u64 ccap, ng_u64* pk,
+                     uint32_t* pcnt, ng_u64 pcap, uint32_t* ctx_tot, uint32_t* ctx_dist, ng_u64* ev, uint32_t* flags,
+                     void* stream);
+int ng_online_top(const ng_u64* uk, const ng_i64* n, ng_i64 m, const ng_u64* pk, const uint32_t* pcnt, ng_u64 pcap,
+                  ng_u64* score, ng_u64* ctx_top, int E, void* stream);
+int ng_online_query(const uint16_t* tok, const int* avail, const unsigned char* has_next, const int* pos, ng_i64 m,
+                    int k, const ng_u64* ck, ng_u64 ccap, const ng_u64* pk, const uint32_t* pcnt, ng_u64 pcap,
+                    const uint32_t* ctx_tot, const uint32_t* ctx_dist, int* qslot, uint32_t* tot, uint16_t* dist,
+                    uint32_t* cnt, int nc, int ci, void* stream);
+int ng_online_rows(const int* pos, ng_i64 m, int nlv, const ng_i64* desc, int E, short* cell, uint16_t* next,
+                   uint16_t* weights, int* hinted, void* stream);
+/* counts/mix.py features: counts int32 [3, L, n] -> float32 tot, dist, min(cnt, tot) [n, L], int64 bin and sparse
+ * indices [n, L] */
+int ng_features(const int* counts, int L, ng_i64 n, int nb, float* tot, float* dist, float* cnt, ng_i64* bin,
+                ng_i64* sparse, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
