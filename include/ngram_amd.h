@@ -119,13 +119,26 @@ int ng_table_compact(const ng_u64* keys, const uint32_t* cnts, ng_u64 cap, ng_u6
 /* per context (pairs sorted by key, seg_bounds' start/end): total and top-k (1, 2, 4, 8) by count desc, token asc */
 int ng_ctx_topk(const ng_u64* uk, const uint32_t* agg, const ng_i64* start, const ng_i64* end, ng_i64 nctx, int topk,
                 ng_u64* tot, uint16_t* top_tok, uint32_t* top_cnt, void* stream);
-/* per query position with context in [lo, hi): tot, dist, cnt (binary search; with thr, only if its score
+/* per query position with context in [lo, hi): tot, dist, cnt (from the split table pkeys/pcnts of pcap slots when
+ * given, else by binary search of the context's sorted pairs; with thr, only if its score
  * count << 16 | 65535 - token >= thr[c]), the first kout of ktop top entries, mask bit li (mask may be NULL) */
 int ng_pos_gather(const int* ctx_of, ng_i64 N, ng_i64 lo, ng_i64 hi, const uint16_t* tgt, const ng_u64* uk,
                   const uint32_t* agg, const ng_i64* start, const ng_i64* end, const ng_u64* tot,
-                  const uint16_t* top_tok, const uint32_t* top_cnt, const ng_u64* thr, int ktop, int kout, int li,
-                  int* out_tot, int* out_dist, int* out_cnt, uint16_t* out_tok, uint32_t* out_tcnt, int* mask,
-                  void* stream);
+                  const uint16_t* top_tok, const uint32_t* top_cnt, const ng_u64* thr, const ng_u64* pkeys,
+                  const uint32_t* pcnts, ng_u64 pcap, int ktop, int kout, int li, int* out_tot, int* out_dist,
+                  int* out_cnt, uint16_t* out_tok, uint32_t* out_tcnt, int* mask, void* stream);
+/* query index without a sort (replaces gpu_val_stats.py:604-651's sort-based one where ids need not agree across
+ * ranks): valid k-contexts of positions pos[0..n) (NULL: 0..n) inserted by compare-and-swap into table (cap + tail
+ * slots, EMPTY-filled, linear probing without wrap from umulhi(key, cap)); ctx_of[i] = slot or -1, rep[slot] = the
+ * inserting position; counters[0] += new contexts, counters[1] = 1 on reaching the table's end, counters[2] += key
+ * collisions found against the representative (k > 4) */
+int ng_query_index(const uint16_t* x, const int* avail, const int* pos, ng_i64 n, int k, ng_u64* table, ng_u64 cap,
+                   ng_u64 slots, uint32_t* rep, int* ctx_of, ng_u64* counters, void* stream);
+/* move a query index into a smaller EMPTY-filled table (cap + tail = slots): ctx_of[0..n) re-pointed, remap
+ * (old_slots ints) scratch, counters[1] = 1 on reaching the new table's end */
+int ng_query_index_shrink(const ng_u64* old_t, const uint32_t* old_rep, ng_u64 old_slots, ng_u64* table, ng_u64 cap,
+                          ng_u64 slots, uint32_t* rep, int* ctx_of, ng_i64 n, int* remap, ng_u64* counters,
+                          void* stream);
 /* corpus-wide level build (count_table.rs build_level): contexts into ck (slot = id), (slot << 16 | next) counted in
  * the split table pk/pcnt; flags[0] bit 0 pair table full, bit 1 context table full */
 int ng_table_build(const uint16_t* tok, ng_i64 L, int k, ng_u64* ck, ng_u64 ccap, ng_u64* pk, uint32_t* pcnt,

@@ -346,7 +346,8 @@ __global__ void __launch_bounds__(256) pos_gather_k(const int* __restrict__ ctx_
                                                     const u32* __restrict__ agg, const i64* __restrict__ start,
                                                     const i64* __restrict__ end, const u64* __restrict__ tot,
                                                     const u16* __restrict__ top_tok, const u32* __restrict__ top_cnt,
-                                                    const u64* __restrict__ thr, int ktop, int kout, int li,
+                                                    const u64* __restrict__ thr, const u64* __restrict__ pkeys,
+                                                    const u32* __restrict__ pcnts, u64 pcap, int ktop, int kout, int li,
                                                     int* __restrict__ out_tot,
                                                     int* __restrict__ out_dist,
                                                     int* __restrict__ out_cnt, u16* __restrict__ out_tok,
@@ -362,13 +363,27 @@ __global__ void __launch_bounds__(256) pos_gather_k(const int* __restrict__ ctx_
     out_tot[i] = (int)(u32)tot[c];
     out_dist[i] = (int)(b - a < 65535 ? b - a : 65535);
     const u64 want = ((u64)c << 16) | tgt[i];
-    while (a < b) {
-        const i64 m = (a + b) >> 1;
-        if (uk[m] < want) a = m + 1;
-        else b = m;
+    u32 n = 0;
+    if (pkeys) {  // the split table's count of (context, target)
+        u64 s = split_home(want + ((u64)lo << 16), pcap);
+        for (u64 probe = 0; probe < pcap; ++probe) {
+            const u64 cur = pkeys[s];
+            if (cur == want + ((u64)lo << 16)) {
+                n = pcnts[s];
+                break;
+            }
+            if (cur == EMPTY) break;
+            s = s + 1 == pcap ? 0 : s + 1;
+        }
+    } else {  // binary search of the context's pairs, sorted by token
+        while (a < b) {
+            const i64 m = (a + b) >> 1;
+            if (uk[m] < want) a = m + 1;
+            else b = m;
+        }
+        if (a < e && uk[a] == want) n = agg[a];
     }
-    if (a < e && uk[a] == want) {
-        const u32 n = agg[a];
+    if (n) {
         // the CNT_TOP rule: with a threshold, only a pair ranked at or above it (its score >= thr) gives its count
         const u64 th = thr ? thr[c] : 0;
         if (th == 0 || rank_score(want, n) >= th) out_cnt[i] = (int)n;
@@ -453,15 +468,19 @@ extern "C" int ng_ctx_topk(const u64* uk, const u32* agg, const i64* start, cons
 
 // Per query position: tot, dist, cnt, the first kout <= ktop top entries (out_tok/out_tcnt [N, kout]; kout 0: none)
 // and mask bit li (mask may be NULL). thr (may be NULL): per context the score (count << 16 | 65535 - token) of its
-// last pair that still gives cnt (0: every pair does).
+// last pair that still gives cnt (0: every pair does). cnt comes from the split table pkeys/pcnts (pcap slots) when
+// given, else by binary search of the context's pairs (uk sorted by key).
 extern "C" int ng_pos_gather(const int* ctx_of, i64 N, i64 lo, i64 hi, const u16* tgt, const u64* uk, const u32* agg,
                              const i64* start, const i64* end, const u64* tot, const u16* top_tok, const u32* top_cnt,
-                             const u64* thr, int ktop, int kout, int li, int* out_tot, int* out_dist, int* out_cnt,
-                             u16* out_tok, u32* out_tcnt, int* mask, void* stream) {
+                             const u64* thr, const u64* pkeys, const u32* pcnts, u64 pcap, int ktop, int kout, int li,
+                             int* out_tot, int* out_dist, int* out_cnt, u16* out_tok, u32* out_tcnt, int* mask,
+                             void* stream) {
+    if (pkeys && pcap == 0) return -1;
     if (kout < 0 || kout > ktop || (mask && (li < 0 || li > 30))) return -1;
     if (N > 0)
         pos_gather_k<<<grid_for(N, 256), 256, 0, (hipStream_t)stream>>>(ctx_of, N, lo, hi, tgt, uk, agg, start, end, tot,
-                                                                        top_tok, top_cnt, thr, ktop, kout, li, out_tot,
+                                                                        top_tok, top_cnt, thr, pkeys, pcnts, pcap, ktop,
+                                                                        kout, li, out_tot,
                                                                         out_dist, out_cnt, out_tok, out_tcnt, mask);
     return (int)hipGetLastError();
 }
@@ -500,5 +519,137 @@ extern "C" int ng_features(const int* counts, int L, i64 n, int nb, float* tot, 
                            i64* sparse, void* stream) {
     if (L < 1 || nb < 1) return -1;
     if (n > 0) features_k<<<grid_for(n * L, 256), 256, 0, (hipStream_t)stream>>>(counts, L, n, nb, tot, dist, cnt, bin, sparse);
+    return (int)hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// The engine's query index: the distinct valid query contexts inserted into an open-addressing table by
+// compare-and-swap (no sort). Slot = context id; linear probing without wrap-around from umulhi(key, cap) over a
+// table of cap + tail slots whose last slot stays empty, which is the layout probe_key walks. rep[slot] = the
+// smallest query position with that context (atomicMin: the same on every run). The canonical, sorted layout of
+// gpu_val_stats' ValIndex is only needed for ids that agree across ranks; on one GPU any layout is exact.
+// ---------------------------------------------------------------------------------------------------------------
+
+namespace {
+template <int K>
+__global__ void qindex_insert_k(const u16* __restrict__ x, const int* __restrict__ avail, const int* __restrict__ pos,
+                                i64 n, int k, u64* table, u64 cap, u64 slots, u32* rep, int* __restrict__ ctx_of,
+                                u64* counters) {
+    const i64 j = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    bool inserted = false;
+    if (j < n) {
+        const i64 i = pos ? pos[j] : j;
+        i64 slot = -1;
+        if (avail[i] >= (K > 0 ? K : k)) {
+            const u64 key = key_at<K>(x + i + 1, k);
+            u64 s = __umul64hi(key, cap);
+            while (true) {
+                if (s + 1 >= slots) {  // the last slot must stay empty
+                    atomicOr((unsigned int*)&counters[1], 1u);
+                    break;
+                }
+                const u64 cur = table[s];
+                if (cur == key) {
+                    slot = (i64)s;
+                    break;
+                }
+                if (cur == EMPTY) {
+                    const u64 prev = atomicCAS((unsigned long long*)&table[s], EMPTY, key);
+                    if (prev == EMPTY) {  // this position inserted the context: it is the representative
+                        rep[s] = (u32)i;
+                        inserted = true;
+                        slot = (i64)s;
+                        break;
+                    }
+                    if (prev == key) {
+                        slot = (i64)s;
+                        break;
+                    }
+                }
+                ++s;
+            }
+        }
+        if (slot >= 0 || !pos) ctx_of[i] = (int)slot;
+    }
+    // one counter atomic per wave (a single address hit by every new context would serialize)
+    const u64 b = __ballot(inserted);
+    if (b && lane_id() == __ffsll((unsigned long long)__ballot(1)) - 1)
+        atomicAdd((unsigned long long*)&counters[0], (unsigned long long)__popcll(b));
+}
+
+// Re-insert a sparse table's keys (and representatives) into a table sized for them: new slot of each old slot.
+__global__ void qindex_shrink_k(const u64* __restrict__ old_t, const u32* __restrict__ old_rep, u64 old_slots,
+                                u64* table, u64 cap, u64 slots, u32* rep, int* __restrict__ remap, u64* counters) {
+    const i64 o = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    if (o >= (i64)old_slots) return;
+    const u64 key = old_t[o];
+    if (key == EMPTY) {
+        remap[o] = -1;
+        return;
+    }
+    u64 s = __umul64hi(key, cap);
+    while (true) {
+        if (s + 1 >= slots) {
+            atomicOr((unsigned int*)&counters[1], 1u);
+            remap[o] = -1;
+            return;
+        }
+        if (atomicCAS((unsigned long long*)&table[s], EMPTY, key) == EMPTY) break;  // keys are distinct here
+        ++s;
+    }
+    rep[s] = old_rep[o];
+    remap[o] = (int)s;
+}
+
+__global__ void qindex_remap_k(int* __restrict__ ctx_of, i64 n, const int* __restrict__ remap) {
+    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int c = ctx_of[i];
+    if (c >= 0) ctx_of[i] = remap[c];
+}
+
+// Hashed contexts (k > 4): each position's k tokens against its slot's representative's; mismatches into *bad.
+__global__ void qindex_verify_k(const u16* __restrict__ x, const int* __restrict__ pos, i64 n, int k,
+                                const int* __restrict__ ctx_of, const u32* __restrict__ rep, u64* bad) {
+    const i64 j = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    if (j >= n) return;
+    const i64 i = pos ? pos[j] : j;
+    const int s = ctx_of[i];
+    if (s < 0) return;
+    const i64 r = rep[s];
+    for (int t = 0; t < k; ++t)
+        if (x[i - t] != x[r - t]) {
+            atomicAdd((unsigned long long*)bad, 1ull);
+            return;
+        }
+}
+}  // namespace
+
+// Move a query index into a smaller table (cap + tail = slots, EMPTY-filled): ctx_of[0..n) re-pointed; remap
+// (old_slots ints) is scratch. counters[1] = 1 if the probes ran into the new table's end.
+extern "C" int ng_query_index_shrink(const u64* old_t, const u32* old_rep, u64 old_slots, u64* table, u64 cap,
+                                     u64 slots, u32* rep, int* ctx_of, i64 n, int* remap, u64* counters,
+                                     void* stream) {
+    if (cap == 0 || slots <= cap || slots > (1ull << 31)) return -1;
+    hipStream_t st = (hipStream_t)stream;
+    if (old_slots > 0)
+        qindex_shrink_k<<<grid_for((i64)old_slots, 256), 256, 0, st>>>(old_t, old_rep, old_slots, table, cap, slots, rep,
+                                                                      remap, counters);
+    if (n > 0) qindex_remap_k<<<grid_for(n, 256), 256, 0, st>>>(ctx_of, n, remap);
+    return (int)hipGetLastError();
+}
+
+// Insert the valid query contexts of positions pos[0..n) (pos NULL: 0..n) into table (cap + tail slots, EMPTY-filled):
+// ctx_of[i] = slot (-1 where invalid; with pos, only listed positions are written), rep[slot] = the position that
+// inserted it.
+// counters[0] += new contexts, counters[1] = 1 if the probes ran into the table's end; with k > 4, counters[2] +=
+// positions whose tokens differ from their slot's representative (a 64-bit key collision).
+extern "C" int ng_query_index(const u16* x, const int* avail, const int* pos, i64 n, int k, u64* table, u64 cap,
+                              u64 slots, u32* rep, int* ctx_of, u64* counters, void* stream) {
+    if (n <= 0) return 0;
+    if (cap == 0 || slots <= cap || slots > (1ull << 31)) return -1;
+    hipStream_t st = (hipStream_t)stream;
+    LEVEL_SWITCH(k, (qindex_insert_k<K><<<grid_for(n, 256), 256, 0, st>>>(x, avail, pos, n, k, table, cap, slots, rep, ctx_of, counters)));
+    if (k > 4) qindex_verify_k<<<grid_for(n, 256), 256, 0, st>>>(x, pos, n, k, ctx_of, rep, counters + 2);
     return (int)hipGetLastError();
 }

@@ -183,14 +183,8 @@ __global__ void online_query_k(const u16* __restrict__ tok, const int* __restric
     }
 }
 
-// Hint rows of the queries pos[i]: the deepest described level (desc[v * 5 ...], deepest first: qslot (int [m]),
-// ctx_tot (u32), ctx_top (u64 [slots, E]), bucket, unused) whose context occurred: cell, E next tokens, weights.
-__global__ void online_rows_k(const int* __restrict__ pos, i64 m, int nlv, const i64* __restrict__ desc, int E,
-                              short* __restrict__ cell, u16* __restrict__ next, u16* __restrict__ weights,
-                              int* __restrict__ hinted) {
-    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
-    if (i >= m) return;
-    const i64 g = pos[i];
+__device__ __forceinline__ bool online_row(i64 g, i64 i, int nlv, const i64* __restrict__ desc, int E,
+                                           short* __restrict__ cell, u16* __restrict__ next, u16* __restrict__ weights) {
     for (int v = 0; v < nlv; ++v) {
         const i64* d = desc + v * 5;
         const int slot = ((const int*)d[0])[i];
@@ -215,9 +209,24 @@ __global__ void online_rows_k(const int* __restrict__ pos, i64 m, int nlv, const
             next[g * E + r] = sc ? (u16)(0xFFFFu - (u32)(sc & 0xFFFF)) : (u16)0;
             weights[g * E + r] = sc ? (u16)rint((double)(u32)(sc >> 16) / sum * 65535.0) : (u16)0;
         }
-        atomicAdd(hinted, 1);
-        return;
+        return true;
     }
+    return false;
+}
+
+
+// Hint rows of the queries pos[i]: the deepest described level (desc[v * 5 ...], deepest first: qslot (int [m]),
+// ctx_tot (u32), ctx_top (u64 [slots, E]), bucket, unused) whose context occurred: cell, E next tokens, weights.
+__global__ void online_rows_k(const int* __restrict__ pos, i64 m, int nlv, const i64* __restrict__ desc, int E,
+                              short* __restrict__ cell, u16* __restrict__ next, u16* __restrict__ weights,
+                              int* __restrict__ hinted) {
+    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    bool done = false;
+    if (i < m) done = online_row(pos[i], i, nlv, desc, E, cell, next, weights);
+    // one counter atomic per wave
+    const u64 b = __ballot(done);
+    if (b && (int)(threadIdx.x & (WAVE - 1)) == __ffsll((unsigned long long)__ballot(1)) - 1)
+        atomicAdd(hinted, __popcll(b));
 }
 
 }  // namespace

@@ -26,6 +26,7 @@ from .data import BOS, HEADER_BYTES, shard_tokens
 from .gpu_val_stats import PAIRS as GVS_PAIRS
 from .gpu_val_stats import ValIndex, layout
 from .lib import Lib, i32, u64
+from .qindex import QueryIndex
 
 GAP = 32
 LEVELS = (2, 3, 4, 5, 6, 10, 20)
@@ -303,7 +304,10 @@ class CountBuild:
         self.kernel_events = []
         self.x = x
         N = x.numel()
-        index = {k: ValIndex(lib, x, avail, k, max_ids=MAX_IDS) for k in self.levels}
+        if self.mode == "engine":
+            index = {k: QueryIndex(self.elib, x, avail, k) for k in self.levels}
+        else:
+            index = {k: ValIndex(lib, x, avail, k, max_ids=MAX_IDS) for k in self.levels}
         lap("index")
         self.grid = torch.cuda.get_device_properties(dev).multi_processor_count * 32
         caps = self.caps()
@@ -374,8 +378,9 @@ class CountBuild:
         return out
 
     def _outputs_engine(self, li, k, vi, t, tgt, out, want):
-        """One level's outputs with the engine: the split table compacted, sorted by pair key, per-context totals and
-        top entries by selection, then one gather per query position."""
+        """One level's outputs with the engine: the split table compacted, its pairs sorted by context, per-context
+        totals and top entries by selection, then one gather per query position (the target's count looked up in the
+        split table)."""
         elib, lib, dev = self.elib, self.lib, self.tok.device
         N, lo, hi = vi.ctx_of.numel(), 0, vi.ids
         counter = torch.zeros(1, dtype=torch.int64, device=dev)
@@ -387,15 +392,14 @@ class CountBuild:
         e0.record()
         elib("ng_table_compact", t["keys"], t["cnts"], u64(cap), ck, cc, counter)
         e1.record()
-        t.pop("keys"), t.pop("cnts")
         U = int(counter.item())
         n_own = hi - lo
         ctx_bits = max(1, (max(n_own, 2) - 1).bit_length())
         uk, agg = torch.empty(U, dtype=torch.int64, device=dev), torch.empty(U, dtype=torch.int32, device=dev)
         e0, e1 = self._event("sort", k, -1, U)
         e0.record()
-        if U:
-            lib.cub("sort_pairs", ck, uk, cc, agg, U, i32(0), i32(16 + ctx_bits))
+        if U:  # by context only: the target's count comes from the split table, the ranking needs no token order
+            lib.cub("sort_pairs", ck, uk, cc, agg, U, i32(16), i32(16 + ctx_bits))
         e1.record()
         del ck, cc
         start = torch.zeros(n_own, dtype=torch.int64, device=dev)
@@ -412,10 +416,11 @@ class CountBuild:
         e0, e1 = self._event("pos_gather", k, -1, N)
         e0.record()
         kout = self.topk
-        elib("ng_pos_gather", vi.ctx_of, N, lo, hi, tgt, uk, agg, start, end, tot, top_tok, top_cnt, None, i32(ktop),
-             i32(kout), i32(li), out[0, li], out[1, li], out[2, li], self.top_tok[li] if kout else None,
-             self.top_cnt[li] if kout else None, None)
+        elib("ng_pos_gather", vi.ctx_of, N, lo, hi, tgt, uk, agg, start, end, tot, top_tok, top_cnt, None, t["keys"],
+             t["cnts"], u64(cap), i32(ktop), i32(kout), i32(li), out[0, li], out[1, li], out[2, li],
+             self.top_tok[li] if kout else None, self.top_cnt[li] if kout else None, None)
         e1.record()
+        t.pop("keys"), t.pop("cnts")
         return U, tot, top_tok, top_cnt, ktop
 
     def _outputs_record(self, li, k, vi, t, tgt, out, want):

@@ -7,8 +7,8 @@ val_hint_rows, the approximate SlotIndex/StreamIndex) are not provided: looking 
 Definitions (kgram.rs:7-9): a query position's k-context is its k tokens ending at it, valid iff they lie in its
 segment (segments start at the first query token, at every BOS and, for kgram_query_counts, at each of `breaks`); an
 occurrence is any k tokens within one shard followed by a token of the same shard. Context ids are this build's
-(the distinct valid contexts in the order of their keys, 0 .. C - 1); every output other than the ids themselves is
-id-independent and equals the reference's. `memory` bounds the CPU build's working set and has no effect here;
+(the distinct valid contexts in the order of their query-table slots, 0 .. C - 1); every output other than the ids
+themselves is id-independent and equals the reference's. `memory` bounds the CPU build's working set and has no effect here;
 `filter` (a bitmap of a smaller k) only saves probes there and is checked, not needed, here."""
 
 from __future__ import annotations
@@ -20,15 +20,15 @@ import torch
 
 from .count_table import CountTable  # noqa: F401  (part of the surface)
 from .data import BOS, HEADER_BYTES, segments, shard_tokens
-from .gpu_val_stats import ValIndex, layout
+from .gpu_val_stats import layout
 from .lib import Lib, i32, u64
 from .online import OnlineRows  # noqa: F401  (part of the surface)
+from .qindex import QueryIndex
 
 COUNTS = [2, 3, 5, 9, 17, 33]
 PURITIES = [0.3, 0.5, 0.7, 0.85, 0.95]
 LEVELS = [10, 20]
 CELLS = (len(LEVELS) + 2) * (len(COUNTS) + 1) * (len(PURITIES) + 1)
-MAX_IDS = (1 << 25) - 4096
 LOAD = 0.7
 NONE32 = 0xFFFFFFFF
 
@@ -92,7 +92,7 @@ def _level(files, tokens: np.ndarray, k: int, top: int, train_tokens=None, break
     x = torch.from_numpy(tokens[:-1].view(np.int16).copy()).to(dev)
     tgt = torch.from_numpy(tokens[1:].view(np.int16).copy()).to(dev)
     avail = torch.from_numpy(segments(tokens[:-1], list(breaks))).to(dev)
-    vi = ValIndex(lib, x, avail, k, max_ids=MAX_IDS)
+    vi = QueryIndex(lib, x, avail, k)
     grid = torch.cuda.get_device_properties(dev).multi_processor_count * 32
     T = sum(sizes)
     cap = max(1 << 16, int(min(T, 64 * vi.n + (1 << 20)) / LOAD))

@@ -25,9 +25,10 @@ import time
 import numpy as np
 import torch
 
-from .counts import MAX_IDS, record_lib
+from .counts import record_lib
 from .data import BOS, HEADER_BYTES, shard_tokens
-from .gpu_val_stats import ValIndex, layout
+from .gpu_val_stats import layout
+from .qindex import QueryIndex
 from .lib import Lib, i32, u64
 
 LOAD = 0.7
@@ -68,7 +69,7 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
         n_act = int(act.sum().item())
         if n_act == 0:
             break
-        vi = ValIndex(lib, x, torch.where(act, avail, torch.zeros_like(avail)), k, max_ids=MAX_IDS)
+        vi = QueryIndex(elib, x, avail, k, torch.nonzero(act).squeeze(1).to(torch.int32))
         hit = torch.zeros(vi.ids, dtype=torch.uint8, device=dev)
         bm = torch.empty(nwords, dtype=torch.int32, device=dev)
         mode = 0 if prev is None or prev_hits * 2 > L else 2  # a lane per position while the gate is dense
@@ -98,7 +99,7 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
         fin = length == k
         if not bool(fin.any()):
             continue
-        vi = ValIndex(lib, x, torch.where(fin, avail, torch.zeros_like(avail)), k, max_ids=MAX_IDS)
+        vi = QueryIndex(elib, x, avail, k, torch.nonzero(fin).squeeze(1).to(torch.int32))
         bm_k = bms[k - 1]
         events = _popcount(lib, bm_k)
         mode = 0 if events * 2 > L else 2
@@ -131,8 +132,8 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
         top_cnt = torch.zeros(vi.ids, dtype=torch.int32, device=dev)
         lib("seg_bounds", uk, U, start, end)
         elib("ng_ctx_topk", uk, agg, start, end, vi.ids, i32(1), tot, top_tok, top_cnt)
-        elib("ng_pos_gather", vi.ctx_of, N, 0, vi.ids, x, uk, agg, start, end, tot, top_tok, top_cnt, None, i32(1),
-             i32(1), i32(0), o_tot, o_dist, o_cnt, nxt, cnt, None)
+        elib("ng_pos_gather", vi.ctx_of, N, 0, vi.ids, x, uk, agg, start, end, tot, top_tok, top_cnt, None, None,
+             None, u64(0), i32(1), i32(1), i32(0), o_tot, o_dist, o_cnt, nxt, cnt, None)
         del vi, uk, agg, start, end, tot, top_tok, top_cnt
     if timing is not None:
         torch.cuda.synchronize()

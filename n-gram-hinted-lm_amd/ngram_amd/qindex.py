@@ -1,0 +1,70 @@
+"""The engine's query index (libngram_amd.so ng_query_index): per level, the distinct valid query k-contexts inserted
+into an open-addressing table by compare-and-swap, with no sort. The same attributes as gpu_val_stats.ValIndex
+(`n`, `valid`, `cap`, `table`, `rep`, `ids`, `ctx_of`), so the engine's scans probe it the same way (linear probing
+without wrap-around from umulhi(key, cap); the table ends with an empty slot). Unlike ValIndex's canonical, sorted
+layout (the reference's, gpu_val_stats.py:604-651, which makes ids agree across ranks), slots follow insertion races;
+on one GPU every output is id-independent, so any layout is exact. Hashed keys (k > 4) are verified against each
+slot's representative (the position whose compare-and-swap inserted it): a 64-bit collision raises, as ValIndex's does."""
+
+from __future__ import annotations
+
+import torch
+
+from .lib import Lib, i32, u64
+
+TAIL = 4096  # slots past cap that linear probing may run into; the last stays empty
+
+
+class QueryIndex:
+    def __init__(self, lib: Lib, x: torch.Tensor, avail: torch.Tensor, k: int, positions: torch.Tensor | None = None):
+        """Index the valid k-contexts of the query positions (all of x, or the int32 `positions`)."""
+        dev = x.device
+        N = x.numel()
+        m = N if positions is None else int(positions.numel())
+        cap = 2 * m + 1024
+        while True:
+            slots = cap + TAIL
+            table = torch.full((slots,), -1, dtype=torch.int64, device=dev)
+            rep = torch.full((slots,), -1, dtype=torch.int32, device=dev)
+            ctx_of = torch.full((N,), -1, dtype=torch.int32, device=dev) if positions is not None else \
+                torch.empty(N, dtype=torch.int32, device=dev)
+            counters = torch.zeros(3, dtype=torch.int64, device=dev)
+            if m:
+                lib("ng_query_index", x, avail, positions, m, i32(k), table, u64(cap), u64(slots), rep, ctx_of,
+                    counters)
+            c = counters.cpu().tolist()
+            if c[1] == 0:
+                break
+            cap *= 2  # a probe run reached the table's end (never at load <= 1/2 in practice): twice the slots
+        if c[2]:
+            raise RuntimeError(f"k={k}: {c[2]} query positions collide with another context's key")
+        n_ctx = int(c[0])
+        if m and cap > 4 * n_ctx + 4096:
+            # sized for every position, used by far fewer contexts: move them to a table sized for them, so that
+            # context ids (slots) take fewer bits
+            small = 2 * n_ctx + 1024
+            while True:
+                t2 = torch.full((small + TAIL,), -1, dtype=torch.int64, device=dev)
+                r2 = torch.full((small + TAIL,), -1, dtype=torch.int32, device=dev)
+                remap = torch.empty(slots, dtype=torch.int32, device=dev)
+                c2 = torch.zeros(3, dtype=torch.int64, device=dev)
+                lib("ng_query_index_shrink", table, rep, u64(slots), t2, u64(small), u64(small + TAIL), r2, ctx_of,
+                    N, remap, c2)
+                if int(c2[1].item()) == 0:
+                    break
+                small *= 2
+            table, rep, cap, slots = t2, r2, small, small + TAIL
+            del remap
+        self.n = n_ctx
+        self.cap = cap
+        self.ids = slots
+        self.table = table
+        self.rep = rep
+        self.ctx_of = ctx_of
+        self._valid = None
+
+    @property
+    def valid(self) -> int:
+        if self._valid is None:
+            self._valid = int((self.ctx_of >= 0).sum().item())
+        return self._valid
