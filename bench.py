@@ -23,6 +23,9 @@ sys.path.insert(0, str(ROOT / "n-gram-hinted-lm_amd"))
 
 HBM_PEAK_GBS = 8000.0
 SCAN_KERNELS = ("scan_count", "scan_level", "scan_emit")  # the level scans, whichever counting CountBuild uses
+# "part" mode counts after the scan (emitted hits packed, hash-partitioned, counted in LDS): its roofline kernel set is
+# the whole count path, whose algorithmic bytes are the build's 2 per position scanned + 16 per hit
+PART_KERNELS = ("scan_emit", "gather", "partition", "count")
 
 
 def parse() -> argparse.Namespace:
@@ -35,7 +38,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--query-tokens", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other configurations' measurements")
-    ap.add_argument("--mode", default="engine", choices=("engine", "record", "partitioned"), help="CountBuild.mode")
+    ap.add_argument("--mode", default="engine", choices=("engine", "part", "record", "partitioned"),
+                    help="CountBuild.mode")
     ap.add_argument("--cpu-tokens", type=int, default=100_000_000, help="CPU baseline: corpus prefix")
     ap.add_argument("--cpu-queries", type=int, default=2_000_000, help="CPU baseline: query positions")
     return ap.parse_args()
@@ -293,6 +297,7 @@ def main() -> None:
     t0 = time.perf_counter()
     class_ms: dict[str, float] = {}
     scan_ms, scan_launches = 0.0, 0
+    roof = PART_KERNELS if cb.mode == "part" else SCAN_KERNELS
     for step in range(args.steps):
         out = cb.counts(x, tgt, avail)
         log(f"step {step}: {sum(cb.timing.values()) / (step + 1):.4f} s/step so far")
@@ -300,7 +305,7 @@ def main() -> None:
         for name, k, i, n, e0, e1 in cb.kernel_events:
             ms = e0.elapsed_time(e1)
             class_ms[name] = class_ms.get(name, 0.0) + ms
-            if name in SCAN_KERNELS:
+            if name in roof:
                 scan_ms += ms
                 scan_launches += 1
     torch.cuda.synchronize()
@@ -313,7 +318,8 @@ def main() -> None:
     for name, k, i, n, _, _ in cb.kernel_events:
         if name in SCAN_KERNELS:
             positions[k] += n
-    step_bytes = sum(2.0 * positions[k] + (8.0 if info[k]["pbits"] else 16.0) * info[k]["hits"] for k in cfg.levels)
+    per_hit = {k: 16.0 if cb.mode == "part" or not info[k]["pbits"] else 8.0 for k in cfg.levels}
+    step_bytes = sum(2.0 * positions[k] + per_hit[k] * info[k]["hits"] for k in cfg.levels)
     scan_bytes = args.steps * step_bytes
     achieved = scan_bytes / (scan_ms / 1e3) / 1e9 if scan_ms > 0 else 0.0
     build_bytes = 2.0 * T + 16.0 * hits  # the count build's B_build = 2 T + 16 E
@@ -330,7 +336,8 @@ def main() -> None:
         "config": {"workload": f"{cfg.name}: count build of {T} corpus tokens ({len(sizes)} shards) for n="
                                f"{list(cfg.levels)} + top-{cfg.topk}/count/hit queries at {N} positions",
                    "corpus_tokens": T, "query_positions": N, "levels": list(cfg.levels), "topk": cfg.topk},
-        "roofline": {"bound": "hbm", "kernel": f"level scan ({cb.mode}: " + ", ".join(sorted({n for n, *_ in cb.kernel_events if n in SCAN_KERNELS})) + ")",
+        "roofline": {"bound": "hbm", "kernel": ("count path" if cb.mode == "part" else "level scan") + f" ({cb.mode}: "
+                     + ", ".join(sorted({n for n, *_ in cb.kernel_events if n in roof})) + ")",
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None,
                      "launches_per_step": scan_launches // max(1, args.steps),

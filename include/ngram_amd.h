@@ -109,6 +109,13 @@ int gen_copies(uint16_t* out, const ng_i64* copies, ng_i64 m, const uint16_t* sr
 int ng_scan_count(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, uint32_t* bm_out, const ng_u64* vt,
                   ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, ng_u64* keys, uint32_t* cnts, ng_u64 cap,
                   uint32_t* flags, int grid, int sparse, void* stream);
+/* the emitting scan: block b of `grid` appends its hits' mix64(context id << 16 | next) to ev[b * region ...] and
+ * stores how many in ev_count[b]; region >= ng_emit_region(L, grid) = ceil(L / (grid * 8192)) * 8192; flags[0] bit 2
+ * a region overflowed. sparse as ng_scan_count's */
+ng_u64 ng_emit_region(ng_i64 L, int grid);
+int ng_scan_emit(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, uint32_t* bm_out, const ng_u64* vt,
+                 ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, ng_u64* ev, ng_u64 region, uint32_t* ev_count,
+                 uint32_t* flags, int grid, int sparse, void* stream);
 /* existence only: hit bitmap and hit[context id] = 1 (hit zeroed by the caller); sparse as ng_scan_count's */
 int ng_scan_exist(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, uint32_t* bm_out, const ng_u64* vt,
                   ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, unsigned char* hit, uint32_t* flags, int grid,
@@ -119,18 +126,18 @@ int ng_table_compact(const ng_u64* keys, const uint32_t* cnts, ng_u64 cap, ng_u6
 /* per context (pairs sorted by key, seg_bounds' start/end): total and top-k (1, 2, 4, 8) by count desc, token asc */
 int ng_ctx_topk(const ng_u64* uk, const uint32_t* agg, const ng_i64* start, const ng_i64* end, ng_i64 nctx, int topk,
                 ng_u64* tot, uint16_t* top_tok, uint32_t* top_cnt, void* stream);
-/* per query position with context in [lo, hi): tot, dist, cnt (from the split table pkeys/pcnts of pcap slots when
- * given, else by binary search of the context's sorted pairs; with thr, only if its score
- * count << 16 | 65535 - token >= thr[c]), the first kout of ktop top entries, mask bit li (mask may be NULL) */
+/* per query position with context in [lo, hi): tot, dist, cnt (qcnt[i] when given, else from the split table
+ * pkeys/pcnts of pcap slots when given, else by binary search of the context's sorted pairs; with thr, only if its
+ * score count << 16 | 65535 - token >= thr[c]), the first kout of ktop top entries, mask bit li (mask may be NULL) */
 int ng_pos_gather(const int* ctx_of, ng_i64 N, ng_i64 lo, ng_i64 hi, const uint16_t* tgt, const ng_u64* uk,
                   const uint32_t* agg, const ng_i64* start, const ng_i64* end, const ng_u64* tot,
                   const uint16_t* top_tok, const uint32_t* top_cnt, const ng_u64* thr, const ng_u64* pkeys,
-                  const uint32_t* pcnts, ng_u64 pcap, int ktop, int kout, int li, int* out_tot, int* out_dist,
-                  int* out_cnt, uint16_t* out_tok, uint32_t* out_tcnt, int* mask, void* stream);
+                  const uint32_t* pcnts, ng_u64 pcap, const uint32_t* qcnt, int ktop, int kout, int li, int* out_tot,
+                  int* out_dist, int* out_cnt, uint16_t* out_tok, uint32_t* out_tcnt, int* mask, void* stream);
 /* query index without a sort (replaces gpu_val_stats.py:604-651's sort-based one where ids need not agree across
  * ranks): valid k-contexts of positions pos[0..n) (NULL: 0..n) inserted by compare-and-swap into table (cap + tail
  * slots, EMPTY-filled, linear probing without wrap from umulhi(key, cap)); ctx_of[i] = slot or -1, rep[slot] = the
- * inserting position; counters[0] += new contexts, counters[1] = 1 on reaching the table's end, counters[2] += key
+ * inserting position; counters[0] += the table's occupied slots afterwards, counters[1] = 1 on reaching the table's end, counters[2] += key
  * collisions found against the representative (k > 4) */
 int ng_query_index(const uint16_t* x, const int* avail, const int* pos, ng_i64 n, int k, ng_u64* table, ng_u64 cap,
                    ng_u64 slots, uint32_t* rep, int* ctx_of, ng_u64* counters, void* stream);
@@ -139,6 +146,22 @@ int ng_query_index(const uint16_t* x, const int* avail, const int* pos, ng_i64 n
 int ng_query_index_shrink(const ng_u64* old_t, const uint32_t* old_rep, ng_u64 old_slots, ng_u64* table, ng_u64 cap,
                           ng_u64 slots, uint32_t* rep, int* ctx_of, ng_i64 n, int* remap, ng_u64* counters,
                           void* stream);
+/* partitioned counting (no global atomics): offsets[s] = cnt[0] + ... + cnt[s - 1], s = 0..nseg */
+int ng_seg_offsets(const uint32_t* cnt, ng_i64 nseg, ng_u64* offsets, void* stream);
+/* segment s = cnt[s] items at src + (bases ? bases[s] : s * region) packed to dst + offsets[s]; values may be NULL */
+int ng_seg_gather(const ng_u64* src_k, const uint32_t* src_v, ng_u64 region, const ng_i64* bases, const uint32_t* cnt,
+                  ng_i64 nseg, const ng_u64* offsets, ng_u64* dst_k, uint32_t* dst_v, void* stream);
+/* start[p], p = 0..2^pbits, of events sorted by their top pbits (pbits <= 24) */
+int ng_part_bounds(const ng_u64* ev, ng_i64 n, int pbits, ng_i64* start, void* stream);
+/* qk[i] = mix64(ctx_of[i] << 16 | tgt[i]) for ids in [lo, hi), else EMPTY; qv[i] = i */
+int ng_part_lookups(const int* ctx_of, const uint16_t* tgt, ng_i64 N, ng_i64 lo, ng_i64 hi, ng_u64* qk, uint32_t* qv,
+                    void* stream);
+/* per partition an LDS hash count of its events; block b's distinct (pair key, count) at out + seg_base[b], seg_cnt[b]
+ * of them; qcnt[qv[j]] = the count of lookup j (qk sorted like ev, bounds qstart); flags[0] bit 0: a partition held
+ * more than 8192 distinct pairs (repartition with one more bit) */
+int ng_part_count(const ng_u64* ev, const ng_i64* start, int pbits, const ng_u64* qk, const uint32_t* qv,
+                  const ng_i64* qstart, ng_u64* out_k, uint32_t* out_c, uint32_t* seg_cnt, ng_i64* seg_base,
+                  uint32_t* qcnt, uint32_t* flags, int grid, void* stream);
 /* corpus-wide level build (count_table.rs build_level): contexts into ck (slot = id), (slot << 16 | next) counted in
  * the split table pk/pcnt; flags[0] bit 0 pair table full, bit 1 context table full */
 int ng_table_build(const uint16_t* tok, ng_i64 L, int k, ng_u64* ck, ng_u64 ccap, ng_u64* pk, uint32_t* pcnt,

@@ -35,19 +35,95 @@ __device__ __forceinline__ void split_add(u64* keys, u32* cnts, u64 cap, u64 key
     atomicOr(&flags[0], 1u);
 }
 
-// Dense levels: a lane per position (a wave per two bitmap words), hits counted in the split table. Once the table
-// has overflowed only the bitmap is still made (the level reruns bigger).
-template <int K>
-__global__ void __launch_bounds__(256) scan_count_dense_k(const u16* __restrict__ tok, i64 L, int k,
-                                                          const u32* __restrict__ bm_in, u32* __restrict__ bm_out,
-                                                          const u64* __restrict__ vt, u64 vcap, const u32* __restrict__ vrep,
-                                                          const u16* __restrict__ x, u64* keys, u32* cnts, u64 cap,
-                                                          u32* flags) {
+// What a level scan does with each hit besides setting its bitmap bit (probe_key's pair key: context id << 16 | next):
+//   CountSink: count it in the split table (once the table has overflowed, only the bitmap is still made: the level
+//              reruns bigger);
+//   ExistSink: flag its context (hit[id] = 1, plain byte stores: every writer stores the same value);
+//   EmitSink:  append mix64(pair key) to the block's own region ev[b * region, (b + 1) * region), at a block-local
+//              cursor in LDS (one LDS atomic per wave and round), and store the block's count in ev_count[b] at the
+//              end. No global atomic: a single global cursor would serialize (same-address atomics run at about
+//              80 M/s on MI355X). region >= ceil(L / (grid * 8192)) * 8192 bounds any block's hits in every mode.
+struct CountSink {
+    static constexpr int KIND = 0;
+    u64* keys;
+    u32* cnts;
+    u64 cap;
+};
+struct ExistSink {
+    static constexpr int KIND = 1;
+    unsigned char* hit;
+};
+struct EmitSink {
+    static constexpr int KIND = 2;
+    u64* ev;
+    u64 region;
+    u32* ev_count;
+};
+
+// A lane's hit (count and exist sinks; the emit sink uses emit_wave / emit_lane).
+template <class S>
+__device__ __forceinline__ void sink_hit(const S& s, u64 key, bool full, u32* flags) {
+    if constexpr (S::KIND == 0) {
+        if (!full) split_add(s.keys, s.cnts, s.cap, key, 1u, flags);
+    } else if constexpr (S::KIND == 1) {
+        s.hit[key >> 16] = 1;
+    }
+}
+
+// The wave's hits (b = ballot of `hit`) appended in lane order: called by every lane of the wave.
+__device__ __forceinline__ void emit_wave(const EmitSink& s, u32* cur, u64 b, bool hit, u64 key, u32* flags) {
+    if (!b) return;
+    u32 off = 0;
+    if (lane_id() == 0) off = atomicAdd(cur, (u32)__popcll(b));
+    off = (u32)__shfl((int)off, 0, WAVE);
+    if (hit) {
+        const u64 at = (u64)off + (u64)__popcll(b & lanemask_lt());
+        if (at < s.region) s.ev[(u64)blockIdx.x * s.region + at] = mix64(key);
+        else atomicOr(&flags[0], 4u);
+    }
+}
+
+__device__ __forceinline__ void emit_lane(const EmitSink& s, u32* cur, u64 key, u32* flags) {
+    const u64 at = atomicAdd(cur, 1u);
+    if (at < s.region) s.ev[(u64)blockIdx.x * s.region + at] = mix64(key);
+    else atomicOr(&flags[0], 4u);
+}
+
+template <class S>
+__device__ __forceinline__ void sink_begin(u32* cur) {
+    if constexpr (S::KIND == 2) {
+        if (threadIdx.x == 0) *cur = 0;
+        __syncthreads();
+    }
+}
+
+template <class S>
+__device__ __forceinline__ void sink_end(const S& s, u32* cur) {
+    if constexpr (S::KIND == 2) {
+        __syncthreads();
+        if (threadIdx.x == 0) s.ev_count[blockIdx.x] = *cur < s.region ? *cur : (u32)s.region;
+    }
+}
+
+template <class S>
+__device__ __forceinline__ bool sink_full(u32* flags) {
+    if constexpr (S::KIND == 0) return *(volatile u32*)&flags[0] != 0u;
+    else return false;
+}
+
+// Dense levels: a lane per position (a wave per two bitmap words).
+template <int K, class S>
+__global__ void __launch_bounds__(256) scan_dense_k(const u16* __restrict__ tok, i64 L, int k, const u32* __restrict__ bm_in,
+                                                    u32* __restrict__ bm_out, const u64* __restrict__ vt, u64 vcap,
+                                                    const u32* __restrict__ vrep, const u16* __restrict__ x, S sink,
+                                                    u32* flags) {
+    __shared__ u32 cur;
+    sink_begin<S>(&cur);
     const int lane = lane_id();
     const i64 nwords = (L + 31) >> 5;
     const i64 stride = (i64)gridDim.x * blockDim.x;
     for (i64 base = blockIdx.x * (i64)blockDim.x + (threadIdx.x & ~(WAVE - 1)); base < L; base += stride) {
-        const bool full = *(volatile u32*)&flags[0] != 0u;
+        const bool full = sink_full<S>(flags);
         const i64 p = base + lane;
         const i64 w = (base >> 5) + (lane >> 5);
         u32 word = 0xFFFFFFFFu;
@@ -58,20 +134,23 @@ __global__ void __launch_bounds__(256) scan_count_dense_k(const u16* __restrict_
         const u64 b = __ballot(hit);
         if (lane == 0) bm_out[base >> 5] = (u32)b;
         if (lane == 32 && w < nwords) bm_out[w] = (u32)(b >> 32);
-        if (hit && !full) split_add(keys, cnts, cap, key, 1u, flags);
+        if constexpr (S::KIND == 2) emit_wave(sink, &cur, b, hit, key, flags);
+        else if (hit) sink_hit(sink, key, full, flags);
     }
+    sink_end(sink, &cur);
 }
 
 // Sparse levels: a lane per bitmap word, its set bits in turn.
-template <int K>
-__global__ void __launch_bounds__(256) scan_count_sparse_k(const u16* __restrict__ tok, i64 L, int k,
-                                                           const u32* __restrict__ bm_in, u32* __restrict__ bm_out,
-                                                           const u64* __restrict__ vt, u64 vcap, const u32* __restrict__ vrep,
-                                                           const u16* __restrict__ x, u64* keys, u32* cnts, u64 cap,
-                                                           u32* flags) {
+template <int K, class S>
+__global__ void __launch_bounds__(256) scan_sparse_k(const u16* __restrict__ tok, i64 L, int k, const u32* __restrict__ bm_in,
+                                                     u32* __restrict__ bm_out, const u64* __restrict__ vt, u64 vcap,
+                                                     const u32* __restrict__ vrep, const u16* __restrict__ x, S sink,
+                                                     u32* flags) {
+    __shared__ u32 cur;
+    sink_begin<S>(&cur);
     const i64 nwords = (L + 31) >> 5;
     for (i64 w = blockIdx.x * (i64)blockDim.x + threadIdx.x; w < nwords; w += (i64)gridDim.x * blockDim.x) {
-        const bool full = *(volatile u32*)&flags[0] != 0u;
+        const bool full = sink_full<S>(flags);
         u32 word = bm_in[w], out = 0;
         while (word) {
             const int b = __ffs(word) - 1;
@@ -81,26 +160,28 @@ __global__ void __launch_bounds__(256) scan_count_sparse_k(const u16* __restrict
             const u64 key = probe_key<K>(tok, p, k, vt, vcap, vrep, x, flags);
             if (key != EMPTY) {
                 out |= 1u << b;
-                if (!full) split_add(keys, cnts, cap, key, 1u, flags);
+                if constexpr (S::KIND == 2) emit_lane(sink, &cur, key, flags);
+                else sink_hit(sink, key, full, flags);
             }
         }
         bm_out[w] = out;
     }
+    sink_end(sink, &cur);
 }
 
 // Gated levels, any density: a block takes 256 bitmap words (8192 positions) at a time; each wave lists its 64 words'
 // set positions in LDS (a wave prefix sum of their popcounts), and its lanes then probe the listed positions 64 at a
 // time, so every lane has work whatever the density and no position outside the bitmap is visited. Hits set their
-// bit in an LDS copy of the words (written out whole) and are counted in the split table, or (COUNT false) only
-// flagged per context in hit[] (the longest match's existence phase).
-template <int K, bool COUNT>
+// bit in an LDS copy of the words (written out whole).
+template <int K, class S>
 __global__ void __launch_bounds__(256) scan_compact_k(const u16* __restrict__ tok, i64 L, int k,
                                                       const u32* __restrict__ bm_in, u32* __restrict__ bm_out,
                                                       const u64* __restrict__ vt, u64 vcap, const u32* __restrict__ vrep,
-                                                      const u16* __restrict__ x, u64* keys, u32* cnts, u64 cap,
-                                                      unsigned char* __restrict__ hit, u32* flags) {
+                                                      const u16* __restrict__ x, S sink, u32* flags) {
     __shared__ u32 list[4][64 * 32];
     __shared__ u32 words[4][64];
+    __shared__ u32 cur;
+    sink_begin<S>(&cur);
     const int lane = lane_id(), w = threadIdx.x / WAVE;
     const i64 nwords = (L + 31) >> 5;
     for (i64 g0 = (i64)blockIdx.x * 256; g0 < nwords; g0 += (i64)gridDim.x * 256) {
@@ -123,90 +204,75 @@ __global__ void __launch_bounds__(256) scan_compact_k(const u16* __restrict__ to
         }
         words[w][lane] = 0;
         __syncthreads();
-        const bool full = COUNT && *(volatile u32*)&flags[0] != 0u;
-        for (u32 r = lane; r < total; r += WAVE) {
-            const u32 lp = list[w][r];
-            const i64 p = ((g0 + w * 64) << 5) + lp;
-            if (p >= L) continue;
-            const u64 key = probe_key<K>(tok, p, k, vt, vcap, vrep, x, flags);
-            if (key == EMPTY) continue;
-            atomicOr(&words[w][lp >> 5], 1u << (lp & 31));
-            if (COUNT) {
-                if (!full) split_add(keys, cnts, cap, key, 1u, flags);
-            } else {
-                hit[key >> 16] = 1;
+        const bool full = sink_full<S>(flags);
+        for (u32 r0 = 0; r0 < total; r0 += WAVE) {  // every lane runs the same rounds (wave-wide emission)
+            const u32 r = r0 + lane;
+            u64 key = EMPTY;
+            u32 lp = 0;
+            if (r < total) {
+                lp = list[w][r];
+                const i64 p = ((g0 + w * 64) << 5) + lp;
+                if (p < L) key = probe_key<K>(tok, p, k, vt, vcap, vrep, x, flags);
             }
+            const bool hit = key != EMPTY;
+            if (hit) atomicOr(&words[w][lp >> 5], 1u << (lp & 31));
+            if constexpr (S::KIND == 2) emit_wave(sink, &cur, __ballot(hit), hit, key, flags);
+            else if (hit) sink_hit(sink, key, full, flags);
         }
         __syncthreads();
         if (wi < nwords) bm_out[wi] = words[w][lane];
         __syncthreads();
     }
+    sink_end(sink, &cur);
 }
 
-// Existence only (the first phase of the longest match): the hit bitmap, and hit[context id] = 1 for every query
-// context that occurred (plain byte stores: every writer stores the same value).
-template <int K>
-__global__ void __launch_bounds__(256) scan_exist_dense_k(const u16* __restrict__ tok, i64 L, int k,
-                                                          const u32* __restrict__ bm_in, u32* __restrict__ bm_out,
-                                                          const u64* __restrict__ vt, u64 vcap, const u32* __restrict__ vrep,
-                                                          const u16* __restrict__ x, unsigned char* __restrict__ hit,
-                                                          u32* flags) {
-    const int lane = lane_id();
-    const i64 nwords = (L + 31) >> 5;
-    const i64 stride = (i64)gridDim.x * blockDim.x;
-    for (i64 base = blockIdx.x * (i64)blockDim.x + (threadIdx.x & ~(WAVE - 1)); base < L; base += stride) {
-        const i64 p = base + lane;
-        const i64 w = (base >> 5) + (lane >> 5);
-        u32 word = 0xFFFFFFFFu;
-        if (bm_in) word = w < nwords ? bm_in[w] : 0u;
-        u64 key = EMPTY;
-        if (p < L && ((word >> (lane & 31)) & 1u)) key = probe_key<K>(tok, p, k, vt, vcap, vrep, x, flags);
-        const u64 b = __ballot(key != EMPTY);
-        if (lane == 0) bm_out[base >> 5] = (u32)b;
-        if (lane == 32 && w < nwords) bm_out[w] = (u32)(b >> 32);
-        if (key != EMPTY) hit[key >> 16] = 1;
+// One level scan with a sink: sparse 0 a lane per position, 1 a lane per bitmap word, 2 LDS-listed (bm_in required
+// for 1 and 2).
+template <class S>
+static int launch_scan(const u16* tok, i64 L, int k, const u32* bm_in, u32* bm_out, const u64* vt, u64 vcap,
+                        const u32* vrep, const u16* x, const S& sink, u32* flags, int grid, int sparse, hipStream_t st) {
+    if (sparse == 2 && bm_in) {
+        LEVEL_SWITCH(k, (scan_compact_k<K, S><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, sink, flags)));
+    } else if (sparse && bm_in) {
+        LEVEL_SWITCH(k, (scan_sparse_k<K, S><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, sink, flags)));
+    } else {
+        LEVEL_SWITCH(k, (scan_dense_k<K, S><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, sink, flags)));
     }
+    return 0;
 }
 
-template <int K>
-__global__ void __launch_bounds__(256) scan_exist_sparse_k(const u16* __restrict__ tok, i64 L, int k,
-                                                           const u32* __restrict__ bm_in, u32* __restrict__ bm_out,
-                                                           const u64* __restrict__ vt, u64 vcap, const u32* __restrict__ vrep,
-                                                           const u16* __restrict__ x, unsigned char* __restrict__ hit,
-                                                           u32* flags) {
-    const i64 nwords = (L + 31) >> 5;
-    for (i64 w = blockIdx.x * (i64)blockDim.x + threadIdx.x; w < nwords; w += (i64)gridDim.x * blockDim.x) {
-        u32 word = bm_in[w], out = 0;
-        while (word) {
-            const int b = __ffs(word) - 1;
-            word &= word - 1;
-            const i64 p = (w << 5) + b;
-            if (p >= L) continue;
-            const u64 key = probe_key<K>(tok, p, k, vt, vcap, vrep, x, flags);
-            if (key != EMPTY) {
-                out |= 1u << b;
-                hit[key >> 16] = 1;
-            }
-        }
-        bm_out[w] = out;
-    }
-}
-
-// Occupied slots appended to (out_k, out_c): a block-wide count, one global atomic per block and tile.
+// Occupied slots appended to (out_k, out_c). Each block owns a contiguous range of slots: it counts the range's
+// occupied slots, takes its place with one global atomic (a single counter hit per tile would serialize), then
+// writes the range tile by tile at a running base.
 #define CP_ITEMS 8
 __global__ void __launch_bounds__(256) table_compact_k(const u64* __restrict__ keys, const u32* __restrict__ cnts, u64 cap,
-                                                       u64* __restrict__ out_k, u32* __restrict__ out_c, u64* counter) {
+                                                       u64 range, u64* __restrict__ out_k, u32* __restrict__ out_c,
+                                                       u64* counter) {
     __shared__ u32 wave_n[4];
     __shared__ u64 block_base;
     const int lane = lane_id(), w = threadIdx.x / WAVE;
     const u64 tile = 256ull * CP_ITEMS;
-    for (u64 t0 = blockIdx.x * tile; t0 < cap; t0 += (u64)gridDim.x * tile) {
+    const u64 lo = blockIdx.x * range, hi = lo + range < cap ? lo + range : cap;
+    u32 mine = 0;
+    for (u64 s = lo + threadIdx.x; s < hi; s += 256) mine += keys[s] != EMPTY;
+    u32 red = mine;
+#pragma unroll
+    for (int d = WAVE / 2; d > 0; d >>= 1) red += (u32)__shfl_down((int)red, d, WAVE);
+    if (lane == 0) wave_n[w] = red;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const u32 total = wave_n[0] + wave_n[1] + wave_n[2] + wave_n[3];
+        block_base = total ? atomicAdd((unsigned long long*)counter, (unsigned long long)total) : 0;
+    }
+    __syncthreads();
+    u64 run = block_base;
+    for (u64 t0 = lo; t0 < hi; t0 += tile) {
         u64 key[CP_ITEMS];
-        u32 mine = 0;
+        mine = 0;
 #pragma unroll
         for (int j = 0; j < CP_ITEMS; ++j) {
             const u64 s = t0 + (u64)j * 256 + threadIdx.x;
-            key[j] = s < cap ? keys[s] : EMPTY;
+            key[j] = s < hi ? keys[s] : EMPTY;
             mine += key[j] != EMPTY;
         }
         // exclusive scan of `mine` over the block
@@ -216,6 +282,7 @@ __global__ void __launch_bounds__(256) table_compact_k(const u64* __restrict__ k
             const u32 o = (u32)__shfl_up((int)incl, d, WAVE);
             if (lane >= d) incl += o;
         }
+        __syncthreads();  // the previous tile's wave totals are read
         if (lane == WAVE - 1) wave_n[w] = incl;
         __syncthreads();
         u32 before = 0, total = 0;
@@ -224,9 +291,7 @@ __global__ void __launch_bounds__(256) table_compact_k(const u64* __restrict__ k
             if (i < w) before += wave_n[i];
             total += wave_n[i];
         }
-        if (threadIdx.x == 0) block_base = total ? atomicAdd((unsigned long long*)counter, (unsigned long long)total) : 0;
-        __syncthreads();
-        u64 at = block_base + before + incl - mine;
+        u64 at = run + before + incl - mine;
 #pragma unroll
         for (int j = 0; j < CP_ITEMS; ++j) {
             if (key[j] != EMPTY) {
@@ -236,7 +301,7 @@ __global__ void __launch_bounds__(256) table_compact_k(const u64* __restrict__ k
                 ++at;
             }
         }
-        __syncthreads();
+        run += total;
     }
 }
 
@@ -338,16 +403,18 @@ __global__ void __launch_bounds__(256) ctx_topk_k(const u64* __restrict__ uk, co
     }
 }
 
-// Per query position i whose context id c is in [lo, hi): tot, dist, cnt (the target's count, binary search of
-// (c - lo) << 16 | tgt in the context's pairs), the first kout of its context's top entries (top_tok/top_cnt
-// [hi - lo, ktop]) and bit li of mask; other positions untouched.
+// Per query position i whose context id c is in [lo, hi): tot, dist, cnt (the target's count: qcnt[i] when given,
+// else looked up in the split table pkeys/pcnts, else by binary search of (c - lo) << 16 | tgt in the context's
+// pairs), the first kout of its context's top entries (top_tok/top_cnt [hi - lo, ktop]) and bit li of mask; other
+// positions untouched.
 __global__ void __launch_bounds__(256) pos_gather_k(const int* __restrict__ ctx_of, i64 N, i64 lo, i64 hi,
                                                     const u16* __restrict__ tgt, const u64* __restrict__ uk,
                                                     const u32* __restrict__ agg, const i64* __restrict__ start,
                                                     const i64* __restrict__ end, const u64* __restrict__ tot,
                                                     const u16* __restrict__ top_tok, const u32* __restrict__ top_cnt,
                                                     const u64* __restrict__ thr, const u64* __restrict__ pkeys,
-                                                    const u32* __restrict__ pcnts, u64 pcap, int ktop, int kout, int li,
+                                                    const u32* __restrict__ pcnts, u64 pcap,
+                                                    const u32* __restrict__ qcnt, int ktop, int kout, int li,
                                                     int* __restrict__ out_tot,
                                                     int* __restrict__ out_dist,
                                                     int* __restrict__ out_cnt, u16* __restrict__ out_tok,
@@ -364,7 +431,9 @@ __global__ void __launch_bounds__(256) pos_gather_k(const int* __restrict__ ctx_
     out_dist[i] = (int)(b - a < 65535 ? b - a : 65535);
     const u64 want = ((u64)c << 16) | tgt[i];
     u32 n = 0;
-    if (pkeys) {  // the split table's count of (context, target)
+    if (qcnt) {  // counted beforehand (ng_part_count's lookups)
+        n = qcnt[i];
+    } else if (pkeys) {  // the split table's count of (context, target)
         u64 s = split_home(want + ((u64)lo << 16), pcap);
         for (u64 probe = 0; probe < pcap; ++probe) {
             const u64 cur = pkeys[s];
@@ -410,14 +479,8 @@ extern "C" int ng_scan_count(const u16* tok, i64 L, int k, const u32* bm_in, u32
     if (L <= 0) return 0;
     if (cap == 0) return -1;
     if (grid <= 0) grid = grid_for(L, 256);
-    hipStream_t st = (hipStream_t)stream;
-    if (sparse == 2 && bm_in) {
-        LEVEL_SWITCH(k, (scan_compact_k<K, true><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, keys, cnts, cap, nullptr, flags)));
-    } else if (sparse && bm_in) {
-        LEVEL_SWITCH(k, (scan_count_sparse_k<K><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, keys, cnts, cap, flags)));
-    } else {
-        LEVEL_SWITCH(k, (scan_count_dense_k<K><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, keys, cnts, cap, flags)));
-    }
+    if (launch_scan(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, CountSink{keys, cnts, cap}, flags, grid, sparse,
+                (hipStream_t)stream) != 0) return -1;
     return (int)hipGetLastError();
 }
 
@@ -428,14 +491,26 @@ extern "C" int ng_scan_exist(const u16* tok, i64 L, int k, const u32* bm_in, u32
                              void* stream) {
     if (L <= 0) return 0;
     if (grid <= 0) grid = grid_for(L, 256);
-    hipStream_t st = (hipStream_t)stream;
-    if (sparse == 2 && bm_in) {
-        LEVEL_SWITCH(k, (scan_compact_k<K, false><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, nullptr, nullptr, 0, hit, flags)));
-    } else if (sparse && bm_in) {
-        LEVEL_SWITCH(k, (scan_exist_sparse_k<K><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, hit, flags)));
-    } else {
-        LEVEL_SWITCH(k, (scan_exist_dense_k<K><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, hit, flags)));
-    }
+    if (launch_scan(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, ExistSink{hit}, flags, grid, sparse, (hipStream_t)stream) != 0) return -1;
+    return (int)hipGetLastError();
+}
+
+// The emitting scan: block b of the `grid` blocks appends its hits' mix64(pair key) to ev[b * region ...] and stores
+// their number in ev_count[b]; region must be at least ng_emit_region(L, grid). flags[0] bit 2: a region overflowed
+// (only with a smaller region). sparse as ng_scan_count's.
+extern "C" u64 ng_emit_region(i64 L, int grid) {
+    if (L <= 0 || grid <= 0) return 0;
+    const u64 per = (u64)grid * 8192ull;
+    return ((u64)L + per - 1) / per * 8192ull;
+}
+
+extern "C" int ng_scan_emit(const u16* tok, i64 L, int k, const u32* bm_in, u32* bm_out, const u64* vt, u64 vcap,
+                            const u32* vrep, const u16* x, u64* ev, u64 region, u32* ev_count, u32* flags, int grid,
+                            int sparse, void* stream) {
+    if (L <= 0) return 0;
+    if (grid <= 0 || region == 0 || region > 0xFFFFFFFFull) return -1;
+    if (launch_scan(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, EmitSink{ev, region, ev_count}, flags, grid, sparse,
+                (hipStream_t)stream) != 0) return -1;
     return (int)hipGetLastError();
 }
 
@@ -443,9 +518,12 @@ extern "C" int ng_scan_exist(const u16* tok, i64 L, int k, const u32* bm_in, u32
 extern "C" int ng_table_compact(const u64* keys, const u32* cnts, u64 cap, u64* out_k, u32* out_c, u64* counter,
                                 void* stream) {
     if (cap == 0) return 0;
-    u64 tiles = (cap + 256 * CP_ITEMS - 1) / (256 * CP_ITEMS);
-    const int g = tiles > 16384 ? 16384 : (int)tiles;
-    table_compact_k<<<g, 256, 0, (hipStream_t)stream>>>(keys, cnts, cap, out_k, out_c, counter);
+    const u64 tile = 256 * CP_ITEMS;
+    const u64 tiles = (cap + tile - 1) / tile;
+    const u64 g = tiles > 2048 ? 2048 : tiles;
+    const u64 range = (tiles + g - 1) / g * tile;
+    table_compact_k<<<(unsigned)((cap + range - 1) / range), 256, 0, (hipStream_t)stream>>>(keys, cnts, cap, range,
+                                                                                          out_k, out_c, counter);
     return (int)hipGetLastError();
 }
 
@@ -472,16 +550,16 @@ extern "C" int ng_ctx_topk(const u64* uk, const u32* agg, const i64* start, cons
 // given, else by binary search of the context's pairs (uk sorted by key).
 extern "C" int ng_pos_gather(const int* ctx_of, i64 N, i64 lo, i64 hi, const u16* tgt, const u64* uk, const u32* agg,
                              const i64* start, const i64* end, const u64* tot, const u16* top_tok, const u32* top_cnt,
-                             const u64* thr, const u64* pkeys, const u32* pcnts, u64 pcap, int ktop, int kout, int li,
-                             int* out_tot, int* out_dist, int* out_cnt, u16* out_tok, u32* out_tcnt, int* mask,
-                             void* stream) {
+                             const u64* thr, const u64* pkeys, const u32* pcnts, u64 pcap, const u32* qcnt, int ktop,
+                             int kout, int li, int* out_tot, int* out_dist, int* out_cnt, u16* out_tok, u32* out_tcnt,
+                             int* mask, void* stream) {
     if (pkeys && pcap == 0) return -1;
     if (kout < 0 || kout > ktop || (mask && (li < 0 || li > 30))) return -1;
     if (N > 0)
         pos_gather_k<<<grid_for(N, 256), 256, 0, (hipStream_t)stream>>>(ctx_of, N, lo, hi, tgt, uk, agg, start, end, tot,
-                                                                        top_tok, top_cnt, thr, pkeys, pcnts, pcap, ktop,
-                                                                        kout, li, out_tot,
-                                                                        out_dist, out_cnt, out_tok, out_tcnt, mask);
+                                                                        top_tok, top_cnt, thr, pkeys, pcnts, pcap, qcnt,
+                                                                        ktop, kout, li, out_tot, out_dist, out_cnt,
+                                                                        out_tok, out_tcnt, mask);
     return (int)hipGetLastError();
 }
 
@@ -526,8 +604,10 @@ extern "C" int ng_features(const int* counts, int L, i64 n, int nb, float* tot, 
 // The engine's query index: the distinct valid query contexts inserted into an open-addressing table by
 // compare-and-swap (no sort). Slot = context id; linear probing without wrap-around from umulhi(key, cap) over a
 // table of cap + tail slots whose last slot stays empty, which is the layout probe_key walks. rep[slot] = the
-// smallest query position with that context (atomicMin: the same on every run). The canonical, sorted layout of
-// gpu_val_stats' ValIndex is only needed for ids that agree across ranks; on one GPU any layout is exact.
+// query position whose compare-and-swap inserted the context. The canonical, sorted layout of gpu_val_stats'
+// ValIndex is only needed for ids that agree across ranks; on one GPU any layout is exact. No kernel here adds to a
+// single global counter per thread or per wave: same-address atomics serialize (about 80 M/s on MI355X), so counts
+// are reduced per block first.
 // ---------------------------------------------------------------------------------------------------------------
 
 namespace {
@@ -536,7 +616,6 @@ __global__ void qindex_insert_k(const u16* __restrict__ x, const int* __restrict
                                 i64 n, int k, u64* table, u64 cap, u64 slots, u32* rep, int* __restrict__ ctx_of,
                                 u64* counters) {
     const i64 j = blockIdx.x * (i64)blockDim.x + threadIdx.x;
-    bool inserted = false;
     if (j < n) {
         const i64 i = pos ? pos[j] : j;
         i64 slot = -1;
@@ -557,7 +636,6 @@ __global__ void qindex_insert_k(const u16* __restrict__ x, const int* __restrict
                     const u64 prev = atomicCAS((unsigned long long*)&table[s], EMPTY, key);
                     if (prev == EMPTY) {  // this position inserted the context: it is the representative
                         rep[s] = (u32)i;
-                        inserted = true;
                         slot = (i64)s;
                         break;
                     }
@@ -571,10 +649,22 @@ __global__ void qindex_insert_k(const u16* __restrict__ x, const int* __restrict
         }
         if (slot >= 0 || !pos) ctx_of[i] = (int)slot;
     }
-    // one counter atomic per wave (a single address hit by every new context would serialize)
-    const u64 b = __ballot(inserted);
-    if (b && lane_id() == __ffsll((unsigned long long)__ballot(1)) - 1)
-        atomicAdd((unsigned long long*)&counters[0], (unsigned long long)__popcll(b));
+}
+
+// Occupied slots of a table added to *out: a block-wide sum, then one atomic per block.
+__global__ void __launch_bounds__(256) count_occupied_k(const u64* __restrict__ table, u64 slots, u64* out) {
+    __shared__ u32 part[4];
+    u32 c = 0;
+    for (u64 s = blockIdx.x * (u64)blockDim.x + threadIdx.x; s < slots; s += (u64)gridDim.x * blockDim.x)
+        c += table[s] != EMPTY;
+#pragma unroll
+    for (int d = WAVE / 2; d > 0; d >>= 1) c += (u32)__shfl_down((int)c, d, WAVE);
+    if (lane_id() == 0) part[threadIdx.x / WAVE] = c;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const u32 t = part[0] + part[1] + part[2] + part[3];
+        if (t) atomicAdd((unsigned long long*)out, (unsigned long long)t);
+    }
 }
 
 // Re-insert a sparse table's keys (and representatives) into a table sized for them: new slot of each old slot.
@@ -642,8 +732,9 @@ extern "C" int ng_query_index_shrink(const u64* old_t, const u32* old_rep, u64 o
 // Insert the valid query contexts of positions pos[0..n) (pos NULL: 0..n) into table (cap + tail slots, EMPTY-filled):
 // ctx_of[i] = slot (-1 where invalid; with pos, only listed positions are written), rep[slot] = the position that
 // inserted it.
-// counters[0] += new contexts, counters[1] = 1 if the probes ran into the table's end; with k > 4, counters[2] +=
-// positions whose tokens differ from their slot's representative (a 64-bit key collision).
+// counters[0] += the table's occupied slots afterwards (its contexts), counters[1] = 1 if the probes ran into the
+// table's end; with k > 4, counters[2] += positions whose tokens differ from their slot's representative (a 64-bit
+// key collision).
 extern "C" int ng_query_index(const u16* x, const int* avail, const int* pos, i64 n, int k, u64* table, u64 cap,
                               u64 slots, u32* rep, int* ctx_of, u64* counters, void* stream) {
     if (n <= 0) return 0;
@@ -651,5 +742,7 @@ extern "C" int ng_query_index(const u16* x, const int* avail, const int* pos, i6
     hipStream_t st = (hipStream_t)stream;
     LEVEL_SWITCH(k, (qindex_insert_k<K><<<grid_for(n, 256), 256, 0, st>>>(x, avail, pos, n, k, table, cap, slots, rep, ctx_of, counters)));
     if (k > 4) qindex_verify_k<<<grid_for(n, 256), 256, 0, st>>>(x, pos, n, k, ctx_of, rep, counters + 2);
+    const int g = grid_for((i64)slots, 256);
+    count_occupied_k<<<g < 1024 ? g : 1024, 256, 0, st>>>(table, slots, counters);
     return (int)hipGetLastError();
 }

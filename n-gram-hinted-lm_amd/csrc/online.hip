@@ -220,13 +220,19 @@ __device__ __forceinline__ bool online_row(i64 g, i64 i, int nlv, const i64* __r
 __global__ void online_rows_k(const int* __restrict__ pos, i64 m, int nlv, const i64* __restrict__ desc, int E,
                               short* __restrict__ cell, u16* __restrict__ next, u16* __restrict__ weights,
                               int* __restrict__ hinted) {
-    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
-    bool done = false;
-    if (i < m) done = online_row(pos[i], i, nlv, desc, E, cell, next, weights);
-    // one counter atomic per wave
-    const u64 b = __ballot(done);
-    if (b && (int)(threadIdx.x & (WAVE - 1)) == __ffsll((unsigned long long)__ballot(1)) - 1)
-        atomicAdd(hinted, __popcll(b));
+    __shared__ int part[4];
+    int c = 0;
+    for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < m; i += (i64)gridDim.x * blockDim.x)
+        c += online_row(pos[i], i, nlv, desc, E, cell, next, weights);
+    // one counter atomic per block: same-address atomics serialize
+#pragma unroll
+    for (int d = WAVE / 2; d > 0; d >>= 1) c += __shfl_down(c, d, WAVE);
+    if ((threadIdx.x & (WAVE - 1)) == 0) part[threadIdx.x / WAVE] = c;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int t = part[0] + part[1] + part[2] + part[3];
+        if (t) atomicAdd(hinted, t);
+    }
 }
 
 }  // namespace
@@ -283,7 +289,7 @@ extern "C" int ng_online_rows(const int* pos, i64 m, int nlv, const i64* desc, i
                               u16* weights, int* hinted, void* stream) {
     if (E < 1 || E > 8) return -1;
     if (m > 0)
-        online_rows_k<<<grid_for(m, 256), 256, 0, (hipStream_t)stream>>>(pos, m, nlv, desc, E, cell, next, weights,
-                                                                         hinted);
+        online_rows_k<<<grid_for(m, 256) < 1024 ? grid_for(m, 256) : 1024, 256, 0, (hipStream_t)stream>>>(
+            pos, m, nlv, desc, E, cell, next, weights, hinted);
     return (int)hipGetLastError();
 }

@@ -239,7 +239,7 @@ class CountTable:
             e0, e1 = self._timed("pos_gather", lv.k)
             e0.record()
             self.lib("ng_pos_gather", slot, n, 0, lv.ccap, tgt, lv.uk, lv.agg, lv.start, lv.end, lv.tot, lv.top_tok,
-                     lv.top_cnt, lv.thr if top == CNT_TOP else None, None, None, u64(0), i32(TOPE), i32(topk), i32(0),
+                     lv.top_cnt, lv.thr if top == CNT_TOP else None, None, None, u64(0), None, i32(TOPE), i32(topk), i32(0),
                      out[0, li],
                      out[1, li], out[2, li], res["top_tok"][li] if topk else None,
                      res["top_cnt"][li] if topk else None, None)

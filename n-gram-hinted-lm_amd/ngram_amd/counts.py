@@ -16,6 +16,7 @@ all-to-all and all-reduce of a multi-GPU build are not part of this build."""
 
 from __future__ import annotations
 
+import math
 import time
 
 import numpy as np
@@ -46,6 +47,16 @@ ROW_PURITIES = (0.3, 0.5, 0.7, 0.85, 0.95)
 SUB_BYTES = 64 << 20
 PART_MIN_BYTES = 128 << 20
 EMIT_CHUNK = 1 << 28  # emitted keys held before a flush (at least one shard's positions)
+# "part" mode: partitions sized for about PART_TARGET distinct pairs each (the LDS table holds 8192), counted by
+# PART_BLOCKS blocks of consecutive partitions.
+PART_TARGET = 4096
+PART_BLOCKS = 2048
+
+
+def emit_region(L: int, grid: int) -> int:
+    """The per-block region an emitting scan of L positions with `grid` blocks needs (ng_emit_region)."""
+    per = grid * 8192
+    return -(-L // per) * 8192
 
 
 def record_lib() -> Lib:
@@ -102,7 +113,9 @@ class CountBuild:
     self.top_cnt [len(levels), N, topk]) when > 0. Construct with `from_device` for tokens already in GPU memory.
 
     `mode` (attribute): "engine" (default) counts in split pair tables (keys and u32 counts apart) and ranks by
-    per-context selection after one sort (libngram_amd.so's ng_* entry points); "record" runs the record's own C ABI
+    per-context selection after one sort (libngram_amd.so's ng_* entry points); "part" counts without global
+    atomics: each level's hits emitted, hash-partitioned by a radix sort and counted partition by partition in LDS,
+    then the engine's owner side; "record" runs the record's own C ABI
     calls, as its host does (one packed table per level, two sorts); "partitioned" is "record" with the large tables'
     hits emitted, grouped by sub-table and counted sub-table by sub-table."""
 
@@ -114,6 +127,7 @@ class CountBuild:
         self.min_cap = 1 << 20
         self.mode = "engine"
         self.density: dict[int, float] = {}  # each level's hit density, from the last build with stats
+        self.dratio: dict[int, float] = {}  # "part" mode: each level's distinct pairs per event, from the last build
         self.levels = tuple(levels)
         if not self.levels or list(self.levels) != sorted(set(self.levels)) or self.levels[0] < 1:
             raise ValueError(f"levels must ascend from >= 1: {self.levels}")
@@ -151,6 +165,7 @@ class CountBuild:
         self.min_cap = 1 << 20
         self.mode = "engine"
         self.density: dict[int, float] = {}  # each level's hit density, from the last build with stats
+        self.dratio: dict[int, float] = {}  # "part" mode: each level's distinct pairs per event, from the last build
         self.levels = tuple(levels)
         ls = LEVEL_SHARDS if level_shards is None else level_shards
         self.topk = topk
@@ -304,12 +319,14 @@ class CountBuild:
         self.kernel_events = []
         self.x = x
         N = x.numel()
-        if self.mode == "engine":
+        if self.mode in ("engine", "part"):
             index = {k: QueryIndex(self.elib, x, avail, k) for k in self.levels}
         else:
             index = {k: ValIndex(lib, x, avail, k, max_ids=MAX_IDS) for k in self.levels}
         lap("index")
         self.grid = torch.cuda.get_device_properties(dev).multi_processor_count * 32
+        if self.mode == "part":
+            return self._counts_part(index, tgt, N, lap)
         caps = self.caps()
         tables = {}
         chunk = max([EMIT_CHUNK] + [(n + 31) // 32 * 32 for n in self.sizes])
@@ -350,23 +367,9 @@ class CountBuild:
                 U, tot, top_tok, top_cnt, want = self._outputs_engine(li, k, vi, t, tgt, out, want)
             else:
                 U, tot, top_tok, top_cnt = self._outputs_record(li, k, vi, t, tgt, out, want)
-            lo, hi = 0, vi.ids
-            if rows and k in ROW_LEVELS:
-                ri = ROW_LEVELS.index(k)
-                ctx = vi.ctx_of.long()
-                at = ((ctx >= lo) & (ctx < hi)).nonzero().squeeze(1)
-                c = ctx[at] - lo
-                tt = top_tok.view(-1, want)[c, :ROW_K].to(torch.int32) & 0xFFFF
-                tc = top_cnt.view(-1, want)[c, :ROW_K].to(torch.int64)
-                top = tc[:, :1].clamp_min(1)
-                # the weights as the model reads them (15 bits): scaled down where the top count is larger
-                w = torch.where(top > 32767, (tc * 32767 + top - 1) // top, tc)
-                row_entries[ri, at] = torch.where(tc > 0, tt | (w.to(torch.int32) << 16), 0)
-                row_top[ri, at] = tc[:, 0].clamp_max((1 << 31) - 1).to(torch.int32)
-                del ctx, at, c, tt, tc, top, w
+            self._level_rows(k, vi, want, tot, top_tok, top_cnt, row_entries if rows else None,
+                             row_top if rows else None)
             del top_tok, top_cnt
-            if vi.ids and int(tot.max().item()) >= 1 << 32:
-                raise RuntimeError(f"k={k}: a total does not fit uint32")
             info[k] = dict(contexts=vi.n, ids=vi.ids, pairs=U, cap=t["cap"], pbits=t["pbits"], hits=hits.get(k),
                            reruns=reruns[k])
             del t, tot, vi
@@ -376,6 +379,171 @@ class CountBuild:
             lap("rows")
         self.out = out
         return out
+
+    def _level_rows(self, k, vi, want, tot, top_tok, top_cnt, row_entries, row_top) -> None:
+        """A level's share of the rows (its top ROW_K entries per position, if k is a row level) and the uint32 check
+        of its totals."""
+        if row_entries is not None and k in ROW_LEVELS:
+            ri = ROW_LEVELS.index(k)
+            ctx = vi.ctx_of.long()
+            at = ((ctx >= 0) & (ctx < vi.ids)).nonzero().squeeze(1)
+            c = ctx[at]
+            tt = top_tok.view(-1, want)[c, :ROW_K].to(torch.int32) & 0xFFFF
+            tc = top_cnt.view(-1, want)[c, :ROW_K].to(torch.int64)
+            top = tc[:, :1].clamp_min(1)
+            # the weights as the model reads them (15 bits): scaled down where the top count is larger
+            w = torch.where(top > 32767, (tc * 32767 + top - 1) // top, tc)
+            row_entries[ri, at] = torch.where(tc > 0, tt | (w.to(torch.int32) << 16), 0)
+            row_top[ri, at] = tc[:, 0].clamp_max((1 << 31) - 1).to(torch.int32)
+        if vi.ids and int(tot.max().item()) >= 1 << 32:
+            raise RuntimeError(f"k={k}: a total does not fit uint32")
+
+    def _counts_part(self, index, tgt, N, lap) -> torch.Tensor:
+        """counts() in "part" mode: level after level, every shard's scan emits its hits (no global atomics), the
+        hits are hash-partitioned by a radix sort of their mixed keys and counted partition by partition in LDS
+        (the query positions' target counts answered there too); then the owner side of the engine mode."""
+        dev, info = self.tok.device, self.info
+        nwords = self.L // 32
+        bms = {k: torch.zeros(nwords, dtype=torch.int32, device=dev) for k in self.levels}
+        out = torch.zeros((3, len(self.levels), N), dtype=torch.int32, device=dev)
+        rows = all(k in self.levels for k in ROW_LEVELS)
+        row_entries = row_top = None
+        if rows:
+            row_entries = torch.zeros((len(ROW_LEVELS), N, ROW_K), dtype=torch.int32, device=dev)
+            row_top = torch.zeros((len(ROW_LEVELS), N), dtype=torch.int32, device=dev)
+        if self.topk:
+            self.top_tok = torch.zeros((len(self.levels), N, self.topk), dtype=torch.int16, device=dev)
+            self.top_cnt = torch.zeros((len(self.levels), N, self.topk), dtype=torch.int32, device=dev)
+        G = self.grid
+        R = max(emit_region((n + 31) // 32 * 32, G) for n in self.sizes)
+        regions = torch.empty(len(self.sizes) * G * R, dtype=torch.int64, device=dev)
+        scan_t = count_t = 0.0
+        for li, k in enumerate(self.levels):
+            vi = index.pop(k)
+            t0 = time.perf_counter()
+            ev, n_ev = self._part_emit(k, vi, bms, regions, R)
+            t1 = time.perf_counter()
+            ck, cc, qcnt, U, pbits = self._part_count(k, vi, ev, n_ev, tgt)
+            del ev
+            t2 = time.perf_counter()
+            scan_t += t1 - t0
+            count_t += t2 - t1
+            want = max(self.topk, ROW_K if (rows and k in ROW_LEVELS) else 0)
+            tot, top_tok, top_cnt, want = self._owner(li, k, vi, ck, cc, U, tgt, out, want, qcnt=qcnt)
+            self._level_rows(k, vi, want, tot, top_tok, top_cnt, row_entries, row_top)
+            info[k] = dict(contexts=vi.n, ids=vi.ids, pairs=U, events=n_ev, pbits=pbits, cap=0, hits=None, reruns=0)
+            del tot, top_tok, top_cnt, vi, qcnt
+        del regions
+        if self.stats:
+            for k in self.levels:
+                h = int(self._popcount(bms[k]).item())
+                info[k]["hits"] = h
+                self.density[k] = h / max(1, sum(self.sizes[: self.level_shards[k]]))
+        del bms
+        lap("outputs")
+        self.timing["part_scan_host"] = self.timing.get("part_scan_host", 0.0) + scan_t
+        self.timing["part_count_host"] = self.timing.get("part_count_host", 0.0) + count_t
+        if rows:
+            self._rows(out, row_entries, row_top, N)
+            lap("rows")
+        self.out = out
+        return out
+
+    def _part_emit(self, k, vi, bms, regions, R):
+        """Level k's scan of every shard it counts, hits emitted to per-block regions, then packed: (events, n)."""
+        elib, dev, G = self.elib, self.tok.device, self.grid
+        shards = [i for i in range(len(self.sizes)) if i < self.level_shards[k]]
+        nseg = len(shards) * G
+        ev_count = torch.zeros(max(nseg, 1), dtype=torch.int32, device=dev)
+        flags = torch.zeros(2, dtype=torch.int32, device=dev)
+        for j, i in enumerate(shards):
+            st, n = self.starts[i], self.sizes[i]
+            n32 = (n + 31) // 32 * 32
+            torch.cuda.current_stream().wait_event(self.events[i])
+            scanned = [q for q in self.levels if i < self.level_shards[q]]
+            si = scanned.index(k)
+            # gated by this shard's previous scanned level; a shard that level skipped is probed whole
+            bm_in = None if si == 0 else bms[scanned[si - 1]][st // 32 :]
+            e0, e1 = self._event("scan_emit", k, i, n32)
+            e0.record()
+            elib("ng_scan_emit", self.tok[st:], n32, i32(k), bm_in, bms[k][st // 32 :], vi.table, u64(vi.cap), vi.rep,
+                 self.x, regions[j * G * R :], u64(R), ev_count[j * G :], flags, i32(G),
+                 i32(self._scan_mode(si, scanned)))
+            e1.record()
+        offs = torch.empty(nseg + 1, dtype=torch.int64, device=dev)
+        e0, e1 = self._event("gather", k, -1, 0)
+        e0.record()
+        elib("ng_seg_offsets", ev_count, nseg, offs)
+        e1.record()
+        n_ev = int(offs[nseg].item())
+        if int(flags[0].item()) & 4:
+            raise RuntimeError(f"k={k}: an emit region overflowed")
+        ev = torch.empty(max(n_ev, 1), dtype=torch.int64, device=dev)
+        e0, e1 = self._event("gather", k, -1, n_ev)
+        e0.record()
+        elib("ng_seg_gather", regions, None, u64(R), None, ev_count, nseg, offs, ev, None)
+        e1.record()
+        return ev, n_ev
+
+    def _part_count(self, k, vi, ev, n_ev, tgt):
+        """Level k's events counted: hash-partitioned (a radix sort of the mixed keys by their top pbits), then an LDS
+        count per partition with the query positions' lookups; a partition with too many distinct pairs repeats the
+        level with one more bit. Returns (pair keys, counts, per-position target counts, pairs, pbits)."""
+        elib, lib, dev = self.elib, self.lib, self.tok.device
+        N = vi.ctx_of.numel()
+        ratio = self.dratio.get(k, 1.0)
+        pbits = max(0, min(24, math.ceil(math.log2(max(1.0, n_ev * ratio / PART_TARGET)))))
+        qk = torch.empty(N, dtype=torch.int64, device=dev)
+        qv = torch.empty(N, dtype=torch.int32, device=dev)
+        e0, e1 = self._event("partition", k, -1, N)
+        e0.record()
+        elib("ng_part_lookups", vi.ctx_of, tgt, N, 0, vi.ids, qk, qv)
+        e1.record()
+        while True:
+            P = 1 << pbits
+            sev = torch.empty(max(n_ev, 1), dtype=torch.int64, device=dev)
+            sqk = torch.empty(N, dtype=torch.int64, device=dev)
+            sqv = torch.empty(N, dtype=torch.int32, device=dev)
+            start = torch.empty(P + 1, dtype=torch.int64, device=dev)
+            qstart = torch.empty(P + 1, dtype=torch.int64, device=dev)
+            e0, e1 = self._event("partition", k, -1, n_ev)
+            e0.record()
+            if n_ev:
+                lib.cub("sort_pairs", ev, sev, None, None, n_ev, i32(64 - pbits), i32(64))
+            elib("ng_part_bounds", sev, n_ev, i32(pbits), start)
+            if N:
+                lib.cub("sort_pairs", qk, sqk, qv, sqv, N, i32(64 - pbits), i32(64))
+            elib("ng_part_bounds", sqk, N, i32(pbits), qstart)
+            e1.record()
+            G2 = min(P, PART_BLOCKS)
+            out_k = torch.empty(max(n_ev, 1), dtype=torch.int64, device=dev)
+            out_c = torch.empty(max(n_ev, 1), dtype=torch.int32, device=dev)
+            seg_cnt = torch.empty(G2, dtype=torch.int32, device=dev)
+            seg_base = torch.empty(G2, dtype=torch.int64, device=dev)
+            qcnt = torch.zeros(max(N, 1), dtype=torch.int32, device=dev)
+            flags = torch.zeros(1, dtype=torch.int32, device=dev)
+            e0, e1 = self._event("count", k, -1, n_ev)
+            e0.record()
+            elib("ng_part_count", sev, start, i32(pbits), sqk, sqv, qstart, out_k, out_c, seg_cnt, seg_base, qcnt, flags,
+                 i32(G2))
+            e1.record()
+            del sev, sqk, sqv, start, qstart
+            if not int(flags[0].item()) & 1:
+                break
+            if pbits >= 24:
+                raise RuntimeError(f"k={k}: a partition holds too many distinct pairs at 24 bits")
+            pbits += 1
+        offs = torch.empty(G2 + 1, dtype=torch.int64, device=dev)
+        elib("ng_seg_offsets", seg_cnt, G2, offs)
+        U = int(offs[G2].item())
+        ck = torch.empty(max(U, 1), dtype=torch.int64, device=dev)
+        cc = torch.empty(max(U, 1), dtype=torch.int32, device=dev)
+        e0, e1 = self._event("count", k, -1, U)
+        e0.record()
+        elib("ng_seg_gather", out_k, out_c, u64(0), seg_base, seg_cnt, G2, offs, ck, cc)
+        e1.record()
+        self.dratio[k] = U / max(1, n_ev)
+        return ck, cc, qcnt, U, pbits
 
     def _outputs_engine(self, li, k, vi, t, tgt, out, want):
         """One level's outputs with the engine: the split table compacted, its pairs sorted by context, per-context
@@ -393,12 +561,22 @@ class CountBuild:
         elib("ng_table_compact", t["keys"], t["cnts"], u64(cap), ck, cc, counter)
         e1.record()
         U = int(counter.item())
+        tot, top_tok, top_cnt, want = self._owner(li, k, vi, ck, cc, U, tgt, out, want, t=t)
+        t.pop("keys"), t.pop("cnts")
+        return U, tot, top_tok, top_cnt, want
+
+    def _owner(self, li, k, vi, ck, cc, U, tgt, out, want, t=None, qcnt=None):
+        """A level's owner side from its U distinct pairs (ck, cc; consumed): sorted by context, per-context totals
+        and top entries by selection, then one gather per query position (the target's count from qcnt, or looked
+        up in the split table t)."""
+        elib, lib, dev = self.elib, self.lib, self.tok.device
+        N, lo, hi = vi.ctx_of.numel(), 0, vi.ids
         n_own = hi - lo
         ctx_bits = max(1, (max(n_own, 2) - 1).bit_length())
         uk, agg = torch.empty(U, dtype=torch.int64, device=dev), torch.empty(U, dtype=torch.int32, device=dev)
         e0, e1 = self._event("sort", k, -1, U)
         e0.record()
-        if U:  # by context only: the target's count comes from the split table, the ranking needs no token order
+        if U:  # by context only: the target's count is looked up apart, the ranking needs no token order
             lib.cub("sort_pairs", ck, uk, cc, agg, U, i32(16), i32(16 + ctx_bits))
         e1.record()
         del ck, cc
@@ -416,12 +594,12 @@ class CountBuild:
         e0, e1 = self._event("pos_gather", k, -1, N)
         e0.record()
         kout = self.topk
-        elib("ng_pos_gather", vi.ctx_of, N, lo, hi, tgt, uk, agg, start, end, tot, top_tok, top_cnt, None, t["keys"],
-             t["cnts"], u64(cap), i32(ktop), i32(kout), i32(li), out[0, li], out[1, li], out[2, li],
+        pk, pc, cap = (t["keys"], t["cnts"], t["cap"]) if qcnt is None else (None, None, 0)
+        elib("ng_pos_gather", vi.ctx_of, N, lo, hi, tgt, uk, agg, start, end, tot, top_tok, top_cnt, None, pk, pc,
+             u64(cap), qcnt, i32(ktop), i32(kout), i32(li), out[0, li], out[1, li], out[2, li],
              self.top_tok[li] if kout else None, self.top_cnt[li] if kout else None, None)
         e1.record()
-        t.pop("keys"), t.pop("cnts")
-        return U, tot, top_tok, top_cnt, ktop
+        return tot, top_tok, top_cnt, ktop
 
     def _outputs_record(self, li, k, vi, t, tgt, out, want):
         """One level's outputs with the record's calls: part_count/part_scatter, sort by pair key, seg_bounds,

@@ -133,7 +133,7 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
         lib("seg_bounds", uk, U, start, end)
         elib("ng_ctx_topk", uk, agg, start, end, vi.ids, i32(1), tot, top_tok, top_cnt)
         elib("ng_pos_gather", vi.ctx_of, N, 0, vi.ids, x, uk, agg, start, end, tot, top_tok, top_cnt, None, None,
-             None, u64(0), i32(1), i32(1), i32(0), o_tot, o_dist, o_cnt, nxt, cnt, None)
+             None, u64(0), None, i32(1), i32(1), i32(0), o_tot, o_dist, o_cnt, nxt, cnt, None)
         del vi, uk, agg, start, end, tot, top_tok, top_cnt
     if timing is not None:
         torch.cuda.synchronize()

@@ -42,14 +42,20 @@ def _partition_small_tables(monkeypatch):
 @pytest.mark.parametrize("level_shards,mode", [({}, "engine"), ({2: 1, 3: 2}, "engine"), ({}, "engine-compact"),
                                                ({2: 1, 3: 2}, "engine-compact"), ({}, "record"),
                                                ({2: 1, 3: 2}, "record"), ({}, "partitioned"),
-                                               ({2: 1, 3: 2}, "partitioned")])
+                                               ({2: 1, 3: 2}, "partitioned"), ({}, "part"), ({2: 1, 3: 2}, "part"),
+                                               ({}, "part-compact"), ({2: 1, 3: 2}, "part-regroup")])
 def test_counts_match_oracle(corpus, level_shards, mode, monkeypatch):
     if mode == "partitioned":
         _partition_small_tables(monkeypatch)
+    if mode == "part-regroup":
+        # one partition per level to start with: each level's LDS table overflows and it is repartitioned bit by bit;
+        # three blocks, each counting a run of partitions
+        monkeypatch.setattr(C, "PART_TARGET", 1 << 30)
+        monkeypatch.setattr(C, "PART_BLOCKS", 3)
     lib = C.record_lib()
     cb = C.CountBuild(corpus.shards(), levels=LEVELS, level_shards=level_shards, topk=4)
     cb.mode = mode.split("-")[0]
-    if mode == "engine-compact":  # every gated level scans its LDS-listed set positions
+    if mode.endswith("-compact"):  # every gated level scans its LDS-listed set positions
         cb.density = {k: 0.0 for k in LEVELS}
     cb.start_load(3)
     cb.pace()
@@ -67,7 +73,10 @@ def test_counts_match_oracle(corpus, level_shards, mode, monkeypatch):
         assert np.array_equal(top_tok[li], o["top_tok"][:, :4]), f"top_tok k={k}"
         assert np.array_equal(top_cnt[li], o["top_cnt"][:, :4]), f"top_cnt k={k}"
         assert cb.info[k]["hits"] == o["events"], f"hits k={k}"
-        assert (cb.info[k]["pbits"] > 0) == (mode == "partitioned"), k
+        if not mode.startswith("part-") and mode != "part":
+            assert (cb.info[k]["pbits"] > 0) == (mode == "partitioned"), k
+    if mode == "part-regroup":
+        assert cb.info[2]["pbits"] >= 3, cb.info[2]
     assert (ref[2]["tot"] > 0).sum() > 1000 and (ref[20]["tot"] > 0).sum() > 10
     # the record's rows from ROW_LEVELS, and a batch of them
     ri = [LEVELS.index(k) for k in C.ROW_LEVELS]
