@@ -38,7 +38,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--query-tokens", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other configurations' measurements")
-    ap.add_argument("--mode", default="engine", choices=("engine", "part", "record", "partitioned"),
+    ap.add_argument("--mode", default="part", choices=("engine", "part", "record", "partitioned"),
                     help="CountBuild.mode")
     ap.add_argument("--cpu-tokens", type=int, default=100_000_000, help="CPU baseline: corpus prefix")
     ap.add_argument("--cpu-queries", type=int, default=2_000_000, help="CPU baseline: query positions")

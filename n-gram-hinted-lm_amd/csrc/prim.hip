@@ -185,53 +185,101 @@ int inclusive_max_i64(const i64* in, i64* out, i64 n, void* temp, hipStream_t st
 // Radix sort
 // ---------------------------------------------------------------------------------------------------------------
 
-__global__ void __launch_bounds__(BLOCK) rs_hist_k(const u64* __restrict__ keys, i64 n, int shift, u32 mask,
-                                                   u32* __restrict__ hist, i64 ntiles) {
-    __shared__ u32 h[256];
-    h[threadIdx.x] = 0;
-    __syncthreads();
-    const i64 base = (i64)blockIdx.x * TILE;
+// Radix passes use their own tiles: 1024 threads x 8 items (8192 items), measured on MI355X at 3.6 TB/s for a
+// keys-only scatter pass and 2.7 TB/s with values, against 2.9 and 1.9 for 256 x 16 (longer per-digit runs, fewer
+// blocks).
+static constexpr int RS_BLOCK = 1024;
+static constexpr int RS_ITEMS = 8;
+static constexpr int RS_TILE = RS_BLOCK * RS_ITEMS;
+static constexpr int RS_NW = RS_BLOCK / WAVE;
+static inline i64 rs_ntiles(i64 n) { return (n + RS_TILE - 1) / RS_TILE; }
+
+// Exclusive scan of one value per thread over the 1024-thread block (a wave scan, then the 16 wave totals).
+__device__ __forceinline__ u32 rs_block_exclusive(u32 v, u32* wt) {
+    const int lane = lane_id(), w = threadIdx.x / WAVE;
+    u32 incl = v;
 #pragma unroll
-    for (int j = 0; j < ITEMS; ++j) {
-        const i64 i = base + (i64)j * BLOCK + threadIdx.x;
-        if (i < n) atomicAdd(&h[(u32)(keys[i] >> shift) & mask], 1u);
+    for (int d = 1; d < WAVE; d <<= 1) {
+        const u32 o = (u32)__shfl_up((int)incl, d, WAVE);
+        if (lane >= d) incl += o;
     }
+    if (lane == WAVE - 1) wt[w] = incl;
     __syncthreads();
-    hist[(i64)threadIdx.x * ntiles + blockIdx.x] = h[threadIdx.x];
+    u32 before = 0;
+#pragma unroll
+    for (int i = 0; i < RS_NW; ++i)
+        if (i < w) before += wt[i];
+    __syncthreads();
+    return before + incl - v;
 }
 
-// Stable scatter of one tile: items in tile order (row j, thread t) = index j * 256 + t; per row, each wave ranks its
+// Per tile its digit counts, hist[digit * ntiles + tile] (one LDS histogram per wave, summed at the end).
+__global__ void __launch_bounds__(RS_BLOCK) rs_hist_k(const u64* __restrict__ keys, i64 n, int shift, u32 mask,
+                                                      u32* __restrict__ hist, i64 ntiles) {
+    __shared__ u32 h[RS_NW * 256];
+    for (int i = threadIdx.x; i < RS_NW * 256; i += RS_BLOCK) h[i] = 0;
+    __syncthreads();
+    u32* hw = h + (threadIdx.x / WAVE) * 256;
+    const i64 base = (i64)blockIdx.x * RS_TILE;
+    u64 k[RS_ITEMS];
+#pragma unroll
+    for (int j = 0; j < RS_ITEMS; ++j) {
+        const i64 i = base + (i64)j * RS_BLOCK + threadIdx.x;
+        k[j] = i < n ? keys[i] : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < RS_ITEMS; ++j) {
+        const i64 i = base + (i64)j * RS_BLOCK + threadIdx.x;
+        if (i < n) atomicAdd(&hw[(u32)(k[j] >> shift) & mask], 1u);
+    }
+    __syncthreads();
+    if (threadIdx.x < 256) {
+        u32 sum = 0;
+#pragma unroll
+        for (int w = 0; w < RS_NW; ++w) sum += h[w * 256 + threadIdx.x];
+        hist[(i64)threadIdx.x * ntiles + blockIdx.x] = sum;
+    }
+}
+
+// Stable scatter of one tile: items in tile order (row j, thread t) = index j * 1024 + t; per row, each wave ranks its
 // lanes by digit with eight ballots; the per-(row, wave, digit) counts (u16) are scanned in LDS in tile order, giving
 // each item its place in the tile sorted by digit. The tile is then staged in LDS in that order (aliasing the counts)
 // and written out by consecutive threads, so each digit's run of the tile leaves as contiguous, coalesced stores.
 template <bool VALUES>
-__global__ void __launch_bounds__(BLOCK) rs_scatter_k(const u64* __restrict__ kin, const u32* __restrict__ vin,
-                                                      u64* __restrict__ kout, u32* __restrict__ vout, i64 n, int shift,
-                                                      int nbits, const u32* __restrict__ hist, i64 ntiles) {
-    constexpr int STAGE_U64 = TILE + TILE / 2;  // keys (TILE u64) then values (TILE u32)
-    static_assert(ITEMS * NWAVES * 256 * 2 <= STAGE_U64 * 8, "the counts fit the staging area");
-    __shared__ u64 smem[STAGE_U64];
+__global__ void __launch_bounds__(RS_BLOCK) rs_scatter_k(const u64* __restrict__ kin, const u32* __restrict__ vin,
+                                                         u64* __restrict__ kout, u32* __restrict__ vout, i64 n,
+                                                         int shift, int nbits, const u32* __restrict__ hist,
+                                                         i64 ntiles) {
+    constexpr int CNT_BYTES = RS_ITEMS * RS_NW * 256 * 2;
+    constexpr int STAGE_BYTES = RS_TILE * (VALUES ? 12 : 8);
+    constexpr int SMEM_U64 = (CNT_BYTES > STAGE_BYTES ? CNT_BYTES : STAGE_BYTES) / 8;
+    __shared__ u64 smem[SMEM_U64];
     __shared__ u32 gbase[256];
     __shared__ u32 tile_off[256];
-    u16* cnt = (u16*)smem;  // [ITEMS][NWAVES][256]
+    __shared__ u32 wt[RS_NW];
+    u16* cnt = (u16*)smem;  // [RS_ITEMS][RS_NW][256]
     u64* stage_k = smem;
-    u32* stage_v = (u32*)(smem + TILE);
+    u32* stage_v = (u32*)(smem + RS_TILE);
     const int t = threadIdx.x, w = t / WAVE;
     const u32 mask = (1u << nbits) - 1u;
-    gbase[t] = hist[(i64)t * ntiles + blockIdx.x];
-    for (int i = t; i < ITEMS * NWAVES * 256 / 2; i += BLOCK) ((u32*)smem)[i] = 0;
+    if (t < 256) gbase[t] = hist[(i64)t * ntiles + blockIdx.x];
+    for (int i = t; i < CNT_BYTES / 4; i += RS_BLOCK) ((u32*)smem)[i] = 0;
     __syncthreads();
-    const i64 base = (i64)blockIdx.x * TILE;
-    const int tile_n = (int)(n - base < TILE ? n - base : TILE);
-    u64 key[ITEMS];
-    u32 val[ITEMS];
-    u32 dr[ITEMS];  // digit | rank << 16 ; rank 0xFFFF = invalid
+    const i64 base = (i64)blockIdx.x * RS_TILE;
+    const int tile_n = (int)(n - base < RS_TILE ? n - base : RS_TILE);
+    u64 key[RS_ITEMS];
+    u32 val[RS_ITEMS];
+    u32 dr[RS_ITEMS];  // digit | rank << 16 ; rank 0xFFFF = invalid
 #pragma unroll
-    for (int j = 0; j < ITEMS; ++j) {
-        const i64 i = base + (i64)j * BLOCK + t;
+    for (int j = 0; j < RS_ITEMS; ++j) {
+        const i64 i = base + (i64)j * RS_BLOCK + t;
         const bool valid = i < n;
         key[j] = valid ? kin[i] : 0;
         if (VALUES) val[j] = valid ? vin[i] : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < RS_ITEMS; ++j) {
+        const bool valid = base + (i64)j * RS_BLOCK + t < n;
         const u32 d = (u32)(key[j] >> shift) & mask;
         u64 peers = __ballot(valid);
 #pragma unroll
@@ -243,38 +291,39 @@ __global__ void __launch_bounds__(BLOCK) rs_scatter_k(const u64* __restrict__ ki
             }
         }
         const u32 rank = (u32)__popcll(peers & lanemask_lt());
-        if (valid && rank == 0) cnt[(j * NWAVES + w) * 256 + d] = (u16)__popcll(peers);
+        if (valid && rank == 0) cnt[(j * RS_NW + w) * 256 + d] = (u16)__popcll(peers);
         dr[j] = valid ? (d | (rank << 16)) : 0xFFFF0000u;
     }
     __syncthreads();
-    u32 run = 0;  // thread t = digit t: its items' exclusive offsets in (row, wave) order, and its tile total
-    for (int j = 0; j < ITEMS; ++j)
+    u32 run = 0;  // thread t < 256 = digit t: its items' exclusive offsets in (row, wave) order, and its tile total
+    if (t < 256) {
+        for (int j = 0; j < RS_ITEMS; ++j)
 #pragma unroll
-        for (int ww = 0; ww < NWAVES; ++ww) {
-            u16* c = &cnt[(j * NWAVES + ww) * 256 + t];
-            const u32 v = *c;
-            *c = (u16)run;
-            run += v;
-        }
-    u32 total;
-    const u32 off = block_exclusive<u32, Sum<u32>>(run, &total);
-    tile_off[t] = off;
+            for (int ww = 0; ww < RS_NW; ++ww) {
+                u16* c = &cnt[(j * RS_NW + ww) * 256 + t];
+                const u32 v = *c;
+                *c = (u16)run;
+                run += v;
+            }
+    }
+    const u32 off = rs_block_exclusive(run, wt);
+    if (t < 256) tile_off[t] = off;
     __syncthreads();
-    u32 local[ITEMS];
+    u32 local[RS_ITEMS];
 #pragma unroll
-    for (int j = 0; j < ITEMS; ++j) {
+    for (int j = 0; j < RS_ITEMS; ++j) {
         const u32 d = dr[j] & 0xFFFFu;
-        local[j] = (dr[j] >> 16) == 0xFFFFu ? 0xFFFFFFFFu : tile_off[d] + cnt[(j * NWAVES + w) * 256 + d] + (dr[j] >> 16);
+        local[j] = (dr[j] >> 16) == 0xFFFFu ? 0xFFFFFFFFu : tile_off[d] + cnt[(j * RS_NW + w) * 256 + d] + (dr[j] >> 16);
     }
     __syncthreads();  // the counts are read: the staging area may overwrite them
 #pragma unroll
-    for (int j = 0; j < ITEMS; ++j) {
+    for (int j = 0; j < RS_ITEMS; ++j) {
         if (local[j] == 0xFFFFFFFFu) continue;
         stage_k[local[j]] = key[j];
         if (VALUES) stage_v[local[j]] = val[j];
     }
     __syncthreads();
-    for (int i = t; i < tile_n; i += BLOCK) {
+    for (int i = t; i < tile_n; i += RS_BLOCK) {
         const u64 k = stage_k[i];
         const u32 d = (u32)(k >> shift) & mask;
         const u32 pos = gbase[d] + (u32)i - tile_off[d];
@@ -292,7 +341,7 @@ __global__ void copy_pairs_k(const u64* kin, u64* kout, const u32* vin, u32* vou
 
 size_t radix_sort_temp_bytes(i64 n, bool with_values) {
     if (n <= 0) return 256;
-    const i64 nt = ntiles_of(n);
+    const i64 nt = rs_ntiles(n);
     size_t b = align_up((size_t)n * 8);
     if (with_values) b += align_up((size_t)n * 4);
     b += align_up((size_t)nt * 256 * 4);
@@ -313,7 +362,7 @@ int radix_sort_pairs(const u64* kin, u64* kout, const u32* vin, u32* vout, i64 n
                                                                                      vout, n);
         return (int)hipGetLastError();
     }
-    const i64 nt = ntiles_of(n);
+    const i64 nt = rs_ntiles(n);
     char* t = (char*)temp;
     u64* tk = (u64*)t;
     t += align_up((size_t)n * 8);
@@ -334,13 +383,13 @@ int radix_sort_pairs(const u64* kin, u64* kout, const u32* vin, u32* vout, i64 n
         const bool to_out = ((passes - 1 - p) % 2) == 0;
         u64* dk = to_out ? kout : tk;
         u32* dv = to_out ? vout : tv;
-        rs_hist_k<<<(unsigned)nt, BLOCK, 0, st>>>(sk, n, shift, (1u << nb) - 1u, hist, nt);
+        rs_hist_k<<<(unsigned)nt, RS_BLOCK, 0, st>>>(sk, n, shift, (1u << nb) - 1u, hist, nt);
         int e = exclusive_scan_u32(hist, hist, nt * 256, nullptr, stemp, st);
         if (e) return e;
         if (values)
-            rs_scatter_k<true><<<(unsigned)nt, BLOCK, 0, st>>>(sk, sv, dk, dv, n, shift, nb, hist, nt);
+            rs_scatter_k<true><<<(unsigned)nt, RS_BLOCK, 0, st>>>(sk, sv, dk, dv, n, shift, nb, hist, nt);
         else
-            rs_scatter_k<false><<<(unsigned)nt, BLOCK, 0, st>>>(sk, nullptr, dk, nullptr, n, shift, nb, hist, nt);
+            rs_scatter_k<false><<<(unsigned)nt, RS_BLOCK, 0, st>>>(sk, nullptr, dk, nullptr, n, shift, nb, hist, nt);
         e = (int)hipGetLastError();
         if (e) return e;
         sk = dk;

@@ -112,10 +112,10 @@ class CountBuild:
     counts; `topk`: per level the first topk ranked next tokens/counts of each position's context (self.top_tok /
     self.top_cnt [len(levels), N, topk]) when > 0. Construct with `from_device` for tokens already in GPU memory.
 
-    `mode` (attribute): "engine" (default) counts in split pair tables (keys and u32 counts apart) and ranks by
-    per-context selection after one sort (libngram_amd.so's ng_* entry points); "part" counts without global
-    atomics: each level's hits emitted, hash-partitioned by a radix sort and counted partition by partition in LDS,
-    then the engine's owner side; "record" runs the record's own C ABI
+    `mode` (attribute): "part" (default) counts without global atomics: each level's hits emitted, hash-partitioned
+    by a radix sort and counted partition by partition in LDS, then the engine's owner side; "engine" counts in split
+    pair tables (keys and u32 counts apart) with global atomics and ranks by per-context selection after one sort
+    (libngram_amd.so's ng_* entry points); "record" runs the record's own C ABI
     calls, as its host does (one packed table per level, two sorts); "partitioned" is "record" with the large tables'
     hits emitted, grouped by sub-table and counted sub-table by sub-table."""
 
@@ -125,7 +125,7 @@ class CountBuild:
             raise ValueError("this build runs on one GPU: world must be 1 (the owner exchange is out of scope)")
         self.rank, self.world = rank, world
         self.min_cap = 1 << 20
-        self.mode = "engine"
+        self.mode = "part"
         self.density: dict[int, float] = {}  # each level's hit density, from the last build with stats
         self.dratio: dict[int, float] = {}  # "part" mode: each level's distinct pairs per event, from the last build
         self.levels = tuple(levels)
@@ -163,7 +163,7 @@ class CountBuild:
         self = cls.__new__(cls)
         self.rank, self.world = 0, 1
         self.min_cap = 1 << 20
-        self.mode = "engine"
+        self.mode = "part"
         self.density: dict[int, float] = {}  # each level's hit density, from the last build with stats
         self.dratio: dict[int, float] = {}  # "part" mode: each level's distinct pairs per event, from the last build
         self.levels = tuple(levels)

@@ -13,6 +13,7 @@ import torch
 from .lib import Lib, i32, u64
 
 TAIL = 4096  # slots past cap that linear probing may run into; the last stays empty
+LOAD = 0.4  # contexts per slot aimed at: measured at c3, 0.4 gives the fastest scans (0.5 +10%, 0.66 +50%)
 
 
 class QueryIndex:
@@ -21,7 +22,7 @@ class QueryIndex:
         dev = x.device
         N = x.numel()
         m = N if positions is None else int(positions.numel())
-        cap = 2 * m + 1024
+        cap = int(m / LOAD) + 1024
         while True:
             slots = cap + TAIL
             table = torch.full((slots,), -1, dtype=torch.int64, device=dev)
@@ -39,10 +40,10 @@ class QueryIndex:
         if c[2]:
             raise RuntimeError(f"k={k}: {c[2]} query positions collide with another context's key")
         n_ctx = int(c[0])
-        if m and cap > 4 * n_ctx + 4096:
-            # sized for every position, used by far fewer contexts: move them to a table sized for them, so that
-            # context ids (slots) take fewer bits
-            small = 2 * n_ctx + 1024
+        if m and cap > 2 * (n_ctx / LOAD) + 4096:
+            # sized for every position, used by far fewer contexts: move them to a table sized for them (fewer bits
+            # per context id, probes that stay in cache more often)
+            small = int(n_ctx / LOAD) + 1024
             while True:
                 t2 = torch.full((small + TAIL,), -1, dtype=torch.int64, device=dev)
                 r2 = torch.full((small + TAIL,), -1, dtype=torch.int32, device=dev)
