@@ -5,9 +5,11 @@ counts of the query contexts for n = 2..8, then for 16M query positions each lev
 tokens with counts, and hit/miss. One step = one whole count build + query over the resident corpus and queries.
 
 Prints one JSON line: value = corpus tokens counted per second (T x steps / timed seconds), plus query positions/s,
-the roofline of the dominant kernel (scan_level: algorithmic bytes 2 per corpus position + 16 per hit, over its
-average launch duration timed with HIP events on the launch stream) and the CPU baseline (the oracle's C++ restatement
-of kgram.rs's query-filtered counting, timed on this host on a bounded sample)."""
+the roofline of the dominant kernel (the level scans: algorithmic bytes 2 per corpus position scanned + 8 per hit
+emitted, or 16 per hit counted in place, over their launch durations timed with HIP events on the launch stream), the
+count path's roofline in "part" mode (scan, pack, partition and LDS count: 2 per position + 16 per hit) and the CPU
+baseline (the oracle's C++ restatement of kgram.rs's query-filtered counting, timed on this host on a bounded
+sample)."""
 
 from __future__ import annotations
 
@@ -26,6 +28,15 @@ SCAN_KERNELS = ("scan_count", "scan_level", "scan_emit")  # the level scans, whi
 # "part" mode counts after the scan (emitted hits packed, hash-partitioned, counted in LDS): its roofline kernel set is
 # the whole count path, whose algorithmic bytes are the build's 2 per position scanned + 16 per hit
 PART_KERNELS = ("scan_emit", "gather", "partition", "count")
+
+
+def scan_traffic(mode: str):
+    """HBM bytes per level-scan launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs (scaled by a plain
+    copy's reading of the same counters), or None where none was measured for this mode."""
+    f = ROOT / "profiles" / f"scan_emit_c3_{mode}_traffic.json"
+    if not f.exists():
+        return None
+    return json.loads(f.read_text())["traffic_bytes_per_launch"]
 
 
 def parse() -> argparse.Namespace:
@@ -296,8 +307,7 @@ def main() -> None:
     cb.timing.clear()
     t0 = time.perf_counter()
     class_ms: dict[str, float] = {}
-    scan_ms, scan_launches = 0.0, 0
-    roof = PART_KERNELS if cb.mode == "part" else SCAN_KERNELS
+    scan_ms, scan_launches, path_ms = 0.0, 0, 0.0
     for step in range(args.steps):
         out = cb.counts(x, tgt, avail)
         log(f"step {step}: {sum(cb.timing.values()) / (step + 1):.4f} s/step so far")
@@ -305,23 +315,28 @@ def main() -> None:
         for name, k, i, n, e0, e1 in cb.kernel_events:
             ms = e0.elapsed_time(e1)
             class_ms[name] = class_ms.get(name, 0.0) + ms
-            if name in roof:
+            if name in SCAN_KERNELS:
                 scan_ms += ms
                 scan_launches += 1
+            if name in PART_KERNELS:
+                path_ms += ms
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     hits = sum(v["hits"] for v in info.values())
     # algorithmic bytes of the scan launches of one step: 2 per position scanned, and per hit 16 (counted in place:
     # the 8-byte slot read and written, or the split table's key read + count read and written) or 8 (emitted: the key
-    # written)
+    # written, read back by the count)
     positions = {k: 0 for k in cfg.levels}
     for name, k, i, n, _, _ in cb.kernel_events:
         if name in SCAN_KERNELS:
             positions[k] += n
-    per_hit = {k: 16.0 if cb.mode == "part" or not info[k]["pbits"] else 8.0 for k in cfg.levels}
+    emits = cb.mode == "part" or any(v["pbits"] for v in info.values())
+    per_hit = {k: 8.0 if cb.mode == "part" or info[k]["pbits"] else 16.0 for k in cfg.levels}
     step_bytes = sum(2.0 * positions[k] + per_hit[k] * info[k]["hits"] for k in cfg.levels)
     scan_bytes = args.steps * step_bytes
     achieved = scan_bytes / (scan_ms / 1e3) / 1e9 if scan_ms > 0 else 0.0
+    # the whole count path of "part" mode (scan, pack, partition, LDS count): 2 per position + 16 per hit
+    path_bytes = sum(2.0 * positions[k] + 16.0 * info[k]["hits"] for k in cfg.levels)
     build_bytes = 2.0 * T + 16.0 * hits  # the count build's B_build = 2 T + 16 E
     ms = dt / args.steps * 1e3
     mask_hits = int((out[0] != 0).sum().item())
@@ -336,14 +351,20 @@ def main() -> None:
         "config": {"workload": f"{cfg.name}: count build of {T} corpus tokens ({len(sizes)} shards) for n="
                                f"{list(cfg.levels)} + top-{cfg.topk}/count/hit queries at {N} positions",
                    "corpus_tokens": T, "query_positions": N, "levels": list(cfg.levels), "topk": cfg.topk},
-        "roofline": {"bound": "hbm", "kernel": ("count path" if cb.mode == "part" else "level scan") + f" ({cb.mode}: "
-                     + ", ".join(sorted({n for n, *_ in cb.kernel_events if n in roof})) + ")",
+        "roofline": {"bound": "hbm", "kernel": f"level scan ({cb.mode}: "
+                     + ", ".join(sorted({n for n, *_ in cb.kernel_events if n in SCAN_KERNELS})) + ")",
+                     "bytes_per_position": 2, "bytes_per_hit": 8 if emits else 16,
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": scan_traffic(cb.mode),
                      "launches_per_step": scan_launches // max(1, args.steps),
                      "avg_launch_ms": scan_ms / max(1, scan_launches),
                      "algorithmic_bytes_per_step": step_bytes,
                      "scan_share_of_step": scan_ms / args.steps / ms},
+        "count_path_roofline": None if cb.mode != "part" else {
+            "kernels": list(PART_KERNELS), "algorithmic_bytes_per_step": path_bytes,
+            "ms_per_step": path_ms / args.steps, "achieved": path_bytes / (path_ms / args.steps / 1e3) / 1e9,
+            "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": path_bytes / (path_ms / args.steps / 1e3) / 1e9 / HBM_PEAK_GBS},
         "build_roofline": {"bytes": build_bytes, "GBps_over_step": build_bytes / (ms / 1e3) / 1e9,
                            "frac_over_step": build_bytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS},
         "kernel_ms_per_step": {k: v / args.steps for k, v in class_ms.items()},
