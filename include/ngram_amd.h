@@ -160,8 +160,23 @@ int ng_part_lookups(const int* ctx_of, const uint16_t* tgt, ng_i64 N, ng_i64 lo,
  * of them; qcnt[qv[j]] = the count of lookup j (qk sorted like ev, bounds qstart); flags[0] bit 0: a partition held
  * more than 8192 distinct pairs (repartition with one more bit) */
 int ng_part_count(const ng_u64* ev, const ng_i64* start, int pbits, const ng_u64* qk, const uint32_t* qv,
-                  const ng_i64* qstart, ng_u64* out_k, uint32_t* out_c, uint32_t* seg_cnt, ng_i64* seg_base,
-                  uint32_t* qcnt, uint32_t* flags, int grid, void* stream);
+                  const ng_i64* qstart, ng_u64* out_k, uint32_t* out_c, int cb, ng_u64* esc_k, uint32_t* esc_c,
+                  ng_u64 esc_cap, uint32_t* seg_cnt, ng_i64* seg_base, uint32_t* qcnt, uint32_t* flags, int grid,
+                  void* stream);
+/* with cb > 0 (ids below 2^cb, cb <= 44) ng_part_count writes packed words pair key << (48 - cb) | min(count, esc),
+ * esc = 2^(48 - cb) - 1, larger counts also into the escape table esc_k/esc_c (EMPTY-filled; full: flags[0] bit 1).
+ * From such words sorted by context: dist[c] (pairs) and the record rec[c] of each present context (callers zero
+ * dist): u32 words total, pairs, the first topk (1, 2, 4, 8) tokens by (count desc, token asc) two per word, their
+ * counts (4, 8, 8, 16 words for topk 1, 2, 4, 8); flags[0] bit 2: a total reached 2^32 */
+int ng_ctx_summary(const ng_u64* w, ng_i64 U, int cb, const ng_u64* esc_k, const uint32_t* esc_c, ng_u64 esc_cap,
+                   int topk, uint32_t* rec, uint32_t* dist, uint32_t* flags, void* stream);
+/* per query position from ng_ctx_summary's records and pair counts and the counted lookups qcnt: tot, dist, cnt
+ * (thr: the CNT_TOP threshold scores, may be NULL), the first kout of ktop top entries, mask bit li (mask may be
+ * NULL) */
+int ng_pos_summary(const int* ctx_of, ng_i64 N, ng_i64 lo, ng_i64 hi, const uint16_t* tgt, const uint32_t* rec,
+                   const uint32_t* dist, const ng_u64* thr, const uint32_t* qcnt, int ktop, int kout, int li,
+                   int* out_tot, int* out_dist, int* out_cnt, uint16_t* out_tok, uint32_t* out_tcnt, int* mask,
+                   void* stream);
 /* corpus-wide level build (count_table.rs build_level): contexts into ck (slot = id), (slot << 16 | next) counted in
  * the split table pk/pcnt; flags[0] bit 0 pair table full, bit 1 context table full */
 int ng_table_build(const uint16_t* tok, ng_i64 L, int k, ng_u64* ck, ng_u64 ccap, ng_u64* pk, uint32_t* pcnt,

@@ -305,20 +305,6 @@ __global__ void __launch_bounds__(256) table_compact_k(const u64* __restrict__ k
     }
 }
 
-// top-k insertion of a score (count << 16 | (65535 - token): larger = ranked higher) into a descending list (static
-// indices only: the list stays in registers)
-template <int KT>
-__device__ __forceinline__ void topk_insert(u64 (&t)[KT], u64 v) {
-#pragma unroll
-    for (int j = 0; j < KT; ++j)
-        if (v > t[j]) {
-            const u64 tmp = t[j];
-            t[j] = v;
-            v = tmp;
-        }
-}
-
-__device__ __forceinline__ u64 rank_score(u64 key, u32 n) { return ((u64)n << 16) | (0xFFFFu - (u32)(key & 0xFFFF)); }
 
 // Per context c in [0, nctx): tot[c] = sum of its pair counts, its first KT pairs by (count desc, token asc) into
 // top_tok/top_cnt [nctx, KT] (0-padded). Pairs sorted by key (context, token), context c's in [start[c], end[c]).

@@ -151,3 +151,19 @@ __device__ __forceinline__ bool wave_seg_tail(u64 seg, bool valid_next) {
     const u64 nxt = shfl_down_u64(seg, 1);
     return lane == WAVE - 1 || !valid_next || nxt != seg;
 }
+
+// top-k insertion of a score (count << 16 | (65535 - token): larger = ranked higher) into a descending list (static
+// indices only: the list stays in registers)
+template <int KT>
+__device__ __forceinline__ void topk_insert(u64 (&t)[KT], u64 v) {
+#pragma unroll
+    for (int j = 0; j < KT; ++j)
+        if (v > t[j]) {
+            const u64 tmp = t[j];
+            t[j] = v;
+            v = tmp;
+        }
+}
+
+// The ranking score of pair key (context << 16 | token) with count n: count descending, then token ascending.
+__device__ __forceinline__ u64 rank_score(u64 key, u32 n) { return ((u64)n << 16) | (0xFFFFu - (u32)(key & 0xFFFF)); }

@@ -137,12 +137,40 @@ __device__ __forceinline__ u32 pt_find(const u64* tk, const u32* tc, u64 key) {
     return 0;
 }
 
+// A count too large for a packed word's count field: (pair key, count) into the escape table (linear probing; each
+// distinct pair is written once). A full table sets flags[0] bit 1.
+__device__ __forceinline__ void esc_put(u64* esc_k, u32* esc_c, u64 cap, u64 key, u32 n, u32* flags) {
+    u64 s = __umul64hi(mix64(key), cap);
+    for (u64 probe = 0; probe < cap; ++probe) {
+        if (atomicCAS((unsigned long long*)&esc_k[s], EMPTY, key) == EMPTY) {
+            esc_c[s] = n;
+            return;
+        }
+        s = s + 1 == cap ? 0 : s + 1;
+    }
+    atomicOr(&flags[0], 2u);
+}
+
+__device__ __forceinline__ u32 esc_get(const u64* __restrict__ esc_k, const u32* __restrict__ esc_c, u64 cap, u64 key) {
+    u64 s = __umul64hi(mix64(key), cap);
+    for (u64 probe = 0; probe < cap; ++probe) {
+        const u64 cur = esc_k[s];
+        if (cur == key) return esc_c[s];
+        if (cur == EMPTY) return 0;
+        s = s + 1 == cap ? 0 : s + 1;
+    }
+    return 0;
+}
+
 // Block b counts partitions [b * ppb, (b + 1) * ppb) in turn. Its distinct pairs (at most its events) go to
 // out[start[p0] ...]: segment b = (seg_base[b], seg_cnt[b]). qcnt[qv[j]] = the count of lookup j (0: absent).
+// cb == 0: out_k = pair key, out_c = count. cb > 0 (context ids below 2^cb, cb <= 44): out_k = the packed word
+// pair key << (48 - cb) | min(count, esc), esc = 2^(48 - cb) - 1, a count >= esc also put in the escape table.
 __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__ ev, const i64* __restrict__ start,
                                                         i64 P, i64 ppb, const u64* __restrict__ qk,
                                                         const u32* __restrict__ qv, const i64* __restrict__ qstart,
-                                                        u64* __restrict__ out_k, u32* __restrict__ out_c,
+                                                        u64* __restrict__ out_k, u32* __restrict__ out_c, int cb,
+                                                        u64* esc_k, u32* esc_c, u64 esc_cap,
                                                         u32* __restrict__ seg_cnt, i64* __restrict__ seg_base,
                                                         u32* __restrict__ qcnt, u32* flags) {
     __shared__ u64 tk[PT_SLOTS];
@@ -203,8 +231,16 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
             off = (u32)__shfl((int)off, 0, WAVE);
             if (occ) {
                 const u64 at = (u64)out_base + off + (u64)__popcll(bal & lanemask_lt());
-                out_k[at] = unmix64(key);
-                out_c[at] = tc[j];
+                const u64 pk = unmix64(key);
+                const u32 n = tc[j];
+                if (cb == 0) {
+                    out_k[at] = pk;
+                    out_c[at] = n;
+                } else {
+                    const u64 esc = (1ull << (48 - cb)) - 1;
+                    out_k[at] = (pk << (48 - cb)) | ((u64)n < esc ? (u64)n : esc);
+                    if ((u64)n >= esc) esc_put(esc_k, esc_c, esc_cap, pk, n, flags);
+                }
             }
         }
         __syncthreads();
@@ -213,6 +249,182 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
         seg_cnt[blockIdx.x] = cur;
         seg_base[blockIdx.x] = out_base;
     }
+}
+
+// Per context from packed words sorted by context (word >> (64 - cb)): a wave per window of 64 words. For each context
+// starting in its window (a lane whose word's context differs from the previous word's), the wave takes the context's
+// lanes (a run: the words are sorted), and while the run reaches the window's end, the next windows' leading lanes of
+// the same context; counts summed and the top KT kept per lane, then reduced across the wave. No dependent loads:
+// every word is read by its own window and at most once more by the window of its context's first word. For present
+// contexts only: dist[c] = its pairs, and its record rec[c] (rec_words(KT) u32: total, pairs, the first KT tokens by
+// (count desc, token asc) two per word, their counts; 0-padded), stored whole as 16-byte vectors; flags[0] bit 2 if a
+// total reaches 2^32.
+template <int KT>
+struct CtxRecord {
+    static constexpr int TOKW = (KT + 1) / 2;
+    static constexpr int USED = 2 + TOKW + KT;
+    static constexpr int WORDS = USED <= 4 ? 4 : USED <= 8 ? 8 : 16;
+};
+
+template <int KT>
+__device__ __forceinline__ void store_record(u32* __restrict__ rec, u64 c, u64 total, u32 pairs, const u64 (&top)[KT]) {
+    using R = CtxRecord<KT>;
+    u32 v[R::WORDS];
+#pragma unroll
+    for (int q = 0; q < R::WORDS; ++q) v[q] = 0;
+    v[0] = (u32)total;
+    v[1] = pairs;
+#pragma unroll
+    for (int r = 0; r < KT; ++r) {
+        const u32 tk = top[r] ? 0xFFFFu - (u32)(top[r] & 0xFFFF) : 0u;
+        v[2 + r / 2] |= tk << (16 * (r & 1));
+        v[2 + R::TOKW + r] = (u32)(top[r] >> 16);
+    }
+    uint4* dst = (uint4*)(rec + c * R::WORDS);
+#pragma unroll
+    for (int q = 0; q < R::WORDS / 4; ++q) dst[q] = make_uint4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+}
+
+template <int KT>
+__global__ void __launch_bounds__(256) ctx_summary_k(const u64* __restrict__ w, i64 U, int cb,
+                                                     const u64* __restrict__ esc_k, const u32* __restrict__ esc_c,
+                                                     u64 esc_cap, u32* __restrict__ rec, u32* __restrict__ dist,
+                                                     u32* flags) {
+    const int sh = 64 - cb, csh = 48 - cb;
+    const u64 esc = (1ull << csh) - 1;
+    const int lane = lane_id();
+    auto count_of = [&](u64 word) -> u32 {
+        const u64 n = word & esc;
+        return n < esc ? (u32)n : esc_get(esc_k, esc_c, esc_cap, word >> csh);
+    };
+    const i64 nwin = (U + WAVE - 1) / WAVE;
+    const i64 wave0 = (blockIdx.x * (i64)blockDim.x + threadIdx.x) / WAVE;
+    const i64 nwaves = ((i64)gridDim.x * blockDim.x) / WAVE;
+    for (i64 wv = wave0; wv < nwin; wv += nwaves) {
+        const i64 i = wv * WAVE + lane;
+        const bool valid = i < U;
+        const u64 word = valid ? w[i] : 0;
+        const u64 ctx = word >> sh;
+        u64 prev = shfl_up_u64(word, 1);
+        if (lane == 0) prev = i > 0 ? w[i - 1] : 0;
+        const bool head = valid && (i == 0 || (prev >> sh) != ctx);
+        const u32 n0 = valid ? count_of(word) : 0u;
+        const u64 sc0 = valid ? rank_score(word >> csh, n0) : 0ull;
+        u64 heads = __ballot(head);
+        while (heads) {
+            const int h = __ffsll((unsigned long long)heads) - 1;
+            heads &= heads - 1;
+            const u64 hc = bcast_u64(ctx, h);
+            const bool in = valid && lane >= h && ctx == hc;
+            const u64 inm = __ballot(in);
+            u32 len = (u32)__popcll(inm);
+            bool cont = ((inm >> (WAVE - 1)) & 1ull) && wv * WAVE + WAVE < U;
+            if (len == 1 && !cont) {  // a single pair: no reduction
+                if (lane == h) {
+                    u64 one[KT];
+                    one[0] = sc0;
+#pragma unroll
+                    for (int r = 1; r < KT; ++r) one[r] = 0;
+                    dist[hc] = 1;
+                    store_record<KT>(rec, hc, n0, 1u, one);
+                }
+                continue;
+            }
+            u64 part = in ? n0 : 0;
+            u64 lt[KT];
+            lt[0] = in ? sc0 : 0;
+#pragma unroll
+            for (int r = 1; r < KT; ++r) lt[r] = 0;
+            for (i64 nx = wv * WAVE + WAVE; cont; nx += WAVE) {
+                const i64 j = nx + lane;
+                const bool v2 = j < U;
+                const u64 w2 = v2 ? w[j] : 0;
+                const bool in2 = v2 && (w2 >> sh) == hc;
+                const u64 m2 = __ballot(in2);
+                if (in2) {
+                    const u32 n = count_of(w2);
+                    part += n;
+                    topk_insert<KT>(lt, rank_score(w2 >> csh, n));
+                }
+                len += (u32)__popcll(m2);
+                cont = ((m2 >> (WAVE - 1)) & 1ull) && nx + WAVE < U;
+            }
+#pragma unroll
+            for (int d = WAVE / 2; d > 0; d >>= 1) part += shfl_down_u64(part, d);
+            part = bcast_u64(part, 0);
+            // merge the lanes' lists: KT rounds of a wave-wide maximum; the lane holding it moves to its next entry
+            // (scores are distinct within a context, so exactly one lane holds a nonzero maximum)
+            int headq = 0;
+            u64 merged[KT];
+#pragma unroll
+            for (int r = 0; r < KT; ++r) {
+                u64 mine = 0;
+#pragma unroll
+                for (int q = 0; q < KT; ++q)
+                    if (q == headq) mine = lt[q];
+                u64 m = mine;
+#pragma unroll
+                for (int d = WAVE / 2; d > 0; d >>= 1) {
+                    const u64 o = shfl_down_u64(m, d);
+                    m = o > m ? o : m;
+                }
+                m = bcast_u64(m, 0);
+                merged[r] = m;
+                if (m != 0 && mine == m) ++headq;
+            }
+            if (lane == h) {
+                dist[hc] = len;
+                store_record<KT>(rec, hc, part, len, merged);
+                if (part >> 32) atomicOr(&flags[0], 4u);
+            }
+        }
+    }
+}
+
+// Per query position i whose context id c is in [lo, hi) and present (dist[c - lo] > 0): from its context's record
+// (ctx_summary_k's) tot, dist (at most 65535), the first kout of ktop top entries; cnt = qcnt[i] (with thr: only if its
+// score reaches thr[c]); mask bit li.
+template <int KT>
+__global__ void __launch_bounds__(256) pos_summary_k(const int* __restrict__ ctx_of, i64 N, i64 lo, i64 hi,
+                                                     const u16* __restrict__ tgt, const u32* __restrict__ rec,
+                                                     const u32* __restrict__ dist, const u64* __restrict__ thr,
+                                                     const u32* __restrict__ qcnt, int kout, int li,
+                                                     int* __restrict__ out_tot, int* __restrict__ out_dist,
+                                                     int* __restrict__ out_cnt, u16* __restrict__ out_tok,
+                                                     u32* __restrict__ out_tcnt, int* __restrict__ mask) {
+    using R = CtxRecord<KT>;
+    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    if (i >= N) return;
+    i64 c = ctx_of[i];
+    if (c < lo || c >= hi) return;
+    c -= lo;
+    const u32 d = dist[c];
+    if (d == 0) return;
+    u32 v[R::WORDS];
+    const uint4* src = (const uint4*)(rec + c * R::WORDS);
+#pragma unroll
+    for (int q = 0; q < R::WORDS / 4; ++q) {
+        const uint4 x = src[q];
+        v[4 * q] = x.x;
+        v[4 * q + 1] = x.y;
+        v[4 * q + 2] = x.z;
+        v[4 * q + 3] = x.w;
+    }
+    out_tot[i] = (int)v[0];
+    out_dist[i] = (int)(d < 65535u ? d : 65535u);
+    const u32 n = qcnt[i];
+    if (n) {
+        const u64 th = thr ? thr[c] : 0;
+        if (th == 0 || rank_score(((u64)c << 16) | tgt[i], n) >= th) out_cnt[i] = (int)n;
+    }
+#pragma unroll
+    for (int r = 0; r < KT; ++r) {
+        if (r < kout) {
+            out_tok[i * kout + r] = (u16)(v[2 + r / 2] >> (16 * (r & 1)));
+            out_tcnt[i * kout + r] = v[2 + R::TOKW + r];
+        }
+    }
+    if (mask) mask[i] |= 1 << li;
 }
 
 }  // namespace
@@ -259,12 +471,55 @@ extern "C" int ng_part_lookups(const int* ctx_of, const u16* tgt, i64 N, i64 lo,
 // bounds) get qcnt[qv[j]] = the pair's count or 0. flags[0] bit 0: a partition held more than 8192 distinct pairs
 // (its count is incomplete: repartition with one more bit).
 extern "C" int ng_part_count(const u64* ev, const i64* start, int pbits, const u64* qk, const u32* qv,
-                             const i64* qstart, u64* out_k, u32* out_c, u32* seg_cnt, i64* seg_base, u32* qcnt,
-                             u32* flags, int grid, void* stream) {
-    if (pbits < 0 || pbits > 24 || grid <= 0) return -1;
+                             const i64* qstart, u64* out_k, u32* out_c, int cb, u64* esc_k, u32* esc_c, u64 esc_cap,
+                             u32* seg_cnt, i64* seg_base, u32* qcnt, u32* flags, int grid, void* stream) {
+    if (pbits < 0 || pbits > 24 || grid <= 0 || cb < 0 || cb > 44) return -1;
+    if (cb > 0 && (esc_k == nullptr || esc_c == nullptr || esc_cap == 0)) return -1;
+    if (cb == 0 && out_c == nullptr) return -1;
     const i64 P = 1ll << pbits;
     const i64 ppb = (P + grid - 1) / grid;
-    part_count_k<<<grid, PT_BLOCK, 0, (hipStream_t)stream>>>(ev, start, P, ppb, qk, qv, qstart, out_k, out_c, seg_cnt,
-                                                             seg_base, qcnt, flags);
+    part_count_k<<<grid, PT_BLOCK, 0, (hipStream_t)stream>>>(ev, start, P, ppb, qk, qv, qstart, out_k, out_c, cb, esc_k,
+                                                             esc_c, esc_cap, seg_cnt, seg_base, qcnt, flags);
+    return (int)hipGetLastError();
+}
+
+// Per context from U packed words (ng_part_count's with cb > 0) sorted by context: dist[c] = its pairs and its record
+// rec[c] (u32 words: total, pairs, the first topk (1, 2, 4, 8) tokens by (count desc, token asc) two per word, their
+// counts; 4, 8, 8, 16 words for topk 1, 2, 4, 8), written for contexts present only (callers zero dist). flags[0]
+// bit 2: a total reached 2^32.
+extern "C" int ng_ctx_summary(const u64* w, i64 U, int cb, const u64* esc_k, const u32* esc_c, u64 esc_cap, int topk,
+                              u32* rec, u32* dist, u32* flags, void* stream) {
+    if (cb <= 0 || cb > 44 || esc_cap == 0) return -1;
+    if (U <= 0) return 0;
+    int g = grid_for((U + WAVE - 1) / WAVE, 4);  // four waves per block, a window each
+    g = g > 65536 ? 65536 : g;
+    hipStream_t st = (hipStream_t)stream;
+    switch (topk) {
+        case 1: ctx_summary_k<1><<<g, 256, 0, st>>>(w, U, cb, esc_k, esc_c, esc_cap, rec, dist, flags); break;
+        case 2: ctx_summary_k<2><<<g, 256, 0, st>>>(w, U, cb, esc_k, esc_c, esc_cap, rec, dist, flags); break;
+        case 4: ctx_summary_k<4><<<g, 256, 0, st>>>(w, U, cb, esc_k, esc_c, esc_cap, rec, dist, flags); break;
+        case 8: ctx_summary_k<8><<<g, 256, 0, st>>>(w, U, cb, esc_k, esc_c, esc_cap, rec, dist, flags); break;
+        default: return -1;
+    }
+    return (int)hipGetLastError();
+}
+
+// Per query position from the per-context records and pair counts (ng_ctx_summary's) and the counted lookups qcnt: tot,
+// dist, cnt (thr may be NULL: the CNT_TOP threshold scores), the first kout <= ktop top entries, mask bit li (mask may
+// be NULL).
+extern "C" int ng_pos_summary(const int* ctx_of, i64 N, i64 lo, i64 hi, const u16* tgt, const u32* rec, const u32* dist,
+                              const u64* thr, const u32* qcnt, int ktop, int kout, int li, int* out_tot, int* out_dist,
+                              int* out_cnt, u16* out_tok, u32* out_tcnt, int* mask, void* stream) {
+    if (kout < 0 || kout > ktop || (mask && (li < 0 || li > 30))) return -1;
+    if (N <= 0) return 0;
+    const int g = grid_for(N, 256);
+    hipStream_t st = (hipStream_t)stream;
+    switch (ktop) {
+        case 1: pos_summary_k<1><<<g, 256, 0, st>>>(ctx_of, N, lo, hi, tgt, rec, dist, thr, qcnt, kout, li, out_tot, out_dist, out_cnt, out_tok, out_tcnt, mask); break;
+        case 2: pos_summary_k<2><<<g, 256, 0, st>>>(ctx_of, N, lo, hi, tgt, rec, dist, thr, qcnt, kout, li, out_tot, out_dist, out_cnt, out_tok, out_tcnt, mask); break;
+        case 4: pos_summary_k<4><<<g, 256, 0, st>>>(ctx_of, N, lo, hi, tgt, rec, dist, thr, qcnt, kout, li, out_tot, out_dist, out_cnt, out_tok, out_tcnt, mask); break;
+        case 8: pos_summary_k<8><<<g, 256, 0, st>>>(ctx_of, N, lo, hi, tgt, rec, dist, thr, qcnt, kout, li, out_tot, out_dist, out_cnt, out_tok, out_tcnt, mask); break;
+        default: return -1;
+    }
     return (int)hipGetLastError();
 }

@@ -51,6 +51,8 @@ EMIT_CHUNK = 1 << 28  # emitted keys held before a flush (at least one shard's p
 # PART_BLOCKS blocks of consecutive partitions.
 PART_TARGET = 4096
 PART_BLOCKS = 2048
+ESC_CAP = 1 << 20  # packed pairs whose count exceeds the word's count field (none at c3), per level
+PACK_MIN_BITS = 0  # context-id bits of the packed words at least this (up to 44: a narrower count field)
 
 
 def emit_region(L: int, grid: int) -> int:
@@ -395,7 +397,7 @@ class CountBuild:
             w = torch.where(top > 32767, (tc * 32767 + top - 1) // top, tc)
             row_entries[ri, at] = torch.where(tc > 0, tt | (w.to(torch.int32) << 16), 0)
             row_top[ri, at] = tc[:, 0].clamp_max((1 << 31) - 1).to(torch.int32)
-        if vi.ids and int(tot.max().item()) >= 1 << 32:
+        if tot is not None and vi.ids and int(tot.max().item()) >= 1 << 32:
             raise RuntimeError(f"k={k}: a total does not fit uint32")
 
     def _counts_part(self, index, tgt, N, lap) -> torch.Tensor:
@@ -423,13 +425,24 @@ class CountBuild:
             t0 = time.perf_counter()
             ev, n_ev = self._part_emit(k, vi, bms, regions, R)
             t1 = time.perf_counter()
-            ck, cc, qcnt, U, pbits = self._part_count(k, vi, ev, n_ev, tgt)
-            del ev
+            # pairs packed with their counts in one word (keys-only sorts) while the context ids leave room for them
+            cb = max(1, (max(vi.ids, 2) - 1).bit_length(), PACK_MIN_BITS)
+            res = self._part_count(k, vi, ev, n_ev, tgt, cb)
+            if res is None:  # too many counts beyond the packed field: the level again, unpacked
+                cb = 0
+                res = self._part_count(k, vi, ev, n_ev, tgt, 0)
+            ck, cc, qcnt, U, pbits = res
+            del ev, res
             t2 = time.perf_counter()
             scan_t += t1 - t0
             count_t += t2 - t1
             want = max(self.topk, ROW_K if (rows and k in ROW_LEVELS) else 0)
-            tot, top_tok, top_cnt, want = self._owner(li, k, vi, ck, cc, U, tgt, out, want, qcnt=qcnt)
+            if cb:
+                tot, top_tok, top_cnt, want = self._owner_packed(li, k, vi, ck, cc, U, cb, tgt, out, want, qcnt,
+                                                                 rows and k in ROW_LEVELS)
+            else:
+                tot, top_tok, top_cnt, want = self._owner(li, k, vi, ck, cc, U, tgt, out, want, qcnt=qcnt)
+            del ck, cc
             self._level_rows(k, vi, want, tot, top_tok, top_cnt, row_entries, row_top)
             info[k] = dict(contexts=vi.n, ids=vi.ids, pairs=U, events=n_ev, pbits=pbits, cap=0, hits=None, reruns=0)
             del tot, top_tok, top_cnt, vi, qcnt
@@ -485,10 +498,12 @@ class CountBuild:
         e1.record()
         return ev, n_ev
 
-    def _part_count(self, k, vi, ev, n_ev, tgt):
+    def _part_count(self, k, vi, ev, n_ev, tgt, cb):
         """Level k's events counted: hash-partitioned (a radix sort of the mixed keys by their top pbits), then an LDS
         count per partition with the query positions' lookups; a partition with too many distinct pairs repeats the
-        level with one more bit. Returns (pair keys, counts, per-position target counts, pairs, pbits)."""
+        level with one more bit. Returns (pair keys, counts, per-position target counts, pairs, pbits); with cb > 0
+        (context ids below 2^cb) the pairs come as packed words and "counts" is the escape table (keys, counts) of
+        those too large for the word, or None if that table overflowed."""
         elib, lib, dev = self.elib, self.lib, self.tok.device
         N = vi.ctx_of.numel()
         ratio = self.dratio.get(k, 1.0)
@@ -517,18 +532,23 @@ class CountBuild:
             e1.record()
             G2 = min(P, PART_BLOCKS)
             out_k = torch.empty(max(n_ev, 1), dtype=torch.int64, device=dev)
-            out_c = torch.empty(max(n_ev, 1), dtype=torch.int32, device=dev)
+            out_c = None if cb else torch.empty(max(n_ev, 1), dtype=torch.int32, device=dev)
+            esc_k = torch.full((ESC_CAP,), -1, dtype=torch.int64, device=dev) if cb else None
+            esc_c = torch.empty(ESC_CAP, dtype=torch.int32, device=dev) if cb else None
             seg_cnt = torch.empty(G2, dtype=torch.int32, device=dev)
             seg_base = torch.empty(G2, dtype=torch.int64, device=dev)
             qcnt = torch.zeros(max(N, 1), dtype=torch.int32, device=dev)
             flags = torch.zeros(1, dtype=torch.int32, device=dev)
             e0, e1 = self._event("count", k, -1, n_ev)
             e0.record()
-            elib("ng_part_count", sev, start, i32(pbits), sqk, sqv, qstart, out_k, out_c, seg_cnt, seg_base, qcnt, flags,
-                 i32(G2))
+            elib("ng_part_count", sev, start, i32(pbits), sqk, sqv, qstart, out_k, out_c, i32(cb), esc_k, esc_c,
+                 u64(ESC_CAP if cb else 0), seg_cnt, seg_base, qcnt, flags, i32(G2))
             e1.record()
             del sev, sqk, sqv, start, qstart
-            if not int(flags[0].item()) & 1:
+            fl = int(flags[0].item())
+            if fl & 2:
+                return None
+            if not fl & 1:
                 break
             if pbits >= 24:
                 raise RuntimeError(f"k={k}: a partition holds too many distinct pairs at 24 bits")
@@ -537,13 +557,53 @@ class CountBuild:
         elib("ng_seg_offsets", seg_cnt, G2, offs)
         U = int(offs[G2].item())
         ck = torch.empty(max(U, 1), dtype=torch.int64, device=dev)
-        cc = torch.empty(max(U, 1), dtype=torch.int32, device=dev)
+        cc = None if cb else torch.empty(max(U, 1), dtype=torch.int32, device=dev)
         e0, e1 = self._event("count", k, -1, U)
         e0.record()
         elib("ng_seg_gather", out_k, out_c, u64(0), seg_base, seg_cnt, G2, offs, ck, cc)
         e1.record()
         self.dratio[k] = U / max(1, n_ev)
-        return ck, cc, qcnt, U, pbits
+        return ck, ((esc_k, esc_c) if cb else cc), qcnt, U, pbits
+
+    def _owner_packed(self, li, k, vi, words, esc, U, cb, tgt, out, want, qcnt, zero_tops):
+        """The owner side from packed words: a keys-only sort by context, then per-context totals, pair counts and top
+        entries straight from the sorted words (only present contexts are written: dist is zeroed, the tops too when
+        rows read every context's), then per query position its context's summary and counted target."""
+        elib, lib, dev = self.elib, self.lib, self.tok.device
+        N, n_own = vi.ctx_of.numel(), vi.ids
+        sw = torch.empty(max(U, 1), dtype=torch.int64, device=dev)
+        e0, e1 = self._event("sort", k, -1, U)
+        e0.record()
+        if U:
+            lib.cub("sort_pairs", words, sw, None, None, U, i32(64 - cb), i32(64))
+        e1.record()
+        del words
+        ktop = 1 if want <= 1 else 2 if want <= 2 else 4 if want <= 4 else 8
+        words_per = {1: 4, 2: 8, 4: 8, 8: 16}[ktop]
+        tokw = (ktop + 1) // 2
+        # per context: its record (total, pairs, top tokens two per word, top counts) and its pair count (zeroed: the
+        # contexts the corpus never showed read 0); the records are zeroed too when rows read every context's
+        rec = (torch.zeros if zero_tops else torch.empty)((n_own, words_per), dtype=torch.int32, device=dev)
+        dist = torch.zeros(n_own, dtype=torch.int32, device=dev)
+        flags = torch.zeros(1, dtype=torch.int32, device=dev)
+        e0, e1 = self._event("ctx_topk", k, -1, U)
+        e0.record()
+        elib("ng_ctx_summary", sw, U, i32(cb), esc[0], esc[1], u64(ESC_CAP), i32(ktop), rec, dist, flags)
+        e1.record()
+        e0, e1 = self._event("pos_gather", k, -1, N)
+        e0.record()
+        kout = self.topk
+        elib("ng_pos_summary", vi.ctx_of, N, 0, n_own, tgt, rec, dist, None, qcnt, i32(ktop), i32(kout), i32(li),
+             out[0, li], out[1, li], out[2, li], self.top_tok[li] if kout else None,
+             self.top_cnt[li] if kout else None, None)
+        e1.record()
+        if int(flags[0].item()) & 4:
+            raise RuntimeError(f"k={k}: a total does not fit uint32")
+        top_tok = top_cnt = None
+        if zero_tops:
+            top_tok = rec[:, 2 : 2 + tokw].contiguous().view(torch.int16)
+            top_cnt = rec[:, 2 + tokw : 2 + tokw + ktop].contiguous()
+        return None, top_tok, top_cnt, ktop
 
     def _outputs_engine(self, li, k, vi, t, tgt, out, want):
         """One level's outputs with the engine: the split table compacted, its pairs sorted by context, per-context

@@ -43,7 +43,8 @@ def _partition_small_tables(monkeypatch):
                                                ({2: 1, 3: 2}, "engine-compact"), ({}, "record"),
                                                ({2: 1, 3: 2}, "record"), ({}, "partitioned"),
                                                ({2: 1, 3: 2}, "partitioned"), ({}, "part"), ({2: 1, 3: 2}, "part"),
-                                               ({}, "part-compact"), ({2: 1, 3: 2}, "part-regroup")])
+                                               ({}, "part-compact"), ({2: 1, 3: 2}, "part-regroup"),
+                                               ({}, "part-escape"), ({}, "part-unpacked")])
 def test_counts_match_oracle(corpus, level_shards, mode, monkeypatch):
     if mode == "partitioned":
         _partition_small_tables(monkeypatch)
@@ -52,6 +53,12 @@ def test_counts_match_oracle(corpus, level_shards, mode, monkeypatch):
         # three blocks, each counting a run of partitions
         monkeypatch.setattr(C, "PART_TARGET", 1 << 30)
         monkeypatch.setattr(C, "PART_BLOCKS", 3)
+    if mode in ("part-escape", "part-unpacked"):
+        # an 8-bit count field: counts of 255 and more go to the escape table; with a 4-slot table it overflows and
+        # every level is counted again unpacked
+        monkeypatch.setattr(C, "PACK_MIN_BITS", 40)
+        if mode == "part-unpacked":
+            monkeypatch.setattr(C, "ESC_CAP", 4)
     lib = C.record_lib()
     cb = C.CountBuild(corpus.shards(), levels=LEVELS, level_shards=level_shards, topk=4)
     cb.mode = mode.split("-")[0]
