@@ -251,14 +251,6 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
     }
 }
 
-// Per context from packed words sorted by context (word >> (64 - cb)): a wave per window of 64 words. For each context
-// starting in its window (a lane whose word's context differs from the previous word's), the wave takes the context's
-// lanes (a run: the words are sorted), and while the run reaches the window's end, the next windows' leading lanes of
-// the same context; counts summed and the top KT kept per lane, then reduced across the wave. No dependent loads:
-// every word is read by its own window and at most once more by the window of its context's first word. For present
-// contexts only: dist[c] = its pairs, and its record rec[c] (rec_words(KT) u32: total, pairs, the first KT tokens by
-// (count desc, token asc) two per word, their counts; 0-padded), stored whole as 16-byte vectors; flags[0] bit 2 if a
-// total reaches 2^32.
 template <int KT>
 struct CtxRecord {
     static constexpr int TOKW = (KT + 1) / 2;
@@ -285,56 +277,79 @@ __device__ __forceinline__ void store_record(u32* __restrict__ rec, u64 c, u64 t
     for (int q = 0; q < R::WORDS / 4; ++q) dst[q] = make_uint4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
 }
 
+// Per context from packed words sorted by context (word >> (64 - cb)): a wave per window of 64 words, staged in LDS.
+// A lane holding a context's first word whose context also ends in the window walks it in LDS alone (every such lane
+// at once); the one context that runs past the window's end, if it starts there, is done by the whole wave over the
+// following windows' leading words, counts summed and the top KT kept per lane, then reduced across the wave. No
+// dependent global loads: every word is read by its own window and at most once more by the window of its context's
+// first word. For present contexts only: dist[c] = its pairs, and its record rec[c] (CtxRecord<KT>::WORDS u32: total,
+// pairs, the first KT tokens by (count desc, token asc) two per word, their counts; 0-padded), stored whole as 16-byte
+// vectors; flags[0] bit 2 if a total reaches 2^32.
 template <int KT>
 __global__ void __launch_bounds__(256) ctx_summary_k(const u64* __restrict__ w, i64 U, int cb,
                                                      const u64* __restrict__ esc_k, const u32* __restrict__ esc_c,
                                                      u64 esc_cap, u32* __restrict__ rec, u32* __restrict__ dist,
                                                      u32* flags) {
+    __shared__ u64 sw[4][WAVE];
     const int sh = 64 - cb, csh = 48 - cb;
     const u64 esc = (1ull << csh) - 1;
-    const int lane = lane_id();
+    const int lane = lane_id(), wid = threadIdx.x / WAVE;
     auto count_of = [&](u64 word) -> u32 {
         const u64 n = word & esc;
         return n < esc ? (u32)n : esc_get(esc_k, esc_c, esc_cap, word >> csh);
     };
     const i64 nwin = (U + WAVE - 1) / WAVE;
-    const i64 wave0 = (blockIdx.x * (i64)blockDim.x + threadIdx.x) / WAVE;
-    const i64 nwaves = ((i64)gridDim.x * blockDim.x) / WAVE;
-    for (i64 wv = wave0; wv < nwin; wv += nwaves) {
+    for (i64 wb = (i64)blockIdx.x * 4; wb < nwin; wb += (i64)gridDim.x * 4) {  // the same rounds for the block's waves
+        const i64 wv = wb + wid;
         const i64 i = wv * WAVE + lane;
         const bool valid = i < U;
         const u64 word = valid ? w[i] : 0;
         const u64 ctx = word >> sh;
+        sw[wid][lane] = word;
         u64 prev = shfl_up_u64(word, 1);
-        if (lane == 0) prev = i > 0 ? w[i - 1] : 0;
+        if (lane == 0) prev = (valid && i > 0) ? w[i - 1] : 0;
+        u64 next = shfl_down_u64(word, 1);
+        if (lane == WAVE - 1) next = i + 1 < U ? w[i + 1] : 0;
         const bool head = valid && (i == 0 || (prev >> sh) != ctx);
-        const u32 n0 = valid ? count_of(word) : 0u;
-        const u64 sc0 = valid ? rank_score(word >> csh, n0) : 0ull;
-        u64 heads = __ballot(head);
-        while (heads) {
-            const int h = __ffsll((unsigned long long)heads) - 1;
-            heads &= heads - 1;
-            const u64 hc = bcast_u64(ctx, h);
-            const bool in = valid && lane >= h && ctx == hc;
-            const u64 inm = __ballot(in);
-            u32 len = (u32)__popcll(inm);
-            bool cont = ((inm >> (WAVE - 1)) & 1ull) && wv * WAVE + WAVE < U;
-            if (len == 1 && !cont) {  // a single pair: no reduction
-                if (lane == h) {
-                    u64 one[KT];
-                    one[0] = sc0;
+        const bool tail = valid && (i + 1 >= U || (next >> sh) != ctx);
+        const u64 tails = __ballot(tail);
+        __syncthreads();
+        if (head) {
+            const u64 after = tails >> lane;  // this lane's context ends at the first tail from here, if any
+            if (after) {
+                const int e = lane + __ffsll((unsigned long long)after) - 1;  // its last word's lane
+                u64 tl[KT];
 #pragma unroll
-                    for (int r = 1; r < KT; ++r) one[r] = 0;
-                    dist[hc] = 1;
-                    store_record<KT>(rec, hc, n0, 1u, one);
+                for (int r = 0; r < KT; ++r) tl[r] = 0;
+                u64 s = 0;
+                for (int j = lane; j <= e; ++j) {
+                    const u64 wj = sw[wid][j];
+                    const u32 n = count_of(wj);
+                    s += n;
+                    topk_insert<KT>(tl, rank_score(wj >> csh, n));
                 }
-                continue;
+                dist[ctx] = (u32)(e - lane + 1);
+                store_record<KT>(rec, ctx, s, (u32)(e - lane + 1), tl);
+                if (s >> 32) atomicOr(&flags[0], 4u);
             }
-            u64 part = in ? n0 : 0;
+        }
+        // the context running past the window, when it starts in it: the whole wave
+        const bool open = head && !(tails >> lane);
+        const u64 opens = __ballot(open);
+        if (opens) {
+            const int h = __ffsll((unsigned long long)opens) - 1;
+            const u64 hc = bcast_u64(ctx, h);
+            const bool in = valid && lane >= h;
+            u64 part = 0;
             u64 lt[KT];
-            lt[0] = in ? sc0 : 0;
 #pragma unroll
-            for (int r = 1; r < KT; ++r) lt[r] = 0;
+            for (int r = 0; r < KT; ++r) lt[r] = 0;
+            if (in) {
+                part = count_of(word);
+                lt[0] = rank_score(word >> csh, (u32)part);
+            }
+            u32 len = (u32)(WAVE - h);
+            bool cont = true;
             for (i64 nx = wv * WAVE + WAVE; cont; nx += WAVE) {
                 const i64 j = nx + lane;
                 const bool v2 = j < U;
@@ -378,6 +393,7 @@ __global__ void __launch_bounds__(256) ctx_summary_k(const u64* __restrict__ w, 
                 if (part >> 32) atomicOr(&flags[0], 4u);
             }
         }
+        __syncthreads();  // the window's staged words are read before the next round writes them
     }
 }
 
@@ -491,7 +507,7 @@ extern "C" int ng_ctx_summary(const u64* w, i64 U, int cb, const u64* esc_k, con
                               u32* rec, u32* dist, u32* flags, void* stream) {
     if (cb <= 0 || cb > 44 || esc_cap == 0) return -1;
     if (U <= 0) return 0;
-    int g = grid_for((U + WAVE - 1) / WAVE, 4);  // four waves per block, a window each
+    int g = grid_for((U + WAVE - 1) / WAVE, 4);  // four waves per block, a window each per round
     g = g > 65536 ? 65536 : g;
     hipStream_t st = (hipStream_t)stream;
     switch (topk) {
