@@ -313,6 +313,12 @@ __global__ void __launch_bounds__(256) ctx_summary_k(const u64* __restrict__ w, 
         const bool head = valid && (i == 0 || (prev >> sh) != ctx);
         const bool tail = valid && (i + 1 >= U || (next >> sh) != ctx);
         const u64 tails = __ballot(tail);
+        // the context running past the window, when it starts in it: its next window is loaded now, so that the
+        // load overlaps the lanes' walks below
+        const bool open = head && !(tails >> lane);
+        const u64 opens = __ballot(open);
+        u64 ahead = 0;
+        if (opens && wv * WAVE + WAVE + lane < U) ahead = w[wv * WAVE + WAVE + lane];
         __syncthreads();
         if (head) {
             const u64 after = tails >> lane;  // this lane's context ends at the first tail from here, if any
@@ -333,9 +339,7 @@ __global__ void __launch_bounds__(256) ctx_summary_k(const u64* __restrict__ w, 
                 if (s >> 32) atomicOr(&flags[0], 4u);
             }
         }
-        // the context running past the window, when it starts in it: the whole wave
-        const bool open = head && !(tails >> lane);
-        const u64 opens = __ballot(open);
+        // the context running past the window: the whole wave, over the following windows
         if (opens) {
             const int h = __ffsll((unsigned long long)opens) - 1;
             const u64 hc = bcast_u64(ctx, h);
@@ -353,7 +357,7 @@ __global__ void __launch_bounds__(256) ctx_summary_k(const u64* __restrict__ w, 
             for (i64 nx = wv * WAVE + WAVE; cont; nx += WAVE) {
                 const i64 j = nx + lane;
                 const bool v2 = j < U;
-                const u64 w2 = v2 ? w[j] : 0;
+                const u64 w2 = !v2 ? 0 : nx == wv * WAVE + WAVE ? ahead : w[j];
                 const bool in2 = v2 && (w2 >> sh) == hc;
                 const u64 m2 = __ballot(in2);
                 if (in2) {

@@ -51,6 +51,7 @@ EMIT_CHUNK = 1 << 28  # emitted keys held before a flush (at least one shard's p
 # PART_BLOCKS blocks of consecutive partitions.
 PART_TARGET = 4096
 PART_BLOCKS = 2048
+PART_MIN_BITS = 11
 ESC_CAP = 1 << 20  # packed pairs whose count exceeds the word's count field (none at c3), per level
 PACK_MIN_BITS = 0  # context-id bits of the packed words at least this (up to 44: a narrower count field)
 
@@ -507,7 +508,8 @@ class CountBuild:
         elib, lib, dev = self.elib, self.lib, self.tok.device
         N = vi.ctx_of.numel()
         ratio = self.dratio.get(k, 1.0)
-        pbits = max(0, min(24, math.ceil(math.log2(max(1.0, n_ev * ratio / PART_TARGET)))))
+        # at least PART_MIN_BITS: every level gets enough partitions (blocks) for its N lookups as well
+        pbits = max(min(PART_MIN_BITS, 24), min(24, math.ceil(math.log2(max(1.0, n_ev * ratio / PART_TARGET)))))
         qk = torch.empty(N, dtype=torch.int64, device=dev)
         qv = torch.empty(N, dtype=torch.int32, device=dev)
         e0, e1 = self._event("partition", k, -1, N)

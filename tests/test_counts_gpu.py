@@ -52,6 +52,7 @@ def test_counts_match_oracle(corpus, level_shards, mode, monkeypatch):
         # one partition per level to start with: each level's LDS table overflows and it is repartitioned bit by bit;
         # three blocks, each counting a run of partitions
         monkeypatch.setattr(C, "PART_TARGET", 1 << 30)
+        monkeypatch.setattr(C, "PART_MIN_BITS", 0)
         monkeypatch.setattr(C, "PART_BLOCKS", 3)
     if mode in ("part-escape", "part-unpacked"):
         # an 8-bit count field: counts of 255 and more go to the escape table; with a 4-slot table it overflows and
