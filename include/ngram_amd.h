@@ -136,11 +136,12 @@ int ng_pos_gather(const int* ctx_of, ng_i64 N, ng_i64 lo, ng_i64 hi, const uint1
                   int* out_dist, int* out_cnt, uint16_t* out_tok, uint32_t* out_tcnt, int* mask, void* stream);
 /* query index without a sort (replaces gpu_val_stats.py:604-651's sort-based one where ids need not agree across
  * ranks): valid k-contexts of positions pos[0..n) (NULL: 0..n) inserted by compare-and-swap into table (cap + tail
- * slots, EMPTY-filled, linear probing without wrap from umulhi(key, cap)); ctx_of[i] = slot or -1, rep[slot] = the
+ * slots, EMPTY-filled, linear probing without wrap from umulhi(key, cap)); ctx_of[i] = slot or -1 (compact:
+ * ctx_of[j] for pos[j]), rep[slot] = the
  * inserting position; counters[0] += the table's occupied slots afterwards, counters[1] = 1 on reaching the table's end, counters[2] += key
  * collisions found against the representative (k > 4) */
 int ng_query_index(const uint16_t* x, const int* avail, const int* pos, ng_i64 n, int k, ng_u64* table, ng_u64 cap,
-                   ng_u64 slots, uint32_t* rep, int* ctx_of, ng_u64* counters, void* stream);
+                   ng_u64 slots, uint32_t* rep, int* ctx_of, int compact, ng_u64* counters, void* stream);
 /* move a query index into a smaller EMPTY-filled table (cap + tail = slots): ctx_of[0..n) re-pointed, remap
  * (old_slots ints) scratch, counters[1] = 1 on reaching the new table's end */
 int ng_query_index_shrink(const ng_u64* old_t, const uint32_t* old_rep, ng_u64 old_slots, ng_u64* table, ng_u64 cap,
@@ -170,9 +171,9 @@ int ng_part_count(const ng_u64* ev, const ng_i64* start, int pbits, const ng_u64
  * counts (4, 8, 8, 16 words for topk 1, 2, 4, 8); flags[0] bit 2: a total reached 2^32 */
 int ng_ctx_summary(const ng_u64* w, ng_i64 U, int cb, const ng_u64* esc_k, const uint32_t* esc_c, ng_u64 esc_cap,
                    int topk, uint32_t* rec, uint32_t* dist, uint32_t* flags, void* stream);
-/* per query position from ng_ctx_summary's records and pair counts and the counted lookups qcnt: tot, dist, cnt
- * (thr: the CNT_TOP threshold scores, may be NULL), the first kout of ktop top entries, mask bit li (mask may be
- * NULL) */
+/* per query position from ng_ctx_summary's records and pair counts and the counted lookups qcnt (may be NULL: no
+ * cnt): tot, dist, cnt (thr: the CNT_TOP threshold scores, may be NULL), the first kout of ktop top entries, mask bit
+ * li (mask may be NULL) */
 int ng_pos_summary(const int* ctx_of, ng_i64 N, ng_i64 lo, ng_i64 hi, const uint16_t* tgt, const uint32_t* rec,
                    const uint32_t* dist, const ng_u64* thr, const uint32_t* qcnt, int ktop, int kout, int li,
                    int* out_tot, int* out_dist, int* out_cnt, uint16_t* out_tok, uint32_t* out_tcnt, int* mask,

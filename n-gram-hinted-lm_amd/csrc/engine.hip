@@ -600,7 +600,7 @@ namespace {
 template <int K>
 __global__ void qindex_insert_k(const u16* __restrict__ x, const int* __restrict__ avail, const int* __restrict__ pos,
                                 i64 n, int k, u64* table, u64 cap, u64 slots, u32* rep, int* __restrict__ ctx_of,
-                                u64* counters) {
+                                int compact, u64* counters) {
     const i64 j = blockIdx.x * (i64)blockDim.x + threadIdx.x;
     if (j < n) {
         const i64 i = pos ? pos[j] : j;
@@ -633,7 +633,8 @@ __global__ void qindex_insert_k(const u16* __restrict__ x, const int* __restrict
                 ++s;
             }
         }
-        if (slot >= 0 || !pos) ctx_of[i] = (int)slot;
+        if (compact) ctx_of[j] = (int)slot;
+        else if (slot >= 0 || !pos) ctx_of[i] = (int)slot;
     }
 }
 
@@ -686,11 +687,11 @@ __global__ void qindex_remap_k(int* __restrict__ ctx_of, i64 n, const int* __res
 
 // Hashed contexts (k > 4): each position's k tokens against its slot's representative's; mismatches into *bad.
 __global__ void qindex_verify_k(const u16* __restrict__ x, const int* __restrict__ pos, i64 n, int k,
-                                const int* __restrict__ ctx_of, const u32* __restrict__ rep, u64* bad) {
+                                const int* __restrict__ ctx_of, int compact, const u32* __restrict__ rep, u64* bad) {
     const i64 j = blockIdx.x * (i64)blockDim.x + threadIdx.x;
     if (j >= n) return;
     const i64 i = pos ? pos[j] : j;
-    const int s = ctx_of[i];
+    const int s = ctx_of[compact ? j : i];
     if (s < 0) return;
     const i64 r = rep[s];
     for (int t = 0; t < k; ++t)
@@ -716,18 +717,19 @@ extern "C" int ng_query_index_shrink(const u64* old_t, const u32* old_rep, u64 o
 }
 
 // Insert the valid query contexts of positions pos[0..n) (pos NULL: 0..n) into table (cap + tail slots, EMPTY-filled):
-// ctx_of[i] = slot (-1 where invalid; with pos, only listed positions are written), rep[slot] = the position that
-// inserted it.
+// ctx_of[i] = slot (-1 where invalid; with pos, only listed positions are written; compact: ctx_of[j] for pos[j],
+// n entries), rep[slot] = the position that inserted it.
 // counters[0] += the table's occupied slots afterwards (its contexts), counters[1] = 1 if the probes ran into the
 // table's end; with k > 4, counters[2] += positions whose tokens differ from their slot's representative (a 64-bit
 // key collision).
 extern "C" int ng_query_index(const u16* x, const int* avail, const int* pos, i64 n, int k, u64* table, u64 cap,
-                              u64 slots, u32* rep, int* ctx_of, u64* counters, void* stream) {
+                              u64 slots, u32* rep, int* ctx_of, int compact, u64* counters,
+                              void* stream) {
     if (n <= 0) return 0;
     if (cap == 0 || slots <= cap || slots > (1ull << 31)) return -1;
     hipStream_t st = (hipStream_t)stream;
-    LEVEL_SWITCH(k, (qindex_insert_k<K><<<grid_for(n, 256), 256, 0, st>>>(x, avail, pos, n, k, table, cap, slots, rep, ctx_of, counters)));
-    if (k > 4) qindex_verify_k<<<grid_for(n, 256), 256, 0, st>>>(x, pos, n, k, ctx_of, rep, counters + 2);
+    LEVEL_SWITCH(k, (qindex_insert_k<K><<<grid_for(n, 256), 256, 0, st>>>(x, avail, pos, n, k, table, cap, slots, rep, ctx_of, compact, counters)));
+    if (k > 4) qindex_verify_k<<<grid_for(n, 256), 256, 0, st>>>(x, pos, n, k, ctx_of, compact, rep, counters + 2);
     const int g = grid_for((i64)slots, 256);
     count_occupied_k<<<g < 1024 ? g : 1024, 256, 0, st>>>(table, slots, counters);
     return (int)hipGetLastError();

@@ -432,7 +432,7 @@ __global__ void __launch_bounds__(256) pos_summary_k(const int* __restrict__ ctx
     }
     out_tot[i] = (int)v[0];
     out_dist[i] = (int)(d < 65535u ? d : 65535u);
-    const u32 n = qcnt[i];
+    const u32 n = qcnt ? qcnt[i] : 0u;
     if (n) {
         const u64 th = thr ? thr[c] : 0;
         if (th == 0 || rank_score(((u64)c << 16) | tgt[i], n) >= th) out_cnt[i] = (int)n;

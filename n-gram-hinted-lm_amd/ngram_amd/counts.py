@@ -16,7 +16,6 @@ all-to-all and all-reduce of a multi-GPU build are not part of this build."""
 
 from __future__ import annotations
 
-import math
 import time
 
 import numpy as np
@@ -27,6 +26,7 @@ from .data import BOS, HEADER_BYTES, shard_tokens
 from .gpu_val_stats import PAIRS as GVS_PAIRS
 from .gpu_val_stats import ValIndex, layout
 from .lib import Lib, i32, u64
+from .partcount import count_events, emit_region, pack_events, record_tops, summarize
 from .qindex import QueryIndex
 
 GAP = 32
@@ -47,21 +47,6 @@ ROW_PURITIES = (0.3, 0.5, 0.7, 0.85, 0.95)
 SUB_BYTES = 64 << 20
 PART_MIN_BYTES = 128 << 20
 EMIT_CHUNK = 1 << 28  # emitted keys held before a flush (at least one shard's positions)
-# "part" mode: partitions sized for about PART_TARGET distinct pairs each (the LDS table holds 8192), counted by
-# PART_BLOCKS blocks of consecutive partitions.
-PART_TARGET = 4096
-PART_BLOCKS = 2048
-PART_MIN_BITS = 11
-ESC_CAP = 1 << 20  # packed pairs whose count exceeds the word's count field (none at c3), per level
-PACK_MIN_BITS = 0  # context-id bits of the packed words at least this (up to 44: a narrower count field)
-
-
-def emit_region(L: int, grid: int) -> int:
-    """The per-block region an emitting scan of L positions with `grid` blocks needs (ng_emit_region)."""
-    per = grid * 8192
-    return -(-L // per) * 8192
-
-
 def record_lib() -> Lib:
     """The record flavour of the library (its scan_level, part_*, rank_scatter and pos_outputs signatures)."""
     return Lib(lib_path(RECORD_LIB_NAME))
@@ -426,27 +411,25 @@ class CountBuild:
             t0 = time.perf_counter()
             ev, n_ev = self._part_emit(k, vi, bms, regions, R)
             t1 = time.perf_counter()
-            # pairs packed with their counts in one word (keys-only sorts) while the context ids leave room for them
-            cb = max(1, (max(vi.ids, 2) - 1).bit_length(), PACK_MIN_BITS)
-            res = self._part_count(k, vi, ev, n_ev, tgt, cb)
-            if res is None:  # too many counts beyond the packed field: the level again, unpacked
-                cb = 0
-                res = self._part_count(k, vi, ev, n_ev, tgt, 0)
-            ck, cc, qcnt, U, pbits = res
-            del ev, res
+            ev_fn = lambda name, n, k=k: self._event(name, k, -1, n)  # noqa: E731
+            c = count_events(self.elib, self.lib, ev, n_ev, vi.ids, self.dratio.get(k, 1.0), (vi.ctx_of, tgt),
+                             event=ev_fn)
+            del ev
+            self.dratio[k] = c.U / max(1, n_ev)
             t2 = time.perf_counter()
             scan_t += t1 - t0
             count_t += t2 - t1
             want = max(self.topk, ROW_K if (rows and k in ROW_LEVELS) else 0)
-            if cb:
-                tot, top_tok, top_cnt, want = self._owner_packed(li, k, vi, ck, cc, U, cb, tgt, out, want, qcnt,
+            if c.cb:
+                tot, top_tok, top_cnt, want = self._owner_packed(li, k, vi, c, tgt, out, want,
                                                                  rows and k in ROW_LEVELS)
-            else:
-                tot, top_tok, top_cnt, want = self._owner(li, k, vi, ck, cc, U, tgt, out, want, qcnt=qcnt)
-            del ck, cc
+            else:  # pairs unpacked (more large counts than the escape table held)
+                tot, top_tok, top_cnt, want = self._owner(li, k, vi, c.pairs, c.counts, c.U, tgt, out, want,
+                                                          qcnt=c.qcnt)
             self._level_rows(k, vi, want, tot, top_tok, top_cnt, row_entries, row_top)
-            info[k] = dict(contexts=vi.n, ids=vi.ids, pairs=U, events=n_ev, pbits=pbits, cap=0, hits=None, reruns=0)
-            del tot, top_tok, top_cnt, vi, qcnt
+            info[k] = dict(contexts=vi.n, ids=vi.ids, pairs=c.U, events=n_ev, pbits=c.pbits, cap=0, hits=None,
+                           reruns=0)
+            del tot, top_tok, top_cnt, vi, c
         del regions
         if self.stats:
             for k in self.levels:
@@ -484,127 +467,30 @@ class CountBuild:
                  self.x, regions[j * G * R :], u64(R), ev_count[j * G :], flags, i32(G),
                  i32(self._scan_mode(si, scanned)))
             e1.record()
-        offs = torch.empty(nseg + 1, dtype=torch.int64, device=dev)
-        e0, e1 = self._event("gather", k, -1, 0)
-        e0.record()
-        elib("ng_seg_offsets", ev_count, nseg, offs)
-        e1.record()
-        n_ev = int(offs[nseg].item())
         if int(flags[0].item()) & 4:
             raise RuntimeError(f"k={k}: an emit region overflowed")
-        ev = torch.empty(max(n_ev, 1), dtype=torch.int64, device=dev)
-        e0, e1 = self._event("gather", k, -1, n_ev)
-        e0.record()
-        elib("ng_seg_gather", regions, None, u64(R), None, ev_count, nseg, offs, ev, None)
-        e1.record()
-        return ev, n_ev
+        return pack_events(elib, regions, R, ev_count, nseg, lambda name, n: self._event(name, k, -1, n))
 
-    def _part_count(self, k, vi, ev, n_ev, tgt, cb):
-        """Level k's events counted: hash-partitioned (a radix sort of the mixed keys by their top pbits), then an LDS
-        count per partition with the query positions' lookups; a partition with too many distinct pairs repeats the
-        level with one more bit. Returns (pair keys, counts, per-position target counts, pairs, pbits); with cb > 0
-        (context ids below 2^cb) the pairs come as packed words and "counts" is the escape table (keys, counts) of
-        those too large for the word, or None if that table overflowed."""
-        elib, lib, dev = self.elib, self.lib, self.tok.device
-        N = vi.ctx_of.numel()
-        ratio = self.dratio.get(k, 1.0)
-        # at least PART_MIN_BITS: every level gets enough partitions (blocks) for its N lookups as well
-        pbits = max(min(PART_MIN_BITS, 24), min(24, math.ceil(math.log2(max(1.0, n_ev * ratio / PART_TARGET)))))
-        qk = torch.empty(N, dtype=torch.int64, device=dev)
-        qv = torch.empty(N, dtype=torch.int32, device=dev)
-        e0, e1 = self._event("partition", k, -1, N)
-        e0.record()
-        elib("ng_part_lookups", vi.ctx_of, tgt, N, 0, vi.ids, qk, qv)
-        e1.record()
-        while True:
-            P = 1 << pbits
-            sev = torch.empty(max(n_ev, 1), dtype=torch.int64, device=dev)
-            sqk = torch.empty(N, dtype=torch.int64, device=dev)
-            sqv = torch.empty(N, dtype=torch.int32, device=dev)
-            start = torch.empty(P + 1, dtype=torch.int64, device=dev)
-            qstart = torch.empty(P + 1, dtype=torch.int64, device=dev)
-            e0, e1 = self._event("partition", k, -1, n_ev)
-            e0.record()
-            if n_ev:
-                lib.cub("sort_pairs", ev, sev, None, None, n_ev, i32(64 - pbits), i32(64))
-            elib("ng_part_bounds", sev, n_ev, i32(pbits), start)
-            if N:
-                lib.cub("sort_pairs", qk, sqk, qv, sqv, N, i32(64 - pbits), i32(64))
-            elib("ng_part_bounds", sqk, N, i32(pbits), qstart)
-            e1.record()
-            G2 = min(P, PART_BLOCKS)
-            out_k = torch.empty(max(n_ev, 1), dtype=torch.int64, device=dev)
-            out_c = None if cb else torch.empty(max(n_ev, 1), dtype=torch.int32, device=dev)
-            esc_k = torch.full((ESC_CAP,), -1, dtype=torch.int64, device=dev) if cb else None
-            esc_c = torch.empty(ESC_CAP, dtype=torch.int32, device=dev) if cb else None
-            seg_cnt = torch.empty(G2, dtype=torch.int32, device=dev)
-            seg_base = torch.empty(G2, dtype=torch.int64, device=dev)
-            qcnt = torch.zeros(max(N, 1), dtype=torch.int32, device=dev)
-            flags = torch.zeros(1, dtype=torch.int32, device=dev)
-            e0, e1 = self._event("count", k, -1, n_ev)
-            e0.record()
-            elib("ng_part_count", sev, start, i32(pbits), sqk, sqv, qstart, out_k, out_c, i32(cb), esc_k, esc_c,
-                 u64(ESC_CAP if cb else 0), seg_cnt, seg_base, qcnt, flags, i32(G2))
-            e1.record()
-            del sev, sqk, sqv, start, qstart
-            fl = int(flags[0].item())
-            if fl & 2:
-                return None
-            if not fl & 1:
-                break
-            if pbits >= 24:
-                raise RuntimeError(f"k={k}: a partition holds too many distinct pairs at 24 bits")
-            pbits += 1
-        offs = torch.empty(G2 + 1, dtype=torch.int64, device=dev)
-        elib("ng_seg_offsets", seg_cnt, G2, offs)
-        U = int(offs[G2].item())
-        ck = torch.empty(max(U, 1), dtype=torch.int64, device=dev)
-        cc = None if cb else torch.empty(max(U, 1), dtype=torch.int32, device=dev)
-        e0, e1 = self._event("count", k, -1, U)
-        e0.record()
-        elib("ng_seg_gather", out_k, out_c, u64(0), seg_base, seg_cnt, G2, offs, ck, cc)
-        e1.record()
-        self.dratio[k] = U / max(1, n_ev)
-        return ck, ((esc_k, esc_c) if cb else cc), qcnt, U, pbits
-
-    def _owner_packed(self, li, k, vi, words, esc, U, cb, tgt, out, want, qcnt, zero_tops):
-        """The owner side from packed words: a keys-only sort by context, then per-context totals, pair counts and top
-        entries straight from the sorted words (only present contexts are written: dist is zeroed, the tops too when
-        rows read every context's), then per query position its context's summary and counted target."""
-        elib, lib, dev = self.elib, self.lib, self.tok.device
+    def _owner_packed(self, li, k, vi, c, tgt, out, want, zero_tops):
+        """The owner side from packed pairs: per present context its record (sorted by context, keys only), then per
+        query position its context's record and counted target (ng_pos_summary)."""
         N, n_own = vi.ctx_of.numel(), vi.ids
-        sw = torch.empty(max(U, 1), dtype=torch.int64, device=dev)
-        e0, e1 = self._event("sort", k, -1, U)
-        e0.record()
-        if U:
-            lib.cub("sort_pairs", words, sw, None, None, U, i32(64 - cb), i32(64))
-        e1.record()
-        del words
         ktop = 1 if want <= 1 else 2 if want <= 2 else 4 if want <= 4 else 8
-        words_per = {1: 4, 2: 8, 4: 8, 8: 16}[ktop]
-        tokw = (ktop + 1) // 2
-        # per context: its record (total, pairs, top tokens two per word, top counts) and its pair count (zeroed: the
-        # contexts the corpus never showed read 0); the records are zeroed too when rows read every context's
-        rec = (torch.zeros if zero_tops else torch.empty)((n_own, words_per), dtype=torch.int32, device=dev)
-        dist = torch.zeros(n_own, dtype=torch.int32, device=dev)
-        flags = torch.zeros(1, dtype=torch.int32, device=dev)
-        e0, e1 = self._event("ctx_topk", k, -1, U)
-        e0.record()
-        elib("ng_ctx_summary", sw, U, i32(cb), esc[0], esc[1], u64(ESC_CAP), i32(ktop), rec, dist, flags)
-        e1.record()
+        try:
+            rec, dist = summarize(self.elib, self.lib, c, n_own, ktop, zero_tops,
+                                  lambda name, n: self._event(name, k, -1, n))
+        except RuntimeError as e:
+            raise RuntimeError(f"k={k}: {e}") from None
         e0, e1 = self._event("pos_gather", k, -1, N)
         e0.record()
         kout = self.topk
-        elib("ng_pos_summary", vi.ctx_of, N, 0, n_own, tgt, rec, dist, None, qcnt, i32(ktop), i32(kout), i32(li),
-             out[0, li], out[1, li], out[2, li], self.top_tok[li] if kout else None,
-             self.top_cnt[li] if kout else None, None)
+        self.elib("ng_pos_summary", vi.ctx_of, N, 0, n_own, tgt, rec, dist, None, c.qcnt, i32(ktop), i32(kout),
+                  i32(li), out[0, li], out[1, li], out[2, li], self.top_tok[li] if kout else None,
+                  self.top_cnt[li] if kout else None, None)
         e1.record()
-        if int(flags[0].item()) & 4:
-            raise RuntimeError(f"k={k}: a total does not fit uint32")
         top_tok = top_cnt = None
         if zero_tops:
-            top_tok = rec[:, 2 : 2 + tokw].contiguous().view(torch.int16)
-            top_cnt = rec[:, 2 + tokw : 2 + tokw + ktop].contiguous()
+            top_tok, top_cnt = record_tops(rec, ktop)
         return None, top_tok, top_cnt, ktop
 
     def _outputs_engine(self, li, k, vi, t, tgt, out, want):

@@ -6,13 +6,15 @@ of that shard), that context's most frequent next token (count descending, then 
 0 if not even the 1-context occurred.
 
 Two phases, both on libngram_amd.so. Existence, k = 1, 2, ...: the query contexts of the positions still matching
-(a query index per level), the corpus positions whose (k-1)-context matched (a hit bitmap per level) probed for
-their k-context (ng_scan_exist: a bitmap and a per-context hit flag, no counting), until no position matches. A match
-is monotone in k (kgram.rs:12-15), so each position's length is its last matching level. Then counting, only for each
-position's final context: per level, the final contexts' query index, the corpus positions of that level's bitmap
-probed and (context, next) counted in a split pair table (ng_scan_count), the pairs sorted, each context's top entry
-(ng_ctx_topk) gathered to its positions (ng_pos_gather). Most positions match past the short levels, whose contexts
-are the corpus' most frequent: counting only final contexts skips nearly all of their occurrences.
+(a query index per level over the list of positions still matching), the corpus positions whose (k-1)-context
+matched (a hit bitmap per level) probed for their k-context (ng_scan_exist: a bitmap and a per-context hit flag, no
+counting), until no position matches. A match is monotone in k (kgram.rs:12-15), so each position's length is its
+last matching level. Then counting, only for each position's final context: per level, the final contexts' query
+index, the corpus positions of that level's bitmap probed and their (context, next) hits emitted, partitioned and
+counted in LDS (partcount.py: no global atomics, so the hot pairs of short contexts cost no serialized chains), each
+context's top entry made from its pairs (ng_ctx_summary) and gathered to its positions (ng_pos_summary). Most
+positions match past the short levels, whose contexts are the corpus' most frequent: counting only final contexts
+skips nearly all of their occurrences.
 
 Surfaces: `longest_match(...)` on GPU tensors, and `LongestMatch.create(files, tokens, threads, cpus)` /
 `build() -> dict` in cache_ladder's shape (cache_ladder/src/lib.rs:1-8, cache_ladder.pyi)."""
@@ -28,16 +30,18 @@ import torch
 from .counts import record_lib
 from .data import BOS, HEADER_BYTES, shard_tokens
 from .gpu_val_stats import layout
-from .qindex import QueryIndex
 from .lib import Lib, i32, u64
-
-LOAD = 0.7
+from .partcount import count_events, emit_region, pack_events, summarize
+from .qindex import QueryIndex
 
 
 def _popcount(lib: Lib, bm: torch.Tensor) -> int:
     c = torch.zeros(1, dtype=torch.int64, device=bm.device)
     lib("popcount", bm, bm.numel(), c)
     return int(c.item())
+
+
+_RATIO: dict[int, float] = {}  # distinct pairs per counted event at each level, from the last count (sizes partitions)
 
 
 def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: int = 64, elib: Lib | None = None,
@@ -57,30 +61,31 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
     grid = torch.cuda.get_device_properties(dev).multi_processor_count * 32
     t0 = time.perf_counter()
     length = torch.zeros(N, dtype=torch.int32, device=dev)
-    active = avail >= 1
-    if query is not None:
-        active &= query
+    # the queried positions, as a list; each level keeps the ones still matching (the lists shrink fast)
+    sel = avail >= 1 if query is None else (avail >= 1) & query
+    act = torch.nonzero(sel).squeeze(1).to(torch.int32)
+    # eligible at level k: queried positions with avail >= k (one histogram for every level)
+    elig = torch.bincount(avail[act.long()].clamp_max(cap).long(), minlength=cap + 1).flip(0).cumsum(0).flip(0)
+    elig = elig.cpu().tolist()
     bms: list[torch.Tensor] = []
     prev = None
+    prev_hits = 0
     ladder = []
     flags = torch.zeros(2, dtype=torch.int32, device=dev)
     for k in range(1, cap + 1):
-        act = active & (avail >= k)
-        n_act = int(act.sum().item())
-        if n_act == 0:
+        act = act[avail[act.long()] >= k]
+        if act.numel() == 0:
             break
-        vi = QueryIndex(elib, x, avail, k, torch.nonzero(act).squeeze(1).to(torch.int32))
+        vi = QueryIndex(elib, x, avail, k, act, compact=True)
         hit = torch.zeros(vi.ids, dtype=torch.uint8, device=dev)
         bm = torch.empty(nwords, dtype=torch.int32, device=dev)
         mode = 0 if prev is None or prev_hits * 2 > L else 2  # a lane per position while the gate is dense
         elib("ng_scan_exist", tok, L, i32(k), prev, bm, vi.table, u64(vi.cap), vi.rep, x, hit, flags, i32(grid),
              i32(mode))
         ctx = vi.ctx_of.long()
-        matched = (ctx >= 0) & (hit[ctx.clamp_min(0)] != 0)
-        length[matched] = k
-        eligible = (avail >= k) if query is None else (avail >= k) & query
-        ladder.append((k, int(eligible.sum().item()), int(matched.sum().item())))
-        active = matched
+        act = act[(ctx >= 0) & (hit[ctx.clamp_min(0)] != 0)]
+        length[act.long()] = k
+        ladder.append((k, int(elig[k]), int(act.numel())))
         bms.append(bm)
         prev = bm
         prev_hits = _popcount(lib, bm)
@@ -91,54 +96,76 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
         t0 = time.perf_counter()
     nxt = torch.zeros(N, dtype=torch.int16, device=dev)
     cnt = torch.zeros(N, dtype=torch.int32, device=dev)
+    # each level's final positions (those whose longest match has that length), grouped by one sort
+    qpos = torch.nonzero(sel).squeeze(1)
+    qlen = length[qpos]
+    order = torch.argsort(qlen, stable=True)
+    qpos, qlen = qpos[order].to(torch.int32), qlen[order]
+    bounds = torch.searchsorted(qlen, torch.arange(len(bms) + 2, device=dev, dtype=torch.int32)).cpu().tolist()
+    R = emit_region(L, grid)
+    regions = torch.empty(grid * R, dtype=torch.int64, device=dev)
+    ev_count = torch.empty(grid, dtype=torch.int32, device=dev)
     scratch_bm = torch.empty(nwords, dtype=torch.int32, device=dev)
-    o_tot = torch.zeros(N, dtype=torch.int32, device=dev)
-    o_dist = torch.zeros(N, dtype=torch.int32, device=dev)
-    o_cnt = torch.zeros(N, dtype=torch.int32, device=dev)
     for k in range(1, len(bms) + 1):
-        fin = length == k
-        if not bool(fin.any()):
+        fpos = qpos[bounds[k] : bounds[k + 1]]
+        m = fpos.numel()
+        if m == 0:
             continue
-        vi = QueryIndex(elib, x, avail, k, torch.nonzero(fin).squeeze(1).to(torch.int32))
+        vi = QueryIndex(elib, x, avail, k, fpos, compact=True)
         bm_k = bms[k - 1]
-        events = _popcount(lib, bm_k)
-        mode = 0 if events * 2 > L else 2
-        tcap = max(1 << 16, int(min(events, 64 * vi.n + (1 << 20)) / LOAD))
-        while True:
-            keys = torch.full((tcap,), -1, dtype=torch.int64, device=dev)
-            cnts = torch.zeros(tcap, dtype=torch.int32, device=dev)
-            flags.zero_()
-            elib("ng_scan_count", tok, L, i32(k), bm_k, scratch_bm, vi.table, u64(vi.cap), vi.rep, x, keys, cnts,
-                 u64(tcap), flags, i32(grid), i32(mode))
-            if int(flags[0].item()) == 0:
-                break
-            tcap *= 2
-        counter = torch.zeros(1, dtype=torch.int64, device=dev)
-        ck = torch.empty(tcap, dtype=torch.int64, device=dev)
-        cc = torch.empty(tcap, dtype=torch.int32, device=dev)
-        elib("ng_table_compact", keys, cnts, u64(tcap), ck, cc, counter)
-        del keys, cnts
-        U = int(counter.item())
-        ctx_bits = max(1, (max(vi.ids, 2) - 1).bit_length())
-        uk = torch.empty(U, dtype=torch.int64, device=dev)
-        agg = torch.empty(U, dtype=torch.int32, device=dev)
-        if U:
-            lib.cub("sort_pairs", ck, uk, cc, agg, U, i32(0), i32(16 + ctx_bits))
-        del ck, cc
-        start = torch.zeros(vi.ids, dtype=torch.int64, device=dev)
-        end = torch.zeros(vi.ids, dtype=torch.int64, device=dev)
-        tot = torch.zeros(vi.ids, dtype=torch.int64, device=dev)
-        top_tok = torch.zeros(vi.ids, dtype=torch.int16, device=dev)
-        top_cnt = torch.zeros(vi.ids, dtype=torch.int32, device=dev)
-        lib("seg_bounds", uk, U, start, end)
-        elib("ng_ctx_topk", uk, agg, start, end, vi.ids, i32(1), tot, top_tok, top_cnt)
-        elib("ng_pos_gather", vi.ctx_of, N, 0, vi.ids, x, uk, agg, start, end, tot, top_tok, top_cnt, None, None,
-             None, u64(0), None, i32(1), i32(1), i32(0), o_tot, o_dist, o_cnt, nxt, cnt, None)
-        del vi, uk, agg, start, end, tot, top_tok, top_cnt
+        mode = 0 if _popcount(lib, bm_k) * 2 > L else 2
+        # the corpus positions of the level's existence bitmap probed against the final contexts; their hits emitted,
+        # partitioned and counted in LDS, then each final context's top entry
+        flags.zero_()
+        elib("ng_scan_emit", tok, L, i32(k), bm_k, scratch_bm, vi.table, u64(vi.cap), vi.rep, x, regions, u64(R),
+             ev_count, flags, i32(grid), i32(mode))
+        ev, n_ev = pack_events(elib, regions, R, ev_count, grid)
+        if int(flags[0].item()) & 4:
+            raise RuntimeError(f"k={k}: an emit region overflowed")
+        c = count_events(elib, lib, ev, n_ev, vi.ids, _RATIO.get(k, 1.0))
+        del ev
+        _RATIO[k] = c.U / max(1, n_ev)
+        o_tok = torch.zeros(m, dtype=torch.int16, device=dev)
+        o_cnt = torch.zeros(m, dtype=torch.int32, device=dev)
+        if c.cb:
+            rec, dist = summarize(elib, lib, c, vi.ids, 1)
+            o_tot = torch.empty(m, dtype=torch.int32, device=dev)
+            o_dist = torch.empty(m, dtype=torch.int32, device=dev)
+            o_tc = torch.empty(m, dtype=torch.int32, device=dev)
+            elib("ng_pos_summary", vi.ctx_of, m, 0, vi.ids, None, rec, dist, None, None, i32(1), i32(1), i32(0),
+                 o_tot, o_dist, o_tc, o_tok, o_cnt, None)
+            del rec, dist, o_tot, o_dist, o_tc
+        else:  # unpacked pairs: sorted by key, per-context top entry by selection
+            _top1_unpacked(elib, lib, vi, c, x, o_tok, o_cnt)
+        nxt[fpos.long()] = o_tok
+        cnt[fpos.long()] = o_cnt
+        del vi, c, o_tok, o_cnt
     if timing is not None:
         torch.cuda.synchronize()
         timing["count"] = timing.get("count", 0.0) + time.perf_counter() - t0
     return length, nxt, cnt, ladder
+
+
+def _top1_unpacked(elib: Lib, lib: Lib, vi, c, x, o_tok, o_cnt) -> None:
+    """The final contexts' top entries from unpacked (pair key, count) pairs (compact ctx_of, m entries)."""
+    dev = x.device
+    m = vi.ctx_of.numel()
+    ctx_bits = max(1, (max(vi.ids, 2) - 1).bit_length())
+    uk = torch.empty(c.U, dtype=torch.int64, device=dev)
+    agg = torch.empty(c.U, dtype=torch.int32, device=dev)
+    if c.U:
+        lib.cub("sort_pairs", c.pairs, uk, c.counts, agg, c.U, i32(0), i32(16 + ctx_bits))
+    start = torch.zeros(vi.ids, dtype=torch.int64, device=dev)
+    end = torch.zeros(vi.ids, dtype=torch.int64, device=dev)
+    tot = torch.zeros(vi.ids, dtype=torch.int64, device=dev)
+    top_tok = torch.zeros(vi.ids, dtype=torch.int16, device=dev)
+    top_cnt = torch.zeros(vi.ids, dtype=torch.int32, device=dev)
+    lib("seg_bounds", uk, c.U, start, end)
+    elib("ng_ctx_topk", uk, agg, start, end, vi.ids, i32(1), tot, top_tok, top_cnt)
+    o = [torch.zeros(m, dtype=torch.int32, device=dev) for _ in range(3)]
+    tgt = torch.zeros(m, dtype=torch.int16, device=dev)
+    elib("ng_pos_gather", vi.ctx_of, m, 0, vi.ids, tgt, uk, agg, start, end, tot, top_tok, top_cnt, None, None, None,
+         u64(0), None, i32(1), i32(1), i32(0), o[0], o[1], o[2], o_tok, o_cnt, None)
 
 
 def _segments(x: torch.Tensor, lib: Lib) -> torch.Tensor:

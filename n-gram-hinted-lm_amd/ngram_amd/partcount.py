@@ -1,0 +1,176 @@
+"""Counting (context id, next token) events without global atomics, shared by CountBuild's "part" mode and the
+longest match's counting phase (libngram_amd.so's partitioned-count entry points; no counterpart in the reference,
+whose counts go through one atomic hash table per level, record_367_gpu_counts/track_1_short/counts/kernels.cu:132-247).
+
+An emitting scan (ng_scan_emit) leaves each block's events — mix64(context id << 16 | next), a bijection of the pair
+key — in the block's own region. `pack_events` packs the regions into one array; `count_events` sorts the events by
+their top pbits (a hash partition of the pairs, sized so a partition holds about PART_TARGET distinct pairs: the LDS
+table holds 8192), counts every partition in LDS (ng_part_count), answers the lookups (the query positions' (context,
+target) pairs, hashed and sorted the same way) and packs the distinct pairs, by default as one word each: pair key <<
+(48 - cb) | count (a count too large for the field also goes to an escape table). `summarize` sorts the words by
+context (keys only) and makes each present context's record: total, pairs, top entries (ng_ctx_summary), which
+ng_pos_summary gathers per query position.
+
+On MI355X, global atomics run at about 27 G/s on scattered slots and 80 M/s on one address (a hot pair's chain);
+here every event is counted by an LDS atomic and moved by coalesced streams."""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from .lib import Lib, i32, u64
+
+PART_TARGET = 4096  # distinct pairs per partition aimed at (the LDS table holds 8192)
+PART_BLOCKS = 2048  # count blocks, each a run of consecutive partitions
+PART_MIN_BITS = 11  # at least this many partition bits: enough blocks for the lookups as well
+ESC_CAP = 1 << 20  # packed pairs whose count exceeds the word's count field, per level
+PACK_MIN_BITS = 0  # context-id bits of the packed words at least this (up to 44: a narrower count field)
+
+
+def emit_region(L: int, grid: int) -> int:
+    """The per-block region an emitting scan of L positions with `grid` blocks needs (ng_emit_region)."""
+    per = grid * 8192
+    return -(-L // per) * 8192
+
+
+def _no_event(name: str, n: int):
+    class _E:
+        def record(self):
+            pass
+
+    return _E(), _E()
+
+
+def pack_events(elib: Lib, regions: torch.Tensor, R: int, ev_count: torch.Tensor, nseg: int, event=_no_event):
+    """The regions' events (segment s = ev_count[s] items at s * R) packed into one array: (events, n)."""
+    dev = regions.device
+    offs = torch.empty(nseg + 1, dtype=torch.int64, device=dev)
+    elib("ng_seg_offsets", ev_count, nseg, offs)
+    n_ev = int(offs[nseg].item())
+    ev = torch.empty(max(n_ev, 1), dtype=torch.int64, device=dev)
+    e0, e1 = event("gather", n_ev)
+    e0.record()
+    elib("ng_seg_gather", regions, None, u64(R), None, ev_count, nseg, offs, ev, None)
+    e1.record()
+    return ev, n_ev
+
+
+@dataclass
+class Counted:
+    """A level's distinct pairs: `pairs` (U packed words when cb > 0, else pair keys with `counts`), the escape table
+    `esc` (keys, counts) of packed words, per-lookup target counts `qcnt`, the partition bits used."""
+
+    pairs: torch.Tensor
+    counts: torch.Tensor | None
+    esc: tuple | None
+    qcnt: torch.Tensor | None
+    U: int
+    pbits: int
+    cb: int
+
+
+def count_events(elib: Lib, lib: Lib, ev: torch.Tensor, n_ev: int, n_ids: int, ratio: float = 1.0,
+                 lookups: tuple | None = None, packed: bool = True, event=_no_event) -> Counted:
+    """Count n_ev events of context ids below n_ids. `ratio`: distinct pairs per event expected (sizes the
+    partitions; a partition found too full repeats the count with one more bit). `lookups` (ctx_of int32 [N], tgt
+    int16 [N]): qcnt[i] = the count of (ctx_of[i], tgt[i]), 0 where absent or ctx_of[i] is out of range. `packed`:
+    pairs as packed words (falls back to keys + counts when the escape table overflows)."""
+    dev = ev.device
+    cb = max(1, (max(n_ids, 2) - 1).bit_length(), PACK_MIN_BITS) if packed else 0
+    N = 0
+    if lookups is not None:
+        ctx_of, tgt = lookups
+        N = ctx_of.numel()
+        qk = torch.empty(N, dtype=torch.int64, device=dev)
+        qv = torch.empty(N, dtype=torch.int32, device=dev)
+        e0, e1 = event("partition", N)
+        e0.record()
+        elib("ng_part_lookups", ctx_of, tgt, N, 0, n_ids, qk, qv)
+        e1.record()
+    pbits = max(min(PART_MIN_BITS, 24), min(24, math.ceil(math.log2(max(1.0, n_ev * ratio / PART_TARGET)))))
+    while True:
+        P = 1 << pbits
+        sev = torch.empty(max(n_ev, 1), dtype=torch.int64, device=dev)
+        start = torch.empty(P + 1, dtype=torch.int64, device=dev)
+        qstart = torch.zeros(P + 1, dtype=torch.int64, device=dev)
+        sqk = sqv = None
+        e0, e1 = event("partition", n_ev)
+        e0.record()
+        if n_ev:
+            lib.cub("sort_pairs", ev, sev, None, None, n_ev, i32(64 - pbits), i32(64))
+        elib("ng_part_bounds", sev, n_ev, i32(pbits), start)
+        if N:
+            sqk = torch.empty(N, dtype=torch.int64, device=dev)
+            sqv = torch.empty(N, dtype=torch.int32, device=dev)
+            lib.cub("sort_pairs", qk, sqk, qv, sqv, N, i32(64 - pbits), i32(64))
+            elib("ng_part_bounds", sqk, N, i32(pbits), qstart)
+        e1.record()
+        G2 = min(P, PART_BLOCKS)
+        out_k = torch.empty(max(n_ev, 1), dtype=torch.int64, device=dev)
+        out_c = None if cb else torch.empty(max(n_ev, 1), dtype=torch.int32, device=dev)
+        esc_k = torch.full((ESC_CAP,), -1, dtype=torch.int64, device=dev) if cb else None
+        esc_c = torch.empty(ESC_CAP, dtype=torch.int32, device=dev) if cb else None
+        seg_cnt = torch.empty(G2, dtype=torch.int32, device=dev)
+        seg_base = torch.empty(G2, dtype=torch.int64, device=dev)
+        qcnt = torch.zeros(max(N, 1), dtype=torch.int32, device=dev) if N else None
+        flags = torch.zeros(1, dtype=torch.int32, device=dev)
+        e0, e1 = event("count", n_ev)
+        e0.record()
+        elib("ng_part_count", sev, start, i32(pbits), sqk, sqv, qstart, out_k, out_c, i32(cb), esc_k, esc_c,
+             u64(ESC_CAP if cb else 0), seg_cnt, seg_base, qcnt, flags, i32(G2))
+        e1.record()
+        del sev, sqk, sqv, start, qstart
+        fl = int(flags[0].item())
+        if fl & 2:  # more large counts than the escape table holds: count again, unpacked
+            cb = 0
+            continue
+        if not fl & 1:
+            break
+        if pbits >= 24:
+            raise RuntimeError("a partition holds too many distinct pairs at 24 bits")
+        pbits += 1
+    offs = torch.empty(G2 + 1, dtype=torch.int64, device=dev)
+    elib("ng_seg_offsets", seg_cnt, G2, offs)
+    U = int(offs[G2].item())
+    pairs = torch.empty(max(U, 1), dtype=torch.int64, device=dev)
+    counts = None if cb else torch.empty(max(U, 1), dtype=torch.int32, device=dev)
+    e0, e1 = event("count", U)
+    e0.record()
+    elib("ng_seg_gather", out_k, out_c, u64(0), seg_base, seg_cnt, G2, offs, pairs, counts)
+    e1.record()
+    return Counted(pairs, counts, (esc_k, esc_c) if cb else None, qcnt, U, pbits, cb)
+
+
+RECORD_WORDS = {1: 4, 2: 8, 4: 8, 8: 16}  # u32 words of a context record for top 1, 2, 4, 8
+
+
+def summarize(elib: Lib, lib: Lib, c: Counted, n_ids: int, ktop: int, zero_records: bool = False, event=_no_event):
+    """Per present context (of packed pairs): its record (int32 [n_ids, RECORD_WORDS[ktop]]: total, pairs, the
+    first ktop tokens two per word, their counts) and its pair count (int32 [n_ids], 0 for absent contexts). The
+    records of absent contexts are zeros only with zero_records. Raises if a total reaches 2^32."""
+    dev = c.pairs.device
+    sw = torch.empty(max(c.U, 1), dtype=torch.int64, device=dev)
+    e0, e1 = event("sort", c.U)
+    e0.record()
+    if c.U:
+        lib.cub("sort_pairs", c.pairs, sw, None, None, c.U, i32(64 - c.cb), i32(64))
+    e1.record()
+    rec = (torch.zeros if zero_records else torch.empty)((n_ids, RECORD_WORDS[ktop]), dtype=torch.int32, device=dev)
+    dist = torch.zeros(n_ids, dtype=torch.int32, device=dev)
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    e0, e1 = event("ctx_topk", c.U)
+    e0.record()
+    elib("ng_ctx_summary", sw, c.U, i32(c.cb), c.esc[0], c.esc[1], u64(ESC_CAP), i32(ktop), rec, dist, flags)
+    e1.record()
+    if int(flags[0].item()) & 4:
+        raise RuntimeError("a total does not fit uint32")
+    return rec, dist
+
+
+def record_tops(rec: torch.Tensor, ktop: int):
+    """The top tokens (int16 [n, ktop]) and counts (int32 [n, ktop]) of context records."""
+    tokw = (ktop + 1) // 2
+    return rec[:, 2 : 2 + tokw].contiguous().view(torch.int16)[:, :ktop], rec[:, 2 + tokw : 2 + tokw + ktop].contiguous()

@@ -17,8 +17,10 @@ LOAD = 0.4  # contexts per slot aimed at: measured at c3, 0.4 gives the fastest 
 
 
 class QueryIndex:
-    def __init__(self, lib: Lib, x: torch.Tensor, avail: torch.Tensor, k: int, positions: torch.Tensor | None = None):
-        """Index the valid k-contexts of the query positions (all of x, or the int32 `positions`)."""
+    def __init__(self, lib: Lib, x: torch.Tensor, avail: torch.Tensor, k: int, positions: torch.Tensor | None = None,
+                 compact: bool = False):
+        """Index the valid k-contexts of the query positions (all of x, or the int32 `positions`). `compact`: ctx_of
+        holds one entry per listed position (in their order) instead of one per position of x."""
         dev = x.device
         N = x.numel()
         m = N if positions is None else int(positions.numel())
@@ -27,12 +29,15 @@ class QueryIndex:
             slots = cap + TAIL
             table = torch.full((slots,), -1, dtype=torch.int64, device=dev)
             rep = torch.full((slots,), -1, dtype=torch.int32, device=dev)
-            ctx_of = torch.full((N,), -1, dtype=torch.int32, device=dev) if positions is not None else \
-                torch.empty(N, dtype=torch.int32, device=dev)
+            if compact and positions is not None:
+                ctx_of = torch.empty(m, dtype=torch.int32, device=dev)
+            else:
+                ctx_of = torch.full((N,), -1, dtype=torch.int32, device=dev) if positions is not None else \
+                    torch.empty(N, dtype=torch.int32, device=dev)
             counters = torch.zeros(3, dtype=torch.int64, device=dev)
             if m:
                 lib("ng_query_index", x, avail, positions, m, i32(k), table, u64(cap), u64(slots), rep, ctx_of,
-                    counters)
+                    i32(int(compact and positions is not None)), counters)
             c = counters.cpu().tolist()
             if c[1] == 0:
                 break
@@ -50,7 +55,7 @@ class QueryIndex:
                 remap = torch.empty(slots, dtype=torch.int32, device=dev)
                 c2 = torch.zeros(3, dtype=torch.int64, device=dev)
                 lib("ng_query_index_shrink", table, rep, u64(slots), t2, u64(small), u64(small + TAIL), r2, ctx_of,
-                    N, remap, c2)
+                    ctx_of.numel(), remap, c2)
                 if int(c2[1].item()) == 0:
                     break
                 small *= 2

@@ -8,6 +8,7 @@ import torch
 
 import oracle as O
 from ngram_amd import counts as C
+from ngram_amd import partcount as P
 from ngram_amd import data
 
 pytestmark = pytest.mark.gpu
@@ -51,15 +52,15 @@ def test_counts_match_oracle(corpus, level_shards, mode, monkeypatch):
     if mode == "part-regroup":
         # one partition per level to start with: each level's LDS table overflows and it is repartitioned bit by bit;
         # three blocks, each counting a run of partitions
-        monkeypatch.setattr(C, "PART_TARGET", 1 << 30)
-        monkeypatch.setattr(C, "PART_MIN_BITS", 0)
-        monkeypatch.setattr(C, "PART_BLOCKS", 3)
+        monkeypatch.setattr(P, "PART_TARGET", 1 << 30)
+        monkeypatch.setattr(P, "PART_MIN_BITS", 0)
+        monkeypatch.setattr(P, "PART_BLOCKS", 3)
     if mode in ("part-escape", "part-unpacked"):
         # an 8-bit count field: counts of 255 and more go to the escape table; with a 4-slot table it overflows and
         # every level is counted again unpacked
-        monkeypatch.setattr(C, "PACK_MIN_BITS", 40)
+        monkeypatch.setattr(P, "PACK_MIN_BITS", 40)
         if mode == "part-unpacked":
-            monkeypatch.setattr(C, "ESC_CAP", 4)
+            monkeypatch.setattr(P, "ESC_CAP", 4)
     lib = C.record_lib()
     cb = C.CountBuild(corpus.shards(), levels=LEVELS, level_shards=level_shards, topk=4)
     cb.mode = mode.split("-")[0]
