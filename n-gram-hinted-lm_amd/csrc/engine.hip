@@ -9,6 +9,7 @@
 //     ascending), then per context its total and top-k (count descending, token ascending) by selection in registers,
 //     and per query position tot / dist / cnt (binary search) / top-k in one gather.
 #include "pairs.h"
+#include "prim.h"
 
 namespace {
 
@@ -39,10 +40,12 @@ __device__ __forceinline__ void split_add(u64* keys, u32* cnts, u64 cap, u64 key
 //   CountSink: count it in the split table (once the table has overflowed, only the bitmap is still made: the level
 //              reruns bigger);
 //   ExistSink: flag its context (hit[id] = 1, plain byte stores: every writer stores the same value);
-//   EmitSink:  append mix64(pair key) to the block's own region ev[b * region, (b + 1) * region), at a block-local
-//              cursor in LDS (one LDS atomic per wave and round), and store the block's count in ev_count[b] at the
-//              end. No global atomic: a single global cursor would serialize (same-address atomics run at about
-//              80 M/s on MI355X). region >= ceil(L / (grid * 8192)) * 8192 bounds any block's hits in every mode.
+//   EmitSink:  append mix64(pair key) (what 0) or the corpus position (what 1) to the block's own region
+//              ev[b * region, (b + 1) * region), at a block-local cursor in LDS (one LDS atomic per wave and round),
+//              and store the block's count in ev_count[b] at the end; with `hit`, also flag the context. No global
+//              atomic: a single global cursor would serialize (same-address atomics run at about 80 M/s on MI355X).
+//              region >= ceil(L / (grid * 8192)) * 8192 (L: positions or list entries) bounds any block's hits in
+//              every mode.
 struct CountSink {
     static constexpr int KIND = 0;
     u64* keys;
@@ -58,6 +61,8 @@ struct EmitSink {
     u64* ev;
     u64 region;
     u32* ev_count;
+    int what;
+    unsigned char* hit;
 };
 
 // A lane's hit (count and exist sinks; the emit sink uses emit_wave / emit_lane).
@@ -71,22 +76,24 @@ __device__ __forceinline__ void sink_hit(const S& s, u64 key, bool full, u32* fl
 }
 
 // The wave's hits (b = ballot of `hit`) appended in lane order: called by every lane of the wave.
-__device__ __forceinline__ void emit_wave(const EmitSink& s, u32* cur, u64 b, bool hit, u64 key, u32* flags) {
+__device__ __forceinline__ void emit_wave(const EmitSink& s, u32* cur, u64 b, bool hit, u64 key, i64 p, u32* flags) {
     if (!b) return;
     u32 off = 0;
     if (lane_id() == 0) off = atomicAdd(cur, (u32)__popcll(b));
     off = (u32)__shfl((int)off, 0, WAVE);
     if (hit) {
         const u64 at = (u64)off + (u64)__popcll(b & lanemask_lt());
-        if (at < s.region) s.ev[(u64)blockIdx.x * s.region + at] = mix64(key);
+        if (at < s.region) s.ev[(u64)blockIdx.x * s.region + at] = s.what ? (u64)p : mix64(key);
         else atomicOr(&flags[0], 4u);
+        if (s.hit) s.hit[key >> 16] = 1;
     }
 }
 
-__device__ __forceinline__ void emit_lane(const EmitSink& s, u32* cur, u64 key, u32* flags) {
+__device__ __forceinline__ void emit_lane(const EmitSink& s, u32* cur, u64 key, i64 p, u32* flags) {
     const u64 at = atomicAdd(cur, 1u);
-    if (at < s.region) s.ev[(u64)blockIdx.x * s.region + at] = mix64(key);
+    if (at < s.region) s.ev[(u64)blockIdx.x * s.region + at] = s.what ? (u64)p : mix64(key);
     else atomicOr(&flags[0], 4u);
+    if (s.hit) s.hit[key >> 16] = 1;
 }
 
 template <class S>
@@ -134,7 +141,33 @@ __global__ void __launch_bounds__(256) scan_dense_k(const u16* __restrict__ tok,
         const u64 b = __ballot(hit);
         if (lane == 0) bm_out[base >> 5] = (u32)b;
         if (lane == 32 && w < nwords) bm_out[w] = (u32)(b >> 32);
-        if constexpr (S::KIND == 2) emit_wave(sink, &cur, b, hit, key, flags);
+        if constexpr (S::KIND == 2) emit_wave(sink, &cur, b, hit, key, p, flags);
+        else if (hit) sink_hit(sink, key, full, flags);
+    }
+    sink_end(sink, &cur);
+}
+
+// Listed positions: a lane per entry of plist (n corpus positions), no bitmap.
+template <int K, class S>
+__global__ void __launch_bounds__(256) scan_list_k(const u16* __restrict__ tok, const u64* __restrict__ plist, i64 n,
+                                                   int k, const u64* __restrict__ vt, u64 vcap,
+                                                   const u32* __restrict__ vrep, const u16* __restrict__ x, S sink,
+                                                   u32* flags) {
+    __shared__ u32 cur;
+    sink_begin<S>(&cur);
+    const int lane = lane_id();
+    const i64 stride = (i64)gridDim.x * blockDim.x;
+    for (i64 base = blockIdx.x * (i64)blockDim.x + (threadIdx.x & ~(WAVE - 1)); base < n; base += stride) {
+        const bool full = sink_full<S>(flags);
+        const i64 j = base + lane;
+        i64 p = 0;
+        u64 key = EMPTY;
+        if (j < n) {
+            p = (i64)plist[j];
+            key = probe_key<K>(tok, p, k, vt, vcap, vrep, x, flags);
+        }
+        const bool hit = key != EMPTY;
+        if constexpr (S::KIND == 2) emit_wave(sink, &cur, __ballot(hit), hit, key, p, flags);
         else if (hit) sink_hit(sink, key, full, flags);
     }
     sink_end(sink, &cur);
@@ -160,7 +193,7 @@ __global__ void __launch_bounds__(256) scan_sparse_k(const u16* __restrict__ tok
             const u64 key = probe_key<K>(tok, p, k, vt, vcap, vrep, x, flags);
             if (key != EMPTY) {
                 out |= 1u << b;
-                if constexpr (S::KIND == 2) emit_lane(sink, &cur, key, flags);
+                if constexpr (S::KIND == 2) emit_lane(sink, &cur, key, p, flags);
                 else sink_hit(sink, key, full, flags);
             }
         }
@@ -216,7 +249,8 @@ __global__ void __launch_bounds__(256) scan_compact_k(const u16* __restrict__ to
             }
             const bool hit = key != EMPTY;
             if (hit) atomicOr(&words[w][lp >> 5], 1u << (lp & 31));
-            if constexpr (S::KIND == 2) emit_wave(sink, &cur, __ballot(hit), hit, key, flags);
+            if constexpr (S::KIND == 2)
+                emit_wave(sink, &cur, __ballot(hit), hit, key, ((g0 + w * 64) << 5) + lp, flags);
             else if (hit) sink_hit(sink, key, full, flags);
         }
         __syncthreads();
@@ -224,6 +258,32 @@ __global__ void __launch_bounds__(256) scan_compact_k(const u16* __restrict__ to
         __syncthreads();
     }
     sink_end(sink, &cur);
+}
+
+__global__ void bits_popc_k(const u32* __restrict__ bm, i64 nwords, u32* __restrict__ off) {
+    const i64 w = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    if (w < nwords) off[w] = (u32)__popc(bm[w]);
+}
+
+__global__ void bits_list_k(const u32* __restrict__ bm, i64 nwords, const u32* __restrict__ off, u64* __restrict__ out) {
+    const i64 w = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    if (w >= nwords) return;
+    u32 word = bm[w];
+    u64 at = off[w];
+    while (word) {
+        const int b = __ffs(word) - 1;
+        word &= word - 1;
+        out[at++] = (u64)((w << 5) + b);
+    }
+}
+
+__global__ void fill_u32_small_k(u32* p, u32 v, i64 n) {
+    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+static void fill_u32_n(u32* p, u32 v, i64 n, hipStream_t st) {
+    if (n > 0) fill_u32_small_k<<<grid_for(n, 256), 256, 0, st>>>(p, v, n);
 }
 
 // One level scan with a sink: sparse 0 a lane per position, 1 a lane per bitmap word, 2 LDS-listed (bm_in required
@@ -495,8 +555,64 @@ extern "C" int ng_scan_emit(const u16* tok, i64 L, int k, const u32* bm_in, u32*
                             int sparse, void* stream) {
     if (L <= 0) return 0;
     if (grid <= 0 || region == 0 || region > 0xFFFFFFFFull) return -1;
-    if (launch_scan(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, EmitSink{ev, region, ev_count}, flags, grid, sparse,
-                (hipStream_t)stream) != 0) return -1;
+    if (launch_scan(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, EmitSink{ev, region, ev_count, 0, nullptr}, flags,
+                    grid, sparse, (hipStream_t)stream) != 0)
+        return -1;
+    return (int)hipGetLastError();
+}
+
+// A level scan with optional outputs, over a bitmap-gated range (plist NULL: positions [0, L) gated by bm_in as
+// ng_scan_count's `sparse` modes, hit bitmap into bm_out) or over listed positions (plist: n corpus positions, bm_*
+// unused). hit (may be NULL): hit[context id] = 1 per hit. ev (may be NULL): block b of `grid` appends per hit
+// mix64(pair key) (what 0) or its position (what 1) to ev[b * region ...] and stores how many in ev_count[b];
+// region >= ng_emit_region(L, grid) over a bitmap, >= ceil(n / (grid * 256)) * 256 over a list.
+extern "C" int ng_scan_sink(const u16* tok, i64 L, int k, const u32* bm_in, u32* bm_out, const u64* plist, i64 n,
+                            const u64* vt, u64 vcap, const u32* vrep, const u16* x, unsigned char* hit, int what,
+                            u64* ev, u64 region, u32* ev_count, u32* flags, int grid, int sparse, void* stream) {
+    if (grid <= 0 || (what != 0 && what != 1)) return -1;
+    if (ev && (region == 0 || region > 0xFFFFFFFFull)) return -1;
+    hipStream_t st = (hipStream_t)stream;
+    if (plist) {
+        if (n <= 0) {
+            if (ev) fill_u32_n(ev_count, 0u, grid, st);
+            return (int)hipGetLastError();
+        }
+        if (ev) {
+            const EmitSink sk{ev, region, ev_count, what, hit};
+            LEVEL_SWITCH(k, (scan_list_k<K, EmitSink><<<grid, 256, 0, st>>>(tok, plist, n, k, vt, vcap, vrep, x, sk, flags)));
+        } else {
+            LEVEL_SWITCH(k, (scan_list_k<K, ExistSink><<<grid, 256, 0, st>>>(tok, plist, n, k, vt, vcap, vrep, x, ExistSink{hit}, flags)));
+        }
+        return (int)hipGetLastError();
+    }
+    if (L <= 0) return 0;
+    int rc;
+    if (ev) rc = launch_scan(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, EmitSink{ev, region, ev_count, what, hit},
+                             flags, grid, sparse, st);
+    else rc = launch_scan(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, ExistSink{hit}, flags, grid, sparse, st);
+    if (rc != 0) return -1;
+    return (int)hipGetLastError();
+}
+
+// The set bits of a bitmap (nwords u32 words) as positions, in order: out[r] = the position of the r-th set bit,
+// *total = their number. Two-phase temp storage (temp NULL: *temp_bytes set).
+extern "C" int ng_bits_list(void* temp, size_t* temp_bytes, const u32* bm, i64 nwords, u64* out, u64* total,
+                            void* stream) {
+    if (!temp_bytes || nwords < 0) return -1;
+    const size_t need = (size_t)(nwords + 64) * 4 + prim::scan_u32_temp_bytes(nwords + 1) + 256;
+    if (!temp) {
+        *temp_bytes = need;
+        return 0;
+    }
+    if (*temp_bytes < need) return -1;
+    hipStream_t st = (hipStream_t)stream;
+    if (nwords == 0) return prim::fill_u64(total, 0ull, 1, st);
+    u32* off = (u32*)temp;
+    void* stemp = (char*)temp + (size_t)(nwords + 64) * 4;
+    bits_popc_k<<<grid_for(nwords, 256), 256, 0, st>>>(bm, nwords, off);
+    int e = prim::exclusive_scan_u32(off, off, nwords, total, stemp, st);
+    if (e) return e;
+    bits_list_k<<<grid_for(nwords, 256), 256, 0, st>>>(bm, nwords, off, out);
     return (int)hipGetLastError();
 }
 

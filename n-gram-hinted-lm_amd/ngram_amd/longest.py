@@ -67,9 +67,9 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
     # eligible at level k: queried positions with avail >= k (one histogram for every level)
     elig = torch.bincount(avail[act.long()].clamp_max(cap).long(), minlength=cap + 1).flip(0).cumsum(0).flip(0)
     elig = elig.cpu().tolist()
-    bms: list[torch.Tensor] = []
-    prev = None
-    prev_hits = 0
+    # each level's hit set (the corpus positions whose k-context is a query context of the level): a bitmap while
+    # dense, then, once sparse, a list of positions, which the next level scans instead of every bitmap word
+    levels: list[tuple[str, torch.Tensor, int]] = []
     ladder = []
     flags = torch.zeros(2, dtype=torch.int32, device=dev)
     for k in range(1, cap + 1):
@@ -78,17 +78,21 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
             break
         vi = QueryIndex(elib, x, avail, k, act, compact=True)
         hit = torch.zeros(vi.ids, dtype=torch.uint8, device=dev)
-        bm = torch.empty(nwords, dtype=torch.int32, device=dev)
-        mode = 0 if prev is None or prev_hits * 2 > L else 2  # a lane per position while the gate is dense
-        elib("ng_scan_exist", tok, L, i32(k), prev, bm, vi.table, u64(vi.cap), vi.rep, x, hit, flags, i32(grid),
-             i32(mode))
+        prev = levels[-1] if levels else None
+        if prev is not None and (prev[0] == "list" or prev[2] * LIST_DIV < L):
+            cand = prev[1] if prev[0] == "list" else _bits_list(elib, prev[1], prev[2])
+            hl, nh = _scan_list(elib, tok, L, k, vi, x, cand, hit, 1, flags, grid)
+            levels.append(("list", hl, nh))
+        else:
+            bm = torch.empty(nwords, dtype=torch.int32, device=dev)
+            mode = 0 if prev is None or prev[2] * 2 > L else 2  # a lane per position while the gate is dense
+            elib("ng_scan_exist", tok, L, i32(k), None if prev is None else prev[1], bm, vi.table, u64(vi.cap),
+                 vi.rep, x, hit, flags, i32(grid), i32(mode))
+            levels.append(("bm", bm, _popcount(lib, bm)))
         ctx = vi.ctx_of.long()
         act = act[(ctx >= 0) & (hit[ctx.clamp_min(0)] != 0)]
         length[act.long()] = k
         ladder.append((k, int(elig[k]), int(act.numel())))
-        bms.append(bm)
-        prev = bm
-        prev_hits = _popcount(lib, bm)
         del vi, hit, ctx
     if timing is not None:
         torch.cuda.synchronize()
@@ -101,25 +105,31 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
     qlen = length[qpos]
     order = torch.argsort(qlen, stable=True)
     qpos, qlen = qpos[order].to(torch.int32), qlen[order]
-    bounds = torch.searchsorted(qlen, torch.arange(len(bms) + 2, device=dev, dtype=torch.int32)).cpu().tolist()
-    R = emit_region(L, grid)
-    regions = torch.empty(grid * R, dtype=torch.int64, device=dev)
-    ev_count = torch.empty(grid, dtype=torch.int32, device=dev)
-    scratch_bm = torch.empty(nwords, dtype=torch.int32, device=dev)
-    for k in range(1, len(bms) + 1):
+    bounds = torch.searchsorted(qlen, torch.arange(len(levels) + 2, device=dev, dtype=torch.int32)).cpu().tolist()
+    big = None  # the regions of a bitmap level's emitting scan, made when one is counted
+    for k in range(1, len(levels) + 1):
         fpos = qpos[bounds[k] : bounds[k + 1]]
         m = fpos.numel()
         if m == 0:
             continue
         vi = QueryIndex(elib, x, avail, k, fpos, compact=True)
-        bm_k = bms[k - 1]
-        mode = 0 if _popcount(lib, bm_k) * 2 > L else 2
-        # the corpus positions of the level's existence bitmap probed against the final contexts; their hits emitted,
-        # partitioned and counted in LDS, then each final context's top entry
+        kind, hs, nh = levels[k - 1]
+        # the level's hit positions probed against the final contexts; their hits emitted, partitioned and counted in
+        # LDS, then each final context's top entry
         flags.zero_()
-        elib("ng_scan_emit", tok, L, i32(k), bm_k, scratch_bm, vi.table, u64(vi.cap), vi.rep, x, regions, u64(R),
-             ev_count, flags, i32(grid), i32(mode))
-        ev, n_ev = pack_events(elib, regions, R, ev_count, grid)
+        if kind == "bm":
+            if big is None:
+                R = emit_region(L, grid)
+                big = (torch.empty(grid * R, dtype=torch.int64, device=dev), R,
+                       torch.empty(grid, dtype=torch.int32, device=dev),
+                       torch.empty(nwords, dtype=torch.int32, device=dev))
+            regions, R, ev_count, scratch_bm = big
+            mode = 0 if nh * 2 > L else 2
+            elib("ng_scan_emit", tok, L, i32(k), hs, scratch_bm, vi.table, u64(vi.cap), vi.rep, x, regions, u64(R),
+                 ev_count, flags, i32(grid), i32(mode))
+            ev, n_ev = pack_events(elib, regions, R, ev_count, grid)
+        else:
+            ev, n_ev = _scan_list(elib, tok, L, k, vi, x, hs, None, 0, flags, grid)
         if int(flags[0].item()) & 4:
             raise RuntimeError(f"k={k}: an emit region overflowed")
         c = count_events(elib, lib, ev, n_ev, vi.ids, _RATIO.get(k, 1.0))
@@ -144,6 +154,31 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
         torch.cuda.synchronize()
         timing["count"] = timing.get("count", 0.0) + time.perf_counter() - t0
     return length, nxt, cnt, ladder
+
+
+LIST_DIV = 64  # a level's hits go to a position list once fewer than L / LIST_DIV (8 B each against L / 8 bitmap bytes)
+
+
+def _bits_list(elib: Lib, bm: torch.Tensor, n: int) -> torch.Tensor:
+    """The set positions of a bitmap (n of them) as a u64 list."""
+    out = torch.empty(max(n, 1), dtype=torch.int64, device=bm.device)
+    total = torch.zeros(1, dtype=torch.int64, device=bm.device)
+    elib.cub("ng_bits_list", bm, bm.numel(), out, total)
+    return out[:n]
+
+
+def _scan_list(elib: Lib, tok, L: int, k: int, vi, x, cand: torch.Tensor, hit, what: int, flags, grid: int):
+    """A level scan of listed corpus positions: hits flagged per context (hit may be None) and emitted as positions
+    (what 1) or mixed pair keys (what 0), packed: (list, n)."""
+    n = cand.numel()
+    g = max(1, min(grid, -(-n // 256)))  # a round of 256 entries per block: as many blocks as fill the GPU
+    R = -(-max(n, 1) // (g * 256)) * 256  # a list scan's block emits at most 256 per round
+    regions = torch.empty(g * R, dtype=torch.int64, device=cand.device)
+    ev_count = torch.empty(g, dtype=torch.int32, device=cand.device)
+    elib("ng_scan_sink", tok, L, i32(k), None, None, cand, n, vi.table, u64(vi.cap), vi.rep, x, hit, i32(what),
+         regions, u64(R), ev_count, flags, i32(g), i32(0))
+    out, m = pack_events(elib, regions, R, ev_count, g)
+    return out[:m] if what else out, m
 
 
 def _top1_unpacked(elib: Lib, lib: Lib, vi, c, x, o_tok, o_cnt) -> None:

@@ -90,7 +90,8 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor, n_ev: int, n_ids: int, r
         e0.record()
         elib("ng_part_lookups", ctx_of, tgt, N, 0, n_ids, qk, qv)
         e1.record()
-    pbits = max(min(PART_MIN_BITS, 24), min(24, math.ceil(math.log2(max(1.0, n_ev * ratio / PART_TARGET)))))
+    min_bits = min(PART_MIN_BITS, 24) if N else 0  # lookups want enough partitions (blocks) to spread over
+    pbits = max(min_bits, min(24, math.ceil(math.log2(max(1.0, n_ev * ratio / PART_TARGET)))))
     while True:
         P = 1 << pbits
         sev = torch.empty(max(n_ev, 1), dtype=torch.int64, device=dev)
