@@ -166,9 +166,10 @@ int ng_seg_gather(const ng_u64* src_k, const uint32_t* src_v, ng_u64 region, con
                   ng_i64 nseg, const ng_u64* offsets, ng_u64* dst_k, uint32_t* dst_v, void* stream);
 /* start[p], p = 0..2^pbits, of events sorted by their top pbits (pbits <= 24) */
 int ng_part_bounds(const ng_u64* ev, ng_i64 n, int pbits, ng_i64* start, void* stream);
-/* qk[i] = mix64(ctx_of[i] << 16 | tgt[i]) for ids in [lo, hi), else EMPTY; qv[i] = i */
-int ng_part_lookups(const int* ctx_of, const uint16_t* tgt, ng_i64 N, ng_i64 lo, ng_i64 hi, ng_u64* qk, uint32_t* qv,
-                    void* stream);
+/* lookups of n query positions i = pos[j] (pos NULL: j): qk[j] = mix64(ctx_of[i] << 16 | tgt[i]) for ids in
+ * [lo, hi), else EMPTY; qv[j] = i */
+int ng_part_lookups(const int* ctx_of, const uint16_t* tgt, const int* pos, ng_i64 n, ng_i64 lo, ng_i64 hi,
+                    ng_u64* qk, uint32_t* qv, void* stream);
 /* per partition an LDS hash count of its events; block b's distinct (pair key, count) at out + seg_base[b], seg_cnt[b]
  * of them; qcnt[qv[j]] = the count of lookup j (qk sorted like ev, bounds qstart); flags[0] bit 0: a partition held
  * more than 8192 distinct pairs (repartition with one more bit) */

@@ -90,15 +90,17 @@ __global__ void part_bounds_k(const u64* __restrict__ ev, i64 n, int pbits, i64 
     start[p] = a;
 }
 
-// Lookup i: the mixed pair key of query position i's (context, target) if its context id is in [lo, hi) (else EMPTY,
-// which no mixed pair key equals: mix64 is a bijection and its preimage of EMPTY is no pair key), value i.
-__global__ void part_lookups_k(const int* __restrict__ ctx_of, const u16* __restrict__ tgt, i64 N, i64 lo, i64 hi,
-                               u64* __restrict__ qk, u32* __restrict__ qv) {
-    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
-    if (i >= N) return;
+// Lookup j of query position i = pos[j] (pos NULL: i = j): the mixed pair key of its (context, target) if its
+// context id is in [lo, hi) (else EMPTY, which no mixed pair key equals: mix64 is a bijection and its preimage of
+// EMPTY is no pair key), value i.
+__global__ void part_lookups_k(const int* __restrict__ ctx_of, const u16* __restrict__ tgt, const int* __restrict__ pos,
+                               i64 n, i64 lo, i64 hi, u64* __restrict__ qk, u32* __restrict__ qv) {
+    const i64 j = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    if (j >= n) return;
+    const i64 i = pos ? pos[j] : j;
     const i64 c = ctx_of[i];
-    qk[i] = (c >= lo && c < hi) ? mix64(((u64)c << 16) | tgt[i]) : EMPTY;
-    qv[i] = (u32)i;
+    qk[j] = (c >= lo && c < hi) ? mix64(((u64)c << 16) | tgt[i]) : EMPTY;
+    qv[j] = (u32)i;
 }
 
 #define PT_SLOTS 8192
@@ -476,12 +478,12 @@ extern "C" int ng_part_bounds(const u64* ev, i64 n, int pbits, i64* start, void*
     return (int)hipGetLastError();
 }
 
-// The N query positions' lookups: qk[i] = mix64(ctx_of[i] << 16 | tgt[i]) for context ids in [lo, hi), else EMPTY;
-// qv[i] = i.
-extern "C" int ng_part_lookups(const int* ctx_of, const u16* tgt, i64 N, i64 lo, i64 hi, u64* qk, u32* qv,
-                               void* stream) {
-    if (N <= 0) return 0;
-    part_lookups_k<<<grid_for(N, 256), 256, 0, (hipStream_t)stream>>>(ctx_of, tgt, N, lo, hi, qk, qv);
+// The lookups of n query positions (pos[j], or j with pos NULL): qk[j] = mix64(ctx_of[i] << 16 | tgt[i]) for context
+// ids in [lo, hi), else EMPTY; qv[j] = i.
+extern "C" int ng_part_lookups(const int* ctx_of, const u16* tgt, const int* pos, i64 n, i64 lo, i64 hi, u64* qk,
+                               u32* qv, void* stream) {
+    if (n <= 0) return 0;
+    part_lookups_k<<<grid_for(n, 256), 256, 0, (hipStream_t)stream>>>(ctx_of, tgt, pos, n, lo, hi, qk, qv);
     return (int)hipGetLastError();
 }
 

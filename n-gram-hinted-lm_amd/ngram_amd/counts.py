@@ -307,14 +307,14 @@ class CountBuild:
         self.kernel_events = []
         self.x = x
         N = x.numel()
-        if self.mode in ("engine", "part"):
+        self.grid = torch.cuda.get_device_properties(dev).multi_processor_count * 32
+        if self.mode == "part":
+            return self._counts_part(x, avail, tgt, N, lap)
+        if self.mode == "engine":
             index = {k: QueryIndex(self.elib, x, avail, k) for k in self.levels}
         else:
             index = {k: ValIndex(lib, x, avail, k, max_ids=MAX_IDS) for k in self.levels}
         lap("index")
-        self.grid = torch.cuda.get_device_properties(dev).multi_processor_count * 32
-        if self.mode == "part":
-            return self._counts_part(index, tgt, N, lap)
         caps = self.caps()
         tables = {}
         chunk = max([EMIT_CHUNK] + [(n + 31) // 32 * 32 for n in self.sizes])
@@ -386,10 +386,12 @@ class CountBuild:
         if tot is not None and vi.ids and int(tot.max().item()) >= 1 << 32:
             raise RuntimeError(f"k={k}: a total does not fit uint32")
 
-    def _counts_part(self, index, tgt, N, lap) -> torch.Tensor:
+    def _counts_part(self, x, avail, tgt, N, lap) -> torch.Tensor:
         """counts() in "part" mode: level after level, every shard's scan emits its hits (no global atomics), the
         hits are hash-partitioned by a radix sort of their mixed keys and counted partition by partition in LDS
-        (the query positions' target counts answered there too); then the owner side of the engine mode."""
+        (the query positions' target counts answered there too); then the owner side of the engine mode. A level's
+        query index holds only the positions whose previous level's context occurred (when the level counts no
+        shard the previous one skips): a context occurs only where its suffix does, so the others stay zero."""
         dev, info = self.tok.device, self.info
         nwords = self.L // 32
         bms = {k: torch.zeros(nwords, dtype=torch.int32, device=dev) for k in self.levels}
@@ -405,14 +407,20 @@ class CountBuild:
         G = self.grid
         R = max(emit_region((n + 31) // 32 * 32, G) for n in self.sizes)
         regions = torch.empty(len(self.sizes) * G * R, dtype=torch.int64, device=dev)
-        scan_t = count_t = 0.0
+        scan_t = count_t = index_t = 0.0
         for li, k in enumerate(self.levels):
-            vi = index.pop(k)
+            t0 = time.perf_counter()
+            prev = self.levels[li - 1] if li else None
+            seen = None
+            if prev is not None and self.level_shards[k] <= self.level_shards[prev]:
+                seen = torch.nonzero(out[1, li - 1] > 0).squeeze(1).to(torch.int32)
+            vi = QueryIndex(self.elib, x, avail, k, seen)
+            index_t += time.perf_counter() - t0
             t0 = time.perf_counter()
             ev, n_ev = self._part_emit(k, vi, bms, regions, R)
             t1 = time.perf_counter()
             ev_fn = lambda name, n, k=k: self._event(name, k, -1, n)  # noqa: E731
-            c = count_events(self.elib, self.lib, ev, n_ev, vi.ids, self.dratio.get(k, 1.0), (vi.ctx_of, tgt),
+            c = count_events(self.elib, self.lib, ev, n_ev, vi.ids, self.dratio.get(k, 1.0), (vi.ctx_of, tgt, seen),
                              event=ev_fn)
             del ev
             self.dratio[k] = c.U / max(1, n_ev)
@@ -429,7 +437,7 @@ class CountBuild:
             self._level_rows(k, vi, want, tot, top_tok, top_cnt, row_entries, row_top)
             info[k] = dict(contexts=vi.n, ids=vi.ids, pairs=c.U, events=n_ev, pbits=c.pbits, cap=0, hits=None,
                            reruns=0)
-            del tot, top_tok, top_cnt, vi, c
+            del tot, top_tok, top_cnt, vi, c, seen
         del regions
         if self.stats:
             for k in self.levels:
@@ -438,6 +446,7 @@ class CountBuild:
                 self.density[k] = h / max(1, sum(self.sizes[: self.level_shards[k]]))
         del bms
         lap("outputs")
+        self.timing["part_index_host"] = self.timing.get("part_index_host", 0.0) + index_t
         self.timing["part_scan_host"] = self.timing.get("part_scan_host", 0.0) + scan_t
         self.timing["part_count_host"] = self.timing.get("part_count_host", 0.0) + count_t
         if rows:

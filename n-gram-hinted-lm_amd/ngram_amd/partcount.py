@@ -76,19 +76,21 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor, n_ev: int, n_ids: int, r
                  lookups: tuple | None = None, packed: bool = True, event=_no_event) -> Counted:
     """Count n_ev events of context ids below n_ids. `ratio`: distinct pairs per event expected (sizes the
     partitions; a partition found too full repeats the count with one more bit). `lookups` (ctx_of int32 [N], tgt
-    int16 [N]): qcnt[i] = the count of (ctx_of[i], tgt[i]), 0 where absent or ctx_of[i] is out of range. `packed`:
-    pairs as packed words (falls back to keys + counts when the escape table overflows)."""
+    int16 [N], positions int32 or None): qcnt[i] = the count of (ctx_of[i], tgt[i]) for the listed positions (all
+    without a list), 0 where absent, out of range or not listed. `packed`: pairs as packed words (falls back to keys +
+    counts when the escape table overflows)."""
     dev = ev.device
     cb = max(1, (max(n_ids, 2) - 1).bit_length(), PACK_MIN_BITS) if packed else 0
-    N = 0
+    N = nq = 0
     if lookups is not None:
-        ctx_of, tgt = lookups
+        ctx_of, tgt, qpos = lookups
         N = ctx_of.numel()
-        qk = torch.empty(N, dtype=torch.int64, device=dev)
-        qv = torch.empty(N, dtype=torch.int32, device=dev)
-        e0, e1 = event("partition", N)
+        nq = N if qpos is None else qpos.numel()
+        qk = torch.empty(max(nq, 1), dtype=torch.int64, device=dev)
+        qv = torch.empty(max(nq, 1), dtype=torch.int32, device=dev)
+        e0, e1 = event("partition", nq)
         e0.record()
-        elib("ng_part_lookups", ctx_of, tgt, N, 0, n_ids, qk, qv)
+        elib("ng_part_lookups", ctx_of, tgt, qpos, nq, 0, n_ids, qk, qv)
         e1.record()
     min_bits = min(PART_MIN_BITS, 24) if N else 0  # lookups want enough partitions (blocks) to spread over
     pbits = max(min_bits, min(24, math.ceil(math.log2(max(1.0, n_ev * ratio / PART_TARGET)))))
@@ -103,11 +105,11 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor, n_ev: int, n_ids: int, r
         if n_ev:
             lib.cub("sort_pairs", ev, sev, None, None, n_ev, i32(64 - pbits), i32(64))
         elib("ng_part_bounds", sev, n_ev, i32(pbits), start)
-        if N:
-            sqk = torch.empty(N, dtype=torch.int64, device=dev)
-            sqv = torch.empty(N, dtype=torch.int32, device=dev)
-            lib.cub("sort_pairs", qk, sqk, qv, sqv, N, i32(64 - pbits), i32(64))
-            elib("ng_part_bounds", sqk, N, i32(pbits), qstart)
+        if nq:
+            sqk = torch.empty(nq, dtype=torch.int64, device=dev)
+            sqv = torch.empty(nq, dtype=torch.int32, device=dev)
+            lib.cub("sort_pairs", qk, sqk, qv, sqv, nq, i32(64 - pbits), i32(64))
+            elib("ng_part_bounds", sqk, nq, i32(pbits), qstart)
         e1.record()
         G2 = min(P, PART_BLOCKS)
         out_k = torch.empty(max(n_ev, 1), dtype=torch.int64, device=dev)
