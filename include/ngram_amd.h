@@ -203,13 +203,16 @@ int ng_ctx_kth(const ng_u64* uk, const uint32_t* agg, const ng_i64* start, const
 /* hint rows over table levels (count_table.rs query_rows); desc[v * 5]: slot_of, tot, top_tok, top_cnt, bucket */
 int ng_pos_rows(ng_i64 N, int nlv, const ng_i64* desc, int entries, short* cell, uint16_t* next, uint16_t* weights,
                 signed char* level, void* stream);
-/* online state (online.rs step rule): insert occurrences ending at pos[i]; merge a step's sorted distinct touched
- * pairs (uk[0..*n)) into their contexts' top-E lists; answer queries; build hint rows */
+/* online state (online.rs step rule): insert occurrences ending at pos[i] (ctx_tot/ctx_dist may be NULL: then the
+ * sorted pass adds them); merge a step's sorted distinct touched pairs (uk[0..*n), agg their occurrences in the step)
+ * into their contexts' top-E lists (ctx_top may be NULL) and, given ctx_tot/ctx_dist, their totals and distinct
+ * counts; answer queries; build hint rows */
 int ng_online_insert(const uint16_t* tok, const int* pos, ng_i64 m, int k, ng_u64* ck, ng_u64 ccap, ng_u64* pk,
                      uint32_t* pcnt, ng_u64 pcap, uint32_t* ctx_tot, uint32_t* ctx_dist, ng_u64* ev, uint32_t* flags,
                      void* stream);
-int ng_online_top(const ng_u64* uk, const ng_i64* n, ng_i64 m, const ng_u64* pk, const uint32_t* pcnt, ng_u64 pcap,
-                  ng_u64* score, ng_u64* ctx_top, int E, void* stream);
+int ng_online_top(const ng_u64* uk, const ng_i64* n, ng_i64 m, const uint32_t* agg, const ng_u64* pk,
+                  const uint32_t* pcnt, ng_u64 pcap, ng_u64* score, ng_u64* ctx_top, int E, uint32_t* ctx_tot,
+                  uint32_t* ctx_dist, void* stream);
 int ng_online_query(const uint16_t* tok, const int* avail, const unsigned char* has_next, const int* pos, ng_i64 m,
                     int k, const ng_u64* ck, ng_u64 ccap, const ng_u64* pk, const uint32_t* pcnt, ng_u64 pcap,
                     const uint32_t* ctx_tot, const uint32_t* ctx_dist, int* qslot, uint32_t* tot, uint16_t* dist,

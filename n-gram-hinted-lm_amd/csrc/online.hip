@@ -95,8 +95,10 @@ __global__ void online_insert_k(const u16* __restrict__ tok, const int* __restri
         ev[i] = EMPTY;
         return;
     }
-    atomicAdd(&ctx_tot[slot], 1u);
-    if (added) atomicAdd(&ctx_dist[slot], 1u);
+    if (ctx_tot) {  // else the step's sorted pass (online_top_k) adds them, once per context
+        atomicAdd(&ctx_tot[slot], 1u);
+        if (added) atomicAdd(&ctx_dist[slot], 1u);
+    }
     ev[i] = pair;
 }
 
@@ -124,37 +126,149 @@ __device__ __forceinline__ void top8_insert(u64 (&t)[8], u64 v) {
         }
 }
 
-// One thread per context group of the sorted touched pairs: the context's top-E list merged with the group's new
-// scores (an old entry of a touched token is superseded by its new score).
-__global__ void online_top_k(const u64* __restrict__ uk, const u64* __restrict__ score, const i64* __restrict__ n, i64 m,
-                             u64* __restrict__ ctx_top, int E) {
-    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
-    const i64 nn = *n;
-    if (i >= m || i >= nn) return;
-    const u64 key = uk[i];
-    if (key == EMPTY) return;
-    const u64 c = key >> 16;
-    if (i > 0 && (uk[i - 1] >> 16) == c) return;  // not the group's head
-    i64 j = i;
-    while (j < nn && uk[j] != EMPTY && (uk[j] >> 16) == c) ++j;
-    u64 t[8];
+// A step's touched pairs uk[0..*n) (distinct, sorted; agg[i] = their occurrences in the step, score[i] their ranking
+// scores, count << 16 | 65535 - token), a wave per window of 64: for each context starting in the window, its total
+// and distinct count grow by the step's occurrences and first-seen pairs (plain stores by the context's first lane: no
+// same-address atomics for hot contexts), and (ctx_top not NULL) its top-E list is merged with the new scores (an old
+// entry of a touched token is superseded by its new score: counts only grow). A context ending in its window is done
+// by its first lane from LDS; the one running past the window by the whole wave.
+__global__ void __launch_bounds__(256) online_top_k(const u64* __restrict__ uk, const u64* __restrict__ score,
+                                                    const u32* __restrict__ agg, const i64* __restrict__ n_ptr, i64 m,
+                                                    u64* __restrict__ ctx_top, int E, u32* __restrict__ ctx_tot,
+                                                    u32* __restrict__ ctx_dist) {
+    __shared__ u64 s_key[4][WAVE];
+    __shared__ u64 s_sc[4][WAVE];
+    __shared__ u32 s_ag[4][WAVE];
+    const i64 n = *n_ptr < m ? *n_ptr : m;
+    const int lane = (int)(threadIdx.x & (WAVE - 1)), wid = threadIdx.x / WAVE;
+    const i64 nwin = (n + WAVE - 1) / WAVE;
+    auto ctx_of = [](u64 key) { return key >> 16; };
+    for (i64 wb = (i64)blockIdx.x * 4; wb < nwin; wb += (i64)gridDim.x * 4) {  // the same rounds for every wave
+        const i64 wv = wb + wid;
+        const i64 i = wv * WAVE + lane;
+        u64 key = i < n ? uk[i] : EMPTY;
+        const bool valid = key != EMPTY;
+        const u64 sc = valid ? score[i] : 0;
+        const u32 ag = valid ? agg[i] : 0;
+        s_key[wid][lane] = key;
+        s_sc[wid][lane] = sc;
+        s_ag[wid][lane] = ag;
+        u64 prev = shfl_up_u64(key, 1);
+        if (lane == 0) prev = (valid && i > 0) ? uk[i - 1] : EMPTY;
+        u64 next = shfl_down_u64(key, 1);
+        if (lane == WAVE - 1) next = i + 1 < n ? uk[i + 1] : EMPTY;
+        const u64 c = ctx_of(key);
+        const bool head = valid && (i == 0 || prev == EMPTY || ctx_of(prev) != c);
+        const bool tail = valid && (next == EMPTY || ctx_of(next) != c);
+        const u64 tails = __ballot(tail);
+        __syncthreads();
+        if (head && (tails >> lane)) {  // the context ends in the window: this lane alone, from LDS
+            const int e = lane + __ffsll((unsigned long long)(tails >> lane)) - 1;
+            u32 add = 0, fresh = 0;
+            u64 t[8];
 #pragma unroll
-    for (int r = 0; r < 8; ++r) t[r] = 0;
-    u64* top = ctx_top + c * E;
-    for (int r = 0; r < E; ++r) {
-        const u64 old = top[r];
-        if (old == 0) break;
-        const u64 tk = (c << 16) | (0xFFFFu - (u32)(old & 0xFFFF));
-        i64 a = i, b = j;  // is the token touched in this step? (the group is sorted by token)
-        while (a < b) {
-            const i64 mid = (a + b) >> 1;
-            if (uk[mid] < tk) a = mid + 1;
-            else b = mid;
+            for (int r = 0; r < 8; ++r) t[r] = 0;
+            for (int q = lane; q <= e; ++q) {
+                add += s_ag[wid][q];
+                fresh += (u32)(s_sc[wid][q] >> 16) == s_ag[wid][q];
+                if (ctx_top) top8_insert(t, s_sc[wid][q]);
+            }
+            if (ctx_tot) {
+                ctx_tot[c] += add;
+                ctx_dist[c] += fresh;
+            }
+            if (ctx_top) {
+                u64* top = ctx_top + c * E;
+                for (int r = 0; r < E; ++r) {
+                    const u64 old = top[r];
+                    if (old == 0) break;
+                    const u64 tk = (c << 16) | (0xFFFFu - (u32)(old & 0xFFFF));
+                    bool touched = false;
+                    for (int q = lane; q <= e; ++q) touched |= s_key[wid][q] == tk;
+                    if (!touched) top8_insert(t, old);
+                }
+                for (int r = 0; r < E; ++r) top[r] = t[r];
+            }
         }
-        if (!(a < j && uk[a] == tk)) top8_insert(t, old);
+        const bool open = head && !(tails >> lane);
+        const u64 opens = __ballot(open);
+        if (opens) {  // the context running past the window: the whole wave, over the following windows
+            const int h = __ffsll((unsigned long long)opens) - 1;
+            const u64 hc = bcast_u64(c, h);
+            const i64 gi = wv * WAVE + h;
+            const bool in = valid && lane >= h;
+            u64 add = in ? ag : 0, fresh = (in && (u32)(sc >> 16) == ag) ? 1 : 0;
+            u64 lt[8];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) lt[r] = 0;
+            if (in && ctx_top) lt[0] = sc;
+            i64 ge = wv * WAVE + WAVE;  // the group's end, found below
+            bool cont = true;
+            for (i64 nx = wv * WAVE + WAVE; cont; nx += WAVE) {
+                const i64 j = nx + lane;
+                const u64 k2 = j < n ? uk[j] : EMPTY;
+                const bool in2 = k2 != EMPTY && ctx_of(k2) == hc;
+                const u64 m2 = __ballot(in2);
+                if (in2) {
+                    const u64 s2 = score[j];
+                    const u32 a2 = agg[j];
+                    add += a2;
+                    fresh += (u32)(s2 >> 16) == a2;
+                    if (ctx_top) top8_insert(lt, s2);
+                }
+                ge = nx + __popcll(m2);
+                cont = ((m2 >> (WAVE - 1)) & 1ull) && nx + WAVE < n;
+            }
+#pragma unroll
+            for (int d = WAVE / 2; d > 0; d >>= 1) {
+                add += shfl_down_u64(add, d);
+                fresh += shfl_down_u64(fresh, d);
+            }
+            if (lane == 0 && ctx_tot) {
+                ctx_tot[hc] += (u32)add;
+                ctx_dist[hc] += (u32)fresh;
+            }
+            if (ctx_top) {
+                u64* top = ctx_top + hc * E;
+                if (lane < E) {  // lane r checks old entry r: kept unless its token was touched in the step
+                    const u64 old = top[lane];
+                    if (old != 0) {
+                        const u64 tk = (hc << 16) | (0xFFFFu - (u32)(old & 0xFFFF));
+                        i64 a = gi, b = ge;
+                        while (a < b) {
+                            const i64 mid = (a + b) >> 1;
+                            if (uk[mid] < tk) a = mid + 1;
+                            else b = mid;
+                        }
+                        if (!(a < ge && uk[a] == tk)) top8_insert(lt, old);
+                    }
+                }
+                // merge the lanes' lists: E rounds of a wave-wide maximum; the lane holding it moves on (scores are
+                // distinct within a context)
+                int headq = 0;
+                u64 merged[8];
+#pragma unroll
+                for (int r = 0; r < 8; ++r) {
+                    u64 mine = 0;
+#pragma unroll
+                    for (int q = 0; q < 8; ++q)
+                        if (q == headq) mine = lt[q];
+                    u64 mx = mine;
+#pragma unroll
+                    for (int d = WAVE / 2; d > 0; d >>= 1) {
+                        const u64 o = shfl_down_u64(mx, d);
+                        mx = o > mx ? o : mx;
+                    }
+                    mx = bcast_u64(mx, 0);
+                    merged[r] = mx;
+                    if (mx != 0 && mine == mx) ++headq;
+                }
+                if (lane == 0)
+                    for (int r = 0; r < E; ++r) top[r] = merged[r];
+            }
+        }
+        __syncthreads();
     }
-    for (i64 q = i; q < j; ++q) top8_insert(t, score[q]);
-    for (int r = 0; r < E; ++r) top[r] = t[r];
 }
 
 // Queries at pos[i] (input position g, context tok[g-k+1..g] valid iff avail[g] >= k): per level its context's
@@ -264,14 +378,20 @@ extern "C" int ng_online_insert(const u16* tok, const int* pos, i64 m, int k, u6
     return (int)hipGetLastError();
 }
 
-// The distinct touched pairs uk[0..*n) (sorted) merged into their contexts' top-E lists (score: scratch [m]).
-extern "C" int ng_online_top(const u64* uk, const i64* n, i64 m, const u64* pk, const u32* pcnt, u64 pcap, u64* score,
-                             u64* ctx_top, int E, void* stream) {
+// The step's distinct touched pairs uk[0..*n) (sorted; agg: their occurrences in the step) merged into their
+// contexts' top-E lists (ctx_top may be NULL) and, when ctx_tot is given (the insert was called without it), added
+// to their contexts' totals and distinct counts. score: scratch [m].
+extern "C" int ng_online_top(const u64* uk, const i64* n, i64 m, const u32* agg, const u64* pk, const u32* pcnt,
+                             u64 pcap, u64* score, u64* ctx_top, int E, u32* ctx_tot, u32* ctx_dist, void* stream) {
     if (E < 1 || E > 8) return -1;
+    if ((ctx_tot == nullptr) != (ctx_dist == nullptr)) return -1;
     if (m <= 0) return 0;
     hipStream_t st = (hipStream_t)stream;
     online_scores_k<<<grid_for(m, 256), 256, 0, st>>>(uk, n, m, pk, pcnt, pcap, score);
-    online_top_k<<<grid_for(m, 256), 256, 0, st>>>(uk, score, n, m, ctx_top, E);
+    const i64 wins = (m + WAVE - 1) / WAVE;
+    const i64 g = (wins + 3) / 4;
+    online_top_k<<<(unsigned)(g < 65536 ? g : 65536), 256, 0, st>>>(uk, score, agg, n, m, ctx_top, E, ctx_tot,
+                                                                     ctx_dist);
     return (int)hipGetLastError();
 }
 

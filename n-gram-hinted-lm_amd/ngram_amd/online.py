@@ -186,13 +186,14 @@ class OnlineRows:
             if m == 0:
                 continue
             ev = st["ev"][:m]
+            # the totals and distinct counts are added per context by the sorted pass (ng_online_top), not per
+            # occurrence: hot contexts would make chains of same-address atomics
             lib("ng_online_insert", self.tok, lv["occ"][a:b], m, i32(k), lv["ck"], u64(lv["ccap"]), lv["pk"], lv["pcnt"],
-                u64(lv["pcap"]), lv["tot"], lv["dist"], ev, lv["flags"])
-            if k in levels:
-                lib.cub("sort_pairs", ev, st["ev_sorted"], None, None, m, i32(0), i32(min(64, 16 + lv["ctx_bits"])))
-                lib.cub("reduce_by_key", st["ev_sorted"], st["uk"], st["ones"], st["agg"], st["nruns"], m)
-                lib("ng_online_top", st["uk"], st["nruns"], m, lv["pk"], lv["pcnt"], u64(lv["pcap"]), st["score"],
-                    lv["top"], i32(E))
+                u64(lv["pcap"]), None, None, ev, lv["flags"])
+            lib.cub("sort_pairs", ev, st["ev_sorted"], None, None, m, i32(0), i32(min(64, 16 + lv["ctx_bits"])))
+            lib.cub("reduce_by_key", st["ev_sorted"], st["uk"], st["ones"], st["agg"], st["nruns"], m)
+            lib("ng_online_top", st["uk"], st["nruns"], m, st["agg"], lv["pk"], lv["pcnt"], u64(lv["pcap"]), st["score"],
+                lv["top"] if k in levels else None, i32(E), lv["tot"], lv["dist"])
         qa, qb = self._range(st["q_step"], s, s + 1)
         mq = qb - qa
         if mq == 0 or not queries:
