@@ -30,6 +30,7 @@ from .partcount import count_events, emit_region, pack_events, record_tops, summ
 from .qindex import QueryIndex
 
 GAP = 32
+SCAN_BLOCKS_PER_CU = 32  # level-scan blocks (grid-stride) per compute unit
 LEVELS = (2, 3, 4, 5, 6, 10, 20)
 LEVEL_SHARDS = {2: 103, 3: 370, 4: 370, 5: 370}
 PAIRS = {2: (82.17e6, 0.620), 3: (62.30e6, 0.667), 4: (26.39e6, 0.694), 5: (8.99e6, 0.706), 6: (3.17e6, 0.705),
@@ -307,7 +308,7 @@ class CountBuild:
         self.kernel_events = []
         self.x = x
         N = x.numel()
-        self.grid = torch.cuda.get_device_properties(dev).multi_processor_count * 32
+        self.grid = torch.cuda.get_device_properties(dev).multi_processor_count * SCAN_BLOCKS_PER_CU
         if self.mode == "part":
             return self._counts_part(x, avail, tgt, N, lap)
         if self.mode == "engine":
