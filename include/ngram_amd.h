@@ -181,7 +181,8 @@ int ng_part_count(const ng_u64* ev, const ng_i64* start, int pbits, const ng_u64
  * esc = 2^(48 - cb) - 1, larger counts also into the escape table esc_k/esc_c (EMPTY-filled; full: flags[0] bit 1).
  * From such words sorted by context: dist[c] (pairs) and the record rec[c] of each present context (callers zero
  * dist): u32 words total, pairs, the first topk (1, 2, 4, 8) tokens by (count desc, token asc) two per word, their
- * counts (4, 8, 8, 16 words for topk 1, 2, 4, 8); flags[0] bit 2: a total reached 2^32 */
+ * counts (4, 8, 8, 16 words for topk 1, 2, 4, 8; for topk 2 and 8 also the index of the context's first word, u64
+ * in the two words after the counts); flags[0] bit 2: a total reached 2^32 */
 int ng_ctx_summary(const ng_u64* w, ng_i64 U, int cb, const ng_u64* esc_k, const uint32_t* esc_c, ng_u64 esc_cap,
                    int topk, uint32_t* rec, uint32_t* dist, uint32_t* flags, void* stream);
 /* per query position from ng_ctx_summary's records and pair counts and the counted lookups qcnt (may be NULL: no
@@ -191,16 +192,25 @@ int ng_pos_summary(const int* ctx_of, ng_i64 N, ng_i64 lo, ng_i64 hi, const uint
                    const uint32_t* dist, const ng_u64* thr, const uint32_t* qcnt, int ktop, int kout, int li,
                    int* out_tot, int* out_dist, int* out_cnt, uint16_t* out_tok, uint32_t* out_tcnt, int* mask,
                    void* stream);
-/* corpus-wide level build (count_table.rs build_level): contexts into ck (slot = id), (slot << 16 | next) counted in
- * the split table pk/pcnt; flags[0] bit 0 pair table full, bit 1 context table full */
-int ng_table_build(const uint16_t* tok, ng_i64 L, int k, ng_u64* ck, ng_u64 ccap, ng_u64* pk, uint32_t* pcnt,
-                   ng_u64 pcap, uint32_t* flags, int grid, void* stream);
+/* corpus-wide level build (count_table.rs build_level :491-631): contexts into ck (slot = id) and per corpus position
+ * its event ev[p] = mix64(slot << 16 | next) (EMPTY: none), counted afterwards by the partitioned count; flags[0]
+ * bit 1: context table full (rerun bigger) */
+int ng_table_emit(const uint16_t* tok, ng_i64 L, int k, ng_u64* ck, ng_u64 ccap, ng_u64* ev, uint32_t* flags,
+                  int grid, void* stream);
 /* per key (EMPTY: none) its context-table slot or -1 */
 int ng_table_lookup(const ng_u64* keys, ng_i64 n, const ng_u64* ck, ng_u64 ccap, int* slot, void* stream);
-/* thr[c] = the kth largest pair score of each listed context (ids[m]; count_table.rs deep_last) */
-int ng_ctx_kth(const ng_u64* uk, const uint32_t* agg, const ng_i64* start, const ng_i64* end, const ng_i64* ids,
-               ng_i64 m, int kth, ng_u64* thr, void* stream);
-/* hint rows over table levels (count_table.rs query_rows); desc[v * 5]: slot_of, tot, top_tok, top_cnt, bucket */
+/* thr[c] = the kth largest pair score of each listed context (ids[m]; count_table.rs:146-158 deep_last) over packed
+ * words sorted by pair key and ng_ctx_summary's topk-8 records */
+int ng_ctx_kth(const ng_u64* w, int cb, const ng_u64* esc_k, const uint32_t* esc_c, ng_u64 esc_cap,
+               const uint32_t* rec, const ng_i64* ids, ng_i64 m, int kth, ng_u64* thr, void* stream);
+/* per query position (count_table.rs query_counts :291-331): tot, dist, cnt (CNT_TOP rule by thr, NULL: none) and
+ * the first kout top entries of its level-k context, from the context table, the packed words sorted by pair key and
+ * the topk-8 records */
+int ng_table_query(const uint16_t* x, const int* avail, const uint16_t* tgt, ng_i64 n, int k, const ng_u64* ck,
+                   ng_u64 ccap, const ng_u64* w, int cb, const ng_u64* esc_k, const uint32_t* esc_c, ng_u64 esc_cap,
+                   const uint32_t* rec, const ng_u64* thr, uint32_t cnt_top, int kout, int* out_tot, int* out_dist,
+                   int* out_cnt, uint16_t* out_tok, uint32_t* out_tcnt, void* stream);
+/* hint rows over table levels (count_table.rs query_rows :338-404); desc[v * 3]: slot_of, records, bucket */
 int ng_pos_rows(ng_i64 N, int nlv, const ng_i64* desc, int entries, short* cell, uint16_t* next, uint16_t* weights,
                 signed char* level, void* stream);
 /* online state (online.rs step rule): insert occurrences ending at pos[i] (ctx_tot/ctx_dist may be NULL: then the

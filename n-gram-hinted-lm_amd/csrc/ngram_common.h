@@ -167,3 +167,32 @@ __device__ __forceinline__ void topk_insert(u64 (&t)[KT], u64 v) {
 
 // The ranking score of pair key (context << 16 | token) with count n: count descending, then token ascending.
 __device__ __forceinline__ u64 rank_score(u64 key, u32 n) { return ((u64)n << 16) | (0xFFFFu - (u32)(key & 0xFFFF)); }
+
+// A corpus-wide context table (u64 keys, slot = context id, linear probing with wrap-around from umulhi(key, cap)):
+// the slot of `key`, inserted if absent, or -1 after MAXPROBE probes (flags[0] |= 2).
+__device__ __forceinline__ i64 ctx_find_insert(u64* ck, u64 ccap, u64 key, u32* flags) {
+    u64 s = __umul64hi(key, ccap);
+    for (int probe = 0; probe < MAXPROBE; ++probe) {
+        const u64 cur = ck[s];
+        if (cur == key) return (i64)s;
+        if (cur == EMPTY) {
+            const u64 prev = atomicCAS((unsigned long long*)&ck[s], EMPTY, key);
+            if (prev == EMPTY || prev == key) return (i64)s;
+        }
+        s = s + 1 == ccap ? 0 : s + 1;
+    }
+    atomicOr(&flags[0], 2u);
+    return -1;
+}
+
+// The slot of `key` in such a table, or -1.
+__device__ __forceinline__ i64 ctx_find(const u64* __restrict__ ck, u64 ccap, u64 key) {
+    u64 s = __umul64hi(key, ccap);
+    for (u64 probe = 0; probe < ccap; ++probe) {
+        const u64 cur = ck[s];
+        if (cur == key) return (i64)s;
+        if (cur == EMPTY) return -1;
+        s = s + 1 == ccap ? 0 : s + 1;
+    }
+    return -1;
+}

@@ -1,0 +1,84 @@
+// Device code shared by the partitioned count (part.hip) and the corpus-wide count tables (table.hip): mix64's
+// inverse, the escape table of packed words' large counts, and the per-context record.
+#pragma once
+#include "ngram_common.h"
+
+namespace {
+
+// mix64's inverse: each step undone in reverse order. A right xorshift by s is undone by r <- h ^ (r >> s) (each round
+// fixes s more bits from the top: three rounds cover 64 bits for s >= 22); a product by an odd constant by the product
+// by its inverse modulo 2^64.
+__device__ __forceinline__ u64 unxorshift(u64 h, int s) {
+    u64 r = h;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) r = h ^ (r >> s);
+    return r;
+}
+__device__ __forceinline__ u64 unmix64(u64 h) {
+    h = unxorshift(h, 31);
+    h *= 0x319642b2d24d8ec3ull;  // 0x94d049bb133111eb^-1 mod 2^64
+    h = unxorshift(h, 27);
+    h *= 0x96de1b173f119089ull;  // 0xbf58476d1ce4e5b9^-1 mod 2^64
+    return unxorshift(h, 30);
+}
+
+// A count too large for a packed word's count field: (pair key, count) into the escape table (linear probing; each
+// distinct pair is written once). A full table sets flags[0] bit 1.
+__device__ __forceinline__ void esc_put(u64* esc_k, u32* esc_c, u64 cap, u64 key, u32 n, u32* flags) {
+    u64 s = __umul64hi(mix64(key), cap);
+    for (u64 probe = 0; probe < cap; ++probe) {
+        if (atomicCAS((unsigned long long*)&esc_k[s], EMPTY, key) == EMPTY) {
+            esc_c[s] = n;
+            return;
+        }
+        s = s + 1 == cap ? 0 : s + 1;
+    }
+    atomicOr(&flags[0], 2u);
+}
+
+__device__ __forceinline__ u32 esc_get(const u64* __restrict__ esc_k, const u32* __restrict__ esc_c, u64 cap, u64 key) {
+    u64 s = __umul64hi(mix64(key), cap);
+    for (u64 probe = 0; probe < cap; ++probe) {
+        const u64 cur = esc_k[s];
+        if (cur == key) return esc_c[s];
+        if (cur == EMPTY) return 0;
+        s = s + 1 == cap ? 0 : s + 1;
+    }
+    return 0;
+}
+
+// A context's record, WORDS u32: total, pairs, the first KT tokens two per word, their counts, and where two words are
+// left (KT 2 and 8) the index of the context's first packed word (u64, low word first); zeros elsewhere.
+template <int KT>
+struct CtxRecord {
+    static constexpr int TOKW = (KT + 1) / 2;
+    static constexpr int USED = 2 + TOKW + KT;
+    static constexpr int WORDS = USED <= 4 ? 4 : USED <= 8 ? 8 : 16;
+    static constexpr int FIRST = WORDS - USED >= 2 ? USED : -1;
+};
+
+template <int KT>
+__device__ __forceinline__ void store_record(u32* __restrict__ rec, u64 c, u64 total, u32 pairs, const u64 (&top)[KT],
+                                             u64 first) {
+    using R = CtxRecord<KT>;
+    u32 v[R::WORDS];
+#pragma unroll
+    for (int q = 0; q < R::WORDS; ++q) v[q] = 0;
+    v[0] = (u32)total;
+    v[1] = pairs;
+    if constexpr (R::FIRST >= 0) {
+        v[R::FIRST] = (u32)first;
+        v[R::FIRST + 1] = (u32)(first >> 32);
+    }
+#pragma unroll
+    for (int r = 0; r < KT; ++r) {
+        const u32 tk = top[r] ? 0xFFFFu - (u32)(top[r] & 0xFFFF) : 0u;
+        v[2 + r / 2] |= tk << (16 * (r & 1));
+        v[2 + R::TOKW + r] = (u32)(top[r] >> 16);
+    }
+    uint4* dst = (uint4*)(rec + c * R::WORDS);
+#pragma unroll
+    for (int q = 0; q < R::WORDS / 4; ++q) dst[q] = make_uint4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+}
+
+}  // namespace

@@ -12,26 +12,9 @@
 //      segment, which ng_seg_gather packs again.
 // Every event is read three times and written twice, in coalesced runs, and counted by LDS atomics; on MI355X global
 // atomics run at about 27 G/s scattered and 80 M/s on one address, far below these streams.
-#include "ngram_common.h"
+#include "part.h"
 
 namespace {
-
-// mix64's inverse: each step undone in reverse order. A right xorshift by s is undone by r <- h ^ (r >> s) (each round
-// fixes s more bits from the top: three rounds cover 64 bits for s >= 22); a product by an odd constant by the product
-// by its inverse modulo 2^64.
-__device__ __forceinline__ u64 unxorshift(u64 h, int s) {
-    u64 r = h;
-#pragma unroll
-    for (int i = 0; i < 3; ++i) r = h ^ (r >> s);
-    return r;
-}
-__device__ __forceinline__ u64 unmix64(u64 h) {
-    h = unxorshift(h, 31);
-    h *= 0x319642b2d24d8ec3ull;  // 0x94d049bb133111eb^-1 mod 2^64
-    h = unxorshift(h, 27);
-    h *= 0x96de1b173f119089ull;  // 0xbf58476d1ce4e5b9^-1 mod 2^64
-    return unxorshift(h, 30);
-}
 
 // offsets[s] = cnt[0] + ... + cnt[s - 1], offsets[n] = the total: one block of 1024 threads, each a contiguous chunk.
 __global__ void __launch_bounds__(1024) seg_offsets_k(const u32* __restrict__ cnt, i64 n, u64* __restrict__ off) {
@@ -139,31 +122,6 @@ __device__ __forceinline__ u32 pt_find(const u64* tk, const u32* tc, u64 key) {
     return 0;
 }
 
-// A count too large for a packed word's count field: (pair key, count) into the escape table (linear probing; each
-// distinct pair is written once). A full table sets flags[0] bit 1.
-__device__ __forceinline__ void esc_put(u64* esc_k, u32* esc_c, u64 cap, u64 key, u32 n, u32* flags) {
-    u64 s = __umul64hi(mix64(key), cap);
-    for (u64 probe = 0; probe < cap; ++probe) {
-        if (atomicCAS((unsigned long long*)&esc_k[s], EMPTY, key) == EMPTY) {
-            esc_c[s] = n;
-            return;
-        }
-        s = s + 1 == cap ? 0 : s + 1;
-    }
-    atomicOr(&flags[0], 2u);
-}
-
-__device__ __forceinline__ u32 esc_get(const u64* __restrict__ esc_k, const u32* __restrict__ esc_c, u64 cap, u64 key) {
-    u64 s = __umul64hi(mix64(key), cap);
-    for (u64 probe = 0; probe < cap; ++probe) {
-        const u64 cur = esc_k[s];
-        if (cur == key) return esc_c[s];
-        if (cur == EMPTY) return 0;
-        s = s + 1 == cap ? 0 : s + 1;
-    }
-    return 0;
-}
-
 // Block b counts partitions [b * ppb, (b + 1) * ppb) in turn. Its distinct pairs (at most its events) go to
 // out[start[p0] ...]: segment b = (seg_base[b], seg_cnt[b]). qcnt[qv[j]] = the count of lookup j (0: absent).
 // cb == 0: out_k = pair key, out_c = count. cb > 0 (context ids below 2^cb, cb <= 44): out_k = the packed word
@@ -253,40 +211,14 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
     }
 }
 
-template <int KT>
-struct CtxRecord {
-    static constexpr int TOKW = (KT + 1) / 2;
-    static constexpr int USED = 2 + TOKW + KT;
-    static constexpr int WORDS = USED <= 4 ? 4 : USED <= 8 ? 8 : 16;
-};
-
-template <int KT>
-__device__ __forceinline__ void store_record(u32* __restrict__ rec, u64 c, u64 total, u32 pairs, const u64 (&top)[KT]) {
-    using R = CtxRecord<KT>;
-    u32 v[R::WORDS];
-#pragma unroll
-    for (int q = 0; q < R::WORDS; ++q) v[q] = 0;
-    v[0] = (u32)total;
-    v[1] = pairs;
-#pragma unroll
-    for (int r = 0; r < KT; ++r) {
-        const u32 tk = top[r] ? 0xFFFFu - (u32)(top[r] & 0xFFFF) : 0u;
-        v[2 + r / 2] |= tk << (16 * (r & 1));
-        v[2 + R::TOKW + r] = (u32)(top[r] >> 16);
-    }
-    uint4* dst = (uint4*)(rec + c * R::WORDS);
-#pragma unroll
-    for (int q = 0; q < R::WORDS / 4; ++q) dst[q] = make_uint4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
-}
-
 // Per context from packed words sorted by context (word >> (64 - cb)): a wave per window of 64 words, staged in LDS.
 // A lane holding a context's first word whose context also ends in the window walks it in LDS alone (every such lane
 // at once); the one context that runs past the window's end, if it starts there, is done by the whole wave over the
 // following windows' leading words, counts summed and the top KT kept per lane, then reduced across the wave. No
 // dependent global loads: every word is read by its own window and at most once more by the window of its context's
 // first word. For present contexts only: dist[c] = its pairs, and its record rec[c] (CtxRecord<KT>::WORDS u32: total,
-// pairs, the first KT tokens by (count desc, token asc) two per word, their counts; 0-padded), stored whole as 16-byte
-// vectors; flags[0] bit 2 if a total reaches 2^32.
+// pairs, the first KT tokens by (count desc, token asc) two per word, their counts; 0-padded; for KT 2 and 8 also the
+// index of its first word), stored whole as 16-byte vectors; flags[0] bit 2 if a total reaches 2^32.
 template <int KT>
 __global__ void __launch_bounds__(256) ctx_summary_k(const u64* __restrict__ w, i64 U, int cb,
                                                      const u64* __restrict__ esc_k, const u32* __restrict__ esc_c,
@@ -337,7 +269,7 @@ __global__ void __launch_bounds__(256) ctx_summary_k(const u64* __restrict__ w, 
                     topk_insert<KT>(tl, rank_score(wj >> csh, n));
                 }
                 dist[ctx] = (u32)(e - lane + 1);
-                store_record<KT>(rec, ctx, s, (u32)(e - lane + 1), tl);
+                store_record<KT>(rec, ctx, s, (u32)(e - lane + 1), tl, (u64)i);
                 if (s >> 32) atomicOr(&flags[0], 4u);
             }
         }
@@ -395,7 +327,7 @@ __global__ void __launch_bounds__(256) ctx_summary_k(const u64* __restrict__ w, 
             }
             if (lane == h) {
                 dist[hc] = len;
-                store_record<KT>(rec, hc, part, len, merged);
+                store_record<KT>(rec, hc, part, len, merged, (u64)(wv * WAVE + h));
                 if (part >> 32) atomicOr(&flags[0], 4u);
             }
         }

@@ -5,73 +5,33 @@
 // Per level k: every corpus position p whose k tokens before it and its next token lie in one shard (the corpus is
 // laid out with SENT gaps, so a context holding a SENT is skipped) inserts its context key (ngram_common.h ctx_key:
 // packed tokens through SplitMix64's finalizer for k <= 4, exact; a polynomial hash for k > 4, ~2^-64 per pair to
-// merge two contexts, as count_table.rs:11-14) into an open-addressing context table (slot = context id), then counts
-// (slot << 16 | next) in a split pair table (engine.hip's layout). Afterwards the engine's owner side: compaction, one
-// sort, per-context totals and top entries, plus here the count threshold of the CNT_TOP rule for contexts with more
-// than CNT_TOP next tokens (the score of their CNT_TOP-th ranked pair, count_table.rs:146-158 deep_last).
+// merge two contexts, as count_table.rs:11-14) into an open-addressing context table (slot = context id) and writes
+// the event mix64(slot << 16 | next) at its own index (EMPTY where it has none). The events are then counted by the
+// partitioned count (part.hip: no global atomics) into packed words (pair key << (48 - cb) | count), sorted by pair
+// key, and summarized per context into records (total, pairs, top 8, first word). A query reads its context's record
+// and finds its target's count by a binary search of the context's words; the CNT_TOP rule (count_table.rs:146-158
+// deep_last) compares its score with thr[c], the CNT_TOP-th largest score of a context with more pairs than that.
 #include "pairs.h"
+#include "part.h"
 
 namespace {
 
-// The context table's slot of `key` (inserted if absent), or -1 after MAXPROBE probes (flags[0] |= 2).
-__device__ __forceinline__ i64 ctx_find_insert(u64* ck, u64 ccap, u64 key, u32* flags) {
-    u64 s = __umul64hi(key, ccap);
-    for (int probe = 0; probe < MAXPROBE; ++probe) {
-        const u64 cur = ck[s];
-        if (cur == key) return (i64)s;
-        if (cur == EMPTY) {
-            const u64 prev = atomicCAS((unsigned long long*)&ck[s], EMPTY, key);
-            if (prev == EMPTY || prev == key) return (i64)s;
-        }
-        s = s + 1 == ccap ? 0 : s + 1;
-    }
-    atomicOr(&flags[0], 2u);
-    return -1;
-}
-
-__device__ __forceinline__ i64 ctx_find(const u64* __restrict__ ck, u64 ccap, u64 key) {
-    u64 s = __umul64hi(key, ccap);
-    for (u64 probe = 0; probe < ccap; ++probe) {
-        const u64 cur = ck[s];
-        if (cur == key) return (i64)s;
-        if (cur == EMPTY) return -1;
-        s = s + 1 == ccap ? 0 : s + 1;
-    }
-    return -1;
-}
-
-__device__ __forceinline__ void pair_split_add(u64* keys, u32* cnts, u64 cap, u64 key, u32* flags) {
-    u64 s = __umul64hi(mix64(key), cap);
-    for (int probe = 0; probe < MAXPROBE; ++probe) {
-        const u64 cur = keys[s];
-        if (cur == key) {
-            atomicAdd(&cnts[s], 1u);
-            return;
-        }
-        if (cur == EMPTY) {
-            const u64 prev = atomicCAS((unsigned long long*)&keys[s], EMPTY, key);
-            if (prev == EMPTY || prev == key) {
-                atomicAdd(&cnts[s], 1u);
-                return;
+template <int K>
+__global__ void __launch_bounds__(256) table_emit_k(const u16* __restrict__ tok, i64 L, int k, u64* ck, u64 ccap,
+                                                    u64* __restrict__ ev, u32* flags) {
+    for (i64 p = blockIdx.x * (i64)blockDim.x + threadIdx.x; p < L; p += (i64)gridDim.x * blockDim.x) {
+        if (*(volatile u32*)&flags[0]) return;  // the context table overflowed: the level reruns bigger
+        const u32 nxt = tok[p];
+        u64 e = EMPTY;
+        if (nxt != SENT) {
+            const u64 key = ctx_key_stop<K>(tok + p, k);
+            if (key != EMPTY) {
+                const i64 s = ctx_find_insert(ck, ccap, key, flags);
+                if (s < 0) return;
+                e = mix64(((u64)s << 16) | nxt);
             }
         }
-        s = s + 1 == cap ? 0 : s + 1;
-    }
-    atomicOr(&flags[0], 1u);
-}
-
-template <int K>
-__global__ void __launch_bounds__(256) table_build_k(const u16* __restrict__ tok, i64 L, int k, u64* ck, u64 ccap,
-                                                     u64* pk, u32* pcnt, u64 pcap, u32* flags) {
-    for (i64 p = blockIdx.x * (i64)blockDim.x + threadIdx.x; p < L; p += (i64)gridDim.x * blockDim.x) {
-        if (*(volatile u32*)&flags[0]) return;  // a table overflowed: the level reruns bigger
-        const u32 nxt = tok[p];
-        if (nxt == SENT) continue;
-        const u64 key = ctx_key_stop<K>(tok + p, k);
-        if (key == EMPTY) continue;
-        const i64 s = ctx_find_insert(ck, ccap, key, flags);
-        if (s < 0) return;
-        pair_split_add(pk, pcnt, pcap, ((u64)s << 16) | nxt, flags);
+        ev[p] = e;
     }
 }
 
@@ -83,27 +43,42 @@ __global__ void table_lookup_k(const u64* __restrict__ keys, i64 n, const u64* _
     slot[i] = key == EMPTY ? -1 : (int)ctx_find(ck, ccap, key);
 }
 
-__device__ __forceinline__ u64 rank_score_t(u64 key, u32 n) { return ((u64)n << 16) | (0xFFFFu - (u32)(key & 0xFFFF)); }
+using Rec8 = CtxRecord<8>;
 
-// One block per listed context c = ids[b] with more than kth pairs: thr[c] = the kth largest pair score
-// (count << 16 | (65535 - token)) by a radix select over 48-bit scores, 12 bits per round.
-__global__ void __launch_bounds__(256) ctx_kth_k(const u64* __restrict__ uk, const u32* __restrict__ agg,
-                                                 const i64* __restrict__ start, const i64* __restrict__ end,
+__device__ __forceinline__ u64 rec_first(const u32* __restrict__ r) {
+    return (u64)r[Rec8::FIRST] | ((u64)r[Rec8::FIRST + 1] << 32);
+}
+
+__device__ __forceinline__ u32 word_count(u64 word, int csh, const u64* __restrict__ esc_k,
+                                          const u32* __restrict__ esc_c, u64 esc_cap) {
+    const u64 esc = (1ull << csh) - 1;
+    const u64 n = word & esc;
+    return n < esc ? (u32)n : esc_get(esc_k, esc_c, esc_cap, word >> csh);
+}
+
+// One block per listed context c = ids[b] (with more than kth pairs): thr[c] = the kth largest score rank_score(pair
+// key, count) among its packed words (w sorted by pair key; its range from its record), by a radix select over the
+// 48-bit scores, 12 bits per round.
+__global__ void __launch_bounds__(256) ctx_kth_k(const u64* __restrict__ w, int cb, const u64* __restrict__ esc_k,
+                                                 const u32* __restrict__ esc_c, u64 esc_cap, const u32* __restrict__ rec,
                                                  const i64* __restrict__ ids, i64 m, int kth, u64* __restrict__ thr) {
     __shared__ u32 hist[4096];
     __shared__ u64 s_prefix;
     __shared__ u32 s_need;
+    const int csh = 48 - cb;
     for (i64 b = blockIdx.x; b < m; b += gridDim.x) {
         const i64 c = ids[b];
-        const i64 a = start[c], e = end[c];
-        u64 prefix = 0;          // the selected score's bits above the current round
-        u32 need = (u32)kth;     // its rank among the scores matching prefix (1 = the largest)
+        const u32* r = rec + c * Rec8::WORDS;
+        const i64 a = (i64)rec_first(r), e = a + r[1];
+        u64 prefix = 0;       // the selected score's bits above the current round
+        u32 need = (u32)kth;  // its rank among the scores matching prefix (1 = the largest)
         for (int round = 0; round < 4; ++round) {
             const int shift = 36 - 12 * round;
             for (int i = threadIdx.x; i < 4096; i += blockDim.x) hist[i] = 0;
             __syncthreads();
             for (i64 j = a + threadIdx.x; j < e; j += blockDim.x) {
-                const u64 sc = rank_score_t(uk[j], agg[j]);
+                const u64 wj = w[j];
+                const u64 sc = rank_score(wj >> csh, word_count(wj, csh, esc_k, esc_c, esc_cap));
                 if (round == 0 || (sc >> (shift + 12)) == (prefix >> (shift + 12)))
                     atomicAdd(&hist[(sc >> shift) & 0xFFF], 1u);
             }
@@ -127,11 +102,66 @@ __global__ void __launch_bounds__(256) ctx_kth_k(const u64* __restrict__ uk, con
     }
 }
 
+// Per query position i whose k-context x[i-k+1..i] lies in its segment (avail[i] >= k) and occurred (context id c):
+// tot and dist (at most 65535) from rec[c], the first kout top entries, and cnt = the count of (c, tgt[i]) found by a
+// binary search of the context's words, kept only if the context has at most cnt_top pairs or thr is NULL or its
+// score reaches thr[c]. Positions without a context are left as they are.
+template <int K>
+__global__ void __launch_bounds__(256) table_query_k(const u16* __restrict__ x, const int* __restrict__ avail,
+                                                     const u16* __restrict__ tgt, i64 n, int k,
+                                                     const u64* __restrict__ ck, u64 ccap, const u64* __restrict__ w,
+                                                     int cb, const u64* __restrict__ esc_k,
+                                                     const u32* __restrict__ esc_c, u64 esc_cap,
+                                                     const u32* __restrict__ rec, const u64* __restrict__ thr,
+                                                     u32 cnt_top, int kout, int* __restrict__ out_tot,
+                                                     int* __restrict__ out_dist, int* __restrict__ out_cnt,
+                                                     u16* __restrict__ out_tok, u32* __restrict__ out_tcnt) {
+    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    if (i >= n || avail[i] < klen<K>(k)) return;
+    const i64 c = ctx_find(ck, ccap, key_at<K>(x + i + 1, k));
+    if (c < 0) return;
+    u32 v[Rec8::WORDS];
+    const uint4* src = (const uint4*)(rec + c * Rec8::WORDS);
+#pragma unroll
+    for (int q = 0; q < Rec8::WORDS / 4; ++q) {
+        const uint4 t = src[q];
+        v[4 * q] = t.x;
+        v[4 * q + 1] = t.y;
+        v[4 * q + 2] = t.z;
+        v[4 * q + 3] = t.w;
+    }
+    const u32 pairs = v[1];
+    out_tot[i] = (int)v[0];
+    out_dist[i] = (int)(pairs < 65535u ? pairs : 65535u);
+    const int csh = 48 - cb;
+    const u64 want = ((u64)c << 16) | tgt[i];
+    const i64 end = (i64)((u64)v[Rec8::FIRST] | ((u64)v[Rec8::FIRST + 1] << 32)) + pairs;
+    i64 a = end - pairs, b = end;
+    while (a < b) {  // the first word whose pair key is not below want
+        const i64 mid = (a + b) >> 1;
+        if ((w[mid] >> csh) < want) a = mid + 1;
+        else b = mid;
+    }
+    if (a < end) {
+        const u64 wa = w[a];
+        if ((wa >> csh) == want) {
+            const u32 cnt = word_count(wa, csh, esc_k, esc_c, esc_cap);
+            if (pairs <= cnt_top || thr == nullptr || rank_score(want, cnt) >= thr[c]) out_cnt[i] = (int)cnt;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        if (r < kout) {
+            out_tok[i * kout + r] = (u16)(v[2 + r / 2] >> (16 * (r & 1)));
+            out_tcnt[i * kout + r] = v[2 + Rec8::TOKW + r];
+        }
+    }
+}
+
 // Hint rows over a CountTable's levels (count_table.rs query_rows :338-404): per position the deepest described level
 // whose context occurred: cell ((1 + bucket) * 7 + count bin) * 6 + purity bin, its first `entries` next tokens, their
 // weights round_half_even(count / sum of those counts * 65535), and the bucket (level), else 0 / 0 / 0 / -1.
-// desc[v * 5 + ...] (deepest first): slot_of (int32 [N]), tot (u64 per slot), top_tok (u16 [slots, 8]), top_cnt
-// (u32 [slots, 8]), bucket.
+// desc[v * 3 + ...] (deepest first): slot_of (int32 [N]), the level's context records (CtxRecord<8>), bucket.
 __constant__ double T_PURITY_EDGES[5] = {0.3, 0.5, 0.7, 0.85, 0.95};
 __constant__ u64 T_COUNT_EDGES[6] = {2, 3, 5, 9, 17, 33};
 
@@ -140,14 +170,20 @@ __global__ void pos_rows_k(i64 N, int nlv, const i64* __restrict__ desc, int ent
     const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
     if (i >= N) return;
     for (int v = 0; v < nlv; ++v) {
-        const i64* d = desc + v * 5;
+        const i64* d = desc + v * 3;
         const int c = ((const int*)d[0])[i];
         if (c < 0) continue;
-        const u64 total = ((const u64*)d[1])[c];
+        const u32* r = (const u32*)d[1] + (i64)c * Rec8::WORDS;
+        const u64 total = r[0];
         if (total == 0) continue;
-        const u16* tt = (const u16*)d[2] + (i64)c * 8;
-        const u32* tc = (const u32*)d[3] + (i64)c * 8;
-        const int b = (int)d[4];
+        const int b = (int)d[2];
+        u32 tc[8];
+        u16 tt[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            tt[e] = (u16)(r[2 + e / 2] >> (16 * (e & 1)));
+            tc[e] = r[2 + Rec8::TOKW + e];
+        }
         int count_bin = 0;
 #pragma unroll
         for (int e = 0; e < 6; ++e) count_bin += T_COUNT_EDGES[e] <= total;
@@ -156,12 +192,17 @@ __global__ void pos_rows_k(i64 N, int nlv, const i64* __restrict__ desc, int ent
 #pragma unroll
         for (int e = 0; e < 5; ++e) purity_bin += T_PURITY_EDGES[e] <= share;
         double sum = 0;
-        for (int r = 0; r < entries; ++r) sum += (double)tc[r];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            if (e < entries) sum += (double)tc[e];
         cell[i] = (short)(((1 + b) * 7 + count_bin) * 6 + purity_bin);
         level[i] = (signed char)b;
-        for (int r = 0; r < entries; ++r) {
-            next[i * entries + r] = tt[r];
-            weights[i * entries + r] = tc[r] ? (u16)rint((double)tc[r] / sum * 65535.0) : (u16)0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            if (e < entries) {
+                next[i * entries + e] = tt[e];
+                weights[i * entries + e] = tc[e] ? (u16)rint((double)tc[e] / sum * 65535.0) : (u16)0;
+            }
         }
         return;
     }
@@ -173,15 +214,16 @@ __global__ void pos_rows_k(i64 N, int nlv, const i64* __restrict__ desc, int ent
 // C ABI (engine extensions)
 // ---------------------------------------------------------------------------------------------------------------
 
-// One level's corpus-wide count: contexts into ck (ccap slots, EMPTY-filled), (slot << 16 | next) counted in the split
-// pair table pk/pcnt (pcap slots). flags[0] bit 0: pair table full, bit 1: context table full (rerun bigger).
-extern "C" int ng_table_build(const u16* tok, i64 L, int k, u64* ck, u64 ccap, u64* pk, u32* pcnt, u64 pcap,
-                              u32* flags, int grid, void* stream) {
+// One level's contexts into ck (ccap slots, EMPTY-filled) and per position p < L its event ev[p] = mix64(slot << 16 |
+// tok[p]), EMPTY where p or its context holds a gap. flags[0] bit 1: the context table is full (rerun bigger; the
+// events are then incomplete).
+extern "C" int ng_table_emit(const u16* tok, i64 L, int k, u64* ck, u64 ccap, u64* ev, u32* flags, int grid,
+                             void* stream) {
     if (L <= 0) return 0;
-    if (ccap == 0 || pcap == 0 || ccap > (1ull << 31)) return -1;
+    if (ccap == 0 || ccap > (1ull << 31)) return -1;
     if (grid <= 0) grid = grid_for(L, 256);
     hipStream_t st = (hipStream_t)stream;
-    LEVEL_SWITCH(k, (table_build_k<K><<<grid, 256, 0, st>>>(tok, L, k, ck, ccap, pk, pcnt, pcap, flags)));
+    LEVEL_SWITCH(k, (table_emit_k<K><<<grid, 256, 0, st>>>(tok, L, k, ck, ccap, ev, flags)));
     return (int)hipGetLastError();
 }
 
@@ -191,17 +233,40 @@ extern "C" int ng_table_lookup(const u64* keys, i64 n, const u64* ck, u64 ccap, 
     return (int)hipGetLastError();
 }
 
-// For each listed context (ids [m]): thr[c] = its kth largest pair score (callers list contexts with > kth pairs).
-extern "C" int ng_ctx_kth(const u64* uk, const u32* agg, const i64* start, const i64* end, const i64* ids, i64 m,
-                          int kth, u64* thr, void* stream) {
-    if (kth < 1) return -1;
+// For each listed context (ids [m], callers list those with more than kth pairs): thr[c] = its kth largest pair score
+// over the packed words w (sorted by pair key, cb context bits, escape table esc_k/esc_c) and its record rec[c]
+// (ng_ctx_summary's with topk 8).
+extern "C" int ng_ctx_kth(const u64* w, int cb, const u64* esc_k, const u32* esc_c, u64 esc_cap, const u32* rec,
+                          const i64* ids, i64 m, int kth, u64* thr, void* stream) {
+    if (kth < 1 || cb <= 0 || cb > 32 || esc_cap == 0) return -1;
     if (m > 0) {
         const int g = m < 65536 ? (int)m : 65536;
-        ctx_kth_k<<<g, 256, 0, (hipStream_t)stream>>>(uk, agg, start, end, ids, m, kth, thr);
+        ctx_kth_k<<<g, 256, 0, (hipStream_t)stream>>>(w, cb, esc_k, esc_c, esc_cap, rec, ids, m, kth, thr);
     }
     return (int)hipGetLastError();
 }
 
+// Per query position i < n (x: the query inputs, avail: tokens since the segment start, tgt: the next tokens): the
+// level-k context table ck (ccap slots), its packed words w sorted by pair key (cb context bits, escape table
+// esc_k/esc_c), its records rec (ng_ctx_summary's with topk 8) and CNT_TOP thresholds thr (NULL: no rank rule; read
+// for contexts with more than cnt_top pairs only) give out_tot, out_dist, out_cnt and the first kout (<= 8) top
+// tokens / counts (out_tok / out_tcnt [n, kout]; NULL with kout 0). Positions without a context are not written.
+extern "C" int ng_table_query(const u16* x, const int* avail, const u16* tgt, i64 n, int k, const u64* ck, u64 ccap,
+                              const u64* w, int cb, const u64* esc_k, const u32* esc_c, u64 esc_cap, const u32* rec,
+                              const u64* thr, u32 cnt_top, int kout, int* out_tot, int* out_dist, int* out_cnt,
+                              u16* out_tok, u32* out_tcnt, void* stream) {
+    if (kout < 0 || kout > 8 || cb <= 0 || cb > 32 || esc_cap == 0 || ccap == 0) return -1;
+    if (kout > 0 && (out_tok == nullptr || out_tcnt == nullptr)) return -1;
+    if (n <= 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    LEVEL_SWITCH(k, (table_query_k<K><<<grid_for(n, 256), 256, 0, st>>>(x, avail, tgt, n, k, ck, ccap, w, cb, esc_k,
+                                                                         esc_c, esc_cap, rec, thr, cnt_top, kout,
+                                                                         out_tot, out_dist, out_cnt, out_tok, out_tcnt)));
+    return (int)hipGetLastError();
+}
+
+// Hint rows (pos_rows_k): desc[v * 3 + ...] = slot_of (int32 [N]) pointer, records pointer, bucket per described level,
+// deepest first.
 extern "C" int ng_pos_rows(i64 N, int nlv, const i64* desc, int entries, short* cell, u16* next, u16* weights,
                            signed char* level, void* stream) {
     if (entries < 1 || entries > 8 || nlv < 0) return -1;

@@ -12,13 +12,17 @@ context's top CNT_TOP = 1024 next tokens by count descending then token ascendin
 0 where the context is invalid or never occurred. Keys: packed tokens for k <= 4 (exact), a 64-bit polynomial hash
 beyond (count_table.rs:11-14: ~2^-64 per pair of contexts to merge).
 
-GPU layout per level (libngram_amd.so: ng_table_build, ng_table_compact, sort_pairs, seg_bounds, ng_ctx_topk,
-ng_ctx_kth, ng_table_lookup, ng_pos_gather, ng_pos_rows): the context table (u64 keys, slot = context id), the pairs
-sorted by (slot << 16 | token) with their u32 counts, per slot its pair range, total, top-8 and the CNT_TOP
-threshold."""
+GPU layout per level (libngram_amd.so: ng_table_emit, the partitioned count of partcount.py, ng_ctx_summary,
+ng_ctx_kth, ng_table_query, ng_table_lookup, ng_pos_rows): the context table (u64 keys, slot = context id), the level's
+distinct pairs as packed words (pair key << (48 - cb) | count, larger counts in an escape table) sorted by pair key,
+one 64-byte record per present context (total, pairs, top 8 tokens and counts, its first word) and the CNT_TOP
+threshold of contexts with more pairs than that. The build writes one event per corpus position and counts them
+without global atomics; a query reads its context's record and binary-searches its target among the context's
+words."""
 
 from __future__ import annotations
 
+import ctypes
 import os
 
 import numpy as np
@@ -26,6 +30,7 @@ import torch
 
 from .data import BOS, HEADER_BYTES, shard_tokens
 from .gpu_val_stats import layout
+from . import partcount as P
 from .lib import Lib, i32, u64
 
 CNT_TOP = 1024
@@ -48,13 +53,14 @@ def _segments_device(x: torch.Tensor, lib: Lib) -> torch.Tensor:
 
 
 class _Level:
-    """One built level on the GPU."""
+    """One built level on the GPU: context table ck (ccap slots), packed words w (U, sorted by pair key; cb context
+    bits; escape table esc), records rec [ccap, 16] (valid for present contexts), CNT_TOP thresholds thr (None when no
+    context has more pairs), counts of contexts and pairs."""
 
-    def __init__(self, k, ck, ccap, uk, agg, start, end, tot, top_tok, top_cnt, thr, U, contexts):
+    def __init__(self, k, ck, ccap, w, U, cb, esc, rec, thr, contexts):
         self.k, self.ck, self.ccap = k, ck, ccap
-        self.uk, self.agg, self.start, self.end = uk, agg, start, end
-        self.tot, self.top_tok, self.top_cnt, self.thr = tot, top_tok, top_cnt, thr
-        self.pairs, self.contexts = U, contexts
+        self.w, self.pairs, self.cb, self.esc = w, U, cb, esc
+        self.rec, self.thr, self.contexts = rec, thr, contexts
 
 
 class CountTable:
@@ -128,6 +134,8 @@ class CountTable:
             raise ValueError("the count table is already built")
         self.built = True
         self.reruns = {}
+        if not hasattr(self, "ratio"):
+            self.ratio = {}
         for k in self._levels:
             self.tables.append(self._build_level(k))
 
@@ -139,66 +147,47 @@ class CountTable:
     def _build_level(self, k: int) -> _Level:
         lib, dev = self.lib, self.tok.device
         n_k = sum(max(0, n - k) for n in self.sizes_)  # occurrences: an upper bound of contexts and of pairs
-        ccap = max(1 << 16, int(n_k / LOAD) + 1)
-        pcap = ccap
+        bound = n_k
+        prev = self.tables[-1] if self.tables else None
+        if prev is not None and prev.k == k - 1:
+            bound = min(bound, prev.pairs)  # a k-context is a (k-1)-context with its next token: one of its pairs
+        ccap = max(1 << 16, int(bound / LOAD) + 1)
         reruns = 0
+        ev = torch.empty(max(self.L, 1), dtype=torch.int64, device=dev)
         while True:
-            if ccap >= 1 << 31:
+            if ccap > 1 << 31:
                 raise RuntimeError(f"k={k}: {n_k} occurrences need more than 2^31 context slots")
             ck = torch.full((ccap,), -1, dtype=torch.int64, device=dev)
-            pk = torch.full((pcap,), -1, dtype=torch.int64, device=dev)
-            pc = torch.zeros(pcap, dtype=torch.int32, device=dev)
-            flags = torch.zeros(2, dtype=torch.int32, device=dev)
-            e0, e1 = self._timed("table_build", k)
+            flags = torch.zeros(1, dtype=torch.int32, device=dev)
+            e0, e1 = self._timed("table_emit", k)
             e0.record()
-            lib("ng_table_build", self.tok, self.L, i32(k), ck, u64(ccap), pk, pc, u64(pcap), flags, i32(self.grid))
+            lib("ng_table_emit", self.tok, self.L, i32(k), ck, u64(ccap), ev, flags, i32(self.grid))
             e1.record()
-            f = int(flags[0].item())
-            if f == 0:
+            if int(flags[0].item()) == 0:
                 break
             reruns += 1
-            if f & 2:
-                ccap *= 2
-            if f & 1:
-                pcap *= 2
-            del ck, pk, pc
+            ccap = min(2 * ccap, 1 << 31)
+            del ck
         self.reruns[k] = reruns
-        counter = torch.zeros(1, dtype=torch.int64, device=dev)
-        ckeys = torch.empty(pcap, dtype=torch.int64, device=dev)
-        ccnt = torch.empty(pcap, dtype=torch.int32, device=dev)
-        e0, e1 = self._timed("compact", k)
+        ev_name = lambda name, n: self._timed(name, k)
+        c = P.count_events(lib, lib, ev, self.L, ccap, self.ratio.get(k, 1.0), None, True, ev_name)
+        del ev
+        self.ratio[k] = max(c.U, 1) / max(self.L, 1)
+        if not c.cb:
+            raise RuntimeError(f"k={k}: more large counts than the escape table holds")
+        rec, dist, w = P.summarize(lib, lib, c, ccap, TOPE, False, ev_name, by_pair=True)
+        del c.pairs
+        e0, e1 = self._timed("ctx_kth", k)
         e0.record()
-        lib("ng_table_compact", pk, pc, u64(pcap), ckeys, ccnt, counter)
-        e1.record()
-        del pk, pc
-        U = int(counter.item())
-        uk = torch.empty(U, dtype=torch.int64, device=dev)
-        agg = torch.empty(U, dtype=torch.int32, device=dev)
-        ctx_bits = max(1, (ccap - 1).bit_length())
-        e0, e1 = self._timed("sort", k)
-        e0.record()
-        if U:
-            lib.cub("sort_pairs", ckeys, uk, ccnt, agg, U, i32(0), i32(16 + ctx_bits))
-        e1.record()
-        del ckeys, ccnt
-        start = torch.zeros(ccap, dtype=torch.int64, device=dev)
-        end = torch.zeros(ccap, dtype=torch.int64, device=dev)
-        tot = torch.zeros(ccap, dtype=torch.int64, device=dev)
-        top_tok = torch.zeros(ccap * TOPE, dtype=torch.int16, device=dev)
-        top_cnt = torch.zeros(ccap * TOPE, dtype=torch.int32, device=dev)
-        thr = torch.zeros(ccap, dtype=torch.int64, device=dev)
-        e0, e1 = self._timed("ctx_stats", k)
-        e0.record()
-        lib("seg_bounds", uk, U, start, end)
-        lib("ng_ctx_topk", uk, agg, start, end, ccap, i32(TOPE), tot, top_tok, top_cnt)
-        deep = ((end - start) > CNT_TOP).nonzero().squeeze(1)
+        deep = (dist > CNT_TOP).nonzero().squeeze(1)
+        thr = None
         if deep.numel():
-            lib("ng_ctx_kth", uk, agg, start, end, deep, deep.numel(), i32(CNT_TOP), thr)
+            thr = torch.empty(ccap, dtype=torch.int64, device=dev)
+            lib("ng_ctx_kth", w, i32(c.cb), c.esc[0], c.esc[1], u64(P.ESC_CAP), rec, deep, deep.numel(), i32(CNT_TOP),
+                thr)
         e1.record()
-        if ccap and int(tot.max().item()) >= 1 << 32:
-            raise RuntimeError(f"k={k}: a context's total does not fit uint32")
-        contexts = int((end > start).sum().item())
-        return _Level(k, ck, ccap, uk, agg, start, end, tot, top_tok, top_cnt, thr, U, contexts)
+        contexts = int((dist > 0).sum().item())
+        return _Level(k, ck, ccap, w, c.U, c.cb, c.esc, rec, thr, contexts)
 
     def _check(self):
         if not self.built or self.released or len(self.tables) != len(self._levels):
@@ -235,14 +224,12 @@ class CountTable:
             res["top_tok"] = torch.zeros((L, n, topk), dtype=torch.int16, device=x.device)
             res["top_cnt"] = torch.zeros((L, n, topk), dtype=torch.int32, device=x.device)
         for li, lv in enumerate(self.tables):
-            slot = self._slots(x, avail, lv)
-            e0, e1 = self._timed("pos_gather", lv.k)
+            e0, e1 = self._timed("query", lv.k)
             e0.record()
-            self.lib("ng_pos_gather", slot, n, 0, lv.ccap, tgt, lv.uk, lv.agg, lv.start, lv.end, lv.tot, lv.top_tok,
-                     lv.top_cnt, lv.thr if top == CNT_TOP else None, None, None, u64(0), None, i32(TOPE), i32(topk), i32(0),
-                     out[0, li],
-                     out[1, li], out[2, li], res["top_tok"][li] if topk else None,
-                     res["top_cnt"][li] if topk else None, None)
+            self.lib("ng_table_query", x, avail, tgt, n, i32(lv.k), lv.ck, u64(lv.ccap), lv.w, i32(lv.cb), lv.esc[0],
+                     lv.esc[1], u64(P.ESC_CAP), lv.rec, lv.thr if top == CNT_TOP else None, ctypes.c_uint32(CNT_TOP),
+                     i32(topk), out[0, li], out[1, li], out[2, li], res["top_tok"][li] if topk else None,
+                     res["top_cnt"][li] if topk else None)
             e1.record()
         return res
 
@@ -298,7 +285,7 @@ class CountTable:
         desc = []
         for (t, b), slot in zip(use, slots):
             lv = self.tables[t]
-            desc += [slot.data_ptr(), lv.tot.data_ptr(), lv.top_tok.data_ptr(), lv.top_cnt.data_ptr(), b]
+            desc += [slot.data_ptr(), lv.rec.data_ptr(), b]
         desc_t = torch.tensor(desc if desc else [0], dtype=torch.int64, device=dev)
         cell = torch.zeros(n, dtype=torch.int16, device=dev)
         nxt = torch.zeros((n, entries), dtype=torch.int16, device=dev)
@@ -313,8 +300,8 @@ class CountTable:
         """Per level (as built): (k, contexts, pairs, bytes held on the GPU)."""
         out = []
         for lv in self.tables:
-            b = sum(t.numel() * t.element_size() for t in (lv.ck, lv.uk, lv.agg, lv.start, lv.end, lv.tot,
-                                                             lv.top_tok, lv.top_cnt, lv.thr))
+            held = (lv.ck, lv.w, lv.rec, lv.esc[0], lv.esc[1]) + ((lv.thr,) if lv.thr is not None else ())
+            b = sum(t.numel() * t.element_size() for t in held)
             out.append((lv.k, lv.contexts, lv.pairs, b))
         return out
 

@@ -150,16 +150,19 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor, n_ev: int, n_ids: int, r
 RECORD_WORDS = {1: 4, 2: 8, 4: 8, 8: 16}  # u32 words of a context record for top 1, 2, 4, 8
 
 
-def summarize(elib: Lib, lib: Lib, c: Counted, n_ids: int, ktop: int, zero_records: bool = False, event=_no_event):
+def summarize(elib: Lib, lib: Lib, c: Counted, n_ids: int, ktop: int, zero_records: bool = False, event=_no_event,
+              by_pair: bool = False):
     """Per present context (of packed pairs): its record (int32 [n_ids, RECORD_WORDS[ktop]]: total, pairs, the
-    first ktop tokens two per word, their counts) and its pair count (int32 [n_ids], 0 for absent contexts). The
-    records of absent contexts are zeros only with zero_records. Raises if a total reaches 2^32."""
+    first ktop tokens two per word, their counts; for ktop 2 and 8 also its first word's index in the sorted words)
+    and its pair count (int32 [n_ids], 0 for absent contexts); returns (records, pair counts, the words sorted by
+    context, or with by_pair by pair key). The records of absent contexts are zeros only with zero_records. Raises if
+    a total reaches 2^32."""
     dev = c.pairs.device
     sw = torch.empty(max(c.U, 1), dtype=torch.int64, device=dev)
     e0, e1 = event("sort", c.U)
     e0.record()
     if c.U:
-        lib.cub("sort_pairs", c.pairs, sw, None, None, c.U, i32(64 - c.cb), i32(64))
+        lib.cub("sort_pairs", c.pairs, sw, None, None, c.U, i32(64 - c.cb - (16 if by_pair else 0)), i32(64))
     e1.record()
     rec = (torch.zeros if zero_records else torch.empty)((n_ids, RECORD_WORDS[ktop]), dtype=torch.int32, device=dev)
     dist = torch.zeros(n_ids, dtype=torch.int32, device=dev)
@@ -170,7 +173,7 @@ def summarize(elib: Lib, lib: Lib, c: Counted, n_ids: int, ktop: int, zero_recor
     e1.record()
     if int(flags[0].item()) & 4:
         raise RuntimeError("a total does not fit uint32")
-    return rec, dist
+    return rec, dist, sw
 
 
 def record_tops(rec: torch.Tensor, ktop: int):
