@@ -182,9 +182,12 @@ int ng_part_count(const ng_u64* ev, const ng_i64* start, int pbits, const ng_u64
  * From such words sorted by context: dist[c] (pairs) and the record rec[c] of each present context (callers zero
  * dist): u32 words total, pairs, the first topk (1, 2, 4, 8) tokens by (count desc, token asc) two per word, their
  * counts (4, 8, 8, 16 words for topk 1, 2, 4, 8; for topk 2 and 8 also the index of the context's first word, u64
- * in the two words after the counts); flags[0] bit 2: a total reached 2^32 */
+ * in the two words after the counts); dist may be NULL; with nstat (u32[257], zeroed) the number of contexts is
+ * nstat[1] + ... + nstat[256] and with deep the contexts of more than deep_min pairs are appended to deep (nstat[0]
+ * of them); flags[0] bit 2: a total reached 2^32 */
 int ng_ctx_summary(const ng_u64* w, ng_i64 U, int cb, const ng_u64* esc_k, const uint32_t* esc_c, ng_u64 esc_cap,
-                   int topk, uint32_t* rec, uint32_t* dist, uint32_t* flags, void* stream);
+                   int topk, uint32_t* rec, uint32_t* dist, uint32_t deep_min, ng_i64* deep, uint32_t* nstat,
+                   uint32_t* flags, void* stream);
 /* per query position from ng_ctx_summary's records and pair counts and the counted lookups qcnt (may be NULL: no
  * cnt): tot, dist, cnt (thr: the CNT_TOP threshold scores, may be NULL), the first kout of ktop top entries, mask bit
  * li (mask may be NULL) */

@@ -218,12 +218,21 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
 // dependent global loads: every word is read by its own window and at most once more by the window of its context's
 // first word. For present contexts only: dist[c] = its pairs, and its record rec[c] (CtxRecord<KT>::WORDS u32: total,
 // pairs, the first KT tokens by (count desc, token asc) two per word, their counts; 0-padded; for KT 2 and 8 also the
-// index of its first word), stored whole as 16-byte vectors; flags[0] bit 2 if a total reaches 2^32.
+// index of its first word), stored whole as 16-byte vectors; flags[0] bit 2 if a total reaches 2^32. dist may be
+// NULL; with nstat: the contexts counted in nstat[1..256] (their sum) and, with deep, each context of more than
+// deep_min pairs appended to deep (nstat[0] of them; callers size deep for U / (deep_min + 1) + 1).
 template <int KT>
 __global__ void __launch_bounds__(256) ctx_summary_k(const u64* __restrict__ w, i64 U, int cb,
                                                      const u64* __restrict__ esc_k, const u32* __restrict__ esc_c,
                                                      u64 esc_cap, u32* __restrict__ rec, u32* __restrict__ dist,
+                                                     u32 deep_min, i64* __restrict__ deep, u32* __restrict__ nstat,
                                                      u32* flags) {
+    u32 nctx = 0;  // contexts this lane summarized
+    auto done = [&](u64 c, u32 pairs) {
+        ++nctx;
+        if (dist) dist[c] = pairs;
+        if (deep && pairs > deep_min) deep[atomicAdd(&nstat[0], 1u)] = (i64)c;
+    };
     __shared__ u64 sw[4][WAVE];
     const int sh = 64 - cb, csh = 48 - cb;
     const u64 esc = (1ull << csh) - 1;
@@ -268,7 +277,7 @@ __global__ void __launch_bounds__(256) ctx_summary_k(const u64* __restrict__ w, 
                     s += n;
                     topk_insert<KT>(tl, rank_score(wj >> csh, n));
                 }
-                dist[ctx] = (u32)(e - lane + 1);
+                done(ctx, (u32)(e - lane + 1));
                 store_record<KT>(rec, ctx, s, (u32)(e - lane + 1), tl, (u64)i);
                 if (s >> 32) atomicOr(&flags[0], 4u);
             }
@@ -326,12 +335,17 @@ __global__ void __launch_bounds__(256) ctx_summary_k(const u64* __restrict__ w, 
                 if (m != 0 && mine == m) ++headq;
             }
             if (lane == h) {
-                dist[hc] = len;
+                done(hc, len);
                 store_record<KT>(rec, hc, part, len, merged, (u64)(wv * WAVE + h));
                 if (part >> 32) atomicOr(&flags[0], 4u);
             }
         }
         __syncthreads();  // the window's staged words are read before the next round writes them
+    }
+    if (nstat) {  // one add per wave, spread over 256 counters
+#pragma unroll
+        for (int d = WAVE / 2; d > 0; d >>= 1) nctx += (u32)__shfl_down((int)nctx, d, WAVE);
+        if (lane == 0 && nctx) atomicAdd(&nstat[1 + (blockIdx.x & 255)], nctx);
     }
 }
 
@@ -439,20 +453,23 @@ extern "C" int ng_part_count(const u64* ev, const i64* start, int pbits, const u
 
 // Per context from U packed words (ng_part_count's with cb > 0) sorted by context: dist[c] = its pairs and its record
 // rec[c] (u32 words: total, pairs, the first topk (1, 2, 4, 8) tokens by (count desc, token asc) two per word, their
-// counts; 4, 8, 8, 16 words for topk 1, 2, 4, 8), written for contexts present only (callers zero dist). flags[0]
-// bit 2: a total reached 2^32.
+// counts; 4, 8, 8, 16 words for topk 1, 2, 4, 8; for topk 2 and 8 the index of the context's first word in the two
+// words after the counts), written for contexts present only (callers zero dist; dist may be NULL). With nstat
+// (u32[257], zeroed): the number of contexts is nstat[1] + ... + nstat[256], and with deep the contexts of more than
+// deep_min pairs are appended to deep (nstat[0] of them; sized U / (deep_min + 1) + 1). flags[0] bit 2: a total
+// reached 2^32.
 extern "C" int ng_ctx_summary(const u64* w, i64 U, int cb, const u64* esc_k, const u32* esc_c, u64 esc_cap, int topk,
-                              u32* rec, u32* dist, u32* flags, void* stream) {
-    if (cb <= 0 || cb > 44 || esc_cap == 0) return -1;
+                              u32* rec, u32* dist, u32 deep_min, i64* deep, u32* nstat, u32* flags, void* stream) {
+    if (cb <= 0 || cb > 44 || esc_cap == 0 || (deep && !nstat)) return -1;
     if (U <= 0) return 0;
     int g = grid_for((U + WAVE - 1) / WAVE, 4);  // four waves per block, a window each per round
     g = g > 65536 ? 65536 : g;
     hipStream_t st = (hipStream_t)stream;
     switch (topk) {
-        case 1: ctx_summary_k<1><<<g, 256, 0, st>>>(w, U, cb, esc_k, esc_c, esc_cap, rec, dist, flags); break;
-        case 2: ctx_summary_k<2><<<g, 256, 0, st>>>(w, U, cb, esc_k, esc_c, esc_cap, rec, dist, flags); break;
-        case 4: ctx_summary_k<4><<<g, 256, 0, st>>>(w, U, cb, esc_k, esc_c, esc_cap, rec, dist, flags); break;
-        case 8: ctx_summary_k<8><<<g, 256, 0, st>>>(w, U, cb, esc_k, esc_c, esc_cap, rec, dist, flags); break;
+        case 1: ctx_summary_k<1><<<g, 256, 0, st>>>(w, U, cb, esc_k, esc_c, esc_cap, rec, dist, deep_min, deep, nstat, flags); break;
+        case 2: ctx_summary_k<2><<<g, 256, 0, st>>>(w, U, cb, esc_k, esc_c, esc_cap, rec, dist, deep_min, deep, nstat, flags); break;
+        case 4: ctx_summary_k<4><<<g, 256, 0, st>>>(w, U, cb, esc_k, esc_c, esc_cap, rec, dist, deep_min, deep, nstat, flags); break;
+        case 8: ctx_summary_k<8><<<g, 256, 0, st>>>(w, U, cb, esc_k, esc_c, esc_cap, rec, dist, deep_min, deep, nstat, flags); break;
         default: return -1;
     }
     return (int)hipGetLastError();

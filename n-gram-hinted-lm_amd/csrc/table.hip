@@ -58,11 +58,12 @@ __device__ __forceinline__ u32 word_count(u64 word, int csh, const u64* __restri
 
 // One block per listed context c = ids[b] (with more than kth pairs): thr[c] = the kth largest score rank_score(pair
 // key, count) among its packed words (w sorted by pair key; its range from its record), by a radix select over the
-// 48-bit scores, 12 bits per round.
+// 48-bit scores, 12 bits per round (256 threads: 16 bins each).
 __global__ void __launch_bounds__(256) ctx_kth_k(const u64* __restrict__ w, int cb, const u64* __restrict__ esc_k,
                                                  const u32* __restrict__ esc_c, u64 esc_cap, const u32* __restrict__ rec,
                                                  const i64* __restrict__ ids, i64 m, int kth, u64* __restrict__ thr) {
     __shared__ u32 hist[4096];
+    __shared__ u32 s_wave[4];
     __shared__ u64 s_prefix;
     __shared__ u32 s_need;
     const int csh = 48 - cb;
@@ -83,10 +84,26 @@ __global__ void __launch_bounds__(256) ctx_kth_k(const u64* __restrict__ w, int 
                     atomicAdd(&hist[(sc >> shift) & 0xFFF], 1u);
             }
             __syncthreads();
-            if (threadIdx.x == 0) {
-                u32 acc = 0;
-                int d = 4095;
-                for (; d > 0; --d) {
+            // the digit holding the need-th largest: thread t sums bins [16t, 16t + 16), a suffix scan over the
+            // threads finds the one thread whose bins cross `need`, which walks them from the top
+            const int t = threadIdx.x, lane = lane_id(), wid = t / WAVE;
+            u32 mine = 0;
+#pragma unroll
+            for (int q = 0; q < 16; ++q) mine += hist[16 * t + q];
+            u32 suf = mine;  // sum over this wave's lanes >= lane
+#pragma unroll
+            for (int d = 1; d < WAVE; d <<= 1) {
+                const u32 o = (u32)__shfl_down((int)suf, d, WAVE);
+                if (lane + d < WAVE) suf += o;
+            }
+            if (lane == 0) s_wave[wid] = suf;
+            __syncthreads();
+            u32 above = suf - mine;
+            for (int v = wid + 1; v < 4; ++v) above += s_wave[v];
+            if (above < need && above + mine >= need) {
+                u32 acc = above;
+                int d = 16 * t + 15;
+                for (; d > 16 * t; --d) {
                     if (acc + hist[d] >= need) break;
                     acc += hist[d];
                 }

@@ -487,8 +487,8 @@ class CountBuild:
         N, n_own = vi.ctx_of.numel(), vi.ids
         ktop = 1 if want <= 1 else 2 if want <= 2 else 4 if want <= 4 else 8
         try:
-            rec, dist, _ = summarize(self.elib, self.lib, c, n_own, ktop, zero_tops,
-                                  lambda name, n: self._event(name, k, -1, n))
+            sm = summarize(self.elib, self.lib, c, n_own, ktop, zero_tops, lambda name, n: self._event(name, k, -1, n))
+            rec, dist = sm.rec, sm.dist
         except RuntimeError as e:
             raise RuntimeError(f"k={k}: {e}") from None
         e0, e1 = self._event("pos_gather", k, -1, N)

@@ -138,7 +138,8 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
         o_tok = torch.zeros(m, dtype=torch.int16, device=dev)
         o_cnt = torch.zeros(m, dtype=torch.int32, device=dev)
         if c.cb:
-            rec, dist, _ = summarize(elib, lib, c, vi.ids, 1)
+            sm = summarize(elib, lib, c, vi.ids, 1)
+            rec, dist = sm.rec, sm.dist
             o_tot = torch.empty(m, dtype=torch.int32, device=dev)
             o_dist = torch.empty(m, dtype=torch.int32, device=dev)
             o_tc = torch.empty(m, dtype=torch.int32, device=dev)

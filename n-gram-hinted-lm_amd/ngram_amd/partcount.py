@@ -16,6 +16,7 @@ here every event is counted by an LDS atomic and moved by coalesced streams."""
 
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass
 
@@ -150,13 +151,25 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor, n_ev: int, n_ids: int, r
 RECORD_WORDS = {1: 4, 2: 8, 4: 8, 8: 16}  # u32 words of a context record for top 1, 2, 4, 8
 
 
+@dataclass
+class Summary:
+    """ng_ctx_summary's outputs: records (int32 [n_ids, RECORD_WORDS[ktop]]), pair counts per context (int32 [n_ids],
+    or None), the sorted words, the number of present contexts, the contexts of more than deep_min pairs (int64)."""
+
+    rec: torch.Tensor
+    dist: torch.Tensor | None
+    words: torch.Tensor
+    contexts: int
+    deep: torch.Tensor | None
+
+
 def summarize(elib: Lib, lib: Lib, c: Counted, n_ids: int, ktop: int, zero_records: bool = False, event=_no_event,
-              by_pair: bool = False):
-    """Per present context (of packed pairs): its record (int32 [n_ids, RECORD_WORDS[ktop]]: total, pairs, the
-    first ktop tokens two per word, their counts; for ktop 2 and 8 also its first word's index in the sorted words)
-    and its pair count (int32 [n_ids], 0 for absent contexts); returns (records, pair counts, the words sorted by
-    context, or with by_pair by pair key). The records of absent contexts are zeros only with zero_records. Raises if
-    a total reaches 2^32."""
+              by_pair: bool = False, with_dist: bool = True, deep_min: int | None = None) -> Summary:
+    """Per present context (of packed pairs): its record (total, pairs, the first ktop tokens two per word, their
+    counts; for ktop 2 and 8 also its first word's index in the sorted words) and, with_dist, its pair count (0 for
+    absent contexts). The words are sorted by context, or with by_pair by pair key. The records of absent contexts are
+    zeros only with zero_records. With deep_min: the contexts of more than deep_min pairs. Raises if a total reaches
+    2^32."""
     dev = c.pairs.device
     sw = torch.empty(max(c.U, 1), dtype=torch.int64, device=dev)
     e0, e1 = event("sort", c.U)
@@ -165,15 +178,21 @@ def summarize(elib: Lib, lib: Lib, c: Counted, n_ids: int, ktop: int, zero_recor
         lib.cub("sort_pairs", c.pairs, sw, None, None, c.U, i32(64 - c.cb - (16 if by_pair else 0)), i32(64))
     e1.record()
     rec = (torch.zeros if zero_records else torch.empty)((n_ids, RECORD_WORDS[ktop]), dtype=torch.int32, device=dev)
-    dist = torch.zeros(n_ids, dtype=torch.int32, device=dev)
+    dist = torch.zeros(n_ids, dtype=torch.int32, device=dev) if with_dist else None
+    nstat = torch.zeros(257, dtype=torch.int32, device=dev)
+    deep = torch.empty(c.U // (deep_min + 1) + 1, dtype=torch.int64, device=dev) if deep_min is not None else None
     flags = torch.zeros(1, dtype=torch.int32, device=dev)
     e0, e1 = event("ctx_topk", c.U)
     e0.record()
-    elib("ng_ctx_summary", sw, c.U, i32(c.cb), c.esc[0], c.esc[1], u64(ESC_CAP), i32(ktop), rec, dist, flags)
+    elib("ng_ctx_summary", sw, c.U, i32(c.cb), c.esc[0], c.esc[1], u64(ESC_CAP), i32(ktop), rec, dist,
+         ctypes.c_uint32(deep_min or 0), deep, nstat, flags)
     e1.record()
     if int(flags[0].item()) & 4:
         raise RuntimeError("a total does not fit uint32")
-    return rec, dist, sw
+    st = nstat.cpu()
+    if deep is not None:
+        deep = deep[: int(st[0])]
+    return Summary(rec, dist, sw, int(st[1:].sum()), deep)
 
 
 def record_tops(rec: torch.Tensor, ktop: int):
