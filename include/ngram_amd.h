@@ -171,8 +171,8 @@ int ng_part_bounds(const ng_u64* ev, ng_i64 n, int pbits, ng_i64* start, void* s
 int ng_part_lookups(const int* ctx_of, const uint16_t* tgt, const int* pos, ng_i64 n, ng_i64 lo, ng_i64 hi,
                     ng_u64* qk, uint32_t* qv, void* stream);
 /* per partition an LDS hash count of its events; block b's distinct (pair key, count) at out + seg_base[b], seg_cnt[b]
- * of them; qcnt[qv[j]] = the count of lookup j (qk sorted like ev, bounds qstart); flags[0] bit 0: a partition held
- * more than 8192 distinct pairs (repartition with one more bit) */
+ * of them; qcnt[qv[j]] = the count of lookup j (qk sorted like ev, bounds qstart); flags[0] bit 0: a partition reached
+ * 7000 distinct pairs (repartition with one more bit) */
 int ng_part_count(const ng_u64* ev, const ng_i64* start, int pbits, const ng_u64* qk, const uint32_t* qv,
                   const ng_i64* qstart, ng_u64* out_k, uint32_t* out_c, int cb, ng_u64* esc_k, uint32_t* esc_c,
                   ng_u64 esc_cap, uint32_t* seg_cnt, ng_i64* seg_base, uint32_t* qcnt, uint32_t* flags, int grid,

@@ -105,6 +105,15 @@ static inline int grid_for(i64 n, int block) {
     return (int)g;
 }
 
+// A workgroup barrier ordering LDS accesses only: unlike __syncthreads it does not wait for the wave's outstanding
+// global stores (a block that scatters results to global memory between LDS phases would otherwise wait for each
+// phase's writes to complete).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Wave helpers (wave64)
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (WAVE - 1)); }
 __device__ __forceinline__ u64 lanemask_lt() { return (1ull << lane_id()) - 1ull; }

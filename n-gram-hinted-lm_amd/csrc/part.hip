@@ -5,8 +5,9 @@
 //   2. ng_seg_offsets + ng_seg_gather pack the regions into one array of events;
 //   3. the events are sorted by their top pbits (sort_pairs, keys only): partition p = events whose mixed key has top
 //      bits p, i.e. a hash partition of the pairs; ng_part_bounds finds each partition's range;
-//   4. ng_part_count: one block per group of partitions counts each partition's events in an LDS hash table (8192
-//      slots; a partition with more distinct pairs sets flags[0] bit 0 and the host repeats 3-4 with one more bit),
+//   4. ng_part_count: one block per group of partitions (about equal events each) counts each partition's events in
+//      an LDS hash table (8192 slots in buckets of four; a partition reaching 7000 distinct pairs sets flags[0] bit 0
+//      and the host repeats 3-4 with one more bit),
 //      answers that partition's lookups (the query positions' (context, target) pairs, hashed and sorted the same way
 //      by ng_part_lookups + sort_pairs), and appends the distinct pairs (unmixed) with their counts to the block's
 //      segment, which ng_seg_gather packs again.
@@ -86,59 +87,114 @@ __global__ void part_lookups_k(const int* __restrict__ ctx_of, const u16* __rest
     qv[j] = (u32)i;
 }
 
-#define PT_SLOTS 8192
-#define PT_MASK (PT_SLOTS - 1)
+#define PT_SLOTS 8192    // 96 KB of LDS per block (keys and counts; measured faster than two blocks per CU of 6400)
+#define PT_BUCKETS (PT_SLOTS / 4)
 #define PT_BLOCK 1024
 #define PT_ITEMS 4
+#define PT_LIMIT 7000  // distinct pairs a partition may reach before it is declared overfull (with every thread's
+                       // insert in flight the table stays below PT_SLOTS, so probes always meet their key or a free slot)
 
-__device__ __forceinline__ void pt_insert(u64* tk, u32* tc, u64 key, u32 add, u32* flags) {
-    u32 s = (u32)key & PT_MASK;
-    for (int probe = 0; probe < PT_SLOTS; ++probe) {
-        const u64 cur = tk[s];
-        if (cur == key) {
-            atomicAdd(&tc[s], add);
-            return;
-        }
-        if (cur == EMPTY) {
-            const u64 prev = atomicCAS((unsigned long long*)&tk[s], EMPTY, key);
+// The LDS table is bucketized: four keys per 32-byte bucket, filled from the front, buckets probed linearly from the
+// key's home bucket. A key lies in the first bucket along its probe sequence that has a free slot, or before it, so
+// one pair of 16-byte reads settles most probes: on MI355X the divergent one-slot probe loop cost about twice as
+// much, in scalar exec-mask work per probe step.
+__device__ __forceinline__ u32 pt_bucket(u64 key) { return (u32)(((u64)(u32)key * PT_BUCKETS) >> 32); }
+__device__ __forceinline__ u32 pt_next(u32 b) { return b + 1 == PT_BUCKETS ? 0 : b + 1; }
+
+__device__ __forceinline__ void pt_read4(const u64* tk, u32 b, u64& k0, u64& k1, u64& k2, u64& k3) {
+    const ulonglong2 a = *(const ulonglong2*)(tk + 4 * b);
+    const ulonglong2 c = *(const ulonglong2*)(tk + 4 * b + 2);
+    k0 = a.x;
+    k1 = a.y;
+    k2 = c.x;
+    k3 = c.y;
+}
+
+// Count `add` occurrences of `key`; returns whether it took a free slot. A lost race for a free slot re-reads the
+// bucket. Unbounded: the occupancy limit keeps a free slot in the table.
+__device__ __forceinline__ bool pt_add(u64* tk, u32* tc, u64 key, u32 add) {
+    u32 b = pt_bucket(key);
+    int slot = -1;
+    bool fresh = false;
+    while (slot < 0) {
+        u64 k0, k1, k2, k3;
+        pt_read4(tk, b, k0, k1, k2, k3);
+        const int q = k0 == key ? 0 : k1 == key ? 1 : k2 == key ? 2 : k3 == key ? 3 : -1;
+        const int e = k0 == EMPTY ? 0 : k1 == EMPTY ? 1 : k2 == EMPTY ? 2 : k3 == EMPTY ? 3 : -1;
+        if (q >= 0) {
+            slot = 4 * (int)b + q;
+        } else if (e >= 0) {
+            const u64 prev = atomicCAS((unsigned long long*)&tk[4 * b + e], EMPTY, key);
             if (prev == EMPTY || prev == key) {
-                atomicAdd(&tc[s], add);
-                return;
+                slot = 4 * (int)b + e;
+                fresh = prev == EMPTY;
             }
+        } else {
+            b = pt_next(b);
         }
-        s = (s + 1) & PT_MASK;
     }
-    atomicOr(&flags[0], 1u);  // more distinct pairs than slots: the host repartitions with one more bit
+    atomicAdd(&tc[slot], add);
+    return fresh;
 }
 
 __device__ __forceinline__ u32 pt_find(const u64* tk, const u32* tc, u64 key) {
-    u32 s = (u32)key & PT_MASK;
-    for (int probe = 0; probe < PT_SLOTS; ++probe) {
-        const u64 cur = tk[s];
-        if (cur == key) return tc[s];
-        if (cur == EMPTY) return 0;
-        s = (s + 1) & PT_MASK;
+    u32 b = pt_bucket(key);
+    while (true) {
+        u64 k0, k1, k2, k3;
+        pt_read4(tk, b, k0, k1, k2, k3);
+        const int q = k0 == key ? 0 : k1 == key ? 1 : k2 == key ? 2 : k3 == key ? 3 : -1;
+        if (q >= 0) return tc[4 * b + q];
+        if (k3 == EMPTY) return 0;
+        b = pt_next(b);
     }
-    return 0;
 }
 
-// Block b counts partitions [b * ppb, (b + 1) * ppb) in turn. Its distinct pairs (at most its events) go to
+// A wave-uniform lane's 64-bit value (readlane: no LDS traffic).
+__device__ __forceinline__ u64 readlane_u64(u64 v, int l) {
+    const u32 lo = (u32)__builtin_amdgcn_readlane((int)(u32)v, l);
+    const u32 hi = (u32)__builtin_amdgcn_readlane((int)(u32)(v >> 32), l);
+    return ((u64)hi << 32) | lo;
+}
+
+// The block owning partition p: the one whose share of the events holds the partition's first event (start[p] * G /
+// n, the last block for trailing empty partitions), so that blocks get equal events, whatever the skew of the
+// partitions' sizes (a partition holding a hot pair has far more events than others). Monotone in p.
+__device__ __forceinline__ i64 part_owner(const i64* __restrict__ start, i64 p, i64 n, i64 G) {
+    if (n <= 0) return 0;
+    const i64 o = (i64)((u64)start[p] * (u64)G / (u64)n);  // start * G < 2^63 for n < 2^47 events, G <= 2^16
+    return o < G - 1 ? o : G - 1;
+}
+
+// The first partition whose owner is at least b (P if none).
+__device__ __forceinline__ i64 part_first(const i64* __restrict__ start, i64 P, i64 n, i64 G, i64 b) {
+    i64 lo = 0, hi = P;
+    while (lo < hi) {
+        const i64 m = (lo + hi) >> 1;
+        if (part_owner(start, m, n, G) < b) lo = m + 1;
+        else hi = m;
+    }
+    return lo;
+}
+
+// Block b counts the partitions it owns (part_owner) in turn. Its distinct pairs (at most its events) go to
 // out[start[p0] ...]: segment b = (seg_base[b], seg_cnt[b]). qcnt[qv[j]] = the count of lookup j (0: absent).
 // cb == 0: out_k = pair key, out_c = count. cb > 0 (context ids below 2^cb, cb <= 44): out_k = the packed word
 // pair key << (48 - cb) | min(count, esc), esc = 2^(48 - cb) - 1, a count >= esc also put in the escape table.
 __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__ ev, const i64* __restrict__ start,
-                                                        i64 P, i64 ppb, const u64* __restrict__ qk,
+                                                        i64 P, const u64* __restrict__ qk,
                                                         const u32* __restrict__ qv, const i64* __restrict__ qstart,
                                                         u64* __restrict__ out_k, u32* __restrict__ out_c, int cb,
                                                         u64* esc_k, u32* esc_c, u64 esc_cap,
                                                         u32* __restrict__ seg_cnt, i64* __restrict__ seg_base,
                                                         u32* __restrict__ qcnt, u32* flags) {
-    __shared__ u64 tk[PT_SLOTS];
+    __shared__ __align__(16) u64 tk[PT_SLOTS];
     __shared__ u32 tc[PT_SLOTS];
     __shared__ u32 cur;
+    __shared__ u32 nocc;  // the partition's distinct pairs counted so far (updated once per wave and item)
     const int t = threadIdx.x, lane = lane_id();
-    const i64 p0 = blockIdx.x * ppb, p1 = p0 + ppb < P ? p0 + ppb : P;
-    if (p0 >= P) {
+    const i64 n_ev = start[P], G = gridDim.x;
+    const i64 p0 = part_first(start, P, n_ev, G, blockIdx.x), p1 = part_first(start, P, n_ev, G, blockIdx.x + 1);
+    if (p0 >= p1) {
         if (t == 0) {
             seg_cnt[blockIdx.x] = 0;
             seg_base[blockIdx.x] = 0;
@@ -146,14 +202,25 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
         return;
     }
     const i64 out_base = start[p0];
-    if (t == 0) cur = 0;
+    if (t == 0) {
+        cur = 0;
+        nocc = 0;
+    }
+    for (int j = t; j < PT_SLOTS; j += PT_BLOCK) {  // the output pass empties the slots for the next partition
+        tk[j] = EMPTY;
+        tc[j] = 0;
+    }
+    __syncthreads();
     for (i64 p = p0; p < p1; ++p) {
-        for (int j = t; j < PT_SLOTS; j += PT_BLOCK) {
-            tk[j] = EMPTY;
-            tc[j] = 0;
+        const i64 a = start[p], b = start[p + 1], qa = qstart[p], qb = qstart[p + 1];
+        // the partition's first lookups are loaded now, so that their latency overlaps the inserts
+        const bool has_q = qa + t < qb;
+        u64 lk = EMPTY;
+        u32 lv = 0;
+        if (has_q) {
+            lk = qk[qa + t];
+            lv = qv[qa + t];
         }
-        __syncthreads();
-        const i64 a = start[p], b = start[p + 1];
         for (i64 i0 = a; i0 < b; i0 += (i64)PT_BLOCK * PT_ITEMS) {  // the same rounds for every wave
             u64 key[PT_ITEMS];
 #pragma unroll
@@ -166,23 +233,33 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
                 const bool valid = key[r] != EMPTY;
                 const u64 vb = __ballot(valid);
                 if (!vb) continue;
+                if (__builtin_amdgcn_readfirstlane(nocc) >= PT_LIMIT) {  // overfull: the host repartitions
+                    if (lane == 0) atomicOr(&flags[0], 1u);
+                    continue;
+                }
                 // the lanes holding the wave's first key add once (a hot pair would serialize the LDS atomics)
-                const int ld = __ffsll((unsigned long long)vb) - 1;
-                const u64 k0 = bcast_u64(key[r], ld);
+                const int ld = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)vb) - 1);
+                const u64 k0 = readlane_u64(key[r], ld);
                 const bool same = valid && key[r] == k0;
                 const u64 m = __ballot(same);
-                if (same && lane != ld) continue;
-                if (valid) pt_insert(tk, tc, key[r], same ? (u32)__popcll(m) : 1u, flags);
+                bool fresh = false;
+                if (valid && (!same || lane == ld)) fresh = pt_add(tk, tc, key[r], same ? (u32)__popcll(m) : 1u);
+                const u64 fb = __ballot(fresh);
+                if (fb && lane == 0) atomicAdd(&nocc, (u32)__popcll(fb));
             }
         }
-        __syncthreads();
-        for (i64 j = qstart[p] + t; j < qstart[p + 1]; j += PT_BLOCK) {
-            const u64 key = qk[j];
-            qcnt[qv[j]] = key == EMPTY ? 0u : pt_find(tk, tc, key);
+        lds_barrier();
+        if (qb > qa) {  // block-uniform
+            if (has_q) qcnt[lv] = lk == EMPTY ? 0u : pt_find(tk, tc, lk);
+            for (i64 j = qa + PT_BLOCK + t; j < qb; j += PT_BLOCK) {
+                const u64 key = qk[j];
+                qcnt[qv[j]] = key == EMPTY ? 0u : pt_find(tk, tc, key);
+            }
+            lds_barrier();  // every lookup has probed before the output pass empties the slots
         }
         for (int j0 = 0; j0 < PT_SLOTS; j0 += PT_BLOCK) {
             const int j = j0 + t;
-            const u64 key = tk[j];
+            const u64 key = j < PT_SLOTS ? tk[j] : EMPTY;
             const bool occ = key != EMPTY;
             const u64 bal = __ballot(occ);
             if (!bal) continue;
@@ -193,6 +270,8 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
                 const u64 at = (u64)out_base + off + (u64)__popcll(bal & lanemask_lt());
                 const u64 pk = unmix64(key);
                 const u32 n = tc[j];
+                tk[j] = EMPTY;
+                tc[j] = 0;
                 if (cb == 0) {
                     out_k[at] = pk;
                     out_c[at] = n;
@@ -203,7 +282,8 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
                 }
             }
         }
-        __syncthreads();
+        if (t == 0) nocc = 0;
+        lds_barrier();  // the slots are empty again (the output stores need not have completed)
     }
     if (t == 0) {
         seg_cnt[blockIdx.x] = cur;
@@ -434,19 +514,18 @@ extern "C" int ng_part_lookups(const int* ctx_of, const u16* tgt, const int* pos
 }
 
 // Count the sorted events partition by partition (start: ng_part_bounds' of 2^pbits partitions) with `grid` blocks
-// of consecutive partitions: block b's distinct pairs (pair key, count) at out_k/out_c + seg_base[b], seg_cnt[b] of
+// (at most 65536) of consecutive partitions holding about n / grid events each: block b's distinct pairs (pair key, count) at out_k/out_c + seg_base[b], seg_cnt[b] of
 // them (out_k/out_c hold as many items as ev). Lookups (qk sorted like ev, qv their query positions, qstart their
-// bounds) get qcnt[qv[j]] = the pair's count or 0. flags[0] bit 0: a partition held more than 8192 distinct pairs
+// bounds) get qcnt[qv[j]] = the pair's count or 0. flags[0] bit 0: a partition reached 7000 distinct pairs
 // (its count is incomplete: repartition with one more bit).
 extern "C" int ng_part_count(const u64* ev, const i64* start, int pbits, const u64* qk, const u32* qv,
                              const i64* qstart, u64* out_k, u32* out_c, int cb, u64* esc_k, u32* esc_c, u64 esc_cap,
                              u32* seg_cnt, i64* seg_base, u32* qcnt, u32* flags, int grid, void* stream) {
-    if (pbits < 0 || pbits > 24 || grid <= 0 || cb < 0 || cb > 44) return -1;
+    if (pbits < 0 || pbits > 24 || grid <= 0 || grid > 65536 || cb < 0 || cb > 44) return -1;
     if (cb > 0 && (esc_k == nullptr || esc_c == nullptr || esc_cap == 0)) return -1;
     if (cb == 0 && out_c == nullptr) return -1;
     const i64 P = 1ll << pbits;
-    const i64 ppb = (P + grid - 1) / grid;
-    part_count_k<<<grid, PT_BLOCK, 0, (hipStream_t)stream>>>(ev, start, P, ppb, qk, qv, qstart, out_k, out_c, cb, esc_k,
+    part_count_k<<<grid, PT_BLOCK, 0, (hipStream_t)stream>>>(ev, start, P, qk, qv, qstart, out_k, out_c, cb, esc_k,
                                                              esc_c, esc_cap, seg_cnt, seg_base, qcnt, flags);
     return (int)hipGetLastError();
 }

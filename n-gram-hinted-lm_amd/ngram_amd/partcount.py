@@ -5,7 +5,7 @@ whose counts go through one atomic hash table per level, record_367_gpu_counts/t
 An emitting scan (ng_scan_emit) leaves each block's events — mix64(context id << 16 | next), a bijection of the pair
 key — in the block's own region. `pack_events` packs the regions into one array; `count_events` sorts the events by
 their top pbits (a hash partition of the pairs, sized so a partition holds about PART_TARGET distinct pairs: the LDS
-table holds 8192), counts every partition in LDS (ng_part_count), answers the lookups (the query positions' (context,
+table holds 7000), counts every partition in LDS (ng_part_count), answers the lookups (the query positions' (context,
 target) pairs, hashed and sorted the same way) and packs the distinct pairs, by default as one word each: pair key <<
 (48 - cb) | count (a count too large for the field also goes to an escape table). `summarize` sorts the words by
 context (keys only) and makes each present context's record: total, pairs, top entries (ng_ctx_summary), which
@@ -24,7 +24,7 @@ import torch
 
 from .lib import Lib, i32, u64
 
-PART_TARGET = 4096  # distinct pairs per partition aimed at (the LDS table holds 8192)
+PART_TARGET = 4096  # distinct pairs per partition aimed at (the LDS table takes up to 7000)
 PART_BLOCKS = 2048  # count blocks, each a run of consecutive partitions
 PART_MIN_BITS = 11  # at least this many partition bits: enough blocks for the lookups as well
 ESC_CAP = 1 << 20  # packed pairs whose count exceeds the word's count field, per level
