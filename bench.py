@@ -49,6 +49,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--query-tokens", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other configurations' measurements")
+    ap.add_argument("--only", default="", choices=("", "c2", "c4", "c5"),
+                    help="measure only this secondary configuration and print its JSON (for profiling)")
     ap.add_argument("--mode", default="part", choices=("engine", "part", "record", "partitioned"),
                     help="CountBuild.mode")
     ap.add_argument("--cpu-tokens", type=int, default=100_000_000, help="CPU baseline: corpus prefix")
@@ -289,7 +291,15 @@ def main() -> None:
     from ngram_amd.counts import CountBuild, device_queries
 
     torch.cuda.set_device(0)
+    if args.only in ("c2", "c4"):
+        r = bench_c2(args.steps, args.warmup, not args.no_cpu) if args.only == "c2" else bench_c4(not args.no_cpu)
+        r.pop("sizes", None)
+        print(json.dumps({"config": args.only, **r}))
+        return
     cfg, flat, bounds, tok, sizes, starts, q, np = make_workload(args.config, args.train_tokens, args.query_tokens)
+    if args.only == "c5":
+        print(json.dumps({"config": "c5", **bench_c5(tok, flat, args.steps, args.warmup, not args.no_cpu)}))
+        return
     T = sum(sizes)
     flat_host = flat[: min(args.cpu_tokens, int(flat.numel()))].cpu()
     q_host = q[: args.cpu_queries + 1].cpu()
