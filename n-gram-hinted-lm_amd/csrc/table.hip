@@ -255,7 +255,7 @@ extern "C" int ng_table_lookup(const u64* keys, i64 n, const u64* ck, u64 ccap, 
 // (ng_ctx_summary's with topk 8).
 extern "C" int ng_ctx_kth(const u64* w, int cb, const u64* esc_k, const u32* esc_c, u64 esc_cap, const u32* rec,
                           const i64* ids, i64 m, int kth, u64* thr, void* stream) {
-    if (kth < 1 || cb <= 0 || cb > 32 || esc_cap == 0) return -1;
+    if (kth < 1 || cb <= 0 || cb > 44 || esc_cap == 0) return -1;
     if (m > 0) {
         const int g = m < 65536 ? (int)m : 65536;
         ctx_kth_k<<<g, 256, 0, (hipStream_t)stream>>>(w, cb, esc_k, esc_c, esc_cap, rec, ids, m, kth, thr);
@@ -272,7 +272,7 @@ extern "C" int ng_table_query(const u16* x, const int* avail, const u16* tgt, i6
                               const u64* w, int cb, const u64* esc_k, const u32* esc_c, u64 esc_cap, const u32* rec,
                               const u64* thr, u32 cnt_top, int kout, int* out_tot, int* out_dist, int* out_cnt,
                               u16* out_tok, u32* out_tcnt, void* stream) {
-    if (kout < 0 || kout > 8 || cb <= 0 || cb > 32 || esc_cap == 0 || ccap == 0) return -1;
+    if (kout < 0 || kout > 8 || cb <= 0 || cb > 44 || esc_cap == 0 || ccap == 0) return -1;
     if (kout > 0 && (out_tok == nullptr || out_tcnt == nullptr)) return -1;
     if (n <= 0) return 0;
     hipStream_t st = (hipStream_t)stream;

@@ -113,6 +113,26 @@ def test_overflow_reruns(corpus, reference, monkeypatch):
     assert np.array_equal(tot[:, 0], reference[4]["tot"]) and np.array_equal(cnt[:, 0], reference[4]["cnt"])
 
 
+def test_escaped_counts(corpus, reference, monkeypatch):
+    """Packed words with a 4-bit count field (context bits forced to 44): every count of 15 or more lives in the
+    escape table, for the summary's totals and tops, the CNT_TOP thresholds and the queries' binary searches."""
+    from ngram_amd import partcount as P
+
+    monkeypatch.setattr(P, "PACK_MIN_BITS", 44)
+    ct = CountTable.create(corpus.shards(), [1, 3], 1, [])
+    ct.build()
+    assert all(lv.cb == 44 for lv in ct.tables)
+    assert int((ct.tables[0].esc[0] != -1).sum().item()) > 100  # level 1 holds many counts >= 15
+    tot, dist, cnt = ct.query_counts(corpus.query)
+    _, _, cnt_all = ct.query_counts(corpus.query, top=1 << 16)
+    tt, tc = ct.query_topk(corpus.query, 8)
+    for li, k in enumerate([1, 3]):
+        o = reference[k]
+        assert np.array_equal(tot[:, li], o["tot"]) and np.array_equal(dist[:, li], o["dist"]), k
+        assert np.array_equal(cnt[:, li], o["cnt"]) and np.array_equal(cnt_all[:, li], o["cnt_all"]), k
+        assert np.array_equal(tt[:, li], o["top_tok"]) and np.array_equal(tc[:, li], o["top_cnt"]), k
+
+
 def test_cache_ladder_rung(corpus, tmp_path):
     from ngram_amd.cache_ladder import GpuCountIndex
 
