@@ -111,11 +111,12 @@ int ng_scan_count(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, u
                   uint32_t* flags, int grid, int sparse, void* stream);
 /* the emitting scan: block b of `grid` appends its hits' mix64(context id << 16 | next) to ev[b * region ...] and
  * stores how many in ev_count[b]; region >= ng_emit_region(L, grid) = ceil(L / (grid * 8192)) * 8192; flags[0] bit 2
- * a region overflowed. sparse as ng_scan_count's */
+ * a region overflowed. sparse as ng_scan_count's. dhist (may be NULL): block b's events per top-8-bit digit d at
+ * dhist[d * dstride + b] (dstride >= grid), for ng_seg_scatter */
 ng_u64 ng_emit_region(ng_i64 L, int grid);
 int ng_scan_emit(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, uint32_t* bm_out, const ng_u64* vt,
                  ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, ng_u64* ev, ng_u64 region, uint32_t* ev_count,
-                 uint32_t* flags, int grid, int sparse, void* stream);
+                 uint32_t* flags, int grid, int sparse, uint32_t* dhist, ng_i64 dstride, void* stream);
 /* a level scan with optional outputs over a bitmap-gated range (plist NULL: [0, L) gated by bm_in in ng_scan_count's
  * sparse modes, hit bitmap into bm_out) or over listed positions (plist: n corpus positions); hit (may be NULL):
  * hit[context id] = 1 per hit; ev (may be NULL): block b of grid appends per hit mix64(pair key) (what 0) or its
@@ -164,8 +165,17 @@ int ng_seg_offsets(const uint32_t* cnt, ng_i64 nseg, ng_u64* offsets, void* stre
 /* segment s = cnt[s] items at src + (bases ? bases[s] : s * region) packed to dst + offsets[s]; values may be NULL */
 int ng_seg_gather(const ng_u64* src_k, const uint32_t* src_v, ng_u64 region, const ng_i64* bases, const uint32_t* cnt,
                   ng_i64 nseg, const ng_u64* offsets, ng_u64* dst_k, uint32_t* dst_v, void* stream);
-/* start[p], p = 0..2^pbits, of events sorted by their top pbits (pbits <= 24) */
-int ng_part_bounds(const ng_u64* ev, ng_i64 n, int pbits, ng_i64* start, void* stream);
+/* start[p], p = 0..2^pbits, of events sorted by their top pbits (pbits <= 24): msd 0 in key order; msd 1 grouped by
+ * the top 8 bits first (ng_seg_scatter), then stably by the pbits - 8 bits below, partition (lo, hi) = lo << 8 | hi */
+int ng_part_bounds(const ng_u64* ev, ng_i64 n, int pbits, int msd, ng_i64* start, void* stream);
+/* the partition sort's first pass from ng_scan_emit's regions: nseg segments of ev_count[s] events at src + s * R
+ * scattered by their top 8 bits to out at dpre (u32 [256 * nseg], the exclusive scan of the digit histograms,
+ * digit-major; fewer than 2^32 events); the order within a digit is free */
+int ng_seg_scatter(const ng_u64* src, ng_u64 R, const uint32_t* ev_count, const uint32_t* dpre, ng_i64 nseg,
+                   ng_u64* out, void* stream);
+/* exclusive prefix sum of n u32 (out may alias in), *total (may be NULL) the sum; CUB-style two-phase temp storage */
+int ng_exclusive_scan_u32(void* temp, size_t* temp_bytes, const uint32_t* in, uint32_t* out, ng_i64 n,
+                          ng_u64* total, void* stream);
 /* lookups of n query positions i = pos[j] (pos NULL: j): qk[j] = mix64(ctx_of[i] << 16 | tgt[i]) for ids in
  * [lo, hi), else EMPTY; qv[j] = i */
 int ng_part_lookups(const int* ctx_of, const uint16_t* tgt, const int* pos, ng_i64 n, ng_i64 lo, ng_i64 hi,

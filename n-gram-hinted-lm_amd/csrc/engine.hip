@@ -63,6 +63,14 @@ struct EmitSink {
     u32* ev_count;
     int what;
     unsigned char* hit;
+    u32* dhist;   // with what 0 (may be NULL): the block's events per top-8-bit digit, at dhist[digit * dstride + block]
+    i64 dstride;
+};
+
+// A scan block's LDS for its sink: the emit cursor and the digit histogram.
+struct SinkShared {
+    u32 cur;
+    u32 dh[256];
 };
 
 // A lane's hit (count and exist sinks; the emit sink uses emit_wave / emit_lane).
@@ -76,39 +84,47 @@ __device__ __forceinline__ void sink_hit(const S& s, u64 key, bool full, u32* fl
 }
 
 // The wave's hits (b = ballot of `hit`) appended in lane order: called by every lane of the wave.
-__device__ __forceinline__ void emit_wave(const EmitSink& s, u32* cur, u64 b, bool hit, u64 key, i64 p, u32* flags) {
+__device__ __forceinline__ void emit_wave(const EmitSink& s, SinkShared* ss, u64 b, bool hit, u64 key, i64 p, u32* flags) {
     if (!b) return;
     u32 off = 0;
-    if (lane_id() == 0) off = atomicAdd(cur, (u32)__popcll(b));
+    if (lane_id() == 0) off = atomicAdd(&ss->cur, (u32)__popcll(b));
     off = (u32)__shfl((int)off, 0, WAVE);
     if (hit) {
         const u64 at = (u64)off + (u64)__popcll(b & lanemask_lt());
-        if (at < s.region) s.ev[(u64)blockIdx.x * s.region + at] = s.what ? (u64)p : mix64(key);
+        const u64 e = s.what ? (u64)p : mix64(key);
+        if (at < s.region) s.ev[(u64)blockIdx.x * s.region + at] = e;
         else atomicOr(&flags[0], 4u);
+        if (s.dhist) atomicAdd(&ss->dh[e >> 56], 1u);
         if (s.hit) s.hit[key >> 16] = 1;
     }
 }
 
-__device__ __forceinline__ void emit_lane(const EmitSink& s, u32* cur, u64 key, i64 p, u32* flags) {
-    const u64 at = atomicAdd(cur, 1u);
-    if (at < s.region) s.ev[(u64)blockIdx.x * s.region + at] = s.what ? (u64)p : mix64(key);
+__device__ __forceinline__ void emit_lane(const EmitSink& s, SinkShared* ss, u64 key, i64 p, u32* flags) {
+    const u64 at = atomicAdd(&ss->cur, 1u);
+    const u64 e = s.what ? (u64)p : mix64(key);
+    if (at < s.region) s.ev[(u64)blockIdx.x * s.region + at] = e;
     else atomicOr(&flags[0], 4u);
+    if (s.dhist) atomicAdd(&ss->dh[e >> 56], 1u);
     if (s.hit) s.hit[key >> 16] = 1;
 }
 
 template <class S>
-__device__ __forceinline__ void sink_begin(u32* cur) {
+__device__ __forceinline__ void sink_begin(const S& s, SinkShared* ss) {
     if constexpr (S::KIND == 2) {
-        if (threadIdx.x == 0) *cur = 0;
+        if (threadIdx.x == 0) ss->cur = 0;
+        if (s.dhist)
+            for (int d = threadIdx.x; d < 256; d += blockDim.x) ss->dh[d] = 0;
         __syncthreads();
     }
 }
 
 template <class S>
-__device__ __forceinline__ void sink_end(const S& s, u32* cur) {
+__device__ __forceinline__ void sink_end(const S& s, SinkShared* ss) {
     if constexpr (S::KIND == 2) {
         __syncthreads();
-        if (threadIdx.x == 0) s.ev_count[blockIdx.x] = *cur < s.region ? *cur : (u32)s.region;
+        if (threadIdx.x == 0) s.ev_count[blockIdx.x] = ss->cur < s.region ? ss->cur : (u32)s.region;
+        if (s.dhist)
+            for (int d = threadIdx.x; d < 256; d += blockDim.x) s.dhist[(i64)d * s.dstride + blockIdx.x] = ss->dh[d];
     }
 }
 
@@ -124,8 +140,8 @@ __global__ void __launch_bounds__(256) scan_dense_k(const u16* __restrict__ tok,
                                                     u32* __restrict__ bm_out, const u64* __restrict__ vt, u64 vcap,
                                                     const u32* __restrict__ vrep, const u16* __restrict__ x, S sink,
                                                     u32* flags) {
-    __shared__ u32 cur;
-    sink_begin<S>(&cur);
+    __shared__ SinkShared ss;
+    sink_begin<S>(sink, &ss);
     const int lane = lane_id();
     const i64 nwords = (L + 31) >> 5;
     const i64 stride = (i64)gridDim.x * blockDim.x;
@@ -141,10 +157,10 @@ __global__ void __launch_bounds__(256) scan_dense_k(const u16* __restrict__ tok,
         const u64 b = __ballot(hit);
         if (lane == 0) bm_out[base >> 5] = (u32)b;
         if (lane == 32 && w < nwords) bm_out[w] = (u32)(b >> 32);
-        if constexpr (S::KIND == 2) emit_wave(sink, &cur, b, hit, key, p, flags);
+        if constexpr (S::KIND == 2) emit_wave(sink, &ss, b, hit, key, p, flags);
         else if (hit) sink_hit(sink, key, full, flags);
     }
-    sink_end(sink, &cur);
+    sink_end(sink, &ss);
 }
 
 // Listed positions: a lane per entry of plist (n corpus positions), no bitmap.
@@ -153,8 +169,8 @@ __global__ void __launch_bounds__(256) scan_list_k(const u16* __restrict__ tok, 
                                                    int k, const u64* __restrict__ vt, u64 vcap,
                                                    const u32* __restrict__ vrep, const u16* __restrict__ x, S sink,
                                                    u32* flags) {
-    __shared__ u32 cur;
-    sink_begin<S>(&cur);
+    __shared__ SinkShared ss;
+    sink_begin<S>(sink, &ss);
     const int lane = lane_id();
     const i64 stride = (i64)gridDim.x * blockDim.x;
     for (i64 base = blockIdx.x * (i64)blockDim.x + (threadIdx.x & ~(WAVE - 1)); base < n; base += stride) {
@@ -167,10 +183,10 @@ __global__ void __launch_bounds__(256) scan_list_k(const u16* __restrict__ tok, 
             key = probe_key<K>(tok, p, k, vt, vcap, vrep, x, flags);
         }
         const bool hit = key != EMPTY;
-        if constexpr (S::KIND == 2) emit_wave(sink, &cur, __ballot(hit), hit, key, p, flags);
+        if constexpr (S::KIND == 2) emit_wave(sink, &ss, __ballot(hit), hit, key, p, flags);
         else if (hit) sink_hit(sink, key, full, flags);
     }
-    sink_end(sink, &cur);
+    sink_end(sink, &ss);
 }
 
 // Sparse levels: a lane per bitmap word, its set bits in turn.
@@ -179,8 +195,8 @@ __global__ void __launch_bounds__(256) scan_sparse_k(const u16* __restrict__ tok
                                                      u32* __restrict__ bm_out, const u64* __restrict__ vt, u64 vcap,
                                                      const u32* __restrict__ vrep, const u16* __restrict__ x, S sink,
                                                      u32* flags) {
-    __shared__ u32 cur;
-    sink_begin<S>(&cur);
+    __shared__ SinkShared ss;
+    sink_begin<S>(sink, &ss);
     const i64 nwords = (L + 31) >> 5;
     for (i64 w = blockIdx.x * (i64)blockDim.x + threadIdx.x; w < nwords; w += (i64)gridDim.x * blockDim.x) {
         const bool full = sink_full<S>(flags);
@@ -193,13 +209,13 @@ __global__ void __launch_bounds__(256) scan_sparse_k(const u16* __restrict__ tok
             const u64 key = probe_key<K>(tok, p, k, vt, vcap, vrep, x, flags);
             if (key != EMPTY) {
                 out |= 1u << b;
-                if constexpr (S::KIND == 2) emit_lane(sink, &cur, key, p, flags);
+                if constexpr (S::KIND == 2) emit_lane(sink, &ss, key, p, flags);
                 else sink_hit(sink, key, full, flags);
             }
         }
         bm_out[w] = out;
     }
-    sink_end(sink, &cur);
+    sink_end(sink, &ss);
 }
 
 // Gated levels, any density: a block takes 256 bitmap words (8192 positions) at a time; each wave lists its 64 words'
@@ -213,8 +229,8 @@ __global__ void __launch_bounds__(256) scan_compact_k(const u16* __restrict__ to
                                                       const u16* __restrict__ x, S sink, u32* flags) {
     __shared__ u32 list[4][64 * 32];
     __shared__ u32 words[4][64];
-    __shared__ u32 cur;
-    sink_begin<S>(&cur);
+    __shared__ SinkShared ss;
+    sink_begin<S>(sink, &ss);
     const int lane = lane_id(), w = threadIdx.x / WAVE;
     const i64 nwords = (L + 31) >> 5;
     for (i64 g0 = (i64)blockIdx.x * 256; g0 < nwords; g0 += (i64)gridDim.x * 256) {
@@ -250,14 +266,14 @@ __global__ void __launch_bounds__(256) scan_compact_k(const u16* __restrict__ to
             const bool hit = key != EMPTY;
             if (hit) atomicOr(&words[w][lp >> 5], 1u << (lp & 31));
             if constexpr (S::KIND == 2)
-                emit_wave(sink, &cur, __ballot(hit), hit, key, ((g0 + w * 64) << 5) + lp, flags);
+                emit_wave(sink, &ss, __ballot(hit), hit, key, ((g0 + w * 64) << 5) + lp, flags);
             else if (hit) sink_hit(sink, key, full, flags);
         }
         __syncthreads();
         if (wi < nwords) bm_out[wi] = words[w][lane];
         __syncthreads();
     }
-    sink_end(sink, &cur);
+    sink_end(sink, &ss);
 }
 
 __global__ void bits_popc_k(const u32* __restrict__ bm, i64 nwords, u32* __restrict__ off) {
@@ -543,7 +559,8 @@ extern "C" int ng_scan_exist(const u16* tok, i64 L, int k, const u32* bm_in, u32
 
 // The emitting scan: block b of the `grid` blocks appends its hits' mix64(pair key) to ev[b * region ...] and stores
 // their number in ev_count[b]; region must be at least ng_emit_region(L, grid). flags[0] bit 2: a region overflowed
-// (only with a smaller region). sparse as ng_scan_count's.
+// (only with a smaller region). sparse as ng_scan_count's. dhist (may be NULL): block b's events per top-8-bit digit
+// d at dhist[d * dstride + b] (dstride >= grid), for ng_seg_scatter.
 extern "C" u64 ng_emit_region(i64 L, int grid) {
     if (L <= 0 || grid <= 0) return 0;
     const u64 per = (u64)grid * 8192ull;
@@ -552,11 +569,16 @@ extern "C" u64 ng_emit_region(i64 L, int grid) {
 
 extern "C" int ng_scan_emit(const u16* tok, i64 L, int k, const u32* bm_in, u32* bm_out, const u64* vt, u64 vcap,
                             const u32* vrep, const u16* x, u64* ev, u64 region, u32* ev_count, u32* flags, int grid,
-                            int sparse, void* stream) {
-    if (L <= 0) return 0;
-    if (grid <= 0 || region == 0 || region > 0xFFFFFFFFull) return -1;
-    if (launch_scan(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, EmitSink{ev, region, ev_count, 0, nullptr}, flags,
-                    grid, sparse, (hipStream_t)stream) != 0)
+                            int sparse, u32* dhist, i64 dstride, void* stream) {
+    if (grid <= 0 || region == 0 || region > 0xFFFFFFFFull || (dhist && dstride < grid)) return -1;
+    if (L <= 0) {
+        fill_u32_n(ev_count, 0u, grid, (hipStream_t)stream);
+        if (dhist)
+            for (int d = 0; d < 256; ++d) fill_u32_n(dhist + (i64)d * dstride, 0u, grid, (hipStream_t)stream);
+        return (int)hipGetLastError();
+    }
+    if (launch_scan(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, EmitSink{ev, region, ev_count, 0, nullptr, dhist, dstride},
+                    flags, grid, sparse, (hipStream_t)stream) != 0)
         return -1;
     return (int)hipGetLastError();
 }

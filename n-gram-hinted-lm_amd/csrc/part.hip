@@ -14,6 +14,7 @@
 // Every event is read three times and written twice, in coalesced runs, and counted by LDS atomics; on MI355X global
 // atomics run at about 27 G/s scattered and 80 M/s on one address, far below these streams.
 #include "part.h"
+#include "prim.h"
 
 namespace {
 
@@ -57,21 +58,101 @@ __global__ void __launch_bounds__(256) seg_gather_k(const u64* __restrict__ src_
     }
 }
 
-// start[p] = the first i with ev[i] >> (64 - pbits) >= p, for p = 0..P (ev sorted by its top pbits; start[P] = n).
-__global__ void part_bounds_k(const u64* __restrict__ ev, i64 n, int pbits, i64 P, i64* __restrict__ start) {
+// An event's partition: its top pbits, numbered in the order the partition sort leaves them. msd 0: sorted by the
+// top pbits (LSD). msd 1: first grouped by the top 8 bits, then stably sorted by the pbits - 8 bits below them, so
+// partition (lo, hi) = (bits [64 - pbits, 56), bits [56, 64)) is numbered lo << 8 | hi.
+__device__ __forceinline__ i64 part_id(u64 e, int pbits, int msd) {
+    if (pbits <= 0) return 0;
+    if (!msd || pbits <= 8) return (i64)(e >> (64 - pbits));
+    const u64 lo = (e >> (64 - pbits)) & ((1ull << (pbits - 8)) - 1);
+    return (i64)((lo << 8) | (e >> 56));
+}
+
+// start[p] = the first i with part_id(ev[i]) >= p, for p = 0..P (start[P] = n).
+__global__ void part_bounds_k(const u64* __restrict__ ev, i64 n, int pbits, int msd, i64 P, i64* __restrict__ start) {
     const i64 p = blockIdx.x * (i64)blockDim.x + threadIdx.x;
     if (p > P) return;
     i64 a = 0, b = n;
     if (p == P) a = n;
     else if (pbits > 0) {
-        const int sh = 64 - pbits;
         while (a < b) {
             const i64 m = (a + b) >> 1;
-            if ((i64)(ev[m] >> sh) < p) a = m + 1;
+            if (part_id(ev[m], pbits, msd) < p) a = m + 1;
             else b = m;
         }
     }  // pbits 0: one partition starting at 0
     start[p] = a;
+}
+
+// The partition sort's first pass straight from the emitting scan's regions: segment s (ev_count[s] events at
+// src + s * R) scattered by its events' top 8 bits, digit d of segment s starting at out + dpre[d * nseg + s] (the
+// exclusive scan of the scan's digit histograms, digit-major). The order within a digit is free (the passes after
+// this one are stable and only need the groups): a chunk of 8192 events is ranked by LDS counters, staged in LDS by
+// digit and written as per-digit runs. Replaces packing the regions into one array and a radix pass over it.
+#define SS_BLOCK 1024
+#define SS_ITEMS 8
+#define SS_CHUNK (SS_BLOCK * SS_ITEMS)
+__global__ void __launch_bounds__(SS_BLOCK) seg_scatter_k(const u64* __restrict__ src, u64 R,
+                                                         const u32* __restrict__ ev_count, const u32* __restrict__ dpre,
+                                                         i64 nseg, u64* __restrict__ out) {
+    __shared__ u64 stage[SS_CHUNK];
+    __shared__ u32 cnt[256], pre[256], base[256], wt[4];
+    const int t = threadIdx.x, lane = lane_id();
+    for (i64 sg = blockIdx.x; sg < nseg; sg += gridDim.x) {
+        const u32 n = ev_count[sg];
+        const u64* in = src + (u64)sg * R;
+        if (t < 256) base[t] = dpre[(i64)t * nseg + sg];
+        for (u32 c0 = 0; c0 < n; c0 += SS_CHUNK) {
+            if (t < 256) cnt[t] = 0;
+            __syncthreads();
+            u64 key[SS_ITEMS];
+            u32 rank[SS_ITEMS];
+#pragma unroll
+            for (int j = 0; j < SS_ITEMS; ++j) {
+                const u32 i = c0 + (u32)(j * SS_BLOCK + t);
+                key[j] = i < n ? in[i] : 0;
+            }
+#pragma unroll
+            for (int j = 0; j < SS_ITEMS; ++j) {
+                const u32 i = c0 + (u32)(j * SS_BLOCK + t);
+                rank[j] = i < n ? atomicAdd(&cnt[key[j] >> 56], 1u) : 0u;
+            }
+            __syncthreads();
+            u32 v = 0, incl = 0;
+            if (t < 256) {  // the first four waves: an exclusive scan of the 256 digit counts
+                v = cnt[t];
+                incl = v;
+#pragma unroll
+                for (int d = 1; d < WAVE; d <<= 1) {
+                    const u32 o = (u32)__shfl_up((int)incl, d, WAVE);
+                    if (lane >= d) incl += o;
+                }
+                if (lane == WAVE - 1) wt[t / WAVE] = incl;
+            }
+            __syncthreads();
+            if (t < 256) {
+                u32 before = 0;
+                for (int w = 0; w < t / WAVE; ++w) before += wt[w];
+                pre[t] = before + incl - v;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < SS_ITEMS; ++j) {
+                const u32 i = c0 + (u32)(j * SS_BLOCK + t);
+                if (i < n) stage[pre[key[j] >> 56] + rank[j]] = key[j];
+            }
+            __syncthreads();
+            const u32 m = n - c0 < (u32)SS_CHUNK ? n - c0 : (u32)SS_CHUNK;
+            for (u32 i = t; i < m; i += SS_BLOCK) {
+                const u64 k = stage[i];
+                const u32 d = (u32)(k >> 56);
+                out[(u64)base[d] + i - pre[d]] = k;
+            }
+            __syncthreads();
+            if (t < 256) base[t] += cnt[t];
+        }
+        __syncthreads();  // base is read before the next segment overwrites it
+    }
 }
 
 // Lookup j of query position i = pos[j] (pos NULL: i = j): the mixed pair key of its (context, target) if its
@@ -496,11 +577,37 @@ extern "C" int ng_seg_gather(const u64* src_k, const u32* src_v, u64 region, con
     return (int)hipGetLastError();
 }
 
-// start[p] for p = 0..2^pbits (i64[2^pbits + 1]) of events sorted by their top pbits (0 <= pbits <= 24).
-extern "C" int ng_part_bounds(const u64* ev, i64 n, int pbits, i64* start, void* stream) {
-    if (pbits < 0 || pbits > 24 || n < 0) return -1;
+// start[p] for p = 0..2^pbits (i64[2^pbits + 1]) of events sorted by their top pbits (0 <= pbits <= 24): msd 0 in
+// key order; msd 1 grouped first by the top 8 bits (ng_seg_scatter), then stably by the pbits - 8 bits below them,
+// partition (lo, hi) numbered lo << 8 | hi.
+extern "C" int ng_part_bounds(const u64* ev, i64 n, int pbits, int msd, i64* start, void* stream) {
+    if (pbits < 0 || pbits > 24 || n < 0 || (msd != 0 && msd != 1)) return -1;
     const i64 P = 1ll << pbits;
-    part_bounds_k<<<grid_for(P + 1, 256), 256, 0, (hipStream_t)stream>>>(ev, n, pbits, P, start);
+    part_bounds_k<<<grid_for(P + 1, 256), 256, 0, (hipStream_t)stream>>>(ev, n, pbits, msd, P, start);
+    return (int)hipGetLastError();
+}
+
+// Exclusive prefix sum of n u32 (out may alias in), *total (device, may be NULL) the sum as u64; CUB-style two-phase
+// temp storage (temp NULL: *temp_bytes set).
+extern "C" int ng_exclusive_scan_u32(void* temp, size_t* temp_bytes, const u32* in, u32* out, i64 n, u64* total,
+                                     void* stream) {
+    if (n < 0 || temp_bytes == nullptr) return -1;
+    if (temp == nullptr) {
+        *temp_bytes = prim::scan_u32_temp_bytes(n);
+        return 0;
+    }
+    return prim::exclusive_scan_u32(in, out, n, total, temp, (hipStream_t)stream);
+}
+
+// The partition sort's first pass from an emitting scan's regions (seg_scatter_k): nseg segments of ev_count[s]
+// events at src + s * R, scattered by their top 8 bits to out at the offsets dpre (u32 [256 * nseg], the exclusive
+// scan of ng_scan_emit's digit histograms, digit-major; the events number below 2^32).
+extern "C" int ng_seg_scatter(const u64* src, u64 R, const u32* ev_count, const u32* dpre, i64 nseg, u64* out,
+                              void* stream) {
+    if (nseg < 0 || R == 0 || R > 0xFFFFFFFFull) return -1;
+    if (nseg == 0) return 0;
+    const i64 g = nseg < 16384 ? nseg : 16384;
+    seg_scatter_k<<<(unsigned)g, SS_BLOCK, 0, (hipStream_t)stream>>>(src, R, ev_count, dpre, nseg, out);
     return (int)hipGetLastError();
 }
 

@@ -26,11 +26,11 @@ from .data import BOS, HEADER_BYTES, shard_tokens
 from .gpu_val_stats import PAIRS as GVS_PAIRS
 from .gpu_val_stats import ValIndex, layout
 from .lib import Lib, i32, u64
-from .partcount import count_events, emit_region, pack_events, record_tops, summarize
+from .partcount import count_events, emit_region, record_tops, summarize
 from .qindex import QueryIndex
 
 GAP = 32
-SCAN_BLOCKS_PER_CU = 32  # level-scan blocks (grid-stride) per compute unit
+SCAN_BLOCKS_PER_CU = 8  # level-scan blocks (grid-stride) per compute unit (c3 sweep: 8 fastest of 4-32)
 LEVELS = (2, 3, 4, 5, 6, 10, 20)
 LEVEL_SHARDS = {2: 103, 3: 370, 4: 370, 5: 370}
 PAIRS = {2: (82.17e6, 0.620), 3: (62.30e6, 0.667), 4: (26.39e6, 0.694), 5: (8.99e6, 0.706), 6: (3.17e6, 0.705),
@@ -418,12 +418,13 @@ class CountBuild:
             vi = QueryIndex(self.elib, x, avail, k, seen)
             index_t += time.perf_counter() - t0
             t0 = time.perf_counter()
-            ev, n_ev = self._part_emit(k, vi, bms, regions, R)
+            seg = self._part_emit(k, vi, bms, regions, R)
             t1 = time.perf_counter()
             ev_fn = lambda name, n, k=k: self._event(name, k, -1, n)  # noqa: E731
-            c = count_events(self.elib, self.lib, ev, n_ev, vi.ids, self.dratio.get(k, 1.0), (vi.ctx_of, tgt, seen),
-                             event=ev_fn)
-            del ev
+            c = count_events(self.elib, self.lib, None, 0, vi.ids, self.dratio.get(k, 1.0), (vi.ctx_of, tgt, seen),
+                             event=ev_fn, seg=seg)
+            del seg
+            n_ev = c.n_ev
             self.dratio[k] = c.U / max(1, n_ev)
             t2 = time.perf_counter()
             scan_t += t1 - t0
@@ -457,11 +458,13 @@ class CountBuild:
         return out
 
     def _part_emit(self, k, vi, bms, regions, R):
-        """Level k's scan of every shard it counts, hits emitted to per-block regions, then packed: (events, n)."""
+        """Level k's scan of every shard it counts, hits emitted to per-block regions with each block's top-digit
+        histogram: count_events' seg = (regions, R, ev_count, dhist, nseg)."""
         elib, dev, G = self.elib, self.tok.device, self.grid
         shards = [i for i in range(len(self.sizes)) if i < self.level_shards[k]]
         nseg = len(shards) * G
         ev_count = torch.zeros(max(nseg, 1), dtype=torch.int32, device=dev)
+        dhist = torch.empty(256 * max(nseg, 1), dtype=torch.int32, device=dev)
         flags = torch.zeros(2, dtype=torch.int32, device=dev)
         for j, i in enumerate(shards):
             st, n = self.starts[i], self.sizes[i]
@@ -475,11 +478,11 @@ class CountBuild:
             e0.record()
             elib("ng_scan_emit", self.tok[st:], n32, i32(k), bm_in, bms[k][st // 32 :], vi.table, u64(vi.cap), vi.rep,
                  self.x, regions[j * G * R :], u64(R), ev_count[j * G :], flags, i32(G),
-                 i32(self._scan_mode(si, scanned)))
+                 i32(self._scan_mode(si, scanned)), dhist[j * G :], nseg)
             e1.record()
         if int(flags[0].item()) & 4:
             raise RuntimeError(f"k={k}: an emit region overflowed")
-        return pack_events(elib, regions, R, ev_count, nseg, lambda name, n: self._event(name, k, -1, n))
+        return regions, R, ev_count, dhist, nseg
 
     def _owner_packed(self, li, k, vi, c, tgt, out, want, zero_tops):
         """The owner side from packed pairs: per present context its record (sorted by context, keys only), then per

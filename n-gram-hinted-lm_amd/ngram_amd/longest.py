@@ -58,7 +58,7 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
     dev = x.device
     N, L = x.numel(), tok.numel()
     nwords = L // 32
-    grid = torch.cuda.get_device_properties(dev).multi_processor_count * 32
+    grid = torch.cuda.get_device_properties(dev).multi_processor_count * SCAN_BLOCKS_PER_CU
     t0 = time.perf_counter()
     length = torch.zeros(N, dtype=torch.int32, device=dev)
     # the queried positions, as a list; each level keeps the ones still matching (the lists shrink fast)
@@ -124,15 +124,18 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
                        torch.empty(grid, dtype=torch.int32, device=dev),
                        torch.empty(nwords, dtype=torch.int32, device=dev))
             regions, R, ev_count, scratch_bm = big
+            dhist = torch.empty(256 * grid, dtype=torch.int32, device=dev)
             mode = 0 if nh * 2 > L else 2
             elib("ng_scan_emit", tok, L, i32(k), hs, scratch_bm, vi.table, u64(vi.cap), vi.rep, x, regions, u64(R),
-                 ev_count, flags, i32(grid), i32(mode))
-            ev, n_ev = pack_events(elib, regions, R, ev_count, grid)
+                 ev_count, flags, i32(grid), i32(mode), dhist, grid)
+            ev, n_ev, seg = None, 0, (regions, R, ev_count, dhist, grid)
         else:
             ev, n_ev = _scan_list(elib, tok, L, k, vi, x, hs, None, 0, flags, grid)
+            seg = None
         if int(flags[0].item()) & 4:
             raise RuntimeError(f"k={k}: an emit region overflowed")
-        c = count_events(elib, lib, ev, n_ev, vi.ids, _RATIO.get(k, 1.0))
+        c = count_events(elib, lib, ev, n_ev, vi.ids, _RATIO.get(k, 1.0), seg=seg)
+        n_ev = c.n_ev
         del ev
         _RATIO[k] = c.U / max(1, n_ev)
         o_tok = torch.zeros(m, dtype=torch.int16, device=dev)
@@ -157,6 +160,7 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
     return length, nxt, cnt, ladder
 
 
+SCAN_BLOCKS_PER_CU = 32  # scan blocks per compute unit
 LIST_DIV = 64  # a level's hits go to a position list once fewer than L / LIST_DIV (8 B each against L / 8 bitmap bytes)
 
 

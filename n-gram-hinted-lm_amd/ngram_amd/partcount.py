@@ -62,7 +62,7 @@ def pack_events(elib: Lib, regions: torch.Tensor, R: int, ev_count: torch.Tensor
 @dataclass
 class Counted:
     """A level's distinct pairs: `pairs` (U packed words when cb > 0, else pair keys with `counts`), the escape table
-    `esc` (keys, counts) of packed words, per-lookup target counts `qcnt`, the partition bits used."""
+    `esc` (keys, counts) of packed words, per-lookup target counts `qcnt`, the partition bits used, the events."""
 
     pairs: torch.Tensor
     counts: torch.Tensor | None
@@ -71,15 +71,36 @@ class Counted:
     U: int
     pbits: int
     cb: int
+    n_ev: int = 0
 
 
-def count_events(elib: Lib, lib: Lib, ev: torch.Tensor, n_ev: int, n_ids: int, ratio: float = 1.0,
-                 lookups: tuple | None = None, packed: bool = True, event=_no_event) -> Counted:
+def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids: int, ratio: float = 1.0,
+                 lookups: tuple | None = None, packed: bool = True, event=_no_event, seg: tuple | None = None) -> Counted:
     """Count n_ev events of context ids below n_ids. `ratio`: distinct pairs per event expected (sizes the
     partitions; a partition found too full repeats the count with one more bit). `lookups` (ctx_of int32 [N], tgt
     int16 [N], positions int32 or None): qcnt[i] = the count of (ctx_of[i], tgt[i]) for the listed positions (all
     without a list), 0 where absent, out of range or not listed. `packed`: pairs as packed words (falls back to keys +
-    counts when the escape table overflows)."""
+    counts when the escape table overflows). `seg` (regions, R, ev_count, dhist, nseg): the events straight from an
+    emitting scan's regions with its digit histograms (ng_scan_emit's dhist, digit-major with stride nseg); ev and
+    n_ev are then unused: the first partition pass reads the regions (ng_seg_scatter) and groups by the top 8 bits,
+    the later passes sort the bits below them."""
+    msd = 0
+    if seg is not None:
+        regions, R, ev_count, dhist, nseg = seg
+        dev = regions.device
+        dpre = torch.empty(max(256 * nseg, 1), dtype=torch.int32, device=dev)
+        total = torch.zeros(1, dtype=torch.int64, device=dev)
+        elib.cub("ng_exclusive_scan_u32", dhist, dpre, 256 * nseg, total)
+        n_ev = int(total.item())
+        if n_ev >= 1 << 32:
+            raise RuntimeError(f"{n_ev} events: the region scatter's offsets are 32-bit")
+        ev = torch.empty(max(n_ev, 1), dtype=torch.int64, device=dev)
+        e0, e1 = event("partition", n_ev)
+        e0.record()
+        elib("ng_seg_scatter", regions, u64(R), ev_count, dpre, nseg, ev)
+        e1.record()
+        del dpre
+        msd = 1
     dev = ev.device
     cb = max(1, (max(n_ids, 2) - 1).bit_length(), PACK_MIN_BITS) if packed else 0
     N = nq = 0
@@ -95,22 +116,45 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor, n_ev: int, n_ids: int, r
         e1.record()
     min_bits = min(PART_MIN_BITS, 24) if N else 0  # lookups want enough partitions (blocks) to spread over
     pbits = max(min_bits, min(24, math.ceil(math.log2(max(1.0, n_ev * ratio / PART_TARGET)))))
+
+    def sort_by_partition(k_in, v_in, n):
+        """Keys (and values) in the partition order of msd / pbits."""
+        k_out = torch.empty(max(n, 1), dtype=torch.int64, device=dev)
+        v_out = torch.empty(max(n, 1), dtype=torch.int32, device=dev) if v_in is not None else None
+        if not n:
+            return k_out, v_out
+        if not msd:
+            lib.cub("sort_pairs", k_in, k_out, v_in, v_out, n, i32(64 - pbits), i32(64))
+        elif pbits > 8:
+            lib.cub("sort_pairs", k_in, k_out, v_in, v_out, n, i32(64 - pbits), i32(56))
+        else:
+            k_out.copy_(k_in[:n])
+            if v_in is not None:
+                v_out.copy_(v_in[:n])
+        return k_out, v_out
+
     while True:
         P = 1 << pbits
-        sev = torch.empty(max(n_ev, 1), dtype=torch.int64, device=dev)
         start = torch.empty(P + 1, dtype=torch.int64, device=dev)
         qstart = torch.zeros(P + 1, dtype=torch.int64, device=dev)
         sqk = sqv = None
         e0, e1 = event("partition", n_ev)
         e0.record()
-        if n_ev:
-            lib.cub("sort_pairs", ev, sev, None, None, n_ev, i32(64 - pbits), i32(64))
-        elib("ng_part_bounds", sev, n_ev, i32(pbits), start)
+        if msd and pbits <= 8:
+            sev = ev  # the first pass's grouping by the top 8 bits is already by the top pbits
+        else:
+            sev, _ = sort_by_partition(ev, None, n_ev)
+        elib("ng_part_bounds", sev, n_ev, i32(pbits), i32(msd), start)
         if nq:
-            sqk = torch.empty(nq, dtype=torch.int64, device=dev)
-            sqv = torch.empty(nq, dtype=torch.int32, device=dev)
-            lib.cub("sort_pairs", qk, sqk, qv, sqv, nq, i32(64 - pbits), i32(64))
-            elib("ng_part_bounds", sqk, nq, i32(pbits), qstart)
+            if msd:  # the lookups take the events' two-step order: the top 8 bits, then (stably) the bits below
+                qk8 = torch.empty(nq, dtype=torch.int64, device=dev)
+                qv8 = torch.empty(nq, dtype=torch.int32, device=dev)
+                lib.cub("sort_pairs", qk, qk8, qv, qv8, nq, i32(56), i32(64))
+                sqk, sqv = sort_by_partition(qk8, qv8, nq) if pbits > 8 else (qk8, qv8)
+                del qk8, qv8
+            else:
+                sqk, sqv = sort_by_partition(qk, qv, nq)
+            elib("ng_part_bounds", sqk, nq, i32(pbits), i32(msd), qstart)
         e1.record()
         G2 = min(P, PART_BLOCKS)
         out_k = torch.empty(max(n_ev, 1), dtype=torch.int64, device=dev)
@@ -136,6 +180,7 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor, n_ev: int, n_ids: int, r
         if pbits >= 24:
             raise RuntimeError("a partition holds too many distinct pairs at 24 bits")
         pbits += 1
+    del ev
     offs = torch.empty(G2 + 1, dtype=torch.int64, device=dev)
     elib("ng_seg_offsets", seg_cnt, G2, offs)
     U = int(offs[G2].item())
@@ -145,7 +190,7 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor, n_ev: int, n_ids: int, r
     e0.record()
     elib("ng_seg_gather", out_k, out_c, u64(0), seg_base, seg_cnt, G2, offs, pairs, counts)
     e1.record()
-    return Counted(pairs, counts, (esc_k, esc_c) if cb else None, qcnt, U, pbits, cb)
+    return Counted(pairs, counts, (esc_k, esc_c) if cb else None, qcnt, U, pbits, cb, n_ev)
 
 
 RECORD_WORDS = {1: 4, 2: 8, 4: 8, 8: 16}  # u32 words of a context record for top 1, 2, 4, 8
