@@ -84,23 +84,25 @@ __global__ void part_bounds_k(const u64* __restrict__ ev, i64 n, int pbits, int 
     start[p] = a;
 }
 
-// The partition sort's first pass straight from the emitting scan's regions: segment s (ev_count[s] events at
-// src + s * R) scattered by its events' top 8 bits, digit d of segment s starting at out + dpre[d * nseg + s] (the
-// exclusive scan of the scan's digit histograms, digit-major). The order within a digit is free (the passes after
-// this one are stable and only need the groups): a chunk of 8192 events is ranked by LDS counters, staged in LDS by
-// digit and written as per-digit runs. Replaces packing the regions into one array and a radix pass over it.
+// A sort's first pass straight from segments (an emitting scan's regions, or the count's per-block outputs): segment
+// s (ev_count[s] keys at src + (bases ? bases[s] : s * R)) scattered by the digit (key >> shift) & 255, digit d of
+// segment s starting at out + dpre[d * nseg + s] (the exclusive scan of the producer's per-segment digit histograms,
+// digit-major). The order within a digit is free (the passes after this one are stable): a chunk of 8192 keys is
+// ranked by LDS counters, staged in LDS by digit and written as per-digit runs. Replaces packing the segments into
+// one array and a radix pass over it.
 #define SS_BLOCK 1024
 #define SS_ITEMS 8
 #define SS_CHUNK (SS_BLOCK * SS_ITEMS)
 __global__ void __launch_bounds__(SS_BLOCK) seg_scatter_k(const u64* __restrict__ src, u64 R,
+                                                         const i64* __restrict__ bases,
                                                          const u32* __restrict__ ev_count, const u32* __restrict__ dpre,
-                                                         i64 nseg, u64* __restrict__ out) {
+                                                         i64 nseg, int shift, u64* __restrict__ out) {
     __shared__ u64 stage[SS_CHUNK];
     __shared__ u32 cnt[256], pre[256], base[256], wt[4];
     const int t = threadIdx.x, lane = lane_id();
     for (i64 sg = blockIdx.x; sg < nseg; sg += gridDim.x) {
         const u32 n = ev_count[sg];
-        const u64* in = src + (u64)sg * R;
+        const u64* in = src + (bases ? (u64)bases[sg] : (u64)sg * R);
         if (t < 256) base[t] = dpre[(i64)t * nseg + sg];
         for (u32 c0 = 0; c0 < n; c0 += SS_CHUNK) {
             if (t < 256) cnt[t] = 0;
@@ -115,7 +117,7 @@ __global__ void __launch_bounds__(SS_BLOCK) seg_scatter_k(const u64* __restrict_
 #pragma unroll
             for (int j = 0; j < SS_ITEMS; ++j) {
                 const u32 i = c0 + (u32)(j * SS_BLOCK + t);
-                rank[j] = i < n ? atomicAdd(&cnt[key[j] >> 56], 1u) : 0u;
+                rank[j] = i < n ? atomicAdd(&cnt[(key[j] >> shift) & 255u], 1u) : 0u;
             }
             __syncthreads();
             u32 v = 0, incl = 0;
@@ -139,13 +141,13 @@ __global__ void __launch_bounds__(SS_BLOCK) seg_scatter_k(const u64* __restrict_
 #pragma unroll
             for (int j = 0; j < SS_ITEMS; ++j) {
                 const u32 i = c0 + (u32)(j * SS_BLOCK + t);
-                if (i < n) stage[pre[key[j] >> 56] + rank[j]] = key[j];
+                if (i < n) stage[pre[(key[j] >> shift) & 255u] + rank[j]] = key[j];
             }
             __syncthreads();
             const u32 m = n - c0 < (u32)SS_CHUNK ? n - c0 : (u32)SS_CHUNK;
             for (u32 i = t; i < m; i += SS_BLOCK) {
                 const u64 k = stage[i];
-                const u32 d = (u32)(k >> 56);
+                const u32 d = (u32)(k >> shift) & 255u;
                 out[(u64)base[d] + i - pre[d]] = k;
             }
             __syncthreads();
@@ -267,9 +269,11 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
                                                         u64* __restrict__ out_k, u32* __restrict__ out_c, int cb,
                                                         u64* esc_k, u32* esc_c, u64 esc_cap,
                                                         u32* __restrict__ seg_cnt, i64* __restrict__ seg_base,
-                                                        u32* __restrict__ qcnt, u32* flags) {
+                                                        u32* __restrict__ qcnt, u32* __restrict__ dhist, int dshift,
+                                                        u32* flags) {
     __shared__ __align__(16) u64 tk[PT_SLOTS];
     __shared__ u32 tc[PT_SLOTS];
+    __shared__ u32 dh[256];  // with dhist: the block's packed words per digit (word >> dshift) & 255
     __shared__ u32 cur;
     __shared__ u32 nocc;  // the partition's distinct pairs counted so far (updated once per wave and item)
     const int t = threadIdx.x, lane = lane_id();
@@ -280,6 +284,8 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
             seg_cnt[blockIdx.x] = 0;
             seg_base[blockIdx.x] = 0;
         }
+        if (dhist)
+            for (int d = t; d < 256; d += PT_BLOCK) dhist[(i64)d * G + blockIdx.x] = 0;
         return;
     }
     const i64 out_base = start[p0];
@@ -287,6 +293,8 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
         cur = 0;
         nocc = 0;
     }
+    if (dhist)
+        for (int d = t; d < 256; d += PT_BLOCK) dh[d] = 0;
     for (int j = t; j < PT_SLOTS; j += PT_BLOCK) {  // the output pass empties the slots for the next partition
         tk[j] = EMPTY;
         tc[j] = 0;
@@ -358,8 +366,10 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
                     out_c[at] = n;
                 } else {
                     const u64 esc = (1ull << (48 - cb)) - 1;
-                    out_k[at] = (pk << (48 - cb)) | ((u64)n < esc ? (u64)n : esc);
+                    const u64 word = (pk << (48 - cb)) | ((u64)n < esc ? (u64)n : esc);
+                    out_k[at] = word;
                     if ((u64)n >= esc) esc_put(esc_k, esc_c, esc_cap, pk, n, flags);
+                    if (dhist) atomicAdd(&dh[(word >> dshift) & 255u], 1u);
                 }
             }
         }
@@ -370,6 +380,8 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
         seg_cnt[blockIdx.x] = cur;
         seg_base[blockIdx.x] = out_base;
     }
+    if (dhist)  // the last partition's barrier has ordered every count
+        for (int d = t; d < 256; d += PT_BLOCK) dhist[(i64)d * G + blockIdx.x] = dh[d];
 }
 
 // Per context from packed words sorted by context (word >> (64 - cb)): a wave per window of 64 words, staged in LDS.
@@ -599,15 +611,16 @@ extern "C" int ng_exclusive_scan_u32(void* temp, size_t* temp_bytes, const u32* 
     return prim::exclusive_scan_u32(in, out, n, total, temp, (hipStream_t)stream);
 }
 
-// The partition sort's first pass from an emitting scan's regions (seg_scatter_k): nseg segments of ev_count[s]
-// events at src + s * R, scattered by their top 8 bits to out at the offsets dpre (u32 [256 * nseg], the exclusive
-// scan of ng_scan_emit's digit histograms, digit-major; the events number below 2^32).
-extern "C" int ng_seg_scatter(const u64* src, u64 R, const u32* ev_count, const u32* dpre, i64 nseg, u64* out,
-                              void* stream) {
-    if (nseg < 0 || R == 0 || R > 0xFFFFFFFFull) return -1;
+// A sort's first pass from segments (seg_scatter_k): nseg segments of ev_count[s] keys at src + (bases ? bases[s] :
+// s * R), scattered by the digit (key >> shift) & 255 to out at the offsets dpre (u32 [256 * nseg], the exclusive
+// scan of the producer's digit histograms, digit-major: ng_scan_emit's with shift 56, ng_part_count's; fewer than
+// 2^32 keys).
+extern "C" int ng_seg_scatter(const u64* src, u64 R, const i64* bases, const u32* ev_count, const u32* dpre, i64 nseg,
+                              int shift, u64* out, void* stream) {
+    if (nseg < 0 || shift < 0 || shift > 56 || (bases == nullptr && (R == 0 || R > 0xFFFFFFFFull))) return -1;
     if (nseg == 0) return 0;
     const i64 g = nseg < 16384 ? nseg : 16384;
-    seg_scatter_k<<<(unsigned)g, SS_BLOCK, 0, (hipStream_t)stream>>>(src, R, ev_count, dpre, nseg, out);
+    seg_scatter_k<<<(unsigned)g, SS_BLOCK, 0, (hipStream_t)stream>>>(src, R, bases, ev_count, dpre, nseg, shift, out);
     return (int)hipGetLastError();
 }
 
@@ -623,17 +636,22 @@ extern "C" int ng_part_lookups(const int* ctx_of, const u16* tgt, const int* pos
 // Count the sorted events partition by partition (start: ng_part_bounds' of 2^pbits partitions) with `grid` blocks
 // (at most 65536) of consecutive partitions holding about n / grid events each: block b's distinct pairs (pair key, count) at out_k/out_c + seg_base[b], seg_cnt[b] of
 // them (out_k/out_c hold as many items as ev). Lookups (qk sorted like ev, qv their query positions, qstart their
-// bounds) get qcnt[qv[j]] = the pair's count or 0. flags[0] bit 0: a partition reached 7000 distinct pairs
+// bounds) get qcnt[qv[j]] = the pair's count or 0. dhist (may be NULL; packed words only): block b's words per digit
+// (word >> dshift) & 255 at dhist[d * grid + b], for ng_seg_scatter. flags[0] bit 0: a partition reached 7000
+// distinct pairs
 // (its count is incomplete: repartition with one more bit).
 extern "C" int ng_part_count(const u64* ev, const i64* start, int pbits, const u64* qk, const u32* qv,
                              const i64* qstart, u64* out_k, u32* out_c, int cb, u64* esc_k, u32* esc_c, u64 esc_cap,
-                             u32* seg_cnt, i64* seg_base, u32* qcnt, u32* flags, int grid, void* stream) {
+                             u32* seg_cnt, i64* seg_base, u32* qcnt, u32* dhist, int dshift, u32* flags, int grid,
+                             void* stream) {
     if (pbits < 0 || pbits > 24 || grid <= 0 || grid > 65536 || cb < 0 || cb > 44) return -1;
     if (cb > 0 && (esc_k == nullptr || esc_c == nullptr || esc_cap == 0)) return -1;
     if (cb == 0 && out_c == nullptr) return -1;
+    if (dhist && (cb == 0 || dshift < 0 || dshift > 56)) return -1;
     const i64 P = 1ll << pbits;
     part_count_k<<<grid, PT_BLOCK, 0, (hipStream_t)stream>>>(ev, start, P, qk, qv, qstart, out_k, out_c, cb, esc_k,
-                                                             esc_c, esc_cap, seg_cnt, seg_base, qcnt, flags);
+                                                             esc_c, esc_cap, seg_cnt, seg_base, qcnt, dhist, dshift,
+                                                             flags);
     return (int)hipGetLastError();
 }
 

@@ -170,7 +170,7 @@ class CountTable:
             del ck
         self.reruns[k] = reruns
         ev_name = lambda name, n: self._timed(name, k)
-        c = P.count_events(lib, lib, ev, self.L, ccap, self.ratio.get(k, 1.0), None, True, ev_name)
+        c = P.count_events(lib, lib, ev, self.L, ccap, self.ratio.get(k, 1.0), None, True, ev_name, presort="pair")
         del ev
         self.ratio[k] = max(c.U, 1) / max(self.L, 1)
         if not c.cb:

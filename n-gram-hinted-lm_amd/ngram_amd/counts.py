@@ -422,7 +422,7 @@ class CountBuild:
             t1 = time.perf_counter()
             ev_fn = lambda name, n, k=k: self._event(name, k, -1, n)  # noqa: E731
             c = count_events(self.elib, self.lib, None, 0, vi.ids, self.dratio.get(k, 1.0), (vi.ctx_of, tgt, seen),
-                             event=ev_fn, seg=seg)
+                             event=ev_fn, seg=seg, presort="ctx")
             del seg
             n_ev = c.n_ev
             self.dratio[k] = c.U / max(1, n_ev)

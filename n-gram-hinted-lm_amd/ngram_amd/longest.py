@@ -134,7 +134,7 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
             seg = None
         if int(flags[0].item()) & 4:
             raise RuntimeError(f"k={k}: an emit region overflowed")
-        c = count_events(elib, lib, ev, n_ev, vi.ids, _RATIO.get(k, 1.0), seg=seg)
+        c = count_events(elib, lib, ev, n_ev, vi.ids, _RATIO.get(k, 1.0), seg=seg, presort="ctx")
         n_ev = c.n_ev
         del ev
         _RATIO[k] = c.U / max(1, n_ev)

@@ -72,10 +72,12 @@ class Counted:
     pbits: int
     cb: int
     n_ev: int = 0
+    presorted: int = -1  # packed words already grouped by the digit (word >> presorted) & 255 (-1: not)
 
 
 def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids: int, ratio: float = 1.0,
-                 lookups: tuple | None = None, packed: bool = True, event=_no_event, seg: tuple | None = None) -> Counted:
+                 lookups: tuple | None = None, packed: bool = True, event=_no_event, seg: tuple | None = None,
+                 presort: str | None = None) -> Counted:
     """Count n_ev events of context ids below n_ids. `ratio`: distinct pairs per event expected (sizes the
     partitions; a partition found too full repeats the count with one more bit). `lookups` (ctx_of int32 [N], tgt
     int16 [N], positions int32 or None): qcnt[i] = the count of (ctx_of[i], tgt[i]) for the listed positions (all
@@ -83,7 +85,8 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids:
     counts when the escape table overflows). `seg` (regions, R, ev_count, dhist, nseg): the events straight from an
     emitting scan's regions with its digit histograms (ng_scan_emit's dhist, digit-major with stride nseg); ev and
     n_ev are then unused: the first partition pass reads the regions (ng_seg_scatter) and groups by the top 8 bits,
-    the later passes sort the bits below them."""
+    the later passes sort the bits below them. `presort` ("ctx" / "pair", packed words only): the words come out
+    already through the first pass of summarize's sort (by context / by pair key), read from the count's outputs."""
     msd = 0
     if seg is not None:
         regions, R, ev_count, dhist, nseg = seg
@@ -97,7 +100,7 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids:
         ev = torch.empty(max(n_ev, 1), dtype=torch.int64, device=dev)
         e0, e1 = event("partition", n_ev)
         e0.record()
-        elib("ng_seg_scatter", regions, u64(R), ev_count, dpre, nseg, ev)
+        elib("ng_seg_scatter", regions, u64(R), None, ev_count, dpre, nseg, i32(56), ev)
         e1.record()
         del dpre
         msd = 1
@@ -165,10 +168,14 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids:
         seg_base = torch.empty(G2, dtype=torch.int64, device=dev)
         qcnt = torch.zeros(max(N, 1), dtype=torch.int32, device=dev) if N else None
         flags = torch.zeros(1, dtype=torch.int32, device=dev)
+        dshift = -1
+        if presort and cb:  # the lowest digit of the words' sort range
+            dshift = 64 - cb - (16 if presort == "pair" else 0)
+        dhist = torch.empty(256 * G2, dtype=torch.int32, device=dev) if dshift >= 0 else None
         e0, e1 = event("count", n_ev)
         e0.record()
         elib("ng_part_count", sev, start, i32(pbits), sqk, sqv, qstart, out_k, out_c, i32(cb), esc_k, esc_c,
-             u64(ESC_CAP if cb else 0), seg_cnt, seg_base, qcnt, flags, i32(G2))
+             u64(ESC_CAP if cb else 0), seg_cnt, seg_base, qcnt, dhist, i32(max(dshift, 0)), flags, i32(G2))
         e1.record()
         del sev, sqk, sqv, start, qstart
         fl = int(flags[0].item())
@@ -181,16 +188,28 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids:
             raise RuntimeError("a partition holds too many distinct pairs at 24 bits")
         pbits += 1
     del ev
-    offs = torch.empty(G2 + 1, dtype=torch.int64, device=dev)
-    elib("ng_seg_offsets", seg_cnt, G2, offs)
-    U = int(offs[G2].item())
-    pairs = torch.empty(max(U, 1), dtype=torch.int64, device=dev)
-    counts = None if cb else torch.empty(max(U, 1), dtype=torch.int32, device=dev)
-    e0, e1 = event("count", U)
-    e0.record()
-    elib("ng_seg_gather", out_k, out_c, u64(0), seg_base, seg_cnt, G2, offs, pairs, counts)
-    e1.record()
-    return Counted(pairs, counts, (esc_k, esc_c) if cb else None, qcnt, U, pbits, cb, n_ev)
+    counts = None
+    if dhist is not None:  # the words scattered by their lowest sort digit: summarize's first radix pass
+        dpre = torch.empty(256 * G2, dtype=torch.int32, device=dev)
+        total = torch.zeros(1, dtype=torch.int64, device=dev)
+        elib.cub("ng_exclusive_scan_u32", dhist, dpre, 256 * G2, total)
+        U = int(total.item())
+        pairs = torch.empty(max(U, 1), dtype=torch.int64, device=dev)
+        e0, e1 = event("sort", U)
+        e0.record()
+        elib("ng_seg_scatter", out_k, u64(0), seg_base, seg_cnt, dpre, G2, i32(dshift), pairs)
+        e1.record()
+    else:
+        offs = torch.empty(G2 + 1, dtype=torch.int64, device=dev)
+        elib("ng_seg_offsets", seg_cnt, G2, offs)
+        U = int(offs[G2].item())
+        pairs = torch.empty(max(U, 1), dtype=torch.int64, device=dev)
+        counts = None if cb else torch.empty(max(U, 1), dtype=torch.int32, device=dev)
+        e0, e1 = event("count", U)
+        e0.record()
+        elib("ng_seg_gather", out_k, out_c, u64(0), seg_base, seg_cnt, G2, offs, pairs, counts)
+        e1.record()
+    return Counted(pairs, counts, (esc_k, esc_c) if cb else None, qcnt, U, pbits, cb, n_ev, dshift)
 
 
 RECORD_WORDS = {1: 4, 2: 8, 4: 8, 8: 16}  # u32 words of a context record for top 1, 2, 4, 8
@@ -216,12 +235,16 @@ def summarize(elib: Lib, lib: Lib, c: Counted, n_ids: int, ktop: int, zero_recor
     zeros only with zero_records. With deep_min: the contexts of more than deep_min pairs. Raises if a total reaches
     2^32."""
     dev = c.pairs.device
-    sw = torch.empty(max(c.U, 1), dtype=torch.int64, device=dev)
-    e0, e1 = event("sort", c.U)
-    e0.record()
-    if c.U:
-        lib.cub("sort_pairs", c.pairs, sw, None, None, c.U, i32(64 - c.cb - (16 if by_pair else 0)), i32(64))
-    e1.record()
+    lo = 64 - c.cb - (16 if by_pair else 0)  # the sort's bit range [lo, 64)
+    if c.presorted == lo and lo + 8 >= 64:  # one digit: count_events' scatter sorted them
+        sw = c.pairs
+    else:
+        sw = torch.empty(max(c.U, 1), dtype=torch.int64, device=dev)
+        e0, e1 = event("sort", c.U)
+        e0.record()
+        if c.U:  # the first digit's pass already done by count_events' scatter when presorted
+            lib.cub("sort_pairs", c.pairs, sw, None, None, c.U, i32(lo + 8 if c.presorted == lo else lo), i32(64))
+        e1.record()
     rec = (torch.zeros if zero_records else torch.empty)((n_ids, RECORD_WORDS[ktop]), dtype=torch.int32, device=dev)
     dist = torch.zeros(n_ids, dtype=torch.int32, device=dev) if with_dist else None
     nstat = torch.zeros(257, dtype=torch.int32, device=dev)
