@@ -169,11 +169,11 @@ int ng_seg_gather(const ng_u64* src_k, const uint32_t* src_v, ng_u64 region, con
  * the top 8 bits first (ng_seg_scatter), then stably by the pbits - 8 bits below, partition (lo, hi) = lo << 8 | hi */
 int ng_part_bounds(const ng_u64* ev, ng_i64 n, int pbits, int msd, ng_i64* start, void* stream);
 /* a sort's first pass from segments: nseg segments of ev_count[s] keys at src + (bases ? bases[s] : s * R) scattered
- * by the digit (key >> shift) & 255 to out at dpre (u32 [256 * nseg], the exclusive scan of the producer's digit
- * histograms, digit-major: ng_scan_emit's with shift 56, ng_part_count's; fewer than 2^32 keys); the order within a
- * digit is free */
+ * by the nbits-bit digit (key >> shift) & (2^nbits - 1), nbits <= 11, to out at dpre (u32 [2^nbits * nseg], the
+ * exclusive scan of the producer's digit histograms, digit-major: ng_scan_emit's with shift 56 and 8 bits,
+ * ng_part_count's; fewer than 2^32 keys); the order within a digit is free */
 int ng_seg_scatter(const ng_u64* src, ng_u64 R, const ng_i64* bases, const uint32_t* ev_count, const uint32_t* dpre,
-                   ng_i64 nseg, int shift, ng_u64* out, void* stream);
+                   ng_i64 nseg, int shift, int nbits, ng_u64* out, void* stream);
 /* exclusive prefix sum of n u32 (out may alias in), *total (may be NULL) the sum; CUB-style two-phase temp storage */
 int ng_exclusive_scan_u32(void* temp, size_t* temp_bytes, const uint32_t* in, uint32_t* out, ng_i64 n,
                           ng_u64* total, void* stream);
@@ -183,12 +183,12 @@ int ng_part_lookups(const int* ctx_of, const uint16_t* tgt, const int* pos, ng_i
                     ng_u64* qk, uint32_t* qv, void* stream);
 /* per partition an LDS hash count of its events; block b's distinct (pair key, count) at out + seg_base[b], seg_cnt[b]
  * of them; qcnt[qv[j]] = the count of lookup j (qk sorted like ev, bounds qstart); dhist (may be NULL, packed words
- * only): block b's words per digit (word >> dshift) & 255 at dhist[d * grid + b]; flags[0] bit 0: a partition reached
- * 7000 distinct pairs (repartition with one more bit) */
+ * only): block b's words per dbits-bit digit (word >> dshift) & (2^dbits - 1), dbits <= 11, at dhist[d * grid + b];
+ * flags[0] bit 0: a partition reached 7000 distinct pairs (repartition with one more bit) */
 int ng_part_count(const ng_u64* ev, const ng_i64* start, int pbits, const ng_u64* qk, const uint32_t* qv,
                   const ng_i64* qstart, ng_u64* out_k, uint32_t* out_c, int cb, ng_u64* esc_k, uint32_t* esc_c,
                   ng_u64 esc_cap, uint32_t* seg_cnt, ng_i64* seg_base, uint32_t* qcnt, uint32_t* dhist, int dshift,
-                  uint32_t* flags, int grid, void* stream);
+                  int dbits, uint32_t* flags, int grid, void* stream);
 /* with cb > 0 (ids below 2^cb, cb <= 44) ng_part_count writes packed words pair key << (48 - cb) | min(count, esc),
  * esc = 2^(48 - cb) - 1, larger counts also into the escape table esc_k/esc_c (EMPTY-filled; full: flags[0] bit 1).
  * From such words sorted by context: dist[c] (pairs) and the record rec[c] of each present context (callers zero

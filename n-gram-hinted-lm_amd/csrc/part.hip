@@ -85,7 +85,7 @@ __global__ void part_bounds_k(const u64* __restrict__ ev, i64 n, int pbits, int 
 }
 
 // A sort's first pass straight from segments (an emitting scan's regions, or the count's per-block outputs): segment
-// s (ev_count[s] keys at src + (bases ? bases[s] : s * R)) scattered by the digit (key >> shift) & 255, digit d of
+// s (ev_count[s] keys at src + (bases ? bases[s] : s * R)) scattered by the nbits-bit digit at `shift`, digit d of
 // segment s starting at out + dpre[d * nseg + s] (the exclusive scan of the producer's per-segment digit histograms,
 // digit-major). The order within a digit is free (the passes after this one are stable): a chunk of 8192 keys is
 // ranked by LDS counters, staged in LDS by digit and written as per-digit runs. Replaces packing the segments into
@@ -93,19 +93,21 @@ __global__ void part_bounds_k(const u64* __restrict__ ev, i64 n, int pbits, int 
 #define SS_BLOCK 1024
 #define SS_ITEMS 8
 #define SS_CHUNK (SS_BLOCK * SS_ITEMS)
+#define SS_MAXB 2048  // digits of up to 11 bits
 __global__ void __launch_bounds__(SS_BLOCK) seg_scatter_k(const u64* __restrict__ src, u64 R,
                                                          const i64* __restrict__ bases,
                                                          const u32* __restrict__ ev_count, const u32* __restrict__ dpre,
-                                                         i64 nseg, int shift, u64* __restrict__ out) {
+                                                         i64 nseg, int shift, int nbits, u64* __restrict__ out) {
     __shared__ u64 stage[SS_CHUNK];
-    __shared__ u32 cnt[256], pre[256], base[256], wt[4];
-    const int t = threadIdx.x, lane = lane_id();
+    __shared__ u32 cnt[SS_MAXB], pre[SS_MAXB], base[SS_MAXB], wt[SS_BLOCK / WAVE];
+    const int t = threadIdx.x, lane = lane_id(), wid = t / WAVE;
+    const u32 B = 1u << nbits, mask = B - 1u;
     for (i64 sg = blockIdx.x; sg < nseg; sg += gridDim.x) {
         const u32 n = ev_count[sg];
         const u64* in = src + (bases ? (u64)bases[sg] : (u64)sg * R);
-        if (t < 256) base[t] = dpre[(i64)t * nseg + sg];
+        for (u32 d = t; d < B; d += SS_BLOCK) base[d] = dpre[(i64)d * nseg + sg];
         for (u32 c0 = 0; c0 < n; c0 += SS_CHUNK) {
-            if (t < 256) cnt[t] = 0;
+            for (u32 d = t; d < B; d += SS_BLOCK) cnt[d] = 0;
             __syncthreads();
             u64 key[SS_ITEMS];
             u32 rank[SS_ITEMS];
@@ -117,41 +119,40 @@ __global__ void __launch_bounds__(SS_BLOCK) seg_scatter_k(const u64* __restrict_
 #pragma unroll
             for (int j = 0; j < SS_ITEMS; ++j) {
                 const u32 i = c0 + (u32)(j * SS_BLOCK + t);
-                rank[j] = i < n ? atomicAdd(&cnt[(key[j] >> shift) & 255u], 1u) : 0u;
+                rank[j] = i < n ? atomicAdd(&cnt[(u32)(key[j] >> shift) & mask], 1u) : 0u;
             }
             __syncthreads();
-            u32 v = 0, incl = 0;
-            if (t < 256) {  // the first four waves: an exclusive scan of the 256 digit counts
-                v = cnt[t];
-                incl = v;
+            // exclusive scan of the B digit counts: thread t holds digits 2t and 2t + 1
+            const u32 d0 = 2u * (u32)t;
+            const u32 a0 = d0 < B ? cnt[d0] : 0u, a1 = d0 + 1 < B ? cnt[d0 + 1] : 0u;
+            u32 incl = a0 + a1;
 #pragma unroll
-                for (int d = 1; d < WAVE; d <<= 1) {
-                    const u32 o = (u32)__shfl_up((int)incl, d, WAVE);
-                    if (lane >= d) incl += o;
-                }
-                if (lane == WAVE - 1) wt[t / WAVE] = incl;
+            for (int d = 1; d < WAVE; d <<= 1) {
+                const u32 o = (u32)__shfl_up((int)incl, d, WAVE);
+                if (lane >= d) incl += o;
             }
+            if (lane == WAVE - 1) wt[wid] = incl;
             __syncthreads();
-            if (t < 256) {
-                u32 before = 0;
-                for (int w = 0; w < t / WAVE; ++w) before += wt[w];
-                pre[t] = before + incl - v;
-            }
+            u32 before = 0;
+            for (int w = 0; w < wid; ++w) before += wt[w];
+            const u32 ex = before + incl - (a0 + a1);
+            if (d0 < B) pre[d0] = ex;
+            if (d0 + 1 < B) pre[d0 + 1] = ex + a0;
             __syncthreads();
 #pragma unroll
             for (int j = 0; j < SS_ITEMS; ++j) {
                 const u32 i = c0 + (u32)(j * SS_BLOCK + t);
-                if (i < n) stage[pre[(key[j] >> shift) & 255u] + rank[j]] = key[j];
+                if (i < n) stage[pre[(u32)(key[j] >> shift) & mask] + rank[j]] = key[j];
             }
             __syncthreads();
             const u32 m = n - c0 < (u32)SS_CHUNK ? n - c0 : (u32)SS_CHUNK;
             for (u32 i = t; i < m; i += SS_BLOCK) {
                 const u64 k = stage[i];
-                const u32 d = (u32)(k >> shift) & 255u;
+                const u32 d = (u32)(k >> shift) & mask;
                 out[(u64)base[d] + i - pre[d]] = k;
             }
             __syncthreads();
-            if (t < 256) base[t] += cnt[t];
+            for (u32 d = t; d < B; d += SS_BLOCK) base[d] += cnt[d];
         }
         __syncthreads();  // base is read before the next segment overwrites it
     }
@@ -270,10 +271,10 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
                                                         u64* esc_k, u32* esc_c, u64 esc_cap,
                                                         u32* __restrict__ seg_cnt, i64* __restrict__ seg_base,
                                                         u32* __restrict__ qcnt, u32* __restrict__ dhist, int dshift,
-                                                        u32* flags) {
+                                                        int dbits, u32* flags) {
     __shared__ __align__(16) u64 tk[PT_SLOTS];
     __shared__ u32 tc[PT_SLOTS];
-    __shared__ u32 dh[256];  // with dhist: the block's packed words per digit (word >> dshift) & 255
+    __shared__ u32 dh[SS_MAXB];  // with dhist: the block's packed words per dbits-bit digit at dshift
     __shared__ u32 cur;
     __shared__ u32 nocc;  // the partition's distinct pairs counted so far (updated once per wave and item)
     const int t = threadIdx.x, lane = lane_id();
@@ -285,7 +286,7 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
             seg_base[blockIdx.x] = 0;
         }
         if (dhist)
-            for (int d = t; d < 256; d += PT_BLOCK) dhist[(i64)d * G + blockIdx.x] = 0;
+            for (int d = t; d < (1 << dbits); d += PT_BLOCK) dhist[(i64)d * G + blockIdx.x] = 0;
         return;
     }
     const i64 out_base = start[p0];
@@ -294,7 +295,7 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
         nocc = 0;
     }
     if (dhist)
-        for (int d = t; d < 256; d += PT_BLOCK) dh[d] = 0;
+        for (int d = t; d < (1 << dbits); d += PT_BLOCK) dh[d] = 0;
     for (int j = t; j < PT_SLOTS; j += PT_BLOCK) {  // the output pass empties the slots for the next partition
         tk[j] = EMPTY;
         tc[j] = 0;
@@ -369,7 +370,7 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
                     const u64 word = (pk << (48 - cb)) | ((u64)n < esc ? (u64)n : esc);
                     out_k[at] = word;
                     if ((u64)n >= esc) esc_put(esc_k, esc_c, esc_cap, pk, n, flags);
-                    if (dhist) atomicAdd(&dh[(word >> dshift) & 255u], 1u);
+                    if (dhist) atomicAdd(&dh[(u32)(word >> dshift) & ((1u << dbits) - 1u)], 1u);
                 }
             }
         }
@@ -381,7 +382,7 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
         seg_base[blockIdx.x] = out_base;
     }
     if (dhist)  // the last partition's barrier has ordered every count
-        for (int d = t; d < 256; d += PT_BLOCK) dhist[(i64)d * G + blockIdx.x] = dh[d];
+        for (int d = t; d < (1 << dbits); d += PT_BLOCK) dhist[(i64)d * G + blockIdx.x] = dh[d];
 }
 
 // Per context from packed words sorted by context (word >> (64 - cb)): a wave per window of 64 words, staged in LDS.
@@ -612,15 +613,18 @@ extern "C" int ng_exclusive_scan_u32(void* temp, size_t* temp_bytes, const u32* 
 }
 
 // A sort's first pass from segments (seg_scatter_k): nseg segments of ev_count[s] keys at src + (bases ? bases[s] :
-// s * R), scattered by the digit (key >> shift) & 255 to out at the offsets dpre (u32 [256 * nseg], the exclusive
-// scan of the producer's digit histograms, digit-major: ng_scan_emit's with shift 56, ng_part_count's; fewer than
-// 2^32 keys).
+// s * R), scattered by the nbits-bit digit (key >> shift) & (2^nbits - 1) (nbits <= 11) to out at the offsets dpre
+// (u32 [2^nbits * nseg], the exclusive scan of the producer's digit histograms, digit-major: ng_scan_emit's with
+// shift 56 and 8 bits, ng_part_count's; fewer than 2^32 keys).
 extern "C" int ng_seg_scatter(const u64* src, u64 R, const i64* bases, const u32* ev_count, const u32* dpre, i64 nseg,
-                              int shift, u64* out, void* stream) {
-    if (nseg < 0 || shift < 0 || shift > 56 || (bases == nullptr && (R == 0 || R > 0xFFFFFFFFull))) return -1;
+                              int shift, int nbits, u64* out, void* stream) {
+    if (nseg < 0 || nbits < 1 || nbits > 11 || shift < 0 || shift + nbits > 64 ||
+        (bases == nullptr && (R == 0 || R > 0xFFFFFFFFull)))
+        return -1;
     if (nseg == 0) return 0;
     const i64 g = nseg < 16384 ? nseg : 16384;
-    seg_scatter_k<<<(unsigned)g, SS_BLOCK, 0, (hipStream_t)stream>>>(src, R, bases, ev_count, dpre, nseg, shift, out);
+    seg_scatter_k<<<(unsigned)g, SS_BLOCK, 0, (hipStream_t)stream>>>(src, R, bases, ev_count, dpre, nseg, shift, nbits,
+                                                                     out);
     return (int)hipGetLastError();
 }
 
@@ -636,22 +640,22 @@ extern "C" int ng_part_lookups(const int* ctx_of, const u16* tgt, const int* pos
 // Count the sorted events partition by partition (start: ng_part_bounds' of 2^pbits partitions) with `grid` blocks
 // (at most 65536) of consecutive partitions holding about n / grid events each: block b's distinct pairs (pair key, count) at out_k/out_c + seg_base[b], seg_cnt[b] of
 // them (out_k/out_c hold as many items as ev). Lookups (qk sorted like ev, qv their query positions, qstart their
-// bounds) get qcnt[qv[j]] = the pair's count or 0. dhist (may be NULL; packed words only): block b's words per digit
-// (word >> dshift) & 255 at dhist[d * grid + b], for ng_seg_scatter. flags[0] bit 0: a partition reached 7000
+// bounds) get qcnt[qv[j]] = the pair's count or 0. dhist (may be NULL; packed words only): block b's words per
+// dbits-bit digit (word >> dshift) & (2^dbits - 1) (dbits <= 11) at dhist[d * grid + b], for ng_seg_scatter. flags[0] bit 0: a partition reached 7000
 // distinct pairs
 // (its count is incomplete: repartition with one more bit).
 extern "C" int ng_part_count(const u64* ev, const i64* start, int pbits, const u64* qk, const u32* qv,
                              const i64* qstart, u64* out_k, u32* out_c, int cb, u64* esc_k, u32* esc_c, u64 esc_cap,
-                             u32* seg_cnt, i64* seg_base, u32* qcnt, u32* dhist, int dshift, u32* flags, int grid,
-                             void* stream) {
+                             u32* seg_cnt, i64* seg_base, u32* qcnt, u32* dhist, int dshift, int dbits, u32* flags,
+                             int grid, void* stream) {
     if (pbits < 0 || pbits > 24 || grid <= 0 || grid > 65536 || cb < 0 || cb > 44) return -1;
     if (cb > 0 && (esc_k == nullptr || esc_c == nullptr || esc_cap == 0)) return -1;
     if (cb == 0 && out_c == nullptr) return -1;
-    if (dhist && (cb == 0 || dshift < 0 || dshift > 56)) return -1;
+    if (dhist && (cb == 0 || dbits < 1 || dbits > 11 || dshift < 0 || dshift + dbits > 64)) return -1;
     const i64 P = 1ll << pbits;
     part_count_k<<<grid, PT_BLOCK, 0, (hipStream_t)stream>>>(ev, start, P, qk, qv, qstart, out_k, out_c, cb, esc_k,
                                                              esc_c, esc_cap, seg_cnt, seg_base, qcnt, dhist, dshift,
-                                                             flags);
+                                                             dbits, flags);
     return (int)hipGetLastError();
 }
 

@@ -72,7 +72,13 @@ class Counted:
     pbits: int
     cb: int
     n_ev: int = 0
-    presorted: int = -1  # packed words already grouped by the digit (word >> presorted) & 255 (-1: not)
+    presorted: int = -1  # packed words already grouped by their presort_bits-bit digit at bit presorted (-1: not)
+    presort_bits: int = 0
+
+
+def presort_bits(total: int) -> int:
+    """The width (8 to 11) of a sort's first digit over `total` bits that leaves the fewest 8-bit passes after it."""
+    return min(range(8, 12), key=lambda w: (-(-max(total - w, 0) // 8), w))
 
 
 def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids: int, ratio: float = 1.0,
@@ -100,7 +106,7 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids:
         ev = torch.empty(max(n_ev, 1), dtype=torch.int64, device=dev)
         e0, e1 = event("partition", n_ev)
         e0.record()
-        elib("ng_seg_scatter", regions, u64(R), None, ev_count, dpre, nseg, i32(56), ev)
+        elib("ng_seg_scatter", regions, u64(R), None, ev_count, dpre, nseg, i32(56), i32(8), ev)
         e1.record()
         del dpre
         msd = 1
@@ -168,14 +174,16 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids:
         seg_base = torch.empty(G2, dtype=torch.int64, device=dev)
         qcnt = torch.zeros(max(N, 1), dtype=torch.int32, device=dev) if N else None
         flags = torch.zeros(1, dtype=torch.int32, device=dev)
-        dshift = -1
-        if presort and cb:  # the lowest digit of the words' sort range
+        dshift = dbits = -1
+        if presort and cb:  # the lowest digit of the words' sort range, as wide as saves summarize a radix pass
             dshift = 64 - cb - (16 if presort == "pair" else 0)
-        dhist = torch.empty(256 * G2, dtype=torch.int32, device=dev) if dshift >= 0 else None
+            dbits = min(presort_bits(64 - dshift), 64 - dshift)
+        dhist = torch.empty((1 << max(dbits, 0)) * G2, dtype=torch.int32, device=dev) if dshift >= 0 else None
         e0, e1 = event("count", n_ev)
         e0.record()
         elib("ng_part_count", sev, start, i32(pbits), sqk, sqv, qstart, out_k, out_c, i32(cb), esc_k, esc_c,
-             u64(ESC_CAP if cb else 0), seg_cnt, seg_base, qcnt, dhist, i32(max(dshift, 0)), flags, i32(G2))
+             u64(ESC_CAP if cb else 0), seg_cnt, seg_base, qcnt, dhist, i32(max(dshift, 0)), i32(max(dbits, 1)),
+             flags, i32(G2))
         e1.record()
         del sev, sqk, sqv, start, qstart
         fl = int(flags[0].item())
@@ -190,14 +198,15 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids:
     del ev
     counts = None
     if dhist is not None:  # the words scattered by their lowest sort digit: summarize's first radix pass
-        dpre = torch.empty(256 * G2, dtype=torch.int32, device=dev)
+        nb = (1 << dbits) * G2
+        dpre = torch.empty(nb, dtype=torch.int32, device=dev)
         total = torch.zeros(1, dtype=torch.int64, device=dev)
-        elib.cub("ng_exclusive_scan_u32", dhist, dpre, 256 * G2, total)
+        elib.cub("ng_exclusive_scan_u32", dhist, dpre, nb, total)
         U = int(total.item())
         pairs = torch.empty(max(U, 1), dtype=torch.int64, device=dev)
         e0, e1 = event("sort", U)
         e0.record()
-        elib("ng_seg_scatter", out_k, u64(0), seg_base, seg_cnt, dpre, G2, i32(dshift), pairs)
+        elib("ng_seg_scatter", out_k, u64(0), seg_base, seg_cnt, dpre, G2, i32(dshift), i32(dbits), pairs)
         e1.record()
     else:
         offs = torch.empty(G2 + 1, dtype=torch.int64, device=dev)
@@ -209,7 +218,8 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids:
         e0.record()
         elib("ng_seg_gather", out_k, out_c, u64(0), seg_base, seg_cnt, G2, offs, pairs, counts)
         e1.record()
-    return Counted(pairs, counts, (esc_k, esc_c) if cb else None, qcnt, U, pbits, cb, n_ev, dshift)
+    return Counted(pairs, counts, (esc_k, esc_c) if cb else None, qcnt, U, pbits, cb, n_ev, dshift,
+                   dbits if dhist is not None else 0)
 
 
 RECORD_WORDS = {1: 4, 2: 8, 4: 8, 8: 16}  # u32 words of a context record for top 1, 2, 4, 8
@@ -236,14 +246,15 @@ def summarize(elib: Lib, lib: Lib, c: Counted, n_ids: int, ktop: int, zero_recor
     2^32."""
     dev = c.pairs.device
     lo = 64 - c.cb - (16 if by_pair else 0)  # the sort's bit range [lo, 64)
-    if c.presorted == lo and lo + 8 >= 64:  # one digit: count_events' scatter sorted them
+    first = lo + c.presort_bits if c.presorted == lo else lo  # count_events' scatter did the bits below `first`
+    if first >= 64:
         sw = c.pairs
     else:
         sw = torch.empty(max(c.U, 1), dtype=torch.int64, device=dev)
         e0, e1 = event("sort", c.U)
         e0.record()
-        if c.U:  # the first digit's pass already done by count_events' scatter when presorted
-            lib.cub("sort_pairs", c.pairs, sw, None, None, c.U, i32(lo + 8 if c.presorted == lo else lo), i32(64))
+        if c.U:
+            lib.cub("sort_pairs", c.pairs, sw, None, None, c.U, i32(first), i32(64))
         e1.record()
     rec = (torch.zeros if zero_records else torch.empty)((n_ids, RECORD_WORDS[ktop]), dtype=torch.int32, device=dev)
     dist = torch.zeros(n_ids, dtype=torch.int32, device=dev) if with_dist else None

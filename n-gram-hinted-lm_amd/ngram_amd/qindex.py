@@ -14,6 +14,7 @@ from .lib import Lib, i32, u64
 
 TAIL = 4096  # slots past cap that linear probing may run into; the last stays empty
 LOAD = 0.4  # contexts per slot aimed at: measured at c3, 0.4 gives the fastest scans (0.5 +10%, 0.66 +50%)
+SHRINK = 2.0  # a table more than this many times the size its contexts need moves to one of that size
 
 
 class QueryIndex:
@@ -45,7 +46,7 @@ class QueryIndex:
         if c[2]:
             raise RuntimeError(f"k={k}: {c[2]} query positions collide with another context's key")
         n_ctx = int(c[0])
-        if m and cap > 2 * (n_ctx / LOAD) + 4096:
+        if m and cap > SHRINK * (n_ctx / LOAD) + 4096:
             # sized for every position, used by far fewer contexts: move them to a table sized for them (fewer bits
             # per context id, probes that stay in cache more often)
             small = int(n_ctx / LOAD) + 1024
