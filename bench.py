@@ -49,8 +49,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--query-tokens", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other configurations' measurements")
-    ap.add_argument("--only", default="", choices=("", "c2", "c4", "c5"),
-                    help="measure only this secondary configuration and print its JSON (for profiling)")
+    ap.add_argument("--only", default="", choices=("", "c2", "c4", "c5", "copy"),
+                    help="measure only this secondary configuration and print its JSON (for profiling); copy: three "
+                         "plain 1 GiB device copies, the calibration of rocprofv3's FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--mode", default="part", choices=("engine", "part", "record", "partitioned"),
                     help="CountBuild.mode")
     ap.add_argument("--cpu-tokens", type=int, default=100_000_000, help="CPU baseline: corpus prefix")
@@ -291,6 +292,14 @@ def main() -> None:
     from ngram_amd.counts import CountBuild, device_queries
 
     torch.cuda.set_device(0)
+    if args.only == "copy":
+        a = torch.ones(1 << 27, dtype=torch.int64, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"config": "copy", "bytes_read": a.numel() * 8, "bytes_written": b.numel() * 8, "copies": 3}))
+        return
     if args.only in ("c2", "c4"):
         r = bench_c2(args.steps, args.warmup, not args.no_cpu) if args.only == "c2" else bench_c4(not args.no_cpu)
         r.pop("sizes", None)
