@@ -301,6 +301,18 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
         tc[j] = 0;
     }
     __syncthreads();
+    // the events stream through in rounds of PT_ITEMS * PT_BLOCK; each round's loads are issued before the previous
+    // round (or the previous partition's output) is worked through, so their latency is hidden
+    constexpr i64 ROUND = (i64)PT_BLOCK * PT_ITEMS;
+    auto load_round = [&](u64 (&dst)[PT_ITEMS], i64 i0, i64 end) {
+#pragma unroll
+        for (int r = 0; r < PT_ITEMS; ++r) {
+            const i64 i = i0 + (i64)r * PT_BLOCK + t;
+            dst[r] = i < end ? ev[i] : EMPTY;
+        }
+    };
+    u64 ahead[PT_ITEMS];
+    i64 ahead_of = -1;  // the partition whose first round `ahead` holds (block-uniform)
     for (i64 p = p0; p < p1; ++p) {
         const i64 a = start[p], b = start[p + 1], qa = qstart[p], qb = qstart[p + 1];
         // the partition's first lookups are loaded now, so that their latency overlaps the inserts
@@ -311,12 +323,17 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
             lk = qk[qa + t];
             lv = qv[qa + t];
         }
-        for (i64 i0 = a; i0 < b; i0 += (i64)PT_BLOCK * PT_ITEMS) {  // the same rounds for every wave
+        if (ahead_of != p && a < b) load_round(ahead, a, b);
+        for (i64 i0 = a; i0 < b; i0 += ROUND) {  // the same rounds for every wave
             u64 key[PT_ITEMS];
 #pragma unroll
-            for (int r = 0; r < PT_ITEMS; ++r) {
-                const i64 i = i0 + (i64)r * PT_BLOCK + t;
-                key[r] = i < b ? ev[i] : EMPTY;
+            for (int r = 0; r < PT_ITEMS; ++r) key[r] = ahead[r];
+            if (i0 + ROUND < b) {
+                load_round(ahead, i0 + ROUND, b);
+                ahead_of = p;
+            } else if (p + 1 < p1) {
+                load_round(ahead, b, start[p + 2]);  // the next partition's first round
+                ahead_of = p + 1;
             }
 #pragma unroll
             for (int r = 0; r < PT_ITEMS; ++r) {
