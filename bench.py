@@ -1,5 +1,5 @@
-"""Benchmark of the n-gram hint path on one MI355X: the one-GPU share of the record's GPU counts build at BASELINE's
-third configuration (c3): a 1B-token seeded synthetic corpus (10 shards of 100M tokens, Zipf(1.1) over permuted ids,
+"""Benchmark of the n-gram hint path on one MI355X: the one-GPU share of the record's GPU counts build at
+configuration c3: a 1B-token seeded synthetic corpus (10 shards of 100M tokens, Zipf(1.1) over permuted ids,
 geometric documents of mean 1024 ending with BOS 50256, 5% of documents with a copied span of 32-1024 tokens), exact
 counts of the query contexts for n = 2..8, then for 16M query positions each level's tot / dist / cnt, the top-4 next
 tokens with counts, and hit/miss. One step = one whole count build + query over the resident corpus and queries.
@@ -91,7 +91,7 @@ def make_workload(cfg_name: str, train_tokens: int, query_tokens: int):
 
 
 def bench_c2(steps: int, warmup: int, with_cpu: bool) -> dict:
-    """BASELINE's second configuration: a corpus-wide CountTable over a 100M-token corpus for n = 2..4, then the
+    """Configuration c2: a corpus-wide CountTable over a 100M-token corpus for n = 2..4, then the
     top-4 continuations (with counts), tot / dist / cnt of 8M query positions; one step = build + query."""
     import numpy as np
     import torch
@@ -149,7 +149,7 @@ def bench_c2(steps: int, warmup: int, with_cpu: bool) -> dict:
 
 
 def bench_c5(tok, flat, steps: int, warmup: int, with_cpu: bool) -> dict:
-    """BASELINE's fifth configuration over the c3 corpus already in `tok` (`flat`: its tokens without gaps): a
+    """Configuration c5 over the c3 corpus already in `tok` (`flat`: its tokens without gaps): a
     held-out 64M-token stream (15% of documents with a copied span of 16-2048 corpus tokens), queried at every
     fourth position (16M positions): the longest exact suffix match (cap 64), its top next token and count."""
     import numpy as np
@@ -203,7 +203,7 @@ def bench_c5(tok, flat, steps: int, warmup: int, with_cpu: bool) -> dict:
 
 
 def bench_c4(with_cpu: bool) -> dict:
-    """BASELINE's fourth configuration: 92 steps of 2^19 fresh tokens (copied-span rate ramping 0 -> 20%); each step
+    """Configuration c4: 92 steps of 2^19 fresh tokens (copied-span rate ramping 0 -> 20%); each step
     answers its 2^19 queries (hint rows at n = 2..6: the deepest level with a count, 8 next tokens and weights, and
     count rows tot / dist / cnt per level) from the occurrences of earlier steps, its own occurrences becoming
     available to the next step (OnlineRows.advance, the step rule). Per-step latency over all 92 steps."""

@@ -1,7 +1,7 @@
 """Corpus-wide exact count tables on one MI355X behind exact_match's CountTable surface (exact_match/exact_match.pyi
 :100-118; exact_match/src/count_table.rs :173-438): `create` (read the shards, before the clock), `build` (on the
 clock: every level), `query_counts`, `query_rows`, `sizes`, `release`, `levels`, `tokens`; plus `query_topk` (each
-level's top-k next tokens per position, BASELINE's second configuration) and `query_device` (the same on GPU
+level's top-k next tokens per position, configuration c2) and `query_device` (the same on GPU
 tensors, for callers that keep their queries in device memory).
 
 Definitions (count_table.rs:6-9, kgram.rs's): an occurrence of a k-context is any k consecutive tokens within one

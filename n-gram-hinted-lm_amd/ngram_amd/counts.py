@@ -8,7 +8,7 @@ positions whose context matched at the previous level: a hit bitmap per level); 
 compacted, sorted by (context, next token), and per query position tot (uint32 bits), dist (at most 65535) and cnt
 (the target's count), plus the record's validation rows from ROW_LEVELS (cells, and the 8 most frequent next tokens with
 their 15-bit weights). Beyond the record: `levels`, `level_shards` and `topk` are parameters (the one-GPU share of
-the record at BASELINE's third configuration counts k = 2..8 over every shard and returns each level's top 4 next
+the record at configuration c3 counts k = 2..8 over every shard and returns each level's top 4 next
 tokens per position), and a level whose pair table overflows reruns with twice the slots (the record raises).
 
 One GPU: `world` must be 1 (the owner exchange is then the identity, as the reference's world == 1 path); the

@@ -250,7 +250,7 @@ def realize_gpu(plan: Plan, zipf: Zipf, lib, source=None, out=None):
 
 
 # ---------------------------------------------------------------------------------------------------------------
-# The configurations (BASELINE.json "configs")
+# The benchmark configurations c1-c5
 # ---------------------------------------------------------------------------------------------------------------
 
 @dataclass(frozen=True)
@@ -338,7 +338,7 @@ C4_STEP_TOKENS = 1 << 19
 
 
 def c4_stream(steps: int = C4_STEPS, step_tokens: int = C4_STEP_TOKENS, copy_rate_end: float = 0.20):
-    """BASELINE's fourth configuration: a stream of `steps` x `step_tokens` tokens (same generator: Zipf(1.1)
+    """Configuration c4: a stream of `steps` x `step_tokens` tokens (same generator: Zipf(1.1)
     documents ending with BOS), the share of documents with a copied span (32-256 tokens of an earlier document)
     ramping linearly from 0 at the stream's start to `copy_rate_end` at its end. Returns (zipf, plan, spans), spans
     (s * step_tokens, (s + 1) * step_tokens, s): step s trains its inputs and, as its last target, the next step's

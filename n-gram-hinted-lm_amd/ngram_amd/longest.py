@@ -1,5 +1,5 @@
-"""Longest exact suffix match of query positions against a training corpus on one MI355X (BASELINE's fifth
-configuration; the match-length notion of exact_match/src/kgram.rs kgram_stats :38-56, 237-278, taken up to k = 64 by
+"""Longest exact suffix match of query positions against a training corpus on one MI355X (configuration c5; the
+match-length notion of exact_match/src/kgram.rs kgram_stats :38-56, 237-278, taken up to k = 64 by
 src/retrieval_blog_post/kgram.py :16, 84-108): per query position i the largest k <= cap whose k-context
 x[i-k+1..i] is valid (within its segment) and occurred in the corpus (k tokens within one shard followed by a token
 of that shard), that context's most frequent next token (count descending, then token ascending) and its count; 0, 0,

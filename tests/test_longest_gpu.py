@@ -1,4 +1,4 @@
-"""GPU: the longest exact suffix match (ngram_amd.longest, BASELINE's fifth configuration) against the oracle's
+"""GPU: the longest exact suffix match (ngram_amd.longest, configuration c5) against the oracle's
 restatement (oracle_longest_match, pinned by brute force on tiny streams): length, next token, its count."""
 
 import numpy as np
