@@ -94,12 +94,13 @@ __global__ void part_bounds_k(const u64* __restrict__ ev, i64 n, int pbits, int 
 #define SS_ITEMS 8
 #define SS_CHUNK (SS_BLOCK * SS_ITEMS)
 #define SS_MAXB 2048  // digits of up to 11 bits
+template <int BMAX>  // the digit arrays' size: 256 keeps two blocks per CU in LDS
 __global__ void __launch_bounds__(SS_BLOCK) seg_scatter_k(const u64* __restrict__ src, u64 R,
                                                          const i64* __restrict__ bases,
                                                          const u32* __restrict__ ev_count, const u32* __restrict__ dpre,
                                                          i64 nseg, int shift, int nbits, u64* __restrict__ out) {
     __shared__ u64 stage[SS_CHUNK];
-    __shared__ u32 cnt[SS_MAXB], pre[SS_MAXB], base[SS_MAXB], wt[SS_BLOCK / WAVE];
+    __shared__ u32 cnt[BMAX], pre[BMAX], base[BMAX], wt[SS_BLOCK / WAVE];
     const int t = threadIdx.x, lane = lane_id(), wid = t / WAVE;
     const u32 B = 1u << nbits, mask = B - 1u;
     for (i64 sg = blockIdx.x; sg < nseg; sg += gridDim.x) {
@@ -122,7 +123,7 @@ __global__ void __launch_bounds__(SS_BLOCK) seg_scatter_k(const u64* __restrict_
                 rank[j] = i < n ? atomicAdd(&cnt[(u32)(key[j] >> shift) & mask], 1u) : 0u;
             }
             __syncthreads();
-            // exclusive scan of the B digit counts: thread t holds digits 2t and 2t + 1
+            // exclusive scan of the B digit counts: thread t holds digits 2t and 2t + 1 (B <= 2 * SS_BLOCK)
             const u32 d0 = 2u * (u32)t;
             const u32 a0 = d0 < B ? cnt[d0] : 0u, a1 = d0 + 1 < B ? cnt[d0 + 1] : 0u;
             u32 incl = a0 + a1;
@@ -640,8 +641,12 @@ extern "C" int ng_seg_scatter(const u64* src, u64 R, const i64* bases, const u32
         return -1;
     if (nseg == 0) return 0;
     const i64 g = nseg < 16384 ? nseg : 16384;
-    seg_scatter_k<<<(unsigned)g, SS_BLOCK, 0, (hipStream_t)stream>>>(src, R, bases, ev_count, dpre, nseg, shift, nbits,
-                                                                     out);
+    if (nbits <= 8)
+        seg_scatter_k<256><<<(unsigned)g, SS_BLOCK, 0, (hipStream_t)stream>>>(src, R, bases, ev_count, dpre, nseg, shift,
+                                                                            nbits, out);
+    else
+        seg_scatter_k<SS_MAXB><<<(unsigned)g, SS_BLOCK, 0, (hipStream_t)stream>>>(src, R, bases, ev_count, dpre, nseg,
+                                                                                shift, nbits, out);
     return (int)hipGetLastError();
 }
 
