@@ -29,6 +29,7 @@ PART_BLOCKS = 2048  # count blocks, each a run of consecutive partitions
 PART_MIN_BITS = 11  # at least this many partition bits: enough blocks for the lookups as well
 ESC_CAP = 1 << 20  # packed pairs whose count exceeds the word's count field, per level
 PACK_MIN_BITS = 0  # context-id bits of the packed words at least this (up to 44: a narrower count field)
+SEG_MIN_EVENTS = 4096  # events per scan region from which the partition sort's first pass reads the regions directly
 
 
 def emit_region(L: int, grid: int) -> int:
@@ -103,13 +104,16 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids:
         n_ev = int(total.item())
         if n_ev >= 1 << 32:
             raise RuntimeError(f"{n_ev} events: the region scatter's offsets are 32-bit")
-        ev = torch.empty(max(n_ev, 1), dtype=torch.int64, device=dev)
-        e0, e1 = event("partition", n_ev)
-        e0.record()
-        elib("ng_seg_scatter", regions, u64(R), None, ev_count, dpre, nseg, i32(56), i32(8), ev)
-        e1.record()
+        if n_ev < SEG_MIN_EVENTS * nseg:  # few events per region: packing them costs less than scattering per region
+            ev, _ = pack_events(elib, regions, R, ev_count, nseg, event)
+        else:
+            ev = torch.empty(max(n_ev, 1), dtype=torch.int64, device=dev)
+            e0, e1 = event("partition", n_ev)
+            e0.record()
+            elib("ng_seg_scatter", regions, u64(R), None, ev_count, dpre, nseg, i32(56), i32(8), ev)
+            e1.record()
+            msd = 1
         del dpre
-        msd = 1
     dev = ev.device
     cb = max(1, (max(n_ids, 2) - 1).bit_length(), PACK_MIN_BITS) if packed else 0
     N = nq = 0

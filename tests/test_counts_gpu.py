@@ -45,7 +45,8 @@ def _partition_small_tables(monkeypatch):
                                                ({2: 1, 3: 2}, "record"), ({}, "partitioned"),
                                                ({2: 1, 3: 2}, "partitioned"), ({}, "part"), ({2: 1, 3: 2}, "part"),
                                                ({}, "part-compact"), ({2: 1, 3: 2}, "part-regroup"),
-                                               ({}, "part-escape"), ({}, "part-unpacked")])
+                                               ({}, "part-escape"), ({}, "part-unpacked"), ({}, "part-seg"),
+                                               ({2: 1, 3: 2}, "part-seg")])
 def test_counts_match_oracle(corpus, level_shards, mode, monkeypatch):
     if mode == "partitioned":
         _partition_small_tables(monkeypatch)
@@ -55,6 +56,8 @@ def test_counts_match_oracle(corpus, level_shards, mode, monkeypatch):
         monkeypatch.setattr(P, "PART_TARGET", 1 << 30)
         monkeypatch.setattr(P, "PART_MIN_BITS", 0)
         monkeypatch.setattr(P, "PART_BLOCKS", 3)
+    if mode == "part-seg":  # the partition sort's first pass reads the scan regions however few events they hold
+        monkeypatch.setattr(P, "SEG_MIN_EVENTS", 0)
     if mode in ("part-escape", "part-unpacked"):
         # an 8-bit count field: counts of 255 and more go to the escape table; with a 4-slot table it overflows and
         # every level is counted again unpacked

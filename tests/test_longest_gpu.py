@@ -20,8 +20,12 @@ def corpus():
     return data.make_corpus("c5", train_tokens=700_000, query_tokens=60_001, shard_tokens=300_000)
 
 
-@pytest.mark.parametrize("cap", [64, 8, 1])
-def test_longest_match_matches_oracle(corpus, cap):
+@pytest.mark.parametrize("cap,seg", [(64, False), (64, True), (8, False), (1, True)])
+def test_longest_match_matches_oracle(corpus, cap, seg, monkeypatch):
+    if seg:  # the bitmap levels' counts read the scan regions directly however few events they hold
+        from ngram_amd import partcount as P
+
+        monkeypatch.setattr(P, "SEG_MIN_EVENTS", 0)
     x = corpus.query[:-1]
     avail = O.segments(x)
     want = O.longest_match(corpus.train, corpus.bounds, x, avail, cap)
