@@ -413,6 +413,8 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
 // index of its first word), stored whole as 16-byte vectors; flags[0] bit 2 if a total reaches 2^32. dist may be
 // NULL; with nstat: the contexts counted in nstat[1..256] (their sum) and, with deep, each context of more than
 // deep_min pairs appended to deep (nstat[0] of them; callers size deep for U / (deep_min + 1) + 1).
+#define SUMMARY_AHEAD 4  // windows of a long context loaded per step
+
 template <int KT>
 __global__ void __launch_bounds__(256) ctx_summary_k(const u64* __restrict__ w, i64 U, int cb,
                                                      const u64* __restrict__ esc_k, const u32* __restrict__ esc_c,
@@ -488,20 +490,41 @@ __global__ void __launch_bounds__(256) ctx_summary_k(const u64* __restrict__ w, 
                 lt[0] = rank_score(word >> csh, (u32)part);
             }
             u32 len = (u32)(WAVE - h);
-            bool cont = true;
-            for (i64 nx = wv * WAVE + WAVE; cont; nx += WAVE) {
-                const i64 j = nx + lane;
-                const bool v2 = j < U;
-                const u64 w2 = !v2 ? 0 : nx == wv * WAVE + WAVE ? ahead : w[j];
-                const bool in2 = v2 && (w2 >> sh) == hc;
+            // the following windows: the next one already loaded (`ahead`), then SUMMARY_AHEAD windows per step, all
+            // their loads issued before any is used (a long context costs one load latency per step, not per window)
+            {
+                const i64 j = wv * WAVE + WAVE + lane;
+                const bool in2 = j < U && (ahead >> sh) == hc;
                 const u64 m2 = __ballot(in2);
                 if (in2) {
-                    const u32 n = count_of(w2);
+                    const u32 n = count_of(ahead);
                     part += n;
-                    topk_insert<KT>(lt, rank_score(w2 >> csh, n));
+                    topk_insert<KT>(lt, rank_score(ahead >> csh, n));
                 }
                 len += (u32)__popcll(m2);
-                cont = ((m2 >> (WAVE - 1)) & 1ull) && nx + WAVE < U;
+                bool cont = ((m2 >> (WAVE - 1)) & 1ull) && wv * WAVE + 2 * WAVE < U;
+                for (i64 nx = wv * WAVE + 2 * WAVE; cont; nx += SUMMARY_AHEAD * WAVE) {
+                    u64 w4[SUMMARY_AHEAD];
+#pragma unroll
+                    for (int q = 0; q < SUMMARY_AHEAD; ++q) {
+                        const i64 jq = nx + q * WAVE + lane;
+                        w4[q] = jq < U ? w[jq] : 0;
+                    }
+#pragma unroll
+                    for (int q = 0; q < SUMMARY_AHEAD; ++q) {
+                        if (!cont) break;  // wave-uniform
+                        const i64 jq = nx + q * WAVE + lane;
+                        const bool iq = jq < U && (w4[q] >> sh) == hc;
+                        const u64 mq = __ballot(iq);
+                        if (iq) {
+                            const u32 n = count_of(w4[q]);
+                            part += n;
+                            topk_insert<KT>(lt, rank_score(w4[q] >> csh, n));
+                        }
+                        len += (u32)__popcll(mq);
+                        cont = ((mq >> (WAVE - 1)) & 1ull) && nx + (q + 1) * WAVE < U;
+                    }
+                }
             }
 #pragma unroll
             for (int d = WAVE / 2; d > 0; d >>= 1) part += shfl_down_u64(part, d);
