@@ -117,6 +117,12 @@ ng_u64 ng_emit_region(ng_i64 L, int grid);
 int ng_scan_emit(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, uint32_t* bm_out, const ng_u64* vt,
                  ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, ng_u64* ev, ng_u64 region, uint32_t* ev_count,
                  uint32_t* flags, int grid, int sparse, uint32_t* dhist, ng_i64 dstride, void* stream);
+/* the emitting scan over listed positions: the first *n_dev entries of plist (a device-side count: no host sync),
+ * events and digit histograms as ng_scan_emit's, each hit's bit set in bm_out (zeroed by the caller; may be NULL);
+ * region >= ceil(n / (grid * 256)) * 256 */
+int ng_scan_emit_list(const uint16_t* tok, const ng_u64* plist, const ng_u64* n_dev, int k, const ng_u64* vt,
+                      ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, uint32_t* bm_out, ng_u64* ev, ng_u64 region,
+                      uint32_t* ev_count, uint32_t* flags, int grid, uint32_t* dhist, ng_i64 dstride, void* stream);
 /* a level scan with optional outputs over a bitmap-gated range (plist NULL: [0, L) gated by bm_in in ng_scan_count's
  * sparse modes, hit bitmap into bm_out) or over listed positions (plist: n corpus positions); hit (may be NULL):
  * hit[context id] = 1 per hit; ev (may be NULL): block b of grid appends per hit mix64(pair key) (what 0) or its

@@ -168,9 +168,10 @@ template <int K, class S>
 __global__ void __launch_bounds__(256) scan_list_k(const u16* __restrict__ tok, const u64* __restrict__ plist, i64 n,
                                                    int k, const u64* __restrict__ vt, u64 vcap,
                                                    const u32* __restrict__ vrep, const u16* __restrict__ x, S sink,
-                                                   u32* flags) {
+                                                   u32* flags, const u64* __restrict__ n_dev, u32* __restrict__ bm_out) {
     __shared__ SinkShared ss;
     sink_begin<S>(sink, &ss);
+    if (n_dev) n = (i64)*n_dev;  // the list's length as a device-side count
     const int lane = lane_id();
     const i64 stride = (i64)gridDim.x * blockDim.x;
     for (i64 base = blockIdx.x * (i64)blockDim.x + (threadIdx.x & ~(WAVE - 1)); base < n; base += stride) {
@@ -183,6 +184,7 @@ __global__ void __launch_bounds__(256) scan_list_k(const u16* __restrict__ tok, 
             key = probe_key<K>(tok, p, k, vt, vcap, vrep, x, flags);
         }
         const bool hit = key != EMPTY;
+        if (bm_out && hit) atomicOr(&bm_out[p >> 5], 1u << (p & 31));
         if constexpr (S::KIND == 2) emit_wave(sink, &ss, __ballot(hit), hit, key, p, flags);
         else if (hit) sink_hit(sink, key, full, flags);
     }
@@ -583,6 +585,21 @@ extern "C" int ng_scan_emit(const u16* tok, i64 L, int k, const u32* bm_in, u32*
     return (int)hipGetLastError();
 }
 
+// The emitting scan over listed positions: the first *n_dev entries of plist (shard-relative corpus positions, a
+// device-side count, so no host sync), hits' mix64(pair key) appended as ng_scan_emit's (block b of `grid` to
+// ev[b * region ...], their number in ev_count[b], digit histograms as ng_scan_emit's), and each hit's bit set in
+// bm_out (zeroed by the caller; may be NULL). region >= ceil(n_max / (grid * 256)) * 256 for n_max >= *n_dev.
+extern "C" int ng_scan_emit_list(const u16* tok, const u64* plist, const u64* n_dev, int k, const u64* vt, u64 vcap,
+                                 const u32* vrep, const u16* x, u32* bm_out, u64* ev, u64 region, u32* ev_count,
+                                 u32* flags, int grid, u32* dhist, i64 dstride, void* stream) {
+    if (grid <= 0 || n_dev == nullptr || region == 0 || region > 0xFFFFFFFFull || (dhist && dstride < grid)) return -1;
+    const EmitSink sk{ev, region, ev_count, 0, nullptr, dhist, dstride};
+    hipStream_t st = (hipStream_t)stream;
+    LEVEL_SWITCH(k, (scan_list_k<K, EmitSink><<<grid, 256, 0, st>>>(tok, plist, 0, k, vt, vcap, vrep, x, sk, flags, n_dev,
+                                                                     bm_out)));
+    return (int)hipGetLastError();
+}
+
 // A level scan with optional outputs, over a bitmap-gated range (plist NULL: positions [0, L) gated by bm_in as
 // ng_scan_count's `sparse` modes, hit bitmap into bm_out) or over listed positions (plist: n corpus positions, bm_*
 // unused). hit (may be NULL): hit[context id] = 1 per hit. ev (may be NULL): block b of `grid` appends per hit
@@ -601,9 +618,11 @@ extern "C" int ng_scan_sink(const u16* tok, i64 L, int k, const u32* bm_in, u32*
         }
         if (ev) {
             const EmitSink sk{ev, region, ev_count, what, hit};
-            LEVEL_SWITCH(k, (scan_list_k<K, EmitSink><<<grid, 256, 0, st>>>(tok, plist, n, k, vt, vcap, vrep, x, sk, flags)));
+            LEVEL_SWITCH(k, (scan_list_k<K, EmitSink><<<grid, 256, 0, st>>>(tok, plist, n, k, vt, vcap, vrep, x, sk, flags,
+                                                                             nullptr, nullptr)));
         } else {
-            LEVEL_SWITCH(k, (scan_list_k<K, ExistSink><<<grid, 256, 0, st>>>(tok, plist, n, k, vt, vcap, vrep, x, ExistSink{hit}, flags)));
+            LEVEL_SWITCH(k, (scan_list_k<K, ExistSink><<<grid, 256, 0, st>>>(tok, plist, n, k, vt, vcap, vrep, x,
+                                                                              ExistSink{hit}, flags, nullptr, nullptr)));
         }
         return (int)hipGetLastError();
     }

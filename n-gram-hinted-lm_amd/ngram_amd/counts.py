@@ -31,6 +31,7 @@ from .qindex import QueryIndex
 
 GAP = 32
 SCAN_BLOCKS_PER_CU = 8  # level-scan blocks (grid-stride) per compute unit (c3 sweep: 8 fastest of 4-32)
+LIST_DENSITY = 0.05  # part mode: a level behind a sparser one probes the previous hits as a position list (c3 sweep)
 LEVELS = (2, 3, 4, 5, 6, 10, 20)
 LEVEL_SHARDS = {2: 103, 3: 370, 4: 370, 5: 370}
 PAIRS = {2: (82.17e6, 0.620), 3: (62.30e6, 0.667), 4: (26.39e6, 0.694), 5: (8.99e6, 0.706), 6: (3.17e6, 0.705),
@@ -116,6 +117,7 @@ class CountBuild:
         self.min_cap = 1 << 20
         self.mode = "part"
         self.density: dict[int, float] = {}  # each level's hit density, from the last build with stats
+        self._plist = None  # part mode: a shard's listed positions (list scans)
         self.dratio: dict[int, float] = {}  # "part" mode: each level's distinct pairs per event, from the last build
         self.levels = tuple(levels)
         if not self.levels or list(self.levels) != sorted(set(self.levels)) or self.levels[0] < 1:
@@ -154,6 +156,7 @@ class CountBuild:
         self.min_cap = 1 << 20
         self.mode = "part"
         self.density: dict[int, float] = {}  # each level's hit density, from the last build with stats
+        self._plist = None  # part mode: a shard's listed positions (list scans)
         self.dratio: dict[int, float] = {}  # "part" mode: each level's distinct pairs per event, from the last build
         self.levels = tuple(levels)
         ls = LEVEL_SHARDS if level_shards is None else level_shards
@@ -256,14 +259,17 @@ class CountBuild:
             if tables[k]["pbits"]:
                 self._flush(tables[k], k)
 
-    def _scan_mode(self, li: int, scanned: list) -> int:
+    def _scan_mode(self, li: int, scanned: list, lists: bool = False) -> int:
         """The engine scan's mode for a shard's li-th scanned level: a lane per position (0) for the first level and
-        behind a dense previous level, else the LDS-listed set positions (2). The previous level's density is the
-        one its last build measured (stats), dense when unknown."""
+        behind a dense previous level, else the LDS-listed set positions (2), or with `lists` (part mode) below
+        LIST_DENSITY the set positions listed in memory first (3). The previous level's density is the one its last
+        build measured (stats), dense when unknown."""
         if li == 0:
             return 0
         d = self.density.get(scanned[li - 1])
-        return 2 if d is not None and d < 0.5 else 0
+        if d is None or d >= 0.5:
+            return 0
+        return 3 if lists and d < LIST_DENSITY else 2
 
     def _flush(self, t: dict, k: int) -> None:
         """Count a partitioned level's emitted keys: group them by sub-table, then count sub-table by sub-table."""
@@ -474,11 +480,21 @@ class CountBuild:
             si = scanned.index(k)
             # gated by this shard's previous scanned level; a shard that level skipped is probed whole
             bm_in = None if si == 0 else bms[scanned[si - 1]][st // 32 :]
+            mode = self._scan_mode(si, scanned, lists=True)
             e0, e1 = self._event("scan_emit", k, i, n32)
             e0.record()
-            elib("ng_scan_emit", self.tok[st:], n32, i32(k), bm_in, bms[k][st // 32 :], vi.table, u64(vi.cap), vi.rep,
-                 self.x, regions[j * G * R :], u64(R), ev_count[j * G :], flags, i32(G),
-                 i32(self._scan_mode(si, scanned)), dhist[j * G :], nseg)
+            if mode == 3:  # the previous level's hits listed, then probed one lane each
+                if self._plist is None or self._plist.numel() < n32:
+                    self._plist = torch.empty(max(self.sizes) + 64, dtype=torch.int64, device=dev)
+                n_list = torch.zeros(1, dtype=torch.int64, device=dev)
+                elib.cub("ng_bits_list", bm_in, n32 // 32, self._plist, n_list)
+                elib("ng_scan_emit_list", self.tok[st:], self._plist, n_list, i32(k), vi.table, u64(vi.cap), vi.rep,
+                     self.x, bms[k][st // 32 :], regions[j * G * R :], u64(R), ev_count[j * G :], flags, i32(G),
+                     dhist[j * G :], nseg)
+            else:
+                elib("ng_scan_emit", self.tok[st:], n32, i32(k), bm_in, bms[k][st // 32 :], vi.table, u64(vi.cap),
+                     vi.rep, self.x, regions[j * G * R :], u64(R), ev_count[j * G :], flags, i32(G), i32(mode),
+                     dhist[j * G :], nseg)
             e1.record()
         if int(flags[0].item()) & 4:
             raise RuntimeError(f"k={k}: an emit region overflowed")

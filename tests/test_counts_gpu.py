@@ -46,7 +46,8 @@ def _partition_small_tables(monkeypatch):
                                                ({2: 1, 3: 2}, "partitioned"), ({}, "part"), ({2: 1, 3: 2}, "part"),
                                                ({}, "part-compact"), ({2: 1, 3: 2}, "part-regroup"),
                                                ({}, "part-escape"), ({}, "part-unpacked"), ({}, "part-seg"),
-                                               ({2: 1, 3: 2}, "part-seg")])
+                                               ({2: 1, 3: 2}, "part-seg"), ({}, "part-list"),
+                                               ({2: 1, 3: 2}, "part-list")])
 def test_counts_match_oracle(corpus, level_shards, mode, monkeypatch):
     if mode == "partitioned":
         _partition_small_tables(monkeypatch)
@@ -67,8 +68,11 @@ def test_counts_match_oracle(corpus, level_shards, mode, monkeypatch):
     lib = C.record_lib()
     cb = C.CountBuild(corpus.shards(), levels=LEVELS, level_shards=level_shards, topk=4)
     cb.mode = mode.split("-")[0]
-    if mode.endswith("-compact"):  # every gated level scans its LDS-listed set positions
+    if mode.endswith("-compact") or mode.endswith("-list"):
+        # every gated level scans its LDS-listed set positions, or (part-list) the positions listed in memory first
         cb.density = {k: 0.0 for k in LEVELS}
+        if mode == "part-compact":
+            monkeypatch.setattr(C, "LIST_DENSITY", 0.0)
     cb.start_load(3)
     cb.pace()
     cb.pace()
