@@ -224,6 +224,7 @@ __global__ void __launch_bounds__(256) scan_sparse_k(const u16* __restrict__ tok
 // set positions in LDS (a wave prefix sum of their popcounts), and its lanes then probe the listed positions 64 at a
 // time, so every lane has work whatever the density and no position outside the bitmap is visited. Hits set their
 // bit in an LDS copy of the words (written out whole).
+#define COMPACT_PPL 4  // listed positions probed per lane at once
 template <int K, class S>
 __global__ void __launch_bounds__(256) scan_compact_k(const u16* __restrict__ tok, i64 L, int k,
                                                       const u32* __restrict__ bm_in, u32* __restrict__ bm_out,
@@ -254,26 +255,35 @@ __global__ void __launch_bounds__(256) scan_compact_k(const u16* __restrict__ to
             list[w][at++] = (u32)(lane * 32 + b);
         }
         words[w][lane] = 0;
-        __syncthreads();
+        // the list and the words are the wave's own: no block barrier (the wave's LDS accesses stay in order)
         const bool full = sink_full<S>(flags);
-        for (u32 r0 = 0; r0 < total; r0 += WAVE) {  // every lane runs the same rounds (wave-wide emission)
-            const u32 r = r0 + lane;
-            u64 key = EMPTY;
-            u32 lp = 0;
-            if (r < total) {
-                lp = list[w][r];
-                const i64 p = ((g0 + w * 64) << 5) + lp;
-                if (p < L) key = probe_key<K>(tok, p, k, vt, vcap, vrep, x, flags);
+        const i64 pbase = (g0 + w * 64) << 5;
+        for (u32 r0 = 0; r0 < total; r0 += WAVE * COMPACT_PPL) {  // every lane runs the same rounds
+            // COMPACT_PPL probes per lane started together: their first loads are in flight at once
+            u64 key[COMPACT_PPL], sl[COMPACT_PPL], v[COMPACT_PPL];
+            u32 nxt[COMPACT_PPL], lp[COMPACT_PPL];
+#pragma unroll
+            for (int q = 0; q < COMPACT_PPL; ++q) {
+                const u32 r = r0 + q * WAVE + lane;
+                key[q] = EMPTY;
+                lp[q] = 0;
+                if (r < total) {
+                    lp[q] = list[w][r];
+                    if (pbase + lp[q] < L) probe_start<K>(tok, pbase + lp[q], k, vt, vcap, key[q], sl[q], v[q], nxt[q]);
+                }
             }
-            const bool hit = key != EMPTY;
-            if (hit) atomicOr(&words[w][lp >> 5], 1u << (lp & 31));
-            if constexpr (S::KIND == 2)
-                emit_wave(sink, &ss, __ballot(hit), hit, key, ((g0 + w * 64) << 5) + lp, flags);
-            else if (hit) sink_hit(sink, key, full, flags);
+#pragma unroll
+            for (int q = 0; q < COMPACT_PPL; ++q) {
+                if (r0 + q * WAVE >= total) break;  // wave-uniform
+                const u64 hk = probe_finish<K>(tok, pbase + lp[q], k, vt, vrep, x, flags, key[q], sl[q], v[q], nxt[q]);
+                const bool hit = hk != EMPTY;
+                if (hit) atomicOr(&words[w][lp[q] >> 5], 1u << (lp[q] & 31));
+                if constexpr (S::KIND == 2)
+                    emit_wave(sink, &ss, __ballot(hit), hit, hk, pbase + lp[q], flags);
+                else if (hit) sink_hit(sink, hk, full, flags);
+            }
         }
-        __syncthreads();
         if (wi < nwords) bm_out[wi] = words[w][lane];
-        __syncthreads();
     }
     sink_end(sink, &ss);
 }

@@ -118,6 +118,46 @@ __device__ __forceinline__ u64 probe_key(const u16* __restrict__ tok, i64 p, int
     }
 }
 
+// A probe in two halves, so that several positions' first loads are in flight together: probe_start computes the
+// position's context key (EMPTY: none, or its next token is a gap) and loads its home slot; probe_finish walks on from
+// there exactly as probe_key does.
+template <int K>
+__device__ __forceinline__ void probe_start(const u16* __restrict__ tok, i64 p, int k, const u64* __restrict__ vt,
+                                            u64 vcap, u64& key, u64& s, u64& v, u32& nxt) {
+    key = EMPTY;
+    nxt = tok[p];
+    if (nxt == SENT) return;
+    key = ctx_key_stop<K>(tok + p, k);
+    if (key == EMPTY) return;
+    s = __umul64hi(key, vcap);
+    v = vt[s];
+}
+
+template <int K>
+__device__ __forceinline__ u64 probe_finish(const u16* __restrict__ tok, i64 p, int k, const u64* __restrict__ vt,
+                                            const u32* __restrict__ vrep, const u16* __restrict__ x, u32* flags,
+                                            u64 key, u64 s, u64 v, u32 nxt) {
+    if (key == EMPTY) return EMPTY;
+    while (true) {
+        if (v == key) {
+            const int kk = klen<K>(k);
+            if (kk > 4) {
+                const u16* a = tok + p - kk;
+                const u16* b = x + (i64)vrep[s] + 1 - kk;
+                bool same = true;
+                for (int j = 0; j < kk; ++j) same &= a[j] == b[j];
+                if (!same) {
+                    atomicAdd(&flags[1], 1u);
+                    return EMPTY;
+                }
+            }
+            return (s << 16) | nxt;
+        }
+        if (v == EMPTY) return EMPTY;
+        v = vt[++s];
+    }
+}
+
 // Dense levels: a lane per position, a wave per 64 positions (two 32-bit bitmap words). Hits are counted directly,
 // or with EMIT appended to `emit` (one atomic per wave for its slots).
 template <int K, bool EMIT, int KB>
