@@ -26,6 +26,7 @@ from .data import BOS, HEADER_BYTES, shard_tokens
 from .gpu_val_stats import PAIRS as GVS_PAIRS
 from .gpu_val_stats import ValIndex, layout
 from .lib import Lib, i32, u64
+from . import partcount
 from .partcount import count_events, emit_region, record_tops, summarize
 from .qindex import QueryIndex
 
@@ -118,6 +119,7 @@ class CountBuild:
         self.mode = "part"
         self.density: dict[int, float] = {}  # each level's hit density, from the last build with stats
         self._plist = None  # part mode: a shard's listed positions (list scans)
+        self.events_of: dict[int, int] = {}  # part mode: each level's events in the last build
         self.dratio: dict[int, float] = {}  # "part" mode: each level's distinct pairs per event, from the last build
         self.levels = tuple(levels)
         if not self.levels or list(self.levels) != sorted(set(self.levels)) or self.levels[0] < 1:
@@ -157,6 +159,7 @@ class CountBuild:
         self.mode = "part"
         self.density: dict[int, float] = {}  # each level's hit density, from the last build with stats
         self._plist = None  # part mode: a shard's listed positions (list scans)
+        self.events_of: dict[int, int] = {}  # part mode: each level's events in the last build
         self.dratio: dict[int, float] = {}  # "part" mode: each level's distinct pairs per event, from the last build
         self.levels = tuple(levels)
         ls = LEVEL_SHARDS if level_shards is None else level_shards
@@ -431,6 +434,7 @@ class CountBuild:
                              event=ev_fn, seg=seg, presort="ctx")
             del seg
             n_ev = c.n_ev
+            self.events_of[k] = n_ev
             self.dratio[k] = c.U / max(1, n_ev)
             t2 = time.perf_counter()
             scan_t += t1 - t0
@@ -470,7 +474,10 @@ class CountBuild:
         shards = [i for i in range(len(self.sizes)) if i < self.level_shards[k]]
         nseg = len(shards) * G
         ev_count = torch.zeros(max(nseg, 1), dtype=torch.int32, device=dev)
-        dhist = torch.empty(256 * max(nseg, 1), dtype=torch.int32, device=dev)
+        # the scan's digit histograms only where the last build's events let the partition sort read the regions
+        last = self.events_of.get(k)
+        dhist = torch.empty(256 * max(nseg, 1), dtype=torch.int32, device=dev) \
+            if last is None or last >= partcount.SEG_MIN_EVENTS * nseg else None
         flags = torch.zeros(2, dtype=torch.int32, device=dev)
         for j, i in enumerate(shards):
             st, n = self.starts[i], self.sizes[i]
@@ -490,11 +497,11 @@ class CountBuild:
                 elib.cub("ng_bits_list", bm_in, n32 // 32, self._plist, n_list)
                 elib("ng_scan_emit_list", self.tok[st:], self._plist, n_list, i32(k), vi.table, u64(vi.cap), vi.rep,
                      self.x, bms[k][st // 32 :], regions[j * G * R :], u64(R), ev_count[j * G :], flags, i32(G),
-                     dhist[j * G :], nseg)
+                     dhist[j * G :] if dhist is not None else None, nseg)
             else:
                 elib("ng_scan_emit", self.tok[st:], n32, i32(k), bm_in, bms[k][st // 32 :], vi.table, u64(vi.cap),
                      vi.rep, self.x, regions[j * G * R :], u64(R), ev_count[j * G :], flags, i32(G), i32(mode),
-                     dhist[j * G :], nseg)
+                     dhist[j * G :] if dhist is not None else None, nseg)
             e1.record()
         if int(flags[0].item()) & 4:
             raise RuntimeError(f"k={k}: an emit region overflowed")

@@ -90,12 +90,15 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids:
     int16 [N], positions int32 or None): qcnt[i] = the count of (ctx_of[i], tgt[i]) for the listed positions (all
     without a list), 0 where absent, out of range or not listed. `packed`: pairs as packed words (falls back to keys +
     counts when the escape table overflows). `seg` (regions, R, ev_count, dhist, nseg): the events straight from an
-    emitting scan's regions with its digit histograms (ng_scan_emit's dhist, digit-major with stride nseg); ev and
-    n_ev are then unused: the first partition pass reads the regions (ng_seg_scatter) and groups by the top 8 bits,
+    emitting scan's regions with its digit histograms (ng_scan_emit's dhist, digit-major with stride nseg; None: the
+    regions are packed); ev and n_ev are then unused: the first partition pass reads the regions (ng_seg_scatter) and groups by the top 8 bits,
     the later passes sort the bits below them. `presort` ("ctx" / "pair", packed words only): the words come out
     already through the first pass of summarize's sort (by context / by pair key), read from the count's outputs."""
     msd = 0
-    if seg is not None:
+    if seg is not None and seg[3] is None:  # no digit histograms: the regions are packed
+        regions, R, ev_count, _, nseg = seg
+        ev, n_ev = pack_events(elib, regions, R, ev_count, nseg, event)
+    elif seg is not None:
         regions, R, ev_count, dhist, nseg = seg
         dev = regions.device
         dpre = torch.empty(max(256 * nseg, 1), dtype=torch.int32, device=dev)
