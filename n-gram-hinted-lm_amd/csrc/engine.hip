@@ -73,13 +73,19 @@ struct SinkShared {
     u32 dh[256];
 };
 
+// A context's hit flag, written only while unset: a hot context's flag is then read from cache rather than written
+// again by every hit.
+__device__ __forceinline__ void set_hit(unsigned char* hit, u64 c) {
+    if (hit[c] == 0) hit[c] = 1;
+}
+
 // A lane's hit (count and exist sinks; the emit sink uses emit_wave / emit_lane).
 template <class S>
 __device__ __forceinline__ void sink_hit(const S& s, u64 key, bool full, u32* flags) {
     if constexpr (S::KIND == 0) {
         if (!full) split_add(s.keys, s.cnts, s.cap, key, 1u, flags);
     } else if constexpr (S::KIND == 1) {
-        s.hit[key >> 16] = 1;
+        set_hit(s.hit, key >> 16);
     }
 }
 
@@ -95,7 +101,7 @@ __device__ __forceinline__ void emit_wave(const EmitSink& s, SinkShared* ss, u64
         if (at < s.region) s.ev[(u64)blockIdx.x * s.region + at] = e;
         else atomicOr(&flags[0], 4u);
         if (s.dhist) atomicAdd(&ss->dh[e >> 56], 1u);
-        if (s.hit) s.hit[key >> 16] = 1;
+        if (s.hit) set_hit(s.hit, key >> 16);
     }
 }
 
@@ -105,7 +111,7 @@ __device__ __forceinline__ void emit_lane(const EmitSink& s, SinkShared* ss, u64
     if (at < s.region) s.ev[(u64)blockIdx.x * s.region + at] = e;
     else atomicOr(&flags[0], 4u);
     if (s.dhist) atomicAdd(&ss->dh[e >> 56], 1u);
-    if (s.hit) s.hit[key >> 16] = 1;
+    if (s.hit) set_hit(s.hit, key >> 16);
 }
 
 template <class S>
