@@ -125,13 +125,13 @@ int ng_scan_emit_list(const uint16_t* tok, const ng_u64* plist, const ng_u64* n_
                       uint32_t* ev_count, uint32_t* flags, int grid, uint32_t* dhist, ng_i64 dstride, void* stream);
 /* a level scan with optional outputs over a bitmap-gated range (plist NULL: [0, L) gated by bm_in in ng_scan_count's
  * sparse modes, hit bitmap into bm_out) or over listed positions (plist: n corpus positions); hit (may be NULL):
- * hit[context id] = 1 per hit; ev (may be NULL): block b of grid appends per hit mix64(pair key) (what 0) or its
+ * hit[context id] = 1 per hit; ev (may be NULL): block b of grid appends per hit mix64(pair key + key_add) (what 0) or its
  * position (what 1) to ev[b * region ...], how many into ev_count[b]; region >= ng_emit_region(L, grid) over a
  * bitmap, >= ceil(n / (grid * 256)) * 256 over a list */
 int ng_scan_sink(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, uint32_t* bm_out, const ng_u64* plist,
                  ng_i64 n, const ng_u64* vt, ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, unsigned char* hit,
                  int what, ng_u64* ev, ng_u64 region, uint32_t* ev_count, uint32_t* flags, int grid, int sparse,
-                 void* stream);
+                 ng_u64 key_add, void* stream);
 /* the set bits of a bitmap as positions in order (out), *total of them; two-phase temp storage (temp NULL: size) */
 int ng_bits_list(void* temp, size_t* temp_bytes, const uint32_t* bm, ng_i64 nwords, ng_u64* out, ng_u64* total,
                  void* stream);

@@ -65,6 +65,7 @@ struct EmitSink {
     unsigned char* hit;
     u32* dhist;   // with what 0 (may be NULL): the block's events per top-8-bit digit, at dhist[digit * dstride + block]
     i64 dstride;
+    u64 key_add;  // added to each pair key before it is mixed (a context-id offset: several levels' ids in one space)
 };
 
 // A scan block's LDS for its sink: the emit cursor and the digit histogram.
@@ -97,7 +98,7 @@ __device__ __forceinline__ void emit_wave(const EmitSink& s, SinkShared* ss, u64
     off = (u32)__shfl((int)off, 0, WAVE);
     if (hit) {
         const u64 at = (u64)off + (u64)__popcll(b & lanemask_lt());
-        const u64 e = s.what ? (u64)p : mix64(key);
+        const u64 e = s.what ? (u64)p : mix64(key + s.key_add);
         if (at < s.region) s.ev[(u64)blockIdx.x * s.region + at] = e;
         else atomicOr(&flags[0], 4u);
         if (s.dhist) atomicAdd(&ss->dh[e >> 56], 1u);
@@ -107,7 +108,7 @@ __device__ __forceinline__ void emit_wave(const EmitSink& s, SinkShared* ss, u64
 
 __device__ __forceinline__ void emit_lane(const EmitSink& s, SinkShared* ss, u64 key, i64 p, u32* flags) {
     const u64 at = atomicAdd(&ss->cur, 1u);
-    const u64 e = s.what ? (u64)p : mix64(key);
+    const u64 e = s.what ? (u64)p : mix64(key + s.key_add);
     if (at < s.region) s.ev[(u64)blockIdx.x * s.region + at] = e;
     else atomicOr(&flags[0], 4u);
     if (s.dhist) atomicAdd(&ss->dh[e >> 56], 1u);
@@ -619,11 +620,12 @@ extern "C" int ng_scan_emit_list(const u16* tok, const u64* plist, const u64* n_
 // A level scan with optional outputs, over a bitmap-gated range (plist NULL: positions [0, L) gated by bm_in as
 // ng_scan_count's `sparse` modes, hit bitmap into bm_out) or over listed positions (plist: n corpus positions, bm_*
 // unused). hit (may be NULL): hit[context id] = 1 per hit. ev (may be NULL): block b of `grid` appends per hit
-// mix64(pair key) (what 0) or its position (what 1) to ev[b * region ...] and stores how many in ev_count[b];
-// region >= ng_emit_region(L, grid) over a bitmap, >= ceil(n / (grid * 256)) * 256 over a list.
+// mix64(pair key + key_add) (what 0) or its position (what 1) to ev[b * region ...] and stores how many in
+// ev_count[b]; region >= ng_emit_region(L, grid) over a bitmap, >= ceil(n / (grid * 256)) * 256 over a list.
 extern "C" int ng_scan_sink(const u16* tok, i64 L, int k, const u32* bm_in, u32* bm_out, const u64* plist, i64 n,
                             const u64* vt, u64 vcap, const u32* vrep, const u16* x, unsigned char* hit, int what,
-                            u64* ev, u64 region, u32* ev_count, u32* flags, int grid, int sparse, void* stream) {
+                            u64* ev, u64 region, u32* ev_count, u32* flags, int grid, int sparse, u64 key_add,
+                            void* stream) {
     if (grid <= 0 || (what != 0 && what != 1)) return -1;
     if (ev && (region == 0 || region > 0xFFFFFFFFull)) return -1;
     hipStream_t st = (hipStream_t)stream;
@@ -633,7 +635,7 @@ extern "C" int ng_scan_sink(const u16* tok, i64 L, int k, const u32* bm_in, u32*
             return (int)hipGetLastError();
         }
         if (ev) {
-            const EmitSink sk{ev, region, ev_count, what, hit};
+            const EmitSink sk{ev, region, ev_count, what, hit, nullptr, 0, key_add};
             LEVEL_SWITCH(k, (scan_list_k<K, EmitSink><<<grid, 256, 0, st>>>(tok, plist, n, k, vt, vcap, vrep, x, sk, flags,
                                                                              nullptr, nullptr)));
         } else {
@@ -644,7 +646,7 @@ extern "C" int ng_scan_sink(const u16* tok, i64 L, int k, const u32* bm_in, u32*
     }
     if (L <= 0) return 0;
     int rc;
-    if (ev) rc = launch_scan(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, EmitSink{ev, region, ev_count, what, hit},
+    if (ev) rc = launch_scan(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, EmitSink{ev, region, ev_count, what, hit, nullptr, 0, key_add},
                              flags, grid, sparse, st);
     else rc = launch_scan(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, ExistSink{hit}, flags, grid, sparse, st);
     if (rc != 0) return -1;

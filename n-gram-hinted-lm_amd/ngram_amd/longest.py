@@ -107,6 +107,8 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
     qpos, qlen = qpos[order].to(torch.int32), qlen[order]
     bounds = torch.searchsorted(qlen, torch.arange(len(levels) + 2, device=dev, dtype=torch.int32)).cpu().tolist()
     big = None  # the regions of a bitmap level's emitting scan, made when one is counted
+    batch: list = []  # list levels waiting to be counted together: (k, final positions, index)
+    batch_ev = 0
     for k in range(1, len(levels) + 1):
         fpos = qpos[bounds[k] : bounds[k + 1]]
         m = fpos.numel()
@@ -114,6 +116,13 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
             continue
         vi = QueryIndex(elib, x, avail, k, fpos, compact=True)
         kind, hs, nh = levels[k - 1]
+        if kind == "list":  # a sparse level: counted with the other list levels, one count for all
+            batch.append((k, fpos, vi))
+            batch_ev += nh
+            if batch_ev >= BATCH_EVENTS:
+                _count_batch(elib, lib, tok, L, x, batch, levels, flags, grid, nxt, cnt)
+                batch, batch_ev = [], 0
+            continue
         # the level's hit positions probed against the final contexts; their hits emitted, partitioned and counted in
         # LDS, then each final context's top entry
         flags.zero_()
@@ -154,6 +163,8 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
         nxt[fpos.long()] = o_tok
         cnt[fpos.long()] = o_cnt
         del vi, c, o_tok, o_cnt
+    if batch:
+        _count_batch(elib, lib, tok, L, x, batch, levels, flags, grid, nxt, cnt)
     if timing is not None:
         torch.cuda.synchronize()
         timing["count"] = timing.get("count", 0.0) + time.perf_counter() - t0
@@ -161,6 +172,7 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
 
 
 SCAN_BLOCKS_PER_CU = 32  # scan blocks per compute unit
+BATCH_EVENTS = 1 << 28  # list levels counted together until their listed positions reach this
 LIST_DIV = 64  # a level's hits go to a position list once fewer than L / LIST_DIV (8 B each against L / 8 bitmap bytes)
 
 
@@ -181,9 +193,60 @@ def _scan_list(elib: Lib, tok, L: int, k: int, vi, x, cand: torch.Tensor, hit, w
     regions = torch.empty(g * R, dtype=torch.int64, device=cand.device)
     ev_count = torch.empty(g, dtype=torch.int32, device=cand.device)
     elib("ng_scan_sink", tok, L, i32(k), None, None, cand, n, vi.table, u64(vi.cap), vi.rep, x, hit, i32(what),
-         regions, u64(R), ev_count, flags, i32(g), i32(0))
+         regions, u64(R), ev_count, flags, i32(g), i32(0), u64(0))
     out, m = pack_events(elib, regions, R, ev_count, g)
     return out[:m] if what else out, m
+
+
+def _count_batch(elib: Lib, lib: Lib, tok, L: int, x, batch: list, levels: list, flags, grid: int, nxt, cnt) -> None:
+    """The counting phase of several list levels at once: level k's context ids offset by the ids before it in the
+    batch, so one partitioned count, one summary and one gather serve them all (per level only its query index and
+    its scan: few launches and no host sync per level)."""
+    dev = x.device
+    bases, n_ids = [], 0
+    for _, _, vi in batch:
+        bases.append(n_ids)
+        n_ids += vi.ids
+    cap_ev = sum(levels[k - 1][2] for k, _, _ in batch)  # each listed position emits at most one event
+    ev = torch.empty(max(cap_ev, 1), dtype=torch.int64, device=dev)
+    at = torch.zeros(1, dtype=torch.int64, device=dev)  # the events packed so far (device side)
+    flags.zero_()
+    for (k, _, vi), b in zip(batch, bases):
+        _, hs, nh = levels[k - 1]
+        g = max(1, min(grid, -(-nh // 256)))
+        R = -(-max(nh, 1) // (g * 256)) * 256
+        regions = torch.empty(g * R, dtype=torch.int64, device=dev)
+        ev_count = torch.empty(g, dtype=torch.int32, device=dev)
+        elib("ng_scan_sink", tok, L, i32(k), None, None, hs, nh, vi.table, u64(vi.cap), vi.rep, x, None, i32(0),
+             regions, u64(R), ev_count, flags, i32(g), i32(0), u64(b << 16))
+        offs = torch.empty(g + 1, dtype=torch.int64, device=dev)
+        elib("ng_seg_offsets", ev_count, g, offs)
+        offs += at
+        elib("ng_seg_gather", regions, None, u64(R), None, ev_count, g, offs, ev, None)
+        at = offs[g : g + 1].clone()
+        del regions, ev_count
+    n_ev = int(at.item())
+    if int(flags[0].item()) & 4:
+        raise RuntimeError(f"levels {batch[0][0]}..{batch[-1][0]}: an emit region overflowed")
+    key = ("batch", batch[0][0])
+    c = count_events(elib, lib, ev, n_ev, n_ids, _RATIO.get(key, 1.0), presort="ctx")
+    del ev
+    _RATIO[key] = c.U / max(1, n_ev)
+    if not c.cb:
+        raise RuntimeError(f"levels {batch[0][0]}..{batch[-1][0]}: more large counts than the escape table holds")
+    sm = summarize(elib, lib, c, n_ids, 1)
+    fpos = torch.cat([f for _, f, _ in batch]).long()
+    ctx_of = torch.cat([torch.where(vi.ctx_of >= 0, vi.ctx_of + b, -1) for (_, _, vi), b in zip(batch, bases)])
+    m = fpos.numel()
+    o_tok = torch.zeros(m, dtype=torch.int16, device=dev)
+    o_cnt = torch.zeros(m, dtype=torch.int32, device=dev)
+    o_tot = torch.empty(m, dtype=torch.int32, device=dev)
+    o_dist = torch.empty(m, dtype=torch.int32, device=dev)
+    o_tc = torch.empty(m, dtype=torch.int32, device=dev)
+    elib("ng_pos_summary", ctx_of, m, 0, n_ids, None, sm.rec, sm.dist, None, None, i32(1), i32(1), i32(0), o_tot, o_dist,
+         o_tc, o_tok, o_cnt, None)
+    nxt[fpos] = o_tok
+    cnt[fpos] = o_cnt
 
 
 def _top1_unpacked(elib: Lib, lib: Lib, vi, c, x, o_tok, o_cnt) -> None:
