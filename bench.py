@@ -49,9 +49,10 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--query-tokens", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other configurations' measurements")
-    ap.add_argument("--only", default="", choices=("", "c2", "c4", "c5", "copy"),
+    ap.add_argument("--only", default="", choices=("", "c2", "c4", "c5", "copy", "load"),
                     help="measure only this secondary configuration and print its JSON (for profiling); copy: three "
-                         "plain 1 GiB device copies, the calibration of rocprofv3's FETCH_SIZE / WRITE_SIZE")
+                         "plain 1 GiB device copies, the calibration of rocprofv3's FETCH_SIZE / WRITE_SIZE; load: "
+                         "c3 from shard files (the threaded loader, and the build overlapped with the copies)")
     ap.add_argument("--mode", default="part", choices=("engine", "part", "record", "partitioned"),
                     help="CountBuild.mode")
     ap.add_argument("--cpu-tokens", type=int, default=100_000_000, help="CPU baseline: corpus prefix")
@@ -259,6 +260,74 @@ def bench_c4(with_cpu: bool) -> dict:
     return res
 
 
+def bench_load(cfg, tok, sizes, starts, q, steps: int) -> dict:
+    """The host data path at c3: the shards written as shard files to tmpfs (untimed), then (1) the threaded loader
+    (preadv into pinned staging buffers, per-thread copy streams) into a fresh token buffer, checked against the
+    resident one; (2) CountBuild from the files (read into pinned host memory before the clock), each step
+    start_load() + counts(): every shard's copy enqueued, each level's scan of a shard waiting for that shard's copy,
+    against the same build over already resident tokens."""
+    import shutil
+    import tempfile
+
+    import numpy as np
+    import torch
+
+    from ngram_amd import data
+    from ngram_amd.counts import CountBuild, device_queries
+    from ngram_amd.loader import Loader
+
+    need = 2 * sum(sizes) * 1.2
+    shm = Path("/dev/shm")
+    root = shm if shm.is_dir() and shutil.disk_usage(shm).free > need else None
+    d = Path(tempfile.mkdtemp(prefix="ngram_load_", dir=root))
+    try:
+        paths = []
+        for i, (st, n) in enumerate(zip(starts, sizes)):
+            p = d / f"train_{i:06d}.bin"
+            data.write_shard(p, tok[st : st + n].cpu().numpy().view(np.uint16))
+            paths.append(str(p))
+        threads = min(16, len(os.sched_getaffinity(0)))
+        res: dict = {"shards": len(paths), "bytes": 2 * sum(sizes), "threads": threads, "files": str(root or "tmp")}
+        loads = []
+        for _ in range(2):
+            ld = Loader(paths, tok.numel(), starts, sizes, threads, chunk_tokens=8 << 20, start=False)
+            ld.preallocate()
+            torch.cuda.synchronize()
+            ld.start()
+            ld.join()
+            assert torch.equal(ld.tok, tok), "the loaded buffer differs from the resident one"
+            loads.append(ld.stats["seconds"])
+            del ld
+        res["loader_s"] = min(loads)
+        res["loader_GBps"] = res["bytes"] / min(loads) / 1e9
+        cb = CountBuild(paths, levels=cfg.levels, level_shards={}, topk=cfg.topk)
+        x, tgt, avail = device_queries(q, cb.lib)
+        cb.start_load(1)
+        want = cb.counts(x, tgt, avail, stats=True).clone()  # the levels' densities, as the headline's first build
+        resident, overlapped, load_ms = [], [], []
+        for _ in range(steps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out = cb.counts(x, tgt, avail)
+            torch.cuda.synchronize()
+            resident.append(time.perf_counter() - t0)
+            cb.tok.fill_(-1)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            cb.start_load(1)
+            out = cb.counts(x, tgt, avail)
+            torch.cuda.synchronize()
+            overlapped.append(time.perf_counter() - t0)
+            load_ms.append(cb.load_ms())
+            assert torch.equal(out, want), "the build over loaded shards differs"
+        res.update(resident_ms=1e3 * min(resident), with_load_ms=1e3 * min(overlapped),
+                   copies_ms=min(load_ms), copies_GBps=res["bytes"] / (min(load_ms) / 1e3) / 1e9,
+                   tokens_per_s_with_load=sum(sizes) / min(overlapped))
+        return res
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+
+
 def cpu_baseline(flat, bounds, q, levels, n_tokens: int, n_queries: int) -> dict:
     """The oracle's query-filtered counting (C++ restatement of kgram.rs, one thread per core) over a bounded sample:
     the corpus' first n_tokens tokens and the first n_queries query positions, every level."""
@@ -308,6 +377,10 @@ def main() -> None:
     cfg, flat, bounds, tok, sizes, starts, q, np = make_workload(args.config, args.train_tokens, args.query_tokens)
     if args.only == "c5":
         print(json.dumps({"config": "c5", **bench_c5(tok, flat, args.steps, args.warmup, not args.no_cpu)}))
+        return
+    if args.only == "load":
+        del flat
+        print(json.dumps({"config": "c3 load", **bench_load(cfg, tok, sizes, starts, q, args.steps)}))
         return
     T = sum(sizes)
     flat_host = flat[: min(args.cpu_tokens, int(flat.numel()))].cpu()

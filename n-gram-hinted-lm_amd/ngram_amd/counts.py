@@ -202,6 +202,8 @@ class CountBuild:
         self.pending.reverse()
         self.per_step = -(-len(self.pending) // max(1, steps))
         self.events = []
+        self.load_start = torch.cuda.Event(enable_timing=True)
+        self.load_start.record(self.stream)
         self.pace()
 
     def pace(self) -> None:
@@ -211,9 +213,17 @@ class CountBuild:
                 at, a, lo, hi, last = self.pending.pop()
                 self.tok[at : at + hi - lo].copy_(a[lo:hi], non_blocking=True)
                 if last:
-                    ev = torch.cuda.Event()
+                    ev = torch.cuda.Event(enable_timing=True)
                     ev.record(self.stream)
                     self.events.append(ev)
+
+    def load_ms(self) -> float:
+        """The copies' time on the device from start_load to the last shard's copy, once all are enqueued
+        (build.py:257-259)."""
+        if self.pending or not self.events or getattr(self, "load_start", None) is None:
+            raise ValueError("the loads have not all been enqueued")
+        self.events[-1].synchronize()
+        return self.load_start.elapsed_time(self.events[-1])
 
     def _event(self, name: str, k: int, i: int, n: int):
         """A pair of timing events around a launch (recorded on the current stream), kept in kernel_events."""

@@ -19,6 +19,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import threading
 import time
 from pathlib import Path
 
@@ -27,6 +28,7 @@ import torch
 
 from .data import BOS, HEADER_BYTES, shard_tokens
 from .lib import Lib, i32, u64
+from .loader import Loader
 
 ALL_LEVELS = (2, 3, 4, 5, 6, 8, 10, 12, 16, 20)
 LEVELS = (2, 3, 4, 5, 6, 10, 20)  # the hint rows' levels and length buckets
@@ -254,9 +256,10 @@ def parse_args(argv: list[str] | None = None) -> argparse.Namespace:
 def build_stats(lib: Lib, tok: torch.Tensor, L: int, starts: list[int], sizes: list[int], x: torch.Tensor,
                 tgt: torch.Tensor, avail: torch.Tensor, *, levels=ALL_LEVELS, variants=VARIANTS, direct=False,
                 fused=False, words_density=0.0, chunk_positions=0, sub_slots=SUB_SLOTS, max_pbits: int | None = None,
-                grid: int | None = None, min_cap: int = 1 << 20) -> dict:
+                grid: int | None = None, min_cap: int = 1 << 20, loader=None) -> dict:
     """The whole build on one GPU from resident tokens and queries (the body of _run :784-1152 with world 1).
-    Returns {"counts", "rows", "levels", "timing"}."""
+    `loader`: a started Loader still copying the shards into `tok`: the query index is built meanwhile, and each
+    shard's first scan waits for that shard's copy only (:877, :959). Returns {"counts", "rows", "levels", "timing"}."""
     N = x.numel()
     n_tokens = sum(sizes)
     clock = Clock()
@@ -288,7 +291,9 @@ def build_stats(lib: Lib, tok: torch.Tensor, L: int, starts: list[int], sizes: l
                                torch.zeros(2, dtype=torch.int32, device=tok.device))
         bms = [bm_next, torch.zeros(nwords, dtype=torch.int32, device=tok.device)]
         bms[0].zero_()
-        for st, n in zip(starts, sizes):
+        for i, (st, n) in enumerate(zip(starts, sizes)):
+            if loader is not None:
+                torch.cuda.current_stream().wait_event(loader.wait(i))
             n32 = (n + 31) // 32 * 32
             for li, k in enumerate(levels):
                 vi = index[k]
@@ -342,7 +347,9 @@ def build_stats(lib: Lib, tok: torch.Tensor, L: int, starts: list[int], sizes: l
                     ranges = [(0, L)]
                 scanner = Scanner(lib, k, vi, x, tok, bm_prev, bm_next, table, grid, partitioned, sparse, chunk, pbits)
                 scanner.words = active * words_density < L if words_density > 0 else False
-                for st, n in ranges:
+                for i, (st, n) in enumerate(ranges):
+                    if first and loader is not None:
+                        torch.cuda.current_stream().wait_event(loader.wait(i))
                     for a in range(0, n, chunk):
                         scanner.scan(st + a, min(n, a + chunk) - a)
                 scanner.flush()
@@ -448,14 +455,19 @@ def run(args: argparse.Namespace) -> dict:
     torch.cuda.set_device(0)
     lib = Lib()
     paths = [p for p in Path(args.shards).read_text().split() if p]
-    tok, sizes, starts, L = load_shards(paths)
+    sizes = [shard_tokens(p) for p in paths]
+    starts, L = layout(sizes)
+    loader = Loader(paths, L, starts, sizes, args.threads, args.load_mode, args.chunk_mb << 19, args.numa)
     n_val = shard_tokens(args.val)
     val = np.fromfile(args.val, dtype="<u2", count=min(n_val, args.val_tokens + 1), offset=HEADER_BYTES)
     x, tgt, avail = query_tensors(val, args.val_tokens)
-    res = build_stats(lib, tok, L, starts, sizes, x, tgt, avail, direct=args.direct, fused=args.fused,
-                      words_density=args.words_density, chunk_positions=args.chunk_positions)
+    res = build_stats(lib, loader.tok, L, starts, sizes, x, tgt, avail, direct=args.direct, fused=args.fused,
+                      words_density=args.words_density, chunk_positions=args.chunk_positions, loader=loader)
+    loader.join()
     torch.cuda.synchronize()
     res["timing"]["total_s"] = time.time() - t0
+    res["timing"]["load"] = {"seconds": loader.stats["seconds"], "bytes": loader.stats["bytes"],
+                             "threads": args.threads}
     out = Path(args.out)
     if not args.no_save:
         out.mkdir(parents=True, exist_ok=True)
@@ -477,9 +489,17 @@ def main() -> None:
 
 
 class InProcess:
-    """The build inside a process that holds the GPU (InProcess of :1235-1316), one GPU: construct (the shards'
-    layout, the GPU token buffer, the library), prepare() (no collectives on one GPU), start_load() (the shards'
-    copies), finish() -> {"counts": int32 [3, len(ALL_LEVELS), N], "rows": int32 [len(variants), N, 9], "timing"}.
+    """The build inside a process that holds the GPU (InProcess of :1235-1316), one GPU:
+      - construct (before the clock): the shards' layout, the GPU token buffer and the loader's pinned staging buffers
+        allocated, the library loaded;
+      - prepare() (before the clock): nothing to connect on one GPU;
+      - start_load() (optional, on the clock): the shard loads start in background threads while the caller runs;
+      - start_background() (optional, instead of start_load): the loads and the whole build on a background thread
+        and a HIP stream of their own (one GPU has no collectives, so nothing has to wait for finish());
+      - finish(): waits for the loads (starting them if nothing did), builds the query index while the last shards
+        land, scans each shard once its copy is done, then the merges and rows -> {"counts": int32
+        [3, len(ALL_LEVELS), N] (tot, dist, cnt; tot and cnt as uint32 bits), "rows": int32 [len(variants), N, 9],
+        "timing"}.
     `variants`: the hint rows' level sets (each of LEVELS)."""
 
     def __init__(self, shard_paths: list[str], val_path: str, variants=(LEVELS,), threads: int = 12, chunk_mb: int = 16,
@@ -492,28 +512,63 @@ class InProcess:
         self.paths = list(shard_paths)
         self.sizes = [shard_tokens(p) for p in self.paths]
         self.starts, self.L = layout(self.sizes)
+        self.device = torch.cuda.current_device()
+        self.loader = Loader(self.paths, self.L, self.starts, self.sizes, threads, "pread", chunk_mb << 19, start=False)
+        self.loader.preallocate()
         self.lib = Lib()
-        self.loaded = None
+        self.thread, self.error, self.result = None, None, None
 
     def prepare(self) -> None:
         torch.cuda.synchronize()
 
     def start_load(self) -> None:
-        if self.loaded is None:
-            self.loaded = load_shards(self.paths)
+        if not self.loader.started:
+            self.loader.start()
 
-    def finish(self) -> dict:
-        t0 = time.time()
+    def start_background(self) -> None:
+        """The loads and the build from now, on a background thread and stream; finish() returns its result."""
+        if self.thread is not None:
+            raise ValueError("the build has already started")
         self.start_load()
-        tok, sizes, starts, L = self.loaded
+        stream = torch.cuda.Stream(device=self.device)
+
+        def work() -> None:
+            try:
+                torch.cuda.set_device(self.device)
+                with torch.cuda.stream(stream):
+                    self.result = self._build()
+                stream.synchronize()
+            except BaseException as e:  # noqa: BLE001 - raised again by finish()
+                self.error = e
+
+        self.thread = threading.Thread(target=work, daemon=True)
+        self.thread.start()
+
+    def _build(self) -> dict:
+        t0 = time.time()
         n_val = shard_tokens(self.args.val)
         val = np.fromfile(self.args.val, dtype="<u2", count=min(n_val, self.args.val_tokens + 1), offset=HEADER_BYTES)
         x, tgt, avail = query_tensors(val, self.args.val_tokens)
-        res = build_stats(self.lib, tok, L, starts, sizes, x, tgt, avail, variants=self.variants,
-                          direct=self.args.direct, fused=self.args.fused, words_density=self.args.words_density,
-                          chunk_positions=self.args.chunk_positions)
+        res = build_stats(self.lib, self.loader.tok, self.L, self.starts, self.sizes, x, tgt, avail,
+                          variants=self.variants, direct=self.args.direct, fused=self.args.fused,
+                          words_density=self.args.words_density, chunk_positions=self.args.chunk_positions,
+                          loader=self.loader)
+        self.loader.join()
         res["timing"]["total_s"] = time.time() - t0
+        res["timing"]["load"] = {"seconds": self.loader.stats["seconds"], "bytes": self.loader.stats["bytes"]}
         return {"counts": res["counts"], "rows": res["rows"], "timing": res["timing"]}
+
+    def finish(self) -> dict:
+        if self.thread is None:
+            self.start_load()
+            return self._build()
+        t0 = time.time()
+        self.thread.join()
+        self.waited = time.time() - t0
+        if self.error is not None:
+            raise self.error
+        torch.cuda.current_stream().synchronize()
+        return self.result
 
 
 if __name__ == "__main__":

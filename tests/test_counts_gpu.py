@@ -74,8 +74,11 @@ def test_counts_match_oracle(corpus, level_shards, mode, monkeypatch):
         if mode == "part-compact":
             monkeypatch.setattr(C, "LIST_DENSITY", 0.0)
     cb.start_load(3)
+    with pytest.raises(ValueError):
+        cb.load_ms()  # a share of the copies is still pending
     cb.pace()
     cb.pace()
+    assert cb.load_ms() > 0
     x, tgt, avail = C.queries(corpus.query, [], "cuda", lib)
     out = cb.counts(x, tgt, avail, stats=True).cpu().numpy()
     ref = _reference(corpus, LEVELS, level_shards)

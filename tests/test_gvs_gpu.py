@@ -73,3 +73,52 @@ def test_overflow_reruns_with_a_bigger_table(lib, corpus, reference):
         G.LOAD = old
     assert res["levels"][2]["reruns"] > 0
     _check(res, reference, (2, 3), ((2, 3),))
+
+
+def test_loader_matches_load_shards(corpus, tmp_path):
+    """Threaded pread into pinned staging buffers: chunks far smaller than a shard (each thread's two buffers reused
+    many times), more threads than some shards get, and an empty shard; the buffer equals the synchronous layout."""
+    from ngram_amd.loader import Loader
+
+    shards = corpus.shards() + [np.zeros(0, np.uint16)]
+    paths = []
+    for i, s in enumerate(shards):
+        p = tmp_path / f"s{i}.bin"
+        data.write_shard(p, s)
+        paths.append(str(p))
+    want, sizes, starts, L = G.load_shards(shards)
+    for threads, chunk in ((1, 70_001), (2, 4096), (5, 1 << 20)):
+        ld = Loader(paths, L, starts, sizes, threads, chunk_tokens=chunk)
+        got = ld.tok
+        ld.wait_all()
+        assert torch.equal(got, want), (threads, chunk)
+        ld.join()
+        assert ld.stats["seconds"] >= 0 and ld.stats["bytes"] == 2 * sum(sizes)
+    with pytest.raises(ValueError):
+        Loader(paths, L, starts, sizes, 2, mode="register")
+    ld = Loader(paths, L, starts, sizes, 2, start=False)
+    with pytest.raises(ValueError):
+        ld.wait(0)  # not started
+    with pytest.raises(ValueError):
+        ld.start(stream_priority=-1)
+    ld = Loader([str(tmp_path / "missing.bin")], L, starts[:1], sizes[:1], 1)
+    with pytest.raises(FileNotFoundError):
+        ld.wait(0)
+
+
+@pytest.mark.parametrize("background", [False, True])
+def test_in_process_loads_and_builds(corpus, reference, tmp_path, background):
+    """InProcess: the shards loaded by the threaded loader while the query index is built, each shard scanned once
+    its copy lands (fused and per-level), on the caller's thread or a background one; outputs equal the oracle's."""
+    paths, val_path = corpus.write(tmp_path)
+    n = len(corpus.query) - 1
+    flags = ("--fused", "--direct") if background else ("--direct",)
+    ip = G.InProcess(paths, val_path, variants=G.VARIANTS, threads=3, chunk_mb=1, flags=flags, val_tokens=n)
+    ip.prepare()
+    if background:
+        ip.start_background()
+    else:
+        ip.start_load()
+    res = ip.finish()
+    _check(res, reference, G.ALL_LEVELS, G.VARIANTS)
+    assert res["timing"]["load"]["bytes"] == 2 * len(corpus.train)
