@@ -254,6 +254,14 @@ int ng_online_rows(const int* pos, ng_i64 m, int nlv, const ng_i64* desc, int E,
  * indices [n, L] */
 int ng_features(const int* counts, int L, ng_i64 n, int nb, float* tot, float* dist, float* cnt, ng_i64* bin,
                 ng_i64* sparse, void* stream);
+/* The hint directory's reader (old_records/hint_runtime.py Hints._upload :171-199, _upload_counts :201-217): a
+ * batch's rows staged back to back (cell int16, tokens uint16, weights uint16) widened to int64 cell, int64 tokens and
+ * float32 weights (u16 * float32(1 / 65535)); count rows tot (u32), dist (u16), cnt (u32) [n, L] to float32
+ * [n, 3, L]. */
+int ng_hint_widen(const short* staged, ng_i64 n_cell, ng_i64 n_tok, ng_i64 n_w, ng_i64* cell, ng_i64* tokens,
+                  float* weights, void* stream);
+int ng_count_rows(const uint32_t* tot, const uint16_t* dist, const uint32_t* cnt, ng_i64 n, int L, float* out,
+                  void* stream);
 
 #ifdef __cplusplus
 }
