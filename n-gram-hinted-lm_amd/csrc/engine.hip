@@ -158,8 +158,13 @@ __global__ void __launch_bounds__(256) scan_dense_k(const u16* __restrict__ tok,
         const i64 w = (base >> 5) + (lane >> 5);
         u32 word = 0xFFFFFFFFu;
         if (bm_in) word = w < nwords ? bm_in[w] : 0u;
+        // the tokens are loaded whatever the bitmap says, together with its word: one round trip for both
+        u32 nxt = SENT;
+        u64 ck = EMPTY;
+        if (p < L) ck = ctx_key_at<K>(tok, p, k, nxt);
         u64 key = EMPTY;
-        if (p < L && ((word >> (lane & 31)) & 1u)) key = probe_key<K>(tok, p, k, vt, vcap, vrep, x, flags);
+        if (((word >> (lane & 31)) & 1u) && nxt != SENT && ck != EMPTY)
+            key = probe_table<K>(tok, p, k, vt, vcap, vrep, x, flags, ck, nxt);
         const bool hit = key != EMPTY;
         const u64 b = __ballot(hit);
         if (lane == 0) bm_out[base >> 5] = (u32)b;

@@ -97,6 +97,35 @@ __device__ __forceinline__ u64 ctx_key_stop(const u16* e, int k) {
     return key_finish(h);
 }
 
+// Position p's next token (nxt = tok[p]) and k-context key (tok[p - k .. p - 1]) as ctx_key_stop's, with all k + 1
+// tokens loaded together (no load waits for another token's value): EMPTY where any of the k is SENT. A token before
+// the buffer's start (p - j < 0) reads as SENT, which is what ctx_key_stop meets there too (the buffer starts with
+// SENT, or the token before it is one); nothing before the buffer is read.
+template <int K>
+__device__ __forceinline__ u64 ctx_key_at(const u16* __restrict__ tok, i64 p, int k, u32& nxt) {
+    if constexpr (K > 0) {
+        u32 t[K + 1];
+#pragma unroll
+        for (int j = 0; j <= K; ++j) t[j] = p - j >= 0 ? (u32)tok[p - j] : SENT;
+        nxt = t[0];
+        u64 h = 0, bp = 1;
+        bool gap = false;
+#pragma unroll
+        for (int j = 1; j <= K; ++j) {
+            gap |= t[j] == SENT;
+            if (K <= 4) h |= (u64)t[j] << (16 * (j - 1));
+            else {
+                h += tok_code(t[j]) * bp;
+                bp *= POLY_BASE;
+            }
+        }
+        return gap ? EMPTY : key_finish(h);
+    } else {
+        nxt = tok[p];
+        return p >= k ? ctx_key_stop<0>(tok + p, k) : EMPTY;
+    }
+}
+
 // Launch helpers
 static inline int grid_for(i64 n, int block) {
     i64 g = (n + block - 1) / block;

@@ -86,16 +86,13 @@ __device__ __forceinline__ u32 slot_count(const u32* wraps, u64 s, u64 v) {
     return (u32)(v >> KB) + (((wraps[s >> 2] >> (8 * (s & 3))) & 0xFFu) << (64 - KB)) - COUNT_OFF(KB);
 }
 
-// Position p's k-context looked up in the query table and, for hashed keys, verified against the context's
-// representative query position: (context id << 16 | next) or EMPTY. The table (canonical linear probing without
-// wrap-around) ends with an empty slot. A false hash hit is counted in flags[1].
+// The query-table walk of position p's valid key (its next token nxt not SENT): (context id << 16 | nxt) or EMPTY;
+// for hashed keys the hit is verified against the context's representative query position (a false hash hit is
+// counted in flags[1]). The table (canonical linear probing without wrap-around) ends with an empty slot.
 template <int K>
-__device__ __forceinline__ u64 probe_key(const u16* __restrict__ tok, i64 p, int k, const u64* __restrict__ vt, u64 vcap,
-                                         const u32* __restrict__ vrep, const u16* __restrict__ x, u32* flags) {
-    const u32 nxt = tok[p];
-    if (nxt == SENT) return EMPTY;
-    const u64 key = ctx_key_stop<K>(tok + p, k);
-    if (key == EMPTY) return EMPTY;
+__device__ __forceinline__ u64 probe_table(const u16* __restrict__ tok, i64 p, int k, const u64* __restrict__ vt,
+                                           u64 vcap, const u32* __restrict__ vrep, const u16* __restrict__ x,
+                                           u32* flags, u64 key, u32 nxt) {
     u64 s = __umul64hi(key, vcap);
     while (true) {
         const u64 v = vt[s];
@@ -118,16 +115,25 @@ __device__ __forceinline__ u64 probe_key(const u16* __restrict__ tok, i64 p, int
     }
 }
 
+// Position p's k-context looked up in the query table: (context id << 16 | next) or EMPTY (no context, a gap token,
+// or not a query context). Its k + 1 tokens are loaded together (ctx_key_at).
+template <int K>
+__device__ __forceinline__ u64 probe_key(const u16* __restrict__ tok, i64 p, int k, const u64* __restrict__ vt, u64 vcap,
+                                         const u32* __restrict__ vrep, const u16* __restrict__ x, u32* flags) {
+    u32 nxt;
+    const u64 key = ctx_key_at<K>(tok, p, k, nxt);
+    if (nxt == SENT || key == EMPTY) return EMPTY;
+    return probe_table<K>(tok, p, k, vt, vcap, vrep, x, flags, key, nxt);
+}
+
 // A probe in two halves, so that several positions' first loads are in flight together: probe_start computes the
 // position's context key (EMPTY: none, or its next token is a gap) and loads its home slot; probe_finish walks on from
 // there exactly as probe_key does.
 template <int K>
 __device__ __forceinline__ void probe_start(const u16* __restrict__ tok, i64 p, int k, const u64* __restrict__ vt,
                                             u64 vcap, u64& key, u64& s, u64& v, u32& nxt) {
-    key = EMPTY;
-    nxt = tok[p];
-    if (nxt == SENT) return;
-    key = ctx_key_stop<K>(tok + p, k);
+    key = ctx_key_at<K>(tok, p, k, nxt);
+    if (nxt == SENT) key = EMPTY;
     if (key == EMPTY) return;
     s = __umul64hi(key, vcap);
     v = vt[s];

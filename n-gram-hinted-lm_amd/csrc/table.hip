@@ -21,15 +21,13 @@ __global__ void __launch_bounds__(256) table_emit_k(const u16* __restrict__ tok,
                                                     u64* __restrict__ ev, u32* flags) {
     for (i64 p = blockIdx.x * (i64)blockDim.x + threadIdx.x; p < L; p += (i64)gridDim.x * blockDim.x) {
         if (*(volatile u32*)&flags[0]) return;  // the context table overflowed: the level reruns bigger
-        const u32 nxt = tok[p];
+        u32 nxt;
+        const u64 key = ctx_key_at<K>(tok, p, k, nxt);  // the k + 1 tokens loaded together
         u64 e = EMPTY;
-        if (nxt != SENT) {
-            const u64 key = ctx_key_stop<K>(tok + p, k);
-            if (key != EMPTY) {
-                const i64 s = ctx_find_insert(ck, ccap, key, flags);
-                if (s < 0) return;
-                e = mix64(((u64)s << 16) | nxt);
-            }
+        if (nxt != SENT && key != EMPTY) {
+            const i64 s = ctx_find_insert(ck, ccap, key, flags);
+            if (s < 0) return;
+            e = mix64(((u64)s << 16) | nxt);
         }
         ev[p] = e;
     }
