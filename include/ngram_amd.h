@@ -125,20 +125,29 @@ int ng_scan_emit_list(const uint16_t* tok, const ng_u64* plist, const ng_u64* n_
                       uint32_t* ev_count, uint32_t* flags, int grid, uint32_t* dhist, ng_i64 dstride, void* stream);
 /* a level scan with optional outputs over a bitmap-gated range (plist NULL: [0, L) gated by bm_in in ng_scan_count's
  * sparse modes, hit bitmap into bm_out) or over listed positions (plist: n corpus positions); hit (may be NULL):
- * hit[context id] = 1 per hit; ev (may be NULL): block b of grid appends per hit mix64(pair key + key_add) (what 0) or its
+ * bit (context id) of the u32 words hit set per hit; ev (may be NULL): block b of grid appends per hit mix64(pair key + key_add) (what 0) or its
  * position (what 1) to ev[b * region ...], how many into ev_count[b]; region >= ng_emit_region(L, grid) over a
  * bitmap, >= ceil(n / (grid * 256)) * 256 over a list */
 int ng_scan_sink(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, uint32_t* bm_out, const ng_u64* plist,
-                 ng_i64 n, const ng_u64* vt, ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, unsigned char* hit,
+                 ng_i64 n, const ng_u64* vt, ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, uint32_t* hit,
                  int what, ng_u64* ev, ng_u64 region, uint32_t* ev_count, uint32_t* flags, int grid, int sparse,
                  ng_u64 key_add, void* stream);
 /* the set bits of a bitmap as positions in order (out), *total of them; two-phase temp storage (temp NULL: size) */
 int ng_bits_list(void* temp, size_t* temp_bytes, const uint32_t* bm, ng_i64 nwords, ng_u64* out, ng_u64* total,
                  void* stream);
-/* existence only: hit bitmap and hit[context id] = 1 (hit zeroed by the caller); sparse as ng_scan_count's */
+/* existence only: hit bitmap and bit (context id) of the u32 words hit set (hit zeroed by the caller); ids (may be
+ * NULL): ids[p] = the context id at each hit position p; sparse as ng_scan_count's */
 int ng_scan_exist(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, uint32_t* bm_out, const ng_u64* vt,
-                  ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, unsigned char* hit, uint32_t* flags, int grid,
-                  int sparse, void* stream);
+                  ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, uint32_t* hit, uint32_t* ids, uint32_t* flags,
+                  int grid, int sparse, void* stream);
+/* a level's counting scan from ng_scan_exist's ids: each position set in bm whose context's bit is set in `final`
+ * emits mix64(id << 16 | tok[p]) as ng_scan_emit's events (regions, ev_count, dhist); L a multiple of 32, tok
+ * 8-byte and ids 16-byte aligned */
+int ng_scan_ids_emit(const uint16_t* tok, ng_i64 L, const uint32_t* bm, const uint32_t* ids, const uint32_t* final,
+                     ng_u64* ev, ng_u64 region, uint32_t* ev_count, uint32_t* flags, int grid, uint32_t* dhist,
+                     ng_i64 dstride, void* stream);
+/* bit ids[i] of the u32 words bits set for each ids[i] >= 0 (bits zeroed by the caller) */
+int ng_mark_bits(const int* ids, ng_i64 n, uint32_t* bits, void* stream);
 /* a split table's occupied slots appended to (out_k, out_c) from *counter (zeroed by the caller) */
 int ng_table_compact(const ng_u64* keys, const uint32_t* cnts, ng_u64 cap, ng_u64* out_k, uint32_t* out_c,
                      ng_u64* counter, void* stream);

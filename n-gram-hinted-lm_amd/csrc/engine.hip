@@ -39,7 +39,7 @@ __device__ __forceinline__ void split_add(u64* keys, u32* cnts, u64 cap, u64 key
 // What a level scan does with each hit besides setting its bitmap bit (probe_key's pair key: context id << 16 | next):
 //   CountSink: count it in the split table (once the table has overflowed, only the bitmap is still made: the level
 //              reruns bigger);
-//   ExistSink: flag its context (hit[id] = 1, plain byte stores: every writer stores the same value);
+//   ExistSink: flag its context (bit id of the u32 words hit, set by atomicOr only while it reads unset);
 //   EmitSink:  append mix64(pair key) (what 0) or the corpus position (what 1) to the block's own region
 //              ev[b * region, (b + 1) * region), at a block-local cursor in LDS (one LDS atomic per wave and round),
 //              and store the block's count in ev_count[b] at the end; with `hit`, also flag the context. No global
@@ -54,7 +54,8 @@ struct CountSink {
 };
 struct ExistSink {
     static constexpr int KIND = 1;
-    unsigned char* hit;
+    u32* hit;
+    u32* ids;  // may be NULL: ids[p] = the context id of each hit position p (other positions left as they are)
 };
 struct EmitSink {
     static constexpr int KIND = 2;
@@ -62,7 +63,7 @@ struct EmitSink {
     u64 region;
     u32* ev_count;
     int what;
-    unsigned char* hit;
+    u32* hit;
     u32* dhist;   // with what 0 (may be NULL): the block's events per top-8-bit digit, at dhist[digit * dstride + block]
     i64 dstride;
     u64 key_add;  // added to each pair key before it is mixed (a context-id offset: several levels' ids in one space)
@@ -74,19 +75,21 @@ struct SinkShared {
     u32 dh[256];
 };
 
-// A context's hit flag, written only while unset: a hot context's flag is then read from cache rather than written
-// again by every hit.
-__device__ __forceinline__ void set_hit(unsigned char* hit, u64 c) {
-    if (hit[c] == 0) hit[c] = 1;
+// A context's hit flag (bit c of the words hit), set only while it reads unset: a hot context's flag is then read
+// from cache rather than set again by every hit, and the bits (an eighth of a byte array) mostly stay in L2.
+__device__ __forceinline__ void set_hit(u32* hit, u64 c) {
+    const u32 m = 1u << (c & 31);
+    if (!(hit[c >> 5] & m)) atomicOr(&hit[c >> 5], m);
 }
 
 // A lane's hit (count and exist sinks; the emit sink uses emit_wave / emit_lane).
 template <class S>
-__device__ __forceinline__ void sink_hit(const S& s, u64 key, bool full, u32* flags) {
+__device__ __forceinline__ void sink_hit(const S& s, u64 key, i64 p, bool full, u32* flags) {
     if constexpr (S::KIND == 0) {
         if (!full) split_add(s.keys, s.cnts, s.cap, key, 1u, flags);
     } else if constexpr (S::KIND == 1) {
         set_hit(s.hit, key >> 16);
+        if (s.ids) s.ids[p] = (u32)(key >> 16);
     }
 }
 
@@ -170,7 +173,7 @@ __global__ void __launch_bounds__(256) scan_dense_k(const u16* __restrict__ tok,
         if (lane == 0) bm_out[base >> 5] = (u32)b;
         if (lane == 32 && w < nwords) bm_out[w] = (u32)(b >> 32);
         if constexpr (S::KIND == 2) emit_wave(sink, &ss, b, hit, key, p, flags);
-        else if (hit) sink_hit(sink, key, full, flags);
+        else if (hit) sink_hit(sink, key, p, full, flags);
     }
     sink_end(sink, &ss);
 }
@@ -198,7 +201,7 @@ __global__ void __launch_bounds__(256) scan_list_k(const u16* __restrict__ tok, 
         const bool hit = key != EMPTY;
         if (bm_out && hit) atomicOr(&bm_out[p >> 5], 1u << (p & 31));
         if constexpr (S::KIND == 2) emit_wave(sink, &ss, __ballot(hit), hit, key, p, flags);
-        else if (hit) sink_hit(sink, key, full, flags);
+        else if (hit) sink_hit(sink, key, p, full, flags);
     }
     sink_end(sink, &ss);
 }
@@ -224,7 +227,7 @@ __global__ void __launch_bounds__(256) scan_sparse_k(const u16* __restrict__ tok
             if (key != EMPTY) {
                 out |= 1u << b;
                 if constexpr (S::KIND == 2) emit_lane(sink, &ss, key, p, flags);
-                else sink_hit(sink, key, full, flags);
+                else sink_hit(sink, key, p, full, flags);
             }
         }
         bm_out[w] = out;
@@ -292,7 +295,7 @@ __global__ void __launch_bounds__(256) scan_compact_k(const u16* __restrict__ to
                 if (hit) atomicOr(&words[w][lp[q] >> 5], 1u << (lp[q] & 31));
                 if constexpr (S::KIND == 2)
                     emit_wave(sink, &ss, __ballot(hit), hit, hk, pbase + lp[q], flags);
-                else if (hit) sink_hit(sink, hk, full, flags);
+                else if (hit) sink_hit(sink, hk, pbase + lp[q], full, flags);
             }
         }
         if (wi < nwords) bm_out[wi] = words[w][lane];
@@ -571,13 +574,93 @@ extern "C" int ng_scan_count(const u16* tok, i64 L, int k, const u32* bm_in, u32
 }
 
 // One level's existence scan: bm_out = the corpus positions (gated by bm_in) whose k-context is a query context of the
-// table, hit[id] = 1 for each such context id (hit zeroed by the caller). sparse as ng_scan_count's.
+// table, bit id of the u32 words hit set for each such context id (hit zeroed by the caller). sparse as
+// ng_scan_count's.
 extern "C" int ng_scan_exist(const u16* tok, i64 L, int k, const u32* bm_in, u32* bm_out, const u64* vt, u64 vcap,
-                             const u32* vrep, const u16* x, unsigned char* hit, u32* flags, int grid, int sparse,
+                             const u32* vrep, const u16* x, u32* hit, u32* ids, u32* flags, int grid, int sparse,
                              void* stream) {
     if (L <= 0) return 0;
     if (grid <= 0) grid = grid_for(L, 256);
-    if (launch_scan(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, ExistSink{hit}, flags, grid, sparse, (hipStream_t)stream) != 0) return -1;
+    if (launch_scan(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, ExistSink{hit, ids}, flags, grid, sparse,
+                    (hipStream_t)stream) != 0)
+        return -1;
+    return (int)hipGetLastError();
+}
+
+namespace {
+// The counting scan of a level whose existence scan stored each hit position's context id (ids): per position p set
+// in bm, a context id whose bit is set in `final` emits mix64(id << 16 | tok[p]) as ng_scan_emit's events. A wave
+// takes 8 bitmap words (256 positions) per step, a lane 4 consecutive positions: their ids in one 16-byte load and
+// their tokens in one 8-byte load, the 4 final-bit loads together; a step whose words are all empty is skipped.
+__global__ void __launch_bounds__(256) scan_ids_k(const u16* __restrict__ tok, i64 L, const u32* __restrict__ bm,
+                                                  const u32* __restrict__ ids, const u32* __restrict__ final,
+                                                  EmitSink sink, u32* flags) {
+    __shared__ SinkShared ss;
+    sink_begin(sink, &ss);
+    const int lane = lane_id();
+    const i64 nwords = (L + 31) >> 5;
+    const i64 wave = (blockIdx.x * (i64)blockDim.x + threadIdx.x) / WAVE;
+    const i64 nwaves = (i64)gridDim.x * (blockDim.x / WAVE);
+    for (i64 w0 = wave * 8; w0 < nwords; w0 += nwaves * 8) {
+        const i64 wi = w0 + (lane & 7);
+        const u32 wd = (lane < 8 && wi < nwords) ? bm[wi] : 0u;
+        const u32 word = (u32)__shfl((int)wd, lane >> 3, WAVE);
+        const u32 bits = (word >> ((lane & 7) * 4)) & 0xFu;
+        if (__ballot(bits != 0u) == 0ull) continue;  // wave-uniform
+        const i64 p0 = (w0 << 5) + 4 * (i64)lane;
+        u32 id[4] = {0, 0, 0, 0};
+        u32 t[4] = {0, 0, 0, 0};
+        if (bits) {  // a set bit lies below L, and so does its whole 4-aligned group (L is a multiple of 32)
+            const uint4 iv = *(const uint4*)(ids + p0);
+            const ushort4 tv = *(const ushort4*)(tok + p0);
+            id[0] = iv.x, id[1] = iv.y, id[2] = iv.z, id[3] = iv.w;
+            t[0] = tv.x, t[1] = tv.y, t[2] = tv.z, t[3] = tv.w;
+        }
+        u32 fw[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) fw[i] = ((bits >> i) & 1u) ? final[id[i] >> 5] : 0u;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const bool hit = (fw[i] >> (id[i] & 31)) & 1u;
+            emit_wave(sink, &ss, __ballot(hit), hit, ((u64)id[i] << 16) | t[i], p0 + i, flags);
+        }
+    }
+    sink_end(sink, &ss);
+}
+
+__global__ void mark_bits_k(const int* __restrict__ ids, i64 n, u32* bits) {
+    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    if (i < n) {
+        const int c = ids[i];
+        if (c >= 0) atomicOr(&bits[c >> 5], 1u << (c & 31));
+    }
+}
+}  // namespace
+
+// A level's counting scan from the context ids its existence scan stored (ng_scan_exist's ids, valid at the
+// positions set in bm): the positions whose context's bit is set in `final` emit their events as ng_scan_emit's
+// (regions, ev_count, dhist; region >= ng_emit_region(L, grid)).
+extern "C" int ng_scan_ids_emit(const u16* tok, i64 L, const u32* bm, const u32* ids, const u32* final, u64* ev,
+                                u64 region, u32* ev_count, u32* flags, int grid, u32* dhist, i64 dstride,
+                                void* stream) {
+    if (grid <= 0 || region == 0 || region > 0xFFFFFFFFull || (dhist && dstride < grid)) return -1;
+    if ((L & 31) || ((uintptr_t)tok & 7) || ((uintptr_t)ids & 15)) return -1;  // the kernel's vector loads
+    hipStream_t st = (hipStream_t)stream;
+    if (L <= 0) {
+        fill_u32_n(ev_count, 0u, grid, st);
+        if (dhist)
+            for (int d = 0; d < 256; ++d) fill_u32_n(dhist + (i64)d * dstride, 0u, grid, st);
+        return (int)hipGetLastError();
+    }
+    const EmitSink sk{ev, region, ev_count, 0, nullptr, dhist, dstride, 0};
+    scan_ids_k<<<grid, 256, 0, st>>>(tok, L, bm, ids, final, sk, flags);
+    return (int)hipGetLastError();
+}
+
+// bits (u32 words, zeroed by the caller): bit ids[i] set for each ids[i] >= 0, i < n.
+extern "C" int ng_mark_bits(const int* ids, i64 n, u32* bits, void* stream) {
+    if (n < 0) return -1;
+    if (n > 0) mark_bits_k<<<grid_for(n, 256), 256, 0, (hipStream_t)stream>>>(ids, n, bits);
     return (int)hipGetLastError();
 }
 
@@ -624,11 +707,11 @@ extern "C" int ng_scan_emit_list(const u16* tok, const u64* plist, const u64* n_
 
 // A level scan with optional outputs, over a bitmap-gated range (plist NULL: positions [0, L) gated by bm_in as
 // ng_scan_count's `sparse` modes, hit bitmap into bm_out) or over listed positions (plist: n corpus positions, bm_*
-// unused). hit (may be NULL): hit[context id] = 1 per hit. ev (may be NULL): block b of `grid` appends per hit
+// unused). hit (may be NULL): bit (context id) of the u32 words hit set per hit. ev (may be NULL): block b of `grid` appends per hit
 // mix64(pair key + key_add) (what 0) or its position (what 1) to ev[b * region ...] and stores how many in
 // ev_count[b]; region >= ng_emit_region(L, grid) over a bitmap, >= ceil(n / (grid * 256)) * 256 over a list.
 extern "C" int ng_scan_sink(const u16* tok, i64 L, int k, const u32* bm_in, u32* bm_out, const u64* plist, i64 n,
-                            const u64* vt, u64 vcap, const u32* vrep, const u16* x, unsigned char* hit, int what,
+                            const u64* vt, u64 vcap, const u32* vrep, const u16* x, u32* hit, int what,
                             u64* ev, u64 region, u32* ev_count, u32* flags, int grid, int sparse, u64 key_add,
                             void* stream) {
     if (grid <= 0 || (what != 0 && what != 1)) return -1;
@@ -645,7 +728,7 @@ extern "C" int ng_scan_sink(const u16* tok, i64 L, int k, const u32* bm_in, u32*
                                                                              nullptr, nullptr)));
         } else {
             LEVEL_SWITCH(k, (scan_list_k<K, ExistSink><<<grid, 256, 0, st>>>(tok, plist, n, k, vt, vcap, vrep, x,
-                                                                              ExistSink{hit}, flags, nullptr, nullptr)));
+                                                                              ExistSink{hit, nullptr}, flags, nullptr, nullptr)));
         }
         return (int)hipGetLastError();
     }
@@ -653,7 +736,7 @@ extern "C" int ng_scan_sink(const u16* tok, i64 L, int k, const u32* bm_in, u32*
     int rc;
     if (ev) rc = launch_scan(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, EmitSink{ev, region, ev_count, what, hit, nullptr, 0, key_add},
                              flags, grid, sparse, st);
-    else rc = launch_scan(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, ExistSink{hit}, flags, grid, sparse, st);
+    else rc = launch_scan(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, ExistSink{hit, nullptr}, flags, grid, sparse, st);
     if (rc != 0) return -1;
     return (int)hipGetLastError();
 }

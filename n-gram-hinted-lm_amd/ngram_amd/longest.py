@@ -7,7 +7,7 @@ of that shard), that context's most frequent next token (count descending, then 
 
 Two phases, both on libngram_amd.so. Existence, k = 1, 2, ...: the query contexts of the positions still matching
 (a query index per level over the list of positions still matching), the corpus positions whose (k-1)-context
-matched (a hit bitmap per level) probed for their k-context (ng_scan_exist: a bitmap and a per-context hit flag, no
+matched (a hit bitmap per level) probed for their k-context (ng_scan_exist: a bitmap and a per-context hit bit, no
 counting), until no position matches. A match is monotone in k (kgram.rs:12-15), so each position's length is its
 last matching level. Then counting, only for each position's final context: per level, the final contexts' query
 index, the corpus positions of that level's bitmap probed and their (context, next) hits emitted, partitioned and
@@ -23,6 +23,7 @@ from __future__ import annotations
 
 import os
 import time
+from types import SimpleNamespace
 
 import numpy as np
 import torch
@@ -77,7 +78,7 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
         if act.numel() == 0:
             break
         vi = QueryIndex(elib, x, avail, k, act, compact=True)
-        hit = torch.zeros(vi.ids, dtype=torch.uint8, device=dev)
+        hit = torch.zeros((vi.ids + 31) // 32, dtype=torch.int32, device=dev)  # a bit per context id
         prev = levels[-1] if levels else None
         if prev is not None and (prev[0] == "list" or prev[2] * LIST_DIV < L):
             cand = prev[1] if prev[0] == "list" else _bits_list(elib, prev[1], prev[2])
@@ -85,12 +86,14 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
             levels.append(("list", hl, nh))
         else:
             bm = torch.empty(nwords, dtype=torch.int32, device=dev)
+            ids = torch.empty(L, dtype=torch.int32, device=dev)  # each hit position's context id, for the counting
             mode = 0 if prev is None or prev[2] * 2 > L else 2  # a lane per position while the gate is dense
             elib("ng_scan_exist", tok, L, i32(k), None if prev is None else prev[1], bm, vi.table, u64(vi.cap),
-                 vi.rep, x, hit, flags, i32(grid), i32(mode))
-            levels.append(("bm", bm, _popcount(lib, bm)))
+                 vi.rep, x, hit, ids, flags, i32(grid), i32(mode))
+            levels.append(("bm", bm, _popcount(lib, bm), ids, act, vi.ctx_of, vi.ids))
         ctx = vi.ctx_of.long()
-        act = act[(ctx >= 0) & (hit[ctx.clamp_min(0)] != 0)]
+        c = ctx.clamp_min(0)
+        act = act[(ctx >= 0) & (((hit[c >> 5] >> (c & 31)) & 1) != 0)]
         length[act.long()] = k
         ladder.append((k, int(elig[k]), int(act.numel())))
         del vi, hit, ctx
@@ -106,16 +109,19 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
     order = torch.argsort(qlen, stable=True)
     qpos, qlen = qpos[order].to(torch.int32), qlen[order]
     bounds = torch.searchsorted(qlen, torch.arange(len(levels) + 2, device=dev, dtype=torch.int32)).cpu().tolist()
-    big = None  # the regions of a bitmap level's emitting scan, made when one is counted
     batch: list = []  # list levels waiting to be counted together: (k, final positions, index)
     batch_ev = 0
     for k in range(1, len(levels) + 1):
+        kind, hs, nh = levels[k - 1][:3]
+        if kind == "bm":  # counted from the context ids the existence scan stored: no second query index or probe
+            _count_ids(elib, lib, tok, L, levels[k - 1], k, length, flags, grid, nxt, cnt)
+            levels[k - 1] = levels[k - 1][:3]
+            continue
         fpos = qpos[bounds[k] : bounds[k + 1]]
         m = fpos.numel()
         if m == 0:
             continue
         vi = QueryIndex(elib, x, avail, k, fpos, compact=True)
-        kind, hs, nh = levels[k - 1]
         if kind == "list":  # a sparse level: counted with the other list levels, one count for all
             batch.append((k, fpos, vi))
             batch_ev += nh
@@ -126,24 +132,10 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
         # the level's hit positions probed against the final contexts; their hits emitted, partitioned and counted in
         # LDS, then each final context's top entry
         flags.zero_()
-        if kind == "bm":
-            if big is None:
-                R = emit_region(L, grid)
-                big = (torch.empty(grid * R, dtype=torch.int64, device=dev), R,
-                       torch.empty(grid, dtype=torch.int32, device=dev),
-                       torch.empty(nwords, dtype=torch.int32, device=dev))
-            regions, R, ev_count, scratch_bm = big
-            dhist = torch.empty(256 * grid, dtype=torch.int32, device=dev)
-            mode = 0 if nh * 2 > L else 2
-            elib("ng_scan_emit", tok, L, i32(k), hs, scratch_bm, vi.table, u64(vi.cap), vi.rep, x, regions, u64(R),
-                 ev_count, flags, i32(grid), i32(mode), dhist, grid)
-            ev, n_ev, seg = None, 0, (regions, R, ev_count, dhist, grid)
-        else:
-            ev, n_ev = _scan_list(elib, tok, L, k, vi, x, hs, None, 0, flags, grid)
-            seg = None
+        ev, n_ev = _scan_list(elib, tok, L, k, vi, x, hs, None, 0, flags, grid)
         if int(flags[0].item()) & 4:
             raise RuntimeError(f"k={k}: an emit region overflowed")
-        c = count_events(elib, lib, ev, n_ev, vi.ids, _RATIO.get(k, 1.0), seg=seg, presort="ctx")
+        c = count_events(elib, lib, ev, n_ev, vi.ids, _RATIO.get(k, 1.0), presort="ctx")
         n_ev = c.n_ev
         del ev
         _RATIO[k] = c.U / max(1, n_ev)
@@ -174,6 +166,47 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
 SCAN_BLOCKS_PER_CU = 32  # scan blocks per compute unit
 BATCH_EVENTS = 1 << 28  # list levels counted together until their listed positions reach this
 LIST_DIV = 64  # a level's hits go to a position list once fewer than L / LIST_DIV (8 B each against L / 8 bitmap bytes)
+
+
+def _count_ids(elib: Lib, lib: Lib, tok, L: int, level: tuple, k: int, length, flags, grid: int, nxt, cnt) -> None:
+    """The counting phase of a bitmap level from what its existence scan kept: the hit bitmap, each hit position's
+    context id, and the level's active positions with their context ids. The final contexts (those of the positions
+    whose match ends at k) are marked in a bit set; the hit positions of final contexts emit their (context, next)
+    events (ng_scan_ids_emit), which are partitioned, counted and summarized per context (top entry), then gathered
+    to the final positions."""
+    _, bm, nh, ids, act, ctx_of, n_ids = level
+    dev = bm.device
+    fin = length[act.long()] == k
+    fids = ctx_of[fin]
+    fpos = act[fin].long()
+    m = fids.numel()
+    if m == 0:
+        return
+    final = torch.zeros((n_ids + 31) // 32, dtype=torch.int32, device=dev)
+    elib("ng_mark_bits", fids, m, final)
+    R = emit_region(L, grid)
+    regions = torch.empty(grid * R, dtype=torch.int64, device=dev)
+    ev_count = torch.empty(grid, dtype=torch.int32, device=dev)
+    dhist = torch.empty(256 * grid, dtype=torch.int32, device=dev)
+    flags.zero_()
+    elib("ng_scan_ids_emit", tok, L, bm, ids, final, regions, u64(R), ev_count, flags, i32(grid), dhist, grid)
+    if int(flags[0].item()) & 4:
+        raise RuntimeError(f"k={k}: an emit region overflowed")
+    c = count_events(elib, lib, None, 0, n_ids, _RATIO.get(k, 1.0), seg=(regions, R, ev_count, dhist, grid),
+                     presort="ctx")
+    del regions
+    _RATIO[k] = c.U / max(1, c.n_ev)
+    o_tok = torch.zeros(m, dtype=torch.int16, device=dev)
+    o_cnt = torch.zeros(m, dtype=torch.int32, device=dev)
+    if c.cb:
+        sm = summarize(elib, lib, c, n_ids, 1)
+        o = [torch.empty(m, dtype=torch.int32, device=dev) for _ in range(3)]
+        elib("ng_pos_summary", fids, m, 0, n_ids, None, sm.rec, sm.dist, None, None, i32(1), i32(1), i32(0), o[0], o[1],
+             o[2], o_tok, o_cnt, None)
+    else:  # unpacked pairs: sorted by key, per-context top entry by selection
+        _top1_unpacked(elib, lib, SimpleNamespace(ctx_of=fids, ids=n_ids), c, None, o_tok, o_cnt)
+    nxt[fpos] = o_tok
+    cnt[fpos] = o_cnt
 
 
 def _bits_list(elib: Lib, bm: torch.Tensor, n: int) -> torch.Tensor:
@@ -251,7 +284,7 @@ def _count_batch(elib: Lib, lib: Lib, tok, L: int, x, batch: list, levels: list,
 
 def _top1_unpacked(elib: Lib, lib: Lib, vi, c, x, o_tok, o_cnt) -> None:
     """The final contexts' top entries from unpacked (pair key, count) pairs (compact ctx_of, m entries)."""
-    dev = x.device
+    dev = o_tok.device
     m = vi.ctx_of.numel()
     ctx_bits = max(1, (max(vi.ids, 2) - 1).bit_length())
     uk = torch.empty(c.U, dtype=torch.int64, device=dev)
