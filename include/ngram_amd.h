@@ -175,6 +175,21 @@ int ng_query_index(const uint16_t* x, const int* avail, const int* pos, ng_i64 n
 int ng_query_index_shrink(const ng_u64* old_t, const uint32_t* old_rep, ng_u64 old_slots, ng_u64* table, ng_u64 cap,
                           ng_u64 slots, uint32_t* rep, int* ctx_of, ng_i64 n, int* remap, ng_u64* counters,
                           void* stream);
+/* the query index of pos[0..*n_dev) (compact ctx_of; n_max >= *n_dev sizes the grid) with no host sync: the table
+ * is EMPTY-filled here, counters[1] / counters[2] added to as ng_query_index's, contexts not counted */
+int ng_query_index_dev(const uint16_t* x, const int* avail, const int* pos, const ng_u64* n_dev, ng_i64 n_max, int k,
+                       ng_u64* table, ng_u64 cap, ng_u64 slots, uint32_t* rep, int* ctx_of, ng_u64* counters,
+                       void* stream);
+/* the longest match's active list one level on: entries i < *n_dev of act whose context's hit bit is set get
+ * length[act[i]] = k and, with avail >= k + 1, go to act_out (*n_out, *matched added to) */
+int ng_act_next(const int* act, const ng_u64* n_dev, ng_i64 n_max, const int* ctx_of, const uint32_t* hit,
+                const int* avail, int k, int* length, int* act_out, ng_u64* n_out, ng_u64* matched, void* stream);
+/* ng_scan_sink's list scan over the first *n_dev entries of plist (n_max >= *n_dev), with no host sync; region >=
+ * ceil(n_max / (grid * 256)) * 256 */
+int ng_scan_list_dev(const uint16_t* tok, int k, const ng_u64* plist, const ng_u64* n_dev, ng_i64 n_max,
+                     const ng_u64* vt, ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, uint32_t* hit, int what,
+                     ng_u64* ev, ng_u64 region, uint32_t* ev_count, uint32_t* flags, int grid, ng_u64 key_add,
+                     void* stream);
 /* partitioned counting (no global atomics): offsets[s] = cnt[0] + ... + cnt[s - 1], s = 0..nseg */
 int ng_seg_offsets(const uint32_t* cnt, ng_i64 nseg, ng_u64* offsets, void* stream);
 /* segment s = cnt[s] items at src + (bases ? bases[s] : s * region) packed to dst + offsets[s]; values may be NULL */

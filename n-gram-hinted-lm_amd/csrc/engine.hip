@@ -186,7 +186,7 @@ __global__ void __launch_bounds__(256) scan_list_k(const u16* __restrict__ tok, 
                                                    u32* flags, const u64* __restrict__ n_dev, u32* __restrict__ bm_out) {
     __shared__ SinkShared ss;
     sink_begin<S>(sink, &ss);
-    if (n_dev) n = (i64)*n_dev;  // the list's length as a device-side count
+    if (n_dev) n = (n > 0 && (i64)*n_dev > n) ? n : (i64)*n_dev;  // a device-side count (at most n when n > 0)
     const int lane = lane_id();
     const i64 stride = (i64)gridDim.x * blockDim.x;
     for (i64 base = blockIdx.x * (i64)blockDim.x + (threadIdx.x & ~(WAVE - 1)); base < n; base += stride) {
@@ -705,6 +705,22 @@ extern "C" int ng_scan_emit_list(const u16* tok, const u64* plist, const u64* n_
     return (int)hipGetLastError();
 }
 
+// The list scan of ng_scan_sink over the first *n_dev entries of plist (n_max >= *n_dev; a device-side count, so no
+// host sync): hit bits and events (positions, what 1, or mixed pair keys, what 0) as ng_scan_sink's;
+// region >= ceil(n_max / (grid * 256)) * 256.
+extern "C" int ng_scan_list_dev(const u16* tok, int k, const u64* plist, const u64* n_dev, i64 n_max, const u64* vt,
+                                u64 vcap, const u32* vrep, const u16* x, u32* hit, int what, u64* ev, u64 region,
+                                u32* ev_count, u32* flags, int grid, u64 key_add, void* stream) {
+    if (grid <= 0 || !n_dev || !ev || (what != 0 && what != 1) || region == 0 || region > 0xFFFFFFFFull ||
+        (u64)n_max > (u64)grid * region)
+        return -1;
+    const EmitSink sk{ev, region, ev_count, what, hit, nullptr, 0, key_add};
+    hipStream_t st = (hipStream_t)stream;
+    LEVEL_SWITCH(k, (scan_list_k<K, EmitSink><<<grid, 256, 0, st>>>(tok, plist, n_max, k, vt, vcap, vrep, x, sk, flags,
+                                                                     n_dev, nullptr)));
+    return (int)hipGetLastError();
+}
+
 // A level scan with optional outputs, over a bitmap-gated range (plist NULL: positions [0, L) gated by bm_in as
 // ng_scan_count's `sparse` modes, hit bitmap into bm_out) or over listed positions (plist: n corpus positions, bm_*
 // unused). hit (may be NULL): bit (context id) of the u32 words hit set per hit. ev (may be NULL): block b of `grid` appends per hit
@@ -863,7 +879,8 @@ namespace {
 template <int K>
 __global__ void qindex_insert_k(const u16* __restrict__ x, const int* __restrict__ avail, const int* __restrict__ pos,
                                 i64 n, int k, u64* table, u64 cap, u64 slots, u32* rep, int* __restrict__ ctx_of,
-                                int compact, u64* counters) {
+                                int compact, u64* counters, const u64* __restrict__ n_dev = nullptr) {
+    if (n_dev && (i64)*n_dev < n) n = (i64)*n_dev;  // a device-side count (at most the grid's n)
     const i64 j = blockIdx.x * (i64)blockDim.x + threadIdx.x;
     if (j < n) {
         const i64 i = pos ? pos[j] : j;
@@ -950,18 +967,16 @@ __global__ void qindex_remap_k(int* __restrict__ ctx_of, i64 n, const int* __res
 
 // Hashed contexts (k > 4): each position's k tokens against its slot's representative's; mismatches into *bad.
 __global__ void qindex_verify_k(const u16* __restrict__ x, const int* __restrict__ pos, i64 n, int k,
-                                const int* __restrict__ ctx_of, int compact, const u32* __restrict__ rep, u64* bad) {
+                                const int* __restrict__ ctx_of, int compact, const u32* __restrict__ rep, u64* bad,
+                                const u64* __restrict__ n_dev = nullptr) {
+    if (n_dev && (i64)*n_dev < n) n = (i64)*n_dev;
     const i64 j = blockIdx.x * (i64)blockDim.x + threadIdx.x;
     if (j >= n) return;
     const i64 i = pos ? pos[j] : j;
     const int s = ctx_of[compact ? j : i];
     if (s < 0) return;
     const i64 r = rep[s];
-    for (int t = 0; t < k; ++t)
-        if (x[i - t] != x[r - t]) {
-            atomicAdd((unsigned long long*)bad, 1ull);
-            return;
-        }
+    if (!same_tokens_rt(x + i + 1, x + r + 1, k)) atomicAdd((unsigned long long*)bad, 1ull);
 }
 }  // namespace
 
@@ -995,5 +1010,99 @@ extern "C" int ng_query_index(const u16* x, const int* avail, const int* pos, i6
     if (k > 4) qindex_verify_k<<<grid_for(n, 256), 256, 0, st>>>(x, pos, n, k, ctx_of, compact, rep, counters + 2);
     const int g = grid_for((i64)slots, 256);
     count_occupied_k<<<g < 1024 ? g : 1024, 256, 0, st>>>(table, slots, counters);
+    return (int)hipGetLastError();
+}
+
+namespace {
+// One step of the longest match's active list: entry i (i < *n_dev) of act whose context (ctx_of[i]) has its hit bit
+// set matched level k (length[act[i]] = k); those with avail >= k + 1 go on to act_out. Each thread takes 4 entries;
+// a block counts its kept entries and matches and takes its place in act_out with one atomic each (a counter bumped
+// per entry or per wave would serialize).
+__global__ void __launch_bounds__(256) act_next_k(const int* __restrict__ act, const u64* __restrict__ n_dev,
+                                                  const int* __restrict__ ctx_of, const u32* __restrict__ hit,
+                                                  const int* __restrict__ avail, int k, int* __restrict__ length,
+                                                  int* __restrict__ act_out, u64* n_out, u64* matched) {
+    __shared__ u32 wave_keep[4], wave_match[4];
+    __shared__ u64 base;
+    const i64 n = (i64)*n_dev;
+    const int lane = lane_id(), w = threadIdx.x / WAVE;
+    const i64 b0 = (i64)blockIdx.x * 1024;
+    int a[4];
+    bool keep[4];
+    u32 nk = 0, nm = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const i64 i = b0 + q * 256 + threadIdx.x;
+        keep[q] = false;
+        a[q] = 0;
+        if (i < n) {
+            a[q] = act[i];
+            const int c = ctx_of[i];
+            if (c >= 0 && ((hit[c >> 5] >> (c & 31)) & 1u)) {
+                length[a[q]] = k;
+                ++nm;
+                keep[q] = avail[a[q]] >= k + 1;
+            }
+        }
+        nk += keep[q];
+    }
+    // the block's kept entries, in order of (q, thread): per-wave sums, then per-round prefix via ballots
+    u32 tk = nk, tm = nm;
+#pragma unroll
+    for (int d = WAVE / 2; d > 0; d >>= 1) {
+        tk += (u32)__shfl_down((int)tk, d, WAVE);
+        tm += (u32)__shfl_down((int)tm, d, WAVE);
+    }
+    if (lane == 0) wave_keep[w] = tk, wave_match[w] = tm;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const u32 bk = wave_keep[0] + wave_keep[1] + wave_keep[2] + wave_keep[3];
+        const u32 bm = wave_match[0] + wave_match[1] + wave_match[2] + wave_match[3];
+        base = bk ? atomicAdd((unsigned long long*)n_out, (unsigned long long)bk) : 0;
+        if (bm) atomicAdd((unsigned long long*)matched, (unsigned long long)bm);
+    }
+    __syncthreads();
+    // positions in act_out: the block's base + the entries kept before this thread's (its wave's earlier lanes and
+    // the earlier waves), entries of one thread in a row
+    u32 incl = nk;
+#pragma unroll
+    for (int d = 1; d < WAVE; d <<= 1) {
+        const u32 o = (u32)__shfl_up((int)incl, d, WAVE);
+        if (lane >= d) incl += o;
+    }
+    u64 at = base + incl - nk;
+    for (int v = 0; v < w; ++v) at += wave_keep[v];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        if (keep[q]) act_out[at++] = a[q];
+}
+}  // namespace
+
+// The query index of the positions pos[0..*n_dev) (n_max >= *n_dev sizes the grid), compact ctx_of, without a host
+// sync: the table (cap + tail = slots) is EMPTY-filled here; counters[1] (a probe reached the table's end) and
+// counters[2] (hashed keys that collided, k > 4) are added to, as ng_query_index's; the contexts are not counted.
+extern "C" int ng_query_index_dev(const u16* x, const int* avail, const int* pos, const u64* n_dev, i64 n_max, int k,
+                                  u64* table, u64 cap, u64 slots, u32* rep, int* ctx_of, u64* counters,
+                                  void* stream) {
+    if (cap == 0 || slots <= cap || slots > (1ull << 31) || !n_dev || !pos || n_max < 0) return -1;
+    hipStream_t st = (hipStream_t)stream;
+    fill_u32_n((u32*)table, 0xFFFFFFFFu, (i64)(2 * slots), st);
+    if (n_max == 0) return (int)hipGetLastError();
+    LEVEL_SWITCH(k, (qindex_insert_k<K><<<grid_for(n_max, 256), 256, 0, st>>>(x, avail, pos, n_max, k, table, cap, slots,
+                                                                                rep, ctx_of, 1, counters, n_dev)));
+    if (k > 4)
+        qindex_verify_k<<<grid_for(n_max, 256), 256, 0, st>>>(x, pos, n_max, k, ctx_of, 1, rep, counters + 2, n_dev);
+    return (int)hipGetLastError();
+}
+
+// The longest match's active list, one level on: see act_next_k. n_out and matched are added to (zero them first);
+// act_out holds at least *n_dev entries; n_max >= *n_dev sizes the grid.
+extern "C" int ng_act_next(const int* act, const u64* n_dev, i64 n_max, const int* ctx_of, const u32* hit,
+                           const int* avail, int k, int* length, int* act_out, u64* n_out, u64* matched,
+                           void* stream) {
+    if (!n_dev || n_max < 0) return -1;
+    if (n_max > 0)
+        act_next_k<<<(int)((n_max + 1023) / 1024), 256, 0, (hipStream_t)stream>>>(act, n_dev, ctx_of, hit, avail, k,
+                                                                                   length, act_out, n_out, matched);
     return (int)hipGetLastError();
 }

@@ -97,6 +97,52 @@ __device__ __forceinline__ u64 ctx_key_stop(const u16* e, int k) {
     return key_finish(h);
 }
 
+// ctx_key's sum (before key_finish) of the k tokens before e for a run-time k, the tokens loaded 8 at a time (each
+// group's loads in flight together: no load waits for another's value); gap |= any of them is SENT.
+__device__ __forceinline__ u64 ctx_hash_rt(const u16* __restrict__ e, int k, bool& gap) {
+    u64 h = 0, bp = 1;
+    int j = 1;
+    for (; j + 7 <= k; j += 8) {
+        u32 t[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) t[q] = e[-(j + q)];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            gap |= t[q] == SENT;
+            if (k <= 4) h |= (u64)t[q] << (16 * (j + q - 1));
+            else {
+                h += tok_code(t[q]) * bp;
+                bp *= POLY_BASE;
+            }
+        }
+    }
+    for (; j <= k; ++j) {
+        const u32 t = e[-j];
+        gap |= t == SENT;
+        if (k <= 4) h |= (u64)t << (16 * (j - 1));
+        else {
+            h += tok_code(t) * bp;
+            bp *= POLY_BASE;
+        }
+    }
+    return h;
+}
+
+// The k tokens before a and before b equal (run-time k; loaded 8 pairs at a time).
+__device__ __forceinline__ bool same_tokens_rt(const u16* __restrict__ a, const u16* __restrict__ b, int k) {
+    bool same = true;
+    int j = 1;
+    for (; j + 7 <= k; j += 8) {
+        u32 ta[8], tb[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) ta[q] = a[-(j + q)], tb[q] = b[-(j + q)];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) same &= ta[q] == tb[q];
+    }
+    for (; j <= k; ++j) same &= a[-j] == b[-j];
+    return same;
+}
+
 // Position p's next token (nxt = tok[p]) and k-context key (tok[p - k .. p - 1]) as ctx_key_stop's, with all k + 1
 // tokens loaded together (no load waits for another token's value): EMPTY where any of the k is SENT. A token before
 // the buffer's start (p - j < 0) reads as SENT, which is what ctx_key_stop meets there too (the buffer starts with
@@ -122,7 +168,10 @@ __device__ __forceinline__ u64 ctx_key_at(const u16* __restrict__ tok, i64 p, in
         return gap ? EMPTY : key_finish(h);
     } else {
         nxt = tok[p];
-        return p >= k ? ctx_key_stop<0>(tok + p, k) : EMPTY;
+        if (p < k) return EMPTY;
+        bool gap = false;
+        const u64 h = ctx_hash_rt(tok + p, k, gap);
+        return gap ? EMPTY : key_finish(h);
     }
 }
 

@@ -41,7 +41,10 @@
 template <int K>
 __device__ __forceinline__ u64 key_at(const u16* e, int k) {
     if constexpr (K > 0) return ctx_key<K>(e);
-    else return ctx_key_rt(e, k);
+    else {
+        bool gap = false;
+        return key_finish(ctx_hash_rt(e, k, gap));
+    }
 }
 
 template <int K>
@@ -98,15 +101,9 @@ __device__ __forceinline__ u64 probe_table(const u16* __restrict__ tok, i64 p, i
         const u64 v = vt[s];
         if (v == key) {
             const int kk = klen<K>(k);
-            if (kk > 4) {
-                const u16* a = tok + p - kk;
-                const u16* b = x + (i64)vrep[s] + 1 - kk;
-                bool same = true;
-                for (int j = 0; j < kk; ++j) same &= a[j] == b[j];
-                if (!same) {
-                    atomicAdd(&flags[1], 1u);
-                    return EMPTY;
-                }
+            if (kk > 4 && !same_tokens_rt(tok + p, x + (i64)vrep[s] + 1, kk)) {
+                atomicAdd(&flags[1], 1u);
+                return EMPTY;
             }
             return (s << 16) | nxt;
         }
@@ -147,15 +144,9 @@ __device__ __forceinline__ u64 probe_finish(const u16* __restrict__ tok, i64 p, 
     while (true) {
         if (v == key) {
             const int kk = klen<K>(k);
-            if (kk > 4) {
-                const u16* a = tok + p - kk;
-                const u16* b = x + (i64)vrep[s] + 1 - kk;
-                bool same = true;
-                for (int j = 0; j < kk; ++j) same &= a[j] == b[j];
-                if (!same) {
-                    atomicAdd(&flags[1], 1u);
-                    return EMPTY;
-                }
+            if (kk > 4 && !same_tokens_rt(tok + p, x + (i64)vrep[s] + 1, kk)) {
+                atomicAdd(&flags[1], 1u);
+                return EMPTY;
             }
             return (s << 16) | nxt;
         }

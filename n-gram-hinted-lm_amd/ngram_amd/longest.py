@@ -33,7 +33,7 @@ from .data import BOS, HEADER_BYTES, shard_tokens
 from .gpu_val_stats import layout
 from .lib import Lib, i32, u64
 from .partcount import count_events, emit_region, pack_events, summarize
-from .qindex import QueryIndex
+from .qindex import LOAD as QLOAD, TAIL as QTAIL, QueryIndex
 
 
 def _popcount(lib: Lib, bm: torch.Tensor) -> int:
@@ -76,6 +76,13 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
     for k in range(1, cap + 1):
         act = act[avail[act.long()] >= k]
         if act.numel() == 0:
+            break
+        if levels and levels[-1][0] == "list" and DEVICE_LEVELS:
+            # the sparse levels' lists shrink slowly from here on: the remaining levels run without a host sync
+            for k2, hl, nh, matched in _exist_device(elib, tok, L, x, avail, act, k, cap, levels[-1][1], length,
+                                                    flags, grid):
+                levels.append(("list", hl, nh))
+                ladder.append((k2, int(elig[k2]), matched))
             break
         vi = QueryIndex(elib, x, avail, k, act, compact=True)
         hit = torch.zeros((vi.ids + 31) // 32, dtype=torch.int32, device=dev)  # a bit per context id
@@ -164,8 +171,67 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
 
 
 SCAN_BLOCKS_PER_CU = 32  # scan blocks per compute unit
+DEVICE_LEVELS = True  # the existence phase's levels after the second list level run without host syncs
 BATCH_EVENTS = 1 << 28  # list levels counted together until their listed positions reach this
 LIST_DIV = 64  # a level's hits go to a position list once fewer than L / LIST_DIV (8 B each against L / 8 bitmap bytes)
+
+
+def _exist_device(elib: Lib, tok, L: int, x, avail, act, k0: int, cap: int, cand, length, flags, grid: int):
+    """Levels k0..cap of the existence phase as one stream of launches with no host sync (ng_query_index_dev,
+    ng_scan_list_dev, ng_seg_offsets / ng_seg_gather, ng_act_next), every buffer sized by level k0's active
+    positions (act, already those with avail >= k0) and candidates (cand: the corpus positions that matched k0 - 1),
+    which bound every later level's. One sync at the end reads each level's sizes; the levels are those whose active
+    list was not empty, as the host loop's. Returns [(k, hit list, its length, matched positions)]."""
+    dev = x.device
+    n0, nc0 = int(act.numel()), int(cand.numel())
+    qcap = int(n0 / QLOAD) + 1024
+    slots = qcap + QTAIL
+    table = torch.empty(slots, dtype=torch.int64, device=dev)
+    rep = torch.empty(slots, dtype=torch.int32, device=dev)
+    ctx_of = torch.empty(max(n0, 1), dtype=torch.int32, device=dev)
+    hit = torch.empty((slots + 31) // 32, dtype=torch.int32, device=dev)
+    acts = [act.contiguous(), torch.empty(max(n0, 1), dtype=torch.int32, device=dev)]
+    nlev = cap - k0 + 1
+    counters = torch.zeros((nlev, 3), dtype=torch.int64, device=dev)
+    sizes = torch.zeros((nlev, 3), dtype=torch.int64, device=dev)  # per level: active, matched, kept for the next
+    g = max(1, min(grid, -(-max(nc0, 1) // 256)))
+    R = -(-max(nc0, 1) // (g * 256)) * 256
+    regions = torch.empty(g * R, dtype=torch.int64, device=dev)
+    ev_count = torch.empty(g, dtype=torch.int32, device=dev)
+    n_act = torch.tensor([n0], dtype=torch.int64, device=dev)
+    n_cand = torch.tensor([nc0], dtype=torch.int64, device=dev)
+    flags.zero_()
+    out = []
+    for j, k in enumerate(range(k0, cap + 1)):
+        cur, nxt = acts[j % 2], acts[(j + 1) % 2]
+        sizes[j, 0:1].copy_(n_act)
+        elib("ng_query_index_dev", x, avail, cur, n_act, n0, i32(k), table, u64(qcap), u64(slots), rep, ctx_of,
+             counters[j])
+        hit.zero_()
+        elib("ng_scan_list_dev", tok, i32(k), cand, n_cand, nc0, table, u64(qcap), rep, x, hit, i32(1), regions,
+             u64(R), ev_count, flags, i32(g), u64(0))
+        offs = torch.empty(g + 1, dtype=torch.int64, device=dev)
+        elib("ng_seg_offsets", ev_count, g, offs)
+        hl = torch.empty(max(nc0, 1), dtype=torch.int64, device=dev)
+        elib("ng_seg_gather", regions, None, u64(R), None, ev_count, g, offs, hl, None)
+        elib("ng_act_next", cur, n_act, n0, ctx_of, hit, avail, i32(k), length, nxt, sizes[j, 2:3], sizes[j, 1:2])
+        out.append((k, hl, offs[g:]))
+        cand, n_cand, n_act = hl, offs[g:], sizes[j, 2:3]
+    host = sizes.cpu().tolist()
+    nhs = torch.cat([o for _, _, o in out]).cpu().tolist()
+    c = counters.cpu()
+    if int(flags[0].item()) & 4:
+        raise RuntimeError(f"levels {k0}..{cap}: an emit region overflowed")
+    if int(c[:, 1].max()):
+        raise RuntimeError(f"levels {k0}..{cap}: a query index probe reached its table's end")
+    if int(c[:, 2].max()):
+        raise RuntimeError(f"levels {k0}..{cap}: query positions collide with another context's key")
+    res = []
+    for (k, hl, _), nh, (n_k, matched, _) in zip(out, nhs, host):
+        if n_k == 0:
+            break
+        res.append((k, hl[:nh], nh, matched))
+    return res
 
 
 def _count_ids(elib: Lib, lib: Lib, tok, L: int, level: tuple, k: int, length, flags, grid: int, nxt, cnt) -> None:

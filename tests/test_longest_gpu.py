@@ -43,6 +43,25 @@ def test_longest_match_matches_oracle(corpus, cap, seg, monkeypatch):
         assert matched == int((want[0] >= k).sum()) and eligible == int((avail >= k).sum())
 
 
+def test_device_levels_match_host_levels(corpus, monkeypatch):
+    """The existence phase's deep levels run as one stream of launches (no host sync) or level by level on the host:
+    the same lengths, next tokens, counts and ladder."""
+    from ngram_amd import longest as LG
+
+    x = corpus.query[:-1]
+    tok, sizes, starts, L = load_shards(corpus.shards())
+    xt = torch.from_numpy(x.view(np.int16).copy()).cuda()
+    av = _segments(xt, record_lib())
+    got = {}
+    for dev_levels in (True, False):
+        monkeypatch.setattr(LG, "DEVICE_LEVELS", dev_levels)
+        length, nxt, cnt, ladder = longest_match(tok, xt, av, 64)
+        got[dev_levels] = (length.cpu(), nxt.cpu(), cnt.cpu(), ladder)
+    for a, b in zip(got[True][:3], got[False][:3]):
+        assert torch.equal(a, b)
+    assert got[True][3] == got[False][3] and len(got[True][3]) == 64
+
+
 def test_ladder_interface(corpus, tmp_path):
     paths, _ = corpus.write(tmp_path)
     lm = LongestMatch.create(paths, corpus.query[:20_001], 4, [])
