@@ -170,6 +170,12 @@ class OnlineRows:
         st["qslot"] = {k: torch.empty(max(1, nq), dtype=torch.int32, device=dev) for k in levels}
         st["hinted"] = torch.zeros(1, dtype=torch.int32, device=dev)
         st["done"] = 0
+        if levels:  # ng_online_rows' per-level descriptors (deepest first): the same buffers every step
+            desc = []
+            for k in sorted(levels, reverse=True):
+                lv = st["levels"][k]
+                desc += [st["qslot"][k].data_ptr(), lv["tot"].data_ptr(), lv["top"].data_ptr(), buckets.index(k), 0]
+            st["rows_desc"] = torch.tensor(desc, dtype=torch.int64, device=dev)
         return st
 
     def _range(self, arr: np.ndarray, lo: int, hi: int) -> tuple[int, int]:
@@ -212,20 +218,14 @@ class OnlineRows:
                 lv["pk"], lv["pcnt"], u64(lv["pcap"]), lv["tot"], lv["dist"], st["qslot"][k], None, None, None,
                 i32(1), i32(0))
         if levels:
-            desc = []
-            for k in sorted(levels, reverse=True):
-                lv = st["levels"][k]
-                desc += [st["qslot"][k].data_ptr(), lv["tot"].data_ptr(), lv["top"].data_ptr(), buckets.index(k), 0]
-            desc_t = torch.tensor(desc, dtype=torch.int64, device=self.dev)
-            lib("ng_online_rows", qpos, mq, i32(len(levels)), desc_t, i32(E), outs["cell"], outs["next"],
+            lib("ng_online_rows", qpos, mq, i32(len(levels)), st["rows_desc"], i32(E), outs["cell"], outs["next"],
                 outs["weights"], st["hinted"])
-            outs["keep"].append(desc_t)  # the descriptor lives until the kernel has run
 
     def _device_outputs(self, cfg) -> dict:
         levels, buckets, entries, count_levels = cfg
         n, dev = self.n, self.dev
         E = max(1, entries)
-        return {"cfg": cfg, "keep": [],
+        return {"cfg": cfg,
                 "cell": torch.zeros(n, dtype=torch.int16, device=dev),
                 "next": torch.zeros((n, E), dtype=torch.int16, device=dev),
                 "weights": torch.zeros((n, E), dtype=torch.int16, device=dev),
@@ -265,7 +265,6 @@ class OnlineRows:
             st["outs"] = self._device_outputs(self.config)
         outs = st["outs"]
         st["hinted"].zero_()
-        outs["keep"] = []
         for s in range(self._done, step_hi):
             self._step(st, s, outs)
         self._check_flags(st)
@@ -282,7 +281,6 @@ class OnlineRows:
         if "outs" not in st:
             st["outs"] = self._device_outputs(self.config)
         outs = st["outs"]
-        outs["keep"] = []
         for s in range(self._done, step_hi):
             self._step(st, s, outs)
         self._done = step_hi
