@@ -450,6 +450,10 @@ def main() -> None:
                      "frac": achieved / HBM_PEAK_GBS, "traffic": scan_traffic(cb.mode),
                      "launches_per_step": scan_launches // max(1, args.steps),
                      "avg_launch_ms": scan_ms / max(1, scan_launches),
+                     # the measured HBM + MALL traffic per launch over the average launch: the rate the scans'
+                     # random line fetches actually move, against the same peak
+                     "traffic_GBps": None if scan_traffic(cb.mode) is None or scan_launches == 0 else
+                     scan_traffic(cb.mode) / (scan_ms / scan_launches / 1e3) / 1e9,
                      "algorithmic_bytes_per_step": step_bytes,
                      "scan_share_of_step": scan_ms / args.steps / ms},
         "count_path_roofline": None if cb.mode != "part" else {
