@@ -196,7 +196,7 @@ class CountBuild:
         self.pending = []
         for a, st in zip(self.host, self.starts):
             n = a.numel()
-            for lo in range(0, n, 4 << 20):
+            for lo in range(0, max(n, 1), 4 << 20):  # an empty shard: one empty copy, so that it has its event too
                 hi = min(n, lo + (4 << 20))
                 self.pending.append((st + lo, a, lo, hi, hi == n))
         self.pending.reverse()
