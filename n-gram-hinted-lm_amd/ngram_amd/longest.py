@@ -7,14 +7,15 @@ of that shard), that context's most frequent next token (count descending, then 
 
 Two phases, both on libngram_amd.so. Existence, k = 1, 2, ...: the query contexts of the positions still matching
 (a query index per level over the list of positions still matching), the corpus positions whose (k-1)-context
-matched (a hit bitmap per level) probed for their k-context (ng_scan_exist: a bitmap and a per-context hit bit, no
-counting), until no position matches. A match is monotone in k (kgram.rs:12-15), so each position's length is its
-last matching level. Then counting, only for each position's final context: per level, the final contexts' query
-index, the corpus positions of that level's bitmap probed and their (context, next) hits emitted, partitioned and
-counted in LDS (partcount.py: no global atomics, so the hot pairs of short contexts cost no serialized chains), each
-context's top entry made from its pairs (ng_ctx_summary) and gathered to its positions (ng_pos_summary). Most
-positions match past the short levels, whose contexts are the corpus' most frequent: counting only final contexts
-skips nearly all of their occurrences.
+matched (a hit bitmap while dense, then a position list) probed for their k-context (ng_scan_exist: a bitmap, a
+per-context hit bit and each hit position's context id, no counting), until no position matches; once the lists
+shrink slowly, the remaining levels run as one stream of launches with device-side counts (no host sync per level).
+A match is monotone in k (kgram.rs:12-15), so each position's length is its last matching level. Then counting,
+only for each position's final context: a bitmap level's hit positions whose stored context id is final emit their
+(context, next) events (ng_scan_ids_emit: no second query index or probe); a list level's final contexts get a query
+index and its listed positions are probed, the list levels counted together. The events are partitioned and counted
+in LDS (partcount.py: no global atomics, so the hot pairs of short contexts cost no serialized chains), each
+context's top entry made from its pairs (ng_ctx_summary) and gathered to its positions (ng_pos_summary).
 
 Surfaces: `longest_match(...)` on GPU tensors, and `LongestMatch.create(files, tokens, threads, cpus)` /
 `build() -> dict` in cache_ladder's shape (cache_ladder/src/lib.rs:1-8, cache_ladder.pyi)."""
