@@ -245,7 +245,11 @@ __global__ void __launch_bounds__(RS_BLOCK) rs_hist_k(const u64* __restrict__ ke
 // lanes by digit with eight ballots; the per-(row, wave, digit) counts (u16) are scanned in LDS in tile order, giving
 // each item its place in the tile sorted by digit. The tile is then staged in LDS in that order (aliasing the counts)
 // and written out by consecutive threads, so each digit's run of the tile leaves as contiguous, coalesced stores.
-template <bool VALUES>
+// RAW: hist holds the per-tile counts themselves (not their exclusive scan); the block then finds its own bases (each
+// digit's total over all tiles, scanned over the digits, plus its count in the tiles before this one), which saves the
+// scan's launches when there are few tiles (RS_RAW_TILES at most: a few thousand counts read per block).
+static constexpr i64 RS_RAW_TILES = 256;
+template <bool VALUES, bool RAW = false>
 __global__ void __launch_bounds__(RS_BLOCK) rs_scatter_k(const u64* __restrict__ kin, const u32* __restrict__ vin,
                                                          u64* __restrict__ kout, u32* __restrict__ vout, i64 n,
                                                          int shift, int nbits, const u32* __restrict__ hist,
@@ -262,7 +266,19 @@ __global__ void __launch_bounds__(RS_BLOCK) rs_scatter_k(const u64* __restrict__
     u32* stage_v = (u32*)(smem + RS_TILE);
     const int t = threadIdx.x, w = t / WAVE;
     const u32 mask = (1u << nbits) - 1u;
-    if (t < 256) gbase[t] = hist[(i64)t * ntiles + blockIdx.x];
+    if constexpr (RAW) {
+        u32 before = 0, total = 0;  // thread t < 256 = digit t
+        if (t < 256)
+            for (i64 b = 0; b < ntiles; ++b) {
+                const u32 c = hist[(i64)t * ntiles + b];
+                before += b < (i64)blockIdx.x ? c : 0u;
+                total += c;
+            }
+        const u32 dbase = rs_block_exclusive(t < 256 ? total : 0u, wt);
+        if (t < 256) gbase[t] = dbase + before;
+    } else {
+        if (t < 256) gbase[t] = hist[(i64)t * ntiles + blockIdx.x];
+    }
     for (int i = t; i < CNT_BYTES / 4; i += RS_BLOCK) ((u32*)smem)[i] = 0;
     __syncthreads();
     const i64 base = (i64)blockIdx.x * RS_TILE;
@@ -384,12 +400,21 @@ int radix_sort_pairs(const u64* kin, u64* kout, const u32* vin, u32* vout, i64 n
         u64* dk = to_out ? kout : tk;
         u32* dv = to_out ? vout : tv;
         rs_hist_k<<<(unsigned)nt, RS_BLOCK, 0, st>>>(sk, n, shift, (1u << nb) - 1u, hist, nt);
-        int e = exclusive_scan_u32(hist, hist, nt * 256, nullptr, stemp, st);
-        if (e) return e;
-        if (values)
-            rs_scatter_k<true><<<(unsigned)nt, RS_BLOCK, 0, st>>>(sk, sv, dk, dv, n, shift, nb, hist, nt);
-        else
-            rs_scatter_k<false><<<(unsigned)nt, RS_BLOCK, 0, st>>>(sk, nullptr, dk, nullptr, n, shift, nb, hist, nt);
+        int e = 0;
+        if (nt <= RS_RAW_TILES) {  // few tiles: each scatter block scans the counts itself
+            if (values)
+                rs_scatter_k<true, true><<<(unsigned)nt, RS_BLOCK, 0, st>>>(sk, sv, dk, dv, n, shift, nb, hist, nt);
+            else
+                rs_scatter_k<false, true><<<(unsigned)nt, RS_BLOCK, 0, st>>>(sk, nullptr, dk, nullptr, n, shift, nb, hist,
+                                                                           nt);
+        } else {
+            e = exclusive_scan_u32(hist, hist, nt * 256, nullptr, stemp, st);
+            if (e) return e;
+            if (values)
+                rs_scatter_k<true><<<(unsigned)nt, RS_BLOCK, 0, st>>>(sk, sv, dk, dv, n, shift, nb, hist, nt);
+            else
+                rs_scatter_k<false><<<(unsigned)nt, RS_BLOCK, 0, st>>>(sk, nullptr, dk, nullptr, n, shift, nb, hist, nt);
+        }
         e = (int)hipGetLastError();
         if (e) return e;
         sk = dk;
