@@ -27,7 +27,7 @@ HBM_PEAK_GBS = 8000.0
 SCAN_KERNELS = ("scan_count", "scan_level", "scan_emit")  # the level scans, whichever counting CountBuild uses
 # "part" mode counts after the scan (emitted hits packed, hash-partitioned, counted in LDS): its roofline kernel set is
 # the whole count path, whose algorithmic bytes are the build's 2 per position scanned + 16 per hit
-PART_KERNELS = ("scan_emit", "gather", "partition", "count")
+PART_KERNELS = ("scan_emit", "bits_list", "gather", "partition", "count")
 
 
 def scan_traffic(mode: str):

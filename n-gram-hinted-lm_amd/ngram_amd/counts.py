@@ -498,13 +498,17 @@ class CountBuild:
             # gated by this shard's previous scanned level; a shard that level skipped is probed whole
             bm_in = None if si == 0 else bms[scanned[si - 1]][st // 32 :]
             mode = self._scan_mode(si, scanned, lists=True)
-            e0, e1 = self._event("scan_emit", k, i, n32)
-            e0.record()
             if mode == 3:  # the previous level's hits listed, then probed one lane each
                 if self._plist is None or self._plist.numel() < n32:
                     self._plist = torch.empty(max(self.sizes) + 64, dtype=torch.int64, device=dev)
                 n_list = torch.zeros(1, dtype=torch.int64, device=dev)
+                b0, b1 = self._event("bits_list", k, i, n32)
+                b0.record()
                 elib.cub("ng_bits_list", bm_in, n32 // 32, self._plist, n_list)
+                b1.record()
+            e0, e1 = self._event("scan_emit", k, i, n32)
+            e0.record()
+            if mode == 3:
                 elib("ng_scan_emit_list", self.tok[st:], self._plist, n_list, i32(k), vi.table, u64(vi.cap), vi.rep,
                      self.x, bms[k][st // 32 :], regions[j * G * R :], u64(R), ev_count[j * G :], flags, i32(G),
                      dhist[j * G :] if dhist is not None else None, nseg)
