@@ -120,6 +120,7 @@ class CountBuild:
         self.density: dict[int, float] = {}  # each level's hit density, from the last build with stats
         self._plist = None  # part mode: a shard's listed positions (list scans)
         self.events_of: dict[int, int] = {}  # part mode: each level's events in the last build
+        self.contexts_of: dict[int, int] = {}  # part mode: each level's query contexts in the last build
         self.dratio: dict[int, float] = {}  # "part" mode: each level's distinct pairs per event, from the last build
         self.levels = tuple(levels)
         if not self.levels or list(self.levels) != sorted(set(self.levels)) or self.levels[0] < 1:
@@ -160,6 +161,7 @@ class CountBuild:
         self.density: dict[int, float] = {}  # each level's hit density, from the last build with stats
         self._plist = None  # part mode: a shard's listed positions (list scans)
         self.events_of: dict[int, int] = {}  # part mode: each level's events in the last build
+        self.contexts_of: dict[int, int] = {}  # part mode: each level's query contexts in the last build
         self.dratio: dict[int, float] = {}  # "part" mode: each level's distinct pairs per event, from the last build
         self.levels = tuple(levels)
         ls = LEVEL_SHARDS if level_shards is None else level_shards
@@ -434,7 +436,8 @@ class CountBuild:
             seen = None
             if prev is not None and self.level_shards[k] <= self.level_shards[prev]:
                 seen = torch.nonzero(out[1, li - 1] > 0).squeeze(1).to(torch.int32)
-            vi = QueryIndex(self.elib, x, avail, k, seen)
+            vi = QueryIndex(self.elib, x, avail, k, seen, expect=self.contexts_of.get(k))
+            self.contexts_of[k] = vi.n
             index_t += time.perf_counter() - t0
             t0 = time.perf_counter()
             seg = self._part_emit(k, vi, bms, regions, R)

@@ -44,6 +44,7 @@ def _popcount(lib: Lib, bm: torch.Tensor) -> int:
 
 
 _RATIO: dict[int, float] = {}  # distinct pairs per counted event at each level, from the last count (sizes partitions)
+_CONTEXTS: dict[int, int] = {}  # each existence level's query contexts in the last call (sizes its query index)
 
 
 def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: int = 64, elib: Lib | None = None,
@@ -85,7 +86,8 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
                 levels.append(("list", hl, nh))
                 ladder.append((k2, int(elig[k2]), matched))
             break
-        vi = QueryIndex(elib, x, avail, k, act, compact=True)
+        vi = QueryIndex(elib, x, avail, k, act, compact=True, expect=_CONTEXTS.get(k))
+        _CONTEXTS[k] = vi.n
         hit = torch.zeros((vi.ids + 31) // 32, dtype=torch.int32, device=dev)  # a bit per context id
         prev = levels[-1] if levels else None
         if prev is not None and (prev[0] == "list" or prev[2] * LIST_DIV < L):

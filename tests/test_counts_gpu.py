@@ -146,3 +146,21 @@ def test_fit_blocks_start_segments(corpus):
     assert av[1000] == 1 and av[1000 + 299] == 1
     xs = np.concatenate([corpus.query[:1000], blocks[0][:-1], blocks[1][:-1]])
     assert np.array_equal(av, data.segments(xs, breaks=[1000, 1299]))
+
+
+def test_context_hints_from_an_earlier_build(corpus):
+    """A build sizes its query indexes from the last build's context counts: far fewer contexts than expected (the
+    tables shrink), then far more (the indexes are built again at their size); every build matches the oracle."""
+    lib = C.record_lib()
+    cb = C.CountBuild(corpus.shards(), levels=LEVELS, level_shards={}, topk=4)
+    cb.start_load(1)
+    full = corpus.query
+    for q in (full, full[:3001], full):
+        x, tgt, avail = C.queries(q, [], "cuda", lib)
+        out = cb.counts(x, tgt, avail).cpu().numpy()
+        xs, ts = q[:-1], q[1:]
+        av = O.segments(xs)
+        for li, k in enumerate(LEVELS):
+            o = O.query_counts(corpus.train, corpus.bounds, xs, ts, av, k, cnt_top=1 << 30, ntop=4)
+            assert np.array_equal(out[0, li].view(np.uint32), o["tot"]), (len(q), k)
+            assert np.array_equal(out[2, li].view(np.uint32), o["cnt"]), (len(q), k)
