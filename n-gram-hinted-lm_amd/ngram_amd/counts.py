@@ -492,6 +492,12 @@ class CountBuild:
         dhist = torch.empty(256 * max(nseg, 1), dtype=torch.int32, device=dev) \
             if last is None or last >= partcount.SEG_MIN_EVENTS * nseg else None
         flags = torch.zeros(2, dtype=torch.int32, device=dev)
+        scans = {tuple(q for q in self.levels if i < self.level_shards[q]) for i in shards}
+        if len(shards) > 1 and len(scans) == 1:
+            scanned = list(scans.pop())
+            si = scanned.index(k)
+            if si > 0 and self._scan_mode(si, scanned, lists=True) == 3:
+                return self._part_emit_lists(k, vi, bms[scanned[si - 1]], bms[k], shards, regions, flags)
         for j, i in enumerate(shards):
             st, n = self.starts[i], self.sizes[i]
             n32 = (n + 31) // 32 * 32
@@ -523,6 +529,39 @@ class CountBuild:
         if int(flags[0].item()) & 4:
             raise RuntimeError(f"k={k}: an emit region overflowed")
         return regions, R, ev_count, dhist, nseg
+
+    def _part_emit_lists(self, k, vi, bm_in, bm_out, shards, regions, flags):
+        """_part_emit of a list level whose shards all scan the same levels: one position list over all of them (the
+        set bits of the previous level's bitmap from the first shard's start to the last one's end) and one list scan,
+        instead of a list and a scan per shard; seg = (regions, R, ev_count, dhist, grid)."""
+        elib, dev, G = self.elib, self.tok.device, self.grid
+        lo = self.starts[shards[0]]
+        hi = self.starts[shards[-1]] + (self.sizes[shards[-1]] + 31) // 32 * 32
+        for i in shards:
+            torch.cuda.current_stream().wait_event(self.events[i])
+        n_max = hi - lo
+        R = -(-max(n_max, 1) // (G * 256)) * 256  # a list scan's block emits at most 256 per round
+        if G * R > regions.numel():
+            raise RuntimeError(f"k={k}: the emit regions are too small for one list scan")
+        if self._plist is None or self._plist.numel() < n_max:
+            self._plist = torch.empty(n_max + 64, dtype=torch.int64, device=dev)
+        n_list = torch.zeros(1, dtype=torch.int64, device=dev)
+        ev_count = torch.zeros(G, dtype=torch.int32, device=dev)
+        last = self.events_of.get(k)
+        dhist = torch.empty(256 * G, dtype=torch.int32, device=dev) \
+            if last is None or last >= partcount.SEG_MIN_EVENTS * G else None
+        b0, b1 = self._event("bits_list", k, -1, n_max)
+        b0.record()
+        elib.cub("ng_bits_list", bm_in[lo // 32 :], n_max // 32, self._plist, n_list)
+        b1.record()
+        e0, e1 = self._event("scan_emit", k, -1, n_max)
+        e0.record()
+        elib("ng_scan_emit_list", self.tok[lo:], self._plist, n_list, i32(k), vi.table, u64(vi.cap), vi.rep, self.x,
+             bm_out[lo // 32 :], regions, u64(R), ev_count, flags, i32(G), dhist, G)
+        e1.record()
+        if int(flags[0].item()) & 4:
+            raise RuntimeError(f"k={k}: an emit region overflowed")
+        return regions, R, ev_count, dhist, G
 
     def _owner_packed(self, li, k, vi, c, tgt, out, want, zero_tops):
         """The owner side from packed pairs: per present context its record (sorted by context, keys only), then per
