@@ -428,7 +428,10 @@ class CountBuild:
             self.top_cnt = torch.zeros((len(self.levels), N, self.topk), dtype=torch.int32, device=dev)
         G = self.grid
         R = max(emit_region((n + 31) // 32 * 32, G) for n in self.sizes)
-        regions = torch.empty(len(self.sizes) * G * R, dtype=torch.int64, device=dev)
+        span = self.starts[-1] + (self.sizes[-1] + 31) // 32 * 32 - self.starts[0] if self.sizes else 0
+        # room for one region per shard and block, or for one scan over every shard (a list scan's regions included)
+        n_reg = max(len(self.sizes) * G * R, G * emit_region(span, G), G * (-(-max(span, 1) // (G * 256)) * 256))
+        regions = torch.empty(n_reg, dtype=torch.int64, device=dev)
         scan_t = count_t = index_t = 0.0
         for li, k in enumerate(self.levels):
             t0 = time.perf_counter()
@@ -494,10 +497,14 @@ class CountBuild:
         flags = torch.zeros(2, dtype=torch.int32, device=dev)
         scans = {tuple(q for q in self.levels if i < self.level_shards[q]) for i in shards}
         if len(shards) > 1 and len(scans) == 1:
+            # every shard scans the same levels: one launch over all of them (the SENT gaps between shards hold no
+            # context), except for a first level whose shards may still be arriving from the host (each shard's scan
+            # then starts once its own copy is done)
             scanned = list(scans.pop())
             si = scanned.index(k)
-            if si > 0 and self._scan_mode(si, scanned, lists=True) == 3:
-                return self._part_emit_lists(k, vi, bms[scanned[si - 1]], bms[k], shards, regions, flags)
+            if si > 0 or not self.host:
+                return self._part_emit_all(k, vi, None if si == 0 else bms[scanned[si - 1]], bms[k], shards, regions,
+                                           flags, self._scan_mode(si, scanned, lists=True))
         for j, i in enumerate(shards):
             st, n = self.starts[i], self.sizes[i]
             n32 = (n + 31) // 32 * 32
@@ -530,34 +537,44 @@ class CountBuild:
             raise RuntimeError(f"k={k}: an emit region overflowed")
         return regions, R, ev_count, dhist, nseg
 
-    def _part_emit_lists(self, k, vi, bm_in, bm_out, shards, regions, flags):
-        """_part_emit of a list level whose shards all scan the same levels: one position list over all of them (the
-        set bits of the previous level's bitmap from the first shard's start to the last one's end) and one list scan,
-        instead of a list and a scan per shard; seg = (regions, R, ev_count, dhist, grid)."""
+    def _part_emit_all(self, k, vi, bm_in, bm_out, shards, regions, flags, mode):
+        """_part_emit of a level whose shards all scan the same levels, in one launch over all of them (from the first
+        shard's start to the last one's end): a lane per position (mode 0), the LDS-listed set positions (2), or one
+        position list of the previous level's set bits and one list scan (3), instead of one of each per shard;
+        seg = (regions, R, ev_count, dhist, grid)."""
         elib, dev, G = self.elib, self.tok.device, self.grid
         lo = self.starts[shards[0]]
         hi = self.starts[shards[-1]] + (self.sizes[shards[-1]] + 31) // 32 * 32
         for i in shards:
             torch.cuda.current_stream().wait_event(self.events[i])
-        n_max = hi - lo
-        R = -(-max(n_max, 1) // (G * 256)) * 256  # a list scan's block emits at most 256 per round
+        n = hi - lo
+        if mode == 3:
+            R = -(-max(n, 1) // (G * 256)) * 256  # a list scan's block emits at most 256 per round
+        else:
+            R = emit_region(n, G)
         if G * R > regions.numel():
-            raise RuntimeError(f"k={k}: the emit regions are too small for one list scan")
-        if self._plist is None or self._plist.numel() < n_max:
-            self._plist = torch.empty(n_max + 64, dtype=torch.int64, device=dev)
-        n_list = torch.zeros(1, dtype=torch.int64, device=dev)
+            raise RuntimeError(f"k={k}: the emit regions are too small for one scan over every shard")
         ev_count = torch.zeros(G, dtype=torch.int32, device=dev)
         last = self.events_of.get(k)
         dhist = torch.empty(256 * G, dtype=torch.int32, device=dev) \
             if last is None or last >= partcount.SEG_MIN_EVENTS * G else None
-        b0, b1 = self._event("bits_list", k, -1, n_max)
-        b0.record()
-        elib.cub("ng_bits_list", bm_in[lo // 32 :], n_max // 32, self._plist, n_list)
-        b1.record()
-        e0, e1 = self._event("scan_emit", k, -1, n_max)
+        if mode == 3:
+            if self._plist is None or self._plist.numel() < n:
+                self._plist = torch.empty(n + 64, dtype=torch.int64, device=dev)
+            n_list = torch.zeros(1, dtype=torch.int64, device=dev)
+            b0, b1 = self._event("bits_list", k, -1, n)
+            b0.record()
+            elib.cub("ng_bits_list", bm_in[lo // 32 :], n // 32, self._plist, n_list)
+            b1.record()
+        e0, e1 = self._event("scan_emit", k, -1, n)
         e0.record()
-        elib("ng_scan_emit_list", self.tok[lo:], self._plist, n_list, i32(k), vi.table, u64(vi.cap), vi.rep, self.x,
-             bm_out[lo // 32 :], regions, u64(R), ev_count, flags, i32(G), dhist, G)
+        if mode == 3:
+            elib("ng_scan_emit_list", self.tok[lo:], self._plist, n_list, i32(k), vi.table, u64(vi.cap), vi.rep,
+                 self.x, bm_out[lo // 32 :], regions, u64(R), ev_count, flags, i32(G), dhist, G)
+        else:
+            elib("ng_scan_emit", self.tok[lo:], n, i32(k), None if bm_in is None else bm_in[lo // 32 :],
+                 bm_out[lo // 32 :], vi.table, u64(vi.cap), vi.rep, self.x, regions, u64(R), ev_count, flags, i32(G),
+                 i32(mode), dhist, G)
         e1.record()
         if int(flags[0].item()) & 4:
             raise RuntimeError(f"k={k}: an emit region overflowed")
