@@ -590,8 +590,9 @@ extern "C" int ng_scan_exist(const u16* tok, i64 L, int k, const u32* bm_in, u32
 namespace {
 // The counting scan of a level whose existence scan stored each hit position's context id (ids): per position p set
 // in bm, a context id whose bit is set in `final` emits mix64(id << 16 | tok[p]) as ng_scan_emit's events. A wave
-// takes 8 bitmap words (256 positions) per step, a lane 4 consecutive positions: their ids in one 16-byte load and
-// their tokens in one 8-byte load, the 4 final-bit loads together; a step whose words are all empty is skipped.
+// loads 64 bitmap words (2048 positions) at a time, skips them if all are empty, else walks them 8 words (256
+// positions) per step, a lane 4 consecutive positions: their ids in one 16-byte load and their tokens in one 8-byte
+// load, the 4 final-bit loads together; a step whose words are all empty is skipped.
 __global__ void __launch_bounds__(256) scan_ids_k(const u16* __restrict__ tok, i64 L, const u32* __restrict__ bm,
                                                   const u32* __restrict__ ids, const u32* __restrict__ final,
                                                   EmitSink sink, u32* flags) {
@@ -601,28 +602,30 @@ __global__ void __launch_bounds__(256) scan_ids_k(const u16* __restrict__ tok, i
     const i64 nwords = (L + 31) >> 5;
     const i64 wave = (blockIdx.x * (i64)blockDim.x + threadIdx.x) / WAVE;
     const i64 nwaves = (i64)gridDim.x * (blockDim.x / WAVE);
-    for (i64 w0 = wave * 8; w0 < nwords; w0 += nwaves * 8) {
-        const i64 wi = w0 + (lane & 7);
-        const u32 wd = (lane < 8 && wi < nwords) ? bm[wi] : 0u;
-        const u32 word = (u32)__shfl((int)wd, lane >> 3, WAVE);
-        const u32 bits = (word >> ((lane & 7) * 4)) & 0xFu;
-        if (__ballot(bits != 0u) == 0ull) continue;  // wave-uniform
-        const i64 p0 = (w0 << 5) + 4 * (i64)lane;
-        u32 id[4] = {0, 0, 0, 0};
-        u32 t[4] = {0, 0, 0, 0};
-        if (bits) {  // a set bit lies below L, and so does its whole 4-aligned group (L is a multiple of 32)
-            const uint4 iv = *(const uint4*)(ids + p0);
-            const ushort4 tv = *(const ushort4*)(tok + p0);
-            id[0] = iv.x, id[1] = iv.y, id[2] = iv.z, id[3] = iv.w;
-            t[0] = tv.x, t[1] = tv.y, t[2] = tv.z, t[3] = tv.w;
-        }
-        u32 fw[4];
+    for (i64 g0 = wave * 64; g0 < nwords; g0 += nwaves * 64) {
+        const u32 wl = g0 + lane < nwords ? bm[g0 + lane] : 0u;  // 64 words (2048 positions) per load
+        if (__ballot(wl != 0u) == 0ull) continue;                   // wave-uniform
+        for (int sub = 0; sub < 8; ++sub) {                          // 8 words (256 positions) per step
+            const u32 word = (u32)__shfl((int)wl, 8 * sub + (lane >> 3), WAVE);
+            const u32 bits = (word >> ((lane & 7) * 4)) & 0xFu;
+            if (__ballot(bits != 0u) == 0ull) continue;  // wave-uniform
+            const i64 p0 = ((g0 + 8 * sub) << 5) + 4 * (i64)lane;
+            u32 id[4] = {0, 0, 0, 0};
+            u32 t[4] = {0, 0, 0, 0};
+            if (bits) {  // a set bit lies below L, and so does its whole 4-aligned group (L is a multiple of 32)
+                const uint4 iv = *(const uint4*)(ids + p0);
+                const ushort4 tv = *(const ushort4*)(tok + p0);
+                id[0] = iv.x, id[1] = iv.y, id[2] = iv.z, id[3] = iv.w;
+                t[0] = tv.x, t[1] = tv.y, t[2] = tv.z, t[3] = tv.w;
+            }
+            u32 fw[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) fw[i] = ((bits >> i) & 1u) ? final[id[i] >> 5] : 0u;
+            for (int i = 0; i < 4; ++i) fw[i] = ((bits >> i) & 1u) ? final[id[i] >> 5] : 0u;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const bool hit = (fw[i] >> (id[i] & 31)) & 1u;
-            emit_wave(sink, &ss, __ballot(hit), hit, ((u64)id[i] << 16) | t[i], p0 + i, flags);
+            for (int i = 0; i < 4; ++i) {
+                const bool hit = (fw[i] >> (id[i] & 31)) & 1u;
+                emit_wave(sink, &ss, __ballot(hit), hit, ((u64)id[i] << 16) | t[i], p0 + i, flags);
+            }
         }
     }
     sink_end(sink, &ss);
