@@ -164,3 +164,29 @@ def test_context_hints_from_an_earlier_build(corpus):
             o = O.query_counts(corpus.train, corpus.bounds, xs, ts, av, k, cnt_top=1 << 30, ntop=4)
             assert np.array_equal(out[0, li].view(np.uint32), o["tot"]), (len(q), k)
             assert np.array_equal(out[2, li].view(np.uint32), o["cnt"]), (len(q), k)
+
+
+@pytest.mark.parametrize("mode", ["part", "engine"])
+def test_counts_from_device_tokens(corpus, mode):
+    """CountBuild.from_device (the shards already laid out in GPU memory, as the benchmark builds): every level's scan
+    is one launch over all the shards, the first level included; tot / dist / cnt and the top-4 match the oracle, in
+    a first build and in a second that uses the first one's densities and sizes."""
+    from ngram_amd.gpu_val_stats import load_shards
+
+    lib = C.record_lib()
+    tok, sizes, starts, L = load_shards(corpus.shards())
+    cb = C.CountBuild.from_device(tok, sizes, starts, levels=LEVELS, level_shards={}, topk=4)
+    cb.mode = mode
+    x, tgt, avail = C.queries(corpus.query, [], "cuda", lib)
+    ref = _reference(corpus, LEVELS, {})
+    for stats in (True, False):
+        out = cb.counts(x, tgt, avail, stats=stats).cpu().numpy()
+        top_tok = cb.top_tok.cpu().numpy().view(np.uint16)
+        top_cnt = cb.top_cnt.cpu().numpy().view(np.uint32)
+        for li, k in enumerate(LEVELS):
+            o = ref[k]
+            assert np.array_equal(out[0, li].view(np.uint32), o["tot"]), (stats, k)
+            assert np.array_equal(out[1, li].astype(np.uint16), o["dist"]), (stats, k)
+            assert np.array_equal(out[2, li].view(np.uint32), o["cnt"]), (stats, k)
+            assert np.array_equal(top_tok[li], o["top_tok"][:, :4]), (stats, k)
+            assert np.array_equal(top_cnt[li], o["top_cnt"][:, :4]), (stats, k)
