@@ -15,7 +15,7 @@ import numpy as np
 import torch
 
 from .count_table import CountTable
-from .data import BOS, HEADER_BYTES, shard_tokens
+from .data import HEADER_BYTES, shard_tokens
 
 LEVELS = (6, 10, 20)
 
