@@ -15,7 +15,9 @@ def _t(a):
 
 
 @pytest.mark.parametrize("n,b0,b1,dups", [(1, 0, 64, 0), (4095, 0, 64, 0), (4097, 0, 64, 16), (100_003, 16, 40, 1000),
-                                           (300_000, 0, 64, 50), (70_000, 8, 8, 0), (65_536, 0, 12, 3)])
+                                           (300_000, 0, 64, 50), (70_000, 8, 8, 0), (65_536, 0, 12, 3),
+                                           # 256 tiles (the scatter scans the digit counts itself), then 257 and more
+                                           (2_097_152, 0, 64, 0), (2_097_153, 16, 48, 7), (5_000_000, 0, 40, 100)])
 def test_sort_pairs_is_a_stable_radix_sort(lib, n, b0, b1, dups):
     rng = np.random.default_rng(n + b0)
     keys = rng.integers(0, 2 ** 63, size=n, dtype=np.int64).astype(np.uint64) * np.uint64(2) + \
