@@ -414,6 +414,7 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
 // NULL; with nstat: the contexts counted in nstat[1..256] (their sum) and, with deep, each context of more than
 // deep_min pairs appended to deep (nstat[0] of them; callers size deep for U / (deep_min + 1) + 1).
 #define SUMMARY_AHEAD 4  // windows of a long context loaded per step
+#define SUMMARY_SHORT 12  // the longest context a lane walks alone within a window
 
 template <int KT>
 __global__ void __launch_bounds__(256) ctx_summary_k(const u64* __restrict__ w, i64 U, int cb,
@@ -457,23 +458,56 @@ __global__ void __launch_bounds__(256) ctx_summary_k(const u64* __restrict__ w, 
         u64 ahead = 0;
         if (opens && wv * WAVE + WAVE + lane < U) ahead = w[wv * WAVE + WAVE + lane];
         __syncthreads();
-        if (head) {
-            const u64 after = tails >> lane;  // this lane's context ends at the first tail from here, if any
-            if (after) {
-                const int e = lane + __ffsll((unsigned long long)after) - 1;  // its last word's lane
-                u64 tl[KT];
+        // a context that starts and ends in the window: walked by its first lane from LDS when short; a long one
+        // (more than SUMMARY_SHORT words) by the whole wave below, one word per lane, so that one lane's long walk
+        // does not hold up the wave
+        int e = -1;  // this head's last word's lane
+        if (head && (tails >> lane)) e = lane + __ffsll((unsigned long long)(tails >> lane)) - 1;
+        const bool walk = e >= 0 && e - lane + 1 <= SUMMARY_SHORT;
+        u64 longs = __ballot(e >= 0 && !walk);
+        if (walk) {
+            u64 tl[KT];
 #pragma unroll
-                for (int r = 0; r < KT; ++r) tl[r] = 0;
-                u64 s = 0;
-                for (int j = lane; j <= e; ++j) {
-                    const u64 wj = sw[wid][j];
-                    const u32 n = count_of(wj);
-                    s += n;
-                    topk_insert<KT>(tl, rank_score(wj >> csh, n));
+            for (int r = 0; r < KT; ++r) tl[r] = 0;
+            u64 s = 0;
+            for (int j = lane; j <= e; ++j) {
+                const u64 wj = sw[wid][j];
+                const u32 n = count_of(wj);
+                s += n;
+                topk_insert<KT>(tl, rank_score(wj >> csh, n));
+            }
+            done(ctx, (u32)(e - lane + 1));
+            store_record<KT>(rec, ctx, s, (u32)(e - lane + 1), tl, (u64)i);
+            if (s >> 32) atomicOr(&flags[0], 4u);
+        }
+        while (longs) {  // wave-uniform
+            const int h = __ffsll((unsigned long long)longs) - 1;
+            longs &= longs - 1;
+            const int eh = __shfl(e, h, WAVE);
+            const bool in = lane >= h && lane <= eh;
+            const u32 n = in ? count_of(word) : 0u;
+            u64 part = n;
+            u64 sc = in ? rank_score(word >> csh, n) : 0;
+#pragma unroll
+            for (int d = WAVE / 2; d > 0; d >>= 1) part += shfl_down_u64(part, d);
+            part = bcast_u64(part, 0);
+            u64 top[KT];
+#pragma unroll
+            for (int r = 0; r < KT; ++r) {  // KT rounds of a wave-wide maximum (scores are distinct within a context)
+                u64 m = sc;
+#pragma unroll
+                for (int d = WAVE / 2; d > 0; d >>= 1) {
+                    const u64 o = shfl_down_u64(m, d);
+                    m = o > m ? o : m;
                 }
-                done(ctx, (u32)(e - lane + 1));
-                store_record<KT>(rec, ctx, s, (u32)(e - lane + 1), tl, (u64)i);
-                if (s >> 32) atomicOr(&flags[0], 4u);
+                m = bcast_u64(m, 0);
+                top[r] = m;
+                if (m != 0 && sc == m) sc = 0;
+            }
+            if (lane == h) {
+                done(ctx, (u32)(eh - h + 1));
+                store_record<KT>(rec, ctx, part, (u32)(eh - h + 1), top, (u64)i);
+                if (part >> 32) atomicOr(&flags[0], 4u);
             }
         }
         // the context running past the window: the whole wave, over the following windows
