@@ -116,6 +116,8 @@ __global__ void online_scores_k(const u64* __restrict__ uk, const i64* __restric
     score[i] = ((u64)c << 16) | (0xFFFFu - (u32)(key & 0xFFFF));
 }
 
+#define ONLINE_SHORT 12  // the longest context of a step's pairs a lane walks alone within a window
+
 __device__ __forceinline__ void top8_insert(u64 (&t)[8], u64 v) {
 #pragma unroll
     for (int j = 0; j < 8; ++j)
@@ -130,8 +132,8 @@ __device__ __forceinline__ void top8_insert(u64 (&t)[8], u64 v) {
 // scores, count << 16 | 65535 - token), a wave per window of 64: for each context starting in the window, its total
 // and distinct count grow by the step's occurrences and first-seen pairs (plain stores by the context's first lane: no
 // same-address atomics for hot contexts), and (ctx_top not NULL) its top-E list is merged with the new scores (an old
-// entry of a touched token is superseded by its new score: counts only grow). A context ending in its window is done
-// by its first lane from LDS; the one running past the window by the whole wave.
+// entry of a touched token is superseded by its new score: counts only grow). A short context ending in its window is
+// done by its first lane from LDS; a long one, and the one running past the window, by the whole wave.
 __global__ void __launch_bounds__(256) online_top_k(const u64* __restrict__ uk, const u64* __restrict__ score,
                                                     const u32* __restrict__ agg, const i64* __restrict__ n_ptr, i64 m,
                                                     u64* __restrict__ ctx_top, int E, u32* __restrict__ ctx_tot,
@@ -162,8 +164,9 @@ __global__ void __launch_bounds__(256) online_top_k(const u64* __restrict__ uk, 
         const bool tail = valid && (next == EMPTY || ctx_of(next) != c);
         const u64 tails = __ballot(tail);
         __syncthreads();
-        if (head && (tails >> lane)) {  // the context ends in the window: this lane alone, from LDS
-            const int e = lane + __ffsll((unsigned long long)(tails >> lane)) - 1;
+        int e = -1;  // where this head's context ends, if in the window
+        if (head && (tails >> lane)) e = lane + __ffsll((unsigned long long)(tails >> lane)) - 1;
+        if (e >= 0 && e - lane + 1 <= ONLINE_SHORT) {  // a short context ending in the window: this lane alone, from LDS
             u32 add = 0, fresh = 0;
             u64 t[8];
 #pragma unroll
@@ -190,20 +193,25 @@ __global__ void __launch_bounds__(256) online_top_k(const u64* __restrict__ uk, 
                 for (int r = 0; r < E; ++r) top[r] = t[r];
             }
         }
+        // the whole wave takes the context running past the window (over the following windows) and the long ones
+        // ending in it (one pair per lane: one lane's long walk would hold up the wave)
         const bool open = head && !(tails >> lane);
-        const u64 opens = __ballot(open);
-        if (opens) {  // the context running past the window: the whole wave, over the following windows
-            const int h = __ffsll((unsigned long long)opens) - 1;
+        u64 waved = __ballot(open || (e >= 0 && e - lane + 1 > ONLINE_SHORT));
+        while (waved) {  // wave-uniform
+            const int h = __ffsll((unsigned long long)waved) - 1;
+            waved &= waved - 1;
+            const int eh = __shfl(e, h, WAVE);  // -1: the context runs past the window
             const u64 hc = bcast_u64(c, h);
             const i64 gi = wv * WAVE + h;
-            const bool in = valid && lane >= h;
+            const bool in = valid && lane >= h && (eh < 0 || lane <= eh);
             u64 add = in ? ag : 0, fresh = (in && (u32)(sc >> 16) == ag) ? 1 : 0;
             u64 lt[8];
 #pragma unroll
             for (int r = 0; r < 8; ++r) lt[r] = 0;
             if (in && ctx_top) lt[0] = sc;
-            i64 ge = wv * WAVE + WAVE;  // the group's end, found below
-            bool cont = true;
+            i64 ge = wv * WAVE + eh + 1;  // the group's end (found below for an open context)
+            bool cont = eh < 0;
+            if (cont) ge = wv * WAVE + WAVE;
             for (i64 nx = wv * WAVE + WAVE; cont; nx += WAVE) {
                 const i64 j = nx + lane;
                 const u64 k2 = j < n ? uk[j] : EMPTY;
