@@ -15,22 +15,23 @@ from .lib import Lib, i32, u64
 TAIL = 4096  # slots past cap that linear probing may run into; the last stays empty
 LOAD = 0.4  # contexts per slot aimed at: measured at c3, 0.4 gives the fastest scans (0.5 +10%, 0.66 +50%)
 SHRINK = 2.0  # a table more than this many times the size its contexts need moves to one of that size
-EXPECT_MARGIN = 1.2  # a table sized from an expected context count holds this many times that count at LOAD
+EXPECT_MARGIN = 1.2  # a table sized from an expected context count holds this many times it at LOAD (1 at least)
 
 
 class QueryIndex:
     def __init__(self, lib: Lib, x: torch.Tensor, avail: torch.Tensor, k: int, positions: torch.Tensor | None = None,
-                 compact: bool = False, expect: int | None = None):
+                 compact: bool = False, expect: int | None = None, _resized: bool = False):
         """Index the valid k-contexts of the query positions (all of x, or the int32 `positions`). `compact`: ctx_of
         holds one entry per listed position (in their order) instead of one per position of x. `expect`: about how
         many contexts there are (e.g. the last build's count): the table is sized for them at once instead of for
-        every position and shrunk; if they turn out many more, the index is built again at their size."""
+        every position and shrunk; if they turn out more than the table holds at LOAD, the index is built once more,
+        sized for the count found (`_resized` marks that second build, which keeps its table whatever its load)."""
         dev = x.device
         N = x.numel()
         m = N if positions is None else int(positions.numel())
         cap = int(m / LOAD) + 1024
         if expect is not None:
-            cap = min(cap, int(max(expect, 1) * EXPECT_MARGIN / LOAD) + 1024)
+            cap = min(cap, int(max(expect, 1) * max(EXPECT_MARGIN, 1.0) / LOAD) + 1024)
         while True:
             slots = cap + TAIL
             table = torch.full((slots,), -1, dtype=torch.int64, device=dev)
@@ -51,8 +52,8 @@ class QueryIndex:
         if c[2]:
             raise RuntimeError(f"k={k}: {c[2]} query positions collide with another context's key")
         n_ctx = int(c[0])
-        if expect is not None and n_ctx > EXPECT_MARGIN * LOAD * cap:  # far more contexts than expected: their size
-            self.__init__(lib, x, avail, k, positions, compact, n_ctx)
+        if expect is not None and not _resized and n_ctx > LOAD * cap:  # fuller than LOAD: once more, at their size
+            self.__init__(lib, x, avail, k, positions, compact, n_ctx, _resized=True)
             return
         if m and cap > SHRINK * (n_ctx / LOAD) + 4096:
             # sized for every position, used by far fewer contexts: move them to a table sized for them (fewer bits

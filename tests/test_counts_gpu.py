@@ -148,9 +148,14 @@ def test_fit_blocks_start_segments(corpus):
     assert np.array_equal(av, data.segments(xs, breaks=[1000, 1299]))
 
 
-def test_context_hints_from_an_earlier_build(corpus):
+@pytest.mark.parametrize("margin", [1.2, 0.5])
+def test_context_hints_from_an_earlier_build(corpus, monkeypatch, margin):
     """A build sizes its query indexes from the last build's context counts: far fewer contexts than expected (the
-    tables shrink), then far more (the indexes are built again at their size); every build matches the oracle."""
+    tables shrink), then far more (the indexes are built again at their size); every build matches the oracle. A
+    margin below 1 (every table fuller than its aimed load) still builds each index at most twice."""
+    from ngram_amd import qindex as Q
+
+    monkeypatch.setattr(Q, "EXPECT_MARGIN", margin)
     lib = C.record_lib()
     cb = C.CountBuild(corpus.shards(), levels=LEVELS, level_shards={}, topk=4)
     cb.start_load(1)
