@@ -485,7 +485,7 @@ class CountBuild:
 
     def _part_emit(self, k, vi, bms, regions, R):
         """Level k's scan of every shard it counts, hits emitted to per-block regions with each block's top-digit
-        histogram: count_events' seg = (regions, R, ev_count, dhist, nseg)."""
+        histogram: count_events' seg = (regions, R, ev_count, dhist, nseg, flags)."""
         elib, dev, G = self.elib, self.tok.device, self.grid
         shards = [i for i in range(len(self.sizes)) if i < self.level_shards[k]]
         nseg = len(shards) * G
@@ -533,15 +533,13 @@ class CountBuild:
                      vi.rep, self.x, regions[j * G * R :], u64(R), ev_count[j * G :], flags, i32(G), i32(mode),
                      dhist[j * G :] if dhist is not None else None, nseg)
             e1.record()
-        if int(flags[0].item()) & 4:
-            raise RuntimeError(f"k={k}: an emit region overflowed")
-        return regions, R, ev_count, dhist, nseg
+        return regions, R, ev_count, dhist, nseg, flags  # count_events checks the flags with its first read
 
     def _part_emit_all(self, k, vi, bm_in, bm_out, shards, regions, flags, mode):
         """_part_emit of a level whose shards all scan the same levels, in one launch over all of them (from the first
         shard's start to the last one's end): a lane per position (mode 0), the LDS-listed set positions (2), or one
         position list of the previous level's set bits and one list scan (3), instead of one of each per shard;
-        seg = (regions, R, ev_count, dhist, grid)."""
+        seg = (regions, R, ev_count, dhist, grid, flags)."""
         elib, dev, G = self.elib, self.tok.device, self.grid
         lo = self.starts[shards[0]]
         hi = self.starts[shards[-1]] + (self.sizes[shards[-1]] + 31) // 32 * 32
@@ -576,9 +574,7 @@ class CountBuild:
                  bm_out[lo // 32 :], vi.table, u64(vi.cap), vi.rep, self.x, regions, u64(R), ev_count, flags, i32(G),
                  i32(mode), dhist, G)
         e1.record()
-        if int(flags[0].item()) & 4:
-            raise RuntimeError(f"k={k}: an emit region overflowed")
-        return regions, R, ev_count, dhist, G
+        return regions, R, ev_count, dhist, G, flags
 
     def _owner_packed(self, li, k, vi, c, tgt, out, want, zero_tops):
         """The owner side from packed pairs: per present context its record (sorted by context, keys only), then per

@@ -89,22 +89,30 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids:
     partitions; a partition found too full repeats the count with one more bit). `lookups` (ctx_of int32 [N], tgt
     int16 [N], positions int32 or None): qcnt[i] = the count of (ctx_of[i], tgt[i]) for the listed positions (all
     without a list), 0 where absent, out of range or not listed. `packed`: pairs as packed words (falls back to keys +
-    counts when the escape table overflows). `seg` (regions, R, ev_count, dhist, nseg): the events straight from an
-    emitting scan's regions with its digit histograms (ng_scan_emit's dhist, digit-major with stride nseg; None: the
-    regions are packed); ev and n_ev are then unused: the first partition pass reads the regions (ng_seg_scatter) and groups by the top 8 bits,
+    counts when the escape table overflows). `seg` (regions, R, ev_count, dhist, nseg[, flags]): the events straight
+    from an emitting scan's regions with its digit histograms (ng_scan_emit's dhist, digit-major with stride nseg;
+    None: the regions are packed) and, if given, the scan's flags (raises on a region overflow, bit 4, before any
+    region is read); ev and n_ev are then unused: the first partition pass reads the regions (ng_seg_scatter) and groups by the top 8 bits,
     the later passes sort the bits below them. `presort` ("ctx" / "pair", packed words only): the words come out
     already through the first pass of summarize's sort (by context / by pair key), read from the count's outputs."""
     msd = 0
+    emit_flags = seg[5] if seg is not None and len(seg) > 5 else None
     if seg is not None and seg[3] is None:  # no digit histograms: the regions are packed
-        regions, R, ev_count, _, nseg = seg
+        regions, R, ev_count, _, nseg = seg[:5]
+        if emit_flags is not None and int(emit_flags[0].item()) & 4:
+            raise RuntimeError("an emit region overflowed")
         ev, n_ev = pack_events(elib, regions, R, ev_count, nseg, event)
     elif seg is not None:
-        regions, R, ev_count, dhist, nseg = seg
+        regions, R, ev_count, dhist, nseg = seg[:5]
         dev = regions.device
         dpre = torch.empty(max(256 * nseg, 1), dtype=torch.int32, device=dev)
-        total = torch.zeros(1, dtype=torch.int64, device=dev)
-        elib.cub("ng_exclusive_scan_u32", dhist, dpre, 256 * nseg, total)
-        n_ev = int(total.item())
+        small = torch.zeros(2, dtype=torch.int64, device=dev)  # [the events, the scan's flags]: one copy
+        elib.cub("ng_exclusive_scan_u32", dhist, dpre, 256 * nseg, small[:1])
+        if emit_flags is not None:
+            small[1:].copy_(emit_flags[:1])
+        n_ev, fl = small.cpu().tolist()
+        if fl & 4:
+            raise RuntimeError("an emit region overflowed")
         if n_ev >= 1 << 32:
             raise RuntimeError(f"{n_ev} events: the region scatter's offsets are 32-bit")
         if n_ev < SEG_MIN_EVENTS * nseg:  # few events per region: packing them costs less than scattering per region
@@ -180,7 +188,8 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids:
         seg_cnt = torch.empty(G2, dtype=torch.int32, device=dev)
         seg_base = torch.empty(G2, dtype=torch.int64, device=dev)
         qcnt = torch.zeros(max(N, 1), dtype=torch.int32, device=dev) if N else None
-        flags = torch.zeros(1, dtype=torch.int32, device=dev)
+        small = torch.zeros(2, dtype=torch.int64, device=dev)  # [the distinct pairs counted, the count's flags]
+        flags = small[1:].view(torch.int32)[:1]
         dshift = dbits = -1
         if presort and cb:  # the lowest digit of the words' sort range, as wide as saves summarize a radix pass
             dshift = 64 - cb - (16 if presort == "pair" else 0)
@@ -193,7 +202,18 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids:
              flags, i32(G2))
         e1.record()
         del sev, sqk, sqv, start, qstart
-        fl = int(flags[0].item())
+        # the pairs' offsets computed before the flags are read (and dropped if the count repeats): one copy returns
+        # both
+        if dhist is not None:  # the words scattered by their lowest sort digit: summarize's first radix pass
+            nb = (1 << dbits) * G2
+            dpre = torch.empty(nb, dtype=torch.int32, device=dev)
+            elib.cub("ng_exclusive_scan_u32", dhist, dpre, nb, small[:1])
+        else:
+            offs = torch.empty(G2 + 1, dtype=torch.int64, device=dev)
+            elib("ng_seg_offsets", seg_cnt, G2, offs)
+            small[:1].copy_(offs[G2:])
+        U, fl = small.cpu().tolist()
+        fl &= 0xFFFFFFFF
         if fl & 2:  # more large counts than the escape table holds: count again, unpacked
             cb = 0
             continue
@@ -204,21 +224,13 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids:
         pbits += 1
     del ev
     counts = None
-    if dhist is not None:  # the words scattered by their lowest sort digit: summarize's first radix pass
-        nb = (1 << dbits) * G2
-        dpre = torch.empty(nb, dtype=torch.int32, device=dev)
-        total = torch.zeros(1, dtype=torch.int64, device=dev)
-        elib.cub("ng_exclusive_scan_u32", dhist, dpre, nb, total)
-        U = int(total.item())
+    if dhist is not None:
         pairs = torch.empty(max(U, 1), dtype=torch.int64, device=dev)
         e0, e1 = event("sort", U)
         e0.record()
         elib("ng_seg_scatter", out_k, u64(0), seg_base, seg_cnt, dpre, G2, i32(dshift), i32(dbits), pairs)
         e1.record()
     else:
-        offs = torch.empty(G2 + 1, dtype=torch.int64, device=dev)
-        elib("ng_seg_offsets", seg_cnt, G2, offs)
-        U = int(offs[G2].item())
         pairs = torch.empty(max(U, 1), dtype=torch.int64, device=dev)
         counts = None if cb else torch.empty(max(U, 1), dtype=torch.int32, device=dev)
         e0, e1 = event("count", U)
@@ -265,20 +277,20 @@ def summarize(elib: Lib, lib: Lib, c: Counted, n_ids: int, ktop: int, zero_recor
         e1.record()
     rec = (torch.zeros if zero_records else torch.empty)((n_ids, RECORD_WORDS[ktop]), dtype=torch.int32, device=dev)
     dist = torch.zeros(n_ids, dtype=torch.int32, device=dev) if with_dist else None
-    nstat = torch.zeros(257, dtype=torch.int32, device=dev)
+    nstat = torch.zeros(258, dtype=torch.int32, device=dev)  # the kernel's statistics, then its flags: one copy
     deep = torch.empty(c.U // (deep_min + 1) + 1, dtype=torch.int64, device=dev) if deep_min is not None else None
-    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    flags = nstat[257:]
     e0, e1 = event("ctx_topk", c.U)
     e0.record()
     elib("ng_ctx_summary", sw, c.U, i32(c.cb), c.esc[0], c.esc[1], u64(ESC_CAP), i32(ktop), rec, dist,
          ctypes.c_uint32(deep_min or 0), deep, nstat, flags)
     e1.record()
-    if int(flags[0].item()) & 4:
-        raise RuntimeError("a total does not fit uint32")
     st = nstat.cpu()
+    if int(st[257]) & 4:
+        raise RuntimeError("a total does not fit uint32")
     if deep is not None:
         deep = deep[: int(st[0])]
-    return Summary(rec, dist, sw, int(st[1:].sum()), deep)
+    return Summary(rec, dist, sw, int(st[1:257].sum()), deep)
 
 
 def record_tops(rec: torch.Tensor, ktop: int):
