@@ -195,3 +195,21 @@ def test_counts_from_device_tokens(corpus, mode):
             assert np.array_equal(out[2, li].view(np.uint32), o["cnt"]), (stats, k)
             assert np.array_equal(top_tok[li], o["top_tok"][:, :4]), (stats, k)
             assert np.array_equal(top_cnt[li], o["top_cnt"][:, :4]), (stats, k)
+
+
+@pytest.mark.parametrize("packed", [False, True])
+def test_emit_region_overflow_raises(corpus, monkeypatch, packed):
+    """A scan whose per-block regions are too small for its hits flags it (the kernel keeps the hits it has room for
+    and writes nothing past its region): the count raises before it reads a region, whether it reads the scan's flags
+    with the event total of the regions' digit histograms or (packed: no histograms, the regions packed) on their
+    own."""
+    lib = C.record_lib()
+    cb = C.CountBuild(corpus.shards(), levels=(2, 3), level_shards={}, topk=4)
+    cb.start_load(1)
+    x, tgt, avail = C.queries(corpus.query, [], "cuda", lib)
+    if packed:
+        cb.counts(x, tgt, avail)  # a first build: its event counts let the next one go without digit histograms
+        monkeypatch.setattr(P, "SEG_MIN_EVENTS", 1 << 40)
+    monkeypatch.setattr(C, "emit_region", lambda L, G: 64)
+    with pytest.raises(RuntimeError, match="emit region overflowed"):
+        cb.counts(x, tgt, avail)
