@@ -259,10 +259,11 @@ def _count_ids(elib: Lib, lib: Lib, tok, L: int, level: tuple, k: int, length, f
     dhist = torch.empty(256 * grid, dtype=torch.int32, device=dev)
     flags.zero_()
     elib("ng_scan_ids_emit", tok, L, bm, ids, final, regions, u64(R), ev_count, flags, i32(grid), dhist, grid)
-    if int(flags[0].item()) & 4:
-        raise RuntimeError(f"k={k}: an emit region overflowed")
-    c = count_events(elib, lib, None, 0, n_ids, _RATIO.get(k, 1.0), seg=(regions, R, ev_count, dhist, grid),
-                     presort="ctx")
+    try:  # the scan's flags read with the event total
+        c = count_events(elib, lib, None, 0, n_ids, _RATIO.get(k, 1.0),
+                         seg=(regions, R, ev_count, dhist, grid, flags), presort="ctx")
+    except RuntimeError as e:
+        raise RuntimeError(f"k={k}: {e}") from None
     del regions
     _RATIO[k] = c.U / max(1, c.n_ev)
     o_tok = torch.zeros(m, dtype=torch.int16, device=dev)
@@ -327,8 +328,8 @@ def _count_batch(elib: Lib, lib: Lib, tok, L: int, x, batch: list, levels: list,
         elib("ng_seg_gather", regions, None, u64(R), None, ev_count, g, offs, ev, None)
         at = offs[g : g + 1].clone()
         del regions, ev_count
-    n_ev = int(at.item())
-    if int(flags[0].item()) & 4:
+    n_ev, fl = torch.cat([at, flags[:1].to(torch.int64)]).tolist()  # one copy
+    if fl & 4:
         raise RuntimeError(f"levels {batch[0][0]}..{batch[-1][0]}: an emit region overflowed")
     key = ("batch", batch[0][0])
     c = count_events(elib, lib, ev, n_ev, n_ids, _RATIO.get(key, 1.0), presort="ctx")
