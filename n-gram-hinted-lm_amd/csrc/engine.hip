@@ -8,7 +8,7 @@
 //   * owner side without a ranking sort: the table compacted, one radix sort by pair key (contexts grouped, tokens
 //     ascending), then per context its total and top-k (count descending, token ascending) by selection in registers,
 //     and per query position tot / dist / cnt (binary search) / top-k in one gather.
-#include "pairs.h"
+#include "probe.h"
 #include "prim.h"
 
 namespace {
@@ -36,7 +36,7 @@ __device__ __forceinline__ void split_add(u64* keys, u32* cnts, u64 cap, u64 key
     atomicOr(&flags[0], 1u);
 }
 
-// What a level scan does with each hit besides setting its bitmap bit (probe_key's pair key: context id << 16 | next):
+// What a level scan does with each hit besides setting its bitmap bit (the lookup's pair key: context id << 16 | next):
 //   CountSink: count it in the split table (once the table has overflowed, only the bitmap is still made: the level
 //              reruns bigger);
 //   ExistSink: flag its context (bit id of the u32 words hit, set by atomicOr only while it reads unset);
@@ -165,9 +165,9 @@ __global__ void __launch_bounds__(256) scan_dense_k(const u16* __restrict__ tok,
         u32 nxt = SENT;
         u64 ck = EMPTY;
         if (p < L) ck = ctx_key_at<K>(tok, p, k, nxt);
-        u64 key = EMPTY;
-        if (((word >> (lane & 31)) & 1u) && nxt != SENT && ck != EMPTY)
-            key = probe_table<K>(tok, p, k, vt, vcap, vrep, x, flags, ck, nxt);
+        Walk wk;
+        walk_seed(vt, vcap, ((word >> (lane & 31)) & 1u) && nxt != SENT ? ck : EMPTY, nxt, wk);
+        const u64 key = walk_end<K, false>(tok, p, k, vt, vrep, x, flags, wk);
         const bool hit = key != EMPTY;
         const u64 b = __ballot(hit);
         if (lane == 0) bm_out[base >> 5] = (u32)b;
@@ -196,7 +196,7 @@ __global__ void __launch_bounds__(256) scan_list_k(const u16* __restrict__ tok, 
         u64 key = EMPTY;
         if (j < n) {
             p = (i64)plist[j];
-            key = probe_key<K>(tok, p, k, vt, vcap, vrep, x, flags);
+            key = walk_lookup<K, false>(tok, p, k, vt, vcap, vrep, x, flags);
         }
         const bool hit = key != EMPTY;
         if (bm_out && hit) atomicOr(&bm_out[p >> 5], 1u << (p & 31));
@@ -223,7 +223,7 @@ __global__ void __launch_bounds__(256) scan_sparse_k(const u16* __restrict__ tok
             word &= word - 1;
             const i64 p = (w << 5) + b;
             if (p >= L) continue;
-            const u64 key = probe_key<K>(tok, p, k, vt, vcap, vrep, x, flags);
+            const u64 key = walk_lookup<K, false>(tok, p, k, vt, vcap, vrep, x, flags);
             if (key != EMPTY) {
                 out |= 1u << b;
                 if constexpr (S::KIND == 2) emit_lane(sink, &ss, key, p, flags);
@@ -275,22 +275,22 @@ __global__ void __launch_bounds__(256) scan_compact_k(const u16* __restrict__ to
         const i64 pbase = (g0 + w * 64) << 5;
         for (u32 r0 = 0; r0 < total; r0 += WAVE * COMPACT_PPL) {  // every lane runs the same rounds
             // COMPACT_PPL probes per lane started together: their first loads are in flight at once
-            u64 key[COMPACT_PPL], sl[COMPACT_PPL], v[COMPACT_PPL];
-            u32 nxt[COMPACT_PPL], lp[COMPACT_PPL];
+            Walk wk[COMPACT_PPL];
+            u32 lp[COMPACT_PPL];
 #pragma unroll
             for (int q = 0; q < COMPACT_PPL; ++q) {
                 const u32 r = r0 + q * WAVE + lane;
-                key[q] = EMPTY;
+                wk[q].key = EMPTY;
                 lp[q] = 0;
                 if (r < total) {
                     lp[q] = list[w][r];
-                    if (pbase + lp[q] < L) probe_start<K>(tok, pbase + lp[q], k, vt, vcap, key[q], sl[q], v[q], nxt[q]);
+                    if (pbase + lp[q] < L) walk_begin<K>(tok, pbase + lp[q], k, vt, vcap, wk[q]);
                 }
             }
 #pragma unroll
             for (int q = 0; q < COMPACT_PPL; ++q) {
                 if (r0 + q * WAVE >= total) break;  // wave-uniform
-                const u64 hk = probe_finish<K>(tok, pbase + lp[q], k, vt, vrep, x, flags, key[q], sl[q], v[q], nxt[q]);
+                const u64 hk = walk_end<K, false>(tok, pbase + lp[q], k, vt, vrep, x, flags, wk[q]);
                 const bool hit = hk != EMPTY;
                 if (hit) atomicOr(&words[w][lp[q] >> 5], 1u << (lp[q] & 31));
                 if constexpr (S::KIND == 2)
@@ -335,11 +335,11 @@ template <class S>
 static int launch_scan(const u16* tok, i64 L, int k, const u32* bm_in, u32* bm_out, const u64* vt, u64 vcap,
                         const u32* vrep, const u16* x, const S& sink, u32* flags, int grid, int sparse, hipStream_t st) {
     if (sparse == 2 && bm_in) {
-        LEVEL_SWITCH(k, (scan_compact_k<K, S><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, sink, flags)));
+        LEVEL_DISPATCH(k, (scan_compact_k<K, S><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, sink, flags)));
     } else if (sparse && bm_in) {
-        LEVEL_SWITCH(k, (scan_sparse_k<K, S><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, sink, flags)));
+        LEVEL_DISPATCH(k, (scan_sparse_k<K, S><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, sink, flags)));
     } else {
-        LEVEL_SWITCH(k, (scan_dense_k<K, S><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, sink, flags)));
+        LEVEL_DISPATCH(k, (scan_dense_k<K, S><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, sink, flags)));
     }
     return 0;
 }
@@ -703,7 +703,7 @@ extern "C" int ng_scan_emit_list(const u16* tok, const u64* plist, const u64* n_
     if (grid <= 0 || n_dev == nullptr || region == 0 || region > 0xFFFFFFFFull || (dhist && dstride < grid)) return -1;
     const EmitSink sk{ev, region, ev_count, 0, nullptr, dhist, dstride};
     hipStream_t st = (hipStream_t)stream;
-    LEVEL_SWITCH(k, (scan_list_k<K, EmitSink><<<grid, 256, 0, st>>>(tok, plist, 0, k, vt, vcap, vrep, x, sk, flags, n_dev,
+    LEVEL_DISPATCH(k, (scan_list_k<K, EmitSink><<<grid, 256, 0, st>>>(tok, plist, 0, k, vt, vcap, vrep, x, sk, flags, n_dev,
                                                                      bm_out)));
     return (int)hipGetLastError();
 }
@@ -719,7 +719,7 @@ extern "C" int ng_scan_list_dev(const u16* tok, int k, const u64* plist, const u
         return -1;
     const EmitSink sk{ev, region, ev_count, what, hit, nullptr, 0, key_add};
     hipStream_t st = (hipStream_t)stream;
-    LEVEL_SWITCH(k, (scan_list_k<K, EmitSink><<<grid, 256, 0, st>>>(tok, plist, n_max, k, vt, vcap, vrep, x, sk, flags,
+    LEVEL_DISPATCH(k, (scan_list_k<K, EmitSink><<<grid, 256, 0, st>>>(tok, plist, n_max, k, vt, vcap, vrep, x, sk, flags,
                                                                      n_dev, nullptr)));
     return (int)hipGetLastError();
 }
@@ -743,10 +743,10 @@ extern "C" int ng_scan_sink(const u16* tok, i64 L, int k, const u32* bm_in, u32*
         }
         if (ev) {
             const EmitSink sk{ev, region, ev_count, what, hit, nullptr, 0, key_add};
-            LEVEL_SWITCH(k, (scan_list_k<K, EmitSink><<<grid, 256, 0, st>>>(tok, plist, n, k, vt, vcap, vrep, x, sk, flags,
+            LEVEL_DISPATCH(k, (scan_list_k<K, EmitSink><<<grid, 256, 0, st>>>(tok, plist, n, k, vt, vcap, vrep, x, sk, flags,
                                                                              nullptr, nullptr)));
         } else {
-            LEVEL_SWITCH(k, (scan_list_k<K, ExistSink><<<grid, 256, 0, st>>>(tok, plist, n, k, vt, vcap, vrep, x,
+            LEVEL_DISPATCH(k, (scan_list_k<K, ExistSink><<<grid, 256, 0, st>>>(tok, plist, n, k, vt, vcap, vrep, x,
                                                                               ExistSink{hit, nullptr}, flags, nullptr, nullptr)));
         }
         return (int)hipGetLastError();
@@ -871,7 +871,7 @@ extern "C" int ng_features(const int* counts, int L, i64 n, int nb, float* tot, 
 // ---------------------------------------------------------------------------------------------------------------
 // The engine's query index: the distinct valid query contexts inserted into an open-addressing table by
 // compare-and-swap (no sort). Slot = context id; linear probing without wrap-around from umulhi(key, cap) over a
-// table of cap + tail slots whose last slot stays empty, which is the layout probe_key walks. rep[slot] = the
+// table of cap + tail slots whose last slot stays empty, which is the layout probe.h walks. rep[slot] = the
 // query position whose compare-and-swap inserted the context. The canonical, sorted layout of gpu_val_stats'
 // ValIndex is only needed for ids that agree across ranks; on one GPU any layout is exact. No kernel here adds to a
 // single global counter per thread or per wave: same-address atomics serialize (about 80 M/s on MI355X), so counts
@@ -889,7 +889,7 @@ __global__ void qindex_insert_k(const u16* __restrict__ x, const int* __restrict
         const i64 i = pos ? pos[j] : j;
         i64 slot = -1;
         if (avail[i] >= (K > 0 ? K : k)) {
-            const u64 key = key_at<K>(x + i + 1, k);
+            const u64 key = qctx_key<K>(x + i + 1, k);
             u64 s = __umul64hi(key, cap);
             while (true) {
                 if (s + 1 >= slots) {  // the last slot must stay empty
@@ -1009,7 +1009,7 @@ extern "C" int ng_query_index(const u16* x, const int* avail, const int* pos, i6
     if (n <= 0) return 0;
     if (cap == 0 || slots <= cap || slots > (1ull << 31)) return -1;
     hipStream_t st = (hipStream_t)stream;
-    LEVEL_SWITCH(k, (qindex_insert_k<K><<<grid_for(n, 256), 256, 0, st>>>(x, avail, pos, n, k, table, cap, slots, rep, ctx_of, compact, counters)));
+    LEVEL_DISPATCH(k, (qindex_insert_k<K><<<grid_for(n, 256), 256, 0, st>>>(x, avail, pos, n, k, table, cap, slots, rep, ctx_of, compact, counters)));
     if (k > 4) qindex_verify_k<<<grid_for(n, 256), 256, 0, st>>>(x, pos, n, k, ctx_of, compact, rep, counters + 2);
     const int g = grid_for((i64)slots, 256);
     count_occupied_k<<<g < 1024 ? g : 1024, 256, 0, st>>>(table, slots, counters);
@@ -1091,7 +1091,7 @@ extern "C" int ng_query_index_dev(const u16* x, const int* avail, const int* pos
     hipStream_t st = (hipStream_t)stream;
     fill_u32_n((u32*)table, 0xFFFFFFFFu, (i64)(2 * slots), st);
     if (n_max == 0) return (int)hipGetLastError();
-    LEVEL_SWITCH(k, (qindex_insert_k<K><<<grid_for(n_max, 256), 256, 0, st>>>(x, avail, pos, n_max, k, table, cap, slots,
+    LEVEL_DISPATCH(k, (qindex_insert_k<K><<<grid_for(n_max, 256), 256, 0, st>>>(x, avail, pos, n_max, k, table, cap, slots,
                                                                                 rep, ctx_of, 1, counters, n_dev)));
     if (k > 4)
         qindex_verify_k<<<grid_for(n_max, 256), 256, 0, st>>>(x, pos, n_max, k, ctx_of, 1, rep, counters + 2, n_dev);

@@ -11,7 +11,7 @@
 // key, and summarized per context into records (total, pairs, top 8, first word). A query reads its context's record
 // and finds its target's count by a binary search of the context's words; the CNT_TOP rule (count_table.rs:146-158
 // deep_last) compares its score with thr[c], the CNT_TOP-th largest score of a context with more pairs than that.
-#include "pairs.h"
+#include "probe.h"
 #include "part.h"
 
 namespace {
@@ -132,8 +132,8 @@ __global__ void __launch_bounds__(256) table_query_k(const u16* __restrict__ x, 
                                                      int* __restrict__ out_dist, int* __restrict__ out_cnt,
                                                      u16* __restrict__ out_tok, u32* __restrict__ out_tcnt) {
     const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
-    if (i >= n || avail[i] < klen<K>(k)) return;
-    const i64 c = ctx_find(ck, ccap, key_at<K>(x + i + 1, k));
+    if (i >= n || avail[i] < ctx_len<K>(k)) return;
+    const i64 c = ctx_find(ck, ccap, qctx_key<K>(x + i + 1, k));
     if (c < 0) return;
     u32 v[Rec8::WORDS];
     const uint4* src = (const uint4*)(rec + c * Rec8::WORDS);
@@ -238,7 +238,7 @@ extern "C" int ng_table_emit(const u16* tok, i64 L, int k, u64* ck, u64 ccap, u6
     if (ccap == 0 || ccap > (1ull << 31)) return -1;
     if (grid <= 0) grid = grid_for(L, 256);
     hipStream_t st = (hipStream_t)stream;
-    LEVEL_SWITCH(k, (table_emit_k<K><<<grid, 256, 0, st>>>(tok, L, k, ck, ccap, ev, flags)));
+    LEVEL_DISPATCH(k, (table_emit_k<K><<<grid, 256, 0, st>>>(tok, L, k, ck, ccap, ev, flags)));
     return (int)hipGetLastError();
 }
 
@@ -274,7 +274,7 @@ extern "C" int ng_table_query(const u16* x, const int* avail, const u16* tgt, i6
     if (kout > 0 && (out_tok == nullptr || out_tcnt == nullptr)) return -1;
     if (n <= 0) return 0;
     hipStream_t st = (hipStream_t)stream;
-    LEVEL_SWITCH(k, (table_query_k<K><<<grid_for(n, 256), 256, 0, st>>>(x, avail, tgt, n, k, ck, ccap, w, cb, esc_k,
+    LEVEL_DISPATCH(k, (table_query_k<K><<<grid_for(n, 256), 256, 0, st>>>(x, avail, tgt, n, k, ck, ccap, w, cb, esc_k,
                                                                          esc_c, esc_cap, rec, thr, cnt_top, kout,
                                                                          out_tot, out_dist, out_cnt, out_tok, out_tcnt)));
     return (int)hipGetLastError();

@@ -20,9 +20,9 @@ LIB_NAME = "libngram_amd.so"
 RECORD_LIB_NAME = "libngram_amd_record.so"
 # each library's sources (relative to csrc/); an object shared by both is compiled once
 LIBS = {
-    LIB_NAME: ["prim.hip", "common_abi.hip", "gvs_abi.hip", "gen.hip", "engine.hip", "part.hip", "table.hip",
+    LIB_NAME: ["prim.hip", "abi/owner.hip", "abi/gvs.hip", "gen.hip", "engine.hip", "part.hip", "table.hip",
                "online.hip", "rows.hip"],
-    RECORD_LIB_NAME: ["prim.hip", "common_abi.hip", "record/record_abi.hip"],
+    RECORD_LIB_NAME: ["prim.hip", "abi/owner.hip", "abi/record.hip"],
 }
 ARCH = os.environ.get("NGRAM_AMD_ARCH", "gfx950")
 

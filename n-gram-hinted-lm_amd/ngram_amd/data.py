@@ -66,6 +66,38 @@ def read_shard(path: str | os.PathLike) -> np.ndarray:
     return np.memmap(path, dtype="<u2", mode="r", offset=HEADER_BYTES, shape=(n,))
 
 
+GAP = 32  # SENT tokens at least before every shard (and after the last) in a device buffer: >= any short context
+
+
+def pack_layout(sizes: list[int], gap: int = GAP) -> tuple[list[int], int]:
+    """Where shards of `sizes` tokens go in one device buffer: each shard starts on a multiple of 32 (a bitmap word)
+    with at least `gap` SENT tokens before it, and the buffer ends with at least `gap` SENT tokens, its length a
+    multiple of 32. So a context reaching back past its shard's start holds a SENT (and matches no query context), a
+    position whose next token is SENT is not an occurrence, and the scans' bitmaps cover the buffer in whole words.
+    Returns (starts, length)."""
+    starts, end = [], 0
+    for n in sizes:
+        at = -(-(end + gap) // 32) * 32
+        starts.append(at)
+        end = at + int(n)
+    return starts, -(-(end + gap) // 32) * 32
+
+
+def device_tokens(shards: list, device="cuda"):
+    """Shards (uint16 arrays, or shard file paths) copied into one int16 device buffer laid out by pack_layout:
+    (tok, sizes, starts, length). Synchronous: ngram_amd.loader overlaps the reads and copies with other work."""
+    import torch
+
+    arrays = [read_shard(s) if isinstance(s, (str, os.PathLike)) else np.asarray(s, np.uint16) for s in shards]
+    sizes = [len(a) for a in arrays]
+    starts, length = pack_layout(sizes)
+    tok = torch.full((length,), -1, dtype=torch.int16, device=device)
+    for a, at in zip(arrays, starts):
+        if len(a):
+            tok[at : at + len(a)].copy_(torch.from_numpy(np.ascontiguousarray(a).view(np.int16)))
+    return tok, sizes, starts, length
+
+
 def segments(x: np.ndarray, breaks: list[int] | tuple[int, ...] = ()) -> np.ndarray:
     """Per position of `x`, the tokens of its segment up to and including it (int32): a segment starts at position 0,
     at every BOS and at every position of `breaks`. A position's k-context is valid iff this is >= k (reference
