@@ -4,12 +4,16 @@ geometric documents of mean 1024 ending with BOS 50256, 5% of documents with a c
 counts of the query contexts for n = 2..8, then for 16M query positions each level's tot / dist / cnt, the top-4 next
 tokens with counts, and hit/miss. One step = one whole count build + query over the resident corpus and queries.
 
-Prints one JSON line: value = corpus tokens counted per second (T x steps / timed seconds), plus query positions/s,
-the roofline of the dominant kernel (the level scans: algorithmic bytes 2 per corpus position scanned + 8 per hit
-emitted, or 16 per hit counted in place, over their launch durations timed with HIP events on the launch stream), the
-count path's roofline in "part" mode (scan, pack, partition and LDS count: 2 per position + 16 per hit) and the CPU
-baseline (the oracle's C++ restatement of kgram.rs's query-filtered counting, timed on this host on a bounded
-sample)."""
+Prints one JSON line: value = corpus tokens counted per second (T x steps / timed seconds), plus query positions/s;
+`roofline`: the dominant kernel (the single launch class that takes the most time per step: a level's scan) at its
+algorithmic bytes (2 per corpus position the scan reads -- every position of its range for a dense scan, the listed
+positions for a gated one -- plus 8 per hit emitted) over its launch durations (HIP events on its stream); beside it the
+same for every level scan together (`roofline_family`), for the count path (scans, partition, LDS counts: 2 per
+position read + 16 per hit) and for the whole build (2 T + 16 E over the step); `parity`: the GPU's outputs against
+the oracle's on the CPU baseline's sample (every output of the first shard x the first query positions) and on
+windows of query positions counted over the whole corpus; `cpu_baseline`: the oracle's C++ restatement of kgram.rs's
+query-filtered counting on this host, on a bounded prefix of the same workload (a tenth of the corpus and of the
+queries)."""
 
 from __future__ import annotations
 
@@ -24,19 +28,20 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "n-gram-hinted-lm_amd"))
 
 HBM_PEAK_GBS = 8000.0
-SCAN_KERNELS = ("scan_count", "scan_level", "scan_emit")  # the level scans, whichever counting CountBuild uses
-# "part" mode counts after the scan (emitted hits packed, hash-partitioned, counted in LDS): its roofline kernel set is
-# the whole count path, whose algorithmic bytes are the build's 2 per position scanned + 16 per hit
-PART_KERNELS = ("scan_emit", "bits_list", "gather", "partition", "count")
+# the count path: the level scans, the bitmap-to-list of sparse levels, the region packing, the partition sort and the
+# LDS counts; its algorithmic bytes are the build's 2 per position read + 16 per hit
+PATH_KERNELS = ("scan_emit", "bits_list", "gather", "partition", "count")
+TRAFFIC = ROOT / "profiles" / "scan_traffic_c3.json"  # rocprofv3 FETCH_SIZE / WRITE_SIZE of the scans, per level
 
 
-def scan_traffic(mode: str):
-    """HBM bytes per level-scan launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs (scaled by a plain
-    copy's reading of the same counters), or None where none was measured for this mode."""
-    f = ROOT / "profiles" / f"scan_emit_c3_{mode}_traffic.json"
-    if not f.exists():
-        return None
-    return json.loads(f.read_text())["traffic_bytes_per_launch"]
+def measured_traffic(k: int):
+    """HBM bytes per launch of level k's scan from the committed rocprofv3 counter runs (FETCH_SIZE and WRITE_SIZE
+    scaled by a plain copy's reading of them), with the commit they were taken at; None where there is none."""
+    if not TRAFFIC.exists():
+        return None, None
+    t = json.loads(TRAFFIC.read_text())
+    v = t.get("bytes_per_launch", {}).get(str(k))
+    return v, t.get("commit")
 
 
 def parse() -> argparse.Namespace:
@@ -53,10 +58,10 @@ def parse() -> argparse.Namespace:
                     help="measure only this secondary configuration and print its JSON (for profiling); copy: three "
                          "plain 1 GiB device copies, the calibration of rocprofv3's FETCH_SIZE / WRITE_SIZE; load: "
                          "c3 from shard files (the threaded loader, and the build overlapped with the copies)")
-    ap.add_argument("--mode", default="part", choices=("engine", "part", "record", "partitioned"),
-                    help="CountBuild.mode")
-    ap.add_argument("--cpu-tokens", type=int, default=100_000_000, help="CPU baseline: corpus prefix")
-    ap.add_argument("--cpu-queries", type=int, default=2_000_000, help="CPU baseline: query positions")
+    ap.add_argument("--cpu-tokens", type=int, default=100_000_000, help="CPU baseline and parity: corpus prefix")
+    ap.add_argument("--cpu-queries", type=int, default=1_600_000, help="CPU baseline and parity: query positions")
+    ap.add_argument("--parity-windows", type=int, default=400,
+                    help="windows of 64 query positions compared against the oracle over the whole corpus (0: none)")
     return ap.parse_args()
 
 
@@ -70,25 +75,12 @@ def make_workload(cfg_name: str, train_tokens: int, query_tokens: int):
     import torch
 
     from ngram_amd import data
-    from ngram_amd.gpu_val_stats import layout
-    from ngram_amd.lib import Lib
 
-    cfg = data.CONFIGS[cfg_name]
     t0 = time.time()
-    zipf, tp, qp = data.make_plans(cfg, train_tokens or None, query_tokens or None)
-    log(f"plans: {time.time() - t0:.1f}s ({len(tp.eos)} documents, {len(tp.copies)} + {len(qp.copies)} copies)")
-    lib = Lib()
-    flat = data.realize_gpu(tp, zipf, lib)
-    q = data.realize_gpu(qp, zipf, lib, source=flat)
-    bounds = data.train_bounds(tp.n, cfg.shard_tokens)
-    sizes = [int(b - a) for a, b in zip(bounds[:-1], bounds[1:])]
-    starts, L = layout(sizes)
-    tok = torch.full((L,), -1, dtype=torch.int16, device=flat.device)
-    for (a, b), st in zip(zip(bounds[:-1], bounds[1:]), starts):
-        tok[st : st + (b - a)].copy_(flat[a:b])
+    dc = data.device_corpus(cfg_name, train_tokens or None, query_tokens or None)
     torch.cuda.synchronize()
     log(f"workload on the GPU: {time.time() - t0:.1f}s")
-    return cfg, flat, bounds, tok, sizes, starts, q, np
+    return dc.config, dc.flat, dc.bounds, dc.tok, dc.sizes, dc.starts, dc.query, np
 
 
 def bench_c2(steps: int, warmup: int, with_cpu: bool) -> dict:
@@ -328,27 +320,106 @@ def bench_load(cfg, tok, sizes, starts, q, steps: int) -> dict:
         shutil.rmtree(d, ignore_errors=True)
 
 
-def cpu_baseline(flat, bounds, q, levels, n_tokens: int, n_queries: int) -> dict:
-    """The oracle's query-filtered counting (C++ restatement of kgram.rs, one thread per core) over a bounded sample:
-    the corpus' first n_tokens tokens and the first n_queries query positions, every level."""
+def cpu_baseline(flat_host, bounds, q_host, levels, n_tokens: int, n_queries: int):
+    """The oracle's query-filtered counting (C++ restatement of kgram.rs, one thread per core) over a bounded sample
+    of the same workload: the corpus' first n_tokens tokens and the first n_queries query positions, every level,
+    tot / dist / cnt + top-4 (no TOP rule, as the record). Returns (the baseline's JSON, the outputs per level)."""
     import numpy as np
 
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle as O
 
-    train = flat[:n_tokens].numpy().view(np.uint16)
-    b = bounds[bounds < n_tokens].tolist() + [n_tokens]
-    qq = q[: n_queries + 1].numpy().view(np.uint16)
+    train = flat_host[:n_tokens].numpy().view(np.uint16)
+    b = [int(v) for v in bounds if v < n_tokens] + [n_tokens]
+    qq = q_host[: n_queries + 1].numpy().view(np.uint16)
     x, tgt = qq[:-1], qq[1:]
     avail = O.segments(x)
     cores = O.threads()
+    outs = {}
     t0 = time.perf_counter()
     for k in levels:
-        O.query_counts(train, np.array(b, np.int64), x, tgt, avail, k, ntop=4, nthreads=cores)
+        outs[k] = O.query_counts(train, np.array(b, np.int64), x, tgt, avail, k, cnt_top=1 << 30, ntop=4,
+                                 nthreads=cores)
     dt = time.perf_counter() - t0
-    return {"value": n_tokens / dt, "unit": "corpus tokens/s", "cores": cores, "kind": "port",
-            "sample": f"first {n_tokens} corpus tokens x {n_queries} query positions, levels {list(levels)}, "
-                      f"tot/dist/cnt + top-4; {dt:.1f} s", "seconds": dt}
+    return {"value": n_tokens / dt, "unit": "corpus tokens/s", "query_positions_per_s": n_queries / dt,
+            "cores": cores, "kind": "port",
+            "sample": f"first {n_tokens} corpus tokens x first {n_queries} query positions (a tenth of each), levels "
+                      f"{list(levels)}, tot/dist/cnt + top-4; {dt:.1f} s", "seconds": dt}, outs
+
+
+def _mismatches(gpu: dict, want, sel=None) -> int:
+    """Positions where any of tot / dist / cnt / top-4 differs (sel: the positions compared)."""
+    import numpy as np
+
+    bad = np.zeros(len(want["tot"]) if sel is None else int(sel.sum()), bool)
+    for name in ("tot", "dist", "cnt", "top_tok", "top_cnt"):
+        w = want[name][:, :4] if name.startswith("top") else want[name]
+        w = w if sel is None else w[sel]
+        d = gpu[name] != w
+        bad |= d if d.ndim == 1 else d.any(1)
+    return int(bad.sum())
+
+
+def parity_prefix(cfg, flat, q, n_tokens: int, n_queries: int, want: dict) -> dict:
+    """The GPU build over the CPU baseline's sample (the first n_tokens corpus tokens, one shard, and the first
+    n_queries query positions) against the oracle's outputs on it: mismatching positions per level."""
+    import numpy as np
+    import torch
+
+    from ngram_amd import data
+    from ngram_amd.counts import CountBuild, device_queries
+
+    starts, length = data.pack_layout([n_tokens])
+    tok = torch.full((length,), -1, dtype=torch.int16, device=flat.device)
+    tok[starts[0] : starts[0] + n_tokens].copy_(flat[:n_tokens])
+    cb = CountBuild.from_device(tok, [n_tokens], starts, levels=cfg.levels, level_shards={}, topk=4)
+    x, tgt, avail = device_queries(q[: n_queries + 1])
+    out = cb.counts(x, tgt, avail).cpu().numpy()
+    tt, tc = cb.top_tok.cpu().numpy().view(np.uint16), cb.top_cnt.cpu().numpy().view(np.uint32)
+    per = {}
+    for li, k in enumerate(cfg.levels):
+        gpu = {"tot": out[0, li].view(np.uint32), "dist": out[1, li].astype(np.uint16),
+               "cnt": out[2, li].view(np.uint32), "top_tok": tt[li], "top_cnt": tc[li]}
+        per[str(k)] = _mismatches(gpu, want[k])
+    return {"positions": n_queries, "corpus_tokens": n_tokens, "levels": len(per),
+            "mismatching_positions": sum(per.values()), "per_level": per}
+
+
+def parity_windows(cfg, flat, q, out, top_tok, top_cnt, windows: int) -> dict:
+    """Windows of 64 consecutive query positions (random ones, and ones at the hottest level-2 contexts), their
+    outputs from the timed build compared with the oracle's over the whole corpus (each level examining only the
+    corpus positions the previous level hit)."""
+    import numpy as np
+
+    from ngram_amd import data
+
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as O
+
+    t0 = time.perf_counter()
+    qq = q.cpu().numpy().view(np.uint16)
+    x, tgt = qq[:-1], qq[1:]
+    av = O.segments(x)
+    N = len(x)
+    rng = np.random.default_rng(2026)
+    hot = np.argsort(out[0, 0].view(np.uint32))[-max(1, windows // 8) :]
+    starts = np.unique(np.clip(np.concatenate([rng.integers(0, N, windows), hot - 32]), 7, N - 64))
+    idx = (starts[:, None] + np.arange(-7, 64)[None, :]).reshape(-1)
+    cmp = np.tile(np.arange(-7, 64) >= 0, len(starts))
+    s_av = np.where(cmp, av[idx], 0).astype(np.int32)
+    train = flat.cpu().numpy().view(np.uint16)
+    b = np.array(data.train_bounds(len(train), cfg.shard_tokens), np.int64)
+    g = idx[cmp]
+    per, gate = {}, None
+    for li, k in enumerate(cfg.levels):
+        o = O.query_counts(train, b, x[idx], tgt[idx], s_av, k, cnt_top=1 << 30, ntop=4, hits=True, gate=gate)
+        gate = o["hits"]
+        gpu = {"tot": out[0, li, g].view(np.uint32), "dist": out[1, li, g].astype(np.uint16),
+               "cnt": out[2, li, g].view(np.uint32), "top_tok": top_tok[li, g], "top_cnt": top_cnt[li, g]}
+        per[str(k)] = _mismatches(gpu, o, cmp)
+    return {"positions": int(cmp.sum()), "corpus_tokens": len(train), "windows": len(starts),
+            "mismatching_positions": sum(per.values()), "per_level": per,
+            "oracle_seconds": time.perf_counter() - t0}
 
 
 def main() -> None:
@@ -383,55 +454,55 @@ def main() -> None:
         print(json.dumps({"config": "c3 load", **bench_load(cfg, tok, sizes, starts, q, args.steps)}))
         return
     T = sum(sizes)
-    flat_host = flat[: min(args.cpu_tokens, int(flat.numel()))].cpu()
-    q_host = q[: args.cpu_queries + 1].cpu()
     cb = CountBuild.from_device(tok, sizes, starts, levels=cfg.levels, level_shards={}, topk=cfg.topk)
-    cb.mode = args.mode
-    x, tgt, avail = device_queries(q, cb.lib)
+    x, tgt, avail = device_queries(q)
     N = x.numel()
-    # one untimed build with hit counts: the events E of the roofline (deterministic, the same every step)
+    # one untimed build with hit counts: the hits E of the roofline (deterministic, the same every step)
     cb.counts(x, tgt, avail, stats=True)
     info = {k: dict(v) for k, v in cb.info.items()}
     log("levels:", json.dumps(info))
     for _ in range(max(0, args.warmup - 1)):
         cb.counts(x, tgt, avail)
     torch.cuda.synchronize()
-    cb.timing.clear()
+    per_kernel: dict[tuple, float] = {}  # (name, level) -> ms over the timed steps
+    modes: dict[int, int] = {}
     t0 = time.perf_counter()
-    class_ms: dict[str, float] = {}
-    scan_ms, scan_launches, path_ms = 0.0, 0, 0.0
+    t_last = t0
     for step in range(args.steps):
         out = cb.counts(x, tgt, avail)
-        log(f"step {step}: {sum(cb.timing.values()) / (step + 1):.4f} s/step so far")
-        # the timed launches of this step (HIP events on the stream they ran on)
-        for name, k, i, n, e0, e1 in cb.kernel_events:
-            ms = e0.elapsed_time(e1)
-            class_ms[name] = class_ms.get(name, 0.0) + ms
-            if name in SCAN_KERNELS:
-                scan_ms += ms
-                scan_launches += 1
-            if name in PART_KERNELS:
-                path_ms += ms
+        torch.cuda.synchronize()  # (the step's events are read below: the step's launches have completed)
+        now = time.perf_counter()
+        log(f"step {step}: {1e3 * (now - t_last):.1f} ms")
+        t_last = now
+        for name, k, n, e0, e1, mode in cb.kernel_events:
+            per_kernel[(name, k)] = per_kernel.get((name, k), 0.0) + e0.elapsed_time(e1)
+            if name == "scan_emit":
+                modes[k] = mode
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    hits = sum(v["hits"] for v in info.values())
-    # algorithmic bytes of the scan launches of one step: 2 per position scanned, and per hit 16 (counted in place:
-    # the 8-byte slot read and written, or the split table's key read + count read and written) or 8 (emitted: the key
-    # written, read back by the count)
-    positions = {k: 0 for k in cfg.levels}
-    for name, k, i, n, _, _ in cb.kernel_events:
-        if name in SCAN_KERNELS:
-            positions[k] += n
-    emits = cb.mode == "part" or any(v["pbits"] for v in info.values())
-    per_hit = {k: 8.0 if cb.mode == "part" or info[k]["pbits"] else 16.0 for k in cfg.levels}
-    step_bytes = sum(2.0 * positions[k] + per_hit[k] * info[k]["hits"] for k in cfg.levels)
-    scan_bytes = args.steps * step_bytes
-    achieved = scan_bytes / (scan_ms / 1e3) / 1e9 if scan_ms > 0 else 0.0
-    # the whole count path of "part" mode (scan, pack, partition, LDS count): 2 per position + 16 per hit
-    path_bytes = sum(2.0 * positions[k] + 16.0 * info[k]["hits"] for k in cfg.levels)
-    build_bytes = 2.0 * T + 16.0 * hits  # the count build's B_build = 2 T + 16 E
     ms = dt / args.steps * 1e3
-    mask_hits = int((out[0] != 0).sum().item())
+    hits = {k: info[k]["hits"] for k in cfg.levels}
+    # positions each level's scan reads: its whole range (dense), or the previous level's hits (gated: listed)
+    read = {}
+    for li, k in enumerate(cfg.levels):
+        read[k] = T if modes.get(k, 0) == 0 else hits[cfg.levels[li - 1]]
+    scan_bytes = {k: 2.0 * read[k] + 8.0 * hits[k] for k in cfg.levels}
+    scan_ms = {k: per_kernel.get(("scan_emit", k), 0.0) / args.steps for k in cfg.levels}
+    dom = max(cfg.levels, key=lambda k: scan_ms[k])
+    top_class = max(per_kernel, key=per_kernel.get)
+
+    def roof(nbytes: float, msec: float) -> dict:
+        gbs = nbytes / (msec / 1e3) / 1e9 if msec > 0 else 0.0
+        return {"achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS}
+
+    traffic, traffic_commit = measured_traffic(dom)
+    path_ms = sum(v for (name, _), v in per_kernel.items() if name in PATH_KERNELS) / args.steps
+    path_bytes = sum(2.0 * read[k] + 16.0 * hits[k] for k in cfg.levels)
+    E = sum(hits.values())
+    build_bytes = 2.0 * T + 16.0 * E  # the count build's B_build = 2 T + 16 E
+    classes: dict[str, float] = {}
+    for (name, _), v in per_kernel.items():
+        classes[name] = classes.get(name, 0.0) + v / args.steps
     res = {
         "metric": "corpus tokens counted/s + hint queries/s on 1 GPU; % of HBM peak GB/s",
         "value": T * args.steps / dt,
@@ -443,34 +514,48 @@ def main() -> None:
         "config": {"workload": f"{cfg.name}: count build of {T} corpus tokens ({len(sizes)} shards) for n="
                                f"{list(cfg.levels)} + top-{cfg.topk}/count/hit queries at {N} positions",
                    "corpus_tokens": T, "query_positions": N, "levels": list(cfg.levels), "topk": cfg.topk},
-        "roofline": {"bound": "hbm", "kernel": f"level scan ({cb.mode}: "
-                     + ", ".join(sorted({n for n, *_ in cb.kernel_events if n in SCAN_KERNELS})) + ")",
-                     "bytes_per_position": 2, "bytes_per_hit": 8 if emits else 16,
-                     "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": scan_traffic(cb.mode),
-                     "launches_per_step": scan_launches // max(1, args.steps),
-                     "avg_launch_ms": scan_ms / max(1, scan_launches),
-                     # the measured HBM + MALL traffic per launch over the average launch: the rate the scans'
-                     # random line fetches actually move, against the same peak
-                     "traffic_GBps": None if scan_traffic(cb.mode) is None or scan_launches == 0 else
-                     scan_traffic(cb.mode) / (scan_ms / scan_launches / 1e3) / 1e9,
-                     "algorithmic_bytes_per_step": step_bytes,
-                     "scan_share_of_step": scan_ms / args.steps / ms},
-        "count_path_roofline": None if cb.mode != "part" else {
-            "kernels": list(PART_KERNELS), "algorithmic_bytes_per_step": path_bytes,
-            "ms_per_step": path_ms / args.steps, "achieved": path_bytes / (path_ms / args.steps / 1e3) / 1e9,
-            "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": path_bytes / (path_ms / args.steps / 1e3) / 1e9 / HBM_PEAK_GBS},
-        "build_roofline": {"bytes": build_bytes, "GBps_over_step": build_bytes / (ms / 1e3) / 1e9,
-                           "frac_over_step": build_bytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS},
-        "kernel_ms_per_step": {k: v / args.steps for k, v in class_ms.items()},
-        "events_per_step": hits, "position_level_hits": mask_hits,
-        "phases_s": {k: v / args.steps for k, v in cb.timing.items()},
-        "levels": info,
+        "roofline": {"bound": "hbm", "kernel": f"scan_emit k={dom} (ng_scan_emit, mode {modes.get(dom, 0)})",
+                     **roof(scan_bytes[dom], scan_ms[dom]), "traffic": traffic,
+                     "traffic_source": None if traffic is None else f"profiles/scan_traffic_c3.json @ {traffic_commit}",
+                     "algorithmic_bytes_per_launch": scan_bytes[dom], "avg_launch_ms": scan_ms[dom],
+                     "positions_read": read[dom], "hits_emitted": hits[dom],
+                     "bytes_per_position_read": 2, "bytes_per_hit": 8},
+        "roofline_family": {"kernels": "scan_emit, every level", **roof(sum(scan_bytes.values()),
+                                                                        sum(scan_ms.values())),
+                            "ms_per_step": sum(scan_ms.values())},
+        "count_path_roofline": {"kernels": list(PATH_KERNELS), "algorithmic_bytes_per_step": path_bytes,
+                                "ms_per_step": path_ms, **roof(path_bytes, path_ms)},
+        "build_roofline": {"bytes": build_bytes, **roof(build_bytes, ms), "streaming_floor_GBps": 2.0 * T / (ms / 1e3) / 1e9},
+        "slowest_launch_class": {"kernel": f"{top_class[0]} k={top_class[1]}", "ms_per_step": per_kernel[top_class] / args.steps},
+        "kernel_ms_per_step": classes,
+        "events_per_step": E,
+        "host_s_per_step": {k: v / (args.steps + args.warmup) for k, v in cb.engine.host_s.items()},
+        "levels": {str(k): {**info[k], "scan_mode": modes.get(k, 0), "positions_read": read[k],
+                            "scan_ms": scan_ms[k]} for k in cfg.levels},
+        "parity": None,
         "cpu_baseline": None,
     }
+    out_np = out.cpu().numpy()
+    tt_np, tc_np = cb.top_tok.cpu().numpy().view(np.uint16), cb.top_cnt.cpu().numpy().view(np.uint32)
+    del cb, out, x, tgt, avail
+    torch.cuda.empty_cache()
+    parity = {}
+    if not args.no_cpu:
+        nt = min(args.cpu_tokens, int(flat.numel()))
+        nq = min(args.cpu_queries, N)
+        cpu, want = cpu_baseline(flat[:nt].cpu(), bounds, q[: nq + 1].cpu(), cfg.levels, nt, nq)
+        log(f"cpu baseline: {cpu['seconds']:.1f}s")
+        res["cpu_baseline"] = cpu
+        parity["prefix"] = parity_prefix(cfg, flat, q, nt, nq, want)
+        del want
+    if args.parity_windows:
+        parity["windows"] = parity_windows(cfg, flat, q, out_np, tt_np, tc_np, args.parity_windows)
+        log(f"parity windows: {parity['windows']['oracle_seconds']:.1f}s")
+    if parity:
+        parity["mismatching_positions"] = sum(p["mismatching_positions"] for p in parity.values())
+        res["parity"] = parity
     if not args.no_secondary:
-        del cb, out, q, x, tgt, avail
+        del q
         torch.cuda.empty_cache()
         res["secondary"] = {}
         log("secondary: c5")
@@ -482,13 +567,10 @@ def main() -> None:
         torch.cuda.empty_cache()
         log("secondary: c4")
         res["secondary"]["c4"] = bench_c4(not args.no_cpu)
-    if not args.no_cpu:
-        nt = min(args.cpu_tokens, int(flat_host.numel()))
-        nq = min(args.cpu_queries, N)
-        cpu = cpu_baseline(flat_host, bounds, q_host, cfg.levels, nt, nq)
-        log(f"cpu baseline: {cpu['seconds']:.1f}s")
-        res["cpu_baseline"] = cpu
     print(json.dumps(res), flush=True)
+    if res["parity"] and res["parity"]["mismatching_positions"]:
+        log("parity: the GPU's outputs differ from the oracle's")
+        sys.exit(1)
 
 
 if __name__ == "__main__":

@@ -29,7 +29,7 @@ import numpy as np
 import torch
 
 from .data import BOS, HEADER_BYTES, shard_tokens
-from .gpu_val_stats import layout
+from .data import pack_layout as layout
 from . import partcount as P
 from .lib import Lib, i32, u64
 

@@ -365,6 +365,44 @@ def make_corpus(name: str, train_tokens: int | None = None, query_tokens: int | 
     return Corpus(cfg, zipf, tp, qp, train, bounds, query)
 
 
+@dataclass
+class DeviceCorpus:
+    """A configuration's streams generated on the GPU: the training tokens without gaps (`flat`, int16), their shard
+    bounds, the same tokens laid out for the scans (`tok`, data.pack_layout's `sizes` / `starts`) and the query stream
+    (`query`, int16: the inputs, then the last target)."""
+
+    config: Config
+    zipf: Zipf
+    train_plan: Plan
+    flat: object
+    bounds: np.ndarray
+    tok: object
+    sizes: list
+    starts: list
+    query: object
+
+
+def device_corpus(name: str, train_tokens: int | None = None, query_tokens: int | None = None, lib=None,
+                  shard_tokens: int | None = None) -> DeviceCorpus:
+    """Configuration `name`'s streams generated on the GPU (byte-identical to make_corpus's)."""
+    import torch
+
+    from .lib import Lib
+
+    cfg = CONFIGS[name]
+    zipf, tp, qp = make_plans(cfg, train_tokens, query_tokens)
+    lib = lib or Lib()
+    flat = realize_gpu(tp, zipf, lib)
+    q = realize_gpu(qp, zipf, lib, source=flat)
+    bounds = train_bounds(tp.n, shard_tokens or cfg.shard_tokens)
+    sizes = [int(b - a) for a, b in zip(bounds[:-1], bounds[1:])]
+    starts, length = pack_layout(sizes)
+    tok = torch.full((length,), -1, dtype=torch.int16, device=flat.device)
+    for a, b, at in zip(bounds[:-1], bounds[1:], starts):
+        tok[at : at + (b - a)].copy_(flat[a:b])
+    return DeviceCorpus(cfg, zipf, tp, flat, bounds, tok, sizes, starts, q)
+
+
 C4_STEPS = 92
 C4_STEP_TOKENS = 1 << 19
 

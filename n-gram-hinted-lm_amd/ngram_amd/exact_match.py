@@ -20,7 +20,7 @@ import torch
 
 from .count_table import CountTable  # noqa: F401  (part of the surface)
 from .data import BOS, HEADER_BYTES, segments, shard_tokens
-from .gpu_val_stats import layout
+from .data import pack_layout as layout
 from .lib import Lib, i32, u64
 from .online import OnlineRows  # noqa: F401  (part of the surface)
 from .qindex import QueryIndex

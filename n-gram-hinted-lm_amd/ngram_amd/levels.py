@@ -1,0 +1,272 @@
+"""The engine's level pipeline: query-filtered exact counts of every (context, next token) pair of a device-resident
+token buffer, level after level, and the per-position outputs. Both host surfaces run on it: the record's CountBuild
+(record_367_gpu_counts/track_1_short/counts/build.py:261-388) and the validation statistics' build
+(old_records/gpu_val_stats.py _run :701-1232). No counterpart in the reference's libraries: there a level's hits are
+counted with global atomics in one hash table and ranked by a second sort; here
+
+  1. the level's query index (ng_query_index, qindex.py) holds only the query positions whose previous level's context
+     occurred (a k-context occurs only where its (k-1)-suffix does);
+  2. the level's scan (ng_scan_emit: every position, or only those its shard's previous level hit) appends each hit's
+     mix64(context id << 16 | next) to its block's own region, no global atomic, and makes the hit bitmap that gates
+     the next level; a level behind a sparse one lists the previous hits first (ng_bits_list) and probes the list;
+  3. the events are hash-partitioned by a radix pass straight from the regions and counted partition by partition in
+     LDS (partcount.count_events), which also answers each query position's (context, target) count;
+  4. the distinct pairs, packed one word each, are sorted by context and summarized per present context
+     (ng_ctx_summary: total, pairs, top entries); with a TOP rule the contexts with more than `cnt_top` pairs get the
+     cnt_top-th largest score (ng_ctx_kth);
+  5. per query position its context's record gives tot, dist, the target's count (if ranked within cnt_top) and the
+     top entries (ng_pos_summary), and the level's mask bit.
+
+Per-level sizes from one build are kept (context counts, events, distinct pairs per event, hit densities) and size the
+next build of the same inputs."""
+
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, field
+
+import torch
+
+from . import partcount
+from .lib import Lib, i32, u64
+from .partcount import count_events, emit_region, summarize
+from .qindex import QueryIndex
+
+SCAN_BLOCKS_PER_CU = 8  # level-scan blocks (grid-stride) per compute unit (c3 sweep: 8 fastest of 4-32)
+LIST_DENSITY = 0.05  # a level behind a sparser one probes the previous hits as a position list (c3 sweep)
+TOPS = (1, 2, 4, 8)  # the record widths ng_ctx_summary writes
+
+
+def _record_width(want: int) -> int:
+    return next(t for t in TOPS if t >= max(want, 1))
+
+
+@dataclass
+class LevelOutputs:
+    """One build's outputs: counts int32 [3, len(levels), N] (tot and cnt as uint32 bits, dist <= 65535), with topk
+    the top entries per level and position (int16 [L, N, topk], int32 [L, N, topk]), with mask the levels whose context
+    occurred (bit li of int32 [N]), and for each kept level (ctx_of int32 [N], records CtxRecord<8> int32 [ids, 16])."""
+
+    counts: torch.Tensor
+    top_tok: torch.Tensor | None = None
+    top_cnt: torch.Tensor | None = None
+    mask: torch.Tensor | None = None
+    kept: dict = field(default_factory=dict)
+    info: dict = field(default_factory=dict)
+
+
+class LevelBuild:
+    """Exact counts of `levels` (ascending k) over the shards laid out in `tok` (int16 [L], data.pack_layout's
+    starts/sizes). `level_shards`: per level, how many leading shards it counts (default: all). `ready`: per shard an
+    event its first scan waits for (its copy from the host), or None for resident tokens."""
+
+    def __init__(self, tok: torch.Tensor, sizes: list[int], starts: list[int], levels, level_shards: dict | None = None,
+                 ready: list | None = None, elib: Lib | None = None):
+        self.levels = tuple(levels)
+        if not self.levels or list(self.levels) != sorted(set(self.levels)) or self.levels[0] < 1:
+            raise ValueError(f"levels must ascend from >= 1: {self.levels}")
+        self.tok, self.sizes, self.starts = tok, list(sizes), list(starts)
+        self.L = int(tok.numel())
+        ls = level_shards or {}
+        self.level_shards = {k: min(len(sizes), ls.get(k, len(sizes))) for k in self.levels}
+        self.ready = ready
+        self.elib = elib or Lib()
+        # sizes learnt from the last build: hit density, events, query contexts, distinct pairs per event
+        self.density: dict[int, float] = {}
+        self.events_of: dict[int, int] = {}
+        self.contexts_of: dict[int, int] = {}
+        self.dratio: dict[int, float] = {}
+        self.kernel_events: list = []
+        self.host_s = {"index": 0.0, "scan": 0.0, "count": 0.0}
+        self._plist = None
+
+    def _event(self, name: str, k: int, n: int, mode: int = -1):
+        """A pair of timing events around a launch on the current stream, kept in kernel_events as (name, k, n, e0,
+        e1, mode): n the items the launch covers (a scan: the positions of its range), mode a scan's (see _mode)."""
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        self.kernel_events.append((name, k, n, e0, e1, mode))
+        return e0, e1
+
+    def _wait(self, i: int) -> None:
+        if self.ready is not None and self.ready[i] is not None:
+            torch.cuda.current_stream().wait_event(self.ready[i])
+
+    def build(self, x: torch.Tensor, tgt: torch.Tensor, avail: torch.Tensor, *, topk: int = 0,
+              cnt_top: int | None = None, keep=(), with_mask: bool = False, stats: bool = False) -> LevelOutputs:
+        """Counts of every level for the N query positions (x int16 [N], tgt int16 [N], avail int32 [N]). `topk`: also
+        each position's context's first topk entries; `cnt_top`: the TOP rule (cnt only if the target ranks below it);
+        `keep`: levels whose records are returned (top-8); `stats`: each level's corpus hits in info."""
+        dev, N, elib = self.tok.device, x.numel(), self.elib
+        self.kernel_events = []
+        self.grid = torch.cuda.get_device_properties(dev).multi_processor_count * SCAN_BLOCKS_PER_CU
+        nwords = self.L // 32
+        bms = {k: torch.zeros(nwords, dtype=torch.int32, device=dev) for k in self.levels}
+        res = LevelOutputs(torch.zeros((3, len(self.levels), N), dtype=torch.int32, device=dev))
+        if topk:
+            res.top_tok = torch.zeros((len(self.levels), N, topk), dtype=torch.int16, device=dev)
+            res.top_cnt = torch.zeros((len(self.levels), N, topk), dtype=torch.int32, device=dev)
+        if with_mask:
+            res.mask = torch.zeros(N, dtype=torch.int32, device=dev)
+        G = self.grid
+        R = max([emit_region((n + 31) // 32 * 32, G) for n in self.sizes] or [8192])
+        span = self.starts[-1] + (self.sizes[-1] + 31) // 32 * 32 - self.starts[0] if self.sizes else 0
+        # room for one region per shard and block, or for one scan over every shard (a list scan's regions included)
+        n_reg = max(len(self.sizes) * G * R, G * emit_region(span, G), G * (-(-max(span, 1) // (G * 256)) * 256))
+        regions = torch.empty(n_reg, dtype=torch.int64, device=dev)
+        out = res.counts
+        for li, k in enumerate(self.levels):
+            t0 = time.perf_counter()
+            prev = self.levels[li - 1] if li else None
+            seen = None
+            if prev is not None and self.level_shards[k] <= self.level_shards[prev]:
+                seen = torch.nonzero(out[1, li - 1] > 0).squeeze(1).to(torch.int32)
+            vi = QueryIndex(elib, x, avail, k, seen, expect=self.contexts_of.get(k))
+            self.contexts_of[k] = vi.n
+            t1 = time.perf_counter()
+            seg = self._emit(k, vi, x, bms, regions, R)
+            t2 = time.perf_counter()
+            ev_fn = lambda name, n, k=k: self._event(name, k, n)  # noqa: E731
+            c = count_events(elib, elib, None, 0, vi.ids, self.dratio.get(k, 1.0), (vi.ctx_of, tgt, seen),
+                             event=ev_fn, seg=seg, presort="ctx")
+            del seg
+            self.events_of[k] = c.n_ev
+            self.dratio[k] = c.U / max(1, c.n_ev)
+            t3 = time.perf_counter()
+            kept = k in keep
+            ktop = 8 if (kept or cnt_top is not None) else _record_width(topk)
+            if not c.cb:
+                raise RuntimeError(f"k={k}: more large counts than the escape table holds")
+            try:
+                sm = summarize(elib, elib, c, vi.ids, ktop, False, ev_fn,
+                               deep_min=cnt_top if cnt_top is not None else None)
+            except RuntimeError as e:
+                raise RuntimeError(f"k={k}: {e}") from None
+            thr = None
+            if cnt_top is not None and sm.deep.numel():
+                thr = torch.zeros(vi.ids, dtype=torch.int64, device=dev)
+                e0, e1 = self._event("ctx_kth", k, int(sm.deep.numel()))
+                e0.record()
+                elib("ng_ctx_kth", sm.words, i32(c.cb), c.esc[0], c.esc[1], u64(partcount.ESC_CAP), sm.rec, sm.deep,
+                     sm.deep.numel(), i32(cnt_top), thr)
+                e1.record()
+            e0, e1 = self._event("pos_gather", k, N)
+            e0.record()
+            elib("ng_pos_summary", vi.ctx_of, N, 0, vi.ids, tgt, sm.rec, sm.dist, thr, c.qcnt, i32(ktop), i32(topk),
+                 i32(li), out[0, li], out[1, li], out[2, li], res.top_tok[li] if topk else None,
+                 res.top_cnt[li] if topk else None, res.mask)
+            e1.record()
+            if kept:
+                res.kept[k] = (vi.ctx_of, sm.rec)
+            res.info[k] = dict(contexts=vi.n, ids=vi.ids, pairs=c.U, events=c.n_ev, pbits=c.pbits, hits=None)
+            self.host_s["index"] += t1 - t0
+            self.host_s["scan"] += t2 - t1
+            self.host_s["count"] += t3 - t2
+            del vi, c, sm, thr, seen
+        del regions
+        if stats:
+            for k in self.levels:
+                h = int(self._popcount(bms[k]))
+                res.info[k]["hits"] = h
+                self.density[k] = h / max(1, sum(self.sizes[: self.level_shards[k]]))
+        return res
+
+    def _popcount(self, bm: torch.Tensor) -> int:
+        n = torch.zeros(1, dtype=torch.int64, device=bm.device)
+        self.elib("popcount", bm, bm.numel(), n)
+        return int(n.item())
+
+    def _mode(self, si: int, scanned: list) -> int:
+        """A shard's si-th scanned level's scan: a lane per position (0) for the first level and behind a dense
+        previous level, the LDS-listed set positions (2) behind a sparser one, or below LIST_DENSITY the set positions
+        listed in memory first (3). Densities are the last build's (dense when unknown)."""
+        if si == 0:
+            return 0
+        d = self.density.get(scanned[si - 1])
+        if d is None or d >= 0.5:
+            return 0
+        return 3 if d < LIST_DENSITY else 2
+
+    def _emit(self, k, vi, x, bms, regions, R):
+        """Level k's scan of every shard it counts, hits emitted to per-block regions with each block's top-digit
+        histogram: count_events' seg = (regions, R, ev_count, dhist, nseg, flags)."""
+        elib, dev, G = self.elib, self.tok.device, self.grid
+        shards = [i for i in range(len(self.sizes)) if i < self.level_shards[k]]
+        nseg = len(shards) * G
+        ev_count = torch.zeros(max(nseg, 1), dtype=torch.int32, device=dev)
+        last = self.events_of.get(k)
+        dhist = torch.empty(256 * max(nseg, 1), dtype=torch.int32, device=dev) \
+            if last is None or last >= partcount.SEG_MIN_EVENTS * nseg else None
+        flags = torch.zeros(2, dtype=torch.int32, device=dev)
+        scans = {tuple(q for q in self.levels if i < self.level_shards[q]) for i in shards}
+        if len(shards) > 1 and len(scans) == 1:
+            # every shard scans the same levels: one launch over all of them (the SENT gaps between shards hold no
+            # context), unless this is the first level and shards may still be arriving (each waits for its copy)
+            scanned = list(scans.pop())
+            si = scanned.index(k)
+            if si > 0 or self.ready is None:
+                return self._emit_all(k, vi, x, None if si == 0 else bms[scanned[si - 1]], bms[k], shards, regions,
+                                      flags, self._mode(si, scanned))
+        for j, i in enumerate(shards):
+            st, n = self.starts[i], self.sizes[i]
+            n32 = (n + 31) // 32 * 32
+            self._wait(i)
+            scanned = [q for q in self.levels if i < self.level_shards[q]]
+            si = scanned.index(k)
+            bm_in = None if si == 0 else bms[scanned[si - 1]][st // 32 :]
+            mode = self._mode(si, scanned)
+            if mode == 3:
+                if self._plist is None or self._plist.numel() < n32:
+                    self._plist = torch.empty(max(self.sizes) + 64, dtype=torch.int64, device=dev)
+                n_list = torch.zeros(1, dtype=torch.int64, device=dev)
+                b0, b1 = self._event("bits_list", k, n32)
+                b0.record()
+                elib.cub("ng_bits_list", bm_in, n32 // 32, self._plist, n_list)
+                b1.record()
+            e0, e1 = self._event("scan_emit", k, n32, mode)
+            e0.record()
+            dh = dhist[j * G :] if dhist is not None else None
+            if mode == 3:
+                elib("ng_scan_emit_list", self.tok[st:], self._plist, n_list, i32(k), vi.table, u64(vi.cap), vi.rep,
+                     x, bms[k][st // 32 :], regions[j * G * R :], u64(R), ev_count[j * G :], flags, i32(G), dh, nseg)
+            else:
+                elib("ng_scan_emit", self.tok[st:], n32, i32(k), bm_in, bms[k][st // 32 :], vi.table, u64(vi.cap),
+                     vi.rep, x, regions[j * G * R :], u64(R), ev_count[j * G :], flags, i32(G), i32(mode), dh, nseg)
+            e1.record()
+        return regions, R, ev_count, dhist, nseg, flags  # count_events checks the flags with its first read
+
+    def _emit_all(self, k, vi, x, bm_in, bm_out, shards, regions, flags, mode):
+        """_emit of a level whose shards all scan the same levels, in one launch from the first shard's start to the
+        last one's end: a lane per position (mode 0), the LDS-listed set positions (2), or one list of the previous
+        level's set bits and one list scan (3)."""
+        elib, dev, G = self.elib, self.tok.device, self.grid
+        lo = self.starts[shards[0]]
+        hi = self.starts[shards[-1]] + (self.sizes[shards[-1]] + 31) // 32 * 32
+        for i in shards:
+            self._wait(i)
+        n = hi - lo
+        R = -(-max(n, 1) // (G * 256)) * 256 if mode == 3 else emit_region(n, G)
+        if G * R > regions.numel():
+            raise RuntimeError(f"k={k}: the emit regions are too small for one scan over every shard")
+        ev_count = torch.zeros(G, dtype=torch.int32, device=dev)
+        last = self.events_of.get(k)
+        dhist = torch.empty(256 * G, dtype=torch.int32, device=dev) \
+            if last is None or last >= partcount.SEG_MIN_EVENTS * G else None
+        if mode == 3:
+            if self._plist is None or self._plist.numel() < n:
+                self._plist = torch.empty(n + 64, dtype=torch.int64, device=dev)
+            n_list = torch.zeros(1, dtype=torch.int64, device=dev)
+            b0, b1 = self._event("bits_list", k, n)
+            b0.record()
+            elib.cub("ng_bits_list", bm_in[lo // 32 :], n // 32, self._plist, n_list)
+            b1.record()
+        e0, e1 = self._event("scan_emit", k, n, mode)
+        e0.record()
+        if mode == 3:
+            elib("ng_scan_emit_list", self.tok[lo:], self._plist, n_list, i32(k), vi.table, u64(vi.cap), vi.rep, x,
+                 bm_out[lo // 32 :], regions, u64(R), ev_count, flags, i32(G), dhist, G)
+        else:
+            elib("ng_scan_emit", self.tok[lo:], n, i32(k), None if bm_in is None else bm_in[lo // 32 :],
+                 bm_out[lo // 32 :], vi.table, u64(vi.cap), vi.rep, x, regions, u64(R), ev_count, flags, i32(G),
+                 i32(mode), dhist, G)
+        e1.record()
+        return regions, R, ev_count, dhist, G, flags

@@ -77,3 +77,9 @@ class Lib:
         fn = getattr(self.so, name)
         fn.restype = ctypes.c_int
         return fn(*args)
+
+    def size(self, name: str, *args: int) -> int:
+        """A sizing call without the stream argument that returns int64 (its arguments int64)."""
+        fn = getattr(self.so, name)
+        fn.restype = ctypes.c_int64
+        return int(fn(*(ctypes.c_int64(a) for a in args)))

@@ -29,9 +29,9 @@ from types import SimpleNamespace
 import numpy as np
 import torch
 
-from .counts import record_lib
+
 from .data import BOS, HEADER_BYTES, shard_tokens
-from .gpu_val_stats import layout
+from .data import pack_layout as layout
 from .lib import Lib, i32, u64
 from .partcount import count_events, emit_region, pack_events, summarize
 from .qindex import LOAD as QLOAD, TAIL as QTAIL, QueryIndex
@@ -57,7 +57,7 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
     if not 1 <= cap <= 64:
         raise ValueError("cap must be in [1, 64]")
     elib = elib or Lib()
-    lib = lib or record_lib()
+    lib = lib or Lib()
     dev = x.device
     N, L = x.numel(), tok.numel()
     nwords = L // 32
@@ -416,7 +416,7 @@ class LongestMatch:
                 self.tok[st : st + len(a)].copy_(torch.from_numpy(a.view(np.int16)))
         self.x = torch.from_numpy(q[:-1].view(np.int16).copy()).to(dev)
         self.cap = cap
-        self.elib, self.lib = Lib(), record_lib()
+        self.elib = self.lib = Lib()
         self.avail = _segments(self.x, self.lib)
         self.tokens = int(sum(sizes))
         torch.cuda.synchronize()

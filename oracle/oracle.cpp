@@ -23,6 +23,10 @@
 // caller checks >= 2^32), dist = distinct next tokens (saturated at 65535), cnt = the target's count if its rank
 // (count descending, token ascending) is below cnt_top, else 0; all 0 where the context is invalid or never occurred.
 #include <algorithm>
+#include <parallel/algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <chrono>
 #include <cmath>
 #include <functional>
 #include <atomic>
@@ -175,24 +179,57 @@ static void position_outputs(const std::vector<u32>& ctx, const std::vector<Rank
     }
 }
 
-// Group sorted (id << 16 | next) entries into per-context ranked lists.
-static void group_entries(std::vector<u64>& all, std::vector<Ranked>& per) {
-    std::sort(all.begin(), all.end());
-    size_t i = 0;
-    while (i < all.size()) {
-        u64 id = all[i] >> 16;
-        Ranked& c = per[id];
-        size_t j = i;
-        while (j < all.size() && (all[j] >> 16) == id) {
-            u64 v = all[j];
-            size_t a = j;
-            while (j < all.size() && all[j] == v) ++j;
-            c.ranked.push_back({(u32)(j - a), (u16)(v & 0xFFFF)});
+// Group (id << 16 | next) entries into per-context ranked lists. Each thread's entries are sorted and run-length
+// encoded in parallel (Zipf-skewed pairs repeat a lot); then ranges of context ids are merged in parallel, each from
+// its slice of every thread's runs.
+static void group_entries(std::vector<std::vector<u64>>& acc, std::vector<Ranked>& per, int threads) {
+    threads = std::max(1, threads);
+    std::vector<std::vector<std::pair<u64, u64>>> runs(acc.size());
+    parallel_for((i64)acc.size(), std::max(1, std::min<int>(threads, (int)acc.size())), [&](i64 a, i64 b, int) {
+        for (i64 t = a; t < b; ++t) {
+            std::vector<u64>& v = acc[t];
+            std::sort(v.begin(), v.end());
+            for (size_t i = 0; i < v.size();) {
+                size_t j = i;
+                while (j < v.size() && v[j] == v[i]) ++j;
+                runs[t].push_back({v[i], (u64)(j - i)});
+                i = j;
+            }
+            std::vector<u64>().swap(v);
         }
-        c.total = j - i;
-        rank_pairs(c.ranked);
-        i = j;
-    }
+    });
+    const i64 nids = (i64)per.size();
+    const i64 R = std::min<i64>(std::max<i64>(nids, 1), 16 * (i64)threads);  // id ranges, taken dynamically
+    std::atomic<i64> next_range(0);
+    std::vector<std::thread> ts;
+    for (int t = 0; t < threads; ++t)
+        ts.emplace_back([&] {
+            for (i64 r; (r = next_range++) < R;) {
+                const u64 lo = (u64)(nids * r / R) << 16, hi = (u64)(nids * (r + 1) / R) << 16;
+                std::vector<std::pair<u64, u64>> all;
+                for (auto& rv : runs) {
+                    auto a = std::lower_bound(rv.begin(), rv.end(), std::make_pair(lo, (u64)0));
+                    auto b = std::lower_bound(rv.begin(), rv.end(), std::make_pair(hi, (u64)0));
+                    all.insert(all.end(), a, b);
+                }
+                std::sort(all.begin(), all.end());
+                for (size_t i = 0; i < all.size();) {
+                    const u64 id = all[i].first >> 16;
+                    Ranked& c = per[id];
+                    size_t j = i;
+                    while (j < all.size() && (all[j].first >> 16) == id) {
+                        const u64 v = all[j].first;
+                        u64 n = 0;
+                        while (j < all.size() && all[j].first == v) n += all[j++].second;
+                        c.ranked.push_back({(u32)n, (u16)(v & 0xFFFF)});
+                        c.total += n;
+                    }
+                    rank_pairs(c.ranked);
+                    i = j;
+                }
+            }
+        });
+    for (auto& th : ts) th.join();
 }
 
 extern "C" {
@@ -204,7 +241,7 @@ extern "C" {
 // Returns the number of matched corpus occurrences, or -1 on bad arguments.
 i64 oracle_query_counts(const u16* tok, const i64* bounds, int nshards, const u16* x, const u16* tgt,
                         const i32* avail, i64 n, int k, int cnt_top, int ntop, u32* tot, u16* dist, u32* cnt,
-                        u16* top_tok, u32* top_cnt, uint8_t* hits, int threads) {
+                        u16* top_tok, u32* top_cnt, uint8_t* hits, const uint8_t* gate, int threads) {
     if (k < 1 || n < 0 || nshards < 1 || ntop < 0) return -1;
     Contexts ctx;
     ctx.build(x, avail, n, k);
@@ -222,6 +259,7 @@ i64 oracle_query_counts(const u16* tok, const i64* bounds, int nshards, const u1
                 size_t q = next_piece++;
                 if (q >= pieces.size()) break;
                 for (i64 p = pieces[q].first; p < pieces[q].second; ++p) {
+                    if (gate && !gate[p]) continue;  // its (k-1)-suffix never matched: neither can its k-context
                     u32 id = ctx.find(tok + p - k);
                     if (id == UINT32_MAX) continue;
                     if (hits) hits[p] = 1;
@@ -230,14 +268,12 @@ i64 oracle_query_counts(const u16* tok, const i64* bounds, int nshards, const u1
             }
         });
     for (auto& th : ts) th.join();
-    std::vector<u64> all;
     size_t total = 0;
     for (auto& a : acc) total += a.size();
-    all.reserve(total);
-    for (auto& a : acc) all.insert(all.end(), a.begin(), a.end());
     std::vector<Ranked> per(ctx.reps.size());
-    group_entries(all, per);
+    group_entries(acc, per, threads);
     position_outputs(ctx.key_of, per, tgt, n, cnt_top, ntop, tot, dist, cnt, top_tok, top_cnt);
+    if (getenv("ORACLE_TRACE")) fprintf(stderr, "oracle query_counts k=%d: %zu events\n", k, total);
     return (i64)total;
 }
 
@@ -315,36 +351,94 @@ i64 oracle_table_counts(const u16* tok, const i64* bounds, int nshards, const u1
 }
 
 // Longest match: per query position, the largest k <= cap whose k-context is valid and occurred in the corpus (0 if
-// none), that context's most frequent next token (count descending, token ascending) and its count.
+// none), that context's most frequent next token (count descending, token ascending) and its count. Two phases, both
+// from the definitions: existence level by level (a corpus position can match at k only if it matched at k - 1,
+// kgram.rs:12-15, so each level examines only the previous level's hit positions, kept as one bitmap per level), then,
+// per level, the (context, next) pairs of only the contexts some position ends at, counted over that level's hits.
+static inline bool bit_at(const std::vector<u64>& b, i64 p) { return (b[p >> 6] >> (p & 63)) & 1; }
+
 int oracle_longest_match(const u16* tok, const i64* bounds, int nshards, const u16* x, const i32* avail, i64 n,
                          int cap, u32* length, u16* next, u32* count, int threads) {
-    if (cap < 1 || n < 0) return -1;
-    std::vector<u32> tt(n), dd(1);
-    std::vector<u16> t1(n);
-    std::vector<u32> c1(n);
+    if (cap < 1 || n < 0 || nshards < 1) return -1;
+    if (threads < 1) threads = 1;
+    const i64 T = bounds[nshards];
+    const i64 W = (T + 63) / 64;
     std::vector<i32> av(avail, avail + n);
-    for (i64 i = 0; i < n; ++i) {
-        length[i] = 0;
-        next[i] = 0;
-        count[i] = 0;
-    }
-    std::vector<u16> dummy_tgt(n, 0);
+    std::vector<u32> final_id(n, UINT32_MAX);
+    std::vector<std::vector<u64>> hit(cap + 1);  // hit[k]: corpus positions whose k-context matched (bitmap)
+    std::vector<Contexts> ctx(cap + 1);
+    for (i64 i = 0; i < n; ++i) length[i] = 0, next[i] = 0, count[i] = 0;
+    std::vector<std::pair<i64, i64>> pieces;
+    for (int s = 0; s < nshards; ++s)
+        for (i64 p = bounds[s]; p < bounds[s + 1]; p += 1 << 20) pieces.push_back({p, std::min(bounds[s + 1], p + (1 << 20))});
+    auto for_pieces = [&](auto body) {
+        std::atomic<size_t> nxt(0);
+        std::vector<std::thread> ts;
+        for (int t = 0; t < threads; ++t)
+            ts.emplace_back([&, t] {
+                for (size_t q; (q = nxt++) < pieces.size();) body(pieces[q].first, pieces[q].second, t);
+            });
+        for (auto& th : ts) th.join();
+    };
+    // shard of each corpus position, to keep a context inside its shard: position p's k-context is p-k..p-1
+    auto shard_start = [&](i64 p) {
+        return *(std::upper_bound(bounds, bounds + nshards + 1, p) - 1);
+    };
+    int top_level = 0;
     for (int k = 1; k <= cap; ++k) {
-        // positions that matched at k - 1 (all valid at k = 1) keep their avail; the others drop out
         bool any = false;
-        for (i64 i = 0; i < n; ++i) {
-            if (k > 1 && length[i] != (u32)(k - 1)) av[i] = 0;
-            if (av[i] >= k) any = true;
-        }
+        for (i64 i = 0; i < n; ++i) any |= av[i] >= k;
         if (!any) break;
-        oracle_query_counts(tok, bounds, nshards, x, dummy_tgt.data(), av.data(), n, k, 1, 1, tt.data(), nullptr,
-                            nullptr, t1.data(), c1.data(), nullptr, threads);
-        for (i64 i = 0; i < n; ++i)
-            if (av[i] >= k && tt[i] > 0) {
-                length[i] = k;
-                next[i] = t1[i];
-                count[i] = c1[i];
+        ctx[k].build(x, av.data(), n, k);
+        std::vector<uint8_t> found(ctx[k].reps.size(), 0);
+        hit[k].assign(W, 0);
+        for_pieces([&](i64 a, i64 b, int) {
+            const i64 s0 = shard_start(a);
+            for (i64 p = std::max(a, s0 + k); p < b; ++p) {
+                if (k > 1 && !bit_at(hit[k - 1], p)) continue;
+                const u32 id = ctx[k].find(tok + p - k);
+                if (id == UINT32_MAX) continue;
+                found[id] = 1;
+                __atomic_fetch_or(&hit[k][p >> 6], 1ull << (p & 63), __ATOMIC_RELAXED);
             }
+        });
+        for (i64 i = 0; i < n; ++i) {
+            if (av[i] < k) continue;
+            const u32 id = ctx[k].key_of[i];
+            if (id != UINT32_MAX && found[id]) {
+                length[i] = (u32)k;
+                final_id[i] = id;
+            } else {
+                av[i] = 0;  // no longer matching: out of the deeper levels
+            }
+        }
+        top_level = k;
+        if (getenv("ORACLE_TRACE")) fprintf(stderr, "exist k=%d %.3f\n", k, std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count());
+    }
+    // counting: per level, the contexts some position ends at, over that level's hit positions
+    for (int k = 1; k <= top_level; ++k) {
+        std::vector<uint8_t> wanted(ctx[k].reps.size(), 0);
+        bool any = false;
+        for (i64 i = 0; i < n; ++i)
+            if (length[i] == (u32)k) wanted[final_id[i]] = 1, any = true;
+        if (!any) continue;
+        std::vector<std::vector<u64>> acc(threads);
+        for_pieces([&](i64 a, i64 b, int t) {
+            const i64 s0 = shard_start(a);
+            for (i64 p = std::max(a, s0 + k); p < b; ++p) {
+                if (!bit_at(hit[k], p)) continue;
+                const u32 id = ctx[k].find(tok + p - k);
+                if (id != UINT32_MAX && wanted[id]) acc[t].push_back(((u64)id << 16) | tok[p]);
+            }
+        });
+        std::vector<Ranked> per(ctx[k].reps.size());
+        group_entries(acc, per, threads);
+        for (i64 i = 0; i < n; ++i)
+            if (length[i] == (u32)k && !per[final_id[i]].ranked.empty()) {
+                next[i] = per[final_id[i]].ranked[0].second;
+                count[i] = per[final_id[i]].ranked[0].first;
+            }
+        if (getenv("ORACLE_TRACE")) fprintf(stderr, "count k=%d %.3f\n", k, std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count());
     }
     return 0;
 }
@@ -360,6 +454,10 @@ i64 oracle_online(const u16* tok, i64 n, const i64* bounds, int nparts, const u3
                   u32 step_lo, u32 step_hi, int16_t* cell, u16* next, u16* weights, u32* tot, u16* dist, u32* cnt) {
     const u32 NONE = 0xFFFFFFFFu;
     if (entries < 1 || nparts < 1 || step_lo > step_hi) return -1;
+    for (int i = 0; i < nl; ++i)
+        if (levels[i] < 1 || levels[i] > 8) return -1;  // contexts pack into 128 bits up to 8 tokens
+    for (int i = 0; i < nc; ++i)
+        if (count_levels[i] < 1 || count_levels[i] > 8) return -1;
     std::vector<u32> seg(n), part_end(n), part_lo(n);
     for (int j = 0; j < nparts; ++j) {
         i64 s0 = bounds[j];
@@ -370,21 +468,29 @@ i64 oracle_online(const u16* tok, i64 n, const i64* bounds, int nparts, const u3
             part_lo[g] = (u32)bounds[j];
         }
     }
+    if (n >= (i64)1 << 32) return -1;
     struct El {
-        i64 g;
-        u32 time;
-        int kind;  // 0 occurrence, 1 query
+        u128 key;  // the k tokens g-k+1..g packed 16 bits each, first token highest: exact, ordered like the tokens
+        u32 tk;    // time << 1 | kind (0 occurrence, 1 query): ordered by time, then occurrences first
+        u32 g;
+    };
+    auto pack = [&](i64 g, int k) {
+        u128 v = 0;
+        for (i64 q = g - k + 1; q <= g; ++q) v = (v << 16) | tok[q];
+        return v;
     };
     std::vector<uint8_t> filled(n, 0);
-    i64 hinted = 0;
-    // levels needed: hint levels (descending) and count levels
+    std::atomic<i64> hinted(0);
+    const int T = std::max(1, (int)std::thread::hardware_concurrency());
+    auto now = [] { return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count(); };
+    // levels needed: hint levels (descending: a position's row comes from its deepest level) and count levels
     std::vector<int> all;
     for (int i = 0; i < nl; ++i) all.push_back(levels[i]);
     for (int i = 0; i < nc; ++i) all.push_back(count_levels[i]);
     std::sort(all.begin(), all.end(), std::greater<int>());
     all.erase(std::unique(all.begin(), all.end()), all.end());
-    std::vector<u32> counts(1 << 16, 0);
     for (int k : all) {
+        const double t0 = now();
         int li = -1, ci = -1;
         for (int i = 0; i < nl; ++i)
             if (levels[i] == k)
@@ -392,95 +498,117 @@ i64 oracle_online(const u16* tok, i64 n, const i64* bounds, int nparts, const u3
                     if (buckets[b] == k) li = b;
         for (int i = 0; i < nc; ++i)
             if (count_levels[i] == k) ci = i;
-        std::vector<El> els;
-        for (i64 g = 0; g < n; ++g) {
-            // occurrence ending at g: tokens g-k+1..g and next g+1 within g's part
-            if (g - k + 1 >= (i64)part_lo[g] && g + 1 < (i64)part_end[g]) {
-                u32 a = 0;
-                bool ok = true;
-                for (i64 q = g - k + 1; q <= g + 1; ++q) {
-                    if (tau[q] == NONE) ok = false;
-                    else a = std::max(a, tau[q]);
+        // the level's elements: occurrences (available at alpha = 1 + max tau over their k + 1 tokens) and queries,
+        // built in parallel ranges of positions
+        std::vector<std::vector<El>> part(T);
+        parallel_for(n, T, [&](i64 lo, i64 hi, int t) {
+            for (i64 g = lo; g < hi; ++g) {
+                // occurrence ending at g: tokens g-k+1..g and next g+1 within g's part
+                if (g - k + 1 >= (i64)part_lo[g] && g + 1 < (i64)part_end[g]) {
+                    u32 a = 0;
+                    bool ok = true;
+                    for (i64 q = g - k + 1; q <= g + 1; ++q) {
+                        if (tau[q] == NONE) ok = false;
+                        else a = std::max(a, tau[q]);
+                    }
+                    if (ok && a + 1 < step_hi) part[t].push_back({pack(g, k), (a + 1) << 1, (u32)g});
                 }
-                if (ok && a + 1 < step_hi) els.push_back({g, a + 1, 0});
+                if (tau_in[g] != NONE && tau_in[g] >= step_lo && tau_in[g] < step_hi && g - (i64)seg[g] + 1 >= k)
+                    part[t].push_back({pack(g, k), (tau_in[g] << 1) | 1u, (u32)g});
             }
-            if (tau_in[g] != NONE && tau_in[g] >= step_lo && tau_in[g] < step_hi && g - (i64)seg[g] + 1 >= k)
-                els.push_back({g, tau_in[g], 1});
-        }
-        auto ctx_less = [&](i64 a, i64 b) {
-            return std::lexicographical_compare(tok + a - k + 1, tok + a + 1, tok + b - k + 1, tok + b + 1);
-        };
-        std::sort(els.begin(), els.end(), [&](const El& x, const El& y) {
-            if (ctx_less(x.g, y.g)) return true;
-            if (ctx_less(y.g, x.g)) return false;
-            if (x.time != y.time) return x.time < y.time;
-            if (x.kind != y.kind) return x.kind < y.kind;
+        });
+        std::vector<El> els;
+        for (auto& v : part) els.insert(els.end(), v.begin(), v.end()), std::vector<El>().swap(v);
+        const double tb = now();
+        __gnu_parallel::sort(els.begin(), els.end(), [](const El& x, const El& y) {
+            if (x.key != y.key) return x.key < y.key;
+            if (x.tk != y.tk) return x.tk < y.tk;
             return x.g < y.g;
         });
-        size_t i = 0;
-        while (i < els.size()) {
-            size_t j = i;
-            while (j < els.size() && !ctx_less(els[i].g, els[j].g) && !ctx_less(els[j].g, els[i].g)) ++j;
-            std::vector<u16> touched;
-            std::vector<std::pair<u32, u16>> top;  // (count, token), best first
-            u32 total = 0;
-            auto better = [](std::pair<u32, u16> a, std::pair<u32, u16> b) {
-                return a.first > b.first || (a.first == b.first && a.second < b.second);
-            };
-            for (size_t e = i; e < j; ++e) {
-                const El& el = els[e];
-                if (el.kind == 0) {
-                    u16 t = tok[el.g + 1];
-                    if (counts[t] == 0) touched.push_back(t);
-                    u32 c = ++counts[t];
-                    ++total;
-                    int pos = -1;
-                    for (size_t q = 0; q < top.size(); ++q)
-                        if (top[q].second == t) pos = (int)q;
-                    if (pos < 0) {
-                        if ((int)top.size() < entries) {
-                            top.push_back({c, t});
-                            pos = (int)top.size() - 1;
-                        } else if (better({c, t}, top[entries - 1])) {
-                            pos = entries - 1;
+        const double t1 = now();
+        // the walk: each context's elements in (time, occurrences first, position) order; chunks of whole contexts
+        // walked in parallel (a query position is in one context per level)
+        std::vector<size_t> cut(T + 1, els.size());
+        cut[0] = 0;
+        for (int t = 1; t < T; ++t) {
+            size_t c = els.size() * t / T;
+            while (c > 0 && c < els.size() && els[c].key == els[c - 1].key) ++c;
+            cut[t] = std::max(c, cut[t - 1]);
+        }
+        parallel_for(T, T, [&](i64 t0c, i64 t1c, int) {
+            std::vector<u32> counts(1 << 16, 0);
+            for (i64 chunk = t0c; chunk < t1c; ++chunk) {
+                size_t i = cut[chunk];
+                const size_t end = cut[chunk + 1];
+                while (i < end) {
+                    size_t j = i;
+                    while (j < els.size() && els[j].key == els[i].key) ++j;
+                    std::vector<u16> touched;
+                    std::vector<std::pair<u32, u16>> top;  // (count, token), best first
+                    u32 total = 0;
+                    auto better = [](std::pair<u32, u16> a, std::pair<u32, u16> b) {
+                        return a.first > b.first || (a.first == b.first && a.second < b.second);
+                    };
+                    for (size_t e = i; e < j; ++e) {
+                        const El& el = els[e];
+                        if ((el.tk & 1) == 0) {
+                            u16 t = tok[el.g + 1];
+                            if (counts[t] == 0) touched.push_back(t);
+                            u32 c = ++counts[t];
+                            ++total;
+                            int pos = -1;
+                            for (size_t q = 0; q < top.size(); ++q)
+                                if (top[q].second == t) pos = (int)q;
+                            if (pos < 0) {
+                                if ((int)top.size() < entries) {
+                                    top.push_back({c, t});
+                                    pos = (int)top.size() - 1;
+                                } else if (better({c, t}, top[entries - 1])) {
+                                    pos = entries - 1;
+                                }
+                            }
+                            if (pos >= 0) {
+                                top[pos] = {c, t};
+                                while (pos > 0 && better(top[pos], top[pos - 1])) {
+                                    std::swap(top[pos], top[pos - 1]);
+                                    --pos;
+                                }
+                            }
+                        } else if (total > 0) {
+                            const i64 g = (i64)el.g;
+                            if (ci >= 0) {
+                                tot[g * nc + ci] = total;
+                                dist[g * nc + ci] = (u16)std::min<size_t>(touched.size(), 65535);
+                                cnt[g * nc + ci] = g + 1 < (i64)part_end[g] ? counts[tok[g + 1]] : 0;
+                            }
+                            if (li >= 0 && !filled[g]) {
+                                static const u32 CE[6] = {2, 3, 5, 9, 17, 33};
+                                static const double PE[5] = {0.3, 0.5, 0.7, 0.85, 0.95};
+                                int cb = 0, pb = 0;
+                                for (u32 c : CE) cb += c <= total;
+                                for (double p : PE) pb += p <= (double)top[0].first / (double)total;
+                                cell[g] = (int16_t)(((1 + li) * 7 + cb) * 6 + pb);
+                                double sum = 0;
+                                for (auto& tc : top) sum += tc.first;
+                                for (int r = 0; r < entries; ++r) {
+                                    next[g * entries + r] = r < (int)top.size() ? top[r].second : 0;
+                                    weights[g * entries + r] =
+                                        r < (int)top.size() ? (u16)std::nearbyint((double)top[r].first / sum * 65535.0)
+                                                            : 0;
+                                }
+                                filled[g] = 1;
+                                ++hinted;
+                            }
                         }
                     }
-                    if (pos >= 0) {
-                        top[pos] = {c, t};
-                        while (pos > 0 && better(top[pos], top[pos - 1])) {
-                            std::swap(top[pos], top[pos - 1]);
-                            --pos;
-                        }
-                    }
-                } else if (total > 0) {
-                    const i64 g = el.g;
-                    if (ci >= 0) {
-                        tot[g * nc + ci] = total;
-                        dist[g * nc + ci] = (u16)std::min<size_t>(touched.size(), 65535);
-                        cnt[g * nc + ci] = g + 1 < (i64)part_end[g] ? counts[tok[g + 1]] : 0;
-                    }
-                    if (li >= 0 && !filled[g]) {
-                        static const u32 CE[6] = {2, 3, 5, 9, 17, 33};
-                        static const double PE[5] = {0.3, 0.5, 0.7, 0.85, 0.95};
-                        int cb = 0, pb = 0;
-                        for (u32 c : CE) cb += c <= total;
-                        for (double p : PE) pb += p <= (double)top[0].first / (double)total;
-                        cell[g] = (int16_t)(((1 + li) * 7 + cb) * 6 + pb);
-                        double sum = 0;
-                        for (auto& tc : top) sum += tc.first;
-                        for (int r = 0; r < entries; ++r) {
-                            next[g * entries + r] = r < (int)top.size() ? top[r].second : 0;
-                            weights[g * entries + r] =
-                                r < (int)top.size() ? (u16)std::nearbyint((double)top[r].first / sum * 65535.0) : 0;
-                        }
-                        filled[g] = 1;
-                        ++hinted;
-                    }
+                    for (u16 t : touched) counts[t] = 0;
+                    i = j;
                 }
             }
-            for (u16 t : touched) counts[t] = 0;
-            i = j;
-        }
+        });
+        if (getenv("ORACLE_TRACE"))
+            fprintf(stderr, "online k=%d: %zu elements, built %.2f s, sorted %.2f s, walked %.2f s\n", k, els.size(),
+                    tb - t0, t1 - tb, now() - t1);
     }
     return hinted;
 }

@@ -53,7 +53,7 @@ def lib() -> ctypes.CDLL:
         P = ctypes.c_void_p
         so.oracle_query_counts.restype = ctypes.c_int64
         so.oracle_query_counts.argtypes = [P, P, ctypes.c_int, P, P, P, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
-                                           ctypes.c_int, P, P, P, P, P, P, ctypes.c_int]
+                                           ctypes.c_int, P, P, P, P, P, P, P, ctypes.c_int]
         so.oracle_table_counts.restype = ctypes.c_int64
         so.oracle_table_counts.argtypes = [P, P, ctypes.c_int, P, P, P, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
                                            ctypes.c_int, P, P, P, P, P, P, P, ctypes.c_int]
@@ -106,19 +106,26 @@ def _alloc(n: int, ntop: int) -> Outputs:
 
 
 def query_counts(train: np.ndarray, bounds: np.ndarray, x: np.ndarray, tgt: np.ndarray, avail: np.ndarray, k: int,
-                 cnt_top: int = TOP, ntop: int = 8, nthreads: int | None = None, hits: bool = False) -> Outputs:
+                 cnt_top: int = TOP, ntop: int = 8, nthreads: int | None = None, hits: bool = False,
+                 gate: np.ndarray | None = None) -> Outputs:
     """Query-filtered counts of level k (kgram.rs restatement). `train` is the shards concatenated, shard s being
-    train[bounds[s]:bounds[s+1]]."""
+    train[bounds[s]:bounds[s+1]]. `hits`: also the corpus positions whose k-context matched (uint8 per position).
+    `gate` (uint8 per corpus position, e.g. the previous level's hits): only its set positions are examined -- exact
+    for the levels above the gate's, since a k-context occurs only where its (k-1)-suffix does (kgram.rs:12-15)."""
     train = np.ascontiguousarray(train, np.uint16)
     bounds = np.ascontiguousarray(bounds, np.int64)
     x = np.ascontiguousarray(x, np.uint16)
     tgt = np.ascontiguousarray(tgt, np.uint16)
     avail = np.ascontiguousarray(avail, np.int32)
+    if gate is not None:
+        gate = np.ascontiguousarray(gate, np.uint8)
+        if len(gate) != len(train):
+            raise ValueError("gate needs one byte per corpus position")
     out = _alloc(len(x), ntop)
     hb = np.zeros(len(train), np.uint8) if hits else None
     events = lib().oracle_query_counts(_p(train), _p(bounds), len(bounds) - 1, _p(x), _p(tgt), _p(avail), len(x), k,
                                        cnt_top, max(ntop, 1), _p(out["tot"]), _p(out["dist"]), _p(out["cnt"]),
-                                       _p(out["top_tok"]), _p(out["top_cnt"]), _p(hb), nthreads or threads())
+                                       _p(out["top_tok"]), _p(out["top_cnt"]), _p(hb), _p(gate), nthreads or threads())
     if events < 0:
         raise ValueError("oracle_query_counts: bad arguments")
     out["events"] = int(events)

@@ -20,8 +20,9 @@ def test_more_than_one_gpu_is_refused():
 @pytest.mark.gpu
 def test_tiny_bench_line():
     r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--train-tokens", "3000000", "--query-tokens",
-                        "200001", "--steps", "1", "--warmup", "1", "--no-secondary", "--cpu-tokens", "300000",
-                        "--cpu-queries", "20000"], capture_output=True, text=True, timeout=600, cwd=ROOT)
+                        "200001", "--steps", "1", "--warmup", "1", "--no-secondary", "--cpu-tokens", "1000000",
+                        "--cpu-queries", "20000", "--parity-windows", "50"], capture_output=True, text=True,
+                       timeout=600, cwd=ROOT)
     assert r.returncode == 0, r.stderr[-2000:]
     lines = [ln for ln in r.stdout.splitlines() if ln.strip()]
     assert len(lines) == 1
@@ -36,3 +37,8 @@ def test_tiny_bench_line():
     assert abs(rf["frac"] - rf["achieved"] / rf["peak"]) < 1e-9 and rf["achieved"] > 0
     cpu = j["cpu_baseline"]
     assert cpu["kind"] == "port" and cpu["cores"] >= 1 and cpu["value"] > 0 and cpu["sample"]
+    # the GPU's outputs against the oracle's: the baseline's prefix sample and windows over the whole corpus
+    par = j["parity"]
+    assert par["mismatching_positions"] == 0
+    assert par["prefix"]["positions"] == 20000 and par["windows"]["positions"] >= 50 * 64
+    assert j["roofline_family"]["frac"] > 0 and j["count_path_roofline"]["frac"] > 0

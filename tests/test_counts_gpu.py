@@ -1,6 +1,7 @@
-"""GPU: the record flavour (libngram_amd_record.so through CountBuild, the mirror of
-record_367_gpu_counts/track_1_short/counts/build.py) bit-exact against the CPU oracle on seeded synthetic streams:
-per level tot / dist / cnt (no TOP rule), the top-4 next tokens, the record's rows and batch_rows."""
+"""GPU: the record's surface (CountBuild, record_367_gpu_counts/track_1_short/counts/build.py, on the engine's level
+pipeline) bit-exact against the CPU oracle on seeded synthetic streams: per level tot / dist / cnt (no TOP rule), the
+top-4 next tokens, the record's rows and batch_rows; the partitioned count's variants (repartitioning, the escape
+table, the scans' listing modes, the regions read directly)."""
 
 import numpy as np
 import pytest
@@ -8,8 +9,9 @@ import torch
 
 import oracle as O
 from ngram_amd import counts as C
-from ngram_amd import partcount as P
 from ngram_amd import data
+from ngram_amd import levels as levels_mod
+from ngram_amd import partcount as P
 
 pytestmark = pytest.mark.gpu
 
@@ -33,53 +35,33 @@ def _reference(corpus, levels, level_shards, ntop=8):
     return ref
 
 
-def _partition_small_tables(monkeypatch):
-    # every table is partitioned into several sub-tables, and each shard's emitted keys are flushed on their own
-    monkeypatch.setattr(C, "PART_MIN_BYTES", 1 << 16)
-    monkeypatch.setattr(C, "SUB_BYTES", 1 << 18)
-    monkeypatch.setattr(C, "EMIT_CHUNK", 1)
-
-
-@pytest.mark.parametrize("level_shards,mode", [({}, "engine"), ({2: 1, 3: 2}, "engine"), ({}, "engine-compact"),
-                                               ({2: 1, 3: 2}, "engine-compact"), ({}, "record"),
-                                               ({2: 1, 3: 2}, "record"), ({}, "partitioned"),
-                                               ({2: 1, 3: 2}, "partitioned"), ({}, "part"), ({2: 1, 3: 2}, "part"),
-                                               ({}, "part-compact"), ({2: 1, 3: 2}, "part-regroup"),
-                                               ({}, "part-escape"), ({}, "part-unpacked"), ({}, "part-seg"),
-                                               ({2: 1, 3: 2}, "part-seg"), ({}, "part-list"),
-                                               ({2: 1, 3: 2}, "part-list")])
+@pytest.mark.parametrize("level_shards,mode", [({}, "part"), ({2: 1, 3: 2}, "part"), ({}, "compact"),
+                                               ({2: 1, 3: 2}, "regroup"), ({}, "escape"), ({}, "seg"),
+                                               ({2: 1, 3: 2}, "seg"), ({}, "list"), ({2: 1, 3: 2}, "list")])
 def test_counts_match_oracle(corpus, level_shards, mode, monkeypatch):
-    if mode == "partitioned":
-        _partition_small_tables(monkeypatch)
-    if mode == "part-regroup":
+    if mode == "regroup":
         # one partition per level to start with: each level's LDS table overflows and it is repartitioned bit by bit;
         # three blocks, each counting a run of partitions
         monkeypatch.setattr(P, "PART_TARGET", 1 << 30)
         monkeypatch.setattr(P, "PART_MIN_BITS", 0)
         monkeypatch.setattr(P, "PART_BLOCKS", 3)
-    if mode == "part-seg":  # the partition sort's first pass reads the scan regions however few events they hold
+    if mode == "seg":  # the partition sort's first pass reads the scan regions however few events they hold
         monkeypatch.setattr(P, "SEG_MIN_EVENTS", 0)
-    if mode in ("part-escape", "part-unpacked"):
-        # an 8-bit count field: counts of 255 and more go to the escape table; with a 4-slot table it overflows and
-        # every level is counted again unpacked
+    if mode == "escape":  # an 8-bit count field: counts of 255 and more go to the escape table
         monkeypatch.setattr(P, "PACK_MIN_BITS", 40)
-        if mode == "part-unpacked":
-            monkeypatch.setattr(P, "ESC_CAP", 4)
-    lib = C.record_lib()
     cb = C.CountBuild(corpus.shards(), levels=LEVELS, level_shards=level_shards, topk=4)
-    cb.mode = mode.split("-")[0]
-    if mode.endswith("-compact") or mode.endswith("-list"):
-        # every gated level scans its LDS-listed set positions, or (part-list) the positions listed in memory first
-        cb.density = {k: 0.0 for k in LEVELS}
-        if mode == "part-compact":
-            monkeypatch.setattr(C, "LIST_DENSITY", 0.0)
+    if mode in ("compact", "list"):
+        # every gated level scans its LDS-listed set positions, or (list) the positions listed in memory first
+        cb.engine.density = {k: 0.0 for k in LEVELS}
+        if mode == "compact":
+            monkeypatch.setattr(levels_mod, "LIST_DENSITY", 0.0)
     cb.start_load(3)
     with pytest.raises(ValueError):
         cb.load_ms()  # a share of the copies is still pending
     cb.pace()
     cb.pace()
     assert cb.load_ms() > 0
-    x, tgt, avail = C.queries(corpus.query, [], "cuda", lib)
+    x, tgt, avail = C.queries(corpus.query, [], "cuda")
     out = cb.counts(x, tgt, avail, stats=True).cpu().numpy()
     ref = _reference(corpus, LEVELS, level_shards)
     top_tok = cb.top_tok.cpu().numpy().view(np.uint16)
@@ -92,13 +74,10 @@ def test_counts_match_oracle(corpus, level_shards, mode, monkeypatch):
         assert np.array_equal(top_tok[li], o["top_tok"][:, :4]), f"top_tok k={k}"
         assert np.array_equal(top_cnt[li], o["top_cnt"][:, :4]), f"top_cnt k={k}"
         assert cb.info[k]["hits"] == o["events"], f"hits k={k}"
-        if not mode.startswith("part-") and mode != "part":
-            assert (cb.info[k]["pbits"] > 0) == (mode == "partitioned"), k
-    if mode == "part-regroup":
+    if mode == "regroup":
         assert cb.info[2]["pbits"] >= 3, cb.info[2]
     assert (ref[2]["tot"] > 0).sum() > 1000 and (ref[20]["tot"] > 0).sum() > 10
-    # the record's rows from ROW_LEVELS, and a batch of them
-    ri = [LEVELS.index(k) for k in C.ROW_LEVELS]
+    # the record's rows from ROW_LEVELS (ng_record_rows), and a batch of them (ng_batch_rows)
     tot_rows = np.stack([ref[k]["tot"] for k in C.ROW_LEVELS])
     cells, entries = O.record_rows(tot_rows, np.stack([ref[k]["top_tok"] for k in C.ROW_LEVELS]),
                                    np.stack([ref[k]["top_cnt"] for k in C.ROW_LEVELS]))
@@ -107,41 +86,21 @@ def test_counts_match_oracle(corpus, level_shards, mode, monkeypatch):
     n = 500
     cap = int((entries[1000 : 1000 + n] != 0).sum()) + 7
     assert np.array_equal(cb.batch_rows(1000, n, cap).cpu().numpy(), O.batch_rows(cells, entries, 1000, n, cap))
-    del ri
-
-
-@pytest.mark.parametrize("mode", ["engine", "record", "partitioned"])
-def test_overflow_reruns_only_the_level(corpus, monkeypatch, mode):
-    if mode == "partitioned":
-        _partition_small_tables(monkeypatch)
-    lib = C.record_lib()
-    tok_cb = C.CountBuild(corpus.shards(), levels=(2, 3, 6), topk=2)
-    tok_cb.start_load(1)
-    x, tgt, avail = C.queries(corpus.query, [], "cuda", lib)
-    monkeypatch.setattr(C, "LOAD", 1e9)
-    tok_cb.min_cap = 1024
-    tok_cb.mode = mode
-    out = tok_cb.counts(x, tgt, avail).cpu().numpy()
-    assert tok_cb.info[2]["reruns"] > 0
-    ref = _reference(corpus, (2, 3, 6), {})
-    for li, k in enumerate((2, 3, 6)):
-        assert np.array_equal(out[0, li].view(np.uint32), ref[k]["tot"]), k
-        assert np.array_equal(out[2, li].view(np.uint32), ref[k]["cnt"]), k
+    with pytest.raises(AssertionError):
+        cb.batch_rows(1000, n, cap - 8)
 
 
 def test_device_queries_match_host_queries(corpus):
-    lib = C.record_lib()
     q = torch.from_numpy(corpus.query.view(np.int16)).cuda()
-    a = C.device_queries(q, lib)
-    b = C.queries(corpus.query, [], "cuda", lib)
+    a = C.device_queries(q)
+    b = C.queries(corpus.query, [], "cuda")
     for u, v in zip(a, b):
         assert torch.equal(u, v)
 
 
 def test_fit_blocks_start_segments(corpus):
-    lib = C.record_lib()
     blocks = [corpus.query[:300], corpus.query[300:700]]
-    x, tgt, avail = C.queries(corpus.query[:1001], blocks, "cuda", lib)
+    x, tgt, avail = C.queries(corpus.query[:1001], blocks, "cuda")
     av = avail.cpu().numpy()
     assert av[1000] == 1 and av[1000 + 299] == 1
     xs = np.concatenate([corpus.query[:1000], blocks[0][:-1], blocks[1][:-1]])
@@ -156,12 +115,11 @@ def test_context_hints_from_an_earlier_build(corpus, monkeypatch, margin):
     from ngram_amd import qindex as Q
 
     monkeypatch.setattr(Q, "EXPECT_MARGIN", margin)
-    lib = C.record_lib()
     cb = C.CountBuild(corpus.shards(), levels=LEVELS, level_shards={}, topk=4)
     cb.start_load(1)
     full = corpus.query
     for q in (full, full[:3001], full):
-        x, tgt, avail = C.queries(q, [], "cuda", lib)
+        x, tgt, avail = C.queries(q, [], "cuda")
         out = cb.counts(x, tgt, avail).cpu().numpy()
         xs, ts = q[:-1], q[1:]
         av = O.segments(xs)
@@ -171,18 +129,13 @@ def test_context_hints_from_an_earlier_build(corpus, monkeypatch, margin):
             assert np.array_equal(out[2, li].view(np.uint32), o["cnt"]), (len(q), k)
 
 
-@pytest.mark.parametrize("mode", ["part", "engine"])
-def test_counts_from_device_tokens(corpus, mode):
+def test_counts_from_device_tokens(corpus):
     """CountBuild.from_device (the shards already laid out in GPU memory, as the benchmark builds): every level's scan
     is one launch over all the shards, the first level included; tot / dist / cnt and the top-4 match the oracle, in
     a first build and in a second that uses the first one's densities and sizes."""
-    from ngram_amd.gpu_val_stats import load_shards
-
-    lib = C.record_lib()
-    tok, sizes, starts, L = load_shards(corpus.shards())
+    tok, sizes, starts, L = data.device_tokens(corpus.shards())
     cb = C.CountBuild.from_device(tok, sizes, starts, levels=LEVELS, level_shards={}, topk=4)
-    cb.mode = mode
-    x, tgt, avail = C.queries(corpus.query, [], "cuda", lib)
+    x, tgt, avail = C.queries(corpus.query, [], "cuda")
     ref = _reference(corpus, LEVELS, {})
     for stats in (True, False):
         out = cb.counts(x, tgt, avail, stats=stats).cpu().numpy()
@@ -203,13 +156,12 @@ def test_emit_region_overflow_raises(corpus, monkeypatch, packed):
     and writes nothing past its region): the count raises before it reads a region, whether it reads the scan's flags
     with the event total of the regions' digit histograms or (packed: no histograms, the regions packed) on their
     own."""
-    lib = C.record_lib()
     cb = C.CountBuild(corpus.shards(), levels=(2, 3), level_shards={}, topk=4)
     cb.start_load(1)
-    x, tgt, avail = C.queries(corpus.query, [], "cuda", lib)
+    x, tgt, avail = C.queries(corpus.query, [], "cuda")
     if packed:
         cb.counts(x, tgt, avail)  # a first build: its event counts let the next one go without digit histograms
         monkeypatch.setattr(P, "SEG_MIN_EVENTS", 1 << 40)
-    monkeypatch.setattr(C, "emit_region", lambda L, G: 64)
+    monkeypatch.setattr(levels_mod, "emit_region", lambda L, G: 64)
     with pytest.raises(RuntimeError, match="emit region overflowed"):
         cb.counts(x, tgt, avail)

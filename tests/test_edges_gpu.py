@@ -8,7 +8,9 @@ import torch
 
 import oracle as O
 from ngram_amd import counts as C
+from ngram_amd import data
 from ngram_amd import gpu_val_stats as G
+from ngram_amd.lib import Lib
 from ngram_amd.count_table import CountTable
 from ngram_amd.longest import _segments, longest_match
 
@@ -33,14 +35,15 @@ def ragged():
     return shards, np.concatenate(shards), bounds, q
 
 
-@pytest.mark.parametrize("mode", ["part", "engine", "record"])
+@pytest.mark.parametrize("mode", ["dense", "list"])
 def test_counts_on_ragged_shards(ragged, mode):
     shards, train, bounds, q = ragged
     levels = (1, 2, 3, 5, 8, 20)
     cb = C.CountBuild(shards, levels=levels, level_shards={}, topk=4)
-    cb.mode = mode
+    if mode == "list":  # every gated level probes the previous level's hits listed in memory
+        cb.engine.density = {k: 0.0 for k in levels}
     cb.start_load(1)
-    x, tgt, avail = C.queries(q, [], "cuda", cb.lib)
+    x, tgt, avail = C.queries(q, [], "cuda")
     out = cb.counts(x, tgt, avail, stats=True).cpu().numpy()
     xs, ts = q[:-1], q[1:]
     av = O.segments(xs)
@@ -56,9 +59,9 @@ def test_counts_on_ragged_shards(ragged, mode):
 
 def test_val_stats_on_ragged_shards(ragged):
     shards, train, bounds, q = ragged
-    tok, sizes, starts, L = G.load_shards(shards)
-    x, tgt, avail = G.query_tensors(q)
-    res = G.build_stats(G.Lib(), tok, L, starts, sizes, x, tgt, avail)
+    tok, sizes, starts, L = data.device_tokens(shards)
+    x, tgt, avail = G.val_queries(q)
+    res = G.build_stats(tok, sizes, starts, x, tgt, avail)
     counts = res["counts"].cpu().numpy()
     xs, ts = q[:-1], q[1:]
     av = O.segments(xs)
@@ -71,10 +74,10 @@ def test_val_stats_on_ragged_shards(ragged):
 @pytest.mark.parametrize("cap", [64, 3])
 def test_longest_on_ragged_shards(ragged, cap):
     shards, train, bounds, q = ragged
-    tok, sizes, starts, L = G.load_shards(shards)
+    tok, sizes, starts, L = data.device_tokens(shards)
     xs = q[:-1]
     xt = torch.from_numpy(xs.view(np.int16).copy()).cuda()
-    av = _segments(xt, C.record_lib())
+    av = _segments(xt, Lib())
     length, nxt, cnt, _ = longest_match(tok, xt, av, cap)
     want = O.longest_match(train, bounds, xs, O.segments(xs), cap)
     assert np.array_equal(length.cpu().numpy().view(np.uint32), want[0])

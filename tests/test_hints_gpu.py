@@ -47,7 +47,7 @@ def test_device_rows_match_cpu_and_torch(hint_dir, monkeypatch):
         assert torch.equal(g.cell.cpu(), c.cell) and torch.equal(g.tokens.cpu(), c.tokens)
         assert torch.equal(g.counts.cpu(), c.counts)
         # the reference's widening by torch on the GPU (division by the scalar): bit-exact
-        raw = torch.from_numpy(np.asarray(H._take(gpu._val.weights, index)).view(np.int16).copy()).cuda()
+        raw = torch.from_numpy(np.asarray(gpu._val.a["weights"][index]).view(np.int16).copy()).cuda()
         assert torch.equal(g.weights, (raw.int() & 0xFFFF).float() / H.WEIGHT_ONE)
         assert torch.allclose(g.weights.cpu(), c.weights, rtol=1e-6, atol=0)
     t = gpu.train(0, np.arange(6000, 7000))
@@ -67,9 +67,9 @@ def test_fake_rows_on_device(monkeypatch):
 def test_val_stats_outputs_through_the_directory(tmp_path, monkeypatch):
     """The validation statistics' rows and counts, written as a hint directory and read back on the device."""
     corpus = data.make_corpus("c1", train_tokens=400_000, query_tokens=30_001, shard_tokens=200_000)
-    tok, sizes, starts, L = G.load_shards(corpus.shards())
-    x, tgt, avail = G.query_tensors(corpus.query)
-    res = G.build_stats(G.Lib(), tok, L, starts, sizes, x, tgt, avail)
+    tok, sizes, starts, L = data.device_tokens(corpus.shards())
+    x, tgt, avail = G.val_queries(corpus.query)
+    res = G.build_stats(tok, sizes, starts, x, tgt, avail)
     host = G.host_outputs(res)
     N = x.numel()
     v = 0  # the first variant (6, 10, 20)

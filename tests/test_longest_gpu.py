@@ -7,8 +7,8 @@ import torch
 
 import oracle as O
 from ngram_amd import data
-from ngram_amd.counts import record_lib
-from ngram_amd.gpu_val_stats import load_shards
+from ngram_amd.data import device_tokens as load_shards
+from ngram_amd.lib import Lib
 from ngram_amd.longest import LongestMatch, _segments, longest_match
 
 pytestmark = pytest.mark.gpu
@@ -31,7 +31,7 @@ def test_longest_match_matches_oracle(corpus, cap, seg, monkeypatch):
     want = O.longest_match(corpus.train, corpus.bounds, x, avail, cap)
     tok, sizes, starts, L = load_shards(corpus.shards())
     xt = torch.from_numpy(x.view(np.int16).copy()).cuda()
-    av = _segments(xt, record_lib())
+    av = _segments(xt, Lib())
     assert np.array_equal(av.cpu().numpy(), avail)
     length, nxt, cnt, ladder = longest_match(tok, xt, av, cap)
     got = (length.cpu().numpy().view(np.uint32), nxt.cpu().numpy().view(np.uint16), cnt.cpu().numpy().view(np.uint32))
@@ -51,7 +51,7 @@ def test_device_levels_match_host_levels(corpus, monkeypatch):
     x = corpus.query[:-1]
     tok, sizes, starts, L = load_shards(corpus.shards())
     xt = torch.from_numpy(x.view(np.int16).copy()).cuda()
-    av = _segments(xt, record_lib())
+    av = _segments(xt, Lib())
     got = {}
     for dev_levels in (True, False):
         monkeypatch.setattr(LG, "DEVICE_LEVELS", dev_levels)
