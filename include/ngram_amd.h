@@ -287,6 +287,23 @@ int ng_hint_widen(const short* staged, ng_i64 n_cell, ng_i64 n_tok, ng_i64 n_w, 
 int ng_count_rows(const uint32_t* tot, const uint16_t* dist, const uint32_t* cnt, ng_i64 n, int L, float* out,
                   void* stream);
 
+/* Hint rows from ng_ctx_summary's top-8 records (CtxRecord<8>: 16 u32 words per context id, 16-byte aligned).
+ * ng_variant_rows: one gpu_val_stats variant's rows int32 [N, 9] (cell, 4 x two tokens, 4 x two weights) -- the
+ * output of old_records/gpu_val_stats.cu variant_rows :646-699 -- from desc int64 [nv, 4] = (mask bit, length bucket,
+ * ctx_of int32 [N], records) per level of the variant, ascending; positions without a level are left as they are.
+ * ng_record_rows: the record's rows (record_367_gpu_counts/track_1_short/counts/build.py:341-387): cells int32 [N],
+ * entries int32 [N, 8] (16-byte aligned) from desc int64 [nr, 3] = (tot row int32 [N], ctx_of int32 [N], records)
+ * of the ROW_LEVELS levels, ascending.
+ * ng_batch_rows: a training batch's rows (build.py batch_rows :390-403): out int32 [n + 2 * capacity] = the n cells,
+ * then `capacity` (position, entry) pairs of the non-zero entries of entries int32 [n, 8] (16-byte aligned) in
+ * position order, padded with (i % n, 0); *total = the non-zero entries (only the first capacity are written: the
+ * caller raises past it); work: ng_batch_rows_work(n) u32 of workspace. */
+int ng_variant_rows(ng_i64 N, const int* mask, int nv, const ng_i64* desc, int* rows, void* stream);
+int ng_record_rows(ng_i64 N, int nr, const ng_i64* desc, int* cells, int* entries, void* stream);
+ng_i64 ng_batch_rows_work(ng_i64 n);
+int ng_batch_rows(const int* cells, const int* entries, ng_i64 n, ng_i64 capacity, int* out, uint32_t* work,
+                  ng_u64* total, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

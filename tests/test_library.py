@@ -13,7 +13,7 @@ HEADERS = {"ngram_amd.h": "libngram_amd.so", "ngram_amd_record.h": "libngram_amd
 
 def declared_symbols(header: str) -> list[str]:
     text = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / header).read_text(), flags=re.S)
-    return re.findall(r"^\s*(?:int|size_t|void)\s+(\w+)\s*\(", text, flags=re.M)
+    return re.findall(r"^\s*(?:int|size_t|void|ng_i64|ng_u64)\s+(\w+)\s*\(", text, flags=re.M)
 
 
 @pytest.fixture(scope="module")

@@ -2,6 +2,7 @@
 
 import numpy as np
 import pytest
+import torch
 
 import oracle as O
 from ngram_amd import data
@@ -218,3 +219,59 @@ def test_spans_tau():
     # two parts [0, 6), [6, 10); step 0 trains inputs 0..2 (target 3), step 1 inputs 3..5 (target 6 is another part)
     tau, tau_in = O.spans_tau(10, [0, 6, 10], [(0, 3, 0), (3, 6, 1), (6, 9, 0)])
     assert list(tau[:7]) == [0, 0, 0, 0, 1, 1, 0] and tau[9] == 0 and tau_in[3] == 1 and tau_in[9] == O.NONE
+
+
+def test_features_bins_at_float32_edges():
+    """floor(log2) of the float32 total at 2^k - 1: log2(2^k - 1) = k - 2^-k / ln 2 + O(4^-k), and float32 values in
+    [16, 32) are 2^-19 apart, so the deficit rounds away (bin k) once 2^-k / ln 2 < 2^-20, i.e. from k = 21 on; below
+    that the bin is k - 1. 2^25 - 1 rounds to 2^25 as a float32; bins clamp at 24. torch's own float32 log2 agrees."""
+    ks = list(range(18, 26))
+    tot = np.array([[(1 << k) - 1 for k in ks] + [(1 << k) for k in ks]], np.int64)
+    counts = np.zeros((3, 1, tot.shape[1]), np.int32)
+    counts[0, 0] = tot[0].astype(np.uint32).view(np.int32)
+    _, _, _, b, _ = O.features(counts)
+    want = [k - 1 if k <= 20 else min(k, 24) for k in ks] + [min(k, 24) for k in ks]
+    assert list(b[:, 0]) == want
+    t = torch.log2(torch.tensor(tot[0].astype(np.float32)))
+    assert list(torch.clamp(torch.floor(t), 0, 24).long().tolist()) == want
+
+
+def test_record_rows_by_hand():
+    """build.py:341-387 on hand-made totals and tops (levels 6, 10, 20):
+      * position 0: deepest occurring level 10 (tot 3), tops (2, 1) of tokens (7, 9): cell ((1 + 1) * 7 + 2) * 6 + 2
+        = 98 (count bin: 2, 3 <= 3; share 2/3: 0.3, 0.5 <= it), entries 7 | 2 << 16, 9 | 1 << 16;
+      * position 1: only level 6 (tot 40001), top count 40000 > 32767: weights ceil(c * 32767 / 40000): 32767,
+        16384 (for 20000) and 1 (for 1); cell ((1 + 0) * 7 + 6) * 6 + 5 = 83 (share 40000/40001 >= 0.95);
+      * position 2: nothing occurred: cell 0, no entries;
+      * position 3: level 20 with a top count of 3e9 (row_top clamped to 2^31 - 1, share 0.716 -> purity 3) and
+        total 3e9 + 5: cell ((1 + 2) * 7 + 6) * 6 + 3 = 165, weight 32767."""
+    tot = np.zeros((3, 4), np.uint32)
+    tt = np.zeros((3, 4, 8), np.uint16)
+    tc = np.zeros((3, 4, 8), np.uint32)
+    tot[:, 0] = [4, 3, 0]
+    tt[1, 0, :2], tc[1, 0, :2] = [7, 9], [2, 1]
+    tt[0, 0, :1], tc[0, 0, :1] = [7], [4]
+    tot[0, 1] = 40001
+    tt[0, 1, :3], tc[0, 1, :3] = [5, 6, 8], [40000, 20000, 1]
+    tot[:, 3] = [3_000_000_005, 3_000_000_005, 3_000_000_005]
+    tt[2, 3, :2], tc[2, 3, :2] = [11, 12], [3_000_000_000, 5]
+    cells, entries = O.record_rows(tot, tt, tc)
+    assert cells.tolist() == [98, 83, 0, 165]
+    assert entries[0, :3].tolist() == [7 | 2 << 16, 9 | 1 << 16, 0]
+    assert entries[1, :4].tolist() == [5 | 32767 << 16, 6 | 16384 << 16, 8 | 1 << 16, 0]
+    assert not entries[2].any()
+    assert entries[3, :2].tolist() == [11 | 32767 << 16, 12 | 1 << 16]
+
+
+def test_batch_rows_by_hand():
+    """build.py:390-403: cells, then (position, entry) pairs of the non-zero entries in position order, padded with
+    (i % n, 0); more entries than capacity raise."""
+    cells = np.array([5, 0, 7, 9], np.int32)
+    entries = np.zeros((4, 8), np.int32)
+    entries[0, :2] = [101, 102]
+    entries[2, 0] = 103
+    entries[3, 1] = 104  # not in the batch below
+    rows = O.batch_rows(cells, entries, 0, 3, 5)
+    assert rows.tolist() == [5, 0, 7, 0, 101, 0, 102, 2, 103, 0, 0, 1, 0]
+    with pytest.raises(AssertionError):
+        O.batch_rows(cells, entries, 0, 3, 2)
