@@ -303,6 +303,13 @@ int ng_record_rows(ng_i64 N, int nr, const ng_i64* desc, int* cells, int* entrie
 ng_i64 ng_batch_rows_work(ng_i64 n);
 int ng_batch_rows(const int* cells, const int* entries, ng_i64 n, ng_i64 capacity, int* out, uint32_t* work,
                   ng_u64* total, void* stream);
+/* No counterpart in the reference: ng_batch_rows for callers that cannot allocate (code under HIP graph capture, a
+ * training step's tight loop, harnesses that forbid hipMalloc). Same outputs; the workspace is the library's own
+ * device array of 65537 u32 (256 KB per GPU, held until the process ends), so n <= 67,108,864 positions (larger: -1,
+ * nothing launched). Every call on one GPU shares that array: calls that overlap on one GPU race. Nothing is
+ * allocated, freed or cleared inside. */
+int ng_batch_rows_noalloc(const int* cells, const int* entries, ng_i64 n, ng_i64 capacity, int* out, ng_u64* total,
+                          void* stream);
 
 #ifdef __cplusplus
 }

@@ -10,6 +10,8 @@
 //     (position, entry) pairs of the non-zero entries in position order, padded with (i % n, 0).
 // One pass per position; every record read is one line. The float64 steps (share, weights) are the reference's
 // definitions, evaluated in the same order.
+#include <mutex>
+
 #include "ngram_common.h"
 #include "part.h"
 
@@ -248,15 +250,9 @@ extern "C" int ng_record_rows(i64 N, int nr, const i64* desc, int* cells, int* e
 // Workspace u32 entries of ng_batch_rows for n positions.
 extern "C" i64 ng_batch_rows_work(i64 n) { return (n + BR_TILE - 1) / BR_TILE + 1; }
 
-// A batch's rows (int32 [n + 2 * capacity]): cells[0..n), then `capacity` (position, entry) pairs of the non-zero
-// entries (entries int32 [n, 8], 16-byte aligned) in position order, padded with (i % n, 0); *total = the non-zero
-// entries (those past capacity are not written: the caller raises). work: ng_batch_rows_work(n) u32.
-extern "C" int ng_batch_rows(const int* cells, const int* entries, i64 n, i64 capacity, int* out, u32* work,
-                             u64* total, void* stream) {
-    if (n <= 0 || capacity < 0 || ((uintptr_t)entries & 15)) return -1;
-    hipStream_t st = (hipStream_t)stream;
+static int launch_batch_rows(const int* cells, const int* entries, i64 n, i64 capacity, int* out, u32* work,
+                             u64* total, hipStream_t st) {
     const i64 tiles = (n + BR_TILE - 1) / BR_TILE;
-    if (tiles >= (1 << 30)) return -1;
     batch_count_k<<<(int)tiles, 256, 0, st>>>(entries, n, work);
     batch_scan_k<<<1, 1024, 0, st>>>(work, tiles, total);
     batch_write_k<<<(int)tiles, 256, 0, st>>>(cells, entries, n, capacity, work, out);
@@ -265,4 +261,60 @@ extern "C" int ng_batch_rows(const int* cells, const int* entries, i64 n, i64 ca
         batch_pad_k<<<g < 1024 ? g : 1024, 256, 0, st>>>(n, capacity, total, out);
     }
     return (int)hipGetLastError();
+}
+
+// A batch's rows (int32 [n + 2 * capacity]): cells[0..n), then `capacity` (position, entry) pairs of the non-zero
+// entries (entries int32 [n, 8], 16-byte aligned) in position order, padded with (i % n, 0); *total = the non-zero
+// entries (those past capacity are not written: the caller raises). work: ng_batch_rows_work(n) u32.
+extern "C" int ng_batch_rows(const int* cells, const int* entries, i64 n, i64 capacity, int* out, u32* work,
+                             u64* total, void* stream) {
+    if (n <= 0 || capacity < 0 || ((uintptr_t)entries & 15)) return -1;
+    if ((n + BR_TILE - 1) / BR_TILE >= (1 << 30)) return -1;
+    return launch_batch_rows(cells, entries, n, capacity, out, work, total, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// ng_batch_rows without a workspace argument, for callers that cannot allocate (HIP graph capture, a training step's
+// tight loop): the per-tile offsets live in `scratch`, a file-scope device array of NOALLOC_TILES + 1 u32 (256 KB),
+// which each GPU holds until the process ends. Its address is looked up once per device (hipGetSymbolAddress, on the
+// first call with that device current) and passed to the kernels. Every call on one GPU shares the array: calls that
+// overlap on one GPU (other streams, other threads) race. Nothing is allocated, freed or cleared by a library call:
+// the kernels write every entry they read.
+// ---------------------------------------------------------------------------------------------------------------
+
+#define NOALLOC_TILES 65536  // at most 65536 * 1024 positions per call
+#define NOALLOC_DEVICES 64
+
+static __device__ __align__(256) u32 scratch[NOALLOC_TILES + 1];
+
+static u32* scratch_on_current_device(int& rc) {
+    static std::mutex mu;
+    static u32* at[NOALLOC_DEVICES] = {};
+    int dev = -1;
+    rc = (int)hipGetDevice(&dev);
+    if (rc != 0) return nullptr;
+    if (dev < 0 || dev >= NOALLOC_DEVICES) {
+        rc = -1;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> hold(mu);
+    if (!at[dev]) {
+        void* p = nullptr;
+        rc = (int)hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (rc != 0) return nullptr;
+        at[dev] = (u32*)p;
+    }
+    return at[dev];
+}
+
+// ng_batch_rows' outputs (out, *total) for n <= NOALLOC_TILES * 1024 = 67,108,864 positions (larger n: -1, nothing
+// launched), the workspace taken from the library's own device array; -1 for the arguments ng_batch_rows refuses.
+extern "C" int ng_batch_rows_noalloc(const int* cells, const int* entries, i64 n, i64 capacity, int* out, u64* total,
+                                     void* stream) {
+    if (n <= 0 || capacity < 0 || ((uintptr_t)entries & 15)) return -1;
+    if ((n + BR_TILE - 1) / BR_TILE > NOALLOC_TILES) return -1;
+    int rc = 0;
+    u32* work = scratch_on_current_device(rc);
+    if (!work) return rc;
+    return launch_batch_rows(cells, entries, n, capacity, out, work, total, (hipStream_t)stream);
 }
