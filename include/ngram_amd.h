@@ -112,11 +112,16 @@ int ng_scan_count(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, u
 /* the emitting scan: block b of `grid` appends its hits' mix64(context id << 16 | next) to ev[b * region ...] and
  * stores how many in ev_count[b]; region >= ng_emit_region(L, grid) = ceil(L / (grid * 8192)) * 8192; flags[0] bit 2
  * a region overflowed. sparse as ng_scan_count's. dhist (may be NULL): block b's events per top-8-bit digit d at
- * dhist[d * dstride + b] (dstride >= grid), for ng_seg_scatter */
+ * dhist[d * dstride + b] (dstride >= grid), for ng_seg_scatter. pre (may be NULL): a device flag; while set, a
+ * position of bm_in is probed only if the position before it is set as well (the prefix rule, ng_avail_closed) */
 ng_u64 ng_emit_region(ng_i64 L, int grid);
 int ng_scan_emit(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, uint32_t* bm_out, const ng_u64* vt,
                  ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, ng_u64* ev, ng_u64 region, uint32_t* ev_count,
-                 uint32_t* flags, int grid, int sparse, uint32_t* dhist, ng_i64 dstride, void* stream);
+                 uint32_t* flags, int grid, int sparse, uint32_t* dhist, ng_i64 dstride, const uint32_t* pre,
+                 void* stream);
+/* *flag = 1 if avail[i] <= max(avail[i - 1], 0) + 1 wherever avail[i] > 1 (every valid query context's prefix is the
+ * previous position's valid context: the prefix rule may gate the scans), else 0; stream-ordered, no host sync */
+int ng_avail_closed(const int* avail, ng_i64 n, uint32_t* flag, void* stream);
 /* the emitting scan over listed positions: the first *n_dev entries of plist (a device-side count: no host sync),
  * events and digit histograms as ng_scan_emit's, each hit's bit set in bm_out (zeroed by the caller; may be NULL);
  * region >= ceil(n / (grid * 256)) * 256 */
@@ -132,9 +137,10 @@ int ng_scan_sink(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, ui
                  ng_i64 n, const ng_u64* vt, ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, uint32_t* hit,
                  int what, ng_u64* ev, ng_u64 region, uint32_t* ev_count, uint32_t* flags, int grid, int sparse,
                  ng_u64 key_add, void* stream);
-/* the set bits of a bitmap as positions in order (out), *total of them; two-phase temp storage (temp NULL: size) */
+/* the set bits of a bitmap as positions in order (out), *total of them; pre (may be NULL) as ng_scan_emit's: while
+ * the device flag is set, only bits whose previous bit is set too; two-phase temp storage (temp NULL: size) */
 int ng_bits_list(void* temp, size_t* temp_bytes, const uint32_t* bm, ng_i64 nwords, ng_u64* out, ng_u64* total,
-                 void* stream);
+                 const uint32_t* pre, void* stream);
 /* existence only: hit bitmap and bit (context id) of the u32 words hit set (hit zeroed by the caller); ids (may be
  * NULL): ids[p] = the context id at each hit position p; sparse as ng_scan_count's */
 int ng_scan_exist(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, uint32_t* bm_out, const ng_u64* vt,
@@ -165,9 +171,9 @@ int ng_pos_gather(const int* ctx_of, ng_i64 N, ng_i64 lo, ng_i64 hi, const uint1
 /* query index without a sort (replaces gpu_val_stats.py:604-651's sort-based one where ids need not agree across
  * ranks): valid k-contexts of positions pos[0..n) (NULL: 0..n) inserted by compare-and-swap into table (cap + tail
  * slots, EMPTY-filled, linear probing without wrap from umulhi(key, cap)); ctx_of[i] = slot or -1 (compact:
- * ctx_of[j] for pos[j]), rep[slot] = the
- * inserting position; counters[0] += the table's occupied slots afterwards, counters[1] = 1 on reaching the table's end, counters[2] += key
- * collisions found against the representative (k > 4) */
+ * ctx_of[j] for pos[j]), rep[slot] = the inserting position; counters[0] += the table's occupied slots
+ * afterwards, counters[1] != 0: the table is too small (a probe reached its end or walked 256 slots),
+ * counters[2] += key collisions found against the representative (k > 4) */
 int ng_query_index(const uint16_t* x, const int* avail, const int* pos, ng_i64 n, int k, ng_u64* table, ng_u64 cap,
                    ng_u64 slots, uint32_t* rep, int* ctx_of, int compact, ng_u64* counters, void* stream);
 /* move a query index into a smaller EMPTY-filled table (cap + tail = slots): ctx_of[0..n) re-pointed, remap

@@ -144,36 +144,69 @@ __device__ __forceinline__ bool sink_full(u32* flags) {
     else return false;
 }
 
-// Dense levels: a lane per position (a wave per two bitmap words).
+// A level's gate word over positions 32w .. 32w + 31 from the previous level's hit words bm: its hits, and with the
+// prefix rule also hits one position earlier. A k-context occurs only where both its (k-1)-suffix (the position's own
+// bit) and its (k-1)-prefix (the bit of the position before) are query contexts that occurred; the prefix rule holds
+// when every query context's prefix is itself a query context (ng_avail_closed: avail[i] <= avail[i - 1] + 1), which
+// the caller states with *pre != 0 (a device-side flag: no host sync). Word -1 of a range counts as all set.
+__device__ __forceinline__ u32 gate_word(const u32* __restrict__ bm, i64 w, bool pre) {
+    const u32 b = bm[w];
+    if (!pre) return b;
+    const u32 before = w > 0 ? bm[w - 1] >> 31 : 1u;
+    return b & ((b << 1) | before);
+}
+
+__device__ __forceinline__ bool pre_on(const u32* pre) { return pre && *pre != 0u; }
+
+// Dense levels: a wave takes DENSE_PPL * 64 consecutive positions at a time, a lane every 64th of them. A probe is a
+// chain of dependent loads (tokens and gate word, then the home slot), so the lane issues the tokens of all its
+// positions, then all their home-slot loads, before it waits for any: DENSE_PPL times the loads in flight of a lane
+// per position (measured on MI355X at c3: one position per lane leaves the scans bound by load latency).
+#define DENSE_PPL 4
 template <int K, class S>
 __global__ void __launch_bounds__(256) scan_dense_k(const u16* __restrict__ tok, i64 L, int k, const u32* __restrict__ bm_in,
                                                     u32* __restrict__ bm_out, const u64* __restrict__ vt, u64 vcap,
                                                     const u32* __restrict__ vrep, const u16* __restrict__ x, S sink,
-                                                    u32* flags) {
+                                                    u32* flags, const u32* pre_flag) {
     __shared__ SinkShared ss;
     sink_begin<S>(sink, &ss);
     const int lane = lane_id();
+    const bool pre = pre_on(pre_flag);
     const i64 nwords = (L + 31) >> 5;
-    const i64 stride = (i64)gridDim.x * blockDim.x;
-    for (i64 base = blockIdx.x * (i64)blockDim.x + (threadIdx.x & ~(WAVE - 1)); base < L; base += stride) {
+    const i64 span = (i64)WAVE * DENSE_PPL;
+    const i64 stride = (i64)gridDim.x * (blockDim.x / WAVE) * span;
+    for (i64 base = (blockIdx.x * (i64)(blockDim.x / WAVE) + threadIdx.x / WAVE) * span; base < L; base += stride) {
         const bool full = sink_full<S>(flags);
-        const i64 p = base + lane;
-        const i64 w = (base >> 5) + (lane >> 5);
-        u32 word = 0xFFFFFFFFu;
-        if (bm_in) word = w < nwords ? bm_in[w] : 0u;
-        // the tokens are loaded whatever the bitmap says, together with its word: one round trip for both
-        u32 nxt = SENT;
-        u64 ck = EMPTY;
-        if (p < L) ck = ctx_key_at<K>(tok, p, k, nxt);
-        Walk wk;
-        walk_seed(vt, vcap, ((word >> (lane & 31)) & 1u) && nxt != SENT ? ck : EMPTY, nxt, wk);
-        const u64 key = walk_end<K, false>(tok, p, k, vt, vrep, x, flags, wk);
-        const bool hit = key != EMPTY;
-        const u64 b = __ballot(hit);
-        if (lane == 0) bm_out[base >> 5] = (u32)b;
-        if (lane == 32 && w < nwords) bm_out[w] = (u32)(b >> 32);
-        if constexpr (S::KIND == 2) emit_wave(sink, &ss, b, hit, key, p, flags);
-        else if (hit) sink_hit(sink, key, p, full, flags);
+        Walk wk[DENSE_PPL];
+#pragma unroll
+        for (int q = 0; q < DENSE_PPL; ++q) {
+            const i64 p = base + q * WAVE + lane;
+            const i64 w = ((base + q * WAVE) >> 5) + (lane >> 5);
+            u32 word = 0xFFFFFFFFu;
+            if (bm_in) word = w < nwords ? gate_word(bm_in, w, pre) : 0u;
+            // the tokens are loaded whatever the bitmap says, together with its word: one round trip for both
+            u32 nxt = SENT;
+            u64 ck = EMPTY;
+            if (p < L) ck = ctx_key_at<K>(tok, p, k, nxt);
+            wk[q].key = ((word >> (lane & 31)) & 1u) && nxt != SENT ? ck : EMPTY;
+            wk[q].next = nxt;
+        }
+#pragma unroll
+        for (int q = 0; q < DENSE_PPL; ++q) walk_seed(vt, vcap, wk[q].key, wk[q].next, wk[q]);
+#pragma unroll
+        for (int q = 0; q < DENSE_PPL; ++q) {
+            const i64 p0 = base + q * WAVE;
+            if (p0 >= L) break;  // wave-uniform
+            const i64 p = p0 + lane;
+            const u64 key = walk_end<K, false>(tok, p, k, vt, vrep, x, flags, wk[q]);
+            const bool hit = key != EMPTY;
+            const u64 b = __ballot(hit);
+            const i64 w = (p0 >> 5) + 1;
+            if (lane == 0) bm_out[p0 >> 5] = (u32)b;
+            if (lane == 32 && w < nwords) bm_out[w] = (u32)(b >> 32);
+            if constexpr (S::KIND == 2) emit_wave(sink, &ss, b, hit, key, p, flags);
+            else if (hit) sink_hit(sink, key, p, full, flags);
+        }
     }
     sink_end(sink, &ss);
 }
@@ -211,13 +244,14 @@ template <int K, class S>
 __global__ void __launch_bounds__(256) scan_sparse_k(const u16* __restrict__ tok, i64 L, int k, const u32* __restrict__ bm_in,
                                                      u32* __restrict__ bm_out, const u64* __restrict__ vt, u64 vcap,
                                                      const u32* __restrict__ vrep, const u16* __restrict__ x, S sink,
-                                                     u32* flags) {
+                                                     u32* flags, const u32* pre_flag) {
     __shared__ SinkShared ss;
     sink_begin<S>(sink, &ss);
+    const bool pre = pre_on(pre_flag);
     const i64 nwords = (L + 31) >> 5;
     for (i64 w = blockIdx.x * (i64)blockDim.x + threadIdx.x; w < nwords; w += (i64)gridDim.x * blockDim.x) {
         const bool full = sink_full<S>(flags);
-        u32 word = bm_in[w], out = 0;
+        u32 word = gate_word(bm_in, w, pre), out = 0;
         while (word) {
             const int b = __ffs(word) - 1;
             word &= word - 1;
@@ -244,16 +278,18 @@ template <int K, class S>
 __global__ void __launch_bounds__(256) scan_compact_k(const u16* __restrict__ tok, i64 L, int k,
                                                       const u32* __restrict__ bm_in, u32* __restrict__ bm_out,
                                                       const u64* __restrict__ vt, u64 vcap, const u32* __restrict__ vrep,
-                                                      const u16* __restrict__ x, S sink, u32* flags) {
+                                                      const u16* __restrict__ x, S sink, u32* flags,
+                                                      const u32* pre_flag) {
     __shared__ u32 list[4][64 * 32];
     __shared__ u32 words[4][64];
     __shared__ SinkShared ss;
     sink_begin<S>(sink, &ss);
     const int lane = lane_id(), w = threadIdx.x / WAVE;
+    const bool pre = pre_on(pre_flag);
     const i64 nwords = (L + 31) >> 5;
     for (i64 g0 = (i64)blockIdx.x * 256; g0 < nwords; g0 += (i64)gridDim.x * 256) {
         const i64 wi = g0 + w * 64 + lane;
-        const u32 word = wi < nwords ? bm_in[wi] : 0u;
+        const u32 word = wi < nwords ? gate_word(bm_in, wi, pre) : 0u;
         const u32 c = __popc(word);
         u32 incl = c;
 #pragma unroll
@@ -303,15 +339,16 @@ __global__ void __launch_bounds__(256) scan_compact_k(const u16* __restrict__ to
     sink_end(sink, &ss);
 }
 
-__global__ void bits_popc_k(const u32* __restrict__ bm, i64 nwords, u32* __restrict__ off) {
+__global__ void bits_popc_k(const u32* __restrict__ bm, i64 nwords, u32* __restrict__ off, const u32* pre_flag) {
     const i64 w = blockIdx.x * (i64)blockDim.x + threadIdx.x;
-    if (w < nwords) off[w] = (u32)__popc(bm[w]);
+    if (w < nwords) off[w] = (u32)__popc(gate_word(bm, w, pre_on(pre_flag)));
 }
 
-__global__ void bits_list_k(const u32* __restrict__ bm, i64 nwords, const u32* __restrict__ off, u64* __restrict__ out) {
+__global__ void bits_list_k(const u32* __restrict__ bm, i64 nwords, const u32* __restrict__ off, u64* __restrict__ out,
+                            const u32* pre_flag) {
     const i64 w = blockIdx.x * (i64)blockDim.x + threadIdx.x;
     if (w >= nwords) return;
-    u32 word = bm[w];
+    u32 word = gate_word(bm, w, pre_on(pre_flag));
     u64 at = off[w];
     while (word) {
         const int b = __ffs(word) - 1;
@@ -333,13 +370,17 @@ static void fill_u32_n(u32* p, u32 v, i64 n, hipStream_t st) {
 // for 1 and 2).
 template <class S>
 static int launch_scan(const u16* tok, i64 L, int k, const u32* bm_in, u32* bm_out, const u64* vt, u64 vcap,
-                        const u32* vrep, const u16* x, const S& sink, u32* flags, int grid, int sparse, hipStream_t st) {
+                        const u32* vrep, const u16* x, const S& sink, u32* flags, int grid, int sparse, hipStream_t st,
+                        const u32* pre = nullptr) {
     if (sparse == 2 && bm_in) {
-        LEVEL_DISPATCH(k, (scan_compact_k<K, S><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, sink, flags)));
+        LEVEL_DISPATCH(k, (scan_compact_k<K, S><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, sink, flags,
+                                                                     pre)));
     } else if (sparse && bm_in) {
-        LEVEL_DISPATCH(k, (scan_sparse_k<K, S><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, sink, flags)));
+        LEVEL_DISPATCH(k, (scan_sparse_k<K, S><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, sink, flags,
+                                                                    pre)));
     } else {
-        LEVEL_DISPATCH(k, (scan_dense_k<K, S><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, sink, flags)));
+        LEVEL_DISPATCH(k, (scan_dense_k<K, S><<<grid, 256, 0, st>>>(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, sink, flags,
+                                                                   pre)));
     }
     return 0;
 }
@@ -670,7 +711,8 @@ extern "C" int ng_mark_bits(const int* ids, i64 n, u32* bits, void* stream) {
 // The emitting scan: block b of the `grid` blocks appends its hits' mix64(pair key) to ev[b * region ...] and stores
 // their number in ev_count[b]; region must be at least ng_emit_region(L, grid). flags[0] bit 2: a region overflowed
 // (only with a smaller region). sparse as ng_scan_count's. dhist (may be NULL): block b's events per top-8-bit digit
-// d at dhist[d * dstride + b] (dstride >= grid), for ng_seg_scatter.
+// d at dhist[d * dstride + b] (dstride >= grid), for ng_seg_scatter. pre (may be NULL): a device flag; while it is
+// set, a position of bm_in is probed only if the position before it is set too (the prefix rule: ng_avail_closed).
 extern "C" u64 ng_emit_region(i64 L, int grid) {
     if (L <= 0 || grid <= 0) return 0;
     const u64 per = (u64)grid * 8192ull;
@@ -679,7 +721,7 @@ extern "C" u64 ng_emit_region(i64 L, int grid) {
 
 extern "C" int ng_scan_emit(const u16* tok, i64 L, int k, const u32* bm_in, u32* bm_out, const u64* vt, u64 vcap,
                             const u32* vrep, const u16* x, u64* ev, u64 region, u32* ev_count, u32* flags, int grid,
-                            int sparse, u32* dhist, i64 dstride, void* stream) {
+                            int sparse, u32* dhist, i64 dstride, const u32* pre, void* stream) {
     if (grid <= 0 || region == 0 || region > 0xFFFFFFFFull || (dhist && dstride < grid)) return -1;
     if (L <= 0) {
         fill_u32_n(ev_count, 0u, grid, (hipStream_t)stream);
@@ -688,7 +730,7 @@ extern "C" int ng_scan_emit(const u16* tok, i64 L, int k, const u32* bm_in, u32*
         return (int)hipGetLastError();
     }
     if (launch_scan(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, EmitSink{ev, region, ev_count, 0, nullptr, dhist, dstride},
-                    flags, grid, sparse, (hipStream_t)stream) != 0)
+                    flags, grid, sparse, (hipStream_t)stream, pre) != 0)
         return -1;
     return (int)hipGetLastError();
 }
@@ -761,9 +803,10 @@ extern "C" int ng_scan_sink(const u16* tok, i64 L, int k, const u32* bm_in, u32*
 }
 
 // The set bits of a bitmap (nwords u32 words) as positions, in order: out[r] = the position of the r-th set bit,
-// *total = their number. Two-phase temp storage (temp NULL: *temp_bytes set).
+// *total = their number. pre (may be NULL): while the device flag is set, only the bits whose previous bit is set too
+// (ng_scan_emit's prefix rule). Two-phase temp storage (temp NULL: *temp_bytes set).
 extern "C" int ng_bits_list(void* temp, size_t* temp_bytes, const u32* bm, i64 nwords, u64* out, u64* total,
-                            void* stream) {
+                            const u32* pre, void* stream) {
     if (!temp_bytes || nwords < 0) return -1;
     const size_t need = (size_t)(nwords + 64) * 4 + prim::scan_u32_temp_bytes(nwords + 1) + 256;
     if (!temp) {
@@ -775,10 +818,30 @@ extern "C" int ng_bits_list(void* temp, size_t* temp_bytes, const u32* bm, i64 n
     if (nwords == 0) return prim::fill_u64(total, 0ull, 1, st);
     u32* off = (u32*)temp;
     void* stemp = (char*)temp + (size_t)(nwords + 64) * 4;
-    bits_popc_k<<<grid_for(nwords, 256), 256, 0, st>>>(bm, nwords, off);
+    bits_popc_k<<<grid_for(nwords, 256), 256, 0, st>>>(bm, nwords, off, pre);
     int e = prim::exclusive_scan_u32(off, off, nwords, total, stemp, st);
     if (e) return e;
-    bits_list_k<<<grid_for(nwords, 256), 256, 0, st>>>(bm, nwords, off, out);
+    bits_list_k<<<grid_for(nwords, 256), 256, 0, st>>>(bm, nwords, off, out, pre);
+    return (int)hipGetLastError();
+}
+
+namespace {
+__global__ void avail_closed_k(const int* __restrict__ avail, i64 n, u32* flag) {
+    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const i64 a = avail[i], before = i ? (i64)avail[i - 1] : 0;
+    if (a > 1 && a > (before > 0 ? before : 0) + 1) atomicAnd(flag, 0u);
+}
+}  // namespace
+
+// *flag = 1 if every query position's valid context has its prefix among the valid contexts of the position before
+// (avail[i] <= max(avail[i - 1], 0) + 1 wherever avail[i] > 1, avail[-1] read as 0), else 0: the prefix rule of
+// ng_scan_emit and ng_bits_list. Stream-ordered, no host sync.
+extern "C" int ng_avail_closed(const int* avail, i64 n, u32* flag, void* stream) {
+    if (n < 0 || !flag) return -1;
+    hipStream_t st = (hipStream_t)stream;
+    fill_u32_n(flag, 1u, 1, st);
+    if (n > 0) avail_closed_k<<<grid_for(n, 256), 256, 0, st>>>(avail, n, flag);
     return (int)hipGetLastError();
 }
 
@@ -880,6 +943,10 @@ extern "C" int ng_features(const int* counts, int L, i64 n, int nb, float* tot, 
 
 namespace {
 template <int K>
+// The longest walk an insert takes before it gives up on the table (counters[1] bit 1). At the load the tables are
+// sized for (at most 0.5) a walk of even 100 slots is vanishingly rare; a table sized from a wrong estimate of its
+// contexts fills up, and without the bound every insert would walk on to the table's end.
+#define QI_MAXWALK 256
 __global__ void qindex_insert_k(const u16* __restrict__ x, const int* __restrict__ avail, const int* __restrict__ pos,
                                 i64 n, int k, u64* table, u64 cap, u64 slots, u32* rep, int* __restrict__ ctx_of,
                                 int compact, u64* counters, const u64* __restrict__ n_dev = nullptr) {
@@ -891,9 +958,13 @@ __global__ void qindex_insert_k(const u16* __restrict__ x, const int* __restrict
         if (avail[i] >= (K > 0 ? K : k)) {
             const u64 key = qctx_key<K>(x + i + 1, k);
             u64 s = __umul64hi(key, cap);
-            while (true) {
+            for (int walked = 0;; ++walked) {
                 if (s + 1 >= slots) {  // the last slot must stay empty
                     atomicOr((unsigned int*)&counters[1], 1u);
+                    break;
+                }
+                if (walked == QI_MAXWALK) {  // a table far too small for its contexts: stop here, rebuilt bigger
+                    atomicOr((unsigned int*)&counters[1], 2u);
                     break;
                 }
                 const u64 cur = table[s];
@@ -1000,8 +1071,8 @@ extern "C" int ng_query_index_shrink(const u64* old_t, const u32* old_rep, u64 o
 // Insert the valid query contexts of positions pos[0..n) (pos NULL: 0..n) into table (cap + tail slots, EMPTY-filled):
 // ctx_of[i] = slot (-1 where invalid; with pos, only listed positions are written; compact: ctx_of[j] for pos[j],
 // n entries), rep[slot] = the position that inserted it.
-// counters[0] += the table's occupied slots afterwards (its contexts), counters[1] = 1 if the probes ran into the
-// table's end; with k > 4, counters[2] += positions whose tokens differ from their slot's representative (a 64-bit
+// counters[0] += the table's occupied slots afterwards (its contexts), counters[1] bit 0 if a probe ran into the
+// table's end, bit 1 if an insert walked QI_MAXWALK slots (a table too small: build it bigger); with k > 4, counters[2] += positions whose tokens differ from their slot's representative (a 64-bit
 // key collision).
 extern "C" int ng_query_index(const u16* x, const int* avail, const int* pos, i64 n, int k, u64* table, u64 cap,
                               u64 slots, u32* rep, int* ctx_of, int compact, u64* counters,
@@ -1082,7 +1153,7 @@ __global__ void __launch_bounds__(256) act_next_k(const int* __restrict__ act, c
 }  // namespace
 
 // The query index of the positions pos[0..*n_dev) (n_max >= *n_dev sizes the grid), compact ctx_of, without a host
-// sync: the table (cap + tail = slots) is EMPTY-filled here; counters[1] (a probe reached the table's end) and
+// sync: the table (cap + tail = slots) is EMPTY-filled here; counters[1] (a table too small) and
 // counters[2] (hashed keys that collided, k > 4) are added to, as ng_query_index's; the contexts are not counted.
 extern "C" int ng_query_index_dev(const u16* x, const int* avail, const int* pos, const u64* n_dev, i64 n_max, int k,
                                   u64* table, u64 cap, u64 slots, u32* rep, int* ctx_of, u64* counters,

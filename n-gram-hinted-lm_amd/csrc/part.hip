@@ -49,7 +49,7 @@ __global__ void __launch_bounds__(256) seg_gather_k(const u64* __restrict__ src_
                                                     u32* __restrict__ dst_v) {
     for (i64 s = blockIdx.x; s < nseg; s += gridDim.x) {
         const u64 base = bases ? (u64)bases[s] : (u64)s * region;
-        const u32 c = cnt[s];
+        const u32 c = !bases && (u64)cnt[s] > region ? (u32)region : cnt[s];  // a region holds at most `region`
         const u64 o = off[s];
         for (u32 i = threadIdx.x; i < c; i += 256) {
             dst_k[o + i] = src_k[base + i];

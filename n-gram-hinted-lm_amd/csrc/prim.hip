@@ -141,26 +141,31 @@ static int scan_impl(const T* in, T* out, i64 n, T* total, char* temp, hipStream
     return (int)hipGetLastError();
 }
 
-__global__ void cast_total_k(const u32* t32, u64* out) { *out = (u64)*t32; }
+// The sum of n u32 as u64 (*total zeroed by the caller): a wave's partial sums one atomic.
+__global__ void __launch_bounds__(BLOCK) sum_wide_k(const u32* __restrict__ in, i64 n, u64* total) {
+    u64 s = 0;
+    for (i64 i = blockIdx.x * (i64)BLOCK + threadIdx.x; i < n; i += (i64)gridDim.x * BLOCK) s += in[i];
+#pragma unroll
+    for (int d = WAVE / 2; d > 0; d >>= 1) s += __shfl_down(s, d, WAVE);
+    if ((threadIdx.x & (WAVE - 1)) == 0 && s) atomicAdd((unsigned long long*)total, (unsigned long long)s);
+}
 
 size_t scan_u32_temp_bytes(i64 n) { return scan_temp<u32>(n) + 256; }
 
+// The offsets are u32 (they wrap once the sum reaches 2^32); *total is the exact u64 sum, read before the scan (out
+// may alias in), so a caller can refuse sums of 2^32 and more.
 int exclusive_scan_u32(const u32* in, u32* out, i64 n, u64* total, void* temp, hipStream_t st) {
     if (n < 0) return -1;
-    if (n == 0) {
-        if (total) return fill_u64(total, 0ull, 1, st);
-        return 0;
-    }
-    char* t = (char*)temp;
-    u32* t32 = (u32*)t;
-    t += 256;
-    int e = scan_impl<u32, Sum<u32>, false>(in, out, n, total ? t32 : nullptr, t, st);
-    if (e) return e;
     if (total) {
-        cast_total_k<<<1, 1, 0, st>>>(t32, total);
-        return (int)hipGetLastError();
+        const int e = fill_u64(total, 0ull, 1, st);
+        if (e) return e;
     }
-    return 0;
+    if (n == 0) return 0;
+    if (total) {
+        const i64 g = (n + BLOCK - 1) / BLOCK;
+        sum_wide_k<<<(unsigned)(g < 1024 ? g : 1024), BLOCK, 0, st>>>(in, n, total);
+    }
+    return scan_impl<u32, Sum<u32>, false>(in, out, n, nullptr, (char*)temp + 256, st);
 }
 
 size_t scan_u64_temp_bytes(i64 n) { return scan_temp<u64>(n); }

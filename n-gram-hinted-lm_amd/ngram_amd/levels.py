@@ -8,7 +8,11 @@ counted with global atomics in one hash table and ranked by a second sort; here
      occurred (a k-context occurs only where its (k-1)-suffix does);
   2. the level's scan (ng_scan_emit: every position, or only those its shard's previous level hit) appends each hit's
      mix64(context id << 16 | next) to its block's own region, no global atomic, and makes the hit bitmap that gates
-     the next level; a level behind a sparse one lists the previous hits first (ng_bits_list) and probes the list;
+     the next level; a level behind a sparse one lists the previous hits first (ng_bits_list) and probes the list.
+     When the query contexts are closed under prefixes (ng_avail_closed: segment-shaped avail, checked on the device)
+     a position is probed only if the previous level hit both there and one position earlier: a k-context occurs
+     only where its (k-1)-suffix and its (k-1)-prefix both do. The scans are bound by random-line requests, so every
+     position the rule drops is a request saved;
   3. the events are hash-partitioned by a radix pass straight from the regions and counted partition by partition in
      LDS (partcount.count_events), which also answers each query position's (context, target) count;
   4. the distinct pairs, packed one word each, are sorted by context and summarized per present context
@@ -102,6 +106,8 @@ class LevelBuild:
         nwords = self.L // 32
         bms = {k: torch.zeros(nwords, dtype=torch.int32, device=dev) for k in self.levels}
         res = LevelOutputs(torch.zeros((3, len(self.levels), N), dtype=torch.int32, device=dev))
+        self._pre = torch.empty(1, dtype=torch.int32, device=dev)  # the prefix rule's device flag
+        elib("ng_avail_closed", avail, N, self._pre)
         if topk:
             res.top_tok = torch.zeros((len(self.levels), N, topk), dtype=torch.int16, device=dev)
             res.top_cnt = torch.zeros((len(self.levels), N, topk), dtype=torch.int32, device=dev)
@@ -220,7 +226,7 @@ class LevelBuild:
                 n_list = torch.zeros(1, dtype=torch.int64, device=dev)
                 b0, b1 = self._event("bits_list", k, n32)
                 b0.record()
-                elib.cub("ng_bits_list", bm_in, n32 // 32, self._plist, n_list)
+                elib.cub("ng_bits_list", bm_in, n32 // 32, self._plist, n_list, self._pre)
                 b1.record()
             e0, e1 = self._event("scan_emit", k, n32, mode)
             e0.record()
@@ -230,7 +236,8 @@ class LevelBuild:
                      x, bms[k][st // 32 :], regions[j * G * R :], u64(R), ev_count[j * G :], flags, i32(G), dh, nseg)
             else:
                 elib("ng_scan_emit", self.tok[st:], n32, i32(k), bm_in, bms[k][st // 32 :], vi.table, u64(vi.cap),
-                     vi.rep, x, regions[j * G * R :], u64(R), ev_count[j * G :], flags, i32(G), i32(mode), dh, nseg)
+                     vi.rep, x, regions[j * G * R :], u64(R), ev_count[j * G :], flags, i32(G), i32(mode), dh, nseg,
+                     self._pre)
             e1.record()
         return regions, R, ev_count, dhist, nseg, flags  # count_events checks the flags with its first read
 
@@ -257,7 +264,7 @@ class LevelBuild:
             n_list = torch.zeros(1, dtype=torch.int64, device=dev)
             b0, b1 = self._event("bits_list", k, n)
             b0.record()
-            elib.cub("ng_bits_list", bm_in[lo // 32 :], n // 32, self._plist, n_list)
+            elib.cub("ng_bits_list", bm_in[lo // 32 :], n // 32, self._plist, n_list, self._pre)
             b1.record()
         e0, e1 = self._event("scan_emit", k, n, mode)
         e0.record()
@@ -267,6 +274,6 @@ class LevelBuild:
         else:
             elib("ng_scan_emit", self.tok[lo:], n, i32(k), None if bm_in is None else bm_in[lo // 32 :],
                  bm_out[lo // 32 :], vi.table, u64(vi.cap), vi.rep, x, regions, u64(R), ev_count, flags, i32(G),
-                 i32(mode), dhist, G)
+                 i32(mode), dhist, G, self._pre)
         e1.record()
         return regions, R, ev_count, dhist, G, flags

@@ -44,7 +44,9 @@ def _popcount(lib: Lib, bm: torch.Tensor) -> int:
 
 
 _RATIO: dict[int, float] = {}  # distinct pairs per counted event at each level, from the last count (sizes partitions)
-_CONTEXTS: dict[int, int] = {}  # each existence level's query contexts in the last call (sizes its query index)
+# each existence level's query contexts per listed position in the last call: sizes the next call's query index for
+# its own number of positions
+_CONTEXTS: dict[int, float] = {}
 
 
 def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: int = 64, elib: Lib | None = None,
@@ -86,8 +88,10 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
                 levels.append(("list", hl, nh))
                 ladder.append((k2, int(elig[k2]), matched))
             break
-        vi = QueryIndex(elib, x, avail, k, act, compact=True, expect=_CONTEXTS.get(k))
-        _CONTEXTS[k] = vi.n
+        per = _CONTEXTS.get(k)
+        vi = QueryIndex(elib, x, avail, k, act, compact=True,
+                        expect=None if per is None else int(per * act.numel()) + 1)
+        _CONTEXTS[k] = vi.n / max(1, act.numel())
         hit = torch.zeros((vi.ids + 31) // 32, dtype=torch.int32, device=dev)  # a bit per context id
         prev = levels[-1] if levels else None
         if prev is not None and (prev[0] == "list" or prev[2] * LIST_DIV < L):
@@ -226,7 +230,7 @@ def _exist_device(elib: Lib, tok, L: int, x, avail, act, k0: int, cap: int, cand
     if int(flags[0].item()) & 4:
         raise RuntimeError(f"levels {k0}..{cap}: an emit region overflowed")
     if int(c[:, 1].max()):
-        raise RuntimeError(f"levels {k0}..{cap}: a query index probe reached its table's end")
+        raise RuntimeError(f"levels {k0}..{cap}: a query index was too small for its contexts")
     if int(c[:, 2].max()):
         raise RuntimeError(f"levels {k0}..{cap}: query positions collide with another context's key")
     res = []
@@ -283,7 +287,7 @@ def _bits_list(elib: Lib, bm: torch.Tensor, n: int) -> torch.Tensor:
     """The set positions of a bitmap (n of them) as a u64 list."""
     out = torch.empty(max(n, 1), dtype=torch.int64, device=bm.device)
     total = torch.zeros(1, dtype=torch.int64, device=bm.device)
-    elib.cub("ng_bits_list", bm, bm.numel(), out, total)
+    elib.cub("ng_bits_list", bm, bm.numel(), out, total, None)
     return out[:n]
 
 

@@ -29,7 +29,8 @@ class QueryIndex:
         dev = x.device
         N = x.numel()
         m = N if positions is None else int(positions.numel())
-        cap = int(m / LOAD) + 1024
+        full = int(m / LOAD) + 1024  # room for every position's context at LOAD
+        cap = full
         if expect is not None:
             cap = min(cap, int(max(expect, 1) * max(EXPECT_MARGIN, 1.0) / LOAD) + 1024)
         while True:
@@ -48,7 +49,9 @@ class QueryIndex:
             c = counters.cpu().tolist()
             if c[1] == 0:
                 break
-            cap *= 2  # a probe run reached the table's end (never at load <= 1/2 in practice): twice the slots
+            # an insert walked too far or reached the table's end: a table sized from a wrong estimate moves to the
+            # size its positions need; one already that size (never at load <= 1/2 in practice) doubles
+            cap = full if cap < full else cap * 2
         if c[2]:
             raise RuntimeError(f"k={k}: {c[2]} query positions collide with another context's key")
         n_ctx = int(c[0])

@@ -371,12 +371,20 @@ int oracle_longest_match(const u16* tok, const i64* bounds, int nshards, const u
     std::vector<std::pair<i64, i64>> pieces;
     for (int s = 0; s < nshards; ++s)
         for (i64 p = bounds[s]; p < bounds[s + 1]; p += 1 << 20) pieces.push_back({p, std::min(bounds[s + 1], p + (1 << 20))});
+    const bool trace = getenv("ORACLE_TRACE") != nullptr;
     auto for_pieces = [&](auto body) {
         std::atomic<size_t> nxt(0);
         std::vector<std::thread> ts;
+        auto last = std::chrono::steady_clock::now();
         for (int t = 0; t < threads; ++t)
             ts.emplace_back([&, t] {
-                for (size_t q; (q = nxt++) < pieces.size();) body(pieces[q].first, pieces[q].second, t);
+                for (size_t q; (q = nxt++) < pieces.size();) {
+                    body(pieces[q].first, pieces[q].second, t);
+                    if (trace && t == 0 && std::chrono::steady_clock::now() - last > std::chrono::seconds(20)) {
+                        fprintf(stderr, "  piece %zu of %zu\n", q, pieces.size());
+                        last = std::chrono::steady_clock::now();
+                    }
+                }
             });
         for (auto& th : ts) th.join();
     };

@@ -129,6 +129,45 @@ def test_context_hints_from_an_earlier_build(corpus, monkeypatch, margin):
             assert np.array_equal(out[2, li].view(np.uint32), o["cnt"]), (len(q), k)
 
 
+@pytest.mark.parametrize("avail,closed", [([0, 1, 2, 3, 0, 1, 2], 1), ([1, 1, 1], 1), ([], 1), ([0, 1, 3], 0),
+                                           ([2, 3], 0), ([0, 0, 5], 0), ([4, 5, 6, 1, 2], 0), ([1, 2, -3, 1], 1)])
+def test_avail_closed_flag_by_hand(avail, closed):
+    """ng_avail_closed: 1 iff avail[i] <= max(avail[i - 1], 0) + 1 wherever avail[i] > 1 (avail[-1] read as 0)."""
+    from ngram_amd.lib import Lib
+
+    a = torch.tensor(avail, dtype=torch.int32, device="cuda")
+    flag = torch.full((1,), 7, dtype=torch.int32, device="cuda")
+    Lib()("ng_avail_closed", a, a.numel(), flag)
+    assert int(flag.item()) == closed
+
+
+def test_counts_with_holes_in_avail(corpus):
+    """Query positions left unanswered (avail 0) break the prefix closure of the query contexts: the flag reads 0,
+    the scans gate by the previous level's hit alone, and the build still matches the oracle run on the same avail;
+    the same build with segment-shaped avail (the prefix rule on) matches it too."""
+    from ngram_amd.lib import Lib
+
+    x, tgt, avail = C.queries(corpus.query, [], "cuda")
+    holes = avail.clone()
+    holes[1000::997] = 0
+    cb = C.CountBuild(corpus.shards(), levels=LEVELS, level_shards={}, topk=4)
+    cb.start_load(1)
+    xs, ts = corpus.query[:-1], corpus.query[1:]
+    for av, closed in ((holes, 0), (avail, 1)):
+        flag = torch.empty(1, dtype=torch.int32, device="cuda")
+        Lib()("ng_avail_closed", av, av.numel(), flag)
+        assert int(flag.item()) == closed
+        out = cb.counts(x, tgt, av).cpu().numpy()
+        a = av.cpu().numpy()
+        for li, k in enumerate(LEVELS):
+            o = O.query_counts(corpus.train, corpus.bounds, xs, ts, a, k, cnt_top=1 << 30, ntop=4)
+            assert np.array_equal(out[0, li].view(np.uint32), o["tot"]), (closed, k)
+            assert np.array_equal(out[1, li].astype(np.uint16), o["dist"]), (closed, k)
+            assert np.array_equal(out[2, li].view(np.uint32), o["cnt"]), (closed, k)
+            if closed == 0 and k == 3:
+                assert (o["tot"][1001::997] > 0).any(), "a position after a hole has an occurring context"
+
+
 def test_counts_from_device_tokens(corpus):
     """CountBuild.from_device (the shards already laid out in GPU memory, as the benchmark builds): every level's scan
     is one launch over all the shards, the first level included; tot / dist / cnt and the top-4 match the oracle, in
@@ -165,3 +204,21 @@ def test_emit_region_overflow_raises(corpus, monkeypatch, packed):
     monkeypatch.setattr(levels_mod, "emit_region", lambda L, G: 64)
     with pytest.raises(RuntimeError, match="emit region overflowed"):
         cb.counts(x, tgt, avail)
+
+
+def test_event_total_of_2_32_or_more_raises():
+    """count_events refuses a scan whose digit histograms sum to 2^32 events or more (the region scatter's offsets
+    are u32): the scan's total is summed in 64 bits, so 2^32 + 5 does not wrap to 5 and the check fires before any
+    region is read."""
+    from ngram_amd.lib import Lib
+
+    lib = Lib()
+    nseg = 4
+    regions = torch.zeros(nseg * 8, dtype=torch.int64, device="cuda")
+    ev_count = torch.zeros(nseg, dtype=torch.int32, device="cuda")
+    dhist = torch.zeros(256 * nseg, dtype=torch.int32, device="cuda")
+    dhist[[3, 300, 600, 1000]] = 1 << 30
+    dhist[7] = 5
+    flags = torch.zeros(2, dtype=torch.int32, device="cuda")
+    with pytest.raises(RuntimeError, match="4294967301 events"):
+        P.count_events(lib, lib, None, 0, 1000, 1.0, None, seg=(regions, 8, ev_count, dhist, nseg, flags))

@@ -72,3 +72,23 @@ def test_ladder_interface(corpus, tmp_path):
     assert np.array_equal(lm.length, want[0]) and np.array_equal(lm.next, want[1]) and np.array_equal(lm.count, want[2])
     with pytest.raises(ValueError):
         LongestMatch.create(paths, np.array([3], np.uint16))
+
+
+def test_context_hint_from_a_much_smaller_call():
+    """The longest match sizes each level's query index from the last call's contexts per position: after a call of
+    a few contexts repeated, a call over varied text gets tables sized far too small from that hint; an insert gives
+    up after a bounded walk and the index is rebuilt at its positions' size, and the result is a first call's."""
+    from ngram_amd import longest as LM
+    from ngram_amd.lib import Lib
+
+    c = data.make_corpus("c3", train_tokens=600_000, query_tokens=200_001, shard_tokens=300_000)
+    tok, _, _, _ = data.device_tokens(c.shards())
+    x = torch.from_numpy(c.query[:-1].view(np.int16)).cuda()
+    LM._CONTEXTS.clear()
+    want = LM.longest_match(tok, x, LM._segments(x, Lib()), 32)
+    small = x[:100].repeat(50)  # 5000 positions, about 100 contexts per level: a hint 30 times too small
+    LM.longest_match(tok, small, LM._segments(small, Lib()), 32)
+    assert LM._CONTEXTS[2] < 0.05
+    got = LM.longest_match(tok, x, LM._segments(x, Lib()), 32)
+    for g, w in zip(got[:3], want[:3]):
+        assert torch.equal(g, w)

@@ -275,3 +275,36 @@ def test_batch_rows_by_hand():
     assert rows.tolist() == [5, 0, 7, 0, 101, 0, 102, 2, 103, 0, 0, 1, 0]
     with pytest.raises(AssertionError):
         O.batch_rows(cells, entries, 0, 3, 2)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_prefix_rule_drops_no_hit_when_avail_is_closed(seed):
+    """The level scans' prefix rule (probe a position only where the previous level hit there and one position
+    earlier) on the oracle's own hit sets: with segment-shaped avail every level-k hit has level-(k-1) hits at both."""
+    shards, train, bounds, x, tgt = _case(np.random.default_rng(seed), 4, 3, 400, 300)
+    avail = O.segments(x)
+    prev = None
+    for k in range(1, 7):
+        h = O.query_counts(train, bounds, x, tgt, avail, k, hits=True)["hits"].astype(bool)
+        if prev is not None:
+            both = prev.copy()
+            both[1:] &= prev[:-1]
+            both[0] = False
+            assert not (h & ~both).any(), k
+            assert h.any() or k > 3, k
+        prev = h
+
+
+def test_prefix_rule_needs_closed_avail():
+    """With a hole in avail (query position 1 not answered) the query context (5, 6, 7) of position 2 is indexed
+    while its prefix (5, 6) is not: its corpus hit has no level-2 hit one position earlier, so the rule must stay off
+    (ng_avail_closed reads such an avail as not closed)."""
+    train = np.array([5, 6, 7, 8], np.uint16)
+    bounds = np.array([0, 4], np.int64)
+    x = np.array([5, 6, 7], np.uint16)
+    tgt = np.array([6, 7, 8], np.uint16)
+    avail = np.array([1, 0, 3], np.int32)
+    h2 = O.query_counts(train, bounds, x, tgt, avail, 2, hits=True)["hits"].astype(bool)
+    h3 = O.query_counts(train, bounds, x, tgt, avail, 3, hits=True)["hits"].astype(bool)
+    (p,) = np.flatnonzero(h3)
+    assert h2[p] and not h2[p - 1]

@@ -137,6 +137,48 @@ def _bounds(train: np.ndarray) -> list[int]:
     return data.train_bounds(len(train), data.CONFIGS["c3"].shard_tokens).tolist()
 
 
+def test_c5_sampled_over_the_whole_corpus(gpu):
+    from ngram_amd.lib import Lib
+    from ngram_amd.longest import _segments, longest_match
+
+    print("c5: corpus", flush=True)
+    dc = data.device_corpus("c3", query_tokens=1001)
+    zipf = dc.zipf
+    n = 64_000_000 + 1
+    qp = data.make_plan(data.stream_key("c5", "query", n), n, copy_rate=0.15, copy_len=(16, 2048), source=dc.train_plan)
+    print("c5: corpus generated", flush=True)
+    q = data.realize_gpu(qp, zipf, Lib(), source=dc.flat)
+    x = q[:-1]
+    avail = _segments(x, Lib())
+    torch.cuda.synchronize()
+    print("c5: held-out stream generated", flush=True)
+    query = torch.zeros(x.numel(), dtype=torch.bool, device=x.device)
+    query[3::4] = True
+    length, nxt, cnt, _ = longest_match(dc.tok, x, avail, 64, query=query)
+    length, nxt, cnt = (t.cpu().numpy() for t in (length, nxt, cnt))
+    print("c5: GPU longest match done", flush=True)
+    N = x.numel()
+    rng = np.random.default_rng(55)
+    av = avail.cpu().numpy()
+    keep = np.zeros(N, bool)
+    keep[3::4] = True
+    long_ones = np.flatnonzero(keep & (length >= 40))
+    starts = np.concatenate([rng.integers(0, N, 6000), rng.choice(long_ones, min(300, len(long_ones)), False) - 32])
+    idx, s_av, cmp = _windows(starts, 63, 64, N, av, keep)
+    assert cmp.sum() >= 100_000
+    xs = x.cpu().numpy().view(np.uint16)[idx]
+    train = dc.flat.cpu().numpy().view(np.uint16)
+    del dc, q, x
+    torch.cuda.empty_cache()
+    print(f"c5: oracle over {len(train)} corpus tokens, {len(xs)} query positions", flush=True)
+    want = O.longest_match(train, np.array(_bounds(train), np.int64), xs, s_av, 64)
+    g = idx[cmp]
+    assert np.array_equal(length[g].view(np.uint32), want[0][cmp])
+    assert np.array_equal(nxt[g].view(np.uint16), want[1][cmp])
+    assert np.array_equal(cnt[g].view(np.uint32), want[2][cmp])
+    assert want[0][cmp].max() == 64
+
+
 def test_c4_whole_stream(gpu):
     from ngram_amd.lib import Lib
     from ngram_amd.online import OnlineRows
@@ -154,39 +196,3 @@ def test_c4_whole_stream(gpu):
     for g, w, name in zip(got, want, ("cell", "next", "weights", "tot", "dist", "cnt")):
         assert np.array_equal(g, w), name
     assert hinted == want[-1] and n == 92 * (1 << 19)
-
-
-def test_c5_sampled_over_the_whole_corpus(gpu):
-    from ngram_amd.lib import Lib
-    from ngram_amd.longest import _segments, longest_match
-
-    dc = data.device_corpus("c3", query_tokens=1001)
-    zipf = dc.zipf
-    n = 64_000_000 + 1
-    qp = data.make_plan(data.stream_key("c5", "query", n), n, copy_rate=0.15, copy_len=(16, 2048), source=dc.train_plan)
-    q = data.realize_gpu(qp, zipf, Lib(), source=dc.flat)
-    x = q[:-1]
-    avail = _segments(x, Lib())
-    query = torch.zeros(x.numel(), dtype=torch.bool, device=x.device)
-    query[3::4] = True
-    length, nxt, cnt, _ = longest_match(dc.tok, x, avail, 64, query=query)
-    length, nxt, cnt = (t.cpu().numpy() for t in (length, nxt, cnt))
-    N = x.numel()
-    rng = np.random.default_rng(55)
-    av = avail.cpu().numpy()
-    keep = np.zeros(N, bool)
-    keep[3::4] = True
-    long_ones = np.flatnonzero(keep & (length >= 40))
-    starts = np.concatenate([rng.integers(0, N, 6000), rng.choice(long_ones, min(300, len(long_ones)), False) - 32])
-    idx, s_av, cmp = _windows(starts, 63, 64, N, av, keep)
-    assert cmp.sum() >= 100_000
-    xs = x.cpu().numpy().view(np.uint16)[idx]
-    train = dc.flat.cpu().numpy().view(np.uint16)
-    del dc, q, x
-    torch.cuda.empty_cache()
-    want = O.longest_match(train, np.array(_bounds(train), np.int64), xs, s_av, 64)
-    g = idx[cmp]
-    assert np.array_equal(length[g].view(np.uint32), want[0][cmp])
-    assert np.array_equal(nxt[g].view(np.uint16), want[1][cmp])
-    assert np.array_equal(cnt[g].view(np.uint32), want[2][cmp])
-    assert want[0][cmp].max() == 64
