@@ -422,6 +422,30 @@ def parity_windows(cfg, flat, q, out, top_tok, top_cnt, windows: int) -> dict:
             "oracle_seconds": time.perf_counter() - t0}
 
 
+def gather_rate(slots: int, loads: int = 1 << 28) -> dict:
+    """The rate of random 8-byte loads from a table of `slots` u64 (ng_gather_probe: the level scans' probe pattern
+    alone), best of three timed launches after a warm one: the probe roofline's peak."""
+    import torch
+
+    from ngram_amd.lib import Lib, i32, u64
+
+    lib = Lib()
+    grid = torch.cuda.get_device_properties(0).multi_processor_count * 32
+    table = torch.zeros(max(slots, 1), dtype=torch.int64, device="cuda")
+    out = torch.empty(grid * 256, dtype=torch.int64, device="cuda")
+    best = float("inf")
+    for rep in range(4):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        lib("ng_gather_probe", table, u64(table.numel()), u64(loads), u64(rep + 1), i32(grid), out)
+        e1.record()
+        e1.synchronize()
+        if rep:
+            best = min(best, e0.elapsed_time(e1))
+    del table, out
+    return {"table_bytes": 8 * max(slots, 1), "loads": loads, "ms": best, "rate": loads / (best / 1e3) / 1e9}
+
+
 def main() -> None:
     args = parse()
     if args.gpus != 1:
@@ -482,10 +506,10 @@ def main() -> None:
     dt = time.perf_counter() - t0
     ms = dt / args.steps * 1e3
     hits = {k: info[k]["hits"] for k in cfg.levels}
-    # positions each level's scan reads: its whole range (dense), or the previous level's hits (gated: listed)
-    read = {}
-    for li, k in enumerate(cfg.levels):
-        read[k] = T if modes.get(k, 0) == 0 else hits[cfg.levels[li - 1]]
+    # positions each level's scan probes (the gate's set positions: the previous level's hits, under the prefix rule
+    # where it applies), and those whose tokens it reads: every position (dense) or the probed ones (listed)
+    probed = {k: info[k]["probed"] for k in cfg.levels}
+    read = {k: T if modes.get(k, 0) == 0 else probed[k] for k in cfg.levels}
     scan_bytes = {k: 2.0 * read[k] + 8.0 * hits[k] for k in cfg.levels}
     scan_ms = {k: per_kernel.get(("scan_emit", k), 0.0) / args.steps for k in cfg.levels}
     dom = max(cfg.levels, key=lambda k: scan_ms[k])
@@ -496,6 +520,7 @@ def main() -> None:
         return {"achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS}
 
     traffic, traffic_commit = measured_traffic(dom)
+    gather = gather_rate(int(info[dom]["ids"]))
     path_ms = sum(v for (name, _), v in per_kernel.items() if name in PATH_KERNELS) / args.steps
     path_bytes = sum(2.0 * read[k] + 16.0 * hits[k] for k in cfg.levels)
     E = sum(hits.values())
@@ -520,6 +545,12 @@ def main() -> None:
                      "algorithmic_bytes_per_launch": scan_bytes[dom], "avg_launch_ms": scan_ms[dom],
                      "positions_read": read[dom], "hits_emitted": hits[dom],
                      "bytes_per_position_read": 2, "bytes_per_hit": 8},
+        # the scans' own bound: random 8-byte loads into a table beyond L2 (one per probe), against the rate the
+        # chip sustains for such loads from a table of the dominant level's size (ng_gather_probe, measured here)
+        "probe_roofline": {"bound": "random 8-byte loads", "kernel": f"scan_emit k={dom}",
+                           "achieved": probed[dom] / (scan_ms[dom] / 1e3) / 1e9, "peak": gather["rate"],
+                           "unit": "G loads/s", "frac": probed[dom] / (scan_ms[dom] / 1e3) / 1e9 / gather["rate"],
+                           "probes_per_launch": probed[dom], "calibration": gather},
         "roofline_family": {"kernels": "scan_emit, every level", **roof(sum(scan_bytes.values()),
                                                                         sum(scan_ms.values())),
                             "ms_per_step": sum(scan_ms.values())},
@@ -531,7 +562,8 @@ def main() -> None:
         "events_per_step": E,
         "host_s_per_step": {k: v / (args.steps + args.warmup) for k, v in cb.engine.host_s.items()},
         "levels": {str(k): {**info[k], "scan_mode": modes.get(k, 0), "positions_read": read[k],
-                            "scan_ms": scan_ms[k]} for k in cfg.levels},
+                            "scan_ms": scan_ms[k], "probes_per_s": probed[k] / max(scan_ms[k], 1e-9) * 1e3}
+                   for k in cfg.levels},
         "parity": None,
         "cpu_baseline": None,
     }

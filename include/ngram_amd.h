@@ -122,6 +122,12 @@ int ng_scan_emit(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, ui
 /* *flag = 1 if avail[i] <= max(avail[i - 1], 0) + 1 wherever avail[i] > 1 (every valid query context's prefix is the
  * previous position's valid context: the prefix rule may gate the scans), else 0; stream-ordered, no host sync */
 int ng_avail_closed(const int* avail, ng_i64 n, uint32_t* flag, void* stream);
+/* *total = the positions a level scan probes behind hit words bm: their set bits, under the prefix rule while the
+ * device flag pre is set (a roofline's probe count) */
+int ng_gate_popcount(const uint32_t* bm, ng_i64 nwords, const uint32_t* pre, ng_u64* total, void* stream);
+/* n random 8-byte loads from table (cap u64) at umulhi(mix64(seed + i), cap), grid blocks of 256, per-thread sums to
+ * out (grid * 256 u64): the random-load rate a level scan's probes are measured against */
+int ng_gather_probe(const ng_u64* table, ng_u64 cap, ng_u64 n, ng_u64 seed, int grid, ng_u64* out, void* stream);
 /* the emitting scan over listed positions: the first *n_dev entries of plist (a device-side count: no host sync),
  * events and digit histograms as ng_scan_emit's, each hit's bit set in bm_out (zeroed by the caller; may be NULL);
  * region >= ceil(n / (grid * 256)) * 256 */

@@ -826,6 +826,57 @@ extern "C" int ng_bits_list(void* temp, size_t* temp_bytes, const u32* bm, i64 n
 }
 
 namespace {
+__global__ void __launch_bounds__(256) gate_popcount_k(const u32* __restrict__ bm, i64 nwords, const u32* pre_flag,
+                                                       u64* total) {
+    const bool pre = pre_on(pre_flag);
+    u64 c = 0;
+    for (i64 w = blockIdx.x * (i64)blockDim.x + threadIdx.x; w < nwords; w += (i64)gridDim.x * blockDim.x)
+        c += (u64)__popc(gate_word(bm, w, pre));
+#pragma unroll
+    for (int d = WAVE / 2; d > 0; d >>= 1) c += __shfl_down(c, d, WAVE);
+    if (lane_id() == 0 && c) atomicAdd((unsigned long long*)total, (unsigned long long)c);
+}
+
+// Random 8-byte loads from a table of cap u64 (the access pattern of a level scan's probes, with nothing else): n
+// loads at slots umulhi(mix64(seed + i), cap), four in flight per lane, their sum stored so none is optimized away.
+__global__ void __launch_bounds__(256) gather_probe_k(const u64* __restrict__ table, u64 cap, u64 n, u64 seed,
+                                                      u64* out) {
+    u64 acc = 0;
+    const u64 stride = (u64)gridDim.x * blockDim.x * 4;
+    for (u64 i = (blockIdx.x * (u64)blockDim.x + threadIdx.x) * 4; i < n; i += stride) {
+        u64 v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = i + q < n ? table[__umul64hi(mix64(seed + i + q), cap)] : 0ull;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc += v[q];
+    }
+    out[blockIdx.x * (u64)blockDim.x + threadIdx.x] = acc;
+}
+}  // namespace
+
+// *total = the positions a level scan probes behind the hit words bm (nwords words): their set bits, under the
+// prefix rule while the device flag pre is set (ng_scan_emit's gate). For a roofline's probe count.
+extern "C" int ng_gate_popcount(const u32* bm, i64 nwords, const u32* pre, u64* total, void* stream) {
+    if (nwords < 0 || !total) return -1;
+    hipStream_t st = (hipStream_t)stream;
+    int e = prim::fill_u64(total, 0ull, 1, st);
+    if (e) return e;
+    if (nwords) {
+        const int g = grid_for(nwords, 256);
+        gate_popcount_k<<<g < 2048 ? g : 2048, 256, 0, st>>>(bm, nwords, pre, total);
+    }
+    return (int)hipGetLastError();
+}
+
+// The random-load rate the level scans are measured against: n loads from table (cap u64, any contents) by grid
+// blocks of 256, their per-thread sums to out (grid * 256 u64). Time it on the stream it is launched on.
+extern "C" int ng_gather_probe(const u64* table, u64 cap, u64 n, u64 seed, int grid, u64* out, void* stream) {
+    if (cap == 0 || grid <= 0 || !out) return -1;
+    gather_probe_k<<<grid, 256, 0, (hipStream_t)stream>>>(table, cap, n, seed, out);
+    return (int)hipGetLastError();
+}
+
+namespace {
 __global__ void avail_closed_k(const int* __restrict__ avail, i64 n, u32* flag) {
     const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
     if (i >= n) return;

@@ -170,10 +170,22 @@ class LevelBuild:
             del vi, c, sm, thr, seen
         del regions
         if stats:
-            for k in self.levels:
+            for li, k in enumerate(self.levels):
                 h = int(self._popcount(bms[k]))
                 res.info[k]["hits"] = h
-                self.density[k] = h / max(1, sum(self.sizes[: self.level_shards[k]]))
+                m = self.level_shards[k]
+                self.density[k] = h / max(1, sum(self.sizes[:m]))
+                # the positions the level's scan probed: every position of its shards for the first level, else the
+                # previous level's hits that pass the gate (the prefix rule included) within its shards
+                probed = sum(self.sizes[:m])
+                if li and m > self.level_shards[self.levels[li - 1]]:
+                    probed = None  # some of its shards are gated by an earlier level's hits: not counted here
+                elif li and m:
+                    end = (self.starts[m - 1] + self.sizes[m - 1] + 31) // 32
+                    n = torch.zeros(1, dtype=torch.int64, device=dev)
+                    elib("ng_gate_popcount", bms[self.levels[li - 1]], end, self._pre, n)
+                    probed = int(n.item())
+                res.info[k]["probed"] = probed
         return res
 
     def _popcount(self, bm: torch.Tensor) -> int:
