@@ -828,13 +828,20 @@ extern "C" int ng_bits_list(void* temp, size_t* temp_bytes, const u32* bm, i64 n
 namespace {
 __global__ void __launch_bounds__(256) gate_popcount_k(const u32* __restrict__ bm, i64 nwords, const u32* pre_flag,
                                                        u64* total) {
+    __shared__ u64 part[256 / WAVE];
     const bool pre = pre_on(pre_flag);
     u64 c = 0;
     for (i64 w = blockIdx.x * (i64)blockDim.x + threadIdx.x; w < nwords; w += (i64)gridDim.x * blockDim.x)
         c += (u64)__popc(gate_word(bm, w, pre));
 #pragma unroll
     for (int d = WAVE / 2; d > 0; d >>= 1) c += __shfl_down(c, d, WAVE);
-    if (lane_id() == 0 && c) atomicAdd((unsigned long long*)total, (unsigned long long)c);
+    if (lane_id() == 0) part[threadIdx.x / WAVE] = c;
+    __syncthreads();
+    if (threadIdx.x == 0) {  // one atomic per block
+        u64 b = 0;
+        for (int w = 0; w < 256 / WAVE; ++w) b += part[w];
+        if (b) atomicAdd((unsigned long long*)total, (unsigned long long)b);
+    }
 }
 
 // Random 8-byte loads from a table of cap u64 (the access pattern of a level scan's probes, with nothing else): n
@@ -863,7 +870,7 @@ extern "C" int ng_gate_popcount(const u32* bm, i64 nwords, const u32* pre, u64* 
     if (e) return e;
     if (nwords) {
         const int g = grid_for(nwords, 256);
-        gate_popcount_k<<<g < 2048 ? g : 2048, 256, 0, st>>>(bm, nwords, pre, total);
+        gate_popcount_k<<<g < 512 ? g : 512, 256, 0, st>>>(bm, nwords, pre, total);
     }
     return (int)hipGetLastError();
 }

@@ -141,13 +141,22 @@ static int scan_impl(const T* in, T* out, i64 n, T* total, char* temp, hipStream
     return (int)hipGetLastError();
 }
 
-// The sum of n u32 as u64 (*total zeroed by the caller): a wave's partial sums one atomic.
+// The sum of n u32 as u64 (*total zeroed by the caller): one atomic per block (atomics on one address serialize, so
+// the grid is kept small: SUM_WIDE_BLOCKS).
+#define SUM_WIDE_BLOCKS 256
 __global__ void __launch_bounds__(BLOCK) sum_wide_k(const u32* __restrict__ in, i64 n, u64* total) {
+    __shared__ u64 part[BLOCK / WAVE];
     u64 s = 0;
     for (i64 i = blockIdx.x * (i64)BLOCK + threadIdx.x; i < n; i += (i64)gridDim.x * BLOCK) s += in[i];
 #pragma unroll
     for (int d = WAVE / 2; d > 0; d >>= 1) s += __shfl_down(s, d, WAVE);
-    if ((threadIdx.x & (WAVE - 1)) == 0 && s) atomicAdd((unsigned long long*)total, (unsigned long long)s);
+    if ((threadIdx.x & (WAVE - 1)) == 0) part[threadIdx.x / WAVE] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        u64 b = 0;
+        for (int w = 0; w < BLOCK / WAVE; ++w) b += part[w];
+        if (b) atomicAdd((unsigned long long*)total, (unsigned long long)b);
+    }
 }
 
 size_t scan_u32_temp_bytes(i64 n) { return scan_temp<u32>(n) + 256; }
@@ -163,7 +172,7 @@ int exclusive_scan_u32(const u32* in, u32* out, i64 n, u64* total, void* temp, h
     if (n == 0) return 0;
     if (total) {
         const i64 g = (n + BLOCK - 1) / BLOCK;
-        sum_wide_k<<<(unsigned)(g < 1024 ? g : 1024), BLOCK, 0, st>>>(in, n, total);
+        sum_wide_k<<<(unsigned)(g < SUM_WIDE_BLOCKS ? g : SUM_WIDE_BLOCKS), BLOCK, 0, st>>>(in, n, total);
     }
     return scan_impl<u32, Sum<u32>, false>(in, out, n, nullptr, (char*)temp + 256, st);
 }
