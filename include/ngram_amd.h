@@ -59,7 +59,8 @@ int sort_pairs(void* temp, size_t* temp_bytes, const ng_u64* kin, ng_u64* kout, 
                ng_i64 n, int begin_bit, int end_bit, void* stream);
 /* inclusive running maximum of int64 (gpu_val_stats.cu:539-543) */
 int inclusive_max(void* temp, size_t* temp_bytes, const ng_i64* in, ng_i64* out, ng_i64 n, void* stream);
-/* runs of equal keys -> unique keys, summed values, *nruns (gpu_val_stats.cu:545-551) */
+/* runs of equal keys -> unique keys, summed values, *nruns (gpu_val_stats.cu:545-551); vin NULL (an extension):
+ * every value counts 1, vout = the runs' lengths */
 int reduce_by_key(void* temp, size_t* temp_bytes, const ng_u64* kin, ng_u64* kout, const uint32_t* vin,
                   uint32_t* vout, ng_i64* nruns, ng_i64 n, void* stream);
 /* per context id: [start, end) of its pairs in sorted keys (gpu_val_stats.cu:561-564) */
@@ -271,15 +272,15 @@ int ng_table_query(const uint16_t* x, const int* avail, const uint16_t* tgt, ng_
 int ng_pos_rows(ng_i64 N, int nlv, const ng_i64* desc, int entries, short* cell, uint16_t* next, uint16_t* weights,
                 signed char* level, void* stream);
 /* online state (online.rs step rule): insert occurrences ending at pos[i] (ctx_tot/ctx_dist may be NULL: then the
- * sorted pass adds them); merge a step's sorted distinct touched pairs (uk[0..*n), agg their occurrences in the step)
- * into their contexts' top-E lists (ctx_top may be NULL) and, given ctx_tot/ctx_dist, their totals and distinct
- * counts; answer queries; build hint rows */
+ * sorted pass adds them), their pair keys | tag into ev (tag: the level's index << tshift, above every pair key);
+ * merge a step's sorted distinct touched pairs of every level at once (uk[0..*n) tagged keys, agg their occurrences
+ * in the step; desc[t * 6]: level t's pair keys, counts, capacity, top lists or 0, totals, distinct counts) into
+ * their contexts' totals, distinct counts and top-E lists; answer queries; build hint rows */
 int ng_online_insert(const uint16_t* tok, const int* pos, ng_i64 m, int k, ng_u64* ck, ng_u64 ccap, ng_u64* pk,
                      uint32_t* pcnt, ng_u64 pcap, uint32_t* ctx_tot, uint32_t* ctx_dist, ng_u64* ev, uint32_t* flags,
-                     void* stream);
-int ng_online_top(const ng_u64* uk, const ng_i64* n, ng_i64 m, const uint32_t* agg, const ng_u64* pk,
-                  const uint32_t* pcnt, ng_u64 pcap, ng_u64* score, ng_u64* ctx_top, int E, uint32_t* ctx_tot,
-                  uint32_t* ctx_dist, void* stream);
+                     ng_u64 tag, void* stream);
+int ng_online_top(const ng_u64* uk, const ng_i64* n, ng_i64 m, const uint32_t* agg, const ng_i64* desc, int ntag,
+                  int tshift, ng_u64* score, int E, void* stream);
 int ng_online_query(const uint16_t* tok, const int* avail, const unsigned char* has_next, const int* pos, ng_i64 m,
                     int k, const ng_u64* ck, ng_u64 ccap, const ng_u64* pk, const uint32_t* pcnt, ng_u64 pcap,
                     const uint32_t* ctx_tot, const uint32_t* ctx_dist, int* qslot, uint32_t* tot, uint16_t* dist,

@@ -75,11 +75,12 @@ __device__ __forceinline__ u64 okey(const u16* e, int k) {
     else return ctx_key_rt(e, k);
 }
 
-// Occurrences ending at pos[i] (context tok[g-k+1..g], next tok[g+1]; the caller lists valid ones only).
+// Occurrences ending at pos[i] (context tok[g-k+1..g], next tok[g+1]; the caller lists valid ones only); ev[i] = the
+// pair key | tag (the level's tag, above every pair key's bits: several levels' events sort as one array).
 template <int K>
 __global__ void online_insert_k(const u16* __restrict__ tok, const int* __restrict__ pos, i64 m, int k, u64* ck,
                                 u64 ccap, u64* pk, u32* pcnt, u64 pcap, u32* ctx_tot, u32* ctx_dist,
-                                u64* __restrict__ ev, u32* flags) {
+                                u64* __restrict__ ev, u32* flags, u64 tag) {
     const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
     if (i >= m) return;
     const i64 g = pos[i];
@@ -99,12 +100,28 @@ __global__ void online_insert_k(const u16* __restrict__ tok, const int* __restri
         atomicAdd(&ctx_tot[slot], 1u);
         if (added) atomicAdd(&ctx_dist[slot], 1u);
     }
-    ev[i] = pair;
+    ev[i] = pair | tag;
 }
 
-// Scores of a step's distinct touched pairs (sorted), i < *n.
-__global__ void online_scores_k(const u64* __restrict__ uk, const i64* __restrict__ n, i64 m, const u64* __restrict__ pk,
-                                const u32* __restrict__ pcnt, u64 pcap, u64* __restrict__ score) {
+// A level's state as the step's merge reads it: desc[t * 6 ...] for tag t = pair table keys, counts, capacity, the
+// contexts' top-E lists (0: not kept), totals, distinct counts.
+struct OLevel {
+    const u64* pk;
+    const u32* pcnt;
+    u64 pcap;
+    u64* top;
+    u32* tot;
+    u32* dist;
+};
+
+__device__ __forceinline__ OLevel olevel(const i64* __restrict__ desc, u64 tag) {
+    const i64* d = desc + tag * 6;
+    return OLevel{(const u64*)d[0], (const u32*)d[1], (u64)d[2], (u64*)d[3], (u32*)d[4], (u32*)d[5]};
+}
+
+// Scores of a step's distinct touched pairs (sorted, tagged keys), i < *n.
+__global__ void online_scores_k(const u64* __restrict__ uk, const i64* __restrict__ n, i64 m,
+                                const i64* __restrict__ desc, int tshift, u64* __restrict__ score) {
     const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
     if (i >= m || i >= *n) return;
     const u64 key = uk[i];
@@ -112,7 +129,8 @@ __global__ void online_scores_k(const u64* __restrict__ uk, const i64* __restric
         score[i] = 0;
         return;
     }
-    const u32 c = opair_count(pk, pcnt, pcap, key);
+    const OLevel lv = olevel(desc, key >> tshift);
+    const u32 c = opair_count(lv.pk, lv.pcnt, lv.pcap, key & ((1ull << tshift) - 1));
     score[i] = ((u64)c << 16) | (0xFFFFu - (u32)(key & 0xFFFF));
 }
 
@@ -128,16 +146,16 @@ __device__ __forceinline__ void top8_insert(u64 (&t)[8], u64 v) {
         }
 }
 
-// A step's touched pairs uk[0..*n) (distinct, sorted; agg[i] = their occurrences in the step, score[i] their ranking
-// scores, count << 16 | 65535 - token), a wave per window of 64: for each context starting in the window, its total
-// and distinct count grow by the step's occurrences and first-seen pairs (plain stores by the context's first lane: no
-// same-address atomics for hot contexts), and (ctx_top not NULL) its top-E list is merged with the new scores (an old
-// entry of a touched token is superseded by its new score: counts only grow). A short context ending in its window is
-// done by its first lane from LDS; a long one, and the one running past the window, by the whole wave.
+// A step's touched pairs uk[0..*n) (distinct, sorted; keys tagged with their level above bit tshift; agg[i] = their
+// occurrences in the step, score[i] their ranking scores, count << 16 | 65535 - token), a wave per window of 64: for
+// each context starting in the window (a context of one level: the tag is part of key >> 16), its total and distinct
+// count grow by the step's occurrences and first-seen pairs (plain stores by the context's first lane: no
+// same-address atomics for hot contexts), and (its level's top lists kept) its top-E list is merged with the new
+// scores (an old entry of a touched token is superseded by its new score: counts only grow). A short context ending in
+// its window is done by its first lane from LDS; a long one, and the one running past the window, by the whole wave.
 __global__ void __launch_bounds__(256) online_top_k(const u64* __restrict__ uk, const u64* __restrict__ score,
                                                     const u32* __restrict__ agg, const i64* __restrict__ n_ptr, i64 m,
-                                                    u64* __restrict__ ctx_top, int E, u32* __restrict__ ctx_tot,
-                                                    u32* __restrict__ ctx_dist) {
+                                                    const i64* __restrict__ desc, int tshift, int E) {
     __shared__ u64 s_key[4][WAVE];
     __shared__ u64 s_sc[4][WAVE];
     __shared__ u32 s_ag[4][WAVE];
@@ -167,6 +185,11 @@ __global__ void __launch_bounds__(256) online_top_k(const u64* __restrict__ uk, 
         int e = -1;  // where this head's context ends, if in the window
         if (head && (tails >> lane)) e = lane + __ffsll((unsigned long long)(tails >> lane)) - 1;
         if (e >= 0 && e - lane + 1 <= ONLINE_SHORT) {  // a short context ending in the window: this lane alone, from LDS
+            const OLevel lv = olevel(desc, key >> tshift);
+            const u64 slot = c & ((1ull << (tshift - 16)) - 1);
+            u64* const ctx_top = lv.top;
+            u32* const ctx_tot = lv.tot;
+            u32* const ctx_dist = lv.dist;
             u32 add = 0, fresh = 0;
             u64 t[8];
 #pragma unroll
@@ -176,12 +199,10 @@ __global__ void __launch_bounds__(256) online_top_k(const u64* __restrict__ uk, 
                 fresh += (u32)(s_sc[wid][q] >> 16) == s_ag[wid][q];
                 if (ctx_top) top8_insert(t, s_sc[wid][q]);
             }
-            if (ctx_tot) {
-                ctx_tot[c] += add;
-                ctx_dist[c] += fresh;
-            }
+            ctx_tot[slot] += add;
+            ctx_dist[slot] += fresh;
             if (ctx_top) {
-                u64* top = ctx_top + c * E;
+                u64* top = ctx_top + slot * E;
                 for (int r = 0; r < E; ++r) {
                     const u64 old = top[r];
                     if (old == 0) break;
@@ -202,6 +223,11 @@ __global__ void __launch_bounds__(256) online_top_k(const u64* __restrict__ uk, 
             waved &= waved - 1;
             const int eh = __shfl(e, h, WAVE);  // -1: the context runs past the window
             const u64 hc = bcast_u64(c, h);
+            const OLevel lv = olevel(desc, hc >> (tshift - 16));
+            const u64 hslot = hc & ((1ull << (tshift - 16)) - 1);
+            u64* const ctx_top = lv.top;
+            u32* const ctx_tot = lv.tot;
+            u32* const ctx_dist = lv.dist;
             const i64 gi = wv * WAVE + h;
             const bool in = valid && lane >= h && (eh < 0 || lane <= eh);
             u64 add = in ? ag : 0, fresh = (in && (u32)(sc >> 16) == ag) ? 1 : 0;
@@ -232,12 +258,12 @@ __global__ void __launch_bounds__(256) online_top_k(const u64* __restrict__ uk, 
                 add += shfl_down_u64(add, d);
                 fresh += shfl_down_u64(fresh, d);
             }
-            if (lane == 0 && ctx_tot) {
-                ctx_tot[hc] += (u32)add;
-                ctx_dist[hc] += (u32)fresh;
+            if (lane == 0) {
+                ctx_tot[hslot] += (u32)add;
+                ctx_dist[hslot] += (u32)fresh;
             }
             if (ctx_top) {
-                u64* top = ctx_top + hc * E;
+                u64* top = ctx_top + hslot * E;
                 if (lane < E) {  // lane r checks old entry r: kept unless its token was touched in the step
                     const u64 old = top[lane];
                     if (old != 0) {
@@ -376,30 +402,31 @@ __global__ void online_rows_k(const int* __restrict__ pos, i64 m, int nlv, const
             break;                                             \
     }
 
-// Insert the occurrences ending at pos[0..m) at level k; ev[i] = their pair keys (EMPTY if a table was full: flags).
+// Insert the occurrences ending at pos[0..m) at level k; ev[i] = their pair keys | tag (EMPTY if a table was full:
+// flags). tag: the level's tag << tshift for ng_online_top (0 for one level), above every pair key of the tables.
 extern "C" int ng_online_insert(const u16* tok, const int* pos, i64 m, int k, u64* ck, u64 ccap, u64* pk, u32* pcnt,
-                                u64 pcap, u32* ctx_tot, u32* ctx_dist, u64* ev, u32* flags, void* stream) {
+                                u64 pcap, u32* ctx_tot, u32* ctx_dist, u64* ev, u32* flags, u64 tag, void* stream) {
     if (m <= 0) return 0;
-    if (ccap == 0 || pcap == 0 || ccap > (1ull << 40)) return -1;
+    if (ccap == 0 || pcap == 0 || ccap > (1ull << 40) || (tag && tag < (ccap << 16))) return -1;
     hipStream_t st = (hipStream_t)stream;
-    OLEVELS(k, (online_insert_k<K><<<grid_for(m, 256), 256, 0, st>>>(tok, pos, m, k, ck, ccap, pk, pcnt, pcap, ctx_tot, ctx_dist, ev, flags)));
+    OLEVELS(k, (online_insert_k<K><<<grid_for(m, 256), 256, 0, st>>>(tok, pos, m, k, ck, ccap, pk, pcnt, pcap, ctx_tot, ctx_dist, ev, flags, tag)));
     return (int)hipGetLastError();
 }
 
-// The step's distinct touched pairs uk[0..*n) (sorted; agg: their occurrences in the step) merged into their
-// contexts' top-E lists (ctx_top may be NULL) and, when ctx_tot is given (the insert was called without it), added
-// to their contexts' totals and distinct counts. score: scratch [m].
-extern "C" int ng_online_top(const u64* uk, const i64* n, i64 m, const u32* agg, const u64* pk, const u32* pcnt,
-                             u64 pcap, u64* score, u64* ctx_top, int E, u32* ctx_tot, u32* ctx_dist, void* stream) {
-    if (E < 1 || E > 8) return -1;
-    if ((ctx_tot == nullptr) != (ctx_dist == nullptr)) return -1;
+// A step's distinct touched pairs of every level at once, uk[0..*n) (sorted tagged keys: level t's pair keys | t <<
+// tshift; agg: their occurrences in the step), merged into their contexts' totals, distinct counts and, where the
+// level keeps them, top-E lists; desc[t * 6 ...] describes level t (OLevel: pair keys, counts, capacity, top lists or
+// 0, totals, distinct counts; device memory), ntag levels. score: scratch [m].
+extern "C" int ng_online_top(const u64* uk, const i64* n, i64 m, const u32* agg, const i64* desc, int ntag, int tshift,
+                             u64* score, int E, void* stream) {
+    if (E < 1 || E > 8 || ntag < 1 || tshift < 17 || tshift > 63 || (tshift + 64 - __builtin_clzll((u64)ntag)) > 64)
+        return -1;
     if (m <= 0) return 0;
     hipStream_t st = (hipStream_t)stream;
-    online_scores_k<<<grid_for(m, 256), 256, 0, st>>>(uk, n, m, pk, pcnt, pcap, score);
+    online_scores_k<<<grid_for(m, 256), 256, 0, st>>>(uk, n, m, desc, tshift, score);
     const i64 wins = (m + WAVE - 1) / WAVE;
     const i64 g = (wins + 3) / 4;
-    online_top_k<<<(unsigned)(g < 65536 ? g : 65536), 256, 0, st>>>(uk, score, agg, n, m, ctx_top, E, ctx_tot,
-                                                                     ctx_dist);
+    online_top_k<<<(unsigned)(g < 65536 ? g : 65536), 256, 0, st>>>(uk, score, agg, n, m, desc, tshift, E);
     return (int)hipGetLastError();
 }
 

@@ -475,6 +475,24 @@ __global__ void rbk_values_k(const u64* __restrict__ k, const u32* __restrict__ 
     }
 }
 
+// Counting mode (no values: each item counts 1): a run's head records where the run starts, then each run's length is
+// the distance to the next run's start. Both passes are coalesced and atomic-free.
+__global__ void rbk_starts_k(const u64* __restrict__ k, i64 n, const u32* __restrict__ excl, u64* __restrict__ kout,
+                             u32* __restrict__ starts) {
+    for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n; i += (i64)gridDim.x * blockDim.x)
+        if (i == 0 || k[i] != k[i - 1]) {
+            kout[excl[i]] = k[i];
+            starts[excl[i]] = (u32)i;
+        }
+}
+
+__global__ void rbk_lengths_k(const u32* __restrict__ starts, const u64* __restrict__ total, i64 n,
+                              u32* __restrict__ vout) {
+    const i64 runs = (i64)*total;
+    for (i64 r = blockIdx.x * (i64)blockDim.x + threadIdx.x; r < runs; r += (i64)gridDim.x * blockDim.x)
+        vout[r] = (r + 1 < runs ? starts[r + 1] : (u32)n) - starts[r];
+}
+
 __global__ void rbk_nruns_k(const u64* total, i64* nruns) { *nruns = (i64)*total; }
 
 __global__ void fill_u64_k(u64* p, u64 v, i64 n) {
@@ -499,7 +517,7 @@ int fill_u32(u32* p, u32 v, i64 n, hipStream_t st) {
 
 size_t reduce_by_key_temp_bytes(i64 n) {
     if (n <= 0) return 512;
-    return align_up((size_t)n * 4) + 256 + scan_u32_temp_bytes(n);
+    return 2 * align_up((size_t)n * 4) + 256 + scan_u32_temp_bytes(n);
 }
 
 int reduce_by_key(const u64* kin, u64* kout, const u32* vin, u32* vout, i64* nruns, i64 n, void* temp,
@@ -510,6 +528,8 @@ int reduce_by_key(const u64* kin, u64* kout, const u32* vin, u32* vout, i64* nru
     char* t = (char*)temp;
     u32* heads = (u32*)t;
     t += align_up((size_t)n * 4);
+    u32* starts = (u32*)t;
+    t += align_up((size_t)n * 4);
     u64* total = (u64*)t;
     t += 256;
     int g = grid_for(n, 256);
@@ -517,6 +537,12 @@ int reduce_by_key(const u64* kin, u64* kout, const u32* vin, u32* vout, i64* nru
     rbk_heads_k<<<g, 256, 0, st>>>(kin, n, heads);
     int e = exclusive_scan_u32(heads, heads, n, total, t, st);
     if (e) return e;
+    if (!vin) {  // counting: the runs' lengths
+        rbk_starts_k<<<g, 256, 0, st>>>(kin, n, heads, kout, starts);
+        rbk_lengths_k<<<g, 256, 0, st>>>(starts, total, n, vout);
+        rbk_nruns_k<<<1, 1, 0, st>>>(total, nruns);
+        return (int)hipGetLastError();
+    }
     rbk_keys_k<<<g, 256, 0, st>>>(kin, n, heads, kout);
     e = fill_u32(vout, 0u, n, st);
     if (e) return e;

@@ -157,12 +157,28 @@ class OnlineRows:
                 "flags": torch.zeros(2, dtype=torch.int32, device=dev),
                 "ctx_bits": max(1, (cap - 1).bit_length()),
             }
-        most = max([1] + [int(np.bincount(lv["alpha"]).max()) if len(lv["alpha"]) else 1
-                          for lv in st["levels"].values()])
+        # a step's events of every level go through one sort, one reduce and one merge, each level's pair keys tagged
+        # with its index above the widest level's pair-key bits (ng_online_insert's tag, ng_online_top's desc)
+        st["tshift"] = 16 + max(lv["ctx_bits"] for lv in st["levels"].values())
+        st["tag_bits"] = max(1, (len(st["levels"]) - 1).bit_length())
+        if st["tshift"] + st["tag_bits"] > 64:
+            raise ValueError("the online tables are too large for one step's tagged pair keys")
+        desc = []
+        for k, lv in st["levels"].items():
+            desc += [lv["pk"].data_ptr(), lv["pcnt"].data_ptr(), lv["pcap"],
+                     lv["top"].data_ptr() if k in levels else 0, lv["tot"].data_ptr(), lv["dist"].data_ptr()]
+        st["top_desc"] = torch.tensor(desc, dtype=torch.int64, device=dev)
+        per_step = np.zeros(1, np.int64)
+        for lv in st["levels"].values():
+            if len(lv["alpha"]):
+                c = np.bincount(lv["alpha"])
+                if len(c) > len(per_step):
+                    per_step = np.pad(per_step, (0, len(c) - len(per_step)))
+                per_step[: len(c)] += c
+        most = max(1, int(per_step.max()))
         st["ev"] = torch.empty(most, dtype=torch.int64, device=dev)
         st["ev_sorted"] = torch.empty(most, dtype=torch.int64, device=dev)
         st["uk"] = torch.empty(most, dtype=torch.int64, device=dev)
-        st["ones"] = torch.ones(most, dtype=torch.int32, device=dev)
         st["agg"] = torch.empty(most, dtype=torch.int32, device=dev)
         st["nruns"] = torch.zeros(1, dtype=torch.int64, device=dev)
         st["score"] = torch.empty(most, dtype=torch.int64, device=dev)
@@ -186,20 +202,21 @@ class OnlineRows:
         lib = self.lib
         levels, buckets, entries, count_levels = outs["cfg"]
         E = st["E"]
-        for k, lv in st["levels"].items():
+        m = 0
+        for t, (k, lv) in enumerate(st["levels"].items()):
             a, b = self._range(lv["alpha"], s, s + 1)
-            m = b - a
-            if m == 0:
+            if b == a:
                 continue
-            ev = st["ev"][:m]
             # the totals and distinct counts are added per context by the sorted pass (ng_online_top), not per
             # occurrence: hot contexts would make chains of same-address atomics
-            lib("ng_online_insert", self.tok, lv["occ"][a:b], m, i32(k), lv["ck"], u64(lv["ccap"]), lv["pk"], lv["pcnt"],
-                u64(lv["pcap"]), None, None, ev, lv["flags"])
-            lib.cub("sort_pairs", ev, st["ev_sorted"], None, None, m, i32(0), i32(min(64, 16 + lv["ctx_bits"])))
-            lib.cub("reduce_by_key", st["ev_sorted"], st["uk"], st["ones"], st["agg"], st["nruns"], m)
-            lib("ng_online_top", st["uk"], st["nruns"], m, st["agg"], lv["pk"], lv["pcnt"], u64(lv["pcap"]), st["score"],
-                lv["top"] if k in levels else None, i32(E), lv["tot"], lv["dist"])
+            lib("ng_online_insert", self.tok, lv["occ"][a:b], b - a, i32(k), lv["ck"], u64(lv["ccap"]), lv["pk"],
+                lv["pcnt"], u64(lv["pcap"]), None, None, st["ev"][m:], lv["flags"], u64(t << st["tshift"]))
+            m += b - a
+        if m:
+            lib.cub("sort_pairs", st["ev"], st["ev_sorted"], None, None, m, i32(0), i32(st["tshift"] + st["tag_bits"]))
+            lib.cub("reduce_by_key", st["ev_sorted"], st["uk"], None, st["agg"], st["nruns"], m)  # run lengths
+            lib("ng_online_top", st["uk"], st["nruns"], m, st["agg"], st["top_desc"], i32(len(st["levels"])),
+                i32(st["tshift"]), st["score"], i32(E))
         qa, qb = self._range(st["q_step"], s, s + 1)
         mq = qb - qa
         if mq == 0 or not queries:

@@ -64,3 +64,19 @@ def test_reduce_by_key(lib, n, runs):
     assert m == len(u)
     assert np.array_equal(kout[:m].cpu().numpy().view(np.uint64), u)
     assert np.array_equal(vout[:m].cpu().numpy().view(np.uint32), sums.astype(np.uint32))
+
+
+@pytest.mark.parametrize("n,runs", [(1, 1), (1000, 7), (100_000, 99_000), (2_000_000, 50), (3_000_000, 2_000_000)])
+def test_reduce_by_key_counting(lib, n, runs):
+    """reduce_by_key without values: each item counts 1, so the outputs are the runs' lengths (np.unique's counts)."""
+    rng = np.random.default_rng(n + 1)
+    keys = np.sort(rng.integers(0, runs, size=n)).astype(np.uint64) * np.uint64(977)
+    kout = torch.empty(n, dtype=torch.int64, device="cuda")
+    vout = torch.empty(n, dtype=torch.int32, device="cuda")
+    nr = torch.zeros(1, dtype=torch.int64, device="cuda")
+    lib.cub("reduce_by_key", _t(keys.view(np.int64)), kout, None, vout, nr, n)
+    u, counts = np.unique(keys, return_counts=True)
+    m = int(nr.item())
+    assert m == len(u)
+    assert np.array_equal(kout[:m].cpu().numpy().view(np.uint64), u)
+    assert np.array_equal(vout[:m].cpu().numpy(), counts.astype(np.int32))
