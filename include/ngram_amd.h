@@ -285,8 +285,10 @@ int ng_online_query(const uint16_t* tok, const int* avail, const unsigned char* 
                     int k, const ng_u64* ck, ng_u64 ccap, const ng_u64* pk, const uint32_t* pcnt, ng_u64 pcap,
                     const uint32_t* ctx_tot, const uint32_t* ctx_dist, int* qslot, uint32_t* tot, uint16_t* dist,
                     uint32_t* cnt, int nc, int ci, void* stream);
-int ng_online_rows(const int* pos, ng_i64 m, int nlv, const ng_i64* desc, int E, short* cell, uint16_t* next,
-                   uint16_t* weights, int* hinted, void* stream);
+/* hint rows of the queries at pos[0..m) in S slots, deepest levels first: cell [n, S], next / weights [n, S, E],
+ * level [n, S] (int8 bucket index; may be NULL); empty slots are left as they are */
+int ng_online_rows(const int* pos, ng_i64 m, int nlv, const ng_i64* desc, int E, int S, short* cell, uint16_t* next,
+                   uint16_t* weights, signed char* level, int* hinted, void* stream);
 /* counts/mix.py features: counts int32 [3, L, n] -> float32 tot, dist, min(cnt, tot) [n, L], int64 bin and sparse
  * indices [n, L] */
 int ng_features(const int* counts, int L, ng_i64 n, int nb, float* tot, float* dist, float* cnt, ng_i64* bin,

@@ -331,9 +331,14 @@ __global__ void online_query_k(const u16* __restrict__ tok, const int* __restric
     }
 }
 
-__device__ __forceinline__ bool online_row(i64 g, i64 i, int nlv, const i64* __restrict__ desc, int E,
-                                           short* __restrict__ cell, u16* __restrict__ next, u16* __restrict__ weights) {
-    for (int v = 0; v < nlv; ++v) {
+// Position g's (query i's) hint rows: the deepest described levels (desc[v * 5 ...], deepest first: qslot (int [m]),
+// ctx_tot (u32), ctx_top (u64 [slots, E]), bucket, unused) whose context occurred, up to S of them, into its slots
+// g * S + j: cell, E next tokens, weights, and (level not NULL) the level's bucket. Returns the slots filled.
+__device__ __forceinline__ int online_row(i64 g, i64 i, int nlv, const i64* __restrict__ desc, int E, int S,
+                                          short* __restrict__ cell, u16* __restrict__ next, u16* __restrict__ weights,
+                                          signed char* __restrict__ level) {
+    int j = 0;
+    for (int v = 0; v < nlv && j < S; ++v) {
         const i64* d = desc + v * 5;
         const int slot = ((const int*)d[0])[i];
         if (slot < 0) continue;
@@ -351,27 +356,28 @@ __device__ __forceinline__ bool online_row(i64 g, i64 i, int nlv, const i64* __r
         for (int e = 0; e < 5; ++e) pb += PE[e] <= share;
         double sum = 0;
         for (int r = 0; r < E; ++r) sum += (double)(u32)(top[r] >> 16);
-        cell[g] = (short)(((1 + b) * 7 + cb) * 6 + pb);
+        const i64 row = g * S + j;
+        cell[row] = (short)(((1 + b) * 7 + cb) * 6 + pb);
+        if (level) level[row] = (signed char)b;
         for (int r = 0; r < E; ++r) {
             const u64 sc = top[r];
-            next[g * E + r] = sc ? (u16)(0xFFFFu - (u32)(sc & 0xFFFF)) : (u16)0;
-            weights[g * E + r] = sc ? (u16)rint((double)(u32)(sc >> 16) / sum * 65535.0) : (u16)0;
+            next[row * E + r] = sc ? (u16)(0xFFFFu - (u32)(sc & 0xFFFF)) : (u16)0;
+            weights[row * E + r] = sc ? (u16)rint((double)(u32)(sc >> 16) / sum * 65535.0) : (u16)0;
         }
-        return true;
+        ++j;
     }
-    return false;
+    return j;
 }
 
 
-// Hint rows of the queries pos[i]: the deepest described level (desc[v * 5 ...], deepest first: qslot (int [m]),
-// ctx_tot (u32), ctx_top (u64 [slots, E]), bucket, unused) whose context occurred: cell, E next tokens, weights.
-__global__ void online_rows_k(const int* __restrict__ pos, i64 m, int nlv, const i64* __restrict__ desc, int E,
+// Hint rows of the queries pos[i] (online_row's, S slots each); *hinted += the queries with at least one row.
+__global__ void online_rows_k(const int* __restrict__ pos, i64 m, int nlv, const i64* __restrict__ desc, int E, int S,
                               short* __restrict__ cell, u16* __restrict__ next, u16* __restrict__ weights,
-                              int* __restrict__ hinted) {
+                              signed char* __restrict__ level, int* __restrict__ hinted) {
     __shared__ int part[4];
     int c = 0;
     for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < m; i += (i64)gridDim.x * blockDim.x)
-        c += online_row(pos[i], i, nlv, desc, E, cell, next, weights);
+        c += online_row(pos[i], i, nlv, desc, E, S, cell, next, weights, level) > 0;
     // one counter atomic per block: same-address atomics serialize
 #pragma unroll
     for (int d = WAVE / 2; d > 0; d >>= 1) c += __shfl_down(c, d, WAVE);
@@ -440,11 +446,13 @@ extern "C" int ng_online_query(const u16* tok, const int* avail, const unsigned 
     return (int)hipGetLastError();
 }
 
-extern "C" int ng_online_rows(const int* pos, i64 m, int nlv, const i64* desc, int E, short* cell, u16* next,
-                              u16* weights, int* hinted, void* stream) {
-    if (E < 1 || E > 8) return -1;
+// Hint rows of the queries at pos[0..m), slots deepest first: cell [n, S], next / weights [n, S, E], level [n, S]
+// (may be NULL) at the query's position; slots with no row are left as they are (callers fill cell 0, level -1).
+extern "C" int ng_online_rows(const int* pos, i64 m, int nlv, const i64* desc, int E, int S, short* cell, u16* next,
+                              u16* weights, signed char* level, int* hinted, void* stream) {
+    if (E < 1 || E > 8 || S < 1 || S > 255) return -1;
     if (m > 0)
         online_rows_k<<<grid_for(m, 256) < 1024 ? grid_for(m, 256) : 1024, 256, 0, (hipStream_t)stream>>>(
-            pos, m, nlv, desc, E, cell, next, weights, hinted);
+            pos, m, nlv, desc, E, S, cell, next, weights, level, hinted);
     return (int)hipGetLastError();
 }

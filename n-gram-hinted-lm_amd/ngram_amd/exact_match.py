@@ -1,8 +1,10 @@
 """exact_match's Python surface (exact_match/exact_match.pyi) on one MI355X: the query-filtered exact counts
 `kgram_counts`, `kgram_query_counts` and `kgram_stats` (exact_match/src/kgram.rs :38-170), the corpus-wide
 `CountTable` (count_table.py), the step-rule `OnlineRows` (online.py), and the module constants (lib.rs :25-32).
-The CPU-only parts of the reference module (train_hints/train_counts with the segment rule, val_overlap, val_scan,
-val_hint_rows, the approximate SlotIndex/StreamIndex) are not provided: looking them up raises AttributeError.
+`train_hints` and `train_counts` (train_hints.rs, train_counts.rs: every training position's rows under the
+segment rule) run on OnlineRows' rule "segment". The other CPU-only parts of the reference module (val_overlap,
+val_scan, val_hint_rows, the approximate SlotIndex/StreamIndex) are not provided: looking them up raises
+AttributeError.
 
 Definitions (kgram.rs:7-9): a query position's k-context is its k tokens ending at it, valid iff they lie in its
 segment (segments start at the first query token, at every BOS and, for kgram_query_counts, at each of `breaks`); an
@@ -216,6 +218,58 @@ def kgram_stats(files, tokens, k: int, depth: int, memory: int, train_tokens=Non
     _check_filter(files, train_tokens, filter)
     r = _level(files, t, k, depth, train_tokens, depth=depth)
     return r["eligible"], r["matched"], r["ranks"], r["hits"]
+
+
+TRAIN_BUCKETS = [2, 3, 4, 5, 6, 10, 20]  # train_hints.rs's default buckets (val_hints.py's LEVELS)
+
+
+def _stream(files) -> tuple[np.ndarray, list[int]]:
+    """The shards (paths, or uint16 arrays) in order as one host stream and its part bounds (empty shards hold no
+    position and no part)."""
+    arrays = []
+    for f in files:
+        if isinstance(f, (str, bytes, os.PathLike)):
+            arrays.append(np.fromfile(f, dtype="<u2", count=shard_tokens(f), offset=HEADER_BYTES))
+        else:
+            arrays.append(np.ascontiguousarray(f, dtype=np.uint16))
+    arrays = [a for a in arrays if len(a)]
+    if not arrays:
+        raise ValueError("the shards hold no tokens")
+    bounds = np.concatenate([[0], np.cumsum([len(a) for a in arrays])]).astype(np.int64).tolist()
+    return np.concatenate(arrays), bounds
+
+
+def train_hints(files, levels, entries: int, buckets=None, slots: int = 1):
+    """Every position of the shards `files` (in order): its hint over the variant `levels` in `slots` slots, the
+    deepest levels whose context occurred before its segment, deepest first (train_hints.rs :41-110: a segment starts
+    at each shard's first token and at every BOS; an occurrence, its k tokens and next token within one shard, counts
+    iff its next token lies before the position's segment start). Returns cell int16, tokens and weights uint16
+    [.., entries] and level int8 (the level's index in `buckets`, -1 for an empty slot): [N] and [N, entries] with one
+    slot, else [N, slots] and [N, slots, entries]. Here at most 8 entries (the GPU's top lists)."""
+    if not files or entries < 1 or not 1 <= slots <= 255:
+        raise ValueError(f"need files, entries >= 1 and 1 <= slots <= 255: {len(files)} files, {entries} entries, "
+                         f"{slots} slots")
+    if entries > 8:
+        raise ValueError(f"at most 8 entries on the GPU: {entries}")
+    buckets = list(TRAIN_BUCKETS if buckets is None else buckets)
+    levels = list(levels)
+    if not buckets or len(buckets) > 127 or buckets[0] == 0 or any(a >= b for a, b in zip(buckets, buckets[1:])):
+        raise ValueError(f"buckets must ascend from 1, at most 127 of them: {buckets}")
+    if not levels or any(k not in buckets for k in levels) or any(a >= b for a, b in zip(levels, levels[1:])):
+        raise ValueError(f"levels must ascend and be of {buckets}: {levels}")
+    tokens, bounds = _stream(files)
+    return OnlineRows(tokens, bounds, np.zeros((0, 3), np.int64)).segment_rows(levels, buckets, entries, slots)
+
+
+def train_counts(files, levels):
+    """Every position of the shards `files` (in order) and level k of `levels` (distinct, >= 1), over the occurrences
+    of its k-context whose next token lies before its segment starts: tot uint32, dist uint16 and cnt uint32 [N, L]
+    (train_counts.rs :20-48; cnt 0 for a shard's last position; all 0 where the k-context leaves the segment)."""
+    levels = [int(k) for k in levels]
+    if not files or not levels or min(levels) < 1 or len(set(levels)) != len(levels):
+        raise ValueError(f"need files and distinct levels >= 1: {len(files)} files, levels {levels}")
+    tokens, bounds = _stream(files)
+    return OnlineRows(tokens, bounds, np.zeros((0, 3), np.int64)).segment_counts(levels)
 
 
 def features(counts: torch.Tensor, nb: int = 25):

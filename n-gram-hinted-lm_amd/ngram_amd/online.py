@@ -11,7 +11,8 @@ a query's k-context must lie in its segment (segments start at each part's start
 totals, distinct counts and exact top-`entries` lists, and a split pair table) persists between calls; a step inserts
 its newly available occurrences, then answers its queries (libngram_amd.so: ng_online_insert, sort_pairs,
 reduce_by_key, ng_online_top, ng_online_query, ng_online_rows). `hints` / `counts` answer a step range from a fresh
-state. rule="segment" (the reference's exactness-test rule) is not provided."""
+state; with rule="segment" (the reference's exactness-test rule) they answer every position from its segment's
+start, one step per segment."""
 
 from __future__ import annotations
 
@@ -23,6 +24,57 @@ from .lib import Lib, i32, u64
 
 NONE = 0xFFFFFFFF
 LOAD = 0.5
+
+
+def loader_plan(ntok, nproc: int, BT: int, accum: int, steps: int) -> np.ndarray:
+    """A training run's plan under llm.c's sequential loader (old_records/r001_llmc_c/llmc/hint_stats.cuh
+    loader_plan :395-409): every rank's micro-batches, [m, 5] int64 rows (step, micro, rank, shard, offset), rank r's
+    b-th micro-batch the inputs [offset, offset + BT) of its shard; a rank moves to the next shard once a shard's
+    (ntok - 1) // (nproc * BT) samples are used. ValueError if the plan runs past the shards."""
+    if nproc < 1 or BT < 1 or accum < 1 or steps < 0:
+        raise ValueError(f"bad plan: nproc {nproc}, BT {BT}, accum {accum}, steps {steps}")
+    plan = []
+    for r in range(nproc):
+        shard = sample = 0
+        for b in range(steps * accum):
+            if sample >= (int(ntok[shard]) - 1) // (nproc * BT):
+                shard, sample = shard + 1, 0
+                if shard >= len(ntok):
+                    raise ValueError(f"the training plan runs past the {len(ntok)} shards")
+            plan.append((b // accum, b % accum, r, shard, sample * nproc * BT + r * BT))
+            sample += 1
+    return np.array(plan, np.int64).reshape(-1, 5)
+
+
+def plan_stream(ntok, plan: np.ndarray, BT: int) -> list[int]:
+    """The training stream's parts for a plan (hint_stats.cuh train_plan :666-676): each shard the plan reads, up to
+    its last trained target (shard 0 whole)."""
+    nshards = int(plan[:, 3].max()) + 1 if len(plan) else 1
+    sizes = [0] * nshards
+    for _, _, _, shard, off in plan:
+        sizes[shard] = max(sizes[shard], int(off) + BT + 1)
+    sizes[0] = max(sizes[0], int(ntok[0]))
+    return sizes
+
+
+def plan_spans(plan: np.ndarray, sizes: list[int], BT: int) -> np.ndarray:
+    """OnlineRows spans [m, 3] (lo, hi, step) of a plan over the stream of `sizes` parts: every micro-batch's inputs
+    [lo, lo + BT) trained in its step, lo + BT its last target (hint_stats.cuh tr_spans_k :411-420)."""
+    starts = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
+    lo = starts[plan[:, 3]] + plan[:, 4]
+    return np.stack([lo, lo + BT, plan[:, 0]], axis=1).astype(np.int64)
+
+
+def plan_rows(plan: np.ndarray, sizes: list[int], BT: int, accum: int, rank: int) -> np.ndarray:
+    """The stream position of each of rank `rank`'s training rows, in training order: row (step * accum + micro) * BT
+    + i is input i of that micro-batch (hint_stats.cuh's row_of :411-420). Gather a stream-sized output with it."""
+    starts = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
+    mine = plan[plan[:, 2] == rank]
+    rows = np.full(int(plan[:, 0].max() + 1) * accum * BT if len(plan) else 0, -1, np.int64)
+    for step, micro, _, shard, off in mine:
+        r0 = (int(step) * accum + int(micro)) * BT
+        rows[r0 : r0 + BT] = starts[shard] + off + np.arange(BT)
+    return rows
 
 
 def _tau(n: int, bounds: list[int], spans: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
@@ -77,6 +129,7 @@ class OnlineRows:
         start = ((self.tok.to(torch.int32) & 0xFFFF) == BOS) | (idx == self.part_lo)
         seg = torch.cummax(torch.where(start, idx, torch.zeros_like(idx)), 0).values
         self.avail = (idx - seg + 1).to(torch.int32)
+        self.seg_index = torch.cumsum(start.to(torch.int64), 0) - 1  # the rule "segment"'s steps
         self.has_next = (idx + 1 < self.part_hi).to(torch.uint8)
         self._done = 0
         self.config = None
@@ -116,15 +169,17 @@ class OnlineRows:
         self.config = cfg
         self.state = self._new_state(cfg)
 
-    def _new_state(self, cfg) -> dict:
+    def _new_state(self, cfg, taus=None) -> dict:
+        """advance()'s state; taus: (tau, tau_in) in place of the spans' (the rule "segment"'s)."""
         levels, buckets, entries, count_levels = cfg
         dev, n = self.dev, self.n
+        tau_all, tau_in_all = taus if taus is not None else (self.tau, self.tau_in)
         E = max(1, entries)
         st = {"levels": {}, "E": E}
         # queries: positions trained as inputs, by step
-        q_valid = self.tau_in != NONE
+        q_valid = tau_in_all != NONE
         q_pos = torch.nonzero(q_valid).squeeze(1)
-        q_step = self.tau_in[q_pos]
+        q_step = tau_in_all[q_pos]
         order = torch.sort(q_step, stable=True).indices
         st["q_pos"] = q_pos[order].to(torch.int32).contiguous()
         st["q_step"] = q_step[order].cpu().numpy()
@@ -137,7 +192,7 @@ class OnlineRows:
                 sh = torch.full((n,), NONE, dtype=torch.int64, device=dev)
                 lo, hi = max(0, -d), min(n, n - d)
                 if hi > lo:
-                    sh[lo:hi] = self.tau[lo + d : hi + d]
+                    sh[lo:hi] = tau_all[lo + d : hi + d]
                 a = torch.maximum(a, sh)
             ok &= a != NONE
             occ = torch.nonzero(ok).squeeze(1)
@@ -235,17 +290,20 @@ class OnlineRows:
                 lv["pk"], lv["pcnt"], u64(lv["pcap"]), lv["tot"], lv["dist"], st["qslot"][k], None, None, None,
                 i32(1), i32(0))
         if levels:
-            lib("ng_online_rows", qpos, mq, i32(len(levels)), st["rows_desc"], i32(E), outs["cell"], outs["next"],
-                outs["weights"], st["hinted"])
+            lib("ng_online_rows", qpos, mq, i32(len(levels)), st["rows_desc"], i32(E), i32(outs["slots"]), outs["cell"],
+                outs["next"], outs["weights"], outs["level"], st["hinted"])
 
-    def _device_outputs(self, cfg) -> dict:
+    def _device_outputs(self, cfg, slots: int = 1, with_level: bool = False) -> dict:
+        """Stream-sized outputs: hint rows in `slots` slots per position (cell [n, slots], next / weights [n, slots,
+        entries], with_level the slots' bucket indices, -1 where empty) and count rows [n, len(count_levels)]."""
         levels, buckets, entries, count_levels = cfg
         n, dev = self.n, self.dev
         E = max(1, entries)
-        return {"cfg": cfg,
-                "cell": torch.zeros(n, dtype=torch.int16, device=dev),
-                "next": torch.zeros((n, E), dtype=torch.int16, device=dev),
-                "weights": torch.zeros((n, E), dtype=torch.int16, device=dev),
+        return {"cfg": cfg, "slots": slots,
+                "cell": torch.zeros((n, slots) if slots > 1 else n, dtype=torch.int16, device=dev),
+                "next": torch.zeros((n, slots, E) if slots > 1 else (n, E), dtype=torch.int16, device=dev),
+                "weights": torch.zeros((n, slots, E) if slots > 1 else (n, E), dtype=torch.int16, device=dev),
+                "level": torch.full((n, slots), -1, dtype=torch.int8, device=dev) if with_level else None,
                 "tot": torch.zeros((n, max(1, len(count_levels))), dtype=torch.int32, device=dev),
                 "dist": torch.zeros((n, max(1, len(count_levels))), dtype=torch.int16, device=dev),
                 "cnt": torch.zeros((n, max(1, len(count_levels))), dtype=torch.int32, device=dev)}
@@ -302,19 +360,45 @@ class OnlineRows:
             self._step(st, s, outs)
         self._done = step_hi
 
-    def _range_rows(self, levels, buckets, entries, count_levels, step_lo, step_hi, rule):
-        if rule != "step":
-            raise ValueError(f"rule must be 'step' (the 'segment' rule is not provided): {rule}")
+    def _range_rows(self, levels, buckets, entries, count_levels, step_lo, step_hi, rule, slots: int = 1,
+                    with_level: bool = False):
+        """A fresh state advanced over steps [0, step_hi), the queries of [step_lo, step_hi) answered. The rule
+        "segment" (online.rs:14-17: every position a query at its segment's start, an occurrence counted iff its next
+        token lies before that start) is the step rule with one step per segment in stream order: tau = tau_in = the
+        position's segment index makes an occurrence's alpha 1 + the segment of its next token, so it counts for a
+        query exactly when that segment lies before the query's; every step then runs as advance()'s do."""
+        taus = None
+        if rule == "segment":
+            taus = (self.seg_index, self.seg_index)
+            step_lo, step_hi = 0, int(self.seg_index[-1].item()) + 1
+        elif rule != "step":
+            raise ValueError(f"rule must be 'step' or 'segment': {rule}")
         if step_lo > step_hi or step_hi >= 1 << 30:
             raise ValueError(f"bad step range [{step_lo}, {step_hi})")
         cfg = self._check_config(levels, buckets, entries, count_levels)
-        st = self._new_state(cfg)
-        outs = self._device_outputs(cfg)
+        st = self._new_state(cfg, taus)
+        outs = self._device_outputs(cfg, slots, with_level)
         for s in range(0, step_hi):  # earlier steps only insert their occurrences
             self._step(st, s, outs, queries=s >= step_lo)
         self._check_flags(st)
         qa, qb = self._range(st["q_step"], step_lo, step_hi)
         return st, outs, st["q_pos"][qa:qb]
+
+    def segment_rows(self, levels, buckets, entries: int, slots: int = 1):
+        """Every position's hint under the rule "segment" in `slots` slots, deepest levels first (train_hints.rs's
+        rows of the stream: cell int16, next and weights uint16 [.., entries], level int8, -1 for an empty slot;
+        [n] / [n, entries] with one slot, else [n, slots] / [n, slots, entries])."""
+        st, outs, _ = self._range_rows(levels, buckets, entries, (), 0, 0, "segment", slots, True)
+        lvl = outs["level"]
+        return (outs["cell"].cpu().numpy(), outs["next"].cpu().numpy().view(np.uint16),
+                outs["weights"].cpu().numpy().view(np.uint16), (lvl[:, 0] if slots == 1 else lvl).cpu().numpy())
+
+    def segment_counts(self, levels):
+        """Every position's count rows under the rule "segment" (train_counts.rs's): tot uint32, dist uint16, cnt
+        uint32 [n, len(levels)]."""
+        st, outs, _ = self._range_rows((), (1,), 0, levels, 0, 0, "segment")
+        return (outs["tot"].cpu().numpy().view(np.uint32), outs["dist"].cpu().numpy().view(np.uint16),
+                outs["cnt"].cpu().numpy().view(np.uint32))
 
     def hints(self, levels, buckets, entries, step_lo, step_hi, cell, next, weights, rule: str = "step") -> int:
         """The hint rows of the queries trained in steps [step_lo, step_hi), written into the stream-sized cell [n],

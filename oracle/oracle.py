@@ -217,9 +217,42 @@ def online(tokens, bounds, tau, tau_in, levels, buckets, entries, count_levels, 
 
 
 def brute_online(tokens, bounds, tau, tau_in, levels, buckets, entries, count_levels, step_lo, step_hi):
-    """online.rs's definitions directly (tiny inputs): per query and level, every valid occurrence of its context with
-    alpha <= the query's step counted from scratch."""
+    """online.rs's definitions directly (tiny inputs), the step rule: per query (a position trained as an input in
+    [step_lo, step_hi)) and level, every valid occurrence of its context with alpha <= the query's step counted from
+    scratch."""
     tok = [int(t) for t in tokens]
+
+    def alpha(h, k, part_lo, part_hi):
+        ts = [int(tau[q]) for q in range(h - k + 1, h + 2)]
+        return None if NONE in ts else 1 + max(ts)
+
+    queries = [g for g in range(len(tok)) if tau_in[g] != NONE and step_lo <= tau_in[g] < step_hi]
+    return _brute_rows(tok, bounds, levels, buckets, entries, count_levels, queries,
+                       lambda h, g, k, seg, lo, hi: (a := alpha(h, k, lo, hi)) is not None and a <= tau_in[g])
+
+
+def brute_segment(tokens, bounds, levels, buckets, entries, count_levels):
+    """online.rs's rule "segment" directly (tiny inputs, online.rs:14-17): every position with a valid context is a
+    query, and an occurrence (its k tokens and next token within one part) counts for it iff its next token lies
+    before the query's segment start."""
+    tok = [int(t) for t in tokens]
+    return _brute_rows(tok, bounds, levels, buckets, entries, count_levels, list(range(len(tok))),
+                       lambda h, g, k, seg, lo, hi: h + 1 < seg[g])
+
+
+def brute_train_hints(tokens, bounds, levels, buckets, entries, slots):
+    """train_hints.rs's rows directly (tiny inputs): every position's deepest `slots` levels with an occurrence counted
+    under the rule "segment", deepest first: cell [n, slots], next / weights [n, slots, entries], level [n, slots]
+    (the level's index in `buckets`, -1 for an empty slot)."""
+    tok = [int(t) for t in tokens]
+    return _brute_rows(tok, bounds, levels, buckets, entries, [], list(range(len(tok))),
+                       lambda h, g, k, seg, lo, hi: h + 1 < seg[g], slots=slots)
+
+
+def _brute_rows(tok, bounds, levels, buckets, entries, count_levels, queries, counts_for, slots=None):
+    """Rows of `queries` from scratch: counts_for(h, g, k, seg, part_lo, part_hi) says whether the occurrence ending at
+    h (valid within its part) counts for the query at g. With `slots`, hint rows in that many slots (deepest levels
+    first) and their levels: (cell, next, weights, level)."""
     n = len(tok)
     part_lo, part_hi, seg = [0] * n, [0] * n, [0] * n
     for a, bnd in zip(bounds[:-1], bounds[1:]):
@@ -228,31 +261,27 @@ def brute_online(tokens, bounds, tau, tau_in, levels, buckets, entries, count_le
             if tok[g] == BOS:
                 s0 = g
             part_lo[g], part_hi[g], seg[g] = a, bnd, s0
-    cell = np.zeros(n, np.int16)
-    nxt = np.zeros((n, entries), np.uint16)
-    w = np.zeros((n, entries), np.uint16)
     nc = len(count_levels)
     tot = np.zeros((n, nc), np.uint32)
     dist = np.zeros((n, nc), np.uint16)
     cnt = np.zeros((n, nc), np.uint32)
 
-    def alpha(g, k):
-        if g - k + 1 < part_lo[g] or g + 1 >= part_hi[g]:
-            return None
-        ts = [int(tau[q]) for q in range(g - k + 1, g + 2)]
-        return None if NONE in ts else 1 + max(ts)
-
     def table(g, k):
         c = tok[g - k + 1 : g + 1]
         found = Counter()
         for h in range(n):
-            a = alpha(h, k)
-            if a is not None and a <= tau_in[g] and tok[h - k + 1 : h + 1] == c:
+            if h - k + 1 < part_lo[h] or h + 1 >= part_hi[h]:
+                continue
+            if counts_for(h, g, k, seg, part_lo, part_hi) and tok[h - k + 1 : h + 1] == c:
                 found[tok[h + 1]] += 1
         return found
 
+    S = slots or 1
+    scell = np.zeros((n, S), np.int16)
+    snxt = np.zeros((n, S, entries), np.uint16)
+    sw = np.zeros((n, S, entries), np.uint16)
+    slevel = np.full((n, S), -1, np.int8)
     hinted = 0
-    queries = [g for g in range(n) if tau_in[g] != NONE and step_lo <= tau_in[g] < step_hi]
     for g in queries:
         for j, k in enumerate(count_levels):
             if g - seg[g] + 1 < k:
@@ -262,7 +291,10 @@ def brute_online(tokens, bounds, tau, tau_in, levels, buckets, entries, count_le
                 tot[g, j] = sum(f.values())
                 dist[g, j] = min(len(f), 65535)
                 cnt[g, j] = f[tok[g + 1]] if g + 1 < part_hi[g] else 0
+        j = 0
         for k in sorted(levels, reverse=True):
+            if j == S:
+                break
             if g - seg[g] + 1 < k:
                 continue
             f = table(g, k)
@@ -273,14 +305,17 @@ def brute_online(tokens, bounds, tau, tau_in, levels, buckets, entries, count_le
             li = list(buckets).index(k)
             cb = sum(e <= total for e in COUNT_EDGES)
             pb = sum(e <= ranked[0][1] / total for e in PURITY_EDGES)
-            cell[g] = ((1 + li) * 7 + cb) * 6 + pb
+            scell[g, j] = ((1 + li) * 7 + cb) * 6 + pb
+            slevel[g, j] = li
             s = float(sum(c for _, c in ranked))
             for r, (t, c) in enumerate(ranked):
-                nxt[g, r] = t
-                w[g, r] = int(np.round(c / s * WEIGHT_ONE))
-            hinted += 1
-            break
-    return cell, nxt, w, tot, dist, cnt, hinted
+                snxt[g, j, r] = t
+                sw[g, j, r] = int(np.round(c / s * WEIGHT_ONE))
+            j += 1
+        hinted += j > 0
+    if slots is not None:
+        return scell, snxt, sw, slevel
+    return scell[:, 0], snxt[:, 0], sw[:, 0], tot, dist, cnt, hinted
 
 
 # ---------------------------------------------------------------------------------------------------------------

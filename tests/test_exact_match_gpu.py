@@ -115,3 +115,39 @@ def test_features():
     want = O.features(counts)
     for g, w, name in zip(got, want, ("tot", "dist", "cnt", "bin", "sparse")):
         assert np.array_equal(g.cpu().numpy(), w), name
+
+
+@pytest.mark.parametrize("slots", [1, 3])
+def test_train_hints_and_counts_match_brute_force(tmp_path, slots):
+    """train_hints / train_counts (the rule "segment" over the shards in order) against the rules' brute force, on
+    three small shard files with BOS tokens."""
+    from ngram_amd import exact_match as X
+
+    rng = np.random.default_rng(90 + slots)
+    shards = []
+    for j, n in enumerate((90, 120, 70)):
+        t = rng.integers(0, 4, size=n).astype(np.uint16)
+        t[rng.random(n) < 0.07] = O.BOS
+        shards.append(t)
+    files = []
+    for j, t in enumerate(shards):
+        f = tmp_path / f"s{j}.bin"
+        data.write_shard(f, t)
+        files.append(str(f))
+    tok = np.concatenate(shards)
+    bounds = [0, 90, 210, 280]
+    levels, buckets = [1, 2, 3], [1, 2, 3, 4]
+    got = X.train_hints(files, levels, 3, buckets, slots)
+    want = O.brute_train_hints(tok, bounds, levels, buckets, 3, slots)
+    if slots == 1:
+        want = (want[0][:, 0], want[1][:, 0], want[2][:, 0], want[3][:, 0])
+    for g, x, name in zip(got, want, ("cell", "tokens", "weights", "level")):
+        assert g.shape == x.shape and np.array_equal(g, x), name
+    assert (got[3] >= 0).sum() > 20
+    tot, dist, cnt = X.train_counts(files, [3, 1])
+    bw = O.brute_segment(tok, bounds, [], [1], 1, [3, 1])
+    assert np.array_equal(tot, bw[3]) and np.array_equal(dist, bw[4]) and np.array_equal(cnt, bw[5])
+    with pytest.raises(ValueError):
+        X.train_hints(files, [2, 7], 3, buckets)
+    with pytest.raises(ValueError):
+        X.train_counts(files, [2, 2])

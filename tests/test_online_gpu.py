@@ -87,6 +87,79 @@ def test_parts_and_interleaved_steps():
         assert np.array_equal(g, w), name
 
 
+@pytest.mark.parametrize("seed", range(4))
+def test_segment_rule_matches_brute_force(seed):
+    """rule="segment" (online.rs:14-17: every position answered from its segment's start) for hints and counts on
+    small random streams of several parts, against the rule's brute force (itself pinned by hand)."""
+    rng = np.random.default_rng(40 + seed)
+    n = int(rng.integers(150, 260))
+    tok = rng.integers(0, 4, size=n).astype(np.uint16)
+    tok[rng.random(n) < 0.06] = O.BOS
+    cuts = sorted(rng.choice(np.arange(20, n - 20), size=int(rng.integers(0, 3)), replace=False).tolist())
+    bounds = [0] + cuts + [n]
+    rows = OnlineRows(tok, bounds, np.zeros((0, 3), np.int64))  # the rule ignores the spans
+    levels, buckets, E, cl = [1, 2, 3], [1, 2, 3, 4], 3, [1, 2, 4]
+    want = O.brute_segment(tok, bounds, levels, buckets, E, cl)
+    cell, nxt, w = np.zeros(n, np.int16), np.zeros((n, E), np.uint16), np.zeros((n, E), np.uint16)
+    hinted = rows.hints(levels, buckets, E, 0, 0, cell, nxt, w, rule="segment")
+    tot, dist, cnt = np.zeros((n, 3), np.uint32), np.zeros((n, 3), np.uint16), np.zeros((n, 3), np.uint32)
+    rows.counts(cl, 0, 0, tot, dist, cnt, rule="segment")
+    for g, x, name in zip((cell, nxt, w, tot, dist, cnt), want, ("cell", "next", "weights", "tot", "dist", "cnt")):
+        assert np.array_equal(g, x), name
+    assert hinted == want[-1] and hinted > 0
+
+
+def test_segment_rule_on_parts_of_a_real_stream():
+    """rule="segment" over three parts of the c1 generator's stream (15K tokens, a few dozen segments) against the
+    oracle's online restatement fed the segment indices as the steps."""
+    shards = [data.make_corpus("c1", train_tokens=20_000, query_tokens=2, shard_tokens=20_000).train[i * 5000:(i + 1) * 5000]
+              for i in range(3)]
+    tok = np.concatenate(shards)
+    n, bounds = len(tok), [0, 5000, 10000, 15000]
+    starts = np.zeros(n, bool)
+    starts[bounds[:-1]] = True
+    starts |= tok == O.BOS
+    seg = (np.cumsum(starts) - 1).astype(np.uint32)
+    want = O.online(tok, bounds, seg, seg, [1, 2, 4], [1, 2, 3, 4], 4, [1, 3], 0, int(seg[-1]) + 1)
+    rows = OnlineRows(tok, bounds, np.zeros((0, 3), np.int64))
+    cell, nxt, w = np.zeros(n, np.int16), np.zeros((n, 4), np.uint16), np.zeros((n, 4), np.uint16)
+    assert rows.hints([1, 2, 4], [1, 2, 3, 4], 4, 0, 0, cell, nxt, w, rule="segment") == want[-1]
+    tot, dist, cnt = np.zeros((n, 2), np.uint32), np.zeros((n, 2), np.uint16), np.zeros((n, 2), np.uint32)
+    rows.counts([1, 3], 0, 0, tot, dist, cnt, rule="segment")
+    for g, x, name in zip((cell, nxt, w, tot, dist, cnt), want, ("cell", "next", "weights", "tot", "dist", "cnt")):
+        assert np.array_equal(g, x), name
+    assert seg[-1] > 10
+
+
+def test_loader_plan_rows():
+    """A training run planned by llm.c's sequential loader (2 ranks, B*T = 256, 2 micro-steps): the stream's parts and
+    spans from the plan, OnlineRows advanced over its steps against the oracle, and each rank's rows gathered in
+    training order."""
+    from ngram_amd.online import loader_plan, plan_rows, plan_spans, plan_stream
+
+    c = data.make_corpus("c1", train_tokens=12_000, query_tokens=2, shard_tokens=12_000).train
+    ntok = [4000, 5000, 3000]
+    shards = [c[:4000], c[4000:9000], c[9000:12000]]
+    plan = loader_plan(ntok, 2, 256, 2, 9)  # 18 micro-batches a rank: 7 in shard 0, 9 in shard 1, 2 in shard 2
+    sizes = plan_stream(ntok, plan, 256)
+    tok = np.concatenate([shards[j][: sizes[j]] for j in range(len(sizes))])
+    bounds = np.concatenate([[0], np.cumsum(sizes)]).tolist()
+    spans = plan_spans(plan, sizes, 256)
+    n = len(tok)
+    tau, tau_in = O.spans_tau(n, bounds, spans)
+    want = O.online(tok, bounds, tau, tau_in, [1, 2, 3], [1, 2, 3], 4, [2, 3], 0, 9)
+    rows = OnlineRows(tok, bounds, spans)
+    got = _empty(n, 4, 2)
+    rows.advance(9, [1, 2, 3], [1, 2, 3], 4, [2, 3], *got)
+    for g, w, name in zip(got, want, ("cell", "next", "weights", "tot", "dist", "cnt")):
+        assert np.array_equal(g, w), name
+    for r in range(2):
+        at = plan_rows(plan, sizes, 256, 2, r)
+        assert len(at) == 9 * 2 * 256 and (at >= 0).all() and len(np.unique(at)) == len(at)
+        assert np.array_equal(got[0][at], want[0][at]) and (got[0][at] != 0).mean() > 0.3
+    assert len(sizes) == 3
+
+
 def test_errors(stream):
     tok, spans = stream
     n = len(tok)

@@ -308,3 +308,73 @@ def test_prefix_rule_needs_closed_avail():
     h3 = O.query_counts(train, bounds, x, tgt, avail, 3, hits=True)["hits"].astype(bool)
     (p,) = np.flatnonzero(h3)
     assert h2[p] and not h2[p - 1]
+
+
+def test_segment_rule_by_hand():
+    """The rule "segment" (online.rs:14-17) on a stream of two segments (the second starts at the BOS at 4): a query
+    sees only occurrences whose next token lies before its own segment's start."""
+    B = O.BOS
+    tok = np.array([5, 6, 5, 6, B, 5, 6, 7], np.uint16)
+    cell, nxt, w, tot, dist, cnt, hinted = O.brute_segment(tok, [0, 8], [1], [1, 2], 2, [1, 2])
+    # position 5, context (5): occurrences at 0 and 2 (next 6, 6); (B, 5) never occurred before 4
+    assert tot[5].tolist() == [2, 0] and dist[5].tolist() == [1, 0] and cnt[5].tolist() == [2, 0]
+    # position 6, contexts (6) and (5, 6): the occurrence at 1 (next 5); the one at 3 has its next token at 4
+    assert tot[6].tolist() == [1, 1] and dist[6].tolist() == [1, 1] and cnt[6].tolist() == [0, 0]
+    # the first segment sees nothing; rows: cell ((1 + 0) * 7 + count bin) * 6 + purity bin
+    assert not tot[:5].any() and not tot[7].any()
+    assert cell.tolist() == [0, 0, 0, 0, 0, (7 + 1) * 6 + 5, 7 * 6 + 5, 0] and hinted == 2
+    assert nxt[5].tolist() == [6, 0] and nxt[6].tolist() == [5, 0]
+    assert w[5].tolist() == [65535, 0] and w[6].tolist() == [65535, 0]
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_segment_rule_is_the_step_rule_over_segments(seed):
+    """The GPU's rule "segment" runs the step engine with one step per segment (tau = tau_in = the segment index):
+    the step rule's oracle fed those steps equals the segment rule's brute force on random multi-part streams."""
+    rng = np.random.default_rng(70 + seed)
+    n = int(rng.integers(60, 140))
+    tok = rng.integers(0, 3, size=n).astype(np.uint16)
+    tok[rng.random(n) < 0.08] = O.BOS
+    cuts = sorted(rng.choice(np.arange(10, n - 10), size=int(rng.integers(0, 3)), replace=False).tolist())
+    bounds = [0] + cuts + [n]
+    starts = np.zeros(n, bool)
+    starts[bounds[:-1]] = True
+    starts |= tok == O.BOS
+    seg = (np.cumsum(starts) - 1).astype(np.uint32)
+    args = ([1, 2, 3], [1, 2, 3, 4], 3, [1, 2, 4])
+    got = O.online(tok, bounds, seg, seg, *args, 0, int(seg[-1]) + 1)
+    want = O.brute_segment(tok, bounds, *args)
+    for g, w, name in zip(got, want, ("cell", "next", "weights", "tot", "dist", "cnt", "hinted")):
+        assert np.array_equal(g, w), name
+
+
+def test_train_hints_slots_by_hand():
+    """train_hints.rs's slots: a position's deepest levels with a counted occurrence fill its slots, deepest first;
+    the hand case's position 6 has both levels, position 5 only level 1, the rest none."""
+    B = O.BOS
+    tok = np.array([5, 6, 5, 6, B, 5, 6, 7], np.uint16)
+    cell, nxt, w, level = O.brute_train_hints(tok, [0, 8], [1, 2], [1, 2], 2, 2)
+    assert cell[6].tolist() == [((1 + 1) * 7 + 0) * 6 + 5, (7 + 0) * 6 + 5] and level[6].tolist() == [1, 0]
+    assert cell[5].tolist() == [(7 + 1) * 6 + 5, 0] and level[5].tolist() == [0, -1]
+    assert nxt[6, :, 0].tolist() == [5, 5] and w[6, :, 0].tolist() == [65535, 65535] and nxt[5, 0, 0] == 6
+    others = [0, 1, 2, 3, 4, 7]
+    assert not cell[others].any() and (level[others] == -1).all()
+
+
+def test_loader_plan_by_hand():
+    """llm.c's sequential loader plan (hint_stats.cuh loader_plan :395-409) for 2 ranks, B*T = 10, 2 micro-steps
+    and 3 steps over shards of 45 and 100 tokens: shard 0 holds (45 - 1) // 20 = 2 samples per rank, then shard 1."""
+    from ngram_amd.online import loader_plan, plan_rows, plan_spans, plan_stream
+
+    plan = loader_plan([45, 100], 2, 10, 2, 3)
+    rank0 = [(0, 0, 0, 0, 0), (0, 1, 0, 0, 20), (1, 0, 0, 1, 0), (1, 1, 0, 1, 20), (2, 0, 0, 1, 40), (2, 1, 0, 1, 60)]
+    rank1 = [(s, m, 1, sh, off + 10) for s, m, _, sh, off in rank0]
+    assert [tuple(r) for r in plan] == rank0 + rank1
+    sizes = plan_stream([45, 100], plan, 10)
+    assert sizes == [45, 81]  # shard 0 whole; shard 1 up to rank 1's last target (70 + 10 + 1)
+    spans = plan_spans(plan, sizes, 10)
+    assert spans[2].tolist() == [45, 55, 1] and spans[6].tolist() == [10, 20, 0]
+    rows = plan_rows(plan, sizes, 10, 2, 1)
+    assert rows[:10].tolist() == list(range(10, 20)) and rows[20:30].tolist() == list(range(55, 65))
+    with pytest.raises(ValueError):
+        loader_plan([45, 100], 2, 10, 2, 4)  # runs past the shards
