@@ -459,7 +459,8 @@ int oracle_longest_match(const u16* tok, const i64* bounds, int nshards, const u
 // exists (callers zero them). Returns the queries hinted, or -1 on bad arguments.
 i64 oracle_online(const u16* tok, i64 n, const i64* bounds, int nparts, const u32* tau, const u32* tau_in,
                   const int* levels, int nl, const int* buckets, int nb, int entries, const int* count_levels, int nc,
-                  u32 step_lo, u32 step_hi, int16_t* cell, u16* next, u16* weights, u32* tot, u16* dist, u32* cnt) {
+                  u32 step_lo, u32 step_hi, int16_t* cell, u16* next, u16* weights, u32* tot, u16* dist, u32* cnt,
+                  int threads) {
     const u32 NONE = 0xFFFFFFFFu;
     if (entries < 1 || nparts < 1 || step_lo > step_hi) return -1;
     for (int i = 0; i < nl; ++i)
@@ -489,7 +490,7 @@ i64 oracle_online(const u16* tok, i64 n, const i64* bounds, int nparts, const u3
     };
     std::vector<uint8_t> filled(n, 0);
     std::atomic<i64> hinted(0);
-    const int T = std::max(1, (int)std::thread::hardware_concurrency());
+    const int T = std::max(1, threads);
     auto now = [] { return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count(); };
     // levels needed: hint levels (descending: a position's row comes from its deepest level) and count levels
     std::vector<int> all;

@@ -59,7 +59,8 @@ def lib() -> ctypes.CDLL:
                                            ctypes.c_int, P, P, P, P, P, P, P, ctypes.c_int]
         so.oracle_online.restype = ctypes.c_int64
         so.oracle_online.argtypes = [P, ctypes.c_int64, P, ctypes.c_int, P, P, P, ctypes.c_int, P, ctypes.c_int,
-                                     ctypes.c_int, P, ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32, P, P, P, P, P, P]
+                                     ctypes.c_int, P, ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32, P, P, P, P, P, P,
+                                     ctypes.c_int]
         so.oracle_longest_match.restype = ctypes.c_int
         so.oracle_longest_match.argtypes = [P, P, ctypes.c_int, P, P, ctypes.c_int64, ctypes.c_int, P, P, P,
                                             ctypes.c_int]
@@ -192,7 +193,8 @@ def spans_tau(n: int, bounds, spans) -> tuple[np.ndarray, np.ndarray]:
     return tau, tau_in
 
 
-def online(tokens, bounds, tau, tau_in, levels, buckets, entries, count_levels, step_lo: int, step_hi: int):
+def online(tokens, bounds, tau, tau_in, levels, buckets, entries, count_levels, step_lo: int, step_hi: int,
+           nthreads: int | None = None):
     """The step rule's hint rows and count rows (oracle_online): (cell int16 [n], next uint16 [n, entries], weights
     uint16 [n, entries], tot uint32 [n, nc], dist uint16 [n, nc], cnt uint32 [n, nc], queries hinted)."""
     tok = np.ascontiguousarray(tokens, np.uint16)
@@ -210,7 +212,7 @@ def online(tokens, bounds, tau, tau_in, levels, buckets, entries, count_levels, 
     hinted = lib().oracle_online(_p(tok), n, _p(b), len(b) - 1, _p(np.ascontiguousarray(tau, np.uint32)),
                                  _p(np.ascontiguousarray(tau_in, np.uint32)), _p(lv), len(lv), _p(bk), len(bk), entries,
                                  _p(cl), len(cl), step_lo, step_hi, _p(cell), _p(nxt), _p(w), _p(tot), _p(dist),
-                                 _p(cnt))
+                                 _p(cnt), nthreads or threads())
     if hinted < 0:
         raise ValueError("oracle_online: bad arguments")
     return cell, nxt, w, tot[:, : len(cl)], dist[:, : len(cl)], cnt[:, : len(cl)], int(hinted)
