@@ -29,19 +29,25 @@ import torch
 from .data import HEADER_BYTES
 
 
+def _cpulist(text: str) -> set[int]:
+    """A sysfs CPU list ("0-3,8,10-11") as a set."""
+    out: set[int] = set()
+    for item in filter(None, text.strip().split(",")):
+        ends = [int(v) for v in item.split("-")]
+        out.update(range(ends[0], ends[-1] + 1))
+    return out
+
+
 def numa_cpus(device: int) -> set[int]:
-    """The CPUs of the GPU's NUMA node that this process may use; empty when the topology is unknown."""
+    """The CPUs of the GPU's NUMA node that this process may use; empty when the topology is unknown (sysfs: the
+    device's PCI function's numa_node, then that node's cpulist)."""
     try:
-        p = torch.cuda.get_device_properties(device)
-        bdf = f"{p.pci_domain_id:04x}:{p.pci_bus_id:02x}:{p.pci_device_id:02x}.0"
-        node = int(Path("/sys/bus/pci/devices", bdf, "numa_node").read_text())
-        if node < 0:
-            return set()
-        cpus = set()
-        for r in Path(f"/sys/devices/system/node/node{node}/cpulist").read_text().strip().split(","):
-            lo, hi = (r.split("-") + [r])[:2]
-            cpus |= set(range(int(lo), int(hi) + 1))
-        return cpus & os.sched_getaffinity(0)
+        props = torch.cuda.get_device_properties(device)
+        pci = Path("/sys/bus/pci/devices") / "{:04x}:{:02x}:{:02x}.0".format(
+            props.pci_domain_id, props.pci_bus_id, props.pci_device_id)
+        node = int((pci / "numa_node").read_text())
+        mine = os.sched_getaffinity(0)
+        return set() if node < 0 else _cpulist(Path(f"/sys/devices/system/node/node{node}/cpulist").read_text()) & mine
     except (OSError, ValueError, AttributeError):
         return set()
 

@@ -115,3 +115,11 @@ def test_fake_rows(monkeypatch):
     assert np.all(dist <= tot) and np.all(cnt <= tot) and (tot[:, 0] > 0).mean() > 0.8
     with pytest.raises(IndexError):
         h.val(slice(H.VAL_TOKENS, H.VAL_TOKENS + 1))
+
+
+def test_cpulist_parsing():
+    """The loader's NUMA pinning reads sysfs CPU lists: ranges, single CPUs, a trailing newline, an empty list."""
+    from ngram_amd.loader import _cpulist
+
+    assert _cpulist("0-3,8,10-11\n") == {0, 1, 2, 3, 8, 10, 11}
+    assert _cpulist("5") == {5} and _cpulist("") == set()
