@@ -404,6 +404,8 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
 }
 
 // Per context from packed words sorted by context (word >> (64 - cb)): a wave per window of 64 words, staged in LDS.
+// Each block is one wave, so that a wave held up by a long context holds up no other (with four waves a block, the
+// barriers made every round wait for the block's slowest wave: 22-27% slower at c3's levels 2 and 3).
 // A lane holding a context's first word whose context also ends in the window walks it in LDS alone (every such lane
 // at once); the one context that runs past the window's end, if it starts there, is done by the whole wave over the
 // following windows' leading words, counts summed and the top KT kept per lane, then reduced across the wave. No
@@ -415,9 +417,10 @@ __global__ void __launch_bounds__(PT_BLOCK) part_count_k(const u64* __restrict__
 // deep_min pairs appended to deep (nstat[0] of them; callers size deep for U / (deep_min + 1) + 1).
 #define SUMMARY_AHEAD 4  // windows of a long context loaded per step
 #define SUMMARY_SHORT 12  // the longest context a lane walks alone within a window
+#define SUMMARY_GRID 262144  // blocks (one wave each) at most; c3 sweep: 2^18 over 2^16 and 2^20
 
 template <int KT>
-__global__ void __launch_bounds__(256) ctx_summary_k(const u64* __restrict__ w, i64 U, int cb,
+__global__ void __launch_bounds__(WAVE) ctx_summary_k(const u64* __restrict__ w, i64 U, int cb,
                                                      const u64* __restrict__ esc_k, const u32* __restrict__ esc_c,
                                                      u64 esc_cap, u32* __restrict__ rec, u32* __restrict__ dist,
                                                      u32 deep_min, i64* __restrict__ deep, u32* __restrict__ nstat,
@@ -428,22 +431,21 @@ __global__ void __launch_bounds__(256) ctx_summary_k(const u64* __restrict__ w, 
         if (dist) dist[c] = pairs;
         if (deep && pairs > deep_min) deep[atomicAdd(&nstat[0], 1u)] = (i64)c;
     };
-    __shared__ u64 sw[4][WAVE];
+    __shared__ u64 sw[WAVE];
     const int sh = 64 - cb, csh = 48 - cb;
     const u64 esc = (1ull << csh) - 1;
-    const int lane = lane_id(), wid = threadIdx.x / WAVE;
+    const int lane = lane_id();
     auto count_of = [&](u64 word) -> u32 {
         const u64 n = word & esc;
         return n < esc ? (u32)n : esc_get(esc_k, esc_c, esc_cap, word >> csh);
     };
     const i64 nwin = (U + WAVE - 1) / WAVE;
-    for (i64 wb = (i64)blockIdx.x * 4; wb < nwin; wb += (i64)gridDim.x * 4) {  // the same rounds for the block's waves
-        const i64 wv = wb + wid;
+    for (i64 wv = blockIdx.x; wv < nwin; wv += gridDim.x) {
         const i64 i = wv * WAVE + lane;
         const bool valid = i < U;
         const u64 word = valid ? w[i] : 0;
         const u64 ctx = word >> sh;
-        sw[wid][lane] = word;
+        sw[lane] = word;
         u64 prev = shfl_up_u64(word, 1);
         if (lane == 0) prev = (valid && i > 0) ? w[i - 1] : 0;
         u64 next = shfl_down_u64(word, 1);
@@ -471,7 +473,7 @@ __global__ void __launch_bounds__(256) ctx_summary_k(const u64* __restrict__ w, 
             for (int r = 0; r < KT; ++r) tl[r] = 0;
             u64 s = 0;
             for (int j = lane; j <= e; ++j) {
-                const u64 wj = sw[wid][j];
+                const u64 wj = sw[j];
                 const u32 n = count_of(wj);
                 s += n;
                 topk_insert<KT>(tl, rank_score(wj >> csh, n));
@@ -749,14 +751,14 @@ extern "C" int ng_ctx_summary(const u64* w, i64 U, int cb, const u64* esc_k, con
                               u32* rec, u32* dist, u32 deep_min, i64* deep, u32* nstat, u32* flags, void* stream) {
     if (cb <= 0 || cb > 44 || esc_cap == 0 || (deep && !nstat)) return -1;
     if (U <= 0) return 0;
-    int g = grid_for((U + WAVE - 1) / WAVE, 4);  // four waves per block, a window each per round
-    g = g > 65536 ? 65536 : g;
+    int g = grid_for((U + WAVE - 1) / WAVE, 1);  // a window per block and round
+    g = g > SUMMARY_GRID ? SUMMARY_GRID : g;
     hipStream_t st = (hipStream_t)stream;
     switch (topk) {
-        case 1: ctx_summary_k<1><<<g, 256, 0, st>>>(w, U, cb, esc_k, esc_c, esc_cap, rec, dist, deep_min, deep, nstat, flags); break;
-        case 2: ctx_summary_k<2><<<g, 256, 0, st>>>(w, U, cb, esc_k, esc_c, esc_cap, rec, dist, deep_min, deep, nstat, flags); break;
-        case 4: ctx_summary_k<4><<<g, 256, 0, st>>>(w, U, cb, esc_k, esc_c, esc_cap, rec, dist, deep_min, deep, nstat, flags); break;
-        case 8: ctx_summary_k<8><<<g, 256, 0, st>>>(w, U, cb, esc_k, esc_c, esc_cap, rec, dist, deep_min, deep, nstat, flags); break;
+        case 1: ctx_summary_k<1><<<g, WAVE, 0, st>>>(w, U, cb, esc_k, esc_c, esc_cap, rec, dist, deep_min, deep, nstat, flags); break;
+        case 2: ctx_summary_k<2><<<g, WAVE, 0, st>>>(w, U, cb, esc_k, esc_c, esc_cap, rec, dist, deep_min, deep, nstat, flags); break;
+        case 4: ctx_summary_k<4><<<g, WAVE, 0, st>>>(w, U, cb, esc_k, esc_c, esc_cap, rec, dist, deep_min, deep, nstat, flags); break;
+        case 8: ctx_summary_k<8><<<g, WAVE, 0, st>>>(w, U, cb, esc_k, esc_c, esc_cap, rec, dist, deep_min, deep, nstat, flags); break;
         default: return -1;
     }
     return (int)hipGetLastError();
