@@ -153,26 +153,26 @@ __device__ __forceinline__ void top8_insert(u64 (&t)[8], u64 v) {
 // same-address atomics for hot contexts), and (its level's top lists kept) its top-E list is merged with the new
 // scores (an old entry of a touched token is superseded by its new score: counts only grow). A short context ending in
 // its window is done by its first lane from LDS; a long one, and the one running past the window, by the whole wave.
-__global__ void __launch_bounds__(256) online_top_k(const u64* __restrict__ uk, const u64* __restrict__ score,
+// Each block is one wave: no barrier makes a wave wait for another's long context.
+__global__ void __launch_bounds__(WAVE) online_top_k(const u64* __restrict__ uk, const u64* __restrict__ score,
                                                     const u32* __restrict__ agg, const i64* __restrict__ n_ptr, i64 m,
                                                     const i64* __restrict__ desc, int tshift, int E) {
-    __shared__ u64 s_key[4][WAVE];
-    __shared__ u64 s_sc[4][WAVE];
-    __shared__ u32 s_ag[4][WAVE];
+    __shared__ u64 s_key[WAVE];
+    __shared__ u64 s_sc[WAVE];
+    __shared__ u32 s_ag[WAVE];
     const i64 n = *n_ptr < m ? *n_ptr : m;
-    const int lane = (int)(threadIdx.x & (WAVE - 1)), wid = threadIdx.x / WAVE;
+    const int lane = (int)(threadIdx.x & (WAVE - 1));
     const i64 nwin = (n + WAVE - 1) / WAVE;
     auto ctx_of = [](u64 key) { return key >> 16; };
-    for (i64 wb = (i64)blockIdx.x * 4; wb < nwin; wb += (i64)gridDim.x * 4) {  // the same rounds for every wave
-        const i64 wv = wb + wid;
+    for (i64 wv = blockIdx.x; wv < nwin; wv += gridDim.x) {
         const i64 i = wv * WAVE + lane;
         u64 key = i < n ? uk[i] : EMPTY;
         const bool valid = key != EMPTY;
         const u64 sc = valid ? score[i] : 0;
         const u32 ag = valid ? agg[i] : 0;
-        s_key[wid][lane] = key;
-        s_sc[wid][lane] = sc;
-        s_ag[wid][lane] = ag;
+        s_key[lane] = key;
+        s_sc[lane] = sc;
+        s_ag[lane] = ag;
         u64 prev = shfl_up_u64(key, 1);
         if (lane == 0) prev = (valid && i > 0) ? uk[i - 1] : EMPTY;
         u64 next = shfl_down_u64(key, 1);
@@ -195,9 +195,9 @@ __global__ void __launch_bounds__(256) online_top_k(const u64* __restrict__ uk, 
 #pragma unroll
             for (int r = 0; r < 8; ++r) t[r] = 0;
             for (int q = lane; q <= e; ++q) {
-                add += s_ag[wid][q];
-                fresh += (u32)(s_sc[wid][q] >> 16) == s_ag[wid][q];
-                if (ctx_top) top8_insert(t, s_sc[wid][q]);
+                add += s_ag[q];
+                fresh += (u32)(s_sc[q] >> 16) == s_ag[q];
+                if (ctx_top) top8_insert(t, s_sc[q]);
             }
             ctx_tot[slot] += add;
             ctx_dist[slot] += fresh;
@@ -208,7 +208,7 @@ __global__ void __launch_bounds__(256) online_top_k(const u64* __restrict__ uk, 
                     if (old == 0) break;
                     const u64 tk = (c << 16) | (0xFFFFu - (u32)(old & 0xFFFF));
                     bool touched = false;
-                    for (int q = lane; q <= e; ++q) touched |= s_key[wid][q] == tk;
+                    for (int q = lane; q <= e; ++q) touched |= s_key[q] == tk;
                     if (!touched) top8_insert(t, old);
                 }
                 for (int r = 0; r < E; ++r) top[r] = t[r];
@@ -431,8 +431,7 @@ extern "C" int ng_online_top(const u64* uk, const i64* n, i64 m, const u32* agg,
     hipStream_t st = (hipStream_t)stream;
     online_scores_k<<<grid_for(m, 256), 256, 0, st>>>(uk, n, m, desc, tshift, score);
     const i64 wins = (m + WAVE - 1) / WAVE;
-    const i64 g = (wins + 3) / 4;
-    online_top_k<<<(unsigned)(g < 65536 ? g : 65536), 256, 0, st>>>(uk, score, agg, n, m, desc, tshift, E);
+    online_top_k<<<(unsigned)(wins < 262144 ? wins : 262144), WAVE, 0, st>>>(uk, score, agg, n, m, desc, tshift, E);
     return (int)hipGetLastError();
 }
 
