@@ -285,6 +285,14 @@ int ng_online_query(const uint16_t* tok, const int* avail, const unsigned char* 
                     int k, const ng_u64* ck, ng_u64 ccap, const ng_u64* pk, const uint32_t* pcnt, ng_u64 pcap,
                     const uint32_t* ctx_tot, const uint32_t* ctx_dist, int* qslot, uint32_t* tot, uint16_t* dist,
                     uint32_t* cnt, int nc, int ci, void* stream);
+/* the inserts / the queries of up to 8 levels of a step in one launch (a level's lookups are chains of dependent
+ * table round trips; one launch pays that latency once for all levels). lv: a host array, 11 int64 per level for
+ * inserts (pos, m, k, ck, ccap, pk, pcnt, pcap, ev, flags, tag) and 14 per level for queries (k, ck, ccap, pk, pcnt,
+ * pcap, ctx_tot, ctx_dist, qslot, tot, dist, cnt, nc, ci), each as the single-level call's argument of that name
+ * (pointers as int64; the inserts leave totals and distinct counts to ng_online_top). -1 on a bad level. */
+int ng_online_insert_levels(const uint16_t* tok, int nlv, const ng_i64* lv, void* stream);
+int ng_online_query_levels(const uint16_t* tok, const int* avail, const unsigned char* has_next, const int* pos,
+                           ng_i64 m, int nlv, const ng_i64* lv, void* stream);
 /* hint rows of the queries at pos[0..m) in S slots, deepest levels first: cell [n, S], next / weights [n, S, E],
  * level [n, S] (int8 bucket index; may be NULL); empty slots are left as they are */
 int ng_online_rows(const int* pos, ng_i64 m, int nlv, const ng_i64* desc, int E, int S, short* cell, uint16_t* next,

@@ -75,14 +75,12 @@ __device__ __forceinline__ u64 okey(const u16* e, int k) {
     else return ctx_key_rt(e, k);
 }
 
-// Occurrences ending at pos[i] (context tok[g-k+1..g], next tok[g+1]; the caller lists valid ones only); ev[i] = the
+// Occurrence i ending at pos[i] (context tok[g-k+1..g], next tok[g+1]; the caller lists valid ones only); ev[i] = the
 // pair key | tag (the level's tag, above every pair key's bits: several levels' events sort as one array).
 template <int K>
-__global__ void online_insert_k(const u16* __restrict__ tok, const int* __restrict__ pos, i64 m, int k, u64* ck,
-                                u64 ccap, u64* pk, u32* pcnt, u64 pcap, u32* ctx_tot, u32* ctx_dist,
-                                u64* __restrict__ ev, u32* flags, u64 tag) {
-    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
-    if (i >= m) return;
+__device__ __forceinline__ void insert_one(const u16* __restrict__ tok, const int* __restrict__ pos, i64 i, int k,
+                                           u64* ck, u64 ccap, u64* pk, u32* pcnt, u64 pcap, u32* ctx_tot,
+                                           u32* ctx_dist, u64* __restrict__ ev, u32* flags, u64 tag) {
     const i64 g = pos[i];
     const u64 key = okey<K>(tok + g + 1, k);
     const i64 slot = octx_find_insert(ck, ccap, key, flags);
@@ -101,6 +99,54 @@ __global__ void online_insert_k(const u16* __restrict__ tok, const int* __restri
         if (added) atomicAdd(&ctx_dist[slot], 1u);
     }
     ev[i] = pair | tag;
+}
+
+template <int K>
+__global__ void online_insert_k(const u16* __restrict__ tok, const int* __restrict__ pos, i64 m, int k, u64* ck,
+                                u64 ccap, u64* pk, u32* pcnt, u64 pcap, u32* ctx_tot, u32* ctx_dist,
+                                u64* __restrict__ ev, u32* flags, u64 tag) {
+    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    if (i < m) insert_one<K>(tok, pos, i, k, ck, ccap, pk, pcnt, pcap, ctx_tot, ctx_dist, ev, flags, tag);
+}
+
+// Every level's inserts of a step in one launch: a step's levels each wait on a chain of dependent table round trips
+// (context, then pair), so one launch per level paid that latency once per level (c4: 60-90 us each). Level t takes
+// the blocks with blockIdx.y == t; its fields (ONLINE_INS_FIELDS i64 each, as ng_online_insert_levels documents) are
+// picked by unrolled compares on that block-uniform index, so no kernel argument is indexed at run time.
+#define ONLINE_MAXL 8
+#define ONLINE_INS_FIELDS 11
+struct OInsArgs {
+    i64 f[ONLINE_MAXL][ONLINE_INS_FIELDS];
+};
+
+template <int K>
+__device__ __forceinline__ void insert_level(const u16* __restrict__ tok, const i64 (&f)[ONLINE_INS_FIELDS], i64 i) {
+    if (i >= f[1]) return;
+    insert_one<K>(tok, (const int*)f[0], i, (int)f[2], (u64*)f[3], (u64)f[4], (u64*)f[5], (u32*)f[6], (u64)f[7],
+                  nullptr, nullptr, (u64*)f[8], (u32*)f[9], (u64)f[10]);
+}
+
+__global__ void __launch_bounds__(256) online_insert_levels_k(const u16* __restrict__ tok, int nlv, OInsArgs a) {
+    const int t = blockIdx.y;
+    i64 f[ONLINE_INS_FIELDS];
+#pragma unroll
+    for (int q = 0; q < ONLINE_INS_FIELDS; ++q) f[q] = 0;
+#pragma unroll
+    for (int l = 0; l < ONLINE_MAXL; ++l)
+        if (l == t)
+#pragma unroll
+            for (int q = 0; q < ONLINE_INS_FIELDS; ++q) f[q] = a.f[l][q];
+    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    switch ((int)f[2]) {
+        case 1: insert_level<1>(tok, f, i); break;
+        case 2: insert_level<2>(tok, f, i); break;
+        case 3: insert_level<3>(tok, f, i); break;
+        case 4: insert_level<4>(tok, f, i); break;
+        case 5: insert_level<5>(tok, f, i); break;
+        case 6: insert_level<6>(tok, f, i); break;
+        case 8: insert_level<8>(tok, f, i); break;
+        default: insert_level<0>(tok, f, i); break;
+    }
 }
 
 // A level's state as the step's merge reads it: desc[t * 6 ...] for tag t = pair table keys, counts, capacity, the
@@ -309,14 +355,13 @@ __global__ void __launch_bounds__(WAVE) online_top_k(const u64* __restrict__ uk,
 // slot (or -1) into qslot[i]; with count outputs (tot != NULL) tot / dist / cnt of the position into row g, column ci
 // of [n, nc] arrays (cnt: the count of tok[g+1] if has_next[g]).
 template <int K>
-__global__ void online_query_k(const u16* __restrict__ tok, const int* __restrict__ avail,
-                               const unsigned char* __restrict__ has_next, const int* __restrict__ pos, i64 m, int k,
-                               const u64* __restrict__ ck, u64 ccap, const u64* __restrict__ pk,
-                               const u32* __restrict__ pcnt, u64 pcap, const u32* __restrict__ ctx_tot,
-                               const u32* __restrict__ ctx_dist, int* __restrict__ qslot, u32* __restrict__ tot,
-                               u16* __restrict__ dist, u32* __restrict__ cnt, int nc, int ci) {
-    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
-    if (i >= m) return;
+__device__ __forceinline__ void query_one(const u16* __restrict__ tok, const int* __restrict__ avail,
+                                          const unsigned char* __restrict__ has_next, const int* __restrict__ pos,
+                                          i64 i, int k, const u64* __restrict__ ck, u64 ccap,
+                                          const u64* __restrict__ pk, const u32* __restrict__ pcnt, u64 pcap,
+                                          const u32* __restrict__ ctx_tot, const u32* __restrict__ ctx_dist,
+                                          int* __restrict__ qslot, u32* __restrict__ tot, u16* __restrict__ dist,
+                                          u32* __restrict__ cnt, int nc, int ci) {
     const i64 g = pos[i];
     i64 slot = -1;
     if (avail[g] >= (K > 0 ? K : k)) slot = octx_find(ck, ccap, okey<K>(tok + g + 1, k));
@@ -328,6 +373,60 @@ __global__ void online_query_k(const u16* __restrict__ tok, const int* __restric
         const u32 d = ctx_dist[slot];
         dist[at] = (u16)(d < 65535u ? d : 65535u);
         cnt[at] = has_next[g] ? opair_count(pk, pcnt, pcap, ((u64)slot << 16) | tok[g + 1]) : 0u;
+    }
+}
+
+template <int K>
+__global__ void online_query_k(const u16* __restrict__ tok, const int* __restrict__ avail,
+                               const unsigned char* __restrict__ has_next, const int* __restrict__ pos, i64 m, int k,
+                               const u64* __restrict__ ck, u64 ccap, const u64* __restrict__ pk,
+                               const u32* __restrict__ pcnt, u64 pcap, const u32* __restrict__ ctx_tot,
+                               const u32* __restrict__ ctx_dist, int* __restrict__ qslot, u32* __restrict__ tot,
+                               u16* __restrict__ dist, u32* __restrict__ cnt, int nc, int ci) {
+    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    if (i < m)
+        query_one<K>(tok, avail, has_next, pos, i, k, ck, ccap, pk, pcnt, pcap, ctx_tot, ctx_dist, qslot, tot, dist,
+                     cnt, nc, ci);
+}
+
+// Every level's queries of a step in one launch (the same reason and layout as online_insert_levels_k).
+#define ONLINE_QRY_FIELDS 14
+struct OQryArgs {
+    i64 f[ONLINE_MAXL][ONLINE_QRY_FIELDS];
+};
+
+template <int K>
+__device__ __forceinline__ void query_level(const u16* __restrict__ tok, const int* __restrict__ avail,
+                                            const unsigned char* __restrict__ has_next, const int* __restrict__ pos,
+                                            i64 i, const i64 (&f)[ONLINE_QRY_FIELDS]) {
+    query_one<K>(tok, avail, has_next, pos, i, (int)f[0], (const u64*)f[1], (u64)f[2], (const u64*)f[3],
+                 (const u32*)f[4], (u64)f[5], (const u32*)f[6], (const u32*)f[7], (int*)f[8], (u32*)f[9], (u16*)f[10],
+                 (u32*)f[11], (int)f[12], (int)f[13]);
+}
+
+__global__ void __launch_bounds__(256) online_query_levels_k(const u16* __restrict__ tok, const int* __restrict__ avail,
+                                                             const unsigned char* __restrict__ has_next,
+                                                             const int* __restrict__ pos, i64 m, OQryArgs a) {
+    const int t = blockIdx.y;
+    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    if (i >= m) return;
+    i64 f[ONLINE_QRY_FIELDS];
+#pragma unroll
+    for (int q = 0; q < ONLINE_QRY_FIELDS; ++q) f[q] = 0;
+#pragma unroll
+    for (int l = 0; l < ONLINE_MAXL; ++l)
+        if (l == t)
+#pragma unroll
+            for (int q = 0; q < ONLINE_QRY_FIELDS; ++q) f[q] = a.f[l][q];
+    switch ((int)f[0]) {
+        case 1: query_level<1>(tok, avail, has_next, pos, i, f); break;
+        case 2: query_level<2>(tok, avail, has_next, pos, i, f); break;
+        case 3: query_level<3>(tok, avail, has_next, pos, i, f); break;
+        case 4: query_level<4>(tok, avail, has_next, pos, i, f); break;
+        case 5: query_level<5>(tok, avail, has_next, pos, i, f); break;
+        case 6: query_level<6>(tok, avail, has_next, pos, i, f); break;
+        case 8: query_level<8>(tok, avail, has_next, pos, i, f); break;
+        default: query_level<0>(tok, avail, has_next, pos, i, f); break;
     }
 }
 
@@ -416,6 +515,46 @@ extern "C" int ng_online_insert(const u16* tok, const int* pos, i64 m, int k, u6
     if (ccap == 0 || pcap == 0 || ccap > (1ull << 40) || (tag && tag < (ccap << 16))) return -1;
     hipStream_t st = (hipStream_t)stream;
     OLEVELS(k, (online_insert_k<K><<<grid_for(m, 256), 256, 0, st>>>(tok, pos, m, k, ck, ccap, pk, pcnt, pcap, ctx_tot, ctx_dist, ev, flags, tag)));
+    return (int)hipGetLastError();
+}
+
+// The inserts of nlv (1..8) levels in one launch: lv[t * 11 ...] = level t's pos, m, k, ck, ccap, pk, pcnt, pcap, ev,
+// flags, tag (host memory, read before the call returns; the pointers device memory), each as ng_online_insert's
+// arguments of the same names (its totals and distinct counts left to ng_online_top). -1 on a bad level.
+extern "C" int ng_online_insert_levels(const u16* tok, int nlv, const i64* lv, void* stream) {
+    if (nlv < 1 || nlv > ONLINE_MAXL || !lv) return -1;
+    OInsArgs a{};
+    i64 mmax = 0;
+    for (int t = 0; t < nlv; ++t) {
+        const i64* f = lv + (i64)t * ONLINE_INS_FIELDS;
+        const i64 m = f[1], k = f[2];
+        const u64 ccap = (u64)f[4], pcap = (u64)f[7], tag = (u64)f[10];
+        if (m < 0 || k < 1 || k > MAXK || ccap == 0 || pcap == 0 || ccap > (1ull << 40) || (tag && tag < (ccap << 16)))
+            return -1;
+        if (m > 0 && (!f[0] || !f[3] || !f[5] || !f[6] || !f[8] || !f[9])) return -1;
+        for (int q = 0; q < ONLINE_INS_FIELDS; ++q) a.f[t][q] = f[q];
+        mmax = m > mmax ? m : mmax;
+    }
+    if (mmax == 0) return 0;
+    online_insert_levels_k<<<dim3((unsigned)grid_for(mmax, 256), (unsigned)nlv), 256, 0, (hipStream_t)stream>>>(tok, nlv, a);
+    return (int)hipGetLastError();
+}
+
+// The queries pos[0..m) of nlv (1..8) levels in one launch: lv[t * 14 ...] = level t's k, ck, ccap, pk, pcnt, pcap,
+// ctx_tot, ctx_dist, qslot, tot, dist, cnt, nc, ci (host memory; as ng_online_query's arguments of the same names).
+extern "C" int ng_online_query_levels(const u16* tok, const int* avail, const unsigned char* has_next, const int* pos,
+                                      i64 m, int nlv, const i64* lv, void* stream) {
+    if (nlv < 1 || nlv > ONLINE_MAXL || !lv) return -1;
+    OQryArgs a{};
+    for (int t = 0; t < nlv; ++t) {
+        const i64* f = lv + (i64)t * ONLINE_QRY_FIELDS;
+        if (f[0] < 1 || f[0] > MAXK || f[2] <= 0 || f[5] <= 0 || !f[1] || !f[3] || !f[4] || !f[6] || !f[7]) return -1;
+        if (f[9] && (!f[10] || !f[11] || f[12] < 1 || f[13] < 0 || f[13] >= f[12])) return -1;
+        for (int q = 0; q < ONLINE_QRY_FIELDS; ++q) a.f[t][q] = f[q];
+    }
+    if (m <= 0) return 0;
+    online_query_levels_k<<<dim3((unsigned)grid_for(m, 256), (unsigned)nlv), 256, 0, (hipStream_t)stream>>>(
+        tok, avail, has_next, pos, m, a);
     return (int)hipGetLastError();
 }
 

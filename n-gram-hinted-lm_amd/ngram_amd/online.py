@@ -9,18 +9,34 @@ a query's k-context must lie in its segment (segments start at each part's start
 
 `advance(step_hi, ...)` is the incremental path (online.rs :333): the GPU state (per level a context table with
 totals, distinct counts and exact top-`entries` lists, and a split pair table) persists between calls; a step inserts
-its newly available occurrences, then answers its queries (libngram_amd.so: ng_online_insert, sort_pairs,
-reduce_by_key, ng_online_top, ng_online_query, ng_online_rows). `hints` / `counts` answer a step range from a fresh
+its newly available occurrences, then answers its queries (libngram_amd.so: ng_online_insert_levels, sort_pairs,
+reduce_by_key, ng_online_top, ng_online_query_levels, ng_online_rows). `hints` / `counts` answer a step range from a fresh
 state; with rule="segment" (the reference's exactness-test rule) they answer every position from its segment's
 start, one step per segment."""
 
 from __future__ import annotations
+
+import ctypes
 
 import numpy as np
 import torch
 
 from .data import BOS
 from .lib import Lib, i32, u64
+
+
+MAX_LAUNCH_LEVELS = 8  # levels per fused insert / query launch (ng_online_insert_levels, ng_online_query_levels)
+
+
+def _ptr(t: torch.Tensor, at: int = 0) -> int:
+    """The device address of element `at` of t."""
+    return t.data_ptr() + at * t.element_size()
+
+
+def _i64_array(rows) -> ctypes.Array:
+    """Level rows of ints as one host int64 array (values of 2^63 and above wrap, as a u64 argument would)."""
+    flat = [v - (1 << 64) if v >= 1 << 63 else v for row in rows for v in row]
+    return (ctypes.c_int64 * len(flat))(*flat)
 
 NONE = 0xFFFFFFFF
 LOAD = 0.5
@@ -258,15 +274,19 @@ class OnlineRows:
         levels, buckets, entries, count_levels = outs["cfg"]
         E = st["E"]
         m = 0
+        ins = []
         for t, (k, lv) in enumerate(st["levels"].items()):
             a, b = self._range(lv["alpha"], s, s + 1)
             if b == a:
                 continue
             # the totals and distinct counts are added per context by the sorted pass (ng_online_top), not per
             # occurrence: hot contexts would make chains of same-address atomics
-            lib("ng_online_insert", self.tok, lv["occ"][a:b], b - a, i32(k), lv["ck"], u64(lv["ccap"]), lv["pk"],
-                lv["pcnt"], u64(lv["pcap"]), None, None, st["ev"][m:], lv["flags"], u64(t << st["tshift"]))
+            ins.append((_ptr(lv["occ"], a), b - a, k, _ptr(lv["ck"]), lv["ccap"], _ptr(lv["pk"]), _ptr(lv["pcnt"]),
+                        lv["pcap"], _ptr(st["ev"], m), _ptr(lv["flags"]), t << st["tshift"]))
             m += b - a
+        for j in range(0, len(ins), MAX_LAUNCH_LEVELS):  # every level's inserts in one launch
+            part = ins[j : j + MAX_LAUNCH_LEVELS]
+            lib("ng_online_insert_levels", self.tok, i32(len(part)), _i64_array(part))
         if m:
             lib.cub("sort_pairs", st["ev"], st["ev_sorted"], None, None, m, i32(0), i32(st["tshift"] + st["tag_bits"]))
             lib.cub("reduce_by_key", st["ev_sorted"], st["uk"], None, st["agg"], st["nruns"], m)  # run lengths
@@ -277,18 +297,19 @@ class OnlineRows:
         if mq == 0 or not queries:
             return
         qpos = st["q_pos"][qa:qb]
-        for ci, k in enumerate(count_levels):
+        qry = []
+        nc = len(count_levels)
+        for k in list(count_levels) + [k for k in levels if k not in count_levels]:
             lv = st["levels"][k]
-            lib("ng_online_query", self.tok, self.avail, self.has_next, qpos, mq, i32(k), lv["ck"], u64(lv["ccap"]),
-                lv["pk"], lv["pcnt"], u64(lv["pcap"]), lv["tot"], lv["dist"], st["qslot"][k] if k in levels else None,
-                outs["tot"], outs["dist"], outs["cnt"], i32(len(count_levels)), i32(ci))
-        for k in levels:
-            if k in count_levels:
-                continue
-            lv = st["levels"][k]
-            lib("ng_online_query", self.tok, self.avail, self.has_next, qpos, mq, i32(k), lv["ck"], u64(lv["ccap"]),
-                lv["pk"], lv["pcnt"], u64(lv["pcap"]), lv["tot"], lv["dist"], st["qslot"][k], None, None, None,
-                i32(1), i32(0))
+            ci = count_levels.index(k) if k in count_levels else -1
+            qry.append((k, _ptr(lv["ck"]), lv["ccap"], _ptr(lv["pk"]), _ptr(lv["pcnt"]), lv["pcap"], _ptr(lv["tot"]),
+                        _ptr(lv["dist"]), _ptr(st["qslot"][k]) if k in levels else 0,
+                        _ptr(outs["tot"]) if ci >= 0 else 0, _ptr(outs["dist"]) if ci >= 0 else 0,
+                        _ptr(outs["cnt"]) if ci >= 0 else 0, nc if ci >= 0 else 1, max(ci, 0)))
+        for j in range(0, len(qry), MAX_LAUNCH_LEVELS):  # every level's queries in one launch
+            part = qry[j : j + MAX_LAUNCH_LEVELS]
+            lib("ng_online_query_levels", self.tok, self.avail, self.has_next, qpos, mq, i32(len(part)),
+                _i64_array(part))
         if levels:
             lib("ng_online_rows", qpos, mq, i32(len(levels)), st["rows_desc"], i32(E), i32(outs["slots"]), outs["cell"],
                 outs["next"], outs["weights"], outs["level"], st["hinted"])
