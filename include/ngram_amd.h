@@ -274,13 +274,14 @@ int ng_pos_rows(ng_i64 N, int nlv, const ng_i64* desc, int entries, short* cell,
 /* online state (online.rs step rule): insert occurrences ending at pos[i] (ctx_tot/ctx_dist may be NULL: then the
  * sorted pass adds them), their pair keys | tag into ev (tag: the level's index << tshift, above every pair key);
  * merge a step's sorted distinct touched pairs of every level at once (uk[0..*n) tagged keys, agg their occurrences
- * in the step; desc[t * 6]: level t's pair keys, counts, capacity, top lists or 0, totals, distinct counts) into
- * their contexts' totals, distinct counts and top-E lists; answer queries; build hint rows */
+ * in the step; desc[t * 7]: level t's pair keys, counts, capacity, top lists or 0, totals, distinct counts, flags)
+ * into their contexts' totals, distinct counts and top-E lists (add_counts: the pairs' counts grow by agg there,
+ * after inserts that did not count them); answer queries; build hint rows */
 int ng_online_insert(const uint16_t* tok, const int* pos, ng_i64 m, int k, ng_u64* ck, ng_u64 ccap, ng_u64* pk,
                      uint32_t* pcnt, ng_u64 pcap, uint32_t* ctx_tot, uint32_t* ctx_dist, ng_u64* ev, uint32_t* flags,
                      ng_u64 tag, void* stream);
 int ng_online_top(const ng_u64* uk, const ng_i64* n, ng_i64 m, const uint32_t* agg, const ng_i64* desc, int ntag,
-                  int tshift, ng_u64* score, int E, void* stream);
+                  int tshift, ng_u64* score, int E, int add_counts, void* stream);
 int ng_online_query(const uint16_t* tok, const int* avail, const unsigned char* has_next, const int* pos, ng_i64 m,
                     int k, const ng_u64* ck, ng_u64 ccap, const ng_u64* pk, const uint32_t* pcnt, ng_u64 pcap,
                     const uint32_t* ctx_tot, const uint32_t* ctx_dist, int* qslot, uint32_t* tot, uint16_t* dist,
@@ -289,8 +290,9 @@ int ng_online_query(const uint16_t* tok, const int* avail, const unsigned char* 
  * table round trips; one launch pays that latency once for all levels). lv: a host array, 11 int64 per level for
  * inserts (pos, m, k, ck, ccap, pk, pcnt, pcap, ev, flags, tag) and 14 per level for queries (k, ck, ccap, pk, pcnt,
  * pcap, ctx_tot, ctx_dist, qslot, tot, dist, cnt, nc, ci), each as the single-level call's argument of that name
- * (pointers as int64; the inserts leave totals and distinct counts to ng_online_top). -1 on a bad level. */
-int ng_online_insert_levels(const uint16_t* tok, int nlv, const ng_i64* lv, void* stream);
+ * (pointers as int64; the inserts leave totals and distinct counts to ng_online_top, and with count_pairs 0 the pair
+ * counts too: ng_online_top's add_counts). -1 on a bad level. */
+int ng_online_insert_levels(const uint16_t* tok, int nlv, const ng_i64* lv, int count_pairs, void* stream);
 int ng_online_query_levels(const uint16_t* tok, const int* avail, const unsigned char* has_next, const int* pos,
                            ng_i64 m, int nlv, const ng_i64* lv, void* stream);
 /* hint rows of the queries at pos[0..m) in S slots, deepest levels first: cell [n, S], next / weights [n, S, E],

@@ -69,6 +69,22 @@ __device__ __forceinline__ u32 opair_count(const u64* __restrict__ keys, const u
     return 0;
 }
 
+// A pair's slot, inserted if absent (-1 and flags[0] bit 0 if the table is full).
+__device__ __forceinline__ i64 opair_slot(u64* keys, u64 cap, u64 key, u32* flags) {
+    u64 s = __umul64hi(mix64(key), cap);
+    for (int probe = 0; probe < MAXPROBE; ++probe) {
+        const u64 cur = keys[s];
+        if (cur == key) return (i64)s;
+        if (cur == EMPTY) {
+            const u64 prev = atomicCAS((unsigned long long*)&keys[s], EMPTY, key);
+            if (prev == EMPTY || prev == key) return (i64)s;
+        }
+        s = s + 1 == cap ? 0 : s + 1;
+    }
+    atomicOr(&flags[0], 1u);
+    return -1;
+}
+
 template <int K>
 __device__ __forceinline__ u64 okey(const u16* e, int k) {
     if constexpr (K > 0) return ctx_key<K>(e);
@@ -80,7 +96,8 @@ __device__ __forceinline__ u64 okey(const u16* e, int k) {
 template <int K>
 __device__ __forceinline__ void insert_one(const u16* __restrict__ tok, const int* __restrict__ pos, i64 i, int k,
                                            u64* ck, u64 ccap, u64* pk, u32* pcnt, u64 pcap, u32* ctx_tot,
-                                           u32* ctx_dist, u64* __restrict__ ev, u32* flags, u64 tag) {
+                                           u32* ctx_dist, u64* __restrict__ ev, u32* flags, u64 tag,
+                                           bool count_pair = true) {
     const i64 g = pos[i];
     const u64 key = okey<K>(tok + g + 1, k);
     const i64 slot = octx_find_insert(ck, ccap, key, flags);
@@ -89,6 +106,10 @@ __device__ __forceinline__ void insert_one(const u16* __restrict__ tok, const in
         return;
     }
     const u64 pair = ((u64)slot << 16) | tok[g + 1];
+    if (!count_pair) {  // the step's merge counts each distinct pair once (ng_online_top with add_counts)
+        ev[i] = pair | tag;
+        return;
+    }
     const int added = opair_add(pk, pcnt, pcap, pair, flags);
     if (added < 0) {
         ev[i] = EMPTY;
@@ -120,13 +141,15 @@ struct OInsArgs {
 };
 
 template <int K>
-__device__ __forceinline__ void insert_level(const u16* __restrict__ tok, const i64 (&f)[ONLINE_INS_FIELDS], i64 i) {
+__device__ __forceinline__ void insert_level(const u16* __restrict__ tok, const i64 (&f)[ONLINE_INS_FIELDS], i64 i,
+                                             bool count_pairs) {
     if (i >= f[1]) return;
     insert_one<K>(tok, (const int*)f[0], i, (int)f[2], (u64*)f[3], (u64)f[4], (u64*)f[5], (u32*)f[6], (u64)f[7],
-                  nullptr, nullptr, (u64*)f[8], (u32*)f[9], (u64)f[10]);
+                  nullptr, nullptr, (u64*)f[8], (u32*)f[9], (u64)f[10], count_pairs);
 }
 
-__global__ void __launch_bounds__(256) online_insert_levels_k(const u16* __restrict__ tok, int nlv, OInsArgs a) {
+__global__ void __launch_bounds__(256) online_insert_levels_k(const u16* __restrict__ tok, int nlv, OInsArgs a,
+                                                              bool count_pairs) {
     const int t = blockIdx.y;
     i64 f[ONLINE_INS_FIELDS];
 #pragma unroll
@@ -138,36 +161,41 @@ __global__ void __launch_bounds__(256) online_insert_levels_k(const u16* __restr
             for (int q = 0; q < ONLINE_INS_FIELDS; ++q) f[q] = a.f[l][q];
     const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
     switch ((int)f[2]) {
-        case 1: insert_level<1>(tok, f, i); break;
-        case 2: insert_level<2>(tok, f, i); break;
-        case 3: insert_level<3>(tok, f, i); break;
-        case 4: insert_level<4>(tok, f, i); break;
-        case 5: insert_level<5>(tok, f, i); break;
-        case 6: insert_level<6>(tok, f, i); break;
-        case 8: insert_level<8>(tok, f, i); break;
-        default: insert_level<0>(tok, f, i); break;
+        case 1: insert_level<1>(tok, f, i, count_pairs); break;
+        case 2: insert_level<2>(tok, f, i, count_pairs); break;
+        case 3: insert_level<3>(tok, f, i, count_pairs); break;
+        case 4: insert_level<4>(tok, f, i, count_pairs); break;
+        case 5: insert_level<5>(tok, f, i, count_pairs); break;
+        case 6: insert_level<6>(tok, f, i, count_pairs); break;
+        case 8: insert_level<8>(tok, f, i, count_pairs); break;
+        default: insert_level<0>(tok, f, i, count_pairs); break;
     }
 }
 
-// A level's state as the step's merge reads it: desc[t * 6 ...] for tag t = pair table keys, counts, capacity, the
-// contexts' top-E lists (0: not kept), totals, distinct counts.
+// A level's state as the step's merge reads it: desc[t * 7 ...] for tag t = pair table keys, counts, capacity, the
+// contexts' top-E lists (0: not kept), totals, distinct counts, the level's flags.
+#define OLEVEL_FIELDS 7
 struct OLevel {
-    const u64* pk;
-    const u32* pcnt;
+    u64* pk;
+    u32* pcnt;
     u64 pcap;
     u64* top;
     u32* tot;
     u32* dist;
+    u32* flags;
 };
 
 __device__ __forceinline__ OLevel olevel(const i64* __restrict__ desc, u64 tag) {
-    const i64* d = desc + tag * 6;
-    return OLevel{(const u64*)d[0], (const u32*)d[1], (u64)d[2], (u64*)d[3], (u32*)d[4], (u32*)d[5]};
+    const i64* d = desc + tag * OLEVEL_FIELDS;
+    return OLevel{(u64*)d[0], (u32*)d[1], (u64)d[2], (u64*)d[3], (u32*)d[4], (u32*)d[5], (u32*)d[6]};
 }
 
-// Scores of a step's distinct touched pairs (sorted, tagged keys), i < *n.
-__global__ void online_scores_k(const u64* __restrict__ uk, const i64* __restrict__ n, i64 m,
-                                const i64* __restrict__ desc, int tshift, u64* __restrict__ score) {
+// Scores of a step's distinct touched pairs (sorted, tagged keys), i < *n. add_counts: each pair's step occurrences
+// agg[i] are added to its count here (found or inserted; a plain update: the keys are distinct), else the inserts
+// counted them.
+__global__ void online_scores_k(const u64* __restrict__ uk, const u32* __restrict__ agg, const i64* __restrict__ n,
+                                i64 m, const i64* __restrict__ desc, int tshift, bool add_counts,
+                                u64* __restrict__ score) {
     const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
     if (i >= m || i >= *n) return;
     const u64 key = uk[i];
@@ -176,7 +204,19 @@ __global__ void online_scores_k(const u64* __restrict__ uk, const i64* __restric
         return;
     }
     const OLevel lv = olevel(desc, key >> tshift);
-    const u32 c = opair_count(lv.pk, lv.pcnt, lv.pcap, key & ((1ull << tshift) - 1));
+    const u64 pair = key & ((1ull << tshift) - 1);
+    u32 c;
+    if (add_counts) {
+        const i64 s = opair_slot(lv.pk, lv.pcap, pair, lv.flags);
+        if (s < 0) {
+            score[i] = 0;
+            return;
+        }
+        c = lv.pcnt[s] + agg[i];
+        lv.pcnt[s] = c;
+    } else {
+        c = opair_count(lv.pk, lv.pcnt, lv.pcap, pair);
+    }
     score[i] = ((u64)c << 16) | (0xFFFFu - (u32)(key & 0xFFFF));
 }
 
@@ -520,8 +560,10 @@ extern "C" int ng_online_insert(const u16* tok, const int* pos, i64 m, int k, u6
 
 // The inserts of nlv (1..8) levels in one launch: lv[t * 11 ...] = level t's pos, m, k, ck, ccap, pk, pcnt, pcap, ev,
 // flags, tag (host memory, read before the call returns; the pointers device memory), each as ng_online_insert's
-// arguments of the same names (its totals and distinct counts left to ng_online_top). -1 on a bad level.
-extern "C" int ng_online_insert_levels(const u16* tok, int nlv, const i64* lv, void* stream) {
+// arguments of the same names (its totals and distinct counts left to ng_online_top). count_pairs 0: only the context
+// is found or inserted and the event written; each distinct pair is then counted once by ng_online_top (add_counts 1)
+// instead of one global atomic per occurrence. -1 on a bad level.
+extern "C" int ng_online_insert_levels(const u16* tok, int nlv, const i64* lv, int count_pairs, void* stream) {
     if (nlv < 1 || nlv > ONLINE_MAXL || !lv) return -1;
     OInsArgs a{};
     i64 mmax = 0;
@@ -536,7 +578,8 @@ extern "C" int ng_online_insert_levels(const u16* tok, int nlv, const i64* lv, v
         mmax = m > mmax ? m : mmax;
     }
     if (mmax == 0) return 0;
-    online_insert_levels_k<<<dim3((unsigned)grid_for(mmax, 256), (unsigned)nlv), 256, 0, (hipStream_t)stream>>>(tok, nlv, a);
+    online_insert_levels_k<<<dim3((unsigned)grid_for(mmax, 256), (unsigned)nlv), 256, 0, (hipStream_t)stream>>>(
+        tok, nlv, a, count_pairs != 0);
     return (int)hipGetLastError();
 }
 
@@ -560,15 +603,17 @@ extern "C" int ng_online_query_levels(const u16* tok, const int* avail, const un
 
 // A step's distinct touched pairs of every level at once, uk[0..*n) (sorted tagged keys: level t's pair keys | t <<
 // tshift; agg: their occurrences in the step), merged into their contexts' totals, distinct counts and, where the
-// level keeps them, top-E lists; desc[t * 6 ...] describes level t (OLevel: pair keys, counts, capacity, top lists or
-// 0, totals, distinct counts; device memory), ntag levels. score: scratch [m].
+// level keeps them, top-E lists; desc[t * 7 ...] describes level t (OLevel: pair keys, counts, capacity, top lists or
+// 0, totals, distinct counts, flags; device memory), ntag levels. score: scratch [m]. add_counts: the pairs' counts
+// grow here by agg (pairs inserted as needed; a full table sets the level's flags[0] bit 0), after inserts made with
+// count_pairs 0; else the inserts counted them.
 extern "C" int ng_online_top(const u64* uk, const i64* n, i64 m, const u32* agg, const i64* desc, int ntag, int tshift,
-                             u64* score, int E, void* stream) {
+                             u64* score, int E, int add_counts, void* stream) {
     if (E < 1 || E > 8 || ntag < 1 || tshift < 17 || tshift > 63 || (tshift + 64 - __builtin_clzll((u64)ntag)) > 64)
         return -1;
     if (m <= 0) return 0;
     hipStream_t st = (hipStream_t)stream;
-    online_scores_k<<<grid_for(m, 256), 256, 0, st>>>(uk, n, m, desc, tshift, score);
+    online_scores_k<<<grid_for(m, 256), 256, 0, st>>>(uk, agg, n, m, desc, tshift, add_counts != 0, score);
     const i64 wins = (m + WAVE - 1) / WAVE;
     online_top_k<<<(unsigned)(wins < 262144 ? wins : 262144), WAVE, 0, st>>>(uk, score, agg, n, m, desc, tshift, E);
     return (int)hipGetLastError();

@@ -237,7 +237,8 @@ class OnlineRows:
         desc = []
         for k, lv in st["levels"].items():
             desc += [lv["pk"].data_ptr(), lv["pcnt"].data_ptr(), lv["pcap"],
-                     lv["top"].data_ptr() if k in levels else 0, lv["tot"].data_ptr(), lv["dist"].data_ptr()]
+                     lv["top"].data_ptr() if k in levels else 0, lv["tot"].data_ptr(), lv["dist"].data_ptr(),
+                     lv["flags"].data_ptr()]
         st["top_desc"] = torch.tensor(desc, dtype=torch.int64, device=dev)
         per_step = np.zeros(1, np.int64)
         for lv in st["levels"].values():
@@ -279,19 +280,20 @@ class OnlineRows:
             a, b = self._range(lv["alpha"], s, s + 1)
             if b == a:
                 continue
-            # the totals and distinct counts are added per context by the sorted pass (ng_online_top), not per
-            # occurrence: hot contexts would make chains of same-address atomics
+            # the pair counts, totals and distinct counts are added per distinct pair and per context by the sorted
+            # pass (ng_online_top), not per occurrence: no global atomic per occurrence, no chains of same-address
+            # atomics on hot contexts
             ins.append((_ptr(lv["occ"], a), b - a, k, _ptr(lv["ck"]), lv["ccap"], _ptr(lv["pk"]), _ptr(lv["pcnt"]),
                         lv["pcap"], _ptr(st["ev"], m), _ptr(lv["flags"]), t << st["tshift"]))
             m += b - a
         for j in range(0, len(ins), MAX_LAUNCH_LEVELS):  # every level's inserts in one launch
             part = ins[j : j + MAX_LAUNCH_LEVELS]
-            lib("ng_online_insert_levels", self.tok, i32(len(part)), _i64_array(part))
+            lib("ng_online_insert_levels", self.tok, i32(len(part)), _i64_array(part), i32(0))
         if m:
             lib.cub("sort_pairs", st["ev"], st["ev_sorted"], None, None, m, i32(0), i32(st["tshift"] + st["tag_bits"]))
             lib.cub("reduce_by_key", st["ev_sorted"], st["uk"], None, st["agg"], st["nruns"], m)  # run lengths
             lib("ng_online_top", st["uk"], st["nruns"], m, st["agg"], st["top_desc"], i32(len(st["levels"])),
-                i32(st["tshift"]), st["score"], i32(E))
+                i32(st["tshift"]), st["score"], i32(E), i32(1))
         qa, qb = self._range(st["q_step"], s, s + 1)
         mq = qb - qa
         if mq == 0 or not queries:
