@@ -492,18 +492,21 @@ def main() -> None:
     modes: dict[int, int] = {}
     t0 = time.perf_counter()
     t_last = t0
+    step_events = []  # each step's launch events, read after the clock stops
     for step in range(args.steps):
         out = cb.counts(x, tgt, avail)
-        torch.cuda.synchronize()  # (the step's events are read below: the step's launches have completed)
+        torch.cuda.synchronize()
         now = time.perf_counter()
         log(f"step {step}: {1e3 * (now - t_last):.1f} ms")
         t_last = now
-        for name, k, n, e0, e1, mode in cb.kernel_events:
+        step_events.append(cb.kernel_events)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    for events in step_events:
+        for name, k, n, e0, e1, mode in events:
             per_kernel[(name, k)] = per_kernel.get((name, k), 0.0) + e0.elapsed_time(e1)
             if name == "scan_emit":
                 modes[k] = mode
-    torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
     ms = dt / args.steps * 1e3
     hits = {k: info[k]["hits"] for k in cfg.levels}
     # positions each level's scan probes (the gate's set positions: the previous level's hits, under the prefix rule

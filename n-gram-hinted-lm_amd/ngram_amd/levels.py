@@ -33,7 +33,7 @@ import torch
 
 from . import partcount
 from .lib import Lib, i32, u64
-from .partcount import count_events, emit_region, summarize
+from .partcount import check_summary, count_events, emit_region, summarize
 from .qindex import QueryIndex
 
 SCAN_BLOCKS_PER_CU = 8  # level-scan blocks (grid-stride) per compute unit (c3 sweep: 8 fastest of 4-32)
@@ -120,6 +120,7 @@ class LevelBuild:
         n_reg = max(len(self.sizes) * G * R, G * emit_region(span, G), G * (-(-max(span, 1) // (G * 256)) * 256))
         regions = torch.empty(n_reg, dtype=torch.int64, device=dev)
         out = res.counts
+        deferred = []  # summarize's checks, read once after every level
         for li, k in enumerate(self.levels):
             t0 = time.perf_counter()
             prev = self.levels[li - 1] if li else None
@@ -144,9 +145,11 @@ class LevelBuild:
                 raise RuntimeError(f"k={k}: more large counts than the escape table holds")
             try:
                 sm = summarize(elib, elib, c, vi.ids, ktop, False, ev_fn,
-                               deep_min=cnt_top if cnt_top is not None else None)
+                               deep_min=cnt_top if cnt_top is not None else None, defer=True)
             except RuntimeError as e:
                 raise RuntimeError(f"k={k}: {e}") from None
+            if sm.stat is not None:  # checked once after the last level: no host read per level
+                deferred.append((f"k={k}", sm.stat))
             thr = None
             if cnt_top is not None and sm.deep.numel():
                 thr = torch.zeros(vi.ids, dtype=torch.int64, device=dev)
@@ -169,6 +172,7 @@ class LevelBuild:
             self.host_s["count"] += t3 - t2
             del vi, c, sm, thr, seen
         del regions
+        check_summary(deferred)
         if stats:
             for li, k in enumerate(self.levels):
                 h = int(self._popcount(bms[k]))

@@ -247,22 +247,26 @@ RECORD_WORDS = {1: 4, 2: 8, 4: 8, 8: 16}  # u32 words of a context record for to
 @dataclass
 class Summary:
     """ng_ctx_summary's outputs: records (int32 [n_ids, RECORD_WORDS[ktop]]), pair counts per context (int32 [n_ids],
-    or None), the sorted words, the number of present contexts, the contexts of more than deep_min pairs (int64)."""
+    or None), the sorted words, the number of present contexts, the contexts of more than deep_min pairs (int64).
+    Deferred (summarize's defer): contexts is -1 and `stat` holds the kernel's statistics and flags for check_summary."""
 
     rec: torch.Tensor
     dist: torch.Tensor | None
     words: torch.Tensor
     contexts: int
     deep: torch.Tensor | None
+    stat: torch.Tensor | None = None
 
 
 def summarize(elib: Lib, lib: Lib, c: Counted, n_ids: int, ktop: int, zero_records: bool = False, event=_no_event,
-              by_pair: bool = False, with_dist: bool = True, deep_min: int | None = None) -> Summary:
+              by_pair: bool = False, with_dist: bool = True, deep_min: int | None = None,
+              defer: bool = False) -> Summary:
     """Per present context (of packed pairs): its record (total, pairs, the first ktop tokens two per word, their
     counts; for ktop 2 and 8 also its first word's index in the sorted words) and, with_dist, its pair count (0 for
     absent contexts). The words are sorted by context, or with by_pair by pair key. The records of absent contexts are
     zeros only with zero_records. With deep_min: the contexts of more than deep_min pairs. Raises if a total reaches
-    2^32."""
+    2^32. `defer` (without deep_min): no host sync here; the caller passes the Summary to check_summary before it uses
+    any output (a host read per level costs the GPU an idle gap)."""
     dev = c.pairs.device
     lo = 64 - c.cb - (16 if by_pair else 0)  # the sort's bit range [lo, 64)
     first = lo + c.presort_bits if c.presorted == lo else lo  # count_events' scatter did the bits below `first`
@@ -285,12 +289,25 @@ def summarize(elib: Lib, lib: Lib, c: Counted, n_ids: int, ktop: int, zero_recor
     elib("ng_ctx_summary", sw, c.U, i32(c.cb), c.esc[0], c.esc[1], u64(ESC_CAP), i32(ktop), rec, dist,
          ctypes.c_uint32(deep_min or 0), deep, nstat, flags)
     e1.record()
+    if defer and deep is None:
+        return Summary(rec, dist, sw, -1, None, nstat)
     st = nstat.cpu()
     if int(st[257]) & 4:
         raise RuntimeError("a total does not fit uint32")
     if deep is not None:
         deep = deep[: int(st[0])]
     return Summary(rec, dist, sw, int(st[1:257].sum()), deep)
+
+
+def check_summary(stats: list) -> None:
+    """The deferred checks of summarize(defer=True) calls, one host read for all: (name, Summary.stat) pairs; raises
+    RuntimeError(f"{name}: a total does not fit uint32") for the first that overflowed."""
+    if not stats:
+        return
+    flags = torch.stack([st[257] for _, st in stats]).cpu().tolist()
+    for (name, _), f in zip(stats, flags):
+        if f & 4:
+            raise RuntimeError(f"{name}: a total does not fit uint32")
 
 
 def record_tops(rec: torch.Tensor, ktop: int):
