@@ -177,7 +177,7 @@ __global__ void __launch_bounds__(256) scan_dense_k(const u16* __restrict__ tok,
     const i64 stride = (i64)gridDim.x * (blockDim.x / WAVE) * span;
     for (i64 base = (blockIdx.x * (i64)(blockDim.x / WAVE) + threadIdx.x / WAVE) * span; base < L; base += stride) {
         const bool full = sink_full<S>(flags);
-        Walk wk[DENSE_PPL];
+        Walk2 wk[DENSE_PPL];
 #pragma unroll
         for (int q = 0; q < DENSE_PPL; ++q) {
             const i64 p = base + q * WAVE + lane;
@@ -192,13 +192,13 @@ __global__ void __launch_bounds__(256) scan_dense_k(const u16* __restrict__ tok,
             wk[q].next = nxt;
         }
 #pragma unroll
-        for (int q = 0; q < DENSE_PPL; ++q) walk_seed(vt, vcap, wk[q].key, wk[q].next, wk[q]);
+        for (int q = 0; q < DENSE_PPL; ++q) walk_seed2(vt, vcap, wk[q].key, wk[q].next, wk[q]);
 #pragma unroll
         for (int q = 0; q < DENSE_PPL; ++q) {
             const i64 p0 = base + q * WAVE;
             if (p0 >= L) break;  // wave-uniform
             const i64 p = p0 + lane;
-            const u64 key = walk_end<K, false>(tok, p, k, vt, vrep, x, flags, wk[q]);
+            const u64 key = walk_end2<K>(tok, p, k, vt, vrep, x, flags, wk[q]);
             const bool hit = key != EMPTY;
             const u64 b = __ballot(hit);
             const i64 w = (p0 >> 5) + 1;
@@ -229,7 +229,7 @@ __global__ void __launch_bounds__(256) scan_list_k(const u16* __restrict__ tok, 
         u64 key = EMPTY;
         if (j < n) {
             p = (i64)plist[j];
-            key = walk_lookup<K, false>(tok, p, k, vt, vcap, vrep, x, flags);
+            key = walk_lookup2<K>(tok, p, k, vt, vcap, vrep, x, flags);
         }
         const bool hit = key != EMPTY;
         if (bm_out && hit) atomicOr(&bm_out[p >> 5], 1u << (p & 31));
@@ -257,7 +257,7 @@ __global__ void __launch_bounds__(256) scan_sparse_k(const u16* __restrict__ tok
             word &= word - 1;
             const i64 p = (w << 5) + b;
             if (p >= L) continue;
-            const u64 key = walk_lookup<K, false>(tok, p, k, vt, vcap, vrep, x, flags);
+            const u64 key = walk_lookup2<K>(tok, p, k, vt, vcap, vrep, x, flags);
             if (key != EMPTY) {
                 out |= 1u << b;
                 if constexpr (S::KIND == 2) emit_lane(sink, &ss, key, p, flags);
@@ -311,7 +311,7 @@ __global__ void __launch_bounds__(256) scan_compact_k(const u16* __restrict__ to
         const i64 pbase = (g0 + w * 64) << 5;
         for (u32 r0 = 0; r0 < total; r0 += WAVE * COMPACT_PPL) {  // every lane runs the same rounds
             // COMPACT_PPL probes per lane started together: their first loads are in flight at once
-            Walk wk[COMPACT_PPL];
+            Walk2 wk[COMPACT_PPL];
             u32 lp[COMPACT_PPL];
 #pragma unroll
             for (int q = 0; q < COMPACT_PPL; ++q) {
@@ -320,13 +320,13 @@ __global__ void __launch_bounds__(256) scan_compact_k(const u16* __restrict__ to
                 lp[q] = 0;
                 if (r < total) {
                     lp[q] = list[w][r];
-                    if (pbase + lp[q] < L) walk_begin<K>(tok, pbase + lp[q], k, vt, vcap, wk[q]);
+                    if (pbase + lp[q] < L) walk_begin2<K>(tok, pbase + lp[q], k, vt, vcap, wk[q]);
                 }
             }
 #pragma unroll
             for (int q = 0; q < COMPACT_PPL; ++q) {
                 if (r0 + q * WAVE >= total) break;  // wave-uniform
-                const u64 hk = walk_end<K, false>(tok, pbase + lp[q], k, vt, vrep, x, flags, wk[q]);
+                const u64 hk = walk_end2<K>(tok, pbase + lp[q], k, vt, vrep, x, flags, wk[q]);
                 const bool hit = hk != EMPTY;
                 if (hit) atomicOr(&words[w][lp[q] >> 5], 1u << (lp[q] & 31));
                 if constexpr (S::KIND == 2)

@@ -111,3 +111,71 @@ __device__ __forceinline__ void walk_seed(const u64* __restrict__ vt, u64 vcap, 
     w.slot = __umul64hi(key, vcap);
     w.seen = vt[w.slot];
 }
+
+// Lookups that load the home slot and the one after it together (the engine's scans). At load 0.4 a walk ends within
+// those two slots for about 93% of hits and 84% of misses, so most lookups wait for one round trip instead of a chain
+// of dependent slot loads. The table must hold at least one slot past vcap (an engine query table has TAIL of them:
+// the home slot is below vcap, so slot + 1 is always inside it).
+struct Walk2 {
+    u64 key;
+    u64 slot;
+    u64 seen;
+    u64 seen2;
+    u32 next;
+};
+
+__device__ __forceinline__ void walk_seed2(const u64* __restrict__ vt, u64 vcap, u64 key, u32 next, Walk2& w) {
+    w.key = key;
+    w.next = next;
+    if (key == EMPTY) return;
+    w.slot = __umul64hi(key, vcap);
+    w.seen = vt[w.slot];
+    w.seen2 = vt[w.slot + 1];
+}
+
+template <int K>
+__device__ __forceinline__ void walk_begin2(const u16* __restrict__ tok, i64 p, int k, const u64* __restrict__ vt,
+                                            u64 vcap, Walk2& w) {
+    u32 next;
+    const u64 key = ctx_key_at<K>(tok, p, k, next);
+    walk_seed2(vt, vcap, next == SENT ? EMPTY : key, next, w);
+}
+
+// The pair key (id << 16 | next) of a verified hit, else EMPTY; the same result as walk_end on the same table.
+template <int K>
+__device__ __forceinline__ u64 walk_end2(const u16* __restrict__ tok, i64 p, int k, const u64* __restrict__ vt,
+                                         const u32* __restrict__ vrep, const u16* __restrict__ x, u32* flags,
+                                         Walk2& w) {
+    if (w.key == EMPTY) return EMPTY;
+    if (w.seen == w.key) {
+    } else if (w.seen == EMPTY) {
+        return EMPTY;
+    } else if (w.seen2 == w.key) {
+        ++w.slot;
+    } else if (w.seen2 == EMPTY) {
+        return EMPTY;
+    } else {
+        w.slot += 2;
+        for (;;) {
+            const u64 seen = vt[w.slot];
+            if (seen == w.key) break;
+            if (seen == EMPTY) return EMPTY;
+            ++w.slot;
+        }
+    }
+    const int kk = ctx_len<K>(k);
+    if (kk > 4 && !same_tokens_rt(tok + p, x + (i64)vrep[w.slot] + 1, kk)) {
+        atomicAdd(&flags[1], 1u);
+        return EMPTY;
+    }
+    return (w.slot << 16) | w.next;
+}
+
+template <int K>
+__device__ __forceinline__ u64 walk_lookup2(const u16* __restrict__ tok, i64 p, int k, const u64* __restrict__ vt,
+                                            u64 vcap, const u32* __restrict__ vrep, const u16* __restrict__ x,
+                                            u32* flags) {
+    Walk2 w;
+    walk_begin2<K>(tok, p, k, vt, vcap, w);
+    return walk_end2<K>(tok, p, k, vt, vrep, x, flags, w);
+}
