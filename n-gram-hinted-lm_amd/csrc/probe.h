@@ -112,9 +112,9 @@ __device__ __forceinline__ void walk_seed(const u64* __restrict__ vt, u64 vcap, 
     w.seen = vt[w.slot];
 }
 
-// Lookups that load the home slot and the one after it together (the engine's scans). At load 0.4 a walk ends within
-// those two slots for about 93% of hits and 84% of misses, so most lookups wait for one round trip instead of a chain
-// of dependent slot loads. The table must hold at least one slot past vcap (an engine query table has TAIL of them:
+// Lookups that load the home slot and the one after it together (the engine's scans). At the query tables' load most
+// walks end within those two slots (a miss does whenever either is empty), so most lookups wait for one round trip
+// instead of a chain of dependent slot loads (c3: the level-2 and level-3 scans 8-11% faster). The table must hold at least one slot past vcap (an engine query table has TAIL of them:
 // the home slot is below vcap, so slot + 1 is always inside it).
 struct Walk2 {
     u64 key;

@@ -13,7 +13,8 @@ import torch
 from .lib import Lib, i32, u64
 
 TAIL = 4096  # slots past cap that linear probing may run into; the last stays empty
-LOAD = 0.4  # contexts per slot aimed at: measured at c3, 0.4 gives the fastest scans (0.5 +10%, 0.66 +50%)
+LOAD = 0.3  # contexts per slot aimed at: at c3 with the scans' two-slot lookups 0.25-0.35 are fastest (0.4 +2%,
+# 0.5 +7%, 0.6 +16% per step): a shorter walk matters more than a smaller table
 SHRINK = 2.0  # a table more than this many times the size its contexts need moves to one of that size
 EXPECT_MARGIN = 1.2  # a table sized from an expected context count holds this many times it at LOAD (1 at least)
 
