@@ -102,7 +102,9 @@ int gen_copies(uint16_t* out, const ng_i64* copies, ng_i64 m, const uint16_t* sr
  * (ngram_amd.counts / count_table / online / longest / exact_match), the query-filtered counting of
  * record_367_gpu_counts/track_1_short/counts/build.py, exact_match/src/count_table.rs, online.rs and kgram.rs with
  * split pair tables (u64 pair keys and u32 counts in two arrays) and selection-based ranking. Same conventions as
- * above. k: 1..64.
+ * above. k: 1..64. A query table (vt, vcap, vrep) passed to an engine scan is an ng_query_index table: linear probing
+ * without wrap-around from umulhi(key, vcap), and at least one slot past vcap (ng_query_index's callers give 4096),
+ * since a lookup loads the home slot and the next one together.
  * ------------------------------------------------------------------------------------------------------------ */
 
 /* one level's scan counted in a split table (keys EMPTY-filled, cnts zeroed); sparse 0: a lane per position, 1: a
