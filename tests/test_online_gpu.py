@@ -174,3 +174,70 @@ def test_errors(stream):
     with pytest.raises(ValueError):
         rows.hints([7], BUCKETS, 8, 0, 1, np.zeros(n, np.int16), np.zeros((n, 8), np.uint16),
                    np.zeros((n, 8), np.uint16))
+
+
+class _PerLevelRows(OnlineRows):
+    """OnlineRows whose steps use the single-level entry points: ng_online_insert per level (pairs counted per
+    occurrence), ng_online_top without add_counts, ng_online_query per level. The same outputs are expected."""
+
+    def _step(self, st, s, outs, queries=True):
+        from ngram_amd.lib import i32, u64
+
+        lib = self.lib
+        levels, buckets, entries, count_levels = outs["cfg"]
+        m = 0
+        for t, (k, lv) in enumerate(st["levels"].items()):
+            a, b = self._range(lv["alpha"], s, s + 1)
+            if b == a:
+                continue
+            lib("ng_online_insert", self.tok, lv["occ"][a:b], b - a, i32(k), lv["ck"], u64(lv["ccap"]), lv["pk"],
+                lv["pcnt"], u64(lv["pcap"]), None, None, st["ev"][m:], lv["flags"], u64(t << st["tshift"]))
+            m += b - a
+        if m:
+            lib.cub("sort_pairs", st["ev"], st["ev_sorted"], None, None, m, i32(0), i32(st["tshift"] + st["tag_bits"]))
+            lib.cub("reduce_by_key", st["ev_sorted"], st["uk"], None, st["agg"], st["nruns"], m)
+            lib("ng_online_top", st["uk"], st["nruns"], m, st["agg"], st["top_desc"], i32(len(st["levels"])),
+                i32(st["tshift"]), st["score"], i32(st["E"]), i32(0))
+        qa, qb = self._range(st["q_step"], s, s + 1)
+        if qb == qa or not queries:
+            return
+        qpos = st["q_pos"][qa:qb]
+        for ci, k in enumerate(count_levels):
+            lv = st["levels"][k]
+            lib("ng_online_query", self.tok, self.avail, self.has_next, qpos, qb - qa, i32(k), lv["ck"],
+                u64(lv["ccap"]), lv["pk"], lv["pcnt"], u64(lv["pcap"]), lv["tot"], lv["dist"],
+                st["qslot"][k] if k in levels else None, outs["tot"], outs["dist"], outs["cnt"], i32(len(count_levels)),
+                i32(ci))
+        for k in levels:
+            if k not in count_levels:
+                lv = st["levels"][k]
+                lib("ng_online_query", self.tok, self.avail, self.has_next, qpos, qb - qa, i32(k), lv["ck"],
+                    u64(lv["ccap"]), lv["pk"], lv["pcnt"], u64(lv["pcap"]), lv["tot"], lv["dist"], st["qslot"][k],
+                    None, None, None, i32(1), i32(0))
+        if levels:
+            lib("ng_online_rows", qpos, qb - qa, i32(len(levels)), st["rows_desc"], i32(st["E"]), i32(outs["slots"]),
+                outs["cell"], outs["next"], outs["weights"], outs["level"], st["hinted"])
+
+
+@pytest.mark.parametrize("how", ["per_level", "chunks_of_3"])
+def test_step_entry_points_agree(stream, monkeypatch, how):
+    """The single-level entry points (pairs counted per occurrence), and the fused launches split in chunks of three
+    levels, give the oracle's rows, as the default path does (test_advance_step_by_step)."""
+    from ngram_amd import online as on
+
+    tok, spans = stream
+    n = len(tok)
+    bounds = [0, n]
+    tau, tau_in = O.spans_tau(n, bounds, spans)
+    count_levels = [2, 4, 6]
+    want = O.online(tok, bounds, tau, tau_in, LEVELS, BUCKETS, 8, count_levels, 0, len(spans))
+    if how == "per_level":
+        rows = _PerLevelRows(tok, bounds, spans, 4, [])
+    else:
+        monkeypatch.setattr(on, "MAX_LAUNCH_LEVELS", 3)
+        rows = OnlineRows(tok, bounds, spans, 4, [])
+    got = _empty(n, 8, len(count_levels))
+    hinted = rows.advance(len(spans), LEVELS, BUCKETS, 8, count_levels, *got)
+    for g, w, name in zip(got, want, ("cell", "next", "weights", "tot", "dist", "cnt")):
+        assert np.array_equal(g, w), name
+    assert hinted == want[-1]
