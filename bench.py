@@ -545,6 +545,10 @@ def main() -> None:
         "roofline": {"bound": "hbm", "kernel": f"scan_emit k={dom} (ng_scan_emit, mode {modes.get(dom, 0)})",
                      **roof(scan_bytes[dom], scan_ms[dom]), "traffic": traffic,
                      "traffic_source": None if traffic is None else f"profiles/scan_traffic_c3.json @ {traffic_commit}",
+                     # the line traffic the kernel really moves (FETCH_SIZE x 2 + WRITE_SIZE of the same launch, from
+                     # the profile) over its time here: a random 8-byte probe costs a 128-byte line beyond L2
+                     "traffic_GBps": None if traffic is None else traffic / (scan_ms[dom] / 1e3) / 1e9,
+                     "traffic_frac": None if traffic is None else traffic / (scan_ms[dom] / 1e3) / 1e9 / HBM_PEAK_GBS,
                      "algorithmic_bytes_per_launch": scan_bytes[dom], "avg_launch_ms": scan_ms[dom],
                      "positions_read": read[dom], "hits_emitted": hits[dom],
                      "bytes_per_position_read": 2, "bytes_per_hit": 8},
