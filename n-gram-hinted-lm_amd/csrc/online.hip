@@ -130,8 +130,9 @@ __global__ void online_insert_k(const u16* __restrict__ tok, const int* __restri
     if (i < m) insert_one<K>(tok, pos, i, k, ck, ccap, pk, pcnt, pcap, ctx_tot, ctx_dist, ev, flags, tag);
 }
 
-// Every level's inserts of a step in one launch: a step's levels each wait on a chain of dependent table round trips
-// (context, then pair), so one launch per level paid that latency once per level (c4: 60-90 us each). Level t takes
+// Every level's inserts of a step in one launch: each level's inserts are chains of dependent table round trips, and
+// in one launch the levels' chains overlap (c4, inserts counting pairs: five launches 409 us per step, one 322 us;
+// with the pairs counted in the step's merge instead, 110 us). Level t takes
 // the blocks with blockIdx.y == t; its fields (ONLINE_INS_FIELDS i64 each, as ng_online_insert_levels documents) are
 // picked by unrolled compares on that block-uniform index, so no kernel argument is indexed at run time.
 #define ONLINE_MAXL 8
