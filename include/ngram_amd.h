@@ -216,9 +216,11 @@ int ng_part_bounds(const ng_u64* ev, ng_i64 n, int pbits, int msd, ng_i64* start
 /* a sort's first pass from segments: nseg segments of ev_count[s] keys at src + (bases ? bases[s] : s * R) scattered
  * by the nbits-bit digit (key >> shift) & (2^nbits - 1), nbits <= 11, to out at dpre (u32 [2^nbits * nseg], the
  * exclusive scan of the producer's digit histograms, digit-major: ng_scan_emit's with shift 56 and 8 bits,
- * ng_part_count's; fewer than 2^32 keys); the order within a digit is free */
+ * ng_part_count's; fewer than 2^32 keys); the order within a digit is free. out holds cap keys: a key whose place is
+ * cap or beyond is dropped, and a region segment (bases NULL) is read up to R keys, so the call may be made before the
+ * host has read the totals */
 int ng_seg_scatter(const ng_u64* src, ng_u64 R, const ng_i64* bases, const uint32_t* ev_count, const uint32_t* dpre,
-                   ng_i64 nseg, int shift, int nbits, ng_u64* out, void* stream);
+                   ng_i64 nseg, int shift, int nbits, ng_u64* out, ng_u64 cap, void* stream);
 /* exclusive prefix sum of n u32 (out may alias in), *total (may be NULL) the sum; CUB-style two-phase temp storage */
 int ng_exclusive_scan_u32(void* temp, size_t* temp_bytes, const uint32_t* in, uint32_t* out, ng_i64 n,
                           ng_u64* total, void* stream);

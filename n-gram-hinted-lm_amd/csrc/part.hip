@@ -89,7 +89,9 @@ __global__ void part_bounds_k(const u64* __restrict__ ev, i64 n, int pbits, int 
 // segment s starting at out + dpre[d * nseg + s] (the exclusive scan of the producer's per-segment digit histograms,
 // digit-major). The order within a digit is free (the passes after this one are stable): a chunk of 8192 keys is
 // ranked by LDS counters, staged in LDS by digit and written as per-digit runs. Replaces packing the segments into
-// one array and a radix pass over it.
+// one array and a radix pass over it. A region segment is read up to R keys, and keys whose place is cap or beyond are
+// dropped, so a launch made before its host has checked the totals (a region overflow, a 32-bit wrap) stays inside
+// out and the regions.
 #define SS_BLOCK 1024
 #define SS_ITEMS 8
 #define SS_CHUNK (SS_BLOCK * SS_ITEMS)
@@ -98,13 +100,14 @@ template <int BMAX>  // the digit arrays' size: 256 keeps two blocks per CU in L
 __global__ void __launch_bounds__(SS_BLOCK) seg_scatter_k(const u64* __restrict__ src, u64 R,
                                                          const i64* __restrict__ bases,
                                                          const u32* __restrict__ ev_count, const u32* __restrict__ dpre,
-                                                         i64 nseg, int shift, int nbits, u64* __restrict__ out) {
+                                                         i64 nseg, int shift, int nbits, u64* __restrict__ out,
+                                                         u64 cap) {
     __shared__ u64 stage[SS_CHUNK];
     __shared__ u32 cnt[BMAX], pre[BMAX], base[BMAX], wt[SS_BLOCK / WAVE];
     const int t = threadIdx.x, lane = lane_id(), wid = t / WAVE;
     const u32 B = 1u << nbits, mask = B - 1u;
     for (i64 sg = blockIdx.x; sg < nseg; sg += gridDim.x) {
-        const u32 n = ev_count[sg];
+        const u32 n = !bases && (u64)ev_count[sg] > R ? (u32)R : ev_count[sg];
         const u64* in = src + (bases ? (u64)bases[sg] : (u64)sg * R);
         for (u32 d = t; d < B; d += SS_BLOCK) base[d] = dpre[(i64)d * nseg + sg];
         for (u32 c0 = 0; c0 < n; c0 += SS_CHUNK) {
@@ -150,7 +153,8 @@ __global__ void __launch_bounds__(SS_BLOCK) seg_scatter_k(const u64* __restrict_
             for (u32 i = t; i < m; i += SS_BLOCK) {
                 const u64 k = stage[i];
                 const u32 d = (u32)(k >> shift) & mask;
-                out[(u64)base[d] + i - pre[d]] = k;
+                const u64 at = (u64)base[d] + i - pre[d];
+                if (at < cap) out[at] = k;
             }
             __syncthreads();
             for (u32 d = t; d < B; d += SS_BLOCK) base[d] += cnt[d];
@@ -694,7 +698,7 @@ extern "C" int ng_exclusive_scan_u32(void* temp, size_t* temp_bytes, const u32* 
 // (u32 [2^nbits * nseg], the exclusive scan of the producer's digit histograms, digit-major: ng_scan_emit's with
 // shift 56 and 8 bits, ng_part_count's; fewer than 2^32 keys).
 extern "C" int ng_seg_scatter(const u64* src, u64 R, const i64* bases, const u32* ev_count, const u32* dpre, i64 nseg,
-                              int shift, int nbits, u64* out, void* stream) {
+                              int shift, int nbits, u64* out, u64 cap, void* stream) {
     if (nseg < 0 || nbits < 1 || nbits > 11 || shift < 0 || shift + nbits > 64 ||
         (bases == nullptr && (R == 0 || R > 0xFFFFFFFFull)))
         return -1;
@@ -702,10 +706,10 @@ extern "C" int ng_seg_scatter(const u64* src, u64 R, const i64* bases, const u32
     const i64 g = nseg < 16384 ? nseg : 16384;
     if (nbits <= 8)
         seg_scatter_k<256><<<(unsigned)g, SS_BLOCK, 0, (hipStream_t)stream>>>(src, R, bases, ev_count, dpre, nseg, shift,
-                                                                            nbits, out);
+                                                                            nbits, out, cap);
     else
         seg_scatter_k<SS_MAXB><<<(unsigned)g, SS_BLOCK, 0, (hipStream_t)stream>>>(src, R, bases, ev_count, dpre, nseg,
-                                                                                shift, nbits, out);
+                                                                                shift, nbits, out, cap);
     return (int)hipGetLastError();
 }
 

@@ -46,6 +46,21 @@ def _no_event(name: str, n: int):
     return _E(), _E()
 
 
+class _HostRead:
+    """A small device tensor copied to pinned host memory without a wait: the launches enqueued after it keep the GPU
+    busy while the host waits for this copy alone (get), instead of the GPU idling until the host's next launch."""
+
+    def __init__(self, t: torch.Tensor):
+        self.host = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+        self.host.copy_(t, non_blocking=True)
+        self.ready = torch.cuda.Event()
+        self.ready.record()
+
+    def get(self) -> list:
+        self.ready.synchronize()
+        return self.host.tolist()
+
+
 def pack_events(elib: Lib, regions: torch.Tensor, R: int, ev_count: torch.Tensor, nseg: int, event=_no_event):
     """The regions' events (segment s = ev_count[s] items at s * R) packed into one array: (events, n)."""
     dev = regions.device
@@ -110,20 +125,22 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids:
         elib.cub("ng_exclusive_scan_u32", dhist, dpre, 256 * nseg, small[:1])
         if emit_flags is not None:
             small[1:].copy_(emit_flags[:1])
-        n_ev, fl = small.cpu().tolist()
+        read = _HostRead(small)
+        # the first partition pass, launched before the host reads the total so that the GPU works while the host
+        # waits: its output holds every region's capacity and the scatter drops anything placed beyond it, so an
+        # overflowed region or a wrapped total, raised below, writes nothing out of bounds
+        cap = nseg * R
+        ev = torch.empty(max(cap, 1), dtype=torch.int64, device=dev)
+        e0, e1 = event("partition", cap)
+        e0.record()
+        elib("ng_seg_scatter", regions, u64(R), None, ev_count, dpre, nseg, i32(56), i32(8), ev, u64(cap))
+        e1.record()
+        msd = 1
+        n_ev, fl = read.get()
         if fl & 4:
             raise RuntimeError("an emit region overflowed")
         if n_ev >= 1 << 32:
             raise RuntimeError(f"{n_ev} events: the region scatter's offsets are 32-bit")
-        if n_ev < SEG_MIN_EVENTS * nseg:  # few events per region: packing them costs less than scattering per region
-            ev, _ = pack_events(elib, regions, R, ev_count, nseg, event)
-        else:
-            ev = torch.empty(max(n_ev, 1), dtype=torch.int64, device=dev)
-            e0, e1 = event("partition", n_ev)
-            e0.record()
-            elib("ng_seg_scatter", regions, u64(R), None, ev_count, dpre, nseg, i32(56), i32(8), ev)
-            e1.record()
-            msd = 1
         del dpre
     dev = ev.device
     cb = max(1, (max(n_ids, 2) - 1).bit_length(), PACK_MIN_BITS) if packed else 0
@@ -212,7 +229,23 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids:
             offs = torch.empty(G2 + 1, dtype=torch.int64, device=dev)
             elib("ng_seg_offsets", seg_cnt, G2, offs)
             small[:1].copy_(offs[G2:])
-        U, fl = small.cpu().tolist()
+        read = _HostRead(small)
+        # the distinct pairs packed before the host reads how many there are (the GPU works while the host waits),
+        # into room for every event, which bounds them; dropped if the count repeats
+        pairs = torch.empty(max(n_ev, 1), dtype=torch.int64, device=dev)
+        counts = None if cb else torch.empty(max(n_ev, 1), dtype=torch.int32, device=dev)
+        if dhist is not None:
+            e0, e1 = event("sort", n_ev)
+            e0.record()
+            elib("ng_seg_scatter", out_k, u64(0), seg_base, seg_cnt, dpre, G2, i32(dshift), i32(dbits), pairs,
+                 u64(pairs.numel()))
+            e1.record()
+        else:
+            e0, e1 = event("count", n_ev)
+            e0.record()
+            elib("ng_seg_gather", out_k, out_c, u64(0), seg_base, seg_cnt, G2, offs, pairs, counts)
+            e1.record()
+        U, fl = read.get()
         fl &= 0xFFFFFFFF
         if fl & 2:  # more large counts than the escape table holds: count again, unpacked
             cb = 0
@@ -223,20 +256,6 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids:
             raise RuntimeError("a partition holds too many distinct pairs at 24 bits")
         pbits += 1
     del ev
-    counts = None
-    if dhist is not None:
-        pairs = torch.empty(max(U, 1), dtype=torch.int64, device=dev)
-        e0, e1 = event("sort", U)
-        e0.record()
-        elib("ng_seg_scatter", out_k, u64(0), seg_base, seg_cnt, dpre, G2, i32(dshift), i32(dbits), pairs)
-        e1.record()
-    else:
-        pairs = torch.empty(max(U, 1), dtype=torch.int64, device=dev)
-        counts = None if cb else torch.empty(max(U, 1), dtype=torch.int32, device=dev)
-        e0, e1 = event("count", U)
-        e0.record()
-        elib("ng_seg_gather", out_k, out_c, u64(0), seg_base, seg_cnt, G2, offs, pairs, counts)
-        e1.record()
     return Counted(pairs, counts, (esc_k, esc_c) if cb else None, qcnt, U, pbits, cb, n_ev, dshift,
                    dbits if dhist is not None else 0)
 
