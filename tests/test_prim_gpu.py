@@ -1,11 +1,12 @@
 """GPU: our device-wide primitives behind the CUB-style ABI calls (sort_pairs, inclusive_max, reduce_by_key) against
-numpy (np.argsort kind="stable", np.maximum.accumulate, run sums) -- pinning the reference's CUB boundary."""
+numpy (np.argsort kind="stable", np.maximum.accumulate, run sums) -- pinning the reference's CUB boundary -- and the
+partition's first pass from segments (ng_seg_scatter: digit ranges, its capacity and region bounds)."""
 
 import numpy as np
 import pytest
 import torch
 
-from ngram_amd.lib import i32
+from ngram_amd.lib import i32, u64
 
 pytestmark = pytest.mark.gpu
 
@@ -80,3 +81,54 @@ def test_reduce_by_key_counting(lib, n, runs):
     assert m == len(u)
     assert np.array_equal(kout[:m].cpu().numpy().view(np.uint64), u)
     assert np.array_equal(vout[:m].cpu().numpy(), counts.astype(np.int32))
+
+
+@pytest.mark.parametrize("nbits", [8, 11])
+def test_seg_scatter_groups_segments_by_digit(lib, nbits):
+    """ng_seg_scatter from region segments: every key lands in its digit's range (the digit-major exclusive scan of the
+    segments' digit histograms), each digit's keys the multiset numpy finds."""
+    rng = np.random.default_rng(nbits)
+    nseg, R = 37, 3000
+    counts = rng.integers(0, R + 1, nseg).astype(np.uint32)
+    counts[3] = 0
+    shift = 64 - nbits
+    keys = rng.integers(0, 1 << 63, (nseg, R), dtype=np.int64).astype(np.uint64) * np.uint64(2) + np.uint64(1)
+    B = 1 << nbits
+    digits = (keys >> np.uint64(shift)).astype(np.int64)
+    hist = np.zeros((B, nseg), np.uint32)
+    for s in range(nseg):
+        np.add.at(hist[:, s], digits[s, : counts[s]], 1)
+    dpre = (np.cumsum(hist.ravel()) - hist.ravel()).astype(np.uint32)
+    n = int(counts.sum())
+    out = torch.full((n + 64,), -1, dtype=torch.int64, device="cuda")
+    regions = torch.from_numpy(keys.view(np.int64).ravel()).cuda()
+    lib("ng_seg_scatter", regions, u64(R), None, torch.from_numpy(counts.view(np.int32)).cuda(),
+        torch.from_numpy(dpre.view(np.int32)).cuda(), nseg, i32(shift), i32(nbits), out, u64(n))
+    got = out.cpu().numpy().view(np.uint64)
+    assert np.all(got[n:] == np.uint64(0xFFFFFFFFFFFFFFFF))  # nothing past n
+    valid = np.concatenate([keys[s, : counts[s]] for s in range(nseg)])
+    start = np.concatenate([np.zeros(1, np.int64), np.cumsum(hist.sum(1)).astype(np.int64)])
+    for d in range(B):
+        a, b = start[d], start[d + 1]
+        assert np.array_equal(np.sort(got[a:b]), np.sort(valid[(valid >> np.uint64(shift)) == d]))
+
+
+def test_seg_scatter_keeps_inside_its_capacity(lib):
+    """A scatter launched before its host has checked the totals: histograms that promise more keys than the segments
+    hold (an overflowed region), and a capacity below the total, write nothing past the capacity and read no region
+    past R keys."""
+    nseg, R, cap = 4, 256, 300
+    keys = (np.arange(nseg * R, dtype=np.uint64) << np.uint64(2)) | np.uint64(1)
+    counts = np.array([R + 500, 10, 0, 200], np.uint32)  # the first region claims more than it holds
+    hist = np.zeros((256, nseg), np.uint32)
+    hist[0, :] = [R + 500, 10, 0, 200]  # every key has digit 0 at shift 56 (the keys are small)
+    dpre = (np.cumsum(hist.ravel()) - hist.ravel()).astype(np.uint32)
+    guard = 4096
+    out = torch.full((cap + guard,), -1, dtype=torch.int64, device="cuda")
+    regions = torch.from_numpy(keys.view(np.int64)).cuda()
+    lib("ng_seg_scatter", regions, u64(R), None, torch.from_numpy(counts.view(np.int32)).cuda(),
+        torch.from_numpy(dpre.view(np.int32)).cuda(), nseg, i32(56), i32(8), out, u64(cap))
+    got = out.cpu().numpy().view(np.uint64)
+    assert np.all(got[cap:] == np.uint64(0xFFFFFFFFFFFFFFFF))
+    # region 0 was read up to R keys: they fill places 0..R-1 (its digit range starts at 0)
+    assert np.array_equal(np.sort(got[:R]), np.sort(keys[:R]))
