@@ -286,6 +286,15 @@ int ng_online_insert(const uint16_t* tok, const int* pos, ng_i64 m, int k, ng_u6
                      ng_u64 tag, void* stream);
 int ng_online_top(const ng_u64* uk, const ng_i64* n, ng_i64 m, const uint32_t* agg, const ng_i64* desc, int ntag,
                   int tshift, ng_u64* score, int E, int add_counts, void* stream);
+/* a step's events ev[0..m) (unsorted, as ng_online_insert_levels writes them with count_pairs 0) merged as
+ * sort_pairs + reduce_by_key + ng_online_top (add_counts 1) merge them, without the sort: the events scattered by the
+ * low 11 bits of their context slot, then a block per bucket counts, sorts and merges its distinct pairs in LDS
+ * (rounds split by a pair hash where a bucket holds more than 4096). desc, ntag, tshift, E: ng_online_top's.
+ * CUB-style two-phase temp storage (temp NULL: *temp_bytes set). -1 where m >= 2^cb - 1 with cb = 64 - tshift -
+ * (tag bits) + 11 (a pair's occurrences must fit the packed words' count bits): the sorted path then applies. No
+ * counterpart in the reference (online.rs merges on the CPU). */
+int ng_online_merge(void* temp, size_t* temp_bytes, const ng_u64* ev, ng_i64 m, const ng_i64* desc, int ntag,
+                    int tshift, int E, void* stream);
 int ng_online_query(const uint16_t* tok, const int* avail, const unsigned char* has_next, const int* pos, ng_i64 m,
                     int k, const ng_u64* ck, ng_u64 ccap, const ng_u64* pk, const uint32_t* pcnt, ng_u64 pcap,
                     const uint32_t* ctx_tot, const uint32_t* ctx_dist, int* qslot, uint32_t* tot, uint16_t* dist,

@@ -7,6 +7,7 @@
 // before s). The top-E lists stay exact: a step's touched pairs are sorted and merged into their context's list with
 // their new counts (counts only grow, so untouched tokens outside a list stay below its last entry).
 #include "ngram_common.h"
+#include "prim.h"
 
 namespace {
 
@@ -392,6 +393,360 @@ __global__ void __launch_bounds__(WAVE) online_top_k(const u64* __restrict__ uk,
     }
 }
 
+// ---- A step's merge by buckets of contexts (ng_online_merge): the step's events are not sorted ----
+// The events (tagged pair keys tag << tshift | slot << 16 | next, as ng_online_top's sort takes them) are scattered by
+// the low OM_BITS bits of their context slot into OM_NB buckets, so that all of a context's events land in one bucket
+// (slots are hashed: the buckets are about equal). A block per bucket then
+//   A. counts the distinct pairs of its events in an LDS hash (a packed word per pair: the pair key without the
+//      bucket's bits, shifted above an occurrence count that LDS atomics add to),
+//   B. sorts the distinct pairs in LDS (bitonic), which makes each context's pairs consecutive,
+//   C. adds each pair's occurrences to its count in the level's pair table (one plain update: every pair of the step
+//      is in one bucket and one round),
+//   D. merges each context's total, distinct count and top-E list as online_top_k does, reading LDS only: a context
+//      with many pairs in the step is walked by the wave over LDS, not over global memory.
+// A bucket with more than OM_DCAP distinct pairs is done in rounds, its events split by a hash of the pair (halving
+// until each round fits; nothing global is written before a round fits). A context whose pairs fall in several rounds
+// is merged once per round: each merge supersedes the old entries of the pairs it touches, and a pair touched in a
+// later round but absent from that round's top 8 scores below all 8 of them, so the list ends as one merge leaves it.
+#define OM_BITS 11
+#define OM_NB (1 << OM_BITS)
+#define OM_BLOCK 512
+#define OM_H 6144        // LDS hash slots
+#define OM_DCAP 4096     // distinct pairs in a round at most (the hash at load <= 2/3; the sort's size)
+#define OM_MAXSPLIT 40   // rounds split at most 40 times (2^40 rounds); beyond it level 0's flags[0] bit 2 is set
+#define OM_CHUNK 8192    // events per histogram segment (ng_seg_scatter's segments)
+#define OM_PER (OM_H / OM_BLOCK)
+#define OM_EV 8       // events a thread loads at once
+#define OM_PB 2       // pairs a thread looks up at once
+
+// Per segment of OM_CHUNK events, its count per bucket (digit-major: hist[d * nseg + s]) and its size.
+__global__ void __launch_bounds__(1024) om_hist_k(const u64* __restrict__ ev, i64 m, i64 nseg, u32* __restrict__ hist,
+                                                  u32* __restrict__ seg_n) {
+    __shared__ u32 h[OM_NB];
+    const int t = threadIdx.x;
+    for (i64 sg = blockIdx.x; sg < nseg; sg += gridDim.x) {
+        for (int d = t; d < OM_NB; d += 1024) h[d] = 0;
+        lds_barrier();
+        const i64 a = sg * OM_CHUNK, b = a + OM_CHUNK < m ? a + OM_CHUNK : m;
+        for (i64 i = a + t; i < b; i += 1024) atomicAdd(&h[(u32)(ev[i] >> 16) & (OM_NB - 1)], 1u);
+        lds_barrier();
+        for (int d = t; d < OM_NB; d += 1024) hist[(i64)d * nseg + sg] = h[d];
+        if (t == 0) seg_n[sg] = (u32)(b - a);
+        lds_barrier();
+    }
+}
+
+// Bucket b = the events evb[dpre[b * nseg], dpre[(b + 1) * nseg]) (the last one ends at m). cb: the count bits of
+// the packed words (a pair's occurrences in the step < 2^cb - 1).
+__global__ void __launch_bounds__(OM_BLOCK) __attribute__((amdgpu_waves_per_eu(4))) om_merge_k(const u64* __restrict__ evb, const u32* __restrict__ dpre,
+                                                       i64 nseg, i64 m, const i64* __restrict__ desc, int tshift,
+                                                       int cb, int E) {
+    __shared__ u64 hs[OM_H];
+    __shared__ u32 cs[OM_DCAP];
+    __shared__ u32 s_part[OM_BLOCK / WAVE];
+    __shared__ u64 s_stack[OM_MAXSPLIT + 2];  // pending rounds: residue << 8 | log2 of the rounds
+    __shared__ int s_sp, s_nd, s_over;
+    const int t = threadIdx.x, lane = lane_id(), wid = t / WAVE;
+    const int hb = tshift - 16 - OM_BITS;  // slot bits above the bucket's
+    const u64 hbm = (1ull << hb) - 1;
+    const u64 cmask = (1ull << cb) - 1;
+    const int csh = cb + 16;  // packed word >> csh = the context within the bucket (tag, slot bits above the bucket's)
+    for (i64 b = blockIdx.x; b < OM_NB; b += gridDim.x) {
+        const i64 e0 = dpre[b * nseg], e1 = b + 1 < OM_NB ? (i64)dpre[(b + 1) * nseg] : m;
+        __syncthreads();  // every thread is done with the previous bucket's round stack
+        if (t == 0) {
+            s_stack[0] = 0;
+            s_sp = 1;
+        }
+        for (;;) {
+            __syncthreads();  // the previous round's global stores visible to this round; the round stack settled
+            const int sp = s_sp;
+            if (sp == 0) break;
+            const u64 rtop = s_stack[sp - 1];
+            const u64 res = rtop >> 8;
+            const int lg = (int)(rtop & 0xFF);
+            for (int i = t; i < OM_H; i += OM_BLOCK) hs[i] = EMPTY;
+            if (t == 0) {
+                s_nd = 0;
+                s_over = 0;
+            }
+            lds_barrier();
+            if (t == 0) s_sp = sp - 1;
+            // A. the round's distinct pairs and their occurrences: OM_EV events a thread loaded together, then counted
+            for (i64 base = e0; base < e1; base += (i64)OM_BLOCK * OM_EV) {
+                if (*(volatile int*)&s_over) break;
+                u64 ev[OM_EV];
+#pragma unroll
+                for (int j = 0; j < OM_EV; ++j) {
+                    const i64 i = base + (i64)j * OM_BLOCK + t;
+                    ev[j] = i < e1 ? evb[i] : EMPTY;
+                }
+#pragma unroll
+                for (int j = 0; j < OM_EV; ++j) {
+                    const u64 e = ev[j];
+                    if (e == EMPTY) continue;
+                    const u64 hx = mix64(e);
+                    if (lg && (hx & ((1ull << lg) - 1)) != res) continue;
+                    const u64 kp = ((e >> (16 + OM_BITS)) << 16) | (e & 0xFFFF);
+                    u32 h = (u32)__umul64hi(hx, (u64)OM_H);
+                    // ends: s_over is set at the (OM_DCAP + 1)-th insert, with a third of the slots still free, and a
+                    // walk that meets it stops
+                    for (;;) {
+                        if (*(volatile int*)&s_over) break;
+                        u64 cur = hs[h];
+                        if (cur == EMPTY) {
+                            cur = atomicCAS((unsigned long long*)&hs[h], EMPTY,
+                                            (unsigned long long)((kp << cb) | 1ull));
+                            if (cur == EMPTY) {
+                                if (atomicAdd(&s_nd, 1) >= OM_DCAP) s_over = 1;
+                                break;
+                            }
+                        }
+                        if ((cur >> cb) == kp) {
+                            atomicAdd((unsigned long long*)&hs[h], 1ull);
+                            break;
+                        }
+                        h = h + 1 == OM_H ? 0 : h + 1;
+                    }
+                }
+            }
+            lds_barrier();
+            if (s_over) {  // block-uniform: split the round in two by one more hash bit
+                if (t == 0) {
+                    if (lg >= OM_MAXSPLIT) {
+                        atomicOr((u32*)desc[6], 4u);
+                    } else {
+                        s_stack[sp - 1] = ((res + (1ull << lg)) << 8) | (u64)(lg + 1);
+                        s_stack[sp] = (res << 8) | (u64)(lg + 1);
+                        s_sp = sp + 1;
+                    }
+                }
+                continue;
+            }
+            const int D = s_nd;
+            // B. the distinct pairs packed to hs[0, D), then sorted (EMPTY pads to a power of two)
+            u64 v[OM_PER];
+            u32 cnt = 0;
+#pragma unroll
+            for (int j = 0; j < OM_PER; ++j) {
+                v[j] = hs[t * OM_PER + j];
+                cnt += v[j] != EMPTY;
+            }
+            u32 incl = cnt;
+#pragma unroll
+            for (int d = 1; d < WAVE; d <<= 1) {
+                const u32 o = (u32)__shfl_up((int)incl, d, WAVE);
+                if (lane >= d) incl += o;
+            }
+            if (lane == WAVE - 1) s_part[wid] = incl;
+            lds_barrier();  // every slot read into registers before any is overwritten
+            u32 o = incl - cnt;
+            for (int w2 = 0; w2 < wid; ++w2) o += s_part[w2];
+#pragma unroll
+            for (int j = 0; j < OM_PER; ++j)
+                if (v[j] != EMPTY) hs[o++] = v[j];
+            u32 P = 1;
+            while (P < (u32)D) P <<= 1;
+            for (u32 i = (u32)D + t; i < P; i += OM_BLOCK) hs[i] = EMPTY;
+            lds_barrier();
+            for (u32 k = 2; k <= P; k <<= 1) {
+                for (u32 j = k >> 1; j > 0; j >>= 1) {
+                    for (u32 q = t; q < P / 2; q += OM_BLOCK) {
+                        const u32 i = ((q & ~(j - 1)) << 1) | (q & (j - 1));
+                        const u32 l = i | j;
+                        const u64 x = hs[i], y = hs[l];
+                        if ((x > y) == ((i & k) == 0)) {
+                            hs[i] = y;
+                            hs[l] = x;
+                        }
+                    }
+                    lds_barrier();
+                }
+            }
+            // C. each pair's count grows by its occurrences: OM_PB pairs a thread, their home slots (key and count)
+            // loaded together; a pair not at its home slot walks on (opair_slot)
+            for (int i0 = 0; i0 < D; i0 += OM_BLOCK * OM_PB) {
+                u64 key[OM_PB], cur[OM_PB];
+                i64 at[OM_PB];
+                u32 cc[OM_PB], tg[OM_PB];
+#pragma unroll
+                for (int j = 0; j < OM_PB; ++j) {
+                    const int i = i0 + j * OM_BLOCK + t;
+                    at[j] = -1;
+                    if (i < D) {
+                        const u64 kp = hs[i] >> cb;
+                        const u64 hi = kp >> 16;
+                        tg[j] = (u32)(hi >> hb);
+                        key[j] = ((((hi & hbm) << OM_BITS) | (u64)b) << 16) | (kp & 0xFFFF);
+                        const OLevel lv = olevel(desc, tg[j]);
+                        at[j] = (i64)__umul64hi(mix64(key[j]), lv.pcap);
+                        cur[j] = lv.pk[at[j]];
+                        cc[j] = lv.pcnt[at[j]];
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < OM_PB; ++j) {
+                    const int i = i0 + j * OM_BLOCK + t;
+                    if (i >= D) continue;
+                    const OLevel lv = olevel(desc, tg[j]);
+                    if (cur[j] != key[j]) {
+                        at[j] = opair_slot(lv.pk, lv.pcap, key[j], lv.flags);
+                        cc[j] = at[j] >= 0 ? lv.pcnt[at[j]] : 0;
+                    }
+                    u32 c = 0;
+                    if (at[j] >= 0) {
+                        c = cc[j] + (u32)(hs[i] & cmask);
+                        lv.pcnt[at[j]] = c;
+                    }
+                    cs[i] = c;
+                }
+            }
+            lds_barrier();
+            // D. per context (its pairs consecutive in hs): windows of 64 pairs, a wave each (online_top_k's scheme)
+            const u32 nwin = ((u32)D + WAVE - 1) / WAVE;
+            for (u32 wv = wid; wv < nwin; wv += OM_BLOCK / WAVE) {
+                const u32 i = wv * WAVE + lane;
+                const bool valid = i < (u32)D;
+                const u64 w = valid ? hs[i] : 0;
+                const u64 cx = w >> csh;
+                const u32 c = valid ? cs[i] : 0;
+                const u32 ag = (u32)(w & cmask);
+                const u64 sc = valid && c ? ((u64)c << 16) | (0xFFFFu - (u32)((w >> cb) & 0xFFFF)) : 0;
+                u64 pcx = shfl_up_u64(cx, 1);
+                if (lane == 0) pcx = valid && i > 0 ? hs[i - 1] >> csh : 0;
+                u64 ncx = shfl_down_u64(cx, 1);
+                if (lane == WAVE - 1) ncx = i + 1 < (u32)D ? hs[i + 1] >> csh : 0;
+                const bool head = valid && (i == 0 || pcx != cx);
+                const bool tail = valid && (i + 1 == (u32)D || ncx != cx);
+                const u64 tails = __ballot(tail);
+                int e = -1;  // where this head's context ends, if in the window
+                if (head && (tails >> lane)) e = lane + __ffsll((unsigned long long)(tails >> lane)) - 1;
+                if (e >= 0 && e - lane + 1 <= ONLINE_SHORT) {  // a short context ending in the window: this lane alone
+                    const OLevel lv = olevel(desc, cx >> hb);
+                    const u64 slot = ((cx & hbm) << OM_BITS) | (u64)b;
+                    const u32 ge = wv * WAVE + (u32)e;
+                    u32 add = 0, fresh = 0;
+                    u64 tt[8];
+#pragma unroll
+                    for (int r = 0; r < 8; ++r) tt[r] = 0;
+                    for (u32 q = i; q <= ge; ++q) {
+                        const u64 wq = hs[q];
+                        const u32 cq = cs[q], aq = (u32)(wq & cmask);
+                        add += aq;
+                        fresh += cq == aq;
+                        if (lv.top && cq) top8_insert(tt, ((u64)cq << 16) | (0xFFFFu - (u32)((wq >> cb) & 0xFFFF)));
+                    }
+                    u64* top = lv.top ? lv.top + slot * E : nullptr;
+                    u64 olds[8];  // the old list up to its first empty entry (loading all E was 13% slower)
+#pragma unroll
+                    for (int r = 0; r < 8; ++r) olds[r] = 0;
+                    if (top)
+                        for (int r = 0; r < E; ++r) {
+                            olds[r] = top[r];
+                            if (olds[r] == 0) break;
+                        }
+                    lv.tot[slot] += add;
+                    lv.dist[slot] += fresh;
+                    if (top) {
+#pragma unroll
+                        for (int r = 0; r < 8; ++r) {
+                            const u64 old = olds[r];
+                            if (old == 0) continue;
+                            const u64 tk = (cx << 16) | (0xFFFFu - (u32)(old & 0xFFFF));
+                            bool touched = false;
+                            for (u32 q = i; q <= ge; ++q) touched |= (hs[q] >> cb) == tk;
+                            if (!touched) top8_insert(tt, old);
+                        }
+                        for (int r = 0; r < E; ++r) top[r] = tt[r];
+                    }
+                }
+                // the whole wave takes the context running past the window and the long ones ending in it
+                const bool open = head && !(tails >> lane);
+                u64 waved = __ballot(open || (e >= 0 && e - lane + 1 > ONLINE_SHORT));
+                while (waved) {  // wave-uniform
+                    const int h = __ffsll((unsigned long long)waved) - 1;
+                    waved &= waved - 1;
+                    const int eh = __shfl(e, h, WAVE);  // -1: the context runs past the window
+                    const u64 hc = bcast_u64(cx, h);
+                    const OLevel lv = olevel(desc, hc >> hb);
+                    const u64 hslot = ((hc & hbm) << OM_BITS) | (u64)b;
+                    const u32 gi = wv * WAVE + (u32)h;
+                    const bool in = valid && lane >= h && (eh < 0 || lane <= eh);
+                    u64 add = in ? ag : 0, fresh = (in && c == ag) ? 1 : 0;
+                    u64 lt[8];
+#pragma unroll
+                    for (int r = 0; r < 8; ++r) lt[r] = 0;
+                    if (in && lv.top) lt[0] = sc;
+                    u32 ge = wv * WAVE + (u32)eh + 1;  // the context's end (found below for an open one)
+                    bool cont = eh < 0;
+                    if (cont) ge = wv * WAVE + WAVE;
+                    for (u32 nx = wv * WAVE + WAVE; cont; nx += WAVE) {
+                        const u32 j = nx + lane;
+                        const bool jv = j < (u32)D;
+                        const u64 w2 = jv ? hs[j] : 0;
+                        const bool in2 = jv && (w2 >> csh) == hc;
+                        const u64 m2 = __ballot(in2);
+                        if (in2) {
+                            const u32 c2 = cs[j], a2 = (u32)(w2 & cmask);
+                            add += a2;
+                            fresh += c2 == a2;
+                            if (lv.top && c2)
+                                top8_insert(lt, ((u64)c2 << 16) | (0xFFFFu - (u32)((w2 >> cb) & 0xFFFF)));
+                        }
+                        ge = nx + (u32)__popcll(m2);
+                        cont = ((m2 >> (WAVE - 1)) & 1ull) && nx + WAVE < (u32)D;
+                    }
+#pragma unroll
+                    for (int d = WAVE / 2; d > 0; d >>= 1) {
+                        add += shfl_down_u64(add, d);
+                        fresh += shfl_down_u64(fresh, d);
+                    }
+                    if (lane == 0) {
+                        lv.tot[hslot] += (u32)add;
+                        lv.dist[hslot] += (u32)fresh;
+                    }
+                    if (lv.top) {
+                        u64* top = lv.top + hslot * E;
+                        if (lane < E) {  // lane r checks old entry r: kept unless its token was touched
+                            const u64 old = top[lane];
+                            if (old != 0) {
+                                const u64 tk = (hc << 16) | (0xFFFFu - (u32)(old & 0xFFFF));
+                                u32 lo = gi, hi2 = ge;
+                                while (lo < hi2) {
+                                    const u32 mid = (lo + hi2) >> 1;
+                                    if ((hs[mid] >> cb) < tk) lo = mid + 1;
+                                    else hi2 = mid;
+                                }
+                                if (!(lo < ge && (hs[lo] >> cb) == tk)) top8_insert(lt, old);
+                            }
+                        }
+                        int headq = 0;
+                        u64 merged[8];
+#pragma unroll
+                        for (int r = 0; r < 8; ++r) {
+                            u64 mine = 0;
+#pragma unroll
+                            for (int q = 0; q < 8; ++q)
+                                if (q == headq) mine = lt[q];
+                            u64 mx = mine;
+#pragma unroll
+                            for (int d = WAVE / 2; d > 0; d >>= 1) {
+                                const u64 ot = shfl_down_u64(mx, d);
+                                mx = ot > mx ? ot : mx;
+                            }
+                            mx = bcast_u64(mx, 0);
+                            merged[r] = mx;
+                            if (mx != 0 && mine == mx) ++headq;
+                        }
+                        if (lane == 0)
+                            for (int r = 0; r < E; ++r) top[r] = merged[r];
+                    }
+                }
+            }
+        }
+    }
+}
+
 // Queries at pos[i] (input position g, context tok[g-k+1..g] valid iff avail[g] >= k): per level its context's
 // slot (or -1) into qslot[i]; with count outputs (tot != NULL) tot / dist / cnt of the position into row g, column ci
 // of [n, nc] arrays (cnt: the count of tok[g+1] if has_next[g]).
@@ -617,6 +972,48 @@ extern "C" int ng_online_top(const u64* uk, const i64* n, i64 m, const u32* agg,
     online_scores_k<<<grid_for(m, 256), 256, 0, st>>>(uk, agg, n, m, desc, tshift, add_counts != 0, score);
     const i64 wins = (m + WAVE - 1) / WAVE;
     online_top_k<<<(unsigned)(wins < 262144 ? wins : 262144), WAVE, 0, st>>>(uk, score, agg, n, m, desc, tshift, E);
+    return (int)hipGetLastError();
+}
+
+extern "C" int ng_seg_scatter(const u64* src, u64 R, const i64* bases, const u32* ev_count, const u32* dpre, i64 nseg,
+                              int shift, int nbits, u64* out, u64 cap, void* stream);
+
+// A step's events ev[0..m) of every level at once (tagged pair keys as ng_online_insert_levels writes them with
+// count_pairs 0: level t's pair keys | t << tshift, EMPTY skipped) merged into the levels' pair counts, totals,
+// distinct counts and top-E lists, as sort_pairs + reduce_by_key + ng_online_top (add_counts 1) do, without sorting
+// the events (om_merge_k). desc, ntag, tshift, E: as ng_online_top's. CUB-style two-phase temp storage (temp NULL:
+// *temp_bytes set for m). -1 where the packed words cannot hold a pair's occurrences (m >= 2^cb - 1, cb = 64 - tshift
+// - tag bits + 11): the caller then takes the sorted path.
+extern "C" int ng_online_merge(void* temp, size_t* temp_bytes, const u64* ev, i64 m, const i64* desc, int ntag,
+                               int tshift, int E, void* stream) {
+    if (!temp_bytes || E < 1 || E > 8 || ntag < 1 || ntag > ONLINE_MAXL || m < 0 || m >= 0xFFFFFFFFll) return -1;
+    const int tagbits = ntag > 1 ? 64 - __builtin_clzll((u64)(ntag - 1)) : 1;
+    if (tshift < 16 + OM_BITS || tshift + tagbits > 64) return -1;
+    const int cb = 64 - (tshift + tagbits - OM_BITS);
+    if (cb < 2 || (u64)m >= (1ull << cb) - 1) return -1;
+    const i64 nseg = (m + OM_CHUNK - 1) / OM_CHUNK;
+    const i64 nh = (i64)OM_NB * (nseg > 0 ? nseg : 1);
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const size_t b_ev = al((size_t)m * 8), b_hist = al((size_t)nh * 4), b_seg = al((size_t)(nseg + 1) * 4);
+    const size_t need = b_ev + b_hist + b_seg + prim::scan_u32_temp_bytes(nh);
+    if (!temp) {
+        *temp_bytes = need;
+        return 0;
+    }
+    if (*temp_bytes < need || !ev || !desc) return -1;
+    if (m == 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    char* p = (char*)temp;
+    u64* evb = (u64*)p;
+    u32* hist = (u32*)(p + b_ev);
+    u32* seg_n = (u32*)(p + b_ev + b_hist);
+    void* stemp = p + b_ev + b_hist + b_seg;
+    om_hist_k<<<(unsigned)(nseg < 16384 ? nseg : 16384), 1024, 0, st>>>(ev, m, nseg, hist, seg_n);
+    int rc = (int)hipGetLastError();
+    if (rc) return rc;
+    if ((rc = prim::exclusive_scan_u32(hist, hist, nh, nullptr, stemp, st))) return rc;
+    if ((rc = ng_seg_scatter(ev, OM_CHUNK, nullptr, seg_n, hist, nseg, 16, OM_BITS, evb, (u64)m, stream))) return rc;
+    om_merge_k<<<OM_NB, OM_BLOCK, 0, st>>>(evb, hist, nseg, m, desc, tshift, cb, E);
     return (int)hipGetLastError();
 }
 

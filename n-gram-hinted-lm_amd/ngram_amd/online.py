@@ -150,6 +150,9 @@ class OnlineRows:
         self._done = 0
         self.config = None
         self.state = None
+        # a step's merge: "buckets" (ng_online_merge: no sort of the step's events, where its packed words hold the
+        # step's occurrences) or "sorted" (sort_pairs + reduce_by_key + ng_online_top); both give the same state
+        self.merge = "buckets"
 
     def __len__(self) -> int:
         return self.n
@@ -254,6 +257,17 @@ class OnlineRows:
         st["agg"] = torch.empty(most, dtype=torch.int32, device=dev)
         st["nruns"] = torch.zeros(1, dtype=torch.int64, device=dev)
         st["score"] = torch.empty(most, dtype=torch.int64, device=dev)
+        st["merge_temp"] = None
+        if self.merge == "buckets":
+            size = ctypes.c_size_t(0)
+            try:
+                self.lib("ng_online_merge", None, ctypes.c_void_p(ctypes.addressof(size)), None, most, None,
+                         i32(len(st["levels"])), i32(st["tshift"]), i32(E))
+            except RuntimeError:  # -1: the step is too large for the packed words; the sorted merge runs instead
+                size = None
+            if size is not None:
+                st["merge_size"] = size
+                st["merge_temp"] = torch.empty(max(1, size.value), dtype=torch.uint8, device=dev)
         nq = int(np.bincount(st["q_step"]).max()) if len(st["q_step"]) else 1
         st["qslot"] = {k: torch.empty(max(1, nq), dtype=torch.int32, device=dev) for k in levels}
         st["hinted"] = torch.zeros(1, dtype=torch.int32, device=dev)
@@ -289,7 +303,10 @@ class OnlineRows:
         for j in range(0, len(ins), MAX_LAUNCH_LEVELS):  # every level's inserts in one launch
             part = ins[j : j + MAX_LAUNCH_LEVELS]
             lib("ng_online_insert_levels", self.tok, i32(len(part)), _i64_array(part), i32(0))
-        if m:
+        if m and st["merge_temp"] is not None:
+            lib("ng_online_merge", st["merge_temp"], ctypes.c_void_p(ctypes.addressof(st["merge_size"])), st["ev"], m,
+                st["top_desc"], i32(len(st["levels"])), i32(st["tshift"]), i32(E))
+        elif m:
             lib.cub("sort_pairs", st["ev"], st["ev_sorted"], None, None, m, i32(0), i32(st["tshift"] + st["tag_bits"]))
             lib.cub("reduce_by_key", st["ev_sorted"], st["uk"], None, st["agg"], st["nruns"], m)  # run lengths
             lib("ng_online_top", st["uk"], st["nruns"], m, st["agg"], st["top_desc"], i32(len(st["levels"])),

@@ -219,10 +219,11 @@ class _PerLevelRows(OnlineRows):
                 outs["cell"], outs["next"], outs["weights"], outs["level"], st["hinted"])
 
 
-@pytest.mark.parametrize("how", ["per_level", "chunks_of_3"])
+@pytest.mark.parametrize("how", ["per_level", "chunks_of_3", "sorted"])
 def test_step_entry_points_agree(stream, monkeypatch, how):
-    """The single-level entry points (pairs counted per occurrence), and the fused launches split in chunks of three
-    levels, give the oracle's rows, as the default path does (test_advance_step_by_step)."""
+    """The single-level entry points (pairs counted per occurrence), the fused launches split in chunks of three
+    levels, and the sorted merge (sort_pairs + reduce_by_key + ng_online_top in place of ng_online_merge) give the
+    oracle's rows, as the default path does (test_advance_step_by_step)."""
     from ngram_amd import online as on
 
     tok, spans = stream
@@ -233,6 +234,9 @@ def test_step_entry_points_agree(stream, monkeypatch, how):
     want = O.online(tok, bounds, tau, tau_in, LEVELS, BUCKETS, 8, count_levels, 0, len(spans))
     if how == "per_level":
         rows = _PerLevelRows(tok, bounds, spans, 4, [])
+    elif how == "sorted":
+        rows = OnlineRows(tok, bounds, spans, 4, [])
+        rows.merge = "sorted"
     else:
         monkeypatch.setattr(on, "MAX_LAUNCH_LEVELS", 3)
         rows = OnlineRows(tok, bounds, spans, 4, [])
@@ -241,3 +245,36 @@ def test_step_entry_points_agree(stream, monkeypatch, how):
     for g, w, name in zip(got, want, ("cell", "next", "weights", "tot", "dist", "cnt")):
         assert np.array_equal(g, w), name
     assert hinted == want[-1]
+
+
+@pytest.mark.parametrize("merge", ["buckets", "sorted"])
+def test_context_with_more_pairs_than_a_merge_round(merge):
+    """A level-2 context followed by 6000 distinct tokens within one step: its bucket holds more distinct pairs than
+    ng_online_merge's LDS round (4096), so the bucket is merged in rounds split by a pair hash, the context's pairs
+    spread over them; the next steps touch half of those pairs again and add new ones. Rows and counts against the
+    oracle, for both merges."""
+    rng = np.random.default_rng(11)
+    a, b = 7, 9
+    seq = []
+    for j in range(6000):
+        seq += [a, b, 1000 + j]
+    for j in range(3000, 9000):
+        seq += [a, b, 1000 + j % 7000, int(rng.integers(0, 50))]
+    seq += list(rng.integers(0, 300, 20000))
+    tok = np.array(seq, np.uint16)
+    n = len(tok)
+    cuts = [0, 18000, 42000, n]
+    spans = np.array([(cuts[s], cuts[s + 1], s) for s in range(3)], np.int64)
+    bounds = [0, n]
+    tau, tau_in = O.spans_tau(n, bounds, spans)
+    want = O.online(tok, bounds, tau, tau_in, LEVELS, BUCKETS, 8, LEVELS, 0, len(spans))
+    rows = OnlineRows(tok, bounds, spans, 4, [])
+    rows.merge = merge
+    got = _empty(n, 8, len(LEVELS))
+    hinted = rows.advance(len(spans), LEVELS, BUCKETS, 8, LEVELS, *got)
+    if merge == "buckets":
+        assert rows.state["merge_temp"] is not None
+    for g, w, name in zip(got, want, ("cell", "next", "weights", "tot", "dist", "cnt")):
+        assert np.array_equal(g, w), name
+    assert hinted == want[-1]
+    assert int(got[3][:, 0].max()) >= 6000  # the context's total reached the step's 6000 occurrences
