@@ -275,15 +275,18 @@ int ng_table_query(const uint16_t* x, const int* avail, const uint16_t* tgt, ng_
 /* hint rows over table levels (count_table.rs query_rows :338-404); desc[v * 3]: slot_of, records, bucket */
 int ng_pos_rows(ng_i64 N, int nlv, const ng_i64* desc, int entries, short* cell, uint16_t* next, uint16_t* weights,
                 signed char* level, void* stream);
-/* online state (online.rs step rule): insert occurrences ending at pos[i] (ctx_tot/ctx_dist may be NULL: then the
- * sorted pass adds them), their pair keys | tag into ev (tag: the level's index << tshift, above every pair key);
- * merge a step's sorted distinct touched pairs of every level at once (uk[0..*n) tagged keys, agg their occurrences
- * in the step; desc[t * 7]: level t's pair keys, counts, capacity, top lists or 0, totals, distinct counts, flags)
- * into their contexts' totals, distinct counts and top-E lists (add_counts: the pairs' counts grow by agg there,
- * after inserts that did not count them); answer queries; build hint rows */
-int ng_online_insert(const uint16_t* tok, const int* pos, ng_i64 m, int k, ng_u64* ck, ng_u64 ccap, ng_u64* pk,
-                     uint32_t* pcnt, ng_u64 pcap, uint32_t* ctx_tot, uint32_t* ctx_dist, ng_u64* ev, uint32_t* flags,
-                     ng_u64 tag, void* stream);
+/* online state (online.rs step rule), per level: a context table ck (slot = context id); a pair table pt of pcap
+ * 16-byte slots (pt[2s] the key slot << 16 | next, EMPTY when free; the low half of pt[2s + 1] its count); a record
+ * per context, rw u32 words: [0] total, [1] distinct next tokens, and with rw = 16 (levels with hint rows) [2, 10) the
+ * top entries' counts and [10, 14) their tokens, two per word (count descending, then token ascending; count 0 ends
+ * the list); rw = 2 without entries. Insert occurrences ending at pos[i] (rec may be NULL: then the sorted pass adds
+ * the totals), their pair keys | tag into ev (tag: the level's index << tshift, above every pair key); merge a step's
+ * sorted distinct touched pairs of every level at once (uk[0..*n) tagged keys, agg their occurrences in the step;
+ * desc[t * 5]: level t's pair table, its capacity, records, 1 if rw = 16 else 0, flags) into their contexts'
+ * records (add_counts: the pairs' counts grow by agg there, after inserts that did not count them); answer queries;
+ * build hint rows */
+int ng_online_insert(const uint16_t* tok, const int* pos, ng_i64 m, int k, ng_u64* ck, ng_u64 ccap, ng_u64* pt,
+                     ng_u64 pcap, uint32_t* rec, int rw, ng_u64* ev, uint32_t* flags, ng_u64 tag, void* stream);
 int ng_online_top(const ng_u64* uk, const ng_i64* n, ng_i64 m, const uint32_t* agg, const ng_i64* desc, int ntag,
                   int tshift, ng_u64* score, int E, int add_counts, void* stream);
 /* a step's events ev[0..m) (unsorted, as ng_online_insert_levels writes them with count_pairs 0) merged as
@@ -296,20 +299,20 @@ int ng_online_top(const ng_u64* uk, const ng_i64* n, ng_i64 m, const uint32_t* a
 int ng_online_merge(void* temp, size_t* temp_bytes, const ng_u64* ev, ng_i64 m, const ng_i64* desc, int ntag,
                     int tshift, int E, void* stream);
 int ng_online_query(const uint16_t* tok, const int* avail, const unsigned char* has_next, const int* pos, ng_i64 m,
-                    int k, const ng_u64* ck, ng_u64 ccap, const ng_u64* pk, const uint32_t* pcnt, ng_u64 pcap,
-                    const uint32_t* ctx_tot, const uint32_t* ctx_dist, int* qslot, uint32_t* tot, uint16_t* dist,
-                    uint32_t* cnt, int nc, int ci, void* stream);
+                    int k, const ng_u64* ck, ng_u64 ccap, const ng_u64* pt, ng_u64 pcap, const uint32_t* rec, int rw,
+                    int* qslot, uint32_t* tot, uint16_t* dist, uint32_t* cnt, int nc, int ci, void* stream);
 /* the inserts / the queries of up to 8 levels of a step in one launch (a level's lookups are chains of dependent
- * table round trips; one launch pays that latency once for all levels). lv: a host array, 11 int64 per level for
- * inserts (pos, m, k, ck, ccap, pk, pcnt, pcap, ev, flags, tag) and 14 per level for queries (k, ck, ccap, pk, pcnt,
- * pcap, ctx_tot, ctx_dist, qslot, tot, dist, cnt, nc, ci), each as the single-level call's argument of that name
- * (pointers as int64; the inserts leave totals and distinct counts to ng_online_top, and with count_pairs 0 the pair
- * counts too: ng_online_top's add_counts). -1 on a bad level. */
+ * table round trips; one launch pays that latency once for all levels). lv: a host array, 10 int64 per level for
+ * inserts (pos, m, k, ck, ccap, pt, pcap, ev, flags, tag) and 13 per level for queries (k, ck, ccap, pt, pcap, rec,
+ * rw, qslot, tot, dist, cnt, nc, ci), each as the single-level call's argument of that name (pointers as int64; the
+ * inserts leave the records to ng_online_top / ng_online_merge, and with count_pairs 0 the pair counts too). -1 on a
+ * bad level. */
 int ng_online_insert_levels(const uint16_t* tok, int nlv, const ng_i64* lv, int count_pairs, void* stream);
 int ng_online_query_levels(const uint16_t* tok, const int* avail, const unsigned char* has_next, const int* pos,
                            ng_i64 m, int nlv, const ng_i64* lv, void* stream);
-/* hint rows of the queries at pos[0..m) in S slots, deepest levels first: cell [n, S], next / weights [n, S, E],
- * level [n, S] (int8 bucket index; may be NULL); empty slots are left as they are */
+/* hint rows of the queries at pos[0..m) in S slots, deepest levels first (desc[v * 3]: the level's qslot from
+ * ng_online_query, its records (rw = 16), its bucket index): cell [n, S], next / weights [n, S, E], level [n, S] (int8
+ * bucket index; may be NULL); empty slots are left as they are */
 int ng_online_rows(const int* pos, ng_i64 m, int nlv, const ng_i64* desc, int E, int S, short* cell, uint16_t* next,
                    uint16_t* weights, signed char* level, int* hinted, void* stream);
 /* counts/mix.py features: counts int32 [3, L, n] -> float32 tot, dist, min(cnt, tot) [n, L], int64 bin and sparse

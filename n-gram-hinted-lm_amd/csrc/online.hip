@@ -1,8 +1,9 @@
 // Online rows under the step rule on the GPU: the incremental state behind ngram_amd/online.py's OnlineRows (the
 // surface of exact_match/src/online.rs :102-1382; no counterpart in the reference's GPU libraries). Per level k the
-// state persists between steps: a context table (u64 keys, slot = context id) with per-context total, distinct next
-// tokens and its top-E (count descending, then token ascending) as packed scores (count << 16 | 65535 - token), and a
-// split pair table ((slot << 16 | next) keys, u32 counts). A step inserts the occurrences that become available in it,
+// state persists between steps: a context table (u64 keys, slot = context id), a record per context (its total,
+// distinct next tokens and top-E entries, count descending then token ascending: one 64-byte load), and a pair table
+// of 16-byte slots ((slot << 16 | next) key beside its u32 count: one line per lookup). A step inserts the occurrences
+// that become available in it,
 // then answers its queries (online.rs:11-13: an occurrence counts for a step-s query iff all its tokens were trained
 // before s). The top-E lists stay exact: a step's touched pairs are sorted and merged into their context's list with
 // their new counts (counts only grow, so untouched tokens outside a list stay below its last entry).
@@ -37,19 +38,22 @@ __device__ __forceinline__ i64 octx_find(const u64* __restrict__ ck, u64 ccap, u
     return -1;
 }
 
+// The pair table: cap slots of 16 bytes, pt[2s] the key (EMPTY when free) and the low half of pt[2s + 1] its count.
+__device__ __forceinline__ u32* opair_cnt(u64* pt, u64 s) { return (u32*)(pt + 2 * s + 1); }
+
 // Count a pair; returns 1 if this call inserted it (its first occurrence), 0 if it was there, -1 if the table is full.
-__device__ __forceinline__ int opair_add(u64* keys, u32* cnts, u64 cap, u64 key, u32* flags) {
+__device__ __forceinline__ int opair_add(u64* pt, u64 cap, u64 key, u32* flags) {
     u64 s = __umul64hi(mix64(key), cap);
     for (int probe = 0; probe < MAXPROBE; ++probe) {
-        const u64 cur = keys[s];
+        const u64 cur = pt[2 * s];
         if (cur == key) {
-            atomicAdd(&cnts[s], 1u);
+            atomicAdd(opair_cnt(pt, s), 1u);
             return 0;
         }
         if (cur == EMPTY) {
-            const u64 prev = atomicCAS((unsigned long long*)&keys[s], EMPTY, key);
+            const u64 prev = atomicCAS((unsigned long long*)&pt[2 * s], EMPTY, key);
             if (prev == EMPTY || prev == key) {
-                atomicAdd(&cnts[s], 1u);
+                atomicAdd(opair_cnt(pt, s), 1u);
                 return prev == EMPTY ? 1 : 0;
             }
         }
@@ -59,31 +63,81 @@ __device__ __forceinline__ int opair_add(u64* keys, u32* cnts, u64 cap, u64 key,
     return -1;
 }
 
-__device__ __forceinline__ u32 opair_count(const u64* __restrict__ keys, const u32* __restrict__ cnts, u64 cap, u64 key) {
+__device__ __forceinline__ u32 opair_count(const u64* __restrict__ pt, u64 cap, u64 key) {
     u64 s = __umul64hi(mix64(key), cap);
     for (u64 probe = 0; probe < cap; ++probe) {
-        const u64 cur = keys[s];
-        if (cur == key) return cnts[s];
-        if (cur == EMPTY) return 0;
+        const ulonglong2 v = *(const ulonglong2*)(pt + 2 * s);  // key and count in one load
+        if (v.x == key) return (u32)v.y;
+        if (v.x == EMPTY) return 0;
         s = s + 1 == cap ? 0 : s + 1;
     }
     return 0;
 }
 
 // A pair's slot, inserted if absent (-1 and flags[0] bit 0 if the table is full).
-__device__ __forceinline__ i64 opair_slot(u64* keys, u64 cap, u64 key, u32* flags) {
+__device__ __forceinline__ i64 opair_slot(u64* pt, u64 cap, u64 key, u32* flags) {
     u64 s = __umul64hi(mix64(key), cap);
     for (int probe = 0; probe < MAXPROBE; ++probe) {
-        const u64 cur = keys[s];
+        const u64 cur = pt[2 * s];
         if (cur == key) return (i64)s;
         if (cur == EMPTY) {
-            const u64 prev = atomicCAS((unsigned long long*)&keys[s], EMPTY, key);
+            const u64 prev = atomicCAS((unsigned long long*)&pt[2 * s], EMPTY, key);
             if (prev == EMPTY || prev == key) return (i64)s;
         }
         s = s + 1 == cap ? 0 : s + 1;
     }
     atomicOr(&flags[0], 1u);
     return -1;
+}
+
+// A context's record, rw u32 words per context slot: [0] its total, [1] its distinct next tokens; where the level keeps
+// top lists (rw = OREC_TOP: 64 bytes, four 16-byte loads) [2, 10) the counts and [10, 14) the tokens (two per word,
+// the lower half first) of its top entries, count descending then token ascending (count 0: no entry). As a ranking
+// score an entry is count << 16 | 65535 - token.
+#define OREC_TOP 16
+#define OREC_CNT 2
+
+struct ORec {
+    u32 tot, dist;
+    u64 sc[8];
+};
+
+__device__ __forceinline__ void orec_load(const u32* __restrict__ r, ORec& o) {
+    const uint4* q = (const uint4*)r;
+    const uint4 a = q[0], b = q[1], c = q[2], d = q[3];
+    o.tot = a.x;
+    o.dist = a.y;
+    const u32 cnt[8] = {a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y};
+    const u32 tk[4] = {c.z, c.w, d.x, d.y};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const u32 t = (tk[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
+        o.sc[j] = cnt[j] ? ((u64)cnt[j] << 16) | (0xFFFFu - t) : 0;
+    }
+}
+
+// The record of total tot, distinct count dist and the entries sc[0, E) (scores, descending; later ones empty).
+__device__ __forceinline__ void orec_store(u32* r, u32 tot, u32 dist, const u64 (&sc)[8], int E) {
+    u32 cnt[8], tk[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const u64 v = j < E ? sc[j] : 0;
+        cnt[j] = (u32)(v >> 16);
+        tk[j >> 1] |= (v ? 0xFFFFu - (u32)(v & 0xFFFF) : 0u) << (16 * (j & 1));
+    }
+    uint4* q = (uint4*)r;
+    q[0] = make_uint4(tot, dist, cnt[0], cnt[1]);
+    q[1] = make_uint4(cnt[2], cnt[3], cnt[4], cnt[5]);
+    q[2] = make_uint4(cnt[6], cnt[7], tk[0], tk[1]);
+    q[3] = make_uint4(tk[2], tk[3], 0u, 0u);
+}
+
+// A context's total and distinct count grown by add and fresh (a record without top entries).
+__device__ __forceinline__ void orec_add(u32* r, u32 add, u32 fresh) {
+    uint2 v = *(uint2*)r;
+    v.x += add;
+    v.y += fresh;
+    *(uint2*)r = v;
 }
 
 template <int K>
@@ -96,9 +150,8 @@ __device__ __forceinline__ u64 okey(const u16* e, int k) {
 // pair key | tag (the level's tag, above every pair key's bits: several levels' events sort as one array).
 template <int K>
 __device__ __forceinline__ void insert_one(const u16* __restrict__ tok, const int* __restrict__ pos, i64 i, int k,
-                                           u64* ck, u64 ccap, u64* pk, u32* pcnt, u64 pcap, u32* ctx_tot,
-                                           u32* ctx_dist, u64* __restrict__ ev, u32* flags, u64 tag,
-                                           bool count_pair = true) {
+                                           u64* ck, u64 ccap, u64* pt, u64 pcap, u32* rec, int rw,
+                                           u64* __restrict__ ev, u32* flags, u64 tag, bool count_pair = true) {
     const i64 g = pos[i];
     const u64 key = okey<K>(tok + g + 1, k);
     const i64 slot = octx_find_insert(ck, ccap, key, flags);
@@ -111,24 +164,24 @@ __device__ __forceinline__ void insert_one(const u16* __restrict__ tok, const in
         ev[i] = pair | tag;
         return;
     }
-    const int added = opair_add(pk, pcnt, pcap, pair, flags);
+    const int added = opair_add(pt, pcap, pair, flags);
     if (added < 0) {
         ev[i] = EMPTY;
         return;
     }
-    if (ctx_tot) {  // else the step's sorted pass (online_top_k) adds them, once per context
-        atomicAdd(&ctx_tot[slot], 1u);
-        if (added) atomicAdd(&ctx_dist[slot], 1u);
+    if (rec) {  // else the step's sorted pass (online_top_k) adds them, once per context
+        atomicAdd(&rec[slot * rw], 1u);
+        if (added) atomicAdd(&rec[slot * rw + 1], 1u);
     }
     ev[i] = pair | tag;
 }
 
 template <int K>
 __global__ void online_insert_k(const u16* __restrict__ tok, const int* __restrict__ pos, i64 m, int k, u64* ck,
-                                u64 ccap, u64* pk, u32* pcnt, u64 pcap, u32* ctx_tot, u32* ctx_dist,
-                                u64* __restrict__ ev, u32* flags, u64 tag) {
+                                u64 ccap, u64* pt, u64 pcap, u32* rec, int rw, u64* __restrict__ ev, u32* flags,
+                                u64 tag) {
     const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
-    if (i < m) insert_one<K>(tok, pos, i, k, ck, ccap, pk, pcnt, pcap, ctx_tot, ctx_dist, ev, flags, tag);
+    if (i < m) insert_one<K>(tok, pos, i, k, ck, ccap, pt, pcap, rec, rw, ev, flags, tag);
 }
 
 // Every level's inserts of a step in one launch: each level's inserts are chains of dependent table round trips, and
@@ -137,7 +190,7 @@ __global__ void online_insert_k(const u16* __restrict__ tok, const int* __restri
 // the blocks with blockIdx.y == t; its fields (ONLINE_INS_FIELDS i64 each, as ng_online_insert_levels documents) are
 // picked by unrolled compares on that block-uniform index, so no kernel argument is indexed at run time.
 #define ONLINE_MAXL 8
-#define ONLINE_INS_FIELDS 11
+#define ONLINE_INS_FIELDS 10
 struct OInsArgs {
     i64 f[ONLINE_MAXL][ONLINE_INS_FIELDS];
 };
@@ -146,8 +199,8 @@ template <int K>
 __device__ __forceinline__ void insert_level(const u16* __restrict__ tok, const i64 (&f)[ONLINE_INS_FIELDS], i64 i,
                                              bool count_pairs) {
     if (i >= f[1]) return;
-    insert_one<K>(tok, (const int*)f[0], i, (int)f[2], (u64*)f[3], (u64)f[4], (u64*)f[5], (u32*)f[6], (u64)f[7],
-                  nullptr, nullptr, (u64*)f[8], (u32*)f[9], (u64)f[10], count_pairs);
+    insert_one<K>(tok, (const int*)f[0], i, (int)f[2], (u64*)f[3], (u64)f[4], (u64*)f[5], (u64)f[6], nullptr, 0,
+                  (u64*)f[7], (u32*)f[8], (u64)f[9], count_pairs);
 }
 
 __global__ void __launch_bounds__(256) online_insert_levels_k(const u16* __restrict__ tok, int nlv, OInsArgs a,
@@ -174,22 +227,21 @@ __global__ void __launch_bounds__(256) online_insert_levels_k(const u16* __restr
     }
 }
 
-// A level's state as the step's merge reads it: desc[t * 7 ...] for tag t = pair table keys, counts, capacity, the
-// contexts' top-E lists (0: not kept), totals, distinct counts, the level's flags.
-#define OLEVEL_FIELDS 7
+// A level's state as the step's merge reads it: desc[t * 5 ...] for tag t = the pair table, its capacity, the
+// contexts' records, whether the level keeps top lists (records of OREC_TOP words, else OREC_CNT), its flags.
+#define OLEVEL_FIELDS 5
 struct OLevel {
-    u64* pk;
-    u32* pcnt;
+    u64* pt;
     u64 pcap;
-    u64* top;
-    u32* tot;
-    u32* dist;
+    u32* rec;
+    bool top;
     u32* flags;
+    __device__ __forceinline__ u32* at(u64 slot) const { return rec + slot * (top ? OREC_TOP : OREC_CNT); }
 };
 
 __device__ __forceinline__ OLevel olevel(const i64* __restrict__ desc, u64 tag) {
     const i64* d = desc + tag * OLEVEL_FIELDS;
-    return OLevel{(u64*)d[0], (u32*)d[1], (u64)d[2], (u64*)d[3], (u32*)d[4], (u32*)d[5], (u32*)d[6]};
+    return OLevel{(u64*)d[0], (u64)d[1], (u32*)d[2], d[3] != 0, (u32*)d[4]};
 }
 
 // Scores of a step's distinct touched pairs (sorted, tagged keys), i < *n. add_counts: each pair's step occurrences
@@ -209,15 +261,15 @@ __global__ void online_scores_k(const u64* __restrict__ uk, const u32* __restric
     const u64 pair = key & ((1ull << tshift) - 1);
     u32 c;
     if (add_counts) {
-        const i64 s = opair_slot(lv.pk, lv.pcap, pair, lv.flags);
+        const i64 s = opair_slot(lv.pt, lv.pcap, pair, lv.flags);
         if (s < 0) {
             score[i] = 0;
             return;
         }
-        c = lv.pcnt[s] + agg[i];
-        lv.pcnt[s] = c;
+        c = *opair_cnt(lv.pt, s) + agg[i];
+        *opair_cnt(lv.pt, s) = c;
     } else {
-        c = opair_count(lv.pk, lv.pcnt, lv.pcap, pair);
+        c = opair_count(lv.pt, lv.pcap, pair);
     }
     score[i] = ((u64)c << 16) | (0xFFFFu - (u32)(key & 0xFFFF));
 }
@@ -274,32 +326,31 @@ __global__ void __launch_bounds__(WAVE) online_top_k(const u64* __restrict__ uk,
         if (head && (tails >> lane)) e = lane + __ffsll((unsigned long long)(tails >> lane)) - 1;
         if (e >= 0 && e - lane + 1 <= ONLINE_SHORT) {  // a short context ending in the window: this lane alone, from LDS
             const OLevel lv = olevel(desc, key >> tshift);
-            const u64 slot = c & ((1ull << (tshift - 16)) - 1);
-            u64* const ctx_top = lv.top;
-            u32* const ctx_tot = lv.tot;
-            u32* const ctx_dist = lv.dist;
+            u32* const r = lv.at(c & ((1ull << (tshift - 16)) - 1));
             u32 add = 0, fresh = 0;
             u64 t[8];
 #pragma unroll
-            for (int r = 0; r < 8; ++r) t[r] = 0;
+            for (int j = 0; j < 8; ++j) t[j] = 0;
             for (int q = lane; q <= e; ++q) {
                 add += s_ag[q];
                 fresh += (u32)(s_sc[q] >> 16) == s_ag[q];
-                if (ctx_top) top8_insert(t, s_sc[q]);
+                if (lv.top) top8_insert(t, s_sc[q]);
             }
-            ctx_tot[slot] += add;
-            ctx_dist[slot] += fresh;
-            if (ctx_top) {
-                u64* top = ctx_top + slot * E;
-                for (int r = 0; r < E; ++r) {
-                    const u64 old = top[r];
-                    if (old == 0) break;
+            if (lv.top) {
+                ORec o;
+                orec_load(r, o);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const u64 old = o.sc[j];
+                    if (old == 0) continue;
                     const u64 tk = (c << 16) | (0xFFFFu - (u32)(old & 0xFFFF));
                     bool touched = false;
                     for (int q = lane; q <= e; ++q) touched |= s_key[q] == tk;
                     if (!touched) top8_insert(t, old);
                 }
-                for (int r = 0; r < E; ++r) top[r] = t[r];
+                orec_store(r, o.tot + add, o.dist + fresh, t, E);
+            } else {
+                orec_add(r, add, fresh);
             }
         }
         // the whole wave takes the context running past the window (over the following windows) and the long ones
@@ -312,17 +363,14 @@ __global__ void __launch_bounds__(WAVE) online_top_k(const u64* __restrict__ uk,
             const int eh = __shfl(e, h, WAVE);  // -1: the context runs past the window
             const u64 hc = bcast_u64(c, h);
             const OLevel lv = olevel(desc, hc >> (tshift - 16));
-            const u64 hslot = hc & ((1ull << (tshift - 16)) - 1);
-            u64* const ctx_top = lv.top;
-            u32* const ctx_tot = lv.tot;
-            u32* const ctx_dist = lv.dist;
+            u32* const hr = lv.at(hc & ((1ull << (tshift - 16)) - 1));
             const i64 gi = wv * WAVE + h;
             const bool in = valid && lane >= h && (eh < 0 || lane <= eh);
             u64 add = in ? ag : 0, fresh = (in && (u32)(sc >> 16) == ag) ? 1 : 0;
             u64 lt[8];
 #pragma unroll
             for (int r = 0; r < 8; ++r) lt[r] = 0;
-            if (in && ctx_top) lt[0] = sc;
+            if (in && lv.top) lt[0] = sc;
             i64 ge = wv * WAVE + eh + 1;  // the group's end (found below for an open context)
             bool cont = eh < 0;
             if (cont) ge = wv * WAVE + WAVE;
@@ -336,7 +384,7 @@ __global__ void __launch_bounds__(WAVE) online_top_k(const u64* __restrict__ uk,
                     const u32 a2 = agg[j];
                     add += a2;
                     fresh += (u32)(s2 >> 16) == a2;
-                    if (ctx_top) top8_insert(lt, s2);
+                    if (lv.top) top8_insert(lt, s2);
                 }
                 ge = nx + __popcll(m2);
                 cont = ((m2 >> (WAVE - 1)) & 1ull) && nx + WAVE < n;
@@ -346,14 +394,15 @@ __global__ void __launch_bounds__(WAVE) online_top_k(const u64* __restrict__ uk,
                 add += shfl_down_u64(add, d);
                 fresh += shfl_down_u64(fresh, d);
             }
-            if (lane == 0) {
-                ctx_tot[hslot] += (u32)add;
-                ctx_dist[hslot] += (u32)fresh;
-            }
-            if (ctx_top) {
-                u64* top = ctx_top + hslot * E;
-                if (lane < E) {  // lane r checks old entry r: kept unless its token was touched in the step
-                    const u64 old = top[lane];
+            if (lane == 0 && !lv.top) orec_add(hr, (u32)add, (u32)fresh);
+            if (lv.top) {
+                ORec o;  // every lane loads the record (one line); lane r checks old entry r
+                orec_load(hr, o);
+                u64 old = 0;
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (j == lane) old = o.sc[j];
+                if (lane < E) {  // kept unless its token was touched in the step
                     if (old != 0) {
                         const u64 tk = (hc << 16) | (0xFFFFu - (u32)(old & 0xFFFF));
                         i64 a = gi, b = ge;
@@ -385,8 +434,7 @@ __global__ void __launch_bounds__(WAVE) online_top_k(const u64* __restrict__ uk,
                     merged[r] = mx;
                     if (mx != 0 && mine == mx) ++headq;
                 }
-                if (lane == 0)
-                    for (int r = 0; r < E; ++r) top[r] = merged[r];
+                if (lane == 0) orec_store(hr, o.tot + (u32)add, o.dist + (u32)fresh, merged, E);
             }
         }
         __syncthreads();
@@ -580,8 +628,9 @@ __global__ void __launch_bounds__(OM_BLOCK) __attribute__((amdgpu_waves_per_eu(4
                         key[j] = ((((hi & hbm) << OM_BITS) | (u64)b) << 16) | (kp & 0xFFFF);
                         const OLevel lv = olevel(desc, tg[j]);
                         at[j] = (i64)__umul64hi(mix64(key[j]), lv.pcap);
-                        cur[j] = lv.pk[at[j]];
-                        cc[j] = lv.pcnt[at[j]];
+                        const ulonglong2 v = *(const ulonglong2*)(lv.pt + 2 * at[j]);  // key and count: one load
+                        cur[j] = v.x;
+                        cc[j] = (u32)v.y;
                     }
                 }
 #pragma unroll
@@ -590,13 +639,13 @@ __global__ void __launch_bounds__(OM_BLOCK) __attribute__((amdgpu_waves_per_eu(4
                     if (i >= D) continue;
                     const OLevel lv = olevel(desc, tg[j]);
                     if (cur[j] != key[j]) {
-                        at[j] = opair_slot(lv.pk, lv.pcap, key[j], lv.flags);
-                        cc[j] = at[j] >= 0 ? lv.pcnt[at[j]] : 0;
+                        at[j] = opair_slot(lv.pt, lv.pcap, key[j], lv.flags);
+                        cc[j] = at[j] >= 0 ? *opair_cnt(lv.pt, at[j]) : 0;
                     }
                     u32 c = 0;
                     if (at[j] >= 0) {
                         c = cc[j] + (u32)(hs[i] & cmask);
-                        lv.pcnt[at[j]] = c;
+                        *opair_cnt(lv.pt, at[j]) = c;
                     }
                     cs[i] = c;
                 }
@@ -636,28 +685,22 @@ __global__ void __launch_bounds__(OM_BLOCK) __attribute__((amdgpu_waves_per_eu(4
                         fresh += cq == aq;
                         if (lv.top && cq) top8_insert(tt, ((u64)cq << 16) | (0xFFFFu - (u32)((wq >> cb) & 0xFFFF)));
                     }
-                    u64* top = lv.top ? lv.top + slot * E : nullptr;
-                    u64 olds[8];  // the old list up to its first empty entry (loading all E was 13% slower)
+                    u32* const r = lv.at(slot);
+                    if (lv.top) {
+                        ORec o;
+                        orec_load(r, o);
 #pragma unroll
-                    for (int r = 0; r < 8; ++r) olds[r] = 0;
-                    if (top)
-                        for (int r = 0; r < E; ++r) {
-                            olds[r] = top[r];
-                            if (olds[r] == 0) break;
-                        }
-                    lv.tot[slot] += add;
-                    lv.dist[slot] += fresh;
-                    if (top) {
-#pragma unroll
-                        for (int r = 0; r < 8; ++r) {
-                            const u64 old = olds[r];
+                        for (int j = 0; j < 8; ++j) {
+                            const u64 old = o.sc[j];
                             if (old == 0) continue;
                             const u64 tk = (cx << 16) | (0xFFFFu - (u32)(old & 0xFFFF));
                             bool touched = false;
                             for (u32 q = i; q <= ge; ++q) touched |= (hs[q] >> cb) == tk;
                             if (!touched) top8_insert(tt, old);
                         }
-                        for (int r = 0; r < E; ++r) top[r] = tt[r];
+                        orec_store(r, o.tot + add, o.dist + fresh, tt, E);
+                    } else {
+                        orec_add(r, add, fresh);
                     }
                 }
                 // the whole wave takes the context running past the window and the long ones ending in it
@@ -669,7 +712,7 @@ __global__ void __launch_bounds__(OM_BLOCK) __attribute__((amdgpu_waves_per_eu(4
                     const int eh = __shfl(e, h, WAVE);  // -1: the context runs past the window
                     const u64 hc = bcast_u64(cx, h);
                     const OLevel lv = olevel(desc, hc >> hb);
-                    const u64 hslot = ((hc & hbm) << OM_BITS) | (u64)b;
+                    u32* const hr = lv.at(((hc & hbm) << OM_BITS) | (u64)b);
                     const u32 gi = wv * WAVE + (u32)h;
                     const bool in = valid && lane >= h && (eh < 0 || lane <= eh);
                     u64 add = in ? ag : 0, fresh = (in && c == ag) ? 1 : 0;
@@ -701,14 +744,15 @@ __global__ void __launch_bounds__(OM_BLOCK) __attribute__((amdgpu_waves_per_eu(4
                         add += shfl_down_u64(add, d);
                         fresh += shfl_down_u64(fresh, d);
                     }
-                    if (lane == 0) {
-                        lv.tot[hslot] += (u32)add;
-                        lv.dist[hslot] += (u32)fresh;
-                    }
+                    if (lane == 0 && !lv.top) orec_add(hr, (u32)add, (u32)fresh);
                     if (lv.top) {
-                        u64* top = lv.top + hslot * E;
-                        if (lane < E) {  // lane r checks old entry r: kept unless its token was touched
-                            const u64 old = top[lane];
+                        ORec o;  // every lane loads the record (one line); lane r checks old entry r
+                        orec_load(hr, o);
+                        u64 old = 0;
+#pragma unroll
+                        for (int j = 0; j < 8; ++j)
+                            if (j == lane) old = o.sc[j];
+                        if (lane < E) {  // kept unless its token was touched
                             if (old != 0) {
                                 const u64 tk = (hc << 16) | (0xFFFFu - (u32)(old & 0xFFFF));
                                 u32 lo = gi, hi2 = ge;
@@ -738,8 +782,7 @@ __global__ void __launch_bounds__(OM_BLOCK) __attribute__((amdgpu_waves_per_eu(4
                             merged[r] = mx;
                             if (mx != 0 && mine == mx) ++headq;
                         }
-                        if (lane == 0)
-                            for (int r = 0; r < E; ++r) top[r] = merged[r];
+                        if (lane == 0) orec_store(hr, o.tot + (u32)add, o.dist + (u32)fresh, merged, E);
                     }
                 }
             }
@@ -749,44 +792,41 @@ __global__ void __launch_bounds__(OM_BLOCK) __attribute__((amdgpu_waves_per_eu(4
 
 // Queries at pos[i] (input position g, context tok[g-k+1..g] valid iff avail[g] >= k): per level its context's
 // slot (or -1) into qslot[i]; with count outputs (tot != NULL) tot / dist / cnt of the position into row g, column ci
-// of [n, nc] arrays (cnt: the count of tok[g+1] if has_next[g]).
+// of [n, nc] arrays (cnt: the count of tok[g+1] if has_next[g]). rec: the level's records, rw words each.
 template <int K>
 __device__ __forceinline__ void query_one(const u16* __restrict__ tok, const int* __restrict__ avail,
                                           const unsigned char* __restrict__ has_next, const int* __restrict__ pos,
                                           i64 i, int k, const u64* __restrict__ ck, u64 ccap,
-                                          const u64* __restrict__ pk, const u32* __restrict__ pcnt, u64 pcap,
-                                          const u32* __restrict__ ctx_tot, const u32* __restrict__ ctx_dist,
+                                          const u64* __restrict__ pt, u64 pcap, const u32* __restrict__ rec, int rw,
                                           int* __restrict__ qslot, u32* __restrict__ tot, u16* __restrict__ dist,
                                           u32* __restrict__ cnt, int nc, int ci) {
     const i64 g = pos[i];
     i64 slot = -1;
     if (avail[g] >= (K > 0 ? K : k)) slot = octx_find(ck, ccap, okey<K>(tok + g + 1, k));
-    if (slot >= 0 && ctx_tot[slot] == 0) slot = -1;
+    uint2 td = make_uint2(0u, 0u);  // the context's total and distinct count: one load
+    if (slot >= 0) td = *(const uint2*)(rec + slot * rw);
+    if (td.x == 0) slot = -1;
     if (qslot) qslot[i] = (int)slot;
     if (tot && slot >= 0) {
         const i64 at = g * nc + ci;
-        tot[at] = ctx_tot[slot];
-        const u32 d = ctx_dist[slot];
-        dist[at] = (u16)(d < 65535u ? d : 65535u);
-        cnt[at] = has_next[g] ? opair_count(pk, pcnt, pcap, ((u64)slot << 16) | tok[g + 1]) : 0u;
+        tot[at] = td.x;
+        dist[at] = (u16)(td.y < 65535u ? td.y : 65535u);
+        cnt[at] = has_next[g] ? opair_count(pt, pcap, ((u64)slot << 16) | tok[g + 1]) : 0u;
     }
 }
 
 template <int K>
 __global__ void online_query_k(const u16* __restrict__ tok, const int* __restrict__ avail,
                                const unsigned char* __restrict__ has_next, const int* __restrict__ pos, i64 m, int k,
-                               const u64* __restrict__ ck, u64 ccap, const u64* __restrict__ pk,
-                               const u32* __restrict__ pcnt, u64 pcap, const u32* __restrict__ ctx_tot,
-                               const u32* __restrict__ ctx_dist, int* __restrict__ qslot, u32* __restrict__ tot,
+                               const u64* __restrict__ ck, u64 ccap, const u64* __restrict__ pt, u64 pcap,
+                               const u32* __restrict__ rec, int rw, int* __restrict__ qslot, u32* __restrict__ tot,
                                u16* __restrict__ dist, u32* __restrict__ cnt, int nc, int ci) {
     const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
-    if (i < m)
-        query_one<K>(tok, avail, has_next, pos, i, k, ck, ccap, pk, pcnt, pcap, ctx_tot, ctx_dist, qslot, tot, dist,
-                     cnt, nc, ci);
+    if (i < m) query_one<K>(tok, avail, has_next, pos, i, k, ck, ccap, pt, pcap, rec, rw, qslot, tot, dist, cnt, nc, ci);
 }
 
 // Every level's queries of a step in one launch (the same reason and layout as online_insert_levels_k).
-#define ONLINE_QRY_FIELDS 14
+#define ONLINE_QRY_FIELDS 13
 struct OQryArgs {
     i64 f[ONLINE_MAXL][ONLINE_QRY_FIELDS];
 };
@@ -795,9 +835,9 @@ template <int K>
 __device__ __forceinline__ void query_level(const u16* __restrict__ tok, const int* __restrict__ avail,
                                             const unsigned char* __restrict__ has_next, const int* __restrict__ pos,
                                             i64 i, const i64 (&f)[ONLINE_QRY_FIELDS]) {
-    query_one<K>(tok, avail, has_next, pos, i, (int)f[0], (const u64*)f[1], (u64)f[2], (const u64*)f[3],
-                 (const u32*)f[4], (u64)f[5], (const u32*)f[6], (const u32*)f[7], (int*)f[8], (u32*)f[9], (u16*)f[10],
-                 (u32*)f[11], (int)f[12], (int)f[13]);
+    query_one<K>(tok, avail, has_next, pos, i, (int)f[0], (const u64*)f[1], (u64)f[2], (const u64*)f[3], (u64)f[4],
+                 (const u32*)f[5], (int)f[6], (int*)f[7], (u32*)f[8], (u16*)f[9], (u32*)f[10], (int)f[11],
+                 (int)f[12]);
 }
 
 __global__ void __launch_bounds__(256) online_query_levels_k(const u16* __restrict__ tok, const int* __restrict__ avail,
@@ -826,20 +866,22 @@ __global__ void __launch_bounds__(256) online_query_levels_k(const u16* __restri
     }
 }
 
-// Position g's (query i's) hint rows: the deepest described levels (desc[v * 5 ...], deepest first: qslot (int [m]),
-// ctx_tot (u32), ctx_top (u64 [slots, E]), bucket, unused) whose context occurred, up to S of them, into its slots
+// Position g's (query i's) hint rows: the deepest described levels (desc[v * 3 ...], deepest first: qslot (int [m]),
+// the level's records (OREC_TOP words each), bucket) whose context occurred, up to S of them, into its slots
 // g * S + j: cell, E next tokens, weights, and (level not NULL) the level's bucket. Returns the slots filled.
 __device__ __forceinline__ int online_row(i64 g, i64 i, int nlv, const i64* __restrict__ desc, int E, int S,
                                           short* __restrict__ cell, u16* __restrict__ next, u16* __restrict__ weights,
                                           signed char* __restrict__ level) {
     int j = 0;
     for (int v = 0; v < nlv && j < S; ++v) {
-        const i64* d = desc + v * 5;
+        const i64* d = desc + v * 3;
         const int slot = ((const int*)d[0])[i];
         if (slot < 0) continue;
-        const u32 total = ((const u32*)d[1])[slot];
-        const u64* top = (const u64*)d[2] + (i64)slot * E;
-        const int b = (int)d[3];
+        ORec o;  // total and entries: one 64-byte record
+        orec_load((const u32*)d[1] + (i64)slot * OREC_TOP, o);
+        const u32 total = o.tot;
+        const u64* top = o.sc;
+        const int b = (int)d[2];
         const u32 top1 = (u32)(top[0] >> 16);
         int cb = 0, pb = 0;
         const u32 CE[6] = {2, 3, 5, 9, 17, 33};
@@ -903,19 +945,22 @@ __global__ void online_rows_k(const int* __restrict__ pos, i64 m, int nlv, const
             break;                                             \
     }
 
-// Insert the occurrences ending at pos[0..m) at level k; ev[i] = their pair keys | tag (EMPTY if a table was full:
-// flags). tag: the level's tag << tshift for ng_online_top (0 for one level), above every pair key of the tables.
-extern "C" int ng_online_insert(const u16* tok, const int* pos, i64 m, int k, u64* ck, u64 ccap, u64* pk, u32* pcnt,
-                                u64 pcap, u32* ctx_tot, u32* ctx_dist, u64* ev, u32* flags, u64 tag, void* stream) {
+// Insert the occurrences ending at pos[0..m) at level k, each counted in the pair table pt (pcap 16-byte slots) and,
+// with rec (rw words per context: OREC_TOP or OREC_CNT), in its context's total and distinct count (else
+// ng_online_top adds those); ev[i] = their pair keys | tag (EMPTY if a table was full: flags). tag: the level's tag <<
+// tshift for ng_online_top (0 for one level), above every pair key of the tables.
+extern "C" int ng_online_insert(const u16* tok, const int* pos, i64 m, int k, u64* ck, u64 ccap, u64* pt, u64 pcap,
+                                u32* rec, int rw, u64* ev, u32* flags, u64 tag, void* stream) {
     if (m <= 0) return 0;
     if (ccap == 0 || pcap == 0 || ccap > (1ull << 40) || (tag && tag < (ccap << 16))) return -1;
+    if (rec && rw != OREC_TOP && rw != OREC_CNT) return -1;
     hipStream_t st = (hipStream_t)stream;
-    OLEVELS(k, (online_insert_k<K><<<grid_for(m, 256), 256, 0, st>>>(tok, pos, m, k, ck, ccap, pk, pcnt, pcap, ctx_tot, ctx_dist, ev, flags, tag)));
+    OLEVELS(k, (online_insert_k<K><<<grid_for(m, 256), 256, 0, st>>>(tok, pos, m, k, ck, ccap, pt, pcap, rec, rw, ev, flags, tag)));
     return (int)hipGetLastError();
 }
 
-// The inserts of nlv (1..8) levels in one launch: lv[t * 11 ...] = level t's pos, m, k, ck, ccap, pk, pcnt, pcap, ev,
-// flags, tag (host memory, read before the call returns; the pointers device memory), each as ng_online_insert's
+// The inserts of nlv (1..8) levels in one launch: lv[t * 10 ...] = level t's pos, m, k, ck, ccap, pt, pcap, ev, flags,
+// tag (host memory, read before the call returns; the pointers device memory), each as ng_online_insert's
 // arguments of the same names (its totals and distinct counts left to ng_online_top). count_pairs 0: only the context
 // is found or inserted and the event written; each distinct pair is then counted once by ng_online_top (add_counts 1)
 // instead of one global atomic per occurrence. -1 on a bad level.
@@ -926,10 +971,10 @@ extern "C" int ng_online_insert_levels(const u16* tok, int nlv, const i64* lv, i
     for (int t = 0; t < nlv; ++t) {
         const i64* f = lv + (i64)t * ONLINE_INS_FIELDS;
         const i64 m = f[1], k = f[2];
-        const u64 ccap = (u64)f[4], pcap = (u64)f[7], tag = (u64)f[10];
+        const u64 ccap = (u64)f[4], pcap = (u64)f[6], tag = (u64)f[9];
         if (m < 0 || k < 1 || k > MAXK || ccap == 0 || pcap == 0 || ccap > (1ull << 40) || (tag && tag < (ccap << 16)))
             return -1;
-        if (m > 0 && (!f[0] || !f[3] || !f[5] || !f[6] || !f[8] || !f[9])) return -1;
+        if (m > 0 && (!f[0] || !f[3] || !f[5] || !f[7] || !f[8])) return -1;
         for (int q = 0; q < ONLINE_INS_FIELDS; ++q) a.f[t][q] = f[q];
         mmax = m > mmax ? m : mmax;
     }
@@ -939,16 +984,18 @@ extern "C" int ng_online_insert_levels(const u16* tok, int nlv, const i64* lv, i
     return (int)hipGetLastError();
 }
 
-// The queries pos[0..m) of nlv (1..8) levels in one launch: lv[t * 14 ...] = level t's k, ck, ccap, pk, pcnt, pcap,
-// ctx_tot, ctx_dist, qslot, tot, dist, cnt, nc, ci (host memory; as ng_online_query's arguments of the same names).
+// The queries pos[0..m) of nlv (1..8) levels in one launch: lv[t * 13 ...] = level t's k, ck, ccap, pt, pcap, rec, rw,
+// qslot, tot, dist, cnt, nc, ci (host memory; as ng_online_query's arguments of the same names).
 extern "C" int ng_online_query_levels(const u16* tok, const int* avail, const unsigned char* has_next, const int* pos,
                                       i64 m, int nlv, const i64* lv, void* stream) {
     if (nlv < 1 || nlv > ONLINE_MAXL || !lv) return -1;
     OQryArgs a{};
     for (int t = 0; t < nlv; ++t) {
         const i64* f = lv + (i64)t * ONLINE_QRY_FIELDS;
-        if (f[0] < 1 || f[0] > MAXK || f[2] <= 0 || f[5] <= 0 || !f[1] || !f[3] || !f[4] || !f[6] || !f[7]) return -1;
-        if (f[9] && (!f[10] || !f[11] || f[12] < 1 || f[13] < 0 || f[13] >= f[12])) return -1;
+        if (f[0] < 1 || f[0] > MAXK || f[2] <= 0 || f[4] <= 0 || !f[1] || !f[3] || !f[5] ||
+            (f[6] != OREC_TOP && f[6] != OREC_CNT))
+            return -1;
+        if (f[8] && (!f[9] || !f[10] || f[11] < 1 || f[12] < 0 || f[12] >= f[11])) return -1;
         for (int q = 0; q < ONLINE_QRY_FIELDS; ++q) a.f[t][q] = f[q];
     }
     if (m <= 0) return 0;
@@ -959,8 +1006,9 @@ extern "C" int ng_online_query_levels(const u16* tok, const int* avail, const un
 
 // A step's distinct touched pairs of every level at once, uk[0..*n) (sorted tagged keys: level t's pair keys | t <<
 // tshift; agg: their occurrences in the step), merged into their contexts' totals, distinct counts and, where the
-// level keeps them, top-E lists; desc[t * 7 ...] describes level t (OLevel: pair keys, counts, capacity, top lists or
-// 0, totals, distinct counts, flags; device memory), ntag levels. score: scratch [m]. add_counts: the pairs' counts
+// level keeps them, top-E lists; desc[t * 5 ...] describes level t (OLevel: the pair table, its capacity, the records,
+// 1 if they hold top lists (OREC_TOP words) else 0 (OREC_CNT), flags; device memory), ntag levels. score: scratch
+// [m]. add_counts: the pairs' counts
 // grow here by agg (pairs inserted as needed; a full table sets the level's flags[0] bit 0), after inserts made with
 // count_pairs 0; else the inserts counted them.
 extern "C" int ng_online_top(const u64* uk, const i64* n, i64 m, const u32* agg, const i64* desc, int ntag, int tshift,
@@ -1018,12 +1066,12 @@ extern "C" int ng_online_merge(void* temp, size_t* temp_bytes, const u64* ev, i6
 }
 
 extern "C" int ng_online_query(const u16* tok, const int* avail, const unsigned char* has_next, const int* pos, i64 m,
-                               int k, const u64* ck, u64 ccap, const u64* pk, const u32* pcnt, u64 pcap,
-                               const u32* ctx_tot, const u32* ctx_dist, int* qslot, u32* tot, u16* dist, u32* cnt,
-                               int nc, int ci, void* stream) {
+                               int k, const u64* ck, u64 ccap, const u64* pt, u64 pcap, const u32* rec, int rw,
+                               int* qslot, u32* tot, u16* dist, u32* cnt, int nc, int ci, void* stream) {
     if (m <= 0) return 0;
+    if (!rec || (rw != OREC_TOP && rw != OREC_CNT)) return -1;
     hipStream_t st = (hipStream_t)stream;
-    OLEVELS(k, (online_query_k<K><<<grid_for(m, 256), 256, 0, st>>>(tok, avail, has_next, pos, m, k, ck, ccap, pk, pcnt, pcap, ctx_tot, ctx_dist, qslot, tot, dist, cnt, nc, ci)));
+    OLEVELS(k, (online_query_k<K><<<grid_for(m, 256), 256, 0, st>>>(tok, avail, has_next, pos, m, k, ck, ccap, pt, pcap, rec, rw, qslot, tot, dist, cnt, nc, ci)));
     return (int)hipGetLastError();
 }
 

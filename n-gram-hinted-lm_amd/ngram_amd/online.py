@@ -26,6 +26,7 @@ from .lib import Lib, i32, u64
 
 
 MAX_LAUNCH_LEVELS = 8  # levels per fused insert / query launch (ng_online_insert_levels, ng_online_query_levels)
+REC_TOP, REC_CNT = 16, 2  # u32 words of a context's record with and without top entries (online.hip OREC_*)
 
 
 def _ptr(t: torch.Tensor, at: int = 0) -> int:
@@ -219,15 +220,15 @@ class OnlineRows:
             o = torch.sort(alpha, stable=True).indices
             m = int(occ.numel())
             cap = max(1 << 16, int(m / LOAD) + 1)
+            # the pair table: 16-byte slots (key, count); a record per context: total, distinct count and, where the
+            # level keeps hint rows, its top entries (REC_TOP u32 words: one 64-byte line), else REC_CNT words
+            pt = torch.full((cap, 2), -1, dtype=torch.int64, device=dev)
+            pt[:, 1] = 0
+            rw = REC_TOP if k in levels else REC_CNT
             st["levels"][k] = {
                 "occ": occ[o].to(torch.int32).contiguous(), "alpha": alpha[o].cpu().numpy(),
                 "ck": torch.full((cap,), -1, dtype=torch.int64, device=dev), "ccap": cap,
-                "pk": torch.full((cap,), -1, dtype=torch.int64, device=dev),
-                "pcnt": torch.zeros(cap, dtype=torch.int32, device=dev), "pcap": cap,
-                "tot": torch.zeros(cap, dtype=torch.int32, device=dev),
-                "dist": torch.zeros(cap, dtype=torch.int32, device=dev),
-                "top": torch.zeros(cap * E, dtype=torch.int64, device=dev) if k in levels else
-                torch.zeros(1, dtype=torch.int64, device=dev),
+                "pt": pt, "pcap": cap, "rec": torch.zeros(cap * rw, dtype=torch.int32, device=dev), "rw": rw,
                 "flags": torch.zeros(2, dtype=torch.int32, device=dev),
                 "ctx_bits": max(1, (cap - 1).bit_length()),
             }
@@ -239,8 +240,7 @@ class OnlineRows:
             raise ValueError("the online tables are too large for one step's tagged pair keys")
         desc = []
         for k, lv in st["levels"].items():
-            desc += [lv["pk"].data_ptr(), lv["pcnt"].data_ptr(), lv["pcap"],
-                     lv["top"].data_ptr() if k in levels else 0, lv["tot"].data_ptr(), lv["dist"].data_ptr(),
+            desc += [lv["pt"].data_ptr(), lv["pcap"], lv["rec"].data_ptr(), int(lv["rw"] == REC_TOP),
                      lv["flags"].data_ptr()]
         st["top_desc"] = torch.tensor(desc, dtype=torch.int64, device=dev)
         per_step = np.zeros(1, np.int64)
@@ -276,7 +276,7 @@ class OnlineRows:
             desc = []
             for k in sorted(levels, reverse=True):
                 lv = st["levels"][k]
-                desc += [st["qslot"][k].data_ptr(), lv["tot"].data_ptr(), lv["top"].data_ptr(), buckets.index(k), 0]
+                desc += [st["qslot"][k].data_ptr(), lv["rec"].data_ptr(), buckets.index(k)]
             st["rows_desc"] = torch.tensor(desc, dtype=torch.int64, device=dev)
         return st
 
@@ -297,8 +297,8 @@ class OnlineRows:
             # the pair counts, totals and distinct counts are added per distinct pair and per context by the sorted
             # pass (ng_online_top), not per occurrence: no global atomic per occurrence, no chains of same-address
             # atomics on hot contexts
-            ins.append((_ptr(lv["occ"], a), b - a, k, _ptr(lv["ck"]), lv["ccap"], _ptr(lv["pk"]), _ptr(lv["pcnt"]),
-                        lv["pcap"], _ptr(st["ev"], m), _ptr(lv["flags"]), t << st["tshift"]))
+            ins.append((_ptr(lv["occ"], a), b - a, k, _ptr(lv["ck"]), lv["ccap"], _ptr(lv["pt"]), lv["pcap"],
+                        _ptr(st["ev"], m), _ptr(lv["flags"]), t << st["tshift"]))
             m += b - a
         for j in range(0, len(ins), MAX_LAUNCH_LEVELS):  # every level's inserts in one launch
             part = ins[j : j + MAX_LAUNCH_LEVELS]
@@ -321,8 +321,8 @@ class OnlineRows:
         for k in list(count_levels) + [k for k in levels if k not in count_levels]:
             lv = st["levels"][k]
             ci = count_levels.index(k) if k in count_levels else -1
-            qry.append((k, _ptr(lv["ck"]), lv["ccap"], _ptr(lv["pk"]), _ptr(lv["pcnt"]), lv["pcap"], _ptr(lv["tot"]),
-                        _ptr(lv["dist"]), _ptr(st["qslot"][k]) if k in levels else 0,
+            qry.append((k, _ptr(lv["ck"]), lv["ccap"], _ptr(lv["pt"]), lv["pcap"], _ptr(lv["rec"]), lv["rw"],
+                        _ptr(st["qslot"][k]) if k in levels else 0,
                         _ptr(outs["tot"]) if ci >= 0 else 0, _ptr(outs["dist"]) if ci >= 0 else 0,
                         _ptr(outs["cnt"]) if ci >= 0 else 0, nc if ci >= 0 else 1, max(ci, 0)))
         for j in range(0, len(qry), MAX_LAUNCH_LEVELS):  # every level's queries in one launch

@@ -190,8 +190,8 @@ class _PerLevelRows(OnlineRows):
             a, b = self._range(lv["alpha"], s, s + 1)
             if b == a:
                 continue
-            lib("ng_online_insert", self.tok, lv["occ"][a:b], b - a, i32(k), lv["ck"], u64(lv["ccap"]), lv["pk"],
-                lv["pcnt"], u64(lv["pcap"]), None, None, st["ev"][m:], lv["flags"], u64(t << st["tshift"]))
+            lib("ng_online_insert", self.tok, lv["occ"][a:b], b - a, i32(k), lv["ck"], u64(lv["ccap"]), lv["pt"],
+                u64(lv["pcap"]), None, i32(0), st["ev"][m:], lv["flags"], u64(t << st["tshift"]))
             m += b - a
         if m:
             lib.cub("sort_pairs", st["ev"], st["ev_sorted"], None, None, m, i32(0), i32(st["tshift"] + st["tag_bits"]))
@@ -205,14 +205,14 @@ class _PerLevelRows(OnlineRows):
         for ci, k in enumerate(count_levels):
             lv = st["levels"][k]
             lib("ng_online_query", self.tok, self.avail, self.has_next, qpos, qb - qa, i32(k), lv["ck"],
-                u64(lv["ccap"]), lv["pk"], lv["pcnt"], u64(lv["pcap"]), lv["tot"], lv["dist"],
+                u64(lv["ccap"]), lv["pt"], u64(lv["pcap"]), lv["rec"], i32(lv["rw"]),
                 st["qslot"][k] if k in levels else None, outs["tot"], outs["dist"], outs["cnt"], i32(len(count_levels)),
                 i32(ci))
         for k in levels:
             if k not in count_levels:
                 lv = st["levels"][k]
                 lib("ng_online_query", self.tok, self.avail, self.has_next, qpos, qb - qa, i32(k), lv["ck"],
-                    u64(lv["ccap"]), lv["pk"], lv["pcnt"], u64(lv["pcap"]), lv["tot"], lv["dist"], st["qslot"][k],
+                    u64(lv["ccap"]), lv["pt"], u64(lv["pcap"]), lv["rec"], i32(lv["rw"]), st["qslot"][k],
                     None, None, None, i32(1), i32(0))
         if levels:
             lib("ng_online_rows", qpos, qb - qa, i32(len(levels)), st["rows_desc"], i32(st["E"]), i32(outs["slots"]),
