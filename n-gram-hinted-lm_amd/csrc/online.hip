@@ -487,14 +487,16 @@ __global__ void __launch_bounds__(1024) om_hist_k(const u64* __restrict__ ev, i6
 // Bucket b = the events evb[dpre[b * nseg], dpre[(b + 1) * nseg]) (the last one ends at m). cb: the count bits of
 // the packed words (a pair's occurrences in the step < 2^cb - 1).
 __global__ void __launch_bounds__(OM_BLOCK) __attribute__((amdgpu_waves_per_eu(4))) om_merge_k(const u64* __restrict__ evb, const u32* __restrict__ dpre,
-                                                       i64 nseg, i64 m, const i64* __restrict__ desc, int tshift,
-                                                       int cb, int E) {
+                                                       i64 nseg, i64 m, const i64* __restrict__ desc, int ntag,
+                                                       int tshift, int cb, int E) {
     __shared__ u64 hs[OM_H];
     __shared__ u32 cs[OM_DCAP];
     __shared__ u32 s_part[OM_BLOCK / WAVE];
     __shared__ u64 s_stack[OM_MAXSPLIT + 2];  // pending rounds: residue << 8 | log2 of the rounds
     __shared__ int s_sp, s_nd, s_over;
+    __shared__ i64 s_desc[ONLINE_MAXL * OLEVEL_FIELDS];  // the levels' descriptors: no global load before a lookup
     const int t = threadIdx.x, lane = lane_id(), wid = t / WAVE;
+    for (int i = t; i < ONLINE_MAXL * OLEVEL_FIELDS; i += OM_BLOCK) s_desc[i] = i < ntag * OLEVEL_FIELDS ? desc[i] : 0;
     const int hb = tshift - 16 - OM_BITS;  // slot bits above the bucket's
     const u64 hbm = (1ull << hb) - 1;
     const u64 cmask = (1ull << cb) - 1;
@@ -626,7 +628,7 @@ __global__ void __launch_bounds__(OM_BLOCK) __attribute__((amdgpu_waves_per_eu(4
                         const u64 hi = kp >> 16;
                         tg[j] = (u32)(hi >> hb);
                         key[j] = ((((hi & hbm) << OM_BITS) | (u64)b) << 16) | (kp & 0xFFFF);
-                        const OLevel lv = olevel(desc, tg[j]);
+                        const OLevel lv = olevel(s_desc, tg[j]);
                         at[j] = (i64)__umul64hi(mix64(key[j]), lv.pcap);
                         const ulonglong2 v = *(const ulonglong2*)(lv.pt + 2 * at[j]);  // key and count: one load
                         cur[j] = v.x;
@@ -637,7 +639,7 @@ __global__ void __launch_bounds__(OM_BLOCK) __attribute__((amdgpu_waves_per_eu(4
                 for (int j = 0; j < OM_PB; ++j) {
                     const int i = i0 + j * OM_BLOCK + t;
                     if (i >= D) continue;
-                    const OLevel lv = olevel(desc, tg[j]);
+                    const OLevel lv = olevel(s_desc, tg[j]);
                     if (cur[j] != key[j]) {
                         at[j] = opair_slot(lv.pt, lv.pcap, key[j], lv.flags);
                         cc[j] = at[j] >= 0 ? *opair_cnt(lv.pt, at[j]) : 0;
@@ -671,7 +673,7 @@ __global__ void __launch_bounds__(OM_BLOCK) __attribute__((amdgpu_waves_per_eu(4
                 int e = -1;  // where this head's context ends, if in the window
                 if (head && (tails >> lane)) e = lane + __ffsll((unsigned long long)(tails >> lane)) - 1;
                 if (e >= 0 && e - lane + 1 <= ONLINE_SHORT) {  // a short context ending in the window: this lane alone
-                    const OLevel lv = olevel(desc, cx >> hb);
+                    const OLevel lv = olevel(s_desc, cx >> hb);
                     const u64 slot = ((cx & hbm) << OM_BITS) | (u64)b;
                     const u32 ge = wv * WAVE + (u32)e;
                     u32 add = 0, fresh = 0;
@@ -711,7 +713,7 @@ __global__ void __launch_bounds__(OM_BLOCK) __attribute__((amdgpu_waves_per_eu(4
                     waved &= waved - 1;
                     const int eh = __shfl(e, h, WAVE);  // -1: the context runs past the window
                     const u64 hc = bcast_u64(cx, h);
-                    const OLevel lv = olevel(desc, hc >> hb);
+                    const OLevel lv = olevel(s_desc, hc >> hb);
                     u32* const hr = lv.at(((hc & hbm) << OM_BITS) | (u64)b);
                     const u32 gi = wv * WAVE + (u32)h;
                     const bool in = valid && lane >= h && (eh < 0 || lane <= eh);
@@ -1061,7 +1063,7 @@ extern "C" int ng_online_merge(void* temp, size_t* temp_bytes, const u64* ev, i6
     if (rc) return rc;
     if ((rc = prim::exclusive_scan_u32(hist, hist, nh, nullptr, stemp, st))) return rc;
     if ((rc = ng_seg_scatter(ev, OM_CHUNK, nullptr, seg_n, hist, nseg, 16, OM_BITS, evb, (u64)m, stream))) return rc;
-    om_merge_k<<<OM_NB, OM_BLOCK, 0, st>>>(evb, hist, nseg, m, desc, tshift, cb, E);
+    om_merge_k<<<OM_NB, OM_BLOCK, 0, st>>>(evb, hist, nseg, m, desc, ntag, tshift, cb, E);
     return (int)hipGetLastError();
 }
 
