@@ -465,7 +465,7 @@ __global__ void __launch_bounds__(WAVE) online_top_k(const u64* __restrict__ uk,
 #define OM_CHUNK 8192    // events per histogram segment (ng_seg_scatter's segments)
 #define OM_PER (OM_H / OM_BLOCK)
 #define OM_EV 8       // events a thread loads at once
-#define OM_PB 1       // pairs a thread looks up at once (2 and 4 were 3-5% slower: fewer waves fit)
+#define OM_PB 1       // pairs a thread looks up at once (2 and 4 measured 3-5% slower)
 
 // Per segment of OM_CHUNK events, its count per bucket (digit-major: hist[d * nseg + s]) and its size.
 __global__ void __launch_bounds__(1024) om_hist_k(const u64* __restrict__ ev, i64 m, i64 nseg, u32* __restrict__ hist,
