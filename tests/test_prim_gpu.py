@@ -36,6 +36,19 @@ def test_sort_pairs_is_a_stable_radix_sort(lib, n, b0, b1, dups):
     assert np.array_equal(kout.cpu().numpy().view(np.uint64), keys[order])
 
 
+@pytest.mark.parametrize("n,b0,b1", [(3_000_000, 0, 64), (20_000_000, 56, 64), (9_000_001, 20, 37)])
+def test_sort_keys_only_across_many_tiles(lib, n, b0, b1):
+    """Keys without values past 256 tiles (each pass's tile offsets from a histogram pass and a scan)."""
+    rng = np.random.default_rng(n)
+    keys = rng.integers(0, 2 ** 63, size=n, dtype=np.int64).astype(np.uint64) * np.uint64(2)
+    kin = _t(keys.view(np.int64))
+    kout = torch.empty_like(kin)
+    lib.cub("sort_pairs", kin, kout, None, None, n, i32(b0), i32(b1))
+    width = b1 - b0
+    sk = (keys >> np.uint64(b0)) & np.uint64((1 << width) - 1) if width < 64 else keys
+    assert np.array_equal(kout.cpu().numpy().view(np.uint64), keys[np.argsort(sk, kind="stable")])
+
+
 def test_sort_pairs_empty_and_temp_query(lib):
     kin = torch.zeros(0, dtype=torch.int64, device="cuda")
     lib.cub("sort_pairs", kin, torch.empty_like(kin), None, None, 0, i32(0), i32(64))
