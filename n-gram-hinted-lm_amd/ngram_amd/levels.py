@@ -96,7 +96,8 @@ class LevelBuild:
             torch.cuda.current_stream().wait_event(self.ready[i])
 
     def build(self, x: torch.Tensor, tgt: torch.Tensor, avail: torch.Tensor, *, topk: int = 0,
-              cnt_top: int | None = None, keep=(), with_mask: bool = False, stats: bool = False) -> LevelOutputs:
+              cnt_top: int | None = None, keep=(), with_mask: bool = False, stats: bool = False,
+              _defer: bool = True) -> LevelOutputs:
         """Counts of every level for the N query positions (x int16 [N], tgt int16 [N], avail int32 [N]). `topk`: also
         each position's context's first topk entries; `cnt_top`: the TOP rule (cnt only if the target ranks below it);
         `keep`: levels whose records are returned (top-8); `stats`: each level's corpus hits in info."""
@@ -121,14 +122,18 @@ class LevelBuild:
         regions = torch.empty(n_reg, dtype=torch.int64, device=dev)
         out = res.counts
         deferred = []  # summarize's checks, read once after every level
+        pending = []  # query indexes sized from the last build's context counts, checked once after every level
         for li, k in enumerate(self.levels):
             t0 = time.perf_counter()
             prev = self.levels[li - 1] if li else None
             seen = None
             if prev is not None and self.level_shards[k] <= self.level_shards[prev]:
                 seen = torch.nonzero(out[1, li - 1] > 0).squeeze(1).to(torch.int32)
-            vi = QueryIndex(elib, x, avail, k, seen, expect=self.contexts_of.get(k))
-            self.contexts_of[k] = vi.n
+            vi = QueryIndex(elib, x, avail, k, seen, expect=self.contexts_of.get(k), defer=_defer)
+            if vi.n is None:
+                pending.append((k, vi.pending))
+            else:
+                self.contexts_of[k] = vi.n
             t1 = time.perf_counter()
             seg = self._emit(k, vi, x, bms, regions, R)
             t2 = time.perf_counter()
@@ -172,6 +177,17 @@ class LevelBuild:
             self.host_s["count"] += t3 - t2
             del vi, c, sm, thr, seen
         del regions
+        if pending:
+            checked = QueryIndex.check(pending)
+            redo = False
+            for (k, _), (n_ctx, ok) in zip(pending, checked):
+                self.contexts_of[k] = n_ctx  # the next build's tables are sized from these
+                res.info[k]["contexts"] = n_ctx
+                redo |= not ok
+            del pending, checked
+            if redo:  # an insert found no slot in a table sized from the last build: once more, each level checked
+                return self.build(x, tgt, avail, topk=topk, cnt_top=cnt_top, keep=keep, with_mask=with_mask,
+                                  stats=stats, _defer=False)
         check_summary(deferred)
         if stats:
             for li, k in enumerate(self.levels):

@@ -21,12 +21,15 @@ EXPECT_MARGIN = 1.2  # a table sized from an expected context count holds this m
 
 class QueryIndex:
     def __init__(self, lib: Lib, x: torch.Tensor, avail: torch.Tensor, k: int, positions: torch.Tensor | None = None,
-                 compact: bool = False, expect: int | None = None, _resized: bool = False):
+                 compact: bool = False, expect: int | None = None, _resized: bool = False, defer: bool = False):
         """Index the valid k-contexts of the query positions (all of x, or the int32 `positions`). `compact`: ctx_of
         holds one entry per listed position (in their order) instead of one per position of x. `expect`: about how
         many contexts there are (e.g. the last build's count): the table is sized for them at once instead of for
         every position and shrunk; if they turn out more than the table holds at LOAD, the index is built once more,
-        sized for the count found (`_resized` marks that second build, which keeps its table whatever its load)."""
+        sized for the count found (`_resized` marks that second build, which keeps its table whatever its load).
+        `defer` (with `expect`): the build's counters are not read here, so the host does not wait for the GPU; the
+        table sized from `expect` stands, `n` is None, and the caller must pass `pending` to `check()` and redo its
+        work if an insert found no slot (its context is then missing from the table)."""
         dev = x.device
         N = x.numel()
         m = N if positions is None else int(positions.numel())
@@ -47,6 +50,11 @@ class QueryIndex:
             if m:
                 lib("ng_query_index", x, avail, positions, m, i32(k), table, u64(cap), u64(slots), rep, ctx_of,
                     i32(int(compact and positions is not None)), counters)
+            if defer and expect is not None and not _resized:
+                self.pending = counters
+                self.n, self.cap, self.ids, self.table, self.rep, self.ctx_of = None, cap, slots, table, rep, ctx_of
+                self._valid = None
+                return
             c = counters.cpu().tolist()
             if c[1] == 0:
                 break
@@ -82,6 +90,20 @@ class QueryIndex:
         self.rep = rep
         self.ctx_of = ctx_of
         self._valid = None
+
+    @staticmethod
+    def check(pending: list) -> list[tuple[int, bool]]:
+        """Deferred builds' counters ((k, the index's `pending`) pairs), read in one copy: per index (n contexts,
+        whether every insert found its slot); a 64-bit key collision raises."""
+        if not pending:
+            return []
+        got = torch.stack([c for _, c in pending]).cpu().tolist()
+        out = []
+        for (k, _), (n, over, coll) in zip(pending, got):
+            if coll:
+                raise RuntimeError(f"k={k}: {coll} query positions collide with another context's key")
+            out.append((int(n), over == 0))
+        return out
 
     @property
     def valid(self) -> int:

@@ -109,18 +109,29 @@ def test_fit_blocks_start_segments(corpus):
 
 @pytest.mark.parametrize("margin", [1.2, 0.5])
 def test_context_hints_from_an_earlier_build(corpus, monkeypatch, margin):
-    """A build sizes its query indexes from the last build's context counts: far fewer contexts than expected (the
-    tables shrink), then far more (the indexes are built again at their size); every build matches the oracle. A
+    """A build sizes its query indexes from the last build's context counts without reading them back before its
+    scans: far fewer contexts than expected (the tables stand), then far more (inserts find no slot, so the build is
+    done once more with every index's counters read: `redo` counts those builds); every build matches the oracle. A
     margin below 1 (every table fuller than its aimed load) still builds each index at most twice."""
     from ngram_amd import qindex as Q
 
     monkeypatch.setattr(Q, "EXPECT_MARGIN", margin)
+    redo = []
+    build = levels_mod.LevelBuild.build
+
+    def counted(self, *a, **kw):
+        redo.append(kw.get("_defer", True) is False)
+        return build(self, *a, **kw)
+
+    monkeypatch.setattr(levels_mod.LevelBuild, "build", counted)
     cb = C.CountBuild(corpus.shards(), levels=LEVELS, level_shards={}, topk=4)
     cb.start_load(1)
     full = corpus.query
-    for q in (full, full[:3001], full):
+    for j, q in enumerate((full, full[:3001], full)):
+        redo.clear()
         x, tgt, avail = C.queries(q, [], "cuda")
         out = cb.counts(x, tgt, avail).cpu().numpy()
+        assert any(redo) == (j == 2), (j, redo)
         xs, ts = q[:-1], q[1:]
         av = O.segments(xs)
         for li, k in enumerate(LEVELS):
