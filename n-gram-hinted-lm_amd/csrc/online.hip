@@ -450,8 +450,8 @@ __global__ void __launch_bounds__(WAVE) online_top_k(const u64* __restrict__ uk,
 //   B. sorts the distinct pairs in LDS (bitonic), which makes each context's pairs consecutive,
 //   C. adds each pair's occurrences to its count in the level's pair table (one plain update: every pair of the step
 //      is in one bucket and one round),
-//   D. merges each context's total, distinct count and top-E list as online_top_k does, reading LDS only: a context
-//      with many pairs in the step is walked by the wave over LDS, not over global memory.
+//   D. merges each context's record (total, distinct count, top-E entries) as online_top_k does, with the step's pairs
+//      read from LDS: a context with many pairs in the step is walked by the wave over LDS, not over global memory.
 // A bucket with more than OM_DCAP distinct pairs is done in rounds, its events split by a hash of the pair (halving
 // until each round fits; nothing global is written before a round fits). A context whose pairs fall in several rounds
 // is merged once per round: each merge supersedes the old entries of the pairs it touches, and a pair touched in a
@@ -485,7 +485,8 @@ __global__ void __launch_bounds__(1024) om_hist_k(const u64* __restrict__ ev, i6
 }
 
 // Bucket b = the events evb[dpre[b * nseg], dpre[(b + 1) * nseg]) (the last one ends at m). cb: the count bits of
-// the packed words (a pair's occurrences in the step < 2^cb - 1).
+// the packed words (a pair's occurrences in the step < 2^cb - 1). At most 128 registers a lane (waves_per_eu 4), so
+// that two blocks share a CU (its LDS allows two); uncapped, the kernel took 141 and ran 15% slower at one block.
 __global__ void __launch_bounds__(OM_BLOCK) __attribute__((amdgpu_waves_per_eu(4))) om_merge_k(const u64* __restrict__ evb, const u32* __restrict__ dpre,
                                                        i64 nseg, i64 m, const i64* __restrict__ desc, int ntag,
                                                        int tshift, int cb, int E) {
