@@ -151,10 +151,12 @@ int ng_scan_sink(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, ui
 int ng_bits_list(void* temp, size_t* temp_bytes, const uint32_t* bm, ng_i64 nwords, ng_u64* out, ng_u64* total,
                  const uint32_t* pre, void* stream);
 /* existence only: hit bitmap and bit (context id) of the u32 words hit set (hit zeroed by the caller); ids (may be
- * NULL): ids[p] = the context id at each hit position p; sparse as ng_scan_count's */
+ * NULL): ids[p] = the context id at each hit position p; sparse as ng_scan_count's; pre (may be NULL): the prefix
+ * rule's device flag, as ng_scan_emit's (valid where every query context's prefix is a query context of the level
+ * before) */
 int ng_scan_exist(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, uint32_t* bm_out, const ng_u64* vt,
                   ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, uint32_t* hit, uint32_t* ids, uint32_t* flags,
-                  int grid, int sparse, void* stream);
+                  int grid, int sparse, const uint32_t* pre, void* stream);
 /* a level's counting scan from ng_scan_exist's ids: each position set in bm whose context's bit is set in `final`
  * emits mix64(id << 16 | tok[p]) as ng_scan_emit's events (regions, ev_count, dhist); L a multiple of 32, tok
  * 8-byte and ids 16-byte aligned */

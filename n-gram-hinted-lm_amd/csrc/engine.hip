@@ -619,11 +619,11 @@ extern "C" int ng_scan_count(const u16* tok, i64 L, int k, const u32* bm_in, u32
 // ng_scan_count's.
 extern "C" int ng_scan_exist(const u16* tok, i64 L, int k, const u32* bm_in, u32* bm_out, const u64* vt, u64 vcap,
                              const u32* vrep, const u16* x, u32* hit, u32* ids, u32* flags, int grid, int sparse,
-                             void* stream) {
+                             const u32* pre, void* stream) {
     if (L <= 0) return 0;
     if (grid <= 0) grid = grid_for(L, 256);
     if (launch_scan(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, ExistSink{hit, ids}, flags, grid, sparse,
-                    (hipStream_t)stream) != 0)
+                    (hipStream_t)stream, pre) != 0)
         return -1;
     return (int)hipGetLastError();
 }

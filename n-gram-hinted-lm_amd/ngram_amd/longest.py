@@ -77,6 +77,15 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
     levels: list[tuple[str, torch.Tensor, int]] = []
     ladder = []
     flags = torch.zeros(2, dtype=torch.int32, device=dev)
+    # the prefix rule for the bitmap scans (a device flag, no host sync): with every position queried, a position
+    # still active at level k has its predecessor active at level k - 1 (its shorter context occurs wherever the
+    # longer one does), so where avail is segment-shaped a level's context also has its prefix among the level before's
+    # and a corpus position is probed only where the level before hit it and the position before it. A query mask can
+    # leave a predecessor out, so it turns the rule off.
+    pre = None
+    if query is None:
+        pre = torch.empty(1, dtype=torch.int32, device=dev)
+        elib("ng_avail_closed", avail, N, pre)
     for k in range(1, cap + 1):
         act = act[avail[act.long()] >= k]
         if act.numel() == 0:
@@ -103,7 +112,7 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
             ids = torch.empty(L, dtype=torch.int32, device=dev)  # each hit position's context id, for the counting
             mode = 0 if prev is None or prev[2] * 2 > L else 2  # a lane per position while the gate is dense
             elib("ng_scan_exist", tok, L, i32(k), None if prev is None else prev[1], bm, vi.table, u64(vi.cap),
-                 vi.rep, x, hit, ids, flags, i32(grid), i32(mode))
+                 vi.rep, x, hit, ids, flags, i32(grid), i32(mode), pre)
             levels.append(("bm", bm, _popcount(lib, bm), ids, act, vi.ctx_of, vi.ids))
         ctx = vi.ctx_of.long()
         c = ctx.clamp_min(0)
