@@ -57,11 +57,12 @@ struct CtxRecord {
     static constexpr int FIRST = WORDS - USED >= 2 ? USED : -1;
 };
 
+// A record's words (CtxRecord<KT>): total, pairs, the top tokens two per word, their counts, and (where room) the
+// first word's index.
 template <int KT>
-__device__ __forceinline__ void store_record(u32* __restrict__ rec, u64 c, u64 total, u32 pairs, const u64 (&top)[KT],
-                                             u64 first) {
+__device__ __forceinline__ void record_words(u32 (&v)[CtxRecord<KT>::WORDS], u64 total, u32 pairs,
+                                             const u64 (&top)[KT], u64 first) {
     using R = CtxRecord<KT>;
-    u32 v[R::WORDS];
 #pragma unroll
     for (int q = 0; q < R::WORDS; ++q) v[q] = 0;
     v[0] = (u32)total;
@@ -76,6 +77,14 @@ __device__ __forceinline__ void store_record(u32* __restrict__ rec, u64 c, u64 t
         v[2 + r / 2] |= tk << (16 * (r & 1));
         v[2 + R::TOKW + r] = (u32)(top[r] >> 16);
     }
+}
+
+template <int KT>
+__device__ __forceinline__ void store_record(u32* __restrict__ rec, u64 c, u64 total, u32 pairs, const u64 (&top)[KT],
+                                             u64 first) {
+    using R = CtxRecord<KT>;
+    u32 v[R::WORDS];
+    record_words<KT>(v, total, pairs, top, first);
     uint4* dst = (uint4*)(rec + c * R::WORDS);
 #pragma unroll
     for (int q = 0; q < R::WORDS / 4; ++q) dst[q] = make_uint4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);

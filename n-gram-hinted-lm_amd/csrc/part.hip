@@ -436,6 +436,9 @@ __global__ void __launch_bounds__(WAVE) ctx_summary_k(const u64* __restrict__ w,
         if (deep && pairs > deep_min) deep[atomicAdd(&nstat[0], 1u)] = (i64)c;
     };
     __shared__ u64 sw[WAVE];
+    using R = CtxRecord<KT>;
+    __shared__ uint4 s_rec[WAVE * R::WORDS / 4];  // the short contexts' records of a window, stored together below
+    __shared__ u64 s_ctx[WAVE];
     const int sh = 64 - cb, csh = 48 - cb;
     const u64 esc = (1ull << csh) - 1;
     const int lane = lane_id();
@@ -471,6 +474,7 @@ __global__ void __launch_bounds__(WAVE) ctx_summary_k(const u64* __restrict__ w,
         if (head && (tails >> lane)) e = lane + __ffsll((unsigned long long)(tails >> lane)) - 1;
         const bool walk = e >= 0 && e - lane + 1 <= SUMMARY_SHORT;
         u64 longs = __ballot(e >= 0 && !walk);
+        const u64 walks = __ballot(walk);
         if (walk) {
             u64 tl[KT];
 #pragma unroll
@@ -483,8 +487,22 @@ __global__ void __launch_bounds__(WAVE) ctx_summary_k(const u64* __restrict__ w,
                 topk_insert<KT>(tl, rank_score(wj >> csh, n));
             }
             done(ctx, (u32)(e - lane + 1));
-            store_record<KT>(rec, ctx, s, (u32)(e - lane + 1), tl, (u64)i);
+            u32 v[R::WORDS];
+            record_words<KT>(v, s, (u32)(e - lane + 1), tl, (u64)i);
+            const int j = __popcll(walks & lanemask_lt());
+#pragma unroll
+            for (int q = 0; q < R::WORDS / 4; ++q)
+                s_rec[j * (R::WORDS / 4) + q] = make_uint4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+            s_ctx[j] = ctx;
             if (s >> 32) atomicOr(&flags[0], 4u);
+        }
+        if (walks) {  // wave-uniform: the records leave as 16-byte chunks of consecutive lanes, a record's chunks side
+                      // by side (one request per record where a lane storing its own made one per chunk)
+            __syncthreads();
+            constexpr int CH = R::WORDS / 4;
+            const int nrec = __popcll(walks);
+            for (int q = lane; q < nrec * CH; q += WAVE)
+                ((uint4*)(rec + s_ctx[q / CH] * R::WORDS))[q % CH] = s_rec[q];
         }
         while (longs) {  // wave-uniform
             const int h = __ffsll((unsigned long long)longs) - 1;
