@@ -232,8 +232,8 @@ class OnlineRows:
                 "flags": torch.zeros(2, dtype=torch.int32, device=dev),
                 "ctx_bits": max(1, (cap - 1).bit_length()),
             }
-        # a step's events of every level go through one sort, one reduce and one merge, each level's pair keys tagged
-        # with its index above the widest level's pair-key bits (ng_online_insert's tag, ng_online_top's desc)
+        # a step's events of every level go through one merge (ng_online_merge, or the sorted one), each level's pair
+        # keys tagged with its index above the widest level's pair-key bits (ng_online_insert's tag, the merge's desc)
         st["tshift"] = 16 + max(lv["ctx_bits"] for lv in st["levels"].values())
         st["tag_bits"] = max(1, (len(st["levels"]) - 1).bit_length())
         if st["tshift"] + st["tag_bits"] > 64:
@@ -252,11 +252,6 @@ class OnlineRows:
                 per_step[: len(c)] += c
         most = max(1, int(per_step.max()))
         st["ev"] = torch.empty(most, dtype=torch.int64, device=dev)
-        st["ev_sorted"] = torch.empty(most, dtype=torch.int64, device=dev)
-        st["uk"] = torch.empty(most, dtype=torch.int64, device=dev)
-        st["agg"] = torch.empty(most, dtype=torch.int32, device=dev)
-        st["nruns"] = torch.zeros(1, dtype=torch.int64, device=dev)
-        st["score"] = torch.empty(most, dtype=torch.int64, device=dev)
         st["merge_temp"] = None
         if self.merge == "buckets":
             size = ctypes.c_size_t(0)
@@ -268,6 +263,12 @@ class OnlineRows:
             if size is not None:
                 st["merge_size"] = size
                 st["merge_temp"] = torch.empty(max(1, size.value), dtype=torch.uint8, device=dev)
+        if st["merge_temp"] is None:  # the sorted merge's buffers
+            st["ev_sorted"] = torch.empty(most, dtype=torch.int64, device=dev)
+            st["uk"] = torch.empty(most, dtype=torch.int64, device=dev)
+            st["agg"] = torch.empty(most, dtype=torch.int32, device=dev)
+            st["nruns"] = torch.zeros(1, dtype=torch.int64, device=dev)
+            st["score"] = torch.empty(most, dtype=torch.int64, device=dev)
         nq = int(np.bincount(st["q_step"]).max()) if len(st["q_step"]) else 1
         st["qslot"] = {k: torch.empty(max(1, nq), dtype=torch.int32, device=dev) for k in levels}
         st["hinted"] = torch.zeros(1, dtype=torch.int32, device=dev)
@@ -294,9 +295,9 @@ class OnlineRows:
             a, b = self._range(lv["alpha"], s, s + 1)
             if b == a:
                 continue
-            # the pair counts, totals and distinct counts are added per distinct pair and per context by the sorted
-            # pass (ng_online_top), not per occurrence: no global atomic per occurrence, no chains of same-address
-            # atomics on hot contexts
+            # the pair counts and the contexts' records are updated per distinct pair and per context by the step's
+            # merge, not per occurrence: no global atomic per occurrence, no chains of same-address atomics on hot
+            # contexts
             ins.append((_ptr(lv["occ"], a), b - a, k, _ptr(lv["ck"]), lv["ccap"], _ptr(lv["pt"]), lv["pcap"],
                         _ptr(st["ev"], m), _ptr(lv["flags"]), t << st["tshift"]))
             m += b - a

@@ -234,6 +234,7 @@ def test_step_entry_points_agree(stream, monkeypatch, how):
     want = O.online(tok, bounds, tau, tau_in, LEVELS, BUCKETS, 8, count_levels, 0, len(spans))
     if how == "per_level":
         rows = _PerLevelRows(tok, bounds, spans, 4, [])
+        rows.merge = "sorted"  # its steps use the sorted merge's buffers
     elif how == "sorted":
         rows = OnlineRows(tok, bounds, spans, 4, [])
         rows.merge = "sorted"
