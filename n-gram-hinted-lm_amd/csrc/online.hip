@@ -3,10 +3,10 @@
 // state persists between steps: a context table (u64 keys, slot = context id), a record per context (its total,
 // distinct next tokens and top-E entries, count descending then token ascending: one 64-byte load), and a pair table
 // of 16-byte slots ((slot << 16 | next) key beside its u32 count: one line per lookup). A step inserts the occurrences
-// that become available in it,
-// then answers its queries (online.rs:11-13: an occurrence counts for a step-s query iff all its tokens were trained
-// before s). The top-E lists stay exact: a step's touched pairs are sorted and merged into their context's list with
-// their new counts (counts only grow, so untouched tokens outside a list stay below its last entry).
+// that become available in it, then answers its queries (online.rs:11-13: an occurrence counts for a step-s query
+// iff all its tokens were trained before s). The top-E lists stay exact: a step's touched pairs are grouped by context
+// (in LDS buckets, ng_online_merge, or by a sort, ng_online_top) and merged into their context's list with their new
+// counts (counts only grow, so untouched tokens outside a list stay below its last entry).
 #include "ngram_common.h"
 #include "prim.h"
 
