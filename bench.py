@@ -619,6 +619,11 @@ def main() -> None:
         parity["mismatching_positions"] = sum(p["mismatching_positions"] for p in parity.values())
         res["parity"] = parity
     if not args.no_secondary:
+        # the same build with every shard copied from pinned host memory inside the step (PCIe included; `value`
+        # above is the resident-token figure)
+        log("pcie-inclusive c3")
+        res["pcie_inclusive"] = bench_load(cfg, tok, sizes, starts, q, 2)
+        res["pcie_inclusive"]["unit"] = "corpus tokens/s (tokens_per_s_with_load: shards copied inside the step)"
         del q
         torch.cuda.empty_cache()
         res["secondary"] = {}
