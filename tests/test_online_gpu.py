@@ -279,3 +279,28 @@ def test_context_with_more_pairs_than_a_merge_round(merge):
         assert np.array_equal(g, w), name
     assert hinted == want[-1]
     assert int(got[3][:, 0].max()) >= 6000  # the context's total reached the step's 6000 occurrences
+
+
+def test_many_count_levels(stream):
+    """Eight levels in one step's merge (three tag bits in the packed words) against the oracle's counts; nine levels
+    (more than ng_online_merge takes: the sorted merge runs) against those and, for the level past the oracle's
+    eight-token limit, the same level counted alone by the bucketed merge."""
+    tok, spans = stream
+    n = len(tok)
+    bounds = [0, n]
+    tau, tau_in = O.spans_tau(n, bounds, spans)
+    eight = [1, 2, 3, 4, 5, 6, 7, 8]
+    want = O.online(tok, bounds, tau, tau_in, [], [1], 1, eight, 0, len(spans))
+
+    def counts(levels):
+        nc = len(levels)
+        out = np.zeros((n, nc), np.uint32), np.zeros((n, nc), np.uint16), np.zeros((n, nc), np.uint32)
+        OnlineRows(tok, bounds, spans, 4, []).counts(levels, 0, len(spans), *out)
+        return out
+
+    got8, got9, alone = counts(eight), counts(eight + [10]), counts([10])
+    for j, name in enumerate(("tot", "dist", "cnt")):
+        assert np.array_equal(got8[j], want[3 + j]), name
+        assert np.array_equal(got9[j][:, :8], want[3 + j]), name
+        assert np.array_equal(got9[j][:, 8:], alone[j]), name
+    assert int(got8[0].max()) > 0 and int(alone[0].max()) > 0
