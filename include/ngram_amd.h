@@ -201,6 +201,10 @@ int ng_query_index_dev(const uint16_t* x, const int* avail, const int* pos, cons
  * length[act[i]] = k and, with avail >= k + 1, go to act_out (*n_out, *matched added to) */
 int ng_act_next(const int* act, const ng_u64* n_dev, ng_i64 n_max, const int* ctx_of, const uint32_t* hit,
                 const int* avail, int k, int* length, int* act_out, ng_u64* n_out, ng_u64* matched, void* stream);
+/* the longest match's active list split at level k: entries i < *n_dev of act whose context's hit bit is set get
+ * length[act[i]] = k (*matched added to); the others go to act_out (*n_out added to) */
+int ng_act_split(const int* act, const ng_u64* n_dev, ng_i64 n_max, const int* ctx_of, const uint32_t* hit, int k,
+                 int* length, int* act_out, ng_u64* n_out, ng_u64* matched, void* stream);
 /* ng_scan_sink's list scan over the first *n_dev entries of plist (n_max >= *n_dev), with no host sync; region >=
  * ceil(n_max / (grid * 256)) * 256 */
 int ng_scan_list_dev(const uint16_t* tok, int k, const ng_u64* plist, const ng_u64* n_dev, ng_i64 n_max,

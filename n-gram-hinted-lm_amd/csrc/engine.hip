@@ -1147,9 +1147,11 @@ extern "C" int ng_query_index(const u16* x, const int* avail, const int* pos, i6
 
 namespace {
 // One step of the longest match's active list: entry i (i < *n_dev) of act whose context (ctx_of[i]) has its hit bit
-// set matched level k (length[act[i]] = k); those with avail >= k + 1 go on to act_out. Each thread takes 4 entries;
-// a block counts its kept entries and matches and takes its place in act_out with one atomic each (a counter bumped
-// per entry or per wave would serialize).
+// set matched level k (length[act[i]] = k); those with avail >= k + 1 go on to act_out. SPLIT: the entries that did
+// not match go on instead (the matched ones are done at length k). Each thread takes 4 entries; a block counts its
+// kept entries and matches and takes its place in act_out with one atomic each (a counter bumped per entry or per
+// wave would serialize).
+template <bool SPLIT>
 __global__ void __launch_bounds__(256) act_next_k(const int* __restrict__ act, const u64* __restrict__ n_dev,
                                                   const int* __restrict__ ctx_of, const u32* __restrict__ hit,
                                                   const int* __restrict__ avail, int k, int* __restrict__ length,
@@ -1173,7 +1175,9 @@ __global__ void __launch_bounds__(256) act_next_k(const int* __restrict__ act, c
             if (c >= 0 && ((hit[c >> 5] >> (c & 31)) & 1u)) {
                 length[a[q]] = k;
                 ++nm;
-                keep[q] = avail[a[q]] >= k + 1;
+                keep[q] = !SPLIT && avail[a[q]] >= k + 1;
+            } else {
+                keep[q] = SPLIT;
             }
         }
         nk += keep[q];
@@ -1234,7 +1238,18 @@ extern "C" int ng_act_next(const int* act, const u64* n_dev, i64 n_max, const in
                            void* stream) {
     if (!n_dev || n_max < 0) return -1;
     if (n_max > 0)
-        act_next_k<<<(int)((n_max + 1023) / 1024), 256, 0, (hipStream_t)stream>>>(act, n_dev, ctx_of, hit, avail, k,
-                                                                                   length, act_out, n_out, matched);
+        act_next_k<false><<<(int)((n_max + 1023) / 1024), 256, 0, (hipStream_t)stream>>>(
+            act, n_dev, ctx_of, hit, avail, k, length, act_out, n_out, matched);
+    return (int)hipGetLastError();
+}
+
+// The longest match's active list split at level k (see act_next_k): entries whose context's hit bit is set get
+// length k and are done; the others go to act_out. n_out and matched are added to (zero them first).
+extern "C" int ng_act_split(const int* act, const u64* n_dev, i64 n_max, const int* ctx_of, const u32* hit, int k,
+                            int* length, int* act_out, u64* n_out, u64* matched, void* stream) {
+    if (!n_dev || n_max < 0) return -1;
+    if (n_max > 0)
+        act_next_k<true><<<(int)((n_max + 1023) / 1024), 256, 0, (hipStream_t)stream>>>(
+            act, n_dev, ctx_of, hit, nullptr, k, length, act_out, n_out, matched);
     return (int)hipGetLastError();
 }

@@ -188,6 +188,7 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
 
 SCAN_BLOCKS_PER_CU = 32  # scan blocks per compute unit
 DEVICE_LEVELS = True  # the existence phase's levels after the second list level run without host syncs
+LONG_FIRST = 8  # the device levels try level cap first when at least this many levels lie between
 BATCH_EVENTS = 1 << 28  # list levels counted together until their listed positions reach this
 LIST_DIV = 64  # a level's hits go to a position list once fewer than L / LIST_DIV (8 B each against L / 8 bitmap bytes)
 
@@ -197,7 +198,13 @@ def _exist_device(elib: Lib, tok, L: int, x, avail, act, k0: int, cap: int, cand
     ng_scan_list_dev, ng_seg_offsets / ng_seg_gather, ng_act_next), every buffer sized by level k0's active
     positions (act, already those with avail >= k0) and candidates (cand: the corpus positions that matched k0 - 1),
     which bound every later level's. One sync at the end reads each level's sizes; the levels are those whose active
-    list was not empty, as the host loop's. Returns [(k, hit list, its length, matched positions)]."""
+    list was not empty, as the host loop's. Returns [(k, hit list, its length, matched positions)].
+
+    With LONG_FIRST or more levels to go, level `cap` is tried first (the cap round): a position whose cap-token
+    context occurs matches every level below it too (a context's suffixes occur wherever it does), so it is done at
+    length cap, and the levels in between are walked by the others only. Their hit lists then hold only those
+    positions' contexts' occurrences, and level cap's is the round's. The long copies of a corpus make most of the
+    deep levels' positions such ones: they would otherwise be probed, and their occurrences listed, at every level."""
     dev = x.device
     n0, nc0 = int(act.numel()), int(cand.numel())
     qcap = int(n0 / QLOAD) + 1024
@@ -217,8 +224,24 @@ def _exist_device(elib: Lib, tok, L: int, x, avail, act, k0: int, cap: int, cand
     n_act = torch.tensor([n0], dtype=torch.int64, device=dev)
     n_cand = torch.tensor([nc0], dtype=torch.int64, device=dev)
     flags.zero_()
+    first = cap - k0 >= LONG_FIRST
+    if first:  # the cap round: the positions matching level cap are done; the others go on from level k0
+        counters_cap = torch.zeros(3, dtype=torch.int64, device=dev)
+        split = torch.zeros(2, dtype=torch.int64, device=dev)  # positions going on, positions done at length cap
+        elib("ng_query_index_dev", x, avail, acts[0], n_act, n0, i32(cap), table, u64(qcap), u64(slots), rep, ctx_of,
+             counters_cap)
+        hit.zero_()
+        elib("ng_scan_list_dev", tok, i32(cap), cand, n_cand, nc0, table, u64(qcap), rep, x, hit, i32(1), regions,
+             u64(R), ev_count, flags, i32(g), u64(0))
+        offs = torch.empty(g + 1, dtype=torch.int64, device=dev)
+        elib("ng_seg_offsets", ev_count, g, offs)
+        hl_cap = torch.empty(max(nc0, 1), dtype=torch.int64, device=dev)
+        elib("ng_seg_gather", regions, None, u64(R), None, ev_count, g, offs, hl_cap, None)
+        elib("ng_act_split", acts[0], n_act, n0, ctx_of, hit, i32(cap), length, acts[1], split[0:1], split[1:2])
+        nh_cap, n_act = offs[g:], split[0:1]
+        acts.reverse()
     out = []
-    for j, k in enumerate(range(k0, cap + 1)):
+    for j, k in enumerate(range(k0, cap if first else cap + 1)):
         cur, nxt = acts[j % 2], acts[(j + 1) % 2]
         sizes[j, 0:1].copy_(n_act)
         elib("ng_query_index_dev", x, avail, cur, n_act, n0, i32(k), table, u64(qcap), u64(slots), rep, ctx_of,
@@ -233,6 +256,10 @@ def _exist_device(elib: Lib, tok, L: int, x, avail, act, k0: int, cap: int, cand
         elib("ng_act_next", cur, n_act, n0, ctx_of, hit, avail, i32(k), length, nxt, sizes[j, 2:3], sizes[j, 1:2])
         out.append((k, hl, offs[g:]))
         cand, n_cand, n_act = hl, offs[g:], sizes[j, 2:3]
+    if first:
+        out.append((cap, hl_cap, nh_cap))
+        counters = torch.cat([counters, counters_cap[None]])
+        sizes[-1, 1:2].copy_(split[1:2])
     host = sizes.cpu().tolist()
     nhs = torch.cat([o for _, _, o in out]).cpu().tolist()
     c = counters.cpu()
@@ -242,8 +269,15 @@ def _exist_device(elib: Lib, tok, L: int, x, avail, act, k0: int, cap: int, cand
         raise RuntimeError(f"levels {k0}..{cap}: a query index was too small for its contexts")
     if int(c[:, 2].max()):
         raise RuntimeError(f"levels {k0}..{cap}: query positions collide with another context's key")
+    done = host[-1][1] if first else 0  # the positions done at length cap: active and matched at every level
+    if first:  # level cap's active positions: the others' that reached it, and the cap round's
+        host[-1][0] = host[-2][2] if len(host) > 1 else 0
     res = []
     for (k, hl, _), nh, (n_k, matched, _) in zip(out, nhs, host):
+        if k < cap:
+            n_k, matched = n_k + done, matched + done
+        else:
+            n_k += done if first else 0
         if n_k == 0:
             break
         res.append((k, hl[:nh], nh, matched))
