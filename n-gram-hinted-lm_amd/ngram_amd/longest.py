@@ -144,14 +144,17 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
         m = fpos.numel()
         if m == 0:
             continue
-        vi = QueryIndex(elib, x, avail, k, fpos, compact=True)
         if kind == "list":  # a sparse level: counted with the other list levels, one count for all
+            # its index is not checked here (no host wait per level): the batch reads every level's counters with its
+            # event total, and is counted again on indexes checked as they are built if an insert found no slot
+            vi = QueryIndex(elib, x, avail, k, fpos, compact=True, expect=m, defer=True)
             batch.append((k, fpos, vi))
             batch_ev += nh
             if batch_ev >= BATCH_EVENTS:
-                _count_batch(elib, lib, tok, L, x, batch, levels, flags, grid, nxt, cnt)
+                _count_batch(elib, lib, tok, L, x, avail, batch, levels, flags, grid, nxt, cnt)
                 batch, batch_ev = [], 0
             continue
+        vi = QueryIndex(elib, x, avail, k, fpos, compact=True)
         # the level's hit positions probed against the final contexts; their hits emitted, partitioned and counted in
         # LDS, then each final context's top entry
         flags.zero_()
@@ -179,7 +182,7 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
         cnt[fpos.long()] = o_cnt
         del vi, c, o_tok, o_cnt
     if batch:
-        _count_batch(elib, lib, tok, L, x, batch, levels, flags, grid, nxt, cnt)
+        _count_batch(elib, lib, tok, L, x, avail, batch, levels, flags, grid, nxt, cnt)
     if timing is not None:
         torch.cuda.synchronize()
         timing["count"] = timing.get("count", 0.0) + time.perf_counter() - t0
@@ -348,7 +351,8 @@ def _scan_list(elib: Lib, tok, L: int, k: int, vi, x, cand: torch.Tensor, hit, w
     return out[:m] if what else out, m
 
 
-def _count_batch(elib: Lib, lib: Lib, tok, L: int, x, batch: list, levels: list, flags, grid: int, nxt, cnt) -> None:
+def _count_batch(elib: Lib, lib: Lib, tok, L: int, x, avail, batch: list, levels: list, flags, grid: int, nxt,
+                 cnt) -> None:
     """The counting phase of several list levels at once: level k's context ids offset by the ids before it in the
     batch, so one partitioned count, one summary and one gather serve them all (per level only its query index and
     its scan: few launches and no host sync per level)."""
@@ -375,9 +379,19 @@ def _count_batch(elib: Lib, lib: Lib, tok, L: int, x, batch: list, levels: list,
         elib("ng_seg_gather", regions, None, u64(R), None, ev_count, g, offs, ev, None)
         at = offs[g : g + 1].clone()
         del regions, ev_count
-    n_ev, fl = torch.cat([at, flags[:1].to(torch.int64)]).tolist()  # one copy
+    pending = [(k, vi.pending) for k, _, vi in batch if vi.n is None]  # deferred indexes' counters
+    got = torch.cat([at, flags[:1].to(torch.int64)] + [c for _, c in pending]).tolist()  # one copy
+    n_ev, fl = got[:2]
     if fl & 4:
         raise RuntimeError(f"levels {batch[0][0]}..{batch[-1][0]}: an emit region overflowed")
+    for j, (k, _) in enumerate(pending):
+        _, over, coll = got[2 + 3 * j : 5 + 3 * j]
+        if coll:
+            raise RuntimeError(f"k={k}: {coll} query positions collide with another context's key")
+        if over:  # an insert found no slot (a walk past its bound): the batch again, its indexes checked
+            del ev
+            redo = [(k2, f, QueryIndex(elib, x, avail, k2, f, compact=True)) for k2, f, _ in batch]
+            return _count_batch(elib, lib, tok, L, x, avail, redo, levels, flags, grid, nxt, cnt)
     key = ("batch", batch[0][0])
     c = count_events(elib, lib, ev, n_ev, n_ids, _RATIO.get(key, 1.0), presort="ctx")
     del ev

@@ -62,6 +62,33 @@ def test_device_levels_match_host_levels(corpus, monkeypatch):
     assert got[True][3] == got[False][3] and len(got[True][3]) == 64
 
 
+def test_unchecked_index_that_overflowed_counts_its_batch_again(corpus, monkeypatch):
+    """The list levels' query indexes are built without a host wait and checked once, with their batch's event
+    total. One that reports an insert without a slot (forced here from the host, on an index that is in fact whole)
+    makes the batch count again on indexes checked as they are built: the same outputs."""
+    from ngram_amd import longest as LG
+
+    x = corpus.query[:-1]
+    tok, sizes, starts, L = load_shards(corpus.shards())
+    xt = torch.from_numpy(x.view(np.int16).copy()).cuda()
+    av = _segments(xt, Lib())
+    want = longest_match(tok, xt, av, 64)
+    flagged = []
+
+    class Flagged(LG.QueryIndex):
+        def __init__(self, *a, **kw):
+            super().__init__(*a, **kw)
+            if kw.get("defer") and self.n is None:
+                self.pending[1] = 1
+                flagged.append(a[3])
+
+    monkeypatch.setattr(LG, "QueryIndex", Flagged)
+    got = longest_match(tok, xt, av, 64)
+    assert len(flagged) > 10
+    for g, w in zip(got[:3], want[:3]):
+        assert torch.equal(g, w)
+
+
 def test_ladder_interface(corpus, tmp_path):
     paths, _ = corpus.write(tmp_path)
     lm = LongestMatch.create(paths, corpus.query[:20_001], 4, [])
