@@ -43,6 +43,26 @@ def test_longest_match_matches_oracle(corpus, cap, seg, monkeypatch):
         assert matched == int((want[0] >= k).sum()) and eligible == int((avail >= k).sum())
 
 
+@pytest.mark.parametrize("every", [40, 64])
+def test_deep_levels_where_no_position_reaches_the_cap(corpus, every):
+    """A segment start every `every` tokens keeps every match below the cap of 64 (avail < 64), while the copies
+    still run the deep levels: the round at the cap finds nothing and the levels in between carry every position."""
+    x = corpus.query[:-1].copy()
+    x[::every] = O.BOS
+    avail = O.segments(x)
+    want = O.longest_match(corpus.train, corpus.bounds, x, avail, 64)
+    assert 20 < want[0].max() < 64
+    tok, sizes, starts, L = load_shards(corpus.shards())
+    xt = torch.from_numpy(x.view(np.int16).copy()).cuda()
+    length, nxt, cnt, ladder = longest_match(tok, xt, _segments(xt, Lib()), 64)
+    got = (length.cpu().numpy().view(np.uint32), nxt.cpu().numpy().view(np.uint16), cnt.cpu().numpy().view(np.uint32))
+    for g, w, name in zip(got, want, ("length", "next", "count")):
+        assert np.array_equal(g, w), name
+    assert len(ladder) == int(want[0].max()) or ladder[-1][2] == 0
+    for k, eligible, matched in ladder:
+        assert matched == int((want[0] >= k).sum()) and eligible == int((avail >= k).sum())
+
+
 def test_device_levels_match_host_levels(corpus, monkeypatch):
     """The existence phase's deep levels run as one stream of launches (no host sync) or level by level on the host:
     the same lengths, next tokens, counts and ladder."""
