@@ -40,7 +40,7 @@ class QueryIndex:
         while True:
             slots = cap + TAIL
             table = torch.full((slots,), -1, dtype=torch.int64, device=dev)
-            rep = torch.full((slots,), -1, dtype=torch.int32, device=dev)
+            rep = torch.empty(slots, dtype=torch.int32, device=dev)  # read only at occupied slots: no fill
             if compact and positions is not None:
                 ctx_of = torch.empty(m, dtype=torch.int32, device=dev)
             else:
@@ -73,7 +73,7 @@ class QueryIndex:
             small = int(n_ctx / LOAD) + 1024
             while True:
                 t2 = torch.full((small + TAIL,), -1, dtype=torch.int64, device=dev)
-                r2 = torch.full((small + TAIL,), -1, dtype=torch.int32, device=dev)
+                r2 = torch.empty(small + TAIL, dtype=torch.int32, device=dev)
                 remap = torch.empty(slots, dtype=torch.int32, device=dev)
                 c2 = torch.zeros(3, dtype=torch.int64, device=dev)
                 lib("ng_query_index_shrink", table, rep, u64(slots), t2, u64(small), u64(small + TAIL), r2, ctx_of,
