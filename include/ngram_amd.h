@@ -112,16 +112,18 @@ int gen_copies(uint16_t* out, const ng_i64* copies, ng_i64 m, const uint16_t* sr
 int ng_scan_count(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, uint32_t* bm_out, const ng_u64* vt,
                   ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, ng_u64* keys, uint32_t* cnts, ng_u64 cap,
                   uint32_t* flags, int grid, int sparse, void* stream);
-/* the emitting scan: block b of `grid` appends its hits' mix64(context id << 16 | next) to ev[b * region ...] and
- * stores how many in ev_count[b]; region >= ng_emit_region(L, grid) = ceil(L / (grid * 8192)) * 8192; flags[0] bit 2
- * a region overflowed. sparse as ng_scan_count's. dhist (may be NULL): block b's events per top-8-bit digit d at
- * dhist[d * dstride + b] (dstride >= grid), for ng_seg_scatter. pre (may be NULL): a device flag; while set, a
+/* the emitting scan: block b of `grid` appends its hits' events to ev[b * region ...] and stores how many in
+ * ev_count[b]; region >= ng_emit_region(L, grid) = ceil(L / (grid * 8192)) * 8192; flags[0] bit 2 a region
+ * overflowed. sparse as ng_scan_count's. Events: wbits 0: mix64(context id << 16 | next), digit its top 8 bits;
+ * wbits in [17, 63]: wmix(pair key, wbits) (the 32-bit count's W-bit bijection, pair keys below 2^wbits), digit its
+ * top dbits bits (1 <= dbits <= 10). dhist (may be NULL): block b's events per digit d at dhist[d * dstride + b]
+ * (dstride >= grid), for ng_seg_scatter / ng_seg_scatter_narrow. pre (may be NULL): a device flag; while set, a
  * position of bm_in is probed only if the position before it is set as well (the prefix rule, ng_avail_closed) */
 ng_u64 ng_emit_region(ng_i64 L, int grid);
 int ng_scan_emit(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, uint32_t* bm_out, const ng_u64* vt,
                  ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, ng_u64* ev, ng_u64 region, uint32_t* ev_count,
                  uint32_t* flags, int grid, int sparse, uint32_t* dhist, ng_i64 dstride, const uint32_t* pre,
-                 void* stream);
+                 int wbits, int dbits, void* stream);
 /* *flag = 1 if avail[i] <= max(avail[i - 1], 0) + 1 wherever avail[i] > 1 (every valid query context's prefix is the
  * previous position's valid context: the prefix rule may gate the scans), else 0; stream-ordered, no host sync */
 int ng_avail_closed(const int* avail, ng_i64 n, uint32_t* flag, void* stream);
@@ -132,11 +134,12 @@ int ng_gate_popcount(const uint32_t* bm, ng_i64 nwords, const uint32_t* pre, ng_
  * out (grid * 256 u64): the random-load rate a level scan's probes are measured against */
 int ng_gather_probe(const ng_u64* table, ng_u64 cap, ng_u64 n, ng_u64 seed, int grid, ng_u64* out, void* stream);
 /* the emitting scan over listed positions: the first *n_dev entries of plist (a device-side count: no host sync),
- * events and digit histograms as ng_scan_emit's, each hit's bit set in bm_out (zeroed by the caller; may be NULL);
- * region >= ceil(n / (grid * 256)) * 256 */
+ * events (by wbits / dbits) and digit histograms as ng_scan_emit's, each hit's bit set in bm_out (zeroed by the
+ * caller; may be NULL); region >= ceil(n / (grid * 256)) * 256 */
 int ng_scan_emit_list(const uint16_t* tok, const ng_u64* plist, const ng_u64* n_dev, int k, const ng_u64* vt,
                       ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, uint32_t* bm_out, ng_u64* ev, ng_u64 region,
-                      uint32_t* ev_count, uint32_t* flags, int grid, uint32_t* dhist, ng_i64 dstride, void* stream);
+                      uint32_t* ev_count, uint32_t* flags, int grid, uint32_t* dhist, ng_i64 dstride, int wbits,
+                      int dbits, void* stream);
 /* a level scan with optional outputs over a bitmap-gated range (plist NULL: [0, L) gated by bm_in in ng_scan_count's
  * sparse modes, hit bitmap into bm_out) or over listed positions (plist: n corpus positions); hit (may be NULL):
  * bit (context id) of the u32 words hit set per hit; ev (may be NULL): block b of grid appends per hit mix64(pair key + key_add) (what 0) or its
@@ -227,6 +230,43 @@ int ng_part_bounds(const ng_u64* ev, ng_i64 n, int pbits, int msd, ng_i64* start
  * host has read the totals */
 int ng_seg_scatter(const ng_u64* src, ng_u64 R, const ng_i64* bases, const uint32_t* ev_count, const uint32_t* dpre,
                    ng_i64 nseg, int shift, int nbits, ng_u64* out, ng_u64 cap, void* stream);
+/* ng_seg_scatter with the keys narrowed to their low 32 bits on the way out (u32 out[cap]); shift <= 32 */
+int ng_seg_scatter_narrow(const ng_u64* src, ng_u64 R, const ng_i64* bases, const uint32_t* ev_count,
+                          const uint32_t* dpre, ng_i64 nseg, int shift, int nbits, uint32_t* out, ng_u64 cap,
+                          void* stream);
+/* The 32-bit count (a level's events as 4-byte keys after the first pass; every present context's record made in
+ * LDS without sorting its pairs): the second pass, most significant digit first. keys (at most cap of them, cap <
+ * 2^32) grouped into nb = 2^nb_bits buckets (1 <= nb_bits <= 11; bucket b from dpre[b * nseg], the last up to *total,
+ * a device-side count) sub-grouped within each bucket by the nbits-bit digit (key >> shift) & (2^nbits - 1)
+ * (0 <= nbits <= 11) into out (cap keys); start (i64[2^(nb_bits + nbits) + 1]) the partitions' starts, partition
+ * p = bucket << nbits | digit (nbits 0: the buckets' starts; keys and out unused). Two-phase temp storage (temp NULL:
+ * *temp_bytes set). ng_msd_pass: u32 keys (the count's events); ng_msd_pass64: u64 keys (its packed words) */
+int ng_msd_pass(void* temp, size_t* temp_bytes, const uint32_t* keys, const uint32_t* dpre, ng_i64 nseg, int nb_bits,
+                const ng_u64* total, ng_u64 cap, int shift, int nbits, uint32_t* out, ng_i64* start, void* stream);
+int ng_msd_pass64(void* temp, size_t* temp_bytes, const ng_u64* keys, const uint32_t* dpre, ng_i64 nseg, int nb_bits,
+                  const ng_u64* total, ng_u64 cap, int shift, int nbits, ng_u64* out, ng_i64* start, void* stream);
+/* lookups of n query positions i = pos[j] (pos NULL: j) for the 32-bit count: qk[j] = wmix(ctx_of[i] << 16 | tgt[i],
+ * W) << (64 - W) for ids in [lo, hi) (hi <= 2^(W - 16)), else EMPTY; qv[j] = i */
+int ng_part_lookups_w(const int* ctx_of, const uint16_t* tgt, const int* pos, ng_i64 n, ng_i64 lo, ng_i64 hi, int W,
+                      ng_u64* qk, uint32_t* qv, void* stream);
+/* the 32-bit count of ng_msd_pass's partitions (2^pbits of them, 1 <= W - pbits <= 31, W = context-id bits + 16) in
+ * LDS with `grid` blocks (<= 65536): block b's distinct pairs as packed words pair key << (48 - cb) | min(count,
+ * esc), esc = 2^(48 - cb) - 1 (W - 16 <= cb <= 44; larger counts also in the escape table), at out_k + seg_base[b],
+ * seg_cnt[b] of them; dhist[d * grid + b] its words per dbits-bit digit (word >> dshift) & (2^dbits - 1), dbits <=
+ * 11; qcnt[qv[j]] = the count of lookup j (ng_part_lookups_w's sorted by their top pbits, bounds qstart); flags[0]
+ * bit 0: a partition reached min(limit, 14000) distinct pairs (count again with a bit more), bit 1: the escape table
+ * is full */
+int ng_part_count32(const uint32_t* ev, const ng_i64* start, int pbits, int W, const ng_u64* qk, const uint32_t* qv,
+                    const ng_i64* qstart, ng_u64* out_k, int cb, ng_u64* esc_k, uint32_t* esc_c, ng_u64 esc_cap,
+                    uint32_t* seg_cnt, ng_i64* seg_base, uint32_t* qcnt, uint32_t* dhist, int dshift, int dbits,
+                    uint32_t limit, uint32_t* flags, int grid, void* stream);
+/* per context id c < n_ids from ng_part_count32's words grouped by context into P partitions (start: i64[P + 1],
+ * partition q = the ids [q << ibits, (q + 1) << ibits), ibits <= 11; ng_seg_scatter then ng_msd_pass64): dist[c] =
+ * its pairs (0: absent) for every id, and for present contexts the record rec[c] of ng_ctx_summary's layout (topk 1,
+ * 2, 4, 8; first-word index 0); flags[0] bit 2: a total reached 2^32 */
+int ng_ctx_agg(const ng_u64* w, const ng_i64* start, ng_i64 P, int ibits, int cb, ng_i64 n_ids, const ng_u64* esc_k,
+               const uint32_t* esc_c, ng_u64 esc_cap, int topk, uint32_t* rec, uint32_t* dist, uint32_t* flags,
+               void* stream);
 /* exclusive prefix sum of n u32 (out may alias in), *total (may be NULL) the sum; CUB-style two-phase temp storage */
 int ng_exclusive_scan_u32(void* temp, size_t* temp_bytes, const uint32_t* in, uint32_t* out, ng_i64 n,
                           ng_u64* total, void* stream);

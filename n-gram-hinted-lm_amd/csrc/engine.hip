@@ -10,6 +10,7 @@
 //     and per query position tot / dist / cnt (binary search) / top-k in one gather.
 #include "probe.h"
 #include "prim.h"
+#include "part.h"
 
 namespace {
 
@@ -64,15 +65,25 @@ struct EmitSink {
     u32* ev_count;
     int what;
     u32* hit;
-    u32* dhist;   // with what 0 (may be NULL): the block's events per top-8-bit digit, at dhist[digit * dstride + block]
+    u32* dhist;   // with what 0 (may be NULL): the block's events per digit, at dhist[digit * dstride + block]
     i64 dstride;
     u64 key_add;  // added to each pair key before it is mixed (a context-id offset: several levels' ids in one space)
+    int wbits;    // 0: events mix64(pair key), digit = the top 8 bits; else wmix(pair key, wbits) (pair keys below
+                  // 2^wbits), digit = its top dbits bits (dbits <= EMIT_MAXD)
+    int dbits;
+    __device__ __forceinline__ u64 event(u64 key, i64 p) const {
+        return what ? (u64)p : wbits ? wmix(key + key_add, wbits) : mix64(key + key_add);
+    }
+    __device__ __forceinline__ u32 digit(u64 e) const { return wbits ? (u32)(e >> (wbits - dbits)) : (u32)(e >> 56); }
+    __device__ __forceinline__ int ndigits() const { return wbits ? 1 << dbits : 256; }
 };
+
+#define EMIT_MAXD 10  // the widest digit of an emitting scan's histogram
 
 // A scan block's LDS for its sink: the emit cursor and the digit histogram.
 struct SinkShared {
     u32 cur;
-    u32 dh[256];
+    u32 dh[1 << EMIT_MAXD];
 };
 
 // A context's hit flag (bit c of the words hit), set only while it reads unset: a hot context's flag is then read
@@ -101,20 +112,20 @@ __device__ __forceinline__ void emit_wave(const EmitSink& s, SinkShared* ss, u64
     off = (u32)__shfl((int)off, 0, WAVE);
     if (hit) {
         const u64 at = (u64)off + (u64)__popcll(b & lanemask_lt());
-        const u64 e = s.what ? (u64)p : mix64(key + s.key_add);
+        const u64 e = s.event(key, p);
         if (at < s.region) s.ev[(u64)blockIdx.x * s.region + at] = e;
         else atomicOr(&flags[0], 4u);
-        if (s.dhist) atomicAdd(&ss->dh[e >> 56], 1u);
+        if (s.dhist) atomicAdd(&ss->dh[s.digit(e)], 1u);
         if (s.hit) set_hit(s.hit, key >> 16);
     }
 }
 
 __device__ __forceinline__ void emit_lane(const EmitSink& s, SinkShared* ss, u64 key, i64 p, u32* flags) {
     const u64 at = atomicAdd(&ss->cur, 1u);
-    const u64 e = s.what ? (u64)p : mix64(key + s.key_add);
+    const u64 e = s.event(key, p);
     if (at < s.region) s.ev[(u64)blockIdx.x * s.region + at] = e;
     else atomicOr(&flags[0], 4u);
-    if (s.dhist) atomicAdd(&ss->dh[e >> 56], 1u);
+    if (s.dhist) atomicAdd(&ss->dh[s.digit(e)], 1u);
     if (s.hit) set_hit(s.hit, key >> 16);
 }
 
@@ -123,7 +134,7 @@ __device__ __forceinline__ void sink_begin(const S& s, SinkShared* ss) {
     if constexpr (S::KIND == 2) {
         if (threadIdx.x == 0) ss->cur = 0;
         if (s.dhist)
-            for (int d = threadIdx.x; d < 256; d += blockDim.x) ss->dh[d] = 0;
+            for (int d = threadIdx.x; d < s.ndigits(); d += blockDim.x) ss->dh[d] = 0;
         __syncthreads();
     }
 }
@@ -134,7 +145,8 @@ __device__ __forceinline__ void sink_end(const S& s, SinkShared* ss) {
         __syncthreads();
         if (threadIdx.x == 0) s.ev_count[blockIdx.x] = ss->cur < s.region ? ss->cur : (u32)s.region;
         if (s.dhist)
-            for (int d = threadIdx.x; d < 256; d += blockDim.x) s.dhist[(i64)d * s.dstride + blockIdx.x] = ss->dh[d];
+            for (int d = threadIdx.x; d < s.ndigits(); d += blockDim.x)
+                s.dhist[(i64)d * s.dstride + blockIdx.x] = ss->dh[d];
     }
 }
 
@@ -708,42 +720,52 @@ extern "C" int ng_mark_bits(const int* ids, i64 n, u32* bits, void* stream) {
     return (int)hipGetLastError();
 }
 
-// The emitting scan: block b of the `grid` blocks appends its hits' mix64(pair key) to ev[b * region ...] and stores
-// their number in ev_count[b]; region must be at least ng_emit_region(L, grid). flags[0] bit 2: a region overflowed
-// (only with a smaller region). sparse as ng_scan_count's. dhist (may be NULL): block b's events per top-8-bit digit
-// d at dhist[d * dstride + b] (dstride >= grid), for ng_seg_scatter. pre (may be NULL): a device flag; while it is
-// set, a position of bm_in is probed only if the position before it is set too (the prefix rule: ng_avail_closed).
+// The emitting scan: block b of the `grid` blocks appends its hits' events to ev[b * region ...] and stores their
+// number in ev_count[b]; region must be at least ng_emit_region(L, grid). flags[0] bit 2: a region overflowed (only
+// with a smaller region). sparse as ng_scan_count's. Events: wbits 0: mix64(pair key), digit its top 8 bits; wbits
+// in [17, 63]: wmix(pair key, wbits) (pair keys below 2^wbits), digit its top dbits bits (1 <= dbits <= 10). dhist
+// (may be NULL): block b's events per digit d at dhist[d * dstride + b] (dstride >= grid), for ng_seg_scatter.
+// pre (may be NULL): a device flag; while it is set, a position of bm_in is probed only if the position before it is
+// set too (the prefix rule: ng_avail_closed).
 extern "C" u64 ng_emit_region(i64 L, int grid) {
     if (L <= 0 || grid <= 0) return 0;
     const u64 per = (u64)grid * 8192ull;
     return ((u64)L + per - 1) / per * 8192ull;
 }
 
+static inline bool emit_mode_ok(int wbits, int dbits) {
+    return wbits == 0 || (wbits >= 17 && wbits <= 63 && dbits >= 1 && dbits <= EMIT_MAXD && dbits < wbits);
+}
+
 extern "C" int ng_scan_emit(const u16* tok, i64 L, int k, const u32* bm_in, u32* bm_out, const u64* vt, u64 vcap,
                             const u32* vrep, const u16* x, u64* ev, u64 region, u32* ev_count, u32* flags, int grid,
-                            int sparse, u32* dhist, i64 dstride, const u32* pre, void* stream) {
+                            int sparse, u32* dhist, i64 dstride, const u32* pre, int wbits, int dbits, void* stream) {
     if (grid <= 0 || region == 0 || region > 0xFFFFFFFFull || (dhist && dstride < grid)) return -1;
+    if (!emit_mode_ok(wbits, dbits)) return -1;
     if (L <= 0) {
         fill_u32_n(ev_count, 0u, grid, (hipStream_t)stream);
         if (dhist)
-            for (int d = 0; d < 256; ++d) fill_u32_n(dhist + (i64)d * dstride, 0u, grid, (hipStream_t)stream);
+            for (int d = 0; d < (wbits ? 1 << dbits : 256); ++d)
+                fill_u32_n(dhist + (i64)d * dstride, 0u, grid, (hipStream_t)stream);
         return (int)hipGetLastError();
     }
-    if (launch_scan(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, EmitSink{ev, region, ev_count, 0, nullptr, dhist, dstride},
-                    flags, grid, sparse, (hipStream_t)stream, pre) != 0)
+    const EmitSink sk{ev, region, ev_count, 0, nullptr, dhist, dstride, 0, wbits, dbits};
+    if (launch_scan(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, sk, flags, grid, sparse, (hipStream_t)stream, pre) != 0)
         return -1;
     return (int)hipGetLastError();
 }
 
 // The emitting scan over listed positions: the first *n_dev entries of plist (shard-relative corpus positions, a
-// device-side count, so no host sync), hits' mix64(pair key) appended as ng_scan_emit's (block b of `grid` to
-// ev[b * region ...], their number in ev_count[b], digit histograms as ng_scan_emit's), and each hit's bit set in
-// bm_out (zeroed by the caller; may be NULL). region >= ceil(n_max / (grid * 256)) * 256 for n_max >= *n_dev.
+// device-side count, so no host sync), hits' events appended as ng_scan_emit's (block b of `grid` to
+// ev[b * region ...], their number in ev_count[b], events and digit histograms by wbits / dbits as ng_scan_emit's),
+// and each hit's bit set in bm_out (zeroed by the caller; may be NULL). region >= ceil(n_max / (grid * 256)) * 256
+// for n_max >= *n_dev.
 extern "C" int ng_scan_emit_list(const u16* tok, const u64* plist, const u64* n_dev, int k, const u64* vt, u64 vcap,
                                  const u32* vrep, const u16* x, u32* bm_out, u64* ev, u64 region, u32* ev_count,
-                                 u32* flags, int grid, u32* dhist, i64 dstride, void* stream) {
+                                 u32* flags, int grid, u32* dhist, i64 dstride, int wbits, int dbits, void* stream) {
     if (grid <= 0 || n_dev == nullptr || region == 0 || region > 0xFFFFFFFFull || (dhist && dstride < grid)) return -1;
-    const EmitSink sk{ev, region, ev_count, 0, nullptr, dhist, dstride};
+    if (!emit_mode_ok(wbits, dbits)) return -1;
+    const EmitSink sk{ev, region, ev_count, 0, nullptr, dhist, dstride, 0, wbits, dbits};
     hipStream_t st = (hipStream_t)stream;
     LEVEL_DISPATCH(k, (scan_list_k<K, EmitSink><<<grid, 256, 0, st>>>(tok, plist, 0, k, vt, vcap, vrep, x, sk, flags, n_dev,
                                                                      bm_out)));

@@ -1,0 +1,546 @@
+// The 32-bit partitioned count: a level's (context id, next token) events counted with 4 bytes per event after the
+// first pass, and each present context's record made in LDS without sorting its pairs (no counterpart in the
+// reference's libraries: there a level's hits go through one atomic hash table and two radix sorts,
+// old_records/gpu_val_stats.cu:340-434,529-644; the ranking follows exact_match/src/kgram.rs:357-368).
+//
+//   1. the emitting scan (ng_scan_emit with wbits = W = cb + 16, cb the context-id bits) writes each hit as
+//      h = wmix(pair key, W) (part.h: a bijection of W-bit values) with a histogram of its top d1 bits;
+//   2. ng_seg_scatter_narrow groups the events by those d1 bits (d1 = max(8, W - 32)) and keeps their low 32 bits;
+//   3. ng_msd_pass sub-groups each of those buckets by the next d2 bits (tiles within a bucket, LDS-staged), giving
+//      2^(d1 + d2) partitions = the top pbits = d1 + d2 bits of h, and each partition's start;
+//   4. ng_part_count32 counts every partition in an LDS table of u32 keys (the h bits below the partition, unique
+//      within it: 16384 slots in buckets of four, one 16-byte read per bucket), answers the partition's lookups and
+//      writes each distinct pair, unhashed, as a packed word (pair key << (48 - cb) | count) with a histogram of the
+//      words' top context bits;
+//   5. ng_seg_scatter groups the words by those context bits (dc = min(11, cb));
+//   6. ng_ctx_agg makes every context's record (total, pairs, top entries by count descending then token ascending)
+//      from its bucket's words in LDS: counts and totals by LDS atomics, the top entries by a cascade of 64-bit
+//      atomic maxima; every id of the bucket gets its pair count (0 for absent contexts).
+// Per event: 8 bytes written by the scan, 8 read + 4 written (pass 2), 4 + 4 + 4 (pass 3: histogram, read, write),
+// 4 read by the count; per distinct pair 8 written, 8 + 8 moved (pass 5) and 8 read at least once (pass 6, whose
+// later rounds over a bucket read it from L2). Nothing here reads a device count on the host: grids are bounded by
+// the capacities and blocks stop at the device-side totals; a wrapped total is raised by the host from the flags
+// and the exact totals afterwards.
+#include "part.h"
+#include "prim.h"
+#include "scatter.h"
+
+namespace {
+
+#define MSD_TILE SS_CHUNK
+
+// Buckets 2t and 2t + 1 (nb <= 2048) of a pass's digit groups are thread t's: bstart[b] = bucket b's first key (the
+// first pass's digit offsets dpre[b * nseg], clamped to cap), tfirst[b] = its first tile of MSD_TILE keys;
+// bstart[nb] = the total (*total, clamped), tfirst[nb] = the number of tiles.
+__global__ void __launch_bounds__(1024) msd_tiles_k(const u32* __restrict__ dpre, i64 nseg, int nb,
+                                                    const u64* __restrict__ total, u64 cap, i64* __restrict__ bstart,
+                                                    u32* __restrict__ tfirst) {
+    __shared__ u32 wt[1024 / WAVE];
+    const int t = threadIdx.x, lane = lane_id(), w = t / WAVE;
+    const u64 tot = *total < cap ? *total : cap;
+    u64 a[2] = {0, 0};
+    u32 nt[2] = {0, 0};
+    for (int h = 0; h < 2; ++h) {
+        const int b = 2 * t + h;
+        if (b >= nb) break;
+        u64 x = dpre[(i64)b * nseg];
+        u64 e = b + 1 < nb ? (u64)dpre[(i64)(b + 1) * nseg] : tot;
+        x = x < cap ? x : cap;
+        e = e < cap ? e : cap;
+        e = e < x ? x : e;
+        a[h] = x;
+        nt[h] = (u32)((e - x + MSD_TILE - 1) / MSD_TILE);
+        if (b == nb - 1) bstart[nb] = (i64)e;
+    }
+    const u32 mine = nt[0] + nt[1];
+    u32 incl = mine;
+#pragma unroll
+    for (int d = 1; d < WAVE; d <<= 1) {
+        const u32 o = (u32)__shfl_up((int)incl, d, WAVE);
+        if (lane >= d) incl += o;
+    }
+    if (lane == WAVE - 1) wt[w] = incl;
+    __syncthreads();
+    u32 before = incl - mine;
+    for (int i = 0; i < w; ++i) before += wt[i];
+    for (int h = 0; h < 2; ++h) {
+        const int b = 2 * t + h;
+        if (b >= nb) break;
+        bstart[b] = (i64)a[h];
+        tfirst[b] = before;
+        before += nt[h];
+        if (b == nb - 1) tfirst[nb] = before;
+    }
+}
+
+// Per tile (grid-stride) its digit counts, at hist[(tfirst[b] << nbits) + d * ntiles(b) + (tile - tfirst[b])].
+template <typename K>
+__global__ void __launch_bounds__(1024) msd_hist_k(const K* __restrict__ keys, const i64* __restrict__ bstart,
+                                                   const u32* __restrict__ tfirst, int nb, int shift, int nbits,
+                                                   i64 max_tiles, u32* __restrict__ hist) {
+    __shared__ u32 h[SS_MAXB];
+    const int t = threadIdx.x;
+    const u32 B = 1u << nbits, mask = B - 1u;
+    const i64 ntl = (i64)tfirst[nb] < max_tiles ? (i64)tfirst[nb] : max_tiles;
+    constexpr int IT = MSD_TILE / 1024;
+    for (i64 s = blockIdx.x; s < ntl; s += gridDim.x) {
+        for (u32 d = t; d < B; d += 1024) h[d] = 0;
+        __syncthreads();
+        const int b = tile_bucket(tfirst, nb, (u32)s);
+        const u64 off = (u64)bstart[b] + (u64)(s - tfirst[b]) * MSD_TILE;
+        const u64 end = (u64)bstart[b + 1];
+        const u32 n = end - off < (u64)MSD_TILE ? (u32)(end - off) : (u32)MSD_TILE;
+        K k[IT];
+#pragma unroll
+        for (int j = 0; j < IT; ++j) {
+            const u32 i = (u32)(j * 1024 + t);
+            k[j] = i < n ? keys[off + i] : (K)0;
+        }
+#pragma unroll
+        for (int j = 0; j < IT; ++j)
+            if ((u32)(j * 1024 + t) < n) atomicAdd(&h[(u32)(k[j] >> shift) & mask], 1u);
+        __syncthreads();
+        const u32 nt = tfirst[b + 1] - tfirst[b];
+        const u64 at = ((u64)tfirst[b] << nbits) + (u64)(s - tfirst[b]);
+        for (u32 d = t; d < B; d += 1024) hist[at + (u64)d * nt] = h[d];
+        __syncthreads();
+    }
+}
+
+// start[p] for the 2^(nb_bits + nbits) partitions p = bucket << nbits | digit, start[P] = the total.
+__global__ void msd_starts_k(const i64* __restrict__ bstart, const u32* __restrict__ tfirst, int nb, int nbits,
+                             const u32* __restrict__ hscan, i64* __restrict__ start) {
+    const i64 P = (i64)nb << nbits;
+    const i64 p = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    if (p > P) return;
+    if (p == P) {
+        start[P] = bstart[nb];
+        return;
+    }
+    const int b = (int)(p >> nbits);
+    const u32 d = (u32)(p & ((1 << nbits) - 1));
+    const u32 nt = tfirst[b + 1] - tfirst[b];
+    start[p] = nt ? (i64)hscan[((u64)tfirst[b] << nbits) + (u64)d * nt] : bstart[b];
+}
+
+// Lookup j of query position i = pos[j] (pos NULL: i = j): wmix(ctx_of[i] << 16 | tgt[i], W) << (64 - W) for context
+// ids in [lo, hi) (the partition digits then are its top bits, as the events'), else EMPTY (no such key: its low
+// 64 - W bits are ones); value i.
+__global__ void lookups_w_k(const int* __restrict__ ctx_of, const u16* __restrict__ tgt, const int* __restrict__ pos,
+                            i64 n, i64 lo, i64 hi, int W, u64* __restrict__ qk, u32* __restrict__ qv) {
+    const i64 j = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    if (j >= n) return;
+    const i64 i = pos ? pos[j] : j;
+    const i64 c = ctx_of[i];
+    qk[j] = (c >= lo && c < hi) ? wmix(((u64)c << 16) | tgt[i], W) << (64 - W) : EMPTY;
+    qv[j] = (u32)i;
+}
+
+#define P32_SLOTS 16384  // 128 KB of LDS (u32 keys and counts): one block per CU
+#define P32_BUCKETS (P32_SLOTS / 4)
+#define P32_BLOCK 1024
+#define P32_ITEMS 8
+#define P32_LIMIT 14000  // distinct pairs a partition may reach before it is declared overfull (a free slot always
+                         // remains: at most P32_LIMIT + P32_BLOCK keys are ever inserted)
+#define EMPTY32 0xFFFFFFFFu
+
+__device__ __forceinline__ u32 p32_bucket(u32 key) {
+    return (u32)(((u64)(key * 0x9E3779B1u) * P32_BUCKETS) >> 32);
+}
+
+// Count `add` occurrences of `key` (below 2^31) in the bucketized table (four keys per 16-byte bucket, filled from the
+// front, buckets probed linearly); returns whether it took a free slot. A lost race for a slot re-reads the bucket.
+__device__ __forceinline__ bool p32_add(u32* tk, u32* tc, u32 key, u32 add) {
+    u32 b = p32_bucket(key);
+    int slot = -1;
+    bool fresh = false;
+    while (slot < 0) {
+        const uint4 q = *(const uint4*)(tk + 4 * b);
+        const int f = q.x == key ? 0 : q.y == key ? 1 : q.z == key ? 2 : q.w == key ? 3 : -1;
+        const int e = q.x == EMPTY32 ? 0 : q.y == EMPTY32 ? 1 : q.z == EMPTY32 ? 2 : q.w == EMPTY32 ? 3 : -1;
+        if (f >= 0) {
+            slot = 4 * (int)b + f;
+        } else if (e >= 0) {
+            const u32 prev = atomicCAS(&tk[4 * b + e], EMPTY32, key);
+            if (prev == EMPTY32 || prev == key) {
+                slot = 4 * (int)b + e;
+                fresh = prev == EMPTY32;
+            }
+        } else {
+            b = (b + 1) & (P32_BUCKETS - 1);
+        }
+    }
+    atomicAdd(&tc[slot], add);
+    return fresh;
+}
+
+__device__ __forceinline__ u32 p32_find(const u32* tk, const u32* tc, u32 key) {
+    u32 b = p32_bucket(key);
+    while (true) {
+        const uint4 q = *(const uint4*)(tk + 4 * b);
+        const int f = q.x == key ? 0 : q.y == key ? 1 : q.z == key ? 2 : q.w == key ? 3 : -1;
+        if (f >= 0) return tc[4 * b + f];
+        if (q.w == EMPTY32) return 0;
+        b = (b + 1) & (P32_BUCKETS - 1);
+    }
+}
+
+// Block b counts the partitions it owns (part_owner: about equal events per block) in turn. Events: u32, a
+// partition's key = its low lbits = W - pbits bits (h = p << lbits | key). Its distinct pairs (at most its events) go
+// to out_k[start[p0] ...] as packed words: segment b = (seg_base[b], seg_cnt[b]); dhist[d * G + b] its words per
+// dbits-bit digit at dshift. Lookups: qk (sorted like the events: wmix keys << (64 - W), or EMPTY), qv their query
+// positions, qstart their partitions' bounds: qcnt[qv[j]] = the pair's count or 0. A partition reaching `limit`
+// distinct pairs (at most P32_LIMIT) sets flags[0] bit 0 and is left incomplete.
+__global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ ev, const i64* __restrict__ start,
+                                                      i64 P, int pbits, int W, const u64* __restrict__ qk,
+                                                      const u32* __restrict__ qv, const i64* __restrict__ qstart,
+                                                      u64* __restrict__ out_k, int cb, u64* esc_k, u32* esc_c,
+                                                      u64 esc_cap, u32* __restrict__ seg_cnt,
+                                                      i64* __restrict__ seg_base, u32* __restrict__ qcnt,
+                                                      u32* __restrict__ dhist, int dshift, int dbits, u32 limit,
+                                                      u32* flags) {
+    __shared__ __align__(16) u32 tk[P32_SLOTS];
+    __shared__ u32 tc[P32_SLOTS];
+    __shared__ u32 dh[SS_MAXB];
+    __shared__ u32 cur;
+    __shared__ u32 nocc;
+    const int t = threadIdx.x, lane = lane_id();
+    const int lbits = W - pbits;
+    const u32 lmask = (1u << lbits) - 1u;
+    const i64 n_ev = start[P], G = gridDim.x;
+    const i64 p0 = part_first(start, P, n_ev, G, blockIdx.x), p1 = part_first(start, P, n_ev, G, blockIdx.x + 1);
+    const int nd = 1 << dbits;
+    if (p0 >= p1) {
+        if (t == 0) {
+            seg_cnt[blockIdx.x] = 0;
+            seg_base[blockIdx.x] = 0;
+        }
+        for (int d = t; d < nd; d += P32_BLOCK) dhist[(i64)d * G + blockIdx.x] = 0;
+        return;
+    }
+    const i64 out_base = start[p0];
+    if (t == 0) {
+        cur = 0;
+        nocc = 0;
+    }
+    for (int d = t; d < nd; d += P32_BLOCK) dh[d] = 0;
+    for (int j = t; j < P32_SLOTS; j += P32_BLOCK) {
+        tk[j] = EMPTY32;
+        tc[j] = 0;
+    }
+    __syncthreads();
+    constexpr i64 ROUND = (i64)P32_BLOCK * P32_ITEMS;
+    auto load_round = [&](u32 (&dst)[P32_ITEMS], i64 i0, i64 end) {
+#pragma unroll
+        for (int r = 0; r < P32_ITEMS; ++r) {
+            const i64 i = i0 + (i64)r * P32_BLOCK + t;
+            dst[r] = i < end ? (ev[i] & lmask) : EMPTY32;
+        }
+    };
+    u32 ahead[P32_ITEMS];
+    i64 ahead_of = -1;
+    const u64 esc = (1ull << (48 - cb)) - 1;
+    for (i64 p = p0; p < p1; ++p) {
+        const i64 a = start[p], b = start[p + 1], qa = qstart[p], qb = qstart[p + 1];
+        const bool has_q = qa + t < qb;
+        u64 lk = EMPTY;
+        u32 lv = 0;
+        if (has_q) {
+            lk = qk[qa + t];
+            lv = qv[qa + t];
+        }
+        if (ahead_of != p && a < b) load_round(ahead, a, b);
+        for (i64 i0 = a; i0 < b; i0 += ROUND) {
+            u32 key[P32_ITEMS];
+#pragma unroll
+            for (int r = 0; r < P32_ITEMS; ++r) key[r] = ahead[r];
+            if (i0 + ROUND < b) {
+                load_round(ahead, i0 + ROUND, b);
+                ahead_of = p;
+            } else if (p + 1 < p1) {
+                load_round(ahead, b, start[p + 2]);
+                ahead_of = p + 1;
+            }
+#pragma unroll
+            for (int r = 0; r < P32_ITEMS; ++r) {
+                const bool valid = key[r] != EMPTY32;
+                const u64 vb = __ballot(valid);
+                if (!vb) continue;
+                if (__builtin_amdgcn_readfirstlane(nocc) >= limit) {  // overfull: counted again with a bit more
+                    if (lane == 0) atomicOr(&flags[0], 1u);
+                    continue;
+                }
+                // the lanes holding the wave's first key add once (a hot pair would serialize the LDS atomics)
+                const int ld = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)vb) - 1);
+                const u32 k0 = (u32)__builtin_amdgcn_readlane((int)key[r], ld);
+                const bool same = valid && key[r] == k0;
+                const u64 m = __ballot(same);
+                bool fresh = false;
+                if (valid && (!same || lane == ld)) fresh = p32_add(tk, tc, key[r], same ? (u32)__popcll(m) : 1u);
+                const u64 fb = __ballot(fresh);
+                if (fb && lane == 0) atomicAdd(&nocc, (u32)__popcll(fb));
+            }
+        }
+        lds_barrier();
+        if (qb > qa) {  // block-uniform
+            auto lkey = [&](u64 q) { return (u32)((q >> (64 - W)) & lmask); };
+            if (has_q) qcnt[lv] = lk == EMPTY ? 0u : p32_find(tk, tc, lkey(lk));
+            for (i64 j = qa + P32_BLOCK + t; j < qb; j += P32_BLOCK) {
+                const u64 q = qk[j];
+                qcnt[qv[j]] = q == EMPTY ? 0u : p32_find(tk, tc, lkey(q));
+            }
+            lds_barrier();  // every lookup has probed before the output pass empties the slots
+        }
+        for (int j0 = 0; j0 < P32_SLOTS; j0 += P32_BLOCK) {
+            const int j = j0 + t;
+            const u32 key = tk[j];
+            const bool occ = key != EMPTY32;
+            const u64 bal = __ballot(occ);
+            if (!bal) continue;
+            u32 off = 0;
+            if (lane == 0) off = atomicAdd(&cur, (u32)__popcll(bal));
+            off = (u32)__shfl((int)off, 0, WAVE);
+            if (occ) {
+                const u64 at = (u64)out_base + off + (u64)__popcll(bal & lanemask_lt());
+                const u64 pk = unwmix(((u64)p << lbits) | key, W);
+                const u32 n = tc[j];
+                tk[j] = EMPTY32;
+                tc[j] = 0;
+                const u64 word = (pk << (48 - cb)) | ((u64)n < esc ? (u64)n : esc);
+                out_k[at] = word;
+                if ((u64)n >= esc) esc_put(esc_k, esc_c, esc_cap, pk, n, flags);
+                atomicAdd(&dh[(u32)(word >> dshift) & (u32)(nd - 1)], 1u);
+            }
+        }
+        if (t == 0) nocc = 0;
+        lds_barrier();
+    }
+    if (t == 0) {
+        seg_cnt[blockIdx.x] = cur;
+        seg_base[blockIdx.x] = out_base;
+    }
+    for (int d = t; d < nd; d += P32_BLOCK) dhist[(i64)d * G + blockIdx.x] = dh[d];
+}
+
+// Per context from packed words grouped by context: partition q (words [start[q], start[q + 1])) holds the
+// contexts of ids [q << ibits, (q + 1) << ibits), 2^ibits <= AGG_IDS. A block per partition (grid-stride) streams
+// its words once, accumulating per id its total, its pairs and its top KT scores (count << 16 | 65535 - token) in
+// LDS. The top scores come from a cascade of atomic maxima: a score displaced from (or kept out of) slot r goes on to
+// slot r + 1, so slot r ends with the r-th largest; a score not above slot KT - 1's current value (which only grows,
+// and below which KT larger scores already exist) is not inserted. Then every id of the partition below n_ids gets
+// dist[c] = its pairs and, if present, its record (CtxRecord<KT>, first-word index 0). flags[0] bit 2: a total
+// reached 2^32.
+#define AGG_BLOCK 1024
+#define AGG_IDS 2048
+template <int KT>
+__global__ void __launch_bounds__(AGG_BLOCK) ctx_agg_k(const u64* __restrict__ w, const i64* __restrict__ start,
+                                                       i64 P, int ibits, int cb, i64 n_ids,
+                                                       const u64* __restrict__ esc_k, const u32* __restrict__ esc_c,
+                                                       u64 esc_cap, u32* __restrict__ rec, u32* __restrict__ dist,
+                                                       u32* flags) {
+    __shared__ u32 s_tot[AGG_IDS], s_dist[AGG_IDS];
+    __shared__ u64 s_top[AGG_IDS * KT];
+    const int t = threadIdx.x, lane = lane_id();
+    const int sh = 64 - cb, csh = 48 - cb;
+    const u64 esc = (1ull << csh) - 1;
+    const int nid = 1 << ibits;
+    for (i64 q = blockIdx.x; q < P; q += gridDim.x) {
+        const i64 lo = q << ibits;
+        if (lo >= n_ids) break;  // partitions ascend with q
+        const i64 wa = start[q], we = start[q + 1];
+        for (int l = t; l < nid; l += AGG_BLOCK) {
+            s_tot[l] = 0;
+            s_dist[l] = 0;
+        }
+        for (int l = t; l < nid * KT; l += AGG_BLOCK) s_top[l] = 0;
+        __syncthreads();
+        for (i64 i0 = wa; i0 < we; i0 += AGG_BLOCK) {  // the same rounds for every wave
+            const i64 i = i0 + t;
+            const bool valid = i < we;
+            const u64 vb = __ballot(valid);
+            if (!vb) continue;
+            const u64 word = valid ? w[i] : 0;
+            const int lid = (int)((i64)(word >> sh) - lo) & (nid - 1);
+            u32 n = 0;
+            if (valid) {
+                const u64 n64 = word & esc;
+                n = n64 < esc ? (u32)n64 : esc_get(esc_k, esc_c, esc_cap, word >> csh);
+            }
+            // the lanes of the wave's first context add its total and pairs once when many share it (a context with
+            // many pairs would serialize the LDS atomics on its two counters)
+            const int ld = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)vb) - 1);
+            const int l0 = __builtin_amdgcn_readlane(lid, ld);
+            const bool same = valid && lid == l0;
+            const u64 m = __ballot(same);
+            bool own = valid;
+            if (__popcll(m) > 4) {  // wave-uniform
+                u64 sm = same ? n : 0;
+#pragma unroll
+                for (int d = WAVE / 2; d > 0; d >>= 1) sm += shfl_down_u64(sm, d);
+                sm = bcast_u64(sm, 0);
+                if (lane == ld) {
+                    const u32 old = atomicAdd(&s_tot[l0], (u32)sm);
+                    if ((sm >> 32) || old + (u32)sm < old) atomicOr(&flags[0], 4u);
+                    atomicAdd(&s_dist[l0], (u32)__popcll(m));
+                }
+                own = valid && !same;
+            }
+            if (own) {
+                const u32 old = atomicAdd(&s_tot[lid], n);
+                if (old + n < old) atomicOr(&flags[0], 4u);
+                atomicAdd(&s_dist[lid], 1u);
+            }
+            if (valid) {
+                u64 v = rank_score(word >> csh, n);
+                u64* tp = &s_top[lid * KT];
+                if (v > __hip_atomic_load(&tp[KT - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) {
+#pragma unroll
+                    for (int r = 0; r < KT; ++r) {
+                        if (!v) break;
+                        const u64 o = atomicMax((unsigned long long*)&tp[r], (unsigned long long)v);
+                        v = o < v ? o : v;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        const int nl = n_ids - lo < nid ? (int)(n_ids - lo) : nid;
+        for (int l = t; l < nl; l += AGG_BLOCK) {
+            const i64 c = lo + l;
+            const u32 d = s_dist[l];
+            dist[c] = d;
+            if (d) {
+                u64 top[KT];
+#pragma unroll
+                for (int r = 0; r < KT; ++r) top[r] = s_top[l * KT + r];
+                store_record<KT>(rec, (u64)c, s_tot[l], d, top, 0);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+static inline int grid_cap(i64 n, int cap) { return n < 1 ? 1 : n > cap ? cap : (int)n; }
+
+static inline i64 msd_max_tiles(u64 cap, int nb) { return (i64)((cap + MSD_TILE - 1) / MSD_TILE) + nb; }
+
+static inline size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+template <typename K>
+static int msd_pass(void* temp, size_t* temp_bytes, const K* keys, const u32* dpre, i64 nseg, int nb_bits,
+                    const u64* total, u64 cap, int shift, int nbits, K* out, i64* start, hipStream_t st) {
+    if (temp_bytes == nullptr || nb_bits < 1 || nb_bits > 11 || nbits < 0 || nbits > 11 || shift < 0 ||
+        shift + nbits > (int)(8 * sizeof(K)) || nseg <= 0 || cap > 0xFFFFFFFFull)
+        return -1;
+    const int nb = 1 << nb_bits;
+    const i64 mt = msd_max_tiles(cap, nb);
+    const i64 nh = nbits ? mt << nbits : 0;
+    const size_t b0 = al256((size_t)(nb + 1) * 8), b1 = al256((size_t)(nb + 1) * 4), b2 = al256((size_t)nh * 4);
+    const size_t need = b0 + b1 + b2 + (nbits ? prim::scan_u32_temp_bytes(nh) : 0);
+    if (temp == nullptr) {
+        *temp_bytes = need;
+        return 0;
+    }
+    if (*temp_bytes < need) return -1;
+    char* tp = (char*)temp;
+    u32* tfirst = (u32*)(tp + b0);
+    if (nbits == 0) {  // the buckets are the partitions
+        msd_tiles_k<<<1, 1024, 0, st>>>(dpre, nseg, nb, total, cap, start, tfirst);
+        return (int)hipGetLastError();
+    }
+    i64* bstart = (i64*)tp;
+    u32* hist = (u32*)(tp + b0 + b1);
+    void* stemp = tp + b0 + b1 + b2;
+    msd_tiles_k<<<1, 1024, 0, st>>>(dpre, nseg, nb, total, cap, bstart, tfirst);
+    const int g = grid_cap(mt, 4096);
+    msd_hist_k<K><<<g, 1024, 0, st>>>(keys, bstart, tfirst, nb, shift, nbits, mt, hist);
+    int e = prim::exclusive_scan_u32(hist, hist, nh, nullptr, stemp, st);
+    if (e) return e;
+    const TileSegs sg{bstart, tfirst, hist, nb, nbits, mt};
+    if (nbits <= 8)
+        scatter_k<256, K, K><<<g, SS_BLOCK, 0, st>>>(keys, sg, shift, nbits, out, cap);
+    else
+        scatter_k<SS_MAXB, K, K><<<g, SS_BLOCK, 0, st>>>(keys, sg, shift, nbits, out, cap);
+    const i64 P = (i64)nb << nbits;
+    msd_starts_k<<<grid_for(P + 1, 256), 256, 0, st>>>(bstart, tfirst, nb, nbits, hist, start);
+    return (int)hipGetLastError();
+}
+
+}  // namespace
+
+// A most-significant-digit-first second pass (see the file's head): keys (at most cap of them, cap < 2^32) grouped
+// into the nb = 2^nb_bits buckets of a first pass's digits (bucket b from dpre[b * nseg], the last up to *total, a
+// device-side count; 1 <= nb_bits <= 11) sub-grouped within each bucket by the nbits-bit digit (key >> shift) &
+// (2^nbits - 1) (0 <= nbits <= 11) into out (cap keys); start (i64[2^(nb_bits + nbits) + 1]) the partitions'
+// starts, partition p = bucket << nbits | digit (nbits 0: the buckets' starts, keys and out unused). CUB-style
+// two-phase temp storage (temp NULL: *temp_bytes set). No host read of the total. ng_msd_pass: u32 keys (the 32-bit
+// count's events); ng_msd_pass64: u64 keys (its packed words, by context).
+extern "C" int ng_msd_pass(void* temp, size_t* temp_bytes, const u32* keys, const u32* dpre, i64 nseg, int nb_bits,
+                           const u64* total, u64 cap, int shift, int nbits, u32* out, i64* start, void* stream) {
+    return msd_pass<u32>(temp, temp_bytes, keys, dpre, nseg, nb_bits, total, cap, shift, nbits, out, start,
+                         (hipStream_t)stream);
+}
+
+extern "C" int ng_msd_pass64(void* temp, size_t* temp_bytes, const u64* keys, const u32* dpre, i64 nseg,
+                             int nb_bits, const u64* total, u64 cap, int shift, int nbits, u64* out, i64* start,
+                             void* stream) {
+    return msd_pass<u64>(temp, temp_bytes, keys, dpre, nseg, nb_bits, total, cap, shift, nbits, out, start,
+                         (hipStream_t)stream);
+}
+
+// The lookups of n query positions (pos[j], or j with pos NULL) for the 32-bit count: qk[j] = wmix(ctx_of[i] << 16 |
+// tgt[i], W) << (64 - W) for context ids in [lo, hi) (below 2^(W - 16)), else EMPTY; qv[j] = i.
+extern "C" int ng_part_lookups_w(const int* ctx_of, const u16* tgt, const int* pos, i64 n, i64 lo, i64 hi, int W,
+                                 u64* qk, u32* qv, void* stream) {
+    if (W < 17 || W > 63 || lo < 0 || hi > (1ll << (W - 16))) return -1;
+    if (n <= 0) return 0;
+    lookups_w_k<<<grid_for(n, 256), 256, 0, (hipStream_t)stream>>>(ctx_of, tgt, pos, n, lo, hi, W, qk, qv);
+    return (int)hipGetLastError();
+}
+
+// Count the 32-bit events (ng_msd_pass's output; start its partitions' starts, 2^pbits of them, 1 <= W - pbits <=
+// 31, W the pair-key bits) partition by partition with `grid` blocks of about equal events (at most 65536): block
+// b's distinct pairs as packed words pair key << (48 - cb) | min(count, esc), esc = 2^(48 - cb) - 1 (larger counts
+// also in the escape table; context ids below 2^(W - 16), W - 16 <= cb <= 44), at out_k + seg_base[b], seg_cnt[b] of
+// them (out_k holds as many words as there are events); dhist[d * grid + b] block b's words per dbits-bit digit
+// (word >> dshift) & (2^dbits - 1) (1 <= dbits <= 11), for ng_seg_scatter. Lookups (ng_part_lookups_w's, sorted by
+// their top pbits; qstart their partitions' bounds; qk and qv may be NULL with qstart all zeros: none) get qcnt[qv[j]]
+// = the pair's count or 0. flags[0] bit 0: a partition reached min(limit, 14000) distinct pairs (its count is
+// incomplete: count again with a bit more); bit 1: the escape table is full.
+extern "C" int ng_part_count32(const u32* ev, const i64* start, int pbits, int W, const u64* qk, const u32* qv,
+                               const i64* qstart, u64* out_k, int cb, u64* esc_k, u32* esc_c, u64 esc_cap,
+                               u32* seg_cnt, i64* seg_base, u32* qcnt, u32* dhist, int dshift, int dbits, u32 limit,
+                               u32* flags, int grid, void* stream) {
+    if (pbits < 1 || pbits > 30 || W < 17 || W - 16 > cb || cb > 44 || W - pbits > 31 || W - pbits < 1 ||
+        grid <= 0 || grid > 65536 || esc_k == nullptr || esc_c == nullptr || esc_cap == 0 || dbits < 1 ||
+        dbits > 11 || dshift < 0 || dshift + dbits > 64 || dhist == nullptr || qstart == nullptr || limit == 0)
+        return -1;
+    const i64 P = 1ll << pbits;
+    limit = limit < P32_LIMIT ? limit : P32_LIMIT;
+    count32_k<<<grid, P32_BLOCK, 0, (hipStream_t)stream>>>(ev, start, P, pbits, W, qk, qv, qstart, out_k, cb, esc_k,
+                                                           esc_c, esc_cap, seg_cnt, seg_base, qcnt, dhist, dshift,
+                                                           dbits, limit, flags);
+    return (int)hipGetLastError();
+}
+
+// Per context of ids below n_ids from ng_part_count32's words (cb context bits) grouped by context into P
+// partitions (start: i64[P + 1]; partition q = the ids [q << ibits, (q + 1) << ibits), ibits <= 11): dist[c] = its
+// pairs (0: absent) for every id, and for present contexts the record rec[c] of ng_ctx_summary's layout (topk 1, 2,
+// 4, 8; first-word index 0); flags[0] bit 2: a total reached 2^32.
+extern "C" int ng_ctx_agg(const u64* w, const i64* start, i64 P, int ibits, int cb, i64 n_ids, const u64* esc_k,
+                          const u32* esc_c, u64 esc_cap, int topk, u32* rec, u32* dist, u32* flags, void* stream) {
+    if (cb < 1 || cb > 44 || ibits < 0 || (1 << ibits) > AGG_IDS || P <= 0 || esc_cap == 0 || n_ids < 0 ||
+        n_ids > (1ll << cb) || (P << ibits) < n_ids)
+        return -1;
+    if (n_ids == 0) return 0;
+    const int g = grid_cap(P, 1 << 20);
+    hipStream_t st = (hipStream_t)stream;
+    switch (topk) {
+        case 1: ctx_agg_k<1><<<g, AGG_BLOCK, 0, st>>>(w, start, P, ibits, cb, n_ids, esc_k, esc_c, esc_cap, rec, dist, flags); break;
+        case 2: ctx_agg_k<2><<<g, AGG_BLOCK, 0, st>>>(w, start, P, ibits, cb, n_ids, esc_k, esc_c, esc_cap, rec, dist, flags); break;
+        case 4: ctx_agg_k<4><<<g, AGG_BLOCK, 0, st>>>(w, start, P, ibits, cb, n_ids, esc_k, esc_c, esc_cap, rec, dist, flags); break;
+        case 8: ctx_agg_k<8><<<g, AGG_BLOCK, 0, st>>>(w, start, P, ibits, cb, n_ids, esc_k, esc_c, esc_cap, rec, dist, flags); break;
+        default: return -1;
+    }
+    return (int)hipGetLastError();
+}

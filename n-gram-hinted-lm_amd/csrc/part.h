@@ -22,6 +22,58 @@ __device__ __forceinline__ u64 unmix64(u64 h) {
     return unxorshift(h, 30);
 }
 
+// A bijection of W-bit values (17 <= W <= 63): a product by an odd constant, a right xorshift by s = ceil(W / 2) (its
+// own inverse, since x >> 2s = 0), again, all modulo 2^W. The 32-bit count hashes pair keys below 2^W with it, so
+// that its top bits spread every context's pairs over the partitions and the bits below the partition digits
+// identify the pair within its partition.
+#define WMIX_C1 0x9E3779B97F4A7C15ull
+#define WMIX_C2 0xBF58476D1CE4E5B9ull
+#define WMIX_I1 0xF1DE83E19937733Dull  // WMIX_C1^-1 mod 2^64
+#define WMIX_I2 0x96DE1B173F119089ull  // WMIX_C2^-1 mod 2^64
+__host__ __device__ __forceinline__ u64 wmix(u64 x, int W) {
+    const u64 m = (1ull << W) - 1ull;
+    const int s = (W + 1) >> 1;
+    x = (x * WMIX_C1) & m;
+    x ^= x >> s;
+    x = (x * WMIX_C2) & m;
+    return x ^ (x >> s);
+}
+__host__ __device__ __forceinline__ u64 unwmix(u64 h, int W) {
+    const u64 m = (1ull << W) - 1ull;
+    const int s = (W + 1) >> 1;
+    h ^= h >> s;
+    h = (h * WMIX_I2) & m;
+    h ^= h >> s;
+    return (h * WMIX_I1) & m;
+}
+
+// A wave-uniform lane's 64-bit value (readlane: no LDS traffic).
+__device__ __forceinline__ u64 readlane_u64(u64 v, int l) {
+    const u32 lo = (u32)__builtin_amdgcn_readlane((int)(u32)v, l);
+    const u32 hi = (u32)__builtin_amdgcn_readlane((int)(u32)(v >> 32), l);
+    return ((u64)hi << 32) | lo;
+}
+
+// The block owning partition p: the one whose share of the events holds the partition's first event (start[p] * G /
+// n, the last block for trailing empty partitions), so that blocks get equal events, whatever the skew of the
+// partitions' sizes (a partition holding a hot pair has far more events than others). Monotone in p.
+__device__ __forceinline__ i64 part_owner(const i64* __restrict__ start, i64 p, i64 n, i64 G) {
+    if (n <= 0) return 0;
+    const i64 o = (i64)((u64)start[p] * (u64)G / (u64)n);  // start * G < 2^63 for n < 2^47 events, G <= 2^16
+    return o < G - 1 ? o : G - 1;
+}
+
+// The first partition whose owner is at least b (P if none).
+__device__ __forceinline__ i64 part_first(const i64* __restrict__ start, i64 P, i64 n, i64 G, i64 b) {
+    i64 lo = 0, hi = P;
+    while (lo < hi) {
+        const i64 m = (lo + hi) >> 1;
+        if (part_owner(start, m, n, G) < b) lo = m + 1;
+        else hi = m;
+    }
+    return lo;
+}
+
 // A count too large for a packed word's count field: (pair key, count) into the escape table (linear probing; each
 // distinct pair is written once). A full table sets flags[0] bit 1.
 __device__ __forceinline__ void esc_put(u64* esc_k, u32* esc_c, u64 cap, u64 key, u32 n, u32* flags) {

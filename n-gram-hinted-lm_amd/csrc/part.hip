@@ -15,6 +15,7 @@
 // atomics run at about 27 G/s scattered and 80 M/s on one address, far below these streams.
 #include "part.h"
 #include "prim.h"
+#include "scatter.h"
 
 namespace {
 
@@ -82,86 +83,6 @@ __global__ void part_bounds_k(const u64* __restrict__ ev, i64 n, int pbits, int 
         }
     }  // pbits 0: one partition starting at 0
     start[p] = a;
-}
-
-// A sort's first pass straight from segments (an emitting scan's regions, or the count's per-block outputs): segment
-// s (ev_count[s] keys at src + (bases ? bases[s] : s * R)) scattered by the nbits-bit digit at `shift`, digit d of
-// segment s starting at out + dpre[d * nseg + s] (the exclusive scan of the producer's per-segment digit histograms,
-// digit-major). The order within a digit is free (the passes after this one are stable): a chunk of 16384 keys is
-// ranked by LDS counters, staged in LDS by digit (128 KB: one block per CU; twice the runs' length of 8192-key chunks
-// at two blocks per CU, measured 0.8 ms faster per c3 step) and written as per-digit runs. Replaces packing the segments into
-// one array and a radix pass over it. A region segment is read up to R keys, and keys whose place is cap or beyond are
-// dropped, so a launch made before its host has checked the totals (a region overflow, a 32-bit wrap) stays inside
-// out and the regions.
-#define SS_BLOCK 1024
-#define SS_ITEMS 16
-#define SS_CHUNK (SS_BLOCK * SS_ITEMS)
-#define SS_MAXB 2048  // digits of up to 11 bits
-template <int BMAX>  // the digit arrays' size: 256 or SS_MAXB (the stage and SS_MAXB's arrays fill 152 KB of LDS)
-__global__ void __launch_bounds__(SS_BLOCK) seg_scatter_k(const u64* __restrict__ src, u64 R,
-                                                         const i64* __restrict__ bases,
-                                                         const u32* __restrict__ ev_count, const u32* __restrict__ dpre,
-                                                         i64 nseg, int shift, int nbits, u64* __restrict__ out,
-                                                         u64 cap) {
-    __shared__ u64 stage[SS_CHUNK];
-    __shared__ u32 cnt[BMAX], pre[BMAX], base[BMAX], wt[SS_BLOCK / WAVE];
-    const int t = threadIdx.x, lane = lane_id(), wid = t / WAVE;
-    const u32 B = 1u << nbits, mask = B - 1u;
-    for (i64 sg = blockIdx.x; sg < nseg; sg += gridDim.x) {
-        const u32 n = !bases && (u64)ev_count[sg] > R ? (u32)R : ev_count[sg];
-        const u64* in = src + (bases ? (u64)bases[sg] : (u64)sg * R);
-        for (u32 d = t; d < B; d += SS_BLOCK) base[d] = dpre[(i64)d * nseg + sg];
-        for (u32 c0 = 0; c0 < n; c0 += SS_CHUNK) {
-            for (u32 d = t; d < B; d += SS_BLOCK) cnt[d] = 0;
-            __syncthreads();
-            u64 key[SS_ITEMS];
-            u32 rank[SS_ITEMS];
-#pragma unroll
-            for (int j = 0; j < SS_ITEMS; ++j) {
-                const u32 i = c0 + (u32)(j * SS_BLOCK + t);
-                key[j] = i < n ? in[i] : 0;
-            }
-#pragma unroll
-            for (int j = 0; j < SS_ITEMS; ++j) {
-                const u32 i = c0 + (u32)(j * SS_BLOCK + t);
-                rank[j] = i < n ? atomicAdd(&cnt[(u32)(key[j] >> shift) & mask], 1u) : 0u;
-            }
-            __syncthreads();
-            // exclusive scan of the B digit counts: thread t holds digits 2t and 2t + 1 (B <= 2 * SS_BLOCK)
-            const u32 d0 = 2u * (u32)t;
-            const u32 a0 = d0 < B ? cnt[d0] : 0u, a1 = d0 + 1 < B ? cnt[d0 + 1] : 0u;
-            u32 incl = a0 + a1;
-#pragma unroll
-            for (int d = 1; d < WAVE; d <<= 1) {
-                const u32 o = (u32)__shfl_up((int)incl, d, WAVE);
-                if (lane >= d) incl += o;
-            }
-            if (lane == WAVE - 1) wt[wid] = incl;
-            __syncthreads();
-            u32 before = 0;
-            for (int w = 0; w < wid; ++w) before += wt[w];
-            const u32 ex = before + incl - (a0 + a1);
-            if (d0 < B) pre[d0] = ex;
-            if (d0 + 1 < B) pre[d0 + 1] = ex + a0;
-            __syncthreads();
-#pragma unroll
-            for (int j = 0; j < SS_ITEMS; ++j) {
-                const u32 i = c0 + (u32)(j * SS_BLOCK + t);
-                if (i < n) stage[pre[(u32)(key[j] >> shift) & mask] + rank[j]] = key[j];
-            }
-            __syncthreads();
-            const u32 m = n - c0 < (u32)SS_CHUNK ? n - c0 : (u32)SS_CHUNK;
-            for (u32 i = t; i < m; i += SS_BLOCK) {
-                const u64 k = stage[i];
-                const u32 d = (u32)(k >> shift) & mask;
-                const u64 at = (u64)base[d] + i - pre[d];
-                if (at < cap) out[at] = k;
-            }
-            __syncthreads();
-            for (u32 d = t; d < B; d += SS_BLOCK) base[d] += cnt[d];
-        }
-        __syncthreads();  // base is read before the next segment overwrites it
-    }
 }
 
 // Lookup j of query position i = pos[j] (pos NULL: i = j): the mixed pair key of its (context, target) if its
@@ -237,33 +158,6 @@ __device__ __forceinline__ u32 pt_find(const u64* tk, const u32* tc, u64 key) {
         if (k3 == EMPTY) return 0;
         b = pt_next(b);
     }
-}
-
-// A wave-uniform lane's 64-bit value (readlane: no LDS traffic).
-__device__ __forceinline__ u64 readlane_u64(u64 v, int l) {
-    const u32 lo = (u32)__builtin_amdgcn_readlane((int)(u32)v, l);
-    const u32 hi = (u32)__builtin_amdgcn_readlane((int)(u32)(v >> 32), l);
-    return ((u64)hi << 32) | lo;
-}
-
-// The block owning partition p: the one whose share of the events holds the partition's first event (start[p] * G /
-// n, the last block for trailing empty partitions), so that blocks get equal events, whatever the skew of the
-// partitions' sizes (a partition holding a hot pair has far more events than others). Monotone in p.
-__device__ __forceinline__ i64 part_owner(const i64* __restrict__ start, i64 p, i64 n, i64 G) {
-    if (n <= 0) return 0;
-    const i64 o = (i64)((u64)start[p] * (u64)G / (u64)n);  // start * G < 2^63 for n < 2^47 events, G <= 2^16
-    return o < G - 1 ? o : G - 1;
-}
-
-// The first partition whose owner is at least b (P if none).
-__device__ __forceinline__ i64 part_first(const i64* __restrict__ start, i64 P, i64 n, i64 G, i64 b) {
-    i64 lo = 0, hi = P;
-    while (lo < hi) {
-        const i64 m = (lo + hi) >> 1;
-        if (part_owner(start, m, n, G) < b) lo = m + 1;
-        else hi = m;
-    }
-    return lo;
 }
 
 // Block b counts the partitions it owns (part_owner) in turn. Its distinct pairs (at most its events) go to
@@ -712,7 +606,7 @@ extern "C" int ng_exclusive_scan_u32(void* temp, size_t* temp_bytes, const u32* 
     return prim::exclusive_scan_u32(in, out, n, total, temp, (hipStream_t)stream);
 }
 
-// A sort's first pass from segments (seg_scatter_k): nseg segments of ev_count[s] keys at src + (bases ? bases[s] :
+// A sort's first pass from segments (scatter.h's scatter_k): nseg segments of ev_count[s] keys at src + (bases ? bases[s] :
 // s * R), scattered by the nbits-bit digit (key >> shift) & (2^nbits - 1) (nbits <= 11) to out at the offsets dpre
 // (u32 [2^nbits * nseg], the exclusive scan of the producer's digit histograms, digit-major: ng_scan_emit's with
 // shift 56 and 8 bits, ng_part_count's; fewer than 2^32 keys).
@@ -723,12 +617,28 @@ extern "C" int ng_seg_scatter(const u64* src, u64 R, const i64* bases, const u32
         return -1;
     if (nseg == 0) return 0;
     const i64 g = nseg < 16384 ? nseg : 16384;
+    const RegionSegs sg{R, bases, ev_count, dpre, nseg};
     if (nbits <= 8)
-        seg_scatter_k<256><<<(unsigned)g, SS_BLOCK, 0, (hipStream_t)stream>>>(src, R, bases, ev_count, dpre, nseg, shift,
-                                                                            nbits, out, cap);
+        scatter_k<256, u64, u64><<<(unsigned)g, SS_BLOCK, 0, (hipStream_t)stream>>>(src, sg, shift, nbits, out, cap);
     else
-        seg_scatter_k<SS_MAXB><<<(unsigned)g, SS_BLOCK, 0, (hipStream_t)stream>>>(src, R, bases, ev_count, dpre, nseg,
-                                                                                shift, nbits, out, cap);
+        scatter_k<SS_MAXB, u64, u64><<<(unsigned)g, SS_BLOCK, 0, (hipStream_t)stream>>>(src, sg, shift, nbits, out, cap);
+    return (int)hipGetLastError();
+}
+
+// ng_seg_scatter with the keys narrowed to their low 32 bits on the way out (u32 out[cap]): for keys whose digit is
+// their top nbits bits and whose bits below the digit fit 32 (shift <= 32), the first pass of the 32-bit count.
+extern "C" int ng_seg_scatter_narrow(const u64* src, u64 R, const i64* bases, const u32* ev_count, const u32* dpre,
+                                     i64 nseg, int shift, int nbits, u32* out, u64 cap, void* stream) {
+    if (nseg < 0 || nbits < 1 || nbits > 11 || shift < 0 || shift > 32 ||
+        (bases == nullptr && (R == 0 || R > 0xFFFFFFFFull)))
+        return -1;
+    if (nseg == 0) return 0;
+    const i64 g = nseg < 16384 ? nseg : 16384;
+    const RegionSegs sg{R, bases, ev_count, dpre, nseg};
+    if (nbits <= 8)
+        scatter_k<256, u64, u32><<<(unsigned)g, SS_BLOCK, 0, (hipStream_t)stream>>>(src, sg, shift, nbits, out, cap);
+    else
+        scatter_k<SS_MAXB, u64, u32><<<(unsigned)g, SS_BLOCK, 0, (hipStream_t)stream>>>(src, sg, shift, nbits, out, cap);
     return (int)hipGetLastError();
 }
 

@@ -21,7 +21,7 @@ RECORD_LIB_NAME = "libngram_amd_record.so"
 # each library's sources (relative to csrc/); an object shared by both is compiled once
 LIBS = {
     LIB_NAME: ["prim.hip", "abi/owner.hip", "abi/gvs.hip", "gen.hip", "engine.hip", "part.hip", "table.hip",
-               "online.hip", "rows.hip", "hintrows.hip"],
+               "online.hip", "rows.hip", "hintrows.hip", "pairs32.hip"],
     RECORD_LIB_NAME: ["prim.hip", "abi/owner.hip", "abi/record.hip"],
 }
 ARCH = os.environ.get("NGRAM_AMD_ARCH", "gfx950")

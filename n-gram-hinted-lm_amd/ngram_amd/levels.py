@@ -33,7 +33,7 @@ import torch
 
 from . import partcount
 from .lib import Lib, i32, u64
-from .partcount import check_summary, count_events, emit_region, summarize
+from .partcount import W_MAX, check_summary, count32, count_events, emit_region, first_digit, summarize, w_bits
 from .qindex import QueryIndex
 
 SCAN_BLOCKS_PER_CU = 8  # level-scan blocks (grid-stride) per compute unit (c3 sweep: 8 fastest of 4-32)
@@ -83,6 +83,8 @@ class LevelBuild:
         self.kernel_events: list = []
         self.host_s = {"index": 0.0, "scan": 0.0, "count": 0.0}
         self._plist = None
+        self.wide: set = set()  # levels counted by the 64-bit path (count_events): their 32-bit count overflowed
+        self.min_pbits: dict[int, int] = {}  # per level, partition bits the 32-bit count found too few, plus one
 
     def _event(self, name: str, k: int, n: int, mode: int = -1):
         """A pair of timing events around a launch on the current stream, kept in kernel_events as (name, k, n, e0,
@@ -122,6 +124,7 @@ class LevelBuild:
         regions = torch.empty(n_reg, dtype=torch.int64, device=dev)
         out = res.counts
         deferred = []  # summarize's checks, read once after every level
+        checks32 = []  # the 32-bit counts' sizes and flags, likewise
         pending = []  # query indexes sized from the last build's context counts, checked once after every level
         for li, k in enumerate(self.levels):
             t0 = time.perf_counter()
@@ -135,26 +138,38 @@ class LevelBuild:
             else:
                 self.contexts_of[k] = vi.n
             t1 = time.perf_counter()
-            seg = self._emit(k, vi, x, bms, regions, R)
-            t2 = time.perf_counter()
-            ev_fn = lambda name, n, k=k: self._event(name, k, n)  # noqa: E731
-            c = count_events(elib, elib, None, 0, vi.ids, self.dratio.get(k, 1.0), (vi.ctx_of, tgt, seen),
-                             event=ev_fn, seg=seg, presort="ctx")
-            del seg
-            self.events_of[k] = c.n_ev
-            self.dratio[k] = c.U / max(1, c.n_ev)
-            t3 = time.perf_counter()
             kept = k in keep
             ktop = 8 if (kept or cnt_top is not None) else _record_width(topk)
-            if not c.cb:
-                raise RuntimeError(f"k={k}: more large counts than the escape table holds")
-            try:
-                sm = summarize(elib, elib, c, vi.ids, ktop, False, ev_fn,
-                               deep_min=cnt_top if cnt_top is not None else None, defer=True)
-            except RuntimeError as e:
-                raise RuntimeError(f"k={k}: {e}") from None
-            if sm.stat is not None:  # checked once after the last level: no host read per level
-                deferred.append((f"k={k}", sm.stat))
+            ev_fn = lambda name, n, k=k: self._event(name, k, n)  # noqa: E731
+            _, W = w_bits(vi.ids)
+            use32 = cnt_top is None and W <= W_MAX and k not in self.wide
+            seg = self._emit(k, vi, x, bms, regions, R, W if use32 else 0)
+            t2 = time.perf_counter()
+            if use32:
+                # the 32-bit count: records made without sorting the pairs, every size read once after the last level
+                c = count32(elib, seg, vi.ids, ktop, (vi.ctx_of, tgt, seen), self.events_of.get(k),
+                            self.dratio.get(k, 1.0), ev_fn, self.min_pbits.get(k, 0))
+                del seg
+                checks32.append((k, c.stat, c.pbits, vi.ids))
+                sm = c
+                res.info[k] = dict(contexts=vi.n, ids=vi.ids, pairs=None, events=None, pbits=c.pbits, hits=None)
+            else:
+                c = count_events(elib, elib, None, 0, vi.ids, self.dratio.get(k, 1.0), (vi.ctx_of, tgt, seen),
+                                 event=ev_fn, seg=seg, presort="ctx")
+                del seg
+                self.events_of[k] = c.n_ev
+                self.dratio[k] = c.U / max(1, c.n_ev)
+                if not c.cb:
+                    raise RuntimeError(f"k={k}: more large counts than the escape table holds")
+                try:
+                    sm = summarize(elib, elib, c, vi.ids, ktop, False, ev_fn,
+                                   deep_min=cnt_top if cnt_top is not None else None, defer=True)
+                except RuntimeError as e:
+                    raise RuntimeError(f"k={k}: {e}") from None
+                if sm.stat is not None:  # checked once after the last level: no host read per level
+                    deferred.append((f"k={k}", sm.stat))
+                res.info[k] = dict(contexts=vi.n, ids=vi.ids, pairs=c.U, events=c.n_ev, pbits=c.pbits, hits=None)
+            t3 = time.perf_counter()
             thr = None
             if cnt_top is not None and sm.deep.numel():
                 thr = torch.zeros(vi.ids, dtype=torch.int64, device=dev)
@@ -171,12 +186,14 @@ class LevelBuild:
             e1.record()
             if kept:
                 res.kept[k] = (vi.ctx_of, sm.rec)
-            res.info[k] = dict(contexts=vi.n, ids=vi.ids, pairs=c.U, events=c.n_ev, pbits=c.pbits, hits=None)
             self.host_s["index"] += t1 - t0
             self.host_s["scan"] += t2 - t1
             self.host_s["count"] += t3 - t2
             del vi, c, sm, thr, seen
         del regions
+        if checks32 and self._check32(checks32, res):
+            return self.build(x, tgt, avail, topk=topk, cnt_top=cnt_top, keep=keep, with_mask=with_mask,
+                              stats=stats, _defer=_defer)
         if pending:
             checked = QueryIndex.check(pending)
             redo = False
@@ -208,6 +225,35 @@ class LevelBuild:
                 res.info[k]["probed"] = probed
         return res
 
+    def _check32(self, checks: list, res: LevelOutputs) -> bool:
+        """The 32-bit counts' device results, read in one copy: each level's events and distinct pairs (kept to size
+        the next build), raising on an overflowed emit region, 2^32 or more events, or a total past uint32. Returns
+        whether the build must be redone: a partition overfull (counted again with more partitions) or the escape
+        table full (the level goes to the 64-bit count)."""
+        vals = torch.stack([c[1] for c in checks]).cpu().tolist()
+        redo = False
+        for (k, _, pbits, ids), (n_ev, n_u, fl, sfl) in zip(checks, vals):
+            fl &= 0xFFFFFFFF
+            if sfl & 4:
+                raise RuntimeError(f"k={k}: an emit region overflowed")
+            if n_ev >= 1 << 32:
+                raise RuntimeError(f"k={k}: {n_ev} events: the region scatter's offsets are 32-bit")
+            if fl & 4:
+                raise RuntimeError(f"k={k}: a total does not fit uint32")
+            self.events_of[k] = n_ev
+            self.dratio[k] = n_u / max(1, n_ev)  # n_u counts an overfull partition's pairs only up to its limit
+            if fl & 1:  # a partition held more distinct pairs than its LDS table takes: one more bit, or the 64-bit
+                redo = True  # count when there is none
+                if pbits >= partcount.pbits32_max(ids):
+                    self.wide.add(k)
+                else:
+                    self.min_pbits[k] = pbits + 1
+            if fl & 2:
+                self.wide.add(k)
+                redo = True
+            res.info[k].update(pairs=n_u, events=n_ev)
+        return redo
+
     def _popcount(self, bm: torch.Tensor) -> int:
         n = torch.zeros(1, dtype=torch.int64, device=bm.device)
         self.elib("popcount", bm, bm.numel(), n)
@@ -224,16 +270,18 @@ class LevelBuild:
             return 0
         return 3 if d < LIST_DENSITY else 2
 
-    def _emit(self, k, vi, x, bms, regions, R):
+    def _emit(self, k, vi, x, bms, regions, R, wbits=0):
         """Level k's scan of every shard it counts, hits emitted to per-block regions with each block's top-digit
-        histogram: count_events' seg = (regions, R, ev_count, dhist, nseg, flags)."""
+        histogram: count_events' seg = (regions, R, ev_count, dhist, nseg, flags). wbits: events wmix(pair key,
+        wbits) with histograms of their first_digit(wbits) top bits (count32's), else mix64(pair key)."""
         elib, dev, G = self.elib, self.tok.device, self.grid
         shards = [i for i in range(len(self.sizes)) if i < self.level_shards[k]]
         nseg = len(shards) * G
         ev_count = torch.zeros(max(nseg, 1), dtype=torch.int32, device=dev)
         last = self.events_of.get(k)
-        dhist = torch.empty(256 * max(nseg, 1), dtype=torch.int32, device=dev) \
-            if last is None or last >= partcount.SEG_MIN_EVENTS * nseg else None
+        dbits = first_digit(wbits) if wbits else 8
+        dhist = torch.empty((1 << dbits) * max(nseg, 1), dtype=torch.int32, device=dev) \
+            if wbits or last is None or last >= partcount.SEG_MIN_EVENTS * nseg else None
         flags = torch.zeros(2, dtype=torch.int32, device=dev)
         scans = {tuple(q for q in self.levels if i < self.level_shards[q]) for i in shards}
         if len(shards) > 1 and len(scans) == 1:
@@ -243,7 +291,7 @@ class LevelBuild:
             si = scanned.index(k)
             if si > 0 or self.ready is None:
                 return self._emit_all(k, vi, x, None if si == 0 else bms[scanned[si - 1]], bms[k], shards, regions,
-                                      flags, self._mode(si, scanned))
+                                      flags, self._mode(si, scanned), wbits)
         for j, i in enumerate(shards):
             st, n = self.starts[i], self.sizes[i]
             n32 = (n + 31) // 32 * 32
@@ -265,18 +313,19 @@ class LevelBuild:
             dh = dhist[j * G :] if dhist is not None else None
             if mode == 3:
                 elib("ng_scan_emit_list", self.tok[st:], self._plist, n_list, i32(k), vi.table, u64(vi.cap), vi.rep,
-                     x, bms[k][st // 32 :], regions[j * G * R :], u64(R), ev_count[j * G :], flags, i32(G), dh, nseg)
+                     x, bms[k][st // 32 :], regions[j * G * R :], u64(R), ev_count[j * G :], flags, i32(G), dh, nseg,
+                     i32(wbits), i32(dbits))
             else:
                 elib("ng_scan_emit", self.tok[st:], n32, i32(k), bm_in, bms[k][st // 32 :], vi.table, u64(vi.cap),
                      vi.rep, x, regions[j * G * R :], u64(R), ev_count[j * G :], flags, i32(G), i32(mode), dh, nseg,
-                     self._pre)
+                     self._pre, i32(wbits), i32(dbits))
             e1.record()
         return regions, R, ev_count, dhist, nseg, flags  # count_events checks the flags with its first read
 
-    def _emit_all(self, k, vi, x, bm_in, bm_out, shards, regions, flags, mode):
+    def _emit_all(self, k, vi, x, bm_in, bm_out, shards, regions, flags, mode, wbits=0):
         """_emit of a level whose shards all scan the same levels, in one launch from the first shard's start to the
         last one's end: a lane per position (mode 0), the LDS-listed set positions (2), or one list of the previous
-        level's set bits and one list scan (3)."""
+        level's set bits and one list scan (3); events as _emit's by wbits."""
         elib, dev, G = self.elib, self.tok.device, self.grid
         lo = self.starts[shards[0]]
         hi = self.starts[shards[-1]] + (self.sizes[shards[-1]] + 31) // 32 * 32
@@ -288,8 +337,9 @@ class LevelBuild:
             raise RuntimeError(f"k={k}: the emit regions are too small for one scan over every shard")
         ev_count = torch.zeros(G, dtype=torch.int32, device=dev)
         last = self.events_of.get(k)
-        dhist = torch.empty(256 * G, dtype=torch.int32, device=dev) \
-            if last is None or last >= partcount.SEG_MIN_EVENTS * G else None
+        dbits = first_digit(wbits) if wbits else 8
+        dhist = torch.empty((1 << dbits) * G, dtype=torch.int32, device=dev) \
+            if wbits or last is None or last >= partcount.SEG_MIN_EVENTS * G else None
         if mode == 3:
             if self._plist is None or self._plist.numel() < n:
                 self._plist = torch.empty(n + 64, dtype=torch.int64, device=dev)
@@ -302,10 +352,10 @@ class LevelBuild:
         e0.record()
         if mode == 3:
             elib("ng_scan_emit_list", self.tok[lo:], self._plist, n_list, i32(k), vi.table, u64(vi.cap), vi.rep, x,
-                 bm_out[lo // 32 :], regions, u64(R), ev_count, flags, i32(G), dhist, G)
+                 bm_out[lo // 32 :], regions, u64(R), ev_count, flags, i32(G), dhist, G, i32(wbits), i32(dbits))
         else:
             elib("ng_scan_emit", self.tok[lo:], n, i32(k), None if bm_in is None else bm_in[lo // 32 :],
                  bm_out[lo // 32 :], vi.table, u64(vi.cap), vi.rep, x, regions, u64(R), ev_count, flags, i32(G),
-                 i32(mode), dhist, G, self._pre)
+                 i32(mode), dhist, G, self._pre, i32(wbits), i32(dbits))
         e1.record()
         return regions, R, ev_count, dhist, G, flags

@@ -262,6 +262,148 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids:
 
 RECORD_WORDS = {1: 4, 2: 8, 4: 8, 8: 16}  # u32 words of a context record for top 1, 2, 4, 8
 
+P32_TARGET = 8192  # distinct pairs per partition aimed at by the 32-bit count (its LDS table takes up to 14000)
+P32_LIMIT = 14000  # distinct pairs at which the 32-bit count declares a partition overfull (at most 14000)
+PACK32_MIN_BITS = 0  # context bits of the 32-bit count's packed words at least this (a narrower count field)
+AGG_ID_BITS = 11  # context ids per group of words whose records ng_ctx_agg makes in one block: at most 2^11
+W_MAX = 42  # the widest pair key (context-id bits + 16) the 32-bit count takes: its first pass's digit is at most 10
+            # bits (the emitting scan's histogram) and must leave at most 32 bits below it
+
+
+def w_bits(n_ids: int) -> tuple[int, int]:
+    """(cb, W) of a level with n_ids context ids: the context-id bits and the pair-key bits W = cb + 16."""
+    cb = max(1, (max(n_ids, 2) - 1).bit_length())
+    return cb, cb + 16
+
+
+def first_digit(W: int) -> int:
+    """The 32-bit count's first-pass digit width for W-bit pair keys: at least 8, and at most 32 bits below it."""
+    return max(8, W - 32)
+
+
+@dataclass
+class Counted32:
+    """A level counted by count32: per context id its record (int32 [n_ids, RECORD_WORDS[ktop]]) and pair count
+    dist (int32 [n_ids], 0 for absent contexts), per query position the target's count qcnt (int32 [N]), and the
+    device-side results the host checks once per build (`stat`: int64 [4] = events, distinct pairs, the count's flags,
+    the scan's flags; bit 0 of the count's flags: a partition overfull, bit 1: the escape table full, bit 2: a total
+    reached 2^32; bit 2 of the scan's: a region overflowed)."""
+
+    rec: torch.Tensor
+    dist: torch.Tensor
+    qcnt: torch.Tensor | None
+    stat: torch.Tensor
+    pbits: int
+    cb: int
+    esc: tuple
+
+
+def pbits32_max(n_ids: int) -> int:
+    """The most partition bits the 32-bit count takes for a level of n_ids context ids."""
+    W = w_bits(n_ids)[1]
+    return min(first_digit(W) + 11, W - 1)
+
+
+def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None, n_events: int | None,
+            ratio: float = 1.0, event=_no_event, min_pbits: int = 0) -> Counted32:
+    """Count a level's events emitted by ng_scan_emit in the W-bit mode (wbits = W = w_bits(n_ids)[1], dbits =
+    first_digit(W); seg = (regions, R, ev_count, dhist, nseg, scan flags)) and make every present context's record
+    (top ktop) without a host read: the passes and the count of pairs32.hip. `n_events`: the level's events (the last
+    build's; None: read from the device here, one host sync), which with `ratio` (distinct pairs per event) sizes the
+    partitions, with at least min_pbits partition bits (and at most pbits32_max(n_ids)); `lookups` as count_events'."""
+    regions, R, ev_count, dhist, nseg, scan_flags = seg
+    dev = regions.device
+    idb, W = w_bits(n_ids)
+    cb = max(idb, PACK32_MIN_BITS)  # the words' context field: idb bits used, cb - idb zero bits above them
+    if W > W_MAX:
+        raise ValueError(f"{n_ids} context ids: wider than the 32-bit count takes")
+    d1 = first_digit(W)
+    cap = nseg * R
+    stat = torch.zeros(4, dtype=torch.int64, device=dev)  # events, distinct pairs, count flags, scan flags
+    ev_tot, u_tot = stat[0:1], stat[1:2]
+    flags = stat[2:3].view(torch.int32)[:1]
+    dpre = torch.empty((1 << d1) * nseg, dtype=torch.int32, device=dev)
+    elib.cub("ng_exclusive_scan_u32", dhist, dpre, (1 << d1) * nseg, ev_tot)
+    stat[3:4].copy_(scan_flags[:1])
+    if n_events is None:
+        n_events = int(ev_tot.item())
+    pbits = max(d1 + 1, PART_MIN_BITS if lookups is not None else 0, min_pbits,
+                math.ceil(math.log2(max(1.0, n_events * ratio / P32_TARGET))))
+    pbits = min(pbits, pbits32_max(n_ids))
+    d2 = pbits - d1
+    e0, e1 = event("partition", cap)
+    e0.record()
+    ev32 = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
+    elib("ng_seg_scatter_narrow", regions, u64(R), None, ev_count, dpre, nseg, i32(W - d1), i32(d1), ev32, u64(cap))
+    ev32b = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
+    P = 1 << pbits
+    start = torch.empty(P + 1, dtype=torch.int64, device=dev)
+    elib.cub("ng_msd_pass", ev32, dpre, nseg, i32(d1), ev_tot, u64(cap), i32(W - pbits), i32(d2), ev32b, start)
+    del ev32, dpre
+    N = nq = 0
+    sqk = sqv = None
+    qstart = torch.zeros(P + 1, dtype=torch.int64, device=dev)
+    if lookups is not None:
+        ctx_of, tgt, qpos = lookups
+        N = ctx_of.numel()
+        nq = N if qpos is None else qpos.numel()
+    if nq:
+        qk = torch.empty(nq, dtype=torch.int64, device=dev)
+        qv = torch.empty(nq, dtype=torch.int32, device=dev)
+        elib("ng_part_lookups_w", ctx_of, tgt, qpos, nq, 0, n_ids, i32(W), qk, qv)
+        sqk = torch.empty(nq, dtype=torch.int64, device=dev)
+        sqv = torch.empty(nq, dtype=torch.int32, device=dev)
+        elib.cub("sort_pairs", qk, sqk, qv, sqv, nq, i32(64 - pbits), i32(64))
+        del qk, qv
+        elib("ng_part_bounds", sqk, nq, i32(pbits), i32(0), qstart)
+    e1.record()
+    G2 = min(P, PART_BLOCKS)
+    dc = min(11, idb)
+    dtop = 64 - (cb - idb)  # the bit above a word's highest id bit
+    out_k = torch.empty(max(cap, 1), dtype=torch.int64, device=dev)
+    esc_k = torch.full((ESC_CAP,), -1, dtype=torch.int64, device=dev)
+    esc_c = torch.empty(ESC_CAP, dtype=torch.int32, device=dev)
+    seg_cnt = torch.empty(G2, dtype=torch.int32, device=dev)
+    seg_base = torch.empty(G2, dtype=torch.int64, device=dev)
+    qcnt = torch.zeros(max(N, 1), dtype=torch.int32, device=dev) if N else None
+    dh2 = torch.empty((1 << dc) * G2, dtype=torch.int32, device=dev)
+    e0, e1 = event("count", cap)
+    e0.record()
+    elib("ng_part_count32", ev32b, start, i32(pbits), i32(W), sqk, sqv, qstart, out_k, i32(cb), esc_k, esc_c,
+         u64(ESC_CAP), seg_cnt, seg_base, qcnt, dh2, i32(dtop - dc), i32(dc), ctypes.c_uint32(P32_LIMIT), flags,
+         i32(G2))
+    e1.record()
+    del ev32b, start, sqk, sqv, qstart
+    # the words grouped by context: by their top dc bits (ng_seg_scatter), then within those groups by the next d2
+    # bits (ng_msd_pass64), so that a group holds at most 2^11 ids, whose records ng_ctx_agg makes in LDS
+    d2 = max(0, idb - dc - AGG_ID_BITS)
+    ibits = idb - dc - d2
+    P2 = 1 << (dc + d2)
+    dpre2 = torch.empty((1 << dc) * G2, dtype=torch.int32, device=dev)
+    words = torch.empty(max(cap, 1), dtype=torch.int64, device=dev)
+    start2 = torch.empty(P2 + 1, dtype=torch.int64, device=dev)
+    e0, e1 = event("sort", cap)
+    e0.record()
+    elib.cub("ng_exclusive_scan_u32", dh2, dpre2, (1 << dc) * G2, u_tot)
+    elib("ng_seg_scatter", out_k, u64(0), seg_base, seg_cnt, dpre2, G2, i32(dtop - dc), i32(dc), words, u64(cap))
+    if d2:
+        elib.cub("ng_msd_pass64", words, dpre2, G2, i32(dc), u_tot, u64(cap), i32(dtop - dc - d2), i32(d2), out_k,
+                 start2)
+        words, out_k = out_k, words
+    else:
+        elib.cub("ng_msd_pass64", None, dpre2, G2, i32(dc), u_tot, u64(cap), i32(0), i32(0), None, start2)
+    e1.record()
+    del out_k, dh2, seg_cnt, seg_base, dpre2
+    rec = torch.empty((max(n_ids, 1), RECORD_WORDS[ktop]), dtype=torch.int32, device=dev)
+    dist = torch.empty(max(n_ids, 1), dtype=torch.int32, device=dev)
+    e0, e1 = event("ctx_topk", cap)
+    e0.record()
+    elib("ng_ctx_agg", words, start2, P2, i32(ibits), i32(cb), n_ids, esc_k, esc_c, u64(ESC_CAP), i32(ktop), rec,
+         dist, flags)
+    e1.record()
+    return Counted32(rec, dist, qcnt, stat, pbits, cb, (esc_k, esc_c))
+
+
 
 @dataclass
 class Summary:

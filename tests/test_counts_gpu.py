@@ -37,8 +37,22 @@ def _reference(corpus, levels, level_shards, ntop=8):
 
 @pytest.mark.parametrize("level_shards,mode", [({}, "part"), ({2: 1, 3: 2}, "part"), ({}, "compact"),
                                                ({2: 1, 3: 2}, "regroup"), ({}, "escape"), ({}, "seg"),
-                                               ({2: 1, 3: 2}, "seg"), ({}, "list"), ({2: 1, 3: 2}, "list")])
+                                               ({2: 1, 3: 2}, "seg"), ({}, "list"), ({2: 1, 3: 2}, "list"),
+                                               ({}, "regroup32"), ({2: 1, 3: 2}, "escape32"), ({}, "wide")])
 def test_counts_match_oracle(corpus, level_shards, mode, monkeypatch):
+    """Modes: the 32-bit count (part, compact, list; regroup32: partitions overfull at 64 distinct pairs, so each
+    level is counted again with one more partition bit until none is; escape32: an 8-bit count field, larger counts in
+    the escape table; wide: that table too small, so the level is counted again by the 64-bit path) and the 64-bit
+    path (regroup, escape, seg: W_MAX 0 sends every level there)."""
+    if mode in ("regroup", "escape", "seg"):
+        monkeypatch.setattr(P, "W_MAX", 0)
+        monkeypatch.setattr(levels_mod, "W_MAX", 0)
+    if mode == "regroup32":
+        monkeypatch.setattr(P, "P32_LIMIT", 64)
+    if mode in ("escape32", "wide"):
+        monkeypatch.setattr(P, "PACK32_MIN_BITS", 40)
+    if mode == "wide":
+        monkeypatch.setattr(P, "ESC_CAP", 16)
     if mode == "regroup":
         # one partition per level to start with: each level's LDS table overflows and it is repartitioned bit by bit;
         # three blocks, each counting a run of partitions
@@ -76,6 +90,12 @@ def test_counts_match_oracle(corpus, level_shards, mode, monkeypatch):
         assert cb.info[k]["hits"] == o["events"], f"hits k={k}"
     if mode == "regroup":
         assert cb.info[2]["pbits"] >= 3, cb.info[2]
+    if mode == "regroup32":
+        assert cb.engine.min_pbits.get(2, 0) > 11, cb.engine.min_pbits
+    if mode == "wide":
+        assert 2 in cb.engine.wide, cb.engine.wide
+    if mode in ("part", "escape32", "regroup32"):
+        assert not cb.engine.wide, cb.engine.wide
     assert (ref[2]["tot"] > 0).sum() > 1000 and (ref[20]["tot"] > 0).sum() > 10
     # the record's rows from ROW_LEVELS (ng_record_rows), and a batch of them (ng_batch_rows)
     tot_rows = np.stack([ref[k]["tot"] for k in C.ROW_LEVELS])

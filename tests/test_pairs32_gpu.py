@@ -1,0 +1,124 @@
+"""GPU: the 32-bit count's passes (pairs32.hip) on their own against numpy: the second, most-significant-digit-first
+pass (ng_msd_pass: every bucket's keys sub-grouped by the next digit, the partitions' starts) and the first pass's
+narrowing scatter (ng_seg_scatter_narrow), with empty buckets, a bucket spanning many tiles, and keys placed beyond
+the capacity dropped."""
+
+import numpy as np
+import pytest
+import torch
+
+from ngram_amd.lib import i32, u64
+
+pytestmark = pytest.mark.gpu
+
+
+def _msd(lib, sizes, nb_bits, nbits, shift, seed=0):
+    rng = np.random.default_rng(seed)
+    nb = 1 << nb_bits
+    assert len(sizes) == nb
+    total = int(sum(sizes))
+    keys = rng.integers(0, 1 << 32, total, dtype=np.uint64).astype(np.uint32)
+    starts = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+    # dpre as a first pass leaves it for one segment: digit b's offset
+    nseg = 1
+    dpre = torch.from_numpy(starts[:-1].astype(np.uint32).view(np.int32)).cuda()
+    tot = torch.tensor([total], dtype=torch.int64, device="cuda")
+    cap = total + 100
+    kin = torch.zeros(cap, dtype=torch.int32, device="cuda")
+    kin[:total] = torch.from_numpy(keys.view(np.int32)).cuda()
+    out = torch.full((cap,), -1, dtype=torch.int32, device="cuda")
+    P = nb << nbits
+    start = torch.empty(P + 1, dtype=torch.int64, device="cuda")
+    lib.cub("ng_msd_pass", kin, dpre, nseg, i32(nb_bits), tot, u64(cap), i32(shift), i32(nbits), out, start)
+    o = out.cpu().numpy().view(np.uint32)[:total]
+    st = start.cpu().numpy()
+    assert st[0] == 0 and st[-1] == total and (np.diff(st) >= 0).all()
+    for b in range(nb):
+        kb = keys[starts[b] : starts[b + 1]]
+        dig = (kb >> shift) & ((1 << nbits) - 1)
+        for d in np.unique(dig) if len(kb) else []:
+            p = (b << nbits) | int(d)
+            got = np.sort(o[st[p] : st[p + 1]])
+            assert np.array_equal(got, np.sort(kb[dig == d])), (b, d)
+        # partitions of digits absent from the bucket are empty
+        present = set(np.unique(dig).tolist()) if len(kb) else set()
+        for d in range(1 << nbits):
+            if d not in present:
+                p = (b << nbits) | d
+                assert st[p] == st[p + 1], (b, d)
+    assert (out.cpu().numpy()[total:] == -1).all()
+
+
+def test_msd_pass_small(lib):
+    sizes = [0, 5, 1, 0, 100, 0, 0, 3] + [7] * 248
+    _msd(lib, sizes, 8, 3, 5)
+
+
+def test_msd_pass_bucket_of_many_tiles(lib):
+    sizes = [0] * 256
+    sizes[3] = 200_000  # 13 tiles of 16384 keys
+    sizes[200] = 16_384
+    sizes[255] = 16_385
+    _msd(lib, sizes, 8, 11, 21, seed=1)
+
+
+def test_msd_pass_wide_buckets(lib):
+    rng = np.random.default_rng(2)
+    sizes = rng.integers(0, 3000, 1024).tolist()
+    _msd(lib, sizes, 10, 7, 25, seed=3)
+
+
+def test_seg_scatter_narrow(lib):
+    """Region segments of u64 keys scattered by their digit at bit 28 (4 bits) and narrowed to the low 32 bits."""
+    rng = np.random.default_rng(4)
+    nseg, R = 5, 3000
+    counts = rng.integers(0, R + 1, nseg).astype(np.uint32)
+    counts[2] = 0
+    regions = rng.integers(0, 1 << 32, nseg * R, dtype=np.uint64)  # keys below 2^32: digit bits [28, 32)
+    shift, nbits = 28, 4
+    hist = np.zeros((1 << nbits, nseg), np.uint32)
+    for s in range(nseg):
+        k = regions[s * R : s * R + counts[s]]
+        hist[:, s] = np.bincount((k >> shift) & 15, minlength=16)
+    flat = hist.reshape(-1)
+    dpre = np.concatenate([[0], np.cumsum(flat)[:-1]]).astype(np.uint32)
+    total = int(flat.sum())
+    out = torch.full((total,), -1, dtype=torch.int32, device="cuda")
+    lib("ng_seg_scatter_narrow", torch.from_numpy(regions.view(np.int64)).cuda(), u64(R), None,
+        torch.from_numpy(counts.view(np.int32)).cuda(), torch.from_numpy(dpre.view(np.int32)).cuda(), nseg,
+        i32(shift), i32(nbits), out, u64(total))
+    o = out.cpu().numpy().view(np.uint32)
+    allk = np.concatenate([regions[s * R : s * R + counts[s]] for s in range(nseg)]).astype(np.uint32)
+    starts = np.concatenate([[0], np.cumsum(hist.sum(axis=1))]).astype(np.int64)
+    for d in range(16):
+        seg = o[starts[d] : starts[d + 1]]
+        assert np.array_equal(np.sort(seg), np.sort(allk[((allk >> shift) & 15) == d])), d
+
+
+def test_msd_pass64_words_by_context(lib):
+    """The words' second pass: u64 keys grouped by their top 11 bits, sub-grouped by the next 4 (ng_msd_pass64), and
+    the buckets' starts alone (nbits 0)."""
+    rng = np.random.default_rng(5)
+    n = 300_000
+    keys = rng.integers(0, 1 << 63, n, dtype=np.uint64) * np.uint64(2) + rng.integers(0, 2, n, dtype=np.uint64)
+    top = (keys >> np.uint64(53)).astype(np.int64)
+    order = np.argsort(top, kind="stable")
+    keys = keys[order]
+    counts = np.bincount(top, minlength=2048)
+    starts = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    dpre = torch.from_numpy(starts[:-1].astype(np.uint32).view(np.int32)).cuda()
+    tot = torch.tensor([n], dtype=torch.int64, device="cuda")
+    kin = torch.from_numpy(keys.view(np.int64)).cuda()
+    out = torch.empty(n, dtype=torch.int64, device="cuda")
+    start = torch.empty(2048 * 16 + 1, dtype=torch.int64, device="cuda")
+    lib.cub("ng_msd_pass64", kin, dpre, 1, i32(11), tot, u64(n), i32(49), i32(4), out, start)
+    o = out.cpu().numpy().view(np.uint64)
+    st = start.cpu().numpy()
+    sub = (keys >> np.uint64(49)).astype(np.int64)  # bucket << 4 | digit
+    cnt = np.bincount(sub, minlength=2048 * 16)
+    assert np.array_equal(st, np.concatenate([[0], np.cumsum(cnt)]))
+    for p in np.unique(sub)[:: 97]:
+        assert np.array_equal(np.sort(o[st[p] : st[p + 1]]), np.sort(keys[sub == p])), p
+    bst = torch.empty(2049, dtype=torch.int64, device="cuda")
+    lib.cub("ng_msd_pass64", None, dpre, 1, i32(11), tot, u64(n), i32(0), i32(0), None, bst)
+    assert np.array_equal(bst.cpu().numpy(), starts)
