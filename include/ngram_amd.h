@@ -183,13 +183,15 @@ int ng_pos_gather(const int* ctx_of, ng_i64 N, ng_i64 lo, ng_i64 hi, const uint1
                   const uint32_t* pcnts, ng_u64 pcap, const uint32_t* qcnt, int ktop, int kout, int li, int* out_tot,
                   int* out_dist, int* out_cnt, uint16_t* out_tok, uint32_t* out_tcnt, int* mask, void* stream);
 /* query index without a sort (replaces gpu_val_stats.py:604-651's sort-based one where ids need not agree across
- * ranks): valid k-contexts of positions pos[0..n) (NULL: 0..n) inserted by compare-and-swap into table (cap + tail
+ * ranks): valid k-contexts of positions pos[0..n) (NULL: 0..n; n_dev (may be NULL, pos required): a device-side count,
+ * pos[0..min(n, *n_dev)) only) inserted by compare-and-swap into table (cap + tail
  * slots, EMPTY-filled, linear probing without wrap from umulhi(key, cap)); ctx_of[i] = slot or -1 (compact:
  * ctx_of[j] for pos[j]), rep[slot] = the inserting position; counters[0] += the table's occupied slots
  * afterwards, counters[1] != 0: the table is too small (a probe reached its end or walked 256 slots),
  * counters[2] += key collisions found against the representative (k > 4) */
-int ng_query_index(const uint16_t* x, const int* avail, const int* pos, ng_i64 n, int k, ng_u64* table, ng_u64 cap,
-                   ng_u64 slots, uint32_t* rep, int* ctx_of, int compact, ng_u64* counters, void* stream);
+int ng_query_index(const uint16_t* x, const int* avail, const int* pos, ng_i64 n, const ng_u64* n_dev, int k,
+                   ng_u64* table, ng_u64 cap, ng_u64 slots, uint32_t* rep, int* ctx_of, int compact,
+                   ng_u64* counters, void* stream);
 /* move a query index into a smaller EMPTY-filled table (cap + tail = slots): ctx_of[0..n) re-pointed, remap
  * (old_slots ints) scratch, counters[1] = 1 on reaching the new table's end */
 int ng_query_index_shrink(const ng_u64* old_t, const uint32_t* old_rep, ng_u64 old_slots, ng_u64* table, ng_u64 cap,
@@ -246,15 +248,20 @@ int ng_msd_pass(void* temp, size_t* temp_bytes, const uint32_t* keys, const uint
 int ng_msd_pass64(void* temp, size_t* temp_bytes, const ng_u64* keys, const uint32_t* dpre, ng_i64 nseg, int nb_bits,
                   const ng_u64* total, ng_u64 cap, int shift, int nbits, ng_u64* out, ng_i64* start, void* stream);
 /* lookups of n query positions i = pos[j] (pos NULL: j) for the 32-bit count: qk[j] = wmix(ctx_of[i] << 16 | tgt[i],
- * W) << (64 - W) for ids in [lo, hi) (hi <= 2^(W - 16)), else EMPTY; qv[j] = i */
-int ng_part_lookups_w(const int* ctx_of, const uint16_t* tgt, const int* pos, ng_i64 n, ng_i64 lo, ng_i64 hi, int W,
-                      ng_u64* qk, uint32_t* qv, void* stream);
+ * W) << (64 - W) for ids in [lo, hi) (hi <= 2^(W - 16)), else EMPTY; qv[j] = i; n_dev (may be NULL, pos required): a
+ * device-side count of pos's entries, lookups j >= *n_dev EMPTY */
+int ng_part_lookups_w(const int* ctx_of, const uint16_t* tgt, const int* pos, ng_i64 n, const ng_u64* n_dev, ng_i64 lo,
+                      ng_i64 hi, int W, ng_u64* qk, uint32_t* qv, void* stream);
+/* the positions i < n with v[i] > 0, in order, into out (at most cap of them); *n_dev = how many (may exceed cap);
+ * two-phase temp storage; no host read */
+int ng_select_positive(void* temp, size_t* temp_bytes, const int* v, ng_i64 n, int* out, ng_i64 cap, ng_u64* n_dev,
+                       void* stream);
 /* the 32-bit count of ng_msd_pass's partitions (2^pbits of them, 1 <= W - pbits <= 31, W = context-id bits + 16) in
  * LDS with `grid` blocks (<= 65536): block b's distinct pairs as packed words pair key << (48 - cb) | min(count,
  * esc), esc = 2^(48 - cb) - 1 (W - 16 <= cb <= 44; larger counts also in the escape table), at out_k + seg_base[b],
  * seg_cnt[b] of them; dhist[d * grid + b] its words per dbits-bit digit (word >> dshift) & (2^dbits - 1), dbits <=
  * 11; qcnt[qv[j]] = the count of lookup j (ng_part_lookups_w's sorted by their top pbits, bounds qstart); flags[0]
- * bit 0: a partition reached min(limit, 14000) distinct pairs (count again with a bit more), bit 1: the escape table
+ * bit 0: a partition reached min(limit, 13000) distinct pairs (count again with a bit more), bit 1: the escape table
  * is full */
 int ng_part_count32(const uint32_t* ev, const ng_i64* start, int pbits, int W, const ng_u64* qk, const uint32_t* qv,
                     const ng_i64* qstart, ng_u64* out_k, int cb, ng_u64* esc_k, uint32_t* esc_c, ng_u64 esc_cap,

@@ -1148,20 +1148,21 @@ extern "C" int ng_query_index_shrink(const u64* old_t, const u32* old_rep, u64 o
     return (int)hipGetLastError();
 }
 
-// Insert the valid query contexts of positions pos[0..n) (pos NULL: 0..n) into table (cap + tail slots, EMPTY-filled):
+// Insert the valid query contexts of positions pos[0..n) (pos NULL: 0..n; with n_dev, pos[0..min(n, *n_dev)): a
+// device-side count) into table (cap + tail slots, EMPTY-filled):
 // ctx_of[i] = slot (-1 where invalid; with pos, only listed positions are written; compact: ctx_of[j] for pos[j],
 // n entries), rep[slot] = the position that inserted it.
 // counters[0] += the table's occupied slots afterwards (its contexts), counters[1] bit 0 if a probe ran into the
 // table's end, bit 1 if an insert walked QI_MAXWALK slots (a table too small: build it bigger); with k > 4, counters[2] += positions whose tokens differ from their slot's representative (a 64-bit
 // key collision).
-extern "C" int ng_query_index(const u16* x, const int* avail, const int* pos, i64 n, int k, u64* table, u64 cap,
-                              u64 slots, u32* rep, int* ctx_of, int compact, u64* counters,
+extern "C" int ng_query_index(const u16* x, const int* avail, const int* pos, i64 n, const u64* n_dev, int k,
+                              u64* table, u64 cap, u64 slots, u32* rep, int* ctx_of, int compact, u64* counters,
                               void* stream) {
     if (n <= 0) return 0;
-    if (cap == 0 || slots <= cap || slots > (1ull << 31)) return -1;
+    if (cap == 0 || slots <= cap || slots > (1ull << 31) || (n_dev && !pos)) return -1;
     hipStream_t st = (hipStream_t)stream;
-    LEVEL_DISPATCH(k, (qindex_insert_k<K><<<grid_for(n, 256), 256, 0, st>>>(x, avail, pos, n, k, table, cap, slots, rep, ctx_of, compact, counters)));
-    if (k > 4) qindex_verify_k<<<grid_for(n, 256), 256, 0, st>>>(x, pos, n, k, ctx_of, compact, rep, counters + 2);
+    LEVEL_DISPATCH(k, (qindex_insert_k<K><<<grid_for(n, 256), 256, 0, st>>>(x, avail, pos, n, k, table, cap, slots, rep, ctx_of, compact, counters, n_dev)));
+    if (k > 4) qindex_verify_k<<<grid_for(n, 256), 256, 0, st>>>(x, pos, n, k, ctx_of, compact, rep, counters + 2, n_dev);
     const int g = grid_for((i64)slots, 256);
     count_occupied_k<<<g < 1024 ? g : 1024, 256, 0, st>>>(table, slots, counters);
     return (int)hipGetLastError();

@@ -9,7 +9,7 @@
 //   3. ng_msd_pass sub-groups each of those buckets by the next d2 bits (tiles within a bucket, LDS-staged), giving
 //      2^(d1 + d2) partitions = the top pbits = d1 + d2 bits of h, and each partition's start;
 //   4. ng_part_count32 counts every partition in an LDS table of u32 keys (the h bits below the partition, unique
-//      within it: 16384 slots in buckets of four, one 16-byte read per bucket), answers the partition's lookups and
+//      within it: 14336 slots in buckets of four, one 16-byte read per bucket), answers the partition's lookups and
 //      writes each distinct pair, unhashed, as a packed word (pair key << (48 - cb) | count) with a histogram of the
 //      words' top context bits;
 //   5. ng_seg_scatter groups the words by those context bits (dc = min(11, cb));
@@ -127,67 +127,124 @@ __global__ void msd_starts_k(const i64* __restrict__ bstart, const u32* __restri
 // ids in [lo, hi) (the partition digits then are its top bits, as the events'), else EMPTY (no such key: its low
 // 64 - W bits are ones); value i.
 __global__ void lookups_w_k(const int* __restrict__ ctx_of, const u16* __restrict__ tgt, const int* __restrict__ pos,
-                            i64 n, i64 lo, i64 hi, int W, u64* __restrict__ qk, u32* __restrict__ qv) {
+                            i64 n, const u64* __restrict__ n_dev, i64 lo, i64 hi, int W, u64* __restrict__ qk,
+                            u32* __restrict__ qv) {
     const i64 j = blockIdx.x * (i64)blockDim.x + threadIdx.x;
     if (j >= n) return;
+    if (n_dev && (u64)j >= *n_dev) {  // past a device-side count of pos's entries
+        qk[j] = EMPTY;
+        qv[j] = 0;
+        return;
+    }
     const i64 i = pos ? pos[j] : j;
     const i64 c = ctx_of[i];
     qk[j] = (c >= lo && c < hi) ? wmix(((u64)c << 16) | tgt[i], W) << (64 - W) : EMPTY;
     qv[j] = (u32)i;
 }
 
-#define P32_SLOTS 16384  // 128 KB of LDS (u32 keys and counts): one block per CU
+// The positions i < n with v[i] > 0, in order: SEL_ITEMS consecutive positions per thread, a block of 256 threads
+// per 256 * SEL_ITEMS. sel_count_k counts each block's; sel_write_k writes them from the blocks' exclusive offsets
+// (at most cap of them: out holds cap).
+#define SEL_ITEMS 16
+__global__ void __launch_bounds__(256) sel_count_k(const int* __restrict__ v, i64 n, u32* __restrict__ cnt) {
+    __shared__ u32 part[256 / WAVE];
+    const i64 a = (blockIdx.x * (i64)256 + threadIdx.x) * SEL_ITEMS;
+    u32 c = 0;
+#pragma unroll
+    for (int j = 0; j < SEL_ITEMS; ++j) c += (a + j < n && v[a + j] > 0) ? 1u : 0u;
+#pragma unroll
+    for (int d = WAVE / 2; d > 0; d >>= 1) c += (u32)__shfl_down((int)c, d, WAVE);
+    if (lane_id() == 0) part[threadIdx.x / WAVE] = c;
+    __syncthreads();
+    if (threadIdx.x == 0) cnt[blockIdx.x] = part[0] + part[1] + part[2] + part[3];
+}
+
+__global__ void __launch_bounds__(256) sel_write_k(const int* __restrict__ v, i64 n, const u32* __restrict__ off,
+                                                   int* __restrict__ out, i64 cap) {
+    __shared__ u32 wt[256 / WAVE];
+    const int lane = lane_id(), w = threadIdx.x / WAVE;
+    const i64 a = (blockIdx.x * (i64)256 + threadIdx.x) * SEL_ITEMS;
+    u32 bits = 0;
+#pragma unroll
+    for (int j = 0; j < SEL_ITEMS; ++j) bits |= (a + j < n && v[a + j] > 0) ? 1u << j : 0u;
+    const u32 c = (u32)__popc(bits);
+    u32 incl = c;
+#pragma unroll
+    for (int d = 1; d < WAVE; d <<= 1) {
+        const u32 o = (u32)__shfl_up((int)incl, d, WAVE);
+        if (lane >= d) incl += o;
+    }
+    if (lane == WAVE - 1) wt[w] = incl;
+    __syncthreads();
+    u64 at = (u64)off[blockIdx.x] + incl - c;
+    for (int i = 0; i < w; ++i) at += wt[i];
+    while (bits) {
+        const int j = __ffs(bits) - 1;
+        bits &= bits - 1;
+        if (at < (u64)cap) out[at] = (int)(a + j);
+        ++at;
+    }
+}
+
+#define P32_SLOTS 14336  // 112 KB of LDS (u32 keys and counts) beside the slot list (28 KB): one block per CU
 #define P32_BUCKETS (P32_SLOTS / 4)
 #define P32_BLOCK 1024
-#define P32_ITEMS 8
-#define P32_LIMIT 14000  // distinct pairs a partition may reach before it is declared overfull (a free slot always
+#define P32_ITEMS 6  // events per thread and round (8 spills registers)
+#define P32_LIMIT 13000  // distinct pairs a partition may reach before it is declared overfull (a free slot always
                          // remains: at most P32_LIMIT + P32_BLOCK keys are ever inserted)
 #define EMPTY32 0xFFFFFFFFu
 
 __device__ __forceinline__ u32 p32_bucket(u32 key) {
     return (u32)(((u64)(key * 0x9E3779B1u) * P32_BUCKETS) >> 32);
 }
+__device__ __forceinline__ u32 p32_next(u32 b) { return b + 1 == P32_BUCKETS ? 0 : b + 1; }
 
-// Count `add` occurrences of `key` (below 2^31) in the bucketized table (four keys per 16-byte bucket, filled from the
-// front, buckets probed linearly); returns whether it took a free slot. A lost race for a slot re-reads the bucket.
-__device__ __forceinline__ bool p32_add(u32* tk, u32* tc, u32 key, u32 add) {
-    u32 b = p32_bucket(key);
-    int slot = -1;
-    bool fresh = false;
-    while (slot < 0) {
-        const uint4 q = *(const uint4*)(tk + 4 * b);
-        const int f = q.x == key ? 0 : q.y == key ? 1 : q.z == key ? 2 : q.w == key ? 3 : -1;
+// The slot of `key` in bucket q (read from bucket b), or -1.
+__device__ __forceinline__ int p32_in(const uint4& q, u32 b, u32 key) {
+    const int f = q.x == key ? 0 : q.y == key ? 1 : q.z == key ? 2 : q.w == key ? 3 : -1;
+    return f < 0 ? -1 : 4 * (int)b + f;
+}
+
+// Insert `key` (below 2^31) into the bucketized table (four keys per 16-byte bucket, filled from the front, buckets
+// probed linearly) from bucket b, whose contents q were read; returns its slot, *fresh whether it took a free slot.
+// A lost race for a slot re-reads the bucket.
+__device__ __forceinline__ int p32_insert(u32* tk, u32 key, u32 b, uint4 q, bool* fresh) {
+    *fresh = false;
+    while (true) {
+        const int s = p32_in(q, b, key);
+        if (s >= 0) return s;
         const int e = q.x == EMPTY32 ? 0 : q.y == EMPTY32 ? 1 : q.z == EMPTY32 ? 2 : q.w == EMPTY32 ? 3 : -1;
-        if (f >= 0) {
-            slot = 4 * (int)b + f;
-        } else if (e >= 0) {
+        if (e >= 0) {
             const u32 prev = atomicCAS(&tk[4 * b + e], EMPTY32, key);
             if (prev == EMPTY32 || prev == key) {
-                slot = 4 * (int)b + e;
-                fresh = prev == EMPTY32;
+                *fresh = prev == EMPTY32;
+                return 4 * (int)b + e;
             }
         } else {
-            b = (b + 1) & (P32_BUCKETS - 1);
+            b = p32_next(b);
         }
+        q = *(const uint4*)(tk + 4 * b);
     }
-    atomicAdd(&tc[slot], add);
-    return fresh;
 }
 
 __device__ __forceinline__ u32 p32_find(const u32* tk, const u32* tc, u32 key) {
     u32 b = p32_bucket(key);
     while (true) {
         const uint4 q = *(const uint4*)(tk + 4 * b);
-        const int f = q.x == key ? 0 : q.y == key ? 1 : q.z == key ? 2 : q.w == key ? 3 : -1;
-        if (f >= 0) return tc[4 * b + f];
+        const int s = p32_in(q, b, key);
+        if (s >= 0) return tc[s];
         if (q.w == EMPTY32) return 0;
-        b = (b + 1) & (P32_BUCKETS - 1);
+        b = p32_next(b);
     }
 }
 
 // Block b counts the partitions it owns (part_owner: about equal events per block) in turn. Events: u32, a
-// partition's key = its low lbits = W - pbits bits (h = p << lbits | key). Its distinct pairs (at most its events) go
-// to out_k[start[p0] ...] as packed words: segment b = (seg_base[b], seg_cnt[b]); dhist[d * G + b] its words per
+// partition's key = its low lbits = W - pbits bits (h = p << lbits | key). A round of P32_ITEMS events per thread:
+// the lanes holding a wave's first key add once for all of them (a hot pair would serialize the LDS atomics); every
+// item's home bucket is read before any is used, an item whose key is there adds to its count, and the others are
+// inserted (a compare-and-swap on the bucket's first free slot), each new slot appended to the partition's slot list.
+// The output pass walks the list only (not the whole table): its distinct pairs (at most its events) go to
+// out_k[start[p0] ...] as packed words, segment b = (seg_base[b], seg_cnt[b]); dhist[d * G + b] the block's words per
 // dbits-bit digit at dshift. Lookups: qk (sorted like the events: wmix keys << (64 - W), or EMPTY), qv their query
 // positions, qstart their partitions' bounds: qcnt[qv[j]] = the pair's count or 0. A partition reaching `limit`
 // distinct pairs (at most P32_LIMIT) sets flags[0] bit 0 and is left incomplete.
@@ -201,9 +258,9 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
                                                       u32* flags) {
     __shared__ __align__(16) u32 tk[P32_SLOTS];
     __shared__ u32 tc[P32_SLOTS];
+    __shared__ u16 list[P32_SLOTS];
     __shared__ u32 dh[SS_MAXB];
-    __shared__ u32 cur;
-    __shared__ u32 nocc;
+    __shared__ u32 nocc;  // the partition's distinct pairs so far = the list's length
     const int t = threadIdx.x, lane = lane_id();
     const int lbits = W - pbits;
     const u32 lmask = (1u << lbits) - 1u;
@@ -219,10 +276,8 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
         return;
     }
     const i64 out_base = start[p0];
-    if (t == 0) {
-        cur = 0;
-        nocc = 0;
-    }
+    u32 cur = 0;  // the block's words so far (block-uniform)
+    if (t == 0) nocc = 0;
     for (int d = t; d < nd; d += P32_BLOCK) dh[d] = 0;
     for (int j = t; j < P32_SLOTS; j += P32_BLOCK) {
         tk[j] = EMPTY32;
@@ -251,7 +306,7 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
         }
         if (ahead_of != p && a < b) load_round(ahead, a, b);
         for (i64 i0 = a; i0 < b; i0 += ROUND) {
-            u32 key[P32_ITEMS];
+            u32 key[P32_ITEMS], add[P32_ITEMS];
 #pragma unroll
             for (int r = 0; r < P32_ITEMS; ++r) key[r] = ahead[r];
             if (i0 + ROUND < b) {
@@ -261,59 +316,90 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
                 load_round(ahead, b, start[p + 2]);
                 ahead_of = p + 1;
             }
+            // the lanes holding the wave's first key add once (a hot pair would serialize the LDS atomics); the
+            // item's add is 0 where another lane adds for it
 #pragma unroll
             for (int r = 0; r < P32_ITEMS; ++r) {
                 const bool valid = key[r] != EMPTY32;
                 const u64 vb = __ballot(valid);
-                if (!vb) continue;
-                if (__builtin_amdgcn_readfirstlane(nocc) >= limit) {  // overfull: counted again with a bit more
-                    if (lane == 0) atomicOr(&flags[0], 1u);
-                    continue;
+                add[r] = valid ? 1u : 0u;
+                if (vb) {
+                    const int ld = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)vb) - 1);
+                    const u32 k0 = (u32)__builtin_amdgcn_readlane((int)key[r], ld);
+                    const bool same = valid && key[r] == k0;
+                    const u64 m = __ballot(same);
+                    if (same) add[r] = lane == ld ? (u32)__popcll(m) : 0u;
                 }
-                // the lanes holding the wave's first key add once (a hot pair would serialize the LDS atomics)
-                const int ld = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)vb) - 1);
-                const u32 k0 = (u32)__builtin_amdgcn_readlane((int)key[r], ld);
-                const bool same = valid && key[r] == k0;
-                const u64 m = __ballot(same);
-                bool fresh = false;
-                if (valid && (!same || lane == ld)) fresh = p32_add(tk, tc, key[r], same ? (u32)__popcll(m) : 1u);
-                const u64 fb = __ballot(fresh);
-                if (fb && lane == 0) atomicAdd(&nocc, (u32)__popcll(fb));
+            }
+            // in two halves (register pressure): every item's home bucket read before any is used; an item whose
+            // key is there adds to its count; the others are inserted one item at a time (a lane per item per wave)
+#pragma unroll
+            for (int h = 0; h < P32_ITEMS; h += P32_ITEMS / 2) {
+                uint4 q[P32_ITEMS / 2];
+                u32 bk[P32_ITEMS / 2];
+#pragma unroll
+                for (int r = 0; r < P32_ITEMS / 2; ++r) {
+                    bk[r] = add[h + r] ? p32_bucket(key[h + r]) : 0u;
+                    if (add[h + r]) q[r] = *(const uint4*)(tk + 4 * bk[r]);
+                }
+#pragma unroll
+                for (int r = 0; r < P32_ITEMS / 2; ++r) {
+                    const int s = add[h + r] ? p32_in(q[r], bk[r], key[h + r]) : -1;
+                    if (s >= 0) {
+                        atomicAdd(&tc[s], add[h + r]);
+                        add[h + r] = 0;
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < P32_ITEMS / 2; ++r) {
+                    const bool ins = add[h + r] != 0;
+                    if (!__ballot(ins)) continue;
+                    if (__builtin_amdgcn_readfirstlane(nocc) >= limit) {  // overfull: counted again with a bit more
+                        if (lane == 0) atomicOr(&flags[0], 1u);
+                        continue;
+                    }
+                    bool fresh = false;
+                    int s = -1;
+                    if (ins) {
+                        s = p32_insert(tk, key[h + r], bk[r], q[r], &fresh);
+                        atomicAdd(&tc[s], add[h + r]);
+                    }
+                    const u64 fb = __ballot(fresh);
+                    if (fb) {
+                        u32 at = 0;
+                        if (lane == 0) at = atomicAdd(&nocc, (u32)__popcll(fb));
+                        at = (u32)__shfl((int)at, 0, WAVE);
+                        if (fresh) list[at + (u32)__popcll(fb & lanemask_lt())] = (u16)s;
+                    }
+                }
             }
         }
         lds_barrier();
         if (qb > qa) {  // block-uniform
-            auto lkey = [&](u64 q) { return (u32)((q >> (64 - W)) & lmask); };
-            if (has_q) qcnt[lv] = lk == EMPTY ? 0u : p32_find(tk, tc, lkey(lk));
+            auto lkey = [&](u64 qq) { return (u32)((qq >> (64 - W)) & lmask); };
+            // an EMPTY lookup (no context, or past the lookups' count) writes nothing: qcnt starts at zero
+            if (has_q && lk != EMPTY) qcnt[lv] = p32_find(tk, tc, lkey(lk));
             for (i64 j = qa + P32_BLOCK + t; j < qb; j += P32_BLOCK) {
-                const u64 q = qk[j];
-                qcnt[qv[j]] = q == EMPTY ? 0u : p32_find(tk, tc, lkey(q));
-            }
-            lds_barrier();  // every lookup has probed before the output pass empties the slots
-        }
-        for (int j0 = 0; j0 < P32_SLOTS; j0 += P32_BLOCK) {
-            const int j = j0 + t;
-            const u32 key = tk[j];
-            const bool occ = key != EMPTY32;
-            const u64 bal = __ballot(occ);
-            if (!bal) continue;
-            u32 off = 0;
-            if (lane == 0) off = atomicAdd(&cur, (u32)__popcll(bal));
-            off = (u32)__shfl((int)off, 0, WAVE);
-            if (occ) {
-                const u64 at = (u64)out_base + off + (u64)__popcll(bal & lanemask_lt());
-                const u64 pk = unwmix(((u64)p << lbits) | key, W);
-                const u32 n = tc[j];
-                tk[j] = EMPTY32;
-                tc[j] = 0;
-                const u64 word = (pk << (48 - cb)) | ((u64)n < esc ? (u64)n : esc);
-                out_k[at] = word;
-                if ((u64)n >= esc) esc_put(esc_k, esc_c, esc_cap, pk, n, flags);
-                atomicAdd(&dh[(u32)(word >> dshift) & (u32)(nd - 1)], 1u);
+                const u64 qq = qk[j];
+                if (qq != EMPTY) qcnt[qv[j]] = p32_find(tk, tc, lkey(qq));
             }
         }
+        const u32 nl = nocc;
+        lds_barrier();  // every lookup has probed and nocc is read before the output pass empties the slots
+        for (u32 i = t; i < nl; i += P32_BLOCK) {
+            const int j = list[i];
+            const u32 key = tk[j], n = tc[j];
+            tk[j] = EMPTY32;
+            tc[j] = 0;
+            const u64 pk = unwmix(((u64)p << lbits) | key, W);
+            const u64 word = (pk << (48 - cb)) | ((u64)n < esc ? (u64)n : esc);
+            out_k[(u64)out_base + cur + i] = word;
+            if ((u64)n >= esc) esc_put(esc_k, esc_c, esc_cap, pk, n, flags);
+            atomicAdd(&dh[(u32)(word >> dshift) & (u32)(nd - 1)], 1u);
+        }
+        cur += nl;
         if (t == 0) nocc = 0;
-        lds_barrier();
+        lds_barrier();  // the slots are empty again (the output stores need not have completed)
     }
     if (t == 0) {
         seg_cnt[blockIdx.x] = cur;
@@ -489,12 +575,36 @@ extern "C" int ng_msd_pass64(void* temp, size_t* temp_bytes, const u64* keys, co
 }
 
 // The lookups of n query positions (pos[j], or j with pos NULL) for the 32-bit count: qk[j] = wmix(ctx_of[i] << 16 |
-// tgt[i], W) << (64 - W) for context ids in [lo, hi) (below 2^(W - 16)), else EMPTY; qv[j] = i.
-extern "C" int ng_part_lookups_w(const int* ctx_of, const u16* tgt, const int* pos, i64 n, i64 lo, i64 hi, int W,
-                                 u64* qk, u32* qv, void* stream) {
-    if (W < 17 || W > 63 || lo < 0 || hi > (1ll << (W - 16))) return -1;
+// tgt[i], W) << (64 - W) for context ids in [lo, hi) (below 2^(W - 16)), else EMPTY; qv[j] = i. n_dev (may be NULL):
+// a device-side count of pos's entries; lookups j >= *n_dev are EMPTY.
+extern "C" int ng_part_lookups_w(const int* ctx_of, const u16* tgt, const int* pos, i64 n, const u64* n_dev, i64 lo,
+                                 i64 hi, int W, u64* qk, u32* qv, void* stream) {
+    if (W < 17 || W > 63 || lo < 0 || hi > (1ll << (W - 16)) || (n_dev && !pos)) return -1;
     if (n <= 0) return 0;
-    lookups_w_k<<<grid_for(n, 256), 256, 0, (hipStream_t)stream>>>(ctx_of, tgt, pos, n, lo, hi, W, qk, qv);
+    lookups_w_k<<<grid_for(n, 256), 256, 0, (hipStream_t)stream>>>(ctx_of, tgt, pos, n, n_dev, lo, hi, W, qk, qv);
+    return (int)hipGetLastError();
+}
+
+// The positions i < n with v[i] > 0 in order into out (at most cap of them), *n_dev = how many there are (which may
+// exceed cap: the caller checks); CUB-style two-phase temp storage. No host read.
+extern "C" int ng_select_positive(void* temp, size_t* temp_bytes, const int* v, i64 n, int* out, i64 cap, u64* n_dev,
+                                  void* stream) {
+    if (temp_bytes == nullptr || n < 0 || cap < 0 || n_dev == nullptr) return -1;
+    const i64 nb = (n + 256 * SEL_ITEMS - 1) / (256 * SEL_ITEMS);
+    const size_t b0 = al256((size_t)(nb > 0 ? nb : 1) * 4);
+    const size_t need = b0 + prim::scan_u32_temp_bytes(nb);
+    if (temp == nullptr) {
+        *temp_bytes = need;
+        return 0;
+    }
+    if (*temp_bytes < need) return -1;
+    hipStream_t st = (hipStream_t)stream;
+    u32* cnt = (u32*)temp;
+    if (nb == 0) return prim::fill_u64(n_dev, 0ull, 1, st);
+    sel_count_k<<<(unsigned)nb, 256, 0, st>>>(v, n, cnt);
+    int e = prim::exclusive_scan_u32(cnt, cnt, nb, n_dev, (char*)temp + b0, st);
+    if (e) return e;
+    sel_write_k<<<(unsigned)nb, 256, 0, st>>>(v, n, cnt, out, cap);
     return (int)hipGetLastError();
 }
 
@@ -505,7 +615,7 @@ extern "C" int ng_part_lookups_w(const int* ctx_of, const u16* tgt, const int* p
 // them (out_k holds as many words as there are events); dhist[d * grid + b] block b's words per dbits-bit digit
 // (word >> dshift) & (2^dbits - 1) (1 <= dbits <= 11), for ng_seg_scatter. Lookups (ng_part_lookups_w's, sorted by
 // their top pbits; qstart their partitions' bounds; qk and qv may be NULL with qstart all zeros: none) get qcnt[qv[j]]
-// = the pair's count or 0. flags[0] bit 0: a partition reached min(limit, 14000) distinct pairs (its count is
+// = the pair's count or 0. flags[0] bit 0: a partition reached min(limit, 13000) distinct pairs (its count is
 // incomplete: count again with a bit more); bit 1: the escape table is full.
 extern "C" int ng_part_count32(const u32* ev, const i64* start, int pbits, int W, const u64* qk, const u32* qv,
                                const i64* qstart, u64* out_k, int cb, u64* esc_k, u32* esc_c, u64 esc_cap,

@@ -38,6 +38,8 @@ from .qindex import QueryIndex
 
 SCAN_BLOCKS_PER_CU = 8  # level-scan blocks (grid-stride) per compute unit (c3 sweep: 8 fastest of 4-32)
 LIST_DENSITY = 0.05  # a level behind a sparser one probes the previous hits as a position list (c3 sweep)
+SEEN_MARGIN = 1.05  # room for a level's query positions listed on the device: this times the last build's count
+# (at least 1: a list that overflowed is listed again in room for the count it found)
 TOPS = (1, 2, 4, 8)  # the record widths ng_ctx_summary writes
 
 
@@ -85,6 +87,7 @@ class LevelBuild:
         self._plist = None
         self.wide: set = set()  # levels counted by the 64-bit path (count_events): their 32-bit count overflowed
         self.min_pbits: dict[int, int] = {}  # per level, partition bits the 32-bit count found too few, plus one
+        self.seen_of: dict[int, int] = {}  # per level, the query positions whose previous level's context occurred
 
     def _event(self, name: str, k: int, n: int, mode: int = -1):
         """A pair of timing events around a launch on the current stream, kept in kernel_events as (name, k, n, e0,
@@ -129,10 +132,20 @@ class LevelBuild:
         for li, k in enumerate(self.levels):
             t0 = time.perf_counter()
             prev = self.levels[li - 1] if li else None
-            seen = None
+            seen = seen_n = None
+            seen_cap = 0
             if prev is not None and self.level_shards[k] <= self.level_shards[prev]:
-                seen = torch.nonzero(out[1, li - 1] > 0).squeeze(1).to(torch.int32)
-            vi = QueryIndex(elib, x, avail, k, seen, expect=self.contexts_of.get(k), defer=_defer)
+                if cnt_top is None and k not in self.wide and k in self.seen_of and _defer:
+                    # listed on the device, sized from the last build's count: no host wait (checked after the last
+                    # level; a list that came out longer than its room makes the build run again)
+                    seen_cap = min(N, int(self.seen_of[k] * max(SEEN_MARGIN, 1.0)) + 4096)
+                    seen = torch.empty(max(seen_cap, 1), dtype=torch.int32, device=dev)
+                    seen_n = torch.empty(1, dtype=torch.int64, device=dev)
+                    elib.cub("ng_select_positive", out[1, li - 1], N, seen, seen_cap, seen_n)
+                else:
+                    seen = torch.nonzero(out[1, li - 1] > 0).squeeze(1).to(torch.int32)
+                    self.seen_of[k] = int(seen.numel())
+            vi = QueryIndex(elib, x, avail, k, seen, expect=self.contexts_of.get(k), defer=_defer, n_dev=seen_n)
             if vi.n is None:
                 pending.append((k, vi.pending))
             else:
@@ -143,14 +156,19 @@ class LevelBuild:
             ev_fn = lambda name, n, k=k: self._event(name, k, n)  # noqa: E731
             _, W = w_bits(vi.ids)
             use32 = cnt_top is None and W <= W_MAX and k not in self.wide
+            if not use32 and seen_n is not None:  # the 64-bit count takes an exact list: read its length
+                seen = seen[: int(seen_n.item())]
+                seen_n = None
             seg = self._emit(k, vi, x, bms, regions, R, W if use32 else 0)
             t2 = time.perf_counter()
             if use32:
                 # the 32-bit count: records made without sorting the pairs, every size read once after the last level
-                c = count32(elib, seg, vi.ids, ktop, (vi.ctx_of, tgt, seen), self.events_of.get(k),
+                c = count32(elib, seg, vi.ids, ktop, (vi.ctx_of, tgt, seen, seen_n), self.events_of.get(k),
                             self.dratio.get(k, 1.0), ev_fn, self.min_pbits.get(k, 0))
                 del seg
-                checks32.append((k, c.stat, c.pbits, vi.ids))
+                if seen_n is not None:
+                    c.stat[4:5].copy_(seen_n)
+                checks32.append((k, c.stat, c.pbits, vi.ids, seen_cap if seen_n is not None else -1))
                 sm = c
                 res.info[k] = dict(contexts=vi.n, ids=vi.ids, pairs=None, events=None, pbits=c.pbits, hits=None)
             else:
@@ -228,11 +246,16 @@ class LevelBuild:
     def _check32(self, checks: list, res: LevelOutputs) -> bool:
         """The 32-bit counts' device results, read in one copy: each level's events and distinct pairs (kept to size
         the next build), raising on an overflowed emit region, 2^32 or more events, or a total past uint32. Returns
-        whether the build must be redone: a partition overfull (counted again with more partitions) or the escape
-        table full (the level goes to the 64-bit count)."""
+        whether the build must be redone: a level's query positions listed on the device outran their room (the
+        levels after it counted from a cut list, so their results are not kept), a partition overfull (counted
+        again with one more partition bit) or the escape table full (the level goes to the 64-bit count)."""
         vals = torch.stack([c[1] for c in checks]).cpu().tolist()
         redo = False
-        for (k, _, pbits, ids), (n_ev, n_u, fl, sfl) in zip(checks, vals):
+        for (k, _, pbits, ids, seen_cap), (n_ev, n_u, fl, sfl, n_seen) in zip(checks, vals):
+            if seen_cap >= 0:  # the level's query positions were listed on the device
+                self.seen_of[k] = max(n_seen, 1)
+                if n_seen > seen_cap:  # more than their room: the build runs again with room for them
+                    return True
             fl &= 0xFFFFFFFF
             if sfl & 4:
                 raise RuntimeError(f"k={k}: an emit region overflowed")

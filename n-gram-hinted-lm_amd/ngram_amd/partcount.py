@@ -262,8 +262,8 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids:
 
 RECORD_WORDS = {1: 4, 2: 8, 4: 8, 8: 16}  # u32 words of a context record for top 1, 2, 4, 8
 
-P32_TARGET = 8192  # distinct pairs per partition aimed at by the 32-bit count (its LDS table takes up to 14000)
-P32_LIMIT = 14000  # distinct pairs at which the 32-bit count declares a partition overfull (at most 14000)
+P32_TARGET = 7168  # distinct pairs per partition aimed at by the 32-bit count (its LDS table takes up to 13000)
+P32_LIMIT = 13000  # distinct pairs at which the 32-bit count declares a partition overfull (at most 13000)
 PACK32_MIN_BITS = 0  # context bits of the 32-bit count's packed words at least this (a narrower count field)
 AGG_ID_BITS = 11  # context ids per group of words whose records ng_ctx_agg makes in one block: at most 2^11
 W_MAX = 42  # the widest pair key (context-id bits + 16) the 32-bit count takes: its first pass's digit is at most 10
@@ -285,9 +285,9 @@ def first_digit(W: int) -> int:
 class Counted32:
     """A level counted by count32: per context id its record (int32 [n_ids, RECORD_WORDS[ktop]]) and pair count
     dist (int32 [n_ids], 0 for absent contexts), per query position the target's count qcnt (int32 [N]), and the
-    device-side results the host checks once per build (`stat`: int64 [4] = events, distinct pairs, the count's flags,
-    the scan's flags; bit 0 of the count's flags: a partition overfull, bit 1: the escape table full, bit 2: a total
-    reached 2^32; bit 2 of the scan's: a region overflowed)."""
+    device-side results the host checks once per build (`stat`: int64 [5] = events, distinct pairs, the count's flags,
+    the scan's flags, a count the caller keeps there; bit 0 of the count's flags: a partition overfull, bit 1: the
+    escape table full, bit 2: a total reached 2^32; bit 2 of the scan's: a region overflowed)."""
 
     rec: torch.Tensor
     dist: torch.Tensor
@@ -310,7 +310,8 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
     first_digit(W); seg = (regions, R, ev_count, dhist, nseg, scan flags)) and make every present context's record
     (top ktop) without a host read: the passes and the count of pairs32.hip. `n_events`: the level's events (the last
     build's; None: read from the device here, one host sync), which with `ratio` (distinct pairs per event) sizes the
-    partitions, with at least min_pbits partition bits (and at most pbits32_max(n_ids)); `lookups` as count_events'."""
+    partitions, with at least min_pbits partition bits (and at most pbits32_max(n_ids)); `lookups` as count_events',
+    and optionally a fourth entry: a device-side count (int64 [1]) of the listed positions, at most their number."""
     regions, R, ev_count, dhist, nseg, scan_flags = seg
     dev = regions.device
     idb, W = w_bits(n_ids)
@@ -319,7 +320,8 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
         raise ValueError(f"{n_ids} context ids: wider than the 32-bit count takes")
     d1 = first_digit(W)
     cap = nseg * R
-    stat = torch.zeros(4, dtype=torch.int64, device=dev)  # events, distinct pairs, count flags, scan flags
+    stat = torch.zeros(5, dtype=torch.int64, device=dev)  # events, distinct pairs, count flags, scan flags, the
+    # caller's fifth (the level's listed query positions)
     ev_tot, u_tot = stat[0:1], stat[1:2]
     flags = stat[2:3].view(torch.int32)[:1]
     dpre = torch.empty((1 << d1) * nseg, dtype=torch.int32, device=dev)
@@ -344,13 +346,14 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
     sqk = sqv = None
     qstart = torch.zeros(P + 1, dtype=torch.int64, device=dev)
     if lookups is not None:
-        ctx_of, tgt, qpos = lookups
+        ctx_of, tgt, qpos = lookups[:3]
+        qn = lookups[3] if len(lookups) > 3 else None  # a device-side count of qpos's entries
         N = ctx_of.numel()
         nq = N if qpos is None else qpos.numel()
     if nq:
         qk = torch.empty(nq, dtype=torch.int64, device=dev)
         qv = torch.empty(nq, dtype=torch.int32, device=dev)
-        elib("ng_part_lookups_w", ctx_of, tgt, qpos, nq, 0, n_ids, i32(W), qk, qv)
+        elib("ng_part_lookups_w", ctx_of, tgt, qpos, nq, qn, 0, n_ids, i32(W), qk, qv)
         sqk = torch.empty(nq, dtype=torch.int64, device=dev)
         sqv = torch.empty(nq, dtype=torch.int32, device=dev)
         elib.cub("sort_pairs", qk, sqk, qv, sqv, nq, i32(64 - pbits), i32(64))

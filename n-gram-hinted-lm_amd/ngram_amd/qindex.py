@@ -21,7 +21,8 @@ EXPECT_MARGIN = 1.2  # a table sized from an expected context count holds this m
 
 class QueryIndex:
     def __init__(self, lib: Lib, x: torch.Tensor, avail: torch.Tensor, k: int, positions: torch.Tensor | None = None,
-                 compact: bool = False, expect: int | None = None, _resized: bool = False, defer: bool = False):
+                 compact: bool = False, expect: int | None = None, _resized: bool = False, defer: bool = False,
+                 n_dev: torch.Tensor | None = None):
         """Index the valid k-contexts of the query positions (all of x, or the int32 `positions`). `compact`: ctx_of
         holds one entry per listed position (in their order) instead of one per position of x. `expect`: about how
         many contexts there are (e.g. the last build's count): the table is sized for them at once instead of for
@@ -29,7 +30,9 @@ class QueryIndex:
         sized for the count found (`_resized` marks that second build, which keeps its table whatever its load).
         `defer` (with `expect`): the build's counters are not read here, so the host does not wait for the GPU; the
         table sized from `expect` stands, `n` is None, and the caller must pass `pending` to `check()` and redo its
-        work if an insert found no slot (its context is then missing from the table)."""
+        work if an insert found no slot (its context is then missing from the table). `n_dev` (int64 [1] on the
+        device, with `positions`): only the first n_dev of the listed positions are indexed (a count the host has not
+        read; `positions` holds at least that many, or the caller checks)."""
         dev = x.device
         N = x.numel()
         m = N if positions is None else int(positions.numel())
@@ -48,8 +51,8 @@ class QueryIndex:
                     torch.empty(N, dtype=torch.int32, device=dev)
             counters = torch.zeros(3, dtype=torch.int64, device=dev)
             if m:
-                lib("ng_query_index", x, avail, positions, m, i32(k), table, u64(cap), u64(slots), rep, ctx_of,
-                    i32(int(compact and positions is not None)), counters)
+                lib("ng_query_index", x, avail, positions, m, n_dev, i32(k), table, u64(cap), u64(slots), rep,
+                    ctx_of, i32(int(compact and positions is not None)), counters)
             if defer and expect is not None and not _resized:
                 self.pending = counters
                 self.n, self.cap, self.ids, self.table, self.rep, self.ctx_of = None, cap, slots, table, rep, ctx_of
@@ -65,7 +68,7 @@ class QueryIndex:
             raise RuntimeError(f"k={k}: {c[2]} query positions collide with another context's key")
         n_ctx = int(c[0])
         if expect is not None and not _resized and n_ctx > LOAD * cap:  # fuller than LOAD: once more, at their size
-            self.__init__(lib, x, avail, k, positions, compact, n_ctx, _resized=True)
+            self.__init__(lib, x, avail, k, positions, compact, n_ctx, _resized=True, n_dev=n_dev)
             return
         if m and cap > SHRINK * (n_ctx / LOAD) + 4096:
             # sized for every position, used by far fewer contexts: move them to a table sized for them (fewer bits

@@ -110,6 +110,45 @@ def test_counts_match_oracle(corpus, level_shards, mode, monkeypatch):
         cb.batch_rows(1000, n, cap - 8)
 
 
+def test_warm_build_lists_query_positions_on_the_device(corpus, monkeypatch):
+    """A build after the first lists each level's query positions on the device (no host read), in room sized from
+    the last build's counts: after a build over a short query stream, the full stream's lists outrun that room, so
+    the build runs once more with room for what it found; both builds match the oracle (the levels after an
+    overflowed list, counted from a cut list, are not taken)."""
+    cb = C.CountBuild(corpus.shards(), levels=LEVELS, level_shards={}, topk=4)
+    cb.start_load(1)
+    short = corpus.query[:20_001]
+    xs, ts, avs = C.queries(short, [], "cuda")
+    first = cb.counts(xs, ts, avs).cpu().numpy()
+    seen_short = dict(cb.engine.seen_of)
+    runs = []
+    build = levels_mod.LevelBuild.build
+
+    def counted(self, *a, **kw):
+        runs.append(1)
+        return build(self, *a, **kw)
+
+    monkeypatch.setattr(levels_mod.LevelBuild, "build", counted)
+    x, tgt, avail = C.queries(corpus.query, [], "cuda")
+    out = cb.counts(x, tgt, avail).cpu().numpy()
+    assert len(runs) >= 2, runs  # the device lists outran their room at least once
+    assert all(cb.engine.seen_of[k] > seen_short[k] for k in seen_short)
+    ref_short = _reference_for(short, corpus, LEVELS)
+    ref = _reference(corpus, LEVELS, {})
+    for li, k in enumerate(LEVELS):
+        assert np.array_equal(first[0, li].view(np.uint32), ref_short[k]["tot"]), f"short tot k={k}"
+        assert np.array_equal(first[2, li].view(np.uint32), ref_short[k]["cnt"]), f"short cnt k={k}"
+        assert np.array_equal(out[0, li].view(np.uint32), ref[k]["tot"]), f"tot k={k}"
+        assert np.array_equal(out[1, li].astype(np.uint16), ref[k]["dist"]), f"dist k={k}"
+        assert np.array_equal(out[2, li].view(np.uint32), ref[k]["cnt"]), f"cnt k={k}"
+
+
+def _reference_for(query, corpus, levels):
+    x, tgt = query[:-1], query[1:]
+    avail = O.segments(x)
+    return {k: O.query_counts(corpus.train, corpus.bounds, x, tgt, avail, k, cnt_top=1 << 30, ntop=8) for k in levels}
+
+
 def test_device_queries_match_host_queries(corpus):
     q = torch.from_numpy(corpus.query.view(np.int16)).cuda()
     a = C.device_queries(q)

@@ -122,3 +122,19 @@ def test_msd_pass64_words_by_context(lib):
     bst = torch.empty(2049, dtype=torch.int64, device="cuda")
     lib.cub("ng_msd_pass64", None, dpre, 1, i32(11), tot, u64(n), i32(0), i32(0), None, bst)
     assert np.array_equal(bst.cpu().numpy(), starts)
+
+
+@pytest.mark.parametrize("cap_frac", [1.0, 0.5])
+def test_select_positive(lib, cap_frac):
+    """ng_select_positive: the positive entries' positions in order and their count, the count exact even when the
+    list is cut at cap."""
+    rng = np.random.default_rng(6)
+    n = 1_000_003
+    v = rng.integers(-3, 3, n).astype(np.int32)
+    want = np.nonzero(v > 0)[0]
+    cap = int(len(want) * cap_frac)
+    out = torch.full((max(cap, 1),), -7, dtype=torch.int32, device="cuda")
+    nd = torch.empty(1, dtype=torch.int64, device="cuda")
+    lib.cub("ng_select_positive", torch.from_numpy(v).cuda(), n, out, cap, nd)
+    assert int(nd.item()) == len(want)
+    assert np.array_equal(out.cpu().numpy()[:cap], want[:cap])
