@@ -51,6 +51,25 @@ def measured_fetch(k: int):
     return json.loads(TRAFFIC.read_text()).get("fetch_bytes_per_launch", {}).get(str(k))
 
 
+def roof(nbytes: float, msec: float) -> dict:
+    """Achieved GB/s of nbytes in msec milliseconds against MI355X's HBM peak."""
+    gbs = nbytes / (msec / 1e3) / 1e9 if msec > 0 else 0.0
+    return {"achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS}
+
+
+def median_runs(fn, runs: int = 3) -> dict:
+    """fn() once untimed (a warm-up: pages touched, caches filled), then `runs` timed runs: their median and range."""
+    import statistics
+
+    fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return {"median_s": statistics.median(ts), "runs_s": ts}
+
+
 def parse() -> argparse.Namespace:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -61,7 +80,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--query-tokens", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other configurations' measurements")
-    ap.add_argument("--only", default="", choices=("", "c2", "c4", "c5", "copy", "load"),
+    ap.add_argument("--only", default="", choices=("", "c1", "c2", "c4", "c5", "copy", "load"),
                     help="measure only this secondary configuration and print its JSON (for profiling); copy: three "
                          "plain 1 GiB device copies, the calibration of rocprofv3's FETCH_SIZE / WRITE_SIZE; load: "
                          "c3 from shard files (the threaded loader, and the build overlapped with the copies)")
@@ -126,25 +145,100 @@ def bench_c2(steps: int, warmup: int, with_cpu: bool) -> dict:
            "workload": f"c2: CountTable of {T} corpus tokens for n={levels} + top-{cfg.topk}/tot/dist/cnt queries at "
                        f"{x.numel()} positions", "kernel_ms_per_step": ev,
            "sizes": [list(v) for v in sizes_out]}
-    build_bytes = 2.0 * T * len(levels) + 16.0 * T * len(levels)  # every position at every level is an event
+    # B_build = 2 T + 16 E with E = T x L (every corpus position is an event at every level, within shard edges)
+    E = T * len(levels)
+    build_bytes = 2.0 * T + 16.0 * E
     res["build_bytes"] = build_bytes
-    res["build_GBps_over_step"] = build_bytes / dt / 1e9
+    res["roofline"] = {"bound": "hbm", "kernel": "whole step (CountTable.build + query_device)",
+                       "algorithmic_bytes_per_step": build_bytes, "events_per_step": E, **roof(build_bytes, dt * 1e3),
+                       "dominant_class": max(ev, key=ev.get), "dominant_ms_per_step": max(ev.values())}
     if with_cpu:
         sys.path.insert(0, str(ROOT / "oracle"))
         import oracle as O
 
-        n_t = 10_000_000
-        train = flat[:n_t].cpu().numpy().view(np.uint16)
-        qq = q[: 1_000_001].cpu().numpy().view(np.uint16)
+        # the whole configuration (100M tokens x 8M queries, every level), median of three after a warm-up run
+        train = flat.cpu().numpy().view(np.uint16)
+        qq = q.cpu().numpy().view(np.uint16)
         xs, ts = qq[:-1], qq[1:]
         av = O.segments(xs)
+        b = np.array([0, len(train)], np.int64)
+        cdt = median_runs(lambda: [O.table_counts(train, b, xs, ts, av, k, ntop=4, nthreads=O.threads())
+                                   for k in levels])
+        res["cpu_baseline"] = {"value": T / cdt["median_s"], "unit": "corpus tokens/s", "cores": O.threads(),
+                               "kind": "port", "query_positions_per_s": len(xs) / cdt["median_s"],
+                               "sample": f"the whole configuration: count_table.rs restatement over {T} tokens x "
+                                         f"{len(xs)} queries, levels {levels}; median of 3 after a warm-up",
+                               **cdt}
+    return res
+
+
+def bench_c1(steps: int, warmup: int, with_cpu: bool) -> dict:
+    """Configuration c1, whole: a 4M-token corpus (four shards of 2^20) and 256K query positions; per position and
+    level k = 2, 3 its tot / dist / cnt and top-1 next token with its count (CountBuild), and its longest exact
+    suffix match up to 32 with the next token and count there (longest_match). One step = both over the resident
+    corpus. With with_cpu: the oracle on the same whole configuration (median of 3 after a warm-up), and every output
+    compared with it."""
+    import numpy as np
+    import torch
+
+    from ngram_amd import data
+    from ngram_amd.counts import CountBuild, device_queries
+    from ngram_amd.lib import Lib
+    from ngram_amd.longest import _segments, longest_match
+
+    dc = data.device_corpus("c1")
+    levels = (2, 3)
+    cb = CountBuild.from_device(dc.tok, dc.sizes, dc.starts, levels=levels, level_shards={}, topk=1)
+    x, tgt, avail = device_queries(dc.query)
+    lib = Lib()
+    seg = _segments(x, lib)
+    times = []
+    for step in range(warmup + steps):
+        torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for k in levels:
-            O.table_counts(train, np.array([0, n_t], np.int64), xs, ts, av, k, ntop=4, nthreads=O.threads())
-        cdt = time.perf_counter() - t0
-        res["cpu_baseline"] = {"value": n_t / cdt, "unit": "corpus tokens/s", "cores": O.threads(), "kind": "port",
-                               "sample": f"count_table.rs restatement over the first {n_t} tokens x 1M queries, "
-                                         f"levels {levels}; {cdt:.1f} s"}
+        out = cb.counts(x, tgt, avail)
+        length, nxt, cnt, _ = longest_match(dc.tok, x, seg, 32, elib=lib, lib=lib)
+        torch.cuda.synchronize()
+        if step >= warmup:
+            times.append(time.perf_counter() - t0)
+    dt = sorted(times)[len(times) // 2]
+    T, N = sum(dc.sizes), x.numel()
+    res = {"value": T / dt, "unit": "corpus tokens/s", "query_positions_per_s": N / dt, "ms_per_step": dt * 1e3,
+           "workload": f"c1: counts (n={list(levels)}, top-1) and the longest suffix match (cap 32) of {N} query "
+                       f"positions against {T} corpus tokens", "steps": steps, "statistic": "median step"}
+    if with_cpu:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as O
+
+        train = dc.flat.cpu().numpy().view(np.uint16)
+        q = dc.query.cpu().numpy().view(np.uint16)
+        xs, ts = q[:-1], q[1:]
+        av = O.segments(xs)
+        b = np.asarray(dc.bounds, np.int64)
+        got = {}
+
+        def cpu():
+            for k in levels:
+                got[k] = O.query_counts(train, b, xs, ts, av, k, cnt_top=1 << 30, ntop=1, nthreads=O.threads())
+            got["long"] = O.longest_match(train, b, xs, av, 32, nthreads=O.threads())
+
+        cdt = median_runs(cpu)
+        res["cpu_baseline"] = {"value": T / cdt["median_s"], "unit": "corpus tokens/s",
+                               "query_positions_per_s": N / cdt["median_s"], "cores": O.threads(), "kind": "port",
+                               "sample": "the whole configuration (kgram.rs counts for n = 2, 3 and the longest-match "
+                                         "ladder, cap 32); median of 3 after a warm-up", **cdt}
+        o = out.cpu().numpy()
+        bad = 0
+        for li, k in enumerate(levels):
+            w = got[k]
+            bad += int(((o[0, li].view(np.uint32) != w["tot"]) | (o[1, li].astype(np.uint16) != w["dist"])
+                        | (o[2, li].view(np.uint32) != w["cnt"])
+                        | (cb.top_tok[li, :, 0].cpu().numpy().view(np.uint16) != w["top_tok"][:, 0])
+                        | (cb.top_cnt[li, :, 0].cpu().numpy().view(np.uint32) != w["top_cnt"][:, 0])).sum())
+        ln, nx, cn = got["long"][:3]
+        bad += int(((length.cpu().numpy().view(np.uint32) != ln) | (nxt.cpu().numpy().view(np.uint16) != nx)
+                    | (cnt.cpu().numpy().view(np.uint32) != cn)).sum())
+        res["parity"] = {"positions": N, "mismatching_positions": bad}
     return res
 
 
@@ -182,10 +276,18 @@ def bench_c5(tok, flat, steps: int, warmup: int, with_cpu: bool) -> dict:
     dt = sum(times) / len(times)
     T = int(flat.numel())
     hist = torch.bincount(length[query].long(), minlength=65).cpu().tolist()
+    E = int(timing.get("events", 0))
+    build_bytes = 2.0 * T + 16.0 * E
     res = {"value": T / dt, "unit": "corpus tokens/s", "query_positions_per_s": nq / dt, "ms_per_step": dt * 1e3,
            "workload": f"c5: longest exact suffix match (cap 64) + top next token and count of {nq} positions of a "
                        f"64M-token held-out stream against {T} corpus tokens", "phases_s": dict(timing),
-           "levels": len(ladder), "length_histogram": hist}
+           "levels": len(ladder), "length_histogram": hist,
+           # B_build = 2 T + 16 E, E the (context, next) events the counting phase counts (the final contexts' hits)
+           "roofline": {"bound": "hbm", "kernel": "whole step (existence + counting phases)",
+                        "algorithmic_bytes_per_step": build_bytes, "events_per_step": E,
+                        **roof(build_bytes, dt * 1e3),
+                        "counting_phase": {"algorithmic_bytes": 16.0 * E,
+                                           **roof(16.0 * E, 1e3 * timing.get("count", 0.0))}}}
     if with_cpu:
         sys.path.insert(0, str(ROOT / "oracle"))
         import oracle as O
@@ -193,12 +295,14 @@ def bench_c5(tok, flat, steps: int, warmup: int, with_cpu: bool) -> dict:
         n_t, n_q = 100_000_000, 200_000
         train = flat[:n_t].cpu().numpy().view(np.uint16)
         xs = x[: 4 * n_q].cpu().numpy().view(np.uint16)
-        t0 = time.perf_counter()
-        O.longest_match(train, np.array([0, n_t], np.int64), xs, O.segments(xs), 64, nthreads=O.threads())
-        cdt = time.perf_counter() - t0
-        res["cpu_baseline"] = {"value": n_t / cdt, "unit": "corpus tokens/s", "cores": O.threads(), "kind": "port",
+        av = O.segments(xs)
+        cdt = median_runs(lambda: O.longest_match(train, np.array([0, n_t], np.int64), xs, av, 64,
+                                                  nthreads=O.threads()))
+        res["cpu_baseline"] = {"value": n_t / cdt["median_s"], "unit": "corpus tokens/s", "cores": O.threads(),
+                               "kind": "port", **cdt,
                                "sample": f"kgram.rs-style ladder over the first {n_t} corpus tokens x {4 * n_q} "
-                                         f"contiguous query positions, cap 64; {cdt:.1f} s"}
+                                         f"contiguous query positions, cap 64 (a tenth of the corpus); median of 3 "
+                                         f"after a warm-up"}
     return res
 
 
@@ -237,7 +341,13 @@ def bench_c4(with_cpu: bool) -> dict:
     rows._check_flags(rows.state)
     lat_ms = np.array(lat) * 1e3
     step_tokens = int(spans[0, 1] - spans[0, 0])
+    # per step: E = step_tokens x levels insert events (2 T + 16 E) and its queries (N (2 + 8 L) + N L 29)
+    E = step_tokens * len(levels)
+    step_bytes = 2.0 * step_tokens + 16.0 * E + step_tokens * (2 + 8 * len(levels)) + step_tokens * len(levels) * 29
     res = {"value": n / sum(lat), "unit": "stream tokens/s (insert + query)", "steps": len(spans),
+           "roofline": {"bound": "hbm", "kernel": "whole step (insert, merge, query, hint rows)",
+                        "algorithmic_bytes_per_step": step_bytes, **roof(step_bytes, float(lat_ms.mean())),
+                        "note": "latency-bound: 2^19 tokens a step leave the chip mostly idle"},
            "step_tokens": step_tokens, "ms_per_step_mean": float(lat_ms.mean()),
            "ms_per_step_median": float(np.median(lat_ms)), "ms_per_step_p99": float(np.percentile(lat_ms, 99)),
            "ms_per_step_max": float(lat_ms.max()),
@@ -343,15 +453,19 @@ def cpu_baseline(flat_host, bounds, q_host, levels, n_tokens: int, n_queries: in
     avail = O.segments(x)
     cores = O.threads()
     outs = {}
-    t0 = time.perf_counter()
-    for k in levels:
-        outs[k] = O.query_counts(train, np.array(b, np.int64), x, tgt, avail, k, cnt_top=1 << 30, ntop=4,
-                                 nthreads=cores)
-    dt = time.perf_counter() - t0
+
+    def run():
+        for k in levels:
+            outs[k] = O.query_counts(train, np.array(b, np.int64), x, tgt, avail, k, cnt_top=1 << 30, ntop=4,
+                                     nthreads=cores)
+
+    cdt = median_runs(run)
+    dt = cdt["median_s"]
     return {"value": n_tokens / dt, "unit": "corpus tokens/s", "query_positions_per_s": n_queries / dt,
-            "cores": cores, "kind": "port",
-            "sample": f"first {n_tokens} corpus tokens x first {n_queries} query positions (a tenth of each), levels "
-                      f"{list(levels)}, tot/dist/cnt + top-4; {dt:.1f} s", "seconds": dt}, outs
+            "cores": cores, "kind": "port", **cdt,
+            "sample": f"first {n_tokens} corpus tokens x first {n_queries} query positions (a tenth of each: the "
+                      f"whole 1B x 16M would take minutes of host time per run), levels {list(levels)}, tot/dist/cnt "
+                      f"+ top-4; median of 3 after a warm-up", "seconds": dt}, outs
 
 
 def _mismatches(gpu: dict, want, sel=None) -> int:
@@ -486,8 +600,9 @@ def main() -> None:
         torch.cuda.synchronize()
         print(json.dumps({"config": "copy", "bytes_read": a.numel() * 8, "bytes_written": b.numel() * 8, "copies": 3}))
         return
-    if args.only in ("c2", "c4"):
-        r = bench_c2(args.steps, args.warmup, not args.no_cpu) if args.only == "c2" else bench_c4(not args.no_cpu)
+    if args.only in ("c1", "c2", "c4"):
+        r = bench_c2(args.steps, args.warmup, not args.no_cpu) if args.only == "c2" else \
+            bench_c1(args.steps, args.warmup, not args.no_cpu) if args.only == "c1" else bench_c4(not args.no_cpu)
         r.pop("sizes", None)
         print(json.dumps({"config": args.only, **r}))
         return
@@ -500,9 +615,20 @@ def main() -> None:
         print(json.dumps({"config": "c3 load", **bench_load(cfg, tok, sizes, starts, q, args.steps)}))
         return
     T = sum(sizes)
-    cb = CountBuild.from_device(tok, sizes, starts, levels=cfg.levels, level_shards={}, topk=cfg.topk)
     x, tgt, avail = device_queries(q)
     N = x.numel()
+    # cold builds: the process's first (module loads and the allocator's growth included), then a fresh engine that
+    # has learnt nothing (its query tables, partitions and lists sized from their own first reads)
+    cold = {}
+    for label in ("first_in_process_ms", "cold_ms"):
+        cb = CountBuild.from_device(tok, sizes, starts, levels=cfg.levels, level_shards={}, topk=cfg.topk)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        cb.counts(x, tgt, avail)
+        torch.cuda.synchronize()
+        cold[label] = 1e3 * (time.perf_counter() - t0)
+    cold["reruns"] = cb.engine.reruns
+    log("cold:", json.dumps(cold))
     # one untimed build with hit counts: the hits E of the roofline (deterministic, the same every step)
     cb.counts(x, tgt, avail, stats=True)
     info = {k: dict(v) for k, v in cb.info.items()}
@@ -510,6 +636,8 @@ def main() -> None:
     for _ in range(max(0, args.warmup - 1)):
         cb.counts(x, tgt, avail)
     torch.cuda.synchronize()
+    reruns0 = cb.engine.reruns
+    torch.cuda.reset_peak_memory_stats()
     per_kernel: dict[tuple, float] = {}  # (name, level) -> ms over the timed steps
     modes: dict[int, int] = {}
     t0 = time.perf_counter()
@@ -524,6 +652,9 @@ def main() -> None:
         step_events.append(cb.kernel_events)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    peak_alloc, peak_reserved = torch.cuda.max_memory_allocated(), torch.cuda.max_memory_reserved()
+    # query-side hits H: (position, level) pairs whose context occurred (dist > 0)
+    H = int((out[1] > 0).sum().item())
     for events in step_events:
         for name, k, n, e0, e1, mode in events:
             per_kernel[(name, k)] = per_kernel.get((name, k), 0.0) + e0.elapsed_time(e1)
@@ -540,10 +671,6 @@ def main() -> None:
     dom = max(cfg.levels, key=lambda k: scan_ms[k])
     top_class = max(per_kernel, key=per_kernel.get)
 
-    def roof(nbytes: float, msec: float) -> dict:
-        gbs = nbytes / (msec / 1e3) / 1e9 if msec > 0 else 0.0
-        return {"achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS}
-
     # the committed counters describe the default workload (c3 at its stated size) only
     profiled = not args.train_tokens and not args.query_tokens
     traffic, traffic_commit = measured_traffic(dom) if profiled else (None, None)
@@ -552,6 +679,9 @@ def main() -> None:
     path_bytes = sum(2.0 * read[k] + 16.0 * hits[k] for k in cfg.levels)
     E = sum(hits.values())
     build_bytes = 2.0 * T + 16.0 * E  # the count build's B_build = 2 T + 16 E
+    nl = len(cfg.levels)
+    q_bytes = N * (2.0 + 8.0 * nl) + H * 6.0 * cfg.topk + N * nl * 29.0
+    q_ms = sum(v for (name, _), v in per_kernel.items() if name in ("qindex", "pos_gather")) / args.steps
     classes: dict[str, float] = {}
     for (name, _), v in per_kernel.items():
         classes[name] = classes.get(name, 0.0) + v / args.steps
@@ -569,10 +699,14 @@ def main() -> None:
         "roofline": {"bound": "hbm", "kernel": f"scan_emit k={dom} (ng_scan_emit, mode {modes.get(dom, 0)})",
                      **roof(scan_bytes[dom], scan_ms[dom]), "traffic": traffic,
                      "traffic_source": None if traffic is None else f"profiles/scan_traffic_c3.json @ {traffic_commit}",
-                     # the line traffic the kernel really moves (FETCH_SIZE x 2 + WRITE_SIZE of the same launch, from
-                     # the profile) over its time here: a random 8-byte probe costs a 128-byte line beyond L2
-                     "traffic_GBps": None if traffic is None else traffic / (scan_ms[dom] / 1e3) / 1e9,
-                     "traffic_frac": None if traffic is None else traffic / (scan_ms[dom] / 1e3) / 1e9 / HBM_PEAK_GBS,
+                     # the line traffic the kernel moves beyond L2 (FETCH_SIZE x 2 + WRITE_SIZE of the same launch,
+                     # from the profile) over its time here: a random 8-byte probe costs a 128-byte line beyond L2.
+                     # FETCH_SIZE counts every request past L2, Infinity-Cache (MALL) hits included, so this is not
+                     # HBM traffic alone
+                     "traffic_is": "beyond L2 (MALL hits included)",
+                     "beyond_l2_GBps": None if traffic is None else traffic / (scan_ms[dom] / 1e3) / 1e9,
+                     "beyond_l2_frac_of_hbm_peak": None if traffic is None else
+                     traffic / (scan_ms[dom] / 1e3) / 1e9 / HBM_PEAK_GBS,
                      "algorithmic_bytes_per_launch": scan_bytes[dom], "avg_launch_ms": scan_ms[dom],
                      "positions_read": read[dom], "hits_emitted": hits[dom],
                      "bytes_per_position_read": 2, "bytes_per_hit": 8},
@@ -590,6 +724,13 @@ def main() -> None:
                                 "ms_per_step": path_ms, **roof(path_bytes, path_ms)},
         "build_roofline": {"bytes": build_bytes, **roof(build_bytes, ms), "streaming_floor_GBps": 2.0 * T / (ms / 1e3) / 1e9},
         "slowest_launch_class": {"kernel": f"{top_class[0]} k={top_class[1]}", "ms_per_step": per_kernel[top_class] / args.steps},
+        # the query side (SURVEY 8d's B_query): the query indexes (2 B per position + an 8-byte key per level) and
+        # the per-position outputs (H hits' top-k records read, 6 B per entry; 29 B written per position and level)
+        "query_roofline": {"kernels": ["qindex", "pos_gather"], "hits": H,
+                           "algorithmic_bytes_per_step": q_bytes, "ms_per_step": q_ms, **roof(q_bytes, q_ms)},
+        "cold": cold,
+        "peak_mem_gb": peak_alloc / 1e9, "peak_reserved_gb": peak_reserved / 1e9,
+        "reruns_in_timed_steps": cb.engine.reruns - reruns0,
         "kernel_ms_per_step": classes,
         "events_per_step": E,
         "host_s_per_step": {k: v / (args.steps + args.warmup) for k, v in cb.engine.host_s.items()},
@@ -627,6 +768,9 @@ def main() -> None:
         del q
         torch.cuda.empty_cache()
         res["secondary"] = {}
+        log("secondary: c1")
+        res["secondary"]["c1"] = bench_c1(5, 1, not args.no_cpu)
+        torch.cuda.empty_cache()
         log("secondary: c5")
         res["secondary"]["c5"] = bench_c5(tok, flat, 2, 1, not args.no_cpu)
         del flat, tok
@@ -637,6 +781,10 @@ def main() -> None:
         log("secondary: c4")
         res["secondary"]["c4"] = bench_c4(not args.no_cpu)
     print(json.dumps(res), flush=True)
+    c1p = res.get("secondary", {}).get("c1", {}).get("parity")
+    if c1p and c1p["mismatching_positions"]:
+        log("parity: the GPU's c1 outputs differ from the oracle's")
+        sys.exit(1)
     if res["parity"] and res["parity"]["mismatching_positions"]:
         log("parity: the GPU's outputs differ from the oracle's")
         sys.exit(1)

@@ -88,6 +88,7 @@ class LevelBuild:
         self.wide: set = set()  # levels counted by the 64-bit path (count_events): their 32-bit count overflowed
         self.min_pbits: dict[int, int] = {}  # per level, partition bits the 32-bit count found too few, plus one
         self.seen_of: dict[int, int] = {}  # per level, the query positions whose previous level's context occurred
+        self.reruns = 0  # builds run again (a size learnt from an earlier build fell short), over this engine's life
 
     def _event(self, name: str, k: int, n: int, mode: int = -1):
         """A pair of timing events around a launch on the current stream, kept in kernel_events as (name, k, n, e0,
@@ -145,7 +146,10 @@ class LevelBuild:
                 else:
                     seen = torch.nonzero(out[1, li - 1] > 0).squeeze(1).to(torch.int32)
                     self.seen_of[k] = int(seen.numel())
+            q0, q1 = self._event("qindex", k, N)
+            q0.record()
             vi = QueryIndex(elib, x, avail, k, seen, expect=self.contexts_of.get(k), defer=_defer, n_dev=seen_n)
+            q1.record()
             if vi.n is None:
                 pending.append((k, vi.pending))
             else:
@@ -210,6 +214,7 @@ class LevelBuild:
             del vi, c, sm, thr, seen
         del regions
         if checks32 and self._check32(checks32, res):
+            self.reruns += 1
             return self.build(x, tgt, avail, topk=topk, cnt_top=cnt_top, keep=keep, with_mask=with_mask,
                               stats=stats, _defer=_defer)
         if pending:
@@ -221,6 +226,7 @@ class LevelBuild:
                 redo |= not ok
             del pending, checked
             if redo:  # an insert found no slot in a table sized from the last build: once more, each level checked
+                self.reruns += 1
                 return self.build(x, tgt, avail, topk=topk, cnt_top=cnt_top, keep=keep, with_mask=with_mask,
                                   stats=stats, _defer=False)
         check_summary(deferred)
@@ -251,7 +257,7 @@ class LevelBuild:
         again with one more partition bit) or the escape table full (the level goes to the 64-bit count)."""
         vals = torch.stack([c[1] for c in checks]).cpu().tolist()
         redo = False
-        for (k, _, pbits, ids, seen_cap), (n_ev, n_u, fl, sfl, n_seen) in zip(checks, vals):
+        for (k, _, pbits, ids, seen_cap), (n_ev, n_u, fl, sfl, n_seen, n_false) in zip(checks, vals):
             if seen_cap >= 0:  # the level's query positions were listed on the device
                 self.seen_of[k] = max(n_seen, 1)
                 if n_seen > seen_cap:  # more than their room: the build runs again with room for them
@@ -274,7 +280,7 @@ class LevelBuild:
             if fl & 2:
                 self.wide.add(k)
                 redo = True
-            res.info[k].update(pairs=n_u, events=n_ev)
+            res.info[k].update(pairs=n_u, events=n_ev, false_hash_hits=n_false)
         return redo
 
     def _popcount(self, bm: torch.Tensor) -> int:

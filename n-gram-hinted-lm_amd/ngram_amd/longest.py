@@ -58,6 +58,7 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
     others get 0, 0, 0."""
     if not 1 <= cap <= 64:
         raise ValueError("cap must be in [1, 64]")
+    EVENTS[0] = 0
     elib = elib or Lib()
     lib = lib or Lib()
     dev = x.device
@@ -163,6 +164,7 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
             raise RuntimeError(f"k={k}: an emit region overflowed")
         c = count_events(elib, lib, ev, n_ev, vi.ids, _RATIO.get(k, 1.0), presort="ctx")
         n_ev = c.n_ev
+        EVENTS[0] += n_ev
         del ev
         _RATIO[k] = c.U / max(1, n_ev)
         o_tok = torch.zeros(m, dtype=torch.int16, device=dev)
@@ -186,10 +188,12 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
     if timing is not None:
         torch.cuda.synchronize()
         timing["count"] = timing.get("count", 0.0) + time.perf_counter() - t0
+        timing["events"] = float(EVENTS[0])
     return length, nxt, cnt, ladder
 
 
 SCAN_BLOCKS_PER_CU = 32  # scan blocks per compute unit
+EVENTS = [0]  # (context, next) events the last longest_match counted (its counting phase), for its timing dict
 DEVICE_LEVELS = True  # the existence phase's levels after the second list level run without host syncs
 LONG_FIRST = 8  # the device levels try level cap first when at least this many levels lie between
 BATCH_EVENTS = 1 << 28  # list levels counted together until their listed positions reach this
@@ -316,6 +320,7 @@ def _count_ids(elib: Lib, lib: Lib, tok, L: int, level: tuple, k: int, length, f
         raise RuntimeError(f"k={k}: {e}") from None
     del regions
     _RATIO[k] = c.U / max(1, c.n_ev)
+    EVENTS[0] += c.n_ev
     o_tok = torch.zeros(m, dtype=torch.int16, device=dev)
     o_cnt = torch.zeros(m, dtype=torch.int32, device=dev)
     if c.cb:
@@ -396,6 +401,7 @@ def _count_batch(elib: Lib, lib: Lib, tok, L: int, x, avail, batch: list, levels
     c = count_events(elib, lib, ev, n_ev, n_ids, _RATIO.get(key, 1.0), presort="ctx")
     del ev
     _RATIO[key] = c.U / max(1, n_ev)
+    EVENTS[0] += n_ev
     if not c.cb:
         raise RuntimeError(f"levels {batch[0][0]}..{batch[-1][0]}: more large counts than the escape table holds")
     sm = summarize(elib, lib, c, n_ids, 1)

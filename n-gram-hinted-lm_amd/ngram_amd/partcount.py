@@ -285,8 +285,9 @@ def first_digit(W: int) -> int:
 class Counted32:
     """A level counted by count32: per context id its record (int32 [n_ids, RECORD_WORDS[ktop]]) and pair count
     dist (int32 [n_ids], 0 for absent contexts), per query position the target's count qcnt (int32 [N]), and the
-    device-side results the host checks once per build (`stat`: int64 [5] = events, distinct pairs, the count's flags,
-    the scan's flags, a count the caller keeps there; bit 0 of the count's flags: a partition overfull, bit 1: the
+    device-side results the host checks once per build (`stat`: int64 [6] = events, distinct pairs, the count's flags,
+    the scan's flags, a count the caller keeps there, the scan's false hash hits (hashed keys of k > 4 found in the
+    query table whose tokens differ); bit 0 of the count's flags: a partition overfull, bit 1: the
     escape table full, bit 2: a total reached 2^32; bit 2 of the scan's: a region overflowed)."""
 
     rec: torch.Tensor
@@ -320,13 +321,14 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
         raise ValueError(f"{n_ids} context ids: wider than the 32-bit count takes")
     d1 = first_digit(W)
     cap = nseg * R
-    stat = torch.zeros(5, dtype=torch.int64, device=dev)  # events, distinct pairs, count flags, scan flags, the
-    # caller's fifth (the level's listed query positions)
+    stat = torch.zeros(6, dtype=torch.int64, device=dev)  # events, distinct pairs, count flags, scan flags, the
+    # caller's fifth (the level's listed query positions), the scan's false hash hits
     ev_tot, u_tot = stat[0:1], stat[1:2]
     flags = stat[2:3].view(torch.int32)[:1]
     dpre = torch.empty((1 << d1) * nseg, dtype=torch.int32, device=dev)
     elib.cub("ng_exclusive_scan_u32", dhist, dpre, (1 << d1) * nseg, ev_tot)
     stat[3:4].copy_(scan_flags[:1])
+    stat[5:6].copy_(scan_flags[1:2])
     if n_events is None:
         n_events = int(ev_tot.item())
     pbits = max(d1 + 1, PART_MIN_BITS if lookups is not None else 0, min_pbits,
