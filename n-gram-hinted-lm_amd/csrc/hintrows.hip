@@ -265,11 +265,12 @@ static int launch_batch_rows(const int* cells, const int* entries, i64 n, i64 ca
 
 // A batch's rows (int32 [n + 2 * capacity]): cells[0..n), then `capacity` (position, entry) pairs of the non-zero
 // entries (entries int32 [n, 8], 16-byte aligned) in position order, padded with (i % n, 0); *total = the non-zero
-// entries (those past capacity are not written: the caller raises). work: ng_batch_rows_work(n) u32.
+// entries (those past capacity are not written: the caller raises). work: ng_batch_rows_work(n) u32. The tiles'
+// offsets and the running offset are u32, so n is at most (2^32 - 1) / 8 (8 entries per position: no offset wraps).
+#define BR_MAX_N (0xFFFFFFFFll / 8)
 extern "C" int ng_batch_rows(const int* cells, const int* entries, i64 n, i64 capacity, int* out, u32* work,
                              u64* total, void* stream) {
-    if (n <= 0 || capacity < 0 || ((uintptr_t)entries & 15)) return -1;
-    if ((n + BR_TILE - 1) / BR_TILE >= (1 << 30)) return -1;
+    if (n <= 0 || n > BR_MAX_N || capacity < 0 || ((uintptr_t)entries & 15)) return -1;
     return launch_batch_rows(cells, entries, n, capacity, out, work, total, (hipStream_t)stream);
 }
 

@@ -564,8 +564,9 @@ __global__ void __launch_bounds__(OM_BLOCK) __attribute__((amdgpu_waves_per_eu(4
             lds_barrier();
             if (s_over) {  // block-uniform: split the round in two by one more hash bit
                 if (t == 0) {
-                    if (lg >= OM_MAXSPLIT) {
-                        atomicOr((u32*)desc[6], 4u);
+                    if (lg >= OM_MAXSPLIT) {  // level 0's flags word (its descriptor's field 4): the host raises
+                        static_assert(OLEVEL_FIELDS == 5, "a level descriptor's flags are its field 4");
+                        atomicOr((u32*)s_desc[4], 4u);
                     } else {
                         s_stack[sp - 1] = ((res + (1ull << lg)) << 8) | (u64)(lg + 1);
                         s_stack[sp] = (res << 8) | (u64)(lg + 1);

@@ -351,7 +351,10 @@ class OnlineRows:
 
     def _check_flags(self, st) -> None:
         for k, lv in st["levels"].items():
-            if int(lv["flags"][0].item()):
+            f = int(lv["flags"][0].item())
+            if f & 4:
+                raise RuntimeError(f"k={k}: a step's merge bucket needed more hash splits than the merge takes")
+            if f:
                 raise RuntimeError(f"k={k}: a table of the online state overflowed")
 
     @staticmethod

@@ -3,21 +3,26 @@
 A hint directory is made from this build's own outputs:
   * validation rows and counts from the validation statistics (gpu_val_stats.build_stats);
   * causal training rows in one or two slots and their counts from train_hints / train_counts (the segment rule).
-It is read back through the reader (`Hints`, HINT_NGRAM=1 for the count rows). Each batch then goes through the
-consumers' forward arithmetic, restated here from old_records/hint_runtime.py (the reference's module needs
-Python >= 3.12 and its experiment framework, so it is read, not imported):
-  * HintEmbedding.forward (:381-396): embedding_bag of the candidates with per-sample weights, the slots summed;
-  * HintEmbedding.mixed_nll's candidate probabilities (:398-418);
-  * NgramMix.gates and log_q (:289-321).
+It is read back through the reader (`Hints`, HINT_NGRAM=1 for the count rows). Each batch then goes through what the
+consumers compute from it (old_records/hint_runtime.py HintEmbedding :381-418, NgramMix :271-321 are the contract;
+the checks below are written from that contract, not from its code):
+  * a candidate mean: the embedding rows of a position's candidate tokens weighted by its row's weights, summed over
+    the slots, zero where the row has no cell;
+  * the probability of the target under a row: the weights of the candidates equal to the target;
+  * interpolated Witten-Bell (Witten & Bell 1991; the interpolated form of Chen & Goodman 1998): per matched level j,
+    lambda_j = tot_j / (tot_j + dist_j), P_j = lambda_j * cnt_j / tot_j + (1 - lambda_j) * P_{j-1}, from a unigram
+    base P_0, levels in increasing length; an unmatched level passes P_{j-1} on;
+  * a gate index from the deepest matched level: that level, the bin of its total among COUNT_EDGES, and whether it
+    has one distinct continuation.
 The test checks the invariants those consumers rely on: dtypes and shapes; cells below the table's; tokens below the
 vocabulary; each row's weights a distribution (sum 1, up to u16 rounding) where it has a cell and all 0 where not;
 cnt <= tot, dist <= tot, and dist >= 1 exactly where tot > 0, which makes every Witten-Bell level a proper
-distribution. It also checks that the losses are finite."""
+distribution (so every P_j lies in (0, 1]); the gate indices within their tables. It also checks that the losses
+are finite."""
 
 import numpy as np
 import pytest
 import torch
-import torch.nn.functional as F
 
 import oracle as O
 from ngram_amd import data
@@ -31,51 +36,55 @@ COUNT_EDGES = (2, 3, 5, 9, 17, 33, 100, 1000, 10000)  # NgramMix.COUNT_EDGES (hi
 
 
 def _embed(rows, weight):
-    """HintEmbedding.forward's candidate mean (hint_runtime.py:388-395), without the learned scales."""
-    cell, tokens, weights = rows.cell, rows.tokens, rows.weights
-    if cell.dim() == 2:
-        cell, tokens, weights = cell.flatten(), tokens.flatten(0, 1), weights.flatten(0, 1)
-    mean = F.embedding_bag(tokens, weight, per_sample_weights=weights, mode="sum")
-    hint = mean * (cell > 0)[:, None]
-    if rows.cell.dim() == 2:
-        hint = hint.view(*rows.cell.shape, -1).sum(1)
-    return hint
+    """The candidate mean: per position and slot the weighted sum of its candidates' embedding rows, masked where the
+    slot has no cell, then summed over the slots."""
+    lead = rows.cell.shape
+    tok = rows.tokens.reshape(-1, rows.tokens.shape[-1])
+    w = rows.weights.reshape(-1, rows.weights.shape[-1])
+    per = (weight[tok] * w[..., None]).sum(1) * (rows.cell.reshape(-1) > 0)[:, None].float()
+    return per.reshape(*lead, -1).sum(1) if len(lead) == 2 else per
 
 
 def _candidate_q(rows, targets):
-    """mixed_nll's per-slot probability of the target (hint_runtime.py:410-412)."""
-    cell, tokens, weights = rows.cell, rows.tokens, rows.weights
-    if cell.dim() == 1:
-        cell, tokens, weights = cell[:, None], tokens[:, None], weights[:, None]
-    return (weights * (tokens == targets[:, None, None])).sum(-1)
+    """Per position and slot, the row's probability of the target: the sum of the weights whose token is it."""
+    tokens, weights = rows.tokens, rows.weights
+    t = targets.view(-1, *([1] * (tokens.dim() - 1)))
+    return torch.where(tokens == t, weights, torch.zeros_like(weights)).sum(-1)
 
 
-def _ngram_log_q(targets, counts, unigram, levels):
-    """NgramMix.log_q with its initial parameters (gamma 0: g_j = 1; hint_runtime.py:305-320)."""
-    tot, dist, cnt = counts.float().unbind(1)
-    assert tot.shape[1] == levels
-    p = torch.log_softmax(torch.log(unigram.clamp_min(1e-12)), 0)[targets].exp()
-    for j in range(levels):
-        matched = tot[:, j] > 0
-        gd = dist[:, j]
-        den = torch.where(matched, tot[:, j] + gd, torch.ones_like(gd))
-        p = torch.where(matched, (cnt[:, j] + gd * p) / den, p)
-    return torch.log(p.clamp_min(1e-30))
+def _witten_bell_log_q(targets, counts, unigram):
+    """log P of the target under interpolated Witten-Bell over the count rows (levels in increasing length), in
+    float64: lambda = tot / (tot + dist) per matched level, P = lambda * cnt / tot + (1 - lambda) * P_lower."""
+    c = counts.double()
+    tot, dist, cnt = c[:, 0], c[:, 1], c[:, 2]
+    base = unigram.double() / unigram.double().sum()
+    p = base[targets]
+    for j in range(tot.shape[1]):
+        t, d, n = tot[:, j], dist[:, j], cnt[:, j]
+        m = t > 0
+        lam = torch.where(m, t / (t + d).clamp_min(1), torch.zeros_like(t))
+        assert torch.all((lam >= 0) & (lam < 1))
+        ml = torch.where(m, n / t.clamp_min(1), torch.zeros_like(t))
+        p = lam * ml + (1 - lam) * p
+    return torch.log(p)
 
 
-def _gates(counts, levels):
-    """NgramMix.gates (hint_runtime.py:289-303): the deepest matched level's gate and sparse index."""
-    tot, dist = counts[:, 0].float(), counts[:, 1].float()
-    matched = tot > 0
-    level = torch.arange(1, levels + 1, device=tot.device)
-    deepest = (matched.long() * level).amax(1) - 1
-    at = deepest.clamp_min(0)[:, None]
-    bins = sum((tot > e).long() for e in COUNT_EDGES)
-    dbin = torch.gather(bins, 1, at)[:, 0]
-    sparse = (torch.gather(dist, 1, at)[:, 0] == 1).long()
-    d = deepest + 1
-    hit = deepest >= 0
-    return torch.where(hit, d * (len(COUNT_EDGES) + 1) + dbin, 0), torch.where(hit, d * 2 + sparse, 0)
+def _gate_index(counts):
+    """(gate, sparse) indices of the deepest matched level (0: none matched): level d = 1..L of it, the bin of its
+    total (how many COUNT_EDGES lie below it), and whether it has exactly one distinct continuation."""
+    tot, dist = counts[:, 0].cpu().numpy(), counts[:, 1].cpu().numpy()
+    n, L = tot.shape
+    edges = np.asarray(COUNT_EDGES, np.float64)
+    gate, sparse = np.zeros(n, np.int64), np.zeros(n, np.int64)
+    for i in range(n):
+        matched = np.flatnonzero(tot[i] > 0)
+        if len(matched) == 0:
+            continue
+        j = matched[-1]
+        d = j + 1
+        gate[i] = d * (len(COUNT_EDGES) + 1) + int(np.searchsorted(edges, tot[i, j], side="left"))
+        sparse[i] = d * 2 + int(dist[i, j] == 1)
+    return gate, sparse
 
 
 def _check_rows(rows, n, slots, cells, count_levels):
@@ -143,11 +152,11 @@ def test_rows_drop_into_the_consumers(tmp_path, monkeypatch, slots):
         assert hint.shape == (m, 64) and torch.isfinite(hint).all()
         q = _candidate_q(rows, targets)
         assert torch.all((q >= 0) & (q <= 1 + 1e-6))
-        lq = _ngram_log_q(targets, rows.counts, unigram, len(count_levels))
-        assert torch.isfinite(lq).all() and torch.all(lq <= 1e-6)
-        gate, sparse = _gates(rows.counts, len(count_levels))
-        assert int(gate.max()) < (len(count_levels) + 1) * (len(COUNT_EDGES) + 1)
-        assert int(sparse.max()) < 2 * (len(count_levels) + 1)
+        lq = _witten_bell_log_q(targets, rows.counts, unigram)
+        assert torch.isfinite(lq).all() and torch.all(lq <= 1e-9)
+        gate, sparse = _gate_index(rows.counts[:2000])
+        assert gate.max() < (len(count_levels) + 1) * (len(COUNT_EDGES) + 1) and gate.min() >= 0
+        assert sparse.max() < 2 * (len(count_levels) + 1) and sparse.min() >= 0
     assert hinted > 1000
     # the causal rows at this scale against the oracle's restatement (contexts of at most 8 tokens: levels 4 and 6)
     # over the first shard, whose positions see only that shard's occurrences

@@ -54,3 +54,47 @@ def test_product_does_not_import_the_oracle():
     for f in list(pkg.rglob("*.py")) + list(pkg.rglob("*.hip")) + list(pkg.rglob("*.h")):
         text = f.read_text()
         assert "import oracle" not in text and "liboracle" not in text, f
+
+
+def test_build_digest_tracks_the_sources(tmp_path, monkeypatch):
+    """build.digest() covers every source and header under csrc/ and the flags: a changed source, a new header or
+    another flag gives another digest (stale() then tells that the libraries in place are not the tree's)."""
+    from ngram_amd import build
+
+    src = tmp_path / "csrc"
+    (src / "abi").mkdir(parents=True)
+    (src / "a.hip").write_text("int a;\n")
+    (src / "abi" / "b.h").write_text("int b;\n")
+    monkeypatch.setattr(build, "CSRC", src)
+    d0 = build.digest()
+    assert d0 == build.digest()
+    (src / "a.hip").write_text("int a2;\n")
+    d1 = build.digest()
+    (src / "abi" / "c.h").write_text("\n")
+    d2 = build.digest()
+    assert len({d0, d1, d2, build.digest(["-DX"])}) == 4
+
+
+def test_builds_take_turns_on_the_lock(tmp_path, monkeypatch):
+    """A build waits for the lock another holds: a second process's build (here one with nothing to do) returns only
+    after the lock is released."""
+    import fcntl
+    import subprocess
+    import sys
+    import time
+
+    from ngram_amd import build
+
+    if build.stale():
+        pytest.skip("the libraries in place are not the tree's: build() first")
+    build.OUT_DIR.mkdir(parents=True, exist_ok=True)
+    code = ("import sys, time; sys.path.insert(0, %r); from ngram_amd import build; t = time.time(); "
+            "build.build(force=False); print(time.time() - t)") % str(ROOT / "n-gram-hinted-lm_amd")
+    with open(build.LOCK_FILE, "a+") as lock:
+        fcntl.flock(lock, fcntl.LOCK_EX)
+        p = subprocess.Popen([sys.executable, "-c", code], stdout=subprocess.PIPE, text=True)
+        time.sleep(1.5)
+        assert p.poll() is None  # still waiting for the lock
+        fcntl.flock(lock, fcntl.LOCK_UN)
+    out, _ = p.communicate(timeout=60)
+    assert p.returncode == 0 and float(out.split()[-1]) >= 1.0

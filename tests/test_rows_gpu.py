@@ -90,6 +90,17 @@ def test_batch_rows_many_tiles(gpu):
     assert np.array_equal(out.cpu().numpy(), O.batch_rows(cells, entries, 0, n, cap))
 
 
+def test_batch_rows_refuses_positions_past_its_offsets(gpu):
+    """The tiles' offsets and the running offset are u32 (8 entries per position): n above (2^32 - 1) / 8 is refused
+    before any launch (the buffers here are far smaller than such an n: nothing may be read)."""
+    lib = Lib()
+    small = torch.zeros(16, dtype=torch.int32, device="cuda")
+    ent = torch.zeros((16, 8), dtype=torch.int32, device="cuda")
+    total = torch.zeros(1, dtype=torch.int64, device="cuda")
+    with pytest.raises(RuntimeError, match="returned -1"):
+        lib("ng_batch_rows", small, ent, (0xFFFFFFFF // 8) + 1, 0, small, small, total)
+
+
 def test_features_at_float32_edges(gpu):
     lib = Lib()
     ks = list(range(18, 26))
