@@ -261,7 +261,7 @@ int ng_select_positive(void* temp, size_t* temp_bytes, const int* v, ng_i64 n, i
  * esc), esc = 2^(48 - cb) - 1 (W - 16 <= cb <= 44; larger counts also in the escape table), at out_k + seg_base[b],
  * seg_cnt[b] of them; dhist[d * grid + b] its words per dbits-bit digit (word >> dshift) & (2^dbits - 1), dbits <=
  * 11; qcnt[qv[j]] = the count of lookup j (ng_part_lookups_w's sorted by their top pbits, bounds qstart); flags[0]
- * bit 0: a partition reached min(limit, 13000) distinct pairs (count again with a bit more), bit 1: the escape table
+ * bit 0: a partition reached min(limit, 11000) distinct pairs (count again with a bit more), bit 1: the escape table
  * is full */
 int ng_part_count32(const uint32_t* ev, const ng_i64* start, int pbits, int W, const ng_u64* qk, const uint32_t* qv,
                     const ng_i64* qstart, ng_u64* out_k, int cb, ng_u64* esc_k, uint32_t* esc_c, ng_u64 esc_cap,

@@ -190,8 +190,9 @@ __global__ void __launch_bounds__(256) sel_write_k(const int* __restrict__ v, i6
 #define P32_BUCKETS (P32_SLOTS / 4)
 #define P32_BLOCK 1024
 #define P32_ITEMS 6  // events per thread and round (8 spills registers)
-#define P32_LIMIT 13000  // distinct pairs a partition may reach before it is declared overfull (a free slot always
-                         // remains: at most P32_LIMIT + P32_BLOCK keys are ever inserted)
+#define P32_LIMIT 11000  // distinct pairs a partition may reach before it is declared overfull (a free slot always
+                         // remains: it is checked once per half-round, in which the block inserts at most
+                         // P32_BLOCK * P32_ITEMS / 2 = 3072 more keys)
 #define EMPTY32 0xFFFFFFFFu
 
 __device__ __forceinline__ u32 p32_bucket(u32 key) {
@@ -247,7 +248,7 @@ __device__ __forceinline__ u32 p32_find(const u32* tk, const u32* tc, u32 key) {
 // out_k[start[p0] ...] as packed words, segment b = (seg_base[b], seg_cnt[b]); dhist[d * G + b] the block's words per
 // dbits-bit digit at dshift. Lookups: qk (sorted like the events: wmix keys << (64 - W), or EMPTY), qv their query
 // positions, qstart their partitions' bounds: qcnt[qv[j]] = the pair's count or 0. A partition reaching `limit`
-// distinct pairs (at most P32_LIMIT) sets flags[0] bit 0 and is left incomplete.
+// distinct pairs (at most P32_LIMIT) sets flags[0] bit 0; its count may be incomplete.
 __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ ev, const i64* __restrict__ start,
                                                       i64 P, int pbits, int W, const u64* __restrict__ qk,
                                                       const u32* __restrict__ qv, const i64* __restrict__ qstart,
@@ -332,44 +333,80 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
                 }
             }
             // in two halves (register pressure): every item's home bucket read before any is used; an item whose
-            // key is there adds to its count; the others are inserted one item at a time (a lane per item per wave)
+            // key is there adds to its count; the others try their bucket's first free slot by compare-and-swap, all
+            // of a half's swaps issued before any result is used (a key already put there by another lane counts as
+            // found); the few whose swap lost to another key, or whose bucket was full, walk on one item at a time;
+            // the half's new slots join the list with one LDS atomic per wave
+            constexpr int HI = P32_ITEMS / 2;
 #pragma unroll
-            for (int h = 0; h < P32_ITEMS; h += P32_ITEMS / 2) {
-                uint4 q[P32_ITEMS / 2];
-                u32 bk[P32_ITEMS / 2];
+            for (int h = 0; h < P32_ITEMS; h += HI) {
+                uint4 q[HI];
+                u32 bk[HI];
 #pragma unroll
-                for (int r = 0; r < P32_ITEMS / 2; ++r) {
+                for (int r = 0; r < HI; ++r) {
                     bk[r] = add[h + r] ? p32_bucket(key[h + r]) : 0u;
                     if (add[h + r]) q[r] = *(const uint4*)(tk + 4 * bk[r]);
                 }
+                bool pend = false;
 #pragma unroll
-                for (int r = 0; r < P32_ITEMS / 2; ++r) {
+                for (int r = 0; r < HI; ++r) {
                     const int s = add[h + r] ? p32_in(q[r], bk[r], key[h + r]) : -1;
                     if (s >= 0) {
                         atomicAdd(&tc[s], add[h + r]);
                         add[h + r] = 0;
                     }
+                    pend |= add[h + r] != 0;
                 }
+                if (!__ballot(pend)) continue;
+                if (__builtin_amdgcn_readfirstlane(nocc) >= limit) {  // overfull: counted again with a bit more
+                    if (lane == 0) atomicOr(&flags[0], 1u);
+                    continue;
+                }
+                int slot[HI];
+                u32 prev[HI];
 #pragma unroll
-                for (int r = 0; r < P32_ITEMS / 2; ++r) {
-                    const bool ins = add[h + r] != 0;
-                    if (!__ballot(ins)) continue;
-                    if (__builtin_amdgcn_readfirstlane(nocc) >= limit) {  // overfull: counted again with a bit more
-                        if (lane == 0) atomicOr(&flags[0], 1u);
-                        continue;
+                for (int r = 0; r < HI; ++r) {
+                    slot[r] = -1;
+                    prev[r] = 0;
+                    if (add[h + r]) {
+                        const uint4 qq = q[r];
+                        const int e = qq.x == EMPTY32 ? 0 : qq.y == EMPTY32 ? 1 : qq.z == EMPTY32 ? 2 : qq.w == EMPTY32 ? 3 : -1;
+                        if (e >= 0) {
+                            slot[r] = 4 * (int)bk[r] + e;
+                            prev[r] = atomicCAS(&tk[slot[r]], EMPTY32, key[h + r]);
+                        }
                     }
-                    bool fresh = false;
-                    int s = -1;
-                    if (ins) {
-                        s = p32_insert(tk, key[h + r], bk[r], q[r], &fresh);
-                        atomicAdd(&tc[s], add[h + r]);
+                }
+                bool fresh[HI];
+#pragma unroll
+                for (int r = 0; r < HI; ++r) {
+                    fresh[r] = false;
+                    if (!add[h + r]) continue;
+                    if (slot[r] >= 0 && prev[r] == EMPTY32) {
+                        fresh[r] = true;
+                    } else if (slot[r] < 0 || prev[r] != key[h + r]) {  // lost to another key, or a full bucket
+                        const uint4 qq = *(const uint4*)(tk + 4 * bk[r]);
+                        bool f = false;
+                        slot[r] = p32_insert(tk, key[h + r], bk[r], qq, &f);
+                        fresh[r] = f;
                     }
-                    const u64 fb = __ballot(fresh);
-                    if (fb) {
-                        u32 at = 0;
-                        if (lane == 0) at = atomicAdd(&nocc, (u32)__popcll(fb));
-                        at = (u32)__shfl((int)at, 0, WAVE);
-                        if (fresh) list[at + (u32)__popcll(fb & lanemask_lt())] = (u16)s;
+                    atomicAdd(&tc[slot[r]], add[h + r]);
+                }
+                u64 fb[HI];
+                u32 nf = 0;
+#pragma unroll
+                for (int r = 0; r < HI; ++r) {
+                    fb[r] = __ballot(fresh[r]);
+                    nf += (u32)__popcll(fb[r]);
+                }
+                if (nf) {  // wave-uniform
+                    u32 at = 0;
+                    if (lane == 0) at = atomicAdd(&nocc, nf);
+                    at = (u32)__shfl((int)at, 0, WAVE);
+#pragma unroll
+                    for (int r = 0; r < HI; ++r) {
+                        if (fresh[r]) list[at + (u32)__popcll(fb[r] & lanemask_lt())] = (u16)slot[r];
+                        at += (u32)__popcll(fb[r]);
                     }
                 }
             }
@@ -385,6 +422,9 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
             }
         }
         const u32 nl = nocc;
+        // a wave checks the limit once per half-round, so a partition can pass it by up to a round's new keys
+        // without a skipped insert: it is declared overfull all the same
+        if (t == 0 && nl >= limit) atomicOr(&flags[0], 1u);
         lds_barrier();  // every lookup has probed and nocc is read before the output pass empties the slots
         for (u32 i = t; i < nl; i += P32_BLOCK) {
             const int j = list[i];
@@ -615,7 +655,7 @@ extern "C" int ng_select_positive(void* temp, size_t* temp_bytes, const int* v, 
 // them (out_k holds as many words as there are events); dhist[d * grid + b] block b's words per dbits-bit digit
 // (word >> dshift) & (2^dbits - 1) (1 <= dbits <= 11), for ng_seg_scatter. Lookups (ng_part_lookups_w's, sorted by
 // their top pbits; qstart their partitions' bounds; qk and qv may be NULL with qstart all zeros: none) get qcnt[qv[j]]
-// = the pair's count or 0. flags[0] bit 0: a partition reached min(limit, 13000) distinct pairs (its count is
+// = the pair's count or 0. flags[0] bit 0: a partition reached min(limit, 11000) distinct pairs (its count is
 // incomplete: count again with a bit more); bit 1: the escape table is full.
 extern "C" int ng_part_count32(const u32* ev, const i64* start, int pbits, int W, const u64* qk, const u32* qv,
                                const i64* qstart, u64* out_k, int cb, u64* esc_k, u32* esc_c, u64 esc_cap,

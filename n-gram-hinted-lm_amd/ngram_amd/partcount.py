@@ -262,8 +262,8 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids:
 
 RECORD_WORDS = {1: 4, 2: 8, 4: 8, 8: 16}  # u32 words of a context record for top 1, 2, 4, 8
 
-P32_TARGET = 7168  # distinct pairs per partition aimed at by the 32-bit count (its LDS table takes up to 13000)
-P32_LIMIT = 13000  # distinct pairs at which the 32-bit count declares a partition overfull (at most 13000)
+P32_TARGET = 6144  # distinct pairs per partition aimed at by the 32-bit count (its LDS table takes up to 11000)
+P32_LIMIT = 11000  # distinct pairs at which the 32-bit count declares a partition overfull (at most 11000)
 PACK32_MIN_BITS = 0  # context bits of the 32-bit count's packed words at least this (a narrower count field)
 AGG_ID_BITS = 11  # context ids per group of words whose records ng_ctx_agg makes in one block: at most 2^11
 W_MAX = 42  # the widest pair key (context-id bits + 16) the 32-bit count takes: its first pass's digit is at most 10
