@@ -186,13 +186,20 @@ __global__ void __launch_bounds__(256) sel_write_k(const int* __restrict__ v, i6
     }
 }
 
+#ifndef P32_SLOTS
 #define P32_SLOTS 14336  // 112 KB of LDS (u32 keys and counts) beside the slot list (28 KB): one block per CU
+#endif
 #define P32_BUCKETS (P32_SLOTS / 4)
+#ifndef P32_BLOCK
 #define P32_BLOCK 1024
+#endif
 #define P32_ITEMS 6  // events per thread and round (8 spills registers)
-#define P32_LIMIT 11000  // distinct pairs a partition may reach before it is declared overfull (a free slot always
-                         // remains: it is checked once per half-round, in which the block inserts at most
-                         // P32_BLOCK * P32_ITEMS / 2 = 3072 more keys)
+// P32_LIMIT: the distinct pairs a partition may reach before it is declared overfull. A free slot always remains: the
+// limit is checked once per half-round, in which the block inserts at most P32_BLOCK * P32_ITEMS / 2 more keys.
+#ifndef P32_LIMIT
+#define P32_LIMIT 11000
+#endif
+static_assert(P32_LIMIT + P32_BLOCK * P32_ITEMS / 2 < P32_SLOTS, "a half-round past the limit must leave a free slot");
 #define EMPTY32 0xFFFFFFFFu
 
 __device__ __forceinline__ u32 p32_bucket(u32 key) {
