@@ -247,6 +247,11 @@ int ng_msd_pass(void* temp, size_t* temp_bytes, const uint32_t* keys, const uint
                 const ng_u64* total, ng_u64 cap, int shift, int nbits, uint32_t* out, ng_i64* start, void* stream);
 int ng_msd_pass64(void* temp, size_t* temp_bytes, const ng_u64* keys, const uint32_t* dpre, ng_i64 nseg, int nb_bits,
                   const ng_u64* total, ng_u64 cap, int shift, int nbits, ng_u64* out, ng_i64* start, void* stream);
+/* ng_msd_pass over u64 keys written out as their low 32 bits (shift <= 32): the second pass of the 32-bit count for
+ * pair keys wider than its first pass narrows (W > 42: the corpus-wide tables' context ids) */
+int ng_msd_pass_narrow(void* temp, size_t* temp_bytes, const ng_u64* keys, const uint32_t* dpre, ng_i64 nseg,
+                       int nb_bits, const ng_u64* total, ng_u64 cap, int shift, int nbits, uint32_t* out, ng_i64* start,
+                       void* stream);
 /* lookups of n query positions i = pos[j] (pos NULL: j) for the 32-bit count: qk[j] = wmix(ctx_of[i] << 16 | tgt[i],
  * W) << (64 - W) for ids in [lo, hi) (hi <= 2^(W - 16)), else EMPTY; qv[j] = i; n_dev (may be NULL, pos required): a
  * device-side count of pos's entries, lookups j >= *n_dev EMPTY */
@@ -262,17 +267,22 @@ int ng_select_positive(void* temp, size_t* temp_bytes, const int* v, ng_i64 n, i
  * seg_cnt[b] of them; dhist[d * grid + b] its words per dbits-bit digit (word >> dshift) & (2^dbits - 1), dbits <=
  * 11; qcnt[qv[j]] = the count of lookup j (ng_part_lookups_w's sorted by their top pbits, bounds qstart); flags[0]
  * bit 0: a partition reached min(limit, 11000) distinct pairs (count again with a bit more), bit 1: the escape table
- * is full */
+ * is full; slab (may be NULL): 2^pbits * 14336 u64, each partition's LDS table written out (slot = count << 32 |
+ * key) for the corpus-wide tables' queries */
 int ng_part_count32(const uint32_t* ev, const ng_i64* start, int pbits, int W, const ng_u64* qk, const uint32_t* qv,
                     const ng_i64* qstart, ng_u64* out_k, int cb, ng_u64* esc_k, uint32_t* esc_c, ng_u64 esc_cap,
                     uint32_t* seg_cnt, ng_i64* seg_base, uint32_t* qcnt, uint32_t* dhist, int dshift, int dbits,
-                    uint32_t limit, uint32_t* flags, int grid, void* stream);
+                    uint32_t limit, uint32_t* flags, int grid, ng_u64* slab, void* stream);
 /* per context id c < n_ids from ng_part_count32's words grouped by context into P partitions (start: i64[P + 1],
  * partition q = the ids [q << ibits, (q + 1) << ibits), ibits <= 11; ng_seg_scatter then ng_msd_pass64): dist[c] =
- * its pairs (0: absent) for every id, and for present contexts the record rec[c] of ng_ctx_summary's layout (topk 1,
- * 2, 4, 8; first-word index 0); flags[0] bit 2: a total reached 2^32 */
+ * its pairs (0: absent) for every id (dist may be NULL), and for present contexts the record rec[c] of ng_ctx_summary's layout (topk 1,
+ * 2, 4, 8; first-word index 0); flags[0] bit 2: a total reached 2^32; deep (may be NULL, deep_n then too): the ids
+ * of the contexts of more than deep_min pairs, in no order (at most deep_cap kept, *deep_n counts all; zeroed by the
+ * caller); present (may be NULL): *present += the present contexts; grid: blocks walking the partitions in turn (0:
+ * one block per partition) */
 int ng_ctx_agg(const ng_u64* w, const ng_i64* start, ng_i64 P, int ibits, int cb, ng_i64 n_ids, const ng_u64* esc_k,
                const uint32_t* esc_c, ng_u64 esc_cap, int topk, uint32_t* rec, uint32_t* dist, uint32_t* flags,
+               uint32_t deep_min, ng_i64* deep, ng_u64 deep_cap, ng_u64* deep_n, ng_u64* present, int grid,
                void* stream);
 /* exclusive prefix sum of n u32 (out may alias in), *total (may be NULL) the sum; CUB-style two-phase temp storage */
 int ng_exclusive_scan_u32(void* temp, size_t* temp_bytes, const uint32_t* in, uint32_t* out, ng_i64 n,
@@ -312,12 +322,23 @@ int ng_pos_summary(const int* ctx_of, ng_i64 N, ng_i64 lo, ng_i64 hi, const uint
  * bit 1: context table full (rerun bigger) */
 int ng_table_emit(const uint16_t* tok, ng_i64 L, int k, ng_u64* ck, ng_u64 ccap, ng_u64* ev, uint32_t* flags,
                   int grid, void* stream);
+/* corpus-wide level build for the 32-bit count (count_table.rs build_level :491-631): contexts into ck (slot = id,
+ * ccap <= 2^(W - 16)) and each position's event wmix(slot << 16 | next, W) appended to its block's region ev[b *
+ * region ...] (region >= ceil(L / (grid * 256)) * 256), ev_count[b] and the top-dbits digit histogram dhist[d * grid
+ * + b] (dbits <= 10); flags[0] bit 1: context table full (rerun bigger), bit 2: a region overflowed */
+int ng_table_emit32(const uint16_t* tok, ng_i64 L, int k, ng_u64* ck, ng_u64 ccap, int W, int dbits, ng_u64* ev,
+                    ng_u64 region, uint32_t* ev_count, uint32_t* dhist, uint32_t* flags, int grid, void* stream);
 /* per key (EMPTY: none) its context-table slot or -1 */
 int ng_table_lookup(const ng_u64* keys, ng_i64 n, const ng_u64* ck, ng_u64 ccap, int* slot, void* stream);
 /* thr[c] = the kth largest pair score of each listed context (ids[m]; count_table.rs:146-158 deep_last) over packed
  * words sorted by pair key and ng_ctx_summary's topk-8 records */
 int ng_ctx_kth(const ng_u64* w, int cb, const ng_u64* esc_k, const uint32_t* esc_c, ng_u64 esc_cap,
                const uint32_t* rec, const ng_i64* ids, ng_i64 m, int kth, ng_u64* thr, void* stream);
+/* ng_ctx_kth over words grouped by context into partitions of 2^ibits ids (gstart: their starts; ng_ctx_agg's
+ * input) for the first min(m, *m_dev) listed ids (m_dev may be NULL) */
+int ng_ctx_kth_grouped(const ng_u64* w, const ng_i64* gstart, int ibits, int cb, const ng_u64* esc_k,
+                       const uint32_t* esc_c, ng_u64 esc_cap, const ng_i64* ids, ng_i64 m, const ng_u64* m_dev, int kth,
+                       ng_u64* thr, void* stream);
 /* per query position (count_table.rs query_counts :291-331): tot, dist, cnt (CNT_TOP rule by thr, NULL: none) and
  * the first kout top entries of its level-k context, from the context table, the packed words sorted by pair key and
  * the topk-8 records */
@@ -325,6 +346,12 @@ int ng_table_query(const uint16_t* x, const int* avail, const uint16_t* tgt, ng_
                    ng_u64 ccap, const ng_u64* w, int cb, const ng_u64* esc_k, const uint32_t* esc_c, ng_u64 esc_cap,
                    const uint32_t* rec, const ng_u64* thr, uint32_t cnt_top, int kout, int* out_tot, int* out_dist,
                    int* out_cnt, uint16_t* out_tok, uint32_t* out_tcnt, void* stream);
+/* ng_table_query over a level counted by the 32-bit count: cnt from its slabs (ng_part_count32's, 2^pbits
+ * partitions of the W-bit pair hash) */
+int ng_table_query32(const uint16_t* x, const int* avail, const uint16_t* tgt, ng_i64 n, int k, const ng_u64* ck,
+                     ng_u64 ccap, const ng_u64* slabs, int pbits, int W, const uint32_t* rec, const ng_u64* thr,
+                     uint32_t cnt_top, int kout, int* out_tot, int* out_dist, int* out_cnt, uint16_t* out_tok,
+                     uint32_t* out_tcnt, void* stream);
 /* hint rows over table levels (count_table.rs query_rows :338-404); desc[v * 3]: slot_of, records, bucket */
 int ng_pos_rows(ng_i64 N, int nlv, const ng_i64* desc, int entries, short* cell, uint16_t* next, uint16_t* weights,
                 signed char* level, void* stream);

@@ -24,6 +24,7 @@
 #include "part.h"
 #include "prim.h"
 #include "scatter.h"
+#include "pairs32.h"
 
 namespace {
 
@@ -186,65 +187,6 @@ __global__ void __launch_bounds__(256) sel_write_k(const int* __restrict__ v, i6
     }
 }
 
-#ifndef P32_SLOTS
-#define P32_SLOTS 14336  // 112 KB of LDS (u32 keys and counts) beside the slot list (28 KB): one block per CU
-#endif
-#define P32_BUCKETS (P32_SLOTS / 4)
-#ifndef P32_BLOCK
-#define P32_BLOCK 1024
-#endif
-#define P32_ITEMS 6  // events per thread and round (8 spills registers)
-// P32_LIMIT: the distinct pairs a partition may reach before it is declared overfull. A free slot always remains: the
-// limit is checked once per half-round, in which the block inserts at most P32_BLOCK * P32_ITEMS / 2 more keys.
-#ifndef P32_LIMIT
-#define P32_LIMIT 11000
-#endif
-static_assert(P32_LIMIT + P32_BLOCK * P32_ITEMS / 2 < P32_SLOTS, "a half-round past the limit must leave a free slot");
-#define EMPTY32 0xFFFFFFFFu
-
-__device__ __forceinline__ u32 p32_bucket(u32 key) {
-    return (u32)(((u64)(key * 0x9E3779B1u) * P32_BUCKETS) >> 32);
-}
-__device__ __forceinline__ u32 p32_next(u32 b) { return b + 1 == P32_BUCKETS ? 0 : b + 1; }
-
-// The slot of `key` in bucket q (read from bucket b), or -1.
-__device__ __forceinline__ int p32_in(const uint4& q, u32 b, u32 key) {
-    const int f = q.x == key ? 0 : q.y == key ? 1 : q.z == key ? 2 : q.w == key ? 3 : -1;
-    return f < 0 ? -1 : 4 * (int)b + f;
-}
-
-// Insert `key` (below 2^31) into the bucketized table (four keys per 16-byte bucket, filled from the front, buckets
-// probed linearly) from bucket b, whose contents q were read; returns its slot, *fresh whether it took a free slot.
-// A lost race for a slot re-reads the bucket.
-__device__ __forceinline__ int p32_insert(u32* tk, u32 key, u32 b, uint4 q, bool* fresh) {
-    *fresh = false;
-    while (true) {
-        const int s = p32_in(q, b, key);
-        if (s >= 0) return s;
-        const int e = q.x == EMPTY32 ? 0 : q.y == EMPTY32 ? 1 : q.z == EMPTY32 ? 2 : q.w == EMPTY32 ? 3 : -1;
-        if (e >= 0) {
-            const u32 prev = atomicCAS(&tk[4 * b + e], EMPTY32, key);
-            if (prev == EMPTY32 || prev == key) {
-                *fresh = prev == EMPTY32;
-                return 4 * (int)b + e;
-            }
-        } else {
-            b = p32_next(b);
-        }
-        q = *(const uint4*)(tk + 4 * b);
-    }
-}
-
-__device__ __forceinline__ u32 p32_find(const u32* tk, const u32* tc, u32 key) {
-    u32 b = p32_bucket(key);
-    while (true) {
-        const uint4 q = *(const uint4*)(tk + 4 * b);
-        const int s = p32_in(q, b, key);
-        if (s >= 0) return tc[s];
-        if (q.w == EMPTY32) return 0;
-        b = p32_next(b);
-    }
-}
 
 // Block b counts the partitions it owns (part_owner: about equal events per block) in turn. Events: u32, a
 // partition's key = its low lbits = W - pbits bits (h = p << lbits | key). A round of P32_ITEMS events per thread:
@@ -263,7 +205,7 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
                                                       u64 esc_cap, u32* __restrict__ seg_cnt,
                                                       i64* __restrict__ seg_base, u32* __restrict__ qcnt,
                                                       u32* __restrict__ dhist, int dshift, int dbits, u32 limit,
-                                                      u32* flags) {
+                                                      u32* flags, u64* __restrict__ slab) {
     __shared__ __align__(16) u32 tk[P32_SLOTS];
     __shared__ u32 tc[P32_SLOTS];
     __shared__ u16 list[P32_SLOTS];
@@ -433,6 +375,11 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
         // without a skipped insert: it is declared overfull all the same
         if (t == 0 && nl >= limit) atomicOr(&flags[0], 1u);
         lds_barrier();  // every lookup has probed and nocc is read before the output pass empties the slots
+        if (slab) {  // the table as it stands, slot s = count << 32 | key (empty slots: 0 << 32 | EMPTY32)
+            u64* sp = slab + (u64)p * P32_SLOTS;
+            for (int j = t; j < P32_SLOTS; j += P32_BLOCK) sp[j] = ((u64)tc[j] << 32) | tk[j];
+            lds_barrier();  // read before the output pass empties the slots
+        }
         for (u32 i = t; i < nl; i += P32_BLOCK) {
             const int j = list[i];
             const u32 key = tk[j], n = tc[j];
@@ -461,38 +408,59 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
 // LDS. The top scores come from a cascade of atomic maxima: a score displaced from (or kept out of) slot r goes on to
 // slot r + 1, so slot r ends with the r-th largest; a score not above slot KT - 1's current value (which only grows,
 // and below which KT larger scores already exist) is not inserted. Then every id of the partition below n_ids gets
-// dist[c] = its pairs and, if present, its record (CtxRecord<KT>, first-word index 0). flags[0] bit 2: a total
-// reached 2^32.
+// dist[c] = its pairs and, if present, its record (CtxRecord<KT>, first-word index 0); with `deep`, every context of
+// more than deep_min pairs is appended to deep (*deep_n counts them). flags[0] bit 2: a total reached 2^32.
 #define AGG_BLOCK 1024
 #define AGG_IDS 2048
+// Two blocks share a compute unit where the LDS allows (KT <= 4: 80 KB each): 8 waves per SIMD, so at most 96
+// scalar registers a wave (amdgpu_waves_per_eu), which the kernel's arguments and walk state would otherwise exceed.
 template <int KT>
-__global__ void __launch_bounds__(AGG_BLOCK) ctx_agg_k(const u64* __restrict__ w, const i64* __restrict__ start,
+__global__ void __launch_bounds__(AGG_BLOCK) __attribute__((amdgpu_waves_per_eu(8))) ctx_agg_k(const u64* __restrict__ w, const i64* __restrict__ start,
                                                        i64 P, int ibits, int cb, i64 n_ids,
                                                        const u64* __restrict__ esc_k, const u32* __restrict__ esc_c,
                                                        u64 esc_cap, u32* __restrict__ rec, u32* __restrict__ dist,
-                                                       u32* flags) {
+                                                       u32* flags, u32 deep_min, i64* __restrict__ deep,
+                                                       u64 deep_cap, u64* deep_n, u64* present) {
     __shared__ u32 s_tot[AGG_IDS], s_dist[AGG_IDS];
     __shared__ u64 s_top[AGG_IDS * KT];
     const int t = threadIdx.x, lane = lane_id();
     const int sh = 64 - cb, csh = 48 - cb;
     const u64 esc = (1ull << csh) - 1;
     const int nid = 1 << ibits;
-    for (i64 q = blockIdx.x; q < P; q += gridDim.x) {
+    // a block walks its partitions with the next round's words (this partition's, else the next partition's first)
+    // and the next partition's bounds loaded ahead, so their latency hides behind the LDS work
+    i64 q = blockIdx.x;
+    if (q >= P) return;
+    u32 mine = 0;  // this thread's present contexts, summed over the block at the end
+    i64 wa = start[q], we = start[q + 1];
+    i64 nwa = 0, nwe = 0;
+    if (q + gridDim.x < P) {
+        nwa = start[q + gridDim.x];
+        nwe = start[q + gridDim.x + 1];
+    }
+    // loads are unconditional (an index past its range reads word 0, which always exists, and is not used), so the
+    // compiler waits for each round's words only, not for the prefetch behind them
+    u64 ahead = w[wa + t < we ? wa + t : 0];
+    for (;;) {
         const i64 lo = q << ibits;
         if (lo >= n_ids) break;  // partitions ascend with q
-        const i64 wa = start[q], we = start[q + 1];
+        const bool more = q + gridDim.x < P;
         for (int l = t; l < nid; l += AGG_BLOCK) {
             s_tot[l] = 0;
             s_dist[l] = 0;
         }
         for (int l = t; l < nid * KT; l += AGG_BLOCK) s_top[l] = 0;
-        __syncthreads();
+        lds_barrier();
+        if (wa >= we) ahead = w[more && nwa + t < nwe ? nwa + t : 0];  // an empty partition: the next one's words
         for (i64 i0 = wa; i0 < we; i0 += AGG_BLOCK) {  // the same rounds for every wave
             const i64 i = i0 + t;
             const bool valid = i < we;
+            const u64 word = valid ? ahead : 0;
+            const i64 j = i0 + AGG_BLOCK < we ? (i0 + AGG_BLOCK + t < we ? i0 + AGG_BLOCK + t : 0)
+                                               : (more && nwa + t < nwe ? nwa + t : 0);
+            ahead = w[j];
             const u64 vb = __ballot(valid);
             if (!vb) continue;
-            const u64 word = valid ? w[i] : 0;
             const int lid = (int)((i64)(word >> sh) - lo) & (nid - 1);
             u32 n = 0;
             if (valid) {
@@ -536,20 +504,39 @@ __global__ void __launch_bounds__(AGG_BLOCK) ctx_agg_k(const u64* __restrict__ w
                 }
             }
         }
-        __syncthreads();
+        lds_barrier();
         const int nl = n_ids - lo < nid ? (int)(n_ids - lo) : nid;
         for (int l = t; l < nl; l += AGG_BLOCK) {
             const i64 c = lo + l;
             const u32 d = s_dist[l];
-            dist[c] = d;
+            if (dist) dist[c] = d;
             if (d) {
+                ++mine;
                 u64 top[KT];
 #pragma unroll
                 for (int r = 0; r < KT; ++r) top[r] = s_top[l * KT + r];
                 store_record<KT>(rec, (u64)c, s_tot[l], d, top, 0);
+                if (deep && d > deep_min) {
+                    const u64 at = atomicAdd((unsigned long long*)deep_n, 1ull);
+                    if (at < deep_cap) deep[at] = c;
+                }
             }
         }
-        __syncthreads();
+        lds_barrier();  // the LDS is read before the next partition clears it
+        if (!more) break;
+        q += gridDim.x;
+        wa = nwa;
+        we = nwe;
+        if (q + gridDim.x < P) {
+            nwa = start[q + gridDim.x];
+            nwe = start[q + gridDim.x + 1];
+        }
+    }
+    if (present) {  // one atomic per wave (a few hundred blocks)
+        u32 sm = mine;
+#pragma unroll
+        for (int d = WAVE / 2; d > 0; d >>= 1) sm += (u32)__shfl_down((int)sm, d, WAVE);
+        if (lane == 0 && sm) atomicAdd((unsigned long long*)present, (unsigned long long)sm);
     }
 }
 
@@ -559,12 +546,13 @@ static inline i64 msd_max_tiles(u64 cap, int nb) { return (i64)((cap + MSD_TILE 
 
 static inline size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-template <typename K>
+template <typename K, typename KO = K>
 static int msd_pass(void* temp, size_t* temp_bytes, const K* keys, const u32* dpre, i64 nseg, int nb_bits,
-                    const u64* total, u64 cap, int shift, int nbits, K* out, i64* start, hipStream_t st) {
+                    const u64* total, u64 cap, int shift, int nbits, KO* out, i64* start, hipStream_t st) {
     if (temp_bytes == nullptr || nb_bits < 1 || nb_bits > 11 || nbits < 0 || nbits > 11 || shift < 0 ||
         shift + nbits > (int)(8 * sizeof(K)) || nseg <= 0 || cap > 0xFFFFFFFFull)
         return -1;
+    if (sizeof(KO) < sizeof(K) && shift > 32) return -1;  // narrowing keeps the low 32 bits: the bits below the digit
     const int nb = 1 << nb_bits;
     const i64 mt = msd_max_tiles(cap, nb);
     const i64 nh = nbits ? mt << nbits : 0;
@@ -591,9 +579,9 @@ static int msd_pass(void* temp, size_t* temp_bytes, const K* keys, const u32* dp
     if (e) return e;
     const TileSegs sg{bstart, tfirst, hist, nb, nbits, mt};
     if (nbits <= 8)
-        scatter_k<256, K, K><<<g, SS_BLOCK, 0, st>>>(keys, sg, shift, nbits, out, cap);
+        scatter_k<256, K, KO><<<g, SS_BLOCK, 0, st>>>(keys, sg, shift, nbits, out, cap);
     else
-        scatter_k<SS_MAXB, K, K><<<g, SS_BLOCK, 0, st>>>(keys, sg, shift, nbits, out, cap);
+        scatter_k<SS_MAXB, K, KO><<<g, SS_BLOCK, 0, st>>>(keys, sg, shift, nbits, out, cap);
     const i64 P = (i64)nb << nbits;
     msd_starts_k<<<grid_for(P + 1, 256), 256, 0, st>>>(bstart, tfirst, nb, nbits, hist, start);
     return (int)hipGetLastError();
@@ -619,6 +607,15 @@ extern "C" int ng_msd_pass64(void* temp, size_t* temp_bytes, const u64* keys, co
                              void* stream) {
     return msd_pass<u64>(temp, temp_bytes, keys, dpre, nseg, nb_bits, total, cap, shift, nbits, out, start,
                          (hipStream_t)stream);
+}
+
+// ng_msd_pass over u64 keys written out as their low 32 bits (shift <= 32): the second pass of the 32-bit count when
+// the events are wider than a first pass's digit can narrow (W > 42, the corpus-wide tables' wide context ids).
+extern "C" int ng_msd_pass_narrow(void* temp, size_t* temp_bytes, const u64* keys, const u32* dpre, i64 nseg,
+                                  int nb_bits, const u64* total, u64 cap, int shift, int nbits, u32* out, i64* start,
+                                  void* stream) {
+    return msd_pass<u64, u32>(temp, temp_bytes, keys, dpre, nseg, nb_bits, total, cap, shift, nbits, out, start,
+                              (hipStream_t)stream);
 }
 
 // The lookups of n query positions (pos[j], or j with pos NULL) for the 32-bit count: qk[j] = wmix(ctx_of[i] << 16 |
@@ -663,11 +660,13 @@ extern "C" int ng_select_positive(void* temp, size_t* temp_bytes, const int* v, 
 // (word >> dshift) & (2^dbits - 1) (1 <= dbits <= 11), for ng_seg_scatter. Lookups (ng_part_lookups_w's, sorted by
 // their top pbits; qstart their partitions' bounds; qk and qv may be NULL with qstart all zeros: none) get qcnt[qv[j]]
 // = the pair's count or 0. flags[0] bit 0: a partition reached min(limit, 11000) distinct pairs (its count is
-// incomplete: count again with a bit more); bit 1: the escape table is full.
+// incomplete: count again with a bit more); bit 1: the escape table is full. slab (may be NULL): 2^pbits * 14336
+// u64, partition p's table written to slab + p * 14336 (slot = count << 32 | key, pairs32.h's layout), for queries
+// of the counts after the build (p32_pair_count).
 extern "C" int ng_part_count32(const u32* ev, const i64* start, int pbits, int W, const u64* qk, const u32* qv,
                                const i64* qstart, u64* out_k, int cb, u64* esc_k, u32* esc_c, u64 esc_cap,
                                u32* seg_cnt, i64* seg_base, u32* qcnt, u32* dhist, int dshift, int dbits, u32 limit,
-                               u32* flags, int grid, void* stream) {
+                               u32* flags, int grid, u64* slab, void* stream) {
     if (pbits < 1 || pbits > 30 || W < 17 || W - 16 > cb || cb > 44 || W - pbits > 31 || W - pbits < 1 ||
         grid <= 0 || grid > 65536 || esc_k == nullptr || esc_c == nullptr || esc_cap == 0 || dbits < 1 ||
         dbits > 11 || dshift < 0 || dshift + dbits > 64 || dhist == nullptr || qstart == nullptr || limit == 0)
@@ -676,28 +675,38 @@ extern "C" int ng_part_count32(const u32* ev, const i64* start, int pbits, int W
     limit = limit < P32_LIMIT ? limit : P32_LIMIT;
     count32_k<<<grid, P32_BLOCK, 0, (hipStream_t)stream>>>(ev, start, P, pbits, W, qk, qv, qstart, out_k, cb, esc_k,
                                                            esc_c, esc_cap, seg_cnt, seg_base, qcnt, dhist, dshift,
-                                                           dbits, limit, flags);
+                                                           dbits, limit, flags, slab);
     return (int)hipGetLastError();
 }
 
 // Per context of ids below n_ids from ng_part_count32's words (cb context bits) grouped by context into P
 // partitions (start: i64[P + 1]; partition q = the ids [q << ibits, (q + 1) << ibits), ibits <= 11): dist[c] = its
-// pairs (0: absent) for every id, and for present contexts the record rec[c] of ng_ctx_summary's layout (topk 1, 2,
-// 4, 8; first-word index 0); flags[0] bit 2: a total reached 2^32.
+// pairs (0: absent) for every id (dist may be NULL), and for present contexts the record rec[c] of ng_ctx_summary's layout (topk 1, 2,
+// 4, 8; first-word index 0); flags[0] bit 2: a total reached 2^32. deep (may be NULL; deep_n then too): the ids of
+// the contexts of more than deep_min pairs, appended in no order (at most deep_cap kept; *deep_n counts all, zeroed by
+// the caller), for ng_ctx_kth_grouped. present (may be NULL): *present += the present contexts (zeroed by the caller).
+// grid: the blocks, each walking partitions q, q + grid, ... with the next one's words loaded ahead (for many light
+// partitions: a couple per compute unit), or 0: a block per partition (for heavy ones, which a fixed walk would leave
+// unbalanced).
 extern "C" int ng_ctx_agg(const u64* w, const i64* start, i64 P, int ibits, int cb, i64 n_ids, const u64* esc_k,
-                          const u32* esc_c, u64 esc_cap, int topk, u32* rec, u32* dist, u32* flags, void* stream) {
+                          const u32* esc_c, u64 esc_cap, int topk, u32* rec, u32* dist, u32* flags, u32 deep_min,
+                          i64* deep, u64 deep_cap, u64* deep_n, u64* present, int grid, void* stream) {
     if (cb < 1 || cb > 44 || ibits < 0 || (1 << ibits) > AGG_IDS || P <= 0 || esc_cap == 0 || n_ids < 0 ||
-        n_ids > (1ll << cb) || (P << ibits) < n_ids)
+        n_ids > (1ll << cb) || (P << ibits) < n_ids || (deep && !deep_n))
         return -1;
     if (n_ids == 0) return 0;
-    const int g = grid_cap(P, 1 << 20);
+    const int g = grid_cap(P, grid > 0 ? grid : 1 << 30);
     hipStream_t st = (hipStream_t)stream;
+#define AGG_LAUNCH(KT)                                                                                         \
+    ctx_agg_k<KT><<<g, AGG_BLOCK, 0, st>>>(w, start, P, ibits, cb, n_ids, esc_k, esc_c, esc_cap, rec, dist, flags, \
+                                           deep_min, deep, deep_cap, deep_n, present)
     switch (topk) {
-        case 1: ctx_agg_k<1><<<g, AGG_BLOCK, 0, st>>>(w, start, P, ibits, cb, n_ids, esc_k, esc_c, esc_cap, rec, dist, flags); break;
-        case 2: ctx_agg_k<2><<<g, AGG_BLOCK, 0, st>>>(w, start, P, ibits, cb, n_ids, esc_k, esc_c, esc_cap, rec, dist, flags); break;
-        case 4: ctx_agg_k<4><<<g, AGG_BLOCK, 0, st>>>(w, start, P, ibits, cb, n_ids, esc_k, esc_c, esc_cap, rec, dist, flags); break;
-        case 8: ctx_agg_k<8><<<g, AGG_BLOCK, 0, st>>>(w, start, P, ibits, cb, n_ids, esc_k, esc_c, esc_cap, rec, dist, flags); break;
+        case 1: AGG_LAUNCH(1); break;
+        case 2: AGG_LAUNCH(2); break;
+        case 4: AGG_LAUNCH(4); break;
+        case 8: AGG_LAUNCH(8); break;
         default: return -1;
     }
+#undef AGG_LAUNCH
     return (int)hipGetLastError();
 }

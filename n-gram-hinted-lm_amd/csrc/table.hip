@@ -13,6 +13,7 @@
 // deep_last) compares its score with thr[c], the CNT_TOP-th largest score of a context with more pairs than that.
 #include "probe.h"
 #include "part.h"
+#include "pairs32.h"
 
 namespace {
 
@@ -31,6 +32,50 @@ __global__ void __launch_bounds__(256) table_emit_k(const u16* __restrict__ tok,
         }
         ev[p] = e;
     }
+}
+
+// The 32-bit count's emitter for a corpus-wide level: as table_emit_k, but each position with a context appends its
+// event e = wmix(slot << 16 | next, W) to its block's region ev[b * region ...] (a block-local cursor in LDS, one LDS
+// atomic per wave), with the block's histogram of the events' top dbits bits (dhist[d * gridDim.x + b]) and its event
+// count (ev_count[b]): the scan-region layout of the 32-bit count's first pass. flags[0] bit 1: the context table is
+// full (the block stops; the level reruns bigger), bit 2: a region overflowed.
+template <int K>
+__global__ void __launch_bounds__(256) table_emit32_k(const u16* __restrict__ tok, i64 L, int k, u64* ck, u64 ccap,
+                                                      int W, int dbits, u64* __restrict__ ev, u64 region,
+                                                      u32* __restrict__ ev_count, u32* __restrict__ dhist,
+                                                      u32* flags) {
+    __shared__ u32 cur;
+    __shared__ u32 dh[1024];
+    const int nd = 1 << dbits, lane = lane_id();
+    if (threadIdx.x == 0) cur = 0;
+    for (int d = threadIdx.x; d < nd; d += blockDim.x) dh[d] = 0;
+    __syncthreads();
+    const i64 stride = (i64)gridDim.x * blockDim.x;
+    for (i64 base = blockIdx.x * (i64)blockDim.x + (threadIdx.x & ~(WAVE - 1)); base < L; base += stride) {
+        if (__builtin_amdgcn_readfirstlane(*(volatile u32*)&flags[0]) & 2u) break;  // wave-uniform
+        const i64 p = base + lane;
+        u32 nxt = SENT;
+        u64 key = EMPTY;
+        if (p < L) key = ctx_key_at<K>(tok, p, k, nxt);
+        i64 s = -1;
+        if (nxt != SENT && key != EMPTY) s = ctx_find_insert(ck, ccap, key, flags);
+        const bool hit = s >= 0;
+        const u64 b = __ballot(hit);
+        if (!b) continue;
+        u32 off = 0;
+        if (lane == 0) off = atomicAdd(&cur, (u32)__popcll(b));
+        off = (u32)__shfl((int)off, 0, WAVE);
+        if (hit) {
+            const u64 at = (u64)off + (u64)__popcll(b & lanemask_lt());
+            const u64 e = wmix(((u64)s << 16) | nxt, W);
+            if (at < region) ev[(u64)blockIdx.x * region + at] = e;
+            else atomicOr(&flags[0], 4u);
+            atomicAdd(&dh[(u32)(e >> (W - dbits))], 1u);
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) ev_count[blockIdx.x] = cur < region ? cur : (u32)region;
+    for (int d = threadIdx.x; d < nd; d += blockDim.x) dhist[(i64)d * gridDim.x + blockIdx.x] = dh[d];
 }
 
 __global__ void table_lookup_k(const u64* __restrict__ keys, i64 n, const u64* __restrict__ ck, u64 ccap,
@@ -55,20 +100,31 @@ __device__ __forceinline__ u32 word_count(u64 word, int csh, const u64* __restri
 }
 
 // One block per listed context c = ids[b] (with more than kth pairs): thr[c] = the kth largest score rank_score(pair
-// key, count) among its packed words (w sorted by pair key; its range from its record), by a radix select over the
-// 48-bit scores, 12 bits per round (256 threads: 16 bins each).
+// key, count) among its packed words, by a radix select over the 48-bit scores, 12 bits per round (256 threads: 16
+// bins each). Its words: w sorted by pair key, its range from its record (gstart NULL); or w grouped by context into
+// partitions of 2^ibits ids (gstart their starts), the words of c's partition whose context is c. m_dev (may be NULL):
+// a device-side count of the listed ids (the first min(m, *m_dev) are taken).
 __global__ void __launch_bounds__(256) ctx_kth_k(const u64* __restrict__ w, int cb, const u64* __restrict__ esc_k,
                                                  const u32* __restrict__ esc_c, u64 esc_cap, const u32* __restrict__ rec,
-                                                 const i64* __restrict__ ids, i64 m, int kth, u64* __restrict__ thr) {
+                                                 const i64* __restrict__ ids, i64 m, int kth, u64* __restrict__ thr,
+                                                 const i64* __restrict__ gstart, int ibits, const u64* m_dev) {
     __shared__ u32 hist[4096];
     __shared__ u32 s_wave[4];
     __shared__ u64 s_prefix;
     __shared__ u32 s_need;
     const int csh = 48 - cb;
+    if (m_dev && (i64)*m_dev < m) m = (i64)*m_dev;
     for (i64 b = blockIdx.x; b < m; b += gridDim.x) {
         const i64 c = ids[b];
-        const u32* r = rec + c * Rec8::WORDS;
-        const i64 a = (i64)rec_first(r), e = a + r[1];
+        i64 a, e;
+        if (gstart) {
+            a = gstart[c >> ibits];
+            e = gstart[(c >> ibits) + 1];
+        } else {
+            const u32* r = rec + c * Rec8::WORDS;
+            a = (i64)rec_first(r);
+            e = a + r[1];
+        }
         u64 prefix = 0;       // the selected score's bits above the current round
         u32 need = (u32)kth;  // its rank among the scores matching prefix (1 = the largest)
         for (int round = 0; round < 4; ++round) {
@@ -77,6 +133,7 @@ __global__ void __launch_bounds__(256) ctx_kth_k(const u64* __restrict__ w, int 
             __syncthreads();
             for (i64 j = a + threadIdx.x; j < e; j += blockDim.x) {
                 const u64 wj = w[j];
+                if (gstart && (i64)(wj >> (64 - cb)) != c) continue;
                 const u64 sc = rank_score(wj >> csh, word_count(wj, csh, esc_k, esc_c, esc_cap));
                 if (round == 0 || (sc >> (shift + 12)) == (prefix >> (shift + 12)))
                     atomicAdd(&hist[(sc >> shift) & 0xFFF], 1u);
@@ -173,6 +230,46 @@ __global__ void __launch_bounds__(256) table_query_k(const u16* __restrict__ x, 
     }
 }
 
+// table_query_k over a level counted by the 32-bit count: cnt = the count of (c, tgt[i]) in the level's slabs (the
+// count's per-partition tables, pairs32.h), with the same CNT_TOP rule.
+template <int K>
+__global__ void __launch_bounds__(256) table_query32_k(const u16* __restrict__ x, const int* __restrict__ avail,
+                                                       const u16* __restrict__ tgt, i64 n, int k,
+                                                       const u64* __restrict__ ck, u64 ccap,
+                                                       const u64* __restrict__ slabs, int pbits, int W,
+                                                       const u32* __restrict__ rec, const u64* __restrict__ thr,
+                                                       u32 cnt_top, int kout, int* __restrict__ out_tot,
+                                                       int* __restrict__ out_dist, int* __restrict__ out_cnt,
+                                                       u16* __restrict__ out_tok, u32* __restrict__ out_tcnt) {
+    const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    if (i >= n || avail[i] < ctx_len<K>(k)) return;
+    const i64 c = ctx_find(ck, ccap, qctx_key<K>(x + i + 1, k));
+    if (c < 0) return;
+    u32 v[Rec8::WORDS];
+    const uint4* src = (const uint4*)(rec + c * Rec8::WORDS);
+#pragma unroll
+    for (int q = 0; q < Rec8::WORDS / 4; ++q) {
+        const uint4 t = src[q];
+        v[4 * q] = t.x;
+        v[4 * q + 1] = t.y;
+        v[4 * q + 2] = t.z;
+        v[4 * q + 3] = t.w;
+    }
+    const u32 pairs = v[1];
+    out_tot[i] = (int)v[0];
+    out_dist[i] = (int)(pairs < 65535u ? pairs : 65535u);
+    const u64 want = ((u64)c << 16) | tgt[i];
+    const u32 cnt = p32_pair_count(slabs, pbits, W, want);
+    if (cnt && (pairs <= cnt_top || thr == nullptr || rank_score(want, cnt) >= thr[c])) out_cnt[i] = (int)cnt;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        if (r < kout) {
+            out_tok[i * kout + r] = (u16)(v[2 + r / 2] >> (16 * (r & 1)));
+            out_tcnt[i * kout + r] = v[2 + Rec8::TOKW + r];
+        }
+    }
+}
+
 // Hint rows over a CountTable's levels (count_table.rs query_rows :338-404): per position the deepest described level
 // whose context occurred: cell ((1 + bucket) * 7 + count bin) * 6 + purity bin, its first `entries` next tokens, their
 // weights round_half_even(count / sum of those counts * 65535), and the bucket (level), else 0 / 0 / 0 / -1.
@@ -242,6 +339,23 @@ extern "C" int ng_table_emit(const u16* tok, i64 L, int k, u64* ck, u64 ccap, u6
     return (int)hipGetLastError();
 }
 
+// One level's contexts into ck (ccap slots, EMPTY-filled, ccap <= 2^(W - 16)) and every position's event (one per
+// position p < L whose k tokens before it and p itself hold no gap) in the 32-bit count's scan-region layout: block b
+// of `grid` appends e = wmix(slot << 16 | tok[p], W) to ev[b * region ...] (region >= ng_emit_region(L, grid)), its
+// count to ev_count[b] and its events per top-dbits digit to dhist[d * grid + b] (1 <= dbits <= 10). flags[0] bit 1:
+// the context table is full (rerun bigger; the events are then incomplete), bit 2: a region overflowed.
+extern "C" int ng_table_emit32(const u16* tok, i64 L, int k, u64* ck, u64 ccap, int W, int dbits, u64* ev, u64 region,
+                               u32* ev_count, u32* dhist, u32* flags, int grid, void* stream) {
+    if (ccap == 0 || ccap > (1ull << 31) || W < 17 || W > 48 || ccap > (1ull << (W - 16)) || dbits < 1 || dbits > 10 ||
+        region == 0 || grid <= 0 || ev_count == nullptr || dhist == nullptr)
+        return -1;
+    if (L <= 0) L = 0;
+    hipStream_t st = (hipStream_t)stream;
+    LEVEL_DISPATCH(k, (table_emit32_k<K><<<grid, 256, 0, st>>>(tok, L, k, ck, ccap, W, dbits, ev, region, ev_count,
+                                                                dhist, flags)));
+    return (int)hipGetLastError();
+}
+
 // Per key (EMPTY: no context): its slot in the context table, or -1.
 extern "C" int ng_table_lookup(const u64* keys, i64 n, const u64* ck, u64 ccap, int* slot, void* stream) {
     if (n > 0) table_lookup_k<<<grid_for(n, 256), 256, 0, (hipStream_t)stream>>>(keys, n, ck, ccap, slot);
@@ -256,7 +370,22 @@ extern "C" int ng_ctx_kth(const u64* w, int cb, const u64* esc_k, const u32* esc
     if (kth < 1 || cb <= 0 || cb > 44 || esc_cap == 0) return -1;
     if (m > 0) {
         const int g = m < 65536 ? (int)m : 65536;
-        ctx_kth_k<<<g, 256, 0, (hipStream_t)stream>>>(w, cb, esc_k, esc_c, esc_cap, rec, ids, m, kth, thr);
+        ctx_kth_k<<<g, 256, 0, (hipStream_t)stream>>>(w, cb, esc_k, esc_c, esc_cap, rec, ids, m, kth, thr, nullptr, 0,
+                                                      nullptr);
+    }
+    return (int)hipGetLastError();
+}
+
+// ng_ctx_kth over words grouped by context (ng_ctx_agg's input: partitions of 2^ibits ids, gstart their starts) for
+// the first min(m, *m_dev) listed ids (m_dev may be NULL).
+extern "C" int ng_ctx_kth_grouped(const u64* w, const i64* gstart, int ibits, int cb, const u64* esc_k,
+                                  const u32* esc_c, u64 esc_cap, const i64* ids, i64 m, const u64* m_dev, int kth,
+                                  u64* thr, void* stream) {
+    if (kth < 1 || cb <= 0 || cb > 44 || esc_cap == 0 || gstart == nullptr || ibits < 0 || ibits > 11) return -1;
+    if (m > 0) {
+        const int g = m < 65536 ? (int)m : 65536;
+        ctx_kth_k<<<g, 256, 0, (hipStream_t)stream>>>(w, cb, esc_k, esc_c, esc_cap, nullptr, ids, m, kth, thr, gstart,
+                                                      ibits, m_dev);
     }
     return (int)hipGetLastError();
 }
@@ -277,6 +406,24 @@ extern "C" int ng_table_query(const u16* x, const int* avail, const u16* tgt, i6
     LEVEL_DISPATCH(k, (table_query_k<K><<<grid_for(n, 256), 256, 0, st>>>(x, avail, tgt, n, k, ck, ccap, w, cb, esc_k,
                                                                          esc_c, esc_cap, rec, thr, cnt_top, kout,
                                                                          out_tot, out_dist, out_cnt, out_tok, out_tcnt)));
+    return (int)hipGetLastError();
+}
+
+// ng_table_query over a level counted by the 32-bit count: cnt from its slabs (2^pbits partitions of 14336 slots,
+// pair keys below 2^W, ng_part_count32's slab output) instead of a search of sorted words.
+extern "C" int ng_table_query32(const u16* x, const int* avail, const u16* tgt, i64 n, int k, const u64* ck, u64 ccap,
+                                const u64* slabs, int pbits, int W, const u32* rec, const u64* thr, u32 cnt_top,
+                                int kout, int* out_tot, int* out_dist, int* out_cnt, u16* out_tok, u32* out_tcnt,
+                                void* stream) {
+    if (kout < 0 || kout > 8 || ccap == 0 || slabs == nullptr || pbits < 1 || W < 17 || W > 63 || W - pbits < 1 ||
+        W - pbits > 31)
+        return -1;
+    if (kout > 0 && (out_tok == nullptr || out_tcnt == nullptr)) return -1;
+    if (n <= 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    LEVEL_DISPATCH(k, (table_query32_k<K><<<grid_for(n, 256), 256, 0, st>>>(x, avail, tgt, n, k, ck, ccap, slabs, pbits,
+                                                                           W, rec, thr, cnt_top, kout, out_tot,
+                                                                           out_dist, out_cnt, out_tok, out_tcnt)));
     return (int)hipGetLastError();
 }
 

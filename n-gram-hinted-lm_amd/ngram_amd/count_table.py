@@ -12,13 +12,15 @@ context's top CNT_TOP = 1024 next tokens by count descending then token ascendin
 0 where the context is invalid or never occurred. Keys: packed tokens for k <= 4 (exact), a 64-bit polynomial hash
 beyond (count_table.rs:11-14: ~2^-64 per pair of contexts to merge).
 
-GPU layout per level (libngram_amd.so: ng_table_emit, the partitioned count of partcount.py, ng_ctx_summary,
-ng_ctx_kth, ng_table_query, ng_table_lookup, ng_pos_rows): the context table (u64 keys, slot = context id), the level's
-distinct pairs as packed words (pair key << (48 - cb) | count, larger counts in an escape table) sorted by pair key,
-one 64-byte record per present context (total, pairs, top 8 tokens and counts, its first word) and the CNT_TOP
-threshold of contexts with more pairs than that. The build writes one event per corpus position and counts them
-without global atomics; a query reads its context's record and binary-searches its target among the context's
-words."""
+GPU layout per level (libngram_amd.so: ng_table_emit32, the 32-bit count of partcount.count32 (pairs32.hip),
+ng_ctx_kth_grouped, ng_table_query32, ng_table_lookup, ng_pos_rows): the context table (u64 keys, slot = context id),
+the count's per-partition pair tables kept as slabs (2^pbits partitions of the W-bit pair hash wmix(context id << 16
+| token, W), W = context-id bits + 16; 14336 u64 slots count << 32 | key each), one 64-byte record per present context
+(total, pairs, top 8 tokens and counts) and the CNT_TOP threshold of contexts with more pairs than that. The build
+inserts every corpus position's context and appends its event to its block's region (one LDS cursor per block), then
+counts the events without global atomics (two grouping passes, an LDS table per partition) and makes the records
+from the distinct pairs grouped by context; a query reads its context's record and looks its pair up in the slab of
+the pair's partition."""
 
 from __future__ import annotations
 
@@ -37,6 +39,9 @@ CNT_TOP = 1024
 TOPE = 8
 COUNTS = (2, 3, 5, 9, 17, 33)
 PURITIES = (0.3, 0.5, 0.7, 0.85, 0.95)
+EMIT_BLOCKS_PER_CU = 16  # the emitting inserts' blocks (256 threads) per compute unit: their regions are the count's
+# first-pass segments, so fewer blocks give longer segments
+CTX_MARGIN = 1.25  # a level's context table sized from the last build's contexts holds this many times them at LOAD
 LOAD = 0.5  # context-table load factor of the level's bound on contexts (measured: 0.7 and 0.35 are slower)
 
 
@@ -53,13 +58,15 @@ def _segments_device(x: torch.Tensor, lib: Lib) -> torch.Tensor:
 
 
 class _Level:
-    """One built level on the GPU: context table ck (ccap slots), packed words w (U, sorted by pair key; cb context
-    bits; escape table esc), records rec [ccap, 16] (valid for present contexts), CNT_TOP thresholds thr (None when no
-    context has more pairs), counts of contexts and pairs."""
+    """One built level on the GPU: context table ck (ccap slots), the count's slabs (2^pbits partitions of W-bit pair
+    hashes), records rec [ccap, 16] (valid for present contexts), CNT_TOP thresholds thr (None when no context has more
+    pairs), the packed words' context bits cb and escape table esc (the records' large counts), counts of contexts and
+    pairs."""
 
-    def __init__(self, k, ck, ccap, w, U, cb, esc, rec, thr, contexts):
+    def __init__(self, k, ck, ccap, slab, pbits, W, U, cb, esc, rec, thr, contexts):
         self.k, self.ck, self.ccap = k, ck, ccap
-        self.w, self.pairs, self.cb, self.esc = w, U, cb, esc
+        self.slab, self.pbits, self.W = slab, pbits, W
+        self.pairs, self.cb, self.esc = U, cb, esc
         self.rec, self.thr, self.contexts = rec, thr, contexts
 
 
@@ -101,24 +108,37 @@ class CountTable:
         self._tokens = int(sum(self.sizes_))
         self.tables: list[_Level] = []
         self.built = self.released = False
-        self.grid = torch.cuda.get_device_properties(dev).multi_processor_count * 32
+        self.grid = torch.cuda.get_device_properties(dev).multi_processor_count * EMIT_BLOCKS_PER_CU
         self.events: list = []
         torch.cuda.synchronize(dev)
         return self
 
     @classmethod
-    def from_device(cls, tok: torch.Tensor, sizes: list[int], starts: list[int], levels: list[int]) -> "CountTable":
-        """A table over shards already laid out in GPU memory (`tok` int16 with SENT gaps at layout()'s starts)."""
+    def from_device(cls, tok: torch.Tensor, sizes: list[int], starts: list[int], levels: list[int],
+                    sizing: dict | None = None) -> "CountTable":
+        """A table over shards already laid out in GPU memory (`tok` int16 with SENT gaps at layout()'s starts).
+        `sizing`: another table's `sizing` (the contexts per occurrence and distinct pairs per event it found per
+        level), so that this build sizes its context tables and partitions from them at once; without it the first
+        build sizes from the occurrences alone (a table found too small is built again bigger)."""
         self = object.__new__(CountTable)
+        if sizing:
+            self.ratio = dict(sizing.get("pairs_per_event", {}))
+            self.cratio = dict(sizing.get("contexts_per_occurrence", {}))
         self.lib = Lib()
         self._levels = list(levels)
         self.sizes_, self.starts, self.L = list(sizes), list(starts), int(tok.numel())
         self.tok = tok
         self._tokens = int(sum(sizes))
         self.tables, self.built, self.released = [], False, False
-        self.grid = torch.cuda.get_device_properties(tok.device).multi_processor_count * 32
+        self.grid = torch.cuda.get_device_properties(tok.device).multi_processor_count * EMIT_BLOCKS_PER_CU
         self.events = []
         return self
+
+    @property
+    def sizing(self) -> dict:
+        """What this table's build found per level, for another table over the same shards (from_device's sizing)."""
+        return {"pairs_per_event": dict(getattr(self, "ratio", {})),
+                "contexts_per_occurrence": dict(getattr(self, "cratio", {}))}
 
     @property
     def levels(self) -> list[int]:
@@ -136,6 +156,7 @@ class CountTable:
         self.reruns = {}
         if not hasattr(self, "ratio"):
             self.ratio = {}
+            self.cratio = {}
         for k in self._levels:
             self.tables.append(self._build_level(k))
 
@@ -146,48 +167,72 @@ class CountTable:
 
     def _build_level(self, k: int) -> _Level:
         lib, dev = self.lib, self.tok.device
-        n_k = sum(max(0, n - k) for n in self.sizes_)  # occurrences: an upper bound of contexts and of pairs
+        n_k = sum(max(0, n - k) for n in self.sizes_)  # occurrences: an upper bound of contexts, pairs and events
         bound = n_k
         prev = self.tables[-1] if self.tables else None
         if prev is not None and prev.k == k - 1:
             bound = min(bound, prev.pairs)  # a k-context is a (k-1)-context with its next token: one of its pairs
+        if k in self.cratio:  # the last build's contexts per occurrence, with a margin (a full table reruns bigger)
+            bound = min(bound, int(self.cratio[k] * n_k * CTX_MARGIN) + 1)
         ccap = max(1 << 16, int(bound / LOAD) + 1)
+        G = self.grid
+        R = -(-max(self.L, 1) // (G * 256)) * 256  # a block's positions at most: its events at most
         reruns = 0
-        ev = torch.empty(max(self.L, 1), dtype=torch.int64, device=dev)
         while True:
             if ccap > 1 << 31:
                 raise RuntimeError(f"k={k}: {n_k} occurrences need more than 2^31 context slots")
+            _, W = P.w_bits(ccap)
+            d1 = P.first_digit(W)
             ck = torch.full((ccap,), -1, dtype=torch.int64, device=dev)
-            flags = torch.zeros(1, dtype=torch.int32, device=dev)
+            flags = torch.zeros(2, dtype=torch.int32, device=dev)
+            regions = torch.empty(G * R, dtype=torch.int64, device=dev)
+            ev_count = torch.empty(G, dtype=torch.int32, device=dev)
+            dhist = torch.empty((1 << d1) * G, dtype=torch.int32, device=dev)
             e0, e1 = self._timed("table_emit", k)
             e0.record()
-            lib("ng_table_emit", self.tok, self.L, i32(k), ck, u64(ccap), ev, flags, i32(self.grid))
+            lib("ng_table_emit32", self.tok, self.L, i32(k), ck, u64(ccap), i32(W), i32(d1), regions, u64(R), ev_count,
+                dhist, flags, i32(G))
             e1.record()
-            if int(flags[0].item()) == 0:
+            f = int(flags[0].item())
+            if f == 0:
                 break
+            if f & 4:
+                raise RuntimeError(f"k={k}: an emit region overflowed")
             reruns += 1
             ccap = min(2 * ccap, 1 << 31)
-            del ck
-        self.reruns[k] = reruns
+            del ck, regions
         ev_name = lambda name, n: self._timed(name, k)
-        c = P.count_events(lib, lib, ev, self.L, ccap, self.ratio.get(k, 1.0), None, True, ev_name, presort="pair")
-        del ev
-        self.ratio[k] = max(c.U, 1) / max(self.L, 1)
-        if not c.cb:
+        seg = (regions, R, ev_count, dhist, G, flags)
+        min_pbits = 0
+        while True:
+            c = P.count32(lib, seg, ccap, TOPE, None, n_k, self.ratio.get(k, 1.0), ev_name, min_pbits, slabs=True,
+                          deep_min=CNT_TOP, with_dist=False, agg_grid=self.grid // EMIT_BLOCKS_PER_CU * 2)
+            st = torch.cat([c.stat, c.deep_n]).cpu().tolist()  # one host read: totals, flags, deep contexts
+            if int(st[2]) & 1 and c.pbits < P.pbits32_max(ccap):  # a partition overfull: count with a bit more
+                min_pbits = c.pbits + 1
+                reruns += 1
+                continue
+            break
+        del regions, seg
+        if int(st[2]) & 1:
+            raise RuntimeError(f"k={k}: a partition holds too many distinct pairs at {c.pbits} bits")
+        if int(st[2]) & 2:
             raise RuntimeError(f"k={k}: more large counts than the escape table holds")
-        sm = P.summarize(lib, lib, c, ccap, TOPE, False, ev_name, by_pair=True, with_dist=False, deep_min=CNT_TOP)
-        c.pairs = None
-        rec, w = sm.rec, sm.words
+        if int(st[2]) & 4:
+            raise RuntimeError(f"k={k}: a total does not fit uint32")
+        self.reruns[k] = reruns
+        n_ev, U, m, contexts = int(st[0]), int(st[1]), int(st[6]), int(st[7])
+        self.ratio[k] = max(U, 1) / max(n_ev, 1)
+        self.cratio[k] = contexts / max(n_k, 1)
         thr = None
-        if sm.deep.numel():
+        if m:
             thr = torch.empty(ccap, dtype=torch.int64, device=dev)
             e0, e1 = self._timed("ctx_kth", k)
             e0.record()
-            lib("ng_ctx_kth", w, i32(c.cb), c.esc[0], c.esc[1], u64(P.ESC_CAP), rec, sm.deep, sm.deep.numel(),
-                i32(CNT_TOP), thr)
+            lib("ng_ctx_kth_grouped", c.words, c.wstart, i32(c.ibits), i32(c.cb), c.esc[0], c.esc[1], u64(P.ESC_CAP),
+                c.deep, m, None, i32(CNT_TOP), thr)
             e1.record()
-        contexts = sm.contexts
-        return _Level(k, ck, ccap, w, c.U, c.cb, c.esc, rec, thr, contexts)
+        return _Level(k, ck, ccap, c.slab, c.pbits, c.W, U, c.cb, c.esc, c.rec, thr, contexts)
 
     def _check(self):
         if not self.built or self.released or len(self.tables) != len(self._levels):
@@ -226,9 +271,9 @@ class CountTable:
         for li, lv in enumerate(self.tables):
             e0, e1 = self._timed("query", lv.k)
             e0.record()
-            self.lib("ng_table_query", x, avail, tgt, n, i32(lv.k), lv.ck, u64(lv.ccap), lv.w, i32(lv.cb), lv.esc[0],
-                     lv.esc[1], u64(P.ESC_CAP), lv.rec, lv.thr if top == CNT_TOP else None, ctypes.c_uint32(CNT_TOP),
-                     i32(topk), out[0, li], out[1, li], out[2, li], res["top_tok"][li] if topk else None,
+            self.lib("ng_table_query32", x, avail, tgt, n, i32(lv.k), lv.ck, u64(lv.ccap), lv.slab, i32(lv.pbits),
+                     i32(lv.W), lv.rec, lv.thr if top == CNT_TOP else None, ctypes.c_uint32(CNT_TOP), i32(topk),
+                     out[0, li], out[1, li], out[2, li], res["top_tok"][li] if topk else None,
                      res["top_cnt"][li] if topk else None)
             e1.record()
         return res
@@ -300,7 +345,7 @@ class CountTable:
         """Per level (as built): (k, contexts, pairs, bytes held on the GPU)."""
         out = []
         for lv in self.tables:
-            held = (lv.ck, lv.w, lv.rec, lv.esc[0], lv.esc[1]) + ((lv.thr,) if lv.thr is not None else ())
+            held = (lv.ck, lv.slab, lv.rec, lv.esc[0], lv.esc[1]) + ((lv.thr,) if lv.thr is not None else ())
             b = sum(t.numel() * t.element_size() for t in held)
             out.append((lv.k, lv.contexts, lv.pairs, b))
         return out

@@ -262,12 +262,14 @@ def count_events(elib: Lib, lib: Lib, ev: torch.Tensor | None, n_ev: int, n_ids:
 
 RECORD_WORDS = {1: 4, 2: 8, 4: 8, 8: 16}  # u32 words of a context record for top 1, 2, 4, 8
 
+P32_SLOTS = 14336  # slots of the 32-bit count's per-partition table (pairs32.h), the size of a partition's slab
 P32_TARGET = 6144  # distinct pairs per partition aimed at by the 32-bit count (its LDS table takes up to 11000)
 P32_LIMIT = 11000  # distinct pairs at which the 32-bit count declares a partition overfull (at most 11000)
 PACK32_MIN_BITS = 0  # context bits of the 32-bit count's packed words at least this (a narrower count field)
 AGG_ID_BITS = 11  # context ids per group of words whose records ng_ctx_agg makes in one block: at most 2^11
-W_MAX = 42  # the widest pair key (context-id bits + 16) the 32-bit count takes: its first pass's digit is at most 10
-            # bits (the emitting scan's histogram) and must leave at most 32 bits below it
+W_MAX = 42  # the widest pair key (context-id bits + 16) the 32-bit count narrows in its first pass: that pass's digit
+            # is at most 10 bits (the emitting scan's histogram) and must leave at most 32 bits below it
+W_WIDE = 47  # the widest it takes at all (wider ones are narrowed by the second pass; context ids below 2^31)
 
 
 def w_bits(n_ids: int) -> tuple[int, int]:
@@ -277,8 +279,9 @@ def w_bits(n_ids: int) -> tuple[int, int]:
 
 
 def first_digit(W: int) -> int:
-    """The 32-bit count's first-pass digit width for W-bit pair keys: at least 8, and at most 32 bits below it."""
-    return max(8, W - 32)
+    """The 32-bit count's first-pass digit width for W-bit pair keys: at least 8, and at most 32 bits below it (at most
+    10 bits: wider keys keep 64 bits through the first pass)."""
+    return min(max(8, W - 32), 10)
 
 
 @dataclass
@@ -291,12 +294,19 @@ class Counted32:
     escape table full, bit 2: a total reached 2^32; bit 2 of the scan's: a region overflowed)."""
 
     rec: torch.Tensor
-    dist: torch.Tensor
+    dist: torch.Tensor | None
     qcnt: torch.Tensor | None
     stat: torch.Tensor
     pbits: int
     cb: int
     esc: tuple
+    W: int = 0
+    slab: torch.Tensor | None = None  # with slabs: the count's per-partition tables (pairs32.h), [2^pbits * 14336]
+    words: torch.Tensor | None = None  # with deep_min: the words grouped by context (ng_ctx_agg's input) ...
+    wstart: torch.Tensor | None = None  # ... their groups' starts (groups of 2^ibits ids)
+    ibits: int = 0
+    deep: torch.Tensor | None = None  # with deep_min: the contexts of more than deep_min pairs (the first deep_n)
+    deep_n: torch.Tensor | None = None  # int64 [2] on the device: the deep contexts, the present contexts
 
 
 def pbits32_max(n_ids: int) -> int:
@@ -306,18 +316,26 @@ def pbits32_max(n_ids: int) -> int:
 
 
 def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None, n_events: int | None,
-            ratio: float = 1.0, event=_no_event, min_pbits: int = 0) -> Counted32:
+            ratio: float = 1.0, event=_no_event, min_pbits: int = 0, slabs: bool = False,
+            deep_min: int | None = None, with_dist: bool = True, agg_grid: int = 0) -> Counted32:
     """Count a level's events emitted by ng_scan_emit in the W-bit mode (wbits = W = w_bits(n_ids)[1], dbits =
     first_digit(W); seg = (regions, R, ev_count, dhist, nseg, scan flags)) and make every present context's record
     (top ktop) without a host read: the passes and the count of pairs32.hip. `n_events`: the level's events (the last
     build's; None: read from the device here, one host sync), which with `ratio` (distinct pairs per event) sizes the
     partitions, with at least min_pbits partition bits (and at most pbits32_max(n_ids)); `lookups` as count_events',
-    and optionally a fourth entry: a device-side count (int64 [1]) of the listed positions, at most their number."""
+    and optionally a fourth entry: a device-side count (int64 [1]) of the listed positions, at most their number.
+    Events wider than W_MAX bits (first digit 10 bits, so more than 32 bits below it) keep 64 bits through the first
+    pass and are narrowed by the second (ng_msd_pass_narrow). `slabs`: also keep the count's per-partition tables
+    (Counted32.slab) for queries after the build; `deep_min`: keep the words grouped by context and list the contexts
+    of more than deep_min pairs (for their CNT_TOP thresholds, ng_ctx_kth_grouped). Without with_dist, dist is None
+    (the records hold each present context's pairs). agg_grid: ng_ctx_agg's blocks (0: one per group of ids; a couple
+    per compute unit for many light groups, each block then walking its groups with the next one's words loaded
+    ahead)."""
     regions, R, ev_count, dhist, nseg, scan_flags = seg
     dev = regions.device
     idb, W = w_bits(n_ids)
     cb = max(idb, PACK32_MIN_BITS)  # the words' context field: idb bits used, cb - idb zero bits above them
-    if W > W_MAX:
+    if W > W_WIDE:
         raise ValueError(f"{n_ids} context ids: wider than the 32-bit count takes")
     d1 = first_digit(W)
     cap = nseg * R
@@ -331,19 +349,25 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
     stat[5:6].copy_(scan_flags[1:2])
     if n_events is None:
         n_events = int(ev_tot.item())
-    pbits = max(d1 + 1, PART_MIN_BITS if lookups is not None else 0, min_pbits,
+    pbits = max(d1 + 1, W - 31, PART_MIN_BITS if lookups is not None else 0, min_pbits,
                 math.ceil(math.log2(max(1.0, n_events * ratio / P32_TARGET))))
     pbits = min(pbits, pbits32_max(n_ids))
     d2 = pbits - d1
     e0, e1 = event("partition", cap)
     e0.record()
-    ev32 = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
-    elib("ng_seg_scatter_narrow", regions, u64(R), None, ev_count, dpre, nseg, i32(W - d1), i32(d1), ev32, u64(cap))
     ev32b = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
     P = 1 << pbits
     start = torch.empty(P + 1, dtype=torch.int64, device=dev)
-    elib.cub("ng_msd_pass", ev32, dpre, nseg, i32(d1), ev_tot, u64(cap), i32(W - pbits), i32(d2), ev32b, start)
-    del ev32, dpre
+    if W <= W_MAX:
+        ev1 = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
+        elib("ng_seg_scatter_narrow", regions, u64(R), None, ev_count, dpre, nseg, i32(W - d1), i32(d1), ev1, u64(cap))
+        elib.cub("ng_msd_pass", ev1, dpre, nseg, i32(d1), ev_tot, u64(cap), i32(W - pbits), i32(d2), ev32b, start)
+    else:  # wide keys: 64 bits through the first pass, narrowed by the second
+        ev1 = torch.empty(max(cap, 1), dtype=torch.int64, device=dev)
+        elib("ng_seg_scatter", regions, u64(R), None, ev_count, dpre, nseg, i32(W - d1), i32(d1), ev1, u64(cap))
+        elib.cub("ng_msd_pass_narrow", ev1, dpre, nseg, i32(d1), ev_tot, u64(cap), i32(W - pbits), i32(d2), ev32b,
+                 start)
+    del ev1, dpre
     N = nq = 0
     sqk = sqv = None
     qstart = torch.zeros(P + 1, dtype=torch.int64, device=dev)
@@ -372,11 +396,12 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
     seg_base = torch.empty(G2, dtype=torch.int64, device=dev)
     qcnt = torch.zeros(max(N, 1), dtype=torch.int32, device=dev) if N else None
     dh2 = torch.empty((1 << dc) * G2, dtype=torch.int32, device=dev)
+    slab = torch.empty(P * P32_SLOTS, dtype=torch.int64, device=dev) if slabs else None
     e0, e1 = event("count", cap)
     e0.record()
     elib("ng_part_count32", ev32b, start, i32(pbits), i32(W), sqk, sqv, qstart, out_k, i32(cb), esc_k, esc_c,
          u64(ESC_CAP), seg_cnt, seg_base, qcnt, dh2, i32(dtop - dc), i32(dc), ctypes.c_uint32(P32_LIMIT), flags,
-         i32(G2))
+         i32(G2), slab)
     e1.record()
     del ev32b, start, sqk, sqv, qstart
     # the words grouped by context: by their top dc bits (ng_seg_scatter), then within those groups by the next d2
@@ -400,13 +425,20 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
     e1.record()
     del out_k, dh2, seg_cnt, seg_base, dpre2
     rec = torch.empty((max(n_ids, 1), RECORD_WORDS[ktop]), dtype=torch.int32, device=dev)
-    dist = torch.empty(max(n_ids, 1), dtype=torch.int32, device=dev)
+    dist = torch.empty(max(n_ids, 1), dtype=torch.int32, device=dev) if with_dist else None
+    deep = deep_n = None
+    if deep_min is not None:  # at most (pairs) / (deep_min + 1) contexts have more than deep_min pairs
+        deep = torch.empty(cap // (deep_min + 1) + 1, dtype=torch.int64, device=dev)
+        deep_n = torch.zeros(2, dtype=torch.int64, device=dev)  # the deep contexts, the present contexts
     e0, e1 = event("ctx_topk", cap)
     e0.record()
     elib("ng_ctx_agg", words, start2, P2, i32(ibits), i32(cb), n_ids, esc_k, esc_c, u64(ESC_CAP), i32(ktop), rec,
-         dist, flags)
+         dist, flags, ctypes.c_uint32(deep_min or 0), deep, u64(deep.numel() if deep is not None else 0), deep_n,
+         deep_n[1:] if deep_n is not None else None, i32(agg_grid))
     e1.record()
-    return Counted32(rec, dist, qcnt, stat, pbits, cb, (esc_k, esc_c))
+    keep = deep_min is not None
+    return Counted32(rec, dist, qcnt, stat, pbits, cb, (esc_k, esc_c), W, slab, words if keep else None,
+                     start2 if keep else None, ibits, deep, deep_n)
 
 
 

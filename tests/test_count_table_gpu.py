@@ -115,10 +115,11 @@ def test_overflow_reruns(corpus, reference, monkeypatch):
 
 def test_escaped_counts(corpus, reference, monkeypatch):
     """Packed words with a 4-bit count field (context bits forced to 44): every count of 15 or more lives in the
-    escape table, for the summary's totals and tops, the CNT_TOP thresholds and the queries' binary searches."""
+    escape table, for the records' totals and tops and the CNT_TOP thresholds (the queries' counts come from the
+    slabs, which hold them whole)."""
     from ngram_amd import partcount as P
 
-    monkeypatch.setattr(P, "PACK_MIN_BITS", 44)
+    monkeypatch.setattr(P, "PACK32_MIN_BITS", 44)
     ct = CountTable.create(corpus.shards(), [1, 3], 1, [])
     ct.build()
     assert all(lv.cb == 44 for lv in ct.tables)
