@@ -403,15 +403,17 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
 }
 
 // Per context from packed words grouped by context: partition q (words [start[q], start[q + 1])) holds the
-// contexts of ids [q << ibits, (q + 1) << ibits), 2^ibits <= AGG_IDS. A block per partition (grid-stride) streams
-// its words once, accumulating per id its total, its pairs and its top KT scores (count << 16 | 65535 - token) in
-// LDS. The top scores come from a cascade of atomic maxima: a score displaced from (or kept out of) slot r goes on to
+// contexts of ids [q << ibits, (q + 1) << ibits), 2^ibits <= AGG_IDS_FOR(KT). A block takes partitions q, q + grid,
+// ... in turn and streams each one's words once, accumulating per id its total, its pairs and its top KT scores
+// (count << 16 | 65535 - token) in LDS. The top scores come from a cascade of atomic maxima: a score displaced from (or kept out of) slot r goes on to
 // slot r + 1, so slot r ends with the r-th largest; a score not above slot KT - 1's current value (which only grows,
 // and below which KT larger scores already exist) is not inserted. Then every id of the partition below n_ids gets
 // dist[c] = its pairs and, if present, its record (CtxRecord<KT>, first-word index 0); with `deep`, every context of
 // more than deep_min pairs is appended to deep (*deep_n counts them). flags[0] bit 2: a total reached 2^32.
 #define AGG_BLOCK 1024
 #define AGG_IDS 2048
+// the ids of a partition at most for top KT: 1024 for KT 8, so that its LDS (72 KB) lets two blocks share a CU
+#define AGG_IDS_FOR(KT) ((KT) >= 8 ? AGG_IDS / 2 : AGG_IDS)
 // Two blocks share a compute unit where the LDS allows (KT <= 4: 80 KB each): 8 waves per SIMD, so at most 96
 // scalar registers a wave (amdgpu_waves_per_eu), which the kernel's arguments and walk state would otherwise exceed.
 template <int KT>
@@ -421,8 +423,8 @@ __global__ void __launch_bounds__(AGG_BLOCK) __attribute__((amdgpu_waves_per_eu(
                                                        u64 esc_cap, u32* __restrict__ rec, u32* __restrict__ dist,
                                                        u32* flags, u32 deep_min, i64* __restrict__ deep,
                                                        u64 deep_cap, u64* deep_n, u64* present) {
-    __shared__ u32 s_tot[AGG_IDS], s_dist[AGG_IDS];
-    __shared__ u64 s_top[AGG_IDS * KT];
+    __shared__ u32 s_tot[AGG_IDS_FOR(KT)], s_dist[AGG_IDS_FOR(KT)];
+    __shared__ u64 s_top[AGG_IDS_FOR(KT) * KT];
     const int t = threadIdx.x, lane = lane_id();
     const int sh = 64 - cb, csh = 48 - cb;
     const u64 esc = (1ull << csh) - 1;
@@ -691,7 +693,8 @@ extern "C" int ng_part_count32(const u32* ev, const i64* start, int pbits, int W
 extern "C" int ng_ctx_agg(const u64* w, const i64* start, i64 P, int ibits, int cb, i64 n_ids, const u64* esc_k,
                           const u32* esc_c, u64 esc_cap, int topk, u32* rec, u32* dist, u32* flags, u32 deep_min,
                           i64* deep, u64 deep_cap, u64* deep_n, u64* present, int grid, void* stream) {
-    if (cb < 1 || cb > 44 || ibits < 0 || (1 << ibits) > AGG_IDS || P <= 0 || esc_cap == 0 || n_ids < 0 ||
+    if (cb < 1 || cb > 44 || ibits < 0 || (1 << ibits) > (topk >= 8 ? AGG_IDS_FOR(8) : AGG_IDS) || P <= 0 ||
+        esc_cap == 0 || n_ids < 0 ||
         n_ids > (1ll << cb) || (P << ibits) < n_ids || (deep && !deep_n))
         return -1;
     if (n_ids == 0) return 0;

@@ -266,7 +266,8 @@ P32_SLOTS = 14336  # slots of the 32-bit count's per-partition table (pairs32.h)
 P32_TARGET = 6144  # distinct pairs per partition aimed at by the 32-bit count (its LDS table takes up to 11000)
 P32_LIMIT = 11000  # distinct pairs at which the 32-bit count declares a partition overfull (at most 11000)
 PACK32_MIN_BITS = 0  # context bits of the 32-bit count's packed words at least this (a narrower count field)
-AGG_ID_BITS = 11  # context ids per group of words whose records ng_ctx_agg makes in one block: at most 2^11
+AGG_ID_BITS = 11  # context ids per group of words whose records ng_ctx_agg makes in one block: at most 2^11 (2^10 for
+                  # top 8, whose LDS then lets two blocks share a compute unit)
 W_MAX = 42  # the widest pair key (context-id bits + 16) the 32-bit count narrows in its first pass: that pass's digit
             # is at most 10 bits (the emitting scan's histogram) and must leave at most 32 bits below it
 W_WIDE = 47  # the widest it takes at all (wider ones are narrowed by the second pass; context ids below 2^31)
@@ -406,7 +407,7 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
     del ev32b, start, sqk, sqv, qstart
     # the words grouped by context: by their top dc bits (ng_seg_scatter), then within those groups by the next d2
     # bits (ng_msd_pass64), so that a group holds at most 2^11 ids, whose records ng_ctx_agg makes in LDS
-    d2 = max(0, idb - dc - AGG_ID_BITS)
+    d2 = max(0, idb - dc - (AGG_ID_BITS - 1 if ktop >= 8 else AGG_ID_BITS))  # top 8: 2^10 ids a group
     ibits = idb - dc - d2
     P2 = 1 << (dc + d2)
     dpre2 = torch.empty((1 << dc) * G2, dtype=torch.int32, device=dev)
