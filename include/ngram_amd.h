@@ -284,6 +284,9 @@ int ng_ctx_agg(const ng_u64* w, const ng_i64* start, ng_i64 P, int ibits, int cb
                const uint32_t* esc_c, ng_u64 esc_cap, int topk, uint32_t* rec, uint32_t* dist, uint32_t* flags,
                uint32_t deep_min, ng_i64* deep, ng_u64 deep_cap, ng_u64* deep_n, ng_u64* present, int grid,
                void* stream);
+/* n words of value v (the hosts' buffer fills, on the caller's stream) */
+int ng_fill_u32(uint32_t* p, ng_i64 n, uint32_t v, void* stream);
+int ng_fill_u64(ng_u64* p, ng_i64 n, ng_u64 v, void* stream);
 /* exclusive prefix sum of n u32 (out may alias in), *total (may be NULL) the sum; CUB-style two-phase temp storage */
 int ng_exclusive_scan_u32(void* temp, size_t* temp_bytes, const uint32_t* in, uint32_t* out, ng_i64 n,
                           ng_u64* total, void* stream);

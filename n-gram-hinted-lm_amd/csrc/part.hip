@@ -594,6 +594,17 @@ extern "C" int ng_part_bounds(const u64* ev, i64 n, int pbits, int msd, i64* sta
     return (int)hipGetLastError();
 }
 
+// Buffer fills on the caller's stream (the hosts' zeroed and EMPTY-filled buffers, so that no framework kernel runs
+// inside a build): n words of value v.
+extern "C" int ng_fill_u32(u32* p, i64 n, u32 v, void* stream) {
+    if (n < 0 || (n > 0 && p == nullptr)) return -1;
+    return prim::fill_u32(p, v, n, (hipStream_t)stream);
+}
+extern "C" int ng_fill_u64(u64* p, i64 n, u64 v, void* stream) {
+    if (n < 0 || (n > 0 && p == nullptr)) return -1;
+    return prim::fill_u64(p, v, n, (hipStream_t)stream);
+}
+
 // Exclusive prefix sum of n u32 (out may alias in), *total (device, may be NULL) the sum as u64; CUB-style two-phase
 // temp storage (temp NULL: *temp_bytes set).
 extern "C" int ng_exclusive_scan_u32(void* temp, size_t* temp_bytes, const u32* in, u32* out, i64 n, u64* total,

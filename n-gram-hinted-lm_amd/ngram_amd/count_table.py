@@ -221,7 +221,8 @@ class CountTable:
         if int(st[2]) & 4:
             raise RuntimeError(f"k={k}: a total does not fit uint32")
         self.reruns[k] = reruns
-        n_ev, U, m, contexts = int(st[0]), int(st[1]), int(st[6]), int(st[7])
+        ns = c.stat.numel()  # then the deep contexts and the present contexts
+        n_ev, U, m, contexts = int(st[0]), int(st[1]), int(st[ns]), int(st[ns + 1])
         self.ratio[k] = max(U, 1) / max(n_ev, 1)
         self.cratio[k] = contexts / max(n_k, 1)
         thr = None

@@ -108,18 +108,19 @@ class LevelBuild:
         each position's context's first topk entries; `cnt_top`: the TOP rule (cnt only if the target ranks below it);
         `keep`: levels whose records are returned (top-8); `stats`: each level's corpus hits in info."""
         dev, N, elib = self.tok.device, x.numel(), self.elib
+        want_stats = stats
         self.kernel_events = []
         self.grid = torch.cuda.get_device_properties(dev).multi_processor_count * SCAN_BLOCKS_PER_CU
         nwords = self.L // 32
-        bms = {k: torch.zeros(nwords, dtype=torch.int32, device=dev) for k in self.levels}
-        res = LevelOutputs(torch.zeros((3, len(self.levels), N), dtype=torch.int32, device=dev))
+        bms = {k: elib.zeros(nwords, torch.int32, dev) for k in self.levels}
+        res = LevelOutputs(elib.zeros((3, len(self.levels), N), torch.int32, dev))
         self._pre = torch.empty(1, dtype=torch.int32, device=dev)  # the prefix rule's device flag
         elib("ng_avail_closed", avail, N, self._pre)
         if topk:
-            res.top_tok = torch.zeros((len(self.levels), N, topk), dtype=torch.int16, device=dev)
-            res.top_cnt = torch.zeros((len(self.levels), N, topk), dtype=torch.int32, device=dev)
+            res.top_tok = elib.zeros((len(self.levels), N, topk), torch.int16, dev)
+            res.top_cnt = elib.zeros((len(self.levels), N, topk), torch.int32, dev)
         if with_mask:
-            res.mask = torch.zeros(N, dtype=torch.int32, device=dev)
+            res.mask = elib.zeros(N, torch.int32, dev)
         G = self.grid
         R = max([emit_region((n + 31) // 32 * 32, G) for n in self.sizes] or [8192])
         span = self.starts[-1] + (self.sizes[-1] + 31) // 32 * 32 - self.starts[0] if self.sizes else 0
@@ -130,6 +131,9 @@ class LevelBuild:
         deferred = []  # summarize's checks, read once after every level
         checks32 = []  # the 32-bit counts' sizes and flags, likewise
         pending = []  # query indexes sized from the last build's context counts, checked once after every level
+        # every level's device-side results in one tensor, read with one copy after the last level: per level the
+        # 32-bit count's events, pairs and flags, the scan's flags, the listed query positions, the index's counters
+        stats = elib.zeros((len(self.levels), 8), torch.int64, dev)
         for li, k in enumerate(self.levels):
             t0 = time.perf_counter()
             prev = self.levels[li - 1] if li else None
@@ -141,17 +145,18 @@ class LevelBuild:
                     # level; a list that came out longer than its room makes the build run again)
                     seen_cap = min(N, int(self.seen_of[k] * max(SEEN_MARGIN, 1.0)) + 4096)
                     seen = torch.empty(max(seen_cap, 1), dtype=torch.int32, device=dev)
-                    seen_n = torch.empty(1, dtype=torch.int64, device=dev)
+                    seen_n = stats[li, 4:5]
                     elib.cub("ng_select_positive", out[1, li - 1], N, seen, seen_cap, seen_n)
                 else:
                     seen = torch.nonzero(out[1, li - 1] > 0).squeeze(1).to(torch.int32)
                     self.seen_of[k] = int(seen.numel())
             q0, q1 = self._event("qindex", k, N)
             q0.record()
-            vi = QueryIndex(elib, x, avail, k, seen, expect=self.contexts_of.get(k), defer=_defer, n_dev=seen_n)
+            vi = QueryIndex(elib, x, avail, k, seen, expect=self.contexts_of.get(k), defer=_defer, n_dev=seen_n,
+                            counters=stats[li, 5:8])
             q1.record()
             if vi.n is None:
-                pending.append((k, vi.pending))
+                pending.append((li, k))
             else:
                 self.contexts_of[k] = vi.n
             t1 = time.perf_counter()
@@ -163,16 +168,15 @@ class LevelBuild:
             if not use32 and seen_n is not None:  # the 64-bit count takes an exact list: read its length
                 seen = seen[: int(seen_n.item())]
                 seen_n = None
-            seg = self._emit(k, vi, x, bms, regions, R, W if use32 else 0)
+            seg = self._emit(k, vi, x, bms, regions, R, W if use32 else 0,
+                             stats[li, 3:4].view(torch.int32) if use32 else None)
             t2 = time.perf_counter()
             if use32:
                 # the 32-bit count: records made without sorting the pairs, every size read once after the last level
                 c = count32(elib, seg, vi.ids, ktop, (vi.ctx_of, tgt, seen, seen_n), self.events_of.get(k),
-                            self.dratio.get(k, 1.0), ev_fn, self.min_pbits.get(k, 0))
+                            self.dratio.get(k, 1.0), ev_fn, self.min_pbits.get(k, 0), stat=stats[li])
                 del seg
-                if seen_n is not None:
-                    c.stat[4:5].copy_(seen_n)
-                checks32.append((k, c.stat, c.pbits, vi.ids, seen_cap if seen_n is not None else -1))
+                checks32.append((k, li, c.pbits, vi.ids, seen_cap if seen_n is not None else -1))
                 sm = c
                 res.info[k] = dict(contexts=vi.n, ids=vi.ids, pairs=None, events=None, pbits=c.pbits, hits=None)
             else:
@@ -194,7 +198,7 @@ class LevelBuild:
             t3 = time.perf_counter()
             thr = None
             if cnt_top is not None and sm.deep.numel():
-                thr = torch.zeros(vi.ids, dtype=torch.int64, device=dev)
+                thr = elib.zeros(vi.ids, torch.int64, dev)
                 e0, e1 = self._event("ctx_kth", k, int(sm.deep.numel()))
                 e0.record()
                 elib("ng_ctx_kth", sm.words, i32(c.cb), c.esc[0], c.esc[1], u64(partcount.ESC_CAP), sm.rec, sm.deep,
@@ -213,14 +217,15 @@ class LevelBuild:
             self.host_s["count"] += t3 - t2
             del vi, c, sm, thr, seen
         del regions
-        if checks32 and self._check32(checks32, res):
+        host = stats.cpu().tolist() if (checks32 or pending) else None  # the build's one host read
+        if checks32 and self._check32(checks32, host, res):
             self.reruns += 1
             return self.build(x, tgt, avail, topk=topk, cnt_top=cnt_top, keep=keep, with_mask=with_mask,
-                              stats=stats, _defer=_defer)
+                              stats=want_stats, _defer=_defer)
         if pending:
-            checked = QueryIndex.check(pending)
+            checked = QueryIndex.check([(k, None) for _, k in pending], [host[li][5:8] for li, _ in pending])
             redo = False
-            for (k, _), (n_ctx, ok) in zip(pending, checked):
+            for (_, k), (n_ctx, ok) in zip(pending, checked):
                 self.contexts_of[k] = n_ctx  # the next build's tables are sized from these
                 res.info[k]["contexts"] = n_ctx
                 redo |= not ok
@@ -228,9 +233,9 @@ class LevelBuild:
             if redo:  # an insert found no slot in a table sized from the last build: once more, each level checked
                 self.reruns += 1
                 return self.build(x, tgt, avail, topk=topk, cnt_top=cnt_top, keep=keep, with_mask=with_mask,
-                                  stats=stats, _defer=False)
+                                  stats=want_stats, _defer=False)
         check_summary(deferred)
-        if stats:
+        if want_stats:
             for li, k in enumerate(self.levels):
                 h = int(self._popcount(bms[k]))
                 res.info[k]["hits"] = h
@@ -249,15 +254,17 @@ class LevelBuild:
                 res.info[k]["probed"] = probed
         return res
 
-    def _check32(self, checks: list, res: LevelOutputs) -> bool:
-        """The 32-bit counts' device results, read in one copy: each level's events and distinct pairs (kept to size
+    def _check32(self, checks: list, host: list, res: LevelOutputs) -> bool:
+        """The 32-bit counts' device results (`host`: the build's stats read in one copy): each level's events and
+        distinct pairs (kept to size
         the next build), raising on an overflowed emit region, 2^32 or more events, or a total past uint32. Returns
         whether the build must be redone: a level's query positions listed on the device outran their room (the
         levels after it counted from a cut list, so their results are not kept), a partition overfull (counted
         again with one more partition bit) or the escape table full (the level goes to the 64-bit count)."""
-        vals = torch.stack([c[1] for c in checks]).cpu().tolist()
         redo = False
-        for (k, _, pbits, ids, seen_cap), (n_ev, n_u, fl, sfl, n_seen, n_false) in zip(checks, vals):
+        for k, li, pbits, ids, seen_cap in checks:
+            n_ev, n_u, fl, scan, n_seen = host[li][:5]
+            sfl, n_false = scan & 0xFFFFFFFF, (scan >> 32) & 0xFFFFFFFF
             if seen_cap >= 0:  # the level's query positions were listed on the device
                 self.seen_of[k] = max(n_seen, 1)
                 if n_seen > seen_cap:  # more than their room: the build runs again with room for them
@@ -299,19 +306,21 @@ class LevelBuild:
             return 0
         return 3 if d < LIST_DENSITY else 2
 
-    def _emit(self, k, vi, x, bms, regions, R, wbits=0):
+    def _emit(self, k, vi, x, bms, regions, R, wbits=0, flags=None):
         """Level k's scan of every shard it counts, hits emitted to per-block regions with each block's top-digit
         histogram: count_events' seg = (regions, R, ev_count, dhist, nseg, flags). wbits: events wmix(pair key,
-        wbits) with histograms of their first_digit(wbits) top bits (count32's), else mix64(pair key)."""
+        wbits) with histograms of their first_digit(wbits) top bits (count32's), else mix64(pair key). flags: the
+        scan's two int32 flags (zeroed; e.g. a view into the build's stats), else new."""
         elib, dev, G = self.elib, self.tok.device, self.grid
         shards = [i for i in range(len(self.sizes)) if i < self.level_shards[k]]
         nseg = len(shards) * G
-        ev_count = torch.zeros(max(nseg, 1), dtype=torch.int32, device=dev)
+        ev_count = elib.zeros(max(nseg, 1), torch.int32, dev)
         last = self.events_of.get(k)
         dbits = first_digit(wbits) if wbits else 8
         dhist = torch.empty((1 << dbits) * max(nseg, 1), dtype=torch.int32, device=dev) \
             if wbits or last is None or last >= partcount.SEG_MIN_EVENTS * nseg else None
-        flags = torch.zeros(2, dtype=torch.int32, device=dev)
+        if flags is None:
+            flags = elib.zeros(2, torch.int32, dev)
         scans = {tuple(q for q in self.levels if i < self.level_shards[q]) for i in shards}
         if len(shards) > 1 and len(scans) == 1:
             # every shard scans the same levels: one launch over all of them (the SENT gaps between shards hold no
@@ -332,7 +341,7 @@ class LevelBuild:
             if mode == 3:
                 if self._plist is None or self._plist.numel() < n32:
                     self._plist = torch.empty(max(self.sizes) + 64, dtype=torch.int64, device=dev)
-                n_list = torch.zeros(1, dtype=torch.int64, device=dev)
+                n_list = elib.zeros(1, torch.int64, dev)
                 b0, b1 = self._event("bits_list", k, n32)
                 b0.record()
                 elib.cub("ng_bits_list", bm_in, n32 // 32, self._plist, n_list, self._pre)
@@ -364,7 +373,7 @@ class LevelBuild:
         R = -(-max(n, 1) // (G * 256)) * 256 if mode == 3 else emit_region(n, G)
         if G * R > regions.numel():
             raise RuntimeError(f"k={k}: the emit regions are too small for one scan over every shard")
-        ev_count = torch.zeros(G, dtype=torch.int32, device=dev)
+        ev_count = elib.zeros(G, torch.int32, dev)
         last = self.events_of.get(k)
         dbits = first_digit(wbits) if wbits else 8
         dhist = torch.empty((1 << dbits) * G, dtype=torch.int32, device=dev) \
@@ -372,7 +381,7 @@ class LevelBuild:
         if mode == 3:
             if self._plist is None or self._plist.numel() < n:
                 self._plist = torch.empty(n + 64, dtype=torch.int64, device=dev)
-            n_list = torch.zeros(1, dtype=torch.int64, device=dev)
+            n_list = elib.zeros(1, torch.int64, dev)
             b0, b1 = self._event("bits_list", k, n)
             b0.record()
             elib.cub("ng_bits_list", bm_in[lo // 32 :], n // 32, self._plist, n_list, self._pre)

@@ -41,24 +41,32 @@ class Lib:
 
     def __init__(self, path: str | Path | None = None):
         self.so = load(path)
+        self._fns: dict = {}
+
+    def _fn(self, name: str):
+        fn = self._fns.get(name)
+        if fn is None:
+            fn = self.so[name]  # a function object of its own (size() sets another return type on the shared one)
+            fn.restype = ctypes.c_int
+            self._fns[name] = fn
+        return fn
 
     def __call__(self, name: str, *args) -> int:
+        # the host side of every launch: kept short, since a build issues a few hundred of them back to back
         conv = []
         for a in args:
             if isinstance(a, torch.Tensor):
                 conv.append(ctypes.c_void_p(a.data_ptr()))
             elif a is None:
-                conv.append(ctypes.c_void_p(0))
-            elif isinstance(a, (ctypes._SimpleCData, ctypes.Array)):
-                conv.append(a)
+                conv.append(None)
             elif isinstance(a, int):
                 conv.append(ctypes.c_int64(a))
+            elif isinstance(a, (ctypes._SimpleCData, ctypes.Array)):
+                conv.append(a)
             else:
                 raise TypeError(f"{name}: argument {a!r}")
-        conv.append(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
-        fn = getattr(self.so, name)
-        fn.restype = ctypes.c_int
-        rc = fn(*conv)
+        conv.append(ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(torch._C._cuda_getDevice())))
+        rc = self._fn(name)(*conv)
         if rc != 0:
             raise RuntimeError(f"{name} returned {rc}")
         return rc
@@ -72,11 +80,31 @@ class Lib:
         self(name, temp, ptr, *args)
         del temp
 
+    def fill(self, t: torch.Tensor, v: int) -> torch.Tensor:
+        """Every element of the contiguous device tensor t set to v, 0 or -1 (a byte pattern: all zeros or all ones),
+        by this library's fill kernel on the current stream; returns t."""
+        if v not in (0, -1) or not t.is_contiguous():
+            raise ValueError("fill takes 0 or -1 over a contiguous tensor")
+        nbytes = t.numel() * t.element_size()
+        if nbytes % 8 == 0:
+            self("ng_fill_u64", t, nbytes // 8, ctypes.c_uint64(0 if v == 0 else (1 << 64) - 1))
+        elif nbytes % 4 == 0:
+            self("ng_fill_u32", t, nbytes // 4, ctypes.c_uint32(0 if v == 0 else (1 << 32) - 1))
+        else:
+            t.fill_(v)
+        return t
+
+    def zeros(self, shape, dtype, device) -> torch.Tensor:
+        """torch.zeros without a framework kernel (this library's fill)."""
+        return self.fill(torch.empty(shape, dtype=dtype, device=device), 0)
+
+    def full_ones(self, shape, dtype, device) -> torch.Tensor:
+        """A tensor of -1 (every bit set) without a framework kernel."""
+        return self.fill(torch.empty(shape, dtype=dtype, device=device), -1)
+
     def plain(self, name: str, *args) -> int:
         """A call without the stream argument (e.g. max_pbits)."""
-        fn = getattr(self.so, name)
-        fn.restype = ctypes.c_int
-        return fn(*args)
+        return self._fn(name)(*args)
 
     def size(self, name: str, *args: int) -> int:
         """A sizing call without the stream argument that returns int64 (its arguments int64)."""

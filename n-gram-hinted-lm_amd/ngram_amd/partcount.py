@@ -289,10 +289,11 @@ def first_digit(W: int) -> int:
 class Counted32:
     """A level counted by count32: per context id its record (int32 [n_ids, RECORD_WORDS[ktop]]) and pair count
     dist (int32 [n_ids], 0 for absent contexts), per query position the target's count qcnt (int32 [N]), and the
-    device-side results the host checks once per build (`stat`: int64 [6] = events, distinct pairs, the count's flags,
-    the scan's flags, a count the caller keeps there, the scan's false hash hits (hashed keys of k > 4 found in the
-    query table whose tokens differ); bit 0 of the count's flags: a partition overfull, bit 1: the
-    escape table full, bit 2: a total reached 2^32; bit 2 of the scan's: a region overflowed)."""
+    device-side results the host checks once per build (`stat`: int64 [8] = events, distinct pairs, the count's flags,
+    the scan's flags as two int32 (its bits; its false hash hits, hashed keys of k > 4 found in the query table whose
+    tokens differ) where the caller's scan wrote them there, then the caller's own; bit 0 of the count's flags: a
+    partition overfull, bit 1: the escape table full, bit 2: a total reached 2^32; bit 2 of the scan's: a region
+    overflowed)."""
 
     rec: torch.Tensor
     dist: torch.Tensor | None
@@ -318,7 +319,8 @@ def pbits32_max(n_ids: int) -> int:
 
 def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None, n_events: int | None,
             ratio: float = 1.0, event=_no_event, min_pbits: int = 0, slabs: bool = False,
-            deep_min: int | None = None, with_dist: bool = True, agg_grid: int = 0) -> Counted32:
+            deep_min: int | None = None, with_dist: bool = True, agg_grid: int = 0,
+            stat: torch.Tensor | None = None) -> Counted32:
     """Count a level's events emitted by ng_scan_emit in the W-bit mode (wbits = W = w_bits(n_ids)[1], dbits =
     first_digit(W); seg = (regions, R, ev_count, dhist, nseg, scan flags)) and make every present context's record
     (top ktop) without a host read: the passes and the count of pairs32.hip. `n_events`: the level's events (the last
@@ -331,7 +333,9 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
     of more than deep_min pairs (for their CNT_TOP thresholds, ng_ctx_kth_grouped). Without with_dist, dist is None
     (the records hold each present context's pairs). agg_grid: ng_ctx_agg's blocks (0: one per group of ids; a couple
     per compute unit for many light groups, each block then walking its groups with the next one's words loaded
-    ahead)."""
+    ahead). `stat`: the caller's int64 [>= 8] of zeros for Counted32.stat (e.g. a row of one tensor every level of a
+    build shares, read once); its fourth entry holds the scan's two int32 flags where the caller's seg flags are a view
+    of it."""
     regions, R, ev_count, dhist, nseg, scan_flags = seg
     dev = regions.device
     idb, W = w_bits(n_ids)
@@ -340,14 +344,14 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
         raise ValueError(f"{n_ids} context ids: wider than the 32-bit count takes")
     d1 = first_digit(W)
     cap = nseg * R
-    stat = torch.zeros(6, dtype=torch.int64, device=dev)  # events, distinct pairs, count flags, scan flags, the
-    # caller's fifth (the level's listed query positions), the scan's false hash hits
+    if stat is None:
+        stat = elib.zeros(8, torch.int64, dev)
+    # stat: events, distinct pairs, count flags, the scan's flags (two int32: overflow bits, false hash hits) where the
+    # caller put them there, the caller's fifth (the level's listed query positions) and beyond
     ev_tot, u_tot = stat[0:1], stat[1:2]
     flags = stat[2:3].view(torch.int32)[:1]
     dpre = torch.empty((1 << d1) * nseg, dtype=torch.int32, device=dev)
     elib.cub("ng_exclusive_scan_u32", dhist, dpre, (1 << d1) * nseg, ev_tot)
-    stat[3:4].copy_(scan_flags[:1])
-    stat[5:6].copy_(scan_flags[1:2])
     if n_events is None:
         n_events = int(ev_tot.item())
     pbits = max(d1 + 1, W - 31, PART_MIN_BITS if lookups is not None else 0, min_pbits,
@@ -371,7 +375,7 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
     del ev1, dpre
     N = nq = 0
     sqk = sqv = None
-    qstart = torch.zeros(P + 1, dtype=torch.int64, device=dev)
+    qstart = elib.zeros(P + 1, torch.int64, dev)
     if lookups is not None:
         ctx_of, tgt, qpos = lookups[:3]
         qn = lookups[3] if len(lookups) > 3 else None  # a device-side count of qpos's entries
@@ -391,11 +395,11 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
     dc = min(11, idb)
     dtop = 64 - (cb - idb)  # the bit above a word's highest id bit
     out_k = torch.empty(max(cap, 1), dtype=torch.int64, device=dev)
-    esc_k = torch.full((ESC_CAP,), -1, dtype=torch.int64, device=dev)
+    esc_k = elib.full_ones(ESC_CAP, torch.int64, dev)
     esc_c = torch.empty(ESC_CAP, dtype=torch.int32, device=dev)
     seg_cnt = torch.empty(G2, dtype=torch.int32, device=dev)
     seg_base = torch.empty(G2, dtype=torch.int64, device=dev)
-    qcnt = torch.zeros(max(N, 1), dtype=torch.int32, device=dev) if N else None
+    qcnt = elib.zeros(max(N, 1), torch.int32, dev) if N else None
     dh2 = torch.empty((1 << dc) * G2, dtype=torch.int32, device=dev)
     slab = torch.empty(P * P32_SLOTS, dtype=torch.int64, device=dev) if slabs else None
     e0, e1 = event("count", cap)
@@ -430,7 +434,7 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
     deep = deep_n = None
     if deep_min is not None:  # at most (pairs) / (deep_min + 1) contexts have more than deep_min pairs
         deep = torch.empty(cap // (deep_min + 1) + 1, dtype=torch.int64, device=dev)
-        deep_n = torch.zeros(2, dtype=torch.int64, device=dev)  # the deep contexts, the present contexts
+        deep_n = elib.zeros(2, torch.int64, dev)  # the deep contexts, the present contexts
     e0, e1 = event("ctx_topk", cap)
     e0.record()
     elib("ng_ctx_agg", words, start2, P2, i32(ibits), i32(cb), n_ids, esc_k, esc_c, u64(ESC_CAP), i32(ktop), rec,

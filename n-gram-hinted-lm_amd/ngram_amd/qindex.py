@@ -22,7 +22,7 @@ EXPECT_MARGIN = 1.2  # a table sized from an expected context count holds this m
 class QueryIndex:
     def __init__(self, lib: Lib, x: torch.Tensor, avail: torch.Tensor, k: int, positions: torch.Tensor | None = None,
                  compact: bool = False, expect: int | None = None, _resized: bool = False, defer: bool = False,
-                 n_dev: torch.Tensor | None = None):
+                 n_dev: torch.Tensor | None = None, counters: torch.Tensor | None = None):
         """Index the valid k-contexts of the query positions (all of x, or the int32 `positions`). `compact`: ctx_of
         holds one entry per listed position (in their order) instead of one per position of x. `expect`: about how
         many contexts there are (e.g. the last build's count): the table is sized for them at once instead of for
@@ -32,7 +32,9 @@ class QueryIndex:
         table sized from `expect` stands, `n` is None, and the caller must pass `pending` to `check()` and redo its
         work if an insert found no slot (its context is then missing from the table). `n_dev` (int64 [1] on the
         device, with `positions`): only the first n_dev of the listed positions are indexed (a count the host has not
-        read; `positions` holds at least that many, or the caller checks)."""
+        read; `positions` holds at least that many, or the caller checks). `counters` (int64 [3] of zeros on the device,
+        with `defer`): where the deferred build's counters go (e.g. a row of the caller's stats, read with its other
+        results in one copy), else new."""
         dev = x.device
         N = x.numel()
         m = N if positions is None else int(positions.numel())
@@ -42,14 +44,15 @@ class QueryIndex:
             cap = min(cap, int(max(expect, 1) * max(EXPECT_MARGIN, 1.0) / LOAD) + 1024)
         while True:
             slots = cap + TAIL
-            table = torch.full((slots,), -1, dtype=torch.int64, device=dev)
+            table = lib.full_ones(slots, torch.int64, dev)
             rep = torch.empty(slots, dtype=torch.int32, device=dev)  # read only at occupied slots: no fill
             if compact and positions is not None:
                 ctx_of = torch.empty(m, dtype=torch.int32, device=dev)
             else:
-                ctx_of = torch.full((N,), -1, dtype=torch.int32, device=dev) if positions is not None else \
+                ctx_of = lib.full_ones(N, torch.int32, dev) if positions is not None else \
                     torch.empty(N, dtype=torch.int32, device=dev)
-            counters = torch.zeros(3, dtype=torch.int64, device=dev)
+            if counters is None or not (defer and expect is not None and not _resized):
+                counters = lib.zeros(3, torch.int64, dev)
             if m:
                 lib("ng_query_index", x, avail, positions, m, n_dev, i32(k), table, u64(cap), u64(slots), rep,
                     ctx_of, i32(int(compact and positions is not None)), counters)
@@ -95,12 +98,13 @@ class QueryIndex:
         self._valid = None
 
     @staticmethod
-    def check(pending: list) -> list[tuple[int, bool]]:
-        """Deferred builds' counters ((k, the index's `pending`) pairs), read in one copy: per index (n contexts,
-        whether every insert found its slot); a 64-bit key collision raises."""
+    def check(pending: list, values: list | None = None) -> list[tuple[int, bool]]:
+        """Deferred builds' counters ((k, the index's `pending`) pairs, read here in one copy; or `values`, their host
+        values the caller read): per index (n contexts, whether every insert found its slot); a 64-bit key collision
+        raises."""
         if not pending:
             return []
-        got = torch.stack([c for _, c in pending]).cpu().tolist()
+        got = values if values is not None else torch.stack([c for _, c in pending]).cpu().tolist()
         out = []
         for (k, _), (n, over, coll) in zip(pending, got):
             if coll:
