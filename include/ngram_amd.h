@@ -161,11 +161,12 @@ int ng_scan_exist(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, u
                   ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, uint32_t* hit, uint32_t* ids, uint32_t* flags,
                   int grid, int sparse, const uint32_t* pre, void* stream);
 /* a level's counting scan from ng_scan_exist's ids: each position set in bm whose context's bit is set in `final`
- * emits mix64(id << 16 | tok[p]) as ng_scan_emit's events (regions, ev_count, dhist); L a multiple of 32, tok
+ * emits its (id << 16 | tok[p]) event as ng_scan_emit's (regions, ev_count, dhist; wbits 0: mix64 with the top 8
+ * bits' histogram, wbits 17..63: wmix(key, wbits) with the top dbits bits', dbits <= 10); L a multiple of 32, tok
  * 8-byte and ids 16-byte aligned */
 int ng_scan_ids_emit(const uint16_t* tok, ng_i64 L, const uint32_t* bm, const uint32_t* ids, const uint32_t* final,
                      ng_u64* ev, ng_u64 region, uint32_t* ev_count, uint32_t* flags, int grid, uint32_t* dhist,
-                     ng_i64 dstride, void* stream);
+                     ng_i64 dstride, int wbits, int dbits, void* stream);
 /* bit ids[i] of the u32 words bits set for each ids[i] >= 0 (bits zeroed by the caller) */
 int ng_mark_bits(const int* ids, ng_i64 n, uint32_t* bits, void* stream);
 /* a split table's occupied slots appended to (out_k, out_c) from *counter (zeroed by the caller) */

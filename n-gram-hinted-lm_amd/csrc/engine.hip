@@ -693,22 +693,31 @@ __global__ void mark_bits_k(const int* __restrict__ ids, i64 n, u32* bits) {
 }
 }  // namespace
 
+// An emitting scan's event mode: mix64 events (wbits 0), or W-bit ones with a dbits-bit histogram digit.
+static inline bool emit_mode_ok(int wbits, int dbits) {
+    return wbits == 0 || (wbits >= 17 && wbits <= 63 && dbits >= 1 && dbits <= EMIT_MAXD && dbits < wbits);
+}
+
 // A level's counting scan from the context ids its existence scan stored (ng_scan_exist's ids, valid at the
 // positions set in bm): the positions whose context's bit is set in `final` emit their events as ng_scan_emit's
-// (regions, ev_count, dhist; region >= ng_emit_region(L, grid)).
+// (regions, ev_count, dhist; region >= ng_emit_region(L, grid)), in its modes: wbits 0: mix64(pair key) with a
+// histogram of the top 8 bits; wbits in [17, 63]: wmix(pair key, wbits) (context ids below 2^(wbits - 16)) with a
+// histogram of the top dbits bits (1 <= dbits <= 10), the 32-bit count's events.
 extern "C" int ng_scan_ids_emit(const u16* tok, i64 L, const u32* bm, const u32* ids, const u32* final, u64* ev,
-                                u64 region, u32* ev_count, u32* flags, int grid, u32* dhist, i64 dstride,
-                                void* stream) {
+                                u64 region, u32* ev_count, u32* flags, int grid, u32* dhist, i64 dstride, int wbits,
+                                int dbits, void* stream) {
     if (grid <= 0 || region == 0 || region > 0xFFFFFFFFull || (dhist && dstride < grid)) return -1;
+    if (!emit_mode_ok(wbits, dbits)) return -1;
     if ((L & 31) || ((uintptr_t)tok & 7) || ((uintptr_t)ids & 15)) return -1;  // the kernel's vector loads
     hipStream_t st = (hipStream_t)stream;
+    const int nd = wbits ? 1 << dbits : 256;
     if (L <= 0) {
         fill_u32_n(ev_count, 0u, grid, st);
         if (dhist)
-            for (int d = 0; d < 256; ++d) fill_u32_n(dhist + (i64)d * dstride, 0u, grid, st);
+            for (int d = 0; d < nd; ++d) fill_u32_n(dhist + (i64)d * dstride, 0u, grid, st);
         return (int)hipGetLastError();
     }
-    const EmitSink sk{ev, region, ev_count, 0, nullptr, dhist, dstride, 0};
+    const EmitSink sk{ev, region, ev_count, 0, nullptr, dhist, dstride, 0, wbits, dbits};
     scan_ids_k<<<grid, 256, 0, st>>>(tok, L, bm, ids, final, sk, flags);
     return (int)hipGetLastError();
 }
@@ -733,9 +742,6 @@ extern "C" u64 ng_emit_region(i64 L, int grid) {
     return ((u64)L + per - 1) / per * 8192ull;
 }
 
-static inline bool emit_mode_ok(int wbits, int dbits) {
-    return wbits == 0 || (wbits >= 17 && wbits <= 63 && dbits >= 1 && dbits <= EMIT_MAXD && dbits < wbits);
-}
 
 extern "C" int ng_scan_emit(const u16* tok, i64 L, int k, const u32* bm_in, u32* bm_out, const u64* vt, u64 vcap,
                             const u32* vrep, const u16* x, u64* ev, u64 region, u32* ev_count, u32* flags, int grid,

@@ -33,7 +33,8 @@ import torch
 from .data import BOS, HEADER_BYTES, shard_tokens
 from .data import pack_layout as layout
 from .lib import Lib, i32, u64
-from .partcount import count_events, emit_region, pack_events, summarize
+from .partcount import (W_MAX, count32, count_events, emit_region, first_digit, pack_events, pbits32_max, summarize,
+                        w_bits)
 from .qindex import LOAD as QLOAD, TAIL as QTAIL, QueryIndex
 
 
@@ -44,6 +45,7 @@ def _popcount(lib: Lib, bm: torch.Tensor) -> int:
 
 
 _RATIO: dict[int, float] = {}  # distinct pairs per counted event at each level, from the last count (sizes partitions)
+_WIDE: set = set()  # levels whose 32-bit count overflowed its escape table: counted by the 64-bit path
 # each existence level's query contexts per listed position in the last call: sizes the next call's query index for
 # its own number of positions
 _CONTEXTS: dict[int, float] = {}
@@ -310,9 +312,20 @@ def _count_ids(elib: Lib, lib: Lib, tok, L: int, level: tuple, k: int, length, f
     R = emit_region(L, grid)
     regions = torch.empty(grid * R, dtype=torch.int64, device=dev)
     ev_count = torch.empty(grid, dtype=torch.int32, device=dev)
+    _, W = w_bits(n_ids)
+    if W <= W_MAX and k not in _WIDE:  # the 32-bit count (pairs32.hip), as the level pipeline's
+        d1 = first_digit(W)
+        dhist = torch.empty((1 << d1) * grid, dtype=torch.int32, device=dev)
+        flags.zero_()
+        elib("ng_scan_ids_emit", tok, L, bm, ids, final, regions, u64(R), ev_count, flags, i32(grid), dhist, grid,
+             i32(W), i32(d1))
+        if _count32_final(elib, (regions, R, ev_count, dhist, grid, flags), n_ids, k, fids, fpos, m, nxt, cnt):
+            return
+        _WIDE.add(k)  # its escape table overflowed: this level takes the 64-bit count from now on
     dhist = torch.empty(256 * grid, dtype=torch.int32, device=dev)
     flags.zero_()
-    elib("ng_scan_ids_emit", tok, L, bm, ids, final, regions, u64(R), ev_count, flags, i32(grid), dhist, grid)
+    elib("ng_scan_ids_emit", tok, L, bm, ids, final, regions, u64(R), ev_count, flags, i32(grid), dhist, grid, i32(0),
+         i32(0))
     try:  # the scan's flags read with the event total
         c = count_events(elib, lib, None, 0, n_ids, _RATIO.get(k, 1.0),
                          seg=(regions, R, ev_count, dhist, grid, flags), presort="ctx")
@@ -332,6 +345,39 @@ def _count_ids(elib: Lib, lib: Lib, tok, L: int, level: tuple, k: int, length, f
         _top1_unpacked(elib, lib, SimpleNamespace(ctx_of=fids, ids=n_ids), c, None, o_tok, o_cnt)
     nxt[fpos] = o_tok
     cnt[fpos] = o_cnt
+
+
+def _count32_final(elib: Lib, seg: tuple, n_ids: int, k: int, fids, fpos, m: int, nxt, cnt) -> bool:
+    """The 32-bit count of a level's final contexts' events (seg: ng_scan_ids_emit's W-bit regions), their top entry
+    gathered to the final positions; an overfull partition is counted again with one more partition bit. False (the
+    caller takes the 64-bit count) when the escape table overflowed."""
+    dev = fids.device
+    min_pbits = 0
+    while True:
+        c = count32(elib, seg, n_ids, 1, None, None, _RATIO.get(k, 1.0), min_pbits=min_pbits)
+        n_ev, n_u, fl, scan = c.stat[:4].cpu().tolist()
+        if int(seg[5][0].item()) & 4:
+            raise RuntimeError(f"k={k}: an emit region overflowed")
+        if fl & 4:
+            raise RuntimeError(f"k={k}: a total does not fit uint32")
+        if fl & 2:
+            return False
+        if fl & 1 and c.pbits < pbits32_max(n_ids):
+            min_pbits = c.pbits + 1
+            continue
+        if fl & 1:
+            return False
+        break
+    _RATIO[k] = n_u / max(1, n_ev)
+    EVENTS[0] += n_ev
+    o = [torch.empty(m, dtype=torch.int32, device=dev) for _ in range(3)]
+    o_tok = torch.zeros(m, dtype=torch.int16, device=dev)
+    o_cnt = torch.zeros(m, dtype=torch.int32, device=dev)
+    elib("ng_pos_summary", fids, m, 0, n_ids, None, c.rec, c.dist, None, None, i32(1), i32(1), i32(0), o[0], o[1],
+         o[2], o_tok, o_cnt, None)
+    nxt[fpos] = o_tok
+    cnt[fpos] = o_cnt
+    return True
 
 
 def _bits_list(elib: Lib, bm: torch.Tensor, n: int) -> torch.Tensor:

@@ -20,12 +20,22 @@ def corpus():
     return data.make_corpus("c5", train_tokens=700_000, query_tokens=60_001, shard_tokens=300_000)
 
 
-@pytest.mark.parametrize("cap,seg", [(64, False), (64, True), (8, False), (1, True)])
-def test_longest_match_matches_oracle(corpus, cap, seg, monkeypatch):
-    if seg:  # the bitmap levels' counts read the scan regions directly however few events they hold
-        from ngram_amd import partcount as P
+@pytest.mark.parametrize("cap,seg,count", [(64, False, "32"), (64, True, "64"), (8, False, "32overfull"),
+                                           (1, True, "64"), (64, False, "64")])
+def test_longest_match_matches_oracle(corpus, cap, seg, count, monkeypatch):
+    """count: the bitmap levels' final contexts counted by the 32-bit count (32; 32overfull: partitions declared
+    overfull at 64 distinct pairs, so levels are counted again with more partition bits, or by the 64-bit count once
+    there are none) or by the 64-bit count (64)."""
+    import ngram_amd.longest as LG
+    from ngram_amd import partcount as P
 
+    monkeypatch.setattr(LG, "_WIDE", set())
+    if seg:  # the bitmap levels' counts read the scan regions directly however few events they hold
         monkeypatch.setattr(P, "SEG_MIN_EVENTS", 0)
+    if count == "64":
+        monkeypatch.setattr(LG, "W_MAX", 0)
+    if count == "32overfull":
+        monkeypatch.setattr(P, "P32_LIMIT", 64)
     x = corpus.query[:-1]
     avail = O.segments(x)
     want = O.longest_match(corpus.train, corpus.bounds, x, avail, cap)
