@@ -351,21 +351,66 @@ __global__ void __launch_bounds__(256) scan_compact_k(const u16* __restrict__ to
     sink_end(sink, &ss);
 }
 
-__global__ void bits_popc_k(const u32* __restrict__ bm, i64 nwords, u32* __restrict__ off, const u32* pre_flag) {
-    const i64 w = blockIdx.x * (i64)blockDim.x + threadIdx.x;
-    if (w < nwords) off[w] = (u32)__popc(gate_word(bm, w, pre_on(pre_flag)));
+// A bitmap's set bits listed in two passes over blocks of BL_BLOCK * BL_ROUNDS words: each block's count, a scan of
+// those counts, then each block lists its bits in order (a round of BL_BLOCK words at a time, their offsets by a
+// block-wide scan), so no per-word offsets go through memory.
+#define BL_BLOCK 256
+#define BL_ROUNDS 32
+__device__ __forceinline__ u32 bl_block_excl(u32 c, u32* s_w, u32& total) {
+    const int lane = lane_id(), wid = threadIdx.x / WAVE;
+    u32 incl = c;
+#pragma unroll
+    for (int d = 1; d < WAVE; d <<= 1) {
+        const u32 o = (u32)__shfl_up((int)incl, d, WAVE);
+        if (lane >= d) incl += o;
+    }
+    if (lane == WAVE - 1) s_w[wid] = incl;
+    __syncthreads();
+    u32 before = 0;
+    total = 0;
+#pragma unroll
+    for (int v = 0; v < BL_BLOCK / WAVE; ++v) {
+        before += v < wid ? s_w[v] : 0u;
+        total += s_w[v];
+    }
+    __syncthreads();  // s_w is read before the next round writes it
+    return before + incl - c;
 }
 
-__global__ void bits_list_k(const u32* __restrict__ bm, i64 nwords, const u32* __restrict__ off, u64* __restrict__ out,
-                            const u32* pre_flag) {
-    const i64 w = blockIdx.x * (i64)blockDim.x + threadIdx.x;
-    if (w >= nwords) return;
-    u32 word = gate_word(bm, w, pre_on(pre_flag));
-    u64 at = off[w];
-    while (word) {
-        const int b = __ffs(word) - 1;
-        word &= word - 1;
-        out[at++] = (u64)((w << 5) + b);
+__global__ void __launch_bounds__(BL_BLOCK) bits_count_k(const u32* __restrict__ bm, i64 nwords, u32* __restrict__ cnt,
+                                                         const u32* pre_flag) {
+    __shared__ u32 s_w[BL_BLOCK / WAVE];
+    const bool pre = pre_on(pre_flag);
+    const i64 w0 = blockIdx.x * (i64)(BL_BLOCK * BL_ROUNDS);
+    u32 c = 0;
+#pragma unroll 4
+    for (int r = 0; r < BL_ROUNDS; ++r) {
+        const i64 w = w0 + r * BL_BLOCK + threadIdx.x;
+        if (w < nwords) c += (u32)__popc(gate_word(bm, w, pre));
+    }
+    u32 total;
+    bl_block_excl(c, s_w, total);
+    if (threadIdx.x == 0) cnt[blockIdx.x] = total;
+}
+
+__global__ void __launch_bounds__(BL_BLOCK) bits_list_k(const u32* __restrict__ bm, i64 nwords,
+                                                        const u32* __restrict__ boff, u64* __restrict__ out,
+                                                        const u32* pre_flag) {
+    __shared__ u32 s_w[BL_BLOCK / WAVE];
+    const bool pre = pre_on(pre_flag);
+    const i64 w0 = blockIdx.x * (i64)(BL_BLOCK * BL_ROUNDS);
+    u64 run = boff[blockIdx.x];
+    for (int r = 0; r < BL_ROUNDS; ++r) {
+        const i64 w = w0 + r * BL_BLOCK + threadIdx.x;
+        u32 word = w < nwords ? gate_word(bm, w, pre) : 0u;
+        u32 total;
+        u64 at = run + bl_block_excl((u32)__popc(word), s_w, total);
+        while (word) {
+            const int b = __ffs(word) - 1;
+            word &= word - 1;
+            out[at++] = (u64)((w << 5) + b);
+        }
+        run += total;
     }
 }
 
@@ -836,7 +881,9 @@ extern "C" int ng_scan_sink(const u16* tok, i64 L, int k, const u32* bm_in, u32*
 extern "C" int ng_bits_list(void* temp, size_t* temp_bytes, const u32* bm, i64 nwords, u64* out, u64* total,
                             const u32* pre, void* stream) {
     if (!temp_bytes || nwords < 0) return -1;
-    const size_t need = (size_t)(nwords + 64) * 4 + prim::scan_u32_temp_bytes(nwords + 1) + 256;
+    const i64 nb = (nwords + BL_BLOCK * BL_ROUNDS - 1) / (BL_BLOCK * BL_ROUNDS);
+    const size_t b0 = ((size_t)(nb + 64) * 4 + 255) & ~(size_t)255;
+    const size_t need = b0 + prim::scan_u32_temp_bytes(nb + 1) + 256;
     if (!temp) {
         *temp_bytes = need;
         return 0;
@@ -845,11 +892,11 @@ extern "C" int ng_bits_list(void* temp, size_t* temp_bytes, const u32* bm, i64 n
     hipStream_t st = (hipStream_t)stream;
     if (nwords == 0) return prim::fill_u64(total, 0ull, 1, st);
     u32* off = (u32*)temp;
-    void* stemp = (char*)temp + (size_t)(nwords + 64) * 4;
-    bits_popc_k<<<grid_for(nwords, 256), 256, 0, st>>>(bm, nwords, off, pre);
-    int e = prim::exclusive_scan_u32(off, off, nwords, total, stemp, st);
+    void* stemp = (char*)temp + b0;
+    bits_count_k<<<(unsigned)nb, BL_BLOCK, 0, st>>>(bm, nwords, off, pre);
+    int e = prim::exclusive_scan_u32(off, off, nb, total, stemp, st);
     if (e) return e;
-    bits_list_k<<<grid_for(nwords, 256), 256, 0, st>>>(bm, nwords, off, out, pre);
+    bits_list_k<<<(unsigned)nb, BL_BLOCK, 0, st>>>(bm, nwords, off, out, pre);
     return (int)hipGetLastError();
 }
 

@@ -145,3 +145,25 @@ def test_seg_scatter_keeps_inside_its_capacity(lib):
     assert np.all(got[cap:] == np.uint64(0xFFFFFFFFFFFFFFFF))
     # region 0 was read up to R keys: they fill places 0..R-1 (its digit range starts at 0)
     assert np.array_equal(np.sort(got[:R]), np.sort(keys[:R]))
+
+
+@pytest.mark.parametrize("nwords", [0, 1, 255, 8191, 8192, 8193, 100_003])
+@pytest.mark.parametrize("density", [0.0, 0.02, 0.5, 1.0])
+@pytest.mark.parametrize("pre", [False, True])
+def test_bits_list_matches_numpy(lib, nwords, density, pre):
+    """ng_bits_list against numpy: every set bit's position in order and their count; with the prefix flag set, only
+    the bits whose previous bit is set too (the bit before position 0 counts as set)."""
+    rng = np.random.default_rng(nwords * 7 + int(density * 100) + pre)
+    bits = rng.random(nwords * 32) < density
+    words = np.packbits(bits.reshape(-1, 8)[:, ::-1], axis=1).reshape(-1).view("<u4") if nwords else np.zeros(0, "<u4")
+    keep = bits.copy()
+    if pre and nwords:
+        keep &= np.concatenate([[True], bits[:-1]])
+    want = np.flatnonzero(keep).astype(np.int64)
+    bm = torch.from_numpy(words.view(np.int32).copy()).cuda()
+    out = torch.full((max(len(want), 1),), -1, dtype=torch.int64, device="cuda")
+    total = torch.zeros(1, dtype=torch.int64, device="cuda")
+    flag = torch.tensor([1 if pre else 0], dtype=torch.int32, device="cuda")
+    lib.cub("ng_bits_list", bm, nwords, out, total, flag)
+    assert int(total.item()) == len(want)
+    assert np.array_equal(out.cpu().numpy()[: len(want)], want)
