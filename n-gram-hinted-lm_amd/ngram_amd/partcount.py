@@ -266,6 +266,7 @@ P32_SLOTS = 14336  # slots of the 32-bit count's per-partition table (pairs32.h)
 P32_TARGET = 6144  # distinct pairs per partition aimed at by the 32-bit count (its LDS table takes up to 11000)
 P32_LIMIT = 11000  # distinct pairs at which the 32-bit count declares a partition overfull (at most 11000)
 PACK32_MIN_BITS = 0  # context bits of the 32-bit count's packed words at least this (a narrower count field)
+WORD_DIGIT = 8  # the 32-bit count's words are grouped by context first by this many top id bits (at least)
 AGG_ID_BITS = 11  # context ids per group of words whose records ng_ctx_agg makes in one block: at most 2^11 (2^10 for
                   # top 8, whose LDS then lets two blocks share a compute unit)
 W_MAX = 42  # the widest pair key (context-id bits + 16) the 32-bit count narrows in its first pass: that pass's digit
@@ -392,7 +393,10 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
         elib("ng_part_bounds", sqk, nq, i32(pbits), i32(0), qstart)
     e1.record()
     G2 = min(P, PART_BLOCKS)
-    dc = min(11, idb)
+    agg = AGG_ID_BITS - 1 if ktop >= 8 else AGG_ID_BITS  # top 8: 2^10 ids a group
+    # the words' first grouping digit: 8 bits (runs of about 64 words per digit in each 16384-word chunk), more only
+    # where the second pass's 11 bits would not reach a group's
+    dc = min(idb, max(WORD_DIGIT, idb - agg - 11))
     dtop = 64 - (cb - idb)  # the bit above a word's highest id bit
     out_k = torch.empty(max(cap, 1), dtype=torch.int64, device=dev)
     esc_k = elib.full_ones(ESC_CAP, torch.int64, dev)
@@ -410,8 +414,8 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
     e1.record()
     del ev32b, start, sqk, sqv, qstart
     # the words grouped by context: by their top dc bits (ng_seg_scatter), then within those groups by the next d2
-    # bits (ng_msd_pass64), so that a group holds at most 2^11 ids, whose records ng_ctx_agg makes in LDS
-    d2 = max(0, idb - dc - (AGG_ID_BITS - 1 if ktop >= 8 else AGG_ID_BITS))  # top 8: 2^10 ids a group
+    # bits (ng_msd_pass64), so that a group holds at most 2^agg ids, whose records ng_ctx_agg makes in LDS
+    d2 = max(0, idb - dc - agg)
     ibits = idb - dc - d2
     P2 = 1 << (dc + d2)
     dpre2 = torch.empty((1 << dc) * G2, dtype=torch.int32, device=dev)
