@@ -731,7 +731,7 @@ def main() -> None:
                                 "ms_per_step": path_ms, **roof(path_bytes, path_ms)},
         "build_roofline": {"bytes": build_bytes, **roof(build_bytes, ms), "streaming_floor_GBps": 2.0 * T / (ms / 1e3) / 1e9},
         "slowest_launch_class": {"kernel": f"{top_class[0]} k={top_class[1]}", "ms_per_step": per_kernel[top_class] / args.steps},
-        # the query side (SURVEY 8d's B_query): the query indexes (2 B per position + an 8-byte key per level) and
+        # the query side's algorithmic bytes B_query: the query indexes (2 B per position + an 8-byte key per level) and
         # the per-position outputs (H hits' top-k records read, 6 B per entry; 29 B written per position and level)
         "query_roofline": {"kernels": ["qindex", "pos_gather"], "hits": H,
                            "algorithmic_bytes_per_step": q_bytes, "ms_per_step": q_ms, **roof(q_bytes, q_ms)},
