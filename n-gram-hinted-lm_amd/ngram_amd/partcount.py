@@ -392,7 +392,9 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
         del qk, qv
         elib("ng_part_bounds", sqk, nq, i32(pbits), i32(0), qstart)
     e1.record()
-    G2 = min(P, PART_BLOCKS)
+    # the count's blocks: about one per 16384 events (a small level's blocks would each wait out their fixed latency
+    # in turns), at least 256 and at most PART_BLOCKS
+    G2 = min(P, PART_BLOCKS, max(256, n_events // 16384 + 1))
     agg = AGG_ID_BITS - 1 if ktop >= 8 else AGG_ID_BITS  # top 8: 2^10 ids a group
     # the words' first grouping digit: 8 bits (runs of about 64 words per digit in each 16384-word chunk), more only
     # where the second pass's 11 bits would not reach a group's
