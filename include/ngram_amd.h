@@ -115,15 +115,16 @@ int ng_scan_count(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, u
 /* the emitting scan: block b of `grid` appends its hits' events to ev[b * region ...] and stores how many in
  * ev_count[b]; region >= ng_emit_region(L, grid) = ceil(L / (grid * 8192)) * 8192; flags[0] bit 2 a region
  * overflowed. sparse as ng_scan_count's. Events: wbits 0: mix64(context id << 16 | next), digit its top 8 bits;
- * wbits in [17, 63]: wmix(pair key, wbits) (the 32-bit count's W-bit bijection, pair keys below 2^wbits), digit its
- * top dbits bits (1 <= dbits <= 10). dhist (may be NULL): block b's events per digit d at dhist[d * dstride + b]
+ * wbits in [17, 63]: kmix(pair key, wbits, mbits) (the 32-bit count's W-bit bijection, pair keys below 2^wbits: the
+ * bits from mbits up kept, the mbits below mixed; 17 <= mbits <= wbits, 0: wbits), digit its top dbits bits
+ * (1 <= dbits <= 10). dhist (may be NULL): block b's events per digit d at dhist[d * dstride + b]
  * (dstride >= grid), for ng_seg_scatter / ng_seg_scatter_narrow. pre (may be NULL): a device flag; while set, a
  * position of bm_in is probed only if the position before it is set as well (the prefix rule, ng_avail_closed) */
 ng_u64 ng_emit_region(ng_i64 L, int grid);
 int ng_scan_emit(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, uint32_t* bm_out, const ng_u64* vt,
                  ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, ng_u64* ev, ng_u64 region, uint32_t* ev_count,
                  uint32_t* flags, int grid, int sparse, uint32_t* dhist, ng_i64 dstride, const uint32_t* pre,
-                 int wbits, int dbits, void* stream);
+                 int wbits, int dbits, int mbits, void* stream);
 /* *flag = 1 if avail[i] <= max(avail[i - 1], 0) + 1 wherever avail[i] > 1 (every valid query context's prefix is the
  * previous position's valid context: the prefix rule may gate the scans), else 0; stream-ordered, no host sync */
 int ng_avail_closed(const int* avail, ng_i64 n, uint32_t* flag, void* stream);
@@ -134,12 +135,12 @@ int ng_gate_popcount(const uint32_t* bm, ng_i64 nwords, const uint32_t* pre, ng_
  * out (grid * 256 u64): the random-load rate a level scan's probes are measured against */
 int ng_gather_probe(const ng_u64* table, ng_u64 cap, ng_u64 n, ng_u64 seed, int grid, ng_u64* out, void* stream);
 /* the emitting scan over listed positions: the first *n_dev entries of plist (a device-side count: no host sync),
- * events (by wbits / dbits) and digit histograms as ng_scan_emit's, each hit's bit set in bm_out (zeroed by the
+ * events (by wbits / dbits / mbits) and digit histograms as ng_scan_emit's, each hit's bit set in bm_out (zeroed by the
  * caller; may be NULL); region >= ceil(n / (grid * 256)) * 256 */
 int ng_scan_emit_list(const uint16_t* tok, const ng_u64* plist, const ng_u64* n_dev, int k, const ng_u64* vt,
                       ng_u64 vcap, const uint32_t* vrep, const uint16_t* x, uint32_t* bm_out, ng_u64* ev, ng_u64 region,
                       uint32_t* ev_count, uint32_t* flags, int grid, uint32_t* dhist, ng_i64 dstride, int wbits,
-                      int dbits, void* stream);
+                      int dbits, int mbits, void* stream);
 /* a level scan with optional outputs over a bitmap-gated range (plist NULL: [0, L) gated by bm_in in ng_scan_count's
  * sparse modes, hit bitmap into bm_out) or over listed positions (plist: n corpus positions); hit (may be NULL):
  * bit (context id) of the u32 words hit set per hit; ev (may be NULL): block b of grid appends per hit mix64(pair key + key_add) (what 0) or its
@@ -162,11 +163,11 @@ int ng_scan_exist(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, u
                   int grid, int sparse, const uint32_t* pre, void* stream);
 /* a level's counting scan from ng_scan_exist's ids: each position set in bm whose context's bit is set in `final`
  * emits its (id << 16 | tok[p]) event as ng_scan_emit's (regions, ev_count, dhist; wbits 0: mix64 with the top 8
- * bits' histogram, wbits 17..63: wmix(key, wbits) with the top dbits bits', dbits <= 10); L a multiple of 32, tok
+ * bits' histogram, wbits 17..63: kmix(key, wbits, mbits) with the top dbits bits', dbits <= 10); L a multiple of 32, tok
  * 8-byte and ids 16-byte aligned */
 int ng_scan_ids_emit(const uint16_t* tok, ng_i64 L, const uint32_t* bm, const uint32_t* ids, const uint32_t* final,
                      ng_u64* ev, ng_u64 region, uint32_t* ev_count, uint32_t* flags, int grid, uint32_t* dhist,
-                     ng_i64 dstride, int wbits, int dbits, void* stream);
+                     ng_i64 dstride, int wbits, int dbits, int mbits, void* stream);
 /* bit ids[i] of the u32 words bits set for each ids[i] >= 0 (bits zeroed by the caller) */
 int ng_mark_bits(const int* ids, ng_i64 n, uint32_t* bits, void* stream);
 /* a split table's occupied slots appended to (out_k, out_c) from *counter (zeroed by the caller) */
@@ -253,27 +254,31 @@ int ng_msd_pass64(void* temp, size_t* temp_bytes, const ng_u64* keys, const uint
 int ng_msd_pass_narrow(void* temp, size_t* temp_bytes, const ng_u64* keys, const uint32_t* dpre, ng_i64 nseg,
                        int nb_bits, const ng_u64* total, ng_u64 cap, int shift, int nbits, uint32_t* out, ng_i64* start,
                        void* stream);
-/* lookups of n query positions i = pos[j] (pos NULL: j) for the 32-bit count: qk[j] = wmix(ctx_of[i] << 16 | tgt[i],
- * W) << (64 - W) for ids in [lo, hi) (hi <= 2^(W - 16)), else EMPTY; qv[j] = i; n_dev (may be NULL, pos required): a
- * device-side count of pos's entries, lookups j >= *n_dev EMPTY */
+/* lookups of n query positions i = pos[j] (pos NULL: j) for the 32-bit count: qk[j] = kmix(ctx_of[i] << 16 | tgt[i],
+ * W, M) << (64 - W) (M 0: W) for ids in [lo, hi) (hi <= 2^(W - 16)), else EMPTY; qv[j] = i; n_dev (may be NULL, pos
+ * required): a device-side count of pos's entries, lookups j >= *n_dev EMPTY */
 int ng_part_lookups_w(const int* ctx_of, const uint16_t* tgt, const int* pos, ng_i64 n, const ng_u64* n_dev, ng_i64 lo,
-                      ng_i64 hi, int W, ng_u64* qk, uint32_t* qv, void* stream);
+                      ng_i64 hi, int W, int M, ng_u64* qk, uint32_t* qv, void* stream);
 /* the positions i < n with v[i] > 0, in order, into out (at most cap of them); *n_dev = how many (may exceed cap);
  * two-phase temp storage; no host read */
 int ng_select_positive(void* temp, size_t* temp_bytes, const int* v, ng_i64 n, int* out, ng_i64 cap, ng_u64* n_dev,
                        void* stream);
-/* the 32-bit count of ng_msd_pass's partitions (2^pbits of them, 1 <= W - pbits <= 31, W = context-id bits + 16) in
- * LDS with `grid` blocks (<= 65536): block b's distinct pairs as packed words pair key << (48 - cb) | min(count,
- * esc), esc = 2^(48 - cb) - 1 (W - 16 <= cb <= 44; larger counts also in the escape table), at out_k + seg_base[b],
- * seg_cnt[b] of them; dhist[d * grid + b] its words per dbits-bit digit (word >> dshift) & (2^dbits - 1), dbits <=
- * 11; qcnt[qv[j]] = the count of lookup j (ng_part_lookups_w's sorted by their top pbits, bounds qstart); flags[0]
+/* the 32-bit count of ng_msd_pass's partitions (2^pbits of them, 1 <= W - pbits <= 31, W = context-id bits + 16;
+ * events kmix(pair key, W, M), M 0: W) in LDS with `grid` blocks (<= 65536): block b's distinct pairs as packed
+ * words pair key << (48 - cb) | min(count, esc), esc = 2^(48 - cb) - 1 (W - 16 <= cb <= 44; larger counts also in
+ * the escape table), at out_k + seg_base[b], seg_cnt[b] of them; dhist[d * grid + b] its words per dbits-bit digit
+ * (word >> dshift) & (2^dbits - 1), dbits <= 11; runs (may be NULL; dhist then unused): each partition's words
+ * grouped by the digit (pair key >> gshift) & (2^gbits - 1) (gbits <= 6), group s of partition p at
+ * out_k[runs[p * (2^gbits + 1) + s] ... runs[p * (2^gbits + 1) + s + 1]); n_words (may be NULL): += the words
+ * written; qcnt[qv[j]] = the count of lookup j (ng_part_lookups_w's sorted by their top pbits, bounds qstart); flags[0]
  * bit 0: a partition reached min(limit, 11000) distinct pairs (count again with a bit more), bit 1: the escape table
  * is full; slab (may be NULL): 2^pbits * 14336 u64, each partition's LDS table written out (slot = count << 32 |
  * key) for the corpus-wide tables' queries */
-int ng_part_count32(const uint32_t* ev, const ng_i64* start, int pbits, int W, const ng_u64* qk, const uint32_t* qv,
-                    const ng_i64* qstart, ng_u64* out_k, int cb, ng_u64* esc_k, uint32_t* esc_c, ng_u64 esc_cap,
-                    uint32_t* seg_cnt, ng_i64* seg_base, uint32_t* qcnt, uint32_t* dhist, int dshift, int dbits,
-                    uint32_t limit, uint32_t* flags, int grid, ng_u64* slab, void* stream);
+int ng_part_count32(const uint32_t* ev, const ng_i64* start, int pbits, int W, int M, const ng_u64* qk,
+                    const uint32_t* qv, const ng_i64* qstart, ng_u64* out_k, int cb, ng_u64* esc_k, uint32_t* esc_c,
+                    ng_u64 esc_cap, uint32_t* seg_cnt, ng_i64* seg_base, uint32_t* qcnt, uint32_t* dhist, int dshift,
+                    int dbits, uint32_t limit, uint32_t* flags, int grid, ng_u64* slab, ng_i64* runs, int gbits,
+                    int gshift, ng_u64* n_words, void* stream);
 /* per context id c < n_ids from ng_part_count32's words grouped by context into P partitions (start: i64[P + 1],
  * partition q = the ids [q << ibits, (q + 1) << ibits), ibits <= 11; ng_seg_scatter then ng_msd_pass64): dist[c] =
  * its pairs (0: absent) for every id (dist may be NULL), and for present contexts the record rec[c] of ng_ctx_summary's layout (topk 1,
@@ -285,6 +290,12 @@ int ng_ctx_agg(const ng_u64* w, const ng_i64* start, ng_i64 P, int ibits, int cb
                const uint32_t* esc_c, ng_u64 esc_cap, int topk, uint32_t* rec, uint32_t* dist, uint32_t* flags,
                uint32_t deep_min, ng_i64* deep, ng_u64 deep_cap, ng_u64* deep_n, ng_u64* present, int grid,
                void* stream);
+/* ng_ctx_agg over ng_part_count32's words left in runs (gshift = 16 + ibits): group g < NG = 2^(d1 + gbits) (ids
+ * [g << ibits, (g + 1) << ibits)) is run g & (2^gbits - 1) of partitions (g >> gbits) << d2 ... + 2^d2 - 1 (d2 <= 8,
+ * gbits <= 6, word indexes below 2^32); outputs as ng_ctx_agg's without the deep list */
+int ng_ctx_agg_runs(const ng_u64* w, const ng_i64* runs, ng_i64 NG, int d2, int gbits, int ibits, int cb,
+                    ng_i64 n_ids, const ng_u64* esc_k, const uint32_t* esc_c, ng_u64 esc_cap, int topk, uint32_t* rec,
+                    uint32_t* dist, uint32_t* flags, ng_u64* present, int grid, void* stream);
 /* n words of value v (the hosts' buffer fills, on the caller's stream) */
 int ng_fill_u32(uint32_t* p, ng_i64 n, uint32_t v, void* stream);
 int ng_fill_u64(ng_u64* p, ng_i64 n, ng_u64 v, void* stream);

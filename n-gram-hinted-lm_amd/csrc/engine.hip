@@ -68,11 +68,12 @@ struct EmitSink {
     u32* dhist;   // with what 0 (may be NULL): the block's events per digit, at dhist[digit * dstride + block]
     i64 dstride;
     u64 key_add;  // added to each pair key before it is mixed (a context-id offset: several levels' ids in one space)
-    int wbits;    // 0: events mix64(pair key), digit = the top 8 bits; else wmix(pair key, wbits) (pair keys below
-                  // 2^wbits), digit = its top dbits bits (dbits <= EMIT_MAXD)
+    int wbits;    // 0: events mix64(pair key), digit = the top 8 bits; else kmix(pair key, wbits, mbits) (pair keys
+                  // below 2^wbits), digit = its top dbits bits (dbits <= EMIT_MAXD)
     int dbits;
+    int mbits;    // with wbits: the bits below which the pair key is mixed (part.h's kmix; wbits: all of them)
     __device__ __forceinline__ u64 event(u64 key, i64 p) const {
-        return what ? (u64)p : wbits ? wmix(key + key_add, wbits) : mix64(key + key_add);
+        return what ? (u64)p : wbits ? kmix(key + key_add, wbits, mbits) : mix64(key + key_add);
     }
     __device__ __forceinline__ u32 digit(u64 e) const { return wbits ? (u32)(e >> (wbits - dbits)) : (u32)(e >> 56); }
     __device__ __forceinline__ int ndigits() const { return wbits ? 1 << dbits : 256; }
@@ -738,21 +739,25 @@ __global__ void mark_bits_k(const int* __restrict__ ids, i64 n, u32* bits) {
 }
 }  // namespace
 
-// An emitting scan's event mode: mix64 events (wbits 0), or W-bit ones with a dbits-bit histogram digit.
-static inline bool emit_mode_ok(int wbits, int dbits) {
-    return wbits == 0 || (wbits >= 17 && wbits <= 63 && dbits >= 1 && dbits <= EMIT_MAXD && dbits < wbits);
+// An emitting scan's event mode: mix64 events (wbits 0), or W-bit ones, kmix(pair key, wbits, mbits) (mbits 0 taken
+// as wbits), with a dbits-bit histogram digit. mbits is made wbits where it is 0.
+static inline bool emit_mode_ok(int wbits, int dbits, int& mbits) {
+    if (wbits == 0) return true;
+    if (mbits == 0) mbits = wbits;
+    return wbits >= 17 && wbits <= 63 && dbits >= 1 && dbits <= EMIT_MAXD && dbits < wbits && mbits >= 17 &&
+           mbits <= wbits;
 }
 
 // A level's counting scan from the context ids its existence scan stored (ng_scan_exist's ids, valid at the
 // positions set in bm): the positions whose context's bit is set in `final` emit their events as ng_scan_emit's
 // (regions, ev_count, dhist; region >= ng_emit_region(L, grid)), in its modes: wbits 0: mix64(pair key) with a
-// histogram of the top 8 bits; wbits in [17, 63]: wmix(pair key, wbits) (context ids below 2^(wbits - 16)) with a
-// histogram of the top dbits bits (1 <= dbits <= 10), the 32-bit count's events.
+// histogram of the top 8 bits; wbits in [17, 63]: kmix(pair key, wbits, mbits) (context ids below 2^(wbits - 16);
+// part.h; mbits 0: wbits) with a histogram of the top dbits bits (1 <= dbits <= 10), the 32-bit count's events.
 extern "C" int ng_scan_ids_emit(const u16* tok, i64 L, const u32* bm, const u32* ids, const u32* final, u64* ev,
                                 u64 region, u32* ev_count, u32* flags, int grid, u32* dhist, i64 dstride, int wbits,
-                                int dbits, void* stream) {
+                                int dbits, int mbits, void* stream) {
     if (grid <= 0 || region == 0 || region > 0xFFFFFFFFull || (dhist && dstride < grid)) return -1;
-    if (!emit_mode_ok(wbits, dbits)) return -1;
+    if (!emit_mode_ok(wbits, dbits, mbits)) return -1;
     if ((L & 31) || ((uintptr_t)tok & 7) || ((uintptr_t)ids & 15)) return -1;  // the kernel's vector loads
     hipStream_t st = (hipStream_t)stream;
     const int nd = wbits ? 1 << dbits : 256;
@@ -762,7 +767,7 @@ extern "C" int ng_scan_ids_emit(const u16* tok, i64 L, const u32* bm, const u32*
             for (int d = 0; d < nd; ++d) fill_u32_n(dhist + (i64)d * dstride, 0u, grid, st);
         return (int)hipGetLastError();
     }
-    const EmitSink sk{ev, region, ev_count, 0, nullptr, dhist, dstride, 0, wbits, dbits};
+    const EmitSink sk{ev, region, ev_count, 0, nullptr, dhist, dstride, 0, wbits, dbits, mbits};
     scan_ids_k<<<grid, 256, 0, st>>>(tok, L, bm, ids, final, sk, flags);
     return (int)hipGetLastError();
 }
@@ -777,7 +782,8 @@ extern "C" int ng_mark_bits(const int* ids, i64 n, u32* bits, void* stream) {
 // The emitting scan: block b of the `grid` blocks appends its hits' events to ev[b * region ...] and stores their
 // number in ev_count[b]; region must be at least ng_emit_region(L, grid). flags[0] bit 2: a region overflowed (only
 // with a smaller region). sparse as ng_scan_count's. Events: wbits 0: mix64(pair key), digit its top 8 bits; wbits
-// in [17, 63]: wmix(pair key, wbits) (pair keys below 2^wbits), digit its top dbits bits (1 <= dbits <= 10). dhist
+// in [17, 63]: kmix(pair key, wbits, mbits) (part.h; pair keys below 2^wbits; mbits 0: wbits, all bits mixed), digit
+// its top dbits bits (1 <= dbits <= 10). dhist
 // (may be NULL): block b's events per digit d at dhist[d * dstride + b] (dstride >= grid), for ng_seg_scatter.
 // pre (may be NULL): a device flag; while it is set, a position of bm_in is probed only if the position before it is
 // set too (the prefix rule: ng_avail_closed).
@@ -790,9 +796,10 @@ extern "C" u64 ng_emit_region(i64 L, int grid) {
 
 extern "C" int ng_scan_emit(const u16* tok, i64 L, int k, const u32* bm_in, u32* bm_out, const u64* vt, u64 vcap,
                             const u32* vrep, const u16* x, u64* ev, u64 region, u32* ev_count, u32* flags, int grid,
-                            int sparse, u32* dhist, i64 dstride, const u32* pre, int wbits, int dbits, void* stream) {
+                            int sparse, u32* dhist, i64 dstride, const u32* pre, int wbits, int dbits, int mbits,
+                            void* stream) {
     if (grid <= 0 || region == 0 || region > 0xFFFFFFFFull || (dhist && dstride < grid)) return -1;
-    if (!emit_mode_ok(wbits, dbits)) return -1;
+    if (!emit_mode_ok(wbits, dbits, mbits)) return -1;
     if (L <= 0) {
         fill_u32_n(ev_count, 0u, grid, (hipStream_t)stream);
         if (dhist)
@@ -800,7 +807,7 @@ extern "C" int ng_scan_emit(const u16* tok, i64 L, int k, const u32* bm_in, u32*
                 fill_u32_n(dhist + (i64)d * dstride, 0u, grid, (hipStream_t)stream);
         return (int)hipGetLastError();
     }
-    const EmitSink sk{ev, region, ev_count, 0, nullptr, dhist, dstride, 0, wbits, dbits};
+    const EmitSink sk{ev, region, ev_count, 0, nullptr, dhist, dstride, 0, wbits, dbits, mbits};
     if (launch_scan(tok, L, k, bm_in, bm_out, vt, vcap, vrep, x, sk, flags, grid, sparse, (hipStream_t)stream, pre) != 0)
         return -1;
     return (int)hipGetLastError();
@@ -808,15 +815,17 @@ extern "C" int ng_scan_emit(const u16* tok, i64 L, int k, const u32* bm_in, u32*
 
 // The emitting scan over listed positions: the first *n_dev entries of plist (shard-relative corpus positions, a
 // device-side count, so no host sync), hits' events appended as ng_scan_emit's (block b of `grid` to
-// ev[b * region ...], their number in ev_count[b], events and digit histograms by wbits / dbits as ng_scan_emit's),
+// ev[b * region ...], their number in ev_count[b], events and digit histograms by wbits / dbits / mbits as
+// ng_scan_emit's),
 // and each hit's bit set in bm_out (zeroed by the caller; may be NULL). region >= ceil(n_max / (grid * 256)) * 256
 // for n_max >= *n_dev.
 extern "C" int ng_scan_emit_list(const u16* tok, const u64* plist, const u64* n_dev, int k, const u64* vt, u64 vcap,
                                  const u32* vrep, const u16* x, u32* bm_out, u64* ev, u64 region, u32* ev_count,
-                                 u32* flags, int grid, u32* dhist, i64 dstride, int wbits, int dbits, void* stream) {
+                                 u32* flags, int grid, u32* dhist, i64 dstride, int wbits, int dbits, int mbits,
+                                 void* stream) {
     if (grid <= 0 || n_dev == nullptr || region == 0 || region > 0xFFFFFFFFull || (dhist && dstride < grid)) return -1;
-    if (!emit_mode_ok(wbits, dbits)) return -1;
-    const EmitSink sk{ev, region, ev_count, 0, nullptr, dhist, dstride, 0, wbits, dbits};
+    if (!emit_mode_ok(wbits, dbits, mbits)) return -1;
+    const EmitSink sk{ev, region, ev_count, 0, nullptr, dhist, dstride, 0, wbits, dbits, mbits};
     hipStream_t st = (hipStream_t)stream;
     LEVEL_DISPATCH(k, (scan_list_k<K, EmitSink><<<grid, 256, 0, st>>>(tok, plist, 0, k, vt, vcap, vrep, x, sk, flags, n_dev,
                                                                      bm_out)));

@@ -124,11 +124,11 @@ __global__ void msd_starts_k(const i64* __restrict__ bstart, const u32* __restri
     start[p] = nt ? (i64)hscan[((u64)tfirst[b] << nbits) + (u64)d * nt] : bstart[b];
 }
 
-// Lookup j of query position i = pos[j] (pos NULL: i = j): wmix(ctx_of[i] << 16 | tgt[i], W) << (64 - W) for context
-// ids in [lo, hi) (the partition digits then are its top bits, as the events'), else EMPTY (no such key: its low
-// 64 - W bits are ones); value i.
+// Lookup j of query position i = pos[j] (pos NULL: i = j): kmix(ctx_of[i] << 16 | tgt[i], W, M) << (64 - W) for
+// context ids in [lo, hi) (the partition digits then are its top bits, as the events'), else EMPTY (no such key: its
+// low 64 - W bits are ones); value i.
 __global__ void lookups_w_k(const int* __restrict__ ctx_of, const u16* __restrict__ tgt, const int* __restrict__ pos,
-                            i64 n, const u64* __restrict__ n_dev, i64 lo, i64 hi, int W, u64* __restrict__ qk,
+                            i64 n, const u64* __restrict__ n_dev, i64 lo, i64 hi, int W, int M, u64* __restrict__ qk,
                             u32* __restrict__ qv) {
     const i64 j = blockIdx.x * (i64)blockDim.x + threadIdx.x;
     if (j >= n) return;
@@ -139,7 +139,7 @@ __global__ void lookups_w_k(const int* __restrict__ ctx_of, const u16* __restric
     }
     const i64 i = pos ? pos[j] : j;
     const i64 c = ctx_of[i];
-    qk[j] = (c >= lo && c < hi) ? wmix(((u64)c << 16) | tgt[i], W) << (64 - W) : EMPTY;
+    qk[j] = (c >= lo && c < hi) ? kmix(((u64)c << 16) | tgt[i], W, M) << (64 - W) : EMPTY;
     qv[j] = (u32)i;
 }
 
@@ -199,13 +199,14 @@ __global__ void __launch_bounds__(256) sel_write_k(const int* __restrict__ v, i6
 // positions, qstart their partitions' bounds: qcnt[qv[j]] = the pair's count or 0. A partition reaching `limit`
 // distinct pairs (at most P32_LIMIT) sets flags[0] bit 0; its count may be incomplete.
 __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ ev, const i64* __restrict__ start,
-                                                      i64 P, int pbits, int W, const u64* __restrict__ qk,
+                                                      i64 P, int pbits, int W, int M, const u64* __restrict__ qk,
                                                       const u32* __restrict__ qv, const i64* __restrict__ qstart,
                                                       u64* __restrict__ out_k, int cb, u64* esc_k, u32* esc_c,
                                                       u64 esc_cap, u32* __restrict__ seg_cnt,
                                                       i64* __restrict__ seg_base, u32* __restrict__ qcnt,
                                                       u32* __restrict__ dhist, int dshift, int dbits, u32 limit,
-                                                      u32* flags, u64* __restrict__ slab) {
+                                                      u32* flags, u64* __restrict__ slab, i64* __restrict__ runs,
+                                                      int gbits, int gshift, u64* n_words) {
     __shared__ __align__(16) u32 tk[P32_SLOTS];
     __shared__ u32 tc[P32_SLOTS];
     __shared__ u16 list[P32_SLOTS];
@@ -216,7 +217,7 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
     const u32 lmask = (1u << lbits) - 1u;
     const i64 n_ev = start[P], G = gridDim.x;
     const i64 p0 = part_first(start, P, n_ev, G, blockIdx.x), p1 = part_first(start, P, n_ev, G, blockIdx.x + 1);
-    const int nd = 1 << dbits;
+    const int nd = runs ? 0 : 1 << dbits;  // with runs: no words' histogram
     if (p0 >= p1) {
         if (t == 0) {
             seg_cnt[blockIdx.x] = 0;
@@ -245,8 +246,19 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
     u32 ahead[P32_ITEMS];
     i64 ahead_of = -1;
     const u64 esc = (1ull << (48 - cb)) - 1;
+    const i64 e_end = start[p1];  // the end of the block's events
     for (i64 p = p0; p < p1; ++p) {
         const i64 a = start[p], b = start[p + 1], qa = qstart[p], qb = qstart[p + 1];
+        if (a == e_end && !slab) {
+            // this partition and the block's later ones hold no events (the trailing partitions of a level whose
+            // context ids fill only part of their bit range, all of them the last block's): no words, and their
+            // lookups' counts stay 0; their runs, empty, are written at once
+            if (runs) {
+                const i64 ng1 = (1ll << gbits) + 1, base = out_base + (i64)cur;
+                for (i64 x = t; x < (p1 - p) * ng1; x += P32_BLOCK) runs[p * ng1 + x] = base;
+            }
+            break;
+        }
         const bool has_q = qa + t < qb;
         u64 lk = EMPTY;
         u32 lv = 0;
@@ -380,16 +392,58 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
             for (int j = t; j < P32_SLOTS; j += P32_BLOCK) sp[j] = ((u64)tc[j] << 32) | tk[j];
             lds_barrier();  // read before the output pass empties the slots
         }
-        for (u32 i = t; i < nl; i += P32_BLOCK) {
-            const int j = list[i];
-            const u32 key = tk[j], n = tc[j];
-            tk[j] = EMPTY32;
-            tc[j] = 0;
-            const u64 pk = unwmix(((u64)p << lbits) | key, W);
-            const u64 word = (pk << (48 - cb)) | ((u64)n < esc ? (u64)n : esc);
-            out_k[(u64)out_base + cur + i] = word;
-            if ((u64)n >= esc) esc_put(esc_k, esc_c, esc_cap, pk, n, flags);
-            atomicAdd(&dh[(u32)(word >> dshift) & (u32)(nd - 1)], 1u);
+        if (runs) {
+            // the partition's words grouped by the gbits-bit digit (pair key >> gshift) of their context ids (an LDS
+            // count, a scan by wave 0, then a slot per word from the group's cursor), group s's run of words at
+            // [runs[p * (2^gbits + 1) + s], runs[p * (2^gbits + 1) + s + 1]) of out_k
+            const u32 ng = 1u << gbits, gm = ng - 1u;
+            if (t < (int)ng) dh[t] = 0;
+            lds_barrier();
+            for (u32 i = t; i < nl; i += P32_BLOCK) {
+                const u64 pk = unkmix(((u64)p << lbits) | tk[list[i]], W, M);
+                atomicAdd(&dh[(u32)(pk >> gshift) & gm], 1u);
+            }
+            lds_barrier();
+            if (t < WAVE) {
+                const u32 c = t < (int)ng ? dh[t] : 0u;
+                u32 incl = c;
+#pragma unroll
+                for (int d = 1; d < WAVE; d <<= 1) {
+                    const u32 o = (u32)__shfl_up((int)incl, d, WAVE);
+                    if (lane >= d) incl += o;
+                }
+                i64* rp = runs + p * (i64)(ng + 1);
+                const i64 base = out_base + (i64)cur;
+                if (t < (int)ng) {
+                    rp[t] = base + (i64)(incl - c);
+                    dh[t] = incl - c;
+                }
+                if (t == (int)ng - 1) rp[ng] = base + (i64)incl;
+            }
+            lds_barrier();
+            for (u32 i = t; i < nl; i += P32_BLOCK) {
+                const int j = list[i];
+                const u32 key = tk[j], n = tc[j];
+                tk[j] = EMPTY32;
+                tc[j] = 0;
+                const u64 pk = unkmix(((u64)p << lbits) | key, W, M);
+                const u64 word = (pk << (48 - cb)) | ((u64)n < esc ? (u64)n : esc);
+                const u32 at = atomicAdd(&dh[(u32)(pk >> gshift) & gm], 1u);
+                out_k[(u64)out_base + cur + at] = word;
+                if ((u64)n >= esc) esc_put(esc_k, esc_c, esc_cap, pk, n, flags);
+            }
+        } else {
+            for (u32 i = t; i < nl; i += P32_BLOCK) {
+                const int j = list[i];
+                const u32 key = tk[j], n = tc[j];
+                tk[j] = EMPTY32;
+                tc[j] = 0;
+                const u64 pk = unkmix(((u64)p << lbits) | key, W, M);
+                const u64 word = (pk << (48 - cb)) | ((u64)n < esc ? (u64)n : esc);
+                out_k[(u64)out_base + cur + i] = word;
+                if ((u64)n >= esc) esc_put(esc_k, esc_c, esc_cap, pk, n, flags);
+                atomicAdd(&dh[(u32)(word >> dshift) & (u32)(nd - 1)], 1u);
+            }
         }
         cur += nl;
         if (t == 0) nocc = 0;
@@ -398,6 +452,7 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
     if (t == 0) {
         seg_cnt[blockIdx.x] = cur;
         seg_base[blockIdx.x] = out_base;
+        if (n_words && cur) atomicAdd((unsigned long long*)n_words, (unsigned long long)cur);
     }
     for (int d = t; d < nd; d += P32_BLOCK) dhist[(i64)d * G + blockIdx.x] = dh[d];
 }
@@ -405,15 +460,113 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
 // Per context from packed words grouped by context: partition q (words [start[q], start[q + 1])) holds the
 // contexts of ids [q << ibits, (q + 1) << ibits), 2^ibits <= AGG_IDS_FOR(KT). A block takes partitions q, q + grid,
 // ... in turn and streams each one's words once, accumulating per id its total, its pairs and its top KT scores
-// (count << 16 | 65535 - token) in LDS. The top scores come from a cascade of atomic maxima: a score displaced from (or kept out of) slot r goes on to
-// slot r + 1, so slot r ends with the r-th largest; a score not above slot KT - 1's current value (which only grows,
-// and below which KT larger scores already exist) is not inserted. Then every id of the partition below n_ids gets
-// dist[c] = its pairs and, if present, its record (CtxRecord<KT>, first-word index 0); with `deep`, every context of
-// more than deep_min pairs is appended to deep (*deep_n counts them). flags[0] bit 2: a total reached 2^32.
+// (count << 16 | 65535 - token) in LDS. The top scores come from a cascade of atomic maxima: a score displaced from
+// (or kept out of) slot r goes on to slot r + 1, so slot r ends with the r-th largest; a score not above slot
+// KT - 1's current value (which only grows, and below which KT larger scores already exist) is not inserted. Then
+// every id of the partition below n_ids gets dist[c] = its pairs and, if present, its record (CtxRecord<KT>,
+// first-word index 0); with `deep`, every context of more than deep_min pairs is appended to deep (*deep_n counts
+// them). flags[0] bit 2: a total reached 2^32.
 #define AGG_BLOCK 1024
 #define AGG_IDS 2048
 // the ids of a partition at most for top KT: 1024 for KT 8, so that its LDS (72 KB) lets two blocks share a CU
 #define AGG_IDS_FOR(KT) ((KT) >= 8 ? AGG_IDS / 2 : AGG_IDS)
+#define AGG_RUN_REGS 4  // ctx_agg_runs_k: the runs a lane holds (at most 64 times this per group)
+
+// One round's words into a group's LDS sums (lo: the group's first id, nid its ids; vb: the wave's valid lanes).
+template <int KT>
+__device__ __forceinline__ void agg_round(u64 word, bool valid, u64 vb, i64 lo, int nid, int cb,
+                                          const u64* __restrict__ esc_k, const u32* __restrict__ esc_c, u64 esc_cap,
+                                          u32* s_tot, u32* s_dist, u64* s_top, u32* flags) {
+    const int lane = lane_id(), sh = 64 - cb, csh = 48 - cb;
+    const u64 esc = (1ull << csh) - 1;
+    const int lid = (int)((i64)(word >> sh) - lo) & (nid - 1);
+    u32 n = 0;
+    if (valid) {
+        const u64 n64 = word & esc;
+        n = n64 < esc ? (u32)n64 : esc_get(esc_k, esc_c, esc_cap, word >> csh);
+    }
+    // the lanes of the wave's first context add its total and pairs once when many share it (a context with many
+    // pairs would serialize the LDS atomics on its two counters)
+    const int ld = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)vb) - 1);
+    const int l0 = __builtin_amdgcn_readlane(lid, ld);
+    const bool same = valid && lid == l0;
+    const u64 m = __ballot(same);
+    bool own = valid;
+    if (__popcll(m) > 4) {  // wave-uniform
+        u64 sm = same ? n : 0;
+#pragma unroll
+        for (int d = WAVE / 2; d > 0; d >>= 1) sm += shfl_down_u64(sm, d);
+        sm = bcast_u64(sm, 0);
+        if (lane == ld) {
+            const u32 old = atomicAdd(&s_tot[l0], (u32)sm);
+            if ((sm >> 32) || old + (u32)sm < old) atomicOr(&flags[0], 4u);
+            atomicAdd(&s_dist[l0], (u32)__popcll(m));
+        }
+        own = valid && !same;
+    }
+    if (own) {
+        const u32 old = atomicAdd(&s_tot[lid], n);
+        if (old + n < old) atomicOr(&flags[0], 4u);
+        atomicAdd(&s_dist[lid], 1u);
+    }
+    if (valid) {
+        u64 v = rank_score(word >> csh, n);
+        u64* tp = &s_top[lid * KT];
+        if (v > __hip_atomic_load(&tp[KT - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) {
+#pragma unroll
+            for (int r = 0; r < KT; ++r) {
+                if (!v) break;
+                const u64 o = atomicMax((unsigned long long*)&tp[r], (unsigned long long)v);
+                v = o < v ? o : v;
+            }
+        }
+    }
+}
+
+// A group's ids below n_ids out of LDS: dist, records of the present ones, the deep list; returns this thread's
+// present contexts.
+template <int KT>
+__device__ __forceinline__ u32 agg_flush(i64 lo, int nid, i64 n_ids, const u32* s_tot, const u32* s_dist,
+                                         const u64* s_top, u32* __restrict__ rec, u32* __restrict__ dist,
+                                         u32 deep_min, i64* __restrict__ deep, u64 deep_cap, u64* deep_n) {
+    u32 mine = 0;
+    const int nl = n_ids - lo < nid ? (int)(n_ids - lo) : nid;
+    for (int l = threadIdx.x; l < nl; l += AGG_BLOCK) {
+        const i64 c = lo + l;
+        const u32 d = s_dist[l];
+        if (dist) dist[c] = d;
+        if (d) {
+            ++mine;
+            u64 top[KT];
+#pragma unroll
+            for (int r = 0; r < KT; ++r) top[r] = s_top[l * KT + r];
+            store_record<KT>(rec, (u64)c, s_tot[l], d, top, 0);
+            if (deep && d > deep_min) {
+                const u64 at = atomicAdd((unsigned long long*)deep_n, 1ull);
+                if (at < deep_cap) deep[at] = c;
+            }
+        }
+    }
+    return mine;
+}
+
+template <int KT>
+__device__ __forceinline__ void agg_clear(int nid, u32* s_tot, u32* s_dist, u64* s_top) {
+    for (int l = threadIdx.x; l < nid; l += AGG_BLOCK) {
+        s_tot[l] = 0;
+        s_dist[l] = 0;
+    }
+    for (int l = threadIdx.x; l < nid * KT; l += AGG_BLOCK) s_top[l] = 0;
+}
+
+// *present += the block's present contexts (one atomic per wave).
+__device__ __forceinline__ void agg_present(u32 mine, u64* present) {
+    u32 sm = mine;
+#pragma unroll
+    for (int d = WAVE / 2; d > 0; d >>= 1) sm += (u32)__shfl_down((int)sm, d, WAVE);
+    if (lane_id() == 0 && sm) atomicAdd((unsigned long long*)present, (unsigned long long)sm);
+}
+
 // Two blocks share a compute unit where the LDS allows (KT <= 4: 80 KB each): 8 waves per SIMD, so at most 96
 // scalar registers a wave (amdgpu_waves_per_eu), which the kernel's arguments and walk state would otherwise exceed.
 template <int KT>
@@ -425,9 +578,7 @@ __global__ void __launch_bounds__(AGG_BLOCK) __attribute__((amdgpu_waves_per_eu(
                                                        u64 deep_cap, u64* deep_n, u64* present) {
     __shared__ u32 s_tot[AGG_IDS_FOR(KT)], s_dist[AGG_IDS_FOR(KT)];
     __shared__ u64 s_top[AGG_IDS_FOR(KT) * KT];
-    const int t = threadIdx.x, lane = lane_id();
-    const int sh = 64 - cb, csh = 48 - cb;
-    const u64 esc = (1ull << csh) - 1;
+    const int t = threadIdx.x;
     const int nid = 1 << ibits;
     // a block walks its partitions with the next round's words (this partition's, else the next partition's first)
     // and the next partition's bounds loaded ahead, so their latency hides behind the LDS work
@@ -447,11 +598,7 @@ __global__ void __launch_bounds__(AGG_BLOCK) __attribute__((amdgpu_waves_per_eu(
         const i64 lo = q << ibits;
         if (lo >= n_ids) break;  // partitions ascend with q
         const bool more = q + gridDim.x < P;
-        for (int l = t; l < nid; l += AGG_BLOCK) {
-            s_tot[l] = 0;
-            s_dist[l] = 0;
-        }
-        for (int l = t; l < nid * KT; l += AGG_BLOCK) s_top[l] = 0;
+        agg_clear<KT>(nid, s_tot, s_dist, s_top);
         lds_barrier();
         if (wa >= we) ahead = w[more && nwa + t < nwe ? nwa + t : 0];  // an empty partition: the next one's words
         for (i64 i0 = wa; i0 < we; i0 += AGG_BLOCK) {  // the same rounds for every wave
@@ -463,67 +610,10 @@ __global__ void __launch_bounds__(AGG_BLOCK) __attribute__((amdgpu_waves_per_eu(
             ahead = w[j];
             const u64 vb = __ballot(valid);
             if (!vb) continue;
-            const int lid = (int)((i64)(word >> sh) - lo) & (nid - 1);
-            u32 n = 0;
-            if (valid) {
-                const u64 n64 = word & esc;
-                n = n64 < esc ? (u32)n64 : esc_get(esc_k, esc_c, esc_cap, word >> csh);
-            }
-            // the lanes of the wave's first context add its total and pairs once when many share it (a context with
-            // many pairs would serialize the LDS atomics on its two counters)
-            const int ld = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)vb) - 1);
-            const int l0 = __builtin_amdgcn_readlane(lid, ld);
-            const bool same = valid && lid == l0;
-            const u64 m = __ballot(same);
-            bool own = valid;
-            if (__popcll(m) > 4) {  // wave-uniform
-                u64 sm = same ? n : 0;
-#pragma unroll
-                for (int d = WAVE / 2; d > 0; d >>= 1) sm += shfl_down_u64(sm, d);
-                sm = bcast_u64(sm, 0);
-                if (lane == ld) {
-                    const u32 old = atomicAdd(&s_tot[l0], (u32)sm);
-                    if ((sm >> 32) || old + (u32)sm < old) atomicOr(&flags[0], 4u);
-                    atomicAdd(&s_dist[l0], (u32)__popcll(m));
-                }
-                own = valid && !same;
-            }
-            if (own) {
-                const u32 old = atomicAdd(&s_tot[lid], n);
-                if (old + n < old) atomicOr(&flags[0], 4u);
-                atomicAdd(&s_dist[lid], 1u);
-            }
-            if (valid) {
-                u64 v = rank_score(word >> csh, n);
-                u64* tp = &s_top[lid * KT];
-                if (v > __hip_atomic_load(&tp[KT - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) {
-#pragma unroll
-                    for (int r = 0; r < KT; ++r) {
-                        if (!v) break;
-                        const u64 o = atomicMax((unsigned long long*)&tp[r], (unsigned long long)v);
-                        v = o < v ? o : v;
-                    }
-                }
-            }
+            agg_round<KT>(word, valid, vb, lo, nid, cb, esc_k, esc_c, esc_cap, s_tot, s_dist, s_top, flags);
         }
         lds_barrier();
-        const int nl = n_ids - lo < nid ? (int)(n_ids - lo) : nid;
-        for (int l = t; l < nl; l += AGG_BLOCK) {
-            const i64 c = lo + l;
-            const u32 d = s_dist[l];
-            if (dist) dist[c] = d;
-            if (d) {
-                ++mine;
-                u64 top[KT];
-#pragma unroll
-                for (int r = 0; r < KT; ++r) top[r] = s_top[l * KT + r];
-                store_record<KT>(rec, (u64)c, s_tot[l], d, top, 0);
-                if (deep && d > deep_min) {
-                    const u64 at = atomicAdd((unsigned long long*)deep_n, 1ull);
-                    if (at < deep_cap) deep[at] = c;
-                }
-            }
-        }
+        mine += agg_flush<KT>(lo, nid, n_ids, s_tot, s_dist, s_top, rec, dist, deep_min, deep, deep_cap, deep_n);
         lds_barrier();  // the LDS is read before the next partition clears it
         if (!more) break;
         q += gridDim.x;
@@ -534,12 +624,102 @@ __global__ void __launch_bounds__(AGG_BLOCK) __attribute__((amdgpu_waves_per_eu(
             nwe = start[q + gridDim.x + 1];
         }
     }
-    if (present) {  // one atomic per wave (a few hundred blocks)
-        u32 sm = mine;
+    if (present) agg_present(mine, present);
+}
+
+// ctx_agg_k over ng_part_count32's words left in runs (its `runs` mode, events keyed by kmix(pair key, W, W - d1)):
+// group g = b << gbits | s (bucket b of the first pass's d1 bits, sub-group s of the gbits context-id bits below
+// them) holds the ids [g << ibits, (g + 1) << ibits), and its words are run s of each of the bucket's 2^d2 <= 256
+// partitions b << d2 | j. A block takes groups g, g + grid, ... and streams a group's words as one sequence: every
+// wave holds the group's runs in its lanes (lane l: runs l, 64 + l, 128 + l and 192 + l, their starts and the
+// exclusive scan of the lengths; no LDS, so that two blocks still share a compute unit). A wave's 64 consecutive words span few runs: the
+// run of its first word is the count of runs starting at or before it, and the runs starting inside its window are
+// walked with lane reads. The next round's words are loaded ahead, as ctx_agg_k's. Outputs as ctx_agg_k's, without
+// the deep list.
+template <int KT>
+__global__ void __launch_bounds__(AGG_BLOCK) __attribute__((amdgpu_waves_per_eu(8))) ctx_agg_runs_k(const u64* __restrict__ w, const i64* __restrict__ runs,
+                                                       i64 NG, int d2, int gbits, int ibits, int cb, i64 n_ids,
+                                                       const u64* __restrict__ esc_k, const u32* __restrict__ esc_c,
+                                                       u64 esc_cap, u32* __restrict__ rec, u32* __restrict__ dist,
+                                                       u32* flags, u64* present) {
+    __shared__ u32 s_tot[AGG_IDS_FOR(KT)], s_dist[AGG_IDS_FOR(KT)];
+    __shared__ u64 s_top[AGG_IDS_FOR(KT) * KT];
+    const int t = threadIdx.x, lane = lane_id();
+    const u32 wbase = (u32)(t & ~(WAVE - 1));  // the wave's first thread
+    const int nid = 1 << ibits, R = 1 << d2, gs = (1 << gbits) + 1;
+    u32 mine = 0;
+    for (i64 g = blockIdx.x; g < NG; g += gridDim.x) {
+        const i64 lo = g << ibits;
+        if (lo >= n_ids) break;  // groups ascend with g
+        const i64 b = g >> gbits, s = g & ((1 << gbits) - 1);
+        agg_clear<KT>(nid, s_tot, s_dist, s_top);
+        // word indexes are below 2^32 (the count's capacity)
+        const i64* rp = runs + (b << d2) * gs + s;
+        u32 rlo[AGG_RUN_REGS], rpre[AGG_RUN_REGS], tot = 0;
 #pragma unroll
-        for (int d = WAVE / 2; d > 0; d >>= 1) sm += (u32)__shfl_down((int)sm, d, WAVE);
-        if (lane == 0 && sm) atomicAdd((unsigned long long*)present, (unsigned long long)sm);
+        for (int h = 0; h < AGG_RUN_REGS; ++h) {
+            const int j = h * WAVE + lane;
+            u32 len = 0;
+            rlo[h] = 0;
+            if (j < R) {
+                const i64 a = rp[(i64)j * gs], e = rp[(i64)j * gs + 1];
+                rlo[h] = (u32)a;
+                len = (u32)(e - a);
+            }
+            u32 incl = len;
+#pragma unroll
+            for (int d = 1; d < WAVE; d <<= 1) {
+                const u32 o = (u32)__shfl_up((int)incl, d, WAVE);
+                if (lane >= d) incl += o;
+            }
+            rpre[h] = tot + incl - len;  // runs past R: the total, never at or below a word
+            tot += (u32)__builtin_amdgcn_readlane((int)incl, WAVE - 1);
+        }
+        lds_barrier();
+        // the index in w of word base + lane (base wave-uniform; meaningful below tot): its run is the last whose
+        // scan is at or below it (a run of length 0 shares its start with the next, which the walk then takes)
+        auto at = [&](u32 base) -> u32 {
+            const u32 i = base + (u32)lane, last = base + (WAVE - 1);
+            int j = -1;  // wave-uniform
+#pragma unroll
+            for (int h = 0; h < AGG_RUN_REGS; ++h) j += __popcll(__ballot(rpre[h] <= base));
+            u32 plo = 0, ppre = 0;
+            for (; j < R; ++j) {
+                u32 pj = 0, lj = 0;
+#pragma unroll
+                for (int h = 0; h < AGG_RUN_REGS; ++h)
+                    if ((j >> 6) == h) {  // wave-uniform
+                        pj = (u32)__builtin_amdgcn_readlane((int)rpre[h], j & (WAVE - 1));
+                        lj = (u32)__builtin_amdgcn_readlane((int)rlo[h], j & (WAVE - 1));
+                    }
+                if (pj > last) break;
+                if (i >= pj) {
+                    plo = lj;
+                    ppre = pj;
+                }
+            }
+            return plo + (i - ppre);
+        };
+        if (tot) {  // wave-uniform
+            const u32 a0 = at(wbase);
+            u64 ahead = w[(u32)t < tot ? a0 : 0u];
+            for (u32 i0 = 0; i0 < tot; i0 += AGG_BLOCK) {  // the same rounds for every wave
+                const u32 i = i0 + (u32)t;
+                const bool valid = i < tot;
+                const u64 word = valid ? ahead : 0;
+                const u32 nx = i + AGG_BLOCK;
+                const u32 ad = at(i0 + AGG_BLOCK + wbase);
+                ahead = w[nx < tot ? ad : 0u];  // unconditional: word 0 always exists
+                const u64 vb = __ballot(valid);
+                if (!vb) continue;
+                agg_round<KT>(word, valid, vb, lo, nid, cb, esc_k, esc_c, esc_cap, s_tot, s_dist, s_top, flags);
+            }
+        }
+        lds_barrier();
+        mine += agg_flush<KT>(lo, nid, n_ids, s_tot, s_dist, s_top, rec, dist, 0, nullptr, 0, nullptr);
+        lds_barrier();  // the LDS is read before the next group clears it
     }
+    if (present) agg_present(mine, present);
 }
 
 static inline int grid_cap(i64 n, int cap) { return n < 1 ? 1 : n > cap ? cap : (int)n; }
@@ -620,14 +800,16 @@ extern "C" int ng_msd_pass_narrow(void* temp, size_t* temp_bytes, const u64* key
                               (hipStream_t)stream);
 }
 
-// The lookups of n query positions (pos[j], or j with pos NULL) for the 32-bit count: qk[j] = wmix(ctx_of[i] << 16 |
-// tgt[i], W) << (64 - W) for context ids in [lo, hi) (below 2^(W - 16)), else EMPTY; qv[j] = i. n_dev (may be NULL):
-// a device-side count of pos's entries; lookups j >= *n_dev are EMPTY.
+// The lookups of n query positions (pos[j], or j with pos NULL) for the 32-bit count: qk[j] = kmix(ctx_of[i] << 16 |
+// tgt[i], W, M) << (64 - W) (part.h; M 0: W) for context ids in [lo, hi) (below 2^(W - 16)), else EMPTY; qv[j] = i.
+// n_dev (may be NULL): a device-side count of pos's entries; lookups j >= *n_dev are EMPTY.
 extern "C" int ng_part_lookups_w(const int* ctx_of, const u16* tgt, const int* pos, i64 n, const u64* n_dev, i64 lo,
-                                 i64 hi, int W, u64* qk, u32* qv, void* stream) {
-    if (W < 17 || W > 63 || lo < 0 || hi > (1ll << (W - 16)) || (n_dev && !pos)) return -1;
+                                 i64 hi, int W, int M, u64* qk, u32* qv, void* stream) {
+    if (M == 0) M = W;
+    if (W < 17 || W > 63 || M < 17 || M > W || lo < 0 || hi > (1ll << (W - 16)) || (n_dev && !pos)) return -1;
     if (n <= 0) return 0;
-    lookups_w_k<<<grid_for(n, 256), 256, 0, (hipStream_t)stream>>>(ctx_of, tgt, pos, n, n_dev, lo, hi, W, qk, qv);
+    lookups_w_k<<<grid_for(n, 256), 256, 0, (hipStream_t)stream>>>(ctx_of, tgt, pos, n, n_dev, lo, hi, W, M, qk,
+                                                                     qv);
     return (int)hipGetLastError();
 }
 
@@ -655,29 +837,39 @@ extern "C" int ng_select_positive(void* temp, size_t* temp_bytes, const int* v, 
 }
 
 // Count the 32-bit events (ng_msd_pass's output; start its partitions' starts, 2^pbits of them, 1 <= W - pbits <=
-// 31, W the pair-key bits) partition by partition with `grid` blocks of about equal events (at most 65536): block
-// b's distinct pairs as packed words pair key << (48 - cb) | min(count, esc), esc = 2^(48 - cb) - 1 (larger counts
-// also in the escape table; context ids below 2^(W - 16), W - 16 <= cb <= 44), at out_k + seg_base[b], seg_cnt[b] of
-// them (out_k holds as many words as there are events); dhist[d * grid + b] block b's words per dbits-bit digit
-// (word >> dshift) & (2^dbits - 1) (1 <= dbits <= 11), for ng_seg_scatter. Lookups (ng_part_lookups_w's, sorted by
+// 31, W the pair-key bits; events kmix(pair key, W, M), part.h, M 0: W) partition by partition with `grid` blocks of
+// about equal events (at most 65536): block b's distinct pairs as packed words pair key << (48 - cb) | min(count,
+// esc), esc = 2^(48 - cb) - 1 (larger counts also in the escape table; context ids below 2^(W - 16), W - 16 <= cb <=
+// 44), at out_k + seg_base[b], seg_cnt[b] of them (out_k holds as many words as there are events); dhist[d * grid +
+// b] block b's words per dbits-bit digit (word >> dshift) & (2^dbits - 1) (1 <= dbits <= 11), for ng_seg_scatter.
+// runs (may be NULL; dhist is then unused and may be NULL): each partition's words are written grouped by the
+// gbits-bit digit (pair key >> gshift) & (2^gbits - 1) (0 <= gbits <= 6, 16 <= gshift, gshift + gbits <= W), group s
+// of partition p at out_k[runs[p * (2^gbits + 1) + s] ...  runs[p * (2^gbits + 1) + s + 1]). n_words (may be NULL):
+// += the words written (the distinct pairs; one atomic per block). Lookups (ng_part_lookups_w's, sorted by
 // their top pbits; qstart their partitions' bounds; qk and qv may be NULL with qstart all zeros: none) get qcnt[qv[j]]
 // = the pair's count or 0. flags[0] bit 0: a partition reached min(limit, 11000) distinct pairs (its count is
 // incomplete: count again with a bit more); bit 1: the escape table is full. slab (may be NULL): 2^pbits * 14336
 // u64, partition p's table written to slab + p * 14336 (slot = count << 32 | key, pairs32.h's layout), for queries
 // of the counts after the build (p32_pair_count).
-extern "C" int ng_part_count32(const u32* ev, const i64* start, int pbits, int W, const u64* qk, const u32* qv,
-                               const i64* qstart, u64* out_k, int cb, u64* esc_k, u32* esc_c, u64 esc_cap,
-                               u32* seg_cnt, i64* seg_base, u32* qcnt, u32* dhist, int dshift, int dbits, u32 limit,
-                               u32* flags, int grid, u64* slab, void* stream) {
+extern "C" int ng_part_count32(const u32* ev, const i64* start, int pbits, int W, int M, const u64* qk,
+                               const u32* qv, const i64* qstart, u64* out_k, int cb, u64* esc_k, u32* esc_c,
+                               u64 esc_cap, u32* seg_cnt, i64* seg_base, u32* qcnt, u32* dhist, int dshift, int dbits,
+                               u32 limit, u32* flags, int grid, u64* slab, i64* runs, int gbits, int gshift,
+                               u64* n_words, void* stream) {
+    if (M == 0) M = W;
     if (pbits < 1 || pbits > 30 || W < 17 || W - 16 > cb || cb > 44 || W - pbits > 31 || W - pbits < 1 ||
-        grid <= 0 || grid > 65536 || esc_k == nullptr || esc_c == nullptr || esc_cap == 0 || dbits < 1 ||
-        dbits > 11 || dshift < 0 || dshift + dbits > 64 || dhist == nullptr || qstart == nullptr || limit == 0)
+        M < 17 || M > W || grid <= 0 || grid > 65536 || esc_k == nullptr || esc_c == nullptr || esc_cap == 0 ||
+        qstart == nullptr || limit == 0)
+        return -1;
+    if (runs ? (gbits < 0 || gbits > 6 || gshift < 16 || gshift + gbits > W)
+             : (dbits < 1 || dbits > 11 || dshift < 0 || dshift + dbits > 64 || dhist == nullptr))
         return -1;
     const i64 P = 1ll << pbits;
     limit = limit < P32_LIMIT ? limit : P32_LIMIT;
-    count32_k<<<grid, P32_BLOCK, 0, (hipStream_t)stream>>>(ev, start, P, pbits, W, qk, qv, qstart, out_k, cb, esc_k,
-                                                           esc_c, esc_cap, seg_cnt, seg_base, qcnt, dhist, dshift,
-                                                           dbits, limit, flags, slab);
+    count32_k<<<grid, P32_BLOCK, 0, (hipStream_t)stream>>>(ev, start, P, pbits, W, M, qk, qv, qstart, out_k, cb,
+                                                           esc_k, esc_c, esc_cap, seg_cnt, seg_base, qcnt, dhist,
+                                                           dshift, dbits, limit, flags, slab, runs, gbits, gshift,
+                                                           n_words);
     return (int)hipGetLastError();
 }
 
@@ -703,6 +895,35 @@ extern "C" int ng_ctx_agg(const u64* w, const i64* start, i64 P, int ibits, int 
 #define AGG_LAUNCH(KT)                                                                                         \
     ctx_agg_k<KT><<<g, AGG_BLOCK, 0, st>>>(w, start, P, ibits, cb, n_ids, esc_k, esc_c, esc_cap, rec, dist, flags, \
                                            deep_min, deep, deep_cap, deep_n, present)
+    switch (topk) {
+        case 1: AGG_LAUNCH(1); break;
+        case 2: AGG_LAUNCH(2); break;
+        case 4: AGG_LAUNCH(4); break;
+        case 8: AGG_LAUNCH(8); break;
+        default: return -1;
+    }
+#undef AGG_LAUNCH
+    return (int)hipGetLastError();
+}
+
+// ng_ctx_agg over ng_part_count32's words left in runs (its runs mode, with gbits and gshift = 16 + ibits): group g
+// (of NG = 2^(d1 + gbits), d1 the first pass's digit bits; ids [g << ibits, (g + 1) << ibits), ibits <= 11, 10 for
+// topk 8) is run g & (2^gbits - 1) of partitions (g >> gbits) << d2 ... + 2^d2 - 1 (0 <= d2 <= 8, 0 <= gbits <= 6;
+// word indexes below 2^32).
+// Outputs and grid as ng_ctx_agg's (no deep list).
+extern "C" int ng_ctx_agg_runs(const u64* w, const i64* runs, i64 NG, int d2, int gbits, int ibits, int cb,
+                               i64 n_ids, const u64* esc_k, const u32* esc_c, u64 esc_cap, int topk, u32* rec,
+                               u32* dist, u32* flags, u64* present, int grid, void* stream) {
+    if (cb < 1 || cb > 44 || ibits < 0 || (1 << ibits) > (topk >= 8 ? AGG_IDS_FOR(8) : AGG_IDS) || NG <= 0 ||
+        d2 < 0 || (1 << d2) > AGG_RUN_REGS * WAVE || gbits < 0 || gbits > 6 || (NG & ((1ll << gbits) - 1)) || esc_cap == 0 ||
+        n_ids < 0 || n_ids > (1ll << cb) || (NG << ibits) < n_ids || runs == nullptr)
+        return -1;
+    if (n_ids == 0) return 0;
+    const int g = grid_cap(NG, grid > 0 ? grid : 1 << 30);
+    hipStream_t st = (hipStream_t)stream;
+#define AGG_LAUNCH(KT)                                                                                             \
+    ctx_agg_runs_k<KT><<<g, AGG_BLOCK, 0, st>>>(w, runs, NG, d2, gbits, ibits, cb, n_ids, esc_k, esc_c, esc_cap, rec, \
+                                                dist, flags, present)
     switch (topk) {
         case 1: AGG_LAUNCH(1); break;
         case 2: AGG_LAUNCH(2); break;

@@ -47,6 +47,19 @@ __host__ __device__ __forceinline__ u64 unwmix(u64 h, int W) {
     return (h * WMIX_I1) & m;
 }
 
+// The 32-bit count's event key of a pair key x below 2^W: its bits from M up kept, the M bits below mixed by
+// wmix (17 <= M <= W). M = W spreads every context's pairs over all partitions; M = W - d1 keeps the top d1 bits of
+// the context id, so that the first pass's buckets are ranges of context ids and a bucket's partitions hold the
+// pairs of its contexts only (spread by the hash below those bits).
+__host__ __device__ __forceinline__ u64 kmix(u64 x, int W, int M) {
+    const u64 lo = (1ull << M) - 1ull;
+    return (x & ~lo & ((1ull << W) - 1ull)) | wmix(x & lo, M);
+}
+__host__ __device__ __forceinline__ u64 unkmix(u64 h, int W, int M) {
+    const u64 lo = (1ull << M) - 1ull;
+    return (h & ~lo & ((1ull << W) - 1ull)) | unwmix(h & lo, M);
+}
+
 // A wave-uniform lane's 64-bit value (readlane: no LDS traffic).
 __device__ __forceinline__ u64 readlane_u64(u64 v, int l) {
     const u32 lo = (u32)__builtin_amdgcn_readlane((int)(u32)v, l);

@@ -33,7 +33,8 @@ import torch
 
 from . import partcount
 from .lib import Lib, i32, u64
-from .partcount import W_MAX, check_summary, count32, count_events, emit_region, first_digit, summarize, w_bits
+from .partcount import (W_MAX, check_summary, count32, count_events, emit_region, first_digit, key_mbits, summarize,
+                        w_bits)
 from .qindex import QueryIndex
 
 SCAN_BLOCKS_PER_CU = 8  # level-scan blocks (grid-stride) per compute unit (c3 sweep: 8 fastest of 4-32)
@@ -174,7 +175,8 @@ class LevelBuild:
             if use32:
                 # the 32-bit count: records made without sorting the pairs, every size read once after the last level
                 c = count32(elib, seg, vi.ids, ktop, (vi.ctx_of, tgt, seen, seen_n), self.events_of.get(k),
-                            self.dratio.get(k, 1.0), ev_fn, self.min_pbits.get(k, 0), stat=stats[li])
+                            self.dratio.get(k, 1.0), ev_fn, self.min_pbits.get(k, 0), stat=stats[li],
+                            mbits=key_mbits(W))
                 del seg
                 checks32.append((k, li, c.pbits, vi.ids, seen_cap if seen_n is not None else -1))
                 sm = c
@@ -308,8 +310,9 @@ class LevelBuild:
 
     def _emit(self, k, vi, x, bms, regions, R, wbits=0, flags=None):
         """Level k's scan of every shard it counts, hits emitted to per-block regions with each block's top-digit
-        histogram: count_events' seg = (regions, R, ev_count, dhist, nseg, flags). wbits: events wmix(pair key,
-        wbits) with histograms of their first_digit(wbits) top bits (count32's), else mix64(pair key). flags: the
+        histogram: count_events' seg = (regions, R, ev_count, dhist, nseg, flags). wbits: events kmix(pair key,
+        wbits, key_mbits(wbits)) (keyed by context range) with histograms of their first_digit(wbits) top bits
+        (count32's), else mix64(pair key). flags: the
         scan's two int32 flags (zeroed; e.g. a view into the build's stats), else new."""
         elib, dev, G = self.elib, self.tok.device, self.grid
         shards = [i for i in range(len(self.sizes)) if i < self.level_shards[k]]
@@ -317,6 +320,7 @@ class LevelBuild:
         ev_count = elib.zeros(max(nseg, 1), torch.int32, dev)
         last = self.events_of.get(k)
         dbits = first_digit(wbits) if wbits else 8
+        mbits = key_mbits(wbits) if wbits else 0
         dhist = torch.empty((1 << dbits) * max(nseg, 1), dtype=torch.int32, device=dev) \
             if wbits or last is None or last >= partcount.SEG_MIN_EVENTS * nseg else None
         if flags is None:
@@ -352,11 +356,11 @@ class LevelBuild:
             if mode == 3:
                 elib("ng_scan_emit_list", self.tok[st:], self._plist, n_list, i32(k), vi.table, u64(vi.cap), vi.rep,
                      x, bms[k][st // 32 :], regions[j * G * R :], u64(R), ev_count[j * G :], flags, i32(G), dh, nseg,
-                     i32(wbits), i32(dbits))
+                     i32(wbits), i32(dbits), i32(mbits))
             else:
                 elib("ng_scan_emit", self.tok[st:], n32, i32(k), bm_in, bms[k][st // 32 :], vi.table, u64(vi.cap),
                      vi.rep, x, regions[j * G * R :], u64(R), ev_count[j * G :], flags, i32(G), i32(mode), dh, nseg,
-                     self._pre, i32(wbits), i32(dbits))
+                     self._pre, i32(wbits), i32(dbits), i32(mbits))
             e1.record()
         return regions, R, ev_count, dhist, nseg, flags  # count_events checks the flags with its first read
 
@@ -376,6 +380,7 @@ class LevelBuild:
         ev_count = elib.zeros(G, torch.int32, dev)
         last = self.events_of.get(k)
         dbits = first_digit(wbits) if wbits else 8
+        mbits = key_mbits(wbits) if wbits else 0
         dhist = torch.empty((1 << dbits) * G, dtype=torch.int32, device=dev) \
             if wbits or last is None or last >= partcount.SEG_MIN_EVENTS * G else None
         if mode == 3:
@@ -390,10 +395,11 @@ class LevelBuild:
         e0.record()
         if mode == 3:
             elib("ng_scan_emit_list", self.tok[lo:], self._plist, n_list, i32(k), vi.table, u64(vi.cap), vi.rep, x,
-                 bm_out[lo // 32 :], regions, u64(R), ev_count, flags, i32(G), dhist, G, i32(wbits), i32(dbits))
+                 bm_out[lo // 32 :], regions, u64(R), ev_count, flags, i32(G), dhist, G, i32(wbits), i32(dbits),
+                 i32(mbits))
         else:
             elib("ng_scan_emit", self.tok[lo:], n, i32(k), None if bm_in is None else bm_in[lo // 32 :],
                  bm_out[lo // 32 :], vi.table, u64(vi.cap), vi.rep, x, regions, u64(R), ev_count, flags, i32(G),
-                 i32(mode), dhist, G, self._pre, i32(wbits), i32(dbits))
+                 i32(mode), dhist, G, self._pre, i32(wbits), i32(dbits), i32(mbits))
         e1.record()
         return regions, R, ev_count, dhist, G, flags

@@ -286,6 +286,13 @@ def first_digit(W: int) -> int:
     return min(max(8, W - 32), 10)
 
 
+def key_mbits(W: int) -> int:
+    """The bits of a W-bit pair key that its 32-bit count event mixes (kmix, part.h) where the event is keyed by context
+    range: those below the first pass's digit, which then holds the top context-id bits (so a first-pass bucket is a
+    range of context ids, and its partitions hold the pairs of those contexts only: count32's runs mode)."""
+    return W - first_digit(W)
+
+
 @dataclass
 class Counted32:
     """A level counted by count32: per context id its record (int32 [n_ids, RECORD_WORDS[ktop]]) and pair count
@@ -321,7 +328,7 @@ def pbits32_max(n_ids: int) -> int:
 def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None, n_events: int | None,
             ratio: float = 1.0, event=_no_event, min_pbits: int = 0, slabs: bool = False,
             deep_min: int | None = None, with_dist: bool = True, agg_grid: int = 0,
-            stat: torch.Tensor | None = None) -> Counted32:
+            stat: torch.Tensor | None = None, mbits: int | None = None) -> Counted32:
     """Count a level's events emitted by ng_scan_emit in the W-bit mode (wbits = W = w_bits(n_ids)[1], dbits =
     first_digit(W); seg = (regions, R, ev_count, dhist, nseg, scan flags)) and make every present context's record
     (top ktop) without a host read: the passes and the count of pairs32.hip. `n_events`: the level's events (the last
@@ -336,7 +343,10 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
     per compute unit for many light groups, each block then walking its groups with the next one's words loaded
     ahead). `stat`: the caller's int64 [>= 8] of zeros for Counted32.stat (e.g. a row of one tensor every level of a
     build shares, read once); its fourth entry holds the scan's two int32 flags where the caller's seg flags are a view
-    of it."""
+    of it. `mbits`: the events' mixed bits (the scan's; None: W, every bit). With key_mbits(W) (events keyed by context
+    range) and without slabs or deep_min, the count leaves each partition's words grouped by context sub-range (runs)
+    and the records are made from those runs directly (ng_ctx_agg_runs), without grouping the words by context, as long
+    as a bucket has at most 256 partitions and 64 sub-ranges."""
     regions, R, ev_count, dhist, nseg, scan_flags = seg
     dev = regions.device
     idb, W = w_bits(n_ids)
@@ -344,6 +354,7 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
     if W > W_WIDE:
         raise ValueError(f"{n_ids} context ids: wider than the 32-bit count takes")
     d1 = first_digit(W)
+    M = W if mbits is None else mbits
     cap = nseg * R
     if stat is None:
         stat = elib.zeros(8, torch.int64, dev)
@@ -355,8 +366,10 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
     elib.cub("ng_exclusive_scan_u32", dhist, dpre, (1 << d1) * nseg, ev_tot)
     if n_events is None:
         n_events = int(ev_tot.item())
+    # events keyed by context range (M < W) fill only the partitions of the used share of the id bits
+    used = n_ids / (1 << idb) if M < W else 1.0
     pbits = max(d1 + 1, W - 31, PART_MIN_BITS if lookups is not None else 0, min_pbits,
-                math.ceil(math.log2(max(1.0, n_events * ratio / P32_TARGET))))
+                math.ceil(math.log2(max(1.0, n_events * ratio / P32_TARGET / used))))
     pbits = min(pbits, pbits32_max(n_ids))
     d2 = pbits - d1
     e0, e1 = event("partition", cap)
@@ -385,7 +398,7 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
     if nq:
         qk = torch.empty(nq, dtype=torch.int64, device=dev)
         qv = torch.empty(nq, dtype=torch.int32, device=dev)
-        elib("ng_part_lookups_w", ctx_of, tgt, qpos, nq, qn, 0, n_ids, i32(W), qk, qv)
+        elib("ng_part_lookups_w", ctx_of, tgt, qpos, nq, qn, 0, n_ids, i32(W), i32(M), qk, qv)
         sqk = torch.empty(nq, dtype=torch.int64, device=dev)
         sqv = torch.empty(nq, dtype=torch.int32, device=dev)
         elib.cub("sort_pairs", qk, sqk, qv, sqv, nq, i32(64 - pbits), i32(64))
@@ -396,6 +409,13 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
     # in turns), at least 256 and at most PART_BLOCKS
     G2 = min(P, PART_BLOCKS, max(256, n_events // 16384 + 1))
     agg = AGG_ID_BITS - 1 if ktop >= 8 else AGG_ID_BITS  # top 8: 2^10 ids a group
+    # runs mode: a group is a sub-range of 2^ribits ids of a first-pass bucket (2^(idb - d1) ids), run s of each of
+    # the bucket's 2^d2 partitions
+    ribits = min(agg, idb - d1)
+    rgbits = idb - d1 - ribits
+    if M == W - d1 and not slabs and deep_min is None and d2 <= 8 and rgbits <= 6:
+        return _count32_runs(elib, n_ids, ktop, W, M, cb, d1, d2, pbits, P, cap, ev32b, start, sqk, sqv, qstart, N,
+                             ribits, rgbits, G2, flags, stat, with_dist, agg_grid, event)
     # the words' first grouping digit: 8 bits (runs of about 64 words per digit in each 16384-word chunk), more only
     # where the second pass's 11 bits would not reach a group's
     dc = min(idb, max(WORD_DIGIT, idb - agg - 11))
@@ -410,9 +430,9 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
     slab = torch.empty(P * P32_SLOTS, dtype=torch.int64, device=dev) if slabs else None
     e0, e1 = event("count", cap)
     e0.record()
-    elib("ng_part_count32", ev32b, start, i32(pbits), i32(W), sqk, sqv, qstart, out_k, i32(cb), esc_k, esc_c,
+    elib("ng_part_count32", ev32b, start, i32(pbits), i32(W), i32(M), sqk, sqv, qstart, out_k, i32(cb), esc_k, esc_c,
          u64(ESC_CAP), seg_cnt, seg_base, qcnt, dh2, i32(dtop - dc), i32(dc), ctypes.c_uint32(P32_LIMIT), flags,
-         i32(G2), slab)
+         i32(G2), slab, None, i32(0), i32(0), None)
     e1.record()
     del ev32b, start, sqk, sqv, qstart
     # the words grouped by context: by their top dc bits (ng_seg_scatter), then within those groups by the next d2
@@ -450,6 +470,36 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
     keep = deep_min is not None
     return Counted32(rec, dist, qcnt, stat, pbits, cb, (esc_k, esc_c), W, slab, words if keep else None,
                      start2 if keep else None, ibits, deep, deep_n)
+
+
+def _count32_runs(elib: Lib, n_ids, ktop, W, M, cb, d1, d2, pbits, P, cap, ev32b, start, sqk, sqv, qstart, N, ibits,
+                  gbits, G2, flags, stat, with_dist, agg_grid, event) -> Counted32:
+    """count32's runs mode: the count writes each partition's words grouped by the gbits context-id bits below the
+    first pass's digit (gshift = 16 + ibits), and ng_ctx_agg_runs makes the records of each group of 2^ibits ids from
+    its runs in the bucket's 2^d2 partitions."""
+    dev = ev32b.device
+    out_k = torch.empty(max(cap, 1), dtype=torch.int64, device=dev)
+    esc_k = elib.full_ones(ESC_CAP, torch.int64, dev)
+    esc_c = torch.empty(ESC_CAP, dtype=torch.int32, device=dev)
+    seg_cnt = torch.empty(G2, dtype=torch.int32, device=dev)
+    seg_base = torch.empty(G2, dtype=torch.int64, device=dev)
+    qcnt = elib.zeros(max(N, 1), torch.int32, dev) if N else None
+    runs = torch.empty(P * ((1 << gbits) + 1), dtype=torch.int64, device=dev)
+    e0, e1 = event("count", cap)
+    e0.record()
+    elib("ng_part_count32", ev32b, start, i32(pbits), i32(W), i32(M), sqk, sqv, qstart, out_k, i32(cb), esc_k, esc_c,
+         u64(ESC_CAP), seg_cnt, seg_base, qcnt, None, i32(0), i32(0), ctypes.c_uint32(P32_LIMIT), flags, i32(G2), None,
+         runs, i32(gbits), i32(16 + ibits), stat[1:2])  # stat[1]: the distinct pairs (zero before)
+    e1.record()
+    del ev32b, start, sqk, sqv, qstart, seg_cnt, seg_base
+    rec = torch.empty((max(n_ids, 1), RECORD_WORDS[ktop]), dtype=torch.int32, device=dev)
+    dist = torch.empty(max(n_ids, 1), dtype=torch.int32, device=dev) if with_dist else None
+    e0, e1 = event("ctx_topk", cap)
+    e0.record()
+    elib("ng_ctx_agg_runs", out_k, runs, 1 << (d1 + gbits), i32(d2), i32(gbits), i32(ibits), i32(cb), n_ids, esc_k,
+         esc_c, u64(ESC_CAP), i32(ktop), rec, dist, flags, None, i32(agg_grid))
+    e1.record()
+    return Counted32(rec, dist, qcnt, stat, pbits, cb, (esc_k, esc_c), W, None, None, None, ibits, None, None)
 
 
 
