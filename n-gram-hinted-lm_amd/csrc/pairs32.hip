@@ -188,6 +188,13 @@ __global__ void __launch_bounds__(256) sel_write_k(const int* __restrict__ v, i6
 }
 
 
+// The runs mode's table: run s (of 2^gbits) of partition p = b << rbits | j (bucket b of the first pass, 2^rbits
+// partitions a bucket) at entry ((b << gbits) + s) << rbits | j, so that a group's runs (one per partition of its
+// bucket) lie side by side: start | end << 32 (word indexes below 2^32).
+__device__ __forceinline__ i64 run_at(i64 p, int s, int gbits, int rbits) {
+    return ((((p >> rbits) << gbits) + s) << rbits) | (p & ((1ll << rbits) - 1));
+}
+
 // Block b counts the partitions it owns (part_owner: about equal events per block) in turn. Events: u32, a
 // partition's key = its low lbits = W - pbits bits (h = p << lbits | key). A round of P32_ITEMS events per thread:
 // the lanes holding a wave's first key add once for all of them (a hot pair would serialize the LDS atomics); every
@@ -205,8 +212,8 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
                                                       u64 esc_cap, u32* __restrict__ seg_cnt,
                                                       i64* __restrict__ seg_base, u32* __restrict__ qcnt,
                                                       u32* __restrict__ dhist, int dshift, int dbits, u32 limit,
-                                                      u32* flags, u64* __restrict__ slab, i64* __restrict__ runs,
-                                                      int gbits, int gshift, u64* n_words) {
+                                                      u32* flags, u64* __restrict__ slab, u64* __restrict__ runs,
+                                                      int gbits, int gshift, int rbits, i64 runs_np, u64* n_words) {
     __shared__ __align__(16) u32 tk[P32_SLOTS];
     __shared__ u32 tc[P32_SLOTS];
     __shared__ u16 list[P32_SLOTS];
@@ -252,10 +259,14 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
         if (a == e_end && !slab) {
             // this partition and the block's later ones hold no events (the trailing partitions of a level whose
             // context ids fill only part of their bit range, all of them the last block's): no words, and their
-            // lookups' counts stay 0; their runs, empty, are written at once
+            // lookups' counts stay 0; their runs, empty, are written at once where they may be read (below runs_np)
             if (runs) {
-                const i64 ng1 = (1ll << gbits) + 1, base = out_base + (i64)cur;
-                for (i64 x = t; x < (p1 - p) * ng1; x += P32_BLOCK) runs[p * ng1 + x] = base;
+                const i64 pe = p1 < runs_np ? p1 : runs_np;
+                const u64 base = (u64)(out_base + (i64)cur);
+                for (i64 x = t; x < (pe - p) << gbits; x += P32_BLOCK) {
+                    const i64 q = p + (x >> gbits);
+                    runs[run_at(q, (int)(x & ((1 << gbits) - 1)), gbits, rbits)] = base | (base << 32);
+                }
             }
             break;
         }
@@ -392,7 +403,7 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
             for (int j = t; j < P32_SLOTS; j += P32_BLOCK) sp[j] = ((u64)tc[j] << 32) | tk[j];
             lds_barrier();  // read before the output pass empties the slots
         }
-        if (runs) {
+        if (runs && p < runs_np) {
             // the partition's words grouped by the gbits-bit digit (pair key >> gshift) of their context ids (an LDS
             // count, a scan by wave 0, then a slot per word from the group's cursor), group s's run of words at
             // [runs[p * (2^gbits + 1) + s], runs[p * (2^gbits + 1) + s + 1]) of out_k
@@ -412,13 +423,11 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
                     const u32 o = (u32)__shfl_up((int)incl, d, WAVE);
                     if (lane >= d) incl += o;
                 }
-                i64* rp = runs + p * (i64)(ng + 1);
-                const i64 base = out_base + (i64)cur;
+                const u64 base = (u64)(out_base + (i64)cur);
                 if (t < (int)ng) {
-                    rp[t] = base + (i64)(incl - c);
+                    runs[run_at(p, t, gbits, rbits)] = (base + incl - c) | ((base + incl) << 32);
                     dh[t] = incl - c;
                 }
-                if (t == (int)ng - 1) rp[ng] = base + (i64)incl;
             }
             lds_barrier();
             for (u32 i = t; i < nl; i += P32_BLOCK) {
@@ -442,7 +451,7 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
                 const u64 word = (pk << (48 - cb)) | ((u64)n < esc ? (u64)n : esc);
                 out_k[(u64)out_base + cur + i] = word;
                 if ((u64)n >= esc) esc_put(esc_k, esc_c, esc_cap, pk, n, flags);
-                atomicAdd(&dh[(u32)(word >> dshift) & (u32)(nd - 1)], 1u);
+                if (nd) atomicAdd(&dh[(u32)(word >> dshift) & (u32)(nd - 1)], 1u);  // none in runs mode
             }
         }
         cur += nl;
@@ -630,14 +639,14 @@ __global__ void __launch_bounds__(AGG_BLOCK) __attribute__((amdgpu_waves_per_eu(
 // ctx_agg_k over ng_part_count32's words left in runs (its `runs` mode, events keyed by kmix(pair key, W, W - d1)):
 // group g = b << gbits | s (bucket b of the first pass's d1 bits, sub-group s of the gbits context-id bits below
 // them) holds the ids [g << ibits, (g + 1) << ibits), and its words are run s of each of the bucket's 2^d2 <= 256
-// partitions b << d2 | j. A block takes groups g, g + grid, ... and streams a group's words as one sequence: every
-// wave holds the group's runs in its lanes (lane l: runs l, 64 + l, 128 + l and 192 + l, their starts and the
-// exclusive scan of the lengths; no LDS, so that two blocks still share a compute unit). A wave's 64 consecutive words span few runs: the
-// run of its first word is the count of runs starting at or before it, and the runs starting inside its window are
-// walked with lane reads. The next round's words are loaded ahead, as ctx_agg_k's. Outputs as ctx_agg_k's, without
+// partitions b << d2 | j, whose bounds are runs[g << d2 | j] (run_at's layout). A block takes groups g, g + grid, ...
+// and streams a group's words as one sequence: every wave holds the group's runs in its lanes (lane l: runs l,
+// 64 + l, 128 + l and 192 + l, their starts and the exclusive scan of the lengths; no LDS, so that two blocks still
+// share a compute unit). A wave's 64 consecutive words span few runs: the run of its first word is the count of runs
+// starting at or before it, and the runs starting inside its window are walked with lane reads. The next round's words are loaded ahead, as ctx_agg_k's. Outputs as ctx_agg_k's, without
 // the deep list.
 template <int KT>
-__global__ void __launch_bounds__(AGG_BLOCK) __attribute__((amdgpu_waves_per_eu(8))) ctx_agg_runs_k(const u64* __restrict__ w, const i64* __restrict__ runs,
+__global__ void __launch_bounds__(AGG_BLOCK) __attribute__((amdgpu_waves_per_eu(8))) ctx_agg_runs_k(const u64* __restrict__ w, const u64* __restrict__ runs,
                                                        i64 NG, int d2, int gbits, int ibits, int cb, i64 n_ids,
                                                        const u64* __restrict__ esc_k, const u32* __restrict__ esc_c,
                                                        u64 esc_cap, u32* __restrict__ rec, u32* __restrict__ dist,
@@ -646,15 +655,14 @@ __global__ void __launch_bounds__(AGG_BLOCK) __attribute__((amdgpu_waves_per_eu(
     __shared__ u64 s_top[AGG_IDS_FOR(KT) * KT];
     const int t = threadIdx.x, lane = lane_id();
     const u32 wbase = (u32)(t & ~(WAVE - 1));  // the wave's first thread
-    const int nid = 1 << ibits, R = 1 << d2, gs = (1 << gbits) + 1;
+    const int nid = 1 << ibits, R = 1 << d2;
     u32 mine = 0;
     for (i64 g = blockIdx.x; g < NG; g += gridDim.x) {
         const i64 lo = g << ibits;
         if (lo >= n_ids) break;  // groups ascend with g
-        const i64 b = g >> gbits, s = g & ((1 << gbits) - 1);
         agg_clear<KT>(nid, s_tot, s_dist, s_top);
         // word indexes are below 2^32 (the count's capacity)
-        const i64* rp = runs + (b << d2) * gs + s;
+        const u64* rp = runs + (g << d2);  // the group's runs, side by side
         u32 rlo[AGG_RUN_REGS], rpre[AGG_RUN_REGS], tot = 0;
 #pragma unroll
         for (int h = 0; h < AGG_RUN_REGS; ++h) {
@@ -662,9 +670,9 @@ __global__ void __launch_bounds__(AGG_BLOCK) __attribute__((amdgpu_waves_per_eu(
             u32 len = 0;
             rlo[h] = 0;
             if (j < R) {
-                const i64 a = rp[(i64)j * gs], e = rp[(i64)j * gs + 1];
-                rlo[h] = (u32)a;
-                len = (u32)(e - a);
+                const u64 r = rp[j];
+                rlo[h] = (u32)r;
+                len = (u32)(r >> 32) - (u32)r;
             }
             u32 incl = len;
 #pragma unroll
@@ -844,7 +852,10 @@ extern "C" int ng_select_positive(void* temp, size_t* temp_bytes, const int* v, 
 // b] block b's words per dbits-bit digit (word >> dshift) & (2^dbits - 1) (1 <= dbits <= 11), for ng_seg_scatter.
 // runs (may be NULL; dhist is then unused and may be NULL): each partition's words are written grouped by the
 // gbits-bit digit (pair key >> gshift) & (2^gbits - 1) (0 <= gbits <= 6, 16 <= gshift, gshift + gbits <= W), group s
-// of partition p at out_k[runs[p * (2^gbits + 1) + s] ...  runs[p * (2^gbits + 1) + s + 1]). n_words (may be NULL):
+// of partition p = b << rbits | j (2^rbits partitions a first-pass bucket) at out_k[lo, hi), lo | hi << 32 =
+// runs[((b << gbits) + s) << rbits | j], for p < runs_np (the partitions of the buckets holding context ids; the others
+// hold no events and their runs are not written; <= 2^pbits).
+// n_words (may be NULL):
 // += the words written (the distinct pairs; one atomic per block). Lookups (ng_part_lookups_w's, sorted by
 // their top pbits; qstart their partitions' bounds; qk and qv may be NULL with qstart all zeros: none) get qcnt[qv[j]]
 // = the pair's count or 0. flags[0] bit 0: a partition reached min(limit, 11000) distinct pairs (its count is
@@ -854,14 +865,15 @@ extern "C" int ng_select_positive(void* temp, size_t* temp_bytes, const int* v, 
 extern "C" int ng_part_count32(const u32* ev, const i64* start, int pbits, int W, int M, const u64* qk,
                                const u32* qv, const i64* qstart, u64* out_k, int cb, u64* esc_k, u32* esc_c,
                                u64 esc_cap, u32* seg_cnt, i64* seg_base, u32* qcnt, u32* dhist, int dshift, int dbits,
-                               u32 limit, u32* flags, int grid, u64* slab, i64* runs, int gbits, int gshift,
-                               u64* n_words, void* stream) {
+                               u32 limit, u32* flags, int grid, u64* slab, u64* runs, int gbits, int gshift,
+                               int rbits, i64 runs_np, u64* n_words, void* stream) {
     if (M == 0) M = W;
     if (pbits < 1 || pbits > 30 || W < 17 || W - 16 > cb || cb > 44 || W - pbits > 31 || W - pbits < 1 ||
         M < 17 || M > W || grid <= 0 || grid > 65536 || esc_k == nullptr || esc_c == nullptr || esc_cap == 0 ||
         qstart == nullptr || limit == 0)
         return -1;
-    if (runs ? (gbits < 0 || gbits > 6 || gshift < 16 || gshift + gbits > W)
+    if (runs ? (gbits < 0 || gbits > 6 || gshift < 16 || gshift + gbits > W || rbits < 0 || rbits > pbits ||
+                runs_np < 0 || runs_np > (1ll << pbits))
              : (dbits < 1 || dbits > 11 || dshift < 0 || dshift + dbits > 64 || dhist == nullptr))
         return -1;
     const i64 P = 1ll << pbits;
@@ -869,7 +881,7 @@ extern "C" int ng_part_count32(const u32* ev, const i64* start, int pbits, int W
     count32_k<<<grid, P32_BLOCK, 0, (hipStream_t)stream>>>(ev, start, P, pbits, W, M, qk, qv, qstart, out_k, cb,
                                                            esc_k, esc_c, esc_cap, seg_cnt, seg_base, qcnt, dhist,
                                                            dshift, dbits, limit, flags, slab, runs, gbits, gshift,
-                                                           n_words);
+                                                           rbits, runs_np, n_words);
     return (int)hipGetLastError();
 }
 
@@ -906,12 +918,12 @@ extern "C" int ng_ctx_agg(const u64* w, const i64* start, i64 P, int ibits, int 
     return (int)hipGetLastError();
 }
 
-// ng_ctx_agg over ng_part_count32's words left in runs (its runs mode, with gbits and gshift = 16 + ibits): group g
-// (of NG = 2^(d1 + gbits), d1 the first pass's digit bits; ids [g << ibits, (g + 1) << ibits), ibits <= 11, 10 for
-// topk 8) is run g & (2^gbits - 1) of partitions (g >> gbits) << d2 ... + 2^d2 - 1 (0 <= d2 <= 8, 0 <= gbits <= 6;
-// word indexes below 2^32).
+// ng_ctx_agg over ng_part_count32's words left in runs (its runs mode, with gbits, rbits = d2 and gshift = 16 +
+// ibits): group g (of NG = 2^(d1 + gbits), d1 the first pass's digit bits; ids [g << ibits, (g + 1) << ibits), ibits
+// <= 11, 10 for topk 8) is run g & (2^gbits - 1) of partitions (g >> gbits) << d2 ... + 2^d2 - 1, their bounds at
+// runs[g << d2 ...] (0 <= d2 <= 8, 0 <= gbits <= 6; word indexes below 2^32).
 // Outputs and grid as ng_ctx_agg's (no deep list).
-extern "C" int ng_ctx_agg_runs(const u64* w, const i64* runs, i64 NG, int d2, int gbits, int ibits, int cb,
+extern "C" int ng_ctx_agg_runs(const u64* w, const u64* runs, i64 NG, int d2, int gbits, int ibits, int cb,
                                i64 n_ids, const u64* esc_k, const u32* esc_c, u64 esc_cap, int topk, u32* rec,
                                u32* dist, u32* flags, u64* present, int grid, void* stream) {
     if (cb < 1 || cb > 44 || ibits < 0 || (1 << ibits) > (topk >= 8 ? AGG_IDS_FOR(8) : AGG_IDS) || NG <= 0 ||

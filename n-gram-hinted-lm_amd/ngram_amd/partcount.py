@@ -405,9 +405,10 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
         del qk, qv
         elib("ng_part_bounds", sqk, nq, i32(pbits), i32(0), qstart)
     e1.record()
-    # the count's blocks: about one per 16384 events (a small level's blocks would each wait out their fixed latency
-    # in turns), at least 256 and at most PART_BLOCKS
-    G2 = min(P, PART_BLOCKS, max(256, n_events // 16384 + 1))
+    # the count's blocks: one per compute unit (its LDS table takes a compute unit's LDS), each a run of consecutive
+    # partitions of about equal events; more blocks, run in turns, were slower (c3: 2048, 768, 512 and 256 blocks,
+    # 12.8, 12.2, 12.0 and 11.7 ms a step; 384, a second round for half the units, 14.8 ms)
+    G2 = min(P, torch.cuda.get_device_properties(dev).multi_processor_count)
     agg = AGG_ID_BITS - 1 if ktop >= 8 else AGG_ID_BITS  # top 8: 2^10 ids a group
     # runs mode: a group is a sub-range of 2^ribits ids of a first-pass bucket (2^(idb - d1) ids), run s of each of
     # the bucket's 2^d2 partitions
@@ -432,7 +433,7 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
     e0.record()
     elib("ng_part_count32", ev32b, start, i32(pbits), i32(W), i32(M), sqk, sqv, qstart, out_k, i32(cb), esc_k, esc_c,
          u64(ESC_CAP), seg_cnt, seg_base, qcnt, dh2, i32(dtop - dc), i32(dc), ctypes.c_uint32(P32_LIMIT), flags,
-         i32(G2), slab, None, i32(0), i32(0), None)
+         i32(G2), slab, None, i32(0), i32(0), i32(0), 0, None)
     e1.record()
     del ev32b, start, sqk, sqv, qstart
     # the words grouped by context: by their top dc bits (ng_seg_scatter), then within those groups by the next d2
@@ -484,12 +485,14 @@ def _count32_runs(elib: Lib, n_ids, ktop, W, M, cb, d1, d2, pbits, P, cap, ev32b
     seg_cnt = torch.empty(G2, dtype=torch.int32, device=dev)
     seg_base = torch.empty(G2, dtype=torch.int64, device=dev)
     qcnt = elib.zeros(max(N, 1), torch.int32, dev) if N else None
-    runs = torch.empty(P * ((1 << gbits) + 1), dtype=torch.int64, device=dev)
+    runs = torch.empty(P << gbits, dtype=torch.int64, device=dev)  # a run's bounds: start | end << 32
+    # the runs ng_ctx_agg_runs reads: those of the buckets holding ids below n_ids (the count writes no others)
+    runs_np = ((max(n_ids, 1) - 1) >> (W - 16 - d1)) + 1 << d2
     e0, e1 = event("count", cap)
     e0.record()
     elib("ng_part_count32", ev32b, start, i32(pbits), i32(W), i32(M), sqk, sqv, qstart, out_k, i32(cb), esc_k, esc_c,
          u64(ESC_CAP), seg_cnt, seg_base, qcnt, None, i32(0), i32(0), ctypes.c_uint32(P32_LIMIT), flags, i32(G2), None,
-         runs, i32(gbits), i32(16 + ibits), stat[1:2])  # stat[1]: the distinct pairs (zero before)
+         runs, i32(gbits), i32(16 + ibits), i32(d2), runs_np, stat[1:2])  # stat[1]: the distinct pairs (zero before)
     e1.record()
     del ev32b, start, sqk, sqv, qstart, seg_cnt, seg_base
     rec = torch.empty((max(n_ids, 1), RECORD_WORDS[ktop]), dtype=torch.int32, device=dev)

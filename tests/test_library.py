@@ -98,3 +98,45 @@ def test_builds_take_turns_on_the_lock(tmp_path, monkeypatch):
         fcntl.flock(lock, fcntl.LOCK_UN)
     out, _ = p.communicate(timeout=60)
     assert p.returncode == 0 and float(out.split()[-1]) >= 1.0
+
+
+def declared_arity(header: str) -> dict[str, int]:
+    """Each declared function's parameter count (the header's prototypes, comments removed)."""
+    text = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / header).read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"^\s*(?:int|size_t|void|ng_i64|ng_u64)\s+(\w+)\s*\(([^;]*?)\)\s*;", text, flags=re.M | re.S):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_engine_calls_match_the_header_arity():
+    """Every call of an ng_* entry point through the ctypes wrapper (`lib("ng_x", ...)`, `lib.cub("ng_x", ...)` for
+    the two-phase ones, `lib.size("ng_x", ...)` for the sizing ones) passes as many arguments as the prototype has,
+    less the stream the wrapper appends (and the temp pair `cub` adds): a missing argument would shift the stream into
+    another parameter."""
+    import ast
+
+    arity = declared_arity("ngram_amd.h")
+    files = list((ROOT / "n-gram-hinted-lm_amd").rglob("*.py")) + [ROOT / "bench.py", ROOT / "__graft_entry__.py"]
+    files += list((ROOT / "tests").glob("*.py"))
+    checked, bad = 0, []
+    for f in files:
+        for node in ast.walk(ast.parse(f.read_text())):
+            if not (isinstance(node, ast.Call) and node.args and isinstance(node.args[0], ast.Constant)):
+                continue
+            name = node.args[0].value
+            if not (isinstance(name, str) and name.startswith("ng_") and name in arity):
+                continue
+            if node.keywords or any(isinstance(a, ast.Starred) for a in node.args):
+                continue
+            kind = node.func.attr if isinstance(node.func, ast.Attribute) else ""
+            if kind == "size":  # sizing calls take no stream
+                want = arity[name]
+            else:
+                want = arity[name] - (3 if kind == "cub" else 1)
+            checked += 1
+            if len(node.args) - 1 != want:
+                bad.append(f"{f.name}:{node.lineno} {name}: {len(node.args) - 1} arguments, the prototype takes {want}")
+    assert checked > 50
+    assert not bad, bad
