@@ -520,6 +520,30 @@ __global__ void __launch_bounds__(WAVE) ctx_summary_k(const u64* __restrict__ w,
 // Per query position i whose context id c is in [lo, hi) and present (dist[c - lo] > 0): from its context's record
 // (ctx_summary_k's) tot, dist (at most 65535), the first kout of ktop top entries; cnt = qcnt[i] (with thr: only if its
 // score reaches thr[c]); mask bit li.
+// A position's first kout (<= KT) entries, tokens tk and counts tc, into rows i of out_tok / out_tcnt ([., kout]): one
+// store each where the row is a whole KT-entry vector (kout == KT, 4 or 8, rows aligned), else entry by entry.
+template <int KT>
+__device__ __forceinline__ void put_top(u16* __restrict__ out_tok, u32* __restrict__ out_tcnt, i64 i, int kout,
+                                        const u16 (&tk)[KT], const u32 (&tc)[KT]) {
+    if constexpr (KT == 4 || KT == 8) {
+        if (kout == KT && !((uintptr_t)out_tok & 7) && !((uintptr_t)out_tcnt & 15)) {
+#pragma unroll
+            for (int h = 0; h < KT / 4; ++h) {
+                *(ushort4*)(out_tok + i * KT + 4 * h) = make_ushort4(tk[4 * h], tk[4 * h + 1], tk[4 * h + 2], tk[4 * h + 3]);
+                *(uint4*)(out_tcnt + i * KT + 4 * h) = make_uint4(tc[4 * h], tc[4 * h + 1], tc[4 * h + 2], tc[4 * h + 3]);
+            }
+            return;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < KT; ++r) {
+        if (r < kout) {
+            out_tok[i * kout + r] = tk[r];
+            out_tcnt[i * kout + r] = tc[r];
+        }
+    }
+}
+
 template <int KT>
 __global__ void __launch_bounds__(256) pos_summary_k(const int* __restrict__ ctx_of, i64 N, i64 lo, i64 hi,
                                                      const u16* __restrict__ tgt, const u32* __restrict__ rec,
@@ -532,10 +556,18 @@ __global__ void __launch_bounds__(256) pos_summary_k(const int* __restrict__ ctx
     const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
     if (i >= N) return;
     i64 c = ctx_of[i];
-    if (c < lo || c >= hi) return;
+    if (c >= 0 && (c < lo || c >= hi)) return;  // a context of another id range: that range's call writes it
+    const u32 d = c >= 0 ? dist[c - lo] : 0u;
+    if (d == 0) {  // no context, or one that never occurred: zeros (so the outputs need no fill before)
+        out_tot[i] = 0;
+        out_dist[i] = 0;
+        out_cnt[i] = 0;
+        const u16 zt[KT] = {};
+        const u32 zc[KT] = {};
+        put_top<KT>(out_tok, out_tcnt, i, kout, zt, zc);
+        return;
+    }
     c -= lo;
-    const u32 d = dist[c];
-    if (d == 0) return;
     u32 v[R::WORDS];
     const uint4* src = (const uint4*)(rec + c * R::WORDS);
 #pragma unroll
@@ -549,17 +581,20 @@ __global__ void __launch_bounds__(256) pos_summary_k(const int* __restrict__ ctx
     out_tot[i] = (int)v[0];
     out_dist[i] = (int)(d < 65535u ? d : 65535u);
     const u32 n = qcnt ? qcnt[i] : 0u;
+    int cnt = 0;
     if (n) {
         const u64 th = thr ? thr[c] : 0;
-        if (th == 0 || rank_score(((u64)c << 16) | tgt[i], n) >= th) out_cnt[i] = (int)n;
+        if (th == 0 || rank_score(((u64)c << 16) | tgt[i], n) >= th) cnt = (int)n;
     }
+    out_cnt[i] = cnt;
+    u16 tk[KT];
+    u32 tc[KT];
 #pragma unroll
     for (int r = 0; r < KT; ++r) {
-        if (r < kout) {
-            out_tok[i * kout + r] = (u16)(v[2 + r / 2] >> (16 * (r & 1)));
-            out_tcnt[i * kout + r] = v[2 + R::TOKW + r];
-        }
+        tk[r] = (u16)(v[2 + r / 2] >> (16 * (r & 1)));
+        tc[r] = v[2 + R::TOKW + r];
     }
+    put_top<KT>(out_tok, out_tcnt, i, kout, tk, tc);
     if (mask) mask[i] |= 1 << li;
 }
 
@@ -710,7 +745,8 @@ extern "C" int ng_ctx_summary(const u64* w, i64 U, int cb, const u64* esc_k, con
 
 // Per query position from the per-context records and pair counts (ng_ctx_summary's) and the counted lookups qcnt: tot,
 // dist, cnt (thr may be NULL: the CNT_TOP threshold scores), the first kout <= ktop top entries, mask bit li (mask may
-// be NULL).
+// be NULL). Every position whose context is absent (ctx_of < 0) or did not occur (dist 0) gets zeros; those whose
+// context id lies outside [lo, hi) are left as they are.
 extern "C" int ng_pos_summary(const int* ctx_of, i64 N, i64 lo, i64 hi, const u16* tgt, const u32* rec, const u32* dist,
                               const u64* thr, const u32* qcnt, int ktop, int kout, int li, int* out_tot, int* out_dist,
                               int* out_cnt, u16* out_tok, u32* out_tcnt, int* mask, void* stream) {

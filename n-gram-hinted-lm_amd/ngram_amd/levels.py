@@ -114,12 +114,13 @@ class LevelBuild:
         self.grid = torch.cuda.get_device_properties(dev).multi_processor_count * SCAN_BLOCKS_PER_CU
         nwords = self.L // 32
         bms = {k: elib.zeros(nwords, torch.int32, dev) for k in self.levels}
-        res = LevelOutputs(elib.zeros((3, len(self.levels), N), torch.int32, dev))
+        # every level's ng_pos_summary writes all N positions of its rows (zeros where the context is absent): no fill
+        res = LevelOutputs(torch.empty((3, len(self.levels), N), dtype=torch.int32, device=dev))
         self._pre = torch.empty(1, dtype=torch.int32, device=dev)  # the prefix rule's device flag
         elib("ng_avail_closed", avail, N, self._pre)
         if topk:
-            res.top_tok = elib.zeros((len(self.levels), N, topk), torch.int16, dev)
-            res.top_cnt = elib.zeros((len(self.levels), N, topk), torch.int32, dev)
+            res.top_tok = torch.empty((len(self.levels), N, topk), dtype=torch.int16, device=dev)
+            res.top_cnt = torch.empty((len(self.levels), N, topk), dtype=torch.int32, device=dev)
         if with_mask:
             res.mask = elib.zeros(N, torch.int32, dev)
         G = self.grid
