@@ -269,8 +269,8 @@ int ng_select_positive(void* temp, size_t* temp_bytes, const int* v, ng_i64 n, i
  * the escape table), at out_k + seg_base[b], seg_cnt[b] of them; dhist[d * grid + b] its words per dbits-bit digit
  * (word >> dshift) & (2^dbits - 1), dbits <= 11; runs (may be NULL; dhist then unused): each partition's words
  * grouped by the digit (pair key >> gshift) & (2^gbits - 1) (gbits <= 6), group s of partition p = b << rbits | j
- * at out_k[lo, hi), lo | hi << 32 = runs[((b << gbits) + s) << rbits | j], for p < runs_np (<= 2^pbits: the
- * partitions whose runs are read; the others hold no events); n_words (may be NULL): += the words written;
+ * at out_k[lo, hi), lo | hi << 32 = runs[((b << gbits) + s) << rbits | j]; live_np (<= 2^pbits): the partitions
+ * whose runs and slabs are written (the others hold no events and are never read); n_words (may be NULL): += the words written;
  * qcnt[qv[j]] = the count of lookup j (ng_part_lookups_w's sorted by their top pbits, bounds qstart); flags[0]
  * bit 0: a partition reached min(limit, 11000) distinct pairs (count again with a bit more), bit 1: the escape table
  * is full; slab (may be NULL): 2^pbits * 14336 u64, each partition's LDS table written out (slot = count << 32 |
@@ -279,7 +279,7 @@ int ng_part_count32(const uint32_t* ev, const ng_i64* start, int pbits, int W, i
                     const uint32_t* qv, const ng_i64* qstart, ng_u64* out_k, int cb, ng_u64* esc_k, uint32_t* esc_c,
                     ng_u64 esc_cap, uint32_t* seg_cnt, ng_i64* seg_base, uint32_t* qcnt, uint32_t* dhist, int dshift,
                     int dbits, uint32_t limit, uint32_t* flags, int grid, ng_u64* slab, ng_u64* runs, int gbits,
-                    int gshift, int rbits, ng_i64 runs_np, ng_u64* n_words, void* stream);
+                    int gshift, int rbits, ng_i64 live_np, ng_u64* n_words, void* stream);
 /* per context id c < n_ids from ng_part_count32's words grouped by context into P partitions (start: i64[P + 1],
  * partition q = the ids [q << ibits, (q + 1) << ibits), ibits <= 11; ng_seg_scatter then ng_msd_pass64): dist[c] =
  * its pairs (0: absent) for every id (dist may be NULL), and for present contexts the record rec[c] of ng_ctx_summary's layout (topk 1,

@@ -213,7 +213,7 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
                                                       i64* __restrict__ seg_base, u32* __restrict__ qcnt,
                                                       u32* __restrict__ dhist, int dshift, int dbits, u32 limit,
                                                       u32* flags, u64* __restrict__ slab, u64* __restrict__ runs,
-                                                      int gbits, int gshift, int rbits, i64 runs_np, u64* n_words) {
+                                                      int gbits, int gshift, int rbits, i64 live_np, u64* n_words) {
     __shared__ __align__(16) u32 tk[P32_SLOTS];
     __shared__ u32 tc[P32_SLOTS];
     __shared__ u16 list[P32_SLOTS];
@@ -256,18 +256,21 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
     const i64 e_end = start[p1];  // the end of the block's events
     for (i64 p = p0; p < p1; ++p) {
         const i64 a = start[p], b = start[p + 1], qa = qstart[p], qb = qstart[p + 1];
-        if (a == e_end && !slab) {
+        if (a == e_end) {
             // this partition and the block's later ones hold no events (the trailing partitions of a level whose
             // context ids fill only part of their bit range, all of them the last block's): no words, and their
-            // lookups' counts stay 0; their runs, empty, are written at once where they may be read (below runs_np)
+            // lookups' counts stay 0; their runs and slabs, empty, are written at once where they may be read (below
+            // live_np)
+            const i64 pe = p1 < live_np ? p1 : live_np;
             if (runs) {
-                const i64 pe = p1 < runs_np ? p1 : runs_np;
                 const u64 base = (u64)(out_base + (i64)cur);
                 for (i64 x = t; x < (pe - p) << gbits; x += P32_BLOCK) {
                     const i64 q = p + (x >> gbits);
                     runs[run_at(q, (int)(x & ((1 << gbits) - 1)), gbits, rbits)] = base | (base << 32);
                 }
             }
+            if (slab)
+                for (i64 x = t; x < (pe - p) * P32_SLOTS; x += P32_BLOCK) slab[(u64)p * P32_SLOTS + x] = EMPTY32;
             break;
         }
         const bool has_q = qa + t < qb;
@@ -403,7 +406,7 @@ __global__ void __launch_bounds__(P32_BLOCK) count32_k(const u32* __restrict__ e
             for (int j = t; j < P32_SLOTS; j += P32_BLOCK) sp[j] = ((u64)tc[j] << 32) | tk[j];
             lds_barrier();  // read before the output pass empties the slots
         }
-        if (runs && p < runs_np) {
+        if (runs && p < live_np) {
             // the partition's words grouped by the gbits-bit digit (pair key >> gshift) of their context ids (an LDS
             // count, a scan by wave 0, then a slot per word from the group's cursor), group s's run of words at
             // [runs[p * (2^gbits + 1) + s], runs[p * (2^gbits + 1) + s + 1]) of out_k
@@ -643,8 +646,8 @@ __global__ void __launch_bounds__(AGG_BLOCK) __attribute__((amdgpu_waves_per_eu(
 // and streams a group's words as one sequence: every wave holds the group's runs in its lanes (lane l: runs l,
 // 64 + l, 128 + l and 192 + l, their starts and the exclusive scan of the lengths; no LDS, so that two blocks still
 // share a compute unit). A wave's 64 consecutive words span few runs: the run of its first word is the count of runs
-// starting at or before it, and the runs starting inside its window are walked with lane reads. The next round's words are loaded ahead, as ctx_agg_k's. Outputs as ctx_agg_k's, without
-// the deep list.
+// starting at or before it, and the runs starting inside its window are walked with lane reads. The next round's
+// words are loaded ahead, as ctx_agg_k's. Outputs as ctx_agg_k's, without the deep list.
 template <int KT>
 __global__ void __launch_bounds__(AGG_BLOCK) __attribute__((amdgpu_waves_per_eu(8))) ctx_agg_runs_k(const u64* __restrict__ w, const u64* __restrict__ runs,
                                                        i64 NG, int d2, int gbits, int ibits, int cb, i64 n_ids,
@@ -853,8 +856,8 @@ extern "C" int ng_select_positive(void* temp, size_t* temp_bytes, const int* v, 
 // runs (may be NULL; dhist is then unused and may be NULL): each partition's words are written grouped by the
 // gbits-bit digit (pair key >> gshift) & (2^gbits - 1) (0 <= gbits <= 6, 16 <= gshift, gshift + gbits <= W), group s
 // of partition p = b << rbits | j (2^rbits partitions a first-pass bucket) at out_k[lo, hi), lo | hi << 32 =
-// runs[((b << gbits) + s) << rbits | j], for p < runs_np (the partitions of the buckets holding context ids; the others
-// hold no events and their runs are not written; <= 2^pbits).
+// runs[((b << gbits) + s) << rbits | j]. live_np (<= 2^pbits): the partitions whose runs and slabs are written (those
+// of the buckets holding context ids: the others hold no events and are never read; 2^pbits without runs).
 // n_words (may be NULL):
 // += the words written (the distinct pairs; one atomic per block). Lookups (ng_part_lookups_w's, sorted by
 // their top pbits; qstart their partitions' bounds; qk and qv may be NULL with qstart all zeros: none) get qcnt[qv[j]]
@@ -866,14 +869,14 @@ extern "C" int ng_part_count32(const u32* ev, const i64* start, int pbits, int W
                                const u32* qv, const i64* qstart, u64* out_k, int cb, u64* esc_k, u32* esc_c,
                                u64 esc_cap, u32* seg_cnt, i64* seg_base, u32* qcnt, u32* dhist, int dshift, int dbits,
                                u32 limit, u32* flags, int grid, u64* slab, u64* runs, int gbits, int gshift,
-                               int rbits, i64 runs_np, u64* n_words, void* stream) {
+                               int rbits, i64 live_np, u64* n_words, void* stream) {
     if (M == 0) M = W;
     if (pbits < 1 || pbits > 30 || W < 17 || W - 16 > cb || cb > 44 || W - pbits > 31 || W - pbits < 1 ||
         M < 17 || M > W || grid <= 0 || grid > 65536 || esc_k == nullptr || esc_c == nullptr || esc_cap == 0 ||
         qstart == nullptr || limit == 0)
         return -1;
-    if (runs ? (gbits < 0 || gbits > 6 || gshift < 16 || gshift + gbits > W || rbits < 0 || rbits > pbits ||
-                runs_np < 0 || runs_np > (1ll << pbits))
+    if (live_np < 0 || live_np > (1ll << pbits)) return -1;
+    if (runs ? (gbits < 0 || gbits > 6 || gshift < 16 || gshift + gbits > W || rbits < 0 || rbits > pbits)
              : (dbits < 1 || dbits > 11 || dshift < 0 || dshift + dbits > 64 || dhist == nullptr))
         return -1;
     const i64 P = 1ll << pbits;
@@ -881,7 +884,7 @@ extern "C" int ng_part_count32(const u32* ev, const i64* start, int pbits, int W
     count32_k<<<grid, P32_BLOCK, 0, (hipStream_t)stream>>>(ev, start, P, pbits, W, M, qk, qv, qstart, out_k, cb,
                                                            esc_k, esc_c, esc_cap, seg_cnt, seg_base, qcnt, dhist,
                                                            dshift, dbits, limit, flags, slab, runs, gbits, gshift,
-                                                           rbits, runs_np, n_words);
+                                                           rbits, live_np, n_words);
     return (int)hipGetLastError();
 }
 

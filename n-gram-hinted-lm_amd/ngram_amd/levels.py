@@ -170,14 +170,15 @@ class LevelBuild:
             if not use32 and seen_n is not None:  # the 64-bit count takes an exact list: read its length
                 seen = seen[: int(seen_n.item())]
                 seen_n = None
+            mbits = self._mbits(W, vi.ids, ktop) if use32 else 0
             seg = self._emit(k, vi, x, bms, regions, R, W if use32 else 0,
-                             stats[li, 3:4].view(torch.int32) if use32 else None)
+                             stats[li, 3:4].view(torch.int32) if use32 else None, mbits)
             t2 = time.perf_counter()
             if use32:
                 # the 32-bit count: records made without sorting the pairs, every size read once after the last level
                 c = count32(elib, seg, vi.ids, ktop, (vi.ctx_of, tgt, seen, seen_n), self.events_of.get(k),
                             self.dratio.get(k, 1.0), ev_fn, self.min_pbits.get(k, 0), stat=stats[li],
-                            mbits=key_mbits(W))
+                            mbits=mbits)
                 del seg
                 checks32.append((k, li, c.pbits, vi.ids, seen_cap if seen_n is not None else -1))
                 sm = c
@@ -309,11 +310,17 @@ class LevelBuild:
             return 0
         return 3 if d < LIST_DENSITY else 2
 
-    def _emit(self, k, vi, x, bms, regions, R, wbits=0, flags=None):
+    @staticmethod
+    def _mbits(W: int, ids: int, ktop: int) -> int:
+        """The 32-bit count's event key bits mixed: those below the first digit (events keyed by context range, the
+        count's runs mode) where the runs mode fits the level, else all W."""
+        return key_mbits(W) if partcount.runs_fit(ids, ktop) else W
+
+    def _emit(self, k, vi, x, bms, regions, R, wbits=0, flags=None, mbits=0):
         """Level k's scan of every shard it counts, hits emitted to per-block regions with each block's top-digit
         histogram: count_events' seg = (regions, R, ev_count, dhist, nseg, flags). wbits: events kmix(pair key,
-        wbits, key_mbits(wbits)) (keyed by context range) with histograms of their first_digit(wbits) top bits
-        (count32's), else mix64(pair key). flags: the
+        wbits, mbits) (part.h; mbits 0: wbits) with histograms of their first_digit(wbits) top bits (count32's), else
+        mix64(pair key). flags: the
         scan's two int32 flags (zeroed; e.g. a view into the build's stats), else new."""
         elib, dev, G = self.elib, self.tok.device, self.grid
         shards = [i for i in range(len(self.sizes)) if i < self.level_shards[k]]
@@ -321,7 +328,6 @@ class LevelBuild:
         ev_count = elib.zeros(max(nseg, 1), torch.int32, dev)
         last = self.events_of.get(k)
         dbits = first_digit(wbits) if wbits else 8
-        mbits = key_mbits(wbits) if wbits else 0
         dhist = torch.empty((1 << dbits) * max(nseg, 1), dtype=torch.int32, device=dev) \
             if wbits or last is None or last >= partcount.SEG_MIN_EVENTS * nseg else None
         if flags is None:
@@ -334,7 +340,7 @@ class LevelBuild:
             si = scanned.index(k)
             if si > 0 or self.ready is None:
                 return self._emit_all(k, vi, x, None if si == 0 else bms[scanned[si - 1]], bms[k], shards, regions,
-                                      flags, self._mode(si, scanned), wbits)
+                                      flags, self._mode(si, scanned), wbits, mbits)
         for j, i in enumerate(shards):
             st, n = self.starts[i], self.sizes[i]
             n32 = (n + 31) // 32 * 32
@@ -365,7 +371,7 @@ class LevelBuild:
             e1.record()
         return regions, R, ev_count, dhist, nseg, flags  # count_events checks the flags with its first read
 
-    def _emit_all(self, k, vi, x, bm_in, bm_out, shards, regions, flags, mode, wbits=0):
+    def _emit_all(self, k, vi, x, bm_in, bm_out, shards, regions, flags, mode, wbits=0, mbits=0):
         """_emit of a level whose shards all scan the same levels, in one launch from the first shard's start to the
         last one's end: a lane per position (mode 0), the LDS-listed set positions (2), or one list of the previous
         level's set bits and one list scan (3); events as _emit's by wbits."""
@@ -381,7 +387,6 @@ class LevelBuild:
         ev_count = elib.zeros(G, torch.int32, dev)
         last = self.events_of.get(k)
         dbits = first_digit(wbits) if wbits else 8
-        mbits = key_mbits(wbits) if wbits else 0
         dhist = torch.empty((1 << dbits) * G, dtype=torch.int32, device=dev) \
             if wbits or last is None or last >= partcount.SEG_MIN_EVENTS * G else None
         if mode == 3:

@@ -34,7 +34,7 @@ from .data import BOS, HEADER_BYTES, shard_tokens
 from .data import pack_layout as layout
 from .lib import Lib, i32, u64
 from .partcount import (W_MAX, count32, count_events, emit_region, first_digit, key_mbits, pack_events, pbits32_max,
-                        summarize, w_bits)
+                        runs_fit, summarize, w_bits)
 from .qindex import LOAD as QLOAD, TAIL as QTAIL, QueryIndex
 
 
@@ -318,7 +318,7 @@ def _count_ids(elib: Lib, lib: Lib, tok, L: int, level: tuple, k: int, length, f
         dhist = torch.empty((1 << d1) * grid, dtype=torch.int32, device=dev)
         flags.zero_()
         elib("ng_scan_ids_emit", tok, L, bm, ids, final, regions, u64(R), ev_count, flags, i32(grid), dhist, grid,
-             i32(W), i32(d1), i32(key_mbits(W)))
+             i32(W), i32(d1), i32(key_mbits(W) if runs_fit(n_ids, 1) else W))
         if _count32_final(elib, (regions, R, ev_count, dhist, grid, flags), n_ids, k, fids, fpos, m, nxt, cnt):
             return
         _WIDE.add(k)  # its escape table overflowed: this level takes the 64-bit count from now on
@@ -355,7 +355,7 @@ def _count32_final(elib: Lib, seg: tuple, n_ids: int, k: int, fids, fpos, m: int
     min_pbits = 0
     while True:
         c = count32(elib, seg, n_ids, 1, None, None, _RATIO.get(k, 1.0), min_pbits=min_pbits,
-                    mbits=key_mbits(w_bits(n_ids)[1]))
+                    mbits=key_mbits(w_bits(n_ids)[1]) if runs_fit(n_ids, 1) else None)
         n_ev, n_u, fl, scan = c.stat[:4].cpu().tolist()
         if int(seg[5][0].item()) & 4:
             raise RuntimeError(f"k={k}: an emit region overflowed")

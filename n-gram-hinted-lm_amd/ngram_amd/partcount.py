@@ -433,7 +433,7 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
     e0.record()
     elib("ng_part_count32", ev32b, start, i32(pbits), i32(W), i32(M), sqk, sqv, qstart, out_k, i32(cb), esc_k, esc_c,
          u64(ESC_CAP), seg_cnt, seg_base, qcnt, dh2, i32(dtop - dc), i32(dc), ctypes.c_uint32(P32_LIMIT), flags,
-         i32(G2), slab, None, i32(0), i32(0), i32(0), 0, None)
+         i32(G2), slab, None, i32(0), i32(0), i32(0), _live_np(n_ids, W, M, d1, d2), None)
     e1.record()
     del ev32b, start, sqk, sqv, qstart
     # the words grouped by context: by their top dc bits (ng_seg_scatter), then within those groups by the next d2
@@ -473,6 +473,24 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
                      start2 if keep else None, ibits, deep, deep_n)
 
 
+def _live_np(n_ids: int, W: int, M: int, d1: int, d2: int) -> int:
+    """The partitions whose runs and slabs may be read: with events keyed by context range (M < W), those of the
+    first-pass buckets holding ids below n_ids (the others hold no events, and the count writes nothing for them);
+    else all of them."""
+    if M == W:
+        return 1 << (d1 + d2)
+    return ((max(n_ids, 1) - 1) >> (W - 16 - d1)) + 1 << d2
+
+
+def runs_fit(n_ids: int, ktop: int) -> bool:
+    """Whether count32's runs mode can take a level of n_ids context ids with top-ktop records: a first-pass bucket
+    holds at most 64 groups of ids (the count's run digit). The events are then best keyed by context range
+    (key_mbits); else by the pair hash over all W bits."""
+    idb, W = w_bits(n_ids)
+    agg = AGG_ID_BITS - 1 if ktop >= 8 else AGG_ID_BITS
+    return idb - first_digit(W) - min(agg, idb - first_digit(W)) <= 6
+
+
 def _count32_runs(elib: Lib, n_ids, ktop, W, M, cb, d1, d2, pbits, P, cap, ev32b, start, sqk, sqv, qstart, N, ibits,
                   gbits, G2, flags, stat, with_dist, agg_grid, event) -> Counted32:
     """count32's runs mode: the count writes each partition's words grouped by the gbits context-id bits below the
@@ -486,13 +504,12 @@ def _count32_runs(elib: Lib, n_ids, ktop, W, M, cb, d1, d2, pbits, P, cap, ev32b
     seg_base = torch.empty(G2, dtype=torch.int64, device=dev)
     qcnt = elib.zeros(max(N, 1), torch.int32, dev) if N else None
     runs = torch.empty(P << gbits, dtype=torch.int64, device=dev)  # a run's bounds: start | end << 32
-    # the runs ng_ctx_agg_runs reads: those of the buckets holding ids below n_ids (the count writes no others)
-    runs_np = ((max(n_ids, 1) - 1) >> (W - 16 - d1)) + 1 << d2
+    live_np = _live_np(n_ids, W, M, d1, d2)
     e0, e1 = event("count", cap)
     e0.record()
     elib("ng_part_count32", ev32b, start, i32(pbits), i32(W), i32(M), sqk, sqv, qstart, out_k, i32(cb), esc_k, esc_c,
          u64(ESC_CAP), seg_cnt, seg_base, qcnt, None, i32(0), i32(0), ctypes.c_uint32(P32_LIMIT), flags, i32(G2), None,
-         runs, i32(gbits), i32(16 + ibits), i32(d2), runs_np, stat[1:2])  # stat[1]: the distinct pairs (zero before)
+         runs, i32(gbits), i32(16 + ibits), i32(d2), live_np, stat[1:2])  # stat[1]: the distinct pairs (zero before)
     e1.record()
     del ev32b, start, sqk, sqv, qstart, seg_cnt, seg_base
     rec = torch.empty((max(n_ids, 1), RECORD_WORDS[ktop]), dtype=torch.int32, device=dev)
