@@ -189,11 +189,12 @@ int ng_pos_gather(const int* ctx_of, ng_i64 N, ng_i64 lo, ng_i64 hi, const uint1
  * pos[0..min(n, *n_dev)) only) inserted by compare-and-swap into table (cap + tail
  * slots, EMPTY-filled, linear probing without wrap from umulhi(key, cap)); ctx_of[i] = slot or -1 (compact:
  * ctx_of[j] for pos[j]), rep[slot] = the inserting position; counters[0] += the table's occupied slots
- * afterwards, counters[1] != 0: the table is too small (a probe reached its end or walked 256 slots),
+ * afterwards (the inserts counted per wave into wave_ins, ceil(n / 256) * 4 u32 of scratch; NULL: a scan of the
+ * table), counters[1] != 0: the table is too small (a probe reached its end or walked 256 slots),
  * counters[2] += key collisions found against the representative (k > 4) */
 int ng_query_index(const uint16_t* x, const int* avail, const int* pos, ng_i64 n, const ng_u64* n_dev, int k,
                    ng_u64* table, ng_u64 cap, ng_u64 slots, uint32_t* rep, int* ctx_of, int compact,
-                   ng_u64* counters, void* stream);
+                   ng_u64* counters, uint32_t* wave_ins, void* stream);
 /* move a query index into a smaller EMPTY-filled table (cap + tail = slots): ctx_of[0..n) re-pointed, remap
  * (old_slots ints) scratch, counters[1] = 1 on reaching the new table's end */
 int ng_query_index_shrink(const ng_u64* old_t, const uint32_t* old_rep, ng_u64 old_slots, ng_u64* table, ng_u64 cap,

@@ -1091,9 +1091,11 @@ template <int K>
 #define QI_MAXWALK 256
 __global__ void qindex_insert_k(const u16* __restrict__ x, const int* __restrict__ avail, const int* __restrict__ pos,
                                 i64 n, int k, u64* table, u64 cap, u64 slots, u32* rep, int* __restrict__ ctx_of,
-                                int compact, u64* counters, const u64* __restrict__ n_dev = nullptr) {
+                                int compact, u64* counters, const u64* __restrict__ n_dev = nullptr,
+                                u32* __restrict__ wave_ins = nullptr) {
     if (n_dev && (i64)*n_dev < n) n = (i64)*n_dev;  // a device-side count (at most the grid's n)
     const i64 j = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+    bool ins = false;  // this position's context took an empty slot
     if (j < n) {
         const i64 i = pos ? pos[j] : j;
         i64 slot = -1;
@@ -1119,6 +1121,7 @@ __global__ void qindex_insert_k(const u16* __restrict__ x, const int* __restrict
                     if (prev == EMPTY) {  // this position inserted the context: it is the representative
                         rep[s] = (u32)i;
                         slot = (i64)s;
+                        ins = true;
                         break;
                     }
                     if (prev == key) {
@@ -1131,6 +1134,11 @@ __global__ void qindex_insert_k(const u16* __restrict__ x, const int* __restrict
         }
         if (compact) ctx_of[j] = (int)slot;
         else if (slot >= 0 || !pos) ctx_of[i] = (int)slot;
+    }
+    // the wave's inserted contexts (no block barrier: a wave done early leaves at once)
+    if (wave_ins) {
+        const u64 m = __ballot(ins);
+        if (lane_id() == 0) wave_ins[j / WAVE] = (u32)__popcll(m);
     }
 }
 
@@ -1214,19 +1222,23 @@ extern "C" int ng_query_index_shrink(const u64* old_t, const u32* old_rep, u64 o
 // device-side count) into table (cap + tail slots, EMPTY-filled):
 // ctx_of[i] = slot (-1 where invalid; with pos, only listed positions are written; compact: ctx_of[j] for pos[j],
 // n entries), rep[slot] = the position that inserted it.
-// counters[0] += the table's occupied slots afterwards (its contexts), counters[1] bit 0 if a probe ran into the
+// counters[0] += the table's occupied slots afterwards (its contexts: the inserts, counted per wave into wave_ins, of
+// grid_for(n, 256) * 4 u32, and summed; wave_ins NULL: a scan of the table), counters[1] bit 0 if a probe ran into the
 // table's end, bit 1 if an insert walked QI_MAXWALK slots (a table too small: build it bigger); with k > 4, counters[2] += positions whose tokens differ from their slot's representative (a 64-bit
 // key collision).
 extern "C" int ng_query_index(const u16* x, const int* avail, const int* pos, i64 n, const u64* n_dev, int k,
                               u64* table, u64 cap, u64 slots, u32* rep, int* ctx_of, int compact, u64* counters,
-                              void* stream) {
+                              u32* wave_ins, void* stream) {
     if (n <= 0) return 0;
     if (cap == 0 || slots <= cap || slots > (1ull << 31) || (n_dev && !pos)) return -1;
     hipStream_t st = (hipStream_t)stream;
-    LEVEL_DISPATCH(k, (qindex_insert_k<K><<<grid_for(n, 256), 256, 0, st>>>(x, avail, pos, n, k, table, cap, slots, rep, ctx_of, compact, counters, n_dev)));
+    const int g = grid_for(n, 256);
+    LEVEL_DISPATCH(k, (qindex_insert_k<K><<<g, 256, 0, st>>>(x, avail, pos, n, k, table, cap, slots, rep, ctx_of,
+                                                             compact, counters, n_dev, wave_ins)));
     if (k > 4) qindex_verify_k<<<grid_for(n, 256), 256, 0, st>>>(x, pos, n, k, ctx_of, compact, rep, counters + 2, n_dev);
-    const int g = grid_for((i64)slots, 256);
-    count_occupied_k<<<g < 1024 ? g : 1024, 256, 0, st>>>(table, slots, counters);
+    if (wave_ins) return prim::sum_u32(wave_ins, (i64)g * (256 / WAVE), counters, st);
+    const int go = grid_for((i64)slots, 256);
+    count_occupied_k<<<go < 1024 ? go : 1024, 256, 0, st>>>(table, slots, counters);
     return (int)hipGetLastError();
 }
 

@@ -28,6 +28,9 @@ size_t reduce_by_key_temp_bytes(i64 n);
 int reduce_by_key(const u64* kin, u64* kout, const u32* vin, u32* vout, i64* nruns, i64 n, void* temp,
                   hipStream_t st);
 
+// *total += the sum of n u32 (a small grid: one atomic per block)
+int sum_u32(const u32* in, i64 n, u64* total, hipStream_t st);
+
 // fill helpers
 int fill_u64(u64* p, u64 v, i64 n, hipStream_t st);
 int fill_u32(u32* p, u32 v, i64 n, hipStream_t st);

@@ -159,6 +159,14 @@ __global__ void __launch_bounds__(BLOCK) sum_wide_k(const u32* __restrict__ in, 
     }
 }
 
+int sum_u32(const u32* in, i64 n, u64* total, hipStream_t st) {
+    if (n < 0) return -1;
+    if (n == 0) return 0;
+    const i64 g = (n + BLOCK - 1) / BLOCK;
+    sum_wide_k<<<(unsigned)(g < SUM_WIDE_BLOCKS ? g : SUM_WIDE_BLOCKS), BLOCK, 0, st>>>(in, n, total);
+    return (int)hipGetLastError();
+}
+
 size_t scan_u32_temp_bytes(i64 n) { return scan_temp<u32>(n) + 256; }
 
 // The offsets are u32 (they wrap once the sum reaches 2^32); *total is the exact u64 sum, read before the scan (out

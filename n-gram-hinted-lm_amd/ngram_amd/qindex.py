@@ -54,8 +54,9 @@ class QueryIndex:
             if counters is None or not (defer and expect is not None and not _resized):
                 counters = lib.zeros(3, torch.int64, dev)
             if m:
+                wave_ins = torch.empty((m + 255) // 256 * 4, dtype=torch.int32, device=dev)  # inserts per wave
                 lib("ng_query_index", x, avail, positions, m, n_dev, i32(k), table, u64(cap), u64(slots), rep,
-                    ctx_of, i32(int(compact and positions is not None)), counters)
+                    ctx_of, i32(int(compact and positions is not None)), counters, wave_ins)
             if defer and expect is not None and not _resized:
                 self.pending = counters
                 self.n, self.cap, self.ids, self.table, self.rep, self.ctx_of = None, cap, slots, table, rep, ctx_of
