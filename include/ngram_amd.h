@@ -154,6 +154,9 @@ int ng_scan_sink(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, ui
  * the device flag is set, only bits whose previous bit is set too; two-phase temp storage (temp NULL: size) */
 int ng_bits_list(void* temp, size_t* temp_bytes, const uint32_t* bm, ng_i64 nwords, ng_u64* out, ng_u64* total,
                  const uint32_t* pre, void* stream);
+/* ng_bits_list's positions as int32 (nwords <= 2^26), the first cap kept (*total counts every set bit) */
+int ng_bits_list32(void* temp, size_t* temp_bytes, const uint32_t* bm, ng_i64 nwords, int* out, ng_i64 cap,
+                   ng_u64* total, const uint32_t* pre, void* stream);
 /* existence only: hit bitmap and bit (context id) of the u32 words hit set (hit zeroed by the caller); ids (may be
  * NULL): ids[p] = the context id at each hit position p; sparse as ng_scan_count's; pre (may be NULL): the prefix
  * rule's device flag, as ng_scan_emit's (valid where every query context's prefix is a query context of the level
@@ -330,11 +333,12 @@ int ng_ctx_summary(const ng_u64* w, ng_i64 U, int cb, const ng_u64* esc_k, const
                    uint32_t* flags, void* stream);
 /* per query position from ng_ctx_summary's records and pair counts and the counted lookups qcnt (may be NULL: no
  * cnt): tot, dist, cnt (thr: the CNT_TOP threshold scores, may be NULL), the first kout of ktop top entries, mask bit
- * li (mask may be NULL) */
+ * li (mask may be NULL); zeros where the context is absent or never occurred, positions of contexts outside [lo, hi)
+ * left alone; hit_bits (may be NULL, lo 0): bit i where position i's context occurred (ceil(N / 64) * 2 u32) */
 int ng_pos_summary(const int* ctx_of, ng_i64 N, ng_i64 lo, ng_i64 hi, const uint16_t* tgt, const uint32_t* rec,
                    const uint32_t* dist, const ng_u64* thr, const uint32_t* qcnt, int ktop, int kout, int li,
                    int* out_tot, int* out_dist, int* out_cnt, uint16_t* out_tok, uint32_t* out_tcnt, int* mask,
-                   void* stream);
+                   uint32_t* hit_bits, void* stream);
 /* corpus-wide level build (count_table.rs build_level :491-631): contexts into ck (slot = id) and per corpus position
  * its event ev[p] = mix64(slot << 16 | next) (EMPTY: none), counted afterwards by the partitioned count; flags[0]
  * bit 1: context table full (rerun bigger) */

@@ -352,9 +352,10 @@ __global__ void __launch_bounds__(256) scan_compact_k(const u16* __restrict__ to
     sink_end(sink, &ss);
 }
 
-// A bitmap's set bits listed in two passes over blocks of BL_BLOCK * BL_ROUNDS words: each block's count, a scan of
-// those counts, then each block lists its bits in order (a round of BL_BLOCK words at a time, their offsets by a
-// block-wide scan), so no per-word offsets go through memory.
+// A bitmap's set bits listed in two passes over blocks of up to BL_ROUNDS rounds of BL_BLOCK words (fewer rounds for
+// a small bitmap, so that it still spreads over about 1024 blocks): each block's count, a scan of those counts, then
+// each block lists its bits in order (a round of BL_BLOCK words at a time, their offsets by a block-wide scan), so no
+// per-word offsets go through memory.
 #define BL_BLOCK 256
 #define BL_ROUNDS 32
 __device__ __forceinline__ u32 bl_block_excl(u32 c, u32* s_w, u32& total) {
@@ -379,13 +380,13 @@ __device__ __forceinline__ u32 bl_block_excl(u32 c, u32* s_w, u32& total) {
 }
 
 __global__ void __launch_bounds__(BL_BLOCK) bits_count_k(const u32* __restrict__ bm, i64 nwords, u32* __restrict__ cnt,
-                                                         const u32* pre_flag) {
+                                                         const u32* pre_flag, int rounds) {
     __shared__ u32 s_w[BL_BLOCK / WAVE];
     const bool pre = pre_on(pre_flag);
-    const i64 w0 = blockIdx.x * (i64)(BL_BLOCK * BL_ROUNDS);
+    const i64 w0 = blockIdx.x * (i64)(BL_BLOCK * rounds);
     u32 c = 0;
 #pragma unroll 4
-    for (int r = 0; r < BL_ROUNDS; ++r) {
+    for (int r = 0; r < rounds; ++r) {
         const i64 w = w0 + r * BL_BLOCK + threadIdx.x;
         if (w < nwords) c += (u32)__popc(gate_word(bm, w, pre));
     }
@@ -394,14 +395,16 @@ __global__ void __launch_bounds__(BL_BLOCK) bits_count_k(const u32* __restrict__
     if (threadIdx.x == 0) cnt[blockIdx.x] = total;
 }
 
+// T: u64 positions, or int (below 2^31) with the first cap kept.
+template <typename T>
 __global__ void __launch_bounds__(BL_BLOCK) bits_list_k(const u32* __restrict__ bm, i64 nwords,
-                                                        const u32* __restrict__ boff, u64* __restrict__ out,
-                                                        const u32* pre_flag) {
+                                                        const u32* __restrict__ boff, T* __restrict__ out,
+                                                        const u32* pre_flag, u64 cap, int rounds) {
     __shared__ u32 s_w[BL_BLOCK / WAVE];
     const bool pre = pre_on(pre_flag);
-    const i64 w0 = blockIdx.x * (i64)(BL_BLOCK * BL_ROUNDS);
+    const i64 w0 = blockIdx.x * (i64)(BL_BLOCK * rounds);
     u64 run = boff[blockIdx.x];
-    for (int r = 0; r < BL_ROUNDS; ++r) {
+    for (int r = 0; r < rounds; ++r) {
         const i64 w = w0 + r * BL_BLOCK + threadIdx.x;
         u32 word = w < nwords ? gate_word(bm, w, pre) : 0u;
         u32 total;
@@ -409,7 +412,8 @@ __global__ void __launch_bounds__(BL_BLOCK) bits_list_k(const u32* __restrict__ 
         while (word) {
             const int b = __ffs(word) - 1;
             word &= word - 1;
-            out[at++] = (u64)((w << 5) + b);
+            if (at < cap) out[at] = (T)((w << 5) + b);
+            ++at;
         }
         run += total;
     }
@@ -887,10 +891,14 @@ extern "C" int ng_scan_sink(const u16* tok, i64 L, int k, const u32* bm_in, u32*
 // The set bits of a bitmap (nwords u32 words) as positions, in order: out[r] = the position of the r-th set bit,
 // *total = their number. pre (may be NULL): while the device flag is set, only the bits whose previous bit is set too
 // (ng_scan_emit's prefix rule). Two-phase temp storage (temp NULL: *temp_bytes set).
-extern "C" int ng_bits_list(void* temp, size_t* temp_bytes, const u32* bm, i64 nwords, u64* out, u64* total,
-                            const u32* pre, void* stream) {
+template <typename T>
+static int bits_list(void* temp, size_t* temp_bytes, const u32* bm, i64 nwords, T* out, u64 cap, u64* total,
+                     const u32* pre, hipStream_t st) {
     if (!temp_bytes || nwords < 0) return -1;
-    const i64 nb = (nwords + BL_BLOCK * BL_ROUNDS - 1) / (BL_BLOCK * BL_ROUNDS);
+    // words per block: BL_ROUNDS rounds of BL_BLOCK, fewer for a small bitmap (about 1024 blocks at least)
+    const i64 per = (nwords + 1023) / 1024;
+    const int rounds = per >= BL_BLOCK * BL_ROUNDS ? BL_ROUNDS : per <= BL_BLOCK ? 1 : (int)((per + BL_BLOCK - 1) / BL_BLOCK);
+    const i64 nb = (nwords + BL_BLOCK * rounds - 1) / (BL_BLOCK * rounds);
     const size_t b0 = ((size_t)(nb + 64) * 4 + 255) & ~(size_t)255;
     const size_t need = b0 + prim::scan_u32_temp_bytes(nb + 1) + 256;
     if (!temp) {
@@ -898,15 +906,26 @@ extern "C" int ng_bits_list(void* temp, size_t* temp_bytes, const u32* bm, i64 n
         return 0;
     }
     if (*temp_bytes < need) return -1;
-    hipStream_t st = (hipStream_t)stream;
     if (nwords == 0) return prim::fill_u64(total, 0ull, 1, st);
     u32* off = (u32*)temp;
     void* stemp = (char*)temp + b0;
-    bits_count_k<<<(unsigned)nb, BL_BLOCK, 0, st>>>(bm, nwords, off, pre);
+    bits_count_k<<<(unsigned)nb, BL_BLOCK, 0, st>>>(bm, nwords, off, pre, rounds);
     int e = prim::exclusive_scan_u32(off, off, nb, total, stemp, st);
     if (e) return e;
-    bits_list_k<<<(unsigned)nb, BL_BLOCK, 0, st>>>(bm, nwords, off, out, pre);
+    bits_list_k<T><<<(unsigned)nb, BL_BLOCK, 0, st>>>(bm, nwords, off, out, pre, cap, rounds);
     return (int)hipGetLastError();
+}
+
+extern "C" int ng_bits_list(void* temp, size_t* temp_bytes, const u32* bm, i64 nwords, u64* out, u64* total,
+                            const u32* pre, void* stream) {
+    return bits_list<u64>(temp, temp_bytes, bm, nwords, out, ~0ull, total, pre, (hipStream_t)stream);
+}
+
+// ng_bits_list's positions as int (the bitmap below 2^31 bits), the first cap of them kept (*total counts them all).
+extern "C" int ng_bits_list32(void* temp, size_t* temp_bytes, const u32* bm, i64 nwords, int* out, i64 cap,
+                              u64* total, const u32* pre, void* stream) {
+    if (nwords > (1ll << 26) || cap < 0) return -1;
+    return bits_list<int>(temp, temp_bytes, bm, nwords, out, (u64)cap, total, pre, (hipStream_t)stream);
 }
 
 namespace {

@@ -551,13 +551,21 @@ __global__ void __launch_bounds__(256) pos_summary_k(const int* __restrict__ ctx
                                                      const u32* __restrict__ qcnt, int kout, int li,
                                                      int* __restrict__ out_tot, int* __restrict__ out_dist,
                                                      int* __restrict__ out_cnt, u16* __restrict__ out_tok,
-                                                     u32* __restrict__ out_tcnt, int* __restrict__ mask) {
+                                                     u32* __restrict__ out_tcnt, int* __restrict__ mask,
+                                                     u32* __restrict__ hit_bits) {
     using R = CtxRecord<KT>;
     const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
-    if (i >= N) return;
-    i64 c = ctx_of[i];
-    if (c >= 0 && (c < lo || c >= hi)) return;  // a context of another id range: that range's call writes it
-    const u32 d = c >= 0 ? dist[c - lo] : 0u;
+    i64 c = i < N ? ctx_of[i] : -1;
+    const bool other = c >= 0 && (c < lo || c >= hi);  // a context of another id range: that range's call writes it
+    const u32 d = c >= 0 && !other ? dist[c - lo] : 0u;
+    if (hit_bits) {  // bit i: position i's context occurred (a wave's 64 positions are two words)
+        const u64 m = __ballot(d != 0);
+        if (lane_id() == 0 && i < N) {
+            hit_bits[i >> 5] = (u32)m;
+            hit_bits[(i >> 5) + 1] = (u32)(m >> 32);
+        }
+    }
+    if (i >= N || other) return;
     if (d == 0) {  // no context, or one that never occurred: zeros (so the outputs need no fill before)
         out_tot[i] = 0;
         out_dist[i] = 0;
@@ -746,19 +754,20 @@ extern "C" int ng_ctx_summary(const u64* w, i64 U, int cb, const u64* esc_k, con
 // Per query position from the per-context records and pair counts (ng_ctx_summary's) and the counted lookups qcnt: tot,
 // dist, cnt (thr may be NULL: the CNT_TOP threshold scores), the first kout <= ktop top entries, mask bit li (mask may
 // be NULL). Every position whose context is absent (ctx_of < 0) or did not occur (dist 0) gets zeros; those whose
-// context id lies outside [lo, hi) are left as they are.
+// context id lies outside [lo, hi) are left as they are. hit_bits (may be NULL; lo 0, every id in range): bit i set
+// where position i's context occurred (ceil(N / 64) * 2 u32 words, all written), for the next level's list.
 extern "C" int ng_pos_summary(const int* ctx_of, i64 N, i64 lo, i64 hi, const u16* tgt, const u32* rec, const u32* dist,
                               const u64* thr, const u32* qcnt, int ktop, int kout, int li, int* out_tot, int* out_dist,
-                              int* out_cnt, u16* out_tok, u32* out_tcnt, int* mask, void* stream) {
-    if (kout < 0 || kout > ktop || (mask && (li < 0 || li > 30))) return -1;
+                              int* out_cnt, u16* out_tok, u32* out_tcnt, int* mask, u32* hit_bits, void* stream) {
+    if (kout < 0 || kout > ktop || (mask && (li < 0 || li > 30)) || (hit_bits && lo != 0)) return -1;
     if (N <= 0) return 0;
     const int g = grid_for(N, 256);
     hipStream_t st = (hipStream_t)stream;
     switch (ktop) {
-        case 1: pos_summary_k<1><<<g, 256, 0, st>>>(ctx_of, N, lo, hi, tgt, rec, dist, thr, qcnt, kout, li, out_tot, out_dist, out_cnt, out_tok, out_tcnt, mask); break;
-        case 2: pos_summary_k<2><<<g, 256, 0, st>>>(ctx_of, N, lo, hi, tgt, rec, dist, thr, qcnt, kout, li, out_tot, out_dist, out_cnt, out_tok, out_tcnt, mask); break;
-        case 4: pos_summary_k<4><<<g, 256, 0, st>>>(ctx_of, N, lo, hi, tgt, rec, dist, thr, qcnt, kout, li, out_tot, out_dist, out_cnt, out_tok, out_tcnt, mask); break;
-        case 8: pos_summary_k<8><<<g, 256, 0, st>>>(ctx_of, N, lo, hi, tgt, rec, dist, thr, qcnt, kout, li, out_tot, out_dist, out_cnt, out_tok, out_tcnt, mask); break;
+        case 1: pos_summary_k<1><<<g, 256, 0, st>>>(ctx_of, N, lo, hi, tgt, rec, dist, thr, qcnt, kout, li, out_tot, out_dist, out_cnt, out_tok, out_tcnt, mask, hit_bits); break;
+        case 2: pos_summary_k<2><<<g, 256, 0, st>>>(ctx_of, N, lo, hi, tgt, rec, dist, thr, qcnt, kout, li, out_tot, out_dist, out_cnt, out_tok, out_tcnt, mask, hit_bits); break;
+        case 4: pos_summary_k<4><<<g, 256, 0, st>>>(ctx_of, N, lo, hi, tgt, rec, dist, thr, qcnt, kout, li, out_tot, out_dist, out_cnt, out_tok, out_tcnt, mask, hit_bits); break;
+        case 8: pos_summary_k<8><<<g, 256, 0, st>>>(ctx_of, N, lo, hi, tgt, rec, dist, thr, qcnt, kout, li, out_tot, out_dist, out_cnt, out_tok, out_tcnt, mask, hit_bits); break;
         default: return -1;
     }
     return (int)hipGetLastError();

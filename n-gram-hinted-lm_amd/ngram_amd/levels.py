@@ -136,6 +136,7 @@ class LevelBuild:
         # every level's device-side results in one tensor, read with one copy after the last level: per level the
         # 32-bit count's events, pairs and flags, the scan's flags, the listed query positions, the index's counters
         stats = elib.zeros((len(self.levels), 8), torch.int64, dev)
+        hit_bits = torch.empty((N + 63) // 64 * 2, dtype=torch.int32, device=dev)  # a level's occurred contexts' positions
         for li, k in enumerate(self.levels):
             t0 = time.perf_counter()
             prev = self.levels[li - 1] if li else None
@@ -148,7 +149,8 @@ class LevelBuild:
                     seen_cap = min(N, int(self.seen_of[k] * max(SEEN_MARGIN, 1.0)) + 4096)
                     seen = torch.empty(max(seen_cap, 1), dtype=torch.int32, device=dev)
                     seen_n = stats[li, 4:5]
-                    elib.cub("ng_select_positive", out[1, li - 1], N, seen, seen_cap, seen_n)
+                    # the positions whose level li - 1 context occurred: the bits its ng_pos_summary set
+                    elib.cub("ng_bits_list32", hit_bits, hit_bits.numel(), seen, seen_cap, seen_n, None)
                 else:
                     seen = torch.nonzero(out[1, li - 1] > 0).squeeze(1).to(torch.int32)
                     self.seen_of[k] = int(seen.numel())
@@ -212,7 +214,7 @@ class LevelBuild:
             e0.record()
             elib("ng_pos_summary", vi.ctx_of, N, 0, vi.ids, tgt, sm.rec, sm.dist, thr, c.qcnt, i32(ktop), i32(topk),
                  i32(li), out[0, li], out[1, li], out[2, li], res.top_tok[li] if topk else None,
-                 res.top_cnt[li] if topk else None, res.mask)
+                 res.top_cnt[li] if topk else None, res.mask, hit_bits if li + 1 < len(self.levels) else None)
             e1.record()
             if kept:
                 res.kept[k] = (vi.ctx_of, sm.rec)

@@ -178,7 +178,7 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
             o_dist = torch.empty(m, dtype=torch.int32, device=dev)
             o_tc = torch.empty(m, dtype=torch.int32, device=dev)
             elib("ng_pos_summary", vi.ctx_of, m, 0, vi.ids, None, rec, dist, None, None, i32(1), i32(1), i32(0),
-                 o_tot, o_dist, o_tc, o_tok, o_cnt, None)
+                 o_tot, o_dist, o_tc, o_tok, o_cnt, None, None)
             del rec, dist, o_tot, o_dist, o_tc
         else:  # unpacked pairs: sorted by key, per-context top entry by selection
             _top1_unpacked(elib, lib, vi, c, x, o_tok, o_cnt)
@@ -340,7 +340,7 @@ def _count_ids(elib: Lib, lib: Lib, tok, L: int, level: tuple, k: int, length, f
         sm = summarize(elib, lib, c, n_ids, 1)
         o = [torch.empty(m, dtype=torch.int32, device=dev) for _ in range(3)]
         elib("ng_pos_summary", fids, m, 0, n_ids, None, sm.rec, sm.dist, None, None, i32(1), i32(1), i32(0), o[0], o[1],
-             o[2], o_tok, o_cnt, None)
+             o[2], o_tok, o_cnt, None, None)
     else:  # unpacked pairs: sorted by key, per-context top entry by selection
         _top1_unpacked(elib, lib, SimpleNamespace(ctx_of=fids, ids=n_ids), c, None, o_tok, o_cnt)
     nxt[fpos] = o_tok
@@ -375,7 +375,7 @@ def _count32_final(elib: Lib, seg: tuple, n_ids: int, k: int, fids, fpos, m: int
     o_tok = torch.zeros(m, dtype=torch.int16, device=dev)
     o_cnt = torch.zeros(m, dtype=torch.int32, device=dev)
     elib("ng_pos_summary", fids, m, 0, n_ids, None, c.rec, c.dist, None, None, i32(1), i32(1), i32(0), o[0], o[1],
-         o[2], o_tok, o_cnt, None)
+         o[2], o_tok, o_cnt, None, None)
     nxt[fpos] = o_tok
     cnt[fpos] = o_cnt
     return True
@@ -461,7 +461,7 @@ def _count_batch(elib: Lib, lib: Lib, tok, L: int, x, avail, batch: list, levels
     o_dist = torch.empty(m, dtype=torch.int32, device=dev)
     o_tc = torch.empty(m, dtype=torch.int32, device=dev)
     elib("ng_pos_summary", ctx_of, m, 0, n_ids, None, sm.rec, sm.dist, None, None, i32(1), i32(1), i32(0), o_tot, o_dist,
-         o_tc, o_tok, o_cnt, None)
+         o_tc, o_tok, o_cnt, None, None)
     nxt[fpos] = o_tok
     cnt[fpos] = o_cnt
 

@@ -167,3 +167,44 @@ def test_bits_list_matches_numpy(lib, nwords, density, pre):
     lib.cub("ng_bits_list", bm, nwords, out, total, flag)
     assert int(total.item()) == len(want)
     assert np.array_equal(out.cpu().numpy()[: len(want)], want)
+
+
+@pytest.mark.parametrize("cap_frac", [1.0, 0.5, 0.0])
+def test_bits_list32_keeps_the_first_cap(lib, cap_frac):
+    """ng_bits_list32 (int32 positions, as the level pipeline lists the next level's query positions) against numpy:
+    the first cap set bits' positions in order, nothing written past cap, and the count of every set bit."""
+    rng = np.random.default_rng(int(cap_frac * 10))
+    nwords = 70_001
+    bits = rng.random(nwords * 32) < 0.3
+    words = np.packbits(bits.reshape(-1, 8)[:, ::-1], axis=1).reshape(-1).view("<u4")
+    want = np.flatnonzero(bits).astype(np.int64)
+    cap = int(len(want) * cap_frac)
+    bm = torch.from_numpy(words.view(np.int32).copy()).cuda()
+    out = torch.full((cap + 64,), -7, dtype=torch.int32, device="cuda")
+    total = torch.zeros(1, dtype=torch.int64, device="cuda")
+    lib.cub("ng_bits_list32", bm, nwords, out, cap, total, None)
+    o = out.cpu().numpy()
+    assert int(total.item()) == len(want)
+    assert np.array_equal(o[:cap], want[:cap])
+    assert (o[cap:] == -7).all()
+
+
+def test_pos_summary_hit_bits(lib):
+    """ng_pos_summary's bitmap of the positions whose context occurred (dist > 0), the next level's list: bit i set
+    exactly where ctx_of[i] >= 0 and dist[ctx_of[i]] > 0; zeros written for the others, over a ragged N."""
+    rng = np.random.default_rng(5)
+    N, n_ids = 100_003, 5000
+    ctx_of = np.where(rng.random(N) < 0.8, rng.integers(0, n_ids, N), -1).astype(np.int32)
+    dist = np.where(rng.random(n_ids) < 0.5, rng.integers(1, 9, n_ids), 0).astype(np.int32)
+    rec = torch.zeros((n_ids, 4), dtype=torch.int32, device="cuda")
+    outs = [torch.full((N,), -9, dtype=torch.int32, device="cuda") for _ in range(3)]
+    tok = torch.full((N,), -9, dtype=torch.int16, device="cuda")
+    tcnt = torch.full((N,), -9, dtype=torch.int32, device="cuda")
+    hb = torch.full(((N + 63) // 64 * 2,), -1, dtype=torch.int32, device="cuda")
+    lib("ng_pos_summary", torch.from_numpy(ctx_of).cuda(), N, 0, n_ids, None, rec, torch.from_numpy(dist).cuda(), None,
+        None, i32(1), i32(1), i32(0), outs[0], outs[1], outs[2], tok, tcnt, None, hb)
+    occ = (ctx_of >= 0) & (dist[np.maximum(ctx_of, 0)] > 0)
+    got = np.unpackbits(hb.cpu().numpy().view(np.uint8), bitorder="little")[:N].astype(bool)
+    assert np.array_equal(got, occ)
+    assert np.array_equal(outs[1].cpu().numpy(), np.where(occ, dist[np.maximum(ctx_of, 0)], 0))
+    assert (outs[2].cpu().numpy() == 0).all() and (tok.cpu().numpy()[~occ] == 0).all()
