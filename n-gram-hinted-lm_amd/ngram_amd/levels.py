@@ -113,7 +113,12 @@ class LevelBuild:
         self.kernel_events = []
         self.grid = torch.cuda.get_device_properties(dev).multi_processor_count * SCAN_BLOCKS_PER_CU
         nwords = self.L // 32
-        bms = {k: elib.zeros(nwords, torch.int32, dev) for k in self.levels}
+        # the levels' hit bitmaps: a dense, sparse or compact scan writes every word of its range, so only a list
+        # scan's range is zeroed (before it sets its bits); hit statistics count whole bitmaps, so they zero them all
+        bms = {k: torch.empty(nwords, dtype=torch.int32, device=dev) for k in self.levels}
+        if want_stats:
+            for bm in bms.values():
+                elib.fill(bm, 0)
         # every level's ng_pos_summary writes all N positions of its rows (zeros where the context is absent): no fill
         res = LevelOutputs(torch.empty((3, len(self.levels), N), dtype=torch.int32, device=dev))
         self._pre = torch.empty(1, dtype=torch.int32, device=dev)  # the prefix rule's device flag
@@ -354,6 +359,7 @@ class LevelBuild:
             if mode == 3:
                 if self._plist is None or self._plist.numel() < n32:
                     self._plist = torch.empty(max(self.sizes) + 64, dtype=torch.int64, device=dev)
+                elib.fill(bms[k][st // 32 : (st + n32) // 32], 0)  # the list scan only sets its hits' bits
                 n_list = elib.zeros(1, torch.int64, dev)
                 b0, b1 = self._event("bits_list", k, n32)
                 b0.record()
@@ -394,6 +400,7 @@ class LevelBuild:
         if mode == 3:
             if self._plist is None or self._plist.numel() < n:
                 self._plist = torch.empty(n + 64, dtype=torch.int64, device=dev)
+            elib.fill(bm_out[lo // 32 : hi // 32], 0)  # the list scan only sets its hits' bits
             n_list = elib.zeros(1, torch.int64, dev)
             b0, b1 = self._event("bits_list", k, n)
             b0.record()
