@@ -35,10 +35,13 @@ from . import partcount
 from .lib import Lib, i32, u64
 from .partcount import (W_MAX, check_summary, count32, count_events, emit_region, first_digit, key_mbits, summarize,
                         w_bits)
-from .qindex import QueryIndex
+from .qindex import EXPECT_MARGIN, LOAD as QLOAD, TAIL as QTAIL, QueryIndex
 
 SCAN_BLOCKS_PER_CU = 8  # level-scan blocks (grid-stride) per compute unit (c3 sweep: 8 fastest of 4-32)
 LIST_DENSITY = 0.05  # a level behind a sparser one probes the previous hits as a position list (c3 sweep)
+DENSE_LOAD = 0.22  # query-table load of a level probed at every position, where it keeps the count's layout (c3,
+# levels 2 and 3: 65.3-65.5 against 66.0-66.2 ms a step; 0.4-0.6 at level 3 made its scan slower, not faster, although
+# its table then fitted the 256 MB cache)
 SEEN_MARGIN = 1.05  # room for a level's query positions listed on the device: this times the last build's count
 # (at least 1: a list that overflowed is listed again in room for the count it found)
 TOPS = (1, 2, 4, 8)  # the record widths ng_ctx_summary writes
@@ -159,18 +162,18 @@ class LevelBuild:
                 else:
                     seen = torch.nonzero(out[1, li - 1] > 0).squeeze(1).to(torch.int32)
                     self.seen_of[k] = int(seen.numel())
+            kept = k in keep
+            ktop = 8 if (kept or cnt_top is not None) else _record_width(topk)
             q0, q1 = self._event("qindex", k, N)
             q0.record()
             vi = QueryIndex(elib, x, avail, k, seen, expect=self.contexts_of.get(k), defer=_defer, n_dev=seen_n,
-                            counters=stats[li, 5:8])
+                            counters=stats[li, 5:8], load=self._load(k, prev, ktop, cnt_top))
             q1.record()
             if vi.n is None:
                 pending.append((li, k))
             else:
                 self.contexts_of[k] = vi.n
             t1 = time.perf_counter()
-            kept = k in keep
-            ktop = 8 if (kept or cnt_top is not None) else _record_width(topk)
             ev_fn = lambda name, n, k=k: self._event(name, k, n)  # noqa: E731
             _, W = w_bits(vi.ids)
             use32 = cnt_top is None and W <= W_MAX and k not in self.wide
@@ -316,6 +319,21 @@ class LevelBuild:
         if d is None or d >= 0.5:
             return 0
         return 3 if d < LIST_DENSITY else 2
+
+    def _load(self, k: int, prev, ktop: int, cnt_top) -> float | None:
+        """Level k's query-table load: DENSE_LOAD where its scan probes every position (the first level, or behind a
+        dense one) and a table at that load keeps the count's layout of one at the default load (the 32-bit count, its
+        runs mode: the same at both sizes, from the last build's context count); else None (the default)."""
+        expect = self.contexts_of.get(k)
+        if expect is None or (prev is not None and self._mode(1, [prev, k]) != 0):
+            return None
+
+        def layout(load: float) -> tuple:
+            ids = int(max(expect, 1) * max(EXPECT_MARGIN, 1.0) / load) + 1024 + QTAIL
+            return w_bits(ids)[1] <= W_MAX, partcount.runs_fit(ids, ktop)
+
+        use32 = cnt_top is None and k not in self.wide
+        return DENSE_LOAD if use32 and layout(DENSE_LOAD) == layout(QLOAD) else None
 
     @staticmethod
     def _mbits(W: int, ids: int, ktop: int) -> int:

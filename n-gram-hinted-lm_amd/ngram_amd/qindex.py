@@ -22,7 +22,7 @@ EXPECT_MARGIN = 1.2  # a table sized from an expected context count holds this m
 class QueryIndex:
     def __init__(self, lib: Lib, x: torch.Tensor, avail: torch.Tensor, k: int, positions: torch.Tensor | None = None,
                  compact: bool = False, expect: int | None = None, _resized: bool = False, defer: bool = False,
-                 n_dev: torch.Tensor | None = None, counters: torch.Tensor | None = None):
+                 n_dev: torch.Tensor | None = None, counters: torch.Tensor | None = None, load: float | None = None):
         """Index the valid k-contexts of the query positions (all of x, or the int32 `positions`). `compact`: ctx_of
         holds one entry per listed position (in their order) instead of one per position of x. `expect`: about how
         many contexts there are (e.g. the last build's count): the table is sized for them at once instead of for
@@ -34,14 +34,16 @@ class QueryIndex:
         device, with `positions`): only the first n_dev of the listed positions are indexed (a count the host has not
         read; `positions` holds at least that many, or the caller checks). `counters` (int64 [3] of zeros on the device,
         with `defer`): where the deferred build's counters go (e.g. a row of the caller's stats, read with its other
-        results in one copy), else new."""
+        results in one copy), else new. `load`: the contexts per slot a table sized from a context count aims at (LOAD
+        if None); a sparser table shortens the probe walks of a level probed at every position."""
         dev = x.device
+        ld = LOAD if load is None else load
         N = x.numel()
         m = N if positions is None else int(positions.numel())
         full = int(m / LOAD) + 1024  # room for every position's context at LOAD
         cap = full
         if expect is not None:
-            cap = min(cap, int(max(expect, 1) * max(EXPECT_MARGIN, 1.0) / LOAD) + 1024)
+            cap = min(cap, int(max(expect, 1) * max(EXPECT_MARGIN, 1.0) / ld) + 1024)
         while True:
             slots = cap + TAIL
             table = lib.full_ones(slots, torch.int64, dev)
@@ -71,13 +73,13 @@ class QueryIndex:
         if c[2]:
             raise RuntimeError(f"k={k}: {c[2]} query positions collide with another context's key")
         n_ctx = int(c[0])
-        if expect is not None and not _resized and n_ctx > LOAD * cap:  # fuller than LOAD: once more, at their size
-            self.__init__(lib, x, avail, k, positions, compact, n_ctx, _resized=True, n_dev=n_dev)
+        if expect is not None and not _resized and n_ctx > ld * cap:  # fuller than aimed at: once more, at their size
+            self.__init__(lib, x, avail, k, positions, compact, n_ctx, _resized=True, n_dev=n_dev, load=load)
             return
-        if m and cap > SHRINK * (n_ctx / LOAD) + 4096:
+        if m and cap > SHRINK * (n_ctx / ld) + 4096:
             # sized for every position, used by far fewer contexts: move them to a table sized for them (fewer bits
             # per context id, probes that stay in cache more often)
-            small = int(n_ctx / LOAD) + 1024
+            small = int(n_ctx / ld) + 1024
             while True:
                 t2 = torch.full((small + TAIL,), -1, dtype=torch.int64, device=dev)
                 r2 = torch.empty(small + TAIL, dtype=torch.int32, device=dev)
