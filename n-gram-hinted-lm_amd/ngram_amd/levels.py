@@ -350,7 +350,8 @@ class LevelBuild:
         elib, dev, G = self.elib, self.tok.device, self.grid
         shards = [i for i in range(len(self.sizes)) if i < self.level_shards[k]]
         nseg = len(shards) * G
-        ev_count = elib.zeros(max(nseg, 1), torch.int32, dev)
+        # every scan block writes its event count (an empty shard's scan writes zeros)
+        ev_count = torch.empty(nseg, dtype=torch.int32, device=dev) if nseg else elib.zeros(1, torch.int32, dev)
         last = self.events_of.get(k)
         dbits = first_digit(wbits) if wbits else 8
         dhist = torch.empty((1 << dbits) * max(nseg, 1), dtype=torch.int32, device=dev) \
@@ -410,7 +411,7 @@ class LevelBuild:
         R = -(-max(n, 1) // (G * 256)) * 256 if mode == 3 else emit_region(n, G)
         if G * R > regions.numel():
             raise RuntimeError(f"k={k}: the emit regions are too small for one scan over every shard")
-        ev_count = elib.zeros(G, torch.int32, dev)
+        ev_count = torch.empty(G, dtype=torch.int32, device=dev)  # every scan block writes its event count
         last = self.events_of.get(k)
         dbits = first_digit(wbits) if wbits else 8
         dhist = torch.empty((1 << dbits) * G, dtype=torch.int32, device=dev) \

@@ -389,7 +389,6 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
     del ev1, dpre
     N = nq = 0
     sqk = sqv = None
-    qstart = elib.zeros(P + 1, torch.int64, dev)
     if lookups is not None:
         ctx_of, tgt, qpos = lookups[:3]
         qn = lookups[3] if len(lookups) > 3 else None  # a device-side count of qpos's entries
@@ -403,7 +402,10 @@ def count32(elib: Lib, seg: tuple, n_ids: int, ktop: int, lookups: tuple | None,
         sqv = torch.empty(nq, dtype=torch.int32, device=dev)
         elib.cub("sort_pairs", qk, sqk, qv, sqv, nq, i32(64 - pbits), i32(64))
         del qk, qv
-        elib("ng_part_bounds", sqk, nq, i32(pbits), i32(0), qstart)
+        qstart = torch.empty(P + 1, dtype=torch.int64, device=dev)
+        elib("ng_part_bounds", sqk, nq, i32(pbits), i32(0), qstart)  # every partition's bound
+    else:
+        qstart = elib.zeros(P + 1, torch.int64, dev)  # no lookups
     e1.record()
     # the count's blocks: one per compute unit (its LDS table takes a compute unit's LDS), each a run of consecutive
     # partitions of about equal events; more blocks, run in turns, were slower (c3: 2048, 768, 512 and 256 blocks,
