@@ -89,6 +89,7 @@ class LevelBuild:
         self.kernel_events: list = []
         self.host_s = {"index": 0.0, "scan": 0.0, "count": 0.0}
         self._plist = None
+        self._no_bm = None  # the level whose list scan sets no hit bits (the last one, without hit statistics)
         self.wide: set = set()  # levels counted by the 64-bit path (count_events): their 32-bit count overflowed
         self.min_pbits: dict[int, int] = {}  # per level, partition bits the 32-bit count found too few, plus one
         self.seen_of: dict[int, int] = {}  # per level, the query positions whose previous level's context occurred
@@ -122,6 +123,8 @@ class LevelBuild:
         if want_stats:
             for bm in bms.values():
                 elib.fill(bm, 0)
+        # no level reads the last one's bitmap (only hit statistics do): its list scan sets no bits
+        self._no_bm = None if want_stats else self.levels[-1]
         # every level's ng_pos_summary writes all N positions of its rows (zeros where the context is absent): no fill
         res = LevelOutputs(torch.empty((3, len(self.levels), N), dtype=torch.int32, device=dev))
         self._pre = torch.empty(1, dtype=torch.int32, device=dev)  # the prefix rule's device flag
@@ -378,7 +381,8 @@ class LevelBuild:
             if mode == 3:
                 if self._plist is None or self._plist.numel() < n32:
                     self._plist = torch.empty(max(self.sizes) + 64, dtype=torch.int64, device=dev)
-                elib.fill(bms[k][st // 32 : (st + n32) // 32], 0)  # the list scan only sets its hits' bits
+                if k != self._no_bm:
+                    elib.fill(bms[k][st // 32 : (st + n32) // 32], 0)  # the list scan only sets its hits' bits
                 n_list = elib.zeros(1, torch.int64, dev)
                 b0, b1 = self._event("bits_list", k, n32)
                 b0.record()
@@ -389,8 +393,8 @@ class LevelBuild:
             dh = dhist[j * G :] if dhist is not None else None
             if mode == 3:
                 elib("ng_scan_emit_list", self.tok[st:], self._plist, n_list, i32(k), vi.table, u64(vi.cap), vi.rep,
-                     x, bms[k][st // 32 :], regions[j * G * R :], u64(R), ev_count[j * G :], flags, i32(G), dh, nseg,
-                     i32(wbits), i32(dbits), i32(mbits))
+                     x, bms[k][st // 32 :] if k != self._no_bm else None, regions[j * G * R :], u64(R),
+                     ev_count[j * G :], flags, i32(G), dh, nseg, i32(wbits), i32(dbits), i32(mbits))
             else:
                 elib("ng_scan_emit", self.tok[st:], n32, i32(k), bm_in, bms[k][st // 32 :], vi.table, u64(vi.cap),
                      vi.rep, x, regions[j * G * R :], u64(R), ev_count[j * G :], flags, i32(G), i32(mode), dh, nseg,
@@ -419,7 +423,8 @@ class LevelBuild:
         if mode == 3:
             if self._plist is None or self._plist.numel() < n:
                 self._plist = torch.empty(n + 64, dtype=torch.int64, device=dev)
-            elib.fill(bm_out[lo // 32 : hi // 32], 0)  # the list scan only sets its hits' bits
+            if k != self._no_bm:
+                elib.fill(bm_out[lo // 32 : hi // 32], 0)  # the list scan only sets its hits' bits
             n_list = elib.zeros(1, torch.int64, dev)
             b0, b1 = self._event("bits_list", k, n)
             b0.record()
@@ -429,8 +434,8 @@ class LevelBuild:
         e0.record()
         if mode == 3:
             elib("ng_scan_emit_list", self.tok[lo:], self._plist, n_list, i32(k), vi.table, u64(vi.cap), vi.rep, x,
-                 bm_out[lo // 32 :], regions, u64(R), ev_count, flags, i32(G), dhist, G, i32(wbits), i32(dbits),
-                 i32(mbits))
+                 bm_out[lo // 32 :] if k != self._no_bm else None, regions, u64(R), ev_count, flags, i32(G), dhist, G,
+                 i32(wbits), i32(dbits), i32(mbits))
         else:
             elib("ng_scan_emit", self.tok[lo:], n, i32(k), None if bm_in is None else bm_in[lo // 32 :],
                  bm_out[lo // 32 :], vi.table, u64(vi.cap), vi.rep, x, regions, u64(R), ev_count, flags, i32(G),
