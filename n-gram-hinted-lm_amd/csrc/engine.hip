@@ -691,6 +691,71 @@ extern "C" int ng_scan_exist(const u16* tok, i64 L, int k, const u32* bm_in, u32
 }
 
 namespace {
+// Level 1's existence scan with each 1-context's token as its id (no table: a 65536-bit set of the query tokens in
+// LDS): position p hits where tok[p - 1] is a query token and neither it nor tok[p] is SENT (ctx_key_at<1>'s context
+// and next token), which sets bm_out bit p, ids[p] = tok[p - 1] and the token's bit in hit (gathered per block in LDS,
+// then one atomicOr per nonzero word). A wave takes TOK1_PPL * 64 consecutive positions at a time, a lane every 64th.
+#define TOK1_PPL 4
+__global__ void __launch_bounds__(256) scan_tok1_k(const u16* __restrict__ tok, i64 L, const u32* __restrict__ member,
+                                                   u32* __restrict__ bm_out, u32* __restrict__ hit,
+                                                   u32* __restrict__ ids) {
+    __shared__ u32 mem[2048], agg[2048];
+    for (int i = threadIdx.x; i < 2048; i += blockDim.x) {
+        mem[i] = member[i];
+        agg[i] = 0u;
+    }
+    __syncthreads();
+    const int lane = lane_id();
+    const i64 nwords = L >> 5;  // L is a multiple of 32
+    const i64 span = (i64)WAVE * TOK1_PPL;
+    const i64 stride = (i64)gridDim.x * (blockDim.x / WAVE) * span;
+    for (i64 base = (blockIdx.x * (i64)(blockDim.x / WAVE) + threadIdx.x / WAVE) * span; base < L; base += stride) {
+        u32 c[TOK1_PPL], n[TOK1_PPL];
+#pragma unroll
+        for (int q = 0; q < TOK1_PPL; ++q) {  // the tokens of every round loaded before any is used
+            const i64 p = base + q * WAVE + lane;
+            c[q] = n[q] = SENT;
+            if (p < L) {
+                n[q] = tok[p];
+                if (p >= 1) c[q] = tok[p - 1];
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < TOK1_PPL; ++q) {
+            const i64 p0 = base + q * WAVE;
+            if (p0 >= L) break;  // wave-uniform
+            const u32 cq = c[q];
+            const bool h = cq != SENT && n[q] != SENT && ((mem[cq >> 5] >> (cq & 31)) & 1u);
+            const u64 b = __ballot(h);
+            if (lane == 0) bm_out[p0 >> 5] = (u32)b;
+            if (lane == 32 && (p0 >> 5) + 1 < nwords) bm_out[(p0 >> 5) + 1] = (u32)(b >> 32);
+            if (h) {
+                ids[p0 + lane] = cq;
+                const u32 m = 1u << (cq & 31);
+                if (!(agg[cq >> 5] & m)) atomicOr(&agg[cq >> 5], m);
+            }
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < 2048; i += blockDim.x)
+        if (agg[i]) atomicOr(&hit[i], agg[i]);
+}
+}  // namespace
+
+// Level 1's existence scan (ng_scan_exist's k = 1 with no gate) with the 1-context's token as its context id:
+// member: 2048 words, bit t set for each query token t; bm_out (L / 32 words) the hit positions; hit (2048 words,
+// zeroed by the caller) bit t set where token t occurred as a context; ids[p] = tok[p - 1] at each hit position p
+// (others left as they are). L a multiple of 32.
+extern "C" int ng_scan_tok1(const u16* tok, i64 L, const u32* member, u32* bm_out, u32* hit, u32* ids, int grid,
+                            void* stream) {
+    if (L < 0 || (L & 31) || (L > 0 && (!tok || !member || !bm_out || !hit || !ids))) return -1;
+    if (L == 0) return 0;
+    if (grid <= 0) grid = 2048;
+    scan_tok1_k<<<grid, 256, 0, (hipStream_t)stream>>>(tok, L, member, bm_out, hit, ids);
+    return (int)hipGetLastError();
+}
+
+namespace {
 // The counting scan of a level whose existence scan stored each hit position's context id (ids): per position p set
 // in bm, a context id whose bit is set in `final` emits mix64(id << 16 | tok[p]) as ng_scan_emit's events. A wave
 // loads 64 bitmap words (2048 positions) at a time, skips them if all are empty, else walks them 8 words (256

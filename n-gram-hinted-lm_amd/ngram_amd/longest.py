@@ -100,12 +100,26 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
                 levels.append(("list", hl, nh))
                 ladder.append((k2, int(elig[k2]), matched))
             break
+        prev = levels[-1] if levels else None
+        if prev is None and k == 1:
+            # level 1: a 1-context's id is its token, so no query table (ng_scan_tok1 holds the query tokens' set)
+            vi = _tok1_index(x, act)
+            hit = torch.zeros(2048, dtype=torch.int32, device=dev)
+            bm = torch.empty(nwords, dtype=torch.int32, device=dev)
+            ids = torch.empty(L, dtype=torch.int32, device=dev)
+            elib("ng_scan_tok1", tok, L, vi.member, bm, hit, ids, i32(TOK1_GRID))
+            levels.append(("bm", bm, _popcount(lib, bm), ids, act, vi.ctx_of, vi.ids))
+            ctx = vi.ctx_of.long()
+            act = act[((hit[ctx >> 5] >> (ctx & 31)) & 1) != 0]
+            length[act.long()] = k
+            ladder.append((k, int(elig[k]), int(act.numel())))
+            del vi, hit, ctx
+            continue
         per = _CONTEXTS.get(k)
         vi = QueryIndex(elib, x, avail, k, act, compact=True,
                         expect=None if per is None else int(per * act.numel()) + 1)
         _CONTEXTS[k] = vi.n / max(1, act.numel())
         hit = torch.zeros((vi.ids + 31) // 32, dtype=torch.int32, device=dev)  # a bit per context id
-        prev = levels[-1] if levels else None
         if prev is not None and (prev[0] == "list" or prev[2] * LIST_DIV < L):
             cand = prev[1] if prev[0] == "list" else _bits_list(elib, prev[1], prev[2])
             hl, nh = _scan_list(elib, tok, L, k, vi, x, cand, hit, 1, flags, grid)
@@ -195,6 +209,7 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
 
 
 SCAN_BLOCKS_PER_CU = 32  # scan blocks per compute unit
+TOK1_GRID = 2048  # level 1's scan blocks (each ORs its hit words into the level's once)
 EVENTS = [0]  # (context, next) events the last longest_match counted (its counting phase), for its timing dict
 DEVICE_LEVELS = True  # the existence phase's levels after the second list level run without host syncs
 LONG_FIRST = 8  # the device levels try level cap first when at least this many levels lie between
@@ -291,6 +306,18 @@ def _exist_device(elib: Lib, tok, L: int, x, avail, act, k0: int, cap: int, cand
             break
         res.append((k, hl[:nh], nh, matched))
     return res
+
+
+def _tok1_index(x: torch.Tensor, act: torch.Tensor) -> SimpleNamespace:
+    """Level 1's index without a table: each listed position's context id is its token (x[act], ids 0..65535), and
+    `member` (int32 [2048]) holds bit t for each token t among them."""
+    dev = x.device
+    ctx_of = x[act.long()].to(torch.int32) & 0xFFFF
+    seen = torch.zeros(65536, dtype=torch.bool, device=dev)
+    seen[ctx_of.long()] = True
+    w = (seen.view(2048, 32).to(torch.int64) << torch.arange(32, device=dev)).sum(1)
+    member = torch.where(w >= 1 << 31, w - (1 << 32), w).to(torch.int32)  # the words' bits, as int32
+    return SimpleNamespace(ctx_of=ctx_of, ids=65536, member=member)
 
 
 def _count_ids(elib: Lib, lib: Lib, tok, L: int, level: tuple, k: int, length, flags, grid: int, nxt, cnt) -> None:

@@ -8,7 +8,7 @@ import torch
 import oracle as O
 from ngram_amd import data
 from ngram_amd.data import device_tokens as load_shards
-from ngram_amd.lib import Lib
+from ngram_amd.lib import Lib, i32
 from ngram_amd.longest import LongestMatch, _segments, longest_match
 
 pytestmark = pytest.mark.gpu
@@ -149,3 +149,43 @@ def test_context_hint_from_a_much_smaller_call():
     got = LM.longest_match(tok, x, LM._segments(x, Lib()), 32)
     for g, w in zip(got[:3], want[:3]):
         assert torch.equal(g, w)
+
+
+@pytest.mark.parametrize("seed,grid", [(3, 2048), (4, 7)])
+def test_level_one_scan_by_token(seed, grid):
+    """ng_scan_tok1 (level 1 with the token as the context id) against numpy: position p hits where tok[p - 1] is a
+    query token and neither it nor tok[p] is SENT; the hit bitmap, the tokens that occurred and each hit's id. The
+    corpus starts and ends with SENT and holds SENT runs; a few blocks (grid 7) walk many rounds each."""
+    rng = np.random.default_rng(seed)
+    L = 32 * 3001
+    tok = rng.zipf(1.3, L).clip(1, 60000).astype(np.uint16)
+    tok[rng.random(L) < 0.02] = 0xFFFF
+    tok[:3] = 0xFFFF
+    tok[-5:] = 0xFFFF
+    query = np.unique(np.concatenate([rng.integers(0, 60000, 300), tok[rng.integers(0, L, 500)]])).astype(np.uint16)
+    query = query[query != 0xFFFF]
+    member = np.zeros(65536, bool)
+    member[query] = True
+    words = np.packbits(member.reshape(-1, 32)[:, ::-1], axis=1).view(">u4").astype(np.uint32).reshape(-1)
+    prev = np.concatenate([[0xFFFF], tok[:-1]]).astype(np.int64)
+    want_hit = (prev != 0xFFFF) & (tok != 0xFFFF) & member[prev]
+    want_bm = np.packbits(want_hit.reshape(-1, 32)[:, ::-1], axis=1).view(">u4").astype(np.uint32).reshape(-1)
+    occurred = np.zeros(65536, bool)
+    occurred[prev[want_hit]] = True
+    want_tokhit = np.packbits(occurred.reshape(-1, 32)[:, ::-1], axis=1).view(">u4").astype(np.uint32).reshape(-1)
+
+    lib = Lib()
+    d_tok = torch.from_numpy(tok.view(np.int16)).cuda()
+    d_member = torch.from_numpy(words.view(np.int32)).cuda()
+    bm = torch.full((L // 32,), -1, dtype=torch.int32, device="cuda")  # every word written: no fill needed
+    hit = torch.zeros(2048, dtype=torch.int32, device="cuda")
+    ids = torch.full((L,), -7, dtype=torch.int32, device="cuda")
+    lib("ng_scan_tok1", d_tok, L, d_member, bm, hit, ids, i32(grid))
+    torch.cuda.synchronize()
+    assert np.array_equal(bm.cpu().numpy().view(np.uint32), want_bm)
+    assert np.array_equal(hit.cpu().numpy().view(np.uint32), want_tokhit)
+    got_ids = ids.cpu().numpy()
+    assert np.array_equal(got_ids[want_hit], prev[want_hit])
+    assert (got_ids[~want_hit] == -7).all()  # positions without a hit are left as they are
+    with pytest.raises(RuntimeError):
+        lib("ng_scan_tok1", d_tok, L - 1, d_member, bm, hit, ids, i32(grid))  # L not a multiple of 32
