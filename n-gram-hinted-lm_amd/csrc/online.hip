@@ -456,6 +456,9 @@ __global__ void __launch_bounds__(WAVE) online_top_k(const u64* __restrict__ uk,
 // until each round fits; nothing global is written before a round fits). A context whose pairs fall in several rounds
 // is merged once per round: each merge supersedes the old entries of the pairs it touches, and a pair touched in a
 // later round but absent from that round's top 8 scores below all 8 of them, so the list ends as one merge leaves it.
+#ifndef OM_FRESH
+#define OM_FRESH 1  // a pair whose home slot reads EMPTY is inserted there at once (no walk, no count read)
+#endif
 #define OM_BITS 11
 #define OM_NB (1 << OM_BITS)
 #define OM_BLOCK 512
@@ -642,9 +645,18 @@ __global__ void __launch_bounds__(OM_BLOCK) __attribute__((amdgpu_waves_per_eu(4
                     const int i = i0 + j * OM_BLOCK + t;
                     if (i >= D) continue;
                     const OLevel lv = olevel(s_desc, tg[j]);
-                    if (cur[j] != key[j]) {
+                    // an empty home slot is taken at once: a slot whose key was EMPTY holds count 0 (counts are
+                    // written only after their key), so neither the slot nor its count is read again
+                    u64 prev = cur[j];
+                    if (OM_FRESH && cur[j] == EMPTY)
+                        prev = atomicCAS((unsigned long long*)(lv.pt + 2 * at[j]), EMPTY, (unsigned long long)key[j]);
+                    if (OM_FRESH && cur[j] == EMPTY && prev == EMPTY) {
+                        cc[j] = 0;
+                    } else if (prev != key[j]) {
                         at[j] = opair_slot(lv.pt, lv.pcap, key[j], lv.flags);
                         cc[j] = at[j] >= 0 ? *opair_cnt(lv.pt, at[j]) : 0;
+                    } else if (cur[j] != key[j]) {  // another lane's insert of the same key (not within a merge)
+                        cc[j] = *opair_cnt(lv.pt, at[j]);
                     }
                     u32 c = 0;
                     if (at[j] >= 0) {
