@@ -166,12 +166,13 @@ int ng_scan_exist(const uint16_t* tok, ng_i64 L, int k, const uint32_t* bm_in, u
                   int grid, int sparse, const uint32_t* pre, void* stream);
 /* level 1 of ng_scan_exist (no gate) with each 1-context's token as its context id, so no table: member (2048
  * words) bit t for each query token t; bm_out (L / 32 words) the hit positions (p: tok[p - 1] a query token, neither
- * it nor tok[p] SENT); hit (2048 words, zeroed by the caller) bit t where token t occurred; ids[p] = tok[p - 1] at
- * each hit position p. L a multiple of 32; grid <= 0: 2048 blocks (each block ORs its hit words into hit once) */
+ * it nor tok[p] SENT); hit (2048 words, zeroed by the caller) bit t where token t occurred; ids (may be NULL)
+ * ids[p] = tok[p - 1] at each hit position p. L a multiple of 32; grid <= 0: 2048 blocks (each block ORs its hit
+ * words into hit once) */
 int ng_scan_tok1(const uint16_t* tok, ng_i64 L, const uint32_t* member, uint32_t* bm_out, uint32_t* hit,
                  uint32_t* ids, int grid, void* stream);
-/* a level's counting scan from ng_scan_exist's ids: each position set in bm whose context's bit is set in `final`
- * emits its (id << 16 | tok[p]) event as ng_scan_emit's (regions, ev_count, dhist; wbits 0: mix64 with the top 8
+/* a level's counting scan from ng_scan_exist's ids (NULL: ng_scan_tok1's level, the id at p being tok[p - 1]): each
+ * position set in bm whose context's bit is set in `final` emits its (id << 16 | tok[p]) event as ng_scan_emit's (regions, ev_count, dhist; wbits 0: mix64 with the top 8
  * bits' histogram, wbits 17..63: kmix(key, wbits, mbits) with the top dbits bits', dbits <= 10); L a multiple of 32, tok
  * 8-byte and ids 16-byte aligned */
 int ng_scan_ids_emit(const uint16_t* tok, ng_i64 L, const uint32_t* bm, const uint32_t* ids, const uint32_t* final,

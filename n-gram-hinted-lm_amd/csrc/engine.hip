@@ -693,8 +693,8 @@ extern "C" int ng_scan_exist(const u16* tok, i64 L, int k, const u32* bm_in, u32
 namespace {
 // Level 1's existence scan with each 1-context's token as its id (no table: a 65536-bit set of the query tokens in
 // LDS): position p hits where tok[p - 1] is a query token and neither it nor tok[p] is SENT (ctx_key_at<1>'s context
-// and next token), which sets bm_out bit p, ids[p] = tok[p - 1] and the token's bit in hit (gathered per block in LDS,
-// then one atomicOr per nonzero word). A wave takes TOK1_PPL * 64 consecutive positions at a time, a lane every 64th.
+// and next token), which sets bm_out bit p, ids[p] = tok[p - 1] (ids may be NULL: the counting scan reads the token)
+// and the token's bit in hit (gathered per block in LDS, then one atomicOr per nonzero word). A wave takes TOK1_PPL * 64 consecutive positions at a time, a lane every 64th.
 #define TOK1_PPL 4
 __global__ void __launch_bounds__(256) scan_tok1_k(const u16* __restrict__ tok, i64 L, const u32* __restrict__ member,
                                                    u32* __restrict__ bm_out, u32* __restrict__ hit,
@@ -730,7 +730,7 @@ __global__ void __launch_bounds__(256) scan_tok1_k(const u16* __restrict__ tok, 
             if (lane == 0) bm_out[p0 >> 5] = (u32)b;
             if (lane == 32 && (p0 >> 5) + 1 < nwords) bm_out[(p0 >> 5) + 1] = (u32)(b >> 32);
             if (h) {
-                ids[p0 + lane] = cq;
+                if (ids) ids[p0 + lane] = cq;
                 const u32 m = 1u << (cq & 31);
                 if (!(agg[cq >> 5] & m)) atomicOr(&agg[cq >> 5], m);
             }
@@ -744,11 +744,11 @@ __global__ void __launch_bounds__(256) scan_tok1_k(const u16* __restrict__ tok, 
 
 // Level 1's existence scan (ng_scan_exist's k = 1 with no gate) with the 1-context's token as its context id:
 // member: 2048 words, bit t set for each query token t; bm_out (L / 32 words) the hit positions; hit (2048 words,
-// zeroed by the caller) bit t set where token t occurred as a context; ids[p] = tok[p - 1] at each hit position p
-// (others left as they are). L a multiple of 32.
+// zeroed by the caller) bit t set where token t occurred as a context; ids (may be NULL) ids[p] = tok[p - 1] at each
+// hit position p (others left as they are). L a multiple of 32.
 extern "C" int ng_scan_tok1(const u16* tok, i64 L, const u32* member, u32* bm_out, u32* hit, u32* ids, int grid,
                             void* stream) {
-    if (L < 0 || (L & 31) || (L > 0 && (!tok || !member || !bm_out || !hit || !ids))) return -1;
+    if (L < 0 || (L & 31) || (L > 0 && (!tok || !member || !bm_out || !hit))) return -1;
     if (L == 0) return 0;
     if (grid <= 0) grid = 2048;
     scan_tok1_k<<<grid, 256, 0, (hipStream_t)stream>>>(tok, L, member, bm_out, hit, ids);
@@ -756,8 +756,9 @@ extern "C" int ng_scan_tok1(const u16* tok, i64 L, const u32* member, u32* bm_ou
 }
 
 namespace {
-// The counting scan of a level whose existence scan stored each hit position's context id (ids): per position p set
-// in bm, a context id whose bit is set in `final` emits mix64(id << 16 | tok[p]) as ng_scan_emit's events. A wave
+// The counting scan of a level whose existence scan stored each hit position's context id (ids; NULL: level 1 by
+// token, whose id at p is tok[p - 1]): per position p set in bm, a context id whose bit is set in `final` emits
+// mix64(id << 16 | tok[p]) as ng_scan_emit's events. A wave
 // loads 64 bitmap words (2048 positions) at a time, skips them if all are empty, else walks them 8 words (256
 // positions) per step, a lane 4 consecutive positions: their ids in one 16-byte load and their tokens in one 8-byte
 // load, the 4 final-bit loads together; a step whose words are all empty is skipped.
@@ -781,10 +782,15 @@ __global__ void __launch_bounds__(256) scan_ids_k(const u16* __restrict__ tok, i
             u32 id[4] = {0, 0, 0, 0};
             u32 t[4] = {0, 0, 0, 0};
             if (bits) {  // a set bit lies below L, and so does its whole 4-aligned group (L is a multiple of 32)
-                const uint4 iv = *(const uint4*)(ids + p0);
                 const ushort4 tv = *(const ushort4*)(tok + p0);
-                id[0] = iv.x, id[1] = iv.y, id[2] = iv.z, id[3] = iv.w;
                 t[0] = tv.x, t[1] = tv.y, t[2] = tv.z, t[3] = tv.w;
+                if (ids) {
+                    const uint4 iv = *(const uint4*)(ids + p0);
+                    id[0] = iv.x, id[1] = iv.y, id[2] = iv.z, id[3] = iv.w;
+                } else {  // level 1 by token (ng_scan_tok1): a hit's context id is the token before it
+                    id[0] = p0 >= 1 ? (u32)tok[p0 - 1] : SENT;
+                    id[1] = t[0], id[2] = t[1], id[3] = t[2];
+                }
             }
             u32 fw[4];
 #pragma unroll

@@ -106,9 +106,9 @@ def longest_match(tok: torch.Tensor, x: torch.Tensor, avail: torch.Tensor, cap: 
             vi = _tok1_index(x, act)
             hit = torch.zeros(2048, dtype=torch.int32, device=dev)
             bm = torch.empty(nwords, dtype=torch.int32, device=dev)
-            ids = torch.empty(L, dtype=torch.int32, device=dev)
-            elib("ng_scan_tok1", tok, L, vi.member, bm, hit, ids, i32(TOK1_GRID))
-            levels.append(("bm", bm, _popcount(lib, bm), ids, act, vi.ctx_of, vi.ids))
+            # no stored ids: a hit's context id is the token before it, which the counting scan reads itself
+            elib("ng_scan_tok1", tok, L, vi.member, bm, hit, None, i32(TOK1_GRID))
+            levels.append(("bm", bm, _popcount(lib, bm), None, act, vi.ctx_of, vi.ids))
             ctx = vi.ctx_of.long()
             act = act[((hit[ctx >> 5] >> (ctx & 31)) & 1) != 0]
             length[act.long()] = k
@@ -322,7 +322,8 @@ def _tok1_index(x: torch.Tensor, act: torch.Tensor) -> SimpleNamespace:
 
 def _count_ids(elib: Lib, lib: Lib, tok, L: int, level: tuple, k: int, length, flags, grid: int, nxt, cnt) -> None:
     """The counting phase of a bitmap level from what its existence scan kept: the hit bitmap, each hit position's
-    context id, and the level's active positions with their context ids. The final contexts (those of the positions
+    context id (None at level 1 by token: the token before the position), and the level's active positions with their
+    context ids. The final contexts (those of the positions
     whose match ends at k) are marked in a bit set; the hit positions of final contexts emit their (context, next)
     events (ng_scan_ids_emit), which are partitioned, counted and summarized per context (top entry), then gathered
     to the final positions."""

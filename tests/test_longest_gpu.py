@@ -187,5 +187,11 @@ def test_level_one_scan_by_token(seed, grid):
     got_ids = ids.cpu().numpy()
     assert np.array_equal(got_ids[want_hit], prev[want_hit])
     assert (got_ids[~want_hit] == -7).all()  # positions without a hit are left as they are
+    # without an ids array (the counting scan then reads the token before each hit): the same bitmap and tokens
+    bm2 = torch.full((L // 32,), -1, dtype=torch.int32, device="cuda")
+    hit2 = torch.zeros(2048, dtype=torch.int32, device="cuda")
+    lib("ng_scan_tok1", d_tok, L, d_member, bm2, hit2, None, i32(grid))
+    torch.cuda.synchronize()
+    assert torch.equal(bm2, bm) and torch.equal(hit2, hit)
     with pytest.raises(RuntimeError):
         lib("ng_scan_tok1", d_tok, L - 1, d_member, bm, hit, ids, i32(grid))  # L not a multiple of 32
