@@ -88,6 +88,13 @@ def test_counts_match_oracle(corpus, level_shards, mode, monkeypatch):
         assert np.array_equal(top_tok[li], o["top_tok"][:, :4]), f"top_tok k={k}"
         assert np.array_equal(top_cnt[li], o["top_cnt"][:, :4]), f"top_cnt k={k}"
         assert cb.info[k]["hits"] == o["events"], f"hits k={k}"
+    if mode in ("part", "list"):
+        # a warm build (sizes learnt, no hit statistics): dense levels' query tables at their sparser load, the last
+        # level's list scan without a bitmap, the device-listed query positions; the same outputs
+        again = cb.counts(x, tgt, avail).cpu().numpy()
+        assert np.array_equal(again, out)
+        assert np.array_equal(cb.top_tok.cpu().numpy().view(np.uint16), top_tok)
+        assert np.array_equal(cb.top_cnt.cpu().numpy().view(np.uint32), top_cnt)
     if mode == "regroup":
         assert cb.info[2]["pbits"] >= 3, cb.info[2]
     if mode == "regroup32":
